@@ -1,0 +1,270 @@
+/*
+ * supa_amd.h -- C ABI of the MI355X (gfx950) kernels behind the PrivateUse1
+ * elementwise + loss operator path.
+ *
+ * Every entry point enqueues work on `stream` (a hipStream_t passed as void*;
+ * NULL is the legacy default stream) and returns without waiting.  Entry points
+ * never allocate device memory and never throw; outputs, and any workspace an
+ * entry point asks for, come pre-allocated from the caller.  All tensors are
+ * borrowed raw device pointers for the duration of the enqueue.
+ *
+ * Return value: SUPA_AMD_OK (0), a negative SUPA_AMD_E* argument error, or a
+ * positive hipError_t from the launch.  supa_amd_status_string() names both.
+ *
+ * Each declaration names the reference interface it replaces.  Paths are in
+ * BIRENSUPA/torch-supa; "NF:<line>" is the schema line in upstream
+ * torchgen/packaged/ATen/native/native_functions.yaml (torch 2.10.0), for ops
+ * whose device kernel the reference takes from its upstream-ATen operator
+ * library (third-party/torch-supa-op, registered by the generated
+ * RegisterSUPANative_0.cpp, script/codegen_native/gen.py:537-612).
+ */
+#ifndef SUPA_AMD_H
+#define SUPA_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SUPA_AMD_ABI_VERSION 1
+
+/* ------------------------------------------------------------ status codes */
+#define SUPA_AMD_OK 0
+#define SUPA_AMD_EINVAL (-1)   /* malformed descriptor or argument */
+#define SUPA_AMD_EDTYPE (-2)   /* dtype combination without a kernel */
+#define SUPA_AMD_ELAYOUT (-3)  /* layout the entry point does not take */
+#define SUPA_AMD_EWORKSPACE (-4) /* workspace missing or too small */
+
+/* ------------------------------------------------------------ dtype codes
+ * Equal to c10::ScalarType so the host layer passes them through. */
+#define SUPA_AMD_U8 0
+#define SUPA_AMD_I8 1
+#define SUPA_AMD_I16 2
+#define SUPA_AMD_I32 3
+#define SUPA_AMD_I64 4
+#define SUPA_AMD_F16 5
+#define SUPA_AMD_F32 6
+#define SUPA_AMD_F64 7
+#define SUPA_AMD_BOOL 11
+#define SUPA_AMD_BF16 15
+
+/* ------------------------------------------------- elementwise descriptor
+ * An already broadcast, dimension-coalesced iteration space (the planner's
+ * output, the role TensorIteratorBase plays for the reference's gpu_kernel,
+ * torch_supa/csrc/aten/ops/kernels/elementwise/Loops.cuh:110-134).
+ * Dimension 0 is the fastest-moving one.  op[0] is the output, op[1..] are
+ * the inputs in the order each entry point documents. */
+#define SUPA_AMD_MAX_DIMS 8
+#define SUPA_AMD_MAX_OPERANDS 5
+
+typedef struct supa_amd_operand {
+  void* data;                          /* element (0,...,0) of the view */
+  int64_t strides[SUPA_AMD_MAX_DIMS];  /* in elements; 0 = broadcast dim */
+  int32_t dtype;                       /* storage dtype code */
+  int32_t is_scalar;                   /* 1: an immediate host scalar; data and strides unused */
+  double scalar;                       /* immediate value for floating/bool ops */
+  int64_t iscalar;                     /* immediate value for integer ops */
+} supa_amd_operand;
+
+typedef struct supa_amd_ew_desc {
+  int64_t sizes[SUPA_AMD_MAX_DIMS];
+  int32_t ndim;          /* 0 means one element */
+  int32_t noperands;     /* outputs + inputs */
+  int32_t common_dtype;  /* inputs are converted to this dtype, then computed in its opmath type */
+  int32_t reserved;
+  supa_amd_operand op[SUPA_AMD_MAX_OPERANDS];
+} supa_amd_ew_desc;
+
+const char* supa_amd_status_string(int status);
+int supa_amd_abi_version(void);
+
+/* ------------------------------------------------------ elementwise binary */
+
+/* out = a + alpha * b in the opmath type of common_dtype (sub is alpha = -alpha).
+ * op = {out, a, b}.  Replaces add_stub: add_kernel,
+ * torch_supa/csrc/aten/ops/kernels/elementwise/UfuncCUDA_add.cu:77-340,
+ * registered at :341-345. */
+int supa_amd_add(const supa_amd_ew_desc* d, double alpha, int64_t ialpha, void* stream);
+
+/* out = a * b (bool: a && b).  op = {out, a, b}.  Replaces mul_stub:
+ * mul_kernel_cuda, .../elementwise/BinaryMulKernel.cu:25-43. */
+int supa_amd_mul(const supa_amd_ew_desc* d, void* stream);
+
+/* Division.  mode 0 = true division (IEEE a / b, also for a CPU-scalar
+ * divisor), 1 = trunc, 2 = floor.  op = {out, a, b}.  Replaces
+ * div_true_stub / div_trunc_stub / div_floor_stub:
+ * .../elementwise/BinaryDivTrueKernel.cu:22-65, BinaryDivTruncKernel.cu:22-55,
+ * BinaryDivFloorKernel.cu:22-82. */
+#define SUPA_AMD_DIV_TRUE 0
+#define SUPA_AMD_DIV_TRUNC 1
+#define SUPA_AMD_DIV_FLOOR 2
+int supa_amd_div(const supa_amd_ew_desc* d, int mode, void* stream);
+
+/* ------------------------------------------------ activations (unary) */
+#define SUPA_AMD_GELU 0
+#define SUPA_AMD_GELU_TANH 1
+#define SUPA_AMD_SILU 2
+#define SUPA_AMD_SIGMOID 3
+#define SUPA_AMD_TANH 4
+#define SUPA_AMD_EXP 5
+#define SUPA_AMD_LOG 6
+#define SUPA_AMD_ERF 7
+#define SUPA_AMD_RELU 8
+#define SUPA_AMD_NEG 9
+
+/* out = f(x), floating dtypes (RELU and NEG also integer).  op = {out, x}.
+ * Replaces the reference's upstream-ATen activation kernels: gelu.out NF:5216,
+ * silu.out NF:5374, sigmoid.out NF:5441, tanh.out, exp.out, log.out, erf.out,
+ * relu, neg.out. */
+int supa_amd_unary(const supa_amd_ew_desc* d, int op, void* stream);
+
+/* grad_in = f'(...) * dy.  op = {grad_in, dy, x} where x is the forward input
+ * for GELU, GELU_TANH, SILU and the forward output for SIGMOID, TANH.
+ * Replaces gelu_backward.grad_input NF:5245, silu_backward.grad_input NF:5383,
+ * sigmoid_backward.grad_input NF:13229, tanh_backward.grad_input. */
+int supa_amd_unary_backward(const supa_amd_ew_desc* d, int op, void* stream);
+
+/* ------------------------------------------------------ copy / fill */
+
+/* out = cast(in), any strides and dtypes.  op = {out, in}.  Replaces the
+ * device-to-device part of SUPANativeFunctions::copy_,
+ * torch_supa/csrc/aten/common/Copy.cpp:154-245, and direct_copy_kernel_cuda,
+ * .../elementwise/copy.cu:791-859. */
+int supa_amd_copy(const supa_amd_ew_desc* d, void* stream);
+
+/* out = value (op[1] is an immediate scalar).  op = {out, value}.  Replaces
+ * fill_.Scalar NF:2727 (upstream FillKernel) and zero_ NF:7079. */
+int supa_amd_fill(const supa_amd_ew_desc* d, void* stream);
+
+/* ------------------------------------------------------ pointwise losses */
+#define SUPA_AMD_LOSS_MSE 0
+#define SUPA_AMD_LOSS_SMOOTH_L1 1
+#define SUPA_AMD_LOSS_BCE_LOGITS 2
+
+#define SUPA_AMD_REDUCTION_NONE 0
+#define SUPA_AMD_REDUCTION_MEAN 1
+#define SUPA_AMD_REDUCTION_SUM 2
+
+/* Loss terms per element.  op = {out, input, target[, pos_weight][, weight]}
+ * (pos_weight only for BCE, flagged by has_pos_weight; weight only for BCE,
+ * flagged by has_weight).
+ * reduction NONE: op[0] is the [n] loss tensor.
+ * reduction MEAN/SUM: op[0] describes the iteration space only (its data is
+ * unused) and the single f32/f64-rounded-to-out_dtype result is written to
+ * `out_scalar` (a one-element device buffer of dtype op[0].dtype); the sum is
+ * accumulated in float32 (float64 for f64), deterministically, in two stages
+ * through `workspace` (see supa_amd_loss_workspace_bytes).
+ * Replaces mse_loss.out NF:11832, smooth_l1_loss.out NF:11988 (upstream
+ * structured kernels + at::sum/at::mean, sum_kernel_cuda
+ * .../kernels/reduce/ReduceSumKernel.cu:102-113, mean_kernel_cuda
+ * ReduceMomentKernel.cu:37-55), and
+ * SUPANativeFunctions::binary_cross_entropy_with_logits,
+ * torch_supa/csrc/aten/ops/BinaryCrossEntropyWithLogits.cpp:23-73 with its
+ * kernel .../elementwise/BinaryCrossEntropyWithLogitsKernel.cu:17-113. */
+int supa_amd_loss_forward(const supa_amd_ew_desc* d, int loss, int reduction, double beta,
+                          int has_pos_weight, int has_weight, void* out_scalar,
+                          void* workspace, int64_t workspace_bytes, void* stream);
+int64_t supa_amd_loss_workspace_bytes(int64_t numel);
+
+/* Loss gradients.  op = {grad_in, grad_out, input, target}; grad_out is
+ * broadcast (0-dim) for MEAN/SUM.  norm is the reduction factor the reference
+ * applies (2/n or 2 for MSE, 1/n or 1 for SMOOTH_L1).  Replaces
+ * mse_loss_backward.grad_input NF:11846 and
+ * smooth_l1_loss_backward.grad_input NF:12002. */
+int supa_amd_loss_backward(const supa_amd_ew_desc* d, int loss, double norm, double beta,
+                           void* stream);
+
+/* ---------------------------------------------------------- reductions */
+
+/* out[0] = scale * sum(in) over every element of the described input
+ * (op = {out, in}; op[0] describes the input's iteration space, its data is
+ * the one-element output).  Accumulates in float32 (float64 for f64 input),
+ * deterministic two-stage tree through `workspace`.  scale = 1 for sum,
+ * 1/n for mean (the reference's mean factor, ReduceMomentKernel.cu:20).
+ * Replaces sum_stub / mean_stub for full reductions:
+ * .../kernels/reduce/ReduceSumKernel.cu:102-113, ReduceMomentKernel.cu:37-55. */
+int supa_amd_sum(const supa_amd_ew_desc* d, double scale, void* workspace,
+                 int64_t workspace_bytes, void* stream);
+int64_t supa_amd_sum_workspace_bytes(int64_t numel);
+
+/* Reduction of the innermost `inner` elements of each of `outer` rows of a
+ * contiguous input: out[r] = scale * sum(in[r*inner .. r*inner+inner)).
+ * Replaces sum_stub / mean_stub for dim reductions over trailing dims. */
+int supa_amd_sum_rows(const void* in, int32_t in_dtype, void* out, int32_t out_dtype,
+                      int64_t outer, int64_t inner, double scale, void* stream);
+
+/* ------------------------------------------------------ row softmax ops */
+
+/* out[r, :] = x[r, :] - max_r - log(sum exp(x[r, :] - max_r)) over rows of a
+ * contiguous [rows, cols] input.  in/out dtypes: f32 -> f32, bf16 -> bf16,
+ * f16 -> f16, bf16/f16 -> f32 (half_to_float).  Replaces _log_softmax.out
+ * NF:3752 (upstream SoftMax.cu, torch/include/ATen/native/cuda/PersistentSoftmax.cuh). */
+int supa_amd_log_softmax_forward(const void* in, int32_t in_dtype, void* out, int32_t out_dtype,
+                                 int64_t rows, int64_t cols, void* stream);
+
+/* grad_in[r, :] = g[r, :] - exp(y[r, :]) * sum(g[r, :]).  g and y share
+ * dtype gy_dtype; grad_in has gin_dtype.  Replaces
+ * _log_softmax_backward_data.out NF:3763. */
+int supa_amd_log_softmax_backward(const void* grad, const void* output, int32_t gy_dtype,
+                                  void* grad_in, int32_t gin_dtype, int64_t rows, int64_t cols,
+                                  void* stream);
+
+/* ------------------------------------------------------------ nll_loss */
+
+/* nll_loss over logp [n, c] (contiguous, dtype f32/bf16/f16/f64), int64
+ * target [n], optional weight [c] (same dtype, or NULL).
+ * reduction NONE: out [n]; MEAN/SUM: out and total_weight are one-element
+ * buffers of the logp dtype.  Rows whose target equals ignore_index
+ * contribute nothing and are not counted (mean of no rows is NaN).
+ * *error_flag (device int32, may be NULL) is set to 1 when a target is out of
+ * range; the caller reads it lazily.  Replaces nll_loss_forward.output
+ * NF:11928; ignore semantics as CrossEntropyLossKernel.cu:71-119. */
+int supa_amd_nll_loss_forward(const void* logp, int32_t dtype, const int64_t* target,
+                              const void* weight, int64_t n, int64_t c, int reduction,
+                              int64_t ignore_index, void* out, void* total_weight,
+                              int32_t* error_flag, void* stream);
+
+/* grad_in [n, c] (fully written: zero except grad_in[i, t_i] = -w[t_i] * g_i,
+ * or -w[t_i] * g / total_weight for MEAN, -w[t_i] * g for SUM).  grad_out is
+ * [n] for NONE, one element otherwise; total_weight is the forward's
+ * one-element buffer.  Replaces nll_loss_backward.grad_input NF:11940. */
+int supa_amd_nll_loss_backward(const void* grad_out, int32_t dtype, const int64_t* target,
+                               const void* weight, const void* total_weight, int64_t n, int64_t c,
+                               int reduction, int64_t ignore_index, void* grad_in,
+                               int32_t* error_flag, void* stream);
+
+/* ------------------------------------------------- multi-tensor apply */
+#define SUPA_AMD_FOREACH_ADD 0   /* out = a + alpha * b  (b list or scalar) */
+#define SUPA_AMD_FOREACH_MUL 1   /* out = a * b          (b list or scalar) */
+
+/* In-place or out-of-place list arithmetic over `ntensors` contiguous tensors
+ * of one dtype.  b == NULL selects the scalar overload (value `scalar`).
+ * out may equal a (the in-place overloads).  Replaces _foreach_add_.List
+ * NF:10685, _foreach_add_.Scalar NF:10668, _foreach_mul_.List NF:10794,
+ * _foreach_mul_.Scalar NF:10777 and their out-of-place forms (upstream
+ * ForeachBinaryOp*.cu over MultiTensorApply.cuh). */
+int supa_amd_foreach_binary(int op, int32_t ntensors, void* const* out, void* const* a,
+                            void* const* b, const int64_t* numel, int32_t dtype, double scalar,
+                            double alpha, void* stream);
+
+/* One fused AdamW step over `ntensors` tensors (params, grads, exp_avgs,
+ * exp_avg_sqs [, max_exp_avg_sqs when amsgrad]) of one dtype (f32, bf16, f16,
+ * f64), each with a one-element f32 state_step on the device.  lr_ptr (device
+ * f32, may be NULL) overrides lr; grad_scale / found_inf (device f32, may be
+ * NULL) follow the AMP contract.  Replaces _fused_adamw_ NF:16041 and
+ * _fused_adamw_.tensor_lr NF:16050 (upstream fused_adamw_impl.cu,
+ * torch/include/ATen/native/cuda/fused_adam_utils.cuh:27-93, :130-137). */
+int supa_amd_fused_adamw(int32_t ntensors, void* const* params, void* const* grads,
+                         void* const* exp_avgs, void* const* exp_avg_sqs,
+                         void* const* max_exp_avg_sqs, void* const* state_steps,
+                         const int64_t* numel, int32_t dtype, double lr, const float* lr_ptr,
+                         double beta1, double beta2, double weight_decay, double eps,
+                         int amsgrad, int maximize, const float* grad_scale,
+                         const float* found_inf, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SUPA_AMD_H */

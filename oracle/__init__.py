@@ -1,0 +1,256 @@
+"""TEST INFRASTRUCTURE ONLY -- numpy front end of the CPU oracle.
+
+The oracle restates, in plain C (``oracle/oracle.c``, ``oracle/oracle_math.h``),
+the arithmetic the reference runs for the elementwise + loss operator path.  Only
+``tests/``, ``bench.py``'s ``cpu_baseline`` leg and ``__graft_entry__.smoke()``
+may import this package, and only as the checker.  The shipped library never
+imports it; its device path fails loudly when the HIP extension is missing.
+
+This module does the plumbing the C side leaves out: broadcasting, dtype
+conversion (bfloat16 travels as ``uint16`` bit patterns), and integer arithmetic
+(done with numpy's wrapping integer ops, which are the C semantics the
+reference's integer kernels use).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_SO = os.path.join(_HERE, "_build", "liboracle.so")
+_lib = None
+
+# op codes shared with oracle.c
+ADD, MUL, DIV, DIV_TRUNC, DIV_FLOOR = 0, 1, 2, 3, 4
+GELU, GELU_TANH, SILU, SIGMOID, TANH, EXP, LOG, ERF, RELU, NEG = range(10)
+MSE, SMOOTH_L1, BCE_LOGITS = 0, 1, 2
+REDUCTION = {"none": 0, "mean": 1, "sum": 2}
+
+_f32p = ctypes.POINTER(ctypes.c_float)
+_f64p = ctypes.POINTER(ctypes.c_double)
+_u16p = ctypes.POINTER(ctypes.c_uint16)
+_i64p = ctypes.POINTER(ctypes.c_int64)
+
+
+def build() -> str:
+    """Compile the oracle with its Makefile (gcc); returns the library path."""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+    return _SO
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_SO):
+            build()
+        L = ctypes.CDLL(_SO)
+        i64, c_int, c_float, c_double = ctypes.c_int64, ctypes.c_int, ctypes.c_float, ctypes.c_double
+        sig = {
+            "or_f32_to_bf16": (None, [_f32p, _u16p, i64]),
+            "or_bf16_to_f32": (None, [_u16p, _f32p, i64]),
+            "or_f64_to_bf16": (None, [_f64p, _u16p, i64]),
+            "or_binary_f32": (None, [c_int, _f32p, _f32p, _f32p, i64, c_float]),
+            "or_binary_f64": (None, [c_int, _f64p, _f64p, _f64p, i64, c_double]),
+            "or_unary_f32": (None, [c_int, _f32p, _f32p, i64]),
+            "or_unary_backward_f32": (None, [c_int, _f32p, _f32p, _f32p, i64]),
+            "or_log_softmax_fwd": (None, [_f32p, _f32p, i64, i64]),
+            "or_log_softmax_bwd": (None, [_f32p, _f32p, _f32p, i64, i64]),
+            "or_nll_loss_fwd": (c_int, [_f32p, _i64p, _f32p, i64, i64, c_int, i64, _f32p, _f32p]),
+            "or_nll_loss_bwd": (c_int, [_f32p, _i64p, _f32p, i64, i64, c_int, i64, c_float, c_int, _f32p]),
+            "or_loss_fwd": (None, [c_int, _f32p, _f32p, _f32p, _f32p, i64, c_int, c_float, _f32p]),
+            "or_loss_bwd": (None, [c_int, _f32p, _f32p, _f32p, _f32p, _f32p, i64, c_int, c_float, _f32p]),
+            "or_sum_f32": (c_double, [_f32p, i64]),
+            "or_adamw_step": (None, [_f32p, _f32p, _f32p, _f32p, i64, c_float, c_double, c_double,
+                                     c_double, c_double, c_double, c_int, _f32p, c_int, _f32p]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _p(a, ptype):
+    if a is None:
+        return None
+    return a.ctypes.data_as(ptype)
+
+
+def _c(a, dtype):
+    return np.ascontiguousarray(a, dtype=dtype)
+
+
+# ------------------------------------------------------------------ casts --
+def f32_to_bf16(x) -> np.ndarray:
+    """float32 -> bfloat16 bit patterns (uint16), round to nearest even."""
+    x = _c(x, np.float32)
+    out = np.empty(x.shape, np.uint16)
+    lib().or_f32_to_bf16(_p(x, _f32p), _p(out, _u16p), x.size)
+    return out
+
+
+def bf16_to_f32(h) -> np.ndarray:
+    h = _c(h, np.uint16)
+    out = np.empty(h.shape, np.float32)
+    lib().or_bf16_to_f32(_p(h, _u16p), _p(out, _f32p), h.size)
+    return out
+
+
+def f64_to_bf16(x) -> np.ndarray:
+    x = _c(x, np.float64)
+    out = np.empty(x.shape, np.uint16)
+    lib().or_f64_to_bf16(_p(x, _f64p), _p(out, _u16p), x.size)
+    return out
+
+
+def round_bf16(x) -> np.ndarray:
+    """float32 values rounded through bfloat16 and back (float32 result)."""
+    return bf16_to_f32(f32_to_bf16(x))
+
+
+# ------------------------------------------------------------ elementwise --
+def binary(op: int, a, b, alpha: float = 1.0, dtype=np.float32) -> np.ndarray:
+    """Binary op on float32/float64 operands after numpy broadcasting.
+
+    For integer dtypes use :func:`binary_int`."""
+    a, b = np.broadcast_arrays(np.asarray(a), np.asarray(b))
+    if dtype == np.float64:
+        a, b = _c(a, np.float64), _c(b, np.float64)
+        out = np.empty(a.shape, np.float64)
+        lib().or_binary_f64(op, _p(a, _f64p), _p(b, _f64p), _p(out, _f64p), a.size, float(alpha))
+        return out
+    a, b = _c(a, np.float32), _c(b, np.float32)
+    out = np.empty(a.shape, np.float32)
+    lib().or_binary_f32(op, _p(a, _f32p), _p(b, _f32p), _p(out, _f32p), a.size, float(alpha))
+    return out
+
+
+def binary_int(op: int, a, b, alpha: int = 1, dtype=np.int64) -> np.ndarray:
+    """Wrapping integer arithmetic (UfuncCUDA_add.cu:13-16 add, BinaryInternal.h
+    mul, BinaryDivTruncKernel.cu / BinaryDivFloorKernel.cu integer paths)."""
+    a = np.asarray(a, dtype=dtype)
+    b = np.asarray(b, dtype=dtype)
+    with np.errstate(over="ignore"):
+        if op == ADD:
+            return (a + (b * dtype(alpha)).astype(dtype)).astype(dtype)
+        if op == MUL:
+            return (a * b).astype(dtype)
+        if op == DIV_TRUNC:
+            q = np.abs(a) // np.abs(b)
+            return np.where((a < 0) != (b < 0), -q, q).astype(dtype)
+        if op == DIV_FLOOR:
+            return np.floor_divide(a, b).astype(dtype)
+    raise ValueError(op)
+
+
+def unary(op: int, x) -> np.ndarray:
+    x = _c(x, np.float32)
+    out = np.empty(x.shape, np.float32)
+    lib().or_unary_f32(op, _p(x, _f32p), _p(out, _f32p), x.size)
+    return out
+
+
+def unary_backward(op: int, dy, x) -> np.ndarray:
+    dy, x = np.broadcast_arrays(np.asarray(dy), np.asarray(x))
+    dy, x = _c(dy, np.float32), _c(x, np.float32)
+    out = np.empty(x.shape, np.float32)
+    lib().or_unary_backward_f32(op, _p(dy, _f32p), _p(x, _f32p), _p(out, _f32p), x.size)
+    return out
+
+
+# ------------------------------------------------------------- row ops --
+def log_softmax(x) -> np.ndarray:
+    """log_softmax over the last dim (float32 in, float32 out)."""
+    x = _c(x, np.float32)
+    cols = x.shape[-1]
+    rows = x.size // max(cols, 1)
+    out = np.empty(x.shape, np.float32)
+    lib().or_log_softmax_fwd(_p(x, _f32p), _p(out, _f32p), rows, cols)
+    return out
+
+
+def log_softmax_backward(g, y) -> np.ndarray:
+    g, y = _c(g, np.float32), _c(y, np.float32)
+    cols = g.shape[-1]
+    rows = g.size // max(cols, 1)
+    out = np.empty(g.shape, np.float32)
+    lib().or_log_softmax_bwd(_p(g, _f32p), _p(y, _f32p), _p(out, _f32p), rows, cols)
+    return out
+
+
+def nll_loss(logp, target, weight=None, reduction="mean", ignore_index=-100):
+    """Returns (output, total_weight) as float32 arrays."""
+    logp = _c(logp, np.float32)
+    target = _c(target, np.int64)
+    n, c = logp.shape
+    w = None if weight is None else _c(weight, np.float32)
+    red = REDUCTION[reduction]
+    out = np.empty(n if red == 0 else 1, np.float32)
+    tw = np.zeros(1, np.float32)
+    rc = lib().or_nll_loss_fwd(_p(logp, _f32p), _p(target, _i64p), _p(w, _f32p), n, c, red,
+                               ignore_index, _p(out, _f32p), _p(tw, _f32p))
+    if rc != 0:
+        raise IndexError("nll_loss: target out of bounds")
+    return (out if red == 0 else out.reshape(())), tw.reshape(())
+
+
+def nll_loss_backward(grad_out, target, n, c, total_weight, weight=None, reduction="mean",
+                      ignore_index=-100, bf16=False) -> np.ndarray:
+    g = _c(grad_out, np.float32).reshape(-1)
+    target = _c(target, np.int64)
+    w = None if weight is None else _c(weight, np.float32)
+    out = np.empty((n, c), np.float32)
+    rc = lib().or_nll_loss_bwd(_p(g, _f32p), _p(target, _i64p), _p(w, _f32p), n, c,
+                               REDUCTION[reduction], ignore_index, float(total_weight),
+                               1 if bf16 else 0, _p(out, _f32p))
+    if rc != 0:
+        raise IndexError("nll_loss_backward: target out of bounds")
+    return out
+
+
+def loss(op: int, x, t, pos_weight=None, weight=None, reduction="mean", beta=1.0):
+    x = _c(x, np.float32)
+    t = _c(np.broadcast_to(t, x.shape), np.float32)
+    pw = None if pos_weight is None else _c(np.broadcast_to(pos_weight, x.shape), np.float32)
+    w = None if weight is None else _c(np.broadcast_to(weight, x.shape), np.float32)
+    red = REDUCTION[reduction]
+    out = np.empty(x.shape if red == 0 else (1,), np.float32)
+    lib().or_loss_fwd(op, _p(x, _f32p), _p(t, _f32p), _p(pw, _f32p), _p(w, _f32p), x.size, red,
+                      float(beta), _p(out, _f32p))
+    return out if red == 0 else out.reshape(())
+
+
+def loss_backward(op: int, grad, x, t, pos_weight=None, weight=None, reduction="mean", beta=1.0):
+    x = _c(x, np.float32)
+    t = _c(np.broadcast_to(t, x.shape), np.float32)
+    pw = None if pos_weight is None else _c(np.broadcast_to(pos_weight, x.shape), np.float32)
+    w = None if weight is None else _c(np.broadcast_to(weight, x.shape), np.float32)
+    red = REDUCTION[reduction]
+    g = _c(grad, np.float32).reshape(-1)
+    out = np.empty(x.shape, np.float32)
+    lib().or_loss_bwd(op, _p(g, _f32p), _p(x, _f32p), _p(t, _f32p), _p(pw, _f32p), _p(w, _f32p),
+                      x.size, red, float(beta), _p(out, _f32p))
+    return out
+
+
+def sum_f32(x) -> float:
+    x = _c(x, np.float32)
+    return float(lib().or_sum_f32(_p(x, _f32p), x.size))
+
+
+def adamw_step(p, g, m, v, step, lr, beta1, beta2, weight_decay, eps, maximize=False,
+               grad_scale=None, amsgrad=False, vmax=None):
+    """In-place AdamW step on float32 numpy arrays (p, m, v and, with
+    grad_scale, g are updated)."""
+    for a in (p, g, m, v):
+        assert a.dtype == np.float32 and a.flags.c_contiguous
+    gs = None if grad_scale is None else np.asarray([grad_scale], np.float32)
+    if amsgrad:
+        assert vmax is not None and vmax.dtype == np.float32
+    lib().or_adamw_step(_p(p, _f32p), _p(g, _f32p), _p(m, _f32p), _p(v, _f32p), p.size,
+                        float(step), lr, beta1, beta2, weight_decay, eps, 1 if maximize else 0,
+                        _p(gs, _f32p), 1 if amsgrad else 0, _p(vmax, _f32p))

@@ -1,0 +1,453 @@
+/*
+ * TEST INFRASTRUCTURE ONLY -- the CPU oracle of the elementwise + loss path.
+ *
+ * A plain-C restatement of the arithmetic the reference runs on its device for
+ * each op, written from the reference sources cited per function.  Only
+ * tests/, bench.py's cpu_baseline leg and __graft_entry__.smoke() may load it,
+ * and only as the checker; the shipped library never links or calls it.
+ *
+ * Conventions.
+ *  - Arrays are flat and contiguous: broadcasting and dtype plumbing are done
+ *    by the numpy wrapper (oracle/__init__.py) before the call.
+ *  - bfloat16 is carried as uint16 bit patterns; conversions are round to
+ *    nearest even with NaN -> 0x7FC0, the rule of c10::BFloat16.
+ *  - "opmath" is float32 for f32/bf16/f16 storage, as in the reference's
+ *    at::opmath_type.
+ *  - Elementwise formulas keep the operation order of the reference functor so
+ *    the float32 result is bit-identical to an IEEE device that evaluates the
+ *    same sequence.  Row and full reductions accumulate in double here, so the
+ *    device (which accumulates in float32 in a different order) is compared
+ *    with a tolerance, not bit for bit.
+ *
+ * Build: oracle/Makefile (gcc -O2 -march=x86-64-v3 -ffp-contract=off).
+ * Parity of every function is pinned by tests/test_oracle_*.py against the
+ * upstream aten CPU kernels (torch 2.10.0, the kernels the reference's
+ * operator library is built from), committed golden vectors, closed forms and
+ * invariants.
+ */
+#include "oracle_math.h"
+
+#include <stddef.h>
+#include <stdint.h>
+#include <stdlib.h>
+
+/* ---------------------------------------------------------------- casts -- */
+
+/* c10/util/BFloat16.h round_to_nearest_even (NaN -> 0x7FC0). */
+static inline uint16_t bf16_from_f32(float f) {
+  if (isnan(f)) return 0x7FC0u;
+  const uint32_t u = or_as_u32(f);
+  return (uint16_t)((u + (((u >> 16) & 1u) + 0x7FFFu)) >> 16);
+}
+static inline float bf16_to_f32(uint16_t h) { return or_as_float((uint32_t)h << 16); }
+
+void or_f32_to_bf16(const float* in, uint16_t* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = bf16_from_f32(in[i]);
+}
+void or_bf16_to_f32(const uint16_t* in, float* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = bf16_to_f32(in[i]);
+}
+void or_f64_to_bf16(const double* in, uint16_t* out, int64_t n) {
+  /* Direct RNE from double (used for exact-math references of bf16 results). */
+  for (int64_t i = 0; i < n; ++i) {
+    const double d = in[i];
+    if (isnan(d)) { out[i] = 0x7FC0u; continue; }
+    const float f = (float)d; /* may round; fix up a double-rounding tie below */
+    uint16_t h = bf16_from_f32(f);
+    const double lo = (double)bf16_to_f32(h);
+    /* choose the nearer of h and its neighbour towards d */
+    const uint16_t h2 = (uint16_t)(d > lo ? h + ((h & 0x8000u) ? -1 : 1)
+                                          : h + ((h & 0x8000u) ? 1 : -1));
+    if (d != lo && !isinf(lo)) {
+      const double alt = (double)bf16_to_f32(h2);
+      if (fabs(alt - d) < fabs(lo - d)) h = h2;
+    }
+    out[i] = h;
+  }
+}
+
+/* ------------------------------------------------------------ binary ops -- */
+
+enum { OR_ADD = 0, OR_MUL = 1, OR_DIV = 2, OR_DIV_TRUNC = 3, OR_DIV_FLOOR = 4 };
+
+/* c10::div_floor_floating (c10/util/generic_math.h), the Python-style floor
+ * division that BinaryDivFloorKernel.cu:22-82 applies to floating types. */
+static inline float div_floor_f32(float a, float b) {
+  if (b == 0.0f) return a / b;
+  float mod = fmodf(a, b);
+  float div = (a - mod) / b;
+  if (mod != 0.0f && ((b < 0.0f) != (mod < 0.0f))) div -= 1.0f;
+  float floordiv;
+  if (div != 0.0f) {
+    floordiv = floorf(div);
+    if (div - floordiv > 0.5f) floordiv += 1.0f;
+  } else {
+    floordiv = copysignf(0.0f, a / b);
+  }
+  return floordiv;
+}
+static inline double div_floor_f64(double a, double b) {
+  if (b == 0.0) return a / b;
+  double mod = fmod(a, b);
+  double div = (a - mod) / b;
+  if (mod != 0.0 && ((b < 0.0) != (mod < 0.0))) div -= 1.0;
+  double floordiv;
+  if (div != 0.0) {
+    floordiv = floor(div);
+    if (div - floordiv > 0.5) floordiv += 1.0;
+  } else {
+    floordiv = copysign(0.0, a / b);
+  }
+  return floordiv;
+}
+
+/* add: ufunc::add `self + alpha * other` in opmath (UfuncCUDA_add.cu:13-16),
+ *      evaluated as one fused multiply-add (the contraction both the CUDA
+ *      compiler and the CPU vectorised kernel apply);
+ * mul: MulFunctor (BinaryInternal.h:17-22);
+ * div: DivFunctor `a / b` (BinaryInternal.h:10-15), true IEEE division;
+ * div trunc / floor: BinaryDivTruncKernel.cu:22-55 / BinaryDivFloorKernel.cu:22-82. */
+void or_binary_f32(int op, const float* a, const float* b, float* out, int64_t n, float alpha) {
+  for (int64_t i = 0; i < n; ++i) {
+    const float x = a[i], y = b[i];
+    float r;
+    switch (op) {
+      case OR_ADD: r = fmaf(alpha, y, x); break;
+      case OR_MUL: r = x * y; break;
+      case OR_DIV: r = x / y; break;
+      case OR_DIV_TRUNC: r = truncf(x / y); break;
+      default: r = div_floor_f32(x, y); break;
+    }
+    out[i] = r;
+  }
+}
+void or_binary_f64(int op, const double* a, const double* b, double* out, int64_t n, double alpha) {
+  for (int64_t i = 0; i < n; ++i) {
+    const double x = a[i], y = b[i];
+    double r;
+    switch (op) {
+      case OR_ADD: r = fma(alpha, y, x); break;
+      case OR_MUL: r = x * y; break;
+      case OR_DIV: r = x / y; break;
+      case OR_DIV_TRUNC: r = trunc(x / y); break;
+      default: r = div_floor_f64(x, y); break;
+    }
+    out[i] = r;
+  }
+}
+
+/* -------------------------------------------------------- activations -- */
+
+enum {
+  OR_GELU = 0, OR_GELU_TANH = 1, OR_SILU = 2, OR_SIGMOID = 3, OR_TANH = 4,
+  OR_EXP = 5, OR_LOG = 6, OR_ERF = 7, OR_RELU = 8, OR_NEG = 9
+};
+
+#define OR_SQRT1_2 0.70710678118654752440f
+#define OR_GELU_BETA_NONE 0.3989422804014327f /* M_2_SQRTPI * M_SQRT1_2 * 0.5 */
+#define OR_GELU_BETA_TANH 0.7978845608028654f /* M_SQRT2 * M_2_SQRTPI * 0.5  */
+#define OR_GELU_KAPPA 0.044715f
+
+/* Forward formulas (all in float32 opmath):
+ *  gelu 'none': x*0.5*(1+erf(x*sqrt(1/2)))            NF:5216, CPU Gelu.h:61-65
+ *  gelu 'tanh': 0.5*x*(1+tanh(b*(x+k*x^3))) rewritten exactly as
+ *               x / (1 + exp(-2*b*(x+k*x^3)))         NF:5216, CPU Gelu.h:34-41
+ *               (the identity 0.5*(1+tanh(u)) = 1/(1+exp(-2u)); it removes the
+ *               cancellation of 1+tanh(u) for u << 0)
+ *  silu:        x / (1 + exp(-x))                     NF:5374
+ *  sigmoid:     1 / (1 + exp(-x))                     NF:5441
+ *  tanh, exp, log, erf: the primitives of oracle_math.h. */
+static inline float act_fwd(int op, float x) {
+  switch (op) {
+    case OR_GELU: return (x * 0.5f) * (1.0f + or_erff(x * OR_SQRT1_2));
+    case OR_GELU_TANH: {
+      const float x3 = (x * x) * x;
+      const float inner = (-2.0f * OR_GELU_BETA_TANH) * fmaf(OR_GELU_KAPPA, x3, x);
+      return x / (1.0f + or_expf(inner));
+    }
+    case OR_SILU: return x / (1.0f + or_expf(-x));
+    case OR_SIGMOID: return 1.0f / (1.0f + or_expf(-x));
+    case OR_TANH: return or_tanhf(x);
+    case OR_EXP: return or_expf(x);
+    case OR_LOG: return or_logf(x);
+    case OR_ERF: return or_erff(x);
+    case OR_RELU: return (x != x) ? x : (x > 0.0f ? x : 0.0f);
+    default: return -x;
+  }
+}
+
+/* Backward formulas (upstream aten activation backward functors, float32):
+ *  gelu 'none': dy*(cdf + x*pdf), cdf = 0.5*(1+erf(x*sqrt(1/2))),
+ *               pdf = exp(-0.5*x*x) * (M_2_SQRTPI*M_SQRT1_2*0.5)     NF:5245
+ *  gelu 'tanh': dy*(0.5*(1+t) + 0.5*x*(1-t*t)*b*(1+3k*x^2)),
+ *               t = tanh(b*(x+k*x^3))                                NF:5245
+ *  silu:        s = 1/(1+exp(-x)); dy*s*(1+x*(1-s))                  NF:5383
+ *  sigmoid:     dy*(1-y)*y        (input is the forward output y)    NF:13229
+ *  tanh:        dy*(1-y*y)        (input is the forward output y) */
+static inline float act_bwd(int op, float dy, float x) {
+  switch (op) {
+    case OR_GELU: {
+      const float cdf = 0.5f * (1.0f + or_erff(x * OR_SQRT1_2));
+      const float pdf = or_expf((-0.5f * x) * x) * OR_GELU_BETA_NONE;
+      return dy * fmaf(x, pdf, cdf);
+    }
+    case OR_GELU_TANH: {
+      const float x2 = x * x;
+      const float x3 = x2 * x;
+      const float inner = OR_GELU_BETA_TANH * fmaf(OR_GELU_KAPPA, x3, x);
+      const float t = or_tanhf(inner);
+      const float left = 0.5f * x;
+      const float right = 1.0f + t;
+      const float left_d = 0.5f * right;
+      const float right_d = fmaf(-t, t, 1.0f);
+      const float inner_d = OR_GELU_BETA_TANH * fmaf(3.0f * OR_GELU_KAPPA, x2, 1.0f);
+      return dy * fmaf(left * right_d, inner_d, left_d);
+    }
+    case OR_SILU: {
+      const float s = 1.0f / (1.0f + or_expf(-x));
+      return (dy * s) * fmaf(x, 1.0f - s, 1.0f);
+    }
+    case OR_SIGMOID: return (dy * (1.0f - x)) * x;
+    case OR_TANH: return dy * fmaf(-x, x, 1.0f);
+    default: return dy;
+  }
+}
+
+void or_unary_f32(int op, const float* x, float* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = act_fwd(op, x[i]);
+}
+void or_unary_backward_f32(int op, const float* dy, const float* x, float* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = act_bwd(op, dy[i], x[i]);
+}
+
+/* ---------------------------------------------------------- log_softmax -- */
+
+/* _log_softmax over the last dim (NF:3752; upstream SoftMax.cu epilogue
+ * `input - max - log(sum(exp(input - max)))`).  max is exact; the sum is
+ * accumulated in double, log(sum) rounded to float, and the output formed in
+ * float as (x - max) - logsum, the order of the upstream epilogue. */
+void or_log_softmax_fwd(const float* x, float* out, int64_t rows, int64_t cols) {
+  for (int64_t r = 0; r < rows; ++r) {
+    const float* xr = x + r * cols;
+    float* o = out + r * cols;
+    float mx = -INFINITY;
+    for (int64_t c = 0; c < cols; ++c) mx = (xr[c] > mx || isnan(xr[c])) ? xr[c] : mx;
+    double s = 0.0;
+    for (int64_t c = 0; c < cols; ++c) s += exp((double)xr[c] - (double)mx);
+    const float logsum = (float)log(s);
+    for (int64_t c = 0; c < cols; ++c) o[c] = (xr[c] - mx) - logsum;
+  }
+}
+
+/* _log_softmax_backward_data (NF:3763): gI = gO - exp(out) * sum(gO) per row;
+ * sum in double, rounded to float; exp(out) exact in double then rounded. */
+void or_log_softmax_bwd(const float* g, const float* y, float* gin, int64_t rows, int64_t cols) {
+  for (int64_t r = 0; r < rows; ++r) {
+    const float* gr = g + r * cols;
+    const float* yr = y + r * cols;
+    double s = 0.0;
+    for (int64_t c = 0; c < cols; ++c) s += (double)gr[c];
+    const float sf = (float)s;
+    for (int64_t c = 0; c < cols; ++c) gin[r * cols + c] = gr[c] - (float)exp((double)yr[c]) * sf;
+  }
+}
+
+/* ------------------------------------------------------------- nll_loss -- */
+
+/* nll_loss_forward (NF:11928; reference semantics CrossEntropyLossKernel.cu:71-119
+ * for ignore handling): rows whose target == ignore_index contribute nothing
+ * and are not counted.  reduction 0 none / 1 mean / 2 sum.  For mean the
+ * result is -sum/total_weight (NaN when every row is ignored).  weight may be
+ * NULL.  Accumulation in double.  Returns 0, or -1 on an out-of-range target. */
+int or_nll_loss_fwd(const float* logp, const int64_t* target, const float* weight,
+                    int64_t n, int64_t c, int reduction, int64_t ignore_index,
+                    float* out, float* total_weight) {
+  double acc = 0.0, tw = 0.0;
+  for (int64_t i = 0; i < n; ++i) {
+    const int64_t t = target[i];
+    if (t == ignore_index) { if (reduction == 0) out[i] = 0.0f; continue; }
+    if (t < 0 || t >= c) return -1;
+    const float w = weight ? weight[t] : 1.0f;
+    const float v = -w * logp[i * c + t];
+    if (reduction == 0) out[i] = v;
+    acc += (double)v;
+    tw += (double)w;
+  }
+  if (reduction == 0) { *total_weight = 0.0f; return 0; }
+  *total_weight = (float)tw;
+  out[0] = reduction == 1 ? (float)(acc / tw) : (float)acc;
+  return 0;
+}
+
+/* nll_loss_backward (NF:11940): grad_input is zero except
+ * grad_input[i, t_i] = -w[t_i] * g_i (none) or -w[t_i] * g / total_weight
+ * (mean) or -w[t_i] * g (sum); ignored rows stay zero.  total_weight is the
+ * stored forward value, so a bf16 total_weight enters rounded, as upstream.
+ * bf16 != 0 applies the storage-type rounding of a bfloat16 run. */
+int or_nll_loss_bwd(const float* grad_out, const int64_t* target, const float* weight,
+                    int64_t n, int64_t c, int reduction, int64_t ignore_index,
+                    float total_weight, int bf16, float* grad_in) {
+  for (int64_t i = 0; i < n * c; ++i) grad_in[i] = 0.0f;
+  for (int64_t i = 0; i < n; ++i) {
+    const int64_t t = target[i];
+    if (t == ignore_index) continue;
+    if (t < 0 || t >= c) return -1;
+    const float w = weight ? weight[t] : 1.0f;
+    float g = reduction == 0 ? grad_out[i] : grad_out[0];
+    if (reduction == 1) g = g / total_weight;
+    /* upstream forms -(g/total_weight) in the storage type (scalar_t), so a
+     * bf16 run rounds it before the weight multiply */
+    if (bf16) g = bf16_to_f32(bf16_from_f32(g));
+    grad_in[i * c + t] = weight ? w * -g : -g;
+  }
+  return 0;
+}
+
+/* ------------------------------------------------------------- losses -- */
+
+enum { OR_MSE = 0, OR_SMOOTH_L1 = 1, OR_BCE_LOGITS = 2 };
+
+/* Pointwise loss terms (float32 opmath):
+ *  mse:        d = x - t; d*d                                   (NF:11832)
+ *  smooth_l1:  z = |x - t|; z < beta ? 0.5*z*z/beta : z - 0.5*beta   (NF:11988)
+ *  bce_logits: (1-t)*x + lw*(m + log(exp(-m) + exp(-x-m))),
+ *              m = max(-x, 0), lw = (pw-1)*t + 1
+ *              (BinaryCrossEntropyWithLogitsKernel.cu:17-35).  exp(-m) and
+ *              exp(-x-m) are 1 and exp(-|x|) in some order, so the sum is
+ *              1 + exp(-|x|) exactly as the reference forms it.  Without
+ *              pos_weight the reference's other variant applies:
+ *              (1-t)*x + m + log(...) (same file :17-23). */
+static inline float loss_term(int op, float x, float t, int has_pw, float pw, float beta) {
+  switch (op) {
+    case OR_MSE: { const float d = x - t; return d * d; }
+    case OR_SMOOTH_L1: {
+      const float z = fabsf(x - t);
+      return z < beta ? ((0.5f * z) * z) / beta : z - 0.5f * beta;
+    }
+    default: {
+      const float m = x < 0.0f ? -x : 0.0f;
+      const float lse = or_logf(1.0f + or_expf(-fabsf(x)));
+      if (!has_pw) return fmaf(1.0f - t, x, m) + lse;
+      const float lw = fmaf(pw - 1.0f, t, 1.0f);
+      return fmaf(1.0f - t, x, lw * (m + lse));
+    }
+  }
+}
+
+/* Loss forward.  pw (pos_weight, already broadcast to n elements) and w
+ * (weight) may be NULL.  reduction 0 none -> out[n]; 1 mean / 2 sum -> out[0],
+ * summed in double (the reference materialises the loss then calls
+ * loss.mean()/loss.sum(): BinaryCrossEntropyWithLogits.cpp:63-72). */
+void or_loss_fwd(int op, const float* x, const float* t, const float* pw, const float* w,
+                 int64_t n, int reduction, float beta, float* out) {
+  double acc = 0.0;
+  for (int64_t i = 0; i < n; ++i) {
+    float v = loss_term(op, x[i], t[i], pw != NULL, pw ? pw[i] : 1.0f, beta);
+    if (w) v = v * w[i];
+    if (reduction == 0) out[i] = v; else acc += (double)v;
+  }
+  if (reduction == 1) out[0] = (float)(acc / (double)n);
+  else if (reduction == 2) out[0] = (float)acc;
+}
+
+/* Loss backward (g is grad_output: n elements for 'none', 1 otherwise):
+ *  mse:        ((x - t) * norm) * g, norm = float(2/n) for mean else 2   (NF:11846)
+ *  smooth_l1:  d = x - t; d < -beta ? -norm*g : d > beta ? norm*g : norm*d*g/beta,
+ *              norm = float(1/n) for mean else 1                         (NF:12002)
+ *  bce_logits: the autograd formula's op sequence
+ *              (torchgen/packaged/autograd/derivatives.yaml:2017-2019):
+ *              u = pw*t; ((u + 1 - t) * sigmoid(x) - u) * g [* w] [/ n]. */
+void or_loss_bwd(int op, const float* g, const float* x, const float* t, const float* pw,
+                 const float* w, int64_t n, int reduction, float beta, float* gin) {
+  const float norm_mse = reduction == 1 ? (float)(2.0 / (double)n) : 2.0f;
+  const float norm_l1 = reduction == 1 ? (float)(1.0 / (double)n) : 1.0f;
+  for (int64_t i = 0; i < n; ++i) {
+    const float gi = reduction == 0 ? g[i] : g[0];
+    float r;
+    switch (op) {
+      case OR_MSE: r = ((x[i] - t[i]) * norm_mse) * gi; break;
+      case OR_SMOOTH_L1: {
+        const float d = x[i] - t[i];
+        r = d < -beta ? (-norm_l1) * gi : (d > beta ? norm_l1 * gi : ((norm_l1 * d) * gi) / beta);
+        break;
+      }
+      default: {
+        const float s = act_fwd(OR_SIGMOID, x[i]);
+        if (pw) {
+          const float u = pw[i] * t[i];
+          r = ((u + 1.0f) - t[i]) * s - u;
+        } else {
+          r = s - t[i];
+        }
+        r = r * gi;
+        if (w) r = r * w[i];
+        if (reduction == 1) r = r / (float)n;
+        break;
+      }
+    }
+    gin[i] = r;
+  }
+}
+
+/* ----------------------------------------------------------- reductions -- */
+
+/* sum / mean over all elements (ReduceSumKernel.cu:102-113,
+ * ReduceMomentKernel.cu:37-55): accumulate in double here. */
+double or_sum_f32(const float* x, int64_t n) {
+  double s = 0.0;
+  for (int64_t i = 0; i < n; ++i) s += (double)x[i];
+  return s;
+}
+
+/* ------------------------------------------------------------ optimizer -- */
+
+/* beta^step for the integral step counts the optimizer keeps (state_steps
+ * holds 1, 2, 3, ... as float): square-and-multiply in double; the device
+ * evaluates the same sequence. */
+static double pow_int_steps(double beta, float step) {
+  double r = 1.0, b = beta;
+  uint64_t k = (uint64_t)step;
+  if ((float)k != step) return pow(beta, (double)step);
+  while (k) { if (k & 1u) r *= b; b *= b; k >>= 1; }
+  return r;
+}
+
+/* One _fused_adamw_ step over one tensor (NF:16041), the order of operations
+ * of upstream adam_math in ADAMW mode
+ * (torch/include/ATen/native/cuda/fused_adam_utils.cuh:27-93, step and bias
+ * correction :130-137): hyper-parameters are double, state is float, and each
+ * mixed expression is evaluated in double and rounded once to float.  The
+ * double expressions are written with the fused multiply-adds the device
+ * compiler forms for them, so the float results match bit for bit. */
+void or_adamw_step(float* p, float* g, float* m, float* v, int64_t n, float step,
+                   double lr, double beta1, double beta2, double weight_decay, double eps,
+                   int maximize, const float* grad_scale, int amsgrad, float* vmax) {
+  const float bc1 = (float)(1.0 - pow_int_steps(beta1, step));
+  const float bc2_sqrt = (float)sqrt(1.0 - pow_int_steps(beta2, step));
+  const float step_size = (float)(lr / (double)bc1);
+  const double lr_wd = lr * weight_decay;
+  for (int64_t i = 0; i < n; ++i) {
+    float param = p[i];
+    float grad = g[i];
+    if (grad_scale) grad = (float)((double)grad / (double)(*grad_scale));
+    const float grad_to_store = grad;
+    if (maximize) grad = -grad;
+    float ea = m[i], eas = v[i];
+    if (weight_decay != 0.0) param = (float)fma(-lr_wd, (double)param, (double)param);
+    ea = (float)fma(beta1, (double)ea, (1.0 - beta1) * (double)grad);
+    eas = (float)fma(beta2, (double)eas, ((1.0 - beta2) * (double)grad) * (double)grad);
+    float denom;
+    if (amsgrad) {
+      const float mx = vmax[i] > eas ? vmax[i] : eas;
+      vmax[i] = mx;
+      denom = (float)((double)(sqrtf(mx) / bc2_sqrt) + eps);
+    } else {
+      denom = (float)((double)(sqrtf(eas) / bc2_sqrt) + eps);
+    }
+    param = param - (step_size * ea) / denom;
+    p[i] = param;
+    if (grad_scale) g[i] = grad_to_store;
+    m[i] = ea;
+    v[i] = eas;
+  }
+}

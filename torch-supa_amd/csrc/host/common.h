@@ -1,0 +1,66 @@
+// Shared declarations of the host layer (PrivateUse1 runtime + operator
+// registrations).  The host layer owns tensors, allocation and the dispatcher
+// contract; every device computation goes through the C ABI in supa_amd.h.
+#pragma once
+
+#include <ATen/ATen.h>
+#include <c10/core/Device.h>
+#include <hip/hip_runtime_api.h>
+
+#include <string>
+
+#include "supa_amd.h"
+
+namespace supa {
+
+constexpr c10::DeviceType kSupa = c10::DeviceType::PrivateUse1;
+
+#define SUPA_HIP_CHECK(expr)                                                              \
+  do {                                                                                    \
+    const hipError_t err__ = (expr);                                                      \
+    TORCH_CHECK(err__ == hipSuccess, "HIP error ", hipGetErrorName(err__), ": ",        \
+                hipGetErrorString(err__), " at ", __FILE__, ":", __LINE__);               \
+  } while (0)
+
+// Turns a non-zero C-ABI status into a c10::Error naming the op.
+void check_status(int status, const char* what);
+
+// ------------------------------------------------------------- runtime
+c10::DeviceIndex device_count() noexcept;
+c10::DeviceIndex current_device();
+void set_device(c10::DeviceIndex d);
+// The stream kernels are enqueued on for device d (the legacy default stream).
+hipStream_t current_stream(c10::DeviceIndex d);
+void synchronize(c10::DeviceIndex d);
+c10::Allocator* allocator();
+
+struct AllocatorStats {
+  int64_t allocated = 0;
+  int64_t reserved = 0;
+  int64_t peak_allocated = 0;
+  int64_t num_allocs = 0;
+  int64_t num_device_mallocs = 0;
+  int64_t num_frees = 0;
+};
+AllocatorStats allocator_stats(c10::DeviceIndex d);
+void allocator_reset_peak(c10::DeviceIndex d);
+void allocator_empty_cache();
+
+// CPU fallback bookkeeping (the fallback never runs for an op this library
+// registers; tests assert that with these counters).
+void set_cpu_fallback_enabled(bool on);
+bool cpu_fallback_enabled();
+std::vector<std::pair<std::string, int64_t>> fallback_counts();
+void reset_fallback_counts();
+
+// ------------------------------------------------------------ helpers
+inline int32_t dtype_code(c10::ScalarType t) { return static_cast<int32_t>(t); }
+bool dtype_supported(c10::ScalarType t);
+
+// An empty tensor on the supa device with explicit strides.
+at::Tensor empty_strided_supa(c10::IntArrayRef size, c10::IntArrayRef stride, c10::ScalarType dtype,
+                              c10::DeviceIndex device);
+at::Tensor empty_supa(c10::IntArrayRef size, c10::ScalarType dtype, c10::DeviceIndex device,
+                      c10::MemoryFormat fmt = c10::MemoryFormat::Contiguous);
+
+}  // namespace supa

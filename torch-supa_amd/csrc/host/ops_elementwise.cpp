@@ -1,0 +1,627 @@
+// PrivateUse1 registrations of the tensor plumbing (factories, views, copies,
+// fill) and of the elementwise operators: add/sub/rsub, mul, div (all rounding
+// modes), the activation family and its gradients.
+//
+// Registration surface: TORCH_LIBRARY_IMPL(aten, PrivateUse1, m), the same
+// one the reference's generated RegisterSUPANative*.cpp use
+// (script/codegen_native/gen.py:106-195, :553-585), with the functional,
+// in-place and out= overload of each op registered by hand.  The kernels these
+// ops end in replace add_stub (UfuncCUDA_add.cu:341-345), mul_stub
+// (BinaryMulKernel.cu:43), div_*_stub (BinaryDiv{True,Trunc,Floor}Kernel.cu)
+// and the upstream activation kernels the reference takes from its operator
+// library.
+#include <ATen/EmptyTensor.h>
+#include <ATen/ExpandUtils.h>
+#include <ATen/MemoryOverlap.h>
+#include <ATen/native/Resize.h>
+#include <ATen/ops/as_strided_native.h>
+#include <ATen/ops/view_native.h>
+#include <ATen/ops/_reshape_alias_native.h>
+#include <c10/core/ScalarType.h>
+#include <torch/library.h>
+
+#include <stdexcept>
+
+#include "common.h"
+#include "ew_apply.h"
+
+namespace supa {
+
+// ------------------------------------------------------------ ew_apply
+EwIn EwIn::of(const at::Tensor& x) {
+  EwIn e;
+  if (x.device().is_cpu() && x.dim() == 0) {
+    e.scalar = true;
+    e.value = x.item();
+  } else {
+    e.t = x;
+  }
+  return e;
+}
+
+c10::DeviceIndex common_device(const std::vector<const at::Tensor*>& ts, const char* name) {
+  c10::DeviceIndex dev = -1;
+  for (const at::Tensor* t : ts) {
+    if (!t || !t->defined()) continue;
+    if (t->device().type() == kSupa) {
+      const auto d = t->device().index();
+      TORCH_CHECK(dev < 0 || dev == d, name, ": expected all tensors on the same supa device, got supa:", int(dev),
+                  " and supa:", int(d));
+      dev = d;
+    } else {
+      TORCH_CHECK(t->device().is_cpu() && t->dim() == 0, name,
+                  ": expected all tensors to be on the same device, but found a ", t->device(), " tensor");
+    }
+  }
+  return dev < 0 ? current_device() : dev;
+}
+
+at::Tensor ew_apply(at::Tensor out, c10::ScalarType out_dtype, c10::ScalarType common_dtype,
+                    const std::vector<EwIn>& ins, const EwLaunch& launch, const char* name) {
+  TORCH_CHECK(dtype_supported(common_dtype), name, ": dtype ", common_dtype, " is not supported on supa");
+  std::vector<const at::Tensor*> ts;
+  if (out.defined()) ts.push_back(&out);
+  for (const EwIn& e : ins)
+    if (!e.scalar) ts.push_back(&e.t);
+  const c10::DeviceIndex dev = common_device(ts, name);
+  for (const EwIn& e : ins)
+    if (!e.scalar) TORCH_CHECK(dtype_supported(e.t.scalar_type()), name, ": dtype ", e.t.scalar_type(), " is not supported on supa");
+
+  std::vector<PlanOperand> pops(1 + ins.size());
+  for (size_t i = 0; i < ins.size(); ++i) {
+    PlanOperand& p = pops[1 + i];
+    if (ins[i].scalar) {
+      p.scalar = true;
+    } else {
+      p.sizes = ins[i].t.sizes().vec();
+      p.strides = ins[i].t.strides().vec();
+    }
+  }
+  pops[0].is_output = true;
+  std::vector<int64_t> shape;
+  try {
+    if (out.defined()) {
+      pops[0].sizes = out.sizes().vec();
+      pops[0].strides = out.strides().vec();
+    }
+    shape = broadcast_shape(pops);
+  } catch (const std::invalid_argument& e) {
+    TORCH_CHECK(false, name, ": ", e.what());
+  }
+  if (out.defined()) {
+    TORCH_CHECK(dtype_supported(out.scalar_type()), name, ": output dtype ", out.scalar_type(), " is not supported on supa");
+    if (out.sizes().vec() != shape) {
+      at::native::resize_output(out, shape);
+    }
+    pops[0].sizes = out.sizes().vec();
+    pops[0].strides = out.strides().vec();
+  } else {
+    pops[0].allocate = true;
+  }
+  Plan plan;
+  try {
+    plan = make_plan(pops);
+  } catch (const std::invalid_argument& e) {
+    TORCH_CHECK(false, name, ": ", e.what());
+  }
+  if (!out.defined()) {
+    out = empty_strided_supa(plan.shape, plan.out_strides[0], out_dtype, dev);
+  } else {
+    at::assert_no_internal_overlap(out);
+    for (const EwIn& e : ins)
+      if (!e.scalar) at::assert_no_partial_overlap(out, e.t);
+  }
+  if (plan.numel == 0) return out;
+  TORCH_CHECK((int)plan.it_sizes.size() <= SUPA_AMD_MAX_DIMS, name, ": more than ", SUPA_AMD_MAX_DIMS,
+              " non-coalescable dimensions");
+  TORCH_CHECK((int)(1 + ins.size()) <= SUPA_AMD_MAX_OPERANDS, name, ": too many operands");
+
+  supa_amd_ew_desc d{};
+  d.ndim = (int32_t)plan.it_sizes.size();
+  d.noperands = (int32_t)(1 + ins.size());
+  d.common_dtype = dtype_code(common_dtype);
+  for (int i = 0; i < d.ndim; ++i) d.sizes[i] = plan.it_sizes[i];
+  for (int k = 0; k < d.noperands; ++k) {
+    supa_amd_operand& o = d.op[k];
+    if (k > 0 && ins[k - 1].scalar) {
+      const c10::Scalar& v = ins[k - 1].value;
+      TORCH_CHECK(!v.isComplex(), name, ": complex scalars are not supported on supa");
+      o.is_scalar = 1;
+      o.dtype = dtype_code(common_dtype);
+      if (v.isBoolean()) {
+        o.scalar = v.toBool() ? 1.0 : 0.0;
+        o.iscalar = v.toBool() ? 1 : 0;
+      } else if (v.isIntegral(false)) {
+        o.iscalar = v.toLong();
+        o.scalar = static_cast<double>(o.iscalar);
+      } else {
+        o.scalar = v.toDouble();
+        o.iscalar = static_cast<int64_t>(o.scalar);
+      }
+      continue;
+    }
+    const at::Tensor& t = k == 0 ? out : ins[k - 1].t;
+    o.data = t.data_ptr();
+    o.dtype = dtype_code(t.scalar_type());
+    for (int i = 0; i < d.ndim; ++i) o.strides[i] = plan.it_strides[k][i];
+  }
+  const auto prev = current_device();
+  if (prev != dev) set_device(dev);
+  const int rc = launch(&d, current_stream(dev));
+  if (prev != dev) set_device(prev);
+  check_status(rc, name);
+  return out;
+}
+
+namespace {
+
+// -------------------------------------------------------------- helpers
+c10::ScalarType default_float() { return c10::typeMetaToScalarType(c10::get_default_dtype()); }
+
+void check_cast(c10::ScalarType common, const at::Tensor& out, const char* name) {
+  TORCH_CHECK(c10::canCast(common, out.scalar_type()), name, ": result type ", common,
+              " can't be cast to the desired output type ", out.scalar_type());
+}
+
+// ----------------------------------------------------- factories / views
+at::Tensor empty_memory_format(c10::IntArrayRef size, std::optional<c10::ScalarType> dtype,
+                               std::optional<c10::Layout> layout, std::optional<c10::Device> device,
+                               std::optional<bool> pin_memory, std::optional<c10::MemoryFormat> fmt) {
+  TORCH_CHECK(!layout || *layout == c10::Layout::Strided, "supa: only strided tensors are supported");
+  TORCH_CHECK(!pin_memory || !*pin_memory, "supa: pin_memory applies to CPU tensors only");
+  const auto dt = dtype.value_or(default_float());
+  const c10::DeviceIndex dev = device && device->has_index() ? device->index() : current_device();
+  return empty_supa(size, dt, dev, fmt.value_or(c10::MemoryFormat::Contiguous));
+}
+
+at::Tensor empty_strided(c10::IntArrayRef size, c10::IntArrayRef stride, std::optional<c10::ScalarType> dtype,
+                         std::optional<c10::Layout> layout, std::optional<c10::Device> device,
+                         std::optional<bool> pin_memory) {
+  TORCH_CHECK(!layout || *layout == c10::Layout::Strided, "supa: only strided tensors are supported");
+  const auto dt = dtype.value_or(default_float());
+  const c10::DeviceIndex dev = device && device->has_index() ? device->index() : current_device();
+  return empty_strided_supa(size, stride, dt, dev);
+}
+
+const at::Tensor& resize_(const at::Tensor& self, c10::IntArrayRef size, std::optional<c10::MemoryFormat> fmt) {
+  c10::TensorImpl* impl = self.unsafeGetTensorImpl();
+  if (self.sizes() == size && !fmt) return self;
+  const int64_t old_numel = self.numel();
+  (void)old_numel;
+  impl->set_sizes_contiguous(size);
+  const size_t needed =
+      at::detail::computeStorageNbytesContiguous(size, self.dtype().itemsize(), impl->storage_offset());
+  const c10::Storage& storage = impl->unsafe_storage();
+  if (needed > storage.nbytes()) {
+    TORCH_CHECK(storage.resizable(), "supa: trying to resize storage that is not resizable");
+    at::detail::getPrivateUse1Hooks().resizePrivateUse1Bytes(storage, needed);
+  }
+  if (fmt) impl->empty_tensor_restride(*fmt);
+  return self;
+}
+
+// Copies between the supa device and the host, and within the device.
+at::Tensor copy_from(const at::Tensor& self, const at::Tensor& dst, bool /*non_blocking*/) {
+  TORCH_CHECK(self.defined() && dst.defined(), "supa copy: undefined tensor");
+  if (dst.numel() == 0) return dst;
+  const bool src_dev = self.device().type() == kSupa;
+  const bool dst_dev = dst.device().type() == kSupa;
+  if (src_dev && dst_dev) {
+    TORCH_CHECK(self.device() == dst.device(), "supa copy across devices is not supported");
+    if (self.scalar_type() == dst.scalar_type() && self.sizes() == dst.sizes() && self.strides() == dst.strides() &&
+        self.is_non_overlapping_and_dense()) {
+      if (self.data_ptr() != dst.data_ptr())
+        SUPA_HIP_CHECK(hipMemcpyAsync(dst.data_ptr(), self.data_ptr(), dst.nbytes(), hipMemcpyDeviceToDevice,
+                                      current_stream(dst.device().index())));
+      return dst;
+    }
+    TORCH_CHECK(dtype_supported(self.scalar_type()) && dtype_supported(dst.scalar_type()),
+                "supa copy: unsupported dtype");
+    at::Tensor src = self;
+    if (at::has_internal_overlap(dst) == at::MemOverlap::Yes) TORCH_CHECK(false, "supa copy: destination overlaps itself");
+    if (at::get_overlap_status(self, dst) == at::MemOverlapStatus::Partial) src = self.clone();
+    EwIn in;
+    in.t = src.expand(dst.sizes());
+    ew_apply(dst, dst.scalar_type(), src.scalar_type(), {in},
+             [](const supa_amd_ew_desc* d, void* s) { return supa_amd_copy(d, s); }, "copy_");
+    return dst;
+  }
+  if (dst_dev) {  // host -> device
+    TORCH_CHECK(self.device().is_cpu(), "supa copy: unsupported source device ", self.device());
+    if (dst.is_contiguous()) {
+      at::Tensor h = self.to(dst.scalar_type()).expand(dst.sizes()).contiguous();
+      SUPA_HIP_CHECK(hipMemcpy(dst.data_ptr(), h.data_ptr(), dst.nbytes(), hipMemcpyHostToDevice));
+    } else {
+      at::Tensor tmp = empty_supa(dst.sizes(), dst.scalar_type(), dst.device().index());
+      copy_from(self, tmp, false);
+      copy_from(tmp, dst, false);
+    }
+    return dst;
+  }
+  // device -> host
+  TORCH_CHECK(dst.device().is_cpu(), "supa copy: unsupported destination device ", dst.device());
+  at::Tensor src = self;
+  if (!src.is_contiguous()) {
+    at::Tensor tmp = empty_supa(src.sizes(), src.scalar_type(), src.device().index());
+    copy_from(src, tmp, false);
+    src = tmp;
+  }
+  if (dst.is_contiguous() && dst.scalar_type() == src.scalar_type() && dst.sizes() == src.sizes()) {
+    SUPA_HIP_CHECK(hipMemcpy(dst.data_ptr(), src.data_ptr(), dst.nbytes(), hipMemcpyDeviceToHost));
+  } else {
+    at::Tensor h = at::empty(src.sizes(), src.options().device(at::kCPU));
+    SUPA_HIP_CHECK(hipMemcpy(h.data_ptr(), src.data_ptr(), h.nbytes(), hipMemcpyDeviceToHost));
+    dst.copy_(h);
+  }
+  return dst;
+}
+
+at::Tensor copy_from_and_resize(const at::Tensor& self, const at::Tensor& dst) {
+  if (dst.sizes() != self.sizes()) {
+    if (dst.device().type() == kSupa) resize_(dst, self.sizes(), std::nullopt);
+    else dst.resize_(self.sizes());
+  }
+  return copy_from(self, dst, false);
+}
+
+c10::Scalar local_scalar_dense(const at::Tensor& self) {
+  TORCH_CHECK(self.numel() == 1, "a Tensor with ", self.numel(), " elements cannot be converted to Scalar");
+  at::Tensor h = at::empty({}, self.options().device(at::kCPU));
+  SUPA_HIP_CHECK(hipMemcpy(h.data_ptr(), self.data_ptr(), self.dtype().itemsize(), hipMemcpyDeviceToHost));
+  return h.item();
+}
+
+at::Tensor& fill_scalar(at::Tensor& self, const c10::Scalar& value) {
+  ew_apply(self, self.scalar_type(), self.scalar_type(), {EwIn::num(value)},
+           [](const supa_amd_ew_desc* d, void* s) { return supa_amd_fill(d, s); }, "fill_");
+  return self;
+}
+
+at::Tensor& fill_tensor(at::Tensor& self, const at::Tensor& value) {
+  TORCH_CHECK(value.dim() == 0, "fill_ only supports 0-dimension value tensor but got tensor with ", value.dim(),
+              " dimensions.");
+  if (value.device().type() == kSupa) {
+    EwIn in;
+    in.t = value.expand(self.sizes());
+    ew_apply(self, self.scalar_type(), value.scalar_type(), {in},
+             [](const supa_amd_ew_desc* d, void* s) { return supa_amd_copy(d, s); }, "fill_");
+    return self;
+  }
+  return fill_scalar(self, value.item());
+}
+
+at::Tensor& zero_(at::Tensor& self) { return fill_scalar(self, 0); }
+
+at::Tensor& set_source_storage_offset(at::Tensor& self, c10::Storage source, int64_t offset, c10::IntArrayRef size,
+                                      c10::IntArrayRef stride) {
+  c10::TensorImpl* impl = self.unsafeGetTensorImpl();
+  impl->set_storage_keep_dtype(std::move(source));
+  impl->set_storage_offset(offset);
+  impl->set_sizes_and_strides(size, stride);
+  return self;
+}
+
+at::Tensor& set_source_storage(at::Tensor& self, c10::Storage source) {
+  const int64_t n = (int64_t)(source.nbytes() / self.dtype().itemsize());
+  return set_source_storage_offset(self, std::move(source), 0, {n}, {1});
+}
+
+at::Tensor& set_source_tensor(at::Tensor& self, const at::Tensor& src) {
+  return set_source_storage_offset(self, src.storage(), src.storage_offset(), src.sizes(), src.strides());
+}
+
+at::Tensor& set_empty(at::Tensor& self) {
+  c10::Storage st(c10::Storage::use_byte_size_t(), 0, allocator(), true);
+  return set_source_storage_offset(self, st, 0, {0}, {1});
+}
+
+// ------------------------------------------------------------ binary ops
+using Launch = EwLaunch;
+
+Launch add_launch(const c10::Scalar& alpha, bool negate = false) {
+  double a = 0.0;
+  int64_t ia = 0;
+  if (alpha.isBoolean()) {
+    a = alpha.toBool() ? 1.0 : 0.0;
+    ia = alpha.toBool() ? 1 : 0;
+  } else if (alpha.isIntegral(false)) {
+    ia = alpha.toLong();
+    a = (double)ia;
+  } else {
+    a = alpha.toDouble();
+    ia = (int64_t)a;
+  }
+  if (negate) {
+    a = -a;
+    ia = -ia;
+  }
+  return [a, ia](const supa_amd_ew_desc* d, void* s) { return supa_amd_add(d, a, ia, s); };
+}
+
+void check_alpha(c10::ScalarType common, const c10::Scalar& alpha) {
+  TORCH_CHECK(!alpha.isBoolean() || common == at::kBool,
+              "Boolean alpha only supported for Boolean results.");
+  TORCH_CHECK(at::isFloatingType(common) || alpha.isIntegral(true),
+              "For integral input tensors, argument alpha must not be a floating point number.");
+}
+
+at::Tensor binary(const at::Tensor& self, const at::Tensor& other, at::Tensor out, bool inplace,
+                  const Launch& fn, const char* name, bool int_to_float = false, bool swap = false,
+                  const c10::Scalar* alpha = nullptr) {
+  c10::ScalarType common = at::result_type(self, other);
+  if (int_to_float && at::isIntegralType(common, /*includeBool=*/true)) common = default_float();
+  if (alpha) check_alpha(common, *alpha);
+  std::vector<EwIn> ins = swap ? std::vector<EwIn>{EwIn::of(other), EwIn::of(self)}
+                               : std::vector<EwIn>{EwIn::of(self), EwIn::of(other)};
+  if (inplace) {
+    check_cast(common, self, name);
+    return ew_apply(self, self.scalar_type(), common, ins, fn, name);
+  }
+  if (out.defined()) {
+    check_cast(common, out, name);
+    return ew_apply(out, out.scalar_type(), common, ins, fn, name);
+  }
+  return ew_apply(at::Tensor(), common, common, ins, fn, name);
+}
+
+at::Tensor add_t(const at::Tensor& s, const at::Tensor& o, const c10::Scalar& a) {
+  return binary(s, o, {}, false, add_launch(a), "add", false, false, &a);
+}
+at::Tensor& add_t_(at::Tensor& s, const at::Tensor& o, const c10::Scalar& a) {
+  binary(s, o, {}, true, add_launch(a), "add_", false, false, &a);
+  return s;
+}
+at::Tensor& add_out(const at::Tensor& s, const at::Tensor& o, const c10::Scalar& a, at::Tensor& out) {
+  binary(s, o, out, false, add_launch(a), "add.out", false, false, &a);
+  return out;
+}
+void check_sub(const at::Tensor& s, const at::Tensor& o) {
+  TORCH_CHECK(s.scalar_type() != at::kBool || o.scalar_type() != at::kBool,
+              "Subtraction, the `-` operator, with two bool tensors is not supported. Use the `^` or `logical_xor()` "
+              "operator instead.");
+}
+at::Tensor sub_t(const at::Tensor& s, const at::Tensor& o, const c10::Scalar& a) {
+  check_sub(s, o);
+  return binary(s, o, {}, false, add_launch(a, true), "sub", false, false, &a);
+}
+at::Tensor& sub_t_(at::Tensor& s, const at::Tensor& o, const c10::Scalar& a) {
+  check_sub(s, o);
+  binary(s, o, {}, true, add_launch(a, true), "sub_", false, false, &a);
+  return s;
+}
+at::Tensor& sub_out(const at::Tensor& s, const at::Tensor& o, const c10::Scalar& a, at::Tensor& out) {
+  check_sub(s, o);
+  binary(s, o, out, false, add_launch(a, true), "sub.out", false, false, &a);
+  return out;
+}
+// rsub(self, other, alpha) = other - alpha * self
+at::Tensor rsub_t(const at::Tensor& s, const at::Tensor& o, const c10::Scalar& a) {
+  check_sub(s, o);
+  return binary(s, o, {}, false, add_launch(a, true), "rsub", false, true, &a);
+}
+
+Launch mul_launch() {
+  return [](const supa_amd_ew_desc* d, void* s) { return supa_amd_mul(d, s); };
+}
+at::Tensor mul_t(const at::Tensor& s, const at::Tensor& o) { return binary(s, o, {}, false, mul_launch(), "mul"); }
+at::Tensor& mul_t_(at::Tensor& s, const at::Tensor& o) {
+  binary(s, o, {}, true, mul_launch(), "mul_");
+  return s;
+}
+at::Tensor& mul_out(const at::Tensor& s, const at::Tensor& o, at::Tensor& out) {
+  binary(s, o, out, false, mul_launch(), "mul.out");
+  return out;
+}
+
+int div_mode(std::optional<c10::string_view> mode) {
+  if (!mode) return SUPA_AMD_DIV_TRUE;
+  if (*mode == "trunc") return SUPA_AMD_DIV_TRUNC;
+  if (*mode == "floor") return SUPA_AMD_DIV_FLOOR;
+  TORCH_CHECK(false, "div expected rounding_mode to be one of None, 'trunc', or 'floor' but found '", *mode, "'");
+}
+Launch div_launch(int mode) {
+  return [mode](const supa_amd_ew_desc* d, void* s) { return supa_amd_div(d, mode, s); };
+}
+at::Tensor div_tensor(const at::Tensor& s, const at::Tensor& o) {
+  return binary(s, o, {}, false, div_launch(SUPA_AMD_DIV_TRUE), "div", true);
+}
+at::Tensor& div_tensor_(at::Tensor& s, const at::Tensor& o) {
+  binary(s, o, {}, true, div_launch(SUPA_AMD_DIV_TRUE), "div_", true);
+  return s;
+}
+at::Tensor& div_out(const at::Tensor& s, const at::Tensor& o, at::Tensor& out) {
+  binary(s, o, out, false, div_launch(SUPA_AMD_DIV_TRUE), "div.out", true);
+  return out;
+}
+at::Tensor div_tm(const at::Tensor& s, const at::Tensor& o, std::optional<c10::string_view> mode) {
+  const int m = div_mode(mode);
+  return binary(s, o, {}, false, div_launch(m), "div", m == SUPA_AMD_DIV_TRUE);
+}
+at::Tensor& div_tm_(at::Tensor& s, const at::Tensor& o, std::optional<c10::string_view> mode) {
+  const int m = div_mode(mode);
+  binary(s, o, {}, true, div_launch(m), "div_", m == SUPA_AMD_DIV_TRUE);
+  return s;
+}
+at::Tensor& div_out_mode(const at::Tensor& s, const at::Tensor& o, std::optional<c10::string_view> mode,
+                         at::Tensor& out) {
+  const int m = div_mode(mode);
+  binary(s, o, out, false, div_launch(m), "div.out_mode", m == SUPA_AMD_DIV_TRUE);
+  return out;
+}
+
+// ---------------------------------------------------------- activations
+enum class UKind { FloatOnly, IntToFloat, Any };
+
+at::Tensor unary(const at::Tensor& self, at::Tensor out, bool inplace, int op, UKind kind, const char* name) {
+  c10::ScalarType common = self.scalar_type();
+  if (kind == UKind::FloatOnly) {
+    TORCH_CHECK(at::isFloatingType(common), name, ": \"", name, "\" not implemented for '", common, "'");
+  } else if (kind == UKind::IntToFloat && at::isIntegralType(common, true)) {
+    common = default_float();
+  }
+  const Launch fn = [op](const supa_amd_ew_desc* d, void* s) { return supa_amd_unary(d, op, s); };
+  std::vector<EwIn> ins{EwIn::of(self)};
+  if (inplace) {
+    check_cast(common, self, name);
+    return ew_apply(self, self.scalar_type(), common, ins, fn, name);
+  }
+  if (out.defined()) {
+    check_cast(common, out, name);
+    return ew_apply(out, out.scalar_type(), common, ins, fn, name);
+  }
+  return ew_apply(at::Tensor(), common, common, ins, fn, name);
+}
+
+at::Tensor unary_bwd(const at::Tensor& grad, const at::Tensor& x, at::Tensor out, int op, const char* name) {
+  const c10::ScalarType common = at::result_type(grad, x);
+  TORCH_CHECK(at::isFloatingType(common), name, ": not implemented for '", common, "'");
+  const Launch fn = [op](const supa_amd_ew_desc* d, void* s) { return supa_amd_unary_backward(d, op, s); };
+  std::vector<EwIn> ins{EwIn::of(grad), EwIn::of(x)};
+  if (out.defined()) {
+    check_cast(common, out, name);
+    return ew_apply(out, out.scalar_type(), common, ins, fn, name);
+  }
+  return ew_apply(at::Tensor(), common, common, ins, fn, name);
+}
+
+int gelu_op(c10::string_view approximate) {
+  if (approximate == "none") return SUPA_AMD_GELU;
+  if (approximate == "tanh") return SUPA_AMD_GELU_TANH;
+  TORCH_CHECK(false, "approximate argument must be either none or tanh.");
+}
+
+at::Tensor gelu(const at::Tensor& s, c10::string_view a) { return unary(s, {}, false, gelu_op(a), UKind::FloatOnly, "gelu"); }
+at::Tensor& gelu_(at::Tensor& s, c10::string_view a) {
+  unary(s, {}, true, gelu_op(a), UKind::FloatOnly, "gelu_");
+  return s;
+}
+at::Tensor& gelu_out(const at::Tensor& s, c10::string_view a, at::Tensor& out) {
+  unary(s, out, false, gelu_op(a), UKind::FloatOnly, "gelu.out");
+  return out;
+}
+at::Tensor gelu_backward(const at::Tensor& g, const at::Tensor& s, c10::string_view a) {
+  return unary_bwd(g, s, {}, gelu_op(a), "gelu_backward");
+}
+at::Tensor& gelu_backward_out(const at::Tensor& g, const at::Tensor& s, c10::string_view a, at::Tensor& gi) {
+  unary_bwd(g, s, gi, gelu_op(a), "gelu_backward.grad_input");
+  return gi;
+}
+
+#define SUPA_UNARY(NAME, OP, KIND)                                                        \
+  at::Tensor u_##NAME(const at::Tensor& s) { return unary(s, {}, false, OP, KIND, #NAME); } \
+  at::Tensor& u_##NAME##_(at::Tensor& s) {                                                \
+    unary(s, {}, true, OP, KIND, #NAME "_");                                              \
+    return s;                                                                             \
+  }                                                                                       \
+  at::Tensor& u_##NAME##_out(const at::Tensor& s, at::Tensor& out) {                      \
+    unary(s, out, false, OP, KIND, #NAME ".out");                                         \
+    return out;                                                                           \
+  }
+
+SUPA_UNARY(silu, SUPA_AMD_SILU, UKind::FloatOnly)
+SUPA_UNARY(sigmoid, SUPA_AMD_SIGMOID, UKind::IntToFloat)
+SUPA_UNARY(tanh, SUPA_AMD_TANH, UKind::IntToFloat)
+SUPA_UNARY(exp, SUPA_AMD_EXP, UKind::IntToFloat)
+SUPA_UNARY(log, SUPA_AMD_LOG, UKind::IntToFloat)
+SUPA_UNARY(erf, SUPA_AMD_ERF, UKind::IntToFloat)
+SUPA_UNARY(neg, SUPA_AMD_NEG, UKind::Any)
+#undef SUPA_UNARY
+
+at::Tensor relu(const at::Tensor& s) {
+  TORCH_CHECK(s.scalar_type() != at::kBool, "Boolean inputs not supported for relu");
+  return unary(s, {}, false, SUPA_AMD_RELU, UKind::Any, "relu");
+}
+at::Tensor& relu_(at::Tensor& s) {
+  TORCH_CHECK(s.scalar_type() != at::kBool, "Boolean inputs not supported for relu");
+  unary(s, {}, true, SUPA_AMD_RELU, UKind::Any, "relu_");
+  return s;
+}
+
+#define SUPA_UNARY_BWD(NAME, OP)                                                             \
+  at::Tensor NAME##_backward(const at::Tensor& g, const at::Tensor& x) {                     \
+    return unary_bwd(g, x, {}, OP, #NAME "_backward");                                       \
+  }                                                                                          \
+  at::Tensor& NAME##_backward_out(const at::Tensor& g, const at::Tensor& x, at::Tensor& gi) { \
+    unary_bwd(g, x, gi, OP, #NAME "_backward.grad_input");                                   \
+    return gi;                                                                               \
+  }
+SUPA_UNARY_BWD(silu, SUPA_AMD_SILU)
+SUPA_UNARY_BWD(sigmoid, SUPA_AMD_SIGMOID)
+SUPA_UNARY_BWD(tanh, SUPA_AMD_TANH)
+#undef SUPA_UNARY_BWD
+
+}  // namespace
+}  // namespace supa
+
+TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
+  using namespace supa;
+  // tensor plumbing
+  m.impl("empty.memory_format", TORCH_FN(empty_memory_format));
+  m.impl("empty_strided", TORCH_FN(empty_strided));
+  m.impl("as_strided", TORCH_FN(at::native::as_strided_tensorimpl));
+  m.impl("view", TORCH_FN(at::native::view));
+  m.impl("_reshape_alias", TORCH_FN(at::native::_reshape_alias));
+  m.impl("resize_", TORCH_FN(resize_));
+  m.impl("_copy_from", TORCH_FN(copy_from));
+  m.impl("_copy_from_and_resize", TORCH_FN(copy_from_and_resize));
+  m.impl("_local_scalar_dense", TORCH_FN(local_scalar_dense));
+  m.impl("fill_.Scalar", TORCH_FN(fill_scalar));
+  m.impl("fill_.Tensor", TORCH_FN(fill_tensor));
+  m.impl("zero_", TORCH_FN(zero_));
+  m.impl("set_.source_Storage", TORCH_FN(set_source_storage));
+  m.impl("set_.source_Storage_storage_offset", TORCH_FN(set_source_storage_offset));
+  m.impl("set_.source_Tensor", TORCH_FN(set_source_tensor));
+  m.impl("set_", TORCH_FN(set_empty));
+  // binary
+  m.impl("add.Tensor", TORCH_FN(add_t));
+  m.impl("add_.Tensor", TORCH_FN(add_t_));
+  m.impl("add.out", TORCH_FN(add_out));
+  m.impl("sub.Tensor", TORCH_FN(sub_t));
+  m.impl("sub_.Tensor", TORCH_FN(sub_t_));
+  m.impl("sub.out", TORCH_FN(sub_out));
+  m.impl("rsub.Tensor", TORCH_FN(rsub_t));
+  m.impl("mul.Tensor", TORCH_FN(mul_t));
+  m.impl("mul_.Tensor", TORCH_FN(mul_t_));
+  m.impl("mul.out", TORCH_FN(mul_out));
+  m.impl("div.Tensor", TORCH_FN(div_tensor));
+  m.impl("div_.Tensor", TORCH_FN(div_tensor_));
+  m.impl("div.out", TORCH_FN(div_out));
+  m.impl("div.Tensor_mode", TORCH_FN(div_tm));
+  m.impl("div_.Tensor_mode", TORCH_FN(div_tm_));
+  m.impl("div.out_mode", TORCH_FN(div_out_mode));
+  // activations
+  m.impl("gelu", TORCH_FN(gelu));
+  m.impl("gelu_", TORCH_FN(gelu_));
+  m.impl("gelu.out", TORCH_FN(gelu_out));
+  m.impl("gelu_backward", TORCH_FN(gelu_backward));
+  m.impl("gelu_backward.grad_input", TORCH_FN(gelu_backward_out));
+  m.impl("silu", TORCH_FN(u_silu));
+  m.impl("silu_", TORCH_FN(u_silu_));
+  m.impl("silu.out", TORCH_FN(u_silu_out));
+  m.impl("silu_backward", TORCH_FN(silu_backward));
+  m.impl("silu_backward.grad_input", TORCH_FN(silu_backward_out));
+  m.impl("sigmoid", TORCH_FN(u_sigmoid));
+  m.impl("sigmoid_", TORCH_FN(u_sigmoid_));
+  m.impl("sigmoid.out", TORCH_FN(u_sigmoid_out));
+  m.impl("sigmoid_backward", TORCH_FN(sigmoid_backward));
+  m.impl("sigmoid_backward.grad_input", TORCH_FN(sigmoid_backward_out));
+  m.impl("tanh", TORCH_FN(u_tanh));
+  m.impl("tanh_", TORCH_FN(u_tanh_));
+  m.impl("tanh.out", TORCH_FN(u_tanh_out));
+  m.impl("tanh_backward", TORCH_FN(tanh_backward));
+  m.impl("tanh_backward.grad_input", TORCH_FN(tanh_backward_out));
+  m.impl("exp", TORCH_FN(u_exp));
+  m.impl("exp_", TORCH_FN(u_exp_));
+  m.impl("exp.out", TORCH_FN(u_exp_out));
+  m.impl("log", TORCH_FN(u_log));
+  m.impl("log_", TORCH_FN(u_log_));
+  m.impl("log.out", TORCH_FN(u_log_out));
+  m.impl("erf", TORCH_FN(u_erf));
+  m.impl("erf_", TORCH_FN(u_erf_));
+  m.impl("erf.out", TORCH_FN(u_erf_out));
+  m.impl("neg", TORCH_FN(u_neg));
+  m.impl("neg_", TORCH_FN(u_neg_));
+  m.impl("neg.out", TORCH_FN(u_neg_out));
+  m.impl("relu", TORCH_FN(relu));
+  m.impl("relu_", TORCH_FN(relu_));
+}

@@ -1,0 +1,432 @@
+// PrivateUse1 runtime for MI355X: caching allocator, device guard, hooks and
+// the boxed CPU fallback.
+//
+// Replaces, at the scale this path needs, the reference's runtime core
+// (torch_supa/csrc/core/supa/): SUPACachingAllocator (REGISTER_ALLOCATOR at
+// SUPACachingAllocator.cpp:3556, malloc :959, free :1224, round_size :1808),
+// SUPAGuardImpl (C10_REGISTER_GUARD_IMPL at impl/SUPAGuardImpl.cpp:254),
+// SUPAHooks, and the CPU fallback of aten/VariableFallbackKernel.cpp:31-64.
+//
+// Allocator design.  Device memory comes from hipMalloc in size classes
+// (512 B granules below 1 MiB, 2 MiB granules above) and is cached per device
+// on free.  All kernels of this library run on one stream per device, so a
+// block freed by the caller is reusable by the next allocation immediately:
+// stream order already places the new user after the old one.  When hipMalloc
+// fails the cache is released and the allocation retried once before an
+// OutOfMemoryError.  Blocks are never split, so a cached block is reused only
+// by a request of at least half its size.
+#include <ATen/detail/PrivateUse1HooksInterface.h>
+#include <ATen/native/CPUFallback.h>
+#include <c10/core/Allocator.h>
+#include <c10/core/impl/DeviceGuardImplInterface.h>
+#include <c10/util/Exception.h>
+#include <torch/library.h>
+
+#include <atomic>
+#include <cstdlib>
+#include <map>
+#include <mutex>
+#include <unordered_map>
+
+#include "common.h"
+
+namespace supa {
+
+void check_status(int status, const char* what) {
+  TORCH_CHECK(status == SUPA_AMD_OK, what, ": ", supa_amd_status_string(status), " (status ", status, ")");
+}
+
+bool dtype_supported(c10::ScalarType t) {
+  switch (t) {
+    case at::kByte: case at::kChar: case at::kShort: case at::kInt: case at::kLong:
+    case at::kHalf: case at::kFloat: case at::kDouble: case at::kBool: case at::kBFloat16:
+      return true;
+    default:
+      return false;
+  }
+}
+
+// --------------------------------------------------------------- devices
+namespace {
+thread_local int tls_device = -1;
+
+int query_device_count() {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  return n;
+}
+}  // namespace
+
+c10::DeviceIndex device_count() noexcept {
+  static const int n = query_device_count();
+  return static_cast<c10::DeviceIndex>(n);
+}
+
+c10::DeviceIndex current_device() {
+  if (tls_device < 0) {
+    int d = 0;
+    SUPA_HIP_CHECK(hipGetDevice(&d));
+    tls_device = d;
+  }
+  return static_cast<c10::DeviceIndex>(tls_device);
+}
+
+void set_device(c10::DeviceIndex d) {
+  TORCH_CHECK(d >= 0 && d < device_count(), "supa: invalid device index ", int(d), " (", int(device_count()),
+              " devices)");
+  if (tls_device != d) {
+    SUPA_HIP_CHECK(hipSetDevice(d));
+    tls_device = d;
+  }
+}
+
+hipStream_t current_stream(c10::DeviceIndex /*d*/) { return nullptr; }
+
+void synchronize(c10::DeviceIndex d) {
+  const auto prev = current_device();
+  set_device(d);
+  SUPA_HIP_CHECK(hipDeviceSynchronize());
+  set_device(prev);
+}
+
+// ------------------------------------------------------------- allocator
+namespace {
+
+constexpr int kMaxDevices = 64;
+
+size_t round_size(size_t n) {
+  if (n == 0) return 0;
+  constexpr size_t kSmall = 512, kLarge = size_t(2) << 20, kSmallLimit = size_t(1) << 20;
+  if (n < kSmallLimit) return (n + kSmall - 1) / kSmall * kSmall;
+  return (n + kLarge - 1) / kLarge * kLarge;
+}
+
+struct Block {
+  void* ptr;
+  size_t size;
+  int device;
+};
+
+class CachingAllocator final : public c10::Allocator {
+ public:
+  c10::DataPtr allocate(size_t nbytes) override {
+    const int dev = current_device();
+    if (nbytes == 0) return {nullptr, nullptr, &CachingAllocator::raw_delete, c10::Device(kSupa, dev)};
+    const size_t sz = round_size(nbytes);
+    void* p = nullptr;
+    {
+      std::lock_guard<std::mutex> g(mu_);
+      auto& fl = free_[dev];
+      auto it = fl.lower_bound(sz);
+      if (it != fl.end() && it->first <= 2 * sz) {
+        p = it->second;
+        const size_t bsz = it->first;
+        fl.erase(it);
+        live_[p] = Block{p, bsz, dev};
+        account_alloc(dev, bsz, false);
+      }
+    }
+    if (!p) p = device_malloc(dev, sz);
+    return {p, p, &CachingAllocator::raw_delete, c10::Device(kSupa, dev)};
+  }
+
+  c10::DeleterFnPtr raw_deleter() const override { return &CachingAllocator::raw_delete; }
+
+  void copy_data(void* dest, const void* src, std::size_t count) const override {
+    SUPA_HIP_CHECK(hipMemcpy(dest, src, count, hipMemcpyDeviceToDevice));
+  }
+
+  static void raw_delete(void* p) {
+    if (p) instance().release(p);
+  }
+
+  static CachingAllocator& instance();
+
+  void release(void* p) {
+    std::lock_guard<std::mutex> g(mu_);
+    auto it = live_.find(p);
+    if (it == live_.end()) return;
+    const Block b = it->second;
+    live_.erase(it);
+    free_[b.device].emplace(b.size, b.ptr);
+    stats_[b.device].allocated -= (int64_t)b.size;
+    stats_[b.device].num_frees += 1;
+  }
+
+  void empty_cache() {
+    std::lock_guard<std::mutex> g(mu_);
+    release_cached_locked(-1);
+  }
+
+  AllocatorStats stats(int dev) {
+    std::lock_guard<std::mutex> g(mu_);
+    return stats_[dev];
+  }
+  void reset_peak(int dev) {
+    std::lock_guard<std::mutex> g(mu_);
+    stats_[dev].peak_allocated = stats_[dev].allocated;
+  }
+
+ private:
+  void account_alloc(int dev, size_t bsz, bool fresh) {
+    auto& s = stats_[dev];
+    s.allocated += (int64_t)bsz;
+    s.peak_allocated = std::max(s.peak_allocated, s.allocated);
+    s.num_allocs += 1;
+    if (fresh) {
+      s.reserved += (int64_t)bsz;
+      s.num_device_mallocs += 1;
+    }
+  }
+
+  void release_cached_locked(int dev) {
+    const int prev = current_device();
+    for (int d = 0; d < kMaxDevices; ++d) {
+      if (dev >= 0 && d != dev) continue;
+      if (free_[d].empty()) continue;
+      (void)hipSetDevice(d);
+      for (auto& kv : free_[d]) {
+        (void)hipFree(kv.second);
+        stats_[d].reserved -= (int64_t)kv.first;
+      }
+      free_[d].clear();
+    }
+    (void)hipSetDevice(prev);
+  }
+
+  void* device_malloc(int dev, size_t sz) {
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p, sz);
+    if (e != hipSuccess) {
+      (void)hipGetLastError();
+      {
+        std::lock_guard<std::mutex> g(mu_);
+        release_cached_locked(dev);
+      }
+      e = hipMalloc(&p, sz);
+    }
+    if (e != hipSuccess) {
+      (void)hipGetLastError();
+      size_t free_b = 0, total_b = 0;
+      (void)hipMemGetInfo(&free_b, &total_b);
+      (void)hipGetLastError();
+      AllocatorStats s = stats(dev);
+      TORCH_CHECK_WITH(OutOfMemoryError, false, "supa out of memory: tried to allocate ", sz, " bytes on device ",
+                       dev, " (", free_b, " of ", total_b, " bytes free; ", s.allocated,
+                       " allocated and ", s.reserved, " reserved by the caching allocator)");
+    }
+    std::lock_guard<std::mutex> g(mu_);
+    live_[p] = Block{p, sz, dev};
+    account_alloc(dev, sz, true);
+    return p;
+  }
+
+  std::mutex mu_;
+  std::multimap<size_t, void*> free_[kMaxDevices];
+  std::unordered_map<void*, Block> live_;
+  AllocatorStats stats_[kMaxDevices];
+};
+
+CachingAllocator& CachingAllocator::instance() {
+  static CachingAllocator* a = new CachingAllocator();  // never destroyed: frees can arrive at exit
+  return *a;
+}
+
+struct AllocatorRegistrar {
+  AllocatorRegistrar() { c10::SetAllocator(kSupa, &CachingAllocator::instance()); }
+};
+AllocatorRegistrar g_allocator_registrar;
+
+}  // namespace
+
+c10::Allocator* allocator() { return &CachingAllocator::instance(); }
+AllocatorStats allocator_stats(c10::DeviceIndex d) { return CachingAllocator::instance().stats(d); }
+void allocator_reset_peak(c10::DeviceIndex d) { CachingAllocator::instance().reset_peak(d); }
+void allocator_empty_cache() { CachingAllocator::instance().empty_cache(); }
+
+at::Tensor empty_strided_supa(c10::IntArrayRef size, c10::IntArrayRef stride, c10::ScalarType dtype,
+                              c10::DeviceIndex device) {
+  const auto prev = current_device();
+  if (device >= 0 && device != prev) set_device(device);
+  const c10::DispatchKeySet ks(c10::DispatchKey::PrivateUse1);
+  at::Tensor t = at::detail::empty_strided_generic(size, stride, allocator(), ks, dtype);
+  if (device >= 0 && device != prev) set_device(prev);
+  return t;
+}
+
+at::Tensor empty_supa(c10::IntArrayRef size, c10::ScalarType dtype, c10::DeviceIndex device,
+                      c10::MemoryFormat fmt) {
+  const auto prev = current_device();
+  if (device >= 0 && device != prev) set_device(device);
+  const c10::DispatchKeySet ks(c10::DispatchKey::PrivateUse1);
+  at::Tensor t = at::detail::empty_generic(size, allocator(), ks, dtype, fmt);
+  if (device >= 0 && device != prev) set_device(prev);
+  return t;
+}
+
+// ------------------------------------------------------------ guard impl
+namespace {
+
+struct SupaGuardImpl final : public c10::impl::DeviceGuardImplInterface {
+  c10::DeviceType type() const override { return kSupa; }
+  c10::Device exchangeDevice(c10::Device d) const override {
+    const auto old = current_device();
+    if (d.index() != old) set_device(d.index());
+    return c10::Device(kSupa, old);
+  }
+  c10::Device getDevice() const override { return c10::Device(kSupa, current_device()); }
+  void setDevice(c10::Device d) const override { set_device(d.index()); }
+  void uncheckedSetDevice(c10::Device d) const noexcept override {
+    if (hipSetDevice(d.index()) == hipSuccess) tls_device = d.index();
+  }
+  c10::Stream getStream(c10::Device d) const override { return c10::Stream(c10::Stream::DEFAULT, d); }
+  c10::Stream getDefaultStream(c10::Device d) const override { return c10::Stream(c10::Stream::DEFAULT, d); }
+  c10::Stream getStreamFromGlobalPool(c10::Device d, bool /*high_priority*/) const override {
+    return c10::Stream(c10::Stream::DEFAULT, d);
+  }
+  c10::Stream getNewStream(c10::Device d, int /*priority*/) const override {
+    return c10::Stream(c10::Stream::DEFAULT, d);
+  }
+  c10::Stream exchangeStream(c10::Stream s) const override { return c10::Stream(c10::Stream::DEFAULT, s.device()); }
+  c10::DeviceIndex deviceCount() const noexcept override { return device_count(); }
+
+  void destroyEvent(void* event, const c10::DeviceIndex /*device_index*/) const noexcept override {
+    if (event) (void)hipEventDestroy(static_cast<hipEvent_t>(event));
+  }
+  void record(void** event, const c10::Stream& stream, const c10::DeviceIndex device_index,
+              const c10::EventFlag flag) const override {
+    TORCH_CHECK(device_index == -1 || device_index == stream.device_index(), "supa event and stream devices differ");
+    const auto prev = current_device();
+    if (stream.device_index() != prev) set_device(stream.device_index());
+    if (!*event) {
+      hipEvent_t e;
+      SUPA_HIP_CHECK(hipEventCreateWithFlags(
+          &e, flag == c10::EventFlag::BACKEND_DEFAULT ? hipEventDisableTiming : hipEventDefault));
+      *event = e;
+    }
+    SUPA_HIP_CHECK(hipEventRecord(static_cast<hipEvent_t>(*event), current_stream(stream.device_index())));
+    if (stream.device_index() != prev) set_device(prev);
+  }
+  void block(void* event, const c10::Stream& stream) const override {
+    if (!event) return;
+    SUPA_HIP_CHECK(hipStreamWaitEvent(current_stream(stream.device_index()), static_cast<hipEvent_t>(event), 0));
+  }
+  bool queryEvent(void* event) const override {
+    if (!event) return true;
+    const hipError_t e = hipEventQuery(static_cast<hipEvent_t>(event));
+    if (e == hipErrorNotReady) {
+      (void)hipGetLastError();
+      return false;
+    }
+    SUPA_HIP_CHECK(e);
+    return true;
+  }
+  bool queryStream(const c10::Stream& stream) const override {
+    const hipError_t e = hipStreamQuery(current_stream(stream.device_index()));
+    if (e == hipErrorNotReady) {
+      (void)hipGetLastError();
+      return false;
+    }
+    SUPA_HIP_CHECK(e);
+    return true;
+  }
+  void synchronizeStream(const c10::Stream& stream) const override {
+    SUPA_HIP_CHECK(hipStreamSynchronize(current_stream(stream.device_index())));
+  }
+  void synchronizeEvent(void* event) const override {
+    if (event) SUPA_HIP_CHECK(hipEventSynchronize(static_cast<hipEvent_t>(event)));
+  }
+  void synchronizeDevice(const c10::DeviceIndex device_index) const override { synchronize(device_index); }
+  void recordDataPtrOnStream(const c10::DataPtr&, const c10::Stream&) const override {}
+  double elapsedTime(void* e1, void* e2, const c10::DeviceIndex /*device_index*/) const override {
+    float ms = 0.f;
+    SUPA_HIP_CHECK(hipEventElapsedTime(&ms, static_cast<hipEvent_t>(e1), static_cast<hipEvent_t>(e2)));
+    return ms;
+  }
+};
+
+C10_REGISTER_GUARD_IMPL(PrivateUse1, SupaGuardImpl);
+
+// ------------------------------------------------------------------ hooks
+struct SupaHooks final : public at::PrivateUse1HooksInterface {
+  bool isBuilt() const override { return true; }
+  bool isAvailable() const override { return device_count() > 0; }
+  bool hasPrimaryContext(c10::DeviceIndex device_index) const override {
+    return device_index >= 0 && device_index < device_count();
+  }
+  c10::DeviceIndex deviceCount() const override { return device_count(); }
+  void setCurrentDevice(c10::DeviceIndex device) const override { set_device(device); }
+  c10::DeviceIndex getCurrentDevice() const override { return current_device(); }
+  c10::DeviceIndex exchangeDevice(c10::DeviceIndex device) const override {
+    const auto old = current_device();
+    set_device(device);
+    return old;
+  }
+  c10::DeviceIndex maybeExchangeDevice(c10::DeviceIndex device) const override { return exchangeDevice(device); }
+  at::Device getDeviceFromPtr(void* data) const override {
+    hipPointerAttribute_t attr;
+    if (hipPointerGetAttributes(&attr, data) == hipSuccess) return at::Device(kSupa, attr.device);
+    (void)hipGetLastError();
+    return at::Device(kSupa, current_device());
+  }
+  bool isPinnedPtr(const void* /*data*/) const override { return false; }
+  at::Allocator* getPinnedMemoryAllocator() const override { return at::getCPUAllocator(); }
+  void resizePrivateUse1Bytes(const c10::Storage& storage, size_t newsize) const override {
+    // grow or shrink by reallocating and copying the overlap
+    c10::StorageImpl* impl = storage.unsafeGetStorageImpl();
+    const size_t old = impl->nbytes();
+    if (newsize == old) return;
+    c10::DataPtr fresh = allocator()->allocate(newsize);
+    const size_t n = std::min(old, newsize);
+    if (n > 0) SUPA_HIP_CHECK(hipMemcpy(fresh.get(), impl->data(), n, hipMemcpyDeviceToDevice));
+    impl->set_data_ptr_noswap(std::move(fresh));
+    impl->set_nbytes(newsize);
+  }
+};
+
+struct HooksRegistrar {
+  HooksRegistrar() { at::RegisterPrivateUse1HooksInterface(new SupaHooks()); }
+};
+HooksRegistrar g_hooks_registrar;
+
+// --------------------------------------------------------- CPU fallback
+std::atomic<bool> g_fallback_enabled{[] {
+  const char* e = std::getenv("SUPA_AMD_CPU_FALLBACK");
+  return !(e && std::string(e) == "0");
+}()};
+std::mutex g_fb_mu;
+std::map<std::string, int64_t> g_fb_counts;
+
+void supa_cpu_fallback(const c10::OperatorHandle& op, torch::jit::Stack* stack) {
+  const std::string name = c10::toString(op.schema().operator_name());
+  {
+    std::lock_guard<std::mutex> g(g_fb_mu);
+    g_fb_counts[name] += 1;
+  }
+  TORCH_CHECK(g_fallback_enabled.load(), "supa: operator ", name,
+              " has no supa kernel and the CPU fallback is disabled");
+  at::native::cpu_fallback(op, stack);
+}
+
+}  // namespace
+
+void set_cpu_fallback_enabled(bool on) { g_fallback_enabled.store(on); }
+bool cpu_fallback_enabled() { return g_fallback_enabled.load(); }
+std::vector<std::pair<std::string, int64_t>> fallback_counts() {
+  std::lock_guard<std::mutex> g(g_fb_mu);
+  return {g_fb_counts.begin(), g_fb_counts.end()};
+}
+void reset_fallback_counts() {
+  std::lock_guard<std::mutex> g(g_fb_mu);
+  g_fb_counts.clear();
+}
+
+}  // namespace supa
+
+TORCH_LIBRARY_IMPL(_, PrivateUse1, m) {
+  m.fallback(torch::CppFunction::makeFromBoxedFunction<&supa::supa_cpu_fallback>());
+}
+

@@ -1,0 +1,57 @@
+// Op factories shared by the elementwise translation units.
+#pragma once
+
+#include "ew_launch.h"
+#include "ops.h"
+
+namespace sa {
+
+template <template <typename> class Op, bool FloatOnly = false>
+struct SimpleFactory {
+  template <typename C> static constexpr bool ok() { return !FloatOnly || std::is_floating_point<C>::value; }
+  template <typename C> Op<C> make() const { return Op<C>{}; }
+};
+
+struct AddFactory {
+  double alpha;
+  int64_t ialpha;
+  template <typename C> static constexpr bool ok() { return true; }
+  template <typename C> AddOp<C> make() const {
+    if constexpr (std::is_floating_point<C>::value) return AddOp<C>{static_cast<C>(alpha)};
+    else if constexpr (std::is_same<C, bool>::value) return AddOp<C>{ialpha != 0 || alpha != 0.0};
+    else return AddOp<C>{static_cast<C>(ialpha)};
+  }
+};
+
+template <int K, bool Bwd>
+struct UnaryFactory {
+  template <typename C> static constexpr bool ok() {
+    if constexpr (Bwd) return std::is_floating_point<C>::value;
+    else if constexpr (K == U_RELU || K == U_NEG) return true;
+    else return std::is_floating_point<C>::value;
+  }
+  template <typename C> auto make() const {
+    if constexpr (Bwd) return UnaryBwdOp<K, C>{};
+    else return UnaryOp<K, C>{};
+  }
+};
+
+template <int K, bool Bwd>
+int run_unary(const supa_amd_ew_desc* d, void* stream) {
+  return run_ew(UnaryFactory<K, Bwd>{}, d, stream, Bwd ? 3 : 2);
+}
+
+struct MseBwdFactory {
+  double norm;
+  template <typename C> static constexpr bool ok() { return std::is_floating_point<C>::value; }
+  template <typename C> MseBwdOp<C> make() const { return MseBwdOp<C>{static_cast<C>(norm)}; }
+};
+struct SmoothL1BwdFactory {
+  double norm, beta;
+  template <typename C> static constexpr bool ok() { return std::is_floating_point<C>::value; }
+  template <typename C> SmoothL1BwdOp<C> make() const {
+    return SmoothL1BwdOp<C>{static_cast<C>(norm), static_cast<C>(beta)};
+  }
+};
+
+}  // namespace sa

@@ -1,0 +1,339 @@
+// Host side of the elementwise engine: validates a descriptor, binds
+// immediate scalars, picks the dtype and layout class and launches.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+
+#include "ew_engine.h"
+
+namespace sa {
+
+inline bool aligned(const void* p, int bytes) { return (reinterpret_cast<uintptr_t>(p) % bytes) == 0; }
+
+inline int64_t desc_numel(const supa_amd_ew_desc* d) {
+  int64_t n = 1;
+  for (int i = 0; i < d->ndim; ++i) n *= d->sizes[i];
+  return n;
+}
+
+inline int check_desc(const supa_amd_ew_desc* d, int min_ops, int max_ops) {
+  if (!d) return SUPA_AMD_EINVAL;
+  if (d->ndim < 0 || d->ndim > SUPA_AMD_MAX_DIMS) return SUPA_AMD_EINVAL;
+  if (d->noperands < min_ops || d->noperands > max_ops || d->noperands > SUPA_AMD_MAX_OPERANDS)
+    return SUPA_AMD_EINVAL;
+  for (int i = 0; i < d->ndim; ++i)
+    if (d->sizes[i] < 0) return SUPA_AMD_EINVAL;
+  if (!dtype_is_known(d->common_dtype)) return SUPA_AMD_EDTYPE;
+  for (int k = 0; k < d->noperands; ++k) {
+    const supa_amd_operand& o = d->op[k];
+    if (!dtype_is_known(o.dtype)) return SUPA_AMD_EDTYPE;
+    if (!o.is_scalar && !o.data && desc_numel(d) > 0) return SUPA_AMD_EINVAL;
+  }
+  if (d->op[0].is_scalar) return SUPA_AMD_EINVAL;
+  return SUPA_AMD_OK;
+}
+
+// Calls fn(sub_desc) on pieces whose element count is below 2^31 (splitting
+// the outermost dims), so the 32-bit coordinate arithmetic of the N-d kernels
+// is exact.  The reference splits the same way (Loops.cuh:100-105).
+template <typename Fn>
+int for_each_32bit_piece(const supa_amd_ew_desc& d, Fn&& fn) {
+  const int64_t lim = (int64_t(1) << 31) - 1;
+  int64_t n = 1;
+  for (int i = 0; i < d.ndim; ++i) n *= d.sizes[i];
+  if (n <= lim) return fn(d);
+  const int last = d.ndim - 1;
+  int64_t inner = 1;
+  for (int i = 0; i < last; ++i) inner *= d.sizes[i];
+  const int64_t outer = d.sizes[last];
+  if (inner <= lim) {
+    const int64_t step = std::max<int64_t>(1, lim / std::max<int64_t>(inner, 1));
+    for (int64_t o = 0; o < outer; o += step) {
+      supa_amd_ew_desc s = d;
+      s.sizes[last] = std::min(step, outer - o);
+      for (int k = 0; k < d.noperands; ++k)
+        if (!s.op[k].is_scalar)
+          s.op[k].data = static_cast<char*>(d.op[k].data) + o * d.op[k].strides[last] * dtype_size(d.op[k].dtype);
+      const int rc = fn(s);
+      if (rc) return rc;
+    }
+    return SUPA_AMD_OK;
+  }
+  for (int64_t o = 0; o < outer; ++o) {
+    supa_amd_ew_desc s = d;
+    s.ndim = last;
+    for (int k = 0; k < d.noperands; ++k)
+      if (!s.op[k].is_scalar)
+        s.op[k].data = static_cast<char*>(d.op[k].data) + o * d.op[k].strides[last] * dtype_size(d.op[k].dtype);
+    const int rc = for_each_32bit_piece(s, fn);
+    if (rc) return rc;
+  }
+  return SUPA_AMD_OK;
+}
+
+inline NdGeom make_geom(const supa_amd_ew_desc& d) {
+  NdGeom g;
+  g.ndim = d.ndim;
+  for (int i = 0; i < SUPA_AMD_MAX_DIMS; ++i) {
+    g.size[i] = i < d.ndim ? (uint32_t)d.sizes[i] : 1u;
+    g.div[i] = FastDiv(i < d.ndim ? (uint32_t)std::max<int64_t>(d.sizes[i], 1) : 1u);
+  }
+  return g;
+}
+
+inline int launch_status() {
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? SUPA_AMD_OK : (int)e;
+}
+
+template <typename T> inline T scalar_as(const supa_amd_operand& o) {
+  if constexpr (std::is_same<T, bool>::value) return o.iscalar != 0 || o.scalar != 0.0;
+  else if constexpr (std::is_floating_point<T>::value) return static_cast<T>(o.scalar);
+  else return static_cast<T>(o.iscalar);
+}
+
+// Storage type for a dtype code, as a template callback.
+template <typename F>
+inline int with_storage(int dtype, F&& f) {
+  switch (dtype) {
+    case SUPA_AMD_F32: return f((float*)nullptr);
+    case SUPA_AMD_BF16: return f((bf16*)nullptr);
+    case SUPA_AMD_F16: return f((f16*)nullptr);
+    case SUPA_AMD_F64: return f((double*)nullptr);
+    case SUPA_AMD_I64: return f((int64_t*)nullptr);
+    case SUPA_AMD_I32: return f((int32_t*)nullptr);
+    case SUPA_AMD_I16: return f((int16_t*)nullptr);
+    case SUPA_AMD_I8: return f((int8_t*)nullptr);
+    case SUPA_AMD_U8: return f((uint8_t*)nullptr);
+    case SUPA_AMD_BOOL: return f((b8*)nullptr);
+    default: return SUPA_AMD_EDTYPE;
+  }
+}
+
+template <typename T> constexpr int cmin(T a, T b) { return a < b ? a : b; }
+template <typename... S> constexpr int min_size() {
+  int m = 16;
+  ((m = cmin<int>(m, (int)sizeof(S))), ...);
+  return m;
+}
+
+// Static-dtype launch: output OT, inputs S..., common CT, compute C.
+template <typename Op, typename C, typename CT, typename OT, typename... S>
+int launch_static(const Op& op, const supa_amd_ew_desc& d, const int* tin, hipStream_t st) {
+  constexpr int N = sizeof...(S);
+  constexpr int VEC0 = 16 / min_size<OT, S...>();
+  constexpr int VEC = VEC0 < 1 ? 1 : VEC0;
+  const int64_t n = desc_numel(&d);
+  if (n == 0) return SUPA_AMD_OK;
+  TArgs<1 + N> a;
+  a.p[0] = d.op[0].data;
+  for (int j = 0; j < SUPA_AMD_MAX_DIMS; ++j) a.st[0][j] = j < d.ndim ? d.op[0].strides[j] : 0;
+  a.mode[0] = 0;
+  for (int i = 0; i < N; ++i) {
+    const supa_amd_operand& o = d.op[tin[i]];
+    a.p[1 + i] = o.data;
+    for (int j = 0; j < SUPA_AMD_MAX_DIMS; ++j) a.st[1 + i][j] = j < d.ndim ? o.strides[j] : 0;
+    a.mode[1 + i] = 0;
+  }
+  const int sizes_of[1 + N > 0 ? 1 + N : 1] = {(int)sizeof(OT), (int)sizeof(S)...};
+
+  // CONTIG?
+  bool contig = d.ndim <= 1;
+  if (contig && d.ndim == 1 && n > 1) {
+    if (a.st[0][0] != 1) contig = false;
+    for (int i = 0; i < N && contig; ++i) {
+      if (a.st[1 + i][0] == 0) a.mode[1 + i] = 1;
+      else if (a.st[1 + i][0] != 1) contig = false;
+    }
+  } else if (contig) {
+    for (int i = 0; i < N; ++i) a.mode[1 + i] = 1;  // one element: read element 0
+  }
+  if (contig) {
+    bool al = true;
+    for (int k = 0; k <= N; ++k)
+      if (!(k > 0 && a.mode[k]) && !aligned(a.p[k], VEC * sizes_of[k])) al = false;
+    if (al) {
+      constexpr int UNROLL = VEC >= 16 ? 1 : (VEC >= 8 ? 2 : 4);
+      const int64_t nvec = n / VEC;
+      const int64_t per_block = (int64_t)UNROLL * kBlock;
+      const int64_t blocks = std::max<int64_t>(1, (nvec + per_block - 1) / per_block);
+      k_contig<VEC, UNROLL, Op, C, CT, OT, S...><<<dim3((unsigned)blocks), dim3(kBlock), 0, st>>>(op, a, n);
+      return launch_status();
+    }
+  }
+  return for_each_32bit_piece(d, [&](const supa_amd_ew_desc& p) -> int {
+    const int64_t pn = desc_numel(&p);
+    if (pn == 0) return SUPA_AMD_OK;
+    TArgs<1 + N> b = a;
+    b.p[0] = p.op[0].data;
+    for (int i = 0; i < N; ++i) b.p[1 + i] = p.op[tin[i]].data;
+    const NdGeom g = make_geom(p);
+    // VECND?
+    bool vnd = p.ndim >= 1 && (p.sizes[0] % VEC) == 0 && b.st[0][0] == 1 && VEC > 1;
+    for (int k = 0; k <= N && vnd; ++k) {
+      const int64_t s0 = b.st[k][0];
+      if (s0 != 0 && s0 != 1) { vnd = false; break; }
+      if (s0 == 1) {
+        if (!aligned(b.p[k], VEC * sizes_of[k])) vnd = false;
+        for (int j = 1; j < p.ndim; ++j)
+          if (b.st[k][j] % VEC) vnd = false;
+      }
+    }
+    if (vnd) {
+      const uint32_t nvec = (uint32_t)(pn / VEC);
+      const unsigned blocks = (nvec + kBlock - 1) / kBlock;
+      k_vecnd<VEC, Op, C, CT, OT, S...><<<blocks, kBlock, 0, st>>>(op, b, g, nvec);
+      return launch_status();
+    }
+    const unsigned blocks = (unsigned)((pn + kBlock - 1) / kBlock);
+    k_strided<Op, C, CT, OT, S...><<<blocks, kBlock, 0, st>>>(op, b, g, (uint32_t)pn);
+    return launch_status();
+  });
+}
+
+template <int NT, typename Op, typename C>
+int launch_dynamic(const Op& op, const supa_amd_ew_desc& d, const int* tin, int common, hipStream_t st) {
+  return for_each_32bit_piece(d, [&](const supa_amd_ew_desc& p) -> int {
+    const int64_t pn = desc_numel(&p);
+    if (pn == 0) return SUPA_AMD_OK;
+    TArgs<NT> a;
+    DynTypes<NT> t;
+    t.common = common;
+    for (int k = 0; k < NT; ++k) {
+      const supa_amd_operand& o = p.op[k == 0 ? 0 : tin[k - 1]];
+      a.p[k] = o.data;
+      a.mode[k] = 0;
+      t.dtype[k] = o.dtype;
+      for (int j = 0; j < SUPA_AMD_MAX_DIMS; ++j) a.st[k][j] = j < p.ndim ? o.strides[j] : 0;
+    }
+    const NdGeom g = make_geom(p);
+    const unsigned blocks = (unsigned)((pn + kBlock - 1) / kBlock);
+    k_dynamic<NT, Op, C><<<blocks, kBlock, 0, st>>>(op, a, t, g, (uint32_t)pn);
+    return launch_status();
+  });
+}
+
+// Compute type used for a storage type: float for the float32/16-bit floats,
+// double for float64, bool for bool, int64 for every integer type (wrapping
+// add/sub/mul are exact modulo 2^bits, so the narrow result is the same).
+template <typename T, typename C> constexpr bool compute_compatible() {
+  if constexpr (std::is_same<C, float>::value)
+    return std::is_same<T, float>::value || std::is_same<T, bf16>::value || std::is_same<T, f16>::value;
+  else if constexpr (std::is_same<C, double>::value) return std::is_same<T, double>::value;
+  else if constexpr (std::is_same<C, bool>::value) return std::is_same<T, b8>::value;
+  else return std::is_integral<T>::value;
+}
+
+// Dispatch over storage types once the op (with scalars bound) is fixed.
+// N = number of tensor inputs.
+template <int N, typename Op, typename C>
+int dispatch_types(const Op& op, const supa_amd_ew_desc& d, const int* tin, hipStream_t st) {
+  const int common = d.common_dtype;
+  bool same = d.op[0].dtype == common;
+  for (int i = 0; i < N; ++i) same = same && d.op[tin[i]].dtype == common;
+  if (same) {
+    return with_storage(common, [&](auto* tag) -> int {
+      using T = std::remove_pointer_t<decltype(tag)>;
+      if constexpr (!compute_compatible<T, C>()) {
+        return SUPA_AMD_EDTYPE;
+      } else if constexpr (N == 0) {
+        return launch_static<Op, C, T, T>(op, d, tin, st);
+      } else if constexpr (N == 1) {
+        return launch_static<Op, C, T, T, T>(op, d, tin, st);
+      } else if constexpr (N == 2) {
+        return launch_static<Op, C, T, T, T, T>(op, d, tin, st);
+      } else if constexpr (N == 3) {
+        return launch_static<Op, C, T, T, T, T, T>(op, d, tin, st);
+      } else {
+        return launch_static<Op, C, T, T, T, T, T, T>(op, d, tin, st);
+      }
+    });
+  }
+  if constexpr (std::is_same<C, float>::value && N >= 1 && N <= 2) {
+    auto fam = [](int dt) { return dt == SUPA_AMD_F32 || dt == SUPA_AMD_BF16 || dt == SUPA_AMD_F16; };
+    bool mixed = common == SUPA_AMD_F32 && d.op[0].dtype == SUPA_AMD_F32;
+    for (int i = 0; i < N; ++i) mixed = mixed && fam(d.op[tin[i]].dtype);
+    if (mixed) {
+      auto w16 = [](int dt, auto&& f) -> int {
+        if (dt == SUPA_AMD_F32) return f((float*)nullptr);
+        if (dt == SUPA_AMD_BF16) return f((bf16*)nullptr);
+        return f((f16*)nullptr);
+      };
+      if constexpr (N == 1) {
+        return w16(d.op[tin[0]].dtype, [&](auto* t0) -> int {
+          using S0 = std::remove_pointer_t<decltype(t0)>;
+          return launch_static<Op, float, float, float, S0>(op, d, tin, st);
+        });
+      } else {
+        return w16(d.op[tin[0]].dtype, [&](auto* t0) -> int {
+          return w16(d.op[tin[1]].dtype, [&](auto* t1) -> int {
+            using S0 = std::remove_pointer_t<decltype(t0)>;
+            using S1 = std::remove_pointer_t<decltype(t1)>;
+            return launch_static<Op, float, float, float, S0, S1>(op, d, tin, st);
+          });
+        });
+      }
+    }
+  }
+  return launch_dynamic<N + 1, Op, C>(op, d, tin, common, st);
+}
+
+// Entry: Factory::make<C>() builds the op for compute type C;
+// Factory::ok<C>() says whether the op exists for C.  Immediate scalar inputs
+// (at most two) are bound into the functor.
+template <typename C, typename Factory>
+int run_with_compute(const Factory& f, const supa_amd_ew_desc& d, hipStream_t st) {
+  if constexpr (!Factory::template ok<C>()) {
+    return SUPA_AMD_EDTYPE;
+  } else {
+    using Op = decltype(f.template make<C>());
+    constexpr int A = Op::arity;
+    if (d.noperands != A + 1) return SUPA_AMD_EINVAL;
+    int tin[kMaxIn];
+    int sc[kMaxIn];
+    int nt = 0, ns = 0;
+    for (int k = 1; k < d.noperands; ++k) {
+      if (d.op[k].is_scalar) sc[ns++] = k;
+      else tin[nt++] = k;
+    }
+    const Op op = f.template make<C>();
+    if (ns == 0) {
+      return dispatch_types<A, Op, C>(op, d, tin, st);
+    }
+    if constexpr (A >= 1) {
+      if (ns == 1) {
+        Bind1<Op, C> b{op, sc[0] - 1, scalar_as<C>(d.op[sc[0]])};
+        return dispatch_types<A - 1, Bind1<Op, C>, C>(b, d, tin, st);
+      }
+    }
+    if constexpr (A >= 3) {
+      if (ns == 2) {
+        // bind the later position first so the earlier index stays valid
+        Bind1<Op, C> b1{op, sc[1] - 1, scalar_as<C>(d.op[sc[1]])};
+        Bind1<Bind1<Op, C>, C> b2{b1, sc[0] - 1, scalar_as<C>(d.op[sc[0]])};
+        return dispatch_types<A - 2, Bind1<Bind1<Op, C>, C>, C>(b2, d, tin, st);
+      }
+    }
+    return SUPA_AMD_EINVAL;
+  }
+}
+
+template <typename Factory>
+int run_ew(const Factory& f, const supa_amd_ew_desc* d, void* stream, int min_ops = 1) {
+  const int rc = check_desc(d, min_ops, SUPA_AMD_MAX_OPERANDS);
+  if (rc) return rc;
+  if (desc_numel(d) == 0) return SUPA_AMD_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (d->common_dtype) {
+    case SUPA_AMD_F32:
+    case SUPA_AMD_BF16:
+    case SUPA_AMD_F16: return run_with_compute<float>(f, *d, st);
+    case SUPA_AMD_F64: return run_with_compute<double>(f, *d, st);
+    case SUPA_AMD_BOOL: return run_with_compute<bool>(f, *d, st);
+    default: return run_with_compute<int64_t>(f, *d, st);
+  }
+}
+
+}  // namespace sa

@@ -1,0 +1,256 @@
+// Op functors of the elementwise path.  Each functor computes one element in
+// the compute type C (float for float32/bfloat16/float16, double, int64 for
+// integers, bool) and keeps the operation order of the reference functor it
+// replaces, so a float32 result is reproducible bit for bit.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <type_traits>
+
+#include "devmath.h"
+
+namespace sa {
+
+template <typename C> constexpr bool is_fp() { return std::is_floating_point<C>::value; }
+
+// a * b + c with one rounding for floating types (the contraction the
+// reference's compiler applies to `self + alpha * other`).
+template <typename C> __device__ __forceinline__ C muladd(C a, C b, C c) {
+  if constexpr (std::is_same<C, float>::value) return fmaf(a, b, c);
+  else if constexpr (std::is_same<C, double>::value) return fma(a, b, c);
+  else if constexpr (std::is_same<C, bool>::value) return c || (a && b);
+  else return (C)((uint64_t)c + (uint64_t)a * (uint64_t)b);  // wrapping
+}
+
+// ------------------------------------------------------------- binary
+// add: ufunc::add `self + alpha * other` (UfuncCUDA_add.cu:13-16).
+template <typename C> struct AddOp {
+  static constexpr int arity = 2;
+  C alpha;
+  __device__ __forceinline__ C operator()(const C* x) const { return muladd<C>(alpha, x[1], x[0]); }
+};
+// mul: MulFunctor (BinaryInternal.h:17-30; bool is &&).
+template <typename C> struct MulOp {
+  static constexpr int arity = 2;
+  __device__ __forceinline__ C operator()(const C* x) const {
+    if constexpr (std::is_same<C, bool>::value) return x[0] && x[1];
+    else if constexpr (std::is_integral<C>::value) return (C)((uint64_t)x[0] * (uint64_t)x[1]);
+    else return x[0] * x[1];
+  }
+};
+// true division: DivFunctor `a / b` (BinaryInternal.h:10-15), IEEE.
+template <typename C> struct DivTrueOp {
+  static constexpr int arity = 2;
+  __device__ __forceinline__ C operator()(const C* x) const { return x[0] / x[1]; }
+};
+// trunc division (BinaryDivTruncKernel.cu:22-55).  Integer division by zero
+// has no defined value on the device; it yields 0 here.
+template <typename C> struct DivTruncOp {
+  static constexpr int arity = 2;
+  __device__ __forceinline__ C operator()(const C* x) const {
+    if constexpr (std::is_floating_point<C>::value) return trunc(x[0] / x[1]);
+    else if constexpr (std::is_same<C, bool>::value) return x[0];
+    else return x[1] == 0 ? C(0) : x[0] / x[1];
+  }
+};
+// floor division with Python semantics: c10::div_floor_floating /
+// c10::div_floor_integer (BinaryDivFloorKernel.cu:22-82).
+template <typename C> struct DivFloorOp {
+  static constexpr int arity = 2;
+  __device__ __forceinline__ C operator()(const C* x) const {
+    const C a = x[0], b = x[1];
+    if constexpr (std::is_floating_point<C>::value) {
+      if (b == C(0)) return a / b;
+      const C mod = fmod(a, b);
+      C div = (a - mod) / b;
+      if (mod != C(0) && ((b < C(0)) != (mod < C(0)))) div -= C(1);
+      C fl;
+      if (div != C(0)) {
+        fl = floor(div);
+        if (div - fl > C(0.5)) fl += C(1);
+      } else {
+        fl = copysign(C(0), a / b);
+      }
+      return fl;
+    } else if constexpr (std::is_same<C, bool>::value) {
+      return a;
+    } else {
+      if (b == 0) return C(0);
+      if ((a < 0) != (b < 0)) {
+        const C q = a / b;
+        const C r = a % b;
+        return r ? q - 1 : q;
+      }
+      return a / b;
+    }
+  }
+};
+
+// -------------------------------------------------------- activations
+// Constants in double; the float kernels use their binary32 roundings.
+constexpr double kSqrt1_2 = 0.70710678118654752440;
+constexpr double kGeluBetaNone = 0.3989422804014327;  // M_2_SQRTPI * M_SQRT1_2 * 0.5
+constexpr double kGeluBetaTanh = 0.7978845608028654;  // M_SQRT2 * M_2_SQRTPI * 0.5
+constexpr double kGeluKappa = 0.044715;
+static_assert((float)kSqrt1_2 == 0.70710678118654752440f, "constant rounding");
+static_assert((float)kGeluBetaNone == 0.3989422804014327f, "constant rounding");
+static_assert((float)kGeluBetaTanh == 0.7978845608028654f, "constant rounding");
+static_assert((float)kGeluKappa == 0.044715f, "constant rounding");
+
+template <typename C> __device__ __forceinline__ C gelu_none(C x) {
+  if constexpr (std::is_same<C, float>::value) return (x * 0.5f) * (1.0f + sa_erff(x * (float)kSqrt1_2));
+  else return (x * C(0.5)) * (C(1) + erf(x * C(kSqrt1_2)));
+}
+// gelu 'tanh' as x * sigmoid(2u), u = b (x + k x^3): the same function as
+// 0.5 x (1 + tanh(u)) without the cancellation of 1 + tanh(u) for u << 0.
+template <typename C> __device__ __forceinline__ C gelu_tanh(C x) {
+  if constexpr (std::is_same<C, float>::value) {
+    const float x3 = (x * x) * x;
+    const float inner = (-2.0f * (float)kGeluBetaTanh) * fmaf((float)kGeluKappa, x3, x);
+    return x / (1.0f + sa_expf(inner));
+  } else {
+    const C x3 = (x * x) * x;
+    const C inner = C(-2.0 * kGeluBetaTanh) * fma(C(kGeluKappa), x3, x);
+    return x / (C(1) + exp(inner));
+  }
+}
+template <typename C> __device__ __forceinline__ C expx(C x) {
+  if constexpr (std::is_same<C, float>::value) return sa_expf(x);
+  else return exp(x);
+}
+template <typename C> __device__ __forceinline__ C logx(C x) {
+  if constexpr (std::is_same<C, float>::value) return sa_logf(x);
+  else return log(x);
+}
+template <typename C> __device__ __forceinline__ C tanhx(C x) {
+  if constexpr (std::is_same<C, float>::value) return sa_tanhf(x);
+  else return tanh(x);
+}
+template <typename C> __device__ __forceinline__ C erfx(C x) {
+  if constexpr (std::is_same<C, float>::value) return sa_erff(x);
+  else return erf(x);
+}
+template <typename C> __device__ __forceinline__ C sigmoidx(C x) { return C(1) / (C(1) + expx<C>(-x)); }
+
+enum UnaryKind { U_GELU = 0, U_GELU_TANH, U_SILU, U_SIGMOID, U_TANH, U_EXP, U_LOG, U_ERF, U_RELU, U_NEG };
+
+template <int K, typename C> struct UnaryOp {
+  static constexpr int arity = 1;
+  __device__ __forceinline__ C operator()(const C* v) const {
+    const C x = v[0];
+    if constexpr (K == U_GELU) return gelu_none<C>(x);
+    else if constexpr (K == U_GELU_TANH) return gelu_tanh<C>(x);
+    else if constexpr (K == U_SILU) return x / (C(1) + expx<C>(-x));
+    else if constexpr (K == U_SIGMOID) return sigmoidx<C>(x);
+    else if constexpr (K == U_TANH) return tanhx<C>(x);
+    else if constexpr (K == U_EXP) return expx<C>(x);
+    else if constexpr (K == U_LOG) return logx<C>(x);
+    else if constexpr (K == U_ERF) return erfx<C>(x);
+    else if constexpr (K == U_RELU) {
+      if constexpr (std::is_same<C, bool>::value) return x;
+      else if constexpr (std::is_floating_point<C>::value) return (x != x) ? x : (x > C(0) ? x : C(0));
+      else return x > C(0) ? x : C(0);
+    } else {
+      if constexpr (std::is_same<C, bool>::value) return x;
+      else if constexpr (std::is_integral<C>::value) return (C)(0 - (uint64_t)x);
+      else return -x;
+    }
+  }
+};
+
+// Backward functors: x[0] = dy, x[1] = forward input (gelu, silu) or forward
+// output (sigmoid, tanh); upstream aten activation backward formulas.
+template <int K, typename C> struct UnaryBwdOp {
+  static constexpr int arity = 2;
+  __device__ __forceinline__ C operator()(const C* v) const {
+    const C dy = v[0], x = v[1];
+    if constexpr (K == U_GELU) {
+      const C cdf = C(0.5) * (C(1) + erfx<C>(x * C(kSqrt1_2)));
+      const C pdf = expx<C>((C(-0.5) * x) * x) * C(kGeluBetaNone);
+      return dy * muladd<C>(x, pdf, cdf);
+    } else if constexpr (K == U_GELU_TANH) {
+      const C x2 = x * x;
+      const C x3 = x2 * x;
+      const C inner = C(kGeluBetaTanh) * muladd<C>(C(kGeluKappa), x3, x);
+      const C t = tanhx<C>(inner);
+      const C left = C(0.5) * x;
+      const C right = C(1) + t;
+      const C left_d = C(0.5) * right;
+      const C right_d = muladd<C>(-t, t, C(1));
+      const C three_kappa = std::is_same<C, float>::value ? C(3.0f * (float)kGeluKappa) : C(3.0 * kGeluKappa);
+      const C inner_d = C(kGeluBetaTanh) * muladd<C>(three_kappa, x2, C(1));
+      return dy * muladd<C>(left * right_d, inner_d, left_d);
+    } else if constexpr (K == U_SILU) {
+      const C s = C(1) / (C(1) + expx<C>(-x));
+      return (dy * s) * muladd<C>(x, C(1) - s, C(1));
+    } else if constexpr (K == U_SIGMOID) {
+      return (dy * (C(1) - x)) * x;
+    } else {
+      return dy * muladd<C>(-x, x, C(1));
+    }
+  }
+};
+
+// ------------------------------------------------------------ copy/fill
+template <typename C> struct IdentityOp {
+  static constexpr int arity = 1;
+  __device__ __forceinline__ C operator()(const C* x) const { return x[0]; }
+};
+
+// ------------------------------------------------------ pointwise losses
+// mse term: d = x - t; d * d.
+template <typename C> struct MseTermOp {
+  static constexpr int arity = 2;
+  __device__ __forceinline__ C operator()(const C* v) const {
+    const C d = v[0] - v[1];
+    return d * d;
+  }
+};
+// smooth_l1 term: z = |x - t|; z < beta ? 0.5 z z / beta : z - 0.5 beta.
+template <typename C> struct SmoothL1TermOp {
+  static constexpr int arity = 2;
+  C beta;
+  __device__ __forceinline__ C operator()(const C* v) const {
+    const C z = fabs(v[0] - v[1]);
+    return z < beta ? ((C(0.5) * z) * z) / beta : z - C(0.5) * beta;
+  }
+};
+// BCE-with-logits term (BinaryCrossEntropyWithLogitsKernel.cu:17-35):
+// m = max(-x, 0); exp(-m) + exp(-x-m) is 1 + exp(-|x|) in either order.
+// inputs: x, t [, pw] [, w]
+template <bool PW, bool W, typename C> struct BceTermOp {
+  static constexpr int arity = 2 + (PW ? 1 : 0) + (W ? 1 : 0);
+  __device__ __forceinline__ C operator()(const C* v) const {
+    const C x = v[0], t = v[1];
+    const C m = x < C(0) ? -x : C(0);
+    const C lse = logx<C>(C(1) + expx<C>(-fabs(x)));
+    C r;
+    if constexpr (PW) {
+      const C lw = muladd<C>(v[2] - C(1), t, C(1));
+      r = muladd<C>(C(1) - t, x, lw * (m + lse));
+    } else {
+      r = muladd<C>(C(1) - t, x, m) + lse;
+    }
+    if constexpr (W) r = r * v[2 + (PW ? 1 : 0)];
+    return r;
+  }
+};
+// mse backward: ((x - t) * norm) * g   (inputs g, x, t)
+template <typename C> struct MseBwdOp {
+  static constexpr int arity = 3;
+  C norm;
+  __device__ __forceinline__ C operator()(const C* v) const { return ((v[1] - v[2]) * norm) * v[0]; }
+};
+// smooth_l1 backward (inputs g, x, t)
+template <typename C> struct SmoothL1BwdOp {
+  static constexpr int arity = 3;
+  C norm, beta;
+  __device__ __forceinline__ C operator()(const C* v) const {
+    const C g = v[0], d = v[1] - v[2];
+    return d < -beta ? (-norm) * g : (d > beta ? norm * g : ((norm * d) * g) / beta);
+  }
+};
+
+}  // namespace sa

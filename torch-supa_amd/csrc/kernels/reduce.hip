@@ -1,0 +1,415 @@
+// Full reductions: sum/mean of a tensor, and the sum/mean reductions of the
+// pointwise losses fused with the loss term (one read of the inputs, no
+// materialised loss tensor).
+//
+// Two-stage and deterministic.  Stage 1: a fixed grid of G blocks; each
+// thread accumulates a strided subset of 16-byte vectors in float32 (float64
+// for float64 data), the block combines its 256 partials in a fixed tree and
+// writes one partial.  Stage 2 runs in the block that finishes last (a
+// completion counter in the workspace): it combines the G partials in a fixed
+// tree, applies the scale (1 for sum, 1/n for mean) and stores the result,
+// then resets the counter.  The order of every addition depends only on n and
+// G, so reruns are bit-identical.
+//
+// Workspace contract: supa_amd_*_workspace_bytes() bytes of device memory
+// that are zero before the first call; each call leaves its counter at zero
+// again, so one buffer serves consecutive calls on one stream.  Calls that
+// overlap in time on different streams need separate buffers.
+#include "ew_launch.h"
+#include "ops.h"
+
+namespace sa {
+
+constexpr int kRedBlocks = 1024;   // stage-1 grid (capped by the work)
+constexpr int kCounterBytes = 256; // counter slot, keeps partials aligned
+
+enum RedLayout { R_CONTIG = 0, R_VECND = 1, R_STRIDED = 2 };
+
+template <typename ACC>
+__device__ __forceinline__ ACC block_sum(ACC v, ACC* lds) {
+  // wavefront (64 lanes) tree, then the 4 wave results in a fixed order
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) lds[wave] = v;
+  __syncthreads();
+  ACC r = ACC(0);
+  if (threadIdx.x == 0) {
+#pragma unroll
+    for (int w = 0; w < kBlock / 64; ++w) r += lds[w];
+  }
+  return r;  // valid in thread 0
+}
+
+// Accumulates op(...) over this thread's share of the iteration space.
+template <int LAYOUT, int VEC, typename Op, typename C, typename CT, typename ACC, typename... S>
+__device__ __forceinline__ ACC accumulate(const Op& op, const TArgs<1 + sizeof...(S)>& a, const NdGeom& g, int64_t n) {
+  constexpr int N = sizeof...(S);
+  ACC acc = ACC(0);
+  const int64_t tid = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  const int64_t nthreads = (int64_t)gridDim.x * kBlock;
+  if constexpr (LAYOUT == R_CONTIG) {
+    const int64_t nvec = n / VEC;
+    for (int64_t v = tid; v < nvec; v += nthreads) {
+      C x[VEC][N > 0 ? N : 1];
+      [&]<int... I>(std::integer_sequence<int, I...>) {
+        (([&] {
+           using St = typename NthT<I, S...>::type;
+           const St* p = static_cast<const St*>(a.p[1 + I]);
+           if (a.mode[1 + I]) {
+             const C s = load_cvt<C, CT>(p[0]);
+#pragma unroll
+             for (int k = 0; k < VEC; ++k) x[k][I] = s;
+           } else {
+             const Vec<St, VEC> w = *reinterpret_cast<const Vec<St, VEC>*>(p + v * VEC);
+#pragma unroll
+             for (int k = 0; k < VEC; ++k) x[k][I] = load_cvt<C, CT>(w.v[k]);
+           }
+         }()),
+         ...);
+      }(std::make_integer_sequence<int, N>{});
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) acc += (ACC)op(x[k]);
+    }
+    const int64_t t = nvec * VEC + tid;
+    if (t < n) {
+      C y[N > 0 ? N : 1];
+      [&]<int... I>(std::integer_sequence<int, I...>) {
+        (([&] {
+           using St = typename NthT<I, S...>::type;
+           const St* p = static_cast<const St*>(a.p[1 + I]);
+           y[I] = load_cvt<C, CT>(a.mode[1 + I] ? p[0] : p[t]);
+         }()),
+         ...);
+      }(std::make_integer_sequence<int, N>{});
+      acc += (ACC)op(y);
+    }
+  } else if constexpr (LAYOUT == R_VECND) {
+    const uint32_t nvec = (uint32_t)(n / VEC);
+    for (uint32_t v = (uint32_t)tid; v < nvec; v += (uint32_t)nthreads) {
+      uint32_t q, r;
+      g.div[0].divmod(v * VEC, q, r);
+      int64_t off[1 + N];
+#pragma unroll
+      for (int k = 0; k <= N; ++k) off[k] = (int64_t)r * a.st[k][0];
+      for (int d = 1; d < g.ndim; ++d) {
+        uint32_t qq, rr;
+        g.div[d].divmod(q, qq, rr);
+        q = qq;
+#pragma unroll
+        for (int k = 0; k <= N; ++k) off[k] += (int64_t)rr * a.st[k][d];
+      }
+      C x[VEC][N > 0 ? N : 1];
+      [&]<int... I>(std::integer_sequence<int, I...>) {
+        (([&] {
+           using St = typename NthT<I, S...>::type;
+           const St* p = static_cast<const St*>(a.p[1 + I]) + off[1 + I];
+           if (a.st[1 + I][0] == 0) {
+             const C s = load_cvt<C, CT>(p[0]);
+#pragma unroll
+             for (int k = 0; k < VEC; ++k) x[k][I] = s;
+           } else {
+             const Vec<St, VEC> w = *reinterpret_cast<const Vec<St, VEC>*>(p);
+#pragma unroll
+             for (int k = 0; k < VEC; ++k) x[k][I] = load_cvt<C, CT>(w.v[k]);
+           }
+         }()),
+         ...);
+      }(std::make_integer_sequence<int, N>{});
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) acc += (ACC)op(x[k]);
+    }
+  } else {
+    for (uint32_t i = (uint32_t)tid; i < (uint32_t)n; i += (uint32_t)nthreads) {
+      int64_t off[1 + N];
+#pragma unroll
+      for (int k = 0; k <= N; ++k) off[k] = 0;
+      uint32_t q = i;
+      for (int d = 0; d < g.ndim; ++d) {
+        uint32_t qq, rr;
+        g.div[d].divmod(q, qq, rr);
+        q = qq;
+#pragma unroll
+        for (int k = 0; k <= N; ++k) off[k] += (int64_t)rr * a.st[k][d];
+      }
+      C y[N > 0 ? N : 1];
+      [&]<int... I>(std::integer_sequence<int, I...>) {
+        (([&] {
+           using St = typename NthT<I, S...>::type;
+           y[I] = load_cvt<C, CT>(static_cast<const St*>(a.p[1 + I])[off[1 + I]]);
+         }()),
+         ...);
+      }(std::make_integer_sequence<int, N>{});
+      acc += (ACC)op(y);
+    }
+  }
+  return acc;
+}
+
+template <int LAYOUT, int VEC, typename Op, typename C, typename CT, typename ACC, typename OT, typename... S>
+__global__ void __launch_bounds__(kBlock)
+k_reduce(Op op, TArgs<1 + sizeof...(S)> a, NdGeom g, int64_t n, ACC scale, void* ws) {
+  __shared__ ACC lds[kBlock / 64];
+  __shared__ bool last;
+  ACC acc = accumulate<LAYOUT, VEC, Op, C, CT, ACC, S...>(op, a, g, n);
+  acc = block_sum<ACC>(acc, lds);
+  unsigned int* counter = static_cast<unsigned int*>(ws);
+  ACC* partial = reinterpret_cast<ACC*>(static_cast<char*>(ws) + kCounterBytes);
+  if (threadIdx.x == 0) {
+    partial[blockIdx.x] = acc;
+    __threadfence();
+    const unsigned int done = atomicAdd(counter, 1u);
+    last = (done == gridDim.x - 1);
+  }
+  __syncthreads();
+  if (!last) return;
+  __threadfence();
+  // stage 2: fixed-order combine of the G partials
+  ACC v = ACC(0);
+  for (unsigned int i = threadIdx.x; i < gridDim.x; i += kBlock) v += partial[i];
+  __syncthreads();
+  v = block_sum<ACC>(v, lds);
+  if (threadIdx.x == 0) {
+    static_cast<OT*>(a.p[0])[0] = from_arith<OT>(v * scale);
+    *counter = 0u;
+  }
+}
+
+template <typename Op, typename C, typename CT, typename OT, typename... S>
+int launch_reduce(const Op& op, const supa_amd_ew_desc& d, const int* tin, double scale, void* ws,
+                  int64_t ws_bytes, hipStream_t st) {
+  constexpr int N = sizeof...(S);
+  using ACC = typename std::conditional<std::is_same<C, double>::value, double, float>::type;
+  constexpr int VEC0 = 16 / min_size<S...>();
+  constexpr int VEC = VEC0 < 1 ? 1 : VEC0;
+  const int64_t n = desc_numel(&d);
+  if (!ws || ws_bytes < kCounterBytes + (int64_t)kRedBlocks * (int64_t)sizeof(double)) return SUPA_AMD_EWORKSPACE;
+  TArgs<1 + N> a;
+  a.p[0] = d.op[0].data;
+  a.mode[0] = 0;
+  for (int j = 0; j < SUPA_AMD_MAX_DIMS; ++j) a.st[0][j] = 0;
+  for (int i = 0; i < N; ++i) {
+    const supa_amd_operand& o = d.op[tin[i]];
+    a.p[1 + i] = o.data;
+    a.mode[1 + i] = 0;
+    for (int j = 0; j < SUPA_AMD_MAX_DIMS; ++j) a.st[1 + i][j] = j < d.ndim ? o.strides[j] : 0;
+  }
+  const int sizes_of[N > 0 ? N : 1] = {(int)sizeof(S)...};
+  int layout = R_STRIDED;
+  bool contig = d.ndim <= 1;
+  if (contig && d.ndim == 1 && n > 1) {
+    for (int i = 0; i < N && contig; ++i) {
+      if (a.st[1 + i][0] == 0) a.mode[1 + i] = 1;
+      else if (a.st[1 + i][0] != 1) contig = false;
+      if (!a.mode[1 + i] && !aligned(a.p[1 + i], VEC * sizes_of[i])) contig = false;
+    }
+  } else if (contig) {
+    for (int i = 0; i < N; ++i) a.mode[1 + i] = 1;
+  }
+  if (contig) layout = R_CONTIG;
+  if (layout != R_CONTIG) {
+    if (n >= (int64_t(1) << 31)) return SUPA_AMD_ELAYOUT;
+    bool vnd = VEC > 1 && d.ndim >= 1 && (d.sizes[0] % VEC) == 0;
+    for (int i = 0; i < N && vnd; ++i) {
+      const int64_t s0 = a.st[1 + i][0];
+      if (s0 != 0 && s0 != 1) vnd = false;
+      if (s0 == 1) {
+        if (!aligned(a.p[1 + i], VEC * sizes_of[i])) vnd = false;
+        for (int j = 1; j < d.ndim; ++j)
+          if (a.st[1 + i][j] % VEC) vnd = false;
+      }
+    }
+    layout = vnd ? R_VECND : R_STRIDED;
+  }
+  const NdGeom g = make_geom(d);
+  const int64_t units = layout == R_STRIDED ? n : std::max<int64_t>(n / VEC, 1);
+  const int64_t want = (units + 4 * kBlock - 1) / (4 * kBlock);
+  const unsigned blocks = (unsigned)std::max<int64_t>(1, std::min<int64_t>(want, kRedBlocks));
+  const ACC sc = static_cast<ACC>(scale);
+  switch (layout) {
+    case R_CONTIG:
+      k_reduce<R_CONTIG, VEC, Op, C, CT, ACC, OT, S...><<<blocks, kBlock, 0, st>>>(op, a, g, n, sc, ws);
+      break;
+    case R_VECND:
+      k_reduce<R_VECND, VEC, Op, C, CT, ACC, OT, S...><<<blocks, kBlock, 0, st>>>(op, a, g, n, sc, ws);
+      break;
+    default:
+      k_reduce<R_STRIDED, 1, Op, C, CT, ACC, OT, S...><<<blocks, kBlock, 0, st>>>(op, a, g, n, sc, ws);
+      break;
+  }
+  return launch_status();
+}
+
+// Same-dtype reduction dispatch (every tensor input has the common dtype; the
+// output has the common dtype or, for sum/mean with a dtype argument, float32
+// / float64 -- handled by the caller converting first).
+template <int N, typename Op, typename C, typename T>
+int reduce_same(const Op& op, const supa_amd_ew_desc& d, const int* tin, double scale, void* ws, int64_t wsb,
+                hipStream_t st) {
+  auto with_out = [&](auto* o) -> int {
+    using OT = std::remove_pointer_t<decltype(o)>;
+    if constexpr (N == 1) return launch_reduce<Op, C, T, OT, T>(op, d, tin, scale, ws, wsb, st);
+    else if constexpr (N == 2) return launch_reduce<Op, C, T, OT, T, T>(op, d, tin, scale, ws, wsb, st);
+    else if constexpr (N == 3) return launch_reduce<Op, C, T, OT, T, T, T>(op, d, tin, scale, ws, wsb, st);
+    else return launch_reduce<Op, C, T, OT, T, T, T, T>(op, d, tin, scale, ws, wsb, st);
+  };
+  const int od = d.op[0].dtype;
+  if (od == d.common_dtype) return with_out((T*)nullptr);
+  if (od == SUPA_AMD_F32) return with_out((float*)nullptr);
+  if (od == SUPA_AMD_F64) return with_out((double*)nullptr);
+  return SUPA_AMD_EDTYPE;
+}
+
+template <typename Factory>
+int run_reduce(const Factory& f, const supa_amd_ew_desc* d, double scale, void* ws, int64_t wsb, void* stream) {
+  int rc = check_desc(d, 2, SUPA_AMD_MAX_OPERANDS);
+  if (rc) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  int tin[kMaxIn];
+  int nt = 0;
+  for (int k = 1; k < d->noperands; ++k) {
+    if (d->op[k].is_scalar) return SUPA_AMD_EINVAL;
+    if (d->op[k].dtype != d->common_dtype) return SUPA_AMD_EDTYPE;
+    tin[nt++] = k;
+  }
+  auto go = [&](auto* ctag, auto* ttag) -> int {
+    using C = std::remove_pointer_t<decltype(ctag)>;
+    using T = std::remove_pointer_t<decltype(ttag)>;
+    using Op = decltype(f.template make<C>());
+    const Op op = f.template make<C>();
+    constexpr int A = Op::arity;
+    if (nt != A) return SUPA_AMD_EINVAL;
+    return reduce_same<A, Op, C, T>(op, *d, tin, scale, ws, wsb, st);
+  };
+  switch (d->common_dtype) {
+    case SUPA_AMD_F32: return go((float*)nullptr, (float*)nullptr);
+    case SUPA_AMD_BF16: return go((float*)nullptr, (bf16*)nullptr);
+    case SUPA_AMD_F16: return go((float*)nullptr, (f16*)nullptr);
+    case SUPA_AMD_F64: return go((double*)nullptr, (double*)nullptr);
+    default: return SUPA_AMD_EDTYPE;
+  }
+}
+
+struct IdentityFactory {
+  template <typename C> IdentityOp<C> make() const { return IdentityOp<C>{}; }
+};
+struct MseTermFactory {
+  template <typename C> MseTermOp<C> make() const { return MseTermOp<C>{}; }
+};
+struct SmoothL1TermFactory {
+  double beta;
+  template <typename C> SmoothL1TermOp<C> make() const { return SmoothL1TermOp<C>{static_cast<C>(beta)}; }
+};
+template <bool PW, bool W>
+struct BceTermFactory {
+  template <typename C> BceTermOp<PW, W, C> make() const { return BceTermOp<PW, W, C>{}; }
+  template <typename C> static constexpr bool ok() { return std::is_floating_point<C>::value; }
+};
+struct MseTermEwFactory {
+  template <typename C> static constexpr bool ok() { return std::is_floating_point<C>::value; }
+  template <typename C> MseTermOp<C> make() const { return MseTermOp<C>{}; }
+};
+struct SmoothL1TermEwFactory {
+  double beta;
+  template <typename C> static constexpr bool ok() { return std::is_floating_point<C>::value; }
+  template <typename C> SmoothL1TermOp<C> make() const { return SmoothL1TermOp<C>{static_cast<C>(beta)}; }
+};
+
+// ---------------------------------------------------------------- rows
+template <typename T, typename OT, typename ACC>
+__global__ void __launch_bounds__(kBlock)
+k_sum_rows(const T* __restrict__ in, OT* __restrict__ out, int64_t inner, ACC scale) {
+  __shared__ ACC lds[kBlock / 64];
+  const T* row = in + (int64_t)blockIdx.x * inner;
+  ACC acc = ACC(0);
+  for (int64_t i = threadIdx.x; i < inner; i += kBlock) acc += (ACC)to_arith(row[i]);
+  acc = block_sum<ACC>(acc, lds);
+  if (threadIdx.x == 0) out[blockIdx.x] = from_arith<OT>(acc * scale);
+}
+
+}  // namespace sa
+
+using namespace sa;
+
+extern "C" {
+
+int64_t supa_amd_sum_workspace_bytes(int64_t /*numel*/) { return kCounterBytes + (int64_t)kRedBlocks * 8; }
+int64_t supa_amd_loss_workspace_bytes(int64_t /*numel*/) { return kCounterBytes + (int64_t)kRedBlocks * 8; }
+
+int supa_amd_sum(const supa_amd_ew_desc* d, double scale, void* workspace, int64_t workspace_bytes, void* stream) {
+  if (!d || d->noperands != 2) return SUPA_AMD_EINVAL;
+  if (desc_numel(d) == 0) return SUPA_AMD_EINVAL;  // the caller writes the empty-sum value
+  return run_reduce(IdentityFactory{}, d, scale, workspace, workspace_bytes, stream);
+}
+
+int supa_amd_sum_rows(const void* in, int32_t in_dtype, void* out, int32_t out_dtype, int64_t outer, int64_t inner,
+                      double scale, void* stream) {
+  if (!in || !out || outer < 0 || inner <= 0 || outer >= (int64_t(1) << 31)) return SUPA_AMD_EINVAL;
+  if (outer == 0) return SUPA_AMD_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  auto go = [&](auto* ti, auto* to) -> int {
+    using T = std::remove_pointer_t<decltype(ti)>;
+    using OT = std::remove_pointer_t<decltype(to)>;
+    using ACC = typename std::conditional<std::is_same<T, double>::value || std::is_same<OT, double>::value, double,
+                                          float>::type;
+    k_sum_rows<T, OT, ACC><<<(unsigned)outer, kBlock, 0, st>>>(static_cast<const T*>(in), static_cast<OT*>(out), inner,
+                                                              (ACC)scale);
+    return launch_status();
+  };
+  auto outsel = [&](auto* ti) -> int {
+    switch (out_dtype) {
+      case SUPA_AMD_F32: return go(ti, (float*)nullptr);
+      case SUPA_AMD_BF16: return go(ti, (bf16*)nullptr);
+      case SUPA_AMD_F16: return go(ti, (f16*)nullptr);
+      case SUPA_AMD_F64: return go(ti, (double*)nullptr);
+      default: return SUPA_AMD_EDTYPE;
+    }
+  };
+  switch (in_dtype) {
+    case SUPA_AMD_F32: return outsel((float*)nullptr);
+    case SUPA_AMD_BF16: return outsel((bf16*)nullptr);
+    case SUPA_AMD_F16: return outsel((f16*)nullptr);
+    case SUPA_AMD_F64: return outsel((double*)nullptr);
+    default: return SUPA_AMD_EDTYPE;
+  }
+}
+
+int supa_amd_loss_forward(const supa_amd_ew_desc* d, int loss, int reduction, double beta, int has_pos_weight,
+                          int has_weight, void* out_scalar, void* workspace, int64_t workspace_bytes, void* stream) {
+  if (!d) return SUPA_AMD_EINVAL;
+  if (loss != SUPA_AMD_LOSS_BCE_LOGITS && (has_pos_weight || has_weight)) return SUPA_AMD_EINVAL;
+  if (reduction == SUPA_AMD_REDUCTION_NONE) {
+    switch (loss) {
+      case SUPA_AMD_LOSS_MSE: return run_ew(MseTermEwFactory{}, d, stream, 3);
+      case SUPA_AMD_LOSS_SMOOTH_L1: return run_ew(SmoothL1TermEwFactory{beta}, d, stream, 3);
+      case SUPA_AMD_LOSS_BCE_LOGITS:
+        if (has_pos_weight && has_weight) return run_ew(BceTermFactory<true, true>{}, d, stream, 5);
+        if (has_pos_weight) return run_ew(BceTermFactory<true, false>{}, d, stream, 4);
+        if (has_weight) return run_ew(BceTermFactory<false, true>{}, d, stream, 4);
+        return run_ew(BceTermFactory<false, false>{}, d, stream, 3);
+      default: return SUPA_AMD_EINVAL;
+    }
+  }
+  if (reduction != SUPA_AMD_REDUCTION_MEAN && reduction != SUPA_AMD_REDUCTION_SUM) return SUPA_AMD_EINVAL;
+  if (!out_scalar) return SUPA_AMD_EINVAL;
+  const int64_t n = desc_numel(d);
+  if (n == 0) return SUPA_AMD_EINVAL;  // the caller writes the empty-reduction value
+  const double scale = reduction == SUPA_AMD_REDUCTION_MEAN ? 1.0 / (double)n : 1.0;
+  supa_amd_ew_desc e = *d;
+  e.op[0].data = out_scalar;
+  switch (loss) {
+    case SUPA_AMD_LOSS_MSE: return run_reduce(MseTermFactory{}, &e, scale, workspace, workspace_bytes, stream);
+    case SUPA_AMD_LOSS_SMOOTH_L1:
+      return run_reduce(SmoothL1TermFactory{beta}, &e, scale, workspace, workspace_bytes, stream);
+    case SUPA_AMD_LOSS_BCE_LOGITS:
+      if (has_pos_weight && has_weight)
+        return run_reduce(BceTermFactory<true, true>{}, &e, scale, workspace, workspace_bytes, stream);
+      if (has_pos_weight)
+        return run_reduce(BceTermFactory<true, false>{}, &e, scale, workspace, workspace_bytes, stream);
+      if (has_weight) return run_reduce(BceTermFactory<false, true>{}, &e, scale, workspace, workspace_bytes, stream);
+      return run_reduce(BceTermFactory<false, false>{}, &e, scale, workspace, workspace_bytes, stream);
+    default: return SUPA_AMD_EINVAL;
+  }
+}
+
+}  // extern "C"
