@@ -1,0 +1,421 @@
+"""Benchmark of the elementwise + loss operator path on one MI355X.
+
+Prints ONE JSON line.  The headline workload (``value``) is BASELINE config 2,
+contiguous leg: y = x + bias (x [64,2048,4096] bf16, bias [4096] f32, result
+f32) followed by gelu(y, approximate='tanh'); one step is that pair of aten
+ops over the whole tensor; ``value`` is algorithmic HBM bytes per step /
+time per step, in GB/s.  ``per_config`` carries every other config
+(c1 ops, c2 transposed leg, c3 cross-entropy fwd+bwd rows/s, c4 losses,
+c5 fused AdamW), each as GB/s of algorithmic bytes and % of the 8 TB/s HBM
+roofline.
+
+Algorithmic bytes: every input read once, every output written once,
+broadcast operands at their storage size (the per-op counts of the path's
+measurement plan).  Inputs are resident in HBM before timing starts; they
+are synthetic, drawn on the device with torch's seeded HIP generator and
+copied into supa buffers.  Timing: HIP events on the stream the supa kernels
+run on, between two device synchronisations.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs c1,c2,c3,c4,c5]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(HERE, "torch-supa_amd"))
+sys.path.insert(0, HERE)
+
+PEAK_GBS = 8000.0  # MI355X HBM3E
+METRIC = "achieved HBM GB/s and % of MI355X roofline per op; cross-entropy fwd+bwd rows/s"
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--configs", default="c1,c2,c3,c4,c5")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    ap.add_argument("--main", default="c2", help="workload reported as value (c2 or c3)")
+    return ap.parse_args()
+
+
+class Timer:
+    """HIP events on the supa stream."""
+
+    def __init__(self, torch):
+        self.torch = torch
+
+    def time(self, fn, iters, warmup=2):
+        t = self.torch
+        for _ in range(warmup):
+            fn()
+        t.supa.synchronize()
+        e0, e1 = t.supa.Event(), t.supa.Event()
+        e0.record()
+        for _ in range(iters):
+            fn()
+        e1.record()
+        e1.synchronize()
+        return e0.elapsed_time(e1) / iters  # ms
+
+
+def gen(torch, shape, seed, dtype, kind="normal", a=0.0, b=1.0):
+    """Synthetic input: generated on the HIP device by torch, copied to supa."""
+    import torch_supa
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    if kind == "normal":
+        src = torch.randn(shape, generator=g, device="cuda") * b + a
+    elif kind == "uniform":
+        src = torch.rand(shape, generator=g, device="cuda") * (b - a) + a
+    else:  # bernoulli(p=a)
+        src = (torch.rand(shape, generator=g, device="cuda") < a).float()
+    src = src.to(dtype)
+    dst = torch.empty(shape, dtype=dtype, device="supa")
+    torch.cuda.synchronize()
+    torch_supa._C.memcpy_d2d(dst.data_ptr(), src.data_ptr(), src.numel() * src.element_size())
+    torch.supa.synchronize()
+    del src
+    return dst
+
+
+def gbs(nbytes, ms):
+    return nbytes / (ms * 1e-3) / 1e9
+
+
+def entry(nbytes, ms):
+    g = gbs(nbytes, ms)
+    return {"ms": round(ms, 5), "bytes": int(nbytes), "GB/s": round(g, 1), "pct_roofline": round(100 * g / PEAK_GBS, 1)}
+
+
+# ------------------------------------------------------------------ configs
+def bench_c1(torch, timer):
+    import torch.nn.functional as F
+    n = 4096 * 4096
+    # six (a, b, out) sets = 1.2 GB rotate so the 256 MB last-level cache cannot hold the working set
+    sets = [(gen(torch, (4096, 4096), 10 + i, torch.float32), gen(torch, (4096, 4096), 20 + i, torch.float32),
+             torch.empty(4096, 4096, device="supa")) for i in range(6)]
+    res = {}
+    for name, fn, nbytes in [
+        ("add", lambda s: torch.add(s[0], s[1], alpha=1, out=s[2]), 12 * n),
+        ("mul", lambda s: torch.mul(s[0], s[1], out=s[2]), 12 * n),
+        ("gelu", lambda s: torch.ops.aten.gelu.out(s[0], approximate="none", out=s[2]), 8 * n),
+        ("silu", lambda s: torch.ops.aten.silu.out(s[0], out=s[2]), 8 * n),
+    ]:
+        k = [0]
+
+        def step():
+            fn(sets[k[0] % 6])
+            k[0] += 1
+        ms = timer.time(step, 300, warmup=6)
+        res[name] = entry(nbytes, ms)
+    del sets
+    return res
+
+
+def c2_inputs(torch, transposed):
+    if transposed:
+        x = gen(torch, (64, 4096, 2048), 2, torch.bfloat16).transpose(1, 2)
+    else:
+        x = gen(torch, (64, 2048, 4096), 1, torch.bfloat16)
+    bias = gen(torch, (4096,), 3, torch.float32, b=0.02)
+    return x, bias
+
+
+C2_N = 64 * 2048 * 4096
+C2_ADD_BYTES = 2 * C2_N + 4 * C2_N + 4 * 4096
+C2_GELU_BYTES = 8 * C2_N
+
+
+def bench_c2(torch, timer, x, bias, iters=20):
+    import torch.nn.functional as F
+    y = torch.empty_strided(x.shape, x.stride(), dtype=torch.float32, device="supa")
+    z = torch.empty_strided(x.shape, x.stride(), dtype=torch.float32, device="supa")
+    t_add = timer.time(lambda: torch.add(x, bias, out=y), iters)
+    t_gelu = timer.time(lambda: torch.ops.aten.gelu.out(y, approximate="tanh", out=z), iters)
+    t_step = timer.time(lambda: F.gelu(x + bias, approximate="tanh"), iters)
+    return {"add": entry(C2_ADD_BYTES, t_add), "gelu_tanh": entry(C2_GELU_BYTES, t_gelu),
+            "step": entry(C2_ADD_BYTES + C2_GELU_BYTES, t_step)}
+
+
+C3_N, C3_V = 8192, 128256
+C3_NV = C3_N * C3_V
+C3_BYTES = {"_log_softmax": 4 * C3_NV, "nll_loss_forward": 81926, "nll_loss_backward": 2 * C3_NV + 65538,
+            "_log_softmax_backward_data": 6 * C3_NV}
+
+
+def bench_c3(torch, timer, iters=10):
+    import torch.nn.functional as F
+    logits = gen(torch, (C3_N, C3_V), 4, torch.bfloat16, b=2.0)
+    g = torch.Generator(device="cuda").manual_seed(5)
+    t = torch.randint(0, C3_V, (C3_N,), generator=g, device="cuda")
+    t[torch.randperm(C3_N, generator=g, device="cuda")[:410]] = -100
+    tgt = torch.empty(C3_N, dtype=torch.int64, device="supa")
+    torch.cuda.synchronize()
+    import torch_supa
+    torch_supa._C.memcpy_d2d(tgt.data_ptr(), t.data_ptr(), C3_N * 8)
+    logits.requires_grad_()
+
+    def step():
+        logits.grad = None
+        loss = F.cross_entropy(logits, tgt, ignore_index=-100, reduction="mean")
+        loss.backward()
+    ms = timer.time(step, iters, warmup=2)
+    res = {"fwd_bwd": dict(entry(sum(C3_BYTES.values()), ms), rows_per_s=round(C3_N / (ms * 1e-3), 1))}
+    lx = logits.detach()
+    lsm = torch.ops.aten._log_softmax(lx, 1, False)
+    out, tw = torch.ops.aten.nll_loss_forward(lsm, tgt, None, 1, -100)
+    go = torch.ones((), dtype=torch.bfloat16, device="supa")
+    gn = torch.ops.aten.nll_loss_backward(go, lsm, tgt, None, 1, -100, tw)
+    res["_log_softmax"] = entry(C3_BYTES["_log_softmax"], timer.time(
+        lambda: torch.ops.aten._log_softmax.out(lx, 1, False, out=lsm), iters))
+    res["nll_loss_forward"] = entry(C3_BYTES["nll_loss_forward"], timer.time(
+        lambda: torch.ops.aten.nll_loss_forward(lsm, tgt, None, 1, -100), iters))
+    res["nll_loss_backward"] = entry(C3_BYTES["nll_loss_backward"], timer.time(
+        lambda: torch.ops.aten.nll_loss_backward.grad_input(go, lsm, tgt, None, 1, -100, tw, grad_input=gn), iters))
+    gi = torch.empty_like(lx)
+    res["_log_softmax_backward_data"] = entry(C3_BYTES["_log_softmax_backward_data"], timer.time(
+        lambda: torch.ops.aten._log_softmax_backward_data.out(gn, lsm, 1, torch.bfloat16, out=gi), iters))
+    return res
+
+
+def bench_c4(torch, timer, iters=20):
+    import torch.nn.functional as F
+    R, C = 32, 1048576
+    n = R * C
+    x = gen(torch, (R, C), 6, torch.float32)
+    t = gen(torch, (R, C), 7, torch.float32)
+    tb = gen(torch, (R, C), 8, torch.float32, kind="bernoulli", a=0.3)
+    pw = gen(torch, (C,), 9, torch.float32, kind="uniform", a=0.5, b=2.0)
+    res = {}
+    pwb = 4 * C
+    for red in ("none", "sum", "mean"):
+        go = gen(torch, (R, C), 11, torch.float32) if red == "none" else torch.ones((), device="supa")
+        fwd_b = 12 * n if red == "none" else 8 * n + 4
+        bwd_b = 16 * n if red == "none" else 12 * n + 4
+        res[f"mse_{red}_fwd"] = entry(fwd_b, timer.time(lambda: F.mse_loss(x, t, reduction=red), iters))
+        res[f"mse_{red}_bwd"] = entry(bwd_b, timer.time(
+            lambda: torch.ops.aten.mse_loss_backward(go, x, t, {"none": 0, "mean": 1, "sum": 2}[red]), iters))
+        res[f"smooth_l1_{red}_fwd"] = entry(fwd_b, timer.time(
+            lambda: F.smooth_l1_loss(x, t, reduction=red, beta=1.0), iters))
+        res[f"smooth_l1_{red}_bwd"] = entry(bwd_b, timer.time(
+            lambda: torch.ops.aten.smooth_l1_loss_backward(go, x, t, {"none": 0, "mean": 1, "sum": 2}[red], 1.0),
+            iters))
+        bce_fwd_b = (12 * n if red == "none" else 8 * n + 4) + pwb
+        res[f"bce_{red}_fwd"] = entry(bce_fwd_b, timer.time(
+            lambda: F.binary_cross_entropy_with_logits(x, tb, pos_weight=pw, reduction=red), iters))
+        xg = x.detach().requires_grad_()
+        loss = F.binary_cross_entropy_with_logits(xg, tb, pos_weight=pw, reduction=red)
+        gsz = 4 if red != "none" else 4 * n
+        # the autograd formula's op sequence: mul, add, sub, sigmoid, mul, sub, mul(grad)[, div]
+        bce_bwd_b = (8 * n + pwb) + 8 * n + 12 * n + 8 * n + 12 * n + 12 * n + (8 * n + gsz) + (8 * n if red == "mean" else 0)
+        res[f"bce_{red}_bwd"] = entry(bce_bwd_b, timer.time(
+            lambda: torch.autograd.grad(loss, xg, go, retain_graph=True), iters))
+    return res
+
+
+C5_SHAPES = ([(4096, 4096)] * 4 + [(11008, 4096)] * 2 + [(4096, 11008)] + [(4096,)] * 2) * 8
+
+
+def bench_c5(torch, timer, steps=10):
+    P = 0
+    params, grads = [], []
+    for i, s in enumerate(C5_SHAPES):
+        params.append(gen(torch, s, 100 + i, torch.float32, b=0.02).requires_grad_())
+        grads.append(gen(torch, s, 1000 + i, torch.float32, b=1e-3))
+        n = 1
+        for d in s:
+            n *= d
+        P += n
+    opt = torch.optim.AdamW(params, lr=1e-4, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01, fused=True)
+    for p, g in zip(params, grads):
+        p.grad = g
+    ms = timer.time(opt.step, steps, warmup=1)
+    res = {"fused_adamw_step": dict(entry(28 * P, ms), params=P)}
+    with torch.no_grad():
+        pd = [p.detach() for p in params]
+        res["_foreach_add_List"] = entry(12 * P, timer.time(lambda: torch._foreach_add_(pd, grads), 3, warmup=1))
+        res["_foreach_mul_Scalar"] = entry(8 * P, timer.time(lambda: torch._foreach_mul_(pd, 1.0), 3, warmup=1))
+    return res
+
+
+# ------------------------------------------------------------ CPU baselines
+def cpu_port_baseline():
+    """The oracle (single-threaded C restatement) on a bounded sample of the
+    headline workload: 1/16 of c2 (x [4,2048,4096]), repeated to ~10 s."""
+    import numpy as np
+    import oracle as O
+    rng = np.random.default_rng(0)
+    n = 4 * 2048 * 4096
+    x = O.f32_to_bf16(rng.standard_normal(n, dtype=np.float32)).reshape(4, 2048, 4096)
+    bias = (rng.standard_normal(4096, dtype=np.float32) * 0.02)
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        y = O.binary(O.ADD, O.bf16_to_f32(x), bias)
+        z = O.unary(O.GELU_TANH, y)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= 10.0:
+            break
+    per = el / reps
+    nbytes = (2 * n + 4 * n + 4 * 4096) + 8 * n
+    return {"value": round(nbytes / per / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"oracle/ C restatement, c2 workload on x[4,2048,4096] (1/16 of the config), "
+                      f"{reps} reps, {per * 1e3:.1f} ms per rep incl. the bf16 widening"}
+
+
+def cpu_aten_baseline(torch):
+    """Upstream aten CPU kernels (torch 2.10.0) on the same 1/16 sample, all
+    host threads."""
+    import torch.nn.functional as F
+    torch.set_num_threads(os.cpu_count() or 1)
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(4, 2048, 4096, generator=g).to(torch.bfloat16)
+    bias = torch.randn(4096, generator=g) * 0.02
+    F.gelu(x + bias, approximate="tanh")
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        F.gelu(x + bias, approximate="tanh")
+        times.append(time.perf_counter() - t0)
+    per = sorted(times)[1]
+    n = x.numel()
+    nbytes = (2 * n + 4 * n + 4 * 4096) + 8 * n
+    cpu_model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": round(nbytes / per / 1e9, 3), "unit": "GB/s", "threads": torch.get_num_threads(),
+            "cpu_count": os.cpu_count(), "cpu": cpu_model, "torch": torch.__version__,
+            "sample": "upstream aten CPU add + gelu(tanh) on x[4,2048,4096] bf16 + bias f32, median of 3"}
+
+
+def traffic_from_profiles():
+    p = os.path.join(HERE, "profiles", "gelu_tanh_c2_traffic.json")
+    if os.path.exists(p):
+        try:
+            return json.load(open(p)).get("bytes_per_launch")
+        except (OSError, ValueError):
+            return None
+    return None
+
+
+def main():
+    a = parse()
+    if a.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {a.gpus} is not supported "
+              "(the path's multi-GPU sharding is described in DESIGN.md, not run)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import torch_supa  # noqa: F401
+    import torch.nn.functional as F
+
+    assert torch.supa.is_available(), "no supa device"
+    timer = Timer(torch)
+    configs = [c.strip() for c in a.configs.split(",") if c.strip()]
+    per = {}
+
+    # headline workload: c2 contiguous leg
+    log("c2: generating inputs")
+    x, bias = c2_inputs(torch, transposed=False)
+    for _ in range(a.warmup):
+        F.gelu(x + bias, approximate="tanh")
+    torch.supa.synchronize()
+    e0, e1 = torch.supa.Event(), torch.supa.Event()
+    e0.record()
+    for _ in range(a.steps):
+        F.gelu(x + bias, approximate="tanh")
+    e1.record()
+    e1.synchronize()
+    torch.supa.synchronize()
+    ms_step = e0.elapsed_time(e1) / a.steps
+    step_bytes = C2_ADD_BYTES + C2_GELU_BYTES
+    value = gbs(step_bytes, ms_step)
+    # dominant kernel: gelu(tanh) over the f32 intermediate
+    y = x + bias
+    z = torch.empty_like(y)
+    t_gelu = timer.time(lambda: torch.ops.aten.gelu.out(y, approximate="tanh", out=z), max(a.steps, 10))
+    achieved = gbs(C2_GELU_BYTES, t_gelu)
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / PEAK_GBS, 4), "traffic": traffic_from_profiles(),
+                "kernel": "gelu(tanh) f32 [64,2048,4096] (k_contig)", "algorithmic_bytes": C2_GELU_BYTES,
+                "avg_launch_ms": round(t_gelu, 5)}
+    del y, z
+    if "c2" in configs:
+        per["c2_contiguous"] = bench_c2(torch, timer, x, bias)
+        del x, bias
+        log("c2 transposed leg")
+        xt, bt = c2_inputs(torch, transposed=True)
+        per["c2_transposed"] = bench_c2(torch, timer, xt, bt)
+        del xt, bt
+    else:
+        del x, bias
+    torch.supa.empty_cache()
+    if "c1" in configs:
+        log("c1")
+        per["c1"] = bench_c1(torch, timer)
+        torch.supa.empty_cache()
+    if "c3" in configs:
+        log("c3")
+        per["c3"] = bench_c3(torch, timer)
+        torch.supa.empty_cache()
+    if "c4" in configs:
+        log("c4")
+        per["c4"] = bench_c4(torch, timer)
+        torch.supa.empty_cache()
+    if "c5" in configs:
+        log("c5")
+        per["c5"] = bench_c5(torch, timer)
+        torch.supa.empty_cache()
+    fb = torch.supa.fallback_counts()
+
+    cpu = None
+    cpu_aten = None
+    if not a.no_cpu:
+        log("cpu baselines")
+        cpu = cpu_port_baseline()
+        cpu_aten = cpu_aten_baseline(torch)
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16+f32 -> f32 (elementwise in f32)",
+        "data": "synthetic: BASELINE config distributions drawn on the device by torch's seeded HIP generator",
+        "config": {"workload": "c2 contiguous: add(x bf16 [64,2048,4096], bias f32 [4096]) -> f32, then "
+                               "gelu(approximate='tanh'); one step = both aten ops",
+                   "pct_roofline": round(100 * value / PEAK_GBS, 1), "parallelism": "none (1 GPU)"},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "cpu_aten": cpu_aten,
+        "per_config": per,
+        "cpu_fallback_ops": fb,
+        "host": platform.node(),
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -112,11 +112,15 @@ int supa_amd_div(const supa_amd_ew_desc* d, int mode, void* stream);
 #define SUPA_AMD_ERF 7
 #define SUPA_AMD_RELU 8
 #define SUPA_AMD_NEG 9
+#define SUPA_AMD_RECIPROCAL 10
+#define SUPA_AMD_ABS 11
+#define SUPA_AMD_SQRT 12
 
-/* out = f(x), floating dtypes (RELU and NEG also integer).  op = {out, x}.
+/* out = f(x), floating dtypes (RELU, NEG and ABS also integer).  op = {out, x}.
  * Replaces the reference's upstream-ATen activation kernels: gelu.out NF:5216,
  * silu.out NF:5374, sigmoid.out NF:5441, tanh.out, exp.out, log.out, erf.out,
- * relu, neg.out. */
+ * relu, neg.out, and the pointwise helpers reciprocal.out (x.__rtruediv__),
+ * abs.out, sqrt.out (IEEE 1/x, |x|, correctly rounded sqrt). */
 int supa_amd_unary(const supa_amd_ew_desc* d, int op, void* stream);
 
 /* grad_in = f'(...) * dy.  op = {grad_in, dy, x} where x is the forward input

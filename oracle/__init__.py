@@ -25,7 +25,7 @@ _lib = None
 
 # op codes shared with oracle.c
 ADD, MUL, DIV, DIV_TRUNC, DIV_FLOOR = 0, 1, 2, 3, 4
-GELU, GELU_TANH, SILU, SIGMOID, TANH, EXP, LOG, ERF, RELU, NEG = range(10)
+GELU, GELU_TANH, SILU, SIGMOID, TANH, EXP, LOG, ERF, RELU, NEG, RECIPROCAL, ABS, SQRT = range(13)
 MSE, SMOOTH_L1, BCE_LOGITS = 0, 1, 2
 REDUCTION = {"none": 0, "mean": 1, "sum": 2}
 

@@ -140,7 +140,8 @@ void or_binary_f64(int op, const double* a, const double* b, double* out, int64_
 
 enum {
   OR_GELU = 0, OR_GELU_TANH = 1, OR_SILU = 2, OR_SIGMOID = 3, OR_TANH = 4,
-  OR_EXP = 5, OR_LOG = 6, OR_ERF = 7, OR_RELU = 8, OR_NEG = 9
+  OR_EXP = 5, OR_LOG = 6, OR_ERF = 7, OR_RELU = 8, OR_NEG = 9, OR_RECIPROCAL = 10, OR_ABS = 11,
+  OR_SQRT = 12
 };
 
 #define OR_SQRT1_2 0.70710678118654752440f
@@ -156,7 +157,8 @@ enum {
  *               cancellation of 1+tanh(u) for u << 0)
  *  silu:        x / (1 + exp(-x))                     NF:5374
  *  sigmoid:     1 / (1 + exp(-x))                     NF:5441
- *  tanh, exp, log, erf: the primitives of oracle_math.h. */
+ *  tanh, exp, log, erf: the primitives of oracle_math.h;
+ *  reciprocal, abs, sqrt: IEEE 1/x, |x| and correctly rounded sqrt. */
 static inline float act_fwd(int op, float x) {
   switch (op) {
     case OR_GELU: return (x * 0.5f) * (1.0f + or_erff(x * OR_SQRT1_2));
@@ -172,6 +174,9 @@ static inline float act_fwd(int op, float x) {
     case OR_LOG: return or_logf(x);
     case OR_ERF: return or_erff(x);
     case OR_RELU: return (x != x) ? x : (x > 0.0f ? x : 0.0f);
+    case OR_RECIPROCAL: return 1.0f / x;
+    case OR_ABS: return fabsf(x);
+    case OR_SQRT: return sqrtf(x);
     default: return -x;
   }
 }

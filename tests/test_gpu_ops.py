@@ -1,0 +1,372 @@
+"""Parity through the PyTorch dispatcher: aten ops on ``supa`` tensors land on
+this library's PrivateUse1 kernels (the CPU fallback is disabled and must stay
+unused) and match the oracle -- bit-exact for IEEE add/mul/div and for the
+float32 activations (same arithmetic), within the path's tolerances for
+reductions and losses.  The BASELINE configs run at full size where the
+oracle finishes in seconds, and through size-independent properties
+otherwise."""
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import oracle as O
+from helpers import bf16_ulp_dist
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(16,), (1024, 512), (1023, 511), (1025, 513), (1028, 2135)]
+
+
+def seeded(shape, seed, scale=1.0, dtype=torch.float32):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(shape, generator=g) * scale).to(dtype)
+
+
+def bits(t):
+    return t.cpu().view(torch.int16).numpy().view(np.uint16)
+
+
+def dev(t):
+    return t.to("supa")
+
+
+# ------------------------------------------------------------ c1 config
+def test_c1_full_size_bit_exact(no_fallback):
+    g = torch.Generator().manual_seed(0)
+    a = torch.randn(4096, 4096, generator=g)
+    b = torch.randn(4096, 4096, generator=g)
+    da, db = dev(a), dev(b)
+    an, bn = a.numpy(), b.numpy()
+    assert np.array_equal(torch.add(da, db, alpha=1).cpu().numpy(), O.binary(O.ADD, an, bn))
+    assert np.array_equal(torch.mul(da, db).cpu().numpy(), O.binary(O.MUL, an, bn))
+    # the same results as the upstream CPU kernels (the config's reference outputs)
+    assert torch.equal(torch.add(da, db).cpu(), a + b)
+    assert torch.equal(torch.mul(da, db).cpu(), a * b)
+    assert np.array_equal(F.gelu(da).cpu().numpy(), O.unary(O.GELU, an))
+    assert np.array_equal(F.silu(da).cpu().numpy(), O.unary(O.SILU, an))
+
+
+# ------------------------------------------------------------ elementwise
+@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_binary_ladder(shape, dtype, no_fallback):
+    a, b = seeded(shape, 1, dtype=dtype), seeded(shape, 2, dtype=dtype)
+    da, db = dev(a), dev(b)
+    for fn in (torch.add, torch.sub, torch.mul, torch.div):
+        got = fn(da, db).cpu()
+        assert got.dtype == dtype
+        assert torch.equal(got, fn(a, b)) or dtype == torch.float16 and torch.allclose(got, fn(a, b), rtol=1e-3), fn
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+def test_activations_ladder_bit_exact(shape, no_fallback):
+    x = seeded(shape, 3, 3.0)
+    dx = dev(x)
+    xn = x.numpy()
+    for fn, op in [(F.gelu, O.GELU), (lambda t: F.gelu(t, approximate="tanh"), O.GELU_TANH), (F.silu, O.SILU),
+                   (torch.sigmoid, O.SIGMOID), (torch.tanh, O.TANH), (torch.exp, O.EXP), (torch.erf, O.ERF),
+                   (torch.reciprocal, O.RECIPROCAL), (torch.abs, O.ABS), (lambda t: torch.sqrt(t.abs()), O.SQRT)]:
+        if op == O.SQRT:
+            assert np.array_equal(fn(dx).cpu().numpy(), O.unary(op, np.abs(xn)))
+            continue
+        assert np.array_equal(fn(dx).cpu().numpy(), O.unary(op, xn))
+
+
+def test_activation_backward_through_autograd(no_fallback):
+    x = seeded((1000, 257), 4, 3.0)
+    dy = seeded((1000, 257), 5)
+    for fn, op, use_out in [(F.gelu, O.GELU, False), (lambda t: F.gelu(t, approximate="tanh"), O.GELU_TANH, False),
+                            (F.silu, O.SILU, False), (torch.sigmoid, O.SIGMOID, True), (torch.tanh, O.TANH, True)]:
+        dx = dev(x).requires_grad_()
+        y = fn(dx)
+        y.backward(dev(dy))
+        inp = y.detach().cpu().numpy() if use_out else x.numpy()
+        assert np.array_equal(dx.grad.cpu().numpy(), O.unary_backward(op, dy.numpy(), inp))
+
+
+def test_broadcast_scalar_inplace_out(no_fallback):
+    a = seeded((64, 128), 6)
+    b = seeded((128,), 7)
+    c = seeded((64, 1), 8)
+    da, db, dc = dev(a), dev(b), dev(c)
+    assert torch.equal((da + db).cpu(), a + b)
+    assert torch.equal((da * dc).cpu(), a * c)
+    assert torch.equal((da - 2.5).cpu(), a - 2.5)
+    assert torch.equal((3.0 / da).cpu(), 3.0 / a)
+    assert torch.equal(torch.add(da, db, alpha=0.25).cpu(), torch.add(a, b, alpha=0.25))
+    assert torch.equal((da + torch.tensor(1.5)).cpu(), a + torch.tensor(1.5))  # 0-dim CPU tensor
+    d0 = dev(torch.tensor(0.75))
+    assert torch.equal((da * d0).cpu(), a * 0.75)  # 0-dim device tensor
+    e = da.clone()
+    e.add_(db).mul_(2.0).div_(dc)
+    assert torch.equal(e.cpu(), ((a + b) * 2.0) / c)
+    out = torch.empty(64, 128, device="supa")
+    torch.mul(da, db, out=out)
+    assert torch.equal(out.cpu(), a * b)
+    # rsub, rounding modes
+    assert torch.equal(torch.rsub(da, db).cpu(), torch.rsub(a, b))
+    assert torch.equal(torch.div(da, dc, rounding_mode="floor").cpu(), torch.div(a, c, rounding_mode="floor"))
+    assert torch.equal(torch.div(da, dc, rounding_mode="trunc").cpu(), torch.div(a, c, rounding_mode="trunc"))
+
+
+def test_transposed_and_strided_views(no_fallback):
+    base = seeded((1, 5120, 1024), 9)
+    a = base.transpose(1, 2)  # [1, 1024, 5120] with strides (5242880, 1, 1024): the reference's worst case
+    b = seeded((1, 1024, 5120), 10)
+    da = dev(base).transpose(1, 2)
+    db = dev(b)
+    got = da + db
+    ref = a + b
+    assert got.stride() == ref.stride()
+    assert torch.equal(got.cpu(), ref)
+    s = dev(seeded((300, 400), 11))[::3, 5:305:2]
+    assert torch.equal(torch.sigmoid(s).cpu(), torch.from_numpy(O.unary(O.SIGMOID, s.cpu().numpy())))
+
+
+def test_integer_bool_and_mixed_dtypes(no_fallback):
+    g = torch.Generator().manual_seed(12)
+    ia = torch.randint(-1000, 1000, (999,), generator=g)
+    ib = torch.randint(1, 50, (999,), generator=g)
+    dia, dib = dev(ia), dev(ib)
+    for fn in (torch.add, torch.sub, torch.mul):
+        assert torch.equal(fn(dia, dib).cpu(), fn(ia, ib))
+    assert torch.equal(torch.div(dia, dib, rounding_mode="floor").cpu(), torch.div(ia, ib, rounding_mode="floor"))
+    assert torch.equal(torch.div(dia, dib).cpu(), torch.div(ia, ib))  # true division promotes to float
+    i8 = torch.randint(-100, 100, (1000,), generator=g, dtype=torch.int8)
+    assert torch.equal((dev(i8) * dev(i8)).cpu(), i8 * i8)  # wrapping
+    ba = torch.rand(500, generator=g) < 0.5
+    bb = torch.rand(500, generator=g) < 0.5
+    assert torch.equal((dev(ba) * dev(bb)).cpu(), ba * bb)
+    assert torch.equal((dev(ba) + dev(bb)).cpu(), ba + bb)
+    x16 = seeded((333,), 13, dtype=torch.bfloat16)
+    f32 = seeded((333,), 14)
+    assert torch.equal((dev(x16) + dev(f32)).cpu(), x16 + f32)
+    assert torch.equal((dev(ia) + dev(f32[:1].expand(999).contiguous())).cpu(), ia + f32[:1].expand(999))
+
+
+def test_empty_and_zero_dim(no_fallback):
+    e = torch.empty(0, 5, device="supa")
+    assert (e + e).shape == (0, 5)
+    z = dev(torch.tensor(2.0))
+    assert (z * z).item() == 4.0
+
+
+def test_copy_fill_and_casts(no_fallback):
+    x = seeded((257, 33), 15, 10.0)
+    dx = dev(x)
+    for dt in (torch.bfloat16, torch.float16, torch.float64, torch.int64, torch.int32, torch.bool):
+        assert torch.equal(dx.to(dt).cpu(), x.to(dt))
+    t = dx.t().contiguous()
+    assert torch.equal(t.cpu(), x.t().contiguous())
+    f = torch.empty(100, device="supa").fill_(0.1)
+    assert torch.equal(f.cpu(), torch.full((100,), 0.1))
+    z = torch.zeros(10, 10, dtype=torch.bfloat16, device="supa")
+    assert torch.equal(z.cpu(), torch.zeros(10, 10, dtype=torch.bfloat16))
+
+
+# ------------------------------------------------------------ c2 config
+@pytest.mark.parametrize("transposed", [False, True])
+def test_c2_full_size(transposed, no_fallback):
+    """bf16 [64,2048,4096] + f32 bias [4096] -> f32, then gelu(tanh); the
+    transposed leg is x given as a [64,4096,2048] tensor transposed."""
+    g = torch.Generator().manual_seed(0)
+    if transposed:
+        x = torch.randn(64, 4096, 2048, generator=g).to(torch.bfloat16).transpose(1, 2)
+    else:
+        x = torch.randn(64, 2048, 4096, generator=g).to(torch.bfloat16)
+    bias = torch.randn(4096, generator=g) * 0.02
+    dx = torch.empty_strided(x.shape, x.stride(), dtype=torch.bfloat16, device="supa")
+    dx.copy_(x)
+    y = dx + dev(bias)
+    assert y.dtype == torch.float32
+    assert y.stride() == ((8388608, 1, 2048) if transposed else (8388608, 4096, 1))
+    xf = x.float().numpy()  # logical order
+    ref_y = O.binary(O.ADD, xf, bias.numpy())
+    assert np.array_equal(y.cpu().numpy(), ref_y)
+    z = F.gelu(y, approximate="tanh")
+    assert z.stride() == y.stride()
+    zc = z.cpu().numpy()
+    del y, z
+    assert np.array_equal(zc, O.unary(O.GELU_TANH, ref_y))
+
+
+# ------------------------------------------------------------ c3 config
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_cross_entropy_small_rows(dtype, no_fallback):
+    N, V = 96, 128256
+    logits = seeded((N, V), 20, 2.0, dtype)
+    g = torch.Generator().manual_seed(21)
+    t = torch.randint(0, V, (N,), generator=g)
+    t[torch.randperm(N, generator=g)[:5]] = -100
+    dl = dev(logits).requires_grad_()
+    lsm = F.log_softmax(dl, dim=1)
+    lsm.retain_grad()
+    loss = F.nll_loss(lsm, dev(t), ignore_index=-100)
+    loss.backward()
+    y = lsm.detach().cpu().float().numpy()
+    ref_lp = O.log_softmax(logits.float().numpy())
+    if dtype == torch.float32:
+        np.testing.assert_allclose(y, ref_lp, rtol=1e-5, atol=1e-5)
+    else:
+        assert bf16_ulp_dist(bits(lsm.detach()), O.f32_to_bf16(ref_lp)).max() <= 1
+    out, tw = O.nll_loss(y, t.numpy(), None, "mean", -100)
+    tol = 1e-5 if dtype == torch.float32 else 1e-2
+    assert abs(loss.float().item() - float(out)) <= tol * abs(float(out))
+    twv = float(O.round_bf16(tw)) if dtype == torch.bfloat16 else float(tw)
+    gn = O.nll_loss_backward(np.ones(1, np.float32), t.numpy(), N, V, twv, None, "mean", -100,
+                             bf16=dtype == torch.bfloat16)
+    gcpu = lsm.grad.cpu().float().numpy()
+    assert np.array_equal(gcpu, O.round_bf16(gn) if dtype == torch.bfloat16 else gn)
+    gin = O.log_softmax_backward(gcpu, y)
+    if dtype == torch.float32:
+        np.testing.assert_allclose(dl.grad.cpu().numpy(), gin, rtol=1e-5, atol=1e-9)
+    else:
+        assert bf16_ulp_dist(bits(dl.grad), O.f32_to_bf16(gin)).max() <= 1
+
+
+def test_cross_entropy_c3_full_size_properties(no_fallback):
+    """[8192,128256] bf16 N(0,2), 5% ignore_index, mean: rows of the
+    log-softmax sum to 1 in probability, 64 random rows match the oracle,
+    the loss equals the mean of the selected log-probabilities, each grad row
+    sums to ~0, and the target column carries (softmax - 1)/count."""
+    N, V = 8192, 128256
+    g = torch.Generator(device="cpu").manual_seed(0)
+    logits = (torch.randn(N, V, generator=g) * 2).to(torch.bfloat16)
+    t = torch.randint(0, V, (N,), generator=g)
+    t[torch.randperm(N, generator=g)[:410]] = -100
+    dl = dev(logits).requires_grad_()
+    loss = F.cross_entropy(dl, dev(t), ignore_index=-100, reduction="mean")
+    loss.backward()
+    lsm = F.log_softmax(dl.detach(), dim=1)
+    rows = torch.randperm(N, generator=g)[:64]
+    y = lsm.cpu()[rows].float().numpy()
+    ref = O.log_softmax(logits[rows].float().numpy())
+    assert bf16_ulp_dist(O.f32_to_bf16(y), O.f32_to_bf16(ref)).max() <= 1
+    p_sum = torch.exp(lsm.float()).sum(1).cpu().numpy()
+    np.testing.assert_allclose(p_sum, 1.0, rtol=2e-2)
+    keep = (t != -100)
+    sel = lsm.cpu().float()[torch.arange(N)[keep], t[keep]]
+    ref_loss = -sel.double().mean().item()
+    assert abs(loss.float().item() - ref_loss) <= 1e-2 * abs(ref_loss)
+    gsum = dl.grad.float().sum(1).cpu().numpy()
+    assert np.abs(gsum).max() <= 1e-5
+    count = float(keep.sum())
+    gt = dl.grad.cpu().float()[torch.arange(N)[keep], t[keep]].double()
+    expect = (torch.exp(sel.double()) - 1) / count
+    np.testing.assert_allclose(gt.numpy(), expect.numpy(), rtol=3e-2, atol=1e-8)
+
+
+def test_nll_out_of_range_target_raises_at_sync():
+    import torch_supa  # noqa: F401
+    lp = dev(torch.log_softmax(seeded((8, 10), 22), 1))
+    t = dev(torch.tensor([0, 1, 2, 3, 4, 5, 6, 12]))
+    loss = F.nll_loss(lp, t)
+    with pytest.raises(IndexError):
+        loss.item()
+    # the flag is cleared after it is reported
+    assert F.nll_loss(lp, dev(torch.tensor([0] * 8))).item() == pytest.approx(-lp[:, 0].mean().item(), rel=1e-6)
+
+
+# ------------------------------------------------------------ c4 config
+@pytest.mark.parametrize("reduction", ["none", "mean", "sum"])
+def test_c4_full_size_losses(reduction, no_fallback):
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(32, 1048576, generator=g)
+    t = torch.randn(32, 1048576, generator=g)
+    tb = (torch.rand(32, 1048576, generator=g) < 0.3).float()
+    pw = torch.rand(1048576, generator=g) * 1.5 + 0.5
+    dx, dt, dtb, dpw = dev(x), dev(t), dev(tb), dev(pw)
+    cases = [(O.MSE, lambda a, b: F.mse_loss(a, b, reduction=reduction), dt, t, None),
+             (O.SMOOTH_L1, lambda a, b: F.smooth_l1_loss(a, b, reduction=reduction, beta=1.0), dt, t, None),
+             (O.BCE_LOGITS, lambda a, b: F.binary_cross_entropy_with_logits(a, b, pos_weight=dpw,
+                                                                             reduction=reduction), dtb, tb, pw)]
+    for op, fn, dtarget, target, pwn in cases:
+        xg = dx.clone().requires_grad_()
+        loss = fn(xg, dtarget)
+        go = torch.ones_like(loss) if reduction != "none" else dev(seeded((32, 1048576), 30))
+        loss.backward(go)
+        ref = O.loss(op, x.numpy(), target.numpy(), None if pwn is None else pwn.numpy(), reduction=reduction,
+                     beta=1.0)
+        got = loss.detach().cpu().numpy()
+        if reduction == "none":
+            assert np.array_equal(got, ref), op
+        else:
+            np.testing.assert_allclose(got, ref, rtol=1e-5)
+        gref = O.loss_backward(op, go.cpu().numpy(), x.numpy(), target.numpy(),
+                               None if pwn is None else pwn.numpy(), reduction=reduction, beta=1.0)
+        assert np.array_equal(xg.grad.cpu().numpy(), gref), op
+
+
+def test_sum_mean_dims(no_fallback):
+    x = seeded((64, 1000, 3), 31)
+    dx = dev(x)
+    np.testing.assert_allclose(dx.sum().item(), x.double().sum().item(), rtol=1e-5)
+    np.testing.assert_allclose(dx.mean().item(), x.double().mean().item(), rtol=1e-5, atol=1e-7)
+    np.testing.assert_allclose(dx.sum(dim=1).cpu().numpy(), x.double().sum(1).numpy(), rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(dx.mean(dim=(0, 2), keepdim=True).cpu().numpy(),
+                               x.double().mean((0, 2), keepdim=True).numpy(), rtol=1e-5, atol=1e-6)
+    xb = seeded((4096, 33), 32, dtype=torch.bfloat16)
+    np.testing.assert_allclose(dev(xb).sum(dtype=torch.float32).item(), xb.double().sum().item(), rtol=1e-5)
+
+
+# ------------------------------------------------------------ c5 config
+def test_c5_one_layer_fused_adamw_bit_exact(no_fallback):
+    """One decoder layer of the c5 shapes (9 tensors, 202M parameters),
+    torch.optim.AdamW(fused=True) for 10 steps on supa against the oracle."""
+    shapes = [(4096, 4096)] * 4 + [(11008, 4096)] * 2 + [(4096, 11008)] + [(4096,)] * 2
+    g = torch.Generator().manual_seed(0)
+    params = [torch.randn(s, generator=g) * 0.02 for s in shapes]
+    grads = [torch.randn(s, generator=g) * 1e-3 for s in shapes]
+    dp = [dev(p).requires_grad_() for p in params]
+    dg = [dev(x) for x in grads]
+    opt = torch.optim.AdamW(dp, lr=1e-4, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01, fused=True)
+    for _ in range(10):
+        for p, gr in zip(dp, dg):
+            p.grad = gr
+        opt.step()
+    for i, s in enumerate(shapes):
+        hp = params[i].numpy().ravel().copy()
+        hg = grads[i].numpy().ravel().copy()
+        hm, hv = np.zeros_like(hp), np.zeros_like(hp)
+        for step in range(1, 11):
+            O.adamw_step(hp, hg, hm, hv, float(step), 1e-4, 0.9, 0.999, 0.01, 1e-8)
+        assert np.array_equal(dp[i].detach().cpu().numpy().ravel(), hp), i
+        st = opt.state[dp[i]]
+        assert np.array_equal(st["exp_avg"].cpu().numpy().ravel(), hm)
+        assert np.array_equal(st["exp_avg_sq"].cpu().numpy().ravel(), hv)
+        assert st["step"].item() == 10.0
+
+
+def test_foreach_list_and_scalar(no_fallback):
+    shapes = [(4096, 4096), (4096,), (333, 17)]
+    xs = [seeded(s, 40 + i) for i, s in enumerate(shapes)]
+    ys = [seeded(s, 50 + i) for i, s in enumerate(shapes)]
+    dxs, dys = [dev(x) for x in xs], [dev(y) for y in ys]
+    torch._foreach_add_(dxs, dys, alpha=0.5)
+    torch._foreach_mul_(dxs, 0.5)
+    for dx, x, y in zip(dxs, xs, ys):
+        ref = O.binary(O.MUL, O.binary(O.ADD, x.numpy(), y.numpy(), 0.5), np.float32(0.5))
+        assert np.array_equal(dx.cpu().numpy(), ref)
+    outs = torch._foreach_mul(dxs, dys)
+    for o, dx, dy in zip(outs, dxs, dys):
+        assert torch.equal(o.cpu(), dx.cpu() * dy.cpu())
+
+
+def test_allocator_stats_and_reuse():
+    import torch_supa  # noqa: F401
+    torch.supa.synchronize()
+    before = torch.supa.memory_stats()
+    x = torch.empty(1 << 20, device="supa")
+    mid = torch.supa.memory_allocated()
+    assert mid >= before["allocated_bytes"] + (1 << 22)
+    mallocs = torch.supa.memory_stats()["num_device_mallocs"]
+    del x
+    y = torch.empty(1 << 20, device="supa")
+    assert torch.supa.memory_stats()["num_device_mallocs"] == mallocs  # served from the cache
+    assert torch.supa.memory_allocated() == mid
+    del y
+    torch.supa.empty_cache()
+    assert torch.supa.memory_reserved() <= torch.supa.memory_stats()["reserved_bytes"]

@@ -1,0 +1,113 @@
+"""Pins the oracle's float32 primitives (oracle/oracle_math.h) against
+double-precision math: random dense samples, edge values and identities.
+
+The same polynomials run on the device (csrc/kernels/devmath.h), so these
+bounds are also the accuracy of the device primitives."""
+import math
+
+import numpy as np
+import pytest
+from scipy import special
+
+import oracle as O
+from helpers import sample_f32, ulp_vs_exact
+
+EDGES = np.array([0.0, -0.0, 1e-45, -1e-45, 1e-38, 1.17549435e-38, 0.5, 1.0, 2.0, 88.7, 88.72283, 89.0,
+                  -87.3, -103.9, -104.0, 3.925, 0.921875, 0.55, 9.01, 20.0, -20.0, np.inf, -np.inf, np.nan],
+                 np.float32)
+
+
+@pytest.mark.parametrize(
+    "op, ref, bound, lo, hi",
+    [
+        (O.EXP, np.exp, 1.01, -104.0, 89.0),
+        (O.LOG, np.log, 0.94, 1e-30, 1e30),
+        (O.ERF, special.erf, 1.12, -6.0, 6.0),
+        (O.TANH, np.tanh, 1.47, -12.0, 12.0),
+    ],
+)
+def test_primitive_accuracy(op, ref, bound, lo, hi):
+    if op == O.LOG:
+        rng = np.random.default_rng(1)
+        x = np.exp(rng.uniform(np.log(1e-44), np.log(3e38), 1 << 21)).astype(np.float32)
+        x = np.concatenate([x, rng.uniform(0.5, 2.0, 1 << 20).astype(np.float32)])
+    else:
+        x = sample_f32(1 << 21, seed=op, lo=lo, hi=hi)
+    got = O.unary(op, x)
+    with np.errstate(all="ignore"):
+        exact = ref(x.astype(np.float64))
+    err = ulp_vs_exact(got, exact)
+    assert err.max() <= bound, (op, float(x[np.argmax(err)]), float(err.max()))
+
+
+def test_primitive_edges():
+    x = EDGES
+    with np.errstate(all="ignore"):
+        for op, ref in [(O.EXP, np.exp), (O.TANH, np.tanh), (O.ERF, special.erf)]:
+            got = O.unary(op, x)
+            ex = ref(x.astype(np.float64))
+            np.testing.assert_array_equal(np.isnan(got), np.isnan(ex))
+            fin = ~np.isnan(ex)
+            assert ulp_vs_exact(got[fin], ex[fin]).max() <= 1.5
+    # log specials: log(0) = -inf, log(<0) = nan, log(inf) = inf, log(1) = 0
+    got = O.unary(O.LOG, np.array([0.0, -0.0, -1.0, np.inf, 1.0, np.nan], np.float32))
+    assert got[0] == -np.inf and got[1] == -np.inf and np.isnan(got[2]) and got[3] == np.inf
+    assert got[4] == 0.0 and np.isnan(got[5])
+    # exp(0) == 1 exactly (the BCE-with-logits restatement relies on it)
+    assert O.unary(O.EXP, np.array([0.0, -0.0], np.float32)).tolist() == [1.0, 1.0]
+
+
+def test_activation_identities():
+    x = np.linspace(-8, 8, 200001, dtype=np.float32)
+    # odd functions
+    np.testing.assert_array_equal(O.unary(O.ERF, -x), -O.unary(O.ERF, x))
+    np.testing.assert_array_equal(O.unary(O.TANH, -x), -O.unary(O.TANH, x))
+    # silu(x) - silu(-x) = x and gelu(x) - gelu(-x) = x, up to float rounding
+    for op in (O.SILU, O.GELU, O.GELU_TANH):
+        d = O.unary(op, x).astype(np.float64) - O.unary(op, -x).astype(np.float64)
+        np.testing.assert_allclose(d, x, rtol=4e-7, atol=1e-7)
+    # fixed points
+    z = np.zeros(1, np.float32)
+    assert O.unary(O.SIGMOID, z)[0] == 0.5
+    for op in (O.GELU, O.GELU_TANH, O.SILU, O.TANH, O.ERF):
+        assert O.unary(op, z)[0] == 0.0
+
+
+@pytest.mark.parametrize("op, exact", [
+    (O.SILU, lambda x: x / (1 + np.exp(-x))),
+    (O.SIGMOID, lambda x: 1 / (1 + np.exp(-x))),
+])
+def test_activation_vs_exact(op, exact):
+    """silu / sigmoid: within 3 ulp of the exact function wherever the exact
+    value is at least 1e-30 in magnitude."""
+    x = np.random.default_rng(7).standard_normal(1 << 20).astype(np.float32) * 3
+    got = O.unary(op, x)
+    ex = exact(x.astype(np.float64))
+    keep = np.abs(ex) > 1e-30
+    assert ulp_vs_exact(got[keep], ex[keep]).max() <= 3.0
+
+
+def test_gelu_tanh_vs_exact():
+    """gelu 'tanh' = x / (1 + exp(v)), v = -2b(x + k x^3) formed in float32:
+    the few-ulp relative rounding of v is amplified by |v| in the result, so
+    the error against the exact function is at most 3 (1 + |v|) ulp."""
+    x = np.random.default_rng(7).standard_normal(1 << 20).astype(np.float32) * 3
+    xd = x.astype(np.float64)
+    v = -2 * math.sqrt(2 / math.pi) * (xd + 0.044715 * xd ** 3)
+    ex = xd / (1 + np.exp(v))
+    got = O.unary(O.GELU_TANH, x)
+    keep = np.abs(ex) > 1e-30
+    err = ulp_vs_exact(got[keep], ex[keep])
+    assert np.all(err <= 3.0 * (1.0 + np.abs(v[keep])))
+
+
+def test_gelu_none_error_is_the_reference_formula_conditioning():
+    """gelu 'none' evaluates the reference formula x*0.5*(1+erf(x/sqrt2)) in
+    float32; its error against the exact function is bounded by the erf
+    rounding scaled by |0.5 x|: |err| <= 2 ulp(y) + |0.5 x| * 2^-23."""
+    x = np.random.default_rng(3).standard_normal(1 << 20).astype(np.float32) * 2
+    got = O.unary(O.GELU, x).astype(np.float64)
+    xd = x.astype(np.float64)
+    ex = 0.5 * xd * special.erfc(-xd / math.sqrt(2))
+    ulp = np.ldexp(1.0, np.maximum(np.frexp(np.abs(ex))[1] - 24, -149))
+    assert np.all(np.abs(got - ex) <= 2 * ulp + np.abs(0.5 * xd) * 2.0 ** -23)

@@ -1,0 +1,312 @@
+"""Pins the oracle against the upstream aten CPU kernels of torch 2.10.0 --
+the kernels the reference's operator library is built from and the producer
+of the reference outputs for this path -- plus closed forms and invariants.
+
+Tolerances are the path's: bit-exact for IEEE add/mul/div, transcendental
+activations within 2 float32 ulp where the formula is well conditioned (the
+CPU's own approximation error is stated where it is not), losses and
+reductions rtol 1e-5 float32 / 1e-2 bfloat16."""
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import oracle as O
+from helpers import bf16_ulp_dist, f32_ulp_dist
+
+SHAPES = [(16,), (1024, 512), (1023, 511), (1025, 513), (1028, 2135)]
+
+
+def randn(shape, seed=0, scale=1.0, dtype=torch.float32):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(shape, generator=g) * scale).to(dtype)
+
+
+# ------------------------------------------------------------- binary ops
+@pytest.mark.parametrize("shape", SHAPES)
+def test_binary_bit_exact_f32(shape):
+    a, b = randn(shape, 0), randn(shape, 1)
+    an, bn = a.numpy(), b.numpy()
+    for op, ref in [(O.ADD, a + b), (O.MUL, a * b), (O.DIV, a / b),
+                    (O.DIV_TRUNC, torch.div(a, b, rounding_mode="trunc")),
+                    (O.DIV_FLOOR, torch.div(a, b, rounding_mode="floor"))]:
+        got = O.binary(op, an, bn)
+        assert np.array_equal(got.view(np.int32), ref.numpy().view(np.int32)), op
+
+
+def test_c1_config_bit_exact():
+    """[4096,4096] N(0,1) from seed 0, add/mul."""
+    g = torch.Generator().manual_seed(0)
+    a = torch.randn(4096, 4096, generator=g)
+    b = torch.randn(4096, 4096, generator=g)
+    assert np.array_equal(O.binary(O.ADD, a.numpy(), b.numpy()), torch.add(a, b, alpha=1).numpy())
+    assert np.array_equal(O.binary(O.MUL, a.numpy(), b.numpy()), torch.mul(a, b).numpy())
+
+
+def test_add_alpha_and_broadcast():
+    a, b = randn((64, 256), 2), randn((256,), 3)
+    for alpha in (1.0, 2.5, -0.75):
+        got = O.binary(O.ADD, a.numpy(), b.numpy(), alpha)
+        ref = torch.add(a, b, alpha=alpha).numpy()
+        assert np.array_equal(got, ref), alpha
+
+
+def test_bf16_binary_matches_cpu():
+    a, b = randn((1024, 512), 4, dtype=torch.bfloat16), randn((1024, 512), 5, dtype=torch.bfloat16)
+    af, bf = a.float().numpy(), b.float().numpy()
+    for op, ref in [(O.ADD, a + b), (O.MUL, a * b), (O.DIV, a / b)]:
+        got = O.f32_to_bf16(O.binary(op, af, bf))
+        assert np.array_equal(got, ref.view(torch.int16).numpy().view(np.uint16)), op
+
+
+def test_mixed_bf16_f32_promotion():
+    """c2's add: bf16 x + f32 bias -> f32 (the bf16 value widens exactly)."""
+    x = randn((8, 64, 128), 6, dtype=torch.bfloat16)
+    bias = randn((128,), 7) * 0.02
+    ref = x + bias
+    assert ref.dtype == torch.float32
+    got = O.binary(O.ADD, O.bf16_to_f32(x.view(torch.int16).numpy().view(np.uint16)), bias.numpy())
+    assert np.array_equal(got, ref.numpy())
+
+
+def test_integer_ops_match_cpu():
+    g = torch.Generator().manual_seed(8)
+    a = torch.randint(-1000, 1000, (4096,), generator=g)
+    b = torch.randint(1, 50, (4096,), generator=g) * torch.where(torch.rand(4096, generator=g) < 0.5, -1, 1)
+    for op, ref in [(O.ADD, a + b), (O.MUL, a * b), (O.DIV_TRUNC, torch.div(a, b, rounding_mode="trunc")),
+                    (O.DIV_FLOOR, torch.div(a, b, rounding_mode="floor"))]:
+        np.testing.assert_array_equal(O.binary_int(op, a.numpy(), b.numpy()), ref.numpy())
+
+
+# ----------------------------------------------------------- activations
+def test_well_conditioned_activations_within_2ulp():
+    x = randn((1 << 20,), 10)
+    for op, ref in [(O.SILU, F.silu(x)), (O.SIGMOID, torch.sigmoid(x)), (O.TANH, torch.tanh(x))]:
+        assert f32_ulp_dist(O.unary(op, x.numpy()), ref.numpy()).max() <= 2, op
+
+
+def test_gelu_vs_cpu():
+    """gelu: float32 formula of the reference.  The CPU kernel evaluates erf
+    with the Abramowitz-Stegun 7.1.26 approximation (ATen vec256 erf, abs
+    error ~1.5e-7), so the agreement is 2 ulp plus that error scaled by 0.5|x|;
+    'tanh': the CPU's 1 + tanh(u) cancels for u << 0 (bounded by |x| 2^-24)."""
+    x = randn((1 << 20,), 11)
+    xn = x.numpy().astype(np.float64)
+    for approx, op, slope in [("none", O.GELU, 1e-6 * 0.5), ("tanh", O.GELU_TANH, 2.0 ** -24)]:
+        ref = F.gelu(x, approximate=approx).numpy()
+        got = O.unary(op, x.numpy())
+        ulp = np.ldexp(1.0, np.maximum(np.frexp(np.abs(ref))[1] - 24, -149))
+        assert np.all(np.abs(got.astype(np.float64) - ref) <= 2 * ulp + slope * np.abs(xn)), approx
+
+
+@pytest.mark.parametrize("name", ["gelu", "gelu_tanh", "silu", "sigmoid", "tanh"])
+def test_activation_backward_vs_cpu(name):
+    x = randn((1 << 18,), 12).requires_grad_()
+    dy = randn((1 << 18,), 13)
+    fn = {"gelu": F.gelu, "gelu_tanh": lambda t: F.gelu(t, approximate="tanh"), "silu": F.silu,
+          "sigmoid": torch.sigmoid, "tanh": torch.tanh}[name]
+    op = {"gelu": O.GELU, "gelu_tanh": O.GELU_TANH, "silu": O.SILU, "sigmoid": O.SIGMOID, "tanh": O.TANH}[name]
+    y = fn(x)
+    y.backward(dy)
+    inp = y.detach().numpy() if name in ("sigmoid", "tanh") else x.detach().numpy()
+    got = O.unary_backward(op, dy.numpy(), inp)
+    np.testing.assert_array_less(np.abs(got - x.grad.numpy()), 1e-6 * np.abs(dy.numpy()) + 1e-30)
+
+
+# ---------------------------------------------------- log_softmax / nll / CE
+@pytest.mark.parametrize("shape", [(4, 10), (64, 1000), (3, 128256)])
+def test_log_softmax_f32(shape):
+    x = randn(shape, 20, 2.0)
+    np.testing.assert_allclose(O.log_softmax(x.numpy()), F.log_softmax(x, -1).numpy(), rtol=1e-5, atol=1e-5)
+
+
+def test_log_softmax_bf16_within_one_ulp():
+    x = randn((16, 128256), 21, 2.0, torch.bfloat16)
+    ref = F.log_softmax(x, -1).view(torch.int16).numpy().view(np.uint16)
+    got = O.f32_to_bf16(O.log_softmax(x.float().numpy()))
+    assert bf16_ulp_dist(got, ref).max() <= 1
+
+
+def test_log_softmax_invariants():
+    x = randn((32, 5000), 22, 3.0).numpy()
+    y = O.log_softmax(x)
+    lse = np.log(np.exp(y.astype(np.float64)).sum(-1))
+    np.testing.assert_allclose(lse, 0.0, atol=2e-6)
+    # uniform logits: every entry is -log(V)
+    V = 128256
+    u = O.log_softmax(np.zeros((2, V), np.float32))
+    np.testing.assert_allclose(u, -math.log(V), rtol=1e-7)
+    # backward rows sum to sum(g) - sum(softmax)*sum(g) = 0
+    g = randn((32, 5000), 23).numpy()
+    gi = O.log_softmax_backward(g, y)
+    np.testing.assert_allclose(gi.astype(np.float64).sum(-1), 0.0, atol=5e-5)
+
+
+@pytest.mark.parametrize("reduction", ["mean", "sum", "none"])
+@pytest.mark.parametrize("weighted", [False, True])
+def test_nll_and_cross_entropy_vs_cpu(reduction, weighted):
+    N, C = 256, 1000
+    logits = randn((N, C), 30, 2.0)
+    g = torch.Generator().manual_seed(31)
+    t = torch.randint(0, C, (N,), generator=g)
+    t[torch.randperm(N, generator=g)[:13]] = -100
+    w = (torch.rand(C, generator=g) + 0.5) if weighted else None
+    lg = logits.clone().requires_grad_()
+    loss = F.cross_entropy(lg, t, weight=w, ignore_index=-100, reduction=reduction)
+    go = torch.ones_like(loss) if reduction != "none" else randn((N,), 32)
+    loss.backward(go)
+    lp = O.log_softmax(logits.numpy())
+    out, tw = O.nll_loss(lp, t.numpy(), None if w is None else w.numpy(), reduction, -100)
+    np.testing.assert_allclose(out, loss.detach().numpy(), rtol=1e-5, atol=1e-6)
+    gnll = O.nll_loss_backward(go.numpy(), t.numpy(), N, C, tw, None if w is None else w.numpy(), reduction, -100)
+    gin = O.log_softmax_backward(gnll, lp)
+    np.testing.assert_allclose(gin, lg.grad.numpy(), rtol=1e-5, atol=1e-7)
+
+
+def test_nll_closed_forms():
+    V = 128256
+    lp = O.log_softmax(np.zeros((4, V), np.float32))
+    out, tw = O.nll_loss(lp, np.array([0, 5, 7, 9]), None, "mean", -100)
+    assert abs(float(out) - math.log(V)) < 1e-5 and float(tw) == 4.0
+    # every row ignored: mean is NaN (0/0), sum is 0
+    out, tw = O.nll_loss(lp, np.full(4, -100), None, "mean", -100)
+    assert np.isnan(out) and float(tw) == 0.0
+    out, _ = O.nll_loss(lp, np.full(4, -100), None, "sum", -100)
+    assert float(out) == 0.0
+    # backward: one nonzero per non-ignored row, equal to -1/count
+    gi = O.nll_loss_backward(np.ones(1, np.float32), np.array([1, -100, 3]), 3, 10, 2.0, None, "mean", -100)
+    assert (gi != 0).sum() == 2 and gi[0, 1] == -0.5 and gi[2, 3] == -0.5 and not gi[1].any()
+    with pytest.raises(IndexError):
+        O.nll_loss(lp, np.array([0, V, 1, 2]), None, "mean", -100)
+
+
+def test_cross_entropy_bf16_decomposition_vs_cpu():
+    """c3's semantics at a small row count: bf16 logits, 5% ignore_index,
+    mean.  Each decomposed op is compared on the reference's own inputs (the
+    backward consumes the forward's rounded output, so a 1-ulp difference in a
+    forward element would otherwise be amplified by exp): _log_softmax within
+    1 bf16 ulp, nll_loss within rtol 1e-2, nll_loss_backward bit-exact (the
+    bf16 total_weight enters rounded), _log_softmax_backward within 1 ulp."""
+    N, V = 64, 4096
+    logits = randn((N, V), 33, 2.0, torch.bfloat16)
+    g = torch.Generator().manual_seed(34)
+    t = torch.randint(0, V, (N,), generator=g)
+    t[torch.randperm(N, generator=g)[:3]] = -100
+    lg = logits.clone().requires_grad_()
+    lsm = F.log_softmax(lg, -1)
+    lsm.retain_grad()
+    loss = F.nll_loss(lsm, t, ignore_index=-100)
+    loss.backward()
+    bits = lambda x: x.detach().view(torch.int16).numpy().view(np.uint16)
+    lp = O.log_softmax(logits.float().numpy())
+    assert bf16_ulp_dist(O.f32_to_bf16(lp), bits(lsm)).max() <= 1
+    y = lsm.detach().float().numpy()
+    out, tw = O.nll_loss(y, t.numpy(), None, "mean", -100)
+    assert abs(float(out) - loss.float().item()) <= 1e-2 * abs(loss.float().item())
+    _, tw_ref = torch.ops.aten.nll_loss_forward(lsm.detach(), t, None, 1, -100)
+    assert float(O.round_bf16(tw)) == tw_ref.float().item()
+    gnll = O.nll_loss_backward(np.ones(1, np.float32), t.numpy(), N, V, tw_ref.float().item(), None, "mean", -100,
+                               bf16=True)
+    assert np.array_equal(O.f32_to_bf16(gnll), bits(lsm.grad))
+    gin = O.f32_to_bf16(O.log_softmax_backward(lsm.grad.float().numpy(), y))
+    assert bf16_ulp_dist(gin, bits(lg.grad)).max() <= 1
+
+
+# ------------------------------------------------------------------ losses
+@pytest.mark.parametrize("reduction", ["none", "mean", "sum"])
+def test_regression_losses_vs_cpu(reduction):
+    x, t = randn((32, 4096), 40), randn((32, 4096), 41)
+    for op, fn in [(O.MSE, lambda a, b: F.mse_loss(a, b, reduction=reduction)),
+                   (O.SMOOTH_L1, lambda a, b: F.smooth_l1_loss(a, b, reduction=reduction, beta=1.0))]:
+        xg = x.clone().requires_grad_()
+        ref = fn(xg, t)
+        go = torch.ones_like(ref) if reduction != "none" else randn(ref.shape, 42)
+        ref.backward(go)
+        got = O.loss(op, x.numpy(), t.numpy(), reduction=reduction, beta=1.0)
+        np.testing.assert_allclose(got, ref.detach().numpy(), rtol=1e-5, atol=1e-7)
+        gg = O.loss_backward(op, go.numpy(), x.numpy(), t.numpy(), reduction=reduction, beta=1.0)
+        np.testing.assert_allclose(gg, xg.grad.numpy(), rtol=1e-5, atol=1e-12)
+
+
+@pytest.mark.parametrize("reduction", ["none", "mean", "sum"])
+@pytest.mark.parametrize("with_pw", [False, True])
+def test_bce_with_logits_vs_cpu(reduction, with_pw):
+    g = torch.Generator().manual_seed(43)
+    x = torch.randn(32, 4096, generator=g)
+    tb = (torch.rand(32, 4096, generator=g) < 0.3).float()
+    pw = torch.rand(4096, generator=g) * 1.5 + 0.5 if with_pw else None
+    xg = x.clone().requires_grad_()
+    ref = F.binary_cross_entropy_with_logits(xg, tb, pos_weight=pw, reduction=reduction)
+    go = torch.ones_like(ref) if reduction != "none" else torch.randn(ref.shape, generator=g)
+    ref.backward(go)
+    got = O.loss(O.BCE_LOGITS, x.numpy(), tb.numpy(), None if pw is None else pw.numpy(), reduction=reduction)
+    np.testing.assert_allclose(got, ref.detach().numpy(), rtol=1e-5, atol=1e-6)
+    gg = O.loss_backward(O.BCE_LOGITS, go.numpy(), x.numpy(), tb.numpy(), None if pw is None else pw.numpy(),
+                         reduction=reduction)
+    np.testing.assert_allclose(gg, xg.grad.numpy(), rtol=1e-5, atol=1e-9)
+
+
+def test_loss_closed_forms():
+    x = np.random.default_rng(44).standard_normal(1000).astype(np.float32)
+    assert float(O.loss(O.MSE, x, x, reduction="sum")) == 0.0
+    z = np.zeros(8, np.float32)
+    t = np.array([0, 1] * 4, np.float32)
+    pw = np.full(8, 3.0, np.float32)
+    bce = O.loss(O.BCE_LOGITS, z, t, reduction="none")
+    np.testing.assert_allclose(bce, math.log(2), rtol=1e-7)
+    bce = O.loss(O.BCE_LOGITS, z, t, pw, reduction="none")
+    np.testing.assert_allclose(bce, np.where(t == 1, 3 * math.log(2), math.log(2)), rtol=1e-7)
+    # smooth_l1 is continuous at |d| = beta
+    b = np.float32(1.0)
+    eps = np.float32(1e-6)
+    lo = O.loss(O.SMOOTH_L1, np.array([b - eps]), np.zeros(1, np.float32), reduction="none")
+    hi = O.loss(O.SMOOTH_L1, np.array([b + eps]), np.zeros(1, np.float32), reduction="none")
+    assert abs(float(lo[0]) - float(hi[0])) < 1e-5
+
+
+# ----------------------------------------------------------------- AdamW
+def test_adamw_first_step_closed_form():
+    rng = np.random.default_rng(50)
+    p = (rng.standard_normal(4096) * 0.02).astype(np.float32)
+    g = (rng.standard_normal(4096) * 1e-3).astype(np.float32)
+    m = np.zeros_like(p)
+    v = np.zeros_like(p)
+    p0 = p.astype(np.float64).copy()
+    lr, b1, b2, wd, eps = 1e-4, 0.9, 0.999, 0.01, 1e-8
+    O.adamw_step(p, g, m, v, 1.0, lr, b1, b2, wd, eps)
+    gd = g.astype(np.float64)
+    np.testing.assert_allclose(m, (1 - b1) * gd, rtol=1e-6)
+    np.testing.assert_allclose(v, (1 - b2) * gd * gd, rtol=1e-6)
+    expect = p0 * (1 - lr * wd) - lr * gd / (np.abs(gd) + eps)
+    np.testing.assert_allclose(p, expect, rtol=1e-6, atol=1e-9)
+
+
+def test_adamw_ten_steps_vs_cpu_and_restart():
+    shapes = [(256, 256), (512, 256), (256,)]
+    g = torch.Generator().manual_seed(51)
+    params = [torch.randn(s, generator=g) * 0.02 for s in shapes]
+    grads = [torch.randn(s, generator=g) * 1e-3 for s in shapes]
+    tp = [p.clone().requires_grad_() for p in params]
+    opt = torch.optim.AdamW(tp, lr=1e-4, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01, fused=True)
+    for _ in range(10):
+        for t, gr in zip(tp, grads):
+            t.grad = gr.clone()
+        opt.step()
+    for i in range(len(shapes)):
+        p = params[i].numpy().copy().ravel()
+        gr = grads[i].numpy().copy().ravel()
+        m, v = np.zeros_like(p), np.zeros_like(p)
+        for step in range(1, 11):
+            O.adamw_step(p, gr, m, v, float(step), 1e-4, 0.9, 0.999, 0.01, 1e-8)
+        np.testing.assert_allclose(p, tp[i].detach().numpy().ravel(), rtol=1e-5, atol=1e-9)
+        # 10 steps == 5 steps, then a state round trip, then 5 more
+        p2 = params[i].numpy().copy().ravel()
+        m2, v2 = np.zeros_like(p2), np.zeros_like(p2)
+        for step in range(1, 6):
+            O.adamw_step(p2, gr, m2, v2, float(step), 1e-4, 0.9, 0.999, 0.01, 1e-8)
+        p2, m2, v2 = (np.frombuffer(a.tobytes(), np.float32).copy() for a in (p2, m2, v2))
+        for step in range(6, 11):
+            O.adamw_step(p2, gr, m2, v2, float(step), 1e-4, 0.9, 0.999, 0.01, 1e-8)
+        assert np.array_equal(p2, p) and np.array_equal(m2, m) and np.array_equal(v2, v)

@@ -46,6 +46,19 @@ AllocatorStats allocator_stats(c10::DeviceIndex d);
 void allocator_reset_peak(c10::DeviceIndex d);
 void allocator_empty_cache();
 
+// Per-device scratch owned by the runtime: allocated and zeroed once, never
+// returned to the caching allocator.  Holds the reduction workspace (whose
+// counter every reduction leaves at zero) and the device error flag.
+struct DeviceScratch {
+  void* reduce_ws = nullptr;
+  int64_t reduce_ws_bytes = 0;
+  int32_t* error_flag = nullptr;
+};
+const DeviceScratch& device_scratch(c10::DeviceIndex d);
+// Raises (and clears) a pending device-side error, e.g. an out-of-range
+// nll_loss target.  Called at every host synchronisation point.
+void check_device_errors(c10::DeviceIndex d);
+
 // CPU fallback bookkeeping (the fallback never runs for an op this library
 // registers; tests assert that with these counters).
 void set_cpu_fallback_enabled(bool on);

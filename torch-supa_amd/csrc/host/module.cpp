@@ -70,6 +70,13 @@ float event_elapsed_ms(uintptr_t a, uintptr_t b) {
 }
 void event_destroy(uintptr_t e) { (void)hipEventDestroy(reinterpret_cast<hipEvent_t>(e)); }
 
+// Device-to-device byte copy on the supa stream (used by harnesses that build
+// inputs with another device API in the same process).
+void memcpy_d2d(uintptr_t dst, uintptr_t src, int64_t nbytes) {
+  SUPA_HIP_CHECK(hipMemcpyAsync(reinterpret_cast<void*>(dst), reinterpret_cast<const void*>(src), (size_t)nbytes,
+                                hipMemcpyDeviceToDevice, supa::current_stream(supa::current_device())));
+}
+
 }  // namespace
 
 PYBIND11_MODULE(_C, m) {
@@ -92,4 +99,5 @@ PYBIND11_MODULE(_C, m) {
   m.def("event_synchronize", &event_synchronize);
   m.def("event_elapsed_ms", &event_elapsed_ms);
   m.def("event_destroy", &event_destroy);
+  m.def("memcpy_d2d", &memcpy_d2d);
 }

@@ -240,6 +240,7 @@ at::Tensor copy_from(const at::Tensor& self, const at::Tensor& dst, bool /*non_b
   }
   // device -> host
   TORCH_CHECK(dst.device().is_cpu(), "supa copy: unsupported destination device ", dst.device());
+  check_device_errors(self.device().index());
   at::Tensor src = self;
   if (!src.is_contiguous()) {
     at::Tensor tmp = empty_supa(src.sizes(), src.scalar_type(), src.device().index());
@@ -268,6 +269,7 @@ c10::Scalar local_scalar_dense(const at::Tensor& self) {
   TORCH_CHECK(self.numel() == 1, "a Tensor with ", self.numel(), " elements cannot be converted to Scalar");
   at::Tensor h = at::empty({}, self.options().device(at::kCPU));
   SUPA_HIP_CHECK(hipMemcpy(h.data_ptr(), self.data_ptr(), self.dtype().itemsize(), hipMemcpyDeviceToHost));
+  check_device_errors(self.device().index());
   return h.item();
 }
 
@@ -525,6 +527,9 @@ SUPA_UNARY(exp, SUPA_AMD_EXP, UKind::IntToFloat)
 SUPA_UNARY(log, SUPA_AMD_LOG, UKind::IntToFloat)
 SUPA_UNARY(erf, SUPA_AMD_ERF, UKind::IntToFloat)
 SUPA_UNARY(neg, SUPA_AMD_NEG, UKind::Any)
+SUPA_UNARY(reciprocal, SUPA_AMD_RECIPROCAL, UKind::IntToFloat)
+SUPA_UNARY(abs, SUPA_AMD_ABS, UKind::Any)
+SUPA_UNARY(sqrt, SUPA_AMD_SQRT, UKind::IntToFloat)
 #undef SUPA_UNARY
 
 at::Tensor relu(const at::Tensor& s) {
@@ -622,6 +627,15 @@ TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
   m.impl("neg", TORCH_FN(u_neg));
   m.impl("neg_", TORCH_FN(u_neg_));
   m.impl("neg.out", TORCH_FN(u_neg_out));
+  m.impl("reciprocal", TORCH_FN(u_reciprocal));
+  m.impl("reciprocal_", TORCH_FN(u_reciprocal_));
+  m.impl("reciprocal.out", TORCH_FN(u_reciprocal_out));
+  m.impl("abs", TORCH_FN(u_abs));
+  m.impl("abs_", TORCH_FN(u_abs_));
+  m.impl("abs.out", TORCH_FN(u_abs_out));
+  m.impl("sqrt", TORCH_FN(u_sqrt));
+  m.impl("sqrt_", TORCH_FN(u_sqrt_));
+  m.impl("sqrt.out", TORCH_FN(u_sqrt_out));
   m.impl("relu", TORCH_FN(relu));
   m.impl("relu_", TORCH_FN(relu_));
 }

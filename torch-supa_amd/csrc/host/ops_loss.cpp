@@ -1,0 +1,485 @@
+// PrivateUse1 registrations of the loss path: sum/mean reductions,
+// mse_loss / smooth_l1_loss / binary_cross_entropy_with_logits (forward with
+// fused reductions, and the mse / smooth_l1 gradients), _log_softmax and its
+// backward, nll_loss forward / backward.
+//
+// cross_entropy_loss is deliberately not registered: it stays
+// CompositeImplicitAutograd and decomposes into _log_softmax + nll_loss, the
+// path the reference takes for every non-fp32 input
+// (torch_supa/csrc/aten/ops/CrossEntropyLoss.cpp:23-52).
+// binary_cross_entropy_with_logits is registered, as the reference registers
+// it (supa_native_functions.yaml:59-61; BinaryCrossEntropyWithLogits.cpp:23-73);
+// its backward is the autograd formula's op sequence on the kernels above.
+#include <ATen/WrapDimUtils.h>
+#include <ATen/native/Resize.h>
+#include <ATen/native/TypeProperties.h>
+#include <c10/core/ScalarType.h>
+#include <torch/library.h>
+
+#include "common.h"
+#include "ew_apply.h"
+#include "planner.h"
+
+namespace supa {
+namespace {
+
+constexpr int64_t kNone = 0, kMean = 1, kSum = 2;  // at::Reduction
+
+int reduction_code(int64_t r) {
+  TORCH_CHECK(r == kNone || r == kMean || r == kSum, "invalid reduction enum: ", r);
+  return r == kNone ? SUPA_AMD_REDUCTION_NONE : (r == kMean ? SUPA_AMD_REDUCTION_MEAN : SUPA_AMD_REDUCTION_SUM);
+}
+
+bool is_float_dtype(c10::ScalarType t) {
+  return t == at::kFloat || t == at::kBFloat16 || t == at::kHalf || t == at::kDouble;
+}
+
+// Full reduction of f(inputs) over the broadcast iteration space into the
+// one-element `out`, through a reduction entry point of the C ABI.
+void reduce_apply(const at::Tensor& out, const std::vector<at::Tensor>& ins, c10::ScalarType common,
+                  const std::function<int(const supa_amd_ew_desc*, void*, int64_t, void*)>& launch, const char* name) {
+  std::vector<const at::Tensor*> ts{&out};
+  for (const auto& t : ins) ts.push_back(&t);
+  const c10::DeviceIndex dev = common_device(ts, name);
+  std::vector<PlanOperand> pops(1 + ins.size());
+  pops[0].is_output = true;
+  pops[0].allocate = true;
+  for (size_t i = 0; i < ins.size(); ++i) {
+    pops[1 + i].sizes = ins[i].sizes().vec();
+    pops[1 + i].strides = ins[i].strides().vec();
+  }
+  Plan plan;
+  try {
+    plan = make_plan(pops);
+  } catch (const std::invalid_argument& e) {
+    TORCH_CHECK(false, name, ": ", e.what());
+  }
+  TORCH_CHECK((int)plan.it_sizes.size() <= SUPA_AMD_MAX_DIMS, name, ": too many dimensions");
+  supa_amd_ew_desc d{};
+  d.ndim = (int32_t)plan.it_sizes.size();
+  d.noperands = (int32_t)(1 + ins.size());
+  d.common_dtype = dtype_code(common);
+  for (int i = 0; i < d.ndim; ++i) d.sizes[i] = plan.it_sizes[i];
+  d.op[0].data = out.data_ptr();
+  d.op[0].dtype = dtype_code(out.scalar_type());
+  for (size_t k = 0; k < ins.size(); ++k) {
+    supa_amd_operand& o = d.op[1 + k];
+    o.data = ins[k].data_ptr();
+    o.dtype = dtype_code(ins[k].scalar_type());
+    for (int i = 0; i < d.ndim; ++i) o.strides[i] = plan.it_strides[1 + k][i];
+  }
+  const DeviceScratch& s = device_scratch(dev);
+  const auto prev = current_device();
+  if (prev != dev) set_device(dev);
+  const int rc = launch(&d, s.reduce_ws, s.reduce_ws_bytes, current_stream(dev));
+  if (prev != dev) set_device(prev);
+  check_status(rc, name);
+}
+
+at::Tensor to_dtype(const at::Tensor& t, c10::ScalarType dt) { return t.scalar_type() == dt ? t : t.to(dt); }
+
+// ------------------------------------------------------------ sum / mean
+std::vector<int64_t> reduce_dims(const at::Tensor& self, at::OptionalIntArrayRef dim) {
+  std::vector<int64_t> dims;
+  const int64_t nd = self.dim();
+  if (!dim.has_value() || dim->empty()) {
+    for (int64_t i = 0; i < nd; ++i) dims.push_back(i);
+  } else {
+    for (int64_t d : *dim) dims.push_back(at::maybe_wrap_dim(d, std::max<int64_t>(nd, 1)));
+    std::sort(dims.begin(), dims.end());
+    dims.erase(std::unique(dims.begin(), dims.end()), dims.end());
+  }
+  if (nd == 0) dims.clear();
+  return dims;
+}
+
+at::Tensor& sum_mean_into(const at::Tensor& self, at::OptionalIntArrayRef dim, bool keepdim,
+                          std::optional<c10::ScalarType> dtype, bool mean, at::Tensor& out, const char* name) {
+  c10::ScalarType acc_dt = dtype.value_or(self.scalar_type());
+  if (!dtype && at::isIntegralType(self.scalar_type(), true)) acc_dt = at::kLong;
+  TORCH_CHECK(is_float_dtype(acc_dt) && is_float_dtype(self.scalar_type()), name,
+              ": supa implements floating-point reductions only (got ", self.scalar_type(), " -> ", acc_dt, ")");
+  const std::vector<int64_t> dims = reduce_dims(self, dim);
+  std::vector<int64_t> oshape;
+  std::vector<bool> red(self.dim(), false);
+  for (int64_t d : dims) red[d] = true;
+  for (int64_t i = 0; i < self.dim(); ++i) {
+    if (!red[i]) oshape.push_back(self.size(i));
+    else if (keepdim) oshape.push_back(1);
+  }
+  if (out.defined()) {
+    TORCH_CHECK(out.scalar_type() == acc_dt, name, ": expected out dtype ", acc_dt, " but got ", out.scalar_type());
+    at::native::resize_output(out, oshape);
+  } else {
+    out = empty_supa(oshape, acc_dt, self.device().index());
+  }
+  int64_t nred = 1;
+  for (int64_t d : dims) nred *= self.size(d);
+  if (out.numel() == 0) return out;
+  if (nred == 0) {
+    out.fill_(mean ? std::numeric_limits<double>::quiet_NaN() : 0.0);
+    return out;
+  }
+  const double scale = mean ? 1.0 / (double)nred : 1.0;
+  // the input must hold the output dtype's family: promote once if asked
+  at::Tensor x = (acc_dt == at::kDouble && self.scalar_type() != at::kDouble) ? self.to(at::kDouble) : self;
+  if ((int64_t)dims.size() == self.dim()) {
+    at::Tensor res = out.is_contiguous() ? out : empty_supa({}, acc_dt, self.device().index());
+    reduce_apply(res, {x}, x.scalar_type(),
+                 [scale](const supa_amd_ew_desc* d, void* ws, int64_t wsb, void* s) {
+                   return supa_amd_sum(d, scale, ws, wsb, s);
+                 },
+                 name);
+    if (!res.is_same(out)) out.copy_(res.reshape(out.sizes()));
+    return out;
+  }
+  // move the reduced dims last, make rows contiguous, reduce each row
+  std::vector<int64_t> perm;
+  for (int64_t i = 0; i < x.dim(); ++i)
+    if (!red[i]) perm.push_back(i);
+  for (int64_t d : dims) perm.push_back(d);
+  at::Tensor rows = x.permute(perm).contiguous();
+  const int64_t outer = rows.numel() / nred;
+  at::Tensor res = out.is_contiguous() ? out : empty_supa(oshape, acc_dt, self.device().index());
+  const int rc = supa_amd_sum_rows(rows.data_ptr(), dtype_code(rows.scalar_type()), res.data_ptr(),
+                                   dtype_code(acc_dt), outer, nred, scale, current_stream(self.device().index()));
+  check_status(rc, name);
+  if (!res.is_same(out)) out.copy_(res);
+  return out;
+}
+
+at::Tensor sum_dim(const at::Tensor& self, at::OptionalIntArrayRef dim, bool keepdim,
+                   std::optional<c10::ScalarType> dtype) {
+  at::Tensor out;
+  return sum_mean_into(self, dim, keepdim, dtype, false, out, "sum");
+}
+at::Tensor& sum_out(const at::Tensor& self, at::OptionalIntArrayRef dim, bool keepdim,
+                    std::optional<c10::ScalarType> dtype, at::Tensor& out) {
+  return sum_mean_into(self, dim, keepdim, dtype, false, out, "sum.IntList_out");
+}
+at::Tensor mean_dim(const at::Tensor& self, at::OptionalIntArrayRef dim, bool keepdim,
+                    std::optional<c10::ScalarType> dtype) {
+  at::Tensor out;
+  return sum_mean_into(self, dim, keepdim, dtype, true, out, "mean");
+}
+at::Tensor& mean_out(const at::Tensor& self, at::OptionalIntArrayRef dim, bool keepdim,
+                     std::optional<c10::ScalarType> dtype, at::Tensor& out) {
+  return sum_mean_into(self, dim, keepdim, dtype, true, out, "mean.out");
+}
+
+// ------------------------------------------------------- pointwise losses
+at::Tensor loss_forward(int loss, const at::Tensor& self, const at::Tensor& target, const at::Tensor& pos_weight,
+                        const at::Tensor& weight, int64_t reduction, double beta, at::Tensor out, const char* name) {
+  const int red = reduction_code(reduction);
+  std::vector<at::Tensor> ins{self, target};
+  if (pos_weight.defined()) ins.push_back(pos_weight);
+  if (weight.defined()) ins.push_back(weight);
+  at::native::ResultTypeState rts{};
+  for (const auto& t : ins) rts = at::native::update_result_type_state(t, rts);
+  const c10::ScalarType common = at::native::result_type(rts);
+  TORCH_CHECK(is_float_dtype(common), name, ": expected a floating-point input, got ", common);
+  const int has_pw = pos_weight.defined() ? 1 : 0, has_w = weight.defined() ? 1 : 0;
+  if (red == SUPA_AMD_REDUCTION_NONE) {
+    std::vector<EwIn> eins;
+    for (const auto& t : ins) eins.push_back(EwIn::of(t));
+    if (!out.defined() && loss == SUPA_AMD_LOSS_BCE_LOGITS) out = empty_supa(self.sizes(), common, self.device().index());
+    return ew_apply(out, out.defined() ? out.scalar_type() : common, common, eins,
+                    [loss, beta, has_pw, has_w](const supa_amd_ew_desc* d, void* s) {
+                      return supa_amd_loss_forward(d, loss, SUPA_AMD_REDUCTION_NONE, beta, has_pw, has_w, nullptr,
+                                                   nullptr, 0, s);
+                    },
+                    name);
+  }
+  const c10::ScalarType out_dt = out.defined() ? out.scalar_type() : common;
+  if (out.defined()) at::native::resize_output(out, {});
+  else out = empty_supa({}, out_dt, self.device().index());
+  int64_t n = 1;
+  for (int64_t s : at::infer_size(self.sizes(), target.sizes())) n *= s;
+  if (n == 0) {
+    out.fill_(red == SUPA_AMD_REDUCTION_MEAN ? std::numeric_limits<double>::quiet_NaN() : 0.0);
+    return out;
+  }
+  for (auto& t : ins) t = to_dtype(t, common);
+  at::Tensor res = out.scalar_type() == common ? out : empty_supa({}, common, self.device().index());
+  reduce_apply(res, ins, common,
+               [loss, red, beta, has_pw, has_w, &res](const supa_amd_ew_desc* d, void* ws, int64_t wsb, void* s) {
+                 return supa_amd_loss_forward(d, loss, red, beta, has_pw, has_w, res.data_ptr(), ws, wsb, s);
+               },
+               name);
+  if (!res.is_same(out)) out.copy_(res);
+  return out;
+}
+
+at::Tensor mse_loss(const at::Tensor& self, const at::Tensor& target, int64_t reduction) {
+  return loss_forward(SUPA_AMD_LOSS_MSE, self, target, {}, {}, reduction, 0.0, {}, "mse_loss");
+}
+at::Tensor& mse_loss_out(const at::Tensor& self, const at::Tensor& target, int64_t reduction, at::Tensor& out) {
+  loss_forward(SUPA_AMD_LOSS_MSE, self, target, {}, {}, reduction, 0.0, out, "mse_loss.out");
+  return out;
+}
+void check_beta(double beta) { TORCH_CHECK(beta >= 0, "smooth_l1_loss does not support negative values for beta."); }
+at::Tensor smooth_l1_loss(const at::Tensor& self, const at::Tensor& target, int64_t reduction, double beta) {
+  check_beta(beta);
+  return loss_forward(SUPA_AMD_LOSS_SMOOTH_L1, self, target, {}, {}, reduction, beta, {}, "smooth_l1_loss");
+}
+at::Tensor& smooth_l1_loss_out(const at::Tensor& self, const at::Tensor& target, int64_t reduction, double beta,
+                               at::Tensor& out) {
+  check_beta(beta);
+  loss_forward(SUPA_AMD_LOSS_SMOOTH_L1, self, target, {}, {}, reduction, beta, out, "smooth_l1_loss.out");
+  return out;
+}
+at::Tensor bce_with_logits(const at::Tensor& self, const at::Tensor& target, const std::optional<at::Tensor>& weight,
+                           const std::optional<at::Tensor>& pos_weight, int64_t reduction) {
+  TORCH_CHECK(self.sizes() == target.sizes(), "Target size (", target.sizes(),
+              ") must be the same as input size (", self.sizes(), ")");
+  TORCH_CHECK(at::isFloatingType(self.scalar_type()),
+              "binary_cross_entropy_with_logits is only implemented for floating dtypes");
+  const at::Tensor pw = pos_weight.has_value() ? *pos_weight : at::Tensor();
+  const at::Tensor w = weight.has_value() ? *weight : at::Tensor();
+  return loss_forward(SUPA_AMD_LOSS_BCE_LOGITS, self, target, pw, w, reduction, 0.0, {},
+                      "binary_cross_entropy_with_logits");
+}
+
+at::Tensor loss_backward(int loss, const at::Tensor& grad, const at::Tensor& self, const at::Tensor& target,
+                         int64_t reduction, double beta, at::Tensor gi, const char* name) {
+  reduction_code(reduction);
+  at::native::ResultTypeState rts{};
+  for (const at::Tensor* t : {&grad, &self, &target}) rts = at::native::update_result_type_state(*t, rts);
+  const c10::ScalarType common = at::native::result_type(rts);
+  TORCH_CHECK(is_float_dtype(common), name, ": expected a floating-point input, got ", common);
+  int64_t n = 1;
+  for (int64_t s : at::infer_size(self.sizes(), target.sizes())) n *= s;
+  double norm;
+  if (loss == SUPA_AMD_LOSS_MSE) norm = reduction == kMean ? 2.0 / (double)n : 2.0;
+  else norm = reduction == kMean ? 1.0 / (double)n : 1.0;
+  std::vector<EwIn> ins{EwIn::of(grad), EwIn::of(self), EwIn::of(target)};
+  return ew_apply(gi, gi.defined() ? gi.scalar_type() : common, common, ins,
+                  [loss, norm, beta](const supa_amd_ew_desc* d, void* s) {
+                    return supa_amd_loss_backward(d, loss, norm, beta, s);
+                  },
+                  name);
+}
+
+at::Tensor mse_loss_backward(const at::Tensor& grad, const at::Tensor& self, const at::Tensor& target,
+                             int64_t reduction) {
+  return loss_backward(SUPA_AMD_LOSS_MSE, grad, self, target, reduction, 0.0, {}, "mse_loss_backward");
+}
+at::Tensor& mse_loss_backward_out(const at::Tensor& grad, const at::Tensor& self, const at::Tensor& target,
+                                  int64_t reduction, at::Tensor& gi) {
+  loss_backward(SUPA_AMD_LOSS_MSE, grad, self, target, reduction, 0.0, gi, "mse_loss_backward.grad_input");
+  return gi;
+}
+at::Tensor smooth_l1_loss_backward(const at::Tensor& grad, const at::Tensor& self, const at::Tensor& target,
+                                   int64_t reduction, double beta) {
+  check_beta(beta);
+  return loss_backward(SUPA_AMD_LOSS_SMOOTH_L1, grad, self, target, reduction, beta, {}, "smooth_l1_loss_backward");
+}
+at::Tensor& smooth_l1_loss_backward_out(const at::Tensor& grad, const at::Tensor& self, const at::Tensor& target,
+                                        int64_t reduction, double beta, at::Tensor& gi) {
+  check_beta(beta);
+  loss_backward(SUPA_AMD_LOSS_SMOOTH_L1, grad, self, target, reduction, beta, gi,
+                "smooth_l1_loss_backward.grad_input");
+  return gi;
+}
+
+// ------------------------------------------------------------ log_softmax
+// Runs `fn(rows, cols)` on contiguous row-major views with `dim` last; the
+// result is returned in the original dim order, contiguous.
+at::Tensor& log_softmax_into(const at::Tensor& self, int64_t dim, bool half_to_float, at::Tensor& out,
+                             const char* name) {
+  TORCH_CHECK(is_float_dtype(self.scalar_type()), name, ": expected a floating-point input, got ", self.scalar_type());
+  if (half_to_float)
+    TORCH_CHECK(self.scalar_type() == at::kHalf || self.scalar_type() == at::kBFloat16,
+                "conversion is supported for Half and BFloat16 type only");
+  const c10::ScalarType odt = half_to_float ? at::kFloat : self.scalar_type();
+  const int64_t d = at::maybe_wrap_dim(dim, std::max<int64_t>(self.dim(), 1));
+  if (out.defined()) {
+    at::native::resize_output(out, self.sizes());
+    TORCH_CHECK(out.scalar_type() == odt, name, ": expected out dtype ", odt);
+  } else {
+    out = empty_supa(self.sizes(), odt, self.device().index());
+  }
+  if (self.numel() == 0) return out;
+  if (self.dim() == 0) {
+    out.fill_(0);
+    return out;
+  }
+  const bool last = d == self.dim() - 1;
+  at::Tensor x = last ? self.contiguous() : self.movedim(d, -1).contiguous();
+  const int64_t cols = x.size(-1);
+  const int64_t rows = x.numel() / cols;
+  at::Tensor res = (last && out.is_contiguous()) ? out : empty_supa(x.sizes(), odt, self.device().index());
+  const int rc = supa_amd_log_softmax_forward(x.data_ptr(), dtype_code(x.scalar_type()), res.data_ptr(),
+                                              dtype_code(odt), rows, cols, current_stream(self.device().index()));
+  check_status(rc, name);
+  if (!res.is_same(out)) out.copy_(last ? res : res.movedim(-1, d));
+  return out;
+}
+at::Tensor log_softmax(const at::Tensor& self, int64_t dim, bool half_to_float) {
+  at::Tensor out;
+  return log_softmax_into(self, dim, half_to_float, out, "_log_softmax");
+}
+at::Tensor& log_softmax_out(const at::Tensor& self, int64_t dim, bool half_to_float, at::Tensor& out) {
+  return log_softmax_into(self, dim, half_to_float, out, "_log_softmax.out");
+}
+
+at::Tensor& log_softmax_bwd_into(const at::Tensor& grad, const at::Tensor& output, int64_t dim,
+                                 c10::ScalarType input_dtype, at::Tensor& gi, const char* name) {
+  TORCH_CHECK(grad.sizes() == output.sizes(), name, ": grad and output sizes differ");
+  const int64_t d = at::maybe_wrap_dim(dim, std::max<int64_t>(grad.dim(), 1));
+  if (gi.defined()) at::native::resize_output(gi, grad.sizes());
+  else gi = empty_supa(grad.sizes(), input_dtype, grad.device().index());
+  if (grad.numel() == 0) return gi;
+  if (grad.dim() == 0) {
+    gi.fill_(0);
+    return gi;
+  }
+  const bool last = d == grad.dim() - 1;
+  const c10::ScalarType gdt = at::promote_types(grad.scalar_type(), output.scalar_type());
+  at::Tensor g = to_dtype(last ? grad.contiguous() : grad.movedim(d, -1).contiguous(), gdt);
+  at::Tensor y = to_dtype(last ? output.contiguous() : output.movedim(d, -1).contiguous(), gdt);
+  const int64_t cols = g.size(-1);
+  const int64_t rows = g.numel() / cols;
+  const c10::ScalarType kdt = (gi.scalar_type() == gdt) ? gdt : at::kFloat;
+  at::Tensor res = (last && gi.is_contiguous() && gi.scalar_type() == kdt)
+                       ? gi
+                       : empty_supa(g.sizes(), kdt, grad.device().index());
+  const int rc = supa_amd_log_softmax_backward(g.data_ptr(), y.data_ptr(), dtype_code(gdt), res.data_ptr(),
+                                               dtype_code(kdt), rows, cols, current_stream(grad.device().index()));
+  check_status(rc, name);
+  if (!res.is_same(gi)) gi.copy_(last ? res : res.movedim(-1, d));
+  return gi;
+}
+at::Tensor log_softmax_backward(const at::Tensor& grad, const at::Tensor& output, int64_t dim,
+                                c10::ScalarType input_dtype) {
+  at::Tensor gi;
+  return log_softmax_bwd_into(grad, output, dim, input_dtype, gi, "_log_softmax_backward_data");
+}
+at::Tensor& log_softmax_backward_out(const at::Tensor& grad, const at::Tensor& output, int64_t dim,
+                                     c10::ScalarType input_dtype, at::Tensor& gi) {
+  return log_softmax_bwd_into(grad, output, dim, input_dtype, gi, "_log_softmax_backward_data.out");
+}
+
+// --------------------------------------------------------------- nll_loss
+void nll_checks(const at::Tensor& self, const at::Tensor& target, const at::Tensor& weight) {
+  TORCH_CHECK(self.dim() > 0 && self.dim() <= 2, "input tensor should be 1D or 2D");
+  TORCH_CHECK(target.dim() <= 1, "0D or 1D target tensor expected, multi-target not supported");
+  const bool no_batch_dim = self.dim() == 1 && target.dim() == 0;
+  TORCH_CHECK(no_batch_dim || (self.size(0) == target.size(0)), "size mismatch (got input: ", self.sizes(),
+              ", target: ", target.sizes(), ")");
+  TORCH_CHECK(target.scalar_type() == at::kLong, "nll_loss: expected target of scalar type Long but found ",
+              target.scalar_type());
+  const int64_t n_classes = self.size(-1);
+  TORCH_CHECK(!weight.defined() || (weight.dim() == 1 && weight.numel() == n_classes),
+              "weight tensor should be defined either for all ", n_classes,
+              " classes or no classes but got weight tensor of shape: ", weight.sizes());
+  TORCH_CHECK(is_float_dtype(self.scalar_type()), "nll_loss: expected a floating-point input");
+}
+
+std::tuple<at::Tensor&, at::Tensor&> nll_fwd_into(const at::Tensor& self, const at::Tensor& target,
+                                                  const std::optional<at::Tensor>& weight_opt, int64_t reduction,
+                                                  int64_t ignore_index, at::Tensor& out, at::Tensor& tw) {
+  const at::Tensor weight = weight_opt.has_value() ? *weight_opt : at::Tensor();
+  nll_checks(self, target, weight);
+  const int red = reduction_code(reduction);
+  const int64_t n = self.dim() == 1 ? 1 : self.size(0);
+  const int64_t c = self.size(-1);
+  const auto dev = self.device().index();
+  std::vector<int64_t> oshape;
+  if (red == SUPA_AMD_REDUCTION_NONE && self.dim() == 2) oshape = {n};
+  if (out.defined()) at::native::resize_output(out, oshape);
+  else out = empty_supa(oshape, self.scalar_type(), dev);
+  if (tw.defined()) at::native::resize_output(tw, {});
+  else tw = empty_supa({}, self.scalar_type(), dev);
+  at::Tensor x = self.contiguous();
+  at::Tensor t = target.contiguous();
+  at::Tensor w = weight.defined() ? to_dtype(weight, self.scalar_type()).contiguous() : at::Tensor();
+  if (red == SUPA_AMD_REDUCTION_NONE) tw.zero_();
+  const DeviceScratch& s = device_scratch(dev);
+  const int rc = supa_amd_nll_loss_forward(x.data_ptr(), dtype_code(x.scalar_type()), t.data_ptr<int64_t>(),
+                                           w.defined() ? w.data_ptr() : nullptr, n, c, red, ignore_index,
+                                           out.data_ptr(), tw.data_ptr(), s.error_flag, current_stream(dev));
+  check_status(rc, "nll_loss_forward");
+  return {out, tw};
+}
+std::tuple<at::Tensor, at::Tensor> nll_loss_forward(const at::Tensor& self, const at::Tensor& target,
+                                                    const std::optional<at::Tensor>& weight, int64_t reduction,
+                                                    int64_t ignore_index) {
+  at::Tensor out, tw;
+  nll_fwd_into(self, target, weight, reduction, ignore_index, out, tw);
+  return {out, tw};
+}
+std::tuple<at::Tensor&, at::Tensor&> nll_loss_forward_out(const at::Tensor& self, const at::Tensor& target,
+                                                          const std::optional<at::Tensor>& weight, int64_t reduction,
+                                                          int64_t ignore_index, at::Tensor& out, at::Tensor& tw) {
+  return nll_fwd_into(self, target, weight, reduction, ignore_index, out, tw);
+}
+
+at::Tensor& nll_bwd_into(const at::Tensor& grad, const at::Tensor& self, const at::Tensor& target,
+                         const std::optional<at::Tensor>& weight_opt, int64_t reduction, int64_t ignore_index,
+                         const at::Tensor& total_weight, at::Tensor& gi) {
+  const at::Tensor weight = weight_opt.has_value() ? *weight_opt : at::Tensor();
+  nll_checks(self, target, weight);
+  const int red = reduction_code(reduction);
+  const int64_t n = self.dim() == 1 ? 1 : self.size(0);
+  const int64_t c = self.size(-1);
+  const auto dev = self.device().index();
+  if (gi.defined()) at::native::resize_output(gi, self.sizes());
+  else gi = empty_supa(self.sizes(), self.scalar_type(), dev);
+  TORCH_CHECK(total_weight.numel() == 1, "expected total_weight to be a single element tensor");
+  at::Tensor res = gi.is_contiguous() ? gi : empty_supa(self.sizes(), self.scalar_type(), dev);
+  at::Tensor g = to_dtype(grad, self.scalar_type()).contiguous();
+  at::Tensor t = target.contiguous();
+  at::Tensor w = weight.defined() ? to_dtype(weight, self.scalar_type()).contiguous() : at::Tensor();
+  at::Tensor tw = to_dtype(total_weight, self.scalar_type());
+  if (red == SUPA_AMD_REDUCTION_NONE && self.dim() == 2)
+    TORCH_CHECK(g.numel() == n, "Expected a tensor of dimension 1 and tensor.size[0] == ", n);
+  const DeviceScratch& s = device_scratch(dev);
+  const int rc = supa_amd_nll_loss_backward(g.data_ptr(), dtype_code(self.scalar_type()), t.data_ptr<int64_t>(),
+                                            w.defined() ? w.data_ptr() : nullptr, tw.data_ptr(), n, c,
+                                            red == SUPA_AMD_REDUCTION_NONE && self.dim() == 1 ? SUPA_AMD_REDUCTION_SUM
+                                                                                               : red,
+                                            ignore_index, res.data_ptr(), s.error_flag, current_stream(dev));
+  check_status(rc, "nll_loss_backward");
+  if (!res.is_same(gi)) gi.copy_(res);
+  return gi;
+}
+at::Tensor nll_loss_backward(const at::Tensor& grad, const at::Tensor& self, const at::Tensor& target,
+                             const std::optional<at::Tensor>& weight, int64_t reduction, int64_t ignore_index,
+                             const at::Tensor& total_weight) {
+  at::Tensor gi;
+  return nll_bwd_into(grad, self, target, weight, reduction, ignore_index, total_weight, gi);
+}
+at::Tensor& nll_loss_backward_out(const at::Tensor& grad, const at::Tensor& self, const at::Tensor& target,
+                                  const std::optional<at::Tensor>& weight, int64_t reduction, int64_t ignore_index,
+                                  const at::Tensor& total_weight, at::Tensor& gi) {
+  return nll_bwd_into(grad, self, target, weight, reduction, ignore_index, total_weight, gi);
+}
+
+}  // namespace
+}  // namespace supa
+
+TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
+  using namespace supa;
+  m.impl("sum.dim_IntList", TORCH_FN(sum_dim));
+  m.impl("sum.IntList_out", TORCH_FN(sum_out));
+  m.impl("mean.dim", TORCH_FN(mean_dim));
+  m.impl("mean.out", TORCH_FN(mean_out));
+  m.impl("mse_loss", TORCH_FN(mse_loss));
+  m.impl("mse_loss.out", TORCH_FN(mse_loss_out));
+  m.impl("mse_loss_backward", TORCH_FN(mse_loss_backward));
+  m.impl("mse_loss_backward.grad_input", TORCH_FN(mse_loss_backward_out));
+  m.impl("smooth_l1_loss", TORCH_FN(smooth_l1_loss));
+  m.impl("smooth_l1_loss.out", TORCH_FN(smooth_l1_loss_out));
+  m.impl("smooth_l1_loss_backward", TORCH_FN(smooth_l1_loss_backward));
+  m.impl("smooth_l1_loss_backward.grad_input", TORCH_FN(smooth_l1_loss_backward_out));
+  m.impl("binary_cross_entropy_with_logits", TORCH_FN(bce_with_logits));
+  m.impl("_log_softmax", TORCH_FN(log_softmax));
+  m.impl("_log_softmax.out", TORCH_FN(log_softmax_out));
+  m.impl("_log_softmax_backward_data", TORCH_FN(log_softmax_backward));
+  m.impl("_log_softmax_backward_data.out", TORCH_FN(log_softmax_backward_out));
+  m.impl("nll_loss_forward", TORCH_FN(nll_loss_forward));
+  m.impl("nll_loss_forward.output", TORCH_FN(nll_loss_forward_out));
+  m.impl("nll_loss_backward", TORCH_FN(nll_loss_backward));
+  m.impl("nll_loss_backward.grad_input", TORCH_FN(nll_loss_backward_out));
+}

@@ -22,6 +22,7 @@
 #include <c10/util/Exception.h>
 #include <torch/library.h>
 
+#include <algorithm>
 #include <atomic>
 #include <cstdlib>
 #include <map>
@@ -90,6 +91,50 @@ void synchronize(c10::DeviceIndex d) {
   set_device(d);
   SUPA_HIP_CHECK(hipDeviceSynchronize());
   set_device(prev);
+  check_device_errors(d);
+}
+
+namespace {
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mu;
+DeviceScratch g_scratch[kScratchDevices];
+}  // namespace
+
+const DeviceScratch& device_scratch(c10::DeviceIndex d) {
+  TORCH_CHECK(d >= 0 && d < kScratchDevices, "supa: device index out of range");
+  std::lock_guard<std::mutex> g(g_scratch_mu);
+  DeviceScratch& s = g_scratch[d];
+  if (!s.reduce_ws) {
+    const auto prev = current_device();
+    if (prev != d) set_device(d);
+    const int64_t ws = std::max(supa_amd_sum_workspace_bytes(0), supa_amd_loss_workspace_bytes(0));
+    const int64_t ws_rounded = (ws + 255) / 256 * 256;
+    void* p = nullptr;
+    SUPA_HIP_CHECK(hipMalloc(&p, ws_rounded + 256));
+    SUPA_HIP_CHECK(hipMemset(p, 0, ws_rounded + 256));
+    s.reduce_ws = p;
+    s.reduce_ws_bytes = ws;
+    s.error_flag = reinterpret_cast<int32_t*>(static_cast<char*>(p) + ws_rounded);
+    if (prev != d) set_device(prev);
+  }
+  return s;
+}
+
+void check_device_errors(c10::DeviceIndex d) {
+  int32_t* flag = nullptr;
+  {
+    std::lock_guard<std::mutex> g(g_scratch_mu);
+    if (d < 0 || d >= kScratchDevices || !g_scratch[d].error_flag) return;
+    flag = g_scratch[d].error_flag;
+  }
+  int32_t h = 0;
+  SUPA_HIP_CHECK(hipMemcpy(&h, flag, sizeof(h), hipMemcpyDeviceToHost));
+  if (h != 0) {
+    const int32_t zero = 0;
+    SUPA_HIP_CHECK(hipMemcpy(flag, &zero, sizeof(zero), hipMemcpyHostToDevice));
+    TORCH_CHECK_INDEX(false, "supa: a kernel reported an out-of-bounds target index (nll_loss target outside "
+                             "[0, n_classes) and not ignore_index)");
+  }
 }
 
 // ------------------------------------------------------------- allocator

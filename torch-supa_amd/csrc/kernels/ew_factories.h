@@ -27,7 +27,7 @@ template <int K, bool Bwd>
 struct UnaryFactory {
   template <typename C> static constexpr bool ok() {
     if constexpr (Bwd) return std::is_floating_point<C>::value;
-    else if constexpr (K == U_RELU || K == U_NEG) return true;
+    else if constexpr (K == U_RELU || K == U_NEG || K == U_ABS) return true;
     else return std::is_floating_point<C>::value;
   }
   template <typename C> auto make() const {

@@ -10,7 +10,7 @@
 
 namespace sa {
 
-inline bool aligned(const void* p, int bytes) { return (reinterpret_cast<uintptr_t>(p) % bytes) == 0; }
+__host__ __device__ inline bool aligned(const void* p, int bytes) { return (reinterpret_cast<uintptr_t>(p) % bytes) == 0; }
 
 inline int64_t desc_numel(const supa_amd_ew_desc* d) {
   int64_t n = 1;

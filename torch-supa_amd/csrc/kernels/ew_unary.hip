@@ -17,6 +17,9 @@ int supa_amd_unary(const supa_amd_ew_desc* d, int op, void* stream) {
     case SUPA_AMD_ERF: return run_unary<U_ERF, false>(d, stream);
     case SUPA_AMD_RELU: return run_unary<U_RELU, false>(d, stream);
     case SUPA_AMD_NEG: return run_unary<U_NEG, false>(d, stream);
+    case SUPA_AMD_RECIPROCAL: return run_unary<U_RECIPROCAL, false>(d, stream);
+    case SUPA_AMD_ABS: return run_unary<U_ABS, false>(d, stream);
+    case SUPA_AMD_SQRT: return run_unary<U_SQRT, false>(d, stream);
     default: return SUPA_AMD_EINVAL;
   }
 }

@@ -1,0 +1,304 @@
+// Multi-tensor apply: _foreach_add / _foreach_mul (list and scalar forms) and
+// the fused AdamW step over a list of tensors.
+//
+// One launch covers up to kMtaTensors tensors.  The tensor table (pointers,
+// element counts, chunk prefix sums) travels in the kernel arguments, so a
+// launch needs no device-side metadata and no allocation.  Each workgroup
+// owns one chunk of kChunk elements of one tensor (found by a scan of the
+// chunk prefix table); inside the chunk every thread moves 16-byte vectors of
+// each operand with all loads of an iteration issued before the math.
+// Tensors whose base is not 16-byte aligned, and the last partial vector of a
+// tensor, take a scalar path.  The reference's counterpart is upstream
+// MultiTensorApply.cuh (kChunkSize 65536, 512 threads, ILP 4, <= 110 / 36
+// tensors per launch) with the adam_math functor of fused_adam_utils.cuh.
+#include "ew_launch.h"
+#include "ops.h"
+
+namespace sa {
+
+constexpr int kMtaTensors = 40;
+constexpr int64_t kChunk = 16384;
+constexpr int kMtaBlock = 256;
+
+// ------------------------------------------------------------- foreach
+struct ForeachTable {
+  void* out[kMtaTensors];
+  const void* a[kMtaTensors];
+  const void* b[kMtaTensors];
+  int64_t numel[kMtaTensors];
+  uint32_t chunk_start[kMtaTensors + 1];
+  int32_t ntensors;
+};
+
+__device__ __forceinline__ int find_tensor(const uint32_t* chunk_start, int nt, uint32_t blk) {
+  int k = 0;
+  while (k + 1 < nt && chunk_start[k + 1] <= blk) ++k;
+  return k;
+}
+
+template <typename T, int OP, bool LIST>
+__global__ void __launch_bounds__(kMtaBlock)
+k_foreach(ForeachTable tab, double scalar, double alpha) {
+  using C = opmath_t<T>;
+  constexpr int V = 16 / sizeof(T);
+  const int k = find_tensor(tab.chunk_start, tab.ntensors, blockIdx.x);
+  const int64_t chunk = blockIdx.x - tab.chunk_start[k];
+  const int64_t n = tab.numel[k];
+  const int64_t lo = chunk * kChunk;
+  const int64_t hi = lo + kChunk < n ? lo + kChunk : n;
+  T* out = static_cast<T*>(tab.out[k]);
+  const T* a = static_cast<const T*>(tab.a[k]);
+  const T* b = LIST ? static_cast<const T*>(tab.b[k]) : nullptr;
+  const C s = static_cast<C>(scalar);
+  const C al = static_cast<C>(alpha);
+  auto f = [&](C x, C y) -> C {
+    if constexpr (OP == SUPA_AMD_FOREACH_ADD) return muladd<C>(al, y, x);
+    else return x * y;
+  };
+  const bool vec = aligned(out, 16) && aligned(a, 16) && (!LIST || aligned(b, 16));
+  int64_t start = lo;
+  if (vec) {
+    const int64_t nv = (hi - lo) / V;
+    for (int64_t v = threadIdx.x; v < nv; v += kMtaBlock) {
+      const int64_t e = lo + v * V;
+      const Vec<T, V> xa = *reinterpret_cast<const Vec<T, V>*>(a + e);
+      Vec<T, V> xb;
+      if constexpr (LIST) xb = *reinterpret_cast<const Vec<T, V>*>(b + e);
+      Vec<T, V> r;
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        const C y = LIST ? (C)to_arith(xb.v[i]) : s;
+        r.v[i] = from_arith<T>(f((C)to_arith(xa.v[i]), y));
+      }
+      *reinterpret_cast<Vec<T, V>*>(out + e) = r;
+    }
+    start = lo + nv * V;
+  }
+  for (int64_t e = start + threadIdx.x; e < hi; e += kMtaBlock) {
+    const C y = LIST ? (C)to_arith(b[e]) : s;
+    out[e] = from_arith<T>(f((C)to_arith(a[e]), y));
+  }
+}
+
+// ----------------------------------------------------------- fused AdamW
+struct AdamTable {
+  void* p[kMtaTensors];
+  void* g[kMtaTensors];
+  void* m[kMtaTensors];
+  void* v[kMtaTensors];
+  void* vmax[kMtaTensors];
+  const float* step[kMtaTensors];
+  int64_t numel[kMtaTensors];
+  uint32_t chunk_start[kMtaTensors + 1];
+  int32_t ntensors;
+};
+
+struct AdamHyper {
+  double lr, beta1, beta2, weight_decay, eps;
+  const float* lr_ptr;
+  const float* grad_scale;
+  const float* found_inf;
+  int amsgrad, maximize;
+};
+
+// beta^step for integral step counts by square-and-multiply in double (the
+// state_steps tensors hold 1, 2, 3, ... as float); pow() otherwise.
+__device__ __forceinline__ double pow_steps(double beta, float step) {
+  const uint64_t k = (uint64_t)step;
+  if ((float)k != step) return pow(beta, (double)step);
+  double r = 1.0, b = beta;
+  uint64_t e = k;
+  while (e) {
+    if (e & 1u) r *= b;
+    b *= b;
+    e >>= 1;
+  }
+  return r;
+}
+
+// One element of upstream adam_math in ADAMW mode
+// (torch/include/ATen/native/cuda/fused_adam_utils.cuh:27-93): hyper-parameters
+// in double, state in the storage type's opmath (float), each mixed
+// expression evaluated in double and rounded once.
+template <typename T>
+__device__ __forceinline__ void adamw_elem(T& pr, T& gr, T& mr, T& vr, T* vmx, const AdamHyper& h, double lr,
+                                           double lr_wd, float bc1, float bc2_sqrt, float step_size) {
+  using C = opmath_t<T>;
+  C param = (C)to_arith(pr);
+  C grad = (C)to_arith(gr);
+  if (h.grad_scale) grad = (C)((double)grad / (double)(*h.grad_scale));
+  const C grad_to_store = grad;
+  if (h.maximize) grad = -grad;
+  C ea = (C)to_arith(mr);
+  C eas = (C)to_arith(vr);
+  if (h.weight_decay != 0.0) param = (C)fma(-lr_wd, (double)param, (double)param);
+  ea = (C)fma(h.beta1, (double)ea, (1.0 - h.beta1) * (double)grad);
+  eas = (C)fma(h.beta2, (double)eas, ((1.0 - h.beta2) * (double)grad) * (double)grad);
+  C denom;
+  if (h.amsgrad) {
+    C mx = (C)to_arith(*vmx);
+    mx = mx > eas ? mx : eas;
+    *vmx = from_arith<T>(mx);
+    denom = (C)((double)(sqrt(mx) / (C)bc2_sqrt) + h.eps);
+  } else {
+    denom = (C)((double)(sqrt(eas) / (C)bc2_sqrt) + h.eps);
+  }
+  param = param - ((C)step_size * ea) / denom;
+  pr = from_arith<T>(param);
+  if (h.grad_scale) gr = from_arith<T>(grad_to_store);
+  mr = from_arith<T>(ea);
+  vr = from_arith<T>(eas);
+}
+
+template <typename T>
+__global__ void __launch_bounds__(kMtaBlock)
+k_adamw(AdamTable tab, AdamHyper h) {
+  if (h.found_inf && *h.found_inf == 1.0f) return;
+  constexpr int V = 16 / sizeof(T);
+  const int k = find_tensor(tab.chunk_start, tab.ntensors, blockIdx.x);
+  const int64_t chunk = blockIdx.x - tab.chunk_start[k];
+  const int64_t n = tab.numel[k];
+  const int64_t lo = chunk * kChunk;
+  const int64_t hi = lo + kChunk < n ? lo + kChunk : n;
+  const double lr = h.lr_ptr ? (double)(*h.lr_ptr) : h.lr;
+  const float step = *tab.step[k];
+  const float bc1 = (float)(1.0 - pow_steps(h.beta1, step));
+  const float bc2_sqrt = (float)sqrt(1.0 - pow_steps(h.beta2, step));
+  const float step_size = (float)(lr / (double)bc1);
+  const double lr_wd = lr * h.weight_decay;
+  T* p = static_cast<T*>(tab.p[k]);
+  T* g = static_cast<T*>(tab.g[k]);
+  T* m = static_cast<T*>(tab.m[k]);
+  T* v = static_cast<T*>(tab.v[k]);
+  T* vm = static_cast<T*>(tab.vmax[k]);
+  const bool vec = !h.amsgrad && aligned(p, 16) && aligned(g, 16) && aligned(m, 16) && aligned(v, 16);
+  int64_t start = lo;
+  if (vec) {
+    const int64_t nv = (hi - lo) / V;
+    for (int64_t i = threadIdx.x; i < nv; i += kMtaBlock) {
+      const int64_t e = lo + i * V;
+      Vec<T, V> P = *reinterpret_cast<const Vec<T, V>*>(p + e);
+      Vec<T, V> G = *reinterpret_cast<const Vec<T, V>*>(g + e);
+      Vec<T, V> M = *reinterpret_cast<const Vec<T, V>*>(m + e);
+      Vec<T, V> W = *reinterpret_cast<const Vec<T, V>*>(v + e);
+#pragma unroll
+      for (int j = 0; j < V; ++j) adamw_elem<T>(P.v[j], G.v[j], M.v[j], W.v[j], nullptr, h, lr, lr_wd, bc1, bc2_sqrt, step_size);
+      *reinterpret_cast<Vec<T, V>*>(p + e) = P;
+      if (h.grad_scale) *reinterpret_cast<Vec<T, V>*>(g + e) = G;
+      *reinterpret_cast<Vec<T, V>*>(m + e) = M;
+      *reinterpret_cast<Vec<T, V>*>(v + e) = W;
+    }
+    start = lo + nv * V;
+  }
+  for (int64_t e = start + threadIdx.x; e < hi; e += kMtaBlock)
+    adamw_elem<T>(p[e], g[e], m[e], v[e], h.amsgrad ? vm + e : nullptr, h, lr, lr_wd, bc1, bc2_sqrt, step_size);
+}
+
+template <typename F>
+int with_mta_storage(int dtype, F&& f) {
+  switch (dtype) {
+    case SUPA_AMD_F32: return f((float*)nullptr);
+    case SUPA_AMD_BF16: return f((bf16*)nullptr);
+    case SUPA_AMD_F16: return f((f16*)nullptr);
+    case SUPA_AMD_F64: return f((double*)nullptr);
+    default: return SUPA_AMD_EDTYPE;
+  }
+}
+
+}  // namespace sa
+
+using namespace sa;
+
+extern "C" {
+
+int supa_amd_foreach_binary(int op, int32_t ntensors, void* const* out, void* const* a, void* const* b,
+                            const int64_t* numel, int32_t dtype, double scalar, double alpha, void* stream) {
+  if (ntensors < 0 || (ntensors > 0 && (!out || !a || !numel))) return SUPA_AMD_EINVAL;
+  if (op != SUPA_AMD_FOREACH_ADD && op != SUPA_AMD_FOREACH_MUL) return SUPA_AMD_EINVAL;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return with_mta_storage(dtype, [&](auto* tag) -> int {
+    using T = std::remove_pointer_t<decltype(tag)>;
+    int i = 0;
+    while (i < ntensors) {
+      ForeachTable tab{};
+      uint32_t chunks = 0;
+      int nt = 0;
+      while (i < ntensors && nt < kMtaTensors) {
+        if (numel[i] < 0) return SUPA_AMD_EINVAL;
+        const int64_t c = (numel[i] + kChunk - 1) / kChunk;
+        if ((int64_t)chunks + c > (int64_t)0x7fffffff) break;
+        if (numel[i] > 0) {
+          tab.out[nt] = out[i];
+          tab.a[nt] = a[i];
+          tab.b[nt] = b ? b[i] : nullptr;
+          tab.numel[nt] = numel[i];
+          tab.chunk_start[nt] = chunks;
+          chunks += (uint32_t)c;
+          ++nt;
+        }
+        ++i;
+      }
+      tab.chunk_start[nt] = chunks;
+      tab.ntensors = nt;
+      if (nt == 0) continue;
+      if (op == SUPA_AMD_FOREACH_ADD) {
+        if (b) k_foreach<T, SUPA_AMD_FOREACH_ADD, true><<<chunks, kMtaBlock, 0, st>>>(tab, scalar, alpha);
+        else k_foreach<T, SUPA_AMD_FOREACH_ADD, false><<<chunks, kMtaBlock, 0, st>>>(tab, scalar, alpha);
+      } else {
+        if (b) k_foreach<T, SUPA_AMD_FOREACH_MUL, true><<<chunks, kMtaBlock, 0, st>>>(tab, scalar, alpha);
+        else k_foreach<T, SUPA_AMD_FOREACH_MUL, false><<<chunks, kMtaBlock, 0, st>>>(tab, scalar, alpha);
+      }
+      const int rc = launch_status();
+      if (rc) return rc;
+    }
+    return SUPA_AMD_OK;
+  });
+}
+
+int supa_amd_fused_adamw(int32_t ntensors, void* const* params, void* const* grads, void* const* exp_avgs,
+                         void* const* exp_avg_sqs, void* const* max_exp_avg_sqs, void* const* state_steps,
+                         const int64_t* numel, int32_t dtype, double lr, const float* lr_ptr, double beta1,
+                         double beta2, double weight_decay, double eps, int amsgrad, int maximize,
+                         const float* grad_scale, const float* found_inf, void* stream) {
+  if (ntensors < 0) return SUPA_AMD_EINVAL;
+  if (ntensors > 0 && (!params || !grads || !exp_avgs || !exp_avg_sqs || !state_steps || !numel)) return SUPA_AMD_EINVAL;
+  if (amsgrad && ntensors > 0 && !max_exp_avg_sqs) return SUPA_AMD_EINVAL;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  AdamHyper h{lr, beta1, beta2, weight_decay, eps, lr_ptr, grad_scale, found_inf, amsgrad ? 1 : 0, maximize ? 1 : 0};
+  return with_mta_storage(dtype, [&](auto* tag) -> int {
+    using T = std::remove_pointer_t<decltype(tag)>;
+    int i = 0;
+    while (i < ntensors) {
+      AdamTable tab{};
+      uint32_t chunks = 0;
+      int nt = 0;
+      while (i < ntensors && nt < kMtaTensors) {
+        if (numel[i] < 0 || !state_steps[i]) return SUPA_AMD_EINVAL;
+        const int64_t c = (numel[i] + kChunk - 1) / kChunk;
+        if ((int64_t)chunks + c > (int64_t)0x7fffffff) break;
+        if (numel[i] > 0) {
+          tab.p[nt] = params[i];
+          tab.g[nt] = grads[i];
+          tab.m[nt] = exp_avgs[i];
+          tab.v[nt] = exp_avg_sqs[i];
+          tab.vmax[nt] = amsgrad ? max_exp_avg_sqs[i] : nullptr;
+          tab.step[nt] = static_cast<const float*>(state_steps[i]);
+          tab.numel[nt] = numel[i];
+          tab.chunk_start[nt] = chunks;
+          chunks += (uint32_t)c;
+          ++nt;
+        }
+        ++i;
+      }
+      tab.chunk_start[nt] = chunks;
+      tab.ntensors = nt;
+      if (nt == 0) continue;
+      k_adamw<T><<<chunks, kMtaBlock, 0, st>>>(tab, h);
+      const int rc = launch_status();
+      if (rc) return rc;
+    }
+    return SUPA_AMD_OK;
+  });
+}
+
+}  // extern "C"

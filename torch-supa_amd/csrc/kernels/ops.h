@@ -134,7 +134,9 @@ template <typename C> __device__ __forceinline__ C erfx(C x) {
 }
 template <typename C> __device__ __forceinline__ C sigmoidx(C x) { return C(1) / (C(1) + expx<C>(-x)); }
 
-enum UnaryKind { U_GELU = 0, U_GELU_TANH, U_SILU, U_SIGMOID, U_TANH, U_EXP, U_LOG, U_ERF, U_RELU, U_NEG };
+enum UnaryKind {
+  U_GELU = 0, U_GELU_TANH, U_SILU, U_SIGMOID, U_TANH, U_EXP, U_LOG, U_ERF, U_RELU, U_NEG, U_RECIPROCAL, U_ABS, U_SQRT
+};
 
 template <int K, typename C> struct UnaryOp {
   static constexpr int arity = 1;
@@ -152,10 +154,18 @@ template <int K, typename C> struct UnaryOp {
       if constexpr (std::is_same<C, bool>::value) return x;
       else if constexpr (std::is_floating_point<C>::value) return (x != x) ? x : (x > C(0) ? x : C(0));
       else return x > C(0) ? x : C(0);
-    } else {
+    } else if constexpr (K == U_NEG) {
       if constexpr (std::is_same<C, bool>::value) return x;
       else if constexpr (std::is_integral<C>::value) return (C)(0 - (uint64_t)x);
       else return -x;
+    } else if constexpr (K == U_RECIPROCAL) {
+      return C(1) / x;
+    } else if constexpr (K == U_ABS) {
+      if constexpr (std::is_same<C, bool>::value) return x;
+      else if constexpr (std::is_integral<C>::value) return x < 0 ? (C)(0 - (uint64_t)x) : x;
+      else return fabs(x);
+    } else {
+      return sqrt(x);
     }
   }
 };

@@ -1,0 +1,281 @@
+// log_softmax forward / backward over the last dim of a contiguous
+// [rows, cols] tensor.
+//
+// Main path (16-byte aligned rows of up to 1024 threads x VPT vectors): one
+// 1024-thread workgroup per row holds the whole row in registers, so the
+// forward reads the row once and writes it once, and the backward reads grad
+// and output once each and writes once -- the HBM minimum for these aten ops.
+// Row statistics: per-thread partials, a 64-lane butterfly inside each
+// wavefront, then the 16 wavefront results through LDS.  exp() of the row
+// statistics uses the hardware base-2 exponential on a pre-scaled argument;
+// the row results are rounded to bf16/f16 (or kept in f32) exactly once.
+//
+// Fallback (any cols, any alignment): one 256-thread workgroup per row,
+// online max/sum in a first pass over memory, the output in a second pass.
+//
+// Replaces _log_softmax.out (NF:3752) and _log_softmax_backward_data.out
+// (NF:3763), upstream SoftMax.cu / PersistentSoftmax.cuh in the reference's
+// operator library.
+#include "devmath.h"
+#include "ew_launch.h"
+
+namespace sa {
+
+constexpr int kRowBlock = 1024;
+constexpr float kLog2e = 1.44269504088896340736f;
+
+__device__ __forceinline__ float fast_exp(float x) {
+  // e^x = 2^(x * log2 e); v_exp_f32 for the power of two
+  return __builtin_amdgcn_exp2f(x * kLog2e);
+}
+
+// NaN-propagating max (a NaN anywhere in the row makes the row NaN, as the
+// upstream kernels' results are).
+__device__ __forceinline__ float nmax(float a, float b) { return (a != a || b != b) ? __builtin_nanf("") : fmaxf(a, b); }
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = nmax(v, __shfl_xor(v, off, 64));
+  return v;
+}
+template <typename ACC>
+__device__ __forceinline__ ACC wave_sum(ACC v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// Block-wide reductions returning the result to every thread.  `lds` holds
+// one slot per wavefront; NW = blockDim / 64.
+template <int NW>
+__device__ __forceinline__ float block_max_all(float v, float* lds) {
+  v = wave_max(v);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) lds[wave] = v;
+  __syncthreads();
+  float r = lds[0];
+#pragma unroll
+  for (int w = 1; w < NW; ++w) r = nmax(r, lds[w]);
+  return r;
+}
+template <int NW>
+__device__ __forceinline__ float block_sum_all(float v, float* lds) {
+  v = wave_sum(v);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) lds[wave] = v;
+  __syncthreads();
+  float r = lds[0];
+#pragma unroll
+  for (int w = 1; w < NW; ++w) r += lds[w];
+  return r;
+}
+
+template <typename T> struct VecOf {
+  static constexpr int V = 16 / sizeof(T);
+  using type = Vec<T, V>;
+};
+
+// ------------------------------------------------------------- forward
+template <typename TI, typename TO, int VPT>
+__global__ void __launch_bounds__(kRowBlock)
+k_lsm_fwd_reg(const TI* __restrict__ in, TO* __restrict__ out, int64_t cols) {
+  constexpr int V = VecOf<TI>::V;
+  using VI = typename VecOf<TI>::type;
+  __shared__ float lds[kRowBlock / 64];
+  const int64_t row = blockIdx.x;
+  const VI* src = reinterpret_cast<const VI*>(in + row * cols);
+  const int nvec = (int)(cols / V);
+  VI x[VPT];
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    const int v = threadIdx.x + j * kRowBlock;
+    if (v < nvec) x[j] = src[v];
+  }
+  float m = -__builtin_inff();
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    const int v = threadIdx.x + j * kRowBlock;
+    if (v < nvec) {
+#pragma unroll
+      for (int k = 0; k < V; ++k) m = nmax(m, (float)to_arith(x[j].v[k]));
+    }
+  }
+  m = block_max_all<kRowBlock / 64>(m, lds);
+  const float mb = (m == -__builtin_inff()) ? 0.0f : m;  // all -inf row: keep exp args finite
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    const int v = threadIdx.x + j * kRowBlock;
+    if (v < nvec) {
+#pragma unroll
+      for (int k = 0; k < V; ++k) s += fast_exp((float)to_arith(x[j].v[k]) - mb);
+    }
+  }
+  s = block_sum_all<kRowBlock / 64>(s, lds);
+  const float logsum = sa_logf(s);
+  Vec<TO, V>* dst = reinterpret_cast<Vec<TO, V>*>(out + row * cols);
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    const int v = threadIdx.x + j * kRowBlock;
+    if (v < nvec) {
+      Vec<TO, V> w;
+#pragma unroll
+      for (int k = 0; k < V; ++k) w.v[k] = from_arith<TO>(((float)to_arith(x[j].v[k]) - m) - logsum);
+      dst[v] = w;
+    }
+  }
+}
+
+// Streaming fallback: any cols.
+template <typename TI, typename TO>
+__global__ void __launch_bounds__(kBlock)
+k_lsm_fwd_stream(const TI* __restrict__ in, TO* __restrict__ out, int64_t cols) {
+  __shared__ float lds[kBlock / 64];
+  const TI* x = in + (int64_t)blockIdx.x * cols;
+  float m = -__builtin_inff();
+  for (int64_t c = threadIdx.x; c < cols; c += kBlock) m = nmax(m, (float)to_arith(x[c]));
+  m = block_max_all<kBlock / 64>(m, lds);
+  const float mb = (m == -__builtin_inff()) ? 0.0f : m;
+  float s = 0.0f;
+  for (int64_t c = threadIdx.x; c < cols; c += kBlock) s += fast_exp((float)to_arith(x[c]) - mb);
+  s = block_sum_all<kBlock / 64>(s, lds);
+  const float logsum = sa_logf(s);
+  TO* o = out + (int64_t)blockIdx.x * cols;
+  for (int64_t c = threadIdx.x; c < cols; c += kBlock) o[c] = from_arith<TO>(((float)to_arith(x[c]) - m) - logsum);
+}
+
+// ------------------------------------------------------------ backward
+template <typename TG, typename TO, int VPT>
+__global__ void __launch_bounds__(kRowBlock)
+k_lsm_bwd_reg(const TG* __restrict__ grad, const TG* __restrict__ outp, TO* __restrict__ gin, int64_t cols) {
+  constexpr int V = VecOf<TG>::V;
+  using VG = typename VecOf<TG>::type;
+  __shared__ float lds[kRowBlock / 64];
+  const int64_t row = blockIdx.x;
+  const VG* g = reinterpret_cast<const VG*>(grad + row * cols);
+  const VG* y = reinterpret_cast<const VG*>(outp + row * cols);
+  const int nvec = (int)(cols / V);
+  VG gv[VPT];
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    const int v = threadIdx.x + j * kRowBlock;
+    if (v < nvec) gv[j] = g[v];
+  }
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    const int v = threadIdx.x + j * kRowBlock;
+    if (v < nvec) {
+#pragma unroll
+      for (int k = 0; k < V; ++k) s += (float)to_arith(gv[j].v[k]);
+    }
+  }
+  s = block_sum_all<kRowBlock / 64>(s, lds);
+  Vec<TO, V>* dst = reinterpret_cast<Vec<TO, V>*>(gin + row * cols);
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    const int v = threadIdx.x + j * kRowBlock;
+    if (v < nvec) {
+      const VG yv = y[v];
+      Vec<TO, V> w;
+#pragma unroll
+      for (int k = 0; k < V; ++k) w.v[k] = from_arith<TO>(fmaf(-fast_exp((float)to_arith(yv.v[k])), s, (float)to_arith(gv[j].v[k])));
+      dst[v] = w;
+    }
+  }
+}
+
+template <typename TG, typename TO>
+__global__ void __launch_bounds__(kBlock)
+k_lsm_bwd_stream(const TG* __restrict__ grad, const TG* __restrict__ outp, TO* __restrict__ gin, int64_t cols) {
+  __shared__ float lds[kBlock / 64];
+  const int64_t base = (int64_t)blockIdx.x * cols;
+  float s = 0.0f;
+  for (int64_t c = threadIdx.x; c < cols; c += kBlock) s += (float)to_arith(grad[base + c]);
+  s = block_sum_all<kBlock / 64>(s, lds);
+  for (int64_t c = threadIdx.x; c < cols; c += kBlock)
+    gin[base + c] = from_arith<TO>(fmaf(-fast_exp((float)to_arith(outp[base + c])), s, (float)to_arith(grad[base + c])));
+}
+
+template <typename F>
+int with_float_storage(int dtype, F&& f) {
+  switch (dtype) {
+    case SUPA_AMD_F32: return f((float*)nullptr);
+    case SUPA_AMD_BF16: return f((bf16*)nullptr);
+    case SUPA_AMD_F16: return f((f16*)nullptr);
+    default: return SUPA_AMD_EDTYPE;
+  }
+}
+
+}  // namespace sa
+
+using namespace sa;
+
+extern "C" {
+
+int supa_amd_log_softmax_forward(const void* in, int32_t in_dtype, void* out, int32_t out_dtype, int64_t rows,
+                                 int64_t cols, void* stream) {
+  if (!in || !out || rows < 0 || cols < 0 || rows >= (int64_t(1) << 31)) return SUPA_AMD_EINVAL;
+  if (rows == 0 || cols == 0) return SUPA_AMD_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return with_float_storage(in_dtype, [&](auto* ti) -> int {
+    return with_float_storage(out_dtype, [&](auto* to) -> int {
+      using TI = std::remove_pointer_t<decltype(ti)>;
+      using TO = std::remove_pointer_t<decltype(to)>;
+      if (in_dtype != out_dtype && out_dtype != SUPA_AMD_F32) return SUPA_AMD_EDTYPE;
+      constexpr int V = VecOf<TI>::V;
+      const bool reg_ok = (cols % V) == 0 && aligned(in, 16) && aligned(out, V * sizeof(TO)) && (cols / V) <= 16 * kRowBlock;
+      if (reg_ok) {
+        const int64_t nvec = cols / V;
+        const int vpt = (int)((nvec + kRowBlock - 1) / kRowBlock);
+        const TI* pi = static_cast<const TI*>(in);
+        TO* po = static_cast<TO*>(out);
+        if (vpt <= 1) k_lsm_fwd_reg<TI, TO, 1><<<(unsigned)rows, kRowBlock, 0, st>>>(pi, po, cols);
+        else if (vpt <= 2) k_lsm_fwd_reg<TI, TO, 2><<<(unsigned)rows, kRowBlock, 0, st>>>(pi, po, cols);
+        else if (vpt <= 4) k_lsm_fwd_reg<TI, TO, 4><<<(unsigned)rows, kRowBlock, 0, st>>>(pi, po, cols);
+        else if (vpt <= 8) k_lsm_fwd_reg<TI, TO, 8><<<(unsigned)rows, kRowBlock, 0, st>>>(pi, po, cols);
+        else k_lsm_fwd_reg<TI, TO, 16><<<(unsigned)rows, kRowBlock, 0, st>>>(pi, po, cols);
+        return launch_status();
+      }
+      k_lsm_fwd_stream<TI, TO><<<(unsigned)rows, kBlock, 0, st>>>(static_cast<const TI*>(in), static_cast<TO*>(out),
+                                                                  cols);
+      return launch_status();
+    });
+  });
+}
+
+int supa_amd_log_softmax_backward(const void* grad, const void* output, int32_t gy_dtype, void* grad_in,
+                                  int32_t gin_dtype, int64_t rows, int64_t cols, void* stream) {
+  if (!grad || !output || !grad_in || rows < 0 || cols < 0 || rows >= (int64_t(1) << 31)) return SUPA_AMD_EINVAL;
+  if (rows == 0 || cols == 0) return SUPA_AMD_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return with_float_storage(gy_dtype, [&](auto* tg) -> int {
+    return with_float_storage(gin_dtype, [&](auto* to) -> int {
+      using TG = std::remove_pointer_t<decltype(tg)>;
+      using TO = std::remove_pointer_t<decltype(to)>;
+      if (gy_dtype != gin_dtype && gin_dtype != SUPA_AMD_F32) return SUPA_AMD_EDTYPE;
+      constexpr int V = VecOf<TG>::V;
+      const bool reg_ok = (cols % V) == 0 && aligned(grad, 16) && aligned(output, 16) && aligned(grad_in, V * sizeof(TO)) &&
+                          (cols / V) <= 16 * kRowBlock;
+      const TG* pg = static_cast<const TG*>(grad);
+      const TG* py = static_cast<const TG*>(output);
+      TO* po = static_cast<TO*>(grad_in);
+      if (reg_ok) {
+        const int64_t nvec = cols / V;
+        const int vpt = (int)((nvec + kRowBlock - 1) / kRowBlock);
+        if (vpt <= 1) k_lsm_bwd_reg<TG, TO, 1><<<(unsigned)rows, kRowBlock, 0, st>>>(pg, py, po, cols);
+        else if (vpt <= 2) k_lsm_bwd_reg<TG, TO, 2><<<(unsigned)rows, kRowBlock, 0, st>>>(pg, py, po, cols);
+        else if (vpt <= 4) k_lsm_bwd_reg<TG, TO, 4><<<(unsigned)rows, kRowBlock, 0, st>>>(pg, py, po, cols);
+        else if (vpt <= 8) k_lsm_bwd_reg<TG, TO, 8><<<(unsigned)rows, kRowBlock, 0, st>>>(pg, py, po, cols);
+        else k_lsm_bwd_reg<TG, TO, 16><<<(unsigned)rows, kRowBlock, 0, st>>>(pg, py, po, cols);
+        return launch_status();
+      }
+      k_lsm_bwd_stream<TG, TO><<<(unsigned)rows, kBlock, 0, st>>>(pg, py, po, cols);
+      return launch_status();
+    });
+  });
+}
+
+}  // extern "C"
