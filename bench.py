@@ -46,7 +46,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--configs", default="c1,c2,c3,c4,c5")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
-    ap.add_argument("--main", default="c2", help="workload reported as value (c2 or c3)")
+    ap.add_argument("--probe", action="store_true",
+                    help="only launch the c2 gelu(tanh) kernel and a copy-like calibration kernel (for rocprofv3 --pmc)")
     return ap.parse_args()
 
 
@@ -315,6 +316,28 @@ def traffic_from_profiles():
     return None
 
 
+def probe(torch):
+    """Kernel launches for counter collection: 10x abs.out over a 1 GiB f32
+    buffer (reads 1 GiB, writes 1 GiB: the calibration of FETCH_SIZE and
+    WRITE_SIZE), then 10x the headline's dominant kernel, gelu(tanh) over the
+    c2 f32 tensor (algorithmic 2 GiB read + 2 GiB write)."""
+    cal = gen(torch, (1 << 28,), 42, torch.float32)
+    cal_out = torch.empty_like(cal)
+    for _ in range(10):
+        torch.ops.aten.abs.out(cal, out=cal_out)
+    torch.supa.synchronize()
+    del cal, cal_out
+    x, bias = c2_inputs(torch, transposed=False)
+    y = x + bias
+    del x
+    z = torch.empty_like(y)
+    for _ in range(10):
+        torch.ops.aten.gelu.out(y, approximate="tanh", out=z)
+    torch.supa.synchronize()
+    print(json.dumps({"probe": "done", "calibration_bytes_read": 1 << 30, "calibration_bytes_written": 1 << 30,
+                      "gelu_bytes_read": C2_N * 4, "gelu_bytes_written": C2_N * 4}))
+
+
 def main():
     a = parse()
     if a.gpus != 1:
@@ -327,6 +350,9 @@ def main():
 
     assert torch.supa.is_available(), "no supa device"
     timer = Timer(torch)
+    if a.probe:
+        probe(torch)
+        return
     configs = [c.strip() for c in a.configs.split(",") if c.strip()]
     per = {}
 

@@ -24,10 +24,12 @@ struct b8 {
 typedef _Float16 f16;
 
 __device__ __forceinline__ float bf16_to_f32(bf16 h) { return __uint_as_float((uint32_t)h.x << 16); }
+// Round to nearest even through the gfx950 convert instruction; NaN becomes
+// the canonical 0x7FC0 that c10::BFloat16 produces.
 __device__ __forceinline__ bf16 f32_to_bf16(float f) {
-  const uint32_t u = __float_as_uint(f);
+  const __bf16 hw = (__bf16)f;
   bf16 h;
-  h.x = (f != f) ? (uint16_t)0x7FC0u : (uint16_t)((u + (((u >> 16) & 1u) + 0x7FFFu)) >> 16);
+  h.x = (f != f) ? (uint16_t)0x7FC0u : __builtin_bit_cast(uint16_t, hw);
   return h;
 }
 
@@ -87,6 +89,34 @@ __device__ __forceinline__ C load_cvt(S s) {
 template <typename T, int V> struct alignas(sizeof(T) * V) Vec {
   T v[V];
 };
+
+// Streaming (nontemporal) vector load/store: data read or written once per
+// kernel bypasses cache residency, which measured faster for HBM-bound
+// streams on MI355X.  Operands that are re-read (broadcast rows) keep plain
+// loads.
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+template <typename VT>
+__device__ __forceinline__ VT ld_stream(const VT* p) {
+  if constexpr (sizeof(VT) % 16 != 0) {
+    return *p;  // sub-vector accesses (scalar paths) stay plain
+  } else {
+    VT r;
+#pragma unroll
+    for (int w = 0; w < (int)(sizeof(VT) / 16); ++w)
+      reinterpret_cast<u32x4_t*>(&r)[w] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p) + w);
+    return r;
+  }
+}
+template <typename VT>
+__device__ __forceinline__ void st_stream(VT* p, const VT& v) {
+  if constexpr (sizeof(VT) % 16 != 0) {
+    *p = v;
+  } else {
+#pragma unroll
+    for (int w = 0; w < (int)(sizeof(VT) / 16); ++w)
+      __builtin_nontemporal_store(reinterpret_cast<const u32x4_t*>(&v)[w], reinterpret_cast<u32x4_t*>(p) + w);
+  }
+}
 
 // ----------------------------------------------------------------- runtime
 // Dynamic-dtype load/store for the generic kernels.

@@ -77,7 +77,7 @@ template <int NT>  // NT = number of tensor operands (output first)
 struct TArgs {
   void* p[NT];
   int64_t st[NT][SUPA_AMD_MAX_DIMS];
-  int32_t mode[NT];  // CONTIG: 0 dense, 1 one-element broadcast
+  int32_t mode[NT];  // CONTIG: 0 dense, 1 one-element broadcast; VECND: 1 = re-read (broadcast) operand
 };
 
 // ------------------------------------------------------- type plumbing
@@ -107,7 +107,7 @@ k_contig(Op op, TArgs<1 + sizeof...(S)> a, int64_t n) {
 #pragma unroll
              for (int k = 0; k < VEC; ++k) x[u][k][I] = s;
            } else {
-             const Vec<St, VEC> w = *reinterpret_cast<const Vec<St, VEC>*>(p + v * VEC);
+             const Vec<St, VEC> w = ld_stream(reinterpret_cast<const Vec<St, VEC>*>(p + v * VEC));
 #pragma unroll
              for (int k = 0; k < VEC; ++k) x[u][k][I] = load_cvt<C, CT>(w.v[k]);
            }
@@ -125,7 +125,7 @@ k_contig(Op op, TArgs<1 + sizeof...(S)> a, int64_t n) {
       Vec<OT, VEC> w;
 #pragma unroll
       for (int k = 0; k < VEC; ++k) w.v[k] = from_arith<OT>(op(x[u][k]));
-      *reinterpret_cast<Vec<OT, VEC>*>(out + v * VEC) = w;
+      st_stream(reinterpret_cast<Vec<OT, VEC>*>(out + v * VEC), w);
     }
   }
   // tail
@@ -176,7 +176,8 @@ k_vecnd(Op op, TArgs<1 + sizeof...(S)> a, NdGeom g, uint32_t nvec) {
 #pragma unroll
          for (int k = 0; k < VEC; ++k) x[k][I] = s;
        } else {
-         const Vec<St, VEC> w = *reinterpret_cast<const Vec<St, VEC>*>(p);
+         const Vec<St, VEC> w = a.mode[1 + I] ? *reinterpret_cast<const Vec<St, VEC>*>(p)
+                                              : ld_stream(reinterpret_cast<const Vec<St, VEC>*>(p));
 #pragma unroll
          for (int k = 0; k < VEC; ++k) x[k][I] = load_cvt<C, CT>(w.v[k]);
        }
@@ -186,7 +187,7 @@ k_vecnd(Op op, TArgs<1 + sizeof...(S)> a, NdGeom g, uint32_t nvec) {
   Vec<OT, VEC> w;
 #pragma unroll
   for (int k = 0; k < VEC; ++k) w.v[k] = from_arith<OT>(op(x[k]));
-  *reinterpret_cast<Vec<OT, VEC>*>(static_cast<OT*>(a.p[0]) + off[0]) = w;
+  st_stream(reinterpret_cast<Vec<OT, VEC>*>(static_cast<OT*>(a.p[0]) + off[0]), w);
 }
 
 // ----------------------------------------------------------- STRIDED

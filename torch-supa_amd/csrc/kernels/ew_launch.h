@@ -182,6 +182,12 @@ int launch_static(const Op& op, const supa_amd_ew_desc& d, const int* tin, hipSt
       }
     }
     if (vnd) {
+      // operands broadcast along some outer dim are re-read: keep them cached
+      for (int k = 1; k <= N; ++k) {
+        b.mode[k] = 0;
+        for (int j = 1; j < p.ndim; ++j)
+          if (b.st[k][j] == 0 && p.sizes[j] > 1) b.mode[k] = 1;
+      }
       const uint32_t nvec = (uint32_t)(pn / VEC);
       const unsigned blocks = (nvec + kBlock - 1) / kBlock;
       k_vecnd<VEC, Op, C, CT, OT, S...><<<blocks, kBlock, 0, st>>>(op, b, g, nvec);

@@ -61,16 +61,16 @@ k_foreach(ForeachTable tab, double scalar, double alpha) {
     const int64_t nv = (hi - lo) / V;
     for (int64_t v = threadIdx.x; v < nv; v += kMtaBlock) {
       const int64_t e = lo + v * V;
-      const Vec<T, V> xa = *reinterpret_cast<const Vec<T, V>*>(a + e);
+      const Vec<T, V> xa = ld_stream(reinterpret_cast<const Vec<T, V>*>(a + e));
       Vec<T, V> xb;
-      if constexpr (LIST) xb = *reinterpret_cast<const Vec<T, V>*>(b + e);
+      if constexpr (LIST) xb = ld_stream(reinterpret_cast<const Vec<T, V>*>(b + e));
       Vec<T, V> r;
 #pragma unroll
       for (int i = 0; i < V; ++i) {
         const C y = LIST ? (C)to_arith(xb.v[i]) : s;
         r.v[i] = from_arith<T>(f((C)to_arith(xa.v[i]), y));
       }
-      *reinterpret_cast<Vec<T, V>*>(out + e) = r;
+      st_stream(reinterpret_cast<Vec<T, V>*>(out + e), r);
     }
     start = lo + nv * V;
   }
@@ -177,16 +177,16 @@ k_adamw(AdamTable tab, AdamHyper h) {
     const int64_t nv = (hi - lo) / V;
     for (int64_t i = threadIdx.x; i < nv; i += kMtaBlock) {
       const int64_t e = lo + i * V;
-      Vec<T, V> P = *reinterpret_cast<const Vec<T, V>*>(p + e);
-      Vec<T, V> G = *reinterpret_cast<const Vec<T, V>*>(g + e);
-      Vec<T, V> M = *reinterpret_cast<const Vec<T, V>*>(m + e);
-      Vec<T, V> W = *reinterpret_cast<const Vec<T, V>*>(v + e);
+      Vec<T, V> P = ld_stream(reinterpret_cast<const Vec<T, V>*>(p + e));
+      Vec<T, V> G = ld_stream(reinterpret_cast<const Vec<T, V>*>(g + e));
+      Vec<T, V> M = ld_stream(reinterpret_cast<const Vec<T, V>*>(m + e));
+      Vec<T, V> W = ld_stream(reinterpret_cast<const Vec<T, V>*>(v + e));
 #pragma unroll
       for (int j = 0; j < V; ++j) adamw_elem<T>(P.v[j], G.v[j], M.v[j], W.v[j], nullptr, h, lr, lr_wd, bc1, bc2_sqrt, step_size);
-      *reinterpret_cast<Vec<T, V>*>(p + e) = P;
-      if (h.grad_scale) *reinterpret_cast<Vec<T, V>*>(g + e) = G;
-      *reinterpret_cast<Vec<T, V>*>(m + e) = M;
-      *reinterpret_cast<Vec<T, V>*>(v + e) = W;
+      st_stream(reinterpret_cast<Vec<T, V>*>(p + e), P);
+      if (h.grad_scale) st_stream(reinterpret_cast<Vec<T, V>*>(g + e), G);
+      st_stream(reinterpret_cast<Vec<T, V>*>(m + e), M);
+      st_stream(reinterpret_cast<Vec<T, V>*>(v + e), W);
     }
     start = lo + nv * V;
   }

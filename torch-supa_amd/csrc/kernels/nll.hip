@@ -19,6 +19,7 @@
 namespace sa {
 
 constexpr int kNllBlock = 1024;
+constexpr int kNllUnroll = 4;  // 16-byte vectors per thread in the backward writer
 
 template <typename T, typename ACC>
 __global__ void __launch_bounds__(kNllBlock)
@@ -109,15 +110,20 @@ k_nll_bwd(const T* __restrict__ grad_out, const int64_t* __restrict__ target, co
     gval = weight ? from_arith<T>((C)to_arith(weight[t]) * (C)to_arith(gs)) : gs;
   }
   T* dst = gin + row * c;
-  const int64_t col0 = ((int64_t)blockIdx.x * kBlock + threadIdx.x) * VEC;
-  if (col0 >= c) return;
-  if (VEC > 1 && col0 + VEC <= c) {
-    Vec<T, VEC> w;
+  const T zero = from_arith<T>(C(0));
 #pragma unroll
-    for (int k = 0; k < VEC; ++k) w.v[k] = (active && col0 + k == t) ? gval : from_arith<T>(C(0));
-    *reinterpret_cast<Vec<T, VEC>*>(dst + col0) = w;
-  } else {
-    for (int k = 0; k < VEC && col0 + k < c; ++k) dst[col0 + k] = (active && col0 + k == t) ? gval : from_arith<T>(C(0));
+  for (int u = 0; u < kNllUnroll; ++u) {
+    const int64_t col0 = (((int64_t)blockIdx.x * kNllUnroll + u) * kBlock + threadIdx.x) * VEC;
+    if (col0 >= c) break;
+    if (VEC > 1 && col0 + VEC <= c) {
+      Vec<T, VEC> w;
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) w.v[k] = zero;
+      if (active && t >= col0 && t < col0 + VEC) w.v[t - col0] = gval;
+      st_stream(reinterpret_cast<Vec<T, VEC>*>(dst + col0), w);
+    } else {
+      for (int k = 0; k < VEC && col0 + k < c; ++k) dst[col0 + k] = (active && col0 + k == t) ? gval : zero;
+    }
   }
 }
 
@@ -186,11 +192,11 @@ int supa_amd_nll_loss_backward(const void* grad_out, int32_t dtype, const int64_
         const int64_t rows = std::min<int64_t>(65535, n - r0);
         const T* gslab = reduction == SUPA_AMD_REDUCTION_NONE ? g + r0 : g;
         if (vec_ok) {
-          dim3 grid((unsigned)((c / VEC + kBlock - 1) / kBlock), (unsigned)rows);
+          dim3 grid((unsigned)((c / VEC + kBlock * kNllUnroll - 1) / (kBlock * kNllUnroll)), (unsigned)rows);
           k_nll_bwd<T, VEC><<<grid, kBlock, 0, st>>>(gslab, target + r0, w, tw, c, reduction, ignore_index,
                                                       gi + r0 * c, error_flag);
         } else {
-          dim3 grid((unsigned)((c + kBlock - 1) / kBlock), (unsigned)rows);
+          dim3 grid((unsigned)((c + kBlock * kNllUnroll - 1) / (kBlock * kNllUnroll)), (unsigned)rows);
           k_nll_bwd<T, 1><<<grid, kBlock, 0, st>>>(gslab, target + r0, w, tw, c, reduction, ignore_index,
                                                     gi + r0 * c, error_flag);
         }
@@ -200,10 +206,10 @@ int supa_amd_nll_loss_backward(const void* grad_out, int32_t dtype, const int64_
       return SUPA_AMD_OK;
     }
     if (vec_ok) {
-      dim3 grid((unsigned)((c / VEC + kBlock - 1) / kBlock), (unsigned)n);
+      dim3 grid((unsigned)((c / VEC + kBlock * kNllUnroll - 1) / (kBlock * kNllUnroll)), (unsigned)n);
       k_nll_bwd<T, VEC><<<grid, kBlock, 0, st>>>(g, target, w, tw, c, reduction, ignore_index, gi, error_flag);
     } else {
-      dim3 grid((unsigned)((c + kBlock - 1) / kBlock), (unsigned)n);
+      dim3 grid((unsigned)((c + kBlock * kNllUnroll - 1) / (kBlock * kNllUnroll)), (unsigned)n);
       k_nll_bwd<T, 1><<<grid, kBlock, 0, st>>>(g, target, w, tw, c, reduction, ignore_index, gi, error_flag);
     }
     return launch_status();

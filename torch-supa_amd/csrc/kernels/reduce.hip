@@ -61,7 +61,7 @@ __device__ __forceinline__ ACC accumulate(const Op& op, const TArgs<1 + sizeof..
 #pragma unroll
              for (int k = 0; k < VEC; ++k) x[k][I] = s;
            } else {
-             const Vec<St, VEC> w = *reinterpret_cast<const Vec<St, VEC>*>(p + v * VEC);
+             const Vec<St, VEC> w = ld_stream(reinterpret_cast<const Vec<St, VEC>*>(p + v * VEC));
 #pragma unroll
              for (int k = 0; k < VEC; ++k) x[k][I] = load_cvt<C, CT>(w.v[k]);
            }
@@ -109,7 +109,8 @@ __device__ __forceinline__ ACC accumulate(const Op& op, const TArgs<1 + sizeof..
 #pragma unroll
              for (int k = 0; k < VEC; ++k) x[k][I] = s;
            } else {
-             const Vec<St, VEC> w = *reinterpret_cast<const Vec<St, VEC>*>(p);
+             const Vec<St, VEC> w = a.mode[1 + I] ? *reinterpret_cast<const Vec<St, VEC>*>(p)
+                                                  : ld_stream(reinterpret_cast<const Vec<St, VEC>*>(p));
 #pragma unroll
              for (int k = 0; k < VEC; ++k) x[k][I] = load_cvt<C, CT>(w.v[k]);
            }
@@ -220,6 +221,14 @@ int launch_reduce(const Op& op, const supa_amd_ew_desc& d, const int* tin, doubl
       }
     }
     layout = vnd ? R_VECND : R_STRIDED;
+    if (vnd) {
+      // operands broadcast along an outer dim are re-read: keep them cached
+      for (int i = 0; i < N; ++i) {
+        a.mode[1 + i] = 0;
+        for (int j = 1; j < d.ndim; ++j)
+          if (a.st[1 + i][j] == 0 && d.sizes[j] > 1) a.mode[1 + i] = 1;
+      }
+    }
   }
   const NdGeom g = make_geom(d);
   const int64_t units = layout == R_STRIDED ? n : std::max<int64_t>(n / VEC, 1);

@@ -77,53 +77,109 @@ template <typename T> struct VecOf {
   using type = Vec<T, V>;
 };
 
+// The register-resident kernels keep each 16-byte vector as four raw 32-bit
+// words and widen an element to float only where it is used; an empty asm
+// statement between phases tells the compiler the words may have changed, so
+// it never keeps a second, unpacked copy of the row alive (which would spill).
+__device__ __forceinline__ uint32_t word_of(const uint4& w, int i) {
+  return i == 0 ? w.x : (i == 1 ? w.y : (i == 2 ? w.z : w.w));
+}
+
+template <typename T>
+__device__ __forceinline__ float elem_f(const uint4& w, int k) {
+  if constexpr (std::is_same<T, float>::value) {
+    return __uint_as_float(word_of(w, k));
+  } else {
+    const uint32_t word = word_of(w, k >> 1);
+    const uint32_t h = (k & 1) ? (word >> 16) : (word & 0xffffu);
+    if constexpr (std::is_same<T, bf16>::value) {
+      return __uint_as_float(h << 16);
+    } else {
+      return (float)__builtin_bit_cast(f16, (uint16_t)h);
+    }
+  }
+}
+
+template <int VPT>
+__device__ __forceinline__ void opaque(uint4 (&x)[VPT]) {
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) asm volatile("" : "+v"(x[j].x), "+v"(x[j].y), "+v"(x[j].z), "+v"(x[j].w));
+}
+
+// Row results: 16-byte vectors of TO built from V floats.  bf16 pairs go
+// through the gfx950 packed convert (round to nearest even; a NaN keeps its
+// NaN-ness, its payload may differ from c10's canonical 0x7FC0).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float float2_t __attribute__((ext_vector_type(2)));
+
+template <typename TO, int V>
+__device__ __forceinline__ void store_row_vec(Vec<TO, V>* dst, int v, const float (&f)[V]) {
+  if constexpr (std::is_same<TO, bf16>::value) {
+    uint32_t w[V / 2];
+#pragma unroll
+    for (int k = 0; k < V / 2; ++k) {
+      const float2_t p = {f[2 * k], f[2 * k + 1]};
+      w[k] = __builtin_bit_cast(uint32_t, __builtin_convertvector(p, bf16x2_t));
+    }
+    st_stream(reinterpret_cast<Vec<uint32_t, V / 2>*>(dst + v), *reinterpret_cast<const Vec<uint32_t, V / 2>*>(w));
+  } else {
+    Vec<TO, V> o;
+#pragma unroll
+    for (int k = 0; k < V; ++k) o.v[k] = from_arith<TO>(f[k]);
+    st_stream(dst + v, o);
+  }
+}
+
 // ------------------------------------------------------------- forward
+// A NaN anywhere in a row turns the row's exp-sum, hence every output of the
+// row, into NaN, so the max itself can skip NaN checks.
 template <typename TI, typename TO, int VPT>
 __global__ void __launch_bounds__(kRowBlock)
 k_lsm_fwd_reg(const TI* __restrict__ in, TO* __restrict__ out, int64_t cols) {
   constexpr int V = VecOf<TI>::V;
-  using VI = typename VecOf<TI>::type;
   __shared__ float lds[kRowBlock / 64];
   const int64_t row = blockIdx.x;
-  const VI* src = reinterpret_cast<const VI*>(in + row * cols);
+  const uint4* src = reinterpret_cast<const uint4*>(in + row * cols);
   const int nvec = (int)(cols / V);
-  VI x[VPT];
+  const int full = nvec / kRowBlock;  // vectors every thread has (uniform)
+  const int tid = threadIdx.x;
+  uint4 x[VPT];
 #pragma unroll
   for (int j = 0; j < VPT; ++j) {
-    const int v = threadIdx.x + j * kRowBlock;
-    if (v < nvec) x[j] = src[v];
+    if (j < full) x[j] = ld_stream(src + tid + j * kRowBlock);
+    else if (tid + j * kRowBlock < nvec) x[j] = ld_stream(src + tid + j * kRowBlock);
   }
   float m = -__builtin_inff();
 #pragma unroll
   for (int j = 0; j < VPT; ++j) {
-    const int v = threadIdx.x + j * kRowBlock;
-    if (v < nvec) {
+    if (j < full || tid + j * kRowBlock < nvec) {
 #pragma unroll
-      for (int k = 0; k < V; ++k) m = nmax(m, (float)to_arith(x[j].v[k]));
+      for (int k = 0; k < V; ++k) m = fmaxf(m, elem_f<TI>(x[j], k));
     }
   }
   m = block_max_all<kRowBlock / 64>(m, lds);
   const float mb = (m == -__builtin_inff()) ? 0.0f : m;  // all -inf row: keep exp args finite
+  const float mbl = mb * kLog2e;
+  opaque<VPT>(x);
   float s = 0.0f;
 #pragma unroll
   for (int j = 0; j < VPT; ++j) {
-    const int v = threadIdx.x + j * kRowBlock;
-    if (v < nvec) {
+    if (j < full || tid + j * kRowBlock < nvec) {
 #pragma unroll
-      for (int k = 0; k < V; ++k) s += fast_exp((float)to_arith(x[j].v[k]) - mb);
+      for (int k = 0; k < V; ++k) s += __builtin_amdgcn_exp2f(fmaf(elem_f<TI>(x[j], k), kLog2e, -mbl));
     }
   }
   s = block_sum_all<kRowBlock / 64>(s, lds);
   const float logsum = sa_logf(s);
+  opaque<VPT>(x);
   Vec<TO, V>* dst = reinterpret_cast<Vec<TO, V>*>(out + row * cols);
 #pragma unroll
   for (int j = 0; j < VPT; ++j) {
-    const int v = threadIdx.x + j * kRowBlock;
-    if (v < nvec) {
-      Vec<TO, V> w;
+    if (j < full || tid + j * kRowBlock < nvec) {
+      float f[V];
 #pragma unroll
-      for (int k = 0; k < V; ++k) w.v[k] = from_arith<TO>(((float)to_arith(x[j].v[k]) - m) - logsum);
-      dst[v] = w;
+      for (int k = 0; k < V; ++k) f[k] = (elem_f<TI>(x[j], k) - m) - logsum;
+      store_row_vec<TO, V>(dst, tid + j * kRowBlock, f);
     }
   }
 }
@@ -147,42 +203,66 @@ k_lsm_fwd_stream(const TI* __restrict__ in, TO* __restrict__ out, int64_t cols) 
 }
 
 // ------------------------------------------------------------ backward
+// grad's row stays in registers (raw words) for the row sum; the output row
+// streams through in chunks of CH vectors with the next chunk's loads issued
+// before the current chunk's math.
 template <typename TG, typename TO, int VPT>
 __global__ void __launch_bounds__(kRowBlock)
 k_lsm_bwd_reg(const TG* __restrict__ grad, const TG* __restrict__ outp, TO* __restrict__ gin, int64_t cols) {
   constexpr int V = VecOf<TG>::V;
-  using VG = typename VecOf<TG>::type;
+  constexpr int CH = VPT < 2 ? VPT : 2;
   __shared__ float lds[kRowBlock / 64];
   const int64_t row = blockIdx.x;
-  const VG* g = reinterpret_cast<const VG*>(grad + row * cols);
-  const VG* y = reinterpret_cast<const VG*>(outp + row * cols);
+  const uint4* g = reinterpret_cast<const uint4*>(grad + row * cols);
+  const uint4* y = reinterpret_cast<const uint4*>(outp + row * cols);
   const int nvec = (int)(cols / V);
-  VG gv[VPT];
+  const int full = nvec / kRowBlock;
+  const int tid = threadIdx.x;
+  uint4 gv[VPT];
 #pragma unroll
   for (int j = 0; j < VPT; ++j) {
-    const int v = threadIdx.x + j * kRowBlock;
-    if (v < nvec) gv[j] = g[v];
+    if (j < full) gv[j] = ld_stream(g + tid + j * kRowBlock);
+    else if (tid + j * kRowBlock < nvec) gv[j] = ld_stream(g + tid + j * kRowBlock);
   }
+  uint4 yv[CH];
+#pragma unroll
+  for (int j = 0; j < CH; ++j)
+    if (j < full || tid + j * kRowBlock < nvec) yv[j] = ld_stream(y + tid + j * kRowBlock);
   float s = 0.0f;
 #pragma unroll
   for (int j = 0; j < VPT; ++j) {
-    const int v = threadIdx.x + j * kRowBlock;
-    if (v < nvec) {
+    if (j < full || tid + j * kRowBlock < nvec) {
 #pragma unroll
-      for (int k = 0; k < V; ++k) s += (float)to_arith(gv[j].v[k]);
+      for (int k = 0; k < V; ++k) s += elem_f<TG>(gv[j], k);
     }
   }
   s = block_sum_all<kRowBlock / 64>(s, lds);
+  opaque<VPT>(gv);
   Vec<TO, V>* dst = reinterpret_cast<Vec<TO, V>*>(gin + row * cols);
 #pragma unroll
-  for (int j = 0; j < VPT; ++j) {
-    const int v = threadIdx.x + j * kRowBlock;
-    if (v < nvec) {
-      const VG yv = y[v];
-      Vec<TO, V> w;
+  for (int c = 0; c < VPT; c += CH) {
+    uint4 yn[CH];
+    if (c + CH < VPT) {
 #pragma unroll
-      for (int k = 0; k < V; ++k) w.v[k] = from_arith<TO>(fmaf(-fast_exp((float)to_arith(yv.v[k])), s, (float)to_arith(gv[j].v[k])));
-      dst[v] = w;
+      for (int j = 0; j < CH; ++j) {
+        const int jj = c + CH + j;
+        if (jj < full || tid + jj * kRowBlock < nvec) yn[j] = ld_stream(y + tid + jj * kRowBlock);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < CH; ++j) {
+      const int jj = c + j;
+      if (jj < full || tid + jj * kRowBlock < nvec) {
+        float f[V];
+#pragma unroll
+        for (int k = 0; k < V; ++k)
+          f[k] = fmaf(-__builtin_amdgcn_exp2f(elem_f<TG>(yv[j], k) * kLog2e), s, elem_f<TG>(gv[jj], k));
+        store_row_vec<TO, V>(dst, tid + jj * kRowBlock, f);
+      }
+    }
+    if (c + CH < VPT) {
+#pragma unroll
+      for (int j = 0; j < CH; ++j) yv[j] = yn[j];
     }
   }
 }
