@@ -48,6 +48,9 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--probe", action="store_true",
                     help="only launch the c2 gelu(tanh) kernel and a copy-like calibration kernel (for rocprofv3 --pmc)")
+    ap.add_argument("--derive-traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="CPU only: turn the counter_collection.csv files of two `rocprofv3 --pmc FETCH_SIZE` / "
+                         "`--pmc WRITE_SIZE` runs of --probe into profiles/gelu_tanh_c2_traffic.json")
     return ap.parse_args()
 
 
@@ -316,6 +319,58 @@ def traffic_from_profiles():
     return None
 
 
+PROBE_CAL_KERNEL = "UnaryOp<11, float>"  # abs.out: the calibration kernel
+PROBE_GELU_KERNEL = "UnaryOp<1, float>"  # gelu(approximate='tanh')
+
+
+def derive_traffic(fetch_csv, write_csv):
+    """HBM bytes per launch of the c2 gelu kernel from two PMC runs of --probe.
+
+    FETCH_SIZE and WRITE_SIZE are reported in KiB per dispatch; each is scaled
+    by known / measured for the calibration kernel (abs.out over 2^28 f32:
+    exactly 1 GiB read and 1 GiB written), then averaged over the gelu
+    dispatches."""
+    import csv
+
+    def per_kernel(path):
+        cal, gel = [], []
+        with open(path) as f:
+            for r in csv.DictReader(f):
+                name, val = r["Kernel_Name"], float(r["Counter_Value"])
+                if "k_contig" not in name:
+                    continue
+                if PROBE_CAL_KERNEL in name:
+                    cal.append(val)
+                elif PROBE_GELU_KERNEL in name:
+                    gel.append(val)
+        if not cal or not gel:
+            raise SystemExit(f"{path}: calibration or gelu dispatches missing")
+        return sum(cal) / len(cal), sum(gel) / len(gel), len(gel)
+
+    known_kib = float(1 << 20)
+    f_cal, f_gel, nf = per_kernel(fetch_csv)
+    w_cal, w_gel, nw = per_kernel(write_csv)
+    f_scale, w_scale = known_kib / f_cal, known_kib / w_cal
+    read_b = f_gel * f_scale * 1024
+    write_b = w_gel * w_scale * 1024
+    out = {
+        "kernel": "k_contig<4,4,UnaryOp<1,float>> gelu(tanh) f32 [64,2048,4096]",
+        "bytes_per_launch": int(round(read_b + write_b)),
+        "read_bytes": int(round(read_b)), "write_bytes": int(round(write_b)),
+        "algorithmic_bytes": C2_GELU_BYTES,
+        "fetch_kib_raw": round(f_gel, 1), "write_kib_raw": round(w_gel, 1),
+        "fetch_scale": round(f_scale, 5), "write_scale": round(w_scale, 5),
+        "calibration": "abs.out over 2^28 f32 (1 GiB read, 1 GiB written): FETCH_SIZE "
+                       f"{f_cal:.1f} KiB, WRITE_SIZE {w_cal:.1f} KiB per dispatch",
+        "dispatches": {"fetch": nf, "write": nw},
+    }
+    path = os.path.join(HERE, "profiles", "gelu_tanh_c2_traffic.json")
+    with open(path, "w") as f:
+        json.dump(out, f, indent=1)
+        f.write("\n")
+    print(json.dumps(out))
+
+
 def probe(torch):
     """Kernel launches for counter collection: 10x abs.out over a 1 GiB f32
     buffer (reads 1 GiB, writes 1 GiB: the calibration of FETCH_SIZE and
@@ -340,6 +395,9 @@ def probe(torch):
 
 def main():
     a = parse()
+    if a.derive_traffic:
+        derive_traffic(*a.derive_traffic)
+        return
     if a.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {a.gpus} is not supported "
               "(the path's multi-GPU sharding is described in DESIGN.md, not run)", file=sys.stderr)
