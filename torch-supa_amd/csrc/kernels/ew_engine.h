@@ -4,8 +4,9 @@
 // Layout classes (chosen on the host, per call):
 //   CONTIG  every tensor operand is dense in the iteration order (1 coalesced
 //           dim, stride 1) or a one-element broadcast (stride 0).  Each thread
-//           moves UNROLL 16-byte vectors per operand, all loads issued before
-//           any arithmetic; the tail (< VEC elements) goes to the last block.
+//           moves UNROLL (the op's kUnroll) 16-byte vectors per operand, all
+//           loads issued before any arithmetic; the tail (< VEC elements) goes
+//           to the last block.
 //   VECND   N-d iteration whose innermost dim is a multiple of VEC and where
 //           every operand's innermost stride is 1 (vector load) or 0 (one
 //           element broadcast across the vector).  Coordinates of a vector's
@@ -44,10 +45,23 @@ constexpr int kMaxIn = SUPA_AMD_MAX_OPERANDS - 1;
 
 // --------------------------------------------------------------- binding
 // Op functors: `static constexpr int arity;` and
-// `template <class C> __device__ C operator()(const C* x) const`.
+// `template <class C> __device__ C operator()(const C* x) const`; optionally
+// `static constexpr int kUnroll;`, the 16-byte vectors per operand each thread
+// of the contiguous kernel handles.  One measured fastest for streaming ops on
+// MI355X (c1 add 80 % of HBM peak against 75 % at four); ops with long
+// arithmetic (gelu) set two so one vector's arithmetic overlaps the other's
+// loads.
+template <typename Op, typename = void> struct UnrollOf {
+  static constexpr int value = 1;
+};
+template <typename Op> struct UnrollOf<Op, std::void_t<decltype(Op::kUnroll)>> {
+  static constexpr int value = Op::kUnroll;
+};
+
 template <typename Op, typename C>
 struct Bind1 {  // binds input position K to value v
   static constexpr int arity = Op::arity - 1;
+  static constexpr int kUnroll = UnrollOf<Op>::value;
   Op op;
   int k;
   C v;

@@ -155,7 +155,7 @@ int launch_static(const Op& op, const supa_amd_ew_desc& d, const int* tin, hipSt
     for (int k = 0; k <= N; ++k)
       if (!(k > 0 && a.mode[k]) && !aligned(a.p[k], VEC * sizes_of[k])) al = false;
     if (al) {
-      constexpr int UNROLL = VEC >= 16 ? 1 : (VEC >= 8 ? 2 : 4);
+      constexpr int UNROLL = UnrollOf<Op>::value;
       const int64_t nvec = n / VEC;
       const int64_t per_block = (int64_t)UNROLL * kBlock;
       const int64_t blocks = std::max<int64_t>(1, (nvec + per_block - 1) / per_block);

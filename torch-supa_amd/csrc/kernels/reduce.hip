@@ -2,26 +2,27 @@
 // pointwise losses fused with the loss term (one read of the inputs, no
 // materialised loss tensor).
 //
-// Two-stage and deterministic.  Stage 1: a fixed grid of G blocks; each
-// thread accumulates a strided subset of 16-byte vectors in float32 (float64
-// for float64 data), the block combines its 256 partials in a fixed tree and
-// writes one partial.  Stage 2 runs in the block that finishes last (a
-// completion counter in the workspace): it combines the G partials in a fixed
-// tree, applies the scale (1 for sum, 1/n for mean) and stores the result,
-// then resets the counter.  The order of every addition depends only on n and
-// G, so reruns are bit-identical.
+// Two kernels, deterministic.  Stage 1: a fixed grid of G blocks; each thread
+// accumulates a strided subset of 16-byte vectors in float32 (float64 for
+// float64 data), the block combines its 256 partials in a fixed tree and
+// writes one partial to the workspace.  Stage 2: one block combines the G
+// partials in a fixed tree, applies the scale (1 for sum, 1/n for mean) and
+// stores the result.  The order of every addition depends only on n and G, so
+// reruns are bit-identical.  The kernel boundary orders the two stages: a
+// last-block-done counter would need a device-scope release per block, which
+// on gfx950 writes back and invalidates the XCD's L2 each time and halved the
+// stream rate when measured.
 //
 // Workspace contract: supa_amd_*_workspace_bytes() bytes of device memory
-// that are zero before the first call; each call leaves its counter at zero
-// again, so one buffer serves consecutive calls on one stream.  Calls that
-// overlap in time on different streams need separate buffers.
+// with no required contents; calls that overlap in time on different streams
+// need separate buffers.
 #include "ew_launch.h"
 #include "ops.h"
 
 namespace sa {
 
 constexpr int kRedBlocks = 1024;   // stage-1 grid (capped by the work)
-constexpr int kCounterBytes = 256; // counter slot, keeps partials aligned
+constexpr int kCounterBytes = 256; // reserved head of the workspace (keeps partials 256-byte aligned)
 
 enum RedLayout { R_CONTIG = 0, R_VECND = 1, R_STRIDED = 2 };
 
@@ -41,8 +42,10 @@ __device__ __forceinline__ ACC block_sum(ACC v, ACC* lds) {
   return r;  // valid in thread 0
 }
 
-// Accumulates op(...) over this thread's share of the iteration space.
-template <int LAYOUT, int VEC, typename Op, typename C, typename CT, typename ACC, typename... S>
+// Accumulates op(...) over this thread's share of the iteration space.  BC:
+// some input is broadcast (a one-element input, or stride 0 / re-read rows in
+// the N-d layout); without it the loop carries no per-operand branches.
+template <int LAYOUT, int VEC, bool BC, typename Op, typename C, typename CT, typename ACC, typename... S>
 __device__ __forceinline__ ACC accumulate(const Op& op, const TArgs<1 + sizeof...(S)>& a, const NdGeom& g, int64_t n) {
   constexpr int N = sizeof...(S);
   ACC acc = ACC(0);
@@ -56,7 +59,7 @@ __device__ __forceinline__ ACC accumulate(const Op& op, const TArgs<1 + sizeof..
         (([&] {
            using St = typename NthT<I, S...>::type;
            const St* p = static_cast<const St*>(a.p[1 + I]);
-           if (a.mode[1 + I]) {
+           if (BC && a.mode[1 + I]) {
              const C s = load_cvt<C, CT>(p[0]);
 #pragma unroll
              for (int k = 0; k < VEC; ++k) x[k][I] = s;
@@ -78,7 +81,7 @@ __device__ __forceinline__ ACC accumulate(const Op& op, const TArgs<1 + sizeof..
         (([&] {
            using St = typename NthT<I, S...>::type;
            const St* p = static_cast<const St*>(a.p[1 + I]);
-           y[I] = load_cvt<C, CT>(a.mode[1 + I] ? p[0] : p[t]);
+           y[I] = load_cvt<C, CT>((BC && a.mode[1 + I]) ? p[0] : p[t]);
          }()),
          ...);
       }(std::make_integer_sequence<int, N>{});
@@ -104,13 +107,13 @@ __device__ __forceinline__ ACC accumulate(const Op& op, const TArgs<1 + sizeof..
         (([&] {
            using St = typename NthT<I, S...>::type;
            const St* p = static_cast<const St*>(a.p[1 + I]) + off[1 + I];
-           if (a.st[1 + I][0] == 0) {
+           if (BC && a.st[1 + I][0] == 0) {
              const C s = load_cvt<C, CT>(p[0]);
 #pragma unroll
              for (int k = 0; k < VEC; ++k) x[k][I] = s;
            } else {
-             const Vec<St, VEC> w = a.mode[1 + I] ? *reinterpret_cast<const Vec<St, VEC>*>(p)
-                                                  : ld_stream(reinterpret_cast<const Vec<St, VEC>*>(p));
+             const Vec<St, VEC> w = (BC && a.mode[1 + I]) ? *reinterpret_cast<const Vec<St, VEC>*>(p)
+                                                          : ld_stream(reinterpret_cast<const Vec<St, VEC>*>(p));
 #pragma unroll
              for (int k = 0; k < VEC; ++k) x[k][I] = load_cvt<C, CT>(w.v[k]);
            }
@@ -147,33 +150,24 @@ __device__ __forceinline__ ACC accumulate(const Op& op, const TArgs<1 + sizeof..
   return acc;
 }
 
-template <int LAYOUT, int VEC, typename Op, typename C, typename CT, typename ACC, typename OT, typename... S>
+template <int LAYOUT, int VEC, bool BC, typename Op, typename C, typename CT, typename ACC, typename... S>
 __global__ void __launch_bounds__(kBlock)
-k_reduce(Op op, TArgs<1 + sizeof...(S)> a, NdGeom g, int64_t n, ACC scale, void* ws) {
+k_reduce_partial(Op op, TArgs<1 + sizeof...(S)> a, NdGeom g, int64_t n, ACC* __restrict__ partial) {
   __shared__ ACC lds[kBlock / 64];
-  __shared__ bool last;
-  ACC acc = accumulate<LAYOUT, VEC, Op, C, CT, ACC, S...>(op, a, g, n);
+  ACC acc = accumulate<LAYOUT, VEC, BC, Op, C, CT, ACC, S...>(op, a, g, n);
   acc = block_sum<ACC>(acc, lds);
-  unsigned int* counter = static_cast<unsigned int*>(ws);
-  ACC* partial = reinterpret_cast<ACC*>(static_cast<char*>(ws) + kCounterBytes);
-  if (threadIdx.x == 0) {
-    partial[blockIdx.x] = acc;
-    __threadfence();
-    const unsigned int done = atomicAdd(counter, 1u);
-    last = (done == gridDim.x - 1);
-  }
-  __syncthreads();
-  if (!last) return;
-  __threadfence();
-  // stage 2: fixed-order combine of the G partials
+  if (threadIdx.x == 0) partial[blockIdx.x] = acc;
+}
+
+// Stage 2: partials 0..nparts-1 in a fixed order, then the fixed block tree.
+template <typename ACC, typename OT>
+__global__ void __launch_bounds__(kBlock)
+k_reduce_final(const ACC* __restrict__ partial, int nparts, ACC scale, OT* __restrict__ out) {
+  __shared__ ACC lds[kBlock / 64];
   ACC v = ACC(0);
-  for (unsigned int i = threadIdx.x; i < gridDim.x; i += kBlock) v += partial[i];
-  __syncthreads();
+  for (int i = threadIdx.x; i < nparts; i += kBlock) v += partial[i];
   v = block_sum<ACC>(v, lds);
-  if (threadIdx.x == 0) {
-    static_cast<OT*>(a.p[0])[0] = from_arith<OT>(v * scale);
-    *counter = 0u;
-  }
+  if (threadIdx.x == 0) out[0] = from_arith<OT>(v * scale);
 }
 
 template <typename Op, typename C, typename CT, typename OT, typename... S>
@@ -234,18 +228,26 @@ int launch_reduce(const Op& op, const supa_amd_ew_desc& d, const int* tin, doubl
   const int64_t units = layout == R_STRIDED ? n : std::max<int64_t>(n / VEC, 1);
   const int64_t want = (units + 4 * kBlock - 1) / (4 * kBlock);
   const unsigned blocks = (unsigned)std::max<int64_t>(1, std::min<int64_t>(want, kRedBlocks));
-  const ACC sc = static_cast<ACC>(scale);
+  bool bc = false;
+  for (int i = 0; i < N; ++i) bc = bc || a.mode[1 + i] != 0 || a.st[1 + i][0] == 0;
+  ACC* partial = reinterpret_cast<ACC*>(static_cast<char*>(ws) + kCounterBytes);
   switch (layout) {
     case R_CONTIG:
-      k_reduce<R_CONTIG, VEC, Op, C, CT, ACC, OT, S...><<<blocks, kBlock, 0, st>>>(op, a, g, n, sc, ws);
+      if (bc) k_reduce_partial<R_CONTIG, VEC, true, Op, C, CT, ACC, S...><<<blocks, kBlock, 0, st>>>(op, a, g, n, partial);
+      else k_reduce_partial<R_CONTIG, VEC, false, Op, C, CT, ACC, S...><<<blocks, kBlock, 0, st>>>(op, a, g, n, partial);
       break;
     case R_VECND:
-      k_reduce<R_VECND, VEC, Op, C, CT, ACC, OT, S...><<<blocks, kBlock, 0, st>>>(op, a, g, n, sc, ws);
+      if (bc) k_reduce_partial<R_VECND, VEC, true, Op, C, CT, ACC, S...><<<blocks, kBlock, 0, st>>>(op, a, g, n, partial);
+      else k_reduce_partial<R_VECND, VEC, false, Op, C, CT, ACC, S...><<<blocks, kBlock, 0, st>>>(op, a, g, n, partial);
       break;
     default:
-      k_reduce<R_STRIDED, 1, Op, C, CT, ACC, OT, S...><<<blocks, kBlock, 0, st>>>(op, a, g, n, sc, ws);
+      k_reduce_partial<R_STRIDED, 1, false, Op, C, CT, ACC, S...><<<blocks, kBlock, 0, st>>>(op, a, g, n, partial);
       break;
   }
+  const int rc = launch_status();
+  if (rc) return rc;
+  k_reduce_final<ACC, OT><<<1, kBlock, 0, st>>>(partial, (int)blocks, static_cast<ACC>(scale),
+                                                  static_cast<OT*>(a.p[0]));
   return launch_status();
 }
 
