@@ -44,6 +44,25 @@ __device__ __forceinline__ float sa_expf(float x) {
   return nan ? x : res;
 }
 
+// sa_expf for callers whose result is NaN whenever x is NaN anyway (x / (1 +
+// exp(..x..)) forms): the same value for every non-NaN x, without the NaN
+// bookkeeping, and the clamp is one v_med3.
+__device__ __forceinline__ float sa_expf_nn(float x) {
+  x = __builtin_amdgcn_fmed3f(x, -104.0f, 89.0f);
+  const float k = rintf(x * 1.44269502f);
+  float r = fmaf(k, -0.693145751953125f, x);
+  r = fmaf(k, -1.42860677e-06f, r);
+  float p = 0.0013814599951729178f;
+  p = fmaf(p, r, 0.008368715643882751f);
+  p = fmaf(p, r, 0.04166838899254799f);
+  p = fmaf(p, r, 0.1666652113199234f);
+  p = fmaf(p, r, 0.4999999403953552f);
+  const float r2 = r * r;
+  p = fmaf(p, r2, r);
+  p = p + 1.0f;
+  return ldexpf(p, (int)k);
+}
+
 __device__ __forceinline__ float sa_logf(float x) {
   const bool tiny = x < 1.17549435e-38f;
   const float xs = tiny ? x * 8388608.0f : x;
@@ -91,9 +110,10 @@ __device__ __forceinline__ float sa_erff(float x) {
   l = fmaf(l, a, -0.6335323452949524f);
   l = fmaf(l, a, -1.1294389963150024f);
   l = fmaf(l, a, 0.00016132958990056068f);
-  float r = 1.0f - sa_expf(l);
+  float r = 1.0f - sa_expf_nn(l);
   r = (a >= 3.925f) ? 1.0f : r;
-  return copysignf(r, x);
+  r = copysignf(r, x);
+  return (x != x) ? x : r;
 }
 
 __device__ __forceinline__ float sa_tanhf(float x) {

@@ -13,6 +13,9 @@
 //           first element come from a chain of magic-number divisions; this
 //           covers a bias broadcast along rows, a per-row scalar broadcast
 //           and inputs that are permuted but dense.
+//   ROW2D   two dims, dense output, each input dense / row-broadcast /
+//           column-broadcast / one element: bias adds without the divider
+//           chain and 64-bit offsets of VECND.
 //   STRIDED anything else: one element per thread, per-operand offsets from
 //           the same divider chain.
 // Dtype classes:
@@ -202,6 +205,47 @@ k_vecnd(Op op, TArgs<1 + sizeof...(S)> a, NdGeom g, uint32_t nvec) {
 #pragma unroll
   for (int k = 0; k < VEC; ++k) w.v[k] = from_arith<OT>(op(x[k]));
   st_stream(reinterpret_cast<Vec<OT, VEC>*>(static_cast<OT*>(a.p[0]) + off[0]), w);
+}
+
+// ------------------------------------------------------------- ROW2D
+// Two iteration dims (inner size a multiple of VEC) with a dense output and
+// inputs that are each dense (strides 1, inner), a row broadcast down the
+// rows (1, 0), a column broadcast along a row (0, 1) or one element (0, 0):
+// the bias-add and per-row-scalar shapes.  One divide by the inner size gives
+// the (row, column) of a vector; every offset is 32-bit.
+enum Row2dKind { R2_DENSE = 0, R2_ROW = 1, R2_COL = 2, R2_ONE = 3 };
+
+template <int VEC, typename Op, typename C, typename CT, typename OT, typename... S>
+__global__ void __launch_bounds__(kBlock)
+k_row2d(Op op, TArgs<1 + sizeof...(S)> a, FastDiv inner, uint32_t nvec) {
+  constexpr int N = sizeof...(S);
+  const uint32_t v = blockIdx.x * kBlock + threadIdx.x;
+  if (v >= nvec) return;
+  uint32_t row, col;
+  inner.divmod(v * VEC, row, col);
+  C x[VEC][N > 0 ? N : 1];
+  [&]<int... I>(std::integer_sequence<int, I...>) {
+    (([&] {
+       using St = typename NthT<I, S...>::type;
+       const St* p = static_cast<const St*>(a.p[1 + I]);
+       const int kind = a.mode[1 + I];
+       if (kind == R2_DENSE || kind == R2_ROW) {
+         const Vec<St, VEC> w = kind == R2_DENSE ? ld_stream(reinterpret_cast<const Vec<St, VEC>*>(p) + v)
+                                                 : *reinterpret_cast<const Vec<St, VEC>*>(p + col);
+#pragma unroll
+         for (int k = 0; k < VEC; ++k) x[k][I] = load_cvt<C, CT>(w.v[k]);
+       } else {
+         const C s = load_cvt<C, CT>(p[kind == R2_COL ? row : 0u]);
+#pragma unroll
+         for (int k = 0; k < VEC; ++k) x[k][I] = s;
+       }
+     }()),
+     ...);
+  }(std::make_integer_sequence<int, N>{});
+  Vec<OT, VEC> w;
+#pragma unroll
+  for (int k = 0; k < VEC; ++k) w.v[k] = from_arith<OT>(op(x[k]));
+  st_stream(reinterpret_cast<Vec<OT, VEC>*>(a.p[0]) + v, w);
 }
 
 // ----------------------------------------------------------- STRIDED

@@ -4,9 +4,9 @@
 // One launch covers up to kMtaTensors tensors.  The tensor table (pointers,
 // element counts, chunk prefix sums) travels in the kernel arguments, so a
 // launch needs no device-side metadata and no allocation.  Each workgroup
-// owns one chunk of kChunk elements of one tensor (found by a scan of the
-// chunk prefix table); inside the chunk every thread moves 16-byte vectors of
-// each operand with all loads of an iteration issued before the math.
+// owns one chunk of one tensor (found by bisection of the chunk prefix
+// table) -- one or two 16-byte vectors of each operand per thread, all loads
+// of a vector issued before the math.
 // Tensors whose base is not 16-byte aligned, and the last partial vector of a
 // tensor, take a scalar path.  The reference's counterpart is upstream
 // MultiTensorApply.cuh (kChunkSize 65536, 512 threads, ILP 4, <= 110 / 36
@@ -17,8 +17,11 @@
 namespace sa {
 
 constexpr int kMtaTensors = 40;
-constexpr int64_t kChunk = 16384;
 constexpr int kMtaBlock = 256;
+// Elements per workgroup: one 16-byte vector per thread for the list forms and
+// AdamW, two for the scalar forms -- the fastest measured on MI355X (c5 AdamW
+// 74 % of HBM peak against 66 % with 16384-element chunks).
+template <typename T> constexpr int64_t chunk_one() { return (int64_t)kMtaBlock * (16 / (int64_t)sizeof(T)); }
 
 // ------------------------------------------------------------- foreach
 struct ForeachTable {
@@ -30,13 +33,19 @@ struct ForeachTable {
   int32_t ntensors;
 };
 
+// The tensor whose chunk range holds block `blk`: the last k with
+// chunk_start[k] <= blk (chunk_start is strictly increasing), by bisection.
 __device__ __forceinline__ int find_tensor(const uint32_t* chunk_start, int nt, uint32_t blk) {
-  int k = 0;
-  while (k + 1 < nt && chunk_start[k + 1] <= blk) ++k;
-  return k;
+  int lo = 0, hi = nt - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (chunk_start[mid] <= blk) lo = mid;
+    else hi = mid - 1;
+  }
+  return lo;
 }
 
-template <typename T, int OP, bool LIST>
+template <typename T, int OP, bool LIST, int64_t CHUNK>
 __global__ void __launch_bounds__(kMtaBlock)
 k_foreach(ForeachTable tab, double scalar, double alpha) {
   using C = opmath_t<T>;
@@ -44,8 +53,8 @@ k_foreach(ForeachTable tab, double scalar, double alpha) {
   const int k = find_tensor(tab.chunk_start, tab.ntensors, blockIdx.x);
   const int64_t chunk = blockIdx.x - tab.chunk_start[k];
   const int64_t n = tab.numel[k];
-  const int64_t lo = chunk * kChunk;
-  const int64_t hi = lo + kChunk < n ? lo + kChunk : n;
+  const int64_t lo = chunk * CHUNK;
+  const int64_t hi = lo + CHUNK < n ? lo + CHUNK : n;
   T* out = static_cast<T*>(tab.out[k]);
   const T* a = static_cast<const T*>(tab.a[k]);
   const T* b = LIST ? static_cast<const T*>(tab.b[k]) : nullptr;
@@ -150,7 +159,7 @@ __device__ __forceinline__ void adamw_elem(T& pr, T& gr, T& mr, T& vr, T* vmx, c
   vr = from_arith<T>(eas);
 }
 
-template <typename T>
+template <typename T, int64_t CHUNK, int UNR>
 __global__ void __launch_bounds__(kMtaBlock)
 k_adamw(AdamTable tab, AdamHyper h) {
   if (h.found_inf && *h.found_inf == 1.0f) return;
@@ -158,8 +167,8 @@ k_adamw(AdamTable tab, AdamHyper h) {
   const int k = find_tensor(tab.chunk_start, tab.ntensors, blockIdx.x);
   const int64_t chunk = blockIdx.x - tab.chunk_start[k];
   const int64_t n = tab.numel[k];
-  const int64_t lo = chunk * kChunk;
-  const int64_t hi = lo + kChunk < n ? lo + kChunk : n;
+  const int64_t lo = chunk * CHUNK;
+  const int64_t hi = lo + CHUNK < n ? lo + CHUNK : n;
   const double lr = h.lr_ptr ? (double)(*h.lr_ptr) : h.lr;
   const float step = *tab.step[k];
   const float bc1 = (float)(1.0 - pow_steps(h.beta1, step));
@@ -175,18 +184,33 @@ k_adamw(AdamTable tab, AdamHyper h) {
   int64_t start = lo;
   if (vec) {
     const int64_t nv = (hi - lo) / V;
-    for (int64_t i = threadIdx.x; i < nv; i += kMtaBlock) {
-      const int64_t e = lo + i * V;
-      Vec<T, V> P = ld_stream(reinterpret_cast<const Vec<T, V>*>(p + e));
-      Vec<T, V> G = ld_stream(reinterpret_cast<const Vec<T, V>*>(g + e));
-      Vec<T, V> M = ld_stream(reinterpret_cast<const Vec<T, V>*>(m + e));
-      Vec<T, V> W = ld_stream(reinterpret_cast<const Vec<T, V>*>(v + e));
+    for (int64_t i0 = threadIdx.x; i0 < nv; i0 += kMtaBlock * UNR) {
+      Vec<T, V> P[UNR], G[UNR], M[UNR], W[UNR];
 #pragma unroll
-      for (int j = 0; j < V; ++j) adamw_elem<T>(P.v[j], G.v[j], M.v[j], W.v[j], nullptr, h, lr, lr_wd, bc1, bc2_sqrt, step_size);
-      st_stream(reinterpret_cast<Vec<T, V>*>(p + e), P);
-      if (h.grad_scale) st_stream(reinterpret_cast<Vec<T, V>*>(g + e), G);
-      st_stream(reinterpret_cast<Vec<T, V>*>(m + e), M);
-      st_stream(reinterpret_cast<Vec<T, V>*>(v + e), W);
+      for (int u = 0; u < UNR; ++u) {
+        const int64_t i = i0 + u * kMtaBlock;
+        if (i < nv) {
+          const int64_t e = lo + i * V;
+          P[u] = ld_stream(reinterpret_cast<const Vec<T, V>*>(p + e));
+          G[u] = ld_stream(reinterpret_cast<const Vec<T, V>*>(g + e));
+          M[u] = ld_stream(reinterpret_cast<const Vec<T, V>*>(m + e));
+          W[u] = ld_stream(reinterpret_cast<const Vec<T, V>*>(v + e));
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < UNR; ++u) {
+        const int64_t i = i0 + u * kMtaBlock;
+        if (i < nv) {
+          const int64_t e = lo + i * V;
+#pragma unroll
+          for (int j = 0; j < V; ++j)
+            adamw_elem<T>(P[u].v[j], G[u].v[j], M[u].v[j], W[u].v[j], nullptr, h, lr, lr_wd, bc1, bc2_sqrt, step_size);
+          st_stream(reinterpret_cast<Vec<T, V>*>(p + e), P[u]);
+          if (h.grad_scale) st_stream(reinterpret_cast<Vec<T, V>*>(g + e), G[u]);
+          st_stream(reinterpret_cast<Vec<T, V>*>(m + e), M[u]);
+          st_stream(reinterpret_cast<Vec<T, V>*>(v + e), W[u]);
+        }
+      }
     }
     start = lo + nv * V;
   }
@@ -209,6 +233,88 @@ int with_mta_storage(int dtype, F&& f) {
 
 using namespace sa;
 
+namespace sa {
+
+template <typename T, int64_t CHUNK>
+int launch_foreach(int op, int32_t ntensors, void* const* out, void* const* a, void* const* b, const int64_t* numel,
+                   double scalar, double alpha, hipStream_t st) {
+  int i = 0;
+  while (i < ntensors) {
+    ForeachTable tab{};
+    uint32_t chunks = 0;
+    int nt = 0;
+    while (i < ntensors && nt < kMtaTensors) {
+      if (numel[i] < 0) return SUPA_AMD_EINVAL;
+      const int64_t c = (numel[i] + CHUNK - 1) / CHUNK;
+      if (c > (int64_t)0x7fffffff) return SUPA_AMD_ELAYOUT;
+      if ((int64_t)chunks + c > (int64_t)0x7fffffff) break;
+      if (numel[i] > 0) {
+        tab.out[nt] = out[i];
+        tab.a[nt] = a[i];
+        tab.b[nt] = b ? b[i] : nullptr;
+        tab.numel[nt] = numel[i];
+        tab.chunk_start[nt] = chunks;
+        chunks += (uint32_t)c;
+        ++nt;
+      }
+      ++i;
+    }
+    tab.chunk_start[nt] = chunks;
+    tab.ntensors = nt;
+    if (nt == 0) continue;
+    if (op == SUPA_AMD_FOREACH_ADD) {
+      if (b) k_foreach<T, SUPA_AMD_FOREACH_ADD, true, CHUNK><<<chunks, kMtaBlock, 0, st>>>(tab, scalar, alpha);
+      else k_foreach<T, SUPA_AMD_FOREACH_ADD, false, CHUNK><<<chunks, kMtaBlock, 0, st>>>(tab, scalar, alpha);
+    } else {
+      if (b) k_foreach<T, SUPA_AMD_FOREACH_MUL, true, CHUNK><<<chunks, kMtaBlock, 0, st>>>(tab, scalar, alpha);
+      else k_foreach<T, SUPA_AMD_FOREACH_MUL, false, CHUNK><<<chunks, kMtaBlock, 0, st>>>(tab, scalar, alpha);
+    }
+    const int rc = launch_status();
+    if (rc) return rc;
+  }
+  return SUPA_AMD_OK;
+}
+
+template <typename T, int64_t CHUNK, int UNR>
+int launch_adamw(int32_t ntensors, void* const* params, void* const* grads, void* const* exp_avgs,
+                 void* const* exp_avg_sqs, void* const* max_exp_avg_sqs, void* const* state_steps,
+                 const int64_t* numel, const AdamHyper& h, hipStream_t st) {
+  int i = 0;
+  while (i < ntensors) {
+    AdamTable tab{};
+    uint32_t chunks = 0;
+    int nt = 0;
+    while (i < ntensors && nt < kMtaTensors) {
+      if (numel[i] < 0 || !state_steps[i]) return SUPA_AMD_EINVAL;
+      const int64_t c = (numel[i] + CHUNK - 1) / CHUNK;
+      if (c > (int64_t)0x7fffffff) return SUPA_AMD_ELAYOUT;
+      if ((int64_t)chunks + c > (int64_t)0x7fffffff) break;
+      if (numel[i] > 0) {
+        tab.p[nt] = params[i];
+        tab.g[nt] = grads[i];
+        tab.m[nt] = exp_avgs[i];
+        tab.v[nt] = exp_avg_sqs[i];
+        tab.vmax[nt] = h.amsgrad ? max_exp_avg_sqs[i] : nullptr;
+        tab.step[nt] = static_cast<const float*>(state_steps[i]);
+        tab.numel[nt] = numel[i];
+        tab.chunk_start[nt] = chunks;
+        chunks += (uint32_t)c;
+        ++nt;
+      }
+      ++i;
+    }
+    tab.chunk_start[nt] = chunks;
+    tab.ntensors = nt;
+    if (nt == 0) continue;
+    k_adamw<T, CHUNK, UNR><<<chunks, kMtaBlock, 0, st>>>(tab, h);
+    const int rc = launch_status();
+    if (rc) return rc;
+  }
+  return SUPA_AMD_OK;
+}
+
+}  // namespace sa
+
 extern "C" {
 
 int supa_amd_foreach_binary(int op, int32_t ntensors, void* const* out, void* const* a, void* const* b,
@@ -218,40 +324,8 @@ int supa_amd_foreach_binary(int op, int32_t ntensors, void* const* out, void* co
   hipStream_t st = static_cast<hipStream_t>(stream);
   return with_mta_storage(dtype, [&](auto* tag) -> int {
     using T = std::remove_pointer_t<decltype(tag)>;
-    int i = 0;
-    while (i < ntensors) {
-      ForeachTable tab{};
-      uint32_t chunks = 0;
-      int nt = 0;
-      while (i < ntensors && nt < kMtaTensors) {
-        if (numel[i] < 0) return SUPA_AMD_EINVAL;
-        const int64_t c = (numel[i] + kChunk - 1) / kChunk;
-        if ((int64_t)chunks + c > (int64_t)0x7fffffff) break;
-        if (numel[i] > 0) {
-          tab.out[nt] = out[i];
-          tab.a[nt] = a[i];
-          tab.b[nt] = b ? b[i] : nullptr;
-          tab.numel[nt] = numel[i];
-          tab.chunk_start[nt] = chunks;
-          chunks += (uint32_t)c;
-          ++nt;
-        }
-        ++i;
-      }
-      tab.chunk_start[nt] = chunks;
-      tab.ntensors = nt;
-      if (nt == 0) continue;
-      if (op == SUPA_AMD_FOREACH_ADD) {
-        if (b) k_foreach<T, SUPA_AMD_FOREACH_ADD, true><<<chunks, kMtaBlock, 0, st>>>(tab, scalar, alpha);
-        else k_foreach<T, SUPA_AMD_FOREACH_ADD, false><<<chunks, kMtaBlock, 0, st>>>(tab, scalar, alpha);
-      } else {
-        if (b) k_foreach<T, SUPA_AMD_FOREACH_MUL, true><<<chunks, kMtaBlock, 0, st>>>(tab, scalar, alpha);
-        else k_foreach<T, SUPA_AMD_FOREACH_MUL, false><<<chunks, kMtaBlock, 0, st>>>(tab, scalar, alpha);
-      }
-      const int rc = launch_status();
-      if (rc) return rc;
-    }
-    return SUPA_AMD_OK;
+    if (b) return launch_foreach<T, chunk_one<T>()>(op, ntensors, out, a, b, numel, scalar, alpha, st);
+    return launch_foreach<T, 2 * chunk_one<T>()>(op, ntensors, out, a, b, numel, scalar, alpha, st);
   });
 }
 
@@ -264,40 +338,11 @@ int supa_amd_fused_adamw(int32_t ntensors, void* const* params, void* const* gra
   if (ntensors > 0 && (!params || !grads || !exp_avgs || !exp_avg_sqs || !state_steps || !numel)) return SUPA_AMD_EINVAL;
   if (amsgrad && ntensors > 0 && !max_exp_avg_sqs) return SUPA_AMD_EINVAL;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  AdamHyper h{lr, beta1, beta2, weight_decay, eps, lr_ptr, grad_scale, found_inf, amsgrad ? 1 : 0, maximize ? 1 : 0};
+  const AdamHyper h{lr, beta1, beta2, weight_decay, eps, lr_ptr, grad_scale, found_inf, amsgrad ? 1 : 0, maximize ? 1 : 0};
   return with_mta_storage(dtype, [&](auto* tag) -> int {
     using T = std::remove_pointer_t<decltype(tag)>;
-    int i = 0;
-    while (i < ntensors) {
-      AdamTable tab{};
-      uint32_t chunks = 0;
-      int nt = 0;
-      while (i < ntensors && nt < kMtaTensors) {
-        if (numel[i] < 0 || !state_steps[i]) return SUPA_AMD_EINVAL;
-        const int64_t c = (numel[i] + kChunk - 1) / kChunk;
-        if ((int64_t)chunks + c > (int64_t)0x7fffffff) break;
-        if (numel[i] > 0) {
-          tab.p[nt] = params[i];
-          tab.g[nt] = grads[i];
-          tab.m[nt] = exp_avgs[i];
-          tab.v[nt] = exp_avg_sqs[i];
-          tab.vmax[nt] = amsgrad ? max_exp_avg_sqs[i] : nullptr;
-          tab.step[nt] = static_cast<const float*>(state_steps[i]);
-          tab.numel[nt] = numel[i];
-          tab.chunk_start[nt] = chunks;
-          chunks += (uint32_t)c;
-          ++nt;
-        }
-        ++i;
-      }
-      tab.chunk_start[nt] = chunks;
-      tab.ntensors = nt;
-      if (nt == 0) continue;
-      k_adamw<T><<<chunks, kMtaBlock, 0, st>>>(tab, h);
-      const int rc = launch_status();
-      if (rc) return rc;
-    }
-    return SUPA_AMD_OK;
+    return launch_adamw<T, chunk_one<T>(), 1>(ntensors, params, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs, state_steps, numel,
+                                   h, st);
   });
 }
 

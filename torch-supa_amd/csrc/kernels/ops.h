@@ -109,7 +109,7 @@ template <typename C> __device__ __forceinline__ C gelu_tanh(C x) {
   if constexpr (std::is_same<C, float>::value) {
     const float x3 = (x * x) * x;
     const float inner = (-2.0f * (float)kGeluBetaTanh) * fmaf((float)kGeluKappa, x3, x);
-    return x / (1.0f + sa_expf(inner));
+    return x / (1.0f + sa_expf_nn(inner));  // a NaN x makes the quotient NaN
   } else {
     const C x3 = (x * x) * x;
     const C inner = C(-2.0 * kGeluBetaTanh) * fma(C(kGeluKappa), x3, x);
@@ -145,7 +145,10 @@ template <int K, typename C> struct UnaryOp {
     const C x = v[0];
     if constexpr (K == U_GELU) return gelu_none<C>(x);
     else if constexpr (K == U_GELU_TANH) return gelu_tanh<C>(x);
-    else if constexpr (K == U_SILU) return x / (C(1) + expx<C>(-x));
+    else if constexpr (K == U_SILU) {
+      if constexpr (std::is_same<C, float>::value) return x / (1.0f + sa_expf_nn(-x));  // NaN x: NaN quotient
+      else return x / (C(1) + expx<C>(-x));
+    }
     else if constexpr (K == U_SIGMOID) return sigmoidx<C>(x);
     else if constexpr (K == U_TANH) return tanhx<C>(x);
     else if constexpr (K == U_EXP) return expx<C>(x);
