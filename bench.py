@@ -193,38 +193,52 @@ def bench_c3(torch, timer, iters=10):
     return res
 
 
-def bench_c4(torch, timer, iters=20):
+def bench_c4(torch, timer, iters=21, sets=3):
+    """c4 with `sets` independent input sets used round-robin, so no op reads
+    its inputs back from the 256 MB MALL (one set of x, t is 256 MB)."""
     import torch.nn.functional as F
     R, C = 32, 1048576
     n = R * C
-    x = gen(torch, (R, C), 6, torch.float32)
-    t = gen(torch, (R, C), 7, torch.float32)
-    tb = gen(torch, (R, C), 8, torch.float32, kind="bernoulli", a=0.3)
+    xs = [gen(torch, (R, C), 6 + 10 * k, torch.float32) for k in range(sets)]
+    ts = [gen(torch, (R, C), 7 + 10 * k, torch.float32) for k in range(sets)]
+    tbs = [gen(torch, (R, C), 8 + 10 * k, torch.float32, kind="bernoulli", a=0.3) for k in range(sets)]
     pw = gen(torch, (C,), 9, torch.float32, kind="uniform", a=0.5, b=2.0)
     res = {}
     pwb = 4 * C
+
+    def rot(fn):
+        it = [0]
+
+        def call():
+            k = it[0] % sets
+            it[0] += 1
+            return fn(k)
+        return call
+
     for red in ("none", "sum", "mean"):
-        go = gen(torch, (R, C), 11, torch.float32) if red == "none" else torch.ones((), device="supa")
+        gos = ([gen(torch, (R, C), 11 + 10 * k, torch.float32) for k in range(sets)] if red == "none"
+               else [torch.ones((), device="supa")] * sets)
+        rc = {"none": 0, "mean": 1, "sum": 2}[red]
         fwd_b = 12 * n if red == "none" else 8 * n + 4
         bwd_b = 16 * n if red == "none" else 12 * n + 4
-        res[f"mse_{red}_fwd"] = entry(fwd_b, timer.time(lambda: F.mse_loss(x, t, reduction=red), iters))
+        res[f"mse_{red}_fwd"] = entry(fwd_b, timer.time(rot(lambda k: F.mse_loss(xs[k], ts[k], reduction=red)), iters))
         res[f"mse_{red}_bwd"] = entry(bwd_b, timer.time(
-            lambda: torch.ops.aten.mse_loss_backward(go, x, t, {"none": 0, "mean": 1, "sum": 2}[red]), iters))
+            rot(lambda k: torch.ops.aten.mse_loss_backward(gos[k], xs[k], ts[k], rc)), iters))
         res[f"smooth_l1_{red}_fwd"] = entry(fwd_b, timer.time(
-            lambda: F.smooth_l1_loss(x, t, reduction=red, beta=1.0), iters))
+            rot(lambda k: F.smooth_l1_loss(xs[k], ts[k], reduction=red, beta=1.0)), iters))
         res[f"smooth_l1_{red}_bwd"] = entry(bwd_b, timer.time(
-            lambda: torch.ops.aten.smooth_l1_loss_backward(go, x, t, {"none": 0, "mean": 1, "sum": 2}[red], 1.0),
-            iters))
+            rot(lambda k: torch.ops.aten.smooth_l1_loss_backward(gos[k], xs[k], ts[k], rc, 1.0)), iters))
         bce_fwd_b = (12 * n if red == "none" else 8 * n + 4) + pwb
         res[f"bce_{red}_fwd"] = entry(bce_fwd_b, timer.time(
-            lambda: F.binary_cross_entropy_with_logits(x, tb, pos_weight=pw, reduction=red), iters))
-        xg = x.detach().requires_grad_()
-        loss = F.binary_cross_entropy_with_logits(xg, tb, pos_weight=pw, reduction=red)
+            rot(lambda k: F.binary_cross_entropy_with_logits(xs[k], tbs[k], pos_weight=pw, reduction=red)), iters))
+        xgs = [x.detach().requires_grad_() for x in xs]
+        losses = [F.binary_cross_entropy_with_logits(xg, tb, pos_weight=pw, reduction=red) for xg, tb in zip(xgs, tbs)]
         gsz = 4 if red != "none" else 4 * n
         # the autograd formula's op sequence: mul, add, sub, sigmoid, mul, sub, mul(grad)[, div]
         bce_bwd_b = (8 * n + pwb) + 8 * n + 12 * n + 8 * n + 12 * n + 12 * n + (8 * n + gsz) + (8 * n if red == "mean" else 0)
         res[f"bce_{red}_bwd"] = entry(bce_bwd_b, timer.time(
-            lambda: torch.autograd.grad(loss, xg, go, retain_graph=True), iters))
+            rot(lambda k: torch.autograd.grad(losses[k], xgs[k], gos[k], retain_graph=True)), iters))
+        del xgs, losses, gos
     return res
 
 

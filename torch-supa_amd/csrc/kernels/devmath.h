@@ -88,6 +88,26 @@ __device__ __forceinline__ float sa_logf(float x) {
   return r;
 }
 
+// sa_logf for finite normal x > 0 (callers whose NaN inputs turn the result
+// NaN elsewhere): the same value there, without the special-case selects.
+__device__ __forceinline__ float sa_logf_normal(float x) {
+  const uint32_t ix = __float_as_uint(x) - 0x3f3504f3u;
+  const int e = (int32_t)ix >> 23;
+  const float f = __uint_as_float((ix & 0x007fffffu) + 0x3f3504f3u) - 1.0f;
+  float q = -0.07634429633617401f;
+  q = fmaf(q, f, 0.12761549651622772f);
+  q = fmaf(q, f, -0.131601944565773f);
+  q = fmaf(q, f, 0.14201761782169342f);
+  q = fmaf(q, f, -0.16623356938362122f);
+  q = fmaf(q, f, 0.20001226663589478f);
+  q = fmaf(q, f, -0.250008225440979f);
+  q = fmaf(q, f, 0.3333333134651184f);
+  const float f2 = f * f;
+  const float y = fmaf(f2, fmaf(f, q, -0.5f), f);
+  const float ef = (float)e;
+  return fmaf(ef, 0.693145751953125f, fmaf(ef, 1.42860677e-06f, y));
+}
+
 __device__ __forceinline__ float sa_erff(float x) {
   const float a = fabsf(x);
   if (a < 0.921875f) {

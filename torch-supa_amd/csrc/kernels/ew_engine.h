@@ -164,7 +164,10 @@ k_contig(Op op, TArgs<1 + sizeof...(S)> a, int64_t n) {
 }
 
 // ------------------------------------------------------------- VECND
-template <int VEC, typename Op, typename C, typename CT, typename OT, typename... S>
+// OFF: the offset type, int32_t when the host has checked that every
+// operand's largest offset fits (one 32-bit multiply per dim and operand
+// instead of a 64-bit product), int64_t otherwise.
+template <int VEC, typename OFF, typename Op, typename C, typename CT, typename OT, typename... S>
 __global__ void __launch_bounds__(kBlock)
 k_vecnd(Op op, TArgs<1 + sizeof...(S)> a, NdGeom g, uint32_t nvec) {
   constexpr int N = sizeof...(S);
@@ -173,15 +176,15 @@ k_vecnd(Op op, TArgs<1 + sizeof...(S)> a, NdGeom g, uint32_t nvec) {
   // coordinates of the vector's first element
   uint32_t q, r;
   g.div[0].divmod(v * VEC, q, r);
-  int64_t off[1 + N];
+  OFF off[1 + N];
 #pragma unroll
-  for (int k = 0; k <= N; ++k) off[k] = (int64_t)r * a.st[k][0];
+  for (int k = 0; k <= N; ++k) off[k] = (OFF)r * (OFF)a.st[k][0];
   for (int d = 1; d < g.ndim; ++d) {
     uint32_t qq, rr;
     g.div[d].divmod(q, qq, rr);
     q = qq;
 #pragma unroll
-    for (int k = 0; k <= N; ++k) off[k] += (int64_t)rr * a.st[k][d];
+    for (int k = 0; k <= N; ++k) off[k] += (OFF)rr * (OFF)a.st[k][d];
   }
   C x[VEC][N > 0 ? N : 1];
   [&]<int... I>(std::integer_sequence<int, I...>) {
@@ -249,13 +252,13 @@ k_row2d(Op op, TArgs<1 + sizeof...(S)> a, FastDiv inner, uint32_t nvec) {
 }
 
 // ----------------------------------------------------------- STRIDED
-template <typename Op, typename C, typename CT, typename OT, typename... S>
+template <typename OFF, typename Op, typename C, typename CT, typename OT, typename... S>
 __global__ void __launch_bounds__(kBlock)
 k_strided(Op op, TArgs<1 + sizeof...(S)> a, NdGeom g, uint32_t n) {
   constexpr int N = sizeof...(S);
   const uint32_t i = blockIdx.x * kBlock + threadIdx.x;
   if (i >= n) return;
-  int64_t off[1 + N];
+  OFF off[1 + N];
 #pragma unroll
   for (int k = 0; k <= N; ++k) off[k] = 0;
   uint32_t q = i;
@@ -264,7 +267,7 @@ k_strided(Op op, TArgs<1 + sizeof...(S)> a, NdGeom g, uint32_t n) {
     g.div[d].divmod(q, qq, rr);
     q = qq;
 #pragma unroll
-    for (int k = 0; k <= N; ++k) off[k] += (int64_t)rr * a.st[k][d];
+    for (int k = 0; k <= N; ++k) off[k] += (OFF)rr * (OFF)a.st[k][d];
   }
   C y[N > 0 ? N : 1];
   [&]<int... I>(std::integer_sequence<int, I...>) {

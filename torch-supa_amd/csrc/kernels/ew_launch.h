@@ -200,6 +200,13 @@ int launch_static(const Op& op, const supa_amd_ew_desc& d, const int* tin, hipSt
       }
     }
     const NdGeom g = make_geom(p);
+    // every operand's largest element offset below 2^31: 32-bit offset math
+    bool off32 = true;
+    for (int k = 0; k <= N; ++k) {
+      int64_t mx = 0;
+      for (int j = 0; j < p.ndim; ++j) mx += (p.sizes[j] - 1) * (b.st[k][j] < 0 ? -b.st[k][j] : b.st[k][j]);
+      if (mx >= (int64_t(1) << 31)) off32 = false;
+    }
     // VECND?
     bool vnd = p.ndim >= 1 && (p.sizes[0] % VEC) == 0 && b.st[0][0] == 1 && VEC > 1;
     for (int k = 0; k <= N && vnd; ++k) {
@@ -220,11 +227,13 @@ int launch_static(const Op& op, const supa_amd_ew_desc& d, const int* tin, hipSt
       }
       const uint32_t nvec = (uint32_t)(pn / VEC);
       const unsigned blocks = (nvec + kBlock - 1) / kBlock;
-      k_vecnd<VEC, Op, C, CT, OT, S...><<<blocks, kBlock, 0, st>>>(op, b, g, nvec);
+      if (off32) k_vecnd<VEC, int32_t, Op, C, CT, OT, S...><<<blocks, kBlock, 0, st>>>(op, b, g, nvec);
+      else k_vecnd<VEC, int64_t, Op, C, CT, OT, S...><<<blocks, kBlock, 0, st>>>(op, b, g, nvec);
       return launch_status();
     }
     const unsigned blocks = (unsigned)((pn + kBlock - 1) / kBlock);
-    k_strided<Op, C, CT, OT, S...><<<blocks, kBlock, 0, st>>>(op, b, g, (uint32_t)pn);
+    if (off32) k_strided<int32_t, Op, C, CT, OT, S...><<<blocks, kBlock, 0, st>>>(op, b, g, (uint32_t)pn);
+    else k_strided<int64_t, Op, C, CT, OT, S...><<<blocks, kBlock, 0, st>>>(op, b, g, (uint32_t)pn);
     return launch_status();
   });
 }

@@ -240,7 +240,11 @@ template <bool PW, bool W, typename C> struct BceTermOp {
   __device__ __forceinline__ C operator()(const C* v) const {
     const C x = v[0], t = v[1];
     const C m = x < C(0) ? -x : C(0);
-    const C lse = logx<C>(C(1) + expx<C>(-fabs(x)));
+    C lse;
+    if constexpr (std::is_same<C, float>::value)
+      lse = sa_logf_normal(1.0f + sa_expf_nn(-fabsf(x)));  // argument in [1, 2]; a NaN x makes r NaN below
+    else
+      lse = logx<C>(C(1) + expx<C>(-fabs(x)));
     C r;
     if constexpr (PW) {
       const C lw = muladd<C>(v[2] - C(1), t, C(1));
