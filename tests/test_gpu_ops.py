@@ -112,6 +112,25 @@ def test_broadcast_scalar_inplace_out(no_fallback):
     assert torch.equal(torch.div(da, dc, rounding_mode="trunc").cpu(), torch.div(a, c, rounding_mode="trunc"))
 
 
+@pytest.mark.parametrize("rows,cols", [(1, 8), (3, 1028), (7, 2048), (65, 1032), (513, 4100)])
+def test_row_and_column_broadcasts(rows, cols, no_fallback):
+    """Two-dim broadcasts (row vector, column vector, one element, and the
+    bf16 + f32 promotion) over odd row counts and rows that do not fill a
+    workgroup; integer-exact against the host kernels."""
+    x = seeded((rows, cols), 40)
+    xb = seeded((rows, cols), 41).to(torch.bfloat16)
+    rowv = seeded((cols,), 42)
+    colv = seeded((rows, 1), 43)
+    one = seeded((1, 1), 44)
+    dx, dxb, drow, dcol, done = dev(x), dev(xb), dev(rowv), dev(colv), dev(one)
+    assert torch.equal((dx + drow).cpu(), x + rowv)
+    assert torch.equal((dx * dcol).cpu(), x * colv)
+    assert torch.equal((dx - done).cpu(), x - one)
+    assert torch.equal((dxb + drow).cpu(), xb + rowv)  # bf16 + f32 -> f32
+    assert torch.equal((drow + dxb * 2).cpu(), rowv + xb * 2)
+    assert torch.equal(torch.div(dcol, drow).cpu(), torch.div(colv, rowv))  # outer-product shape
+
+
 def test_transposed_and_strided_views(no_fallback):
     base = seeded((1, 5120, 1024), 9)
     a = base.transpose(1, 2)  # [1, 1024, 5120] with strides (5242880, 1, 1024): the reference's worst case

@@ -39,6 +39,10 @@ HIP_FLAGS = [
     "-ffp-contract=off",
     # no packed fp32 VALU instructions
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # without packed fp32 the SLP vectorizer's <2 x float> groups gain nothing,
+    # and some (f16 negation in the two-row broadcast kernel) fail instruction
+    # selection
+    "-fno-slp-vectorize",
     "-I", INCLUDE, "-I", KERNEL_DIR,
 ]
 

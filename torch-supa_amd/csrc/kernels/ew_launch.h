@@ -193,10 +193,13 @@ int launch_static(const Op& op, const supa_amd_ew_desc& d, const int* tin, hipSt
         if (ok && s0 == 1 && !aligned(b.p[k], VEC * sizes_of[k])) ok = false;
       }
       if (ok) {
-        const uint32_t nvec = (uint32_t)(pn / VEC);
-        const unsigned blocks = (nvec + kBlock - 1) / kBlock;
-        k_row2d<VEC, Op, C, CT, OT, S...><<<blocks, kBlock, 0, st>>>(op, c, FastDiv((uint32_t)p.sizes[0]), nvec);
-        return launch_status();
+        const uint32_t inner = (uint32_t)p.sizes[0], rows = (uint32_t)p.sizes[1];
+        const uint32_t bpr = (inner / VEC + kBlock - 1) / kBlock;
+        const uint64_t blocks = (uint64_t)bpr * ((rows + kRow2dRows - 1) / kRow2dRows);
+        if (blocks < (1ull << 31)) {
+          k_row2d<VEC, Op, C, CT, OT, S...><<<(unsigned)blocks, kBlock, 0, st>>>(op, c, inner, rows, FastDiv(bpr));
+          return launch_status();
+        }
       }
     }
     const NdGeom g = make_geom(p);
