@@ -346,6 +346,8 @@ def derive_traffic(fetch_csv, write_csv):
     dispatches."""
     import csv
 
+    names = set()
+
     def per_kernel(path):
         cal, gel = [], []
         with open(path) as f:
@@ -357,6 +359,7 @@ def derive_traffic(fetch_csv, write_csv):
                     cal.append(val)
                 elif PROBE_GELU_KERNEL in name:
                     gel.append(val)
+                    names.add(name.split("(")[0].replace("void ", ""))
         if not cal or not gel:
             raise SystemExit(f"{path}: calibration or gelu dispatches missing")
         return sum(cal) / len(cal), sum(gel) / len(gel), len(gel)
@@ -368,7 +371,7 @@ def derive_traffic(fetch_csv, write_csv):
     read_b = f_gel * f_scale * 1024
     write_b = w_gel * w_scale * 1024
     out = {
-        "kernel": "k_contig<4,4,UnaryOp<1,float>> gelu(tanh) f32 [64,2048,4096]",
+        "kernel": " / ".join(sorted(names)) + " -- gelu(tanh) f32 [64,2048,4096]",
         "bytes_per_launch": int(round(read_b + write_b)),
         "read_bytes": int(round(read_b)), "write_bytes": int(round(write_b)),
         "algorithmic_bytes": C2_GELU_BYTES,
