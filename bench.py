@@ -176,6 +176,17 @@ def bench_c3(torch, timer, iters=10):
         loss.backward()
     ms = timer.time(step, iters, warmup=2)
     res = {"fwd_bwd": dict(entry(sum(C3_BYTES.values()), ms), rows_per_s=round(C3_N / (ms * 1e-3), 1))}
+    # the opt-in fused path (not the config's decomposition): forward reads the
+    # logits once, backward reads them once and writes the gradient once --
+    # 6 N V bytes plus per-row targets, lse and losses
+    torch.supa.set_fused_cross_entropy_enabled(True)
+    try:
+        ms_f = timer.time(step, iters, warmup=2)
+    finally:
+        torch.supa.set_fused_cross_entropy_enabled(False)
+    fused_bytes = 6 * C3_NV + C3_N * (8 + 4 + 4) * 2
+    res["fused_fwd_bwd"] = dict(entry(fused_bytes, ms_f), rows_per_s=round(C3_N / (ms_f * 1e-3), 1),
+                                speedup_vs_decomposition=round(ms / ms_f, 3))
     lx = logits.detach()
     lsm = torch.ops.aten._log_softmax(lx, 1, False)
     out, tw = torch.ops.aten.nll_loss_forward(lsm, tgt, None, 1, -100)

@@ -238,6 +238,39 @@ int supa_amd_nll_loss_backward(const void* grad_out, int32_t dtype, const int64_
                                int reduction, int64_t ignore_index, void* grad_in,
                                int32_t* error_flag, void* stream);
 
+/* ------------------------------------------------- fused cross-entropy
+ * cross_entropy over contiguous logits [n, c] (f32 / bf16 / f16) with int64
+ * targets [n], no class weight, no label smoothing: the forward reads the
+ * logits once and saves lse[i] = log(sum_j exp(x[i, j])) in float32; the
+ * backward reads them once more and writes
+ * grad[i, j] = (exp(x[i, j] - lse[i]) - [j == t_i]) * g_i.  Rows whose target
+ * is ignore_index have loss 0 and gradient 0 and are not counted; a mean over
+ * no rows is NaN.  This generalises the reference's fp32-only fast path to
+ * bf16 / f16 and ignore_index, with a fused backward:
+ * SUPANativeFunctions::cross_entropy_loss and CrossEntropyLossFastPathFunction,
+ * torch_supa/csrc/aten/ops/CrossEntropyLoss.cpp:23-151, and
+ * cross_entropy_loss_2d_kernel_supa,
+ * .../kernels/elementwise/CrossEntropyLossKernel.cu:71-195. */
+
+/* Bytes of workspace the forward needs (float32 per-row losses). */
+int64_t supa_amd_cross_entropy_workspace_bytes(int64_t n);
+
+/* reduction NONE: out is [n] in the logits dtype.  MEAN / SUM: out is one
+ * element in the logits dtype (sum over rows in a fixed order, float32), and
+ * count (one float32, may be NULL for SUM) receives the kept-row count.
+ * lse: [n] float32, written for the backward (0 for ignored rows). */
+int supa_amd_cross_entropy_forward(const void* logits, int32_t dtype, const int64_t* target, int64_t n,
+                                   int64_t c, int64_t ignore_index, int reduction, void* out, float* lse,
+                                   float* count, void* workspace, int64_t workspace_bytes,
+                                   int32_t* error_flag, void* stream);
+
+/* grad_out: [n] for NONE, one element otherwise (logits dtype); lse and count
+ * as written by the forward.  grad_logits: [n, c], every element written. */
+int supa_amd_cross_entropy_backward(const void* grad_out, const void* logits, int32_t dtype,
+                                    const int64_t* target, const float* lse, const float* count, int64_t n,
+                                    int64_t c, int64_t ignore_index, int reduction, void* grad_logits,
+                                    int32_t* error_flag, void* stream);
+
 /* ------------------------------------------------- multi-tensor apply */
 #define SUPA_AMD_FOREACH_ADD 0   /* out = a + alpha * b  (b list or scalar) */
 #define SUPA_AMD_FOREACH_MUL 1   /* out = a * b          (b list or scalar) */

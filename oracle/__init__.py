@@ -63,6 +63,8 @@ def lib():
             "or_loss_fwd": (None, [c_int, _f32p, _f32p, _f32p, _f32p, i64, c_int, c_float, _f32p]),
             "or_loss_bwd": (None, [c_int, _f32p, _f32p, _f32p, _f32p, _f32p, i64, c_int, c_float, _f32p]),
             "or_sum_f32": (c_double, [_f32p, i64]),
+            "or_ce_fwd": (c_int, [_f64p, _i64p, i64, i64, i64, c_int, _f64p, _f64p, _f64p]),
+            "or_ce_bwd": (None, [_f64p, _f64p, _i64p, _f64p, c_double, i64, i64, i64, c_int, _f64p]),
             "or_adamw_step": (None, [_f32p, _f32p, _f32p, _f32p, i64, c_float, c_double, c_double,
                                      c_double, c_double, c_double, c_int, _f32p, c_int, _f32p]),
         }
@@ -209,6 +211,37 @@ def nll_loss_backward(grad_out, target, n, c, total_weight, weight=None, reducti
                                1 if bf16 else 0, _p(out, _f32p))
     if rc != 0:
         raise IndexError("nll_loss_backward: target out of bounds")
+    return out
+
+
+def cross_entropy(x, target, reduction="mean", ignore_index=-100):
+    """Fused cross-entropy in float64 (x: [n, c], any float dtype, converted
+    to float64).  Returns (loss, lse, count): loss [n] for 'none', a 0-d array
+    otherwise."""
+    x = _c(x, np.float64)
+    n, c = x.shape
+    target = _c(target, np.int64)
+    red = REDUCTION[reduction]
+    loss = np.empty(n if red == 0 else 1, np.float64)
+    lse = np.empty(n, np.float64)
+    cnt = np.zeros(1, np.float64)
+    rc = lib().or_ce_fwd(_p(x, _f64p), _p(target, _i64p), n, c, ignore_index, red, _p(loss, _f64p),
+                         _p(lse, _f64p), _p(cnt, _f64p))
+    if rc != 0:
+        raise IndexError("cross_entropy: target out of bounds")
+    return (loss if red == 0 else loss.reshape(())), lse, float(cnt[0])
+
+
+def cross_entropy_backward(g, x, target, lse, count, reduction="mean", ignore_index=-100) -> np.ndarray:
+    """Gradient of cross_entropy w.r.t. x in float64 (lse, count from cross_entropy)."""
+    x = _c(x, np.float64)
+    n, c = x.shape
+    g = _c(g, np.float64).reshape(-1)
+    target = _c(target, np.int64)
+    lse = _c(lse, np.float64)
+    out = np.empty((n, c), np.float64)
+    lib().or_ce_bwd(_p(g, _f64p), _p(x, _f64p), _p(target, _i64p), _p(lse, _f64p), float(count), n, c,
+                    ignore_index, REDUCTION[reduction], _p(out, _f64p))
     return out
 
 

@@ -308,6 +308,63 @@ int or_nll_loss_bwd(const float* grad_out, const int64_t* target, const float* w
   return 0;
 }
 
+/* ------------------------------------------------- fused cross-entropy -- */
+
+/* Cross-entropy over logits [n, c] with int64 targets, in double: the
+ * reference's fast-path row loss lse_i - x[i, t_i], lse_i = max + log(sum
+ * exp(x - max)) (CrossEntropyLossKernel.cu:71-119), ignore_index rows
+ * contributing 0 and not counted, mean = sum / count (NaN for count 0,
+ * :191-193).  reduction: 0 none (loss[n]), 1 mean, 2 sum (loss[0]).  lse[n]
+ * is written (0 for ignored rows) and *count receives the kept-row count.
+ * Returns -1 for an out-of-range target. */
+int or_ce_fwd(const double* x, const int64_t* target, int64_t n, int64_t c, int64_t ignore_index,
+              int reduction, double* loss, double* lse, double* count) {
+  double sum = 0.0, cnt = 0.0;
+  for (int64_t i = 0; i < n; ++i) {
+    const int64_t t = target[i];
+    const double* r = x + i * c;
+    if (t == ignore_index) {
+      lse[i] = 0.0;
+      if (reduction == 0) loss[i] = 0.0;
+      continue;
+    }
+    if (t < 0 || t >= c) return -1;
+    double m = -INFINITY;
+    for (int64_t j = 0; j < c; ++j) m = r[j] > m ? r[j] : m;
+    double s = 0.0;
+    for (int64_t j = 0; j < c; ++j) s += exp(r[j] - m);
+    const double l = m + log(s);
+    lse[i] = l;
+    if (reduction == 0) loss[i] = l - r[t];
+    sum += l - r[t];
+    cnt += 1.0;
+  }
+  if (reduction == 1) loss[0] = sum / cnt;
+  else if (reduction == 2) loss[0] = sum;
+  *count = cnt;
+  return 0;
+}
+
+/* Its gradient: (exp(x - lse_i) - [j == t_i]) * g_i, g_i = g[i] (none),
+ * g / count (mean), g (sum); ignored rows 0.  This is what the reference's
+ * backward composition nll_loss_backward + _log_softmax_backward_data
+ * computes (CrossEntropyLoss.cpp:94-135): grad_lp = -g_i at t_i, and
+ * grad_x = grad_lp - softmax * sum(grad_lp). */
+void or_ce_bwd(const double* g, const double* x, const int64_t* target, const double* lse, double count,
+               int64_t n, int64_t c, int64_t ignore_index, int reduction, double* gx) {
+  for (int64_t i = 0; i < n; ++i) {
+    const int64_t t = target[i];
+    double* o = gx + i * c;
+    if (t == ignore_index || t < 0 || t >= c) {
+      for (int64_t j = 0; j < c; ++j) o[j] = 0.0;
+      continue;
+    }
+    const double gi = reduction == 0 ? g[i] : (reduction == 1 ? g[0] / count : g[0]);
+    const double* r = x + i * c;
+    for (int64_t j = 0; j < c; ++j) o[j] = (exp(r[j] - lse[i]) - (j == t ? 1.0 : 0.0)) * gi;
+  }
+}
+
 /* ------------------------------------------------------------- losses -- */
 
 enum { OR_MSE = 0, OR_SMOOTH_L1 = 1, OR_BCE_LOGITS = 2 };

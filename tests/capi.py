@@ -53,6 +53,8 @@ def lib():
             "supa_amd_foreach_binary": [ctypes.c_int, i32, vp, vp, vp, vp, i32, dbl, dbl, vp],
             "supa_amd_fused_adamw": [i32, vp, vp, vp, vp, vp, vp, vp, i32, dbl, vp, dbl, dbl, dbl, dbl,
                                      ctypes.c_int, ctypes.c_int, vp, vp, vp],
+            "supa_amd_cross_entropy_forward": [vp, i32, vp, i64, i64, i64, ctypes.c_int, vp, vp, vp, vp, i64, vp, vp],
+            "supa_amd_cross_entropy_backward": [vp, vp, i32, vp, vp, vp, i64, i64, i64, ctypes.c_int, vp, vp, vp],
         }
         for name, args in sig.items():
             fn = getattr(L, name)
@@ -63,6 +65,8 @@ def lib():
         L.supa_amd_sum_workspace_bytes.argtypes = [i64]
         L.supa_amd_loss_workspace_bytes.restype = i64
         L.supa_amd_loss_workspace_bytes.argtypes = [i64]
+        L.supa_amd_cross_entropy_workspace_bytes.restype = i64
+        L.supa_amd_cross_entropy_workspace_bytes.argtypes = [i64]
         _lib = L
     return _lib
 

@@ -42,3 +42,11 @@ def no_fallback(supa):
     counts = supa.supa.fallback_counts()
     supa.supa.set_cpu_fallback_enabled(True)
     assert counts == {}, f"ops went through the CPU fallback: {counts}"
+
+
+@pytest.fixture
+def fused_ce(supa):
+    """Route cross_entropy through the fused kernels for one test."""
+    supa.supa.set_fused_cross_entropy_enabled(True)
+    yield
+    supa.supa.set_fused_cross_entropy_enabled(False)

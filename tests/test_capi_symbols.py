@@ -45,3 +45,16 @@ def test_argument_errors_need_no_device(lib):
     assert lib.supa_amd_log_softmax_forward(None, 6, None, 6, 1, 1, None) == -1
     lib.supa_amd_sum_workspace_bytes.restype = ctypes.c_int64
     assert lib.supa_amd_sum_workspace_bytes(ctypes.c_int64(1 << 30)) > 0
+    i64 = ctypes.c_int64
+    lib.supa_amd_cross_entropy_workspace_bytes.restype = i64
+    assert lib.supa_amd_cross_entropy_workspace_bytes(i64(1000)) == 4000
+    # fused cross-entropy: bad reduction, missing output, missing workspace
+    fake = ctypes.c_void_p(256)  # never dereferenced: the checks come first
+    assert lib.supa_amd_cross_entropy_forward(fake, 6, fake, i64(4), i64(10), i64(-100), 9, fake, fake, fake,
+                                              fake, i64(16), None, None) == -1
+    assert lib.supa_amd_cross_entropy_forward(fake, 6, fake, i64(4), i64(10), i64(-100), 1, None, fake, fake,
+                                              fake, i64(16), None, None) == -1
+    assert lib.supa_amd_cross_entropy_forward(fake, 6, fake, i64(4), i64(10), i64(-100), 1, fake, fake, fake,
+                                              None, i64(0), None, None) == -4
+    assert lib.supa_amd_cross_entropy_backward(None, fake, 6, fake, fake, fake, i64(4), i64(10), i64(-100), 1,
+                                               fake, None, None) == -1

@@ -278,3 +278,38 @@ def test_foreach_and_fused_adamw_bit_exact():
     for i in range(len(shapes)):
         ref = O.binary(O.MUL, O.binary(O.ADD, hp[i], grads[i].numpy().ravel(), -2.0), np.float32(0.5))
         assert np.array_equal(out[i].cpu().numpy().ravel(), ref)
+
+
+@pytest.mark.parametrize("dtype,code", [(torch.float32, A.F32), (torch.bfloat16, A.BF16)])
+def test_fused_cross_entropy_capi(dtype, code):
+    L = A.lib()
+    N, C = 200, 4104
+    x = seeded((N, C), 90, 2.0, dtype)
+    g = torch.Generator().manual_seed(91)
+    t = torch.randint(0, C, (N,), generator=g)
+    t[torch.randperm(N, generator=g)[:9]] = -100
+    dx, dt = x.to(DEV), t.to(DEV)
+    lse = torch.empty(N, device=DEV)
+    cnt = torch.empty(1, device=DEV)
+    ws = torch.empty(L.supa_amd_cross_entropy_workspace_bytes(N) // 4, device=DEV)
+    flag = torch.zeros(1, dtype=torch.int32, device=DEV)
+    out = torch.empty((), dtype=dtype, device=DEV)
+    run(L.supa_amd_cross_entropy_forward(dx.data_ptr(), code, dt.data_ptr(), N, C, -100, A.RED_MEAN, out.data_ptr(),
+                                         lse.data_ptr(), cnt.data_ptr(), ws.data_ptr(), ws.numel() * 4,
+                                         flag.data_ptr(), None))
+    ref, rlse, rcnt = O.cross_entropy(x.double().numpy(), t.numpy(), "mean", -100)
+    tol = 1e-5 if dtype == torch.float32 else 1e-2
+    assert abs(out.double().item() - float(ref)) <= tol * abs(float(ref))
+    assert cnt.item() == rcnt == N - 9
+    np.testing.assert_allclose(lse.cpu().double().numpy(), rlse, rtol=1e-6)
+    go = torch.ones((), dtype=dtype, device=DEV)
+    gx = torch.full((N, C), 7.0, dtype=dtype, device=DEV)  # every element must be overwritten
+    run(L.supa_amd_cross_entropy_backward(go.data_ptr(), dx.data_ptr(), code, dt.data_ptr(), lse.data_ptr(),
+                                          cnt.data_ptr(), N, C, -100, A.RED_MEAN, gx.data_ptr(), flag.data_ptr(),
+                                          None))
+    gref = O.cross_entropy_backward(np.ones(1), x.double().numpy(), t.numpy(), rlse, rcnt, "mean", -100)
+    if dtype == torch.float32:
+        np.testing.assert_allclose(gx.cpu().numpy(), gref, rtol=1e-5, atol=1e-6 * np.abs(gref).max())
+    else:
+        assert bf16_ulp_dist(bits(gx), O.f64_to_bf16(gref)).max() <= 1
+    assert flag.item() == 0

@@ -246,6 +246,111 @@ def test_cross_entropy_small_rows(dtype, no_fallback):
         assert bf16_ulp_dist(bits(dl.grad), O.f32_to_bf16(gin)).max() <= 1
 
 
+# ---------------------------------------------------- fused cross-entropy
+CE_TOL = {torch.float32: 1e-5, torch.bfloat16: 1e-2, torch.float16: 2e-3}
+
+
+@pytest.mark.parametrize("shape", [(96, 128256), (33, 1000), (7, 13)])
+@pytest.mark.parametrize("reduction", ["mean", "sum", "none"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_fused_cross_entropy(dtype, reduction, shape, no_fallback, fused_ce):
+    """Fused forward + backward against the float64 oracle on the same
+    dtype-rounded logits; (7, 13) takes the kernels' scalar path (rows not a
+    whole number of 16-byte vectors)."""
+    N, C = shape
+    logits = seeded(shape, 80, 2.0, dtype)
+    g = torch.Generator().manual_seed(81)
+    t = torch.randint(0, C, (N,), generator=g)
+    t[torch.randperm(N, generator=g)[: max(1, N // 20)]] = -100
+    dl = dev(logits).requires_grad_()
+    loss = F.cross_entropy(dl, dev(t), ignore_index=-100, reduction=reduction)
+    assert loss.dtype == dtype and loss.shape == ((N,) if reduction == "none" else ())
+    go = (torch.ones(()) if reduction != "none" else seeded((N,), 82)).to(dtype)
+    loss.backward(dev(go))
+    x64 = logits.double().numpy()
+    ref, lse, cnt = O.cross_entropy(x64, t.numpy(), reduction, -100)
+    tol = CE_TOL[dtype]
+    np.testing.assert_allclose(loss.detach().cpu().double().numpy(), ref, rtol=tol, atol=1e-6)
+    gref = O.cross_entropy_backward(go.double().numpy(), x64, t.numpy(), lse, cnt, reduction, -100)
+    gd = dl.grad.cpu()
+    assert gd.dtype == dtype
+    if dtype == torch.float32:
+        np.testing.assert_allclose(gd.numpy(), gref, rtol=1e-5, atol=1e-6 * np.abs(gref).max())
+    elif dtype == torch.bfloat16:
+        assert bf16_ulp_dist(bits(gd), O.f64_to_bf16(gref)).max() <= 1
+    else:
+        np.testing.assert_allclose(gd.double().numpy(), gref, rtol=2e-3, atol=1e-7)
+    # ignored rows have a zero gradient
+    assert not gd[t == -100].any()
+
+
+def test_fused_cross_entropy_matches_decomposition_and_edges(no_fallback, supa):
+    """The fused path against the default log_softmax + nll_loss path on the
+    same bf16 input (within the bf16 tolerance), every row ignored (mean NaN,
+    sum 0, zero gradient), and an out-of-range target (IndexError at sync)."""
+    N, V = 64, 32000
+    logits = seeded((N, V), 83, 2.0, torch.bfloat16)
+    g = torch.Generator().manual_seed(84)
+    t = torch.randint(0, V, (N,), generator=g)
+    t[:3] = -100
+    res = {}
+    for fused in (False, True):
+        supa.supa.set_fused_cross_entropy_enabled(fused)
+        try:
+            dl = dev(logits).requires_grad_()
+            loss = F.cross_entropy(dl, dev(t), ignore_index=-100)
+            loss.backward()
+            res[fused] = (loss.float().item(), dl.grad.float().cpu())
+        finally:
+            supa.supa.set_fused_cross_entropy_enabled(False)
+    assert abs(res[True][0] - res[False][0]) <= 1e-2 * abs(res[False][0])
+    gdiff = (res[True][1] - res[False][1]).abs().max().item()
+    assert gdiff <= 1e-2 * res[False][1].abs().max().item()
+    supa.supa.set_fused_cross_entropy_enabled(True)
+    try:
+        dl = dev(logits).requires_grad_()
+        ign = dev(torch.full((N,), -100))
+        loss = F.cross_entropy(dl, ign, ignore_index=-100)
+        loss.backward()
+        assert math.isnan(loss.float().item()) and not dl.grad.cpu().float().any()
+        assert F.cross_entropy(dev(logits), ign, ignore_index=-100, reduction="sum").float().item() == 0.0
+        bad = t.clone()
+        bad[5] = V + 1
+        F.cross_entropy(dev(logits), dev(bad), ignore_index=-100)
+        with pytest.raises(IndexError):
+            torch.supa.synchronize()
+    finally:
+        supa.supa.set_fused_cross_entropy_enabled(False)
+
+
+def test_fused_cross_entropy_c3_full_size(no_fallback, fused_ce):
+    """c3's shape through the fused path: per-row losses of 64 rows against
+    the float64 oracle, the mean against the mean of the per-row losses, and
+    each kept gradient row summing to ~0 with the target column < 0."""
+    N, V = 8192, 128256
+    g = torch.Generator(device="cpu").manual_seed(0)
+    logits = (torch.randn(N, V, generator=g) * 2).to(torch.bfloat16)
+    t = torch.randint(0, V, (N,), generator=g)
+    t[torch.randperm(N, generator=g)[:410]] = -100
+    dl, dt = dev(logits), dev(t)
+    rows = F.cross_entropy(dl, dt, ignore_index=-100, reduction="none").float().cpu()
+    pick = torch.randperm(N, generator=g)[:64]
+    ref, _, _ = O.cross_entropy(logits[pick].double().numpy(), t[pick].numpy(), "none", -100)
+    np.testing.assert_allclose(rows[pick].double().numpy(), ref, rtol=1e-2)
+    dlg = dl.clone().requires_grad_()
+    loss = F.cross_entropy(dlg, dt, ignore_index=-100)
+    keep = t != -100
+    assert abs(loss.float().item() - rows[keep].double().mean().item()) <= 1e-2 * loss.float().item()
+    loss.backward()
+    gs = dlg.grad.float().sum(1).cpu()
+    count = float(keep.sum())
+    assert gs.abs().max().item() <= 0.02 / count
+    gcpu = dlg.grad.cpu()
+    tg = gcpu[torch.arange(N)[keep], t[keep]].float()
+    assert (tg < 0).all()
+    assert not gcpu[~keep].any()
+
+
 def test_cross_entropy_c3_full_size_properties(no_fallback):
     """[8192,128256] bf16 N(0,2), 5% ignore_index, mean: rows of the
     log-softmax sum to 1 in probability, 64 random rows match the oracle,

@@ -182,6 +182,45 @@ def test_nll_closed_forms():
         O.nll_loss(lp, np.array([0, V, 1, 2]), None, "mean", -100)
 
 
+@pytest.mark.parametrize("reduction", ["none", "mean", "sum"])
+def test_fused_cross_entropy_oracle_vs_cpu_f64(reduction):
+    """The fused cross-entropy oracle (float64) against upstream's float64
+    cross_entropy and its autograd gradient on the CPU, with ignore_index."""
+    N, C = 200, 3001
+    x = randn((N, C), 35, 3.0).double()
+    g = torch.Generator().manual_seed(36)
+    t = torch.randint(0, C, (N,), generator=g)
+    t[torch.randperm(N, generator=g)[:11]] = -100
+    xg = x.clone().requires_grad_()
+    loss = F.cross_entropy(xg, t, ignore_index=-100, reduction=reduction)
+    go = torch.ones_like(loss) if reduction != "none" else randn((N,), 37).double()
+    loss.backward(go)
+    out, lse, cnt = O.cross_entropy(x.numpy(), t.numpy(), reduction, -100)
+    assert cnt == N - 11
+    np.testing.assert_allclose(out, loss.detach().numpy(), rtol=1e-12, atol=1e-12)
+    gx = O.cross_entropy_backward(go.numpy(), x.numpy(), t.numpy(), lse, cnt, reduction, -100)
+    np.testing.assert_allclose(gx, xg.grad.numpy(), rtol=1e-10, atol=1e-15)
+
+
+def test_fused_cross_entropy_closed_forms():
+    V = 128256
+    out, lse, cnt = O.cross_entropy(np.zeros((3, V)), np.array([0, 7, -100]), "mean", -100)
+    assert abs(float(out) - math.log(V)) < 1e-12 and cnt == 2.0 and lse[2] == 0.0
+    out, _, cnt = O.cross_entropy(np.zeros((2, 5)), np.array([-100, -100]), "mean", -100)
+    assert np.isnan(out) and cnt == 0.0
+    # gradient rows sum to zero; the target column carries (p - 1) * g
+    x = np.random.default_rng(3).standard_normal((4, 50)) * 2
+    t = np.array([3, 0, 49, -100])
+    _, lse, cnt = O.cross_entropy(x, t, "sum", -100)
+    gx = O.cross_entropy_backward(np.ones(1), x, t, lse, cnt, "sum", -100)
+    np.testing.assert_allclose(gx.sum(1), 0.0, atol=1e-14)
+    assert not gx[3].any()
+    p = np.exp(x[0] - lse[0])
+    assert abs(gx[0, 3] - (p[3] - 1.0)) < 1e-15
+    with pytest.raises(IndexError):
+        O.cross_entropy(x, np.array([0, 1, 50, 2]), "mean", -100)
+
+
 def test_cross_entropy_bf16_decomposition_vs_cpu():
     """c3's semantics at a small row count: bf16 logits, 5% ignore_index,
     mean.  Each decomposed op is compared on the reference's own inputs (the

@@ -63,6 +63,9 @@ void check_device_errors(c10::DeviceIndex d);
 // registers; tests assert that with these counters).
 void set_cpu_fallback_enabled(bool on);
 bool cpu_fallback_enabled();
+// Fused cross-entropy (opt-in; default off, env SUPA_AMD_FUSED_CE=1 turns it on).
+void set_fused_cross_entropy_enabled(bool on);
+bool fused_cross_entropy_enabled();
 std::vector<std::pair<std::string, int64_t>> fallback_counts();
 void reset_fallback_counts();
 

@@ -90,6 +90,8 @@ PYBIND11_MODULE(_C, m) {
   m.def("empty_cache", []() { supa::allocator_empty_cache(); });
   m.def("set_cpu_fallback_enabled", &supa::set_cpu_fallback_enabled);
   m.def("cpu_fallback_enabled", &supa::cpu_fallback_enabled);
+  m.def("set_fused_cross_entropy_enabled", &supa::set_fused_cross_entropy_enabled);
+  m.def("fused_cross_entropy_enabled", &supa::fused_cross_entropy_enabled);
   m.def("fallback_counts", &supa::fallback_counts);
   m.def("reset_fallback_counts", &supa::reset_fallback_counts);
   m.def("plan", &plan);

@@ -3,14 +3,20 @@
 // fused reductions, and the mse / smooth_l1 gradients), _log_softmax and its
 // backward, nll_loss forward / backward.
 //
-// cross_entropy_loss is deliberately not registered: it stays
-// CompositeImplicitAutograd and decomposes into _log_softmax + nll_loss, the
-// path the reference takes for every non-fp32 input
-// (torch_supa/csrc/aten/ops/CrossEntropyLoss.cpp:23-52).
+// cross_entropy_loss is registered the way the reference registers it
+// (SUPANativeFunctions::cross_entropy_loss, CrossEntropyLoss.cpp:140-151): by
+// default it calls upstream's composite cross_entropy_loss_symint, i.e. the
+// _log_softmax + nll_loss decomposition whose nested calls record autograd --
+// the path the reference takes for every non-fp32 input (:23-52).  With the
+// fused path enabled (torch.supa.set_fused_cross_entropy_enabled), 2-d
+// f32/bf16/f16 logits with int64 targets, no weight and no label smoothing go
+// through a custom autograd function on the fused kernels instead.
 // binary_cross_entropy_with_logits is registered, as the reference registers
 // it (supa_native_functions.yaml:59-61; BinaryCrossEntropyWithLogits.cpp:23-73);
 // its backward is the autograd formula's op sequence on the kernels above.
 #include <ATen/WrapDimUtils.h>
+#include <ATen/ops/cross_entropy_loss_native.h>
+#include <torch/csrc/autograd/custom_function.h>
 #include <ATen/native/Resize.h>
 #include <ATen/native/TypeProperties.h>
 #include <c10/core/ScalarType.h>
@@ -456,6 +462,75 @@ at::Tensor& nll_loss_backward_out(const at::Tensor& grad, const at::Tensor& self
   return nll_bwd_into(grad, self, target, weight, reduction, ignore_index, total_weight, gi);
 }
 
+// ------------------------------------------------------ fused cross-entropy
+bool fused_ce_supported(const at::Tensor& self, const at::Tensor& target, const std::optional<at::Tensor>& weight,
+                        double label_smoothing) {
+  const auto dt = self.scalar_type();
+  return fused_cross_entropy_enabled() && self.dim() == 2 &&
+         (dt == at::kFloat || dt == at::kBFloat16 || dt == at::kHalf) && target.dim() == 1 &&
+         target.scalar_type() == at::kLong && target.size(0) == self.size(0) &&
+         !(weight.has_value() && weight->defined()) && label_smoothing == 0.0 && target.device() == self.device();
+}
+
+class FusedCrossEntropy : public torch::autograd::Function<FusedCrossEntropy> {
+ public:
+  static at::Tensor forward(torch::autograd::AutogradContext* ctx, const at::Tensor& self, const at::Tensor& target,
+                            int64_t reduction, int64_t ignore_index) {
+    const int red = reduction_code(reduction);
+    const int64_t n = self.size(0), c = self.size(1);
+    TORCH_CHECK(c > 0, "cross_entropy: expected at least one class");
+    const auto dev = self.device().index();
+    at::Tensor x = self.contiguous();
+    at::Tensor t = target.contiguous();
+    at::Tensor out = empty_supa(red == SUPA_AMD_REDUCTION_NONE ? std::vector<int64_t>{n} : std::vector<int64_t>{},
+                                self.scalar_type(), dev);
+    at::Tensor lse = empty_supa({n}, at::kFloat, dev);
+    at::Tensor count = empty_supa({}, at::kFloat, dev);
+    at::Tensor ws = empty_supa({std::max<int64_t>(n, 1)}, at::kFloat, dev);
+    const DeviceScratch& s = device_scratch(dev);
+    const int rc = supa_amd_cross_entropy_forward(x.data_ptr(), dtype_code(x.scalar_type()), t.data_ptr<int64_t>(), n,
+                                                  c, ignore_index, red, out.data_ptr(), lse.data_ptr<float>(),
+                                                  count.data_ptr<float>(), ws.data_ptr(), ws.numel() * 4,
+                                                  s.error_flag, current_stream(dev));
+    check_status(rc, "cross_entropy (fused forward)");
+    ctx->save_for_backward({x, t, lse, count});
+    ctx->saved_data["reduction"] = reduction;
+    ctx->saved_data["ignore_index"] = ignore_index;
+    return out;
+  }
+
+  static torch::autograd::variable_list backward(torch::autograd::AutogradContext* ctx,
+                                                 torch::autograd::variable_list grads) {
+    const auto saved = ctx->get_saved_variables();
+    const at::Tensor& x = saved[0];
+    const at::Tensor& t = saved[1];
+    const at::Tensor& lse = saved[2];
+    const at::Tensor& count = saved[3];
+    const int red = reduction_code(ctx->saved_data["reduction"].toInt());
+    const int64_t ignore_index = ctx->saved_data["ignore_index"].toInt();
+    const int64_t n = x.size(0), c = x.size(1);
+    const auto dev = x.device().index();
+    at::Tensor g = to_dtype(grads[0], x.scalar_type()).contiguous();
+    at::Tensor gx = empty_supa(x.sizes(), x.scalar_type(), dev);
+    const DeviceScratch& s = device_scratch(dev);
+    const int rc = supa_amd_cross_entropy_backward(g.data_ptr(), x.data_ptr(), dtype_code(x.scalar_type()),
+                                                   t.data_ptr<int64_t>(), lse.data_ptr<float>(),
+                                                   count.data_ptr<float>(), n, c, ignore_index, red, gx.data_ptr(),
+                                                   s.error_flag, current_stream(dev));
+    check_status(rc, "cross_entropy (fused backward)");
+    return {gx, at::Tensor(), at::Tensor(), at::Tensor()};
+  }
+};
+
+at::Tensor cross_entropy_loss(const at::Tensor& self, const at::Tensor& target,
+                              const std::optional<at::Tensor>& weight, int64_t reduction, c10::SymInt ignore_index,
+                              double label_smoothing) {
+  if (fused_ce_supported(self, target, weight, label_smoothing))
+    return FusedCrossEntropy::apply(self, target, reduction, ignore_index.expect_int());
+  return at::native::cross_entropy_loss_symint(self, target, weight, reduction, std::move(ignore_index),
+                                               label_smoothing);
+}
+
 }  // namespace
 }  // namespace supa
 
@@ -482,4 +557,14 @@ TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
   m.impl("nll_loss_forward.output", TORCH_FN(nll_loss_forward_out));
   m.impl("nll_loss_backward", TORCH_FN(nll_loss_backward));
   m.impl("nll_loss_backward.grad_input", TORCH_FN(nll_loss_backward_out));
+  m.impl("cross_entropy_loss", TORCH_FN(cross_entropy_loss));
+}
+
+// cross_entropy_loss has no autograd formula of its own (it is composite), so
+// the autograd key needs the same kernel: the fused path attaches its own
+// backward, and the composite path records autograd through its nested
+// _log_softmax / nll_loss calls, as under the reference's autograd
+// fallthrough (VariableFallbackKernel.cpp:31-33).
+TORCH_LIBRARY_IMPL(aten, AutogradPrivateUse1, m) {
+  m.impl("cross_entropy_loss", TORCH_FN(supa::cross_entropy_loss));
 }

@@ -460,6 +460,15 @@ void supa_cpu_fallback(const c10::OperatorHandle& op, torch::jit::Stack* stack) 
 
 void set_cpu_fallback_enabled(bool on) { g_fallback_enabled.store(on); }
 bool cpu_fallback_enabled() { return g_fallback_enabled.load(); }
+
+namespace {
+std::atomic<bool> g_fused_ce{[] {
+  const char* e = std::getenv("SUPA_AMD_FUSED_CE");
+  return e && std::string(e) == "1";
+}()};
+}  // namespace
+void set_fused_cross_entropy_enabled(bool on) { g_fused_ce.store(on); }
+bool fused_cross_entropy_enabled() { return g_fused_ce.load(); }
 std::vector<std::pair<std::string, int64_t>> fallback_counts() {
   std::lock_guard<std::mutex> g(g_fb_mu);
   return {g_fb_counts.begin(), g_fb_counts.end()};

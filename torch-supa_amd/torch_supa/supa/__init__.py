@@ -119,6 +119,18 @@ def set_cpu_fallback_enabled(on: bool) -> None:
     _C.set_cpu_fallback_enabled(bool(on))
 
 
+def set_fused_cross_entropy_enabled(on: bool) -> None:
+    """Route 2-d cross_entropy (f32/bf16/f16 logits, int64 targets, no class
+    weight, no label smoothing) through the fused kernels: one read of the
+    logits forward, one read + one write backward.  Off by default: the
+    default is the reference's log_softmax + nll_loss decomposition."""
+    _C.set_fused_cross_entropy_enabled(bool(on))
+
+
+def fused_cross_entropy_enabled() -> bool:
+    return bool(_C.fused_cross_entropy_enabled())
+
+
 def fallback_counts() -> dict:
     """Ops that went through the CPU fallback since the last reset, with counts."""
     return dict(_C.fallback_counts())
