@@ -245,8 +245,8 @@ def bench_c4(torch, timer, iters=21, sets=3):
         xgs = [x.detach().requires_grad_() for x in xs]
         losses = [F.binary_cross_entropy_with_logits(xg, tb, pos_weight=pw, reduction=red) for xg, tb in zip(xgs, tbs)]
         gsz = 4 if red != "none" else 4 * n
-        # the autograd formula's op sequence: mul, add, sub, sigmoid, mul, sub, mul(grad)[, div]
-        bce_bwd_b = (8 * n + pwb) + 8 * n + 12 * n + 8 * n + 12 * n + 12 * n + (8 * n + gsz) + (8 * n if red == "mean" else 0)
+        # one fused kernel (the default): reads grad, x, target, pos_weight; writes grad_x
+        bce_bwd_b = gsz + 12 * n + pwb
         res[f"bce_{red}_bwd"] = entry(bce_bwd_b, timer.time(
             rot(lambda k: torch.autograd.grad(losses[k], xgs[k], gos[k], retain_graph=True)), iters))
         del xgs, losses, gos

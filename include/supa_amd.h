@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define SUPA_AMD_ABI_VERSION 1
+#define SUPA_AMD_ABI_VERSION 2
 
 /* ------------------------------------------------------------ status codes */
 #define SUPA_AMD_OK 0
@@ -56,7 +56,7 @@ extern "C" {
  * Dimension 0 is the fastest-moving one.  op[0] is the output, op[1..] are
  * the inputs in the order each entry point documents. */
 #define SUPA_AMD_MAX_DIMS 8
-#define SUPA_AMD_MAX_OPERANDS 5
+#define SUPA_AMD_MAX_OPERANDS 6
 
 typedef struct supa_amd_operand {
   void* data;                          /* element (0,...,0) of the view */
@@ -178,6 +178,22 @@ int64_t supa_amd_loss_workspace_bytes(int64_t numel);
  * smooth_l1_loss_backward.grad_input NF:12002. */
 int supa_amd_loss_backward(const supa_amd_ew_desc* d, int loss, double norm, double beta,
                            void* stream);
+
+/* Gradient of binary_cross_entropy_with_logits w.r.t. its input in one pass.
+ * op = {grad_in, grad_out, input, target[, pos_weight][, weight]} (pos_weight
+ * flagged by has_pos_weight, weight by has_weight; grad_out broadcast 0-dim
+ * for MEAN/SUM).  Evaluates the autograd formula's op sequence in its order
+ * -- u = pos_weight * target; ((u + 1) - target) * sigmoid(input) - u
+ * (sigmoid(input) - target without pos_weight); * grad_out; * weight;
+ * / numel for MEAN (mean != 0) -- rounding every intermediate to the
+ * tensors' dtype, so the result is bit-identical to running those ops one by
+ * one.  Every tensor operand has the descriptor's common dtype.  Replaces the
+ * 7-8 elementwise kernels the reference runs for this gradient
+ * (binary_cross_entropy_with_logits_backward of upstream's autograd,
+ * torchgen/packaged/autograd/derivatives.yaml:2017-2019; the reference
+ * registers only the forward, BinaryCrossEntropyWithLogits.cpp:23-73). */
+int supa_amd_bce_logits_backward(const supa_amd_ew_desc* d, int has_pos_weight, int has_weight, int mean,
+                                 double numel, void* stream);
 
 /* ---------------------------------------------------------- reductions */
 

@@ -9,7 +9,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.path.join(ROOT, "torch-supa_amd", "torch_supa", "libsupa_amd_kernels.so")
 
 MAX_DIMS = 8
-MAX_OPERANDS = 5
+MAX_OPERANDS = 6
 
 U8, I8, I16, I32, I64, F16, F32, F64, BOOL, BF16 = 0, 1, 2, 3, 4, 5, 6, 7, 11, 15
 GELU, GELU_TANH, SILU, SIGMOID, TANH, EXP, LOG, ERF, RELU, NEG = range(10)

@@ -313,3 +313,25 @@ def test_fused_cross_entropy_capi(dtype, code):
     else:
         assert bf16_ulp_dist(bits(gx), O.f64_to_bf16(gref)).max() <= 1
     assert flag.item() == 0
+
+
+@pytest.mark.parametrize("reduction", [A.RED_NONE, A.RED_MEAN])
+def test_bce_logits_backward_capi(reduction):
+    L = A.lib()
+    R, C = 8, 70000
+    g = torch.Generator().manual_seed(95)
+    x = torch.randn(R, C, generator=g)
+    t = (torch.rand(R, C, generator=g) < 0.3).float()
+    pw = torch.rand(C, generator=g) * 1.5 + 0.5
+    w = torch.rand(R, C, generator=g) + 0.5
+    go = torch.randn(R, C, generator=g) if reduction == A.RED_NONE else torch.ones(())
+    dx, dt, dpw, dw, dgo = x.to(DEV), t.to(DEV), pw.to(DEV), w.to(DEV), go.to(DEV)
+    gi = torch.empty(R, C, device=DEV)
+    gstr = [1, C] if reduction == A.RED_NONE else [0, 0]
+    d = A.nd_desc([C, R], [(gi, [1, C]), (dgo, gstr), (dx, [1, C]), (dt, [1, C]), (dpw, [1, 0]), (dw, [1, C])], A.F32)
+    L.supa_amd_bce_logits_backward.argtypes = [ctypes.POINTER(A.EwDesc), ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                               ctypes.c_double, ctypes.c_void_p]
+    run(L.supa_amd_bce_logits_backward(ctypes.byref(d), 1, 1, 1 if reduction == A.RED_MEAN else 0, float(R * C), None))
+    red = "none" if reduction == A.RED_NONE else "mean"
+    gref = O.loss_backward(O.BCE_LOGITS, go.numpy(), x.numpy(), t.numpy(), pw.numpy(), w.numpy(), reduction=red)
+    assert np.array_equal(gi.cpu().numpy(), gref)

@@ -424,6 +424,59 @@ def test_c4_full_size_losses(reduction, no_fallback):
         assert np.array_equal(xg.grad.cpu().numpy(), gref), op
 
 
+@pytest.mark.parametrize("reduction", ["none", "mean", "sum"])
+@pytest.mark.parametrize("with_pw,with_w", [(False, False), (True, False), (False, True), (True, True)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_fused_bce_backward_matches_op_sequence(reduction, with_pw, with_w, dtype, no_fallback, supa):
+    """The one-kernel BCE-with-logits input gradient is bit-identical to the
+    autograd formula's op-by-op evaluation on the same kernels (and, in
+    float32, to the oracle), for every pos_weight / weight combination."""
+    R, C = 33, 4100
+    g = torch.Generator().manual_seed(101)
+    x = (torch.randn(R, C, generator=g) * 2).to(dtype)
+    tb = (torch.rand(R, C, generator=g) < 0.3).to(dtype)
+    pw = (torch.rand(C, generator=g) * 1.5 + 0.5).to(dtype) if with_pw else None
+    w = (torch.rand(R, 1, generator=g) + 0.5).to(dtype) if with_w else None
+    go = (torch.randn(R, C, generator=g) if reduction == "none" else torch.ones(())).to(dtype)
+    grads = {}
+    for fused in (True, False):
+        supa.supa.set_fused_bce_backward_enabled(fused)
+        try:
+            xg = dev(x).requires_grad_()
+            loss = F.binary_cross_entropy_with_logits(xg, dev(tb), weight=None if w is None else dev(w),
+                                                      pos_weight=None if pw is None else dev(pw),
+                                                      reduction=reduction)
+            loss.backward(dev(go))
+            grads[fused] = xg.grad.cpu()
+        finally:
+            supa.supa.set_fused_bce_backward_enabled(True)
+    assert torch.equal(grads[True], grads[False])
+    if dtype == torch.float32:
+        gref = O.loss_backward(O.BCE_LOGITS, go.numpy(), x.numpy(), tb.numpy(), None if pw is None else pw.numpy(),
+                               None if w is None else w.numpy(), reduction=reduction)
+        assert np.array_equal(grads[True].numpy(), gref)
+
+
+def test_bce_double_backward_and_target_grad(supa):
+    """create_graph: the gradient is built from differentiable ops, so a
+    second derivative exists and matches upstream's on the CPU; a target
+    that requires grad gets upstream's target gradient."""
+    g = torch.Generator().manual_seed(102)
+    x = torch.randn(16, 300, generator=g)
+    t = torch.rand(16, 300, generator=g)
+    pw = torch.rand(300, generator=g) + 0.5
+    res = []
+    for d in ("cpu", "supa"):
+        xg = x.to(d).detach().requires_grad_()
+        tg = t.to(d).detach().requires_grad_()
+        loss = F.binary_cross_entropy_with_logits(xg, tg, pos_weight=pw.to(d))
+        gx, gt = torch.autograd.grad(loss, (xg, tg), create_graph=True)
+        (gx * gx).sum().backward()
+        res.append((gx.detach().cpu(), gt.detach().cpu(), xg.grad.cpu()))
+    for a, b in zip(*res):
+        np.testing.assert_allclose(b.numpy(), a.numpy(), rtol=1e-5, atol=1e-8)
+
+
 def test_sum_mean_dims(no_fallback):
     x = seeded((64, 1000, 3), 31)
     dx = dev(x)

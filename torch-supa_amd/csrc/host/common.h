@@ -66,6 +66,9 @@ bool cpu_fallback_enabled();
 // Fused cross-entropy (opt-in; default off, env SUPA_AMD_FUSED_CE=1 turns it on).
 void set_fused_cross_entropy_enabled(bool on);
 bool fused_cross_entropy_enabled();
+// One-pass BCE-with-logits gradient (default on, env SUPA_AMD_FUSED_BCE=0 turns it off).
+void set_fused_bce_backward_enabled(bool on);
+bool fused_bce_backward_enabled();
 std::vector<std::pair<std::string, int64_t>> fallback_counts();
 void reset_fallback_counts();
 

@@ -92,6 +92,8 @@ PYBIND11_MODULE(_C, m) {
   m.def("cpu_fallback_enabled", &supa::cpu_fallback_enabled);
   m.def("set_fused_cross_entropy_enabled", &supa::set_fused_cross_entropy_enabled);
   m.def("fused_cross_entropy_enabled", &supa::fused_cross_entropy_enabled);
+  m.def("set_fused_bce_backward_enabled", &supa::set_fused_bce_backward_enabled);
+  m.def("fused_bce_backward_enabled", &supa::fused_bce_backward_enabled);
   m.def("fallback_counts", &supa::fallback_counts);
   m.def("reset_fallback_counts", &supa::reset_fallback_counts);
   m.def("plan", &plan);

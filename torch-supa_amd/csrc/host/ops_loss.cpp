@@ -16,6 +16,7 @@
 // its backward is the autograd formula's op sequence on the kernels above.
 #include <ATen/WrapDimUtils.h>
 #include <ATen/ops/cross_entropy_loss_native.h>
+#include <ATen/ops/log_sigmoid.h>
 #include <torch/csrc/autograd/custom_function.h>
 #include <ATen/native/Resize.h>
 #include <ATen/native/TypeProperties.h>
@@ -462,6 +463,115 @@ at::Tensor& nll_loss_backward_out(const at::Tensor& grad, const at::Tensor& self
   return nll_bwd_into(grad, self, target, weight, reduction, ignore_index, total_weight, gi);
 }
 
+// ------------------------------------------ BCE-with-logits autograd
+// binary_cross_entropy_with_logits' input gradient, the autograd formula
+// (binary_cross_entropy_with_logits_backward of upstream's FunctionsManual;
+// derivatives.yaml:2017-2019) op by op on this backend's kernels: used under
+// create_graph (so the gradient is itself differentiable), for mixed dtypes,
+// and when the fused kernel is switched off.
+at::Tensor bce_input_grad_ops(const at::Tensor& g, const at::Tensor& self, const at::Tensor& target,
+                              const at::Tensor& weight, const at::Tensor& pos_weight, int64_t reduction) {
+  at::Tensor gi;
+  if (pos_weight.defined()) {
+    at::Tensor u = pos_weight.mul(target);
+    gi = u.add(1).sub(target).mul(self.sigmoid()).sub(u);
+  } else {
+    gi = self.sigmoid().sub(target);
+  }
+  gi = gi.mul(g);
+  if (weight.defined()) gi = gi.mul(weight);
+  if (reduction == kMean) gi = gi.div(self.numel());
+  return gi;
+}
+
+// binary_cross_entropy_with_logits_target_backward, op by op.
+at::Tensor bce_target_grad_ops(const at::Tensor& g, const at::Tensor& self, const at::Tensor& target,
+                               const at::Tensor& weight, const at::Tensor& pos_weight, int64_t reduction) {
+  at::Tensor gt;
+  if (pos_weight.defined()) gt = at::log_sigmoid(self.neg()).sub(at::log_sigmoid(self).mul(pos_weight)).mul(g);
+  else gt = self.neg().mul(g);
+  if (weight.defined()) gt = gt.mul(weight);
+  if (reduction == kMean) gt = gt.div(target.numel());
+  return gt;
+}
+
+// The same gradient in one kernel when every tensor shares one floating
+// dtype (bit-identical: each intermediate is rounded to that dtype).
+bool bce_fusable(const at::Tensor& g, const at::Tensor& self, const at::Tensor& target, const at::Tensor& weight,
+                 const at::Tensor& pos_weight) {
+  const auto dt = self.scalar_type();
+  if (!fused_bce_backward_enabled() || !is_float_dtype(dt) || self.device().type() != c10::DeviceType::PrivateUse1)
+    return false;
+  for (const at::Tensor* t : {&g, &target, &weight, &pos_weight})
+    if (t->defined() && (t->scalar_type() != dt || t->device() != self.device())) return false;
+  return true;
+}
+
+at::Tensor bce_input_grad_fused(const at::Tensor& g, const at::Tensor& self, const at::Tensor& target,
+                                const at::Tensor& weight, const at::Tensor& pos_weight, int64_t reduction) {
+  std::vector<EwIn> ins{EwIn::of(g), EwIn::of(self), EwIn::of(target)};
+  if (pos_weight.defined()) ins.push_back(EwIn::of(pos_weight));
+  if (weight.defined()) ins.push_back(EwIn::of(weight));
+  const int has_pw = pos_weight.defined() ? 1 : 0, has_w = weight.defined() ? 1 : 0;
+  const int mean = reduction == kMean ? 1 : 0;
+  const double numel = (double)self.numel();
+  at::Tensor gi = ew_apply({}, self.scalar_type(), self.scalar_type(), ins,
+                           [=](const supa_amd_ew_desc* d, void* st) {
+                             return supa_amd_bce_logits_backward(d, has_pw, has_w, mean, numel, st);
+                           },
+                           "binary_cross_entropy_with_logits_backward");
+  TORCH_CHECK(gi.sizes() == self.sizes(), "binary_cross_entropy_with_logits_backward: gradient shape ", gi.sizes(),
+              " does not match the input ", self.sizes());
+  return gi;
+}
+
+class BceWithLogitsFunction : public torch::autograd::Function<BceWithLogitsFunction> {
+ public:
+  // weight / pos_weight travel as optionals: an undefined at::Tensor is not a
+  // valid autograd Function input
+  static at::Tensor forward(torch::autograd::AutogradContext* ctx, const at::Tensor& self, const at::Tensor& target,
+                            const std::optional<at::Tensor>& weight, const std::optional<at::Tensor>& pos_weight,
+                            int64_t reduction) {
+    at::Tensor out = bce_with_logits(self, target, weight, pos_weight, reduction);
+    ctx->save_for_backward({self, target, weight.value_or(at::Tensor()), pos_weight.value_or(at::Tensor())});
+    ctx->saved_data["reduction"] = reduction;
+    return out;
+  }
+
+  static torch::autograd::variable_list backward(torch::autograd::AutogradContext* ctx,
+                                                 torch::autograd::variable_list grads) {
+    const auto saved = ctx->get_saved_variables();
+    const at::Tensor& self = saved[0];
+    const at::Tensor& target = saved[1];
+    const at::Tensor& weight = saved[2];
+    const at::Tensor& pos_weight = saved[3];
+    const int64_t reduction = ctx->saved_data["reduction"].toInt();
+    const at::Tensor& g = grads[0];
+    at::Tensor gself, gtarget;
+    if (ctx->needs_input_grad(0)) {
+      if (!at::GradMode::is_enabled() && bce_fusable(g, self, target, weight, pos_weight))
+        gself = bce_input_grad_fused(g, self, target, weight, pos_weight, reduction);
+      else
+        gself = bce_input_grad_ops(g, self, target, weight, pos_weight, reduction);
+    }
+    if (ctx->needs_input_grad(1)) gtarget = bce_target_grad_ops(g, self, target, weight, pos_weight, reduction);
+    return {gself, gtarget, at::Tensor(), at::Tensor(), at::Tensor()};
+  }
+};
+
+// The autograd-key kernel: weight and pos_weight have no derivative upstream
+// either.
+at::Tensor bce_with_logits_autograd(const at::Tensor& self, const at::Tensor& target,
+                                    const std::optional<at::Tensor>& weight,
+                                    const std::optional<at::Tensor>& pos_weight, int64_t reduction) {
+  const bool w = weight.has_value() && weight->defined();
+  const bool pw = pos_weight.has_value() && pos_weight->defined();
+  TORCH_CHECK(!(w && weight->requires_grad()), "the derivative for 'weight' is not implemented.");
+  TORCH_CHECK(!(pw && pos_weight->requires_grad()), "the derivative for 'pos_weight' is not implemented.");
+  return BceWithLogitsFunction::apply(self, target, w ? weight : std::nullopt, pw ? pos_weight : std::nullopt,
+                                      reduction);
+}
+
 // ------------------------------------------------------ fused cross-entropy
 bool fused_ce_supported(const at::Tensor& self, const at::Tensor& target, const std::optional<at::Tensor>& weight,
                         double label_smoothing) {
@@ -567,4 +677,6 @@ TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
 // fallthrough (VariableFallbackKernel.cpp:31-33).
 TORCH_LIBRARY_IMPL(aten, AutogradPrivateUse1, m) {
   m.impl("cross_entropy_loss", TORCH_FN(supa::cross_entropy_loss));
+  // one-pass input gradient (bit-identical to the formula's op sequence)
+  m.impl("binary_cross_entropy_with_logits", TORCH_FN(supa::bce_with_logits_autograd));
 }

@@ -469,6 +469,15 @@ std::atomic<bool> g_fused_ce{[] {
 }  // namespace
 void set_fused_cross_entropy_enabled(bool on) { g_fused_ce.store(on); }
 bool fused_cross_entropy_enabled() { return g_fused_ce.load(); }
+
+namespace {
+std::atomic<bool> g_fused_bce{[] {
+  const char* e = std::getenv("SUPA_AMD_FUSED_BCE");
+  return !(e && std::string(e) == "0");
+}()};
+}  // namespace
+void set_fused_bce_backward_enabled(bool on) { g_fused_bce.store(on); }
+bool fused_bce_backward_enabled() { return g_fused_bce.load(); }
 std::vector<std::pair<std::string, int64_t>> fallback_counts() {
   std::lock_guard<std::mutex> g(g_fb_mu);
   return {g_fb_counts.begin(), g_fb_counts.end()};

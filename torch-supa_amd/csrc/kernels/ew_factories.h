@@ -54,4 +54,12 @@ struct SmoothL1BwdFactory {
   }
 };
 
+template <bool PW, bool W>
+struct BceBwdFactory {
+  double n;
+  int mean, rt;
+  template <typename C> static constexpr bool ok() { return std::is_floating_point<C>::value; }
+  template <typename C> BceBwdOp<PW, W, C> make() const { return BceBwdOp<PW, W, C>{static_cast<C>(n), mean, rt}; }
+};
+
 }  // namespace sa

@@ -294,8 +294,10 @@ int dispatch_types(const Op& op, const supa_amd_ew_desc& d, const int* tin, hipS
         return launch_static<Op, C, T, T, T, T>(op, d, tin, st);
       } else if constexpr (N == 3) {
         return launch_static<Op, C, T, T, T, T, T>(op, d, tin, st);
-      } else {
+      } else if constexpr (N == 4) {
         return launch_static<Op, C, T, T, T, T, T, T>(op, d, tin, st);
+      } else {
+        return launch_static<Op, C, T, T, T, T, T, T, T>(op, d, tin, st);
       }
     });
   }

@@ -24,4 +24,19 @@ int supa_amd_loss_backward(const supa_amd_ew_desc* d, int loss, double norm, dou
   }
 }
 
+int supa_amd_bce_logits_backward(const supa_amd_ew_desc* d, int has_pos_weight, int has_weight, int mean,
+                                 double numel, void* stream) {
+  if (!d) return SUPA_AMD_EINVAL;
+  const int want = 4 + (has_pos_weight ? 1 : 0) + (has_weight ? 1 : 0);
+  if (d->noperands != want) return SUPA_AMD_EINVAL;
+  for (int k = 0; k < d->noperands; ++k)
+    if (!d->op[k].is_scalar && d->op[k].dtype != d->common_dtype) return SUPA_AMD_EDTYPE;
+  const int rt = d->common_dtype == SUPA_AMD_BF16 ? 1 : (d->common_dtype == SUPA_AMD_F16 ? 2 : 0);
+  const int m = mean ? 1 : 0;
+  if (has_pos_weight && has_weight) return run_ew(BceBwdFactory<true, true>{numel, m, rt}, d, stream, want);
+  if (has_pos_weight) return run_ew(BceBwdFactory<true, false>{numel, m, rt}, d, stream, want);
+  if (has_weight) return run_ew(BceBwdFactory<false, true>{numel, m, rt}, d, stream, want);
+  return run_ew(BceBwdFactory<false, false>{numel, m, rt}, d, stream, want);
+}
+
 }  // extern "C"

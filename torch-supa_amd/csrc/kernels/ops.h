@@ -256,6 +256,39 @@ template <bool PW, bool W, typename C> struct BceTermOp {
     return r;
   }
 };
+// BCE-with-logits gradient in the autograd formula's op order (inputs g, x,
+// t [, pw] [, w]): u = pw * t; ((u + 1) - t) * sigmoid(x) - u, or
+// sigmoid(x) - t; * g; * w; / n.  rt: the storage dtype every intermediate is
+// rounded to (0 keep C, 1 bf16, 2 f16), as the op-by-op evaluation stores
+// each intermediate tensor.
+template <bool PW, bool W, typename C> struct BceBwdOp {
+  static constexpr int arity = 3 + (PW ? 1 : 0) + (W ? 1 : 0);
+  C n;
+  int mean;
+  int rt;
+  __device__ __forceinline__ C rnd(C v) const {
+    if constexpr (std::is_same<C, float>::value) {
+      if (rt == 1) return bf16_to_f32(f32_to_bf16(v));
+      if (rt == 2) return (float)(f16)v;
+    }
+    return v;
+  }
+  __device__ __forceinline__ C operator()(const C* v) const {
+    const C g = v[0], x = v[1], t = v[2];
+    const C s = rnd(sigmoidx<C>(x));
+    C r;
+    if constexpr (PW) {
+      const C u = rnd(v[3] * t);
+      r = rnd(rnd(rnd(rnd(u + C(1)) - t) * s) - u);
+    } else {
+      r = rnd(s - t);
+    }
+    r = rnd(r * g);
+    if constexpr (W) r = rnd(r * v[3 + (PW ? 1 : 0)]);
+    if (mean) r = r / n;
+    return r;
+  }
+};
 // mse backward: ((x - t) * norm) * g   (inputs g, x, t)
 template <typename C> struct MseBwdOp {
   static constexpr int arity = 3;

@@ -131,6 +131,18 @@ def fused_cross_entropy_enabled() -> bool:
     return bool(_C.fused_cross_entropy_enabled())
 
 
+def set_fused_bce_backward_enabled(on: bool) -> None:
+    """Compute binary_cross_entropy_with_logits' input gradient in one kernel
+    (on by default; bit-identical to the autograd formula's op-by-op
+    evaluation, which is used when off, under create_graph, or for mixed
+    dtypes)."""
+    _C.set_fused_bce_backward_enabled(bool(on))
+
+
+def fused_bce_backward_enabled() -> bool:
+    return bool(_C.fused_bce_backward_enabled())
+
+
 def fallback_counts() -> dict:
     """Ops that went through the CPU fallback since the last reset, with counts."""
     return dict(_C.fallback_counts())
