@@ -131,6 +131,26 @@ def test_row_and_column_broadcasts(rows, cols, no_fallback):
     assert torch.equal(torch.div(dcol, drow).cpu(), torch.div(colv, rowv))  # outer-product shape
 
 
+@pytest.mark.parametrize("shape", [(4, 7, 3, 40), (2, 33, 1, 8), (5, 3, 16, 1024)])
+def test_per_channel_broadcasts(shape, no_fallback):
+    """NCHW-like tensors with per-channel operands (strides (0, 1, 0) over the
+    coalesced (HW, C, N) iteration), a per-sample scalar and a transposed
+    view whose output inherits the permutation."""
+    N, C, H, W = shape
+    x = seeded(shape, 45)
+    ch = seeded((C, 1, 1), 46)
+    per_n = seeded((N, 1, 1, 1), 47)
+    dx, dch, dn = dev(x), dev(ch), dev(per_n)
+    assert torch.equal((dx + dch).cpu(), x + ch)
+    assert torch.equal((dx * dch + dn).cpu(), x * ch + per_n)
+    xb = seeded(shape, 48).to(torch.bfloat16)
+    assert torch.equal((dev(xb) * dch).cpu(), xb * ch)  # bf16 * f32 -> f32
+    xt = x.transpose(2, 3)
+    got = dev(x).transpose(2, 3) + dev(seeded((W, 1), 49))
+    assert got.stride() == (xt + seeded((W, 1), 49)).stride()
+    assert torch.equal(got.cpu(), xt + seeded((W, 1), 49))
+
+
 def test_transposed_and_strided_views(no_fallback):
     base = seeded((1, 5120, 1024), 9)
     a = base.transpose(1, 2)  # [1, 1024, 5120] with strides (5242880, 1, 1024): the reference's worst case

@@ -13,9 +13,10 @@
 //           first element come from a chain of magic-number divisions; this
 //           covers a bias broadcast along rows, a per-row scalar broadcast
 //           and inputs that are permuted but dense.
-//   ROW2D   two dims, dense output, each input dense / row-broadcast /
-//           column-broadcast / one element: bias adds without the divider
-//           chain and 64-bit offsets of VECND.
+//   ROW2D   two dims (or three, rows flattened), dense output, each input
+//           dense / row-broadcast / column-broadcast / middle-dim-broadcast /
+//           one element: bias adds without the divider chain and 64-bit
+//           offsets of VECND.
 //   STRIDED anything else: one element per thread, per-operand offsets from
 //           the same divider chain.
 // Dtype classes:
@@ -219,12 +220,16 @@ k_vecnd(Op op, TArgs<1 + sizeof...(S)> a, NdGeom g, uint32_t nvec) {
 // once per thread and reused (measured 7 % faster than one row per thread);
 // every offset is 32-bit.  Workgroup b covers column block b % bpr of row
 // group b / bpr.
-enum Row2dKind { R2_DENSE = 0, R2_ROW = 1, R2_COL = 2, R2_ONE = 3 };
+// With three iteration dims (inner, d1, d2) the rows are the flattened
+// (d1, d2) pairs, and R2_MID is an operand indexed by the middle coordinate
+// alone (strides (0, 1, 0)): a per-channel vector over an NCHW-like layout,
+// or c2's bias under its transposed view.
+enum Row2dKind { R2_DENSE = 0, R2_ROW = 1, R2_COL = 2, R2_ONE = 3, R2_MID = 4 };
 constexpr int kRow2dRows = 2;
 
 template <int VEC, typename Op, typename C, typename CT, typename OT, typename... S>
 __global__ void __launch_bounds__(kBlock)
-k_row2d(Op op, TArgs<1 + sizeof...(S)> a, uint32_t inner, uint32_t rows, FastDiv bpr) {
+k_row2d(Op op, TArgs<1 + sizeof...(S)> a, uint32_t inner, uint32_t rows, FastDiv bpr, FastDiv mid) {
   constexpr int N = sizeof...(S);
   constexpr int R = kRow2dRows;
   uint32_t rg, cb;
@@ -254,7 +259,14 @@ k_row2d(Op op, TArgs<1 + sizeof...(S)> a, uint32_t inner, uint32_t rows, FastDiv
 #pragma unroll
                for (int k = 0; k < VEC; ++k) x[r][k][I] = load_cvt<C, CT>(w.v[k]);
              } else {
-               const C s = load_cvt<C, CT>(p[kind == R2_COL ? row : 0u]);
+               uint32_t idx = 0u;
+               if (kind == R2_COL) {
+                 idx = row;
+               } else if (kind == R2_MID) {
+                 uint32_t q;
+                 mid.divmod(row, q, idx);
+               }
+               const C s = load_cvt<C, CT>(p[idx]);
 #pragma unroll
                for (int k = 0; k < VEC; ++k) x[r][k][I] = s;
              }

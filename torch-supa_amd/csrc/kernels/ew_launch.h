@@ -177,27 +177,33 @@ int launch_static(const Op& op, const supa_amd_ew_desc& d, const int* tin, hipSt
     TArgs<1 + N> b = a;
     b.p[0] = p.op[0].data;
     for (int i = 0; i < N; ++i) b.p[1 + i] = p.op[tin[i]].data;
-    // ROW2D?
-    if (p.ndim == 2 && VEC > 1 && (p.sizes[0] % VEC) == 0 && b.st[0][0] == 1 && b.st[0][1] == p.sizes[0] &&
+    // ROW2D?  Two dims, or three with the outer two flattened into rows.
+    if ((p.ndim == 2 || p.ndim == 3) && VEC > 1 && (p.sizes[0] % VEC) == 0 && b.st[0][0] == 1 &&
+        b.st[0][1] == p.sizes[0] && (p.ndim == 2 || b.st[0][2] == p.sizes[0] * p.sizes[1]) &&
         aligned(b.p[0], VEC * sizes_of[0]) && (uint64_t)pn / VEC < (1ull << 32)) {
+      const int64_t d0 = p.sizes[0], d1 = p.sizes[1];
       bool ok = true;
       TArgs<1 + N> c = b;
       c.mode[0] = R2_DENSE;
       for (int k = 1; k <= N && ok; ++k) {
-        const int64_t s0 = b.st[k][0], s1 = b.st[k][1];
-        if (s0 == 1 && s1 == p.sizes[0]) c.mode[k] = R2_DENSE;
-        else if (s0 == 1 && s1 == 0) c.mode[k] = R2_ROW;
-        else if (s0 == 0 && s1 == 1) c.mode[k] = R2_COL;
-        else if (s0 == 0 && s1 == 0) c.mode[k] = R2_ONE;
+        const int64_t s0 = b.st[k][0], s1 = b.st[k][1], s2 = p.ndim == 3 ? b.st[k][2] : -1;
+        const bool two = p.ndim == 2;
+        if (s0 == 1 && s1 == d0 && (two || s2 == d0 * d1)) c.mode[k] = R2_DENSE;
+        else if (s0 == 1 && s1 == 0 && (two || s2 == 0)) c.mode[k] = R2_ROW;
+        else if (s0 == 0 && s1 == 1 && (two || s2 == d1)) c.mode[k] = R2_COL;
+        else if (s0 == 0 && s1 == 0 && (two || s2 == 0)) c.mode[k] = R2_ONE;
+        else if (!two && s0 == 0 && s1 == 1 && s2 == 0) c.mode[k] = R2_MID;
         else ok = false;
         if (ok && s0 == 1 && !aligned(b.p[k], VEC * sizes_of[k])) ok = false;
       }
       if (ok) {
-        const uint32_t inner = (uint32_t)p.sizes[0], rows = (uint32_t)p.sizes[1];
+        const uint32_t inner = (uint32_t)d0;
+        const uint32_t rows = (uint32_t)(pn / d0);
         const uint32_t bpr = (inner / VEC + kBlock - 1) / kBlock;
         const uint64_t blocks = (uint64_t)bpr * ((rows + kRow2dRows - 1) / kRow2dRows);
         if (blocks < (1ull << 31)) {
-          k_row2d<VEC, Op, C, CT, OT, S...><<<(unsigned)blocks, kBlock, 0, st>>>(op, c, inner, rows, FastDiv(bpr));
+          k_row2d<VEC, Op, C, CT, OT, S...><<<(unsigned)blocks, kBlock, 0, st>>>(op, c, inner, rows, FastDiv(bpr),
+                                                                              FastDiv((uint32_t)d1));
           return launch_status();
         }
       }
