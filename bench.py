@@ -474,6 +474,10 @@ def main():
         log("c2 transposed leg")
         xt, bt = c2_inputs(torch, transposed=True)
         per["c2_transposed"] = bench_c2(torch, timer, xt, bt)
+        # .contiguous() of the transposed view (LDS-tiled transpose): 1 GiB read + 1 GiB written
+        xc = torch.empty(xt.shape, dtype=xt.dtype, device="supa")
+        per["c2_transposed"]["contiguous_copy"] = entry(2 * 2 * C2_N, timer.time(lambda: xc.copy_(xt), 10))
+        del xc
         del xt, bt
     else:
         del x, bias

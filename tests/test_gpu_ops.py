@@ -151,6 +151,28 @@ def test_per_channel_broadcasts(shape, no_fallback):
     assert torch.equal(got.cpu(), xt + seeded((W, 1), 49))
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.int64, torch.bool])
+@pytest.mark.parametrize("shape", [(300, 517), (7, 64, 1000), (3, 1030, 20)])
+def test_transpose_copies(shape, dtype, no_fallback):
+    """The LDS-tiled transpose path: .contiguous() of transposed / permuted
+    views (edge tiles included), a cast while transposing, and a unary op from
+    a transposed input into a contiguous out=."""
+    x = seeded(shape, 50, 3.0)
+    x = x.to(dtype) if dtype != torch.bool else x > 0
+    dx = dev(x)
+    perms = [(1, 0)] if len(shape) == 2 else [(0, 2, 1), (2, 1, 0), (1, 2, 0)]
+    for perm in perms:
+        got = dx.permute(*perm).contiguous()
+        assert got.is_contiguous()
+        assert torch.equal(got.cpu(), x.permute(*perm).contiguous()), perm
+    if dtype in (torch.float32, torch.bfloat16):
+        xt = x.transpose(-1, -2)
+        assert torch.equal(dev(x).transpose(-1, -2).to(torch.float32).contiguous().cpu(), xt.float().contiguous())
+        out = torch.empty(xt.shape, dtype=dtype, device="supa")
+        torch.neg(dev(x).transpose(-1, -2), out=out)
+        assert torch.equal(out.cpu(), torch.neg(xt))
+
+
 def test_transposed_and_strided_views(no_fallback):
     base = seeded((1, 5120, 1024), 9)
     a = base.transpose(1, 2)  # [1, 1024, 5120] with strides (5242880, 1, 1024): the reference's worst case

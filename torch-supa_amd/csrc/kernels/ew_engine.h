@@ -288,6 +288,94 @@ k_row2d(Op op, TArgs<1 + sizeof...(S)> a, uint32_t inner, uint32_t rows, FastDiv
   }
 }
 
+// --------------------------------------------------------- TRANSPOSE
+// One input whose unit-stride dim is k != 0 while the output is dense in the
+// iteration order (dim 0 fastest): a (batched) transpose, e.g. .contiguous()
+// of a transposed view.  A 64 x 64 tile goes through LDS so the reads run
+// along the input's contiguous dim and the writes along the output's; the
+// third dim (if any) is the batch.  Workgroup b covers tile (b % t0, (b / t0)
+// % tk) of batch b / (t0 tk).
+constexpr int kTile = 64;
+
+struct TransposeGeom {
+  uint32_t d0, dk, db;     // sizes: output-contiguous dim, input-contiguous dim, batch dim
+  int64_t in_s0, in_sb;    // input strides (elements) of dims 0 and batch; dim k has stride 1
+  int64_t out_sk, out_sb;  // output strides of dims k and batch; dim 0 has stride 1
+  FastDiv t0, tk;          // tiles along dim 0 and along dim k
+};
+
+template <typename Op, typename C, typename CT, typename OT, typename S>
+__global__ void __launch_bounds__(kBlock)
+k_transpose(Op op, const S* __restrict__ in, OT* __restrict__ out, TransposeGeom g) {
+  __shared__ C tile[kTile][kTile + 1];
+  uint32_t q, i0t, ikt, ib;
+  g.t0.divmod(blockIdx.x, q, i0t);
+  g.tk.divmod(q, ib, ikt);
+  const uint32_t a0 = i0t * kTile, ak = ikt * kTile;
+  const S* src = in + (int64_t)ib * g.in_sb;
+  OT* dst = out + (int64_t)ib * g.out_sb;
+  const int tx = threadIdx.x & (kTile - 1), ty = threadIdx.x >> 6;  // 64 x 4 threads
+  // read: lanes run along dim k (the input's contiguous dim)
+#pragma unroll
+  for (int i = 0; i < kTile / 4; ++i) {
+    const uint32_t r0 = a0 + ty + 4 * i, rk = ak + tx;
+    if (r0 < g.d0 && rk < g.dk) tile[ty + 4 * i][tx] = load_cvt<C, CT>(src[(int64_t)r0 * g.in_s0 + rk]);
+  }
+  __syncthreads();
+  // write: lanes run along dim 0 (the output's contiguous dim)
+#pragma unroll
+  for (int i = 0; i < kTile / 4; ++i) {
+    const uint32_t r0 = a0 + tx, rk = ak + ty + 4 * i;
+    if (r0 < g.d0 && rk < g.dk) {
+      const C x = tile[tx][ty + 4 * i];
+      dst[(int64_t)rk * g.out_sk + r0] = from_arith<OT>(op(&x));
+    }
+  }
+}
+
+// The same with 16-byte global accesses on both sides: a tile row (64 input
+// elements along dim k) loads as 16-byte vectors into LDS in the storage
+// type, and each thread assembles a 16-byte output vector along dim 0 from
+// one LDS column.  Needs d0 % VO == 0, dk % VI == 0, every stride a multiple
+// of the vector and 16-byte aligned bases (checked on the host).
+template <typename Op, typename C, typename CT, typename OT, typename S>
+__global__ void __launch_bounds__(kBlock)
+k_transpose_vec(Op op, const S* __restrict__ in, OT* __restrict__ out, TransposeGeom g) {
+  constexpr int VI = 16 / sizeof(S), VO = 16 / sizeof(OT);
+  __shared__ __align__(16) S tile[kTile][kTile + VI];
+  uint32_t q, i0t, ikt, ib;
+  g.t0.divmod(blockIdx.x, q, i0t);
+  g.tk.divmod(q, ib, ikt);
+  const uint32_t a0 = i0t * kTile, ak = ikt * kTile;
+  const S* src = in + (int64_t)ib * g.in_sb;
+  OT* dst = out + (int64_t)ib * g.out_sb;
+  constexpr int VPR = kTile / VI, RPI = kBlock / VPR;  // load: vectors per tile row, rows per pass
+  const int lv = threadIdx.x % VPR, lr = threadIdx.x / VPR;
+#pragma unroll
+  for (int r = lr; r < kTile; r += RPI) {
+    const uint32_t i0 = a0 + r, ik = ak + lv * VI;
+    if (i0 < g.d0 && ik < g.dk)
+      *reinterpret_cast<Vec<S, VI>*>(&tile[r][lv * VI]) =
+          ld_stream(reinterpret_cast<const Vec<S, VI>*>(src + (int64_t)i0 * g.in_s0 + ik));
+  }
+  __syncthreads();
+  constexpr int VPC = kTile / VO, CPI = kBlock / VPC;  // store: vectors per tile column, columns per pass
+  const int wv = threadIdx.x % VPC, wc = threadIdx.x / VPC;
+#pragma unroll
+  for (int c = wc; c < kTile; c += CPI) {
+    const uint32_t ik = ak + c, i0 = a0 + wv * VO;
+    if (ik < g.dk && i0 < g.d0) {
+      Vec<OT, VO> o;
+#pragma unroll
+      for (int j = 0; j < VO; ++j) {
+        const C x = load_cvt<C, CT>(tile[wv * VO + j][c]);
+        o.v[j] = from_arith<OT>(op(&x));
+      }
+      st_stream(reinterpret_cast<Vec<OT, VO>*>(dst + (int64_t)ik * g.out_sk + i0), o);
+    }
+  }
+}
+
 // ----------------------------------------------------------- STRIDED
 template <typename OFF, typename Op, typename C, typename CT, typename OT, typename... S>
 __global__ void __launch_bounds__(kBlock)

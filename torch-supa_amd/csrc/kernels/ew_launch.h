@@ -177,6 +177,45 @@ int launch_static(const Op& op, const supa_amd_ew_desc& d, const int* tin, hipSt
     TArgs<1 + N> b = a;
     b.p[0] = p.op[0].data;
     for (int i = 0; i < N; ++i) b.p[1 + i] = p.op[tin[i]].data;
+    // TRANSPOSE?  One input, dense output, the input contiguous along dim 1 or 2.
+    if constexpr (N == 1) {
+      if ((p.ndim == 2 || p.ndim == 3) && b.st[0][0] == 1 && b.st[0][1] == p.sizes[0] &&
+          (p.ndim == 2 || b.st[0][2] == p.sizes[0] * p.sizes[1]) && b.st[1][0] != 1 && b.st[1][0] != 0 &&
+          p.sizes[0] >= 16) {
+        int k = -1;
+        for (int j = 1; j < p.ndim; ++j)
+          if (b.st[1][j] == 1 && p.sizes[j] >= 16) k = j;
+        if (k > 0) {
+          const int bd = p.ndim == 3 ? 3 - k : -1;  // the batch dim
+          TransposeGeom tg;
+          tg.d0 = (uint32_t)p.sizes[0];
+          tg.dk = (uint32_t)p.sizes[k];
+          tg.db = bd > 0 ? (uint32_t)p.sizes[bd] : 1u;
+          tg.in_s0 = b.st[1][0];
+          tg.in_sb = bd > 0 ? b.st[1][bd] : 0;
+          tg.out_sk = b.st[0][k];
+          tg.out_sb = bd > 0 ? b.st[0][bd] : 0;
+          const uint32_t t0 = (tg.d0 + kTile - 1) / kTile, tk = (tg.dk + kTile - 1) / kTile;
+          tg.t0 = FastDiv(t0);
+          tg.tk = FastDiv(tk);
+          const uint64_t blocks = (uint64_t)t0 * tk * tg.db;
+          if (blocks < (1ull << 31)) {
+            using S0 = typename NthT<0, S...>::type;
+            constexpr int VI = 16 / (int)sizeof(S0), VO = 16 / (int)sizeof(OT);
+            const bool vec = VI > 1 && VO > 1 && tg.d0 % VO == 0 && tg.dk % VI == 0 && tg.in_s0 % VI == 0 &&
+                             tg.in_sb % VI == 0 && tg.out_sk % VO == 0 && tg.out_sb % VO == 0 && aligned(b.p[1], 16) &&
+                             aligned(b.p[0], 16);
+            if (vec)
+              k_transpose_vec<Op, C, CT, OT, S0><<<(unsigned)blocks, kBlock, 0, st>>>(
+                  op, static_cast<const S0*>(b.p[1]), static_cast<OT*>(b.p[0]), tg);
+            else
+              k_transpose<Op, C, CT, OT, S0><<<(unsigned)blocks, kBlock, 0, st>>>(
+                  op, static_cast<const S0*>(b.p[1]), static_cast<OT*>(b.p[0]), tg);
+            return launch_status();
+          }
+        }
+      }
+    }
     // ROW2D?  Two dims, or three with the outer two flattened into rows.
     if ((p.ndim == 2 || p.ndim == 3) && VEC > 1 && (p.sizes[0] % VEC) == 0 && b.st[0][0] == 1 &&
         b.st[0][1] == p.sizes[0] && (p.ndim == 2 || b.st[0][2] == p.sizes[0] * p.sizes[1]) &&
