@@ -301,6 +301,25 @@ int supa_amd_foreach_binary(int op, int32_t ntensors, void* const* out, void* co
                             void* const* b, const int64_t* numel, int32_t dtype, double scalar,
                             double alpha, void* stream);
 
+/* Mixed-precision gradient unscale: every element of the `ntensors`
+ * contiguous tensors (f32 / bf16 / f16 / f64) is multiplied in place by
+ * *inv_scale (left as is when that is exactly 1), and *found_inf (device
+ * float) is set to 1.0 if any element is inf or NaN.  Replaces
+ * _amp_foreach_non_finite_check_and_unscale_ NF:10632 (upstream
+ * AmpKernels.cu over MultiTensorApply.cuh). */
+int supa_amd_amp_unscale(int32_t ntensors, void* const* tensors, const int64_t* numel, int32_t dtype,
+                         float* found_inf, const float* inv_scale, void* stream);
+
+/* Dynamic loss-scale update, one device thread: after an overflow
+ * (*found_inf != 0) scale *= backoff and growth_tracker = 0; otherwise the
+ * tracker counts successful steps and, on reaching growth_interval, the scale
+ * grows by growth_factor (unless that overflows float32) and the tracker
+ * resets.  scale and found_inf are one device float each, growth_tracker one
+ * device int32.  Replaces _amp_update_scale_ NF:10640. */
+int supa_amd_amp_update_scale(float* scale, int32_t* growth_tracker, const float* found_inf,
+                              double growth_factor, double backoff_factor, int64_t growth_interval,
+                              void* stream);
+
 /* One fused AdamW step over `ntensors` tensors (params, grads, exp_avgs,
  * exp_avg_sqs [, max_exp_avg_sqs when amsgrad]) of one dtype (f32, bf16, f16,
  * f64), each with a one-element f32 state_step on the device.  lr_ptr (device

@@ -63,6 +63,8 @@ def lib():
             "or_loss_fwd": (None, [c_int, _f32p, _f32p, _f32p, _f32p, i64, c_int, c_float, _f32p]),
             "or_loss_bwd": (None, [c_int, _f32p, _f32p, _f32p, _f32p, _f32p, i64, c_int, c_float, _f32p]),
             "or_sum_f32": (c_double, [_f32p, i64]),
+            "or_amp_unscale_f32": (c_int, [_f32p, i64, c_float]),
+            "or_amp_update_scale": (None, [_f32p, ctypes.POINTER(ctypes.c_int32), c_float, c_double, c_double, i64]),
             "or_ce_fwd": (c_int, [_f64p, _i64p, i64, i64, i64, c_int, _f64p, _f64p, _f64p]),
             "or_ce_bwd": (None, [_f64p, _f64p, _i64p, _f64p, c_double, i64, i64, i64, c_int, _f64p]),
             "or_adamw_step": (None, [_f32p, _f32p, _f32p, _f32p, i64, c_float, c_double, c_double,
@@ -212,6 +214,22 @@ def nll_loss_backward(grad_out, target, n, c, total_weight, weight=None, reducti
     if rc != 0:
         raise IndexError("nll_loss_backward: target out of bounds")
     return out
+
+
+def amp_unscale(x, inv_scale):
+    """Returns (x * inv_scale as float32, found_inf)."""
+    x = np.array(x, np.float32, copy=True).reshape(-1)
+    bad = lib().or_amp_unscale_f32(_p(x, _f32p), x.size, float(np.float32(inv_scale)))
+    return x, bool(bad)
+
+
+def amp_update_scale(scale, tracker, found_inf, growth, backoff, interval):
+    """Returns the new (scale, tracker)."""
+    s = np.array([scale], np.float32)
+    t = np.array([tracker], np.int32)
+    lib().or_amp_update_scale(_p(s, _f32p), t.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), float(found_inf),
+                              float(growth), float(backoff), int(interval))
+    return float(s[0]), int(t[0])
 
 
 def cross_entropy(x, target, reduction="mean", ignore_index=-100):

@@ -451,6 +451,39 @@ void or_loss_bwd(int op, const float* g, const float* x, const float* t, const f
   }
 }
 
+/* --------------------------------------------------------------- AMP -- */
+
+/* _amp_foreach_non_finite_check_and_unscale_ (AmpKernels.cu): x *= inv_scale
+ * in place unless inv_scale is exactly 1; returns 1 if any element was inf or
+ * NaN before the multiply. */
+int or_amp_unscale_f32(float* x, int64_t n, float inv_scale) {
+  int bad = 0;
+  for (int64_t i = 0; i < n; ++i) {
+    if (!isfinite(x[i])) bad = 1;
+    x[i] = inv_scale == 1.0f ? x[i] : x[i] * inv_scale;
+  }
+  return bad;
+}
+
+/* _amp_update_scale_ (AmpKernels.cu): backoff on overflow, growth after
+ * growth_interval successful steps; products in double rounded to float. */
+void or_amp_update_scale(float* scale, int32_t* tracker, float found_inf, double growth, double backoff,
+                         int64_t interval) {
+  if (found_inf != 0.0f) {
+    *scale = (float)((double)*scale * backoff);
+    *tracker = 0;
+  } else {
+    const int64_t successful = (int64_t)*tracker + 1;
+    if (successful == interval) {
+      const float grown = (float)((double)*scale * growth);
+      if (isfinite(grown)) *scale = grown;
+      *tracker = 0;
+    } else {
+      *tracker = (int32_t)successful;
+    }
+  }
+}
+
 /* ----------------------------------------------------------- reductions -- */
 
 /* sum / mean over all elements (ReduceSumKernel.cu:102-113,

@@ -589,3 +589,70 @@ def test_allocator_stats_and_reuse():
     del y
     torch.supa.empty_cache()
     assert torch.supa.memory_reserved() <= torch.supa.memory_stats()["reserved_bytes"]
+
+
+# ---------------------------------------------------------------- AMP
+def test_amp_unscale_and_update_scale(no_fallback):
+    """_amp_foreach_non_finite_check_and_unscale_ over a mixed-dtype list
+    (with a non-contiguous member) and _amp_update_scale_ over a sequence of
+    overflow flags, against upstream's CPU kernels."""
+    xs = [seeded((1000, 33), 70, 100.0), seeded((4097,), 71, 100.0).to(torch.bfloat16),
+          seeded((64, 50), 72).t(), seeded((7,), 73).to(torch.float16)]
+    for inv, poison in ((0.125, False), (1.0, False), (0.5, True)):
+        cpu = [x.clone() for x in xs]
+        if poison:
+            cpu[1][5] = float("inf")
+        gpu = [dev(x) for x in cpu]
+        fi_c, fi_g = torch.zeros(1), dev(torch.zeros(1))
+        torch._amp_foreach_non_finite_check_and_unscale_(cpu, fi_c, torch.tensor([inv]))
+        torch._amp_foreach_non_finite_check_and_unscale_(gpu, fi_g, dev(torch.tensor([inv])))
+        for a, b in zip(cpu, gpu):
+            assert torch.equal(a, b.cpu())
+        assert fi_g.item() == fi_c.item() == float(poison)
+    scale_c, tr_c = torch.tensor([65536.0]), torch.zeros(1, dtype=torch.int32)
+    scale_g, tr_g = dev(scale_c.clone()), dev(tr_c.clone())
+    for i, inf in enumerate([0, 0, 1, 0, 0, 0, 1, 1, 0, 0]):
+        f = torch.tensor([float(inf)])
+        torch._amp_update_scale_(scale_c, tr_c, f, 2.0, 0.5, 2)
+        torch._amp_update_scale_(scale_g, tr_g, dev(f), 2.0, 0.5, 2)
+        assert scale_g.item() == scale_c.item() and tr_g.item() == tr_c.item(), i
+
+
+def test_grad_scaler_with_fused_adamw(supa):
+    """torch.amp.GradScaler + AdamW(fused=True) on supa: the scaled backward,
+    the non-finite check, the fused step with grad_scale / found_inf and the
+    scale update match the oracle step for step, and an overflowing step is
+    skipped while the scale backs off."""
+    supa.supa.reset_fallback_counts()
+    g = torch.Generator().manual_seed(74)
+    shapes = [(256, 300), (300,), (17, 5)]
+    p0 = [torch.randn(s, generator=g) * 0.02 for s in shapes]
+    cs = [torch.randn(s, generator=g) * 1e-3 for s in shapes]
+    dp = [dev(p).requires_grad_() for p in p0]
+    dc = [dev(c) for c in cs]
+    opt = torch.optim.AdamW(dp, lr=1e-3, weight_decay=0.01, fused=True)
+    scaler = torch.amp.GradScaler("supa", init_scale=2.0 ** 10, growth_interval=2)
+    hp = [p.numpy().ravel().copy() for p in p0]
+    hm = [np.zeros_like(x) for x in hp]
+    hv = [np.zeros_like(x) for x in hp]
+    scale, tracker, step = 2.0 ** 10, 0, 0
+    for it in range(5):
+        opt.zero_grad()
+        loss = sum((p * c).sum() for p, c in zip(dp, dc))
+        if it == 2:
+            loss = loss * float("inf")  # every gradient overflows
+        scaler.scale(loss).backward()
+        scaler.step(opt)
+        scaler.update()
+        overflow = it == 2
+        if not overflow:
+            step += 1
+            for i in range(len(shapes)):
+                hg = (cs[i].numpy().ravel() * np.float32(scale)).astype(np.float32)
+                O.adamw_step(hp[i], hg, hm[i], hv[i], float(step), 1e-3, 0.9, 0.999, 0.01, 1e-8, grad_scale=scale)
+        scale, tracker = O.amp_update_scale(scale, tracker, float(overflow), 2.0, 0.5, 2)
+        assert scaler.get_scale() == scale, it
+    for i in range(len(shapes)):
+        np.testing.assert_allclose(dp[i].detach().cpu().numpy().ravel(), hp[i], rtol=1e-6, atol=1e-9)
+    used = supa.supa.fallback_counts()
+    assert not any("amp" in k or "adamw" in k for k in used), used

@@ -349,3 +349,30 @@ def test_adamw_ten_steps_vs_cpu_and_restart():
         for step in range(6, 11):
             O.adamw_step(p2, gr, m2, v2, float(step), 1e-4, 0.9, 0.999, 0.01, 1e-8)
         assert np.array_equal(p2, p) and np.array_equal(m2, m) and np.array_equal(v2, v)
+
+
+# ------------------------------------------------------------------ AMP
+def test_amp_unscale_vs_cpu():
+    x = randn((5000,), 60, 1000.0)
+    x[17] = float("inf")
+    x[300] = float("nan")
+    for inv, xs in ((0.125, x), (1.0, x), (3.0e-5, x[:100]), (0.5, x[400:])):
+        ref = [xs.clone()]
+        fi = torch.zeros(1)
+        torch._amp_foreach_non_finite_check_and_unscale_(ref, fi, torch.tensor([inv]))
+        got, bad = O.amp_unscale(xs.numpy(), inv)
+        np.testing.assert_array_equal(got, ref[0].numpy())
+        assert bad == bool(fi.item())
+
+
+def test_amp_update_scale_vs_cpu():
+    rng = np.random.default_rng(61)
+    for growth, backoff, interval in ((2.0, 0.5, 3), (1.7, 0.3, 1), (65536.0, 0.5, 2)):
+        scale = torch.tensor([65536.0])
+        tracker = torch.zeros(1, dtype=torch.int32)
+        s, t = 65536.0, 0
+        for _ in range(40):
+            inf = float(rng.random() < 0.2)
+            torch._amp_update_scale_(scale, tracker, torch.tensor([inf]), growth, backoff, interval)
+            s, t = O.amp_update_scale(s, t, inf, growth, backoff, interval)
+            assert s == scale.item() and t == tracker.item()

@@ -1,5 +1,7 @@
 // PrivateUse1 registrations of the optimizer path: _foreach_add / _foreach_mul
-// (List and Scalar overloads, in-place and out-of-place) and _fused_adamw_.
+// (List and Scalar overloads, in-place and out-of-place), _fused_adamw_, and
+// the mixed-precision pieces beside it (_amp_foreach_non_finite_check_and_unscale_,
+// _amp_update_scale_).
 //
 // Fast path: every tensor on one supa device, one floating dtype, dense and
 // contiguous (and, for List overloads, matching shapes) -- then one
@@ -8,6 +10,8 @@
 // elementwise op per tensor (still on the supa kernels).
 #include <ATen/native/ForeachUtils.h>
 #include <torch/library.h>
+
+#include <map>
 
 #include "common.h"
 
@@ -207,6 +211,60 @@ void fused_adamw_tensor_lr_(at::TensorList params, at::TensorList grads, at::Ten
                    weight_decay, eps, amsgrad, maximize, grad_scale, found_inf);
 }
 
+// ------------------------------------------------------------- AMP
+// _amp_foreach_non_finite_check_and_unscale_: one multi-tensor launch per
+// dtype group of contiguous supa tensors; anything else (non-contiguous
+// tensors) is unscaled tensor by tensor through the same kernel on a
+// contiguous copy.
+void amp_unscale_(at::TensorList self, at::Tensor& found_inf, const at::Tensor& inv_scale) {
+  TORCH_CHECK(found_inf.numel() == 1 && found_inf.scalar_type() == at::kFloat && found_inf.device().type() == kSupa,
+              "found_inf must be a one-element float tensor on the supa device");
+  TORCH_CHECK(inv_scale.numel() == 1 && inv_scale.scalar_type() == at::kFloat && inv_scale.device().type() == kSupa,
+              "inv_scale must be a one-element float tensor on the supa device");
+  if (self.empty()) return;
+  const auto dev = found_inf.device().index();
+  std::map<c10::ScalarType, std::vector<at::Tensor>> groups;
+  for (const at::Tensor& t : self) {
+    TORCH_CHECK(t.device() == found_inf.device(), "_amp_foreach_non_finite_check_and_unscale_: tensors on ",
+                t.device(), " and ", found_inf.device());
+    TORCH_CHECK(float_family(t.scalar_type()), "_amp_foreach_non_finite_check_and_unscale_: expected floating "
+                "tensors, got ", t.scalar_type());
+    groups[t.scalar_type()].push_back(t);
+  }
+  for (auto& [dt, ts] : groups) {
+    std::vector<at::Tensor> work, back;
+    std::vector<void*> ptrs;
+    std::vector<int64_t> numel;
+    for (const at::Tensor& t : ts) {
+      at::Tensor w = t.is_contiguous() ? t : t.contiguous();
+      ptrs.push_back(w.data_ptr());
+      numel.push_back(w.numel());
+      work.push_back(w);
+    }
+    const int rc = supa_amd_amp_unscale((int32_t)ptrs.size(), ptrs.data(), numel.data(), dtype_code(dt),
+                                        found_inf.data_ptr<float>(), inv_scale.data_ptr<float>(), current_stream(dev));
+    check_status(rc, "_amp_foreach_non_finite_check_and_unscale_");
+    for (size_t i = 0; i < ts.size(); ++i)
+      if (!work[i].is_same(ts[i])) ts[i].copy_(work[i]);
+  }
+}
+
+at::Tensor& amp_update_scale_(at::Tensor& self, at::Tensor& growth_tracker, const at::Tensor& found_inf,
+                              double growth_factor, double backoff_factor, int64_t growth_interval) {
+  TORCH_CHECK(self.numel() == 1 && self.scalar_type() == at::kFloat, "_amp_update_scale_: scale must be a "
+              "one-element float tensor");
+  TORCH_CHECK(growth_tracker.numel() == 1 && growth_tracker.scalar_type() == at::kInt,
+              "_amp_update_scale_: growth_tracker must be a one-element int tensor");
+  TORCH_CHECK(found_inf.numel() == 1 && found_inf.scalar_type() == at::kFloat,
+              "_amp_update_scale_: found_inf must be a one-element float tensor");
+  const auto dev = self.device().index();
+  const int rc = supa_amd_amp_update_scale(self.data_ptr<float>(), growth_tracker.data_ptr<int32_t>(),
+                                           found_inf.data_ptr<float>(), growth_factor, backoff_factor,
+                                           growth_interval, current_stream(dev));
+  check_status(rc, "_amp_update_scale_");
+  return self;
+}
+
 }  // namespace
 }  // namespace supa
 
@@ -222,4 +280,6 @@ TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
   m.impl("_foreach_mul.List", TORCH_FN(foreach_mul_list));
   m.impl("_fused_adamw_", TORCH_FN(fused_adamw_));
   m.impl("_fused_adamw_.tensor_lr", TORCH_FN(fused_adamw_tensor_lr_));
+  m.impl("_amp_foreach_non_finite_check_and_unscale_", TORCH_FN(amp_unscale_));
+  m.impl("_amp_update_scale_", TORCH_FN(amp_update_scale_));
 }

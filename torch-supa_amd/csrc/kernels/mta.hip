@@ -218,6 +218,63 @@ k_adamw(AdamTable tab, AdamHyper h) {
     adamw_elem<T>(p[e], g[e], m[e], v[e], h.amsgrad ? vm + e : nullptr, h, lr, lr_wd, bc1, bc2_sqrt, step_size);
 }
 
+// ------------------------------------------------------------ AMP
+// In-place unscale of a gradient list with the non-finite check of upstream
+// _amp_foreach_non_finite_check_and_unscale_ (AmpKernels.cu): each element is
+// widened to opmath, *found_inf becomes 1 if it is inf or NaN, and it is
+// multiplied by *inv_scale unless that is exactly 1.  Every writer of
+// *found_inf stores the same 1.0f.
+template <typename T, int64_t CHUNK>
+__global__ void __launch_bounds__(kMtaBlock)
+k_amp_unscale(ForeachTable tab, float* __restrict__ found_inf, const float* __restrict__ inv_scale) {
+  using C = opmath_t<T>;
+  constexpr int V = 16 / sizeof(T);
+  const int k = find_tensor(tab.chunk_start, tab.ntensors, blockIdx.x);
+  const int64_t chunk = blockIdx.x - tab.chunk_start[k];
+  const int64_t n = tab.numel[k];
+  const int64_t lo = chunk * CHUNK;
+  const int64_t hi = lo + CHUNK < n ? lo + CHUNK : n;
+  T* x = static_cast<T*>(tab.out[k]);
+  const C inv = (C)*inv_scale;
+  bool bad = false;
+  auto f = [&](C v) -> C {
+    bad = bad || !isfinite(v);
+    return inv == C(1) ? v : v * inv;
+  };
+  int64_t start = lo;
+  if (aligned(x, 16)) {
+    const int64_t nv = (hi - lo) / V;
+    for (int64_t i = threadIdx.x; i < nv; i += kMtaBlock) {
+      Vec<T, V> w = ld_stream(reinterpret_cast<const Vec<T, V>*>(x + lo + i * V));
+#pragma unroll
+      for (int j = 0; j < V; ++j) w.v[j] = from_arith<T>(f((C)to_arith(w.v[j])));
+      st_stream(reinterpret_cast<Vec<T, V>*>(x + lo + i * V), w);
+    }
+    start = lo + nv * V;
+  }
+  for (int64_t e = start + threadIdx.x; e < hi; e += kMtaBlock) x[e] = from_arith<T>(f((C)to_arith(x[e])));
+  if (bad) *found_inf = 1.0f;
+}
+
+// Loss-scale update of upstream _amp_update_scale_ (AmpKernels.cu): one thread.
+__global__ void k_amp_update_scale(float* scale, int32_t* growth_tracker, const float* found_inf, double growth,
+                                   double backoff, int64_t interval) {
+  // products in double, rounded once to float, as upstream's float * double
+  if (*found_inf) {
+    *scale = (float)((double)(*scale) * backoff);
+    *growth_tracker = 0;
+  } else {
+    const int64_t successful = (int64_t)(*growth_tracker) + 1;
+    if (successful == interval) {
+      const float grown = (float)((double)(*scale) * growth);
+      if (isfinite(grown)) *scale = grown;
+      *growth_tracker = 0;
+    } else {
+      *growth_tracker = (int32_t)successful;
+    }
+  }
+}
+
 template <typename F>
 int with_mta_storage(int dtype, F&& f) {
   switch (dtype) {
@@ -327,6 +384,51 @@ int supa_amd_foreach_binary(int op, int32_t ntensors, void* const* out, void* co
     if (b) return launch_foreach<T, chunk_one<T>()>(op, ntensors, out, a, b, numel, scalar, alpha, st);
     return launch_foreach<T, 2 * chunk_one<T>()>(op, ntensors, out, a, b, numel, scalar, alpha, st);
   });
+}
+
+int supa_amd_amp_unscale(int32_t ntensors, void* const* tensors, const int64_t* numel, int32_t dtype,
+                         float* found_inf, const float* inv_scale, void* stream) {
+  if (ntensors < 0 || (ntensors > 0 && (!tensors || !numel || !found_inf || !inv_scale))) return SUPA_AMD_EINVAL;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return with_mta_storage(dtype, [&](auto* tag) -> int {
+    using T = std::remove_pointer_t<decltype(tag)>;
+    constexpr int64_t CHUNK = chunk_one<T>();
+    int i = 0;
+    while (i < ntensors) {
+      ForeachTable tab{};
+      uint32_t chunks = 0;
+      int nt = 0;
+      while (i < ntensors && nt < kMtaTensors) {
+        if (numel[i] < 0) return SUPA_AMD_EINVAL;
+        const int64_t c = (numel[i] + CHUNK - 1) / CHUNK;
+        if (c > (int64_t)0x7fffffff) return SUPA_AMD_ELAYOUT;
+        if ((int64_t)chunks + c > (int64_t)0x7fffffff) break;
+        if (numel[i] > 0) {
+          tab.out[nt] = tensors[i];
+          tab.numel[nt] = numel[i];
+          tab.chunk_start[nt] = chunks;
+          chunks += (uint32_t)c;
+          ++nt;
+        }
+        ++i;
+      }
+      tab.chunk_start[nt] = chunks;
+      tab.ntensors = nt;
+      if (nt == 0) continue;
+      k_amp_unscale<T, CHUNK><<<chunks, kMtaBlock, 0, st>>>(tab, found_inf, inv_scale);
+      const int rc = launch_status();
+      if (rc) return rc;
+    }
+    return SUPA_AMD_OK;
+  });
+}
+
+int supa_amd_amp_update_scale(float* scale, int32_t* growth_tracker, const float* found_inf, double growth_factor,
+                              double backoff_factor, int64_t growth_interval, void* stream) {
+  if (!scale || !growth_tracker || !found_inf) return SUPA_AMD_EINVAL;
+  k_amp_update_scale<<<1, 1, 0, static_cast<hipStream_t>(stream)>>>(scale, growth_tracker, found_inf, growth_factor,
+                                                                     backoff_factor, growth_interval);
+  return launch_status();
 }
 
 int supa_amd_fused_adamw(int32_t ntensors, void* const* params, void* const* grads, void* const* exp_avgs,
