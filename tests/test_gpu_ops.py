@@ -656,3 +656,32 @@ def test_grad_scaler_with_fused_adamw(supa):
         np.testing.assert_allclose(dp[i].detach().cpu().numpy().ravel(), hp[i], rtol=1e-6, atol=1e-9)
     used = supa.supa.fallback_counts()
     assert not any("amp" in k or "adamw" in k for k in used), used
+
+
+def test_fused_adamw_bf16_params(no_fallback):
+    """bf16 parameters and state: every element is loaded to float, stepped
+    with the float32 arithmetic and stored back as bf16 (upstream's opmath
+    rule), so the oracle's float step on bf16-rounded values, rounded after
+    every step, is bit-identical."""
+    shapes = [(1024, 513), (77,)]
+    g = torch.Generator().manual_seed(75)
+    params = [(torch.randn(s, generator=g) * 0.02).to(torch.bfloat16) for s in shapes]
+    grads = [(torch.randn(s, generator=g) * 1e-3).to(torch.bfloat16) for s in shapes]
+    dp = [dev(p).requires_grad_() for p in params]
+    opt = torch.optim.AdamW(dp, lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01, fused=True)
+    for _ in range(4):
+        for p, gr in zip(dp, grads):
+            p.grad = dev(gr)
+        opt.step()
+    for i in range(len(shapes)):
+        hp = params[i].float().numpy().ravel().copy()
+        hg = grads[i].float().numpy().ravel().copy()
+        hm, hv = np.zeros_like(hp), np.zeros_like(hp)
+        for step in range(1, 5):
+            O.adamw_step(hp, hg, hm, hv, float(step), 1e-3, 0.9, 0.999, 0.01, 1e-8)
+            for a in (hp, hm, hv):
+                a[:] = O.round_bf16(a)
+        assert np.array_equal(dp[i].detach().float().cpu().numpy().ravel(), hp), i
+        st = opt.state[dp[i]]
+        assert np.array_equal(st["exp_avg"].float().cpu().numpy().ravel(), hm)
+        assert np.array_equal(st["exp_avg_sq"].float().cpu().numpy().ravel(), hv)
