@@ -275,6 +275,11 @@ def bench_c5(torch, timer, steps=10):
         pd = [p.detach() for p in params]
         res["_foreach_add_List"] = entry(12 * P, timer.time(lambda: torch._foreach_add_(pd, grads), 3, warmup=1))
         res["_foreach_mul_Scalar"] = entry(8 * P, timer.time(lambda: torch._foreach_mul_(pd, 1.0), 3, warmup=1))
+        # GradScaler's unscale of the 72 gradients (inv_scale 1: check only, values kept)
+        found_inf = torch.zeros(1, device="supa")
+        inv = torch.ones(1, device="supa")
+        res["_amp_foreach_non_finite_check_and_unscale_"] = entry(8 * P, timer.time(
+            lambda: torch._amp_foreach_non_finite_check_and_unscale_(grads, found_inf, inv), 3, warmup=1))
     return res
 
 
