@@ -101,6 +101,27 @@ int supa_amd_mul(const supa_amd_ew_desc* d, void* stream);
 #define SUPA_AMD_DIV_FLOOR 2
 int supa_amd_div(const supa_amd_ew_desc* d, int mode, void* stream);
 
+/* out = maximum(a, b) (is_max) or minimum(a, b); a NaN operand is the
+ * result.  op = {out, a, b}.  Replaces maximum.out / minimum.out (upstream
+ * MaxMinElementwiseKernel.cu) and, with a bound operand, clamp_min /
+ * clamp_max. */
+int supa_amd_minmax(const supa_amd_ew_desc* d, int is_max, void* stream);
+
+/* Ternary pointwise ops, op = {out, self, t1, t2}:
+ *   ADDCMUL  out = self + value * (t1 * t2)
+ *   ADDCDIV  out = self + value * (t1 / t2)        (floating dtypes)
+ *   LERP     out = lerp(self, end = t1, weight = t2): |w| < 0.5 ?
+ *            self + w (end - self) : end - (end - self)(1 - w)  (floating)
+ * value / ivalue: the bound value for floating / integer results (unused by
+ * LERP, whose weight may be an immediate scalar operand).  Each `a + v * x`
+ * is one fused multiply-add.  Replaces addcmul.out / addcdiv.out (upstream
+ * PointwiseOpsKernel.cu) and lerp.Scalar_out / lerp.Tensor_out (upstream
+ * Lerp.cu), which the reference takes from its operator library. */
+#define SUPA_AMD_ADDCMUL 0
+#define SUPA_AMD_ADDCDIV 1
+#define SUPA_AMD_LERP 2
+int supa_amd_pointwise(const supa_amd_ew_desc* d, int op, double value, int64_t ivalue, void* stream);
+
 /* ------------------------------------------------ activations (unary) */
 #define SUPA_AMD_GELU 0
 #define SUPA_AMD_GELU_TANH 1

@@ -24,7 +24,8 @@ _SO = os.path.join(_HERE, "_build", "liboracle.so")
 _lib = None
 
 # op codes shared with oracle.c
-ADD, MUL, DIV, DIV_TRUNC, DIV_FLOOR = 0, 1, 2, 3, 4
+ADD, MUL, DIV, DIV_TRUNC, DIV_FLOOR, MAXIMUM, MINIMUM = 0, 1, 2, 3, 4, 5, 6
+ADDCMUL, ADDCDIV, LERP = 0, 1, 2
 GELU, GELU_TANH, SILU, SIGMOID, TANH, EXP, LOG, ERF, RELU, NEG, RECIPROCAL, ABS, SQRT = range(13)
 MSE, SMOOTH_L1, BCE_LOGITS = 0, 1, 2
 REDUCTION = {"none": 0, "mean": 1, "sum": 2}
@@ -55,6 +56,7 @@ def lib():
             "or_binary_f32": (None, [c_int, _f32p, _f32p, _f32p, i64, c_float]),
             "or_binary_f64": (None, [c_int, _f64p, _f64p, _f64p, i64, c_double]),
             "or_unary_f32": (None, [c_int, _f32p, _f32p, i64]),
+            "or_ternary_f32": (None, [c_int, _f32p, _f32p, _f32p, _f32p, i64, c_float]),
             "or_unary_backward_f32": (None, [c_int, _f32p, _f32p, _f32p, i64]),
             "or_log_softmax_fwd": (None, [_f32p, _f32p, i64, i64]),
             "or_log_softmax_bwd": (None, [_f32p, _f32p, _f32p, i64, i64]),
@@ -167,6 +169,16 @@ def unary_backward(op: int, dy, x) -> np.ndarray:
 
 
 # ------------------------------------------------------------- row ops --
+def ternary(op: int, a, b, c, value=1.0) -> np.ndarray:
+    """addcmul / addcdiv (value) / lerp (c = weight) in float32, broadcast."""
+    a, b, c = np.broadcast_arrays(np.asarray(a, np.float32), np.asarray(b, np.float32), np.asarray(c, np.float32))
+    a, b, c = _c(a, np.float32), _c(b, np.float32), _c(c, np.float32)
+    out = np.empty(a.shape, np.float32)
+    lib().or_ternary_f32(op, _p(a, _f32p), _p(b, _f32p), _p(c, _f32p), _p(out, _f32p), a.size,
+                         float(np.float32(value)))
+    return out
+
+
 def log_softmax(x) -> np.ndarray:
     """log_softmax over the last dim (float32 in, float32 out)."""
     x = _c(x, np.float32)

@@ -68,7 +68,12 @@ void or_f64_to_bf16(const double* in, uint16_t* out, int64_t n) {
 
 /* ------------------------------------------------------------ binary ops -- */
 
-enum { OR_ADD = 0, OR_MUL = 1, OR_DIV = 2, OR_DIV_TRUNC = 3, OR_DIV_FLOOR = 4 };
+enum { OR_ADD = 0, OR_MUL = 1, OR_DIV = 2, OR_DIV_TRUNC = 3, OR_DIV_FLOOR = 4, OR_MAX = 5, OR_MIN = 6 };
+
+/* maximum / minimum (upstream MaxMinElementwiseKernel.cu): a NaN operand is
+ * the result. */
+static inline float max_nan_f32(float a, float b) { return isnan(a) ? a : (isnan(b) ? b : (a > b ? a : b)); }
+static inline float min_nan_f32(float a, float b) { return isnan(a) ? a : (isnan(b) ? b : (a < b ? a : b)); }
 
 /* c10::div_floor_floating (c10/util/generic_math.h), the Python-style floor
  * division that BinaryDivFloorKernel.cu:22-82 applies to floating types. */
@@ -116,6 +121,8 @@ void or_binary_f32(int op, const float* a, const float* b, float* out, int64_t n
       case OR_MUL: r = x * y; break;
       case OR_DIV: r = x / y; break;
       case OR_DIV_TRUNC: r = truncf(x / y); break;
+      case OR_MAX: r = max_nan_f32(x, y); break;
+      case OR_MIN: r = min_nan_f32(x, y); break;
       default: r = div_floor_f32(x, y); break;
     }
     out[i] = r;
@@ -135,6 +142,33 @@ void or_binary_f64(int op, const double* a, const double* b, double* out, int64_
     out[i] = r;
   }
 }
+
+/* ---------------------------------------------------- ternary pointwise -- */
+
+enum { OR_ADDCMUL = 0, OR_ADDCDIV = 1, OR_LERP = 2 };
+
+/* addcmul / addcdiv: self + value * (t1 op t2) with the product-sum as one
+ * fma (upstream CUDA PointwiseOpsKernel.cu / ForeachPointwiseOp.cu as the
+ * CUDA compiler contracts it); lerp: upstream Lerp.h,
+ * |w| < 0.5 ? self + w (end - self) : end - (end - self)(1 - w), each
+ * product-sum one fma.  c is t2 (addc*) or the weight (lerp). */
+void or_ternary_f32(int op, const float* a, const float* b, const float* c, float* out, int64_t n, float value) {
+  for (int64_t i = 0; i < n; ++i) {
+    const float x = a[i], y = b[i], z = c[i];
+    float r;
+    switch (op) {
+      case OR_ADDCMUL: r = fmaf(value, y * z, x); break;
+      case OR_ADDCDIV: r = fmaf(value, y / z, x); break;
+      default: {
+        const float d = y - x;
+        r = fabsf(z) < 0.5f ? fmaf(z, d, x) : fmaf(-d, 1.0f - z, y);
+        break;
+      }
+    }
+    out[i] = r;
+  }
+}
+
 
 /* -------------------------------------------------------- activations -- */
 

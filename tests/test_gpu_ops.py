@@ -58,7 +58,7 @@ def test_binary_ladder(shape, dtype, no_fallback):
     for fn in (torch.add, torch.sub, torch.mul, torch.div):
         got = fn(da, db).cpu()
         assert got.dtype == dtype
-        assert torch.equal(got, fn(a, b)) or dtype == torch.float16 and torch.allclose(got, fn(a, b), rtol=1e-3), fn
+        assert torch.equal(got, fn(a, b)), fn
 
 
 @pytest.mark.parametrize("shape", SHAPES)
@@ -685,3 +685,94 @@ def test_fused_adamw_bf16_params(no_fallback):
         st = opt.state[dp[i]]
         assert np.array_equal(st["exp_avg"].float().cpu().numpy().ravel(), hm)
         assert np.array_equal(st["exp_avg_sq"].float().cpu().numpy().ravel(), hv)
+
+
+# ------------------------------------------------ pointwise ternary / minmax
+def _exact(got, ref):
+    torch.testing.assert_close(got.cpu(), ref, rtol=0, atol=0, equal_nan=True)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("shape", [(1000,), (513, 4100)])
+def test_addcmul_addcdiv_lerp_bit_exact(shape, dtype, no_fallback):
+    """addcmul / addcdiv / lerp (Scalar and Tensor weight) are the oracle's
+    float32 arithmetic rounded once to the tensor dtype."""
+    x, y = seeded(shape, 70, 2.0, dtype), seeded(shape, 71, 2.0, dtype)
+    z = seeded(shape, 72, 2.0)
+    z = (z.sign() * (z.abs() + 0.25)).to(dtype)
+    w = (torch.rand(shape, generator=torch.Generator().manual_seed(73)) * 1.4 - 0.2).to(dtype)
+    dx, dy, dz, dw = dev(x), dev(y), dev(z), dev(w)
+    f = [t.float().numpy() for t in (x, y, z, w)]
+
+    def want(arr):
+        return torch.from_numpy(arr).to(dtype)
+
+    _exact(torch.addcmul(dx, dy, dz, value=-0.37), want(O.ternary(O.ADDCMUL, f[0], f[1], f[2], -0.37)))
+    _exact(torch.addcdiv(dx, dy, dz, value=0.5), want(O.ternary(O.ADDCDIV, f[0], f[1], f[2], 0.5)))
+    _exact(torch.lerp(dx, dy, dw), want(O.ternary(O.LERP, f[0], f[1], f[3])))
+    for ws in (0.1, 0.75):
+        wf = np.full(f[0].shape, np.float32(ws), np.float32)
+        _exact(torch.lerp(dx, dy, ws), want(O.ternary(O.LERP, f[0], f[1], wf)))
+    # in-place and out= forms run the same kernels
+    e = dx.clone()
+    e.addcmul_(dy, dz, value=2.0).lerp_(dy, 0.25)
+    ref = O.ternary(O.ADDCMUL, f[0], f[1], f[2], 2.0)
+    ref = O.ternary(O.LERP, want(ref).float().numpy(), f[1], np.full(ref.shape, 0.25, np.float32))
+    _exact(e, want(ref))
+    out = torch.empty_like(dx)
+    torch.addcdiv(dx, dy, dz, out=out)
+    _exact(out, want(O.ternary(O.ADDCDIV, f[0], f[1], f[2], 1.0)))
+    if dtype == torch.float32:  # same results as upstream's CPU kernels where both round once
+        assert torch.equal(torch.lerp(dx, dy, dw).cpu(), torch.lerp(x, y, w))
+
+
+def test_pointwise_broadcast_and_integer(no_fallback):
+    x = seeded((64, 1, 300), 74)
+    y = seeded((300,), 75)
+    z = seeded((1, 5, 1), 76)
+    dx, dy, dz = dev(x), dev(y), dev(z)
+    ref = O.ternary(O.ADDCMUL, *np.broadcast_arrays(x.numpy(), y.numpy(), z.numpy()), 0.5)
+    _exact(torch.addcmul(dx, dy, dz, value=0.5), torch.from_numpy(np.ascontiguousarray(ref)))
+    # integers: exact integer arithmetic, value an int
+    a = torch.randint(-1000, 1000, (777,), generator=torch.Generator().manual_seed(77))
+    b = torch.randint(-30, 30, (777,), generator=torch.Generator().manual_seed(78))
+    c = torch.randint(-30, 30, (777,), generator=torch.Generator().manual_seed(79))
+    assert torch.equal(torch.addcmul(dev(a), dev(b), dev(c), value=3).cpu(), torch.addcmul(a, b, c, value=3))
+    with pytest.raises(RuntimeError, match="Integer division"):
+        torch.addcdiv(dev(a), dev(b), dev(c))
+    with pytest.raises(RuntimeError):
+        torch.lerp(dx, dev(y.double()), 0.5)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.int64])
+def test_maximum_minimum_clamp(dtype, no_fallback):
+    """Selection ops are exact: same values as upstream's CPU kernels,
+    including NaN propagation and clamp with min > max."""
+    g = torch.Generator().manual_seed(80)
+    if dtype.is_floating_point:
+        a = (torch.randn(257, 1031, generator=g) * 3).to(dtype)
+        b = (torch.randn(257, 1031, generator=g) * 3).to(dtype)
+        a[::13, ::7] = float("nan")
+        b[::11, ::5] = float("nan")
+    else:
+        a = torch.randint(-100, 100, (257, 1031), generator=g, dtype=dtype)
+        b = torch.randint(-100, 100, (257, 1031), generator=g, dtype=dtype)
+    da, db = dev(a), dev(b)
+    _exact(torch.maximum(da, db), torch.maximum(a, b))
+    _exact(torch.minimum(da, db), torch.minimum(a, b))
+    _exact(torch.maximum(da, db[:1]), torch.maximum(a, b[:1]))  # broadcast row
+    _exact(torch.clamp(da, -1, 2), torch.clamp(a, -1, 2))
+    _exact(torch.clamp(da, 2, -1), torch.clamp(a, 2, -1))  # min > max gives max
+    _exact(torch.clamp(da, min=0), torch.clamp(a, min=0))
+    _exact(torch.clamp(da, max=0), torch.clamp(a, max=0))
+    _exact(torch.clamp_min(da, db), torch.clamp_min(a, b))
+    _exact(torch.clamp_max(da, db), torch.clamp_max(a, b))
+    e = da.clone()
+    e.clamp_(-2, 1).clamp_min_(-1).clamp_max_(db)
+    _exact(e, a.clone().clamp_(-2, 1).clamp_min_(-1).clamp_max_(b))
+    out = torch.empty_like(da)
+    torch.maximum(da, db, out=out)
+    _exact(out, torch.maximum(a, b))
+    if dtype == torch.int64:
+        # an integer tensor clamped by a float bound promotes, as upstream
+        _exact(torch.clamp(da, -1.5, 2.5), torch.clamp(a, -1.5, 2.5))

@@ -376,3 +376,51 @@ def test_amp_update_scale_vs_cpu():
             torch._amp_update_scale_(scale, tracker, torch.tensor([inf]), growth, backoff, interval)
             s, t = O.amp_update_scale(s, t, inf, growth, backoff, interval)
             assert s == scale.item() and t == tracker.item()
+
+
+# ------------------------------------------------- pointwise (ternary) ops
+def test_maximum_minimum_vs_cpu():
+    a, b = randn((3000,), 62), randn((3000,), 63)
+    a[::7] = float("nan")
+    b[::11] = float("nan")
+    a[5], b[5] = 0.0, -0.0
+    for op, fn in ((O.MAXIMUM, torch.maximum), (O.MINIMUM, torch.minimum)):
+        got = O.binary(op, a.numpy(), b.numpy())
+        ref = fn(a, b).numpy()
+        np.testing.assert_array_equal(np.isnan(got), np.isnan(ref))
+        m = ~np.isnan(ref)
+        np.testing.assert_array_equal(got[m], ref[m])
+
+
+@pytest.mark.parametrize("op", ["addcmul", "addcdiv"])
+def test_addcmul_addcdiv_vs_exact_and_cpu(op):
+    """self + v * (t1 op t2) as one fma: within half an ulp of the product
+    rounding of the exact value, and within the CPU kernel's own rounding of
+    upstream's CPU result (which multiplies (v * t1) * t2 first)."""
+    x, y, z = randn((20000,), 64, 4.0), randn((20000,), 65, 4.0), randn((20000,), 66, 4.0)
+    if op == "addcdiv":
+        z = z.sign() * (z.abs() + 0.5)
+    v = -0.37
+    got = O.ternary(O.ADDCMUL if op == "addcmul" else O.ADDCDIV, x.numpy(), y.numpy(), z.numpy(), v)
+    xd, yd, zd = x.double(), y.double(), z.double()
+    t = yd * zd if op == "addcmul" else yd / zd
+    exact = (xd + np.float32(v) * t).numpy()
+    scale = (xd.abs() + (np.float32(v) * t).abs()).numpy()
+    eps = 2.0 ** -24
+    assert np.all(np.abs(got - exact) <= 2 * eps * scale)
+    ref = (torch.addcmul if op == "addcmul" else torch.addcdiv)(x, y, z, value=v).numpy()
+    assert np.all(np.abs(got - ref) <= 4 * eps * scale)
+
+
+def test_lerp_vs_exact_and_cpu():
+    x, e = randn((20000,), 67, 3.0), randn((20000,), 68, 3.0)
+    w = torch.rand(20000, generator=torch.Generator().manual_seed(69)) * 1.4 - 0.2
+    got = O.ternary(O.LERP, x.numpy(), e.numpy(), w.numpy())
+    exact = (x.double() + w.double() * (e.double() - x.double())).numpy()
+    scale = (x.double().abs() + e.double().abs()).numpy()
+    eps = 2.0 ** -24
+    assert np.all(np.abs(got - exact) <= 4 * eps * scale)
+    np.testing.assert_allclose(got, torch.lerp(x, e, w).numpy(), rtol=0, atol=8 * eps * scale.max())
+    # the weight-1 and weight-0 endpoints are exact
+    assert np.array_equal(O.ternary(O.LERP, x.numpy(), e.numpy(), np.ones(20000, np.float32)), e.numpy())
+    assert np.array_equal(O.ternary(O.LERP, x.numpy(), e.numpy(), np.zeros(20000, np.float32)), x.numpy())

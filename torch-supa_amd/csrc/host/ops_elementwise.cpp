@@ -18,6 +18,7 @@
 #include <ATen/ops/view_native.h>
 #include <ATen/ops/_reshape_alias_native.h>
 #include <c10/core/ScalarType.h>
+#include <ATen/native/TypeProperties.h>
 #include <torch/library.h>
 
 #include <stdexcept>
@@ -451,6 +452,218 @@ at::Tensor& div_out_mode(const at::Tensor& s, const at::Tensor& o, std::optional
   return out;
 }
 
+// ------------------------------------------------- maximum / minimum / clamp
+Launch minmax_launch(bool is_max) {
+  return [is_max](const supa_amd_ew_desc* d, void* s) { return supa_amd_minmax(d, is_max ? 1 : 0, s); };
+}
+at::Tensor maximum_t(const at::Tensor& s, const at::Tensor& o) { return binary(s, o, {}, false, minmax_launch(true), "maximum"); }
+at::Tensor& maximum_out(const at::Tensor& s, const at::Tensor& o, at::Tensor& out) {
+  binary(s, o, out, false, minmax_launch(true), "maximum.out");
+  return out;
+}
+at::Tensor minimum_t(const at::Tensor& s, const at::Tensor& o) { return binary(s, o, {}, false, minmax_launch(false), "minimum"); }
+at::Tensor& minimum_out(const at::Tensor& s, const at::Tensor& o, at::Tensor& out) {
+  binary(s, o, out, false, minmax_launch(false), "minimum.out");
+  return out;
+}
+
+// clamp_min / clamp_max against a Scalar or a Tensor bound, with type
+// promotion, as upstream's structured clamp_min / clamp_max.
+at::Tensor clamp_bound(const at::Tensor& self, const c10::Scalar& bound, at::Tensor out, bool inplace, bool is_max_op,
+                       const char* name) {
+  TORCH_CHECK(self.scalar_type() != at::kBool, name, ": not implemented for 'Bool'");
+  const c10::ScalarType common = at::result_type(self, bound);
+  std::vector<EwIn> ins{EwIn::of(self), EwIn::num(bound)};
+  const Launch fn = minmax_launch(is_max_op);
+  if (inplace) {
+    check_cast(common, self, name);
+    return ew_apply(self, self.scalar_type(), common, ins, fn, name);
+  }
+  if (out.defined()) {
+    check_cast(common, out, name);
+    return ew_apply(out, out.scalar_type(), common, ins, fn, name);
+  }
+  return ew_apply(at::Tensor(), common, common, ins, fn, name);
+}
+// clamp_min(x, lo) = max(x, lo); clamp_max(x, hi) = min(x, hi)
+at::Tensor clamp_min_s(const at::Tensor& s, const c10::Scalar& b) { return clamp_bound(s, b, {}, false, true, "clamp_min"); }
+at::Tensor& clamp_min_s_(at::Tensor& s, const c10::Scalar& b) {
+  clamp_bound(s, b, {}, true, true, "clamp_min_");
+  return s;
+}
+at::Tensor& clamp_min_s_out(const at::Tensor& s, const c10::Scalar& b, at::Tensor& out) {
+  clamp_bound(s, b, out, false, true, "clamp_min.out");
+  return out;
+}
+at::Tensor clamp_max_s(const at::Tensor& s, const c10::Scalar& b) { return clamp_bound(s, b, {}, false, false, "clamp_max"); }
+at::Tensor& clamp_max_s_(at::Tensor& s, const c10::Scalar& b) {
+  clamp_bound(s, b, {}, true, false, "clamp_max_");
+  return s;
+}
+at::Tensor& clamp_max_s_out(const at::Tensor& s, const c10::Scalar& b, at::Tensor& out) {
+  clamp_bound(s, b, out, false, false, "clamp_max.out");
+  return out;
+}
+at::Tensor clamp_min_t(const at::Tensor& s, const at::Tensor& b) { return binary(s, b, {}, false, minmax_launch(true), "clamp_min"); }
+at::Tensor& clamp_min_t_(at::Tensor& s, const at::Tensor& b) {
+  binary(s, b, {}, true, minmax_launch(true), "clamp_min_");
+  return s;
+}
+at::Tensor& clamp_min_t_out(const at::Tensor& s, const at::Tensor& b, at::Tensor& out) {
+  binary(s, b, out, false, minmax_launch(true), "clamp_min.Tensor_out");
+  return out;
+}
+at::Tensor clamp_max_t(const at::Tensor& s, const at::Tensor& b) { return binary(s, b, {}, false, minmax_launch(false), "clamp_max"); }
+at::Tensor& clamp_max_t_(at::Tensor& s, const at::Tensor& b) {
+  binary(s, b, {}, true, minmax_launch(false), "clamp_max_");
+  return s;
+}
+at::Tensor& clamp_max_t_out(const at::Tensor& s, const at::Tensor& b, at::Tensor& out) {
+  binary(s, b, out, false, minmax_launch(false), "clamp_max.Tensor_out");
+  return out;
+}
+// clamp(x, lo, hi) = min(max(x, lo), hi): a NaN x stays NaN, and lo > hi gives hi.
+at::Tensor clamp_into(const at::Tensor& self, const std::optional<c10::Scalar>& lo,
+                      const std::optional<c10::Scalar>& hi, at::Tensor dst, bool inplace, const char* name) {
+  TORCH_CHECK(lo.has_value() || hi.has_value(), "torch.clamp: At least one of 'min' or 'max' must not be None");
+  TORCH_CHECK(self.scalar_type() != at::kBool, name, ": not implemented for 'Bool'");
+  at::native::ResultTypeState st = at::native::update_result_type_state(self, {});
+  if (lo) st = at::native::update_result_type_state(*lo, st);
+  if (hi) st = at::native::update_result_type_state(*hi, st);
+  const c10::ScalarType common = at::native::result_type(st);
+  if (dst.defined()) check_cast(common, dst, name);
+  const c10::ScalarType out_dt = dst.defined() ? dst.scalar_type() : common;
+  if (lo && hi) {
+    at::Tensor tmp = ew_apply(at::Tensor(), common, common, {EwIn::of(self), EwIn::num(*lo)}, minmax_launch(true), name);
+    return ew_apply(dst, out_dt, common, {EwIn::of(tmp), EwIn::num(*hi)}, minmax_launch(false), name);
+  }
+  return ew_apply(dst, out_dt, common, {EwIn::of(self), EwIn::num(lo ? *lo : *hi)}, minmax_launch(lo.has_value()),
+                  name);
+}
+at::Tensor clamp_s(const at::Tensor& s, const std::optional<c10::Scalar>& lo, const std::optional<c10::Scalar>& hi) {
+  return clamp_into(s, lo, hi, at::Tensor(), false, "clamp");
+}
+at::Tensor& clamp_s_(at::Tensor& s, const std::optional<c10::Scalar>& lo, const std::optional<c10::Scalar>& hi) {
+  clamp_into(s, lo, hi, s, true, "clamp_");
+  return s;
+}
+at::Tensor& clamp_s_out(const at::Tensor& s, const std::optional<c10::Scalar>& lo, const std::optional<c10::Scalar>& hi,
+                        at::Tensor& out) {
+  clamp_into(s, lo, hi, out, false, "clamp.out");
+  return out;
+}
+
+// ---------------------------------------------- addcmul / addcdiv / lerp
+Launch pointwise_launch(int op, const c10::Scalar& value) {
+  double a = 0.0;
+  int64_t ia = 0;
+  if (value.isBoolean()) {
+    a = value.toBool() ? 1.0 : 0.0;
+    ia = value.toBool() ? 1 : 0;
+  } else if (value.isIntegral(false)) {
+    ia = value.toLong();
+    a = (double)ia;
+  } else {
+    a = value.toDouble();
+    ia = (int64_t)a;
+  }
+  return [op, a, ia](const supa_amd_ew_desc* d, void* s) { return supa_amd_pointwise(d, op, a, ia, s); };
+}
+
+at::Tensor ternary(const at::Tensor& self, const EwIn& b, const EwIn& c, c10::ScalarType common, at::Tensor out,
+                   bool inplace, const Launch& fn, const char* name) {
+  std::vector<EwIn> ins{EwIn::of(self), b, c};
+  if (inplace) {
+    check_cast(common, self, name);
+    return ew_apply(self, self.scalar_type(), common, ins, fn, name);
+  }
+  if (out.defined()) {
+    check_cast(common, out, name);
+    return ew_apply(out, out.scalar_type(), common, ins, fn, name);
+  }
+  return ew_apply(at::Tensor(), common, common, ins, fn, name);
+}
+
+c10::ScalarType addc_common(const at::Tensor& self, const at::Tensor& t1, const at::Tensor& t2, bool div,
+                            const char* name) {
+  at::native::ResultTypeState st{};
+  for (const at::Tensor* t : {&self, &t1, &t2}) st = at::native::update_result_type_state(*t, st);
+  const c10::ScalarType common = at::native::result_type(st);
+  if (div)
+    TORCH_CHECK(!(at::isIntegralType(t1.scalar_type(), true) && at::isIntegralType(t2.scalar_type(), true)),
+                "Integer division with addcdiv is no longer supported, and in a future release addcdiv will perform a "
+                "true division of tensor1 and tensor2. The historic addcdiv behavior can be implemented as "
+                "(input + value * torch.trunc(tensor1 / tensor2)).to(input.dtype) for integer inputs and as "
+                "(input + value * tensor1 / tensor2) for float inputs. The future addcdiv behavior is just the "
+                "latter implementation: (input + value * tensor1 / tensor2), for all dtypes.");
+  (void)name;
+  return common;
+}
+
+#define SUPA_ADDC(NAME, OP, DIV)                                                                                  \
+  at::Tensor NAME(const at::Tensor& s, const at::Tensor& t1, const at::Tensor& t2, const c10::Scalar& v) {        \
+    return ternary(s, EwIn::of(t1), EwIn::of(t2), addc_common(s, t1, t2, DIV, #NAME), {}, false,                   \
+                   pointwise_launch(OP, v), #NAME);                                                                \
+  }                                                                                                                \
+  at::Tensor& NAME##_(at::Tensor& s, const at::Tensor& t1, const at::Tensor& t2, const c10::Scalar& v) {          \
+    ternary(s, EwIn::of(t1), EwIn::of(t2), addc_common(s, t1, t2, DIV, #NAME), {}, true, pointwise_launch(OP, v),  \
+            #NAME "_");                                                                                            \
+    return s;                                                                                                      \
+  }                                                                                                                \
+  at::Tensor& NAME##_out(const at::Tensor& s, const at::Tensor& t1, const at::Tensor& t2, const c10::Scalar& v,   \
+                         at::Tensor& out) {                                                                        \
+    ternary(s, EwIn::of(t1), EwIn::of(t2), addc_common(s, t1, t2, DIV, #NAME), out, false,                         \
+            pointwise_launch(OP, v), #NAME ".out");                                                                \
+    return out;                                                                                                    \
+  }
+SUPA_ADDC(addcmul, SUPA_AMD_ADDCMUL, false)
+SUPA_ADDC(addcdiv, SUPA_AMD_ADDCDIV, true)
+#undef SUPA_ADDC
+
+void lerp_checks(const at::Tensor& self, const at::Tensor& end, const at::Tensor* weight) {
+  TORCH_CHECK(self.scalar_type() == end.scalar_type(), "expected dtype ", self.scalar_type(),
+              " for `end` but got dtype ", end.scalar_type());
+  if (weight)
+    TORCH_CHECK(self.scalar_type() == weight->scalar_type(), "expected dtype ", self.scalar_type(),
+                " for `weight` but got dtype ", weight->scalar_type());
+  TORCH_CHECK(at::isFloatingType(self.scalar_type()), "lerp: expected a floating-point input, got ",
+              self.scalar_type());
+}
+const Launch& lerp_launch() {
+  static const Launch fn = [](const supa_amd_ew_desc* d, void* s) {
+    return supa_amd_pointwise(d, SUPA_AMD_LERP, 0.0, 0, s);
+  };
+  return fn;
+}
+at::Tensor lerp_s(const at::Tensor& s, const at::Tensor& e, const c10::Scalar& w) {
+  lerp_checks(s, e, nullptr);
+  return ternary(s, EwIn::of(e), EwIn::num(w), s.scalar_type(), {}, false, lerp_launch(), "lerp");
+}
+at::Tensor& lerp_s_(at::Tensor& s, const at::Tensor& e, const c10::Scalar& w) {
+  lerp_checks(s, e, nullptr);
+  ternary(s, EwIn::of(e), EwIn::num(w), s.scalar_type(), {}, true, lerp_launch(), "lerp_");
+  return s;
+}
+at::Tensor& lerp_s_out(const at::Tensor& s, const at::Tensor& e, const c10::Scalar& w, at::Tensor& out) {
+  lerp_checks(s, e, nullptr);
+  ternary(s, EwIn::of(e), EwIn::num(w), s.scalar_type(), out, false, lerp_launch(), "lerp.Scalar_out");
+  return out;
+}
+at::Tensor lerp_t(const at::Tensor& s, const at::Tensor& e, const at::Tensor& w) {
+  lerp_checks(s, e, &w);
+  return ternary(s, EwIn::of(e), EwIn::of(w), s.scalar_type(), {}, false, lerp_launch(), "lerp");
+}
+at::Tensor& lerp_t_(at::Tensor& s, const at::Tensor& e, const at::Tensor& w) {
+  lerp_checks(s, e, &w);
+  ternary(s, EwIn::of(e), EwIn::of(w), s.scalar_type(), {}, true, lerp_launch(), "lerp_");
+  return s;
+}
+at::Tensor& lerp_t_out(const at::Tensor& s, const at::Tensor& e, const at::Tensor& w, at::Tensor& out) {
+  lerp_checks(s, e, &w);
+  ternary(s, EwIn::of(e), EwIn::of(w), s.scalar_type(), out, false, lerp_launch(), "lerp.Tensor_out");
+  return out;
+}
+
 // ---------------------------------------------------------- activations
 enum class UKind { FloatOnly, IntToFloat, Any };
 
@@ -595,6 +808,37 @@ TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
   m.impl("div_.Tensor_mode", TORCH_FN(div_tm_));
   m.impl("div.out_mode", TORCH_FN(div_out_mode));
   // activations
+  m.impl("maximum", TORCH_FN(maximum_t));
+  m.impl("maximum.out", TORCH_FN(maximum_out));
+  m.impl("minimum", TORCH_FN(minimum_t));
+  m.impl("minimum.out", TORCH_FN(minimum_out));
+  m.impl("clamp_min", TORCH_FN(clamp_min_s));
+  m.impl("clamp_min_", TORCH_FN(clamp_min_s_));
+  m.impl("clamp_min.out", TORCH_FN(clamp_min_s_out));
+  m.impl("clamp_min.Tensor", TORCH_FN(clamp_min_t));
+  m.impl("clamp_min_.Tensor", TORCH_FN(clamp_min_t_));
+  m.impl("clamp_min.Tensor_out", TORCH_FN(clamp_min_t_out));
+  m.impl("clamp_max", TORCH_FN(clamp_max_s));
+  m.impl("clamp_max_", TORCH_FN(clamp_max_s_));
+  m.impl("clamp_max.out", TORCH_FN(clamp_max_s_out));
+  m.impl("clamp_max.Tensor", TORCH_FN(clamp_max_t));
+  m.impl("clamp_max_.Tensor", TORCH_FN(clamp_max_t_));
+  m.impl("clamp_max.Tensor_out", TORCH_FN(clamp_max_t_out));
+  m.impl("clamp", TORCH_FN(clamp_s));
+  m.impl("clamp_", TORCH_FN(clamp_s_));
+  m.impl("clamp.out", TORCH_FN(clamp_s_out));
+  m.impl("addcmul", TORCH_FN(addcmul));
+  m.impl("addcmul_", TORCH_FN(addcmul_));
+  m.impl("addcmul.out", TORCH_FN(addcmul_out));
+  m.impl("addcdiv", TORCH_FN(addcdiv));
+  m.impl("addcdiv_", TORCH_FN(addcdiv_));
+  m.impl("addcdiv.out", TORCH_FN(addcdiv_out));
+  m.impl("lerp.Scalar", TORCH_FN(lerp_s));
+  m.impl("lerp_.Scalar", TORCH_FN(lerp_s_));
+  m.impl("lerp.Scalar_out", TORCH_FN(lerp_s_out));
+  m.impl("lerp.Tensor", TORCH_FN(lerp_t));
+  m.impl("lerp_.Tensor", TORCH_FN(lerp_t_));
+  m.impl("lerp.Tensor_out", TORCH_FN(lerp_t_out));
   m.impl("gelu", TORCH_FN(gelu));
   m.impl("gelu_", TORCH_FN(gelu_));
   m.impl("gelu.out", TORCH_FN(gelu_out));

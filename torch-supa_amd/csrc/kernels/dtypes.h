@@ -32,6 +32,14 @@ __device__ __forceinline__ bf16 f32_to_bf16(float f) {
   h.x = (f != f) ? (uint16_t)0x7FC0u : __builtin_bit_cast(uint16_t, hw);
   return h;
 }
+// Round a float result to f16.  The empty asm pins the value as a float32
+// first: without it the compiler folds a producing fma into v_fma_mixlo_f16,
+// which rounds the exact product-sum once to f16, while the upstream kernels
+// round it to float and then to half (about 1 result in 10^4 differs).
+__device__ __forceinline__ f16 f32_to_f16(float f) {
+  __asm__("" : "+v"(f));
+  return static_cast<f16>(f);
+}
 
 // opmath: the type an op computes in for a given storage type.
 template <typename T> struct opmath { using type = T; };
@@ -62,7 +70,7 @@ template <> struct FromArith<bf16> {
   template <typename A> __device__ __forceinline__ static bf16 f(A v) { return f32_to_bf16(static_cast<float>(v)); }
 };
 template <> struct FromArith<f16> {
-  template <typename A> __device__ __forceinline__ static f16 f(A v) { return static_cast<f16>(static_cast<float>(v)); }
+  template <typename A> __device__ __forceinline__ static f16 f(A v) { return f32_to_f16(static_cast<float>(v)); }
 };
 template <> struct FromArith<b8> {
   template <typename A> __device__ __forceinline__ static b8 f(A v) {
@@ -143,7 +151,7 @@ __device__ __forceinline__ C round_to_dtype(C v, int dtype) {
   switch (dtype) {
     case SUPA_AMD_F32: return static_cast<C>(static_cast<float>(v));
     case SUPA_AMD_BF16: return static_cast<C>(bf16_to_f32(f32_to_bf16(static_cast<float>(v))));
-    case SUPA_AMD_F16: return static_cast<C>(static_cast<float>(static_cast<f16>(static_cast<float>(v))));
+    case SUPA_AMD_F16: return static_cast<C>(static_cast<float>(f32_to_f16(static_cast<float>(v))));
     case SUPA_AMD_F64: return static_cast<C>(static_cast<double>(v));
     case SUPA_AMD_I64: return static_cast<C>(static_cast<int64_t>(v));
     case SUPA_AMD_I32: return static_cast<C>(static_cast<int32_t>(v));
@@ -159,7 +167,7 @@ __device__ __forceinline__ void store_dyn(void* p, int64_t off, int dtype, C v) 
   switch (dtype) {
     case SUPA_AMD_F32: static_cast<float*>(p)[off] = static_cast<float>(v); break;
     case SUPA_AMD_BF16: static_cast<bf16*>(p)[off] = f32_to_bf16(static_cast<float>(v)); break;
-    case SUPA_AMD_F16: static_cast<f16*>(p)[off] = static_cast<f16>(static_cast<float>(v)); break;
+    case SUPA_AMD_F16: static_cast<f16*>(p)[off] = f32_to_f16(static_cast<float>(v)); break;
     case SUPA_AMD_F64: static_cast<double*>(p)[off] = static_cast<double>(v); break;
     case SUPA_AMD_I64: static_cast<int64_t*>(p)[off] = static_cast<int64_t>(v); break;
     case SUPA_AMD_I32: static_cast<int32_t*>(p)[off] = static_cast<int32_t>(v); break;

@@ -54,6 +54,18 @@ struct SmoothL1BwdFactory {
   }
 };
 
+template <template <typename> class Op, bool FloatOnly = false>
+struct ValueFactory {  // ternary ops with one bound value (addcmul, addcdiv)
+  double value;
+  int64_t ivalue;
+  template <typename C> static constexpr bool ok() { return !FloatOnly || std::is_floating_point<C>::value; }
+  template <typename C> Op<C> make() const {
+    if constexpr (std::is_floating_point<C>::value) return Op<C>{static_cast<C>(value)};
+    else if constexpr (std::is_same<C, bool>::value) return Op<C>{ivalue != 0 || value != 0.0};
+    else return Op<C>{static_cast<C>(ivalue)};
+  }
+};
+
 template <bool PW, bool W>
 struct BceBwdFactory {
   double n;

@@ -208,6 +208,59 @@ template <int K, typename C> struct UnaryBwdOp {
   }
 };
 
+// ------------------------------------------------------------ ternary
+// addcmul / addcdiv: self + value * (t1 op t2), the reference's CUDA
+// functors (PointwiseOpsKernel.cu; ForeachPointwiseOp.cu) with `a + v * x`
+// contracted into one fma as its compiler does.  inputs: self, t1, t2.
+template <typename C> struct AddcmulOp {
+  static constexpr int arity = 3;
+  C value;
+  __device__ __forceinline__ C operator()(const C* x) const {
+    if constexpr (std::is_same<C, bool>::value) return x[0] || (value && x[1] && x[2]);
+    else return muladd<C>(value, (C)(x[1] * x[2]), x[0]);
+  }
+};
+template <typename C> struct AddcdivOp {
+  static constexpr int arity = 3;
+  C value;
+  __device__ __forceinline__ C operator()(const C* x) const { return muladd<C>(value, x[1] / x[2], x[0]); }
+};
+// lerp (upstream Lerp.h): |w| < 0.5 ? self + w (end - self)
+// : end - (end - self)(1 - w), each product-sum one fma.  inputs: self, end, w.
+template <typename C> struct LerpOp {
+  static constexpr int arity = 3;
+  __device__ __forceinline__ C operator()(const C* x) const {
+    const C a = x[0], e = x[1], w = x[2];
+    const C d = e - a;
+    return fabs(w) < C(0.5) ? muladd<C>(w, d, a) : muladd<C>(-d, C(1) - w, e);
+  }
+};
+
+// maximum / minimum: a NaN in either operand is the result (upstream
+// maximum / minimum kernels); also clamp_min / clamp_max with a bound.
+template <typename C> struct MaxOp {
+  static constexpr int arity = 2;
+  __device__ __forceinline__ C operator()(const C* x) const {
+    const C a = x[0], b = x[1];
+    if constexpr (std::is_floating_point<C>::value) {
+      if (a != a) return a;
+      if (b != b) return b;
+    }
+    return a > b ? a : b;
+  }
+};
+template <typename C> struct MinOp {
+  static constexpr int arity = 2;
+  __device__ __forceinline__ C operator()(const C* x) const {
+    const C a = x[0], b = x[1];
+    if constexpr (std::is_floating_point<C>::value) {
+      if (a != a) return a;
+      if (b != b) return b;
+    }
+    return a < b ? a : b;
+  }
+};
+
 // ------------------------------------------------------------ copy/fill
 template <typename C> struct IdentityOp {
   static constexpr int arity = 1;
@@ -269,7 +322,7 @@ template <bool PW, bool W, typename C> struct BceBwdOp {
   __device__ __forceinline__ C rnd(C v) const {
     if constexpr (std::is_same<C, float>::value) {
       if (rt == 1) return bf16_to_f32(f32_to_bf16(v));
-      if (rt == 2) return (float)(f16)v;
+      if (rt == 2) return (float)f32_to_f16(v);
     }
     return v;
   }
