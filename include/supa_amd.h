@@ -309,18 +309,62 @@ int supa_amd_cross_entropy_backward(const void* grad_out, const void* logits, in
                                     int32_t* error_flag, void* stream);
 
 /* ------------------------------------------------- multi-tensor apply */
-#define SUPA_AMD_FOREACH_ADD 0   /* out = a + alpha * b  (b list or scalar) */
-#define SUPA_AMD_FOREACH_MUL 1   /* out = a * b          (b list or scalar) */
+#define SUPA_AMD_FOREACH_ADD 0      /* out = a + alpha * y                    */
+#define SUPA_AMD_FOREACH_MUL 1      /* out = a * y                            */
+#define SUPA_AMD_FOREACH_DIV 2      /* out = a / y                            */
+#define SUPA_AMD_FOREACH_MAXIMUM 3  /* out = max(a, y), a NaN in either wins  */
+#define SUPA_AMD_FOREACH_MINIMUM 4  /* out = min(a, y), a NaN in either wins  */
+#define SUPA_AMD_FOREACH_ADDCMUL 5  /* out = a + s * (b * c)                  */
+#define SUPA_AMD_FOREACH_ADDCDIV 6  /* out = a + s * (b / c)                  */
+#define SUPA_AMD_FOREACH_LERP 7     /* out = lerp(a, b, w)                    */
+#define SUPA_AMD_FOREACH_ZERO 8     /* out = 0                                */
+#define SUPA_AMD_FOREACH_UNARY 32   /* + SUPA_AMD_SIGMOID, _TANH, _EXP, _LOG, _ERF,
+                                       _NEG, _RECIPROCAL, _ABS, _SQRT: out = f(a) */
+/* Where y (lerp: the weight w) comes from: */
+#define SUPA_AMD_FOREACH_LIST 0       /* y = b[k][i]; lerp w = c[k][i]            */
+#define SUPA_AMD_FOREACH_SCALARS 1    /* y = scalars[k] (a Scalar repeats)        */
+#define SUPA_AMD_FOREACH_DEVSCALAR 2  /* y = *scalar_ptr, one device element of `dtype` */
 
 /* In-place or out-of-place list arithmetic over `ntensors` contiguous tensors
- * of one dtype.  b == NULL selects the scalar overload (value `scalar`).
- * out may equal a (the in-place overloads).  Replaces _foreach_add_.List
+ * of one dtype (f32 / bf16 / f16 / f64), computed in float (double for f64)
+ * exactly as the elementwise entry points do, so every output equals the
+ * per-tensor op bit for bit.  out may equal a (the in-place overloads).
+ * addcmul / addcdiv take their value from scalars[k] whatever `form` says;
+ * the unary ops and ZERO ignore `form`.  One launch covers up to 40 tensors.
+ * Replaces the fast paths of upstream ForeachBinaryOpList.cu,
+ * ForeachBinaryOpScalar.cu, ForeachBinaryOpScalarList.cu,
+ * ForeachBinaryOpScalarTensor.cu, ForeachPointwiseOp.cu, ForeachTernaryOp.cu
+ * and ForeachUnaryOp.cu that the reference registers through its codegen
+ * (script/codegen_supa/gen.py:1708-1734): _foreach_add_.Tensor NF:10716,
+ * _foreach_sub_ NF:10732-10762, _foreach_mul_.Tensor NF:10826, _foreach_div_
+ * NF:10842-10890, _foreach_clamp_max_ / _clamp_min_ NF:10906-10981,
+ * _foreach_maximum_ / _minimum_ NF:10997-11075, _foreach_addcdiv_
+ * NF:11104-11120, _foreach_addcmul_ NF:11150-11167, _foreach_lerp_
+ * NF:11380-11412, _foreach_sqrt_ NF:11691, _foreach_zero_ NF:11745, the
+ * other unary ops listed above, and the out-of-place forms. */
+int supa_amd_foreach(int op, int form, int32_t ntensors, void* const* out, const void* const* a,
+                     const void* const* b, const void* const* c, const int64_t* numel, int32_t dtype,
+                     const double* scalars, double alpha, const void* scalar_ptr, void* stream);
+
+/* The add / mul subset with one scalar for every tensor; b == NULL selects
+ * the scalar overload (value `scalar`).  Replaces _foreach_add_.List
  * NF:10685, _foreach_add_.Scalar NF:10668, _foreach_mul_.List NF:10794,
- * _foreach_mul_.Scalar NF:10777 and their out-of-place forms (upstream
- * ForeachBinaryOp*.cu over MultiTensorApply.cuh). */
+ * _foreach_mul_.Scalar NF:10777 and their out-of-place forms. */
 int supa_amd_foreach_binary(int op, int32_t ntensors, void* const* out, void* const* a,
                             void* const* b, const int64_t* numel, int32_t dtype, double scalar,
                             double alpha, void* stream);
+
+/* Per-tensor vector norms: out[k] = ||x[k]||_ord for ord 1, 2 or +inf
+ * (HUGE_VAL), accumulated in float (double for f64 inputs) per chunk and
+ * combined per tensor in a second kernel; an empty tensor gives 0, a NaN
+ * anywhere gives NaN.  out: `ntensors` contiguous elements of out_dtype
+ * (the input dtype, f32 or f64).  The workspace holds one partial per chunk:
+ * supa_amd_foreach_norm_workspace_bytes, no content requirement.  Replaces
+ * _foreach_norm.Scalar NF:11518 (upstream ForeachReduceOp.cu). */
+int64_t supa_amd_foreach_norm_workspace_bytes(int32_t ntensors, const int64_t* numel, int32_t dtype);
+int supa_amd_foreach_norm(int32_t ntensors, const void* const* x, const int64_t* numel, int32_t dtype,
+                          double ord, void* out, int32_t out_dtype, void* workspace, int64_t ws_bytes,
+                          void* stream);
 
 /* Mixed-precision gradient unscale: every element of the `ntensors`
  * contiguous tensors (f32 / bf16 / f16 / f64) is multiplied in place by

@@ -317,3 +317,21 @@ def adamw_step(p, g, m, v, step, lr, beta1, beta2, weight_decay, eps, maximize=F
     lib().or_adamw_step(_p(p, _f32p), _p(g, _f32p), _p(m, _f32p), _p(v, _f32p), p.size,
                         float(step), lr, beta1, beta2, weight_decay, eps, 1 if maximize else 0,
                         _p(gs, _f32p), 1 if amsgrad else 0, _p(vmax, _f32p))
+
+
+def vector_norm(x, ord=2.0) -> float:
+    """||x||_ord for ord 1, 2 or inf, accumulated in float64: the quantity
+    upstream's _foreach_norm (ForeachReduceOp.cu) and linalg_vector_norm
+    (ReduceNormKernel) estimate in float.  A NaN anywhere gives NaN and an
+    empty x gives 0."""
+    x = np.asarray(x, dtype=np.float64).ravel()
+    if x.size == 0:
+        return 0.0
+    a = np.abs(x)
+    if ord == 1:
+        return float(a.sum())
+    if ord == 2:
+        return float(np.sqrt((a * a).sum()))
+    if ord == float("inf"):
+        return float("nan") if np.isnan(a).any() else float(a.max())
+    raise ValueError(f"ord {ord} not supported")

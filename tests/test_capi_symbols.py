@@ -60,3 +60,21 @@ def test_argument_errors_need_no_device(lib):
                                               None, i64(0), None, None) == -4
     assert lib.supa_amd_cross_entropy_backward(None, fake, 6, fake, fake, fake, i64(4), i64(10), i64(-100), 1,
                                                fake, None, None) == -1
+
+
+def test_foreach_argument_errors(lib):
+    i64 = ctypes.c_int64
+    lib.supa_amd_foreach_norm_workspace_bytes.restype = i64
+    numel = (i64 * 3)(1000, 0, 5000)  # f32: 2048-element chunks -> 1 + 0 + 3 partials of 4 bytes
+    assert lib.supa_amd_foreach_norm_workspace_bytes(3, numel, 6) == 16
+    assert lib.supa_amd_foreach_norm_workspace_bytes(3, numel, 4) == -2  # int64: no kernel
+    fake = (ctypes.c_void_p * 3)(256, 256, 256)
+    # ord 3 is not a fast-path norm; a missing workspace is reported before any launch
+    assert lib.supa_amd_foreach_norm(3, fake, numel, 6, ctypes.c_double(3.0), fake, 6, None, i64(0), None) == -1
+    assert lib.supa_amd_foreach_norm(3, fake, numel, 6, ctypes.c_double(2.0), fake, 6, None, i64(0), None) == -4
+    # bad form; a ScalarList form without scalars; lerp from a device scalar
+    d0 = ctypes.c_double(0.0)
+    assert lib.supa_amd_foreach(0, 7, 3, fake, fake, fake, None, numel, 6, None, d0, None, None) == -1
+    assert lib.supa_amd_foreach(2, 1, 3, fake, fake, None, None, numel, 6, None, d0, None, None) == -1
+    assert lib.supa_amd_foreach(7, 2, 3, fake, fake, fake, None, numel, 6, None, d0, fake, None) == -1
+    assert lib.supa_amd_foreach(99, 1, 3, fake, fake, None, None, numel, 6, None, d0, None, None) == -1

@@ -1,0 +1,250 @@
+"""The _foreach_* family on the supa device: every fast-path form (List,
+Scalar, ScalarList, Tensor; pointwise ternary; unary; zero_; norm) is one
+multi-tensor launch whose results equal the oracle's elementwise arithmetic
+bit for bit (f32; bf16 is the f32 result rounded once), and the default
+torch.optim.AdamW (the foreach implementation) and clip_grad_norm_ run on it
+with the CPU fallback disabled."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+# ragged sizes: a partial last vector, a tensor smaller than one vector, and
+# one that spans many chunks
+SHAPES = [(4096 * 257 + 3,), (1000, 33), (5,), (64, 1024)]
+
+
+def lists(seed, dtype=torch.float32, positive=False, n=len(SHAPES)):
+    g = torch.Generator().manual_seed(seed)
+    out = []
+    for s in SHAPES[:n]:
+        t = torch.randn(s, generator=g) * 2
+        if positive:
+            t = t.abs() + 0.25
+        out.append(t.to(dtype))
+    return out
+
+
+def dev(ts):
+    return [t.to("supa") for t in ts]
+
+
+def f32(t):
+    return t.float().numpy()
+
+
+def want(arr, dtype):
+    return torch.from_numpy(np.ascontiguousarray(arr)).to(dtype)
+
+
+def same(got, ref):
+    torch.testing.assert_close(got.cpu(), ref, rtol=0, atol=0, equal_nan=True)
+
+
+BINARY = [  # (foreach name, oracle op, in-place name)
+    ("add", O.ADD), ("sub", O.ADD), ("mul", O.MUL), ("div", O.DIV),
+    ("maximum", O.MAXIMUM), ("minimum", O.MINIMUM), ("clamp_min", O.MAXIMUM), ("clamp_max", O.MINIMUM),
+]
+
+
+def oracle_binary(name, op, a, b, alpha=1.0):
+    """The per-element oracle of one binary foreach op; sub is add of -y."""
+    if not isinstance(b, np.ndarray):
+        b = np.float32(b)
+    if name == "sub":
+        if b.ndim:
+            return O.binary(O.ADD, a, b, -alpha)
+        return O.binary(O.ADD, a, -b)
+    return O.binary(op, a, b, alpha)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("name,op", BINARY)
+def test_binary_forms(name, op, dtype, no_fallback):
+    xs, ys = lists(1, dtype), lists(2, dtype, positive=(name == "div"))
+    dxs, dys = dev(xs), dev(ys)
+    fn = getattr(torch, f"_foreach_{name}")
+    fn_ = getattr(torch, f"_foreach_{name}_")
+    # List (add / sub with alpha)
+    kw = {"alpha": 0.5} if name in ("add", "sub") else {}
+    for o, x, y in zip(fn(dxs, dys, **kw), xs, ys):
+        same(o, want(oracle_binary(name, op, f32(x), f32(y), kw.get("alpha", 1.0)), dtype))
+    # Scalar and ScalarList
+    for o, x in zip(fn(dxs, 0.75), xs):
+        same(o, want(oracle_binary(name, op, f32(x), 0.75), dtype))
+    sl = [0.5, -1.25, 3.0, 0.1]
+    for o, x, s in zip(fn(dxs, sl), xs, sl):
+        same(o, want(oracle_binary(name, op, f32(x), s), dtype))
+    # in place, then a second op on the result
+    work = [t.clone() for t in dxs]
+    fn_(work, dys, **kw)
+    fn_(work, sl)
+    for w, x, y, s in zip(work, xs, ys, sl):
+        r = want(oracle_binary(name, op, f32(x), f32(y), kw.get("alpha", 1.0)), dtype)
+        same(w, want(oracle_binary(name, op, f32(r), s), dtype))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("name,op", [("add", O.ADD), ("mul", O.MUL), ("div", O.DIV)])
+def test_binary_tensor_form(name, op, dtype, no_fallback):
+    """A 0-dim device tensor as the second operand (clip_grad_norm_'s
+    `_foreach_mul_(grads, clip_coef)`), cast to the list dtype first."""
+    xs = lists(3, dtype)
+    dxs = dev(xs)
+    other = torch.tensor(0.3, dtype=torch.float32)
+    s = float(other.to(dtype).float())
+    fn = getattr(torch, f"_foreach_{name}")
+    kw = {"alpha": 2.0} if name == "add" else {}
+    for o, x in zip(fn(dxs, other.to("supa"), **kw), xs):
+        if name == "add":
+            ref = O.binary(O.ADD, f32(x), np.full(x.shape, s, np.float32), 2.0)
+        else:
+            ref = O.binary(op, f32(x), np.float32(s))
+        same(o, want(ref, dtype))
+    work = [t.clone() for t in dxs]
+    getattr(torch, f"_foreach_{name}_")(work, other.to("supa"), **kw)
+    for w, o in zip(work, fn(dxs, other.to("supa"), **kw)):
+        same(w, o.cpu())
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_pointwise_forms(dtype, no_fallback):
+    xs, ys, zs = lists(4, dtype), lists(5, dtype), lists(6, dtype, positive=True)
+    ws = [(torch.rand(s, generator=torch.Generator().manual_seed(7)) * 1.4 - 0.2).to(dtype) for s in SHAPES]
+    dxs, dys, dzs, dws = dev(xs), dev(ys), dev(zs), dev(ws)
+    sl = [0.5, -1.25, 3.0, 0.1]
+    for name, op in (("addcmul", O.ADDCMUL), ("addcdiv", O.ADDCDIV)):
+        fn = getattr(torch, f"_foreach_{name}")
+        for o, x, y, z in zip(fn(dxs, dys, dzs, value=-0.37), xs, ys, zs):
+            same(o, want(O.ternary(op, f32(x), f32(y), f32(z), -0.37), dtype))
+        for o, x, y, z, s in zip(fn(dxs, dys, dzs, sl), xs, ys, zs, sl):
+            same(o, want(O.ternary(op, f32(x), f32(y), f32(z), s), dtype))
+        for o, x, y, z, s in zip(fn(dxs, dys, dzs, torch.tensor(sl)), xs, ys, zs, sl):  # Tensor of scalars
+            same(o, want(O.ternary(op, f32(x), f32(y), f32(z), s), dtype))
+        work = [t.clone() for t in dxs]
+        getattr(torch, f"_foreach_{name}_")(work, dys, dzs, sl)
+        for w, x, y, z, s in zip(work, xs, ys, zs, sl):
+            same(w, want(O.ternary(op, f32(x), f32(y), f32(z), s), dtype))
+    for o, x, y, w in zip(torch._foreach_lerp(dxs, dys, dws), xs, ys, ws):
+        same(o, want(O.ternary(O.LERP, f32(x), f32(y), f32(w)), dtype))
+    for o, x, y in zip(torch._foreach_lerp(dxs, dys, 0.1), xs, ys):
+        same(o, want(O.ternary(O.LERP, f32(x), f32(y), np.full(x.shape, 0.1, np.float32)), dtype))
+    work = [t.clone() for t in dxs]
+    torch._foreach_lerp_(work, dys, sl)
+    for w, x, y, s in zip(work, xs, ys, sl):
+        same(w, want(O.ternary(O.LERP, f32(x), f32(y), np.full(x.shape, s, np.float32)), dtype))
+
+
+UNARY = [("sigmoid", O.SIGMOID), ("tanh", O.TANH), ("exp", O.EXP), ("log", O.LOG), ("erf", O.ERF),
+         ("neg", O.NEG), ("reciprocal", O.RECIPROCAL), ("abs", O.ABS), ("sqrt", O.SQRT)]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_unary_and_zero(dtype, no_fallback):
+    xs = lists(8, dtype)
+    pos = [t.abs() + 0.01 for t in xs]
+    for name, op in UNARY:
+        src = pos if name in ("log", "sqrt") else xs
+        d = dev(src)
+        for o, x in zip(getattr(torch, f"_foreach_{name}")(d), src):
+            same(o, want(O.unary(op, f32(x)), dtype))
+        getattr(torch, f"_foreach_{name}_")(d)
+        for o, x in zip(d, src):
+            same(o, want(O.unary(op, f32(x)), dtype))
+    d = dev(xs)
+    torch._foreach_zero_(d)
+    for t in d:
+        assert not t.cpu().any()
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_norm(dtype, no_fallback):
+    xs = lists(9, dtype) + [torch.zeros(0, dtype=dtype), torch.full((3000,), 0.5, dtype=dtype)]
+    d = dev(xs)
+    rtol = 1e-5 if dtype == torch.float32 else 1e-2
+    for p in (1, 2, math.inf):
+        norms = torch._foreach_norm(d, p)
+        assert len(norms) == len(xs)
+        for nm, x in zip(norms, xs):
+            assert nm.dim() == 0 and nm.dtype == dtype
+            ref = O.vector_norm(x.double().numpy(), p)
+            if p == math.inf:  # the largest |x| is exact
+                assert nm.item() == ref
+            else:
+                assert nm.item() == pytest.approx(ref, rel=rtol, abs=0)
+        assert norms[-2].item() == 0.0
+    # an f32 result for bf16 inputs, as with dtype=
+    if dtype == torch.bfloat16:
+        for nm, x in zip(torch._foreach_norm(d, 2, dtype=torch.float32), xs):
+            assert nm.dtype == torch.float32
+            assert nm.item() == pytest.approx(O.vector_norm(x.double().numpy(), 2), rel=1e-5)
+    # NaN propagates
+    bad = [t.clone() for t in d[:2]]
+    bad[1][3] = float("nan")
+    out = torch._foreach_norm(bad, 2)
+    assert not math.isnan(out[0].item()) and math.isnan(out[1].item())
+
+
+def test_many_tensors_span_launches(no_fallback):
+    """More tensors than one launch's table (40), with empty ones mixed in."""
+    g = torch.Generator().manual_seed(10)
+    xs = [torch.randn(int(n), generator=g) for n in torch.randint(0, 3000, (97,), generator=g)]
+    xs[5] = torch.zeros(0)
+    d = dev(xs)
+    torch._foreach_mul_(d, 1.5)
+    torch._foreach_add_(d, d, alpha=-0.25)
+    for t, x in zip(d, xs):
+        r = O.binary(O.MUL, x.numpy(), np.float32(1.5))
+        same(t, torch.from_numpy(O.binary(O.ADD, r, r, -0.25)))
+    norms = torch._foreach_norm(d)
+    for nm, t in zip(norms, d):
+        assert nm.item() == pytest.approx(O.vector_norm(t.cpu().double().numpy(), 2), rel=1e-5)
+
+
+def test_slow_path_matches_per_tensor(no_fallback):
+    """Non-contiguous members and mixed dtypes take the per-tensor path."""
+    x = torch.randn(64, 96)
+    y = torch.randn(96, 64)
+    dx, dy = x.to("supa"), y.to("supa")
+    out = torch._foreach_add([dx.t(), dx], [dy, dy.t()], alpha=2.0)
+    same(out[0], torch.add(x.t(), y, alpha=2.0))
+    same(out[1], torch.add(x, y.t(), alpha=2.0))
+    mixed = torch._foreach_mul([dx, dy.to(torch.bfloat16)], 0.5)
+    assert mixed[1].dtype == torch.bfloat16
+    same(mixed[0], x * 0.5)
+
+
+@pytest.mark.parametrize("amsgrad", [False, True])
+def test_default_adamw_is_foreach_and_matches_single_tensor(amsgrad, no_fallback):
+    """torch.optim.AdamW's default (foreach) implementation on supa: every
+    list op is native, and the parameters equal the single-tensor
+    implementation's (the same ops one tensor at a time) bit for bit."""
+    g = torch.Generator().manual_seed(11)
+    shapes = [(1024, 257), (257,), (33, 7)]
+    init = [torch.randn(s, generator=g) * 0.02 for s in shapes]
+    grads = [[torch.randn(s, generator=g) * 1e-3 for s in shapes] for _ in range(3)]
+    results = []
+    for foreach in (True, False):
+        ps = [p.clone().to("supa").requires_grad_() for p in init]
+        opt = torch.optim.AdamW(ps, lr=1e-3, weight_decay=0.01, amsgrad=amsgrad, foreach=foreach)
+        for step in grads:
+            for p, gr in zip(ps, step):
+                p.grad = gr.to("supa")
+            opt.step()
+        results.append([p.detach().cpu() for p in ps])
+    for a, b in zip(*results):
+        assert torch.equal(a, b)
+    # and close to the CPU implementation (whose addcmul rounds once more)
+    ps = [p.clone().requires_grad_() for p in init]
+    opt = torch.optim.AdamW(ps, lr=1e-3, weight_decay=0.01, amsgrad=amsgrad, foreach=False)
+    for step in grads:
+        for p, gr in zip(ps, step):
+            p.grad = gr
+        opt.step()
+    for a, p in zip(results[0], ps):
+        torch.testing.assert_close(a, p.detach(), rtol=1e-5, atol=1e-7)

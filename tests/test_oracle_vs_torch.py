@@ -424,3 +424,17 @@ def test_lerp_vs_exact_and_cpu():
     # the weight-1 and weight-0 endpoints are exact
     assert np.array_equal(O.ternary(O.LERP, x.numpy(), e.numpy(), np.ones(20000, np.float32)), e.numpy())
     assert np.array_equal(O.ternary(O.LERP, x.numpy(), e.numpy(), np.zeros(20000, np.float32)), x.numpy())
+
+
+def test_vector_norm_vs_cpu_and_closed_forms():
+    x = randn((10007,), 81, 3.0).double()
+    for p in (1, 2, float("inf")):
+        assert O.vector_norm(x.numpy(), p) == pytest.approx(torch.linalg.vector_norm(x, p).item(), rel=1e-13)
+    n = 4096
+    assert O.vector_norm(np.ones(n), 2) == 64.0
+    assert O.vector_norm(np.full(n, -0.5), 1) == n / 2
+    assert O.vector_norm(np.array([3.0, -4.0]), 2) == 5.0
+    assert O.vector_norm(np.array([1.0, -7.5, 2.0]), float("inf")) == 7.5
+    assert O.vector_norm(np.zeros(0), 2) == 0.0
+    assert math.isnan(O.vector_norm(np.array([1.0, float("nan")]), float("inf")))
+    assert math.isnan(O.vector_norm(np.array([1.0, float("nan")]), 2))

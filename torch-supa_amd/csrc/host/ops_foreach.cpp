@@ -1,14 +1,17 @@
-// PrivateUse1 registrations of the optimizer path: _foreach_add / _foreach_mul
-// (List and Scalar overloads, in-place and out-of-place), _fused_adamw_, and
-// the mixed-precision pieces beside it (_amp_foreach_non_finite_check_and_unscale_,
-// _amp_update_scale_).
+// PrivateUse1 registrations of the optimizer path: the _foreach_* family
+// (add / sub / mul / div / maximum / minimum / clamp_min / clamp_max in their
+// List, Scalar, ScalarList and Tensor forms; addcmul / addcdiv; lerp; the
+// unary ops the elementwise kernels have; zero_; norm), in-place and
+// out-of-place, _fused_adamw_, and the mixed-precision pieces beside it
+// (_amp_foreach_non_finite_check_and_unscale_, _amp_update_scale_).
 //
 // Fast path: every tensor on one supa device, one floating dtype, dense and
-// contiguous (and, for List overloads, matching shapes) -- then one
+// contiguous (and, across lists, matching shapes), real scalars -- then one
 // multi-tensor-apply launch per 40 tensors.  Anything else takes the slow
 // path the upstream CompositeExplicitAutograd foreach kernels take: one
-// elementwise op per tensor (still on the supa kernels).
+// elementwise op per tensor (still on the supa kernels where they exist).
 #include <ATen/native/ForeachUtils.h>
+#include <ATen/ops/linalg_vector_norm.h>
 #include <torch/library.h>
 
 #include <map>
@@ -45,91 +48,371 @@ bool fast_ok(std::initializer_list<at::TensorList> lists) {
   return true;
 }
 
-void launch_foreach(int op, at::TensorList out, at::TensorList a, at::TensorList b, double scalar, double alpha) {
-  const size_t n = a.size();
+// ------------------------------------------------------- generic launch
+std::vector<at::Tensor> empty_like_list(at::TensorList a) {
+  std::vector<at::Tensor> out;
+  out.reserve(a.size());
+  for (const auto& t : a) out.push_back(at::empty_like(t));
+  return out;
+}
+
+// One supa_amd_foreach call over lists that passed fast_ok.
+void fe_launch(int op, int form, at::TensorList out, at::TensorList a, at::TensorList b, at::TensorList c,
+               const std::vector<double>& scalars, double alpha, const at::Tensor& dev_scalar, const char* name) {
+  const size_t n = out.size();
   if (n == 0) return;
-  std::vector<void*> po(n), pa(n), pb(b.empty() ? 0 : n);
+  std::vector<void*> po(n);
+  std::vector<const void*> pa(a.size()), pb(b.size()), pc(c.size());
   std::vector<int64_t> numel(n);
   for (size_t i = 0; i < n; ++i) {
     po[i] = out[i].data_ptr();
-    pa[i] = a[i].data_ptr();
-    if (!b.empty()) pb[i] = b[i].data_ptr();
-    numel[i] = a[i].numel();
+    numel[i] = out[i].numel();
   }
-  const auto dev = a[0].device().index();
-  const int rc = supa_amd_foreach_binary(op, (int32_t)n, po.data(), pa.data(), b.empty() ? nullptr : pb.data(),
-                                         numel.data(), dtype_code(a[0].scalar_type()), scalar, alpha,
-                                         current_stream(dev));
-  check_status(rc, op == SUPA_AMD_FOREACH_ADD ? "_foreach_add" : "_foreach_mul");
+  for (size_t i = 0; i < a.size(); ++i) pa[i] = a[i].data_ptr();
+  for (size_t i = 0; i < b.size(); ++i) pb[i] = b[i].data_ptr();
+  for (size_t i = 0; i < c.size(); ++i) pc[i] = c[i].data_ptr();
+  const auto dev = out[0].device().index();
+  const int rc = supa_amd_foreach(op, form, (int32_t)n, po.data(), a.empty() ? nullptr : pa.data(),
+                                  b.empty() ? nullptr : pb.data(), c.empty() ? nullptr : pc.data(), numel.data(),
+                                  dtype_code(out[0].scalar_type()), scalars.empty() ? nullptr : scalars.data(), alpha,
+                                  dev_scalar.defined() ? dev_scalar.data_ptr() : nullptr, current_stream(dev));
+  check_status(rc, name);
 }
 
-double scalar_value(const c10::Scalar& s) {
-  TORCH_CHECK(!s.isComplex(), "supa foreach: complex scalars are not supported");
-  return s.toDouble();
+// A real (not complex, not bool) scalar: bool scalars keep upstream's
+// per-tensor semantics through the slow path.
+bool real_scalar(const c10::Scalar& s) { return !s.isComplex() && !s.isBoolean(); }
+bool real_scalars(at::ArrayRef<c10::Scalar> ss) {
+  for (const auto& s : ss)
+    if (!real_scalar(s)) return false;
+  return true;
+}
+std::vector<double> to_doubles(at::ArrayRef<c10::Scalar> ss) {
+  std::vector<double> v;
+  v.reserve(ss.size());
+  for (const auto& s : ss) v.push_back(s.toDouble());
+  return v;
 }
 
-// ------------------------------------------------------------- add / mul
-void foreach_add_scalar_(at::TensorList self, const c10::Scalar& s) {
-  if (fast_ok({self}) && !s.isBoolean()) return launch_foreach(SUPA_AMD_FOREACH_ADD, self, self, {}, scalar_value(s), 1.0);
-  for (const auto& t : self) const_cast<at::Tensor&>(t).add_(s);
+// ------------------------------------------------------------- binary
+// clamp_min is maximum and clamp_max is minimum (both NaN-propagating).
+enum class Bop { Add, Sub, Mul, Div, Max, Min };
+
+int bop_code(Bop o) {
+  switch (o) {
+    case Bop::Add:
+    case Bop::Sub: return SUPA_AMD_FOREACH_ADD;
+    case Bop::Mul: return SUPA_AMD_FOREACH_MUL;
+    case Bop::Div: return SUPA_AMD_FOREACH_DIV;
+    case Bop::Max: return SUPA_AMD_FOREACH_MAXIMUM;
+    default: return SUPA_AMD_FOREACH_MINIMUM;
+  }
 }
-std::vector<at::Tensor> foreach_add_scalar(at::TensorList self, const c10::Scalar& s) {
-  if (fast_ok({self}) && !s.isBoolean()) {
-    std::vector<at::Tensor> out;
-    for (const auto& t : self) out.push_back(at::empty_like(t));
-    launch_foreach(SUPA_AMD_FOREACH_ADD, out, self, {}, scalar_value(s), 1.0);
+const char* bop_name(Bop o) {
+  static const char* names[] = {"_foreach_add", "_foreach_sub", "_foreach_mul", "_foreach_div", "_foreach_maximum",
+                                "_foreach_minimum"};
+  return names[(int)o];
+}
+
+// The slow path: the per-tensor op (upstream's CompositeExplicit foreach
+// kernels do the same), with a tensor or a scalar second operand.
+at::Tensor bop_one(Bop o, const at::Tensor& a, const at::Tensor& y, const c10::Scalar& alpha, bool inplace) {
+  at::Tensor& s = const_cast<at::Tensor&>(a);
+  switch (o) {
+    case Bop::Add: return inplace ? s.add_(y, alpha) : at::add(a, y, alpha);
+    case Bop::Sub: return inplace ? s.sub_(y, alpha) : at::sub(a, y, alpha);
+    case Bop::Mul: return inplace ? s.mul_(y) : at::mul(a, y);
+    case Bop::Div: return inplace ? s.div_(y) : at::div(a, y);
+    case Bop::Max: return inplace ? s.clamp_min_(y) : at::clamp_min(a, y);
+    default: return inplace ? s.clamp_max_(y) : at::clamp_max(a, y);
+  }
+}
+at::Tensor bop_one(Bop o, const at::Tensor& a, const c10::Scalar& y, bool inplace) {
+  at::Tensor& s = const_cast<at::Tensor&>(a);
+  switch (o) {
+    case Bop::Add: return inplace ? s.add_(y) : at::add(a, y);
+    case Bop::Sub: return inplace ? s.sub_(y) : at::sub(a, y);
+    case Bop::Mul: return inplace ? s.mul_(y) : at::mul(a, y);
+    case Bop::Div: return inplace ? s.div_(y) : at::div(a, y);
+    case Bop::Max: return inplace ? s.clamp_min_(y) : at::clamp_min(a, y);
+    default: return inplace ? s.clamp_max_(y) : at::clamp_max(a, y);
+  }
+}
+
+// List form: out[k] = a[k] op b[k] (add / sub with alpha).
+std::vector<at::Tensor> bop_list(Bop o, at::TensorList self, at::TensorList other, const c10::Scalar& alpha,
+                                 bool inplace) {
+  at::native::check_foreach_api_restrictions(self, other);
+  if (fast_ok({self, other}) && real_scalar(alpha)) {
+    std::vector<at::Tensor> out = inplace ? self.vec() : empty_like_list(self);
+    const double al = o == Bop::Sub ? -alpha.toDouble() : alpha.toDouble();
+    fe_launch(bop_code(o), SUPA_AMD_FOREACH_LIST, out, self, other, {}, {}, al, {}, bop_name(o));
     return out;
   }
   std::vector<at::Tensor> out;
-  for (const auto& t : self) out.push_back(t.add(s));
+  for (size_t i = 0; i < self.size(); ++i) out.push_back(bop_one(o, self[i], other[i], alpha, inplace));
   return out;
 }
-void foreach_add_list_(at::TensorList self, at::TensorList other, const c10::Scalar& alpha) {
-  at::native::check_foreach_api_restrictions(self, other);
-  if (fast_ok({self, other})) return launch_foreach(SUPA_AMD_FOREACH_ADD, self, self, other, 0.0, scalar_value(alpha));
-  for (size_t i = 0; i < self.size(); ++i) const_cast<at::Tensor&>(self[i]).add_(other[i], alpha);
-}
-std::vector<at::Tensor> foreach_add_list(at::TensorList self, at::TensorList other, const c10::Scalar& alpha) {
-  at::native::check_foreach_api_restrictions(self, other);
-  std::vector<at::Tensor> out;
-  if (fast_ok({self, other})) {
-    for (const auto& t : self) out.push_back(at::empty_like(t));
-    launch_foreach(SUPA_AMD_FOREACH_ADD, out, self, other, 0.0, scalar_value(alpha));
+
+// Scalar and ScalarList forms: out[k] = a[k] op s[k]; sub is add of -s.
+std::vector<at::Tensor> bop_scalars(Bop o, at::TensorList self, at::ArrayRef<c10::Scalar> ss, bool inplace) {
+  at::native::check_foreach_api_restrictions(self, ss);
+  if (fast_ok({self}) && real_scalars(ss)) {
+    std::vector<at::Tensor> out = inplace ? self.vec() : empty_like_list(self);
+    std::vector<double> v = to_doubles(ss);
+    if (o == Bop::Sub)
+      for (double& x : v) x = -x;
+    fe_launch(bop_code(o), SUPA_AMD_FOREACH_SCALARS, out, self, {}, {}, v, 1.0, {}, bop_name(o));
     return out;
   }
-  for (size_t i = 0; i < self.size(); ++i) out.push_back(self[i].add(other[i], alpha));
+  std::vector<at::Tensor> out;
+  for (size_t i = 0; i < self.size(); ++i) out.push_back(bop_one(o, self[i], ss[i], inplace));
   return out;
 }
-void foreach_mul_scalar_(at::TensorList self, const c10::Scalar& s) {
-  if (fast_ok({self}) && !s.isBoolean()) return launch_foreach(SUPA_AMD_FOREACH_MUL, self, self, {}, scalar_value(s), 1.0);
-  for (const auto& t : self) const_cast<at::Tensor&>(t).mul_(s);
+std::vector<at::Tensor> bop_scalar(Bop o, at::TensorList self, const c10::Scalar& s, bool inplace) {
+  std::vector<c10::Scalar> ss(self.size(), s);
+  at::native::check_foreach_api_restrictions(self);
+  return bop_scalars(o, self, ss, inplace);
 }
-std::vector<at::Tensor> foreach_mul_scalar(at::TensorList self, const c10::Scalar& s) {
-  std::vector<at::Tensor> out;
-  if (fast_ok({self}) && !s.isBoolean()) {
-    for (const auto& t : self) out.push_back(at::empty_like(t));
-    launch_foreach(SUPA_AMD_FOREACH_MUL, out, self, {}, scalar_value(s), 1.0);
+
+// Tensor form: a 0-dim tensor on the list's device is read by the kernel
+// (after a cast to the list dtype, which is what the per-tensor op does with
+// a 0-dim operand of the same category); elsewhere the per-tensor op.
+std::vector<at::Tensor> bop_tensor(Bop o, at::TensorList self, const at::Tensor& other, const c10::Scalar& alpha,
+                                   bool inplace) {
+  at::native::check_foreach_api_restrictions(self);
+  TORCH_CHECK(other.dim() == 0 && other.numel() == 1, "scalar tensor expected to be 0 dim but it has ", other.dim(),
+              " dimensions and ", other.numel(), " elements.");
+  if (fast_ok({self}) && other.device() == self[0].device() && float_family(other.scalar_type()) &&
+      real_scalar(alpha)) {
+    std::vector<at::Tensor> out = inplace ? self.vec() : empty_like_list(self);
+    const at::Tensor y = other.scalar_type() == self[0].scalar_type() ? other : other.to(self[0].scalar_type());
+    const double al = o == Bop::Sub ? -alpha.toDouble() : alpha.toDouble();
+    fe_launch(bop_code(o), SUPA_AMD_FOREACH_DEVSCALAR, out, self, {}, {}, {}, al, y, bop_name(o));
     return out;
   }
-  for (const auto& t : self) out.push_back(t.mul(s));
+  std::vector<at::Tensor> out;
+  for (size_t i = 0; i < self.size(); ++i) out.push_back(bop_one(o, self[i], other, alpha, inplace));
   return out;
 }
-void foreach_mul_list_(at::TensorList self, at::TensorList other) {
-  at::native::check_foreach_api_restrictions(self, other);
-  if (fast_ok({self, other})) return launch_foreach(SUPA_AMD_FOREACH_MUL, self, self, other, 0.0, 1.0);
-  for (size_t i = 0; i < self.size(); ++i) const_cast<at::Tensor&>(self[i]).mul_(other[i]);
-}
-std::vector<at::Tensor> foreach_mul_list(at::TensorList self, at::TensorList other) {
-  at::native::check_foreach_api_restrictions(self, other);
-  std::vector<at::Tensor> out;
-  if (fast_ok({self, other})) {
-    for (const auto& t : self) out.push_back(at::empty_like(t));
-    launch_foreach(SUPA_AMD_FOREACH_MUL, out, self, other, 0.0, 1.0);
+
+// ------------------------------------------------------------ ternary
+std::vector<at::Tensor> addc(bool div, at::TensorList self, at::TensorList t1, at::TensorList t2,
+                             at::ArrayRef<c10::Scalar> values, bool inplace) {
+  at::native::check_foreach_api_restrictions(self, t1, t2, values);
+  const char* name = div ? "_foreach_addcdiv" : "_foreach_addcmul";
+  if (fast_ok({self, t1, t2}) && real_scalars(values)) {
+    std::vector<at::Tensor> out = inplace ? self.vec() : empty_like_list(self);
+    fe_launch(div ? SUPA_AMD_FOREACH_ADDCDIV : SUPA_AMD_FOREACH_ADDCMUL, SUPA_AMD_FOREACH_SCALARS, out, self, t1, t2,
+              to_doubles(values), 1.0, {}, name);
     return out;
   }
-  for (size_t i = 0; i < self.size(); ++i) out.push_back(self[i].mul(other[i]));
+  std::vector<at::Tensor> out;
+  for (size_t i = 0; i < self.size(); ++i) {
+    at::Tensor& s = const_cast<at::Tensor&>(self[i]);
+    if (div) out.push_back(inplace ? s.addcdiv_(t1[i], t2[i], values[i]) : at::addcdiv(s, t1[i], t2[i], values[i]));
+    else out.push_back(inplace ? s.addcmul_(t1[i], t2[i], values[i]) : at::addcmul(s, t1[i], t2[i], values[i]));
+  }
   return out;
 }
+
+std::vector<at::Tensor> lerp_list(at::TensorList self, at::TensorList ends, at::TensorList weights, bool inplace) {
+  at::native::check_foreach_api_restrictions(self, ends, weights);
+  if (fast_ok({self, ends, weights})) {
+    std::vector<at::Tensor> out = inplace ? self.vec() : empty_like_list(self);
+    fe_launch(SUPA_AMD_FOREACH_LERP, SUPA_AMD_FOREACH_LIST, out, self, ends, weights, {}, 1.0, {}, "_foreach_lerp");
+    return out;
+  }
+  std::vector<at::Tensor> out;
+  for (size_t i = 0; i < self.size(); ++i) {
+    at::Tensor& s = const_cast<at::Tensor&>(self[i]);
+    out.push_back(inplace ? s.lerp_(ends[i], weights[i]) : at::lerp(s, ends[i], weights[i]));
+  }
+  return out;
+}
+std::vector<at::Tensor> lerp_scalars(at::TensorList self, at::TensorList ends, at::ArrayRef<c10::Scalar> w,
+                                     bool inplace) {
+  at::native::check_foreach_api_restrictions(self, ends, w);
+  if (fast_ok({self, ends}) && real_scalars(w)) {
+    std::vector<at::Tensor> out = inplace ? self.vec() : empty_like_list(self);
+    fe_launch(SUPA_AMD_FOREACH_LERP, SUPA_AMD_FOREACH_SCALARS, out, self, ends, {}, to_doubles(w), 1.0, {},
+              "_foreach_lerp");
+    return out;
+  }
+  std::vector<at::Tensor> out;
+  for (size_t i = 0; i < self.size(); ++i) {
+    at::Tensor& s = const_cast<at::Tensor&>(self[i]);
+    out.push_back(inplace ? s.lerp_(ends[i], w[i]) : at::lerp(s, ends[i], w[i]));
+  }
+  return out;
+}
+
+// -------------------------------------------------------------- unary
+at::Tensor unary_one(int u, const at::Tensor& a, bool inplace) {
+  at::Tensor& s = const_cast<at::Tensor&>(a);
+  switch (u) {
+    case SUPA_AMD_SIGMOID: return inplace ? s.sigmoid_() : at::sigmoid(a);
+    case SUPA_AMD_TANH: return inplace ? s.tanh_() : at::tanh(a);
+    case SUPA_AMD_EXP: return inplace ? s.exp_() : at::exp(a);
+    case SUPA_AMD_LOG: return inplace ? s.log_() : at::log(a);
+    case SUPA_AMD_ERF: return inplace ? s.erf_() : at::erf(a);
+    case SUPA_AMD_NEG: return inplace ? s.neg_() : at::neg(a);
+    case SUPA_AMD_RECIPROCAL: return inplace ? s.reciprocal_() : at::reciprocal(a);
+    case SUPA_AMD_ABS: return inplace ? s.abs_() : at::abs(a);
+    default: return inplace ? s.sqrt_() : at::sqrt(a);
+  }
+}
+std::vector<at::Tensor> unary(int u, at::TensorList self, bool inplace, const char* name) {
+  at::native::check_foreach_api_restrictions(self);
+  if (fast_ok({self})) {
+    std::vector<at::Tensor> out = inplace ? self.vec() : empty_like_list(self);
+    fe_launch(SUPA_AMD_FOREACH_UNARY + u, SUPA_AMD_FOREACH_SCALARS, out, self, {}, {}, {}, 1.0, {}, name);
+    return out;
+  }
+  std::vector<at::Tensor> out;
+  for (const auto& t : self) out.push_back(unary_one(u, t, inplace));
+  return out;
+}
+
+void foreach_zero_(at::TensorList self) {
+  if (fast_ok({self})) return fe_launch(SUPA_AMD_FOREACH_ZERO, SUPA_AMD_FOREACH_SCALARS, self, {}, {}, {}, {}, 1.0, {},
+                                        "_foreach_zero_");
+  for (const auto& t : self) const_cast<at::Tensor&>(t).zero_();
+}
+
+// --------------------------------------------------------------- norm
+// Per-tensor 1-, 2- and inf-norms in one pair of launches; the results are
+// views of one n-element tensor, as upstream's.  Other orders and dtypes take
+// the per-tensor linalg_vector_norm.
+std::vector<at::Tensor> foreach_norm(at::TensorList self, const c10::Scalar& ord, std::optional<at::ScalarType> dtype) {
+  at::native::check_foreach_api_restrictions(self);
+  const double p = ord.isComplex() ? -1.0 : ord.toDouble();
+  const c10::ScalarType in_dt = self[0].scalar_type();
+  const c10::ScalarType res_dt = dtype.value_or(in_dt);
+  const bool fast = fast_ok({self}) && (p == 1.0 || p == 2.0 || p == HUGE_VAL) &&
+                    (res_dt == in_dt || res_dt == at::kFloat || res_dt == at::kDouble);
+  std::vector<at::Tensor> res;
+  if (!fast) {
+    for (const auto& t : self) res.push_back(at::linalg_vector_norm(t, ord, at::OptionalIntArrayRef{}, false, dtype));
+    return res;
+  }
+  const size_t n = self.size();
+  std::vector<const void*> px(n);
+  std::vector<int64_t> numel(n);
+  for (size_t i = 0; i < n; ++i) {
+    px[i] = self[i].data_ptr();
+    numel[i] = self[i].numel();
+  }
+  const int32_t dt = dtype_code(in_dt);
+  const int64_t ws_bytes = supa_amd_foreach_norm_workspace_bytes((int32_t)n, numel.data(), dt);
+  TORCH_CHECK(ws_bytes >= 0, "_foreach_norm: ", supa_amd_status_string((int)ws_bytes));
+  at::Tensor out = at::empty({(int64_t)n}, self[0].options().dtype(res_dt));
+  at::Tensor ws = at::empty({std::max<int64_t>(ws_bytes, 1)}, self[0].options().dtype(at::kByte));
+  const int rc = supa_amd_foreach_norm((int32_t)n, px.data(), numel.data(), dt, p, out.data_ptr(), dtype_code(res_dt),
+                                       ws.data_ptr(), ws_bytes, current_stream(self[0].device().index()));
+  check_status(rc, "_foreach_norm");
+  res.reserve(n);
+  for (size_t i = 0; i < n; ++i) res.push_back(out.select(0, (int64_t)i));
+  return res;
+}
+
+// ------------------------------------------------ registered signatures
+#define SUPA_FE_BINARY(NAME, OP)                                                                                    \
+  void NAME##_list_(at::TensorList s, at::TensorList o) { bop_list(OP, s, o, 1, true); }                            \
+  std::vector<at::Tensor> NAME##_list(at::TensorList s, at::TensorList o) { return bop_list(OP, s, o, 1, false); } \
+  void NAME##_scalar_(at::TensorList s, const c10::Scalar& v) { bop_scalar(OP, s, v, true); }                       \
+  std::vector<at::Tensor> NAME##_scalar(at::TensorList s, const c10::Scalar& v) { return bop_scalar(OP, s, v, false); } \
+  void NAME##_scalarlist_(at::TensorList s, at::ArrayRef<c10::Scalar> v) { bop_scalars(OP, s, v, true); }          \
+  std::vector<at::Tensor> NAME##_scalarlist(at::TensorList s, at::ArrayRef<c10::Scalar> v) {                        \
+    return bop_scalars(OP, s, v, false);                                                                            \
+  }
+// add / sub take alpha in the List form
+void add_list_(at::TensorList s, at::TensorList o, const c10::Scalar& a) { bop_list(Bop::Add, s, o, a, true); }
+std::vector<at::Tensor> add_list(at::TensorList s, at::TensorList o, const c10::Scalar& a) {
+  return bop_list(Bop::Add, s, o, a, false);
+}
+void sub_list_(at::TensorList s, at::TensorList o, const c10::Scalar& a) { bop_list(Bop::Sub, s, o, a, true); }
+std::vector<at::Tensor> sub_list(at::TensorList s, at::TensorList o, const c10::Scalar& a) {
+  return bop_list(Bop::Sub, s, o, a, false);
+}
+void add_scalar_(at::TensorList s, const c10::Scalar& v) { bop_scalar(Bop::Add, s, v, true); }
+std::vector<at::Tensor> add_scalar(at::TensorList s, const c10::Scalar& v) { return bop_scalar(Bop::Add, s, v, false); }
+void add_scalarlist_(at::TensorList s, at::ArrayRef<c10::Scalar> v) { bop_scalars(Bop::Add, s, v, true); }
+std::vector<at::Tensor> add_scalarlist(at::TensorList s, at::ArrayRef<c10::Scalar> v) {
+  return bop_scalars(Bop::Add, s, v, false);
+}
+void sub_scalar_(at::TensorList s, const c10::Scalar& v) { bop_scalar(Bop::Sub, s, v, true); }
+std::vector<at::Tensor> sub_scalar(at::TensorList s, const c10::Scalar& v) { return bop_scalar(Bop::Sub, s, v, false); }
+void sub_scalarlist_(at::TensorList s, at::ArrayRef<c10::Scalar> v) { bop_scalars(Bop::Sub, s, v, true); }
+std::vector<at::Tensor> sub_scalarlist(at::TensorList s, at::ArrayRef<c10::Scalar> v) {
+  return bop_scalars(Bop::Sub, s, v, false);
+}
+void add_tensor_(at::TensorList s, const at::Tensor& o, const c10::Scalar& a) { bop_tensor(Bop::Add, s, o, a, true); }
+std::vector<at::Tensor> add_tensor(at::TensorList s, const at::Tensor& o, const c10::Scalar& a) {
+  return bop_tensor(Bop::Add, s, o, a, false);
+}
+SUPA_FE_BINARY(mul, Bop::Mul)
+SUPA_FE_BINARY(div, Bop::Div)
+SUPA_FE_BINARY(maximum, Bop::Max)
+SUPA_FE_BINARY(minimum, Bop::Min)
+#undef SUPA_FE_BINARY
+void mul_tensor_(at::TensorList s, const at::Tensor& o) { bop_tensor(Bop::Mul, s, o, 1, true); }
+std::vector<at::Tensor> mul_tensor(at::TensorList s, const at::Tensor& o) { return bop_tensor(Bop::Mul, s, o, 1, false); }
+void div_tensor_(at::TensorList s, const at::Tensor& o) { bop_tensor(Bop::Div, s, o, 1, true); }
+std::vector<at::Tensor> div_tensor(at::TensorList s, const at::Tensor& o) { return bop_tensor(Bop::Div, s, o, 1, false); }
+
+#define SUPA_FE_ADDC(NAME, DIV)                                                                                     \
+  void NAME##_scalar_(at::TensorList s, at::TensorList a, at::TensorList b, const c10::Scalar& v) {                 \
+    addc(DIV, s, a, b, std::vector<c10::Scalar>(s.size(), v), true);                                                \
+  }                                                                                                                 \
+  std::vector<at::Tensor> NAME##_scalar(at::TensorList s, at::TensorList a, at::TensorList b, const c10::Scalar& v) { \
+    return addc(DIV, s, a, b, std::vector<c10::Scalar>(s.size(), v), false);                                        \
+  }                                                                                                                 \
+  void NAME##_scalarlist_(at::TensorList s, at::TensorList a, at::TensorList b, at::ArrayRef<c10::Scalar> v) {      \
+    addc(DIV, s, a, b, v, true);                                                                                    \
+  }                                                                                                                 \
+  std::vector<at::Tensor> NAME##_scalarlist(at::TensorList s, at::TensorList a, at::TensorList b,                   \
+                                            at::ArrayRef<c10::Scalar> v) {                                          \
+    return addc(DIV, s, a, b, v, false);                                                                            \
+  }                                                                                                                 \
+  void NAME##_tensor_(at::TensorList s, at::TensorList a, at::TensorList b, const at::Tensor& v) {                  \
+    addc(DIV, s, a, b, at::native::convert_tensor_to_scalar_list(v, s.size()), true);                               \
+  }                                                                                                                 \
+  std::vector<at::Tensor> NAME##_tensor(at::TensorList s, at::TensorList a, at::TensorList b, const at::Tensor& v) { \
+    return addc(DIV, s, a, b, at::native::convert_tensor_to_scalar_list(v, s.size()), false);                       \
+  }
+SUPA_FE_ADDC(addcmul, false)
+SUPA_FE_ADDC(addcdiv, true)
+#undef SUPA_FE_ADDC
+
+void lerp_list_(at::TensorList s, at::TensorList e, at::TensorList w) { lerp_list(s, e, w, true); }
+std::vector<at::Tensor> lerp_list_f(at::TensorList s, at::TensorList e, at::TensorList w) {
+  return lerp_list(s, e, w, false);
+}
+void lerp_scalar_(at::TensorList s, at::TensorList e, const c10::Scalar& w) {
+  lerp_scalars(s, e, std::vector<c10::Scalar>(s.size(), w), true);
+}
+std::vector<at::Tensor> lerp_scalar(at::TensorList s, at::TensorList e, const c10::Scalar& w) {
+  return lerp_scalars(s, e, std::vector<c10::Scalar>(s.size(), w), false);
+}
+void lerp_scalarlist_(at::TensorList s, at::TensorList e, at::ArrayRef<c10::Scalar> w) { lerp_scalars(s, e, w, true); }
+std::vector<at::Tensor> lerp_scalarlist(at::TensorList s, at::TensorList e, at::ArrayRef<c10::Scalar> w) {
+  return lerp_scalars(s, e, w, false);
+}
+
+#define SUPA_FE_UNARY(NAME, U)                                                                             \
+  void fe_##NAME##_(at::TensorList s) { unary(U, s, true, "_foreach_" #NAME "_"); }                         \
+  std::vector<at::Tensor> fe_##NAME(at::TensorList s) { return unary(U, s, false, "_foreach_" #NAME); }
+SUPA_FE_UNARY(sigmoid, SUPA_AMD_SIGMOID)
+SUPA_FE_UNARY(tanh, SUPA_AMD_TANH)
+SUPA_FE_UNARY(exp, SUPA_AMD_EXP)
+SUPA_FE_UNARY(log, SUPA_AMD_LOG)
+SUPA_FE_UNARY(erf, SUPA_AMD_ERF)
+SUPA_FE_UNARY(neg, SUPA_AMD_NEG)
+SUPA_FE_UNARY(reciprocal, SUPA_AMD_RECIPROCAL)
+SUPA_FE_UNARY(abs, SUPA_AMD_ABS)
+SUPA_FE_UNARY(sqrt, SUPA_AMD_SQRT)
+#undef SUPA_FE_UNARY
 
 // ------------------------------------------------------------ fused AdamW
 void fused_adamw_impl(at::TensorList params, at::TensorList grads, at::TensorList exp_avgs,
@@ -270,14 +553,72 @@ at::Tensor& amp_update_scale_(at::Tensor& self, at::Tensor& growth_tracker, cons
 
 TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
   using namespace supa;
-  m.impl("_foreach_add_.Scalar", TORCH_FN(foreach_add_scalar_));
-  m.impl("_foreach_add.Scalar", TORCH_FN(foreach_add_scalar));
-  m.impl("_foreach_add_.List", TORCH_FN(foreach_add_list_));
-  m.impl("_foreach_add.List", TORCH_FN(foreach_add_list));
-  m.impl("_foreach_mul_.Scalar", TORCH_FN(foreach_mul_scalar_));
-  m.impl("_foreach_mul.Scalar", TORCH_FN(foreach_mul_scalar));
-  m.impl("_foreach_mul_.List", TORCH_FN(foreach_mul_list_));
-  m.impl("_foreach_mul.List", TORCH_FN(foreach_mul_list));
+  // binary: List / Scalar / ScalarList / Tensor
+  m.impl("_foreach_add_.List", TORCH_FN(add_list_));
+  m.impl("_foreach_add.List", TORCH_FN(add_list));
+  m.impl("_foreach_add_.Scalar", TORCH_FN(add_scalar_));
+  m.impl("_foreach_add.Scalar", TORCH_FN(add_scalar));
+  m.impl("_foreach_add_.ScalarList", TORCH_FN(add_scalarlist_));
+  m.impl("_foreach_add.ScalarList", TORCH_FN(add_scalarlist));
+  m.impl("_foreach_add_.Tensor", TORCH_FN(add_tensor_));
+  m.impl("_foreach_add.Tensor", TORCH_FN(add_tensor));
+  m.impl("_foreach_sub_.List", TORCH_FN(sub_list_));
+  m.impl("_foreach_sub.List", TORCH_FN(sub_list));
+  m.impl("_foreach_sub_.Scalar", TORCH_FN(sub_scalar_));
+  m.impl("_foreach_sub.Scalar", TORCH_FN(sub_scalar));
+  m.impl("_foreach_sub_.ScalarList", TORCH_FN(sub_scalarlist_));
+  m.impl("_foreach_sub.ScalarList", TORCH_FN(sub_scalarlist));
+#define SUPA_FE_REG_BINARY(SCHEMA, NAME)                                 \
+  m.impl("_foreach_" SCHEMA "_.List", TORCH_FN(NAME##_list_));             \
+  m.impl("_foreach_" SCHEMA ".List", TORCH_FN(NAME##_list));               \
+  m.impl("_foreach_" SCHEMA "_.Scalar", TORCH_FN(NAME##_scalar_));         \
+  m.impl("_foreach_" SCHEMA ".Scalar", TORCH_FN(NAME##_scalar));           \
+  m.impl("_foreach_" SCHEMA "_.ScalarList", TORCH_FN(NAME##_scalarlist_)); \
+  m.impl("_foreach_" SCHEMA ".ScalarList", TORCH_FN(NAME##_scalarlist));
+  SUPA_FE_REG_BINARY("mul", mul)
+  SUPA_FE_REG_BINARY("div", div)
+  SUPA_FE_REG_BINARY("maximum", maximum)
+  SUPA_FE_REG_BINARY("minimum", minimum)
+  SUPA_FE_REG_BINARY("clamp_min", maximum)
+  SUPA_FE_REG_BINARY("clamp_max", minimum)
+#undef SUPA_FE_REG_BINARY
+  m.impl("_foreach_mul_.Tensor", TORCH_FN(mul_tensor_));
+  m.impl("_foreach_mul.Tensor", TORCH_FN(mul_tensor));
+  m.impl("_foreach_div_.Tensor", TORCH_FN(div_tensor_));
+  m.impl("_foreach_div.Tensor", TORCH_FN(div_tensor));
+  // pointwise ternary
+#define SUPA_FE_REG_ADDC(NAME)                                                \
+  m.impl("_foreach_" #NAME "_.Scalar", TORCH_FN(NAME##_scalar_));             \
+  m.impl("_foreach_" #NAME ".Scalar", TORCH_FN(NAME##_scalar));               \
+  m.impl("_foreach_" #NAME "_.ScalarList", TORCH_FN(NAME##_scalarlist_));     \
+  m.impl("_foreach_" #NAME ".ScalarList", TORCH_FN(NAME##_scalarlist));       \
+  m.impl("_foreach_" #NAME "_.Tensor", TORCH_FN(NAME##_tensor_));             \
+  m.impl("_foreach_" #NAME ".Tensor", TORCH_FN(NAME##_tensor));
+  SUPA_FE_REG_ADDC(addcmul)
+  SUPA_FE_REG_ADDC(addcdiv)
+#undef SUPA_FE_REG_ADDC
+  m.impl("_foreach_lerp_.List", TORCH_FN(lerp_list_));
+  m.impl("_foreach_lerp.List", TORCH_FN(lerp_list_f));
+  m.impl("_foreach_lerp_.Scalar", TORCH_FN(lerp_scalar_));
+  m.impl("_foreach_lerp.Scalar", TORCH_FN(lerp_scalar));
+  m.impl("_foreach_lerp_.ScalarList", TORCH_FN(lerp_scalarlist_));
+  m.impl("_foreach_lerp.ScalarList", TORCH_FN(lerp_scalarlist));
+  // unary, zero_, norm
+#define SUPA_FE_REG_UNARY(NAME)                             \
+  m.impl("_foreach_" #NAME "_", TORCH_FN(fe_##NAME##_));   \
+  m.impl("_foreach_" #NAME, TORCH_FN(fe_##NAME));
+  SUPA_FE_REG_UNARY(sigmoid)
+  SUPA_FE_REG_UNARY(tanh)
+  SUPA_FE_REG_UNARY(exp)
+  SUPA_FE_REG_UNARY(log)
+  SUPA_FE_REG_UNARY(erf)
+  SUPA_FE_REG_UNARY(neg)
+  SUPA_FE_REG_UNARY(reciprocal)
+  SUPA_FE_REG_UNARY(abs)
+  SUPA_FE_REG_UNARY(sqrt)
+#undef SUPA_FE_REG_UNARY
+  m.impl("_foreach_zero_", TORCH_FN(foreach_zero_));
+  m.impl("_foreach_norm.Scalar", TORCH_FN(foreach_norm));
   m.impl("_fused_adamw_", TORCH_FN(fused_adamw_));
   m.impl("_fused_adamw_.tensor_lr", TORCH_FN(fused_adamw_tensor_lr_));
   m.impl("_amp_foreach_non_finite_check_and_unscale_", TORCH_FN(amp_unscale_));

@@ -1,93 +1,14 @@
-// Multi-tensor apply: _foreach_add / _foreach_mul (list and scalar forms) and
-// the fused AdamW step over a list of tensors.
-//
-// One launch covers up to kMtaTensors tensors.  The tensor table (pointers,
-// element counts, chunk prefix sums) travels in the kernel arguments, so a
-// launch needs no device-side metadata and no allocation.  Each workgroup
-// owns one chunk of one tensor (found by bisection of the chunk prefix
-// table) -- one or two 16-byte vectors of each operand per thread, all loads
-// of a vector issued before the math.
-// Tensors whose base is not 16-byte aligned, and the last partial vector of a
-// tensor, take a scalar path.  The reference's counterpart is upstream
-// MultiTensorApply.cuh (kChunkSize 65536, 512 threads, ILP 4, <= 110 / 36
-// tensors per launch) with the adam_math functor of fused_adam_utils.cuh.
-#include "ew_launch.h"
+// Multi-tensor apply kernels of the optimizer step: the fused AdamW update and
+// the mixed-precision unscale / loss-scale update beside it.  Each workgroup
+// owns one chunk of one tensor (mta.h) -- one 16-byte vector of each operand
+// per thread, all loads of a vector issued before the math.  Tensors whose
+// base is not 16-byte aligned, and the last partial vector of a tensor, take
+// a scalar path.  The reference's counterpart is the adam_math functor of
+// upstream fused_adam_utils.cuh and AmpKernels.cu over MultiTensorApply.cuh.
+#include "mta.h"
 #include "ops.h"
 
 namespace sa {
-
-constexpr int kMtaTensors = 40;
-constexpr int kMtaBlock = 256;
-// Elements per workgroup: one 16-byte vector per thread for the list forms and
-// AdamW, two for the scalar forms -- the fastest measured on MI355X (c5 AdamW
-// 74 % of HBM peak against 66 % with 16384-element chunks).
-template <typename T> constexpr int64_t chunk_one() { return (int64_t)kMtaBlock * (16 / (int64_t)sizeof(T)); }
-
-// ------------------------------------------------------------- foreach
-struct ForeachTable {
-  void* out[kMtaTensors];
-  const void* a[kMtaTensors];
-  const void* b[kMtaTensors];
-  int64_t numel[kMtaTensors];
-  uint32_t chunk_start[kMtaTensors + 1];
-  int32_t ntensors;
-};
-
-// The tensor whose chunk range holds block `blk`: the last k with
-// chunk_start[k] <= blk (chunk_start is strictly increasing), by bisection.
-__device__ __forceinline__ int find_tensor(const uint32_t* chunk_start, int nt, uint32_t blk) {
-  int lo = 0, hi = nt - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (chunk_start[mid] <= blk) lo = mid;
-    else hi = mid - 1;
-  }
-  return lo;
-}
-
-template <typename T, int OP, bool LIST, int64_t CHUNK>
-__global__ void __launch_bounds__(kMtaBlock)
-k_foreach(ForeachTable tab, double scalar, double alpha) {
-  using C = opmath_t<T>;
-  constexpr int V = 16 / sizeof(T);
-  const int k = find_tensor(tab.chunk_start, tab.ntensors, blockIdx.x);
-  const int64_t chunk = blockIdx.x - tab.chunk_start[k];
-  const int64_t n = tab.numel[k];
-  const int64_t lo = chunk * CHUNK;
-  const int64_t hi = lo + CHUNK < n ? lo + CHUNK : n;
-  T* out = static_cast<T*>(tab.out[k]);
-  const T* a = static_cast<const T*>(tab.a[k]);
-  const T* b = LIST ? static_cast<const T*>(tab.b[k]) : nullptr;
-  const C s = static_cast<C>(scalar);
-  const C al = static_cast<C>(alpha);
-  auto f = [&](C x, C y) -> C {
-    if constexpr (OP == SUPA_AMD_FOREACH_ADD) return muladd<C>(al, y, x);
-    else return x * y;
-  };
-  const bool vec = aligned(out, 16) && aligned(a, 16) && (!LIST || aligned(b, 16));
-  int64_t start = lo;
-  if (vec) {
-    const int64_t nv = (hi - lo) / V;
-    for (int64_t v = threadIdx.x; v < nv; v += kMtaBlock) {
-      const int64_t e = lo + v * V;
-      const Vec<T, V> xa = ld_stream(reinterpret_cast<const Vec<T, V>*>(a + e));
-      Vec<T, V> xb;
-      if constexpr (LIST) xb = ld_stream(reinterpret_cast<const Vec<T, V>*>(b + e));
-      Vec<T, V> r;
-#pragma unroll
-      for (int i = 0; i < V; ++i) {
-        const C y = LIST ? (C)to_arith(xb.v[i]) : s;
-        r.v[i] = from_arith<T>(f((C)to_arith(xa.v[i]), y));
-      }
-      st_stream(reinterpret_cast<Vec<T, V>*>(out + e), r);
-    }
-    start = lo + nv * V;
-  }
-  for (int64_t e = start + threadIdx.x; e < hi; e += kMtaBlock) {
-    const C y = LIST ? (C)to_arith(b[e]) : s;
-    out[e] = from_arith<T>(f((C)to_arith(a[e]), y));
-  }
-}
 
 // ----------------------------------------------------------- fused AdamW
 struct AdamTable {
@@ -164,11 +85,9 @@ __global__ void __launch_bounds__(kMtaBlock)
 k_adamw(AdamTable tab, AdamHyper h) {
   if (h.found_inf && *h.found_inf == 1.0f) return;
   constexpr int V = 16 / sizeof(T);
-  const int k = find_tensor(tab.chunk_start, tab.ntensors, blockIdx.x);
-  const int64_t chunk = blockIdx.x - tab.chunk_start[k];
-  const int64_t n = tab.numel[k];
-  const int64_t lo = chunk * CHUNK;
-  const int64_t hi = lo + CHUNK < n ? lo + CHUNK : n;
+  const MtaRange r = mta_range<CHUNK>(tab.chunk_start, tab.numel, tab.ntensors);
+  const int k = r.k;
+  const int64_t lo = r.lo, hi = r.hi;
   const double lr = h.lr_ptr ? (double)(*h.lr_ptr) : h.lr;
   const float step = *tab.step[k];
   const float bc1 = (float)(1.0 - pow_steps(h.beta1, step));
@@ -224,17 +143,21 @@ k_adamw(AdamTable tab, AdamHyper h) {
 // widened to opmath, *found_inf becomes 1 if it is inf or NaN, and it is
 // multiplied by *inv_scale unless that is exactly 1.  Every writer of
 // *found_inf stores the same 1.0f.
+struct UnscaleTable {
+  void* x[kMtaTensors];
+  int64_t numel[kMtaTensors];
+  uint32_t chunk_start[kMtaTensors + 1];
+  int32_t ntensors;
+};
+
 template <typename T, int64_t CHUNK>
 __global__ void __launch_bounds__(kMtaBlock)
-k_amp_unscale(ForeachTable tab, float* __restrict__ found_inf, const float* __restrict__ inv_scale) {
+k_amp_unscale(UnscaleTable tab, float* __restrict__ found_inf, const float* __restrict__ inv_scale) {
   using C = opmath_t<T>;
   constexpr int V = 16 / sizeof(T);
-  const int k = find_tensor(tab.chunk_start, tab.ntensors, blockIdx.x);
-  const int64_t chunk = blockIdx.x - tab.chunk_start[k];
-  const int64_t n = tab.numel[k];
-  const int64_t lo = chunk * CHUNK;
-  const int64_t hi = lo + CHUNK < n ? lo + CHUNK : n;
-  T* x = static_cast<T*>(tab.out[k]);
+  const MtaRange r = mta_range<CHUNK>(tab.chunk_start, tab.numel, tab.ntensors);
+  const int64_t lo = r.lo, hi = r.hi;
+  T* x = static_cast<T*>(tab.x[r.k]);
   const C inv = (C)*inv_scale;
   bool bad = false;
   auto f = [&](C v) -> C {
@@ -275,116 +198,30 @@ __global__ void k_amp_update_scale(float* scale, int32_t* growth_tracker, const 
   }
 }
 
-template <typename F>
-int with_mta_storage(int dtype, F&& f) {
-  switch (dtype) {
-    case SUPA_AMD_F32: return f((float*)nullptr);
-    case SUPA_AMD_BF16: return f((bf16*)nullptr);
-    case SUPA_AMD_F16: return f((f16*)nullptr);
-    case SUPA_AMD_F64: return f((double*)nullptr);
-    default: return SUPA_AMD_EDTYPE;
-  }
+template <typename T, int64_t CHUNK, int UNR>
+int launch_adamw(int32_t ntensors, void* const* params, void* const* grads, void* const* exp_avgs,
+                 void* const* exp_avg_sqs, void* const* max_exp_avg_sqs, void* const* state_steps,
+                 const int64_t* numel, const AdamHyper& h, hipStream_t st) {
+  return mta_for_tables<CHUNK, AdamTable>(
+      ntensors, numel,
+      [&](AdamTable& tab, int slot, int i) -> int {
+        if (!state_steps[i]) return SUPA_AMD_EINVAL;
+        tab.p[slot] = params[i];
+        tab.g[slot] = grads[i];
+        tab.m[slot] = exp_avgs[i];
+        tab.v[slot] = exp_avg_sqs[i];
+        tab.vmax[slot] = h.amsgrad ? max_exp_avg_sqs[i] : nullptr;
+        tab.step[slot] = static_cast<const float*>(state_steps[i]);
+        return SUPA_AMD_OK;
+      },
+      [&](const AdamTable& tab, uint32_t chunks) { k_adamw<T, CHUNK, UNR><<<chunks, kMtaBlock, 0, st>>>(tab, h); });
 }
 
 }  // namespace sa
 
 using namespace sa;
 
-namespace sa {
-
-template <typename T, int64_t CHUNK>
-int launch_foreach(int op, int32_t ntensors, void* const* out, void* const* a, void* const* b, const int64_t* numel,
-                   double scalar, double alpha, hipStream_t st) {
-  int i = 0;
-  while (i < ntensors) {
-    ForeachTable tab{};
-    uint32_t chunks = 0;
-    int nt = 0;
-    while (i < ntensors && nt < kMtaTensors) {
-      if (numel[i] < 0) return SUPA_AMD_EINVAL;
-      const int64_t c = (numel[i] + CHUNK - 1) / CHUNK;
-      if (c > (int64_t)0x7fffffff) return SUPA_AMD_ELAYOUT;
-      if ((int64_t)chunks + c > (int64_t)0x7fffffff) break;
-      if (numel[i] > 0) {
-        tab.out[nt] = out[i];
-        tab.a[nt] = a[i];
-        tab.b[nt] = b ? b[i] : nullptr;
-        tab.numel[nt] = numel[i];
-        tab.chunk_start[nt] = chunks;
-        chunks += (uint32_t)c;
-        ++nt;
-      }
-      ++i;
-    }
-    tab.chunk_start[nt] = chunks;
-    tab.ntensors = nt;
-    if (nt == 0) continue;
-    if (op == SUPA_AMD_FOREACH_ADD) {
-      if (b) k_foreach<T, SUPA_AMD_FOREACH_ADD, true, CHUNK><<<chunks, kMtaBlock, 0, st>>>(tab, scalar, alpha);
-      else k_foreach<T, SUPA_AMD_FOREACH_ADD, false, CHUNK><<<chunks, kMtaBlock, 0, st>>>(tab, scalar, alpha);
-    } else {
-      if (b) k_foreach<T, SUPA_AMD_FOREACH_MUL, true, CHUNK><<<chunks, kMtaBlock, 0, st>>>(tab, scalar, alpha);
-      else k_foreach<T, SUPA_AMD_FOREACH_MUL, false, CHUNK><<<chunks, kMtaBlock, 0, st>>>(tab, scalar, alpha);
-    }
-    const int rc = launch_status();
-    if (rc) return rc;
-  }
-  return SUPA_AMD_OK;
-}
-
-template <typename T, int64_t CHUNK, int UNR>
-int launch_adamw(int32_t ntensors, void* const* params, void* const* grads, void* const* exp_avgs,
-                 void* const* exp_avg_sqs, void* const* max_exp_avg_sqs, void* const* state_steps,
-                 const int64_t* numel, const AdamHyper& h, hipStream_t st) {
-  int i = 0;
-  while (i < ntensors) {
-    AdamTable tab{};
-    uint32_t chunks = 0;
-    int nt = 0;
-    while (i < ntensors && nt < kMtaTensors) {
-      if (numel[i] < 0 || !state_steps[i]) return SUPA_AMD_EINVAL;
-      const int64_t c = (numel[i] + CHUNK - 1) / CHUNK;
-      if (c > (int64_t)0x7fffffff) return SUPA_AMD_ELAYOUT;
-      if ((int64_t)chunks + c > (int64_t)0x7fffffff) break;
-      if (numel[i] > 0) {
-        tab.p[nt] = params[i];
-        tab.g[nt] = grads[i];
-        tab.m[nt] = exp_avgs[i];
-        tab.v[nt] = exp_avg_sqs[i];
-        tab.vmax[nt] = h.amsgrad ? max_exp_avg_sqs[i] : nullptr;
-        tab.step[nt] = static_cast<const float*>(state_steps[i]);
-        tab.numel[nt] = numel[i];
-        tab.chunk_start[nt] = chunks;
-        chunks += (uint32_t)c;
-        ++nt;
-      }
-      ++i;
-    }
-    tab.chunk_start[nt] = chunks;
-    tab.ntensors = nt;
-    if (nt == 0) continue;
-    k_adamw<T, CHUNK, UNR><<<chunks, kMtaBlock, 0, st>>>(tab, h);
-    const int rc = launch_status();
-    if (rc) return rc;
-  }
-  return SUPA_AMD_OK;
-}
-
-}  // namespace sa
-
 extern "C" {
-
-int supa_amd_foreach_binary(int op, int32_t ntensors, void* const* out, void* const* a, void* const* b,
-                            const int64_t* numel, int32_t dtype, double scalar, double alpha, void* stream) {
-  if (ntensors < 0 || (ntensors > 0 && (!out || !a || !numel))) return SUPA_AMD_EINVAL;
-  if (op != SUPA_AMD_FOREACH_ADD && op != SUPA_AMD_FOREACH_MUL) return SUPA_AMD_EINVAL;
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  return with_mta_storage(dtype, [&](auto* tag) -> int {
-    using T = std::remove_pointer_t<decltype(tag)>;
-    if (b) return launch_foreach<T, chunk_one<T>()>(op, ntensors, out, a, b, numel, scalar, alpha, st);
-    return launch_foreach<T, 2 * chunk_one<T>()>(op, ntensors, out, a, b, numel, scalar, alpha, st);
-  });
-}
 
 int supa_amd_amp_unscale(int32_t ntensors, void* const* tensors, const int64_t* numel, int32_t dtype,
                          float* found_inf, const float* inv_scale, void* stream) {
@@ -393,33 +230,15 @@ int supa_amd_amp_unscale(int32_t ntensors, void* const* tensors, const int64_t* 
   return with_mta_storage(dtype, [&](auto* tag) -> int {
     using T = std::remove_pointer_t<decltype(tag)>;
     constexpr int64_t CHUNK = chunk_one<T>();
-    int i = 0;
-    while (i < ntensors) {
-      ForeachTable tab{};
-      uint32_t chunks = 0;
-      int nt = 0;
-      while (i < ntensors && nt < kMtaTensors) {
-        if (numel[i] < 0) return SUPA_AMD_EINVAL;
-        const int64_t c = (numel[i] + CHUNK - 1) / CHUNK;
-        if (c > (int64_t)0x7fffffff) return SUPA_AMD_ELAYOUT;
-        if ((int64_t)chunks + c > (int64_t)0x7fffffff) break;
-        if (numel[i] > 0) {
-          tab.out[nt] = tensors[i];
-          tab.numel[nt] = numel[i];
-          tab.chunk_start[nt] = chunks;
-          chunks += (uint32_t)c;
-          ++nt;
-        }
-        ++i;
-      }
-      tab.chunk_start[nt] = chunks;
-      tab.ntensors = nt;
-      if (nt == 0) continue;
-      k_amp_unscale<T, CHUNK><<<chunks, kMtaBlock, 0, st>>>(tab, found_inf, inv_scale);
-      const int rc = launch_status();
-      if (rc) return rc;
-    }
-    return SUPA_AMD_OK;
+    return mta_for_tables<CHUNK, UnscaleTable>(
+        ntensors, numel,
+        [&](UnscaleTable& tab, int slot, int i) -> int {
+          tab.x[slot] = tensors[i];
+          return SUPA_AMD_OK;
+        },
+        [&](const UnscaleTable& tab, uint32_t chunks) {
+          k_amp_unscale<T, CHUNK><<<chunks, kMtaBlock, 0, st>>>(tab, found_inf, inv_scale);
+        });
   });
 }
 
