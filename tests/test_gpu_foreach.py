@@ -248,3 +248,64 @@ def test_default_adamw_is_foreach_and_matches_single_tensor(amsgrad, no_fallback
         opt.step()
     for a, p in zip(results[0], ps):
         torch.testing.assert_close(a, p.detach(), rtol=1e-5, atol=1e-7)
+
+
+# ------------------------------------------- clip_grad_norm_ and its pieces
+def test_cat_and_stack(no_fallback):
+    a, b, e = torch.randn(3, 5), torch.randn(4, 5), torch.randn(0)
+    d = [t.to("supa") for t in (a, b, e)]
+    assert torch.equal(torch.cat(d).cpu(), torch.cat([a, b, e]))  # legacy 1-D empty input skipped
+    x, y = torch.randn(6, 2, 7), torch.randn(6, 3, 7).to(torch.bfloat16)
+    got = torch.cat([x.to("supa"), y.to("supa")], dim=1)
+    assert got.dtype == torch.float32 and torch.equal(got.cpu(), torch.cat([x, y], dim=1))  # type promotion
+    s = [torch.randn(()) for _ in range(5)]
+    assert torch.equal(torch.stack([t.to("supa") for t in s]).cpu(), torch.stack(s))
+    m = [torch.randn(4, 9) for _ in range(3)]
+    assert torch.equal(torch.stack([t.to("supa") for t in m], dim=1).cpu(), torch.stack(m, dim=1))
+    with pytest.raises(RuntimeError, match="Sizes of tensors must match"):
+        torch.cat([d[0], torch.randn(2, 4).to("supa")])
+
+
+def test_linalg_vector_norm(no_fallback):
+    x = torch.randn(1000, 37)
+    dx = x.to("supa")
+    for p in (1, 2, math.inf):
+        got = torch.linalg.vector_norm(dx, p)
+        assert got.dim() == 0 and got.dtype == torch.float32
+        assert got.item() == pytest.approx(O.vector_norm(x.double().numpy(), p), rel=1e-5)
+    assert torch.linalg.vector_norm(dx, 2, keepdim=True).shape == (1, 1)
+    h = torch.linalg.vector_norm(dx.bfloat16(), 2, dtype=torch.float32)
+    assert h.dtype == torch.float32
+    assert h.item() == pytest.approx(O.vector_norm(x.bfloat16().double().numpy(), 2), rel=1e-5)
+    assert torch.linalg.vector_norm(torch.zeros(0, device="supa")).item() == 0.0
+
+
+def test_linalg_vector_norm_other_cases_use_counted_fallback(supa):
+    """A reduction over some dims is not on the path: the CPU fallback runs
+    it, and counts it."""
+    x = torch.randn(40, 30)
+    supa.supa.reset_fallback_counts()
+    got = torch.linalg.vector_norm(x.to("supa"), 2, dim=0)
+    torch.testing.assert_close(got.cpu(), torch.linalg.vector_norm(x, 2, dim=0))
+    assert supa.supa.fallback_counts().get("aten::linalg_vector_norm", 0) == 1
+
+
+@pytest.mark.parametrize("norm_type", [2.0, math.inf])
+def test_clip_grad_norm(norm_type, no_fallback):
+    """torch.nn.utils.clip_grad_norm_ (foreach): _foreach_norm, stack,
+    linalg_vector_norm, clamp and _foreach_mul_.Tensor, all native."""
+    g = torch.Generator().manual_seed(12)
+    shapes = [(1024, 257), (257,), (33, 7)]
+    grads = [torch.randn(s, generator=g) for s in shapes]
+    ps = [torch.zeros(s, device="supa", requires_grad=True) for s in shapes]
+    ps_cpu = [torch.zeros(s, requires_grad=True) for s in shapes]
+    for p, pc, gr in zip(ps, ps_cpu, grads):
+        p.grad = gr.to("supa")
+        pc.grad = gr.clone()
+    total = torch.nn.utils.clip_grad_norm_(ps, max_norm=1.0, norm_type=norm_type)
+    total_cpu = torch.nn.utils.clip_grad_norm_(ps_cpu, max_norm=1.0, norm_type=norm_type)
+    whole = np.concatenate([gr.double().numpy().ravel() for gr in grads])
+    assert total.item() == pytest.approx(O.vector_norm(whole, norm_type), rel=1e-5)
+    assert total.item() == pytest.approx(total_cpu.item(), rel=1e-5)
+    for p, pc in zip(ps, ps_cpu):
+        torch.testing.assert_close(p.grad.cpu(), pc.grad, rtol=1e-5, atol=1e-9)

@@ -4,6 +4,7 @@
 #pragma once
 
 #include <ATen/ATen.h>
+#include <ATen/core/dispatch/Dispatcher.h>
 #include <c10/core/Device.h>
 #include <hip/hip_runtime_api.h>
 
@@ -71,6 +72,9 @@ void set_fused_bce_backward_enabled(bool on);
 bool fused_bce_backward_enabled();
 std::vector<std::pair<std::string, int64_t>> fallback_counts();
 void reset_fallback_counts();
+// The boxed CPU fallback itself (counted; an error while disabled), for
+// registered kernels that hand a case they do not cover over to it.
+void supa_cpu_fallback(const c10::OperatorHandle& op, std::vector<c10::IValue>* stack);
 
 // ------------------------------------------------------------ helpers
 inline int32_t dtype_code(c10::ScalarType t) { return static_cast<int32_t>(t); }

@@ -664,6 +664,52 @@ at::Tensor& lerp_t_out(const at::Tensor& s, const at::Tensor& e, const at::Tenso
   return out;
 }
 
+// ------------------------------------------------------------------ cat
+// cat (and stack, which upstream builds on it): each input is copied into
+// its slice of the output by the copy kernel.  Upstream's rules: one result
+// dtype over all inputs, legacy 1-D empty tensors skipped, every other input
+// equal to the first in all dims but `dim`.
+at::Tensor cat_supa(const at::ITensorListRef& tensors, int64_t dim) {
+  const auto ts = tensors.materialize();
+  TORCH_CHECK(!ts.empty(), "torch.cat(): expected a non-empty list of Tensors");
+  auto legacy_empty = [](const at::Tensor& t) { return t.dim() == 1 && t.size(0) == 0; };
+  const at::Tensor& first = ts[0].get();
+  const c10::ScalarType dt = at::native::result_type(tensors);
+  const at::Tensor* ref = nullptr;
+  for (size_t i = 0; i < ts.size(); ++i) {
+    const at::Tensor& t = ts[i].get();
+    TORCH_CHECK(t.device() == first.device(), "Expected all tensors to be on the same device, but found at least "
+                "two devices, ", first.device(), " and ", t.device(), "!");
+    TORCH_CHECK(t.dim() > 0, "zero-dimensional tensor (at position ", i, ") cannot be concatenated");
+    if (!ref && !legacy_empty(t)) ref = &t;
+  }
+  if (!ref) return at::empty({0}, first.options().dtype(dt));
+  const int64_t d = at::maybe_wrap_dim(dim, ref->dim());
+  std::vector<int64_t> size = ref->sizes().vec();
+  int64_t total = 0;
+  for (size_t i = 0; i < ts.size(); ++i) {
+    const at::Tensor& t = ts[i].get();
+    if (legacy_empty(t)) continue;
+    TORCH_CHECK(t.dim() == ref->dim(), "Tensors must have same number of dimensions: got ", ref->dim(), " and ",
+                t.dim());
+    for (int64_t k = 0; k < t.dim(); ++k)
+      TORCH_CHECK(k == d || t.size(k) == ref->size(k), "Sizes of tensors must match except in dimension ", d,
+                  ". Expected size ", ref->size(k), " but got size ", t.size(k), " for tensor number ", i,
+                  " in the list.");
+    total += t.size(d);
+  }
+  size[d] = total;
+  at::Tensor out = at::empty(size, first.options().dtype(dt));
+  int64_t off = 0;
+  for (const auto& r : ts) {
+    const at::Tensor& t = r.get();
+    if (legacy_empty(t) || t.size(d) == 0) continue;
+    out.narrow(d, off, t.size(d)).copy_(t);
+    off += t.size(d);
+  }
+  return out;
+}
+
 // ---------------------------------------------------------- activations
 enum class UKind { FloatOnly, IntToFloat, Any };
 
@@ -808,6 +854,7 @@ TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
   m.impl("div_.Tensor_mode", TORCH_FN(div_tm_));
   m.impl("div.out_mode", TORCH_FN(div_out_mode));
   // activations
+  m.impl("cat", TORCH_FN(cat_supa));
   m.impl("maximum", TORCH_FN(maximum_t));
   m.impl("maximum.out", TORCH_FN(maximum_out));
   m.impl("minimum", TORCH_FN(minimum_t));

@@ -11,7 +11,9 @@
 // path the upstream CompositeExplicitAutograd foreach kernels take: one
 // elementwise op per tensor (still on the supa kernels where they exist).
 #include <ATen/native/ForeachUtils.h>
+#include <ATen/native/CPUFallback.h>
 #include <ATen/ops/linalg_vector_norm.h>
+#include <ATen/ops/linalg_vector_norm_ops.h>
 #include <torch/library.h>
 
 #include <map>
@@ -281,39 +283,74 @@ void foreach_zero_(at::TensorList self) {
 }
 
 // --------------------------------------------------------------- norm
-// Per-tensor 1-, 2- and inf-norms in one pair of launches; the results are
-// views of one n-element tensor, as upstream's.  Other orders and dtypes take
-// the per-tensor linalg_vector_norm.
+bool norm_ord_ok(const c10::Scalar& ord, double* p) {
+  if (ord.isComplex()) return false;
+  *p = ord.toDouble();
+  return *p == 1.0 || *p == 2.0 || *p == HUGE_VAL;
+}
+
+// Norms of the listed (contiguous, one dtype) tensors into the n contiguous
+// elements of `out`, in one pair of launches.
+void norms_into(at::TensorList xs, double p, const at::Tensor& out, const char* name) {
+  const size_t n = xs.size();
+  std::vector<const void*> px(n);
+  std::vector<int64_t> numel(n);
+  for (size_t i = 0; i < n; ++i) {
+    px[i] = xs[i].data_ptr();
+    numel[i] = xs[i].numel();
+  }
+  const int32_t dt = dtype_code(xs[0].scalar_type());
+  const int64_t ws_bytes = supa_amd_foreach_norm_workspace_bytes((int32_t)n, numel.data(), dt);
+  TORCH_CHECK(ws_bytes >= 0, name, ": ", supa_amd_status_string((int)ws_bytes));
+  at::Tensor ws = at::empty({std::max<int64_t>(ws_bytes, 1)}, xs[0].options().dtype(at::kByte));
+  const int rc = supa_amd_foreach_norm((int32_t)n, px.data(), numel.data(), dt, p, out.data_ptr(),
+                                       dtype_code(out.scalar_type()), ws.data_ptr(), ws_bytes,
+                                       current_stream(xs[0].device().index()));
+  check_status(rc, name);
+}
+
+// Per-tensor 1-, 2- and inf-norms; the results are views of one n-element
+// tensor, as upstream's.  Other orders and dtypes take the per-tensor
+// linalg_vector_norm.
 std::vector<at::Tensor> foreach_norm(at::TensorList self, const c10::Scalar& ord, std::optional<at::ScalarType> dtype) {
   at::native::check_foreach_api_restrictions(self);
-  const double p = ord.isComplex() ? -1.0 : ord.toDouble();
+  double p = 0.0;
   const c10::ScalarType in_dt = self[0].scalar_type();
   const c10::ScalarType res_dt = dtype.value_or(in_dt);
-  const bool fast = fast_ok({self}) && (p == 1.0 || p == 2.0 || p == HUGE_VAL) &&
+  const bool fast = fast_ok({self}) && norm_ord_ok(ord, &p) &&
                     (res_dt == in_dt || res_dt == at::kFloat || res_dt == at::kDouble);
   std::vector<at::Tensor> res;
   if (!fast) {
     for (const auto& t : self) res.push_back(at::linalg_vector_norm(t, ord, at::OptionalIntArrayRef{}, false, dtype));
     return res;
   }
-  const size_t n = self.size();
-  std::vector<const void*> px(n);
-  std::vector<int64_t> numel(n);
-  for (size_t i = 0; i < n; ++i) {
-    px[i] = self[i].data_ptr();
-    numel[i] = self[i].numel();
-  }
-  const int32_t dt = dtype_code(in_dt);
-  const int64_t ws_bytes = supa_amd_foreach_norm_workspace_bytes((int32_t)n, numel.data(), dt);
-  TORCH_CHECK(ws_bytes >= 0, "_foreach_norm: ", supa_amd_status_string((int)ws_bytes));
-  at::Tensor out = at::empty({(int64_t)n}, self[0].options().dtype(res_dt));
-  at::Tensor ws = at::empty({std::max<int64_t>(ws_bytes, 1)}, self[0].options().dtype(at::kByte));
-  const int rc = supa_amd_foreach_norm((int32_t)n, px.data(), numel.data(), dt, p, out.data_ptr(), dtype_code(res_dt),
-                                       ws.data_ptr(), ws_bytes, current_stream(self[0].device().index()));
-  check_status(rc, "_foreach_norm");
-  res.reserve(n);
-  for (size_t i = 0; i < n; ++i) res.push_back(out.select(0, (int64_t)i));
+  at::Tensor out = at::empty({(int64_t)self.size()}, self[0].options().dtype(res_dt));
+  norms_into(self, p, out, "_foreach_norm");
+  res.reserve(self.size());
+  for (size_t i = 0; i < self.size(); ++i) res.push_back(out.select(0, (int64_t)i));
   return res;
+}
+
+// linalg_vector_norm over every element (dim None) of a contiguous tensor,
+// ord 1 / 2 / inf: the same kernels with a one-tensor list.  Reductions over
+// some dims, other orders, and the inf-norm of an empty tensor (an error
+// upstream) go to the CPU fallback, which counts them.
+at::Tensor vector_norm_supa(const at::Tensor& self, const c10::Scalar& ord, at::OptionalIntArrayRef dim,
+                            bool keepdim, std::optional<at::ScalarType> dtype) {
+  double p = 0.0;
+  const c10::ScalarType res_dt = dtype.value_or(self.scalar_type());
+  const bool all_dims = !dim.has_value() || dim->empty();
+  if (self.device().type() == kSupa && self.is_contiguous() && float_family(self.scalar_type()) && all_dims &&
+      norm_ord_ok(ord, &p) && !(p == HUGE_VAL && self.numel() == 0) &&
+      (res_dt == self.scalar_type() || res_dt == at::kFloat || res_dt == at::kDouble)) {
+    std::vector<int64_t> shape(keepdim ? self.dim() : 0, 1);
+    at::Tensor out = at::empty(shape, self.options().dtype(res_dt));
+    const at::Tensor list[1] = {self};
+    norms_into(at::TensorList(list, 1), p, out, "linalg_vector_norm");
+    return out;
+  }
+  return at::native::call_fallback_fn<&supa_cpu_fallback, at::_ops::linalg_vector_norm>::call(self, ord, dim, keepdim,
+                                                                                           dtype);
 }
 
 // ------------------------------------------------ registered signatures
@@ -619,6 +656,7 @@ TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
 #undef SUPA_FE_REG_UNARY
   m.impl("_foreach_zero_", TORCH_FN(foreach_zero_));
   m.impl("_foreach_norm.Scalar", TORCH_FN(foreach_norm));
+  m.impl("linalg_vector_norm", TORCH_FN(vector_norm_supa));
   m.impl("_fused_adamw_", TORCH_FN(fused_adamw_));
   m.impl("_fused_adamw_.tensor_lr", TORCH_FN(fused_adamw_tensor_lr_));
   m.impl("_amp_foreach_non_finite_check_and_unscale_", TORCH_FN(amp_unscale_));

@@ -445,6 +445,8 @@ std::atomic<bool> g_fallback_enabled{[] {
 std::mutex g_fb_mu;
 std::map<std::string, int64_t> g_fb_counts;
 
+}  // namespace
+
 void supa_cpu_fallback(const c10::OperatorHandle& op, torch::jit::Stack* stack) {
   const std::string name = c10::toString(op.schema().operator_name());
   {
@@ -455,8 +457,6 @@ void supa_cpu_fallback(const c10::OperatorHandle& op, torch::jit::Stack* stack) 
               " has no supa kernel and the CPU fallback is disabled");
   at::native::cpu_fallback(op, stack);
 }
-
-}  // namespace
 
 void set_cpu_fallback_enabled(bool on) { g_fallback_enabled.store(on); }
 bool cpu_fallback_enabled() { return g_fallback_enabled.load(); }
