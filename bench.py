@@ -271,6 +271,15 @@ def bench_c5(torch, timer, steps=10):
         p.grad = g
     ms = timer.time(opt.step, steps, warmup=1)
     res = {"fused_adamw_step": dict(entry(28 * P, ms), params=P)}
+    # The default implementation (foreach=None picks foreach on supa): eight
+    # list ops per step, 80P algorithmic bytes -- mul 8P, lerp 12P, mul 8P,
+    # addcmul 12P (grads read once), sqrt 8P, div 8P, add 8P, addcdiv 16P.
+    opt_fe = torch.optim.AdamW(params, lr=1e-4, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01)
+    res["foreach_adamw_step"] = dict(entry(80 * P, timer.time(opt_fe.step, steps, warmup=1)), params=P)
+    del opt_fe
+    # clip_grad_norm_ over the 72 gradients: _foreach_norm (4P) + _foreach_mul_ (8P)
+    res["clip_grad_norm_"] = entry(12 * P, timer.time(lambda: torch.nn.utils.clip_grad_norm_(params, 1e9), 3,
+                                                      warmup=1))
     with torch.no_grad():
         pd = [p.detach() for p in params]
         res["_foreach_add_List"] = entry(12 * P, timer.time(lambda: torch._foreach_add_(pd, grads), 3, warmup=1))
