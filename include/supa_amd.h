@@ -251,6 +251,18 @@ int supa_amd_log_softmax_backward(const void* grad, const void* output, int32_t 
                                   void* grad_in, int32_t gin_dtype, int64_t rows, int64_t cols,
                                   void* stream);
 
+/* out[r, :] = exp(x[r, :] - max_r) / sum(exp(x[r, :] - max_r)), dtypes as
+ * for log_softmax; a row holding NaN or +inf, or only -inf, is NaN.
+ * Replaces _softmax.out NF:5697 (upstream SoftMax.cu, PersistentSoftmax.cuh). */
+int supa_amd_softmax_forward(const void* in, int32_t in_dtype, void* out, int32_t out_dtype,
+                             int64_t rows, int64_t cols, void* stream);
+
+/* grad_in[r, :] = y[r, :] * (g[r, :] - sum(g[r, :] * y[r, :])), dtypes as
+ * for the log_softmax backward.  Replaces _softmax_backward_data.out NF:5709. */
+int supa_amd_softmax_backward(const void* grad, const void* output, int32_t gy_dtype,
+                              void* grad_in, int32_t gin_dtype, int64_t rows, int64_t cols,
+                              void* stream);
+
 /* ------------------------------------------------------------ nll_loss */
 
 /* nll_loss over logp [n, c] (contiguous, dtype f32/bf16/f16/f64), int64

@@ -60,6 +60,8 @@ def lib():
             "or_unary_backward_f32": (None, [c_int, _f32p, _f32p, _f32p, i64]),
             "or_log_softmax_fwd": (None, [_f32p, _f32p, i64, i64]),
             "or_log_softmax_bwd": (None, [_f32p, _f32p, _f32p, i64, i64]),
+            "or_softmax_fwd": (None, [_f32p, _f32p, i64, i64]),
+            "or_softmax_bwd": (None, [_f32p, _f32p, _f32p, i64, i64]),
             "or_nll_loss_fwd": (c_int, [_f32p, _i64p, _f32p, i64, i64, c_int, i64, _f32p, _f32p]),
             "or_nll_loss_bwd": (c_int, [_f32p, _i64p, _f32p, i64, i64, c_int, i64, c_float, c_int, _f32p]),
             "or_loss_fwd": (None, [c_int, _f32p, _f32p, _f32p, _f32p, i64, c_int, c_float, _f32p]),
@@ -195,6 +197,25 @@ def log_softmax_backward(g, y) -> np.ndarray:
     rows = g.size // max(cols, 1)
     out = np.empty(g.shape, np.float32)
     lib().or_log_softmax_bwd(_p(g, _f32p), _p(y, _f32p), _p(out, _f32p), rows, cols)
+    return out
+
+
+def softmax(x) -> np.ndarray:
+    """softmax over the last dim (float32 in, float32 out)."""
+    x = _c(x, np.float32)
+    cols = x.shape[-1]
+    rows = x.size // max(cols, 1)
+    out = np.empty(x.shape, np.float32)
+    lib().or_softmax_fwd(_p(x, _f32p), _p(out, _f32p), rows, cols)
+    return out
+
+
+def softmax_backward(g, y) -> np.ndarray:
+    g, y = _c(g, np.float32), _c(y, np.float32)
+    cols = g.shape[-1]
+    rows = g.size // max(cols, 1)
+    out = np.empty(g.shape, np.float32)
+    lib().or_softmax_bwd(_p(g, _f32p), _p(y, _f32p), _p(out, _f32p), rows, cols)
     return out
 
 

@@ -291,6 +291,34 @@ void or_log_softmax_bwd(const float* g, const float* y, float* gin, int64_t rows
   }
 }
 
+/* _softmax (NF:5690; upstream SoftMax.cu epilogue exp(x - max) / sum): the
+ * row max as float, the sum of exp(x - max) in double, each output
+ * exp(x - max) / sum in double rounded to float. */
+void or_softmax_fwd(const float* x, float* out, int64_t rows, int64_t cols) {
+  for (int64_t r = 0; r < rows; ++r) {
+    const float* xr = x + r * cols;
+    float* o = out + r * cols;
+    float mx = -INFINITY;
+    for (int64_t c = 0; c < cols; ++c) mx = (xr[c] > mx || isnan(xr[c])) ? xr[c] : mx;
+    double s = 0.0;
+    for (int64_t c = 0; c < cols; ++c) s += exp((double)xr[c] - (double)mx);
+    for (int64_t c = 0; c < cols; ++c) o[c] = (float)(exp((double)xr[c] - (double)mx) / s);
+  }
+}
+
+/* _softmax_backward_data (NF:5704; upstream SoftMaxBackwardEpilogue):
+ * gI = out * (gO - sum(gO * out)) per row, the sum in double rounded to float. */
+void or_softmax_bwd(const float* g, const float* y, float* gin, int64_t rows, int64_t cols) {
+  for (int64_t r = 0; r < rows; ++r) {
+    const float* gr = g + r * cols;
+    const float* yr = y + r * cols;
+    double s = 0.0;
+    for (int64_t c = 0; c < cols; ++c) s += (double)gr[c] * (double)yr[c];
+    const float sf = (float)s;
+    for (int64_t c = 0; c < cols; ++c) gin[r * cols + c] = yr[c] * (gr[c] - sf);
+  }
+}
+
 /* ------------------------------------------------------------- nll_loss -- */
 
 /* nll_loss_forward (NF:11928; reference semantics CrossEntropyLossKernel.cu:71-119

@@ -288,6 +288,56 @@ def test_cross_entropy_small_rows(dtype, no_fallback):
         assert bf16_ulp_dist(bits(dl.grad), O.f32_to_bf16(gin)).max() <= 1
 
 
+# ------------------------------------------------------------- softmax
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("shape", [(7, 13), (33, 1000), (5, 70000), (4, 128256)])
+def test_softmax_forward_backward(shape, dtype, no_fallback):
+    """_softmax and _softmax_backward_data against the oracle: register-resident
+    rows, the streaming kernels (rows too long for registers), odd widths."""
+    x = seeded(shape, 90, 3.0, dtype)
+    g = seeded(shape, 91, 1.0, dtype)
+    dx = dev(x).requires_grad_()
+    y = torch.softmax(dx, -1)
+    y.backward(dev(g))
+    yc = y.detach().cpu()
+    ref_y = O.softmax(x.float().numpy())
+    ref_gi = O.softmax_backward(g.float().numpy(), yc.float().numpy())
+    gi = dx.grad.cpu()
+    if dtype == torch.float32:
+        np.testing.assert_allclose(yc.numpy(), ref_y, rtol=1e-5, atol=1e-12)
+        np.testing.assert_allclose(gi.numpy(), ref_gi, rtol=1e-5, atol=1e-9)
+    elif dtype == torch.bfloat16:
+        assert bf16_ulp_dist(bits(yc), O.f32_to_bf16(ref_y)).max() <= 1
+        scale = np.abs(ref_gi).max()
+        np.testing.assert_allclose(gi.float().numpy(), ref_gi, rtol=1e-2, atol=1e-2 * scale)
+    else:
+        np.testing.assert_allclose(yc.float().numpy(), ref_y, rtol=2e-3, atol=1e-7)
+        np.testing.assert_allclose(gi.float().numpy(), ref_gi, rtol=2e-3, atol=2e-3 * np.abs(ref_gi).max())
+
+
+def test_softmax_dims_and_edges(no_fallback):
+    x = seeded((6, 50, 9), 92, 2.0)
+    dx = dev(x)
+    for d in (0, 1, 2):
+        ref = np.moveaxis(O.softmax(np.moveaxis(x.numpy(), d, -1)), -1, d)
+        np.testing.assert_allclose(torch.softmax(dx, d).cpu().numpy(), ref, rtol=1e-5, atol=1e-12)
+    # NaN / +inf rows turn NaN, all -inf rows are NaN, the rest untouched
+    e = seeded((4, 100), 93)
+    e[0, 3], e[1, 9] = float("nan"), float("inf")
+    e[2] = float("-inf")
+    got = torch.softmax(dev(e), -1).cpu()
+    assert got[:3].isnan().all() and not got[3].isnan().any()
+    assert torch.allclose(got[3], torch.softmax(e[3], -1), rtol=1e-5, atol=1e-9)
+    # 0-dim and empty
+    assert torch.softmax(dev(torch.tensor(3.0)), 0).item() == 1.0
+    assert torch.softmax(torch.zeros(0, 5, device="supa"), -1).shape == (0, 5)
+    # half_to_float
+    xb = seeded((8, 4096), 94, 2.0, torch.bfloat16)
+    h = torch._softmax(dev(xb), -1, True)
+    assert h.dtype == torch.float32
+    np.testing.assert_allclose(h.cpu().numpy(), O.softmax(xb.float().numpy()), rtol=1e-5, atol=1e-12)
+
+
 # ---------------------------------------------------- fused cross-entropy
 CE_TOL = {torch.float32: 1e-5, torch.bfloat16: 1e-2, torch.float16: 2e-3}
 

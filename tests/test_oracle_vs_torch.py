@@ -144,6 +144,28 @@ def test_log_softmax_invariants():
     np.testing.assert_allclose(gi.astype(np.float64).sum(-1), 0.0, atol=5e-5)
 
 
+def test_softmax_vs_cpu_and_invariants():
+    x = randn((64, 3000), 24, 3.0)
+    y = O.softmax(x.numpy())
+    np.testing.assert_allclose(y, F.softmax(x, -1).numpy(), rtol=1e-6, atol=1e-9)
+    np.testing.assert_allclose(y.astype(np.float64).sum(-1), 1.0, atol=1e-5)
+    # softmax = exp(log_softmax)
+    np.testing.assert_allclose(y, np.exp(O.log_softmax(x.numpy()).astype(np.float64)), rtol=1e-5, atol=1e-9)
+    assert np.all(O.softmax(np.zeros((2, 1000), np.float32)) == np.float32(1e-3))
+    # a NaN or +inf anywhere makes the row NaN; the other rows are untouched
+    bad = x[:3].clone().numpy()
+    bad[0, 5], bad[1, 7] = np.nan, np.inf
+    yb = O.softmax(bad)
+    assert np.isnan(yb[0]).all() and np.isnan(yb[1]).all() and not np.isnan(yb[2]).any()
+    # backward against autograd on the CPU, and rows summing to zero
+    g = randn((64, 3000), 25)
+    xr = x.clone().requires_grad_()
+    F.softmax(xr, -1).backward(g)
+    gi = O.softmax_backward(g.numpy(), y)
+    np.testing.assert_allclose(gi, xr.grad.numpy(), rtol=1e-5, atol=1e-8)  # g - sum cancels
+    np.testing.assert_allclose(gi.astype(np.float64).sum(-1), 0.0, atol=1e-7)
+
+
 @pytest.mark.parametrize("reduction", ["mean", "sum", "none"])
 @pytest.mark.parametrize("weighted", [False, True])
 def test_nll_and_cross_entropy_vs_cpu(reduction, weighted):

@@ -1,7 +1,7 @@
 // PrivateUse1 registrations of the loss path: sum/mean reductions,
 // mse_loss / smooth_l1_loss / binary_cross_entropy_with_logits (forward with
-// fused reductions, and the mse / smooth_l1 gradients), _log_softmax and its
-// backward, nll_loss forward / backward.
+// fused reductions, and the mse / smooth_l1 gradients), _log_softmax and
+// _softmax with their backwards, nll_loss forward / backward.
 //
 // cross_entropy_loss is registered the way the reference registers it
 // (SUPANativeFunctions::cross_entropy_loss, CrossEntropyLoss.cpp:140-151): by
@@ -292,8 +292,10 @@ at::Tensor& smooth_l1_loss_backward_out(const at::Tensor& grad, const at::Tensor
 // ------------------------------------------------------------ log_softmax
 // Runs `fn(rows, cols)` on contiguous row-major views with `dim` last; the
 // result is returned in the original dim order, contiguous.
-at::Tensor& log_softmax_into(const at::Tensor& self, int64_t dim, bool half_to_float, at::Tensor& out,
-                             const char* name) {
+// log_softmax (LOG) and softmax share the layout handling: the reduced dim
+// is moved last (a copy when it is not), rows run through the row kernels.
+at::Tensor& softmax_into(bool log, const at::Tensor& self, int64_t dim, bool half_to_float, at::Tensor& out,
+                         const char* name) {
   TORCH_CHECK(is_float_dtype(self.scalar_type()), name, ": expected a floating-point input, got ", self.scalar_type());
   if (half_to_float)
     TORCH_CHECK(self.scalar_type() == at::kHalf || self.scalar_type() == at::kBFloat16,
@@ -308,7 +310,7 @@ at::Tensor& log_softmax_into(const at::Tensor& self, int64_t dim, bool half_to_f
   }
   if (self.numel() == 0) return out;
   if (self.dim() == 0) {
-    out.fill_(0);
+    out.fill_(log ? 0 : 1);
     return out;
   }
   const bool last = d == self.dim() - 1;
@@ -316,22 +318,30 @@ at::Tensor& log_softmax_into(const at::Tensor& self, int64_t dim, bool half_to_f
   const int64_t cols = x.size(-1);
   const int64_t rows = x.numel() / cols;
   at::Tensor res = (last && out.is_contiguous()) ? out : empty_supa(x.sizes(), odt, self.device().index());
-  const int rc = supa_amd_log_softmax_forward(x.data_ptr(), dtype_code(x.scalar_type()), res.data_ptr(),
-                                              dtype_code(odt), rows, cols, current_stream(self.device().index()));
+  const auto fwd = log ? supa_amd_log_softmax_forward : supa_amd_softmax_forward;
+  const int rc = fwd(x.data_ptr(), dtype_code(x.scalar_type()), res.data_ptr(), dtype_code(odt), rows, cols,
+                     current_stream(self.device().index()));
   check_status(rc, name);
   if (!res.is_same(out)) out.copy_(last ? res : res.movedim(-1, d));
   return out;
 }
 at::Tensor log_softmax(const at::Tensor& self, int64_t dim, bool half_to_float) {
   at::Tensor out;
-  return log_softmax_into(self, dim, half_to_float, out, "_log_softmax");
+  return softmax_into(true, self, dim, half_to_float, out, "_log_softmax");
 }
 at::Tensor& log_softmax_out(const at::Tensor& self, int64_t dim, bool half_to_float, at::Tensor& out) {
-  return log_softmax_into(self, dim, half_to_float, out, "_log_softmax.out");
+  return softmax_into(true, self, dim, half_to_float, out, "_log_softmax.out");
+}
+at::Tensor softmax(const at::Tensor& self, int64_t dim, bool half_to_float) {
+  at::Tensor out;
+  return softmax_into(false, self, dim, half_to_float, out, "_softmax");
+}
+at::Tensor& softmax_out(const at::Tensor& self, int64_t dim, bool half_to_float, at::Tensor& out) {
+  return softmax_into(false, self, dim, half_to_float, out, "_softmax.out");
 }
 
-at::Tensor& log_softmax_bwd_into(const at::Tensor& grad, const at::Tensor& output, int64_t dim,
-                                 c10::ScalarType input_dtype, at::Tensor& gi, const char* name) {
+at::Tensor& softmax_bwd_into(bool log, const at::Tensor& grad, const at::Tensor& output, int64_t dim,
+                             c10::ScalarType input_dtype, at::Tensor& gi, const char* name) {
   TORCH_CHECK(grad.sizes() == output.sizes(), name, ": grad and output sizes differ");
   const int64_t d = at::maybe_wrap_dim(dim, std::max<int64_t>(grad.dim(), 1));
   if (gi.defined()) at::native::resize_output(gi, grad.sizes());
@@ -351,8 +361,9 @@ at::Tensor& log_softmax_bwd_into(const at::Tensor& grad, const at::Tensor& outpu
   at::Tensor res = (last && gi.is_contiguous() && gi.scalar_type() == kdt)
                        ? gi
                        : empty_supa(g.sizes(), kdt, grad.device().index());
-  const int rc = supa_amd_log_softmax_backward(g.data_ptr(), y.data_ptr(), dtype_code(gdt), res.data_ptr(),
-                                               dtype_code(kdt), rows, cols, current_stream(grad.device().index()));
+  const auto bwd = log ? supa_amd_log_softmax_backward : supa_amd_softmax_backward;
+  const int rc = bwd(g.data_ptr(), y.data_ptr(), dtype_code(gdt), res.data_ptr(), dtype_code(kdt), rows, cols,
+                     current_stream(grad.device().index()));
   check_status(rc, name);
   if (!res.is_same(gi)) gi.copy_(last ? res : res.movedim(-1, d));
   return gi;
@@ -360,11 +371,20 @@ at::Tensor& log_softmax_bwd_into(const at::Tensor& grad, const at::Tensor& outpu
 at::Tensor log_softmax_backward(const at::Tensor& grad, const at::Tensor& output, int64_t dim,
                                 c10::ScalarType input_dtype) {
   at::Tensor gi;
-  return log_softmax_bwd_into(grad, output, dim, input_dtype, gi, "_log_softmax_backward_data");
+  return softmax_bwd_into(true, grad, output, dim, input_dtype, gi, "_log_softmax_backward_data");
 }
 at::Tensor& log_softmax_backward_out(const at::Tensor& grad, const at::Tensor& output, int64_t dim,
                                      c10::ScalarType input_dtype, at::Tensor& gi) {
-  return log_softmax_bwd_into(grad, output, dim, input_dtype, gi, "_log_softmax_backward_data.out");
+  return softmax_bwd_into(true, grad, output, dim, input_dtype, gi, "_log_softmax_backward_data.out");
+}
+at::Tensor softmax_backward(const at::Tensor& grad, const at::Tensor& output, int64_t dim,
+                            c10::ScalarType input_dtype) {
+  at::Tensor gi;
+  return softmax_bwd_into(false, grad, output, dim, input_dtype, gi, "_softmax_backward_data");
+}
+at::Tensor& softmax_backward_out(const at::Tensor& grad, const at::Tensor& output, int64_t dim,
+                                 c10::ScalarType input_dtype, at::Tensor& gi) {
+  return softmax_bwd_into(false, grad, output, dim, input_dtype, gi, "_softmax_backward_data.out");
 }
 
 // --------------------------------------------------------------- nll_loss
@@ -663,6 +683,10 @@ TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
   m.impl("_log_softmax.out", TORCH_FN(log_softmax_out));
   m.impl("_log_softmax_backward_data", TORCH_FN(log_softmax_backward));
   m.impl("_log_softmax_backward_data.out", TORCH_FN(log_softmax_backward_out));
+  m.impl("_softmax", TORCH_FN(softmax));
+  m.impl("_softmax.out", TORCH_FN(softmax_out));
+  m.impl("_softmax_backward_data", TORCH_FN(softmax_backward));
+  m.impl("_softmax_backward_data.out", TORCH_FN(softmax_backward_out));
   m.impl("nll_loss_forward", TORCH_FN(nll_loss_forward));
   m.impl("nll_loss_forward.output", TORCH_FN(nll_loss_forward_out));
   m.impl("nll_loss_backward", TORCH_FN(nll_loss_backward));

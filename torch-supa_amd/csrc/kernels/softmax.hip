@@ -1,5 +1,5 @@
-// log_softmax forward / backward over the last dim of a contiguous
-// [rows, cols] tensor.
+// log_softmax and softmax, forward and backward, over the last dim of a
+// contiguous [rows, cols] tensor.
 //
 // Main path (16-byte aligned rows of up to 1024 threads x VPT vectors): one
 // 1024-thread workgroup per row holds the whole row in registers, so the
@@ -14,9 +14,10 @@
 // Fallback (any cols, any alignment): one 256-thread workgroup per row,
 // online max/sum in a first pass over memory, the output in a second pass.
 //
-// Replaces _log_softmax.out (NF:3752) and _log_softmax_backward_data.out
-// (NF:3763), upstream SoftMax.cu / PersistentSoftmax.cuh in the reference's
-// operator library.
+// Replaces _log_softmax.out (NF:3752), _log_softmax_backward_data.out
+// (NF:3763), _softmax.out and _softmax_backward_data.out, upstream SoftMax.cu /
+// PersistentSoftmax.cuh in the reference's operator library.  softmax's
+// epilogue is exp(x - max) * (1 / sum) and its gradient y (g - sum(g y)).
 #include "devmath.h"
 #include "ew_launch.h"
 
@@ -150,7 +151,7 @@ __device__ __forceinline__ void lse_combine(float& m, float& s, float m2, float 
   m = M;
 }
 
-template <typename TI, typename TO, int VPT>
+template <typename TI, typename TO, int VPT, bool LOG>
 __global__ void __launch_bounds__(kRowBlock)
 k_lsm_fwd_reg(const TI* __restrict__ in, TO* __restrict__ out, int64_t rows, int64_t cols) {
   constexpr int V = VecOf<TI>::V;
@@ -198,7 +199,11 @@ k_lsm_fwd_reg(const TI* __restrict__ in, TO* __restrict__ out, int64_t rows, int
     float M = lds_m[0], S = lds_s[0];
 #pragma unroll
     for (int w = 1; w < NW; ++w) lse_combine(M, S, lds_m[w], lds_s[w]);
-    const float logsum = sa_logf(S);
+    // log: (x - M) - log S;  softmax: 2^(x log2e - M log2e) / S with the
+    // scaled max of the sum (an all -inf row gives 0 * inf = NaN, as upstream)
+    const float logsum = LOG ? sa_logf(S) : 0.0f;
+    const float inv = LOG ? 0.0f : 1.0f / S;
+    const float Mb = (M == -__builtin_inff() ? 0.0f : M) * kLog2e;
     opaque<VPT>(x);
     Vec<TO, V>* dst = reinterpret_cast<Vec<TO, V>*>(out + row * cols);
 #pragma unroll
@@ -206,7 +211,10 @@ k_lsm_fwd_reg(const TI* __restrict__ in, TO* __restrict__ out, int64_t rows, int
       if (j < full || tid + j * kRowBlock < nvec) {
         float f[V];
 #pragma unroll
-        for (int k = 0; k < V; ++k) f[k] = (elem_f<TI>(x[j], k) - M) - logsum;
+        for (int k = 0; k < V; ++k) {
+          if constexpr (LOG) f[k] = (elem_f<TI>(x[j], k) - M) - logsum;
+          else f[k] = __builtin_amdgcn_exp2f(fmaf(elem_f<TI>(x[j], k), kLog2e, -Mb)) * inv;
+        }
         store_row_vec<TO, V>(dst, tid + j * kRowBlock, f);
       }
     }
@@ -214,7 +222,7 @@ k_lsm_fwd_reg(const TI* __restrict__ in, TO* __restrict__ out, int64_t rows, int
 }
 
 // Streaming fallback: any cols.
-template <typename TI, typename TO>
+template <typename TI, typename TO, bool LOG>
 __global__ void __launch_bounds__(kBlock)
 k_lsm_fwd_stream(const TI* __restrict__ in, TO* __restrict__ out, int64_t cols) {
   __shared__ float lds[kBlock / 64];
@@ -226,9 +234,14 @@ k_lsm_fwd_stream(const TI* __restrict__ in, TO* __restrict__ out, int64_t cols) 
   float s = 0.0f;
   for (int64_t c = threadIdx.x; c < cols; c += kBlock) s += fast_exp((float)to_arith(x[c]) - mb);
   s = block_sum_all<kBlock / 64>(s, lds);
-  const float logsum = sa_logf(s);
   TO* o = out + (int64_t)blockIdx.x * cols;
-  for (int64_t c = threadIdx.x; c < cols; c += kBlock) o[c] = from_arith<TO>(((float)to_arith(x[c]) - m) - logsum);
+  if constexpr (LOG) {
+    const float logsum = sa_logf(s);
+    for (int64_t c = threadIdx.x; c < cols; c += kBlock) o[c] = from_arith<TO>(((float)to_arith(x[c]) - m) - logsum);
+  } else {
+    const float inv = 1.0f / s;
+    for (int64_t c = threadIdx.x; c < cols; c += kBlock) o[c] = from_arith<TO>(fast_exp((float)to_arith(x[c]) - mb) * inv);
+  }
 }
 
 // ------------------------------------------------------------ backward
@@ -307,6 +320,63 @@ k_lsm_bwd_stream(const TG* __restrict__ grad, const TG* __restrict__ outp, TO* _
     gin[base + c] = from_arith<TO>(fmaf(-fast_exp((float)to_arith(outp[base + c])), s, (float)to_arith(grad[base + c])));
 }
 
+// softmax backward: gi = y (g - sum(g y)).  Both rows stay in registers
+// (up to 8 vectors each per thread); longer rows take the streaming kernel.
+template <typename TG, typename TO, int VPT>
+__global__ void __launch_bounds__(kRowBlock)
+k_sm_bwd_reg(const TG* __restrict__ grad, const TG* __restrict__ outp, TO* __restrict__ gin, int64_t cols) {
+  constexpr int V = VecOf<TG>::V;
+  __shared__ float lds[kRowBlock / 64];
+  const int64_t row = blockIdx.x;
+  const uint4* g = reinterpret_cast<const uint4*>(grad + row * cols);
+  const uint4* y = reinterpret_cast<const uint4*>(outp + row * cols);
+  const int nvec = (int)(cols / V);
+  const int full = nvec / kRowBlock;
+  const int tid = threadIdx.x;
+  uint4 gv[VPT], yv[VPT];
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    if (j < full || tid + j * kRowBlock < nvec) {
+      gv[j] = ld_stream(g + tid + j * kRowBlock);
+      yv[j] = ld_stream(y + tid + j * kRowBlock);
+    }
+  }
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    if (j < full || tid + j * kRowBlock < nvec) {
+#pragma unroll
+      for (int k = 0; k < V; ++k) s = fmaf(elem_f<TG>(gv[j], k), elem_f<TG>(yv[j], k), s);
+    }
+  }
+  s = block_sum_all<kRowBlock / 64>(s, lds);
+  opaque<VPT>(gv);
+  opaque<VPT>(yv);
+  Vec<TO, V>* dst = reinterpret_cast<Vec<TO, V>*>(gin + row * cols);
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    if (j < full || tid + j * kRowBlock < nvec) {
+      float f[V];
+#pragma unroll
+      for (int k = 0; k < V; ++k) f[k] = elem_f<TG>(yv[j], k) * (elem_f<TG>(gv[j], k) - s);
+      store_row_vec<TO, V>(dst, tid + j * kRowBlock, f);
+    }
+  }
+}
+
+template <typename TG, typename TO>
+__global__ void __launch_bounds__(kBlock)
+k_sm_bwd_stream(const TG* __restrict__ grad, const TG* __restrict__ outp, TO* __restrict__ gin, int64_t cols) {
+  __shared__ float lds[kBlock / 64];
+  const int64_t base = (int64_t)blockIdx.x * cols;
+  float s = 0.0f;
+  for (int64_t c = threadIdx.x; c < cols; c += kBlock)
+    s = fmaf((float)to_arith(grad[base + c]), (float)to_arith(outp[base + c]), s);
+  s = block_sum_all<kBlock / 64>(s, lds);
+  for (int64_t c = threadIdx.x; c < cols; c += kBlock)
+    gin[base + c] = from_arith<TO>((float)to_arith(outp[base + c]) * ((float)to_arith(grad[base + c]) - s));
+}
+
 template <typename F>
 int with_float_storage(int dtype, F&& f) {
   switch (dtype) {
@@ -317,14 +387,9 @@ int with_float_storage(int dtype, F&& f) {
   }
 }
 
-}  // namespace sa
-
-using namespace sa;
-
-extern "C" {
-
-int supa_amd_log_softmax_forward(const void* in, int32_t in_dtype, void* out, int32_t out_dtype, int64_t rows,
-                                 int64_t cols, void* stream) {
+template <bool LOG>
+int softmax_forward(const void* in, int32_t in_dtype, void* out, int32_t out_dtype, int64_t rows, int64_t cols,
+                    void* stream) {
   if (!in || !out || rows < 0 || cols < 0 || rows >= (int64_t(1) << 31)) return SUPA_AMD_EINVAL;
   if (rows == 0 || cols == 0) return SUPA_AMD_OK;
   hipStream_t st = static_cast<hipStream_t>(stream);
@@ -341,18 +406,34 @@ int supa_amd_log_softmax_forward(const void* in, int32_t in_dtype, void* out, in
         const TI* pi = static_cast<const TI*>(in);
         TO* po = static_cast<TO*>(out);
         const unsigned grid = (unsigned)std::min<int64_t>(rows, kLsmGrid);
-        if (vpt <= 1) k_lsm_fwd_reg<TI, TO, 1><<<grid, kRowBlock, 0, st>>>(pi, po, rows, cols);
-        else if (vpt <= 2) k_lsm_fwd_reg<TI, TO, 2><<<grid, kRowBlock, 0, st>>>(pi, po, rows, cols);
-        else if (vpt <= 4) k_lsm_fwd_reg<TI, TO, 4><<<grid, kRowBlock, 0, st>>>(pi, po, rows, cols);
-        else if (vpt <= 8) k_lsm_fwd_reg<TI, TO, 8><<<grid, kRowBlock, 0, st>>>(pi, po, rows, cols);
-        else k_lsm_fwd_reg<TI, TO, 16><<<grid, kRowBlock, 0, st>>>(pi, po, rows, cols);
+        if (vpt <= 1) k_lsm_fwd_reg<TI, TO, 1, LOG><<<grid, kRowBlock, 0, st>>>(pi, po, rows, cols);
+        else if (vpt <= 2) k_lsm_fwd_reg<TI, TO, 2, LOG><<<grid, kRowBlock, 0, st>>>(pi, po, rows, cols);
+        else if (vpt <= 4) k_lsm_fwd_reg<TI, TO, 4, LOG><<<grid, kRowBlock, 0, st>>>(pi, po, rows, cols);
+        else if (vpt <= 8) k_lsm_fwd_reg<TI, TO, 8, LOG><<<grid, kRowBlock, 0, st>>>(pi, po, rows, cols);
+        else k_lsm_fwd_reg<TI, TO, 16, LOG><<<grid, kRowBlock, 0, st>>>(pi, po, rows, cols);
         return launch_status();
       }
-      k_lsm_fwd_stream<TI, TO><<<(unsigned)rows, kBlock, 0, st>>>(static_cast<const TI*>(in), static_cast<TO*>(out),
-                                                                  cols);
+      k_lsm_fwd_stream<TI, TO, LOG><<<(unsigned)rows, kBlock, 0, st>>>(static_cast<const TI*>(in),
+                                                                       static_cast<TO*>(out), cols);
       return launch_status();
     });
   });
+}
+
+}  // namespace sa
+
+using namespace sa;
+
+extern "C" {
+
+int supa_amd_log_softmax_forward(const void* in, int32_t in_dtype, void* out, int32_t out_dtype, int64_t rows,
+                                 int64_t cols, void* stream) {
+  return softmax_forward<true>(in, in_dtype, out, out_dtype, rows, cols, stream);
+}
+
+int supa_amd_softmax_forward(const void* in, int32_t in_dtype, void* out, int32_t out_dtype, int64_t rows,
+                             int64_t cols, void* stream) {
+  return softmax_forward<false>(in, in_dtype, out, out_dtype, rows, cols, stream);
 }
 
 int supa_amd_log_softmax_backward(const void* grad, const void* output, int32_t gy_dtype, void* grad_in,
@@ -382,6 +463,37 @@ int supa_amd_log_softmax_backward(const void* grad, const void* output, int32_t 
         return launch_status();
       }
       k_lsm_bwd_stream<TG, TO><<<(unsigned)rows, kBlock, 0, st>>>(pg, py, po, cols);
+      return launch_status();
+    });
+  });
+}
+
+int supa_amd_softmax_backward(const void* grad, const void* output, int32_t gy_dtype, void* grad_in,
+                              int32_t gin_dtype, int64_t rows, int64_t cols, void* stream) {
+  if (!grad || !output || !grad_in || rows < 0 || cols < 0 || rows >= (int64_t(1) << 31)) return SUPA_AMD_EINVAL;
+  if (rows == 0 || cols == 0) return SUPA_AMD_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return with_float_storage(gy_dtype, [&](auto* tg) -> int {
+    return with_float_storage(gin_dtype, [&](auto* to) -> int {
+      using TG = std::remove_pointer_t<decltype(tg)>;
+      using TO = std::remove_pointer_t<decltype(to)>;
+      if (gy_dtype != gin_dtype && gin_dtype != SUPA_AMD_F32) return SUPA_AMD_EDTYPE;
+      constexpr int V = VecOf<TG>::V;
+      const bool reg_ok = (cols % V) == 0 && aligned(grad, 16) && aligned(output, 16) && aligned(grad_in, V * sizeof(TO)) &&
+                          (cols / V) <= 8 * kRowBlock;
+      const TG* pg = static_cast<const TG*>(grad);
+      const TG* py = static_cast<const TG*>(output);
+      TO* po = static_cast<TO*>(grad_in);
+      if (reg_ok) {
+        const int64_t nvec = cols / V;
+        const int vpt = (int)((nvec + kRowBlock - 1) / kRowBlock);
+        if (vpt <= 1) k_sm_bwd_reg<TG, TO, 1><<<(unsigned)rows, kRowBlock, 0, st>>>(pg, py, po, cols);
+        else if (vpt <= 2) k_sm_bwd_reg<TG, TO, 2><<<(unsigned)rows, kRowBlock, 0, st>>>(pg, py, po, cols);
+        else if (vpt <= 4) k_sm_bwd_reg<TG, TO, 4><<<(unsigned)rows, kRowBlock, 0, st>>>(pg, py, po, cols);
+        else k_sm_bwd_reg<TG, TO, 8><<<(unsigned)rows, kRowBlock, 0, st>>>(pg, py, po, cols);
+        return launch_status();
+      }
+      k_sm_bwd_stream<TG, TO><<<(unsigned)rows, kBlock, 0, st>>>(pg, py, po, cols);
       return launch_status();
     });
   });
