@@ -287,6 +287,26 @@ int supa_amd_nll_loss_backward(const void* grad_out, int32_t dtype, const int64_
                                int reduction, int64_t ignore_index, void* grad_in,
                                int32_t* error_flag, void* stream);
 
+/* nll_loss2d over logp [n, c, s] (contiguous; s = H * W), int64 target
+ * [n, s]: out [n, s] for `none`, else the weighted sum or mean and
+ * total_weight as for nll_loss.  The mean/sum forward reduces in two stages
+ * through `workspace` (supa_amd_nll_loss2d_workspace_bytes(), no content
+ * requirement).  Replaces nll_loss2d_forward.output NF:11960 (upstream
+ * LossNLL2d.cu). */
+int64_t supa_amd_nll_loss2d_workspace_bytes(void);
+int supa_amd_nll_loss2d_forward(const void* logp, int32_t dtype, const int64_t* target,
+                                const void* weight, int64_t n, int64_t c, int64_t s, int reduction,
+                                int64_t ignore_index, void* out, void* total_weight, void* workspace,
+                                int64_t ws_bytes, int32_t* error_flag, void* stream);
+
+/* grad_in [n, c, s]: every element written once, -w[t] g at (i, t[i, p], p)
+ * and zero elsewhere (g per position for `none`, g / total_weight for
+ * mean).  Replaces nll_loss2d_backward.grad_input NF:11974. */
+int supa_amd_nll_loss2d_backward(const void* grad_out, int32_t dtype, const int64_t* target,
+                                 const void* weight, const void* total_weight, int64_t n, int64_t c,
+                                 int64_t s, int reduction, int64_t ignore_index, void* grad_in,
+                                 int32_t* error_flag, void* stream);
+
 /* ------------------------------------------------- fused cross-entropy
  * cross_entropy over contiguous logits [n, c] (f32 / bf16 / f16) with int64
  * targets [n], no class weight, no label smoothing: the forward reads the

@@ -249,6 +249,26 @@ def nll_loss_backward(grad_out, target, n, c, total_weight, weight=None, reducti
     return out
 
 
+def nll_loss2d(logp, target, weight=None, reduction="mean", ignore_index=-100):
+    """nll_loss2d (NF:11967; upstream LossNLL2d): the [N, C, H, W] problem is
+    nll_loss over the N*H*W positions, each a row of C log-probabilities.
+    Returns (output [N, H, W] or scalar, total_weight)."""
+    logp = np.asarray(logp, np.float32)
+    n, c, h, w = logp.shape
+    rows = np.ascontiguousarray(np.moveaxis(logp, 1, -1).reshape(-1, c))
+    out, tw = nll_loss(rows, np.asarray(target, np.int64).reshape(-1), weight, reduction, ignore_index)
+    return (out.reshape(n, h, w) if reduction == "none" else out), tw
+
+
+def nll_loss2d_backward(grad_out, target, shape, total_weight, weight=None, reduction="mean",
+                        ignore_index=-100, bf16=False) -> np.ndarray:
+    """grad_input [N, C, H, W] of nll_loss2d (NF:11981), through the row form."""
+    n, c, h, w = shape
+    g = nll_loss_backward(np.asarray(grad_out, np.float32).reshape(-1), np.asarray(target, np.int64).reshape(-1),
+                          n * h * w, c, total_weight, weight, reduction, ignore_index, bf16)
+    return np.ascontiguousarray(np.moveaxis(g.reshape(n, h, w, c), -1, 1))
+
+
 def amp_unscale(x, inv_scale):
     """Returns (x * inv_scale as float32, found_inf)."""
     x = np.array(x, np.float32, copy=True).reshape(-1)

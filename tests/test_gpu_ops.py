@@ -338,6 +338,59 @@ def test_softmax_dims_and_edges(no_fallback):
     np.testing.assert_allclose(h.cpu().numpy(), O.softmax(xb.float().numpy()), rtol=1e-5, atol=1e-12)
 
 
+# ----------------------------------------------------------- nll_loss2d
+@pytest.mark.parametrize("shape", [(3, 21, 17, 24), (2, 5, 7, 9)])
+@pytest.mark.parametrize("reduction", ["none", "mean", "sum"])
+@pytest.mark.parametrize("weighted", [False, True])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_nll_loss2d(dtype, weighted, reduction, shape, no_fallback):
+    """nll_loss2d forward and backward against the oracle (the row form over
+    the N*H*W positions); the backward is exact, as the 2-D one is."""
+    N, C, H, W = shape
+    g = torch.Generator().manual_seed(97)
+    lp = (torch.randn(shape, generator=g) * 2 - 3).to(dtype)
+    t = torch.randint(0, C, (N, H, W), generator=g)
+    t.view(-1)[torch.randperm(t.numel(), generator=g)[:7]] = -100
+    w = (torch.rand(C, generator=g) + 0.5).to(dtype) if weighted else None
+    red = {"none": 0, "mean": 1, "sum": 2}[reduction]
+    out, tw = torch.ops.aten.nll_loss2d_forward(dev(lp), dev(t), None if w is None else dev(w), red, -100)
+    wn = None if w is None else w.float().numpy()
+    ref, rtw = O.nll_loss2d(lp.float().numpy(), t.numpy(), wn, reduction, -100)
+    if reduction == "none":
+        assert torch.equal(out.cpu(), torch.from_numpy(ref).to(dtype))
+    else:
+        tol = 1e-5 if dtype == torch.float32 else 1e-2
+        assert abs(out.float().item() - float(ref)) <= tol * abs(float(ref))
+        assert tw.float().item() == pytest.approx(float(rtw), rel=tol)
+    go = (torch.randn((N, H, W), generator=g) if reduction == "none" else torch.tensor(1.3)).to(dtype)
+    gi = torch.ops.aten.nll_loss2d_backward(dev(go), dev(lp), dev(t), None if w is None else dev(w), red, -100, tw)
+    twv = float(tw.float().item())
+    ref_gi = O.nll_loss2d_backward(go.float().numpy(), t.numpy(), shape, twv, wn, reduction, -100,
+                                   bf16=dtype == torch.bfloat16)
+    want = O.round_bf16(ref_gi) if dtype == torch.bfloat16 else ref_gi
+    assert np.array_equal(gi.float().cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_spatial_cross_entropy(dtype, no_fallback):
+    """F.cross_entropy on [N, C, H, W] logits (log_softmax over dim 1, then
+    nll_loss2d) and on [N, C, L] (upstream reshapes to 4-D) against the CPU."""
+    g = torch.Generator().manual_seed(98)
+    for shape, tshape in (((4, 19, 32, 40), (4, 32, 40)), ((2, 11, 300), (2, 300))):
+        x = (torch.randn(shape, generator=g) * 2).to(dtype)
+        t = torch.randint(0, shape[1], tshape, generator=g)
+        t.view(-1)[:5] = -100
+        dx = dev(x).requires_grad_()
+        loss = F.cross_entropy(dx, dev(t), ignore_index=-100, label_smoothing=0.0)
+        loss.backward()
+        xc = x.float().clone().requires_grad_()
+        ref = F.cross_entropy(xc, t, ignore_index=-100)
+        ref.backward()
+        tol = 1e-5 if dtype == torch.float32 else 2e-2
+        assert loss.float().item() == pytest.approx(ref.item(), rel=tol)
+        torch.testing.assert_close(dx.grad.float().cpu(), xc.grad, rtol=tol, atol=tol * xc.grad.abs().max().item())
+
+
 # ---------------------------------------------------- fused cross-entropy
 CE_TOL = {torch.float32: 1e-5, torch.bfloat16: 1e-2, torch.float16: 2e-3}
 

@@ -460,3 +460,28 @@ def test_vector_norm_vs_cpu_and_closed_forms():
     assert O.vector_norm(np.zeros(0), 2) == 0.0
     assert math.isnan(O.vector_norm(np.array([1.0, float("nan")]), float("inf")))
     assert math.isnan(O.vector_norm(np.array([1.0, float("nan")]), 2))
+
+
+@pytest.mark.parametrize("reduction", ["mean", "sum", "none"])
+@pytest.mark.parametrize("weighted", [False, True])
+def test_nll_loss2d_vs_cpu(reduction, weighted):
+    g = torch.Generator().manual_seed(96)
+    N, C, H, W = 3, 7, 5, 6
+    lp = F.log_softmax(torch.randn(N, C, H, W, generator=g) * 2, 1)
+    t = torch.randint(0, C, (N, H, W), generator=g)
+    t[0, 1, 2] = t[2, 4, 0] = -100
+    w = (torch.rand(C, generator=g) + 0.5) if weighted else None
+    lpr = lp.clone().requires_grad_()
+    ref = F.nll_loss(lpr, t, weight=w, ignore_index=-100, reduction=reduction)
+    out, tw = O.nll_loss2d(lp.numpy(), t.numpy(), None if w is None else w.numpy(), reduction, -100)
+    np.testing.assert_allclose(out, ref.detach().numpy(), rtol=1e-6, atol=1e-7)
+    go = torch.randn(ref.shape, generator=g) if reduction == "none" else torch.tensor(1.0)
+    ref.backward(go)
+    gi = O.nll_loss2d_backward(go.numpy(), t.numpy(), (N, C, H, W), float(tw),
+                               None if w is None else w.numpy(), reduction, -100)
+    np.testing.assert_allclose(gi, lpr.grad.numpy(), rtol=1e-6, atol=1e-8)
+    # total weight (mean/sum): the weight sum over the positions that count
+    wt = np.ones(C, np.float32) if w is None else w.numpy()
+    tf = t.numpy().ravel()
+    if reduction != "none":
+        assert float(tw) == pytest.approx(float(wt[tf[tf != -100]].sum()), rel=1e-6)

@@ -1,7 +1,7 @@
 // PrivateUse1 registrations of the loss path: sum/mean reductions,
 // mse_loss / smooth_l1_loss / binary_cross_entropy_with_logits (forward with
 // fused reductions, and the mse / smooth_l1 gradients), _log_softmax and
-// _softmax with their backwards, nll_loss forward / backward.
+// _softmax with their backwards, nll_loss and nll_loss2d forward / backward.
 //
 // cross_entropy_loss is registered the way the reference registers it
 // (SUPANativeFunctions::cross_entropy_loss, CrossEntropyLoss.cpp:140-151): by
@@ -483,6 +483,110 @@ at::Tensor& nll_loss_backward_out(const at::Tensor& grad, const at::Tensor& self
   return nll_bwd_into(grad, self, target, weight, reduction, ignore_index, total_weight, gi);
 }
 
+// ------------------------------------------------------------ nll_loss2d
+// [N, C, H, W] log-probabilities with [N, H, W] targets (what
+// cross_entropy uses for inputs of more than two dims) on the spatial nll
+// kernels; the checks and messages are upstream's (LossNLL2d.cpp).
+void nll2d_checks(const at::Tensor& self, const at::Tensor& target, const at::Tensor& weight) {
+  TORCH_CHECK(target.dim() == 3, "only batches of spatial targets supported (3D tensors) but got targets of dimension: ",
+              target.dim());
+  TORCH_CHECK(self.dim() == 4, "only batches of spatial inputs supported (4D tensors), but got input of dimension: ",
+              self.dim());
+  TORCH_CHECK(!weight.defined() || weight.numel() == self.size(1),
+              "weight tensor should be defined either for all or no classes");
+  TORCH_CHECK(self.size(0) == target.size(0) && self.size(2) == target.size(1) && self.size(3) == target.size(2),
+              "input and target batch or spatial sizes don't match: target ", target.sizes(), ", input ",
+              self.sizes());
+  TORCH_CHECK(target.scalar_type() == at::kLong, "nll_loss2d: expected target of scalar type Long but found ",
+              target.scalar_type());
+  TORCH_CHECK(is_float_dtype(self.scalar_type()), "nll_loss2d: expected a floating-point input");
+}
+
+std::tuple<at::Tensor&, at::Tensor&> nll2d_fwd_into(const at::Tensor& self, const at::Tensor& target,
+                                                    const std::optional<at::Tensor>& weight_opt, int64_t reduction,
+                                                    int64_t ignore_index, at::Tensor& out, at::Tensor& tw) {
+  const at::Tensor weight = weight_opt.has_value() ? *weight_opt : at::Tensor();
+  nll2d_checks(self, target, weight);
+  const int red = reduction_code(reduction);
+  const int64_t n = self.size(0), c = self.size(1), sp = self.size(2) * self.size(3);
+  const auto dev = self.device().index();
+  std::vector<int64_t> oshape;
+  if (red == SUPA_AMD_REDUCTION_NONE) oshape = {n, self.size(2), self.size(3)};
+  if (out.defined()) at::native::resize_output(out, oshape);
+  else out = empty_supa(oshape, self.scalar_type(), dev);
+  if (tw.defined()) at::native::resize_output(tw, {});
+  else tw = empty_supa({}, self.scalar_type(), dev);
+  at::Tensor x = self.contiguous();
+  at::Tensor t = target.contiguous();
+  at::Tensor w = weight.defined() ? to_dtype(weight, self.scalar_type()).contiguous() : at::Tensor();
+  if (red == SUPA_AMD_REDUCTION_NONE) tw.zero_();
+  at::Tensor res = out.is_contiguous() ? out : empty_supa(oshape, self.scalar_type(), dev);
+  const DeviceScratch& s = device_scratch(dev);
+  const int rc = supa_amd_nll_loss2d_forward(x.data_ptr(), dtype_code(x.scalar_type()), t.data_ptr<int64_t>(),
+                                             w.defined() ? w.data_ptr() : nullptr, n, c, sp, red, ignore_index,
+                                             res.data_ptr(), tw.data_ptr(), s.reduce_ws, s.reduce_ws_bytes,
+                                             s.error_flag, current_stream(dev));
+  check_status(rc, "nll_loss2d_forward");
+  if (!res.is_same(out)) out.copy_(res);
+  return {out, tw};
+}
+std::tuple<at::Tensor, at::Tensor> nll_loss2d_forward(const at::Tensor& self, const at::Tensor& target,
+                                                      const std::optional<at::Tensor>& weight, int64_t reduction,
+                                                      int64_t ignore_index) {
+  at::Tensor out, tw;
+  nll2d_fwd_into(self, target, weight, reduction, ignore_index, out, tw);
+  return {out, tw};
+}
+std::tuple<at::Tensor&, at::Tensor&> nll_loss2d_forward_out(const at::Tensor& self, const at::Tensor& target,
+                                                            const std::optional<at::Tensor>& weight,
+                                                            int64_t reduction, int64_t ignore_index, at::Tensor& out,
+                                                            at::Tensor& tw) {
+  return nll2d_fwd_into(self, target, weight, reduction, ignore_index, out, tw);
+}
+
+at::Tensor& nll2d_bwd_into(const at::Tensor& grad, const at::Tensor& self, const at::Tensor& target,
+                           const std::optional<at::Tensor>& weight_opt, int64_t reduction, int64_t ignore_index,
+                           const at::Tensor& total_weight, at::Tensor& gi) {
+  const at::Tensor weight = weight_opt.has_value() ? *weight_opt : at::Tensor();
+  nll2d_checks(self, target, weight);
+  const int red = reduction_code(reduction);
+  const int64_t n = self.size(0), c = self.size(1), sp = self.size(2) * self.size(3);
+  const auto dev = self.device().index();
+  TORCH_CHECK(total_weight.numel() == 1, "expected total_weight to be a single element tensor, got: ",
+              total_weight.sizes(), " (", total_weight.numel(), " elements)");
+  if (red == SUPA_AMD_REDUCTION_NONE) {
+    TORCH_CHECK(grad.dim() == 3 && grad.size(0) == n && grad.size(1) == self.size(2) && grad.size(2) == self.size(3),
+                "nll_loss2d_backward: expected grad_output of size ", target.sizes(), ", got ", grad.sizes());
+  } else {
+    TORCH_CHECK(grad.numel() == 1, "nll_loss2d_backward: expected a single-element grad_output");
+  }
+  if (gi.defined()) at::native::resize_output(gi, self.sizes());
+  else gi = empty_supa(self.sizes(), self.scalar_type(), dev);
+  at::Tensor res = gi.is_contiguous() ? gi : empty_supa(self.sizes(), self.scalar_type(), dev);
+  at::Tensor g = to_dtype(grad, self.scalar_type()).contiguous();
+  at::Tensor t = target.contiguous();
+  at::Tensor w = weight.defined() ? to_dtype(weight, self.scalar_type()).contiguous() : at::Tensor();
+  at::Tensor tw = to_dtype(total_weight, self.scalar_type());
+  const DeviceScratch& s = device_scratch(dev);
+  const int rc = supa_amd_nll_loss2d_backward(g.data_ptr(), dtype_code(self.scalar_type()), t.data_ptr<int64_t>(),
+                                              w.defined() ? w.data_ptr() : nullptr, tw.data_ptr(), n, c, sp, red,
+                                              ignore_index, res.data_ptr(), s.error_flag, current_stream(dev));
+  check_status(rc, "nll_loss2d_backward");
+  if (!res.is_same(gi)) gi.copy_(res);
+  return gi;
+}
+at::Tensor nll_loss2d_backward(const at::Tensor& grad, const at::Tensor& self, const at::Tensor& target,
+                               const std::optional<at::Tensor>& weight, int64_t reduction, int64_t ignore_index,
+                               const at::Tensor& total_weight) {
+  at::Tensor gi;
+  return nll2d_bwd_into(grad, self, target, weight, reduction, ignore_index, total_weight, gi);
+}
+at::Tensor& nll_loss2d_backward_out(const at::Tensor& grad, const at::Tensor& self, const at::Tensor& target,
+                                    const std::optional<at::Tensor>& weight, int64_t reduction, int64_t ignore_index,
+                                    const at::Tensor& total_weight, at::Tensor& gi) {
+  return nll2d_bwd_into(grad, self, target, weight, reduction, ignore_index, total_weight, gi);
+}
+
 // ------------------------------------------ BCE-with-logits autograd
 // binary_cross_entropy_with_logits' input gradient, the autograd formula
 // (binary_cross_entropy_with_logits_backward of upstream's FunctionsManual;
@@ -691,6 +795,10 @@ TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
   m.impl("nll_loss_forward.output", TORCH_FN(nll_loss_forward_out));
   m.impl("nll_loss_backward", TORCH_FN(nll_loss_backward));
   m.impl("nll_loss_backward.grad_input", TORCH_FN(nll_loss_backward_out));
+  m.impl("nll_loss2d_forward", TORCH_FN(nll_loss2d_forward));
+  m.impl("nll_loss2d_forward.output", TORCH_FN(nll_loss2d_forward_out));
+  m.impl("nll_loss2d_backward", TORCH_FN(nll_loss2d_backward));
+  m.impl("nll_loss2d_backward.grad_input", TORCH_FN(nll_loss2d_backward_out));
   m.impl("cross_entropy_loss", TORCH_FN(cross_entropy_loss));
 }
 

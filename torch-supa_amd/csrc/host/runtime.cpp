@@ -107,7 +107,8 @@ const DeviceScratch& device_scratch(c10::DeviceIndex d) {
   if (!s.reduce_ws) {
     const auto prev = current_device();
     if (prev != d) set_device(d);
-    const int64_t ws = std::max(supa_amd_sum_workspace_bytes(0), supa_amd_loss_workspace_bytes(0));
+    const int64_t ws = std::max({supa_amd_sum_workspace_bytes(0), supa_amd_loss_workspace_bytes(0),
+                                 supa_amd_nll_loss2d_workspace_bytes()});
     const int64_t ws_rounded = (ws + 255) / 256 * 256;
     void* p = nullptr;
     SUPA_HIP_CHECK(hipMalloc(&p, ws_rounded + 256));

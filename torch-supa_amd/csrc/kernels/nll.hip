@@ -12,9 +12,16 @@
 // zeros, with the row's target element replaced by its gradient -- so the
 // [n, c] tensor costs one HBM write and no separate zero fill.
 //
+// Spatial form (nll_loss2d: logp [n, c, s], target [n, s], s = H * W): the
+// forward gathers with a multi-workgroup two-stage reduction (a fixed number
+// of partials, so the order is deterministic); the backward writes every
+// element of grad_input once in 16-byte vectors along s, each vector's
+// (image, class) found by two magic-number divisions.
+//
 // Out-of-range targets set *error_flag (when given) and contribute nothing;
 // the host reads the flag lazily.
 #include "ew_launch.h"
+#include "divmod.h"
 
 namespace sa {
 
@@ -127,6 +134,123 @@ k_nll_bwd(const T* __restrict__ grad_out, const int64_t* __restrict__ target, co
   }
 }
 
+// ------------------------------------------------------- spatial (2d)
+constexpr int kNll2dParts = 512;  // partial (value, weight) pairs of the forward
+
+// Row i of the [n * s] target is image i / s, position i % s; its selected
+// log-probability is logp[(i / s) * c * s + t * s + i % s].
+template <typename T, typename ACC>
+__global__ void __launch_bounds__(kBlock)
+k_nll2d_fwd_partial(const T* __restrict__ logp, const int64_t* __restrict__ target, const T* __restrict__ weight,
+                    int64_t rows, int64_t c, int64_t s, int64_t ignore_index, int none, T* __restrict__ out,
+                    ACC* __restrict__ ws, int32_t* error_flag) {
+  __shared__ ACC lds_v[kBlock / 64];
+  __shared__ ACC lds_w[kBlock / 64];
+  ACC v = ACC(0), w = ACC(0);
+  bool bad = false;
+  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < rows; i += (int64_t)gridDim.x * kBlock) {
+    const int64_t t = target[i];
+    if (t == ignore_index || t < 0 || t >= c) {
+      bad = bad || t != ignore_index;
+      if (none) out[i] = from_arith<T>(ACC(0));
+      continue;
+    }
+    const int64_t img = i / s, pos = i - img * s;
+    const ACC wt = weight ? (ACC)to_arith(weight[t]) : ACC(1);
+    const ACC term = -wt * (ACC)to_arith(logp[(img * c + t) * s + pos]);
+    if (none) {
+      out[i] = from_arith<T>(term);
+    } else {
+      v += term;
+      w += wt;
+    }
+  }
+  if (bad && error_flag) *error_flag = 1;
+  if (none) return;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    v += __shfl_xor(v, off, 64);
+    w += __shfl_xor(w, off, 64);
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) {
+    lds_v[wave] = v;
+    lds_w[wave] = w;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    ACC sv = ACC(0), sw = ACC(0);
+#pragma unroll
+    for (int k = 0; k < kBlock / 64; ++k) {
+      sv += lds_v[k];
+      sw += lds_w[k];
+    }
+    ws[2 * blockIdx.x] = sv;
+    ws[2 * blockIdx.x + 1] = sw;
+  }
+}
+
+// Stage 2: one wavefront adds the partials in a fixed order.
+template <typename T, typename ACC>
+__global__ void __launch_bounds__(64)
+k_nll2d_fwd_final(const ACC* __restrict__ ws, int nparts, int mean, T* __restrict__ out, T* __restrict__ total_weight) {
+  ACC v = ACC(0), w = ACC(0);
+  for (int k = threadIdx.x; k < nparts; k += 64) {
+    v += ws[2 * k];
+    w += ws[2 * k + 1];
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    v += __shfl_xor(v, off, 64);
+    w += __shfl_xor(w, off, 64);
+  }
+  if (threadIdx.x == 0) {
+    total_weight[0] = from_arith<T>(w);
+    out[0] = from_arith<T>(mean ? v / w : v);
+  }
+}
+
+// grad_in [n, c, s], one VEC-wide vector along s per thread (s % VEC == 0;
+// VEC = 1 otherwise).  The element (img, k, pos) is the gradient when
+// target[img, pos] == k, else zero.
+template <typename T, int VEC>
+__global__ void __launch_bounds__(kBlock)
+k_nll2d_bwd(const T* __restrict__ grad_out, const int64_t* __restrict__ target, const T* __restrict__ weight,
+            const T* __restrict__ total_weight, uint32_t nvec, FastDiv vps, FastDiv cdiv, int64_t s,
+            int reduction, int64_t ignore_index, T* __restrict__ gin, int32_t* error_flag) {
+  using C = opmath_t<T>;
+  const uint32_t v = blockIdx.x * kBlock + threadIdx.x;
+  if (v >= nvec) return;
+  uint32_t nc, sv, img, k;
+  vps.divmod(v, nc, sv);
+  cdiv.divmod(nc, img, k);
+  const int64_t c = cdiv.d;
+  const int64_t pos0 = (int64_t)sv * VEC;
+  C gsc = C(0);
+  if (reduction == SUPA_AMD_REDUCTION_MEAN) gsc = (C)to_arith(grad_out[0]) / (C)to_arith(total_weight[0]);
+  else if (reduction == SUPA_AMD_REDUCTION_SUM) gsc = (C)to_arith(grad_out[0]);
+  const C wk = weight ? (C)to_arith(weight[k]) : C(1);
+  Vec<T, VEC> o;
+  bool bad = false;
+#pragma unroll
+  for (int j = 0; j < VEC; ++j) {
+    const int64_t r = (int64_t)img * s + pos0 + j;
+    const int64_t t = target[r];
+    bad = bad || (t != ignore_index && (t < 0 || t >= c));
+    C val = C(0);
+    if (t == (int64_t)k && t != ignore_index) {
+      const C g = reduction == SUPA_AMD_REDUCTION_NONE ? (C)to_arith(grad_out[r]) : gsc;
+      const T gs = from_arith<T>(-g);  // rounded to the storage type, as upstream forms it
+      val = weight ? wk * (C)to_arith(gs) : (C)to_arith(gs);
+    }
+    o.v[j] = from_arith<T>(val);
+  }
+  if (bad && k == 0 && error_flag) *error_flag = 1;
+  T* dst = gin + ((int64_t)nc * s + pos0);
+  if constexpr (VEC > 1) st_stream(reinterpret_cast<Vec<T, VEC>*>(dst), o);
+  else dst[0] = o.v[0];
+}
+
 template <typename F>
 int with_nll_storage(int dtype, F&& f) {
   switch (dtype) {
@@ -212,6 +336,71 @@ int supa_amd_nll_loss_backward(const void* grad_out, int32_t dtype, const int64_
       dim3 grid((unsigned)((c + kBlock * kNllUnroll - 1) / (kBlock * kNllUnroll)), (unsigned)n);
       k_nll_bwd<T, 1><<<grid, kBlock, 0, st>>>(g, target, w, tw, c, reduction, ignore_index, gi, error_flag);
     }
+    return launch_status();
+  });
+}
+
+int64_t supa_amd_nll_loss2d_workspace_bytes(void) { return 2 * kNll2dParts * (int64_t)sizeof(double); }
+
+int supa_amd_nll_loss2d_forward(const void* logp, int32_t dtype, const int64_t* target, const void* weight,
+                                int64_t n, int64_t c, int64_t s, int reduction, int64_t ignore_index, void* out,
+                                void* total_weight, void* workspace, int64_t ws_bytes, int32_t* error_flag,
+                                void* stream) {
+  if (n < 0 || c < 0 || s < 0 || !out) return SUPA_AMD_EINVAL;
+  const int64_t rows = n * s;
+  if (rows > 0 && (!logp || !target)) return SUPA_AMD_EINVAL;
+  const bool none = reduction == SUPA_AMD_REDUCTION_NONE;
+  if (!none && reduction != SUPA_AMD_REDUCTION_MEAN && reduction != SUPA_AMD_REDUCTION_SUM) return SUPA_AMD_EINVAL;
+  if (!none && !total_weight) return SUPA_AMD_EINVAL;
+  if (!none && (!workspace || ws_bytes < supa_amd_nll_loss2d_workspace_bytes())) return SUPA_AMD_EWORKSPACE;
+  if (none && rows == 0) return SUPA_AMD_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return with_nll_storage(dtype, [&](auto* tag) -> int {
+    using T = std::remove_pointer_t<decltype(tag)>;
+    using ACC = typename std::conditional<std::is_same<T, double>::value, double, float>::type;
+    const int parts = (int)std::max<int64_t>(1, std::min<int64_t>(kNll2dParts, (rows + kBlock - 1) / kBlock));
+    ACC* ws = static_cast<ACC*>(workspace);
+    k_nll2d_fwd_partial<T, ACC><<<parts, kBlock, 0, st>>>(static_cast<const T*>(logp), target,
+                                                          static_cast<const T*>(weight), rows, c, s, ignore_index,
+                                                          none ? 1 : 0, static_cast<T*>(out), ws, error_flag);
+    int rc = launch_status();
+    if (rc || none) return rc;
+    k_nll2d_fwd_final<T, ACC><<<1, 64, 0, st>>>(ws, parts, reduction == SUPA_AMD_REDUCTION_MEAN ? 1 : 0,
+                                                static_cast<T*>(out), static_cast<T*>(total_weight));
+    return launch_status();
+  });
+}
+
+int supa_amd_nll_loss2d_backward(const void* grad_out, int32_t dtype, const int64_t* target, const void* weight,
+                                 const void* total_weight, int64_t n, int64_t c, int64_t s, int reduction,
+                                 int64_t ignore_index, void* grad_in, int32_t* error_flag, void* stream) {
+  if (n < 0 || c < 0 || s < 0) return SUPA_AMD_EINVAL;
+  if (n == 0 || c == 0 || s == 0) return SUPA_AMD_OK;
+  if (!grad_out || !target || !grad_in) return SUPA_AMD_EINVAL;
+  if (reduction != SUPA_AMD_REDUCTION_NONE && reduction != SUPA_AMD_REDUCTION_MEAN &&
+      reduction != SUPA_AMD_REDUCTION_SUM)
+    return SUPA_AMD_EINVAL;
+  if (reduction == SUPA_AMD_REDUCTION_MEAN && !total_weight) return SUPA_AMD_EINVAL;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return with_nll_storage(dtype, [&](auto* tag) -> int {
+    using T = std::remove_pointer_t<decltype(tag)>;
+    constexpr int VEC = 16 / sizeof(T);
+    const bool vec_ok = (s % VEC) == 0 && aligned(grad_in, 16);
+    const int64_t per = vec_ok ? s / VEC : s;  // vectors per (image, class) row
+    const int64_t nvec = n * c * per;
+    // 32-bit magic division: every quotient and dividend below 2^31
+    if (nvec >= (int64_t(1) << 31) || per >= (int64_t(1) << 31) || c >= (int64_t(1) << 31)) return SUPA_AMD_ELAYOUT;
+    const T* g = static_cast<const T*>(grad_out);
+    const T* w = static_cast<const T*>(weight);
+    const T* tw = static_cast<const T*>(total_weight);
+    T* gi = static_cast<T*>(grad_in);
+    const unsigned grid = (unsigned)((nvec + kBlock - 1) / kBlock);
+    if (vec_ok)
+      k_nll2d_bwd<T, VEC><<<grid, kBlock, 0, st>>>(g, target, w, tw, (uint32_t)nvec, FastDiv((uint32_t)per),
+                                                    FastDiv((uint32_t)c), s, reduction, ignore_index, gi, error_flag);
+    else
+      k_nll2d_bwd<T, 1><<<grid, kBlock, 0, st>>>(g, target, w, tw, (uint32_t)nvec, FastDiv((uint32_t)per),
+                                                  FastDiv((uint32_t)c), s, reduction, ignore_index, gi, error_flag);
     return launch_status();
   });
 }
