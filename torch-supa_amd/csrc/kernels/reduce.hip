@@ -311,9 +311,9 @@ struct SmoothL1TermFactory {
   double beta;
   template <typename C> SmoothL1TermOp<C> make() const { return SmoothL1TermOp<C>{static_cast<C>(beta)}; }
 };
-template <bool PW, bool W>
+template <bool PW, bool W, bool HW = false>
 struct BceTermFactory {
-  template <typename C> BceTermOp<PW, W, C> make() const { return BceTermOp<PW, W, C>{}; }
+  template <typename C> BceTermOp<PW, W, C, HW> make() const { return BceTermOp<PW, W, C, HW>{}; }
   template <typename C> static constexpr bool ok() { return std::is_floating_point<C>::value; }
 };
 struct MseTermEwFactory {
@@ -414,11 +414,12 @@ int supa_amd_loss_forward(const supa_amd_ew_desc* d, int loss, int reduction, do
       return run_reduce(SmoothL1TermFactory{beta}, &e, scale, workspace, workspace_bytes, stream);
     case SUPA_AMD_LOSS_BCE_LOGITS:
       if (has_pos_weight && has_weight)
-        return run_reduce(BceTermFactory<true, true>{}, &e, scale, workspace, workspace_bytes, stream);
+        return run_reduce(BceTermFactory<true, true, true>{}, &e, scale, workspace, workspace_bytes, stream);
       if (has_pos_weight)
-        return run_reduce(BceTermFactory<true, false>{}, &e, scale, workspace, workspace_bytes, stream);
-      if (has_weight) return run_reduce(BceTermFactory<false, true>{}, &e, scale, workspace, workspace_bytes, stream);
-      return run_reduce(BceTermFactory<false, false>{}, &e, scale, workspace, workspace_bytes, stream);
+        return run_reduce(BceTermFactory<true, false, true>{}, &e, scale, workspace, workspace_bytes, stream);
+      if (has_weight)
+        return run_reduce(BceTermFactory<false, true, true>{}, &e, scale, workspace, workspace_bytes, stream);
+      return run_reduce(BceTermFactory<false, false, true>{}, &e, scale, workspace, workspace_bytes, stream);
     default: return SUPA_AMD_EINVAL;
   }
 }
