@@ -136,12 +136,15 @@ int supa_amd_pointwise(const supa_amd_ew_desc* d, int op, double value, int64_t 
 #define SUPA_AMD_RECIPROCAL 10
 #define SUPA_AMD_ABS 11
 #define SUPA_AMD_SQRT 12
+#define SUPA_AMD_EXPM1 13
+#define SUPA_AMD_LOG1P 14
 
 /* out = f(x), floating dtypes (RELU, NEG and ABS also integer).  op = {out, x}.
  * Replaces the reference's upstream-ATen activation kernels: gelu.out NF:5216,
  * silu.out NF:5374, sigmoid.out NF:5441, tanh.out, exp.out, log.out, erf.out,
- * relu, neg.out, and the pointwise helpers reciprocal.out (x.__rtruediv__),
- * abs.out, sqrt.out (IEEE 1/x, |x|, correctly rounded sqrt). */
+ * relu, neg.out, expm1.out NF:2650, log1p.out NF:3585, and the pointwise
+ * helpers reciprocal.out (x.__rtruediv__), abs.out, sqrt.out (IEEE 1/x, |x|,
+ * correctly rounded sqrt). */
 int supa_amd_unary(const supa_amd_ew_desc* d, int op, void* stream);
 
 /* grad_in = f'(...) * dy.  op = {grad_in, dy, x} where x is the forward input
@@ -149,6 +152,34 @@ int supa_amd_unary(const supa_amd_ew_desc* d, int op, void* stream);
  * Replaces gelu_backward.grad_input NF:5245, silu_backward.grad_input NF:5383,
  * sigmoid_backward.grad_input NF:13229, tanh_backward.grad_input. */
 int supa_amd_unary_backward(const supa_amd_ew_desc* d, int op, void* stream);
+
+/* Parameterised activations, floating dtypes (THRESHOLD: every non-bool
+ * dtype).  Forward op = {out, x}; backward op = {grad_in, grad, x}.
+ *   LEAKY_RELU   p0 negative_slope           leaky_relu.out NF:12217, _backward NF:12234
+ *   HARDTANH     p0 min, p1 max (backward; the forward is clamp)  hardtanh_backward NF:12174
+ *   ELU          p0 alpha, p1 scale, p2 input_scale; backward flag = is_result
+ *                (x is then the forward output)  elu.out NF:12057, elu_backward NF:12071
+ *   SOFTPLUS     p0 beta, p1 threshold        softplus.out NF:12318, _backward NF:12333
+ *   HARDSWISH    -                            hardswish.out NF:12193, _backward NF:12211
+ *   HARDSIGMOID  -                            hardsigmoid.out NF:12126, _backward NF:12148
+ *   MISH         -                            mish.out NF:5409, mish_backward NF:5417
+ *   LOG_SIGMOID  -                            log_sigmoid_forward NF:12260, _backward NF:12276
+ *   THRESHOLD    p0 threshold, p1 value (forward); backward: x <= p0 ? 0 : grad
+ *                                             threshold.out NF:6244, threshold_backward NF:6252
+ * The formulas are upstream's CUDA activation functors, evaluated in float
+ * (double for f64) with the parameters rounded to it. */
+#define SUPA_AMD_ACT_LEAKY_RELU 0
+#define SUPA_AMD_ACT_HARDTANH 1
+#define SUPA_AMD_ACT_ELU 2
+#define SUPA_AMD_ACT_SOFTPLUS 3
+#define SUPA_AMD_ACT_HARDSWISH 4
+#define SUPA_AMD_ACT_HARDSIGMOID 5
+#define SUPA_AMD_ACT_MISH 6
+#define SUPA_AMD_ACT_LOG_SIGMOID 7
+#define SUPA_AMD_ACT_THRESHOLD 8
+int supa_amd_activation(const supa_amd_ew_desc* d, int act, double p0, double p1, double p2, void* stream);
+int supa_amd_activation_backward(const supa_amd_ew_desc* d, int act, double p0, double p1, double p2, int flag,
+                                 void* stream);
 
 /* ------------------------------------------------------ copy / fill */
 
@@ -351,7 +382,8 @@ int supa_amd_cross_entropy_backward(const void* grad_out, const void* logits, in
 #define SUPA_AMD_FOREACH_LERP 7     /* out = lerp(a, b, w)                    */
 #define SUPA_AMD_FOREACH_ZERO 8     /* out = 0                                */
 #define SUPA_AMD_FOREACH_UNARY 32   /* + SUPA_AMD_SIGMOID, _TANH, _EXP, _LOG, _ERF,
-                                       _NEG, _RECIPROCAL, _ABS, _SQRT: out = f(a) */
+                                       _NEG, _RECIPROCAL, _ABS, _SQRT, _EXPM1,
+                                       _LOG1P: out = f(a) */
 /* Where y (lerp: the weight w) comes from: */
 #define SUPA_AMD_FOREACH_LIST 0       /* y = b[k][i]; lerp w = c[k][i]            */
 #define SUPA_AMD_FOREACH_SCALARS 1    /* y = scalars[k] (a Scalar repeats)        */

@@ -26,7 +26,9 @@ _lib = None
 # op codes shared with oracle.c
 ADD, MUL, DIV, DIV_TRUNC, DIV_FLOOR, MAXIMUM, MINIMUM = 0, 1, 2, 3, 4, 5, 6
 ADDCMUL, ADDCDIV, LERP = 0, 1, 2
-GELU, GELU_TANH, SILU, SIGMOID, TANH, EXP, LOG, ERF, RELU, NEG, RECIPROCAL, ABS, SQRT = range(13)
+GELU, GELU_TANH, SILU, SIGMOID, TANH, EXP, LOG, ERF, RELU, NEG, RECIPROCAL, ABS, SQRT, EXPM1, LOG1P = range(15)
+(ACT_LEAKY_RELU, ACT_HARDTANH, ACT_ELU, ACT_SOFTPLUS, ACT_HARDSWISH, ACT_HARDSIGMOID, ACT_MISH, ACT_LOG_SIGMOID,
+ ACT_THRESHOLD) = range(9)
 MSE, SMOOTH_L1, BCE_LOGITS = 0, 1, 2
 REDUCTION = {"none": 0, "mean": 1, "sum": 2}
 
@@ -58,6 +60,9 @@ def lib():
             "or_unary_f32": (None, [c_int, _f32p, _f32p, i64]),
             "or_ternary_f32": (None, [c_int, _f32p, _f32p, _f32p, _f32p, i64, c_float]),
             "or_unary_backward_f32": (None, [c_int, _f32p, _f32p, _f32p, i64]),
+            "or_activation_f32": (None, [c_int, _f32p, _f32p, i64, c_float, c_float, c_float]),
+            "or_activation_backward_f32": (None, [c_int, _f32p, _f32p, _f32p, i64, c_float, c_float, c_float,
+                                                  c_int]),
             "or_log_softmax_fwd": (None, [_f32p, _f32p, i64, i64]),
             "or_log_softmax_bwd": (None, [_f32p, _f32p, _f32p, i64, i64]),
             "or_softmax_fwd": (None, [_f32p, _f32p, i64, i64]),
@@ -167,6 +172,22 @@ def unary_backward(op: int, dy, x) -> np.ndarray:
     dy, x = _c(dy, np.float32), _c(x, np.float32)
     out = np.empty(x.shape, np.float32)
     lib().or_unary_backward_f32(op, _p(dy, _f32p), _p(x, _f32p), _p(out, _f32p), x.size)
+    return out
+
+
+def activation(act: int, x, p0=0.0, p1=0.0, p2=0.0) -> np.ndarray:
+    """Parameterised activation forward (float32)."""
+    x = _c(x, np.float32)
+    out = np.empty(x.shape, np.float32)
+    lib().or_activation_f32(act, _p(x, _f32p), _p(out, _f32p), x.size, p0, p1, p2)
+    return out
+
+
+def activation_backward(act: int, g, x, p0=0.0, p1=0.0, p2=0.0, flag=0) -> np.ndarray:
+    g, x = np.broadcast_arrays(np.asarray(g), np.asarray(x))
+    g, x = _c(g, np.float32), _c(x, np.float32)
+    out = np.empty(x.shape, np.float32)
+    lib().or_activation_backward_f32(act, _p(g, _f32p), _p(x, _f32p), _p(out, _f32p), x.size, p0, p1, p2, flag)
     return out
 
 

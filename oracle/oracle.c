@@ -175,7 +175,7 @@ void or_ternary_f32(int op, const float* a, const float* b, const float* c, floa
 enum {
   OR_GELU = 0, OR_GELU_TANH = 1, OR_SILU = 2, OR_SIGMOID = 3, OR_TANH = 4,
   OR_EXP = 5, OR_LOG = 6, OR_ERF = 7, OR_RELU = 8, OR_NEG = 9, OR_RECIPROCAL = 10, OR_ABS = 11,
-  OR_SQRT = 12
+  OR_SQRT = 12, OR_EXPM1 = 13, OR_LOG1P = 14
 };
 
 #define OR_SQRT1_2 0.70710678118654752440f
@@ -191,7 +191,7 @@ enum {
  *               cancellation of 1+tanh(u) for u << 0)
  *  silu:        x / (1 + exp(-x))                     NF:5374
  *  sigmoid:     1 / (1 + exp(-x))                     NF:5441
- *  tanh, exp, log, erf: the primitives of oracle_math.h;
+ *  tanh, exp, log, erf, expm1, log1p: the primitives of oracle_math.h;
  *  reciprocal, abs, sqrt: IEEE 1/x, |x| and correctly rounded sqrt. */
 static inline float act_fwd(int op, float x) {
   switch (op) {
@@ -211,6 +211,8 @@ static inline float act_fwd(int op, float x) {
     case OR_RECIPROCAL: return 1.0f / x;
     case OR_ABS: return fabsf(x);
     case OR_SQRT: return sqrtf(x);
+    case OR_EXPM1: return or_expm1f(x);
+    case OR_LOG1P: return or_log1pf(x);
     default: return -x;
   }
 }
@@ -257,6 +259,96 @@ void or_unary_f32(int op, const float* x, float* out, int64_t n) {
 }
 void or_unary_backward_f32(int op, const float* dy, const float* x, float* out, int64_t n) {
   for (int64_t i = 0; i < n; ++i) out[i] = act_bwd(op, dy[i], x[i]);
+}
+
+/* --------------------------------------- parameterised activations -- */
+
+enum {
+  OR_ACT_LEAKY_RELU = 0, OR_ACT_HARDTANH = 1, OR_ACT_ELU = 2, OR_ACT_SOFTPLUS = 3, OR_ACT_HARDSWISH = 4,
+  OR_ACT_HARDSIGMOID = 5, OR_ACT_MISH = 6, OR_ACT_LOG_SIGMOID = 7, OR_ACT_THRESHOLD = 8
+};
+
+/* std::max / std::min as the device code of upstream's kernels evaluates
+ * them: (a < b) ? b : a and (b < a) ? b : a (a NaN first operand passes). */
+static inline float max_lt(float a, float b) { return (a < b) ? b : a; }
+static inline float min_lt(float a, float b) { return (b < a) ? b : a; }
+
+/* Forward formulas of upstream's CUDA activation kernels (ActivationLeakyReluKernel.cu,
+ * ActivationEluKernel.cu, ActivationSoftplusKernel.cu, ActivationHardswishKernel.cu,
+ * ActivationHardsigmoidKernel.cu, ActivationMishKernel.cu, ActivationLogSigmoidKernel.cu,
+ * ActivationThresholdKernel.cu), float32 opmath, parameters rounded to float:
+ *  leaky_relu  x > 0 ? x : x*p0                                     NF:12226
+ *  elu         x > 0 ? x*p1 : expm1(x*p2) * (p0*p1)  (alpha, scale, input_scale)  NF:12065
+ *  softplus    x*p0 > p1 ? x : log1p(exp(x*p0)) / p0  (beta, threshold)  NF:12327
+ *  hardswish   x * min(max(x+3, 0), 6) * (1/6)                      NF:12199
+ *  hardsigmoid min(max(x+3, 0), 6) * (1/6)                          NF:12135
+ *  mish        x * tanh(log1p(exp(x)))                              NF:5400
+ *  log_sigmoid min(0, x) - log1p(exp(-|x|))                         NF:12268
+ *  threshold   x <= p0 ? p1 : x                                     NF:6231
+ * (hardtanh's forward is clamp.) */
+static inline float act_p_fwd(int act, float x, float p0, float p1, float p2) {
+  switch (act) {
+    case OR_ACT_LEAKY_RELU: return x > 0.0f ? x : x * p0;
+    case OR_ACT_ELU: return x > 0.0f ? x * p1 : or_expm1f(x * p2) * (p0 * p1);
+    case OR_ACT_SOFTPLUS: return (x * p0) > p1 ? x : or_log1pf(or_expf(x * p0)) / p0;
+    case OR_ACT_HARDSWISH: return (x * min_lt(max_lt(x + 3.0f, 0.0f), 6.0f)) * (1.0f / 6.0f);
+    case OR_ACT_HARDSIGMOID: return min_lt(max_lt(x + 3.0f, 0.0f), 6.0f) * (1.0f / 6.0f);
+    case OR_ACT_MISH: return x * or_tanhf(or_log1pf(or_expf(x)));
+    case OR_ACT_LOG_SIGMOID: return min_lt(0.0f, x) - or_log1pf(or_expf(-fabsf(x)));
+    case OR_ACT_THRESHOLD: return x <= p0 ? p1 : x;
+    default: return x;
+  }
+}
+
+/* Backward formulas (the same files' backward functors; g the incoming
+ * gradient, x the forward input -- the forward output for elu with flag set);
+ * `a + b*c` forms are one fma, as upstream's compiler contracts them:
+ *  leaky_relu  x > 0 ? g : g*p0                                     NF:12241
+ *  hardtanh    x <= p0 || x >= p1 ? 0 : g  (min, max)               NF:12180
+ *  elu         result form: x <= 0 ? g*p2*(x + p0*p1) : g*p1;
+ *              input form:  x <= 0 ? g*p2*(p0*p1)*exp(x*p2) : g*p1  NF:12078
+ *  softplus    z = exp(x*p0); x*p0 > p1 ? g : g*z/(z+1)             NF:12341
+ *  hardswish   x < -3 ? 0 : x <= 3 ? g*(x/3 + 0.5) : g              NF:12211
+ *  hardsigmoid -3 < x < 3 ? g/6 : 0                                 NF:12155
+ *  mish        s = 1/(1+exp(-x)), t = tanh(log1p(exp(x))); g*(t + x*s*(1 - t*t))  NF:5417
+ *  log_sigmoid z = exp(-|x|); g*(d - sg * z/(1+z)), d = x<0, sg = x<0 ? 1 : -1  NF:12283
+ *  threshold   x <= p0 ? 0 : g                                      NF:6261 */
+static inline float act_p_bwd(int act, float g, float x, float p0, float p1, float p2, int flag) {
+  switch (act) {
+    case OR_ACT_LEAKY_RELU: return x > 0.0f ? g : g * p0;
+    case OR_ACT_HARDTANH: return (x <= p0 || x >= p1) ? 0.0f : g;
+    case OR_ACT_ELU: {
+      const float negcoef = p0 * p1;
+      if (flag) return x <= 0.0f ? (g * p2) * (x + negcoef) : g * p1;
+      return x <= 0.0f ? ((g * p2) * negcoef) * or_expf(x * p2) : g * p1;
+    }
+    case OR_ACT_SOFTPLUS: {
+      const float z = or_expf(x * p0);
+      return (x * p0) > p1 ? g : (g * z) / (z + 1.0f);
+    }
+    case OR_ACT_HARDSWISH: return x < -3.0f ? 0.0f : (x <= 3.0f ? g * ((x / 3.0f) + 0.5f) : g);
+    case OR_ACT_HARDSIGMOID: return (x > -3.0f && x < 3.0f) ? g * (1.0f / 6.0f) : 0.0f;
+    case OR_ACT_MISH: {
+      const float sg = 1.0f / (1.0f + or_expf(-x));
+      const float t = or_tanhf(or_log1pf(or_expf(x)));
+      return g * fmaf(x * sg, fmaf(-t, t, 1.0f), t);
+    }
+    case OR_ACT_LOG_SIGMOID: {
+      const int neg = x < 0.0f;
+      const float z = or_expf(-fabsf(x));
+      return g * fmaf(neg ? -1.0f : 1.0f, z / (1.0f + z), neg ? 1.0f : 0.0f);
+    }
+    case OR_ACT_THRESHOLD: return x <= p0 ? 0.0f : g;
+    default: return g;
+  }
+}
+
+void or_activation_f32(int act, const float* x, float* out, int64_t n, float p0, float p1, float p2) {
+  for (int64_t i = 0; i < n; ++i) out[i] = act_p_fwd(act, x[i], p0, p1, p2);
+}
+void or_activation_backward_f32(int act, const float* g, const float* x, float* out, int64_t n, float p0, float p1,
+                                float p2, int flag) {
+  for (int64_t i = 0; i < n; ++i) out[i] = act_p_bwd(act, g[i], x[i], p0, p1, p2, flag);
 }
 
 /* ---------------------------------------------------------- log_softmax -- */

@@ -13,7 +13,8 @@
  * Lawson reweighting towards minimax, then rounded to binary32); they do not
  * come from any vendor math library.  Their accuracy against double-precision
  * libm is pinned by tests/test_oracle_math.py:
- *   or_expf  <= 1 ulp,  or_logf <= 1 ulp,  or_erff <= 2 ulp,  or_tanhf <= 2 ulp.
+ *   or_expf  <= 1 ulp,  or_logf <= 1 ulp,  or_erff <= 2 ulp,  or_tanhf <= 2 ulp,
+ *   or_expm1f <= 2 ulp, or_log1pf <= 2 ulp.
  *
  * The reductions used by every primitive:
  *   exp:  Cody-Waite split x = k*ln2 + r, |r| <= ln2/2, e^r = 1 + r + r^2 P(r).
@@ -117,6 +118,41 @@ static inline float or_tanhf(float x) {
   const float e = or_expf(a + a);
   const float r = 1.0f - 2.0f / (e + 1.0f);
   return copysignf(r, x);
+}
+
+/* expm1: the same reduction and polynomial as or_expf (its r + r^2 P(r) is
+ * e^r - 1 to 0.85 ulp on |r| <= ln2/2), then 2^k (e^r - 1) + (2^k - 1), or
+ * 2^k e^r - 1 once 2^k - 1 is no longer exact (k >= 25). <= 1.5 ulp. */
+static inline float or_expm1f(float x) {
+  if (isnan(x)) return x;
+  x = (x > 89.0f) ? 89.0f : x;
+  x = (x < -104.0f) ? -104.0f : x;
+  const float k = rintf(x * 1.44269502f);
+  float r = fmaf(k, -0.693145751953125f, x);
+  r = fmaf(k, -1.42860677e-06f, r);
+  float p = 0.0013814599951729178f;
+  p = fmaf(p, r, 0.008368715643882751f);
+  p = fmaf(p, r, 0.04166838899254799f);
+  p = fmaf(p, r, 0.1666652113199234f);
+  p = fmaf(p, r, 0.4999999403953552f);
+  const float r2 = r * r;
+  const float q = fmaf(p, r2, r);
+  const int ki = (int)k;
+  const float big = ldexpf(q + 1.0f, ki) - 1.0f;
+  const float small = ldexpf(q, ki) + (ldexpf(1.0f, ki) - 1.0f);
+  return ki >= 25 ? big : small;
+}
+
+/* log1p: u = 1 + z rounded, then log(u) + (z - (u - 1)) / u for |z| <= 1
+ * (the parenthesis is the exact rounding error of u), log(u) otherwise. */
+static inline float or_log1pf(float z) {
+  if (isnan(z)) return z;
+  if (z < -1.0f) return NAN;
+  if (z == -1.0f) return -INFINITY;
+  if (isinf(z)) return z;
+  const float u = 1.0f + z;
+  const float c = (fabsf(z) <= 1.0f) ? z - (u - 1.0f) : 0.0f;
+  return or_logf(u) + c / u;
 }
 
 #endif

@@ -40,6 +40,29 @@ def test_primitive_accuracy(op, ref, bound, lo, hi):
     assert err.max() <= bound, (op, float(x[np.argmax(err)]), float(err.max()))
 
 
+def test_expm1_log1p_accuracy_and_edges():
+    """expm1 reuses the exp reduction and polynomial; log1p adds the exact
+    rounding error of 1 + z back.  Both within 2 ulp of double precision."""
+    x = np.concatenate([sample_f32(1 << 21, seed=31, lo=-110.0, hi=89.0),
+                        sample_f32(1 << 20, seed=32, lo=-1.0, hi=1.0),
+                        np.float32([1e-30, -1e-30, 1e-8, -1e-8, 0.3466, -0.3466, 17.0, 24.0, 88.7])])
+    with np.errstate(all="ignore"):
+        ex = np.expm1(x.astype(np.float64))
+    fin = np.isfinite(ex) & (np.abs(ex) < 3.4e38)
+    assert ulp_vs_exact(O.unary(O.EXPM1, x)[fin], ex[fin]).max() <= 1.5
+    z = np.concatenate([np.exp(np.random.default_rng(33).uniform(np.log(1e-38), np.log(3e38), 1 << 20)),
+                        np.random.default_rng(34).uniform(-0.999999, 1.0, 1 << 20),
+                        [1e-45, -1e-45, 6e-8, -6e-8, 1.0, -0.5, -0.75]]).astype(np.float32)
+    assert ulp_vs_exact(O.unary(O.LOG1P, z), np.log1p(z.astype(np.float64))).max() <= 2.0
+    # specials: expm1(0) = 0 and the tiny-argument identity, log1p(-1) = -inf, log1p(< -1) = nan
+    e = O.unary(O.EXPM1, np.float32([0.0, -0.0, 1e-30, -200.0, np.inf, -np.inf, np.nan]))
+    assert e[0] == 0.0 and e[2] == np.float32(1e-30) and e[3] == -1.0 and e[4] == np.inf and e[5] == -1.0
+    assert np.isnan(e[6])
+    l = O.unary(O.LOG1P, np.float32([0.0, 1e-30, -1.0, -2.0, np.inf, np.nan]))
+    assert l[0] == 0.0 and l[1] == np.float32(1e-30) and l[2] == -np.inf and np.isnan(l[3]) and l[4] == np.inf
+    assert np.isnan(l[5])
+
+
 def test_primitive_edges():
     x = EDGES
     with np.errstate(all="ignore"):

@@ -485,3 +485,79 @@ def test_nll_loss2d_vs_cpu(reduction, weighted):
     tf = t.numpy().ravel()
     if reduction != "none":
         assert float(tw) == pytest.approx(float(wt[tf[tf != -100]].sum()), rel=1e-6)
+
+
+# --------------------------------------------- parameterised activations
+ACTS = [  # (name, oracle act, params, torch forward on a tensor)
+    ("leaky_relu", O.ACT_LEAKY_RELU, (0.01, 0.0, 0.0), lambda t: F.leaky_relu(t, 0.01)),
+    ("elu", O.ACT_ELU, (1.0, 1.0, 1.0), F.elu),
+    ("selu", O.ACT_ELU, (1.6732632423543772, 1.0507009873554805, 1.0), torch.selu),
+    ("celu", O.ACT_ELU, (0.7, 1.0, 1.0 / 0.7), lambda t: F.celu(t, 0.7)),
+    ("softplus", O.ACT_SOFTPLUS, (1.0, 20.0, 0.0), F.softplus),
+    ("softplus_b2", O.ACT_SOFTPLUS, (2.0, 5.0, 0.0), lambda t: F.softplus(t, 2.0, 5.0)),
+    ("hardswish", O.ACT_HARDSWISH, (0.0, 0.0, 0.0), F.hardswish),
+    ("hardsigmoid", O.ACT_HARDSIGMOID, (0.0, 0.0, 0.0), F.hardsigmoid),
+    ("mish", O.ACT_MISH, (0.0, 0.0, 0.0), F.mish),
+    ("logsigmoid", O.ACT_LOG_SIGMOID, (0.0, 0.0, 0.0), F.logsigmoid),
+    ("threshold", O.ACT_THRESHOLD, (0.5, -2.0, 0.0), lambda t: F.threshold(t, 0.5, -2.0)),
+]
+
+
+@pytest.mark.parametrize("name,act,ps,fn", ACTS, ids=[a[0] for a in ACTS])
+def test_activation_forward_vs_cpu(name, act, ps, fn):
+    """Within 2 ulp of double precision wherever upstream's CPU float32 is,
+    and never more than 1 ulp worse than it (mish composes three
+    primitives: 3.5 ulp against the CPU's 2.8)."""
+    from helpers import sample_f32, ulp_vs_exact
+    x = np.concatenate([sample_f32(1 << 20, seed=40, lo=-30.0, hi=30.0),
+                        np.float32([0.0, -0.0, -3.0, 3.0, 20.0, 20.000002, -1e-30, 0.5, 0.49999997])])
+    got = O.activation(act, x, *ps)
+    exact = fn(torch.from_numpy(x.astype(np.float64))).numpy()
+    cpu = fn(torch.from_numpy(x)).numpy()
+    e_or, e_cpu = ulp_vs_exact(got, exact), ulp_vs_exact(cpu, exact)
+    assert e_or.max() <= max(2.0, e_cpu.max() + 1.0), (name, float(e_or.max()), float(e_cpu.max()))
+
+
+BWD = [  # (name, oracle act, params, flag, torch forward whose autograd backward is the reference)
+    ("leaky_relu", O.ACT_LEAKY_RELU, (0.01, 0.0, 0.0), 0, lambda t: F.leaky_relu(t, 0.01)),
+    ("hardtanh", O.ACT_HARDTANH, (-1.5, 2.0, 0.0), 0, lambda t: F.hardtanh(t, -1.5, 2.0)),
+    ("elu", O.ACT_ELU, (1.0, 1.0, 1.0), 0, F.elu),
+    ("selu", O.ACT_ELU, (1.6732632423543772, 1.0507009873554805, 1.0), 0, torch.selu),
+    ("softplus", O.ACT_SOFTPLUS, (1.0, 20.0, 0.0), 0, F.softplus),
+    ("hardswish", O.ACT_HARDSWISH, (0.0, 0.0, 0.0), 0, F.hardswish),
+    ("hardsigmoid", O.ACT_HARDSIGMOID, (0.0, 0.0, 0.0), 0, F.hardsigmoid),
+    ("mish", O.ACT_MISH, (0.0, 0.0, 0.0), 0, F.mish),
+    ("logsigmoid", O.ACT_LOG_SIGMOID, (0.0, 0.0, 0.0), 0, F.logsigmoid),
+    ("relu", O.ACT_THRESHOLD, (0.0, 0.0, 0.0), 0, F.relu),
+]
+
+
+@pytest.mark.parametrize("name,act,ps,flag,fn", BWD, ids=[b[0] for b in BWD])
+def test_activation_backward_vs_cpu(name, act, ps, flag, fn):
+    """Against autograd in double: within a few ulp of the gradient's scale
+    |g| (1 + |x|) -- mish's and hardswish's gradients cross zero, so a
+    relative bound would be meaningless there, as it is for the CPU's own."""
+    from helpers import sample_f32
+    x = sample_f32(1 << 19, seed=41, lo=-12.0, hi=12.0)
+    g = sample_f32(1 << 19, seed=42, lo=-2.0, hi=2.0)
+    xd = torch.from_numpy(x.astype(np.float64)).requires_grad_()
+    fn(xd).backward(torch.from_numpy(g.astype(np.float64)))
+    exact = xd.grad.numpy()
+    # relu's backward reads the forward output (threshold_backward(grad, result, 0))
+    inp = np.maximum(x, 0).astype(np.float32) if name == "relu" else x
+    got = O.activation_backward(act, g, inp, *ps, flag).astype(np.float64)
+    scale = np.abs(g).astype(np.float64) * (1.0 + np.abs(x))
+    # 6 units: selu's float-rounded alpha * scale alone costs 4.4 (as on the CPU)
+    assert np.all(np.abs(got - exact) <= 6 * 2.0 ** -24 * scale + 1e-30), name
+
+
+def test_elu_backward_from_result():
+    """elu_backward with is_result (the in-place form): x is the output."""
+    x = randn((5000,), 43, 3.0)
+    g = randn((5000,), 44)
+    for alpha in (1.0, 0.5):
+        y = F.elu(x.double(), alpha)
+        xr = x.double().clone().requires_grad_()
+        F.elu(xr, alpha).backward(g.double())
+        got = O.activation_backward(O.ACT_ELU, g.numpy(), y.float().numpy(), alpha, 1.0, 1.0, 1)
+        np.testing.assert_allclose(got, xr.grad.numpy(), rtol=2e-6, atol=1e-7)

@@ -789,6 +789,8 @@ SUPA_UNARY(neg, SUPA_AMD_NEG, UKind::Any)
 SUPA_UNARY(reciprocal, SUPA_AMD_RECIPROCAL, UKind::IntToFloat)
 SUPA_UNARY(abs, SUPA_AMD_ABS, UKind::Any)
 SUPA_UNARY(sqrt, SUPA_AMD_SQRT, UKind::IntToFloat)
+SUPA_UNARY(expm1, SUPA_AMD_EXPM1, UKind::IntToFloat)
+SUPA_UNARY(log1p, SUPA_AMD_LOG1P, UKind::IntToFloat)
 #undef SUPA_UNARY
 
 at::Tensor relu(const at::Tensor& s) {
@@ -813,6 +815,208 @@ SUPA_UNARY_BWD(silu, SUPA_AMD_SILU)
 SUPA_UNARY_BWD(sigmoid, SUPA_AMD_SIGMOID)
 SUPA_UNARY_BWD(tanh, SUPA_AMD_TANH)
 #undef SUPA_UNARY_BWD
+
+// ------------------------------------------------ parameterised activations
+// leaky_relu, elu, softplus, hardswish, hardsigmoid, mish, log_sigmoid,
+// threshold and their backwards (hardtanh's forward is clamp), with
+// upstream's argument checks (Activation.cpp).
+at::Tensor act_apply(const at::Tensor& self, at::Tensor out, bool inplace, int act, double p0, double p1, double p2,
+                     const char* name) {
+  const c10::ScalarType common = self.scalar_type();
+  if (act == SUPA_AMD_ACT_THRESHOLD) {
+    TORCH_CHECK(common != at::kBool, name, ": \"", name, "\" not implemented for 'Bool'");
+  } else {
+    TORCH_CHECK(at::isFloatingType(common), name, ": \"", name, "\" not implemented for '", common, "'");
+  }
+  const Launch fn = [=](const supa_amd_ew_desc* d, void* s) { return supa_amd_activation(d, act, p0, p1, p2, s); };
+  std::vector<EwIn> ins{EwIn::of(self)};
+  if (inplace) return ew_apply(self, self.scalar_type(), common, ins, fn, name);
+  if (out.defined()) {
+    check_cast(common, out, name);
+    return ew_apply(out, out.scalar_type(), common, ins, fn, name);
+  }
+  return ew_apply(at::Tensor(), common, common, ins, fn, name);
+}
+
+at::Tensor act_bwd_apply(const at::Tensor& grad, const at::Tensor& x, at::Tensor out, int act, double p0, double p1,
+                         double p2, int flag, const char* name) {
+  const c10::ScalarType common = at::result_type(grad, x);
+  TORCH_CHECK(at::isFloatingType(common), name, ": not implemented for '", common, "'");
+  const Launch fn = [=](const supa_amd_ew_desc* d, void* s) {
+    return supa_amd_activation_backward(d, act, p0, p1, p2, flag, s);
+  };
+  std::vector<EwIn> ins{EwIn::of(grad), EwIn::of(x)};
+  if (out.defined()) {
+    check_cast(common, out, name);
+    return ew_apply(out, out.scalar_type(), common, ins, fn, name);
+  }
+  return ew_apply(at::Tensor(), common, common, ins, fn, name);
+}
+
+double sd(const c10::Scalar& v) { return v.toDouble(); }
+
+// leaky_relu
+at::Tensor leaky_relu(const at::Tensor& s, const c10::Scalar& ns) {
+  return act_apply(s, {}, false, SUPA_AMD_ACT_LEAKY_RELU, sd(ns), 0, 0, "leaky_relu");
+}
+at::Tensor& leaky_relu_(at::Tensor& s, const c10::Scalar& ns) {
+  act_apply(s, {}, true, SUPA_AMD_ACT_LEAKY_RELU, sd(ns), 0, 0, "leaky_relu_");
+  return s;
+}
+at::Tensor& leaky_relu_out(const at::Tensor& s, const c10::Scalar& ns, at::Tensor& out) {
+  act_apply(s, out, false, SUPA_AMD_ACT_LEAKY_RELU, sd(ns), 0, 0, "leaky_relu.out");
+  return out;
+}
+at::Tensor leaky_relu_bwd_into(const at::Tensor& g, const at::Tensor& s, const c10::Scalar& ns, bool self_is_result,
+                               at::Tensor out, const char* name) {
+  TORCH_CHECK(!self_is_result || ns.toDouble() >= 0.0,
+              "In-place leakyReLu backward calculation is triggered with a negative slope which is not supported. "
+              "This is caused by calling in-place forward function with a negative slope, please call out-of-place "
+              "version instead. File an issue at https://github.com/pytorch/pytorch if you do require supporting "
+              "in-place leakRelu backward calculation with negative slope");
+  return act_bwd_apply(g, s, out, SUPA_AMD_ACT_LEAKY_RELU, sd(ns), 0, 0, 0, name);
+}
+at::Tensor leaky_relu_backward(const at::Tensor& g, const at::Tensor& s, const c10::Scalar& ns, bool r) {
+  return leaky_relu_bwd_into(g, s, ns, r, {}, "leaky_relu_backward");
+}
+at::Tensor& leaky_relu_backward_out(const at::Tensor& g, const at::Tensor& s, const c10::Scalar& ns, bool r,
+                                    at::Tensor& gi) {
+  leaky_relu_bwd_into(g, s, ns, r, gi, "leaky_relu_backward.grad_input");
+  return gi;
+}
+
+// hardtanh: the forward is clamp (upstream's hardtanh_out calls clamp_out)
+at::Tensor hardtanh(const at::Tensor& s, const c10::Scalar& lo, const c10::Scalar& hi) {
+  TORCH_CHECK(s.scalar_type() != at::kBool, "Bool inputs not supported for hardtanh");
+  return at::clamp(s, lo, hi);
+}
+at::Tensor& hardtanh_(at::Tensor& s, const c10::Scalar& lo, const c10::Scalar& hi) {
+  TORCH_CHECK(s.scalar_type() != at::kBool, "Bool inputs not supported for hardtanh");
+  return at::clamp_(s, lo, hi);
+}
+at::Tensor& hardtanh_out(const at::Tensor& s, const c10::Scalar& lo, const c10::Scalar& hi, at::Tensor& out) {
+  TORCH_CHECK(s.scalar_type() != at::kBool, "Bool inputs not supported for hardtanh");
+  return at::clamp_out(out, s, lo, hi);
+}
+at::Tensor hardtanh_backward(const at::Tensor& g, const at::Tensor& s, const c10::Scalar& lo, const c10::Scalar& hi) {
+  return act_bwd_apply(g, s, {}, SUPA_AMD_ACT_HARDTANH, sd(lo), sd(hi), 0, 0, "hardtanh_backward");
+}
+at::Tensor& hardtanh_backward_out(const at::Tensor& g, const at::Tensor& s, const c10::Scalar& lo,
+                                  const c10::Scalar& hi, at::Tensor& gi) {
+  act_bwd_apply(g, s, gi, SUPA_AMD_ACT_HARDTANH, sd(lo), sd(hi), 0, 0, "hardtanh_backward.grad_input");
+  return gi;
+}
+
+// elu
+at::Tensor elu(const at::Tensor& s, const c10::Scalar& a, const c10::Scalar& sc, const c10::Scalar& is) {
+  return act_apply(s, {}, false, SUPA_AMD_ACT_ELU, sd(a), sd(sc), sd(is), "elu");
+}
+at::Tensor& elu_(at::Tensor& s, const c10::Scalar& a, const c10::Scalar& sc, const c10::Scalar& is) {
+  act_apply(s, {}, true, SUPA_AMD_ACT_ELU, sd(a), sd(sc), sd(is), "elu_");
+  return s;
+}
+at::Tensor& elu_out(const at::Tensor& s, const c10::Scalar& a, const c10::Scalar& sc, const c10::Scalar& is,
+                    at::Tensor& out) {
+  act_apply(s, out, false, SUPA_AMD_ACT_ELU, sd(a), sd(sc), sd(is), "elu.out");
+  return out;
+}
+at::Tensor elu_bwd_into(const at::Tensor& g, const c10::Scalar& a, const c10::Scalar& sc, const c10::Scalar& is,
+                        bool is_result, const at::Tensor& x, at::Tensor out, const char* name) {
+  if (is_result) {
+    TORCH_CHECK(a.toDouble() >= 0.0, "In-place elu backward calculation is triggered with a negative slope which "
+                "is not supported. This is caused by calling in-place forward function with a negative slope, "
+                "please call out-of-place version instead.");
+  }
+  return act_bwd_apply(g, x, out, SUPA_AMD_ACT_ELU, sd(a), sd(sc), sd(is), is_result ? 1 : 0, name);
+}
+at::Tensor elu_backward(const at::Tensor& g, const c10::Scalar& a, const c10::Scalar& sc, const c10::Scalar& is,
+                        bool r, const at::Tensor& x) {
+  return elu_bwd_into(g, a, sc, is, r, x, {}, "elu_backward");
+}
+at::Tensor& elu_backward_out(const at::Tensor& g, const c10::Scalar& a, const c10::Scalar& sc, const c10::Scalar& is,
+                             bool r, const at::Tensor& x, at::Tensor& gi) {
+  elu_bwd_into(g, a, sc, is, r, x, gi, "elu_backward.grad_input");
+  return gi;
+}
+
+// softplus
+at::Tensor softplus(const at::Tensor& s, const c10::Scalar& b, const c10::Scalar& th) {
+  return act_apply(s, {}, false, SUPA_AMD_ACT_SOFTPLUS, sd(b), sd(th), 0, "softplus");
+}
+at::Tensor& softplus_out(const at::Tensor& s, const c10::Scalar& b, const c10::Scalar& th, at::Tensor& out) {
+  act_apply(s, out, false, SUPA_AMD_ACT_SOFTPLUS, sd(b), sd(th), 0, "softplus.out");
+  return out;
+}
+at::Tensor softplus_backward(const at::Tensor& g, const at::Tensor& s, const c10::Scalar& b, const c10::Scalar& th) {
+  return act_bwd_apply(g, s, {}, SUPA_AMD_ACT_SOFTPLUS, sd(b), sd(th), 0, 0, "softplus_backward");
+}
+at::Tensor& softplus_backward_out(const at::Tensor& g, const at::Tensor& s, const c10::Scalar& b,
+                                  const c10::Scalar& th, at::Tensor& gi) {
+  act_bwd_apply(g, s, gi, SUPA_AMD_ACT_SOFTPLUS, sd(b), sd(th), 0, 0, "softplus_backward.grad_input");
+  return gi;
+}
+
+// hardswish, hardsigmoid, mish: no parameters
+#define SUPA_ACT0(NAME, ACT)                                                                       \
+  at::Tensor NAME(const at::Tensor& s) { return act_apply(s, {}, false, ACT, 0, 0, 0, #NAME); }     \
+  at::Tensor& NAME##_(at::Tensor& s) {                                                             \
+    act_apply(s, {}, true, ACT, 0, 0, 0, #NAME "_");                                               \
+    return s;                                                                                      \
+  }                                                                                                \
+  at::Tensor& NAME##_out(const at::Tensor& s, at::Tensor& out) {                                   \
+    act_apply(s, out, false, ACT, 0, 0, 0, #NAME ".out");                                          \
+    return out;                                                                                    \
+  }                                                                                                \
+  at::Tensor NAME##_backward(const at::Tensor& g, const at::Tensor& s) {                           \
+    return act_bwd_apply(g, s, {}, ACT, 0, 0, 0, 0, #NAME "_backward");                            \
+  }                                                                                                \
+  at::Tensor& NAME##_backward_out(const at::Tensor& g, const at::Tensor& s, at::Tensor& gi) {      \
+    act_bwd_apply(g, s, gi, ACT, 0, 0, 0, 0, #NAME "_backward.grad_input");                        \
+    return gi;                                                                                     \
+  }
+SUPA_ACT0(hardswish, SUPA_AMD_ACT_HARDSWISH)
+SUPA_ACT0(hardsigmoid, SUPA_AMD_ACT_HARDSIGMOID)
+SUPA_ACT0(mish, SUPA_AMD_ACT_MISH)
+#undef SUPA_ACT0
+
+// log_sigmoid: the forward's buffer is empty, as on upstream's CUDA backend
+std::tuple<at::Tensor, at::Tensor> log_sigmoid_forward(const at::Tensor& s) {
+  at::Tensor out = act_apply(s, {}, false, SUPA_AMD_ACT_LOG_SIGMOID, 0, 0, 0, "log_sigmoid_forward");
+  return {out, at::empty({0}, s.options())};
+}
+std::tuple<at::Tensor&, at::Tensor&> log_sigmoid_forward_out(const at::Tensor& s, at::Tensor& out, at::Tensor& buf) {
+  act_apply(s, out, false, SUPA_AMD_ACT_LOG_SIGMOID, 0, 0, 0, "log_sigmoid_forward.output");
+  at::native::resize_output(buf, {0});
+  return {out, buf};
+}
+at::Tensor log_sigmoid_backward(const at::Tensor& g, const at::Tensor& s, const at::Tensor& /*buffer*/) {
+  return act_bwd_apply(g, s, {}, SUPA_AMD_ACT_LOG_SIGMOID, 0, 0, 0, 0, "log_sigmoid_backward");
+}
+at::Tensor& log_sigmoid_backward_out(const at::Tensor& g, const at::Tensor& s, const at::Tensor& /*buffer*/,
+                                     at::Tensor& gi) {
+  act_bwd_apply(g, s, gi, SUPA_AMD_ACT_LOG_SIGMOID, 0, 0, 0, 0, "log_sigmoid_backward.grad_input");
+  return gi;
+}
+
+// threshold (relu's backward is threshold_backward(grad, result, 0))
+at::Tensor threshold(const at::Tensor& s, const c10::Scalar& th, const c10::Scalar& v) {
+  return act_apply(s, {}, false, SUPA_AMD_ACT_THRESHOLD, sd(th), sd(v), 0, "threshold");
+}
+at::Tensor& threshold_(at::Tensor& s, const c10::Scalar& th, const c10::Scalar& v) {
+  act_apply(s, {}, true, SUPA_AMD_ACT_THRESHOLD, sd(th), sd(v), 0, "threshold_");
+  return s;
+}
+at::Tensor& threshold_out(const at::Tensor& s, const c10::Scalar& th, const c10::Scalar& v, at::Tensor& out) {
+  act_apply(s, out, false, SUPA_AMD_ACT_THRESHOLD, sd(th), sd(v), 0, "threshold.out");
+  return out;
+}
+at::Tensor threshold_backward(const at::Tensor& g, const at::Tensor& s, const c10::Scalar& th) {
+  return act_bwd_apply(g, s, {}, SUPA_AMD_ACT_THRESHOLD, sd(th), 0, 0, 0, "threshold_backward");
+}
+at::Tensor& threshold_backward_out(const at::Tensor& g, const at::Tensor& s, const c10::Scalar& th, at::Tensor& gi) {
+  act_bwd_apply(g, s, gi, SUPA_AMD_ACT_THRESHOLD, sd(th), 0, 0, 0, "threshold_backward.grad_input");
+  return gi;
+}
 
 }  // namespace
 }  // namespace supa
@@ -886,6 +1090,47 @@ TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
   m.impl("lerp.Tensor", TORCH_FN(lerp_t));
   m.impl("lerp_.Tensor", TORCH_FN(lerp_t_));
   m.impl("lerp.Tensor_out", TORCH_FN(lerp_t_out));
+  m.impl("leaky_relu", TORCH_FN(leaky_relu));
+  m.impl("leaky_relu_", TORCH_FN(leaky_relu_));
+  m.impl("leaky_relu.out", TORCH_FN(leaky_relu_out));
+  m.impl("leaky_relu_backward", TORCH_FN(leaky_relu_backward));
+  m.impl("leaky_relu_backward.grad_input", TORCH_FN(leaky_relu_backward_out));
+  m.impl("hardtanh", TORCH_FN(hardtanh));
+  m.impl("hardtanh_", TORCH_FN(hardtanh_));
+  m.impl("hardtanh.out", TORCH_FN(hardtanh_out));
+  m.impl("hardtanh_backward", TORCH_FN(hardtanh_backward));
+  m.impl("hardtanh_backward.grad_input", TORCH_FN(hardtanh_backward_out));
+  m.impl("elu", TORCH_FN(elu));
+  m.impl("elu_", TORCH_FN(elu_));
+  m.impl("elu.out", TORCH_FN(elu_out));
+  m.impl("elu_backward", TORCH_FN(elu_backward));
+  m.impl("elu_backward.grad_input", TORCH_FN(elu_backward_out));
+  m.impl("softplus", TORCH_FN(softplus));
+  m.impl("softplus.out", TORCH_FN(softplus_out));
+  m.impl("softplus_backward", TORCH_FN(softplus_backward));
+  m.impl("softplus_backward.grad_input", TORCH_FN(softplus_backward_out));
+  m.impl("hardswish", TORCH_FN(hardswish));
+  m.impl("hardswish_", TORCH_FN(hardswish_));
+  m.impl("hardswish.out", TORCH_FN(hardswish_out));
+  m.impl("hardswish_backward", TORCH_FN(hardswish_backward));
+  m.impl("hardsigmoid", TORCH_FN(hardsigmoid));
+  m.impl("hardsigmoid_", TORCH_FN(hardsigmoid_));
+  m.impl("hardsigmoid.out", TORCH_FN(hardsigmoid_out));
+  m.impl("hardsigmoid_backward", TORCH_FN(hardsigmoid_backward));
+  m.impl("hardsigmoid_backward.grad_input", TORCH_FN(hardsigmoid_backward_out));
+  m.impl("mish", TORCH_FN(mish));
+  m.impl("mish_", TORCH_FN(mish_));
+  m.impl("mish.out", TORCH_FN(mish_out));
+  m.impl("mish_backward", TORCH_FN(mish_backward));
+  m.impl("log_sigmoid_forward", TORCH_FN(log_sigmoid_forward));
+  m.impl("log_sigmoid_forward.output", TORCH_FN(log_sigmoid_forward_out));
+  m.impl("log_sigmoid_backward", TORCH_FN(log_sigmoid_backward));
+  m.impl("log_sigmoid_backward.grad_input", TORCH_FN(log_sigmoid_backward_out));
+  m.impl("threshold", TORCH_FN(threshold));
+  m.impl("threshold_", TORCH_FN(threshold_));
+  m.impl("threshold.out", TORCH_FN(threshold_out));
+  m.impl("threshold_backward", TORCH_FN(threshold_backward));
+  m.impl("threshold_backward.grad_input", TORCH_FN(threshold_backward_out));
   m.impl("gelu", TORCH_FN(gelu));
   m.impl("gelu_", TORCH_FN(gelu_));
   m.impl("gelu.out", TORCH_FN(gelu_out));
@@ -927,6 +1172,12 @@ TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
   m.impl("sqrt", TORCH_FN(u_sqrt));
   m.impl("sqrt_", TORCH_FN(u_sqrt_));
   m.impl("sqrt.out", TORCH_FN(u_sqrt_out));
+  m.impl("expm1", TORCH_FN(u_expm1));
+  m.impl("expm1_", TORCH_FN(u_expm1_));
+  m.impl("expm1.out", TORCH_FN(u_expm1_out));
+  m.impl("log1p", TORCH_FN(u_log1p));
+  m.impl("log1p_", TORCH_FN(u_log1p_));
+  m.impl("log1p.out", TORCH_FN(u_log1p_out));
   m.impl("relu", TORCH_FN(relu));
   m.impl("relu_", TORCH_FN(relu_));
 }

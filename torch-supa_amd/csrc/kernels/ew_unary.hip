@@ -20,6 +20,8 @@ int supa_amd_unary(const supa_amd_ew_desc* d, int op, void* stream) {
     case SUPA_AMD_RECIPROCAL: return run_unary<U_RECIPROCAL, false>(d, stream);
     case SUPA_AMD_ABS: return run_unary<U_ABS, false>(d, stream);
     case SUPA_AMD_SQRT: return run_unary<U_SQRT, false>(d, stream);
+    case SUPA_AMD_EXPM1: return run_unary<U_EXPM1, false>(d, stream);
+    case SUPA_AMD_LOG1P: return run_unary<U_LOG1P, false>(d, stream);
     default: return SUPA_AMD_EINVAL;
   }
 }

@@ -176,6 +176,8 @@ int fe_dispatch(int op, int form, const FeArgs& a, hipStream_t st) {
     SA_FE_UNARY(SUPA_AMD_RECIPROCAL)
     SA_FE_UNARY(SUPA_AMD_ABS)
     SA_FE_UNARY(SUPA_AMD_SQRT)
+    SA_FE_UNARY(SUPA_AMD_EXPM1)
+    SA_FE_UNARY(SUPA_AMD_LOG1P)
     default: return SUPA_AMD_EINVAL;
   }
 #undef SA_FE_BINARY

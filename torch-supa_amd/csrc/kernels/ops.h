@@ -132,10 +132,19 @@ template <typename C> __device__ __forceinline__ C erfx(C x) {
   if constexpr (std::is_same<C, float>::value) return sa_erff(x);
   else return erf(x);
 }
+template <typename C> __device__ __forceinline__ C expm1x(C x) {
+  if constexpr (std::is_same<C, float>::value) return sa_expm1f(x);
+  else return expm1(x);
+}
+template <typename C> __device__ __forceinline__ C log1px(C x) {
+  if constexpr (std::is_same<C, float>::value) return sa_log1pf(x);
+  else return log1p(x);
+}
 template <typename C> __device__ __forceinline__ C sigmoidx(C x) { return C(1) / (C(1) + expx<C>(-x)); }
 
 enum UnaryKind {
-  U_GELU = 0, U_GELU_TANH, U_SILU, U_SIGMOID, U_TANH, U_EXP, U_LOG, U_ERF, U_RELU, U_NEG, U_RECIPROCAL, U_ABS, U_SQRT
+  U_GELU = 0, U_GELU_TANH, U_SILU, U_SIGMOID, U_TANH, U_EXP, U_LOG, U_ERF, U_RELU, U_NEG, U_RECIPROCAL, U_ABS, U_SQRT,
+  U_EXPM1, U_LOG1P
 };
 
 template <int K, typename C> struct UnaryOp {
@@ -164,6 +173,10 @@ template <int K, typename C> struct UnaryOp {
       else return -x;
     } else if constexpr (K == U_RECIPROCAL) {
       return C(1) / x;
+    } else if constexpr (K == U_EXPM1) {
+      return expm1x<C>(x);
+    } else if constexpr (K == U_LOG1P) {
+      return log1px<C>(x);
     } else if constexpr (K == U_ABS) {
       if constexpr (std::is_same<C, bool>::value) return x;
       else if constexpr (std::is_integral<C>::value) return x < 0 ? (C)(0 - (uint64_t)x) : x;
@@ -204,6 +217,75 @@ template <int K, typename C> struct UnaryBwdOp {
       return (dy * (C(1) - x)) * x;
     } else {
       return dy * muladd<C>(-x, x, C(1));
+    }
+  }
+};
+
+// ------------------------------------------ parameterised activations
+// Upstream's CUDA activation functors (ActivationLeakyReluKernel.cu,
+// ActivationEluKernel.cu, ActivationSoftplusKernel.cu,
+// ActivationHardswishKernel.cu, ActivationHardsigmoidKernel.cu,
+// ActivationMishKernel.cu, ActivationLogSigmoidKernel.cu,
+// ActivationThresholdKernel.cu) in opmath with the parameters rounded to it;
+// `a + b * c` forms are one fma, as that compiler contracts them.  std::max /
+// std::min are the device forms (a < b) ? b : a and (b < a) ? b : a.
+enum ActKind {
+  A_LEAKY_RELU = 0, A_HARDTANH, A_ELU, A_SOFTPLUS, A_HARDSWISH, A_HARDSIGMOID, A_MISH, A_LOG_SIGMOID, A_THRESHOLD
+};
+template <typename C> __device__ __forceinline__ C max_lt(C a, C b) { return (a < b) ? b : a; }
+template <typename C> __device__ __forceinline__ C min_lt(C a, C b) { return (b < a) ? b : a; }
+
+// p0, p1, p2: leaky_relu (slope); elu (alpha, scale, input_scale); softplus
+// (beta, threshold); threshold (threshold, value).
+template <int K, typename C> struct ActOp {
+  static constexpr int arity = 1;
+  C p0, p1, p2;
+  __device__ __forceinline__ C operator()(const C* v) const {
+    const C x = v[0];
+    if constexpr (K == A_LEAKY_RELU) return x > C(0) ? x : x * p0;
+    else if constexpr (K == A_ELU) return x > C(0) ? x * p1 : expm1x<C>(x * p2) * (p0 * p1);
+    else if constexpr (K == A_SOFTPLUS) return (x * p0) > p1 ? x : log1px<C>(expx<C>(x * p0)) / p0;
+    else if constexpr (K == A_HARDSWISH) return (x * min_lt<C>(max_lt<C>(x + C(3), C(0)), C(6))) * C(1.0f / 6.0f);
+    else if constexpr (K == A_HARDSIGMOID) return min_lt<C>(max_lt<C>(x + C(3), C(0)), C(6)) * C(1.0f / 6.0f);
+    else if constexpr (K == A_MISH) return x * tanhx<C>(log1px<C>(expx<C>(x)));
+    else if constexpr (K == A_LOG_SIGMOID) return min_lt<C>(C(0), x) - log1px<C>(expx<C>(-fabs(x)));
+    else return x <= p0 ? p1 : x;  // threshold
+  }
+};
+
+// Inputs: the incoming gradient, then the forward input (elu with `flag`: the
+// forward output).  hardtanh: p0 = min, p1 = max.
+template <int K, typename C> struct ActBwdOp {
+  static constexpr int arity = 2;
+  C p0, p1, p2;
+  int flag;
+  __device__ __forceinline__ C operator()(const C* v) const {
+    const C g = v[0], x = v[1];
+    if constexpr (K == A_LEAKY_RELU) {
+      return x > C(0) ? g : g * p0;
+    } else if constexpr (K == A_HARDTANH) {
+      return (x <= p0 || x >= p1) ? C(0) : g;
+    } else if constexpr (K == A_ELU) {
+      const C negcoef = p0 * p1;
+      if (flag) return x <= C(0) ? (g * p2) * (x + negcoef) : g * p1;
+      return x <= C(0) ? ((g * p2) * negcoef) * expx<C>(x * p2) : g * p1;
+    } else if constexpr (K == A_SOFTPLUS) {
+      const C z = expx<C>(x * p0);
+      return (x * p0) > p1 ? g : (g * z) / (z + C(1));
+    } else if constexpr (K == A_HARDSWISH) {
+      return x < C(-3) ? C(0) : (x <= C(3) ? g * ((x / C(3)) + C(0.5)) : g);
+    } else if constexpr (K == A_HARDSIGMOID) {
+      return (x > C(-3) && x < C(3)) ? g * C(1.0f / 6.0f) : C(0);
+    } else if constexpr (K == A_MISH) {
+      const C sg = C(1) / (C(1) + expx<C>(-x));
+      const C t = tanhx<C>(log1px<C>(expx<C>(x)));
+      return g * muladd<C>(x * sg, muladd<C>(-t, t, C(1)), t);
+    } else if constexpr (K == A_LOG_SIGMOID) {
+      const bool neg = x < C(0);
+      const C z = expx<C>(-fabs(x));
+      return g * muladd<C>(neg ? C(-1) : C(1), z / (C(1) + z), neg ? C(1) : C(0));
+    } else {
+      return x <= p0 ? C(0) : g;  // threshold_backward
     }
   }
 };
