@@ -181,6 +181,30 @@ int supa_amd_activation(const supa_amd_ew_desc* d, int act, double p0, double p1
 int supa_amd_activation_backward(const supa_amd_ew_desc* d, int act, double p0, double p1, double p2, int flag,
                                  void* stream);
 
+/* ------------------------------------------ comparisons and selects */
+
+/* out = (a OP b) as 1 / 0, compared in common_dtype (NaN unequal to
+ * everything); out is usually bool.  op = {out, a, b}.  Replaces
+ * ne.Scalar_out / ne.Tensor_out NF:9089 / 9107, eq NF:9152 / 9171, ge NF:9190 /
+ * 9209, le NF:9254 / 9272, gt NF:9317 / 9336, lt NF:9381 / 9399 (upstream
+ * CompareEQKernel.cu, CompareKernels.cu). */
+#define SUPA_AMD_CMP_EQ 0
+#define SUPA_AMD_CMP_NE 1
+#define SUPA_AMD_CMP_LT 2
+#define SUPA_AMD_CMP_LE 3
+#define SUPA_AMD_CMP_GT 4
+#define SUPA_AMD_CMP_GE 5
+int supa_amd_compare(const supa_amd_ew_desc* d, int kind, void* stream);
+
+/* out = (x != x).  op = {out, x}.  Replaces isnan NF:3219 (upstream: self != self). */
+int supa_amd_isnan(const supa_amd_ew_desc* d, void* stream);
+
+/* out = cond ? a : b, cond bool; a or b may be immediate scalars.
+ * op = {out, cond, a, b}.  Replaces where.self_out NF:6701 (upstream
+ * TensorCompare.cu where_kernel) and, with a = value and b = out = self,
+ * masked_fill_.Scalar NF:8254 (upstream masked_fill_kernel). */
+int supa_amd_where(const supa_amd_ew_desc* d, void* stream);
+
 /* ------------------------------------------------------ copy / fill */
 
 /* out = cast(in), any strides and dtypes.  op = {out, in}.  Replaces the

@@ -879,3 +879,45 @@ def test_maximum_minimum_clamp(dtype, no_fallback):
     if dtype == torch.int64:
         # an integer tensor clamped by a float bound promotes, as upstream
         _exact(torch.clamp(da, -1.5, 2.5), torch.clamp(a, -1.5, 2.5))
+
+
+# --------------------------------------------- comparisons and selects
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.int64])
+def test_comparisons_where_masked_fill(dtype, no_fallback):
+    """Exact logical ops: the same booleans / selections as upstream's CPU
+    kernels, NaN included, over broadcasts, scalars, mixed dtypes and the
+    in-place / out= forms."""
+    g = torch.Generator().manual_seed(99)
+    if dtype.is_floating_point:
+        a = torch.randn(257, 1031, generator=g).to(dtype)
+        b = torch.randn(257, 1031, generator=g).to(dtype)
+        a[::13, ::7] = float("nan")
+        b[:, ::9] = a[:, ::9]
+    else:
+        a = torch.randint(-5, 5, (257, 1031), generator=g, dtype=dtype)
+        b = torch.randint(-5, 5, (257, 1031), generator=g, dtype=dtype)
+    da, db = dev(a), dev(b)
+    for fn in (torch.eq, torch.ne, torch.lt, torch.le, torch.gt, torch.ge):
+        assert torch.equal(fn(da, db).cpu(), fn(a, b)), fn
+        assert torch.equal(fn(da, 0.25).cpu(), fn(a, 0.25)), fn
+        assert torch.equal(fn(da, db[0]).cpu(), fn(a, b[0])), fn  # row broadcast
+    assert torch.equal((da < db.double()).cpu(), a < b.double())  # promotion
+    out = torch.empty(257, 1031, dtype=torch.bool, device="supa")
+    torch.ge(da, db, out=out)
+    assert torch.equal(out.cpu(), a >= b)
+    c = da.clone()
+    c.lt_(db)
+    assert torch.equal(c.cpu(), a.clone().lt_(b))
+    if dtype.is_floating_point:
+        assert torch.equal(torch.isnan(da).cpu(), torch.isnan(a))
+    cond = da > 0
+    _exact(torch.where(cond, da, db), torch.where(a > 0, a, b))  # NaN-aware equality
+    _exact(torch.where(cond, da, 0), torch.where(a > 0, a, 0))
+    _exact(torch.where(cond[0], da, db), torch.where((a > 0)[0], a, b))
+    m = da.clone()
+    m.masked_fill_(cond, -7)
+    _exact(m, a.clone().masked_fill_(a > 0, -7))
+    m = da.clone()
+    m.masked_fill_((db > 0)[:, :1], torch.tensor(3))  # column mask, 0-dim value
+    _exact(m, a.clone().masked_fill_((b > 0)[:, :1], torch.tensor(3)))
+    _exact(torch.masked_fill(da, cond, 1), torch.masked_fill(a, a > 0, 1))

@@ -816,6 +816,91 @@ SUPA_UNARY_BWD(sigmoid, SUPA_AMD_SIGMOID)
 SUPA_UNARY_BWD(tanh, SUPA_AMD_TANH)
 #undef SUPA_UNARY_BWD
 
+// ------------------------------------------------ comparisons and selects
+// eq/ne/lt/le/gt/ge: compared in the promoted dtype, a bool result (the out=
+// tensor's dtype for .out, self's for the in-place forms).
+Launch cmp_launch(int kind) {
+  return [kind](const supa_amd_ew_desc* d, void* s) { return supa_amd_compare(d, kind, s); };
+}
+at::Tensor compare(const at::Tensor& self, const EwIn& other, c10::ScalarType common, at::Tensor out, bool inplace,
+                   int kind, const char* name) {
+  std::vector<EwIn> ins{EwIn::of(self), other};
+  if (inplace) return ew_apply(self, self.scalar_type(), common, ins, cmp_launch(kind), name);
+  if (out.defined()) return ew_apply(out, out.scalar_type(), common, ins, cmp_launch(kind), name);
+  return ew_apply(at::Tensor(), at::kBool, common, ins, cmp_launch(kind), name);
+}
+#define SUPA_CMP(NAME, KIND)                                                                                      \
+  at::Tensor NAME##_t(const at::Tensor& s, const at::Tensor& o) {                                                 \
+    return compare(s, EwIn::of(o), at::result_type(s, o), {}, false, KIND, #NAME ".Tensor");                      \
+  }                                                                                                               \
+  at::Tensor& NAME##_t_(at::Tensor& s, const at::Tensor& o) {                                                     \
+    compare(s, EwIn::of(o), at::result_type(s, o), {}, true, KIND, #NAME "_.Tensor");                             \
+    return s;                                                                                                     \
+  }                                                                                                               \
+  at::Tensor& NAME##_t_out(const at::Tensor& s, const at::Tensor& o, at::Tensor& out) {                           \
+    compare(s, EwIn::of(o), at::result_type(s, o), out, false, KIND, #NAME ".Tensor_out");                        \
+    return out;                                                                                                   \
+  }                                                                                                               \
+  at::Tensor NAME##_s(const at::Tensor& s, const c10::Scalar& o) {                                                \
+    return compare(s, EwIn::num(o), at::result_type(s, o), {}, false, KIND, #NAME ".Scalar");                     \
+  }                                                                                                               \
+  at::Tensor& NAME##_s_(at::Tensor& s, const c10::Scalar& o) {                                                    \
+    compare(s, EwIn::num(o), at::result_type(s, o), {}, true, KIND, #NAME "_.Scalar");                            \
+    return s;                                                                                                     \
+  }                                                                                                               \
+  at::Tensor& NAME##_s_out(const at::Tensor& s, const c10::Scalar& o, at::Tensor& out) {                          \
+    compare(s, EwIn::num(o), at::result_type(s, o), out, false, KIND, #NAME ".Scalar_out");                       \
+    return out;                                                                                                   \
+  }
+SUPA_CMP(eq, SUPA_AMD_CMP_EQ)
+SUPA_CMP(ne, SUPA_AMD_CMP_NE)
+SUPA_CMP(lt, SUPA_AMD_CMP_LT)
+SUPA_CMP(le, SUPA_AMD_CMP_LE)
+SUPA_CMP(gt, SUPA_AMD_CMP_GT)
+SUPA_CMP(ge, SUPA_AMD_CMP_GE)
+#undef SUPA_CMP
+
+at::Tensor isnan_t(const at::Tensor& s) {
+  const Launch fn = [](const supa_amd_ew_desc* d, void* st) { return supa_amd_isnan(d, st); };
+  return ew_apply(at::Tensor(), at::kBool, s.scalar_type(), {EwIn::of(s)}, fn, "isnan");
+}
+
+Launch where_launch() {
+  return [](const supa_amd_ew_desc* d, void* s) { return supa_amd_where(d, s); };
+}
+at::Tensor where_into(const at::Tensor& cond, const at::Tensor& a, const at::Tensor& b, at::Tensor out,
+                      const char* name) {
+  TORCH_CHECK(cond.scalar_type() == at::kBool,
+              "where expected condition to be a boolean tensor, but got a tensor with dtype ", cond.scalar_type());
+  const c10::ScalarType common = at::result_type(a, b);
+  std::vector<EwIn> ins{EwIn::of(cond), EwIn::of(a), EwIn::of(b)};
+  if (out.defined()) return ew_apply(out, out.scalar_type(), common, ins, where_launch(), name);
+  return ew_apply(at::Tensor(), common, common, ins, where_launch(), name);
+}
+at::Tensor where_self(const at::Tensor& c, const at::Tensor& a, const at::Tensor& b) {
+  return where_into(c, a, b, {}, "where.self");
+}
+at::Tensor& where_self_out(const at::Tensor& c, const at::Tensor& a, const at::Tensor& b, at::Tensor& out) {
+  where_into(c, a, b, out, "where.self_out");
+  return out;
+}
+
+// masked_fill_: self = mask ? value : self, the mask broadcast to self.
+at::Tensor& masked_fill_s(at::Tensor& self, const at::Tensor& mask, const c10::Scalar& value) {
+  TORCH_CHECK(mask.scalar_type() == at::kBool, "masked_fill_ only supports boolean masks, but got mask with dtype ",
+              mask.scalar_type());
+  TORCH_CHECK(self.device() == mask.device(), "expected self and mask to be on the same device, but got mask on ",
+              mask.device(), " and self on ", self.device());
+  ew_apply(self, self.scalar_type(), self.scalar_type(), {EwIn::of(mask), EwIn::num(value), EwIn::of(self)},
+           where_launch(), "masked_fill_");
+  return self;
+}
+at::Tensor& masked_fill_t(at::Tensor& self, const at::Tensor& mask, const at::Tensor& value) {
+  TORCH_CHECK(value.dim() == 0, "masked_fill_ only supports a 0-dimensional value tensor, but got tensor with ",
+              value.dim(), " dimension(s).");
+  return masked_fill_s(self, mask, value.item());
+}
+
 // ------------------------------------------------ parameterised activations
 // leaky_relu, elu, softplus, hardswish, hardsigmoid, mish, log_sigmoid,
 // threshold and their backwards (hardtanh's forward is clamp), with
@@ -1090,6 +1175,25 @@ TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
   m.impl("lerp.Tensor", TORCH_FN(lerp_t));
   m.impl("lerp_.Tensor", TORCH_FN(lerp_t_));
   m.impl("lerp.Tensor_out", TORCH_FN(lerp_t_out));
+#define SUPA_REG_CMP(NAME)                                    \
+  m.impl(#NAME ".Tensor", TORCH_FN(NAME##_t));                \
+  m.impl(#NAME "_.Tensor", TORCH_FN(NAME##_t_));              \
+  m.impl(#NAME ".Tensor_out", TORCH_FN(NAME##_t_out));        \
+  m.impl(#NAME ".Scalar", TORCH_FN(NAME##_s));                \
+  m.impl(#NAME "_.Scalar", TORCH_FN(NAME##_s_));              \
+  m.impl(#NAME ".Scalar_out", TORCH_FN(NAME##_s_out));
+  SUPA_REG_CMP(eq)
+  SUPA_REG_CMP(ne)
+  SUPA_REG_CMP(lt)
+  SUPA_REG_CMP(le)
+  SUPA_REG_CMP(gt)
+  SUPA_REG_CMP(ge)
+#undef SUPA_REG_CMP
+  m.impl("isnan", TORCH_FN(isnan_t));
+  m.impl("where.self", TORCH_FN(where_self));
+  m.impl("where.self_out", TORCH_FN(where_self_out));
+  m.impl("masked_fill_.Scalar", TORCH_FN(masked_fill_s));
+  m.impl("masked_fill_.Tensor", TORCH_FN(masked_fill_t));
   m.impl("leaky_relu", TORCH_FN(leaky_relu));
   m.impl("leaky_relu_", TORCH_FN(leaky_relu_));
   m.impl("leaky_relu.out", TORCH_FN(leaky_relu_out));

@@ -62,10 +62,22 @@ template <typename Op> struct UnrollOf<Op, std::void_t<decltype(Op::kUnroll)>> {
   static constexpr int value = Op::kUnroll;
 };
 
+// Storage pattern an op has static kernels for beyond "every operand in the
+// common dtype": 1 = bool output from common-dtype inputs (comparisons,
+// isnan); 2 = a bool first input, the rest and the output common (where,
+// masked_fill).  Other combinations take the dynamic kernel.
+template <typename Op, typename = void> struct DtypeModeOf {
+  static constexpr int value = 0;
+};
+template <typename Op> struct DtypeModeOf<Op, std::void_t<decltype(Op::kDtypeMode)>> {
+  static constexpr int value = Op::kDtypeMode;
+};
+
 template <typename Op, typename C>
 struct Bind1 {  // binds input position K to value v
   static constexpr int arity = Op::arity - 1;
   static constexpr int kUnroll = UnrollOf<Op>::value;
+  static constexpr int kDtypeMode = DtypeModeOf<Op>::value;
   Op op;
   int k;
   C v;

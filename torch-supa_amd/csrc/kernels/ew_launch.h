@@ -129,6 +129,8 @@ template <typename... S> constexpr int max_size() {
 template <typename Op, typename C, typename CT, typename OT, typename... S>
 int launch_static(const Op& op, const supa_amd_ew_desc& d, const int* tin, hipStream_t st) {
   constexpr int N = sizeof...(S);
+  // one storage type per tensor input of the (scalar-bound) op
+  static_assert(N == Op::arity, "launch_static: the input storage types must match the op's tensor inputs");
   // one 16-byte access for the widest operand: a bf16 -> f32 widening moves
   // 8-byte input and 16-byte output vectors (66 % faster than 16 / 32 bytes)
   constexpr int VEC0 = 16 / max_size<OT, S...>();
@@ -345,6 +347,32 @@ int dispatch_types(const Op& op, const supa_amd_ew_desc& d, const int* tin, hipS
         return launch_static<Op, C, T, T, T, T, T, T, T>(op, d, tin, st);
       }
     });
+  }
+  constexpr int mode = DtypeModeOf<Op>::value;
+  if constexpr (mode == 1 && N >= 1 && N <= 2) {  // bool output, common-dtype inputs
+    bool ok = d.op[0].dtype == SUPA_AMD_BOOL && common != SUPA_AMD_BOOL;
+    for (int i = 0; i < N; ++i) ok = ok && d.op[tin[i]].dtype == common;
+    if (ok) {
+      return with_storage(common, [&](auto* tag) -> int {
+        using T = std::remove_pointer_t<decltype(tag)>;
+        if constexpr (!compute_compatible<T, C>()) return SUPA_AMD_EDTYPE;
+        else if constexpr (N == 1) return launch_static<Op, C, T, b8, T>(op, d, tin, st);
+        else return launch_static<Op, C, T, b8, T, T>(op, d, tin, st);
+      });
+    }
+  }
+  if constexpr (mode == 2 && N >= 1 && N <= 3) {  // bool first input, the rest common
+    bool ok = d.op[0].dtype == common && d.op[tin[0]].dtype == SUPA_AMD_BOOL && common != SUPA_AMD_BOOL;
+    for (int i = 1; i < N; ++i) ok = ok && d.op[tin[i]].dtype == common;
+    if (ok) {
+      return with_storage(common, [&](auto* tag) -> int {
+        using T = std::remove_pointer_t<decltype(tag)>;
+        if constexpr (!compute_compatible<T, C>()) return SUPA_AMD_EDTYPE;
+        else if constexpr (N == 1) return launch_static<Op, C, T, T, b8>(op, d, tin, st);
+        else if constexpr (N == 2) return launch_static<Op, C, T, T, b8, T>(op, d, tin, st);
+        else return launch_static<Op, C, T, T, b8, T, T>(op, d, tin, st);
+      });
+    }
   }
   if constexpr (std::is_same<C, float>::value && N >= 1 && N <= 2) {
     auto fam = [](int dt) { return dt == SUPA_AMD_F32 || dt == SUPA_AMD_BF16 || dt == SUPA_AMD_F16; };

@@ -343,6 +343,36 @@ template <typename C> struct MinOp {
   }
 };
 
+// ---------------------------------------------- comparisons and selects
+// eq/ne/lt/le/gt/ge in the common dtype (NaN compares unequal to
+// everything), 1 or 0 in the compute type; the output is usually bool.
+enum CmpKind { CMP_EQ = 0, CMP_NE, CMP_LT, CMP_LE, CMP_GT, CMP_GE };
+template <int K, typename C> struct CmpOp {
+  static constexpr int arity = 2;
+  static constexpr int kDtypeMode = 1;
+  __device__ __forceinline__ C operator()(const C* x) const {
+    bool r;
+    if constexpr (K == CMP_EQ) r = x[0] == x[1];
+    else if constexpr (K == CMP_NE) r = x[0] != x[1];
+    else if constexpr (K == CMP_LT) r = x[0] < x[1];
+    else if constexpr (K == CMP_LE) r = x[0] <= x[1];
+    else if constexpr (K == CMP_GT) r = x[0] > x[1];
+    else r = x[0] >= x[1];
+    return r ? C(1) : C(0);
+  }
+};
+template <typename C> struct IsNanOp {
+  static constexpr int arity = 1;
+  static constexpr int kDtypeMode = 1;
+  __device__ __forceinline__ C operator()(const C* x) const { return x[0] != x[0] ? C(1) : C(0); }
+};
+// where(cond, a, b) and masked_fill (cond = mask, a = value, b = self).
+template <typename C> struct WhereOp {
+  static constexpr int arity = 3;
+  static constexpr int kDtypeMode = 2;
+  __device__ __forceinline__ C operator()(const C* x) const { return x[0] != C(0) ? x[1] : x[2]; }
+};
+
 // ------------------------------------------------------------ copy/fill
 template <typename C> struct IdentityOp {
   static constexpr int arity = 1;
