@@ -184,7 +184,9 @@ enum {
 #define OR_GELU_KAPPA 0.044715f
 
 /* Forward formulas (all in float32 opmath):
- *  gelu 'none': x*0.5*(1+erf(x*sqrt(1/2)))            NF:5216, CPU Gelu.h:61-65
+ *  gelu 'none': x*0.5*(1+erf(x*sqrt(1/2))) rewritten as x - (x/2) erfc(|x|/sqrt2)
+ *               (x >= 0) or (x/2) erfc(|x|/sqrt2) (x < 0)   NF:5216, CPU Gelu.h:61-65
+ *               (or_gelu_none: no cancellation of 1 + erf for x << 0)
  *  gelu 'tanh': 0.5*x*(1+tanh(b*(x+k*x^3))) rewritten exactly as
  *               x / (1 + exp(-2*b*(x+k*x^3)))         NF:5216, CPU Gelu.h:34-41
  *               (the identity 0.5*(1+tanh(u)) = 1/(1+exp(-2u)); it removes the
@@ -195,7 +197,7 @@ enum {
  *  reciprocal, abs, sqrt: IEEE 1/x, |x| and correctly rounded sqrt. */
 static inline float act_fwd(int op, float x) {
   switch (op) {
-    case OR_GELU: return (x * 0.5f) * (1.0f + or_erff(x * OR_SQRT1_2));
+    case OR_GELU: return or_gelu_none(x);
     case OR_GELU_TANH: {
       const float x3 = (x * x) * x;
       const float inner = (-2.0f * OR_GELU_BETA_TANH) * fmaf(OR_GELU_KAPPA, x3, x);
@@ -218,7 +220,7 @@ static inline float act_fwd(int op, float x) {
 }
 
 /* Backward formulas (upstream aten activation backward functors, float32):
- *  gelu 'none': dy*(cdf + x*pdf), cdf = 0.5*(1+erf(x*sqrt(1/2))),
+ *  gelu 'none': dy*(cdf + x*pdf), cdf = Phi(x) (or_phif, the same erfc form),
  *               pdf = exp(-0.5*x*x) * (M_2_SQRTPI*M_SQRT1_2*0.5)     NF:5245
  *  gelu 'tanh': dy*(0.5*(1+t) + 0.5*x*(1-t*t)*b*(1+3k*x^2)),
  *               t = tanh(b*(x+k*x^3))                                NF:5245
@@ -228,7 +230,7 @@ static inline float act_fwd(int op, float x) {
 static inline float act_bwd(int op, float dy, float x) {
   switch (op) {
     case OR_GELU: {
-      const float cdf = 0.5f * (1.0f + or_erff(x * OR_SQRT1_2));
+      const float cdf = or_phif(x);
       const float pdf = or_expf((-0.5f * x) * x) * OR_GELU_BETA_NONE;
       return dy * fmaf(x, pdf, cdf);
     }

@@ -168,6 +168,44 @@ __device__ __forceinline__ float sa_log1pf(float z) {
   return (u == 0.0f) ? -__builtin_inff() : r;
 }
 
+// Normal CDF pieces for gelu 'none': with t = |x| / sqrt(2) (clamped to
+// 3.925), E = erfc(t) = exp(L(t)), L ~ log(erfc) fitted on [0, 3.925]
+// (degree 11).  Then gelu(x) = x - (x/2) E for x >= 0 and (x/2) E for x < 0
+// -- the same function as x (1 + erf(x / sqrt 2)) / 2 without the
+// cancellation of 1 + erf for x << 0 -- and x or -0 once t > 3.925.
+__device__ __forceinline__ float sa_erfc_core(float x) {
+  const float tc = fminf(fabsf(x) * 0.70710678118654752f, 3.925f);
+  float l = 8.385092797880134e-08f;
+  l = fmaf(l, tc, -2.177875103370752e-06f);
+  l = fmaf(l, tc, 2.5186680431943387e-05f);
+  l = fmaf(l, tc, -0.00016940578643698245f);
+  l = fmaf(l, tc, 0.0007112529128789902f);
+  l = fmaf(l, tc, -0.001697514788247645f);
+  l = fmaf(l, tc, 9.264998516300693e-05f);
+  l = fmaf(l, tc, 0.01925601065158844f);
+  l = fmaf(l, tc, -0.10283640027046204f);
+  l = fmaf(l, tc, -0.6366046667098999f);
+  l = fmaf(l, tc, -1.128380537033081f);
+  l = fmaf(l, tc, 2.0115285437327657e-08f);
+  return sa_expf_nn(l);  // l in [-17.5, 0]
+}
+__device__ __forceinline__ float sa_gelu_none(float x) {
+  const float t = fabsf(x) * 0.70710678118654752f;
+  const float e = sa_erfc_core(x);
+  const float hx = 0.5f * x;
+  float g = (x >= 0.0f) ? fmaf(-hx, e, x) : hx * e;  // a NaN x stays NaN
+  g = (t > 3.925f) ? ((x >= 0.0f) ? x : x * 0.0f) : g;
+  return g;
+}
+// Phi(x) = P(N(0, 1) <= x) through the same E: 1 - E/2 or E/2.
+__device__ __forceinline__ float sa_phif(float x) {
+  const float t = fabsf(x) * 0.70710678118654752f;
+  const float e = sa_erfc_core(x);
+  float p = (x >= 0.0f) ? fmaf(-0.5f, e, 1.0f) : 0.5f * e;
+  p = (t > 3.925f) ? ((x >= 0.0f) ? 1.0f : 0.0f) : p;
+  return (x != x) ? x : p;
+}
+
 __device__ __forceinline__ float sa_tanhf(float x) {
   const float a = fabsf(x);
   if (a < 0.55f) {

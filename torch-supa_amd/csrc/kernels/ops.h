@@ -100,7 +100,7 @@ static_assert((float)kGeluBetaTanh == 0.7978845608028654f, "constant rounding");
 static_assert((float)kGeluKappa == 0.044715f, "constant rounding");
 
 template <typename C> __device__ __forceinline__ C gelu_none(C x) {
-  if constexpr (std::is_same<C, float>::value) return (x * 0.5f) * (1.0f + sa_erff(x * (float)kSqrt1_2));
+  if constexpr (std::is_same<C, float>::value) return sa_gelu_none(x);
   else return (x * C(0.5)) * (C(1) + erf(x * C(kSqrt1_2)));
 }
 // gelu 'tanh' as x * sigmoid(2u), u = b (x + k x^3): the same function as
@@ -195,7 +195,9 @@ template <int K, typename C> struct UnaryBwdOp {
   __device__ __forceinline__ C operator()(const C* v) const {
     const C dy = v[0], x = v[1];
     if constexpr (K == U_GELU) {
-      const C cdf = C(0.5) * (C(1) + erfx<C>(x * C(kSqrt1_2)));
+      C cdf;
+      if constexpr (std::is_same<C, float>::value) cdf = sa_phif(x);
+      else cdf = C(0.5) * (C(1) + erf(x * C(kSqrt1_2)));
       const C pdf = expx<C>((C(-0.5) * x) * x) * C(kGeluBetaNone);
       return dy * muladd<C>(x, pdf, cdf);
     } else if constexpr (K == U_GELU_TANH) {
