@@ -205,6 +205,28 @@ int supa_amd_isnan(const supa_amd_ew_desc* d, void* stream);
  * masked_fill_.Scalar NF:8254 (upstream masked_fill_kernel). */
 int supa_amd_where(const supa_amd_ew_desc* d, void* stream);
 
+/* out = (mask * grad) * scale, mask bool.  op = {out, mask, grad}.
+ * Replaces native_dropout_backward NF:296 (upstream masked_scale_kernel). */
+int supa_amd_mask_scale(const supa_amd_ew_desc* d, double scale, void* stream);
+
+/* ------------------------------------------------------ random numbers */
+
+/* Counter-based Philox4x32-10 draws: element i of a call with (seed, offset)
+ * is word i % 4 of philox(counter = (i / 4, offset), key = seed), u =
+ * (word >> 8) * 2^-24 in [0, 1).  out is a contiguous f32 / bf16 / f16
+ * buffer of n elements.  The caller's generator supplies (seed, offset) and
+ * advances offset by one per call.
+ *   uniform:   out = fma(u, hi - lo, lo)        uniform_ NF:8983
+ *   bernoulli: out = u < p ? 1 : 0              bernoulli_.float NF:1146
+ *   dropout:   mask = u < keep, out = (x * mask) * (1 / keep)
+ *                                               native_dropout NF:286
+ * (The reference draws through curand's Philox; the streams differ.) */
+int supa_amd_uniform(void* out, int32_t dtype, int64_t n, double lo, double hi, uint64_t seed, uint64_t offset,
+                     void* stream);
+int supa_amd_bernoulli(void* out, int32_t dtype, int64_t n, double p, uint64_t seed, uint64_t offset, void* stream);
+int supa_amd_dropout(const void* x, int32_t dtype, void* out, uint8_t* mask, int64_t n, double keep, uint64_t seed,
+                     uint64_t offset, void* stream);
+
 /* ------------------------------------------------------ copy / fill */
 
 /* out = cast(in), any strides and dtypes.  op = {out, in}.  Replaces the

@@ -33,6 +33,7 @@ MSE, SMOOTH_L1, BCE_LOGITS = 0, 1, 2
 REDUCTION = {"none": 0, "mean": 1, "sum": 2}
 
 _f32p = ctypes.POINTER(ctypes.c_float)
+_u32p = ctypes.POINTER(ctypes.c_uint32)
 _f64p = ctypes.POINTER(ctypes.c_double)
 _u16p = ctypes.POINTER(ctypes.c_uint16)
 _i64p = ctypes.POINTER(ctypes.c_int64)
@@ -66,6 +67,11 @@ def lib():
             "or_log_softmax_fwd": (None, [_f32p, _f32p, i64, i64]),
             "or_log_softmax_bwd": (None, [_f32p, _f32p, _f32p, i64, i64]),
             "or_softmax_fwd": (None, [_f32p, _f32p, i64, i64]),
+            "or_philox4x32_10": (None, [_u32p, _u32p, _u32p]),
+            "or_rng_u32": (None, [ctypes.c_uint64, ctypes.c_uint64, i64, _u32p]),
+            "or_uniform_f32": (None, [ctypes.c_uint64, ctypes.c_uint64, i64, c_float, c_float, _u32p, _f32p]),
+            "or_dropout_f32": (None, [ctypes.c_uint64, ctypes.c_uint64, i64, _f32p, c_float, _u32p, _f32p,
+                                      ctypes.POINTER(ctypes.c_uint8)]),
             "or_softmax_bwd": (None, [_f32p, _f32p, _f32p, i64, i64]),
             "or_nll_loss_fwd": (c_int, [_f32p, _i64p, _f32p, i64, i64, c_int, i64, _f32p, _f32p]),
             "or_nll_loss_bwd": (c_int, [_f32p, _i64p, _f32p, i64, i64, c_int, i64, c_float, c_int, _f32p]),
@@ -397,3 +403,36 @@ def vector_norm(x, ord=2.0) -> float:
     if ord == float("inf"):
         return float("nan") if np.isnan(a).any() else float(a.max())
     raise ValueError(f"ord {ord} not supported")
+
+
+# ------------------------------------------------------------ random numbers
+def philox4x32_10(ctr, key) -> np.ndarray:
+    c = np.ascontiguousarray(ctr, np.uint32)
+    k = np.ascontiguousarray(key, np.uint32)
+    out = np.empty(4, np.uint32)
+    lib().or_philox4x32_10(_p(c, _u32p), _p(k, _u32p), _p(out, _u32p))
+    return out
+
+
+def rng_u32(seed: int, offset: int, n: int) -> np.ndarray:
+    out = np.empty(n, np.uint32)
+    lib().or_rng_u32(seed, offset, n, _p(out, _u32p))
+    return out
+
+
+def uniform(seed: int, offset: int, n: int, lo=0.0, hi=1.0) -> np.ndarray:
+    scratch = np.empty(n, np.uint32)
+    out = np.empty(n, np.float32)
+    lib().or_uniform_f32(seed, offset, n, lo, hi, _p(scratch, _u32p), _p(out, _f32p))
+    return out
+
+
+def dropout(seed: int, offset: int, x, keep: float):
+    """Returns (out, mask) of dropout with keep probability `keep`."""
+    x = _c(x, np.float32).reshape(-1)
+    scratch = np.empty(x.size, np.uint32)
+    out = np.empty(x.size, np.float32)
+    mask = np.empty(x.size, np.uint8)
+    lib().or_dropout_f32(seed, offset, x.size, _p(x, _f32p), keep, _p(scratch, _u32p), _p(out, _f32p),
+                         mask.ctypes.data_as(ctypes.POINTER(ctypes.c_uint8)))
+    return out, mask.astype(bool)

@@ -702,3 +702,61 @@ void or_adamw_step(float* p, float* g, float* m, float* v, int64_t n, float step
     v[i] = eas;
   }
 }
+
+/* ------------------------------------------------------ random numbers -- */
+
+/* Philox4x32-10 (Salmon, Moraes, Dror, Shaw, "Parallel random numbers: as
+ * easy as 1, 2, 3", SC 2011): ten rounds of the two 32x32->64 multiplies
+ * (0xD2511F53, 0xCD9E8D57), the key bumped by the Weyl constants
+ * (0x9E3779B9, 0xBB67AE85) between rounds.  Pinned by the Random123
+ * known-answer vectors in tests/test_oracle_rng.py. */
+void or_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]) {
+  uint32_t c0 = ctr[0], c1 = ctr[1], c2 = ctr[2], c3 = ctr[3], k0 = key[0], k1 = key[1];
+  for (int r = 0; r < 10; ++r) {
+    if (r) { k0 += 0x9E3779B9u; k1 += 0xBB67AE85u; }
+    const uint64_t p0 = (uint64_t)0xD2511F53u * c0, p1 = (uint64_t)0xCD9E8D57u * c2;
+    const uint32_t n0 = (uint32_t)(p1 >> 32) ^ c1 ^ k0, n2 = (uint32_t)(p0 >> 32) ^ c3 ^ k1;
+    c1 = (uint32_t)p1;
+    c3 = (uint32_t)p0;
+    c0 = n0;
+    c2 = n2;
+  }
+  out[0] = c0; out[1] = c1; out[2] = c2; out[3] = c3;
+}
+
+/* The device's element stream: element i is word i % 4 of
+ * philox(counter = (i / 4 as 64 bits, offset as 64 bits), key = seed). */
+void or_rng_u32(uint64_t seed, uint64_t offset, int64_t n, uint32_t* out) {
+  const uint32_t key[2] = {(uint32_t)seed, (uint32_t)(seed >> 32)};
+  for (int64_t q = 0; q * 4 < n; ++q) {
+    const uint32_t ctr[4] = {(uint32_t)q, (uint32_t)((uint64_t)q >> 32), (uint32_t)offset, (uint32_t)(offset >> 32)};
+    uint32_t r[4];
+    or_philox4x32_10(ctr, key, r);
+    for (int j = 0; j < 4 && q * 4 + j < n; ++j) out[q * 4 + j] = r[j];
+  }
+}
+
+/* u in [0, 1) from the top 24 bits of a word. */
+static inline float or_u01(uint32_t r) { return (float)(r >> 8) * 5.9604644775390625e-08f; }
+
+/* uniform_(from, to): fma(u, to - from, from) in float, with `to - from`
+ * rounded to float first. */
+void or_uniform_f32(uint64_t seed, uint64_t offset, int64_t n, float lo, float hi, uint32_t* scratch, float* out) {
+  or_rng_u32(seed, offset, n, scratch);
+  const float range = hi - lo;
+  for (int64_t i = 0; i < n; ++i) out[i] = fmaf(or_u01(scratch[i]), range, lo);
+}
+
+/* dropout with keep probability q: mask = u < q; out = (x * mask) * scale,
+ * scale = 1.0 / q divided in double and rounded to float (upstream
+ * Dropout.cu fused_dropout_kernel: accscalar_t scale = 1.0 / p). */
+void or_dropout_f32(uint64_t seed, uint64_t offset, int64_t n, const float* x, float q, uint32_t* scratch,
+                    float* out, uint8_t* mask) {
+  or_rng_u32(seed, offset, n, scratch);
+  const float scale = (float)(1.0 / (double)q);
+  for (int64_t i = 0; i < n; ++i) {
+    const int keep = or_u01(scratch[i]) < q;
+    mask[i] = (uint8_t)keep;
+    out[i] = (x[i] * (keep ? 1.0f : 0.0f)) * scale;
+  }
+}

@@ -7,6 +7,7 @@
 #include <torch/extension.h>
 
 #include "common.h"
+#include "generator.h"
 #include "planner.h"
 
 namespace py = pybind11;
@@ -77,6 +78,32 @@ void memcpy_d2d(uintptr_t dst, uintptr_t src, int64_t nbytes) {
                                 hipMemcpyDeviceToDevice, supa::current_stream(supa::current_device())));
 }
 
+// The device's default Philox generator, for torch.supa's seeding API.
+supa::SupaGenerator* gen_of(int dev) {
+  return supa::default_generator(static_cast<c10::DeviceIndex>(dev)).get<supa::SupaGenerator>();
+}
+void rng_manual_seed(int dev, uint64_t seed) {
+  supa::SupaGenerator* g = gen_of(dev);
+  std::lock_guard<std::mutex> lock(g->mutex_);
+  g->set_current_seed(seed);
+}
+uint64_t rng_seed(int dev) {
+  supa::SupaGenerator* g = gen_of(dev);
+  std::lock_guard<std::mutex> lock(g->mutex_);
+  return g->seed();
+}
+uint64_t rng_initial_seed(int dev) { return gen_of(dev)->current_seed(); }
+at::Tensor rng_get_state(int dev) {
+  supa::SupaGenerator* g = gen_of(dev);
+  std::lock_guard<std::mutex> lock(g->mutex_);
+  return at::Tensor::wrap_tensor_impl(g->get_state());
+}
+void rng_set_state(int dev, const at::Tensor& st) {
+  supa::SupaGenerator* g = gen_of(dev);
+  std::lock_guard<std::mutex> lock(g->mutex_);
+  g->set_state(*st.unsafeGetTensorImpl());
+}
+
 }  // namespace
 
 PYBIND11_MODULE(_C, m) {
@@ -104,4 +131,9 @@ PYBIND11_MODULE(_C, m) {
   m.def("event_elapsed_ms", &event_elapsed_ms);
   m.def("event_destroy", &event_destroy);
   m.def("memcpy_d2d", &memcpy_d2d);
+  m.def("rng_manual_seed", &rng_manual_seed);
+  m.def("rng_seed", &rng_seed);
+  m.def("rng_initial_seed", &rng_initial_seed);
+  m.def("rng_get_state", &rng_get_state);
+  m.def("rng_set_state", &rng_set_state);
 }

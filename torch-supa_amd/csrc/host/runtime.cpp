@@ -22,6 +22,8 @@
 #include <c10/util/Exception.h>
 #include <torch/library.h>
 
+#include "generator.h"
+
 #include <algorithm>
 #include <atomic>
 #include <cstdlib>
@@ -418,6 +420,10 @@ struct SupaHooks final : public at::PrivateUse1HooksInterface {
     (void)hipGetLastError();
     return at::Device(kSupa, current_device());
   }
+  const at::Generator& getDefaultGenerator(c10::DeviceIndex device_index) const override {
+    return default_generator(device_index);
+  }
+  at::Generator getNewGenerator(c10::DeviceIndex device_index) const override { return new_generator(device_index); }
   bool isPinnedPtr(const void* /*data*/) const override { return false; }
   at::Allocator* getPinnedMemoryAllocator() const override { return at::getCPUAllocator(); }
   void resizePrivateUse1Bytes(const c10::Storage& storage, size_t newsize) const override {

@@ -368,6 +368,14 @@ template <typename C> struct IsNanOp {
   static constexpr int kDtypeMode = 1;
   __device__ __forceinline__ C operator()(const C* x) const { return x[0] != x[0] ? C(1) : C(0); }
 };
+// native_dropout_backward: (mask * grad) * scale, upstream masked_scale's
+// order (a NaN gradient under a zero mask stays NaN there too).
+template <typename C> struct MaskScaleOp {
+  static constexpr int arity = 2;
+  static constexpr int kDtypeMode = 2;
+  C scale;
+  __device__ __forceinline__ C operator()(const C* x) const { return (x[0] * x[1]) * scale; }
+};
 // where(cond, a, b) and masked_fill (cond = mask, a = value, b = self).
 template <typename C> struct WhereOp {
   static constexpr int arity = 3;

@@ -84,34 +84,50 @@ def empty_cache() -> None:
     _C.empty_cache()
 
 
-# Random numbers for this backend are drawn by the CPU generator (the CPU
-# fallback runs the sampling ops); seeding therefore goes to the CPU generator.
+# Each supa device has a default Philox generator (seed + call offset) that
+# the native random ops (uniform_, bernoulli_, dropout) draw from.
+# torch.manual_seed reaches manual_seed_all through the PrivateUse1 module
+# hooks (it checks _is_in_bad_fork, then calls manual_seed_all).  Same API as
+# the reference's torch_supa/supa/random.py:26-172.
 def manual_seed(seed: int) -> None:
-    torch.random.default_generator.manual_seed(int(seed))
+    _C.rng_manual_seed(_C.current_device(), int(seed) & 0xFFFFFFFFFFFFFFFF)
 
 
 def manual_seed_all(seed: int) -> None:
-    manual_seed(seed)
+    for d in range(device_count()):
+        _C.rng_manual_seed(d, int(seed) & 0xFFFFFFFFFFFFFFFF)
 
 
 def seed() -> None:
-    torch.random.seed()
+    _C.rng_seed(_C.current_device())
 
 
 def seed_all() -> None:
-    torch.random.seed()
+    s = _C.rng_seed(0) if device_count() else 0
+    for d in range(1, device_count()):
+        _C.rng_manual_seed(d, s)
 
 
 def initial_seed() -> int:
-    return torch.random.initial_seed()
+    return _C.rng_initial_seed(_C.current_device())
 
 
-def get_rng_state(device=None):
-    return torch.random.get_rng_state()
+def get_rng_state(device=None) -> torch.Tensor:
+    """16 bytes (uint8, CPU): the seed, then the call offset, little endian."""
+    return _C.rng_get_state(_index(device) if device is not None else _C.current_device())
 
 
-def set_rng_state(state, device=None) -> None:
-    torch.random.set_rng_state(state)
+def set_rng_state(state: torch.Tensor, device=None) -> None:
+    _C.rng_set_state(_index(device) if device is not None else _C.current_device(), state)
+
+
+def get_rng_state_all() -> list:
+    return [_C.rng_get_state(d) for d in range(device_count())]
+
+
+def set_rng_state_all(states) -> None:
+    for d, st in enumerate(states):
+        _C.rng_set_state(d, st)
 
 
 def set_cpu_fallback_enabled(on: bool) -> None:
