@@ -4,9 +4,10 @@
 // Layout classes (chosen on the host, per call):
 //   CONTIG  every tensor operand is dense in the iteration order (1 coalesced
 //           dim, stride 1) or a one-element broadcast (stride 0).  Each thread
-//           moves UNROLL (the op's kUnroll) 16-byte vectors per operand, all
-//           loads issued before any arithmetic; the tail (< VEC elements) goes
-//           to the last block.
+//           moves one 16-byte vector per operand, or, for ops with kUnroll 2
+//           on large tensors, two vectors kPairBytes apart with all loads
+//           issued before any arithmetic; the tail (< VEC elements) goes to
+//           the last block.
 //   VECND   N-d iteration whose innermost dim is a multiple of VEC and where
 //           every operand's innermost stride is 1 (vector load) or 0 (one
 //           element broadcast across the vector).  Coordinates of a vector's
@@ -53,8 +54,8 @@ constexpr int kMaxIn = SUPA_AMD_MAX_OPERANDS - 1;
 // `static constexpr int kUnroll;`, the 16-byte vectors per operand each thread
 // of the contiguous kernel handles.  One measured fastest for streaming ops on
 // MI355X (c1 add 80 % of HBM peak against 75 % at four); ops with long
-// arithmetic (gelu) set two so one vector's arithmetic overlaps the other's
-// loads.
+// arithmetic (gelu) set two, used on large tensors, so one vector's
+// arithmetic overlaps the other's loads.
 template <typename Op, typename = void> struct UnrollOf {
   static constexpr int value = 1;
 };
@@ -116,17 +117,32 @@ template <typename H, typename... R> struct NthT<0, H, R...> { using type = H; }
 template <int I, typename H, typename... R> struct NthT<I, H, R...> { using type = typename NthT<I - 1, R...>::type; };
 
 // ------------------------------------------------------------ CONTIG
-template <int VEC, int UNROLL, typename Op, typename C, typename CT, typename OT, typename... S>
+// Block mapping: blocks below `full_blocks` work in tiles of 2^tile_shift
+// blocks; a thread's UNROLL vectors sit kBlock << tile_shift vectors apart,
+// so a tile covers UNROLL * (kBlock << tile_shift) consecutive vectors.  The
+// remaining blocks (and every block when full_blocks = 0) take UNROLL
+// consecutive kBlock-vector slices.  ORDER 1 waits for each slice's loads
+// before the next slice's loads issue.
+template <int VEC, int UNROLL, int ORDER, typename Op, typename C, typename CT, typename OT, typename... S>
 __global__ void __launch_bounds__(kBlock)
-k_contig(Op op, TArgs<1 + sizeof...(S)> a, int64_t n) {
+k_contig(Op op, TArgs<1 + sizeof...(S)> a, int64_t n, uint32_t tile_shift, uint32_t full_blocks) {
   constexpr int N = sizeof...(S);
   const int64_t nvec = n / VEC;
-  const int64_t base = (int64_t)blockIdx.x * (UNROLL * kBlock) + threadIdx.x;
+  const uint32_t b = blockIdx.x;
+  int64_t base, step;
+  if (b < full_blocks) {
+    const uint32_t tile = b >> tile_shift, j = b & ((1u << tile_shift) - 1u);
+    step = (int64_t)kBlock << tile_shift;
+    base = (int64_t)tile * UNROLL * step + (int64_t)j * kBlock + threadIdx.x;
+  } else {
+    step = kBlock;
+    base = (int64_t)full_blocks * (UNROLL * kBlock) + (int64_t)(b - full_blocks) * (UNROLL * kBlock) + threadIdx.x;
+  }
   C x[UNROLL][VEC][N > 0 ? N : 1];
   // loads
 #pragma unroll
   for (int u = 0; u < UNROLL; ++u) {
-    const int64_t v = base + (int64_t)u * kBlock;
+    const int64_t v = base + (int64_t)u * step;
     if (v < nvec) {
       [&]<int... I>(std::integer_sequence<int, I...>) {
         (([&] {
@@ -145,12 +161,15 @@ k_contig(Op op, TArgs<1 + sizeof...(S)> a, int64_t n) {
          ...);
       }(std::make_integer_sequence<int, N>{});
     }
+    if constexpr (ORDER == 1 && UNROLL > 1) {
+      if (u + 1 < UNROLL) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
   }
   // compute + stores
   OT* out = static_cast<OT*>(a.p[0]);
 #pragma unroll
   for (int u = 0; u < UNROLL; ++u) {
-    const int64_t v = base + (int64_t)u * kBlock;
+    const int64_t v = base + (int64_t)u * step;
     if (v < nvec) {
       Vec<OT, VEC> w;
 #pragma unroll
@@ -159,7 +178,7 @@ k_contig(Op op, TArgs<1 + sizeof...(S)> a, int64_t n) {
     }
   }
   // tail
-  if (blockIdx.x == gridDim.x - 1) {
+  if (b == gridDim.x - 1) {
     const int64_t t = nvec * VEC + threadIdx.x;
     if (t < n) {
       C y[N > 0 ? N : 1];
@@ -174,6 +193,20 @@ k_contig(Op op, TArgs<1 + sizeof...(S)> a, int64_t n) {
       out[t] = from_arith<OT>(op(y));
     }
   }
+}
+
+// Grid of k_contig for n elements: {blocks, full_blocks}.
+struct ContigGrid {
+  uint32_t blocks, full_blocks;
+};
+inline ContigGrid contig_grid(int64_t n, int vec, int unroll, uint32_t tile_shift) {
+  const int64_t nvec = n / vec;
+  const int64_t per_tile = ((int64_t)unroll * kBlock) << tile_shift;
+  const int64_t full = tile_shift ? (nvec / per_tile) << tile_shift : 0;
+  const int64_t rest = nvec - full * unroll * kBlock;
+  const int64_t per_block = (int64_t)unroll * kBlock;
+  const int64_t blocks = std::max<int64_t>(1, full + (rest + per_block - 1) / per_block);
+  return {(uint32_t)blocks, (uint32_t)full};
 }
 
 // ------------------------------------------------------------- VECND
@@ -228,10 +261,12 @@ k_vecnd(Op op, TArgs<1 + sizeof...(S)> a, NdGeom g, uint32_t nvec) {
 // inputs that are each dense (strides 1, inner), a row broadcast down the
 // rows (1, 0), a column broadcast along a row (0, 1) or one element (0, 0):
 // the bias-add and per-row-scalar shapes.  A thread owns one VEC-wide column
-// slice in kRow2dRows consecutive rows, so a row-broadcast operand is loaded
-// once per thread and reused (measured 7 % faster than one row per thread);
-// every offset is 32-bit.  Workgroup b covers column block b % bpr of row
-// group b / bpr.
+// slice in kRow2dRows rows, K rows apart (K from row2d_pair: the rows sit
+// about kPairBytes of output apart), so a row-broadcast operand is loaded
+// once per thread and reused; every offset is 32-bit.  Workgroup b covers
+// column block b % bpr of row group g = b / bpr, whose rows are
+// (g / K) 2K + g % K + {0, K}.  Dense rows are loaded raw and converted
+// after every load has issued.
 // With three iteration dims (inner, d1, d2) the rows are the flattened
 // (d1, d2) pairs, and R2_MID is an operand indexed by the middle coordinate
 // alone (strides (0, 1, 0)): a per-channel vector over an NCHW-like layout,
@@ -239,23 +274,75 @@ k_vecnd(Op op, TArgs<1 + sizeof...(S)> a, NdGeom g, uint32_t nvec) {
 enum Row2dKind { R2_DENSE = 0, R2_ROW = 1, R2_COL = 2, R2_ONE = 3, R2_MID = 4 };
 constexpr int kRow2dRows = 2;
 
-template <int VEC, typename Op, typename C, typename CT, typename OT, typename... S>
+// A thread's two vectors of one operand sit kPairBytes of output apart: on
+// MI355X a streaming kernel whose concurrent accesses pair up 32 KiB apart
+// moved 80-83 % of peak HBM bandwidth against 74-78 % with the pairs at
+// 4-16 KiB (c2's gelu(tanh), bf16 + f32 bias adds with per-column,
+// per-row and per-channel bias).
+constexpr uint32_t kPairBytes = 32768;
+// Contiguous launches of UNROLL-2 ops pair vectors from this many vectors up.
+constexpr int64_t kPairMinVecs = int64_t(1) << 23;
+
+// Distance, in rows, between a thread's two rows for an output row of
+// `row_bytes`: the power of two nearest kPairBytes / row_bytes from below,
+// at least 1, and small enough that a tile (2 K rows) fits in `rows`.
+inline uint32_t row2d_pair(uint32_t row_bytes, uint32_t rows) {
+  uint32_t K = 1;
+  while ((uint64_t)2 * K * row_bytes <= kPairBytes && 4 * K <= rows) K *= 2;
+  return K;
+}
+
+template <int VEC, int ORDER, typename Op, typename C, typename CT, typename OT, typename... S>
 __global__ void __launch_bounds__(kBlock)
-k_row2d(Op op, TArgs<1 + sizeof...(S)> a, uint32_t inner, uint32_t rows, FastDiv bpr, FastDiv mid) {
+k_row2d(Op op, TArgs<1 + sizeof...(S)> a, uint32_t inner, uint32_t rows, FastDiv bpr, FastDiv mid, FastDiv pair) {
   constexpr int N = sizeof...(S);
   constexpr int R = kRow2dRows;
-  uint32_t rg, cb;
+  using Raw = Vec<uint32_t, 4>;  // one operand's VEC elements as loaded (at most 16 bytes)
+  uint32_t rg, cb, tile, j;
   bpr.divmod(blockIdx.x, rg, cb);
+  pair.divmod(rg, tile, j);
+  const uint32_t K = pair.d;
+  const uint32_t r0 = tile * (R * K) + j;  // this thread's rows: r0 + r K
   const uint32_t col = (cb * kBlock + threadIdx.x) * VEC;
-  if (col >= inner) return;
-  const uint32_t r0 = rg * R;
+  if (col >= inner || r0 >= rows) return;
+  Raw raw[R][N > 0 ? N : 1];
+  // dense rows: raw loads only, converted once every load has issued
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const uint32_t row = r0 + r * K;
+    if (row < rows) {
+      [&]<int... I>(std::integer_sequence<int, I...>) {
+        (([&] {
+           using St = typename NthT<I, S...>::type;
+           static_assert(sizeof(Vec<St, VEC>) <= sizeof(Raw), "vector wider than 16 bytes");
+           if (a.mode[1 + I] == R2_DENSE) {
+             const St* p = static_cast<const St*>(a.p[1 + I]);
+             const Vec<St, VEC> w = ld_stream(reinterpret_cast<const Vec<St, VEC>*>(p + row * inner + col));
+             __builtin_memcpy(&raw[r][I], &w, sizeof(w));
+           }
+         }()),
+         ...);
+    }(std::make_integer_sequence<int, N>{});
+    }
+    if constexpr (ORDER == 1) {
+      if (r + 1 < R) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+  }
   C x[R][VEC][N > 0 ? N : 1];
   [&]<int... I>(std::integer_sequence<int, I...>) {
     (([&] {
        using St = typename NthT<I, S...>::type;
        const St* p = static_cast<const St*>(a.p[1 + I]);
        const int kind = a.mode[1 + I];
-       if (kind == R2_ROW) {
+       if (kind == R2_DENSE) {
+#pragma unroll
+         for (int r = 0; r < R; ++r) {
+           Vec<St, VEC> w;
+           __builtin_memcpy(&w, &raw[r][I], sizeof(w));
+#pragma unroll
+           for (int k = 0; k < VEC; ++k) x[r][k][I] = load_cvt<C, CT>(w.v[k]);
+         }
+       } else if (kind == R2_ROW) {
          const Vec<St, VEC> w = *reinterpret_cast<const Vec<St, VEC>*>(p + col);
 #pragma unroll
          for (int r = 0; r < R; ++r)
@@ -264,25 +351,17 @@ k_row2d(Op op, TArgs<1 + sizeof...(S)> a, uint32_t inner, uint32_t rows, FastDiv
        } else {
 #pragma unroll
          for (int r = 0; r < R; ++r) {
-           const uint32_t row = r0 + r;
-           if (row < rows) {
-             if (kind == R2_DENSE) {
-               const Vec<St, VEC> w = ld_stream(reinterpret_cast<const Vec<St, VEC>*>(p + row * inner + col));
-#pragma unroll
-               for (int k = 0; k < VEC; ++k) x[r][k][I] = load_cvt<C, CT>(w.v[k]);
-             } else {
-               uint32_t idx = 0u;
-               if (kind == R2_COL) {
-                 idx = row;
-               } else if (kind == R2_MID) {
-                 uint32_t q;
-                 mid.divmod(row, q, idx);
-               }
-               const C s = load_cvt<C, CT>(p[idx]);
-#pragma unroll
-               for (int k = 0; k < VEC; ++k) x[r][k][I] = s;
-             }
+           const uint32_t row = r0 + r * K < rows ? r0 + r * K : r0;
+           uint32_t idx = 0u;
+           if (kind == R2_COL) {
+             idx = row;
+           } else if (kind == R2_MID) {
+             uint32_t q;
+             mid.divmod(row, q, idx);
            }
+           const C v = load_cvt<C, CT>(p[idx]);
+#pragma unroll
+           for (int k = 0; k < VEC; ++k) x[r][k][I] = v;
          }
        }
      }()),
@@ -290,7 +369,7 @@ k_row2d(Op op, TArgs<1 + sizeof...(S)> a, uint32_t inner, uint32_t rows, FastDiv
   }(std::make_integer_sequence<int, N>{});
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const uint32_t row = r0 + r;
+    const uint32_t row = r0 + r * K;
     if (row < rows) {
       Vec<OT, VEC> w;
 #pragma unroll
