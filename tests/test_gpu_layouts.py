@@ -1,11 +1,10 @@
-"""Block mappings of the streaming kernels: the contiguous kernel's paired
-mapping (two vectors per thread 32 KiB apart, used for the gelu family on
-tensors of 2^23 vectors and up, with a remainder that does not fill a tile)
-against the one-vector mapping it replaces on smaller tensors, and the
+"""Block mappings of the streaming kernels: the contiguous kernel (one
+wavefront per workgroup, one vector per thread, an element tail in the last
+workgroup) on a whole tensor against the same op over slices of it, and the
 row-broadcast kernel's row pairing (a thread's two rows K apart) over row
 counts that leave a tile part-filled.  Each result is compared bit for bit
-with the same op computed by another mapping or by the upstream CPU kernels,
-and a slice with the oracle."""
+with the same op computed over other launch shapes or by the upstream CPU
+kernels, and a slice with the oracle."""
 import numpy as np
 import pytest
 import torch
@@ -15,11 +14,8 @@ import oracle as O
 
 pytestmark = pytest.mark.gpu
 
-PAIR_MIN_VECS = 1 << 23
-
-
 def chunked(fn, xs, pieces=8):
-    """fn over `pieces` slices (each below the pairing threshold), rejoined."""
+    """fn over `pieces` slices (other grids, other tails), rejoined."""
     n = xs[0].numel()
     step = ((n // pieces) // 64) * 64  # 64-element steps keep every slice 16-byte aligned
     outs, s = [], 0
@@ -32,8 +28,8 @@ def chunked(fn, xs, pieces=8):
 
 @pytest.mark.parametrize("dtype,vec", [(torch.float32, 4), (torch.bfloat16, 8)])
 @pytest.mark.parametrize("approx", ["none", "tanh"])
-def test_paired_contiguous_gelu(approx, dtype, vec, no_fallback):
-    n = PAIR_MIN_VECS * vec + 1000 * vec + 3  # above the threshold; part tile and element tail
+def test_contiguous_gelu_whole_and_sliced(approx, dtype, vec, no_fallback):
+    n = (1 << 22) * vec + 1000 * vec + 3  # a partial last workgroup and an element tail
     g = torch.Generator().manual_seed(60)
     x = (torch.randn(n, generator=g) * 3).to(dtype).to("supa")
     gy = torch.randn(n, generator=g).to(dtype).to("supa")

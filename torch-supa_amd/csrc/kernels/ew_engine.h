@@ -4,10 +4,8 @@
 // Layout classes (chosen on the host, per call):
 //   CONTIG  every tensor operand is dense in the iteration order (1 coalesced
 //           dim, stride 1) or a one-element broadcast (stride 0).  Each thread
-//           moves one 16-byte vector per operand, or, for ops with kUnroll 2
-//           on large tensors, two vectors kPairBytes apart with all loads
-//           issued before any arithmetic; the tail (< VEC elements) goes to
-//           the last block.
+//           moves one 16-byte vector per operand, in one-wavefront
+//           workgroups; the tail (< VEC elements) goes to the last one.
 //   VECND   N-d iteration whose innermost dim is a multiple of VEC and where
 //           every operand's innermost stride is 1 (vector load) or 0 (one
 //           element broadcast across the vector).  Coordinates of a vector's
@@ -46,22 +44,15 @@
 namespace sa {
 
 constexpr int kBlock = 256;
+// Workgroup of the contiguous kernel: one wavefront.  On MI355X a 1R1W /
+// 2R1W stream with 64-thread workgroups moved 77-83 % of peak HBM bandwidth
+// against 73-81 % with 256 (16M to 128M float32 elements).
+constexpr int kContigBlock = 64;
 constexpr int kMaxIn = SUPA_AMD_MAX_OPERANDS - 1;
 
 // --------------------------------------------------------------- binding
 // Op functors: `static constexpr int arity;` and
-// `template <class C> __device__ C operator()(const C* x) const`; optionally
-// `static constexpr int kUnroll;`, the 16-byte vectors per operand each thread
-// of the contiguous kernel handles.  One measured fastest for streaming ops on
-// MI355X (c1 add 80 % of HBM peak against 75 % at four); ops with long
-// arithmetic (gelu) set two, used on large tensors, so one vector's
-// arithmetic overlaps the other's loads.
-template <typename Op, typename = void> struct UnrollOf {
-  static constexpr int value = 1;
-};
-template <typename Op> struct UnrollOf<Op, std::void_t<decltype(Op::kUnroll)>> {
-  static constexpr int value = Op::kUnroll;
-};
+// `template <class C> __device__ C operator()(const C* x) const`.
 
 // Storage pattern an op has static kernels for beyond "every operand in the
 // common dtype": 1 = bool output from common-dtype inputs (comparisons,
@@ -77,7 +68,6 @@ template <typename Op> struct DtypeModeOf<Op, std::void_t<decltype(Op::kDtypeMod
 template <typename Op, typename C>
 struct Bind1 {  // binds input position K to value v
   static constexpr int arity = Op::arity - 1;
-  static constexpr int kUnroll = UnrollOf<Op>::value;
   static constexpr int kDtypeMode = DtypeModeOf<Op>::value;
   Op op;
   int k;
@@ -117,68 +107,40 @@ template <typename H, typename... R> struct NthT<0, H, R...> { using type = H; }
 template <int I, typename H, typename... R> struct NthT<I, H, R...> { using type = typename NthT<I - 1, R...>::type; };
 
 // ------------------------------------------------------------ CONTIG
-// Block mapping: blocks below `full_blocks` work in tiles of 2^tile_shift
-// blocks; a thread's UNROLL vectors sit kBlock << tile_shift vectors apart,
-// so a tile covers UNROLL * (kBlock << tile_shift) consecutive vectors.  The
-// remaining blocks (and every block when full_blocks = 0) take UNROLL
-// consecutive kBlock-vector slices.  ORDER 1 waits for each slice's loads
-// before the next slice's loads issue.
-template <int VEC, int UNROLL, int ORDER, typename Op, typename C, typename CT, typename OT, typename... S>
-__global__ void __launch_bounds__(kBlock)
-k_contig(Op op, TArgs<1 + sizeof...(S)> a, int64_t n, uint32_t tile_shift, uint32_t full_blocks) {
+// One kContigBlock-thread workgroup per kContigBlock vectors; thread t of
+// workgroup b moves vector b * kContigBlock + t of every operand.
+template <int VEC, typename Op, typename C, typename CT, typename OT, typename... S>
+__global__ void __launch_bounds__(kContigBlock)
+k_contig(Op op, TArgs<1 + sizeof...(S)> a, int64_t n) {
   constexpr int N = sizeof...(S);
   const int64_t nvec = n / VEC;
-  const uint32_t b = blockIdx.x;
-  int64_t base, step;
-  if (b < full_blocks) {
-    const uint32_t tile = b >> tile_shift, j = b & ((1u << tile_shift) - 1u);
-    step = (int64_t)kBlock << tile_shift;
-    base = (int64_t)tile * UNROLL * step + (int64_t)j * kBlock + threadIdx.x;
-  } else {
-    step = kBlock;
-    base = (int64_t)full_blocks * (UNROLL * kBlock) + (int64_t)(b - full_blocks) * (UNROLL * kBlock) + threadIdx.x;
-  }
-  C x[UNROLL][VEC][N > 0 ? N : 1];
-  // loads
-#pragma unroll
-  for (int u = 0; u < UNROLL; ++u) {
-    const int64_t v = base + (int64_t)u * step;
-    if (v < nvec) {
-      [&]<int... I>(std::integer_sequence<int, I...>) {
-        (([&] {
-           using St = typename NthT<I, S...>::type;
-           const St* p = static_cast<const St*>(a.p[1 + I]);
-           if (a.mode[1 + I]) {
-             const C s = load_cvt<C, CT>(p[0]);
-#pragma unroll
-             for (int k = 0; k < VEC; ++k) x[u][k][I] = s;
-           } else {
-             const Vec<St, VEC> w = ld_stream(reinterpret_cast<const Vec<St, VEC>*>(p + v * VEC));
-#pragma unroll
-             for (int k = 0; k < VEC; ++k) x[u][k][I] = load_cvt<C, CT>(w.v[k]);
-           }
-         }()),
-         ...);
-      }(std::make_integer_sequence<int, N>{});
-    }
-    if constexpr (ORDER == 1 && UNROLL > 1) {
-      if (u + 1 < UNROLL) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    }
-  }
-  // compute + stores
+  const int64_t v = (int64_t)blockIdx.x * kContigBlock + threadIdx.x;
   OT* out = static_cast<OT*>(a.p[0]);
+  if (v < nvec) {
+    C x[VEC][N > 0 ? N : 1];
+    [&]<int... I>(std::integer_sequence<int, I...>) {
+      (([&] {
+         using St = typename NthT<I, S...>::type;
+         const St* p = static_cast<const St*>(a.p[1 + I]);
+         if (a.mode[1 + I]) {
+           const C s = load_cvt<C, CT>(p[0]);
 #pragma unroll
-  for (int u = 0; u < UNROLL; ++u) {
-    const int64_t v = base + (int64_t)u * step;
-    if (v < nvec) {
-      Vec<OT, VEC> w;
+           for (int k = 0; k < VEC; ++k) x[k][I] = s;
+         } else {
+           const Vec<St, VEC> w = ld_stream(reinterpret_cast<const Vec<St, VEC>*>(p + v * VEC));
 #pragma unroll
-      for (int k = 0; k < VEC; ++k) w.v[k] = from_arith<OT>(op(x[u][k]));
-      st_stream(reinterpret_cast<Vec<OT, VEC>*>(out + v * VEC), w);
-    }
+           for (int k = 0; k < VEC; ++k) x[k][I] = load_cvt<C, CT>(w.v[k]);
+         }
+       }()),
+       ...);
+    }(std::make_integer_sequence<int, N>{});
+    Vec<OT, VEC> w;
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) w.v[k] = from_arith<OT>(op(x[k]));
+    st_stream(reinterpret_cast<Vec<OT, VEC>*>(out + v * VEC), w);
   }
-  // tail
-  if (b == gridDim.x - 1) {
+  // tail (fewer than VEC elements): the last workgroup
+  if (blockIdx.x == gridDim.x - 1) {
     const int64_t t = nvec * VEC + threadIdx.x;
     if (t < n) {
       C y[N > 0 ? N : 1];
@@ -193,20 +155,6 @@ k_contig(Op op, TArgs<1 + sizeof...(S)> a, int64_t n, uint32_t tile_shift, uint3
       out[t] = from_arith<OT>(op(y));
     }
   }
-}
-
-// Grid of k_contig for n elements: {blocks, full_blocks}.
-struct ContigGrid {
-  uint32_t blocks, full_blocks;
-};
-inline ContigGrid contig_grid(int64_t n, int vec, int unroll, uint32_t tile_shift) {
-  const int64_t nvec = n / vec;
-  const int64_t per_tile = ((int64_t)unroll * kBlock) << tile_shift;
-  const int64_t full = tile_shift ? (nvec / per_tile) << tile_shift : 0;
-  const int64_t rest = nvec - full * unroll * kBlock;
-  const int64_t per_block = (int64_t)unroll * kBlock;
-  const int64_t blocks = std::max<int64_t>(1, full + (rest + per_block - 1) / per_block);
-  return {(uint32_t)blocks, (uint32_t)full};
 }
 
 // ------------------------------------------------------------- VECND
@@ -274,14 +222,11 @@ k_vecnd(Op op, TArgs<1 + sizeof...(S)> a, NdGeom g, uint32_t nvec) {
 enum Row2dKind { R2_DENSE = 0, R2_ROW = 1, R2_COL = 2, R2_ONE = 3, R2_MID = 4 };
 constexpr int kRow2dRows = 2;
 
-// A thread's two vectors of one operand sit kPairBytes of output apart: on
-// MI355X a streaming kernel whose concurrent accesses pair up 32 KiB apart
-// moved 80-83 % of peak HBM bandwidth against 74-78 % with the pairs at
-// 4-16 KiB (c2's gelu(tanh), bf16 + f32 bias adds with per-column,
-// per-row and per-channel bias).
+// A thread's two rows sit about kPairBytes of output apart: on MI355X the
+// bf16 + f32 bias adds (per-column, per-row and per-channel bias) moved
+// 80-83 % of peak HBM bandwidth with the rows 32 KiB apart against 76-78 %
+// with adjacent rows (8-16 KiB).
 constexpr uint32_t kPairBytes = 32768;
-// Contiguous launches of UNROLL-2 ops pair vectors from this many vectors up.
-constexpr int64_t kPairMinVecs = int64_t(1) << 23;
 
 // Distance, in rows, between a thread's two rows for an output row of
 // `row_bytes`: the power of two nearest kPairBytes / row_bytes from below,
@@ -292,7 +237,7 @@ inline uint32_t row2d_pair(uint32_t row_bytes, uint32_t rows) {
   return K;
 }
 
-template <int VEC, int ORDER, typename Op, typename C, typename CT, typename OT, typename... S>
+template <int VEC, typename Op, typename C, typename CT, typename OT, typename... S>
 __global__ void __launch_bounds__(kBlock)
 k_row2d(Op op, TArgs<1 + sizeof...(S)> a, uint32_t inner, uint32_t rows, FastDiv bpr, FastDiv mid, FastDiv pair) {
   constexpr int N = sizeof...(S);
@@ -323,9 +268,6 @@ k_row2d(Op op, TArgs<1 + sizeof...(S)> a, uint32_t inner, uint32_t rows, FastDiv
          }()),
          ...);
     }(std::make_integer_sequence<int, N>{});
-    }
-    if constexpr (ORDER == 1) {
-      if (r + 1 < R) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
   }
   C x[R][VEC][N > 0 ? N : 1];

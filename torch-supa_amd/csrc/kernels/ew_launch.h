@@ -164,24 +164,9 @@ int launch_static(const Op& op, const supa_amd_ew_desc& d, const int* tin, hipSt
     bool al = true;
     for (int k = 0; k <= N; ++k)
       if (!(k > 0 && a.mode[k]) && !aligned(a.p[k], VEC * sizes_of[k])) al = false;
-    if (al) {
-      // Ops with long arithmetic (UNROLL 2) move two vectors per thread,
-      // kPairBytes apart, on large tensors; below kPairMinVecs one vector
-      // per thread balances the short grid better (c1: gelu 70.6 % of peak
-      // at one against 67 % at two).
-      constexpr int UNROLL = UnrollOf<Op>::value;
-      if constexpr (UNROLL == 2) {
-        if (n / VEC >= kPairMinVecs) {
-          uint32_t shift = 0;
-          while (((uint64_t)kBlock * VEC * sizeof(OT) << (shift + 1)) <= kPairBytes) ++shift;
-          const ContigGrid g = contig_grid(n, VEC, 2, shift);
-          k_contig<VEC, 2, 0, Op, C, CT, OT, S...><<<dim3(g.blocks), dim3(kBlock), 0, st>>>(op, a, n, shift,
-                                                                                           g.full_blocks);
-          return launch_status();
-        }
-      }
-      const ContigGrid g = contig_grid(n, VEC, 1, 0);
-      k_contig<VEC, 1, 0, Op, C, CT, OT, S...><<<dim3(g.blocks), dim3(kBlock), 0, st>>>(op, a, n, 0, 0);
+    if (al && n / VEC < (int64_t(1) << 31)) {  // grid of at most 2^31 threads
+      const int64_t blocks = std::max<int64_t>(1, (n / VEC + kContigBlock - 1) / kContigBlock);
+      k_contig<VEC, Op, C, CT, OT, S...><<<dim3((unsigned)blocks), dim3(kContigBlock), 0, st>>>(op, a, n);
       return launch_status();
     }
   }
@@ -256,7 +241,7 @@ int launch_static(const Op& op, const supa_amd_ew_desc& d, const int* tin, hipSt
         const uint32_t K = row2d_pair(inner * (uint32_t)sizeof(OT), rows);
         const uint64_t blocks = (uint64_t)bpr * K * ((rows + kRow2dRows * K - 1) / (kRow2dRows * K));
         if (blocks < (1ull << 31)) {
-          k_row2d<VEC, 0, Op, C, CT, OT, S...><<<(unsigned)blocks, kBlock, 0, st>>>(
+          k_row2d<VEC, Op, C, CT, OT, S...><<<(unsigned)blocks, kBlock, 0, st>>>(
               op, c, inner, rows, FastDiv(bpr), FastDiv((uint32_t)d1), FastDiv(K));
           return launch_status();
         }

@@ -186,6 +186,9 @@ int fe_dispatch(int op, int form, const FeArgs& a, hipStream_t st) {
 
 // ------------------------------------------------------------- norm
 constexpr int kOrdInf = 0;
+// The norm kernels keep four wavefronts per workgroup: stage 2 walks every
+// chunk partial of a tensor with one workgroup.
+constexpr int kNormBlock = 256;
 
 template <int ORD, typename A> __device__ __forceinline__ A norm_term(A x) {
   if constexpr (ORD == 2) return x * x;
@@ -198,20 +201,20 @@ template <int ORD, typename A> __device__ __forceinline__ A norm_combine(A a, A 
 }
 // Reduce over the workgroup; the result is valid in thread 0.
 template <int ORD, typename A> __device__ __forceinline__ A norm_block(A v) {
-  __shared__ A part[kMtaBlock / 64];
+  __shared__ A part[kNormBlock / 64];
   for (int off = 32; off > 0; off >>= 1) v = norm_combine<ORD>(v, __shfl_xor(v, off, 64));
   if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = v;
   __syncthreads();
   if (threadIdx.x == 0) {
 #pragma unroll
-    for (int w = 1; w < kMtaBlock / 64; ++w) v = norm_combine<ORD>(v, part[w]);
+    for (int w = 1; w < kNormBlock / 64; ++w) v = norm_combine<ORD>(v, part[w]);
   }
   return v;
 }
 
 // Stage 1: ws[table base + block] = the combine of |x|^ord over one chunk.
 template <typename T, int ORD, int64_t CHUNK>
-__global__ void __launch_bounds__(kMtaBlock)
+__global__ void __launch_bounds__(kNormBlock)
 k_norm_partial(MtaTable tab, opmath_t<T>* __restrict__ ws) {
   using A = opmath_t<T>;
   constexpr int V = 16 / sizeof(T);
@@ -221,14 +224,14 @@ k_norm_partial(MtaTable tab, opmath_t<T>* __restrict__ ws) {
   int64_t start = r.lo;
   if (aligned(x, 16)) {
     const int64_t nv = (r.hi - r.lo) / V;
-    for (int64_t v = threadIdx.x; v < nv; v += kMtaBlock) {
+    for (int64_t v = threadIdx.x; v < nv; v += kNormBlock) {
       const Vec<T, V> w = ld_stream(reinterpret_cast<const Vec<T, V>*>(x + r.lo + v * V));
 #pragma unroll
       for (int i = 0; i < V; ++i) acc = norm_combine<ORD>(acc, norm_term<ORD>((A)to_arith(w.v[i])));
     }
     start = r.lo + nv * V;
   }
-  for (int64_t e = start + threadIdx.x; e < r.hi; e += kMtaBlock)
+  for (int64_t e = start + threadIdx.x; e < r.hi; e += kNormBlock)
     acc = norm_combine<ORD>(acc, norm_term<ORD>((A)to_arith(x[e])));
   acc = norm_block<ORD>(acc);
   if (threadIdx.x == 0) ws[blockIdx.x] = acc;
@@ -237,11 +240,11 @@ k_norm_partial(MtaTable tab, opmath_t<T>* __restrict__ ws) {
 // Stage 2: one workgroup per tensor combines its chunks' partials (none for
 // an empty tensor: norm 0) and writes the norm.
 template <typename A, typename OT, int ORD>
-__global__ void __launch_bounds__(kMtaBlock)
+__global__ void __launch_bounds__(kNormBlock)
 k_norm_final(MtaTable tab, const A* __restrict__ ws) {
   const int k = blockIdx.x;
   A acc = A(0);
-  for (uint32_t c = tab.chunk_start[k] + threadIdx.x; c < tab.chunk_start[k + 1]; c += kMtaBlock)
+  for (uint32_t c = tab.chunk_start[k] + threadIdx.x; c < tab.chunk_start[k + 1]; c += kNormBlock)
     acc = norm_combine<ORD>(acc, ws[c]);
   acc = norm_block<ORD>(acc);
   if (threadIdx.x == 0) *static_cast<OT*>(tab.out[k]) = from_arith<OT>(ORD == 2 ? sqrt(acc) : acc);
@@ -277,7 +280,7 @@ int norm_tables(int32_t n, const int64_t* numel, F&& per_table) {
   return SUPA_AMD_OK;
 }
 
-template <typename T> constexpr int64_t norm_chunk() { return 2 * chunk_one<T>(); }
+template <typename T> constexpr int64_t norm_chunk() { return 2 * kNormBlock * (16 / (int64_t)sizeof(T)); }
 
 template <typename T>
 int64_t norm_ws_bytes(int32_t n, const int64_t* numel) {
@@ -302,11 +305,11 @@ int norm_launch(int32_t n, const void* const* x, const int64_t* numel, void* out
     }
     if (chunks > 0) {
       // the partial kernel only sees non-empty tensors' blocks
-      k_norm_partial<T, ORD, CHUNK><<<chunks, kMtaBlock, 0, st>>>(tab, base);
+      k_norm_partial<T, ORD, CHUNK><<<chunks, kNormBlock, 0, st>>>(tab, base);
       const int rc = launch_status();
       if (rc) return rc;
     }
-    k_norm_final<A, OT, ORD><<<tab.ntensors, kMtaBlock, 0, st>>>(tab, base);
+    k_norm_final<A, OT, ORD><<<tab.ntensors, kNormBlock, 0, st>>>(tab, base);
     base += chunks;
     return launch_status();
   });

@@ -149,7 +149,6 @@ enum UnaryKind {
 
 template <int K, typename C> struct UnaryOp {
   static constexpr int arity = 1;
-  static constexpr int kUnroll = (K == U_GELU || K == U_GELU_TANH) ? 2 : 1;
   __device__ __forceinline__ C operator()(const C* v) const {
     const C x = v[0];
     if constexpr (K == U_GELU) return gelu_none<C>(x);
@@ -191,7 +190,6 @@ template <int K, typename C> struct UnaryOp {
 // output (sigmoid, tanh); upstream aten activation backward formulas.
 template <int K, typename C> struct UnaryBwdOp {
   static constexpr int arity = 2;
-  static constexpr int kUnroll = (K == U_GELU || K == U_GELU_TANH) ? 2 : 1;
   __device__ __forceinline__ C operator()(const C* v) const {
     const C dy = v[0], x = v[1];
     if constexpr (K == U_GELU) {
