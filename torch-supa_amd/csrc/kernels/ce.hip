@@ -145,9 +145,23 @@ k_ce_final(const float* __restrict__ loss_rows, const int64_t* __restrict__ targ
   __shared__ float lds_v[NW];
   __shared__ float lds_c[NW];
   float v = 0.0f, k = 0.0f;
-  for (int64_t i = threadIdx.x; i < n; i += kCeBlock) {
-    v += loss_rows[i];
-    k += ce_kept(target[i], c, ignore_index) ? 1.0f : 0.0f;
+  constexpr int U = 8;  // loads in flight per step; the sums keep the row order
+  for (int64_t i0 = threadIdx.x; i0 < n; i0 += (int64_t)U * kCeBlock) {
+    float lv[U];
+    int64_t tg[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t i = i0 + (int64_t)u * kCeBlock;
+      lv[u] = i < n ? loss_rows[i] : 0.0f;
+      tg[u] = i < n ? target[i] : ignore_index;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (i0 + (int64_t)u * kCeBlock < n) {
+        v += lv[u];
+        k += ce_kept(tg[u], c, ignore_index) ? 1.0f : 0.0f;
+      }
+    }
   }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) {

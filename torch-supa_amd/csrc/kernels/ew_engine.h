@@ -44,10 +44,11 @@
 namespace sa {
 
 constexpr int kBlock = 256;
-// Workgroup of the contiguous kernel: one wavefront.  On MI355X a 1R1W /
-// 2R1W stream with 64-thread workgroups moved 77-83 % of peak HBM bandwidth
-// against 73-81 % with 256 (16M to 128M float32 elements).
-constexpr int kContigBlock = 64;
+// Workgroup of the streaming kernels (CONTIG, ROW2D, VECND, STRIDED): one
+// wavefront.  On MI355X a 1R1W / 2R1W stream with 64-thread workgroups moved
+// 77-83 % of peak HBM bandwidth against 73-81 % with 256 (16M to 128M
+// float32 elements), and c2's bias adds 82-84 % against 80-82 %.
+constexpr int kStreamBlock = 64;
 constexpr int kMaxIn = SUPA_AMD_MAX_OPERANDS - 1;
 
 // --------------------------------------------------------------- binding
@@ -106,15 +107,37 @@ template <int I, typename... S> struct NthT;
 template <typename H, typename... R> struct NthT<0, H, R...> { using type = H; };
 template <int I, typename H, typename... R> struct NthT<I, H, R...> { using type = typename NthT<I - 1, R...>::type; };
 
+// ------------------------------------------------------------ folds
+// acc = comb(acc, load(i)) for i = first, first + stride, ... (< n), in that
+// order, with U loads in flight per step.  A loop that loads and combines one
+// element per iteration waits out one memory latency per element; this one
+// waits once per U elements and combines in the same order, so the result is
+// the same.
+template <int U, typename A, typename Load, typename Comb>
+__device__ __forceinline__ A fold_strided(A acc, int64_t first, int64_t stride, int64_t n, Load&& load, Comb&& comb) {
+  for (int64_t i0 = first; i0 < n; i0 += (int64_t)U * stride) {
+    A x[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t i = i0 + (int64_t)u * stride;
+      x[u] = i < n ? load(i) : A(0);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (i0 + (int64_t)u * stride < n) acc = comb(acc, x[u]);
+  }
+  return acc;
+}
+
 // ------------------------------------------------------------ CONTIG
-// One kContigBlock-thread workgroup per kContigBlock vectors; thread t of
-// workgroup b moves vector b * kContigBlock + t of every operand.
+// One kStreamBlock-thread workgroup per kStreamBlock vectors; thread t of
+// workgroup b moves vector b * kStreamBlock + t of every operand.
 template <int VEC, typename Op, typename C, typename CT, typename OT, typename... S>
-__global__ void __launch_bounds__(kContigBlock)
+__global__ void __launch_bounds__(kStreamBlock)
 k_contig(Op op, TArgs<1 + sizeof...(S)> a, int64_t n) {
   constexpr int N = sizeof...(S);
   const int64_t nvec = n / VEC;
-  const int64_t v = (int64_t)blockIdx.x * kContigBlock + threadIdx.x;
+  const int64_t v = (int64_t)blockIdx.x * kStreamBlock + threadIdx.x;
   OT* out = static_cast<OT*>(a.p[0]);
   if (v < nvec) {
     C x[VEC][N > 0 ? N : 1];
@@ -162,10 +185,10 @@ k_contig(Op op, TArgs<1 + sizeof...(S)> a, int64_t n) {
 // operand's largest offset fits (one 32-bit multiply per dim and operand
 // instead of a 64-bit product), int64_t otherwise.
 template <int VEC, typename OFF, typename Op, typename C, typename CT, typename OT, typename... S>
-__global__ void __launch_bounds__(kBlock)
+__global__ void __launch_bounds__(kStreamBlock)
 k_vecnd(Op op, TArgs<1 + sizeof...(S)> a, NdGeom g, uint32_t nvec) {
   constexpr int N = sizeof...(S);
-  const uint32_t v = blockIdx.x * kBlock + threadIdx.x;
+  const uint32_t v = blockIdx.x * kStreamBlock + threadIdx.x;
   if (v >= nvec) return;
   // coordinates of the vector's first element
   uint32_t q, r;
@@ -237,8 +260,8 @@ inline uint32_t row2d_pair(uint32_t row_bytes, uint32_t rows) {
   return K;
 }
 
-template <int VEC, typename Op, typename C, typename CT, typename OT, typename... S>
-__global__ void __launch_bounds__(kBlock)
+template <int BS, int VEC, typename Op, typename C, typename CT, typename OT, typename... S>
+__global__ void __launch_bounds__(BS)
 k_row2d(Op op, TArgs<1 + sizeof...(S)> a, uint32_t inner, uint32_t rows, FastDiv bpr, FastDiv mid, FastDiv pair) {
   constexpr int N = sizeof...(S);
   constexpr int R = kRow2dRows;
@@ -248,7 +271,7 @@ k_row2d(Op op, TArgs<1 + sizeof...(S)> a, uint32_t inner, uint32_t rows, FastDiv
   pair.divmod(rg, tile, j);
   const uint32_t K = pair.d;
   const uint32_t r0 = tile * (R * K) + j;  // this thread's rows: r0 + r K
-  const uint32_t col = (cb * kBlock + threadIdx.x) * VEC;
+  const uint32_t col = (cb * BS + threadIdx.x) * VEC;
   if (col >= inner || r0 >= rows) return;
   Raw raw[R][N > 0 ? N : 1];
   // dense rows: raw loads only, converted once every load has issued
@@ -411,10 +434,10 @@ k_transpose_vec(Op op, const S* __restrict__ in, OT* __restrict__ out, Transpose
 
 // ----------------------------------------------------------- STRIDED
 template <typename OFF, typename Op, typename C, typename CT, typename OT, typename... S>
-__global__ void __launch_bounds__(kBlock)
+__global__ void __launch_bounds__(kStreamBlock)
 k_strided(Op op, TArgs<1 + sizeof...(S)> a, NdGeom g, uint32_t n) {
   constexpr int N = sizeof...(S);
-  const uint32_t i = blockIdx.x * kBlock + threadIdx.x;
+  const uint32_t i = blockIdx.x * kStreamBlock + threadIdx.x;
   if (i >= n) return;
   OFF off[1 + N];
 #pragma unroll

@@ -165,8 +165,8 @@ int launch_static(const Op& op, const supa_amd_ew_desc& d, const int* tin, hipSt
     for (int k = 0; k <= N; ++k)
       if (!(k > 0 && a.mode[k]) && !aligned(a.p[k], VEC * sizes_of[k])) al = false;
     if (al && n / VEC < (int64_t(1) << 31)) {  // grid of at most 2^31 threads
-      const int64_t blocks = std::max<int64_t>(1, (n / VEC + kContigBlock - 1) / kContigBlock);
-      k_contig<VEC, Op, C, CT, OT, S...><<<dim3((unsigned)blocks), dim3(kContigBlock), 0, st>>>(op, a, n);
+      const int64_t blocks = std::max<int64_t>(1, (n / VEC + kStreamBlock - 1) / kStreamBlock);
+      k_contig<VEC, Op, C, CT, OT, S...><<<dim3((unsigned)blocks), dim3(kStreamBlock), 0, st>>>(op, a, n);
       return launch_status();
     }
   }
@@ -237,11 +237,11 @@ int launch_static(const Op& op, const supa_amd_ew_desc& d, const int* tin, hipSt
       if (ok) {
         const uint32_t inner = (uint32_t)d0;
         const uint32_t rows = (uint32_t)(pn / d0);
-        const uint32_t bpr = (inner / VEC + kBlock - 1) / kBlock;
+        const uint32_t bpr = (inner / VEC + kStreamBlock - 1) / kStreamBlock;
         const uint32_t K = row2d_pair(inner * (uint32_t)sizeof(OT), rows);
         const uint64_t blocks = (uint64_t)bpr * K * ((rows + kRow2dRows * K - 1) / (kRow2dRows * K));
         if (blocks < (1ull << 31)) {
-          k_row2d<VEC, Op, C, CT, OT, S...><<<(unsigned)blocks, kBlock, 0, st>>>(
+          k_row2d<kStreamBlock, VEC, Op, C, CT, OT, S...><<<(unsigned)blocks, kStreamBlock, 0, st>>>(
               op, c, inner, rows, FastDiv(bpr), FastDiv((uint32_t)d1), FastDiv(K));
           return launch_status();
         }
@@ -274,14 +274,14 @@ int launch_static(const Op& op, const supa_amd_ew_desc& d, const int* tin, hipSt
           if (b.st[k][j] == 0 && p.sizes[j] > 1) b.mode[k] = 1;
       }
       const uint32_t nvec = (uint32_t)(pn / VEC);
-      const unsigned blocks = (nvec + kBlock - 1) / kBlock;
-      if (off32) k_vecnd<VEC, int32_t, Op, C, CT, OT, S...><<<blocks, kBlock, 0, st>>>(op, b, g, nvec);
-      else k_vecnd<VEC, int64_t, Op, C, CT, OT, S...><<<blocks, kBlock, 0, st>>>(op, b, g, nvec);
+      const unsigned blocks = (nvec + kStreamBlock - 1) / kStreamBlock;
+      if (off32) k_vecnd<VEC, int32_t, Op, C, CT, OT, S...><<<blocks, kStreamBlock, 0, st>>>(op, b, g, nvec);
+      else k_vecnd<VEC, int64_t, Op, C, CT, OT, S...><<<blocks, kStreamBlock, 0, st>>>(op, b, g, nvec);
       return launch_status();
     }
-    const unsigned blocks = (unsigned)((pn + kBlock - 1) / kBlock);
-    if (off32) k_strided<int32_t, Op, C, CT, OT, S...><<<blocks, kBlock, 0, st>>>(op, b, g, (uint32_t)pn);
-    else k_strided<int64_t, Op, C, CT, OT, S...><<<blocks, kBlock, 0, st>>>(op, b, g, (uint32_t)pn);
+    const unsigned blocks = (unsigned)((pn + kStreamBlock - 1) / kStreamBlock);
+    if (off32) k_strided<int32_t, Op, C, CT, OT, S...><<<blocks, kStreamBlock, 0, st>>>(op, b, g, (uint32_t)pn);
+    else k_strided<int64_t, Op, C, CT, OT, S...><<<blocks, kStreamBlock, 0, st>>>(op, b, g, (uint32_t)pn);
     return launch_status();
   });
 }

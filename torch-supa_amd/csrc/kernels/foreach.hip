@@ -243,9 +243,9 @@ template <typename A, typename OT, int ORD>
 __global__ void __launch_bounds__(kNormBlock)
 k_norm_final(MtaTable tab, const A* __restrict__ ws) {
   const int k = blockIdx.x;
-  A acc = A(0);
-  for (uint32_t c = tab.chunk_start[k] + threadIdx.x; c < tab.chunk_start[k + 1]; c += kNormBlock)
-    acc = norm_combine<ORD>(acc, ws[c]);
+  A acc = fold_strided<8>(
+      A(0), (int64_t)tab.chunk_start[k] + threadIdx.x, kNormBlock, (int64_t)tab.chunk_start[k + 1],
+      [&](int64_t c) { return ws[c]; }, [](A a, A b) { return norm_combine<ORD>(a, b); });
   acc = norm_block<ORD>(acc);
   if (threadIdx.x == 0) *static_cast<OT*>(tab.out[k]) = from_arith<OT>(ORD == 2 ? sqrt(acc) : acc);
 }

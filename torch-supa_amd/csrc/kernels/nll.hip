@@ -37,16 +37,33 @@ k_nll_fwd_reduce(const T* __restrict__ logp, const int64_t* __restrict__ target,
   __shared__ ACC lds_w[kNllBlock / 64];
   ACC v = ACC(0), w = ACC(0);
   bool bad = false;
-  for (int64_t i = threadIdx.x; i < n; i += kNllBlock) {
-    const int64_t t = target[i];
-    if (t == ignore_index) continue;
-    if (t < 0 || t >= c) {
-      bad = true;
-      continue;
+  constexpr int U = 8;  // rows in flight per step (targets, then their gathers); sums keep the row order
+  for (int64_t i0 = threadIdx.x; i0 < n; i0 += (int64_t)U * kNllBlock) {
+    int64_t tg[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t i = i0 + (int64_t)u * kNllBlock;
+      tg[u] = i < n ? target[i] : ignore_index;
     }
-    const ACC wt = weight ? (ACC)to_arith(weight[t]) : ACC(1);
-    v += -wt * (ACC)to_arith(logp[i * c + t]);
-    w += wt;
+    ACC lp[U], wt[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t i = i0 + (int64_t)u * kNllBlock, t = tg[u];
+      const bool use = i < n && t != ignore_index && t >= 0 && t < c;
+      lp[u] = use ? (ACC)to_arith(logp[i * c + t]) : ACC(0);
+      wt[u] = use ? (weight ? (ACC)to_arith(weight[t]) : ACC(1)) : ACC(0);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t t = tg[u];
+      if (i0 + (int64_t)u * kNllBlock >= n || t == ignore_index) continue;
+      if (t < 0 || t >= c) {
+        bad = true;
+        continue;
+      }
+      v += -wt[u] * lp[u];
+      w += wt[u];
+    }
   }
   if (bad && error_flag) *error_flag = 1;
 #pragma unroll
@@ -195,9 +212,20 @@ template <typename T, typename ACC>
 __global__ void __launch_bounds__(64)
 k_nll2d_fwd_final(const ACC* __restrict__ ws, int nparts, int mean, T* __restrict__ out, T* __restrict__ total_weight) {
   ACC v = ACC(0), w = ACC(0);
-  for (int k = threadIdx.x; k < nparts; k += 64) {
-    v += ws[2 * k];
-    w += ws[2 * k + 1];
+  constexpr int U = kNll2dParts / 64;  // every partial's load in flight at once
+  ACC pv[U], pw[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int k = threadIdx.x + 64 * u;
+    pv[u] = k < nparts ? ws[2 * k] : ACC(0);
+    pw[u] = k < nparts ? ws[2 * k + 1] : ACC(0);
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    if (threadIdx.x + 64 * u < nparts) {
+      v += pv[u];
+      w += pw[u];
+    }
   }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) {

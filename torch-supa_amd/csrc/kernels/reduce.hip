@@ -164,8 +164,9 @@ template <typename ACC, typename OT>
 __global__ void __launch_bounds__(kBlock)
 k_reduce_final(const ACC* __restrict__ partial, int nparts, ACC scale, OT* __restrict__ out) {
   __shared__ ACC lds[kBlock / 64];
-  ACC v = ACC(0);
-  for (int i = threadIdx.x; i < nparts; i += kBlock) v += partial[i];
+  ACC v = fold_strided<kRedBlocks / kBlock>(
+      ACC(0), threadIdx.x, kBlock, nparts, [&](int64_t i) { return partial[i]; },
+      [](ACC a, ACC b) { return a + b; });
   v = block_sum<ACC>(v, lds);
   if (threadIdx.x == 0) out[0] = from_arith<OT>(v * scale);
 }
@@ -332,8 +333,9 @@ __global__ void __launch_bounds__(kBlock)
 k_sum_rows(const T* __restrict__ in, OT* __restrict__ out, int64_t inner, ACC scale) {
   __shared__ ACC lds[kBlock / 64];
   const T* row = in + (int64_t)blockIdx.x * inner;
-  ACC acc = ACC(0);
-  for (int64_t i = threadIdx.x; i < inner; i += kBlock) acc += (ACC)to_arith(row[i]);
+  ACC acc = fold_strided<8>(
+      ACC(0), threadIdx.x, kBlock, inner, [&](int64_t i) { return (ACC)to_arith(row[i]); },
+      [](ACC a, ACC b) { return a + b; });
   acc = block_sum<ACC>(acc, lds);
   if (threadIdx.x == 0) out[blockIdx.x] = from_arith<OT>(acc * scale);
 }
