@@ -21,6 +21,9 @@
 namespace sa {
 
 constexpr int kCeBlock = 256;
+// The backward is a pure stream (one vector in, one out per thread): one
+// wavefront per workgroup, as the elementwise kernels.
+constexpr int kCeBwdBlock = 64;
 constexpr int kCeUnroll = 4;  // 16-byte vectors in flight per thread in the forward
 constexpr float kCeLog2e = 1.44269504088896340736f;
 
@@ -187,9 +190,9 @@ k_ce_final(const float* __restrict__ loss_rows, const int64_t* __restrict__ targ
 }
 
 // grad[i, :] over a 2-d grid: blockIdx.y = row in the slab, x = column blocks
-// of kCeBlock vectors.
+// of kCeBwdBlock vectors.
 template <typename T, bool VECOK>
-__global__ void __launch_bounds__(kCeBlock)
+__global__ void __launch_bounds__(kCeBwdBlock)
 k_ce_bwd(const T* __restrict__ grad_out, const T* __restrict__ x, const int64_t* __restrict__ target,
          const float* __restrict__ lse, const float* __restrict__ count, int64_t c, int64_t ignore_index,
          int reduction, T* __restrict__ gx) {
@@ -206,7 +209,7 @@ k_ce_bwd(const T* __restrict__ grad_out, const T* __restrict__ x, const int64_t*
   const float ll = kept ? lse[row] * kCeLog2e : 0.0f;
   const T* xr = x + row * c;
   T* dst = gx + row * c;
-  const int64_t col0 = ((int64_t)blockIdx.x * kCeBlock + threadIdx.x) * V;
+  const int64_t col0 = ((int64_t)blockIdx.x * kCeBwdBlock + threadIdx.x) * V;
   if (col0 >= c) return;
   if (VECOK && col0 + V <= c) {
     Vec<T, V> o;
@@ -303,16 +306,16 @@ int supa_amd_cross_entropy_backward(const void* grad_out, const void* logits, in
     const T* g = static_cast<const T*>(grad_out);
     const T* x = static_cast<const T*>(logits);
     T* gx = static_cast<T*>(grad_logits);
-    const unsigned gx_blocks = (unsigned)((c + (int64_t)kCeBlock * V - 1) / ((int64_t)kCeBlock * V));
+    const unsigned gx_blocks = (unsigned)((c + (int64_t)kCeBwdBlock * V - 1) / ((int64_t)kCeBwdBlock * V));
     for (int64_t r0 = 0; r0 < n; r0 += 65535) {
       const int64_t rows = std::min<int64_t>(65535, n - r0);
       const T* gs = reduction == SUPA_AMD_REDUCTION_NONE ? g + r0 : g;
       const dim3 grid(gx_blocks, (unsigned)rows);
       if (vecok)
-        k_ce_bwd<T, true><<<grid, kCeBlock, 0, st>>>(gs, x + r0 * c, target + r0, lse + r0, count, c, ignore_index,
+        k_ce_bwd<T, true><<<grid, kCeBwdBlock, 0, st>>>(gs, x + r0 * c, target + r0, lse + r0, count, c, ignore_index,
                                                      reduction, gx + r0 * c);
       else
-        k_ce_bwd<T, false><<<grid, kCeBlock, 0, st>>>(gs, x + r0 * c, target + r0, lse + r0, count, c, ignore_index,
+        k_ce_bwd<T, false><<<grid, kCeBwdBlock, 0, st>>>(gs, x + r0 * c, target + r0, lse + r0, count, c, ignore_index,
                                                       reduction, gx + r0 * c);
       const int rc = launch_status();
       if (rc) return rc;

@@ -130,14 +130,14 @@ __device__ __forceinline__ A fold_strided(A acc, int64_t first, int64_t stride, 
 }
 
 // ------------------------------------------------------------ CONTIG
-// One kStreamBlock-thread workgroup per kStreamBlock vectors; thread t of
-// workgroup b moves vector b * kStreamBlock + t of every operand.
-template <int VEC, typename Op, typename C, typename CT, typename OT, typename... S>
-__global__ void __launch_bounds__(kStreamBlock)
+// One BS-thread workgroup per BS vectors; thread t of workgroup b moves
+// vector b * BS + t of every operand.
+template <int BS, int VEC, typename Op, typename C, typename CT, typename OT, typename... S>
+__global__ void __launch_bounds__(BS)
 k_contig(Op op, TArgs<1 + sizeof...(S)> a, int64_t n) {
   constexpr int N = sizeof...(S);
   const int64_t nvec = n / VEC;
-  const int64_t v = (int64_t)blockIdx.x * kStreamBlock + threadIdx.x;
+  const int64_t v = (int64_t)blockIdx.x * BS + threadIdx.x;
   OT* out = static_cast<OT*>(a.p[0]);
   if (v < nvec) {
     C x[VEC][N > 0 ? N : 1];

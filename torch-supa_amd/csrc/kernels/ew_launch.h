@@ -165,8 +165,11 @@ int launch_static(const Op& op, const supa_amd_ew_desc& d, const int* tin, hipSt
     for (int k = 0; k <= N; ++k)
       if (!(k > 0 && a.mode[k]) && !aligned(a.p[k], VEC * sizes_of[k])) al = false;
     if (al && n / VEC < (int64_t(1) << 31)) {  // grid of at most 2^31 threads
-      const int64_t blocks = std::max<int64_t>(1, (n / VEC + kStreamBlock - 1) / kStreamBlock);
-      k_contig<VEC, Op, C, CT, OT, S...><<<dim3((unsigned)blocks), dim3(kStreamBlock), 0, st>>>(op, a, n);
+      // write-only streams (fills) keep four wavefronts per workgroup: 83-85 %
+      // of peak against 47-60 % with one
+      constexpr int BS = N == 0 ? kBlock : kStreamBlock;
+      const int64_t blocks = std::max<int64_t>(1, (n / VEC + BS - 1) / BS);
+      k_contig<BS, VEC, Op, C, CT, OT, S...><<<dim3((unsigned)blocks), dim3(BS), 0, st>>>(op, a, n);
       return launch_status();
     }
   }
