@@ -22,11 +22,12 @@
 namespace sa {
 
 constexpr int kRedBlocks = 1024;   // stage-1 grid (capped by the work)
+constexpr int kRedBlock = 256;     // stage-1 workgroup
 constexpr int kCounterBytes = 256; // reserved head of the workspace (keeps partials 256-byte aligned)
 
 enum RedLayout { R_CONTIG = 0, R_VECND = 1, R_STRIDED = 2 };
 
-template <typename ACC>
+template <int BS, typename ACC>
 __device__ __forceinline__ ACC block_sum(ACC v, ACC* lds) {
   // wavefront (64 lanes) tree, then the 4 wave results in a fixed order
 #pragma unroll
@@ -37,7 +38,7 @@ __device__ __forceinline__ ACC block_sum(ACC v, ACC* lds) {
   ACC r = ACC(0);
   if (threadIdx.x == 0) {
 #pragma unroll
-    for (int w = 0; w < kBlock / 64; ++w) r += lds[w];
+    for (int w = 0; w < BS / 64; ++w) r += lds[w];
   }
   return r;  // valid in thread 0
 }
@@ -45,12 +46,12 @@ __device__ __forceinline__ ACC block_sum(ACC v, ACC* lds) {
 // Accumulates op(...) over this thread's share of the iteration space.  BC:
 // some input is broadcast (a one-element input, or stride 0 / re-read rows in
 // the N-d layout); without it the loop carries no per-operand branches.
-template <int LAYOUT, int VEC, bool BC, typename Op, typename C, typename CT, typename ACC, typename... S>
+template <int BS, int LAYOUT, int VEC, bool BC, typename Op, typename C, typename CT, typename ACC, typename... S>
 __device__ __forceinline__ ACC accumulate(const Op& op, const TArgs<1 + sizeof...(S)>& a, const NdGeom& g, int64_t n) {
   constexpr int N = sizeof...(S);
   ACC acc = ACC(0);
-  const int64_t tid = (int64_t)blockIdx.x * kBlock + threadIdx.x;
-  const int64_t nthreads = (int64_t)gridDim.x * kBlock;
+  const int64_t tid = (int64_t)blockIdx.x * BS + threadIdx.x;
+  const int64_t nthreads = (int64_t)gridDim.x * BS;
   if constexpr (LAYOUT == R_CONTIG) {
     const int64_t nvec = n / VEC;
     for (int64_t v = tid; v < nvec; v += nthreads) {
@@ -150,12 +151,12 @@ __device__ __forceinline__ ACC accumulate(const Op& op, const TArgs<1 + sizeof..
   return acc;
 }
 
-template <int LAYOUT, int VEC, bool BC, typename Op, typename C, typename CT, typename ACC, typename... S>
-__global__ void __launch_bounds__(kBlock)
+template <int BS, int LAYOUT, int VEC, bool BC, typename Op, typename C, typename CT, typename ACC, typename... S>
+__global__ void __launch_bounds__(BS)
 k_reduce_partial(Op op, TArgs<1 + sizeof...(S)> a, NdGeom g, int64_t n, ACC* __restrict__ partial) {
-  __shared__ ACC lds[kBlock / 64];
-  ACC acc = accumulate<LAYOUT, VEC, BC, Op, C, CT, ACC, S...>(op, a, g, n);
-  acc = block_sum<ACC>(acc, lds);
+  __shared__ ACC lds[BS / 64];
+  ACC acc = accumulate<BS, LAYOUT, VEC, BC, Op, C, CT, ACC, S...>(op, a, g, n);
+  acc = block_sum<BS, ACC>(acc, lds);
   if (threadIdx.x == 0) partial[blockIdx.x] = acc;
 }
 
@@ -167,7 +168,7 @@ k_reduce_final(const ACC* __restrict__ partial, int nparts, ACC scale, OT* __res
   ACC v = fold_strided<kRedBlocks / kBlock>(
       ACC(0), threadIdx.x, kBlock, nparts, [&](int64_t i) { return partial[i]; },
       [](ACC a, ACC b) { return a + b; });
-  v = block_sum<ACC>(v, lds);
+  v = block_sum<kBlock, ACC>(v, lds);
   if (threadIdx.x == 0) out[0] = from_arith<OT>(v * scale);
 }
 
@@ -227,22 +228,22 @@ int launch_reduce(const Op& op, const supa_amd_ew_desc& d, const int* tin, doubl
   }
   const NdGeom g = make_geom(d);
   const int64_t units = layout == R_STRIDED ? n : std::max<int64_t>(n / VEC, 1);
-  const int64_t want = (units + 4 * kBlock - 1) / (4 * kBlock);
+  const int64_t want = (units + 4 * kRedBlock - 1) / (4 * kRedBlock);
   const unsigned blocks = (unsigned)std::max<int64_t>(1, std::min<int64_t>(want, kRedBlocks));
   bool bc = false;
   for (int i = 0; i < N; ++i) bc = bc || a.mode[1 + i] != 0 || a.st[1 + i][0] == 0;
   ACC* partial = reinterpret_cast<ACC*>(static_cast<char*>(ws) + kCounterBytes);
   switch (layout) {
     case R_CONTIG:
-      if (bc) k_reduce_partial<R_CONTIG, VEC, true, Op, C, CT, ACC, S...><<<blocks, kBlock, 0, st>>>(op, a, g, n, partial);
-      else k_reduce_partial<R_CONTIG, VEC, false, Op, C, CT, ACC, S...><<<blocks, kBlock, 0, st>>>(op, a, g, n, partial);
+      if (bc) k_reduce_partial<kRedBlock, R_CONTIG, VEC, true, Op, C, CT, ACC, S...><<<blocks, kRedBlock, 0, st>>>(op, a, g, n, partial);
+      else k_reduce_partial<kRedBlock, R_CONTIG, VEC, false, Op, C, CT, ACC, S...><<<blocks, kRedBlock, 0, st>>>(op, a, g, n, partial);
       break;
     case R_VECND:
-      if (bc) k_reduce_partial<R_VECND, VEC, true, Op, C, CT, ACC, S...><<<blocks, kBlock, 0, st>>>(op, a, g, n, partial);
-      else k_reduce_partial<R_VECND, VEC, false, Op, C, CT, ACC, S...><<<blocks, kBlock, 0, st>>>(op, a, g, n, partial);
+      if (bc) k_reduce_partial<kRedBlock, R_VECND, VEC, true, Op, C, CT, ACC, S...><<<blocks, kRedBlock, 0, st>>>(op, a, g, n, partial);
+      else k_reduce_partial<kRedBlock, R_VECND, VEC, false, Op, C, CT, ACC, S...><<<blocks, kRedBlock, 0, st>>>(op, a, g, n, partial);
       break;
     default:
-      k_reduce_partial<R_STRIDED, 1, false, Op, C, CT, ACC, S...><<<blocks, kBlock, 0, st>>>(op, a, g, n, partial);
+      k_reduce_partial<kRedBlock, R_STRIDED, 1, false, Op, C, CT, ACC, S...><<<blocks, kRedBlock, 0, st>>>(op, a, g, n, partial);
       break;
   }
   const int rc = launch_status();
@@ -336,7 +337,7 @@ k_sum_rows(const T* __restrict__ in, OT* __restrict__ out, int64_t inner, ACC sc
   ACC acc = fold_strided<8>(
       ACC(0), threadIdx.x, kBlock, inner, [&](int64_t i) { return (ACC)to_arith(row[i]); },
       [](ACC a, ACC b) { return a + b; });
-  acc = block_sum<ACC>(acc, lds);
+  acc = block_sum<kBlock, ACC>(acc, lds);
   if (threadIdx.x == 0) out[blockIdx.x] = from_arith<OT>(acc * scale);
 }
 
