@@ -921,3 +921,35 @@ def test_comparisons_where_masked_fill(dtype, no_fallback):
     m.masked_fill_((db > 0)[:, :1], torch.tensor(3))  # column mask, 0-dim value
     _exact(m, a.clone().masked_fill_((b > 0)[:, :1], torch.tensor(3)))
     _exact(torch.masked_fill(da, cond, 1), torch.masked_fill(a, a > 0, 1))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_half_with_float32_device_scalar(dtype, no_fallback):
+    """A half-precision tensor with a 0-dim float32 device tensor: the common
+    dtype is the half type (0-dim tensors do not promote a dimensioned one).
+    Upstream's device kernels load both operands as the common type
+    (Loops.cuh opmath_gpu_kernel_with_scalars -> BinaryFunctor<scalar_t,
+    scalar_t>), so the float32 value is rounded to it first; the static
+    kernels match the upstream CPU kernels given that rounded value, bit for
+    bit, contiguous or not.  (Upstream's CPU kernels would use the unrounded
+    value of a CPU 0-dim tensor: that is a different operand kind, bound as
+    an immediate here.)"""
+    x = seeded((257, 1030), 70, 3.0, dtype)
+    s = torch.tensor(0.3000001, dtype=torch.float32)  # not representable in the half type
+    sr = s.to(dtype)
+    dx, ds = dev(x), dev(s)
+    for got, want in (
+        (dx * ds, x * sr),
+        (ds * dx, sr * x),
+        (dx + ds, x + sr),
+        (torch.add(dx, ds, alpha=2), torch.add(x, sr, alpha=2)),
+        (ds / dx, sr / x),
+        (dx / ds, x / sr),
+        (dx.t() * ds, x.t() * sr),
+        (dx[:, 1::3] - ds, x[:, 1::3] - sr),
+    ):
+        assert got.dtype == dtype
+        assert torch.equal(got.cpu(), want)
+    y = dx.clone()
+    y.mul_(ds)
+    assert torch.equal(y.cpu(), x * sr)

@@ -55,6 +55,23 @@ constexpr int kMaxIn = SUPA_AMD_MAX_OPERANDS - 1;
 // Op functors: `static constexpr int arity;` and
 // `template <class C> __device__ C operator()(const C* x) const`.
 
+// Binary ops with static kernels for a bf16 / f16 common dtype whose second
+// or first input is a 0-dim float32 device tensor next to a half-precision
+// tensor (`static constexpr bool kLowpMix = true;`): the 0-dim operand is
+// bound with BindDev1, so the kernel streams the half tensor alone.  The
+// float32 input is rounded to the common dtype on load and the result is
+// rounded to it once: upstream's device kernels load both operands as the
+// common type (opmath_gpu_kernel_with_scalars -> BinaryFunctor<scalar_t,
+// scalar_t>, Loops.cuh), before the float arithmetic.  (A 0-dim CPU tensor
+// is not such an operand: it is bound as an immediate at full precision, as
+// the is_cpu_scalar branch there reads it.)
+template <typename Op, typename = void> struct LowpMixOf {
+  static constexpr bool value = false;
+};
+template <typename Op> struct LowpMixOf<Op, std::void_t<decltype(Op::kLowpMix)>> {
+  static constexpr bool value = Op::kLowpMix;
+};
+
 // Storage pattern an op has static kernels for beyond "every operand in the
 // common dtype": 1 = bool output from common-dtype inputs (comparisons,
 // isnan); 2 = a bool first input, the rest and the output common (where,
@@ -74,6 +91,33 @@ struct Bind1 {  // binds input position K to value v
   int k;
   C v;
   __device__ __forceinline__ C operator()(const C* x) const {
+    C y[Op::arity];
+#pragma unroll
+    for (int i = 0, j = 0; i < Op::arity; ++i) {
+      if (i == k) {
+        y[i] = v;
+      } else {
+        y[i] = x[j];
+        ++j;
+      }
+    }
+    return op(y);
+  }
+};
+
+// Binds input position k to the one element at device address p (a 0-dim
+// device tensor of storage type S), read in the kernel and rounded through
+// the common type CT like any other operand; the compiler reads it once per
+// thread.
+template <typename Op, typename C, typename CT, typename S>
+struct BindDev1 {
+  static constexpr int arity = Op::arity - 1;
+  static constexpr int kDtypeMode = DtypeModeOf<Op>::value;
+  Op op;
+  int k;
+  const S* p;
+  __device__ __forceinline__ C operator()(const C* x) const {
+    const C v = load_cvt<C, CT>(*p);
     C y[Op::arity];
 #pragma unroll
     for (int i = 0, j = 0; i < Op::arity; ++i) {

@@ -375,6 +375,27 @@ int dispatch_types(const Op& op, const supa_amd_ew_desc& d, const int* tin, hipS
       });
     }
   }
+  if constexpr (std::is_same<C, float>::value && N == 2 && LowpMixOf<Op>::value) {
+    // bf16 / f16 common dtype and output, one input a 0-dim float32 tensor
+    const int d0 = d.op[tin[0]].dtype, d1 = d.op[tin[1]].dtype;
+    if ((common == SUPA_AMD_BF16 || common == SUPA_AMD_F16) && d.op[0].dtype == common &&
+        ((d0 == common && d1 == SUPA_AMD_F32) || (d0 == SUPA_AMD_F32 && d1 == common))) {
+      const int fpos = d1 == SUPA_AMD_F32 ? 1 : 0;
+      const supa_amd_operand& fo = d.op[tin[fpos]];
+      bool one = true;
+      for (int j = 0; j < d.ndim; ++j) one = one && fo.strides[j] == 0;
+      if (one) {
+        const int rest[1] = {tin[1 - fpos]};
+        auto go = [&](auto* tag) -> int {
+          using T = std::remove_pointer_t<decltype(tag)>;
+          using B = BindDev1<Op, float, T, float>;
+          const B b{op, fpos, static_cast<const float*>(fo.data)};
+          return launch_static<B, float, T, T, T>(b, d, rest, st);
+        };
+        return common == SUPA_AMD_BF16 ? go((bf16*)nullptr) : go((f16*)nullptr);
+      }
+    }
+  }
   if constexpr (std::is_same<C, float>::value && N >= 1 && N <= 2) {
     auto fam = [](int dt) { return dt == SUPA_AMD_F32 || dt == SUPA_AMD_BF16 || dt == SUPA_AMD_F16; };
     bool mixed = common == SUPA_AMD_F32 && d.op[0].dtype == SUPA_AMD_F32;

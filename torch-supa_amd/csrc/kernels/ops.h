@@ -27,12 +27,14 @@ template <typename C> __device__ __forceinline__ C muladd(C a, C b, C c) {
 // ------------------------------------------------------------- binary
 // add: ufunc::add `self + alpha * other` (UfuncCUDA_add.cu:13-16).
 template <typename C> struct AddOp {
+  static constexpr bool kLowpMix = true;
   static constexpr int arity = 2;
   C alpha;
   __device__ __forceinline__ C operator()(const C* x) const { return muladd<C>(alpha, x[1], x[0]); }
 };
 // mul: MulFunctor (BinaryInternal.h:17-30; bool is &&).
 template <typename C> struct MulOp {
+  static constexpr bool kLowpMix = true;
   static constexpr int arity = 2;
   __device__ __forceinline__ C operator()(const C* x) const {
     if constexpr (std::is_same<C, bool>::value) return x[0] && x[1];
@@ -42,6 +44,7 @@ template <typename C> struct MulOp {
 };
 // true division: DivFunctor `a / b` (BinaryInternal.h:10-15), IEEE.
 template <typename C> struct DivTrueOp {
+  static constexpr bool kLowpMix = true;
   static constexpr int arity = 2;
   __device__ __forceinline__ C operator()(const C* x) const { return x[0] / x[1]; }
 };
