@@ -138,6 +138,13 @@ int supa_amd_pointwise(const supa_amd_ew_desc* d, int op, double value, int64_t 
 #define SUPA_AMD_SQRT 12
 #define SUPA_AMD_EXPM1 13
 #define SUPA_AMD_LOG1P 14
+#define SUPA_AMD_SIGN 15
+#define SUPA_AMD_FLOOR 16
+#define SUPA_AMD_CEIL 17
+#define SUPA_AMD_ROUND 18
+#define SUPA_AMD_TRUNC 19
+#define SUPA_AMD_RSQRT 20
+#define SUPA_AMD_BITWISE_NOT 21
 
 /* out = f(x), floating dtypes (RELU, NEG and ABS also integer).  op = {out, x}.
  * Replaces the reference's upstream-ATen activation kernels: gelu.out NF:5216,
@@ -146,6 +153,42 @@ int supa_amd_pointwise(const supa_amd_ew_desc* d, int op, double value, int64_t 
  * helpers reciprocal.out (x.__rtruediv__), abs.out, sqrt.out (IEEE 1/x, |x|,
  * correctly rounded sqrt). */
 int supa_amd_unary(const supa_amd_ew_desc* d, int op, void* stream);
+/* The rounding / sign family and friends on the same entry: SIGN (also sgn
+ * for real dtypes; (0 < x) - (x < 0), NaN -> 0) sign.out NF:9892 / sgn.out NF:445; FLOOR,
+ * CEIL, TRUNC, ROUND (halves to even; integers copy) floor.out NF:2768,
+ * ceil.out NF:1490, trunc.out NF:6505, round.out NF:5123; RSQRT (IEEE 1 /
+ * correctly rounded sqrt, as upstream CPU) rsqrt.out NF:5303; BITWISE_NOT
+ * (bool: not; integers: ~) bitwise_not.out NF:1231. */
+
+/* Bitwise and / or / xor on bool and integer dtypes.  op = {out, a, b}.
+ * Replaces bitwise_and.Tensor_out NF:8549, bitwise_or.Tensor_out NF:8616,
+ * bitwise_xor.Tensor_out NF:8683 (upstream BinaryBitwiseOpsKernels.cu). */
+#define SUPA_AMD_BIT_AND 0
+#define SUPA_AMD_BIT_OR 1
+#define SUPA_AMD_BIT_XOR 2
+int supa_amd_bitwise(const supa_amd_ew_desc* d, int op, void* stream);
+
+/* Logical and / or / xor (op = {out, a, b}) and not (op = {out, x}): every
+ * operand tested against zero, the output bool (or any dtype: 1 / 0).
+ * Replaces logical_and.out NF:1339, logical_or.out NF:1360, logical_xor.out
+ * NF:1318, logical_not.out NF:1297 (upstream LogicalOpsKernels.cu). */
+#define SUPA_AMD_LOGICAL_AND 0
+#define SUPA_AMD_LOGICAL_OR 1
+#define SUPA_AMD_LOGICAL_XOR 2
+#define SUPA_AMD_LOGICAL_NOT 3
+int supa_amd_logical(const supa_amd_ew_desc* d, int op, void* stream);
+
+/* out = x ** exponent, floating dtypes, op = {out, x}.  The exponent is first
+ * rounded to the tensor's dtype; 2 -> x*x, 3 -> x*x*x, -2 -> 1/(x*x) (products
+ * rounded to a 16-bit storage type between factors), otherwise pow evaluated
+ * in double and rounded once.  (0, 1, 0.5, -0.5 and -1 are the caller's
+ * fill / copy / sqrt / rsqrt / reciprocal.)  Replaces pow.Tensor_Scalar_out
+ * NF:10494 (upstream PowKernel.cu pow_tensor_scalar_kernel). */
+int supa_amd_pow_scalar(const supa_amd_ew_desc* d, double exponent, void* stream);
+/* out = base ** exponent elementwise, floating dtypes, pow in double rounded
+ * once; op = {out, base, exponent}, either may be an immediate scalar.
+ * Replaces pow.Tensor_Tensor_out NF:10466 and pow.Scalar_out NF:10481. */
+int supa_amd_pow(const supa_amd_ew_desc* d, void* stream);
 
 /* grad_in = f'(...) * dy.  op = {grad_in, dy, x} where x is the forward input
  * for GELU, GELU_TANH, SILU and the forward output for SIGMOID, TANH.
@@ -297,7 +340,8 @@ int supa_amd_bce_logits_backward(const supa_amd_ew_desc* d, int has_pos_weight, 
 
 /* out[0] = scale * sum(in) over every element of the described input
  * (op = {out, in}; op[0] describes the input's iteration space, its data is
- * the one-element output).  Accumulates in float32 (float64 for f64 input),
+ * the one-element output).  Accumulates in float32 (float64 for f64 input;
+ * int64 for bool and integer input, whose output must be int64 and scale 1),
  * deterministic two-stage tree through `workspace`.  scale = 1 for sum,
  * 1/n for mean (the reference's mean factor, ReduceMomentKernel.cu:20).
  * Replaces sum_stub / mean_stub for full reductions:
@@ -308,6 +352,7 @@ int64_t supa_amd_sum_workspace_bytes(int64_t numel);
 
 /* Reduction of the innermost `inner` elements of each of `outer` rows of a
  * contiguous input: out[r] = scale * sum(in[r*inner .. r*inner+inner)).
+ * Bool / integer input sums into an int64 output (scale 1).
  * Replaces sum_stub / mean_stub for dim reductions over trailing dims. */
 int supa_amd_sum_rows(const void* in, int32_t in_dtype, void* out, int32_t out_dtype,
                       int64_t outer, int64_t inner, double scale, void* stream);

@@ -953,3 +953,43 @@ def test_half_with_float32_device_scalar(dtype, no_fallback):
     y = dx.clone()
     y.mul_(ds)
     assert torch.equal(y.cpu(), x * sr)
+
+
+def test_integer_and_bool_sums(no_fallback):
+    """Sums of bool and integer tensors are int64 (upstream's rule), full and
+    over dims, and a floating dtype argument converts first."""
+    g = torch.Generator().manual_seed(71)
+    b = torch.rand(300, 517, generator=g) > 0.3
+    i32 = torch.randint(-1000, 1000, (300, 517), generator=g, dtype=torch.int32)
+    i64 = torch.randint(-(2**40), 2**40, (4099,), generator=g)
+    u8 = torch.randint(0, 255, (77, 5), generator=g, dtype=torch.uint8)
+    for t in (b, i32, i64, u8):
+        d = dev(t)
+        got = d.sum()
+        assert got.dtype == torch.int64 and torch.equal(got.cpu(), t.sum())
+    for t, dims in ((b, 1), (i32, 0), (i32, (0, 1)), (u8, -1)):
+        assert torch.equal(dev(t).sum(dims).cpu(), t.sum(dims))
+        assert torch.equal(dev(t).sum(dims, keepdim=True).cpu(), t.sum(dims, keepdim=True))
+    assert torch.equal(dev(i32).sum(dtype=torch.float32).cpu(), i32.sum(dtype=torch.float32))
+    assert dev(torch.zeros(0, dtype=torch.bool)).sum().item() == 0
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_cross_entropy_label_smoothing(dtype, no_fallback):
+    """The composite label-smoothing path (log_softmax, the nll term, a
+    smoothing sum and the kept-row count over a bool mask) on the device,
+    forward and backward, against upstream CPU."""
+    g = torch.Generator().manual_seed(72)
+    x = (torch.randn(300, 1000, generator=g) * 2).to(dtype)
+    t = torch.randint(0, 1000, (300,), generator=g)
+    t[::7] = -100
+    for red in ("mean", "sum", "none"):
+        dx = dev(x).requires_grad_()
+        xc = x.clone().requires_grad_()
+        got = F.cross_entropy(dx, dev(t), label_smoothing=0.1, reduction=red)
+        want = F.cross_entropy(xc.float(), t, label_smoothing=0.1, reduction=red)
+        tol = dict(rtol=1e-5, atol=1e-5) if dtype == torch.float32 else dict(rtol=2e-2, atol=2e-2)
+        torch.testing.assert_close(got.float().cpu(), want.detach(), **tol)
+        got.sum().backward()
+        want.sum().backward()
+        torch.testing.assert_close(dx.grad.float().cpu(), xc.grad.float(), **tol)

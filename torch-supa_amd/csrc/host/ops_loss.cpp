@@ -103,9 +103,14 @@ std::vector<int64_t> reduce_dims(const at::Tensor& self, at::OptionalIntArrayRef
 at::Tensor& sum_mean_into(const at::Tensor& self, at::OptionalIntArrayRef dim, bool keepdim,
                           std::optional<c10::ScalarType> dtype, bool mean, at::Tensor& out, const char* name) {
   c10::ScalarType acc_dt = dtype.value_or(self.scalar_type());
-  if (!dtype && at::isIntegralType(self.scalar_type(), true)) acc_dt = at::kLong;
-  TORCH_CHECK(is_float_dtype(acc_dt) && is_float_dtype(self.scalar_type()), name,
-              ": supa implements floating-point reductions only (got ", self.scalar_type(), " -> ", acc_dt, ")");
+  const bool int_in = at::isIntegralType(self.scalar_type(), true);
+  if (!dtype && int_in) acc_dt = at::kLong;
+  // integer / bool sums accumulate in int64 (upstream's sum of integral
+  // tensors); a floating dtype argument converts the input first
+  const bool int_sum = !mean && int_in && acc_dt == at::kLong;
+  TORCH_CHECK(int_sum || (is_float_dtype(acc_dt) && (int_in || is_float_dtype(self.scalar_type()))), name,
+              ": supa implements floating-point reductions and integer sums (got ", self.scalar_type(), " -> ",
+              acc_dt, ")");
   const std::vector<int64_t> dims = reduce_dims(self, dim);
   std::vector<int64_t> oshape;
   std::vector<bool> red(self.dim(), false);
@@ -129,7 +134,9 @@ at::Tensor& sum_mean_into(const at::Tensor& self, at::OptionalIntArrayRef dim, b
   }
   const double scale = mean ? 1.0 / (double)nred : 1.0;
   // the input must hold the output dtype's family: promote once if asked
-  at::Tensor x = (acc_dt == at::kDouble && self.scalar_type() != at::kDouble) ? self.to(at::kDouble) : self;
+  at::Tensor x = self;
+  if (int_in && !int_sum) x = self.to(acc_dt);
+  else if (acc_dt == at::kDouble && self.scalar_type() != at::kDouble) x = self.to(at::kDouble);
   if ((int64_t)dims.size() == self.dim()) {
     at::Tensor res = out.is_contiguous() ? out : empty_supa({}, acc_dt, self.device().index());
     reduce_apply(res, {x}, x.scalar_type(),

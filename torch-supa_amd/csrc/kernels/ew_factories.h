@@ -27,13 +27,33 @@ template <int K, bool Bwd>
 struct UnaryFactory {
   template <typename C> static constexpr bool ok() {
     if constexpr (Bwd) return std::is_floating_point<C>::value;
-    else if constexpr (K == U_RELU || K == U_NEG || K == U_ABS) return true;
+    else if constexpr (K == U_RELU || K == U_NEG || K == U_ABS || K == U_SIGN || K == U_FLOOR || K == U_CEIL ||
+                       K == U_ROUND || K == U_TRUNC)
+      return true;
+    else if constexpr (K == U_BITNOT) return std::is_integral<C>::value;
     else return std::is_floating_point<C>::value;
   }
   template <typename C> auto make() const {
     if constexpr (Bwd) return UnaryBwdOp<K, C>{};
     else return UnaryOp<K, C>{};
   }
+};
+
+template <int K>
+struct BitFactory {
+  template <typename C> static constexpr bool ok() { return std::is_integral<C>::value; }
+  template <typename C> BitOp<K, C> make() const { return BitOp<K, C>{}; }
+};
+template <int K>
+struct LogicalFactory {
+  template <typename C> static constexpr bool ok() { return true; }
+  template <typename C> LogicalOp<K, C> make() const { return LogicalOp<K, C>{}; }
+};
+struct PowScalarFactory {
+  int mode, half;
+  double e;
+  template <typename C> static constexpr bool ok() { return std::is_floating_point<C>::value; }
+  template <typename C> PowScalarOp<C> make() const { return PowScalarOp<C>{mode, half, e}; }
 };
 
 template <int K, bool Bwd>

@@ -3,6 +3,20 @@
 
 using namespace sa;
 
+namespace {
+// float -> bf16 -> float on the host: round to nearest even, NaN kept NaN.
+float host_round_bf16(float f) {
+  uint32_t u;
+  __builtin_memcpy(&u, &f, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return f;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  u &= 0xffff0000u;
+  float r;
+  __builtin_memcpy(&r, &u, 4);
+  return r;
+}
+}  // namespace
+
 extern "C" {
 
 int supa_amd_unary(const supa_amd_ew_desc* d, int op, void* stream) {
@@ -22,8 +36,52 @@ int supa_amd_unary(const supa_amd_ew_desc* d, int op, void* stream) {
     case SUPA_AMD_SQRT: return run_unary<U_SQRT, false>(d, stream);
     case SUPA_AMD_EXPM1: return run_unary<U_EXPM1, false>(d, stream);
     case SUPA_AMD_LOG1P: return run_unary<U_LOG1P, false>(d, stream);
+    case SUPA_AMD_SIGN: return run_unary<U_SIGN, false>(d, stream);
+    case SUPA_AMD_FLOOR: return run_unary<U_FLOOR, false>(d, stream);
+    case SUPA_AMD_CEIL: return run_unary<U_CEIL, false>(d, stream);
+    case SUPA_AMD_ROUND: return run_unary<U_ROUND, false>(d, stream);
+    case SUPA_AMD_TRUNC: return run_unary<U_TRUNC, false>(d, stream);
+    case SUPA_AMD_RSQRT: return run_unary<U_RSQRT, false>(d, stream);
+    case SUPA_AMD_BITWISE_NOT: return run_unary<U_BITNOT, false>(d, stream);
     default: return SUPA_AMD_EINVAL;
   }
+}
+
+int supa_amd_bitwise(const supa_amd_ew_desc* d, int op, void* stream) {
+  switch (op) {
+    case SUPA_AMD_BIT_AND: return run_ew(BitFactory<BIT_AND>{}, d, stream, 3);
+    case SUPA_AMD_BIT_OR: return run_ew(BitFactory<BIT_OR>{}, d, stream, 3);
+    case SUPA_AMD_BIT_XOR: return run_ew(BitFactory<BIT_XOR>{}, d, stream, 3);
+    default: return SUPA_AMD_EINVAL;
+  }
+}
+
+int supa_amd_logical(const supa_amd_ew_desc* d, int op, void* stream) {
+  switch (op) {
+    case SUPA_AMD_LOGICAL_AND: return run_ew(LogicalFactory<LOG_AND>{}, d, stream, 3);
+    case SUPA_AMD_LOGICAL_OR: return run_ew(LogicalFactory<LOG_OR>{}, d, stream, 3);
+    case SUPA_AMD_LOGICAL_XOR: return run_ew(LogicalFactory<LOG_XOR>{}, d, stream, 3);
+    case SUPA_AMD_LOGICAL_NOT: return run_ew(LogicalFactory<LOG_NOT>{}, d, stream, 2);
+    default: return SUPA_AMD_EINVAL;
+  }
+}
+
+int supa_amd_pow_scalar(const supa_amd_ew_desc* d, double exponent, void* stream) {
+  if (!d) return SUPA_AMD_EINVAL;
+  // the exponent in the tensor's dtype, as upstream's exp_scalar.to<scalar_t>()
+  if (d->common_dtype == SUPA_AMD_F32) exponent = (double)(float)exponent;
+  else if (d->common_dtype == SUPA_AMD_BF16) exponent = (double)host_round_bf16((float)exponent);
+  else if (d->common_dtype == SUPA_AMD_F16) exponent = (double)(float)(_Float16)(float)exponent;
+  const int mode = exponent == 2.0 ? POW_SQUARE
+                   : exponent == 3.0 ? POW_CUBE
+                   : exponent == -2.0 ? POW_INV_SQUARE
+                                      : POW_GENERAL;
+  const int half = d->common_dtype == SUPA_AMD_BF16 ? 1 : (d->common_dtype == SUPA_AMD_F16 ? 2 : 0);
+  return run_ew(PowScalarFactory{mode, half, exponent}, d, stream, 2);
+}
+
+int supa_amd_pow(const supa_amd_ew_desc* d, void* stream) {
+  return run_ew(SimpleFactory<PowOp, true>{}, d, stream, 3);
 }
 
 }  // extern "C"

@@ -147,7 +147,7 @@ template <typename C> __device__ __forceinline__ C sigmoidx(C x) { return C(1) /
 
 enum UnaryKind {
   U_GELU = 0, U_GELU_TANH, U_SILU, U_SIGMOID, U_TANH, U_EXP, U_LOG, U_ERF, U_RELU, U_NEG, U_RECIPROCAL, U_ABS, U_SQRT,
-  U_EXPM1, U_LOG1P
+  U_EXPM1, U_LOG1P, U_SIGN, U_FLOOR, U_CEIL, U_ROUND, U_TRUNC, U_RSQRT, U_BITNOT
 };
 
 template <int K, typename C> struct UnaryOp {
@@ -183,6 +183,21 @@ template <int K, typename C> struct UnaryOp {
       if constexpr (std::is_same<C, bool>::value) return x;
       else if constexpr (std::is_integral<C>::value) return x < 0 ? (C)(0 - (uint64_t)x) : x;
       else return fabs(x);
+    } else if constexpr (K == U_SIGN) {
+      // upstream sign_kernel: (0 < a) - (a < 0); NaN and -0 give +0
+      if constexpr (std::is_same<C, bool>::value) return x;
+      else return (C)((int)(C(0) < x) - (int)(x < C(0)));
+    } else if constexpr (K == U_FLOOR || K == U_CEIL || K == U_ROUND || K == U_TRUNC) {
+      if constexpr (!std::is_floating_point<C>::value) return x;  // integers: a copy, as upstream
+      else if constexpr (K == U_FLOOR) return floor(x);
+      else if constexpr (K == U_CEIL) return ceil(x);
+      else if constexpr (K == U_ROUND) return rint(x);  // nearbyint: halves to even
+      else return trunc(x);
+    } else if constexpr (K == U_RSQRT) {
+      return C(1) / sqrt(x);  // IEEE quotient of the correctly rounded root, as upstream CPU
+    } else if constexpr (K == U_BITNOT) {
+      if constexpr (std::is_same<C, bool>::value) return !x;
+      else return ~x;
     } else {
       return sqrt(x);
     }
@@ -363,6 +378,68 @@ template <int K, typename C> struct CmpOp {
     else r = x[0] >= x[1];
     return r ? C(1) : C(0);
   }
+};
+// bitwise and / or / xor on bool and integer storage (computed in bool or
+// int64; truncation to the storage width commutes with these ops).
+enum BitKind { BIT_AND = 0, BIT_OR, BIT_XOR };
+template <int K, typename C> struct BitOp {
+  static constexpr int arity = 2;
+  __device__ __forceinline__ C operator()(const C* x) const {
+    if constexpr (K == BIT_AND) return x[0] & x[1];
+    else if constexpr (K == BIT_OR) return x[0] | x[1];
+    else return x[0] ^ x[1];
+  }
+};
+// logical and / or / xor / not: operands tested against zero (NaN is
+// nonzero), the result 1 or 0 -- a bool output.
+enum LogicalKind { LOG_AND = 0, LOG_OR, LOG_XOR, LOG_NOT };
+template <int K, typename C> struct LogicalOp {
+  static constexpr int arity = K == LOG_NOT ? 1 : 2;
+  static constexpr int kDtypeMode = 1;
+  __device__ __forceinline__ C operator()(const C* x) const {
+    const bool a = x[0] != C(0);
+    bool r;
+    if constexpr (K == LOG_NOT) {
+      r = !a;
+    } else {
+      const bool b = x[1] != C(0);
+      if constexpr (K == LOG_AND) r = a && b;
+      else if constexpr (K == LOG_OR) r = a || b;
+      else r = a != b;
+    }
+    return r ? C(1) : C(0);
+  }
+};
+// pow(x, e) for a scalar exponent, floating types, upstream
+// pow_tensor_scalar_kernel_impl's cases: e = 2 -> x*x, 3 -> x*x*x, -2 ->
+// 1/(x*x) (the quotient in double), otherwise pow in double rounded once.
+// `half` = 1 (bf16) / 2 (f16): products are rounded to the storage type
+// between factors, as the upstream kernel multiplies in that type.
+enum PowMode { POW_GENERAL = 0, POW_SQUARE, POW_CUBE, POW_INV_SQUARE };
+template <typename C> struct PowScalarOp {
+  static constexpr int arity = 1;
+  int mode;
+  int half;
+  double e;
+  __device__ __forceinline__ C rnd(C v) const {
+    if constexpr (std::is_same<C, float>::value) {
+      if (half == 1) return to_arith(from_arith<bf16>(v));
+      if (half == 2) return to_arith(from_arith<f16>(v));
+    }
+    return v;
+  }
+  __device__ __forceinline__ C operator()(const C* x) const {
+    const C b = x[0];
+    if (mode == POW_SQUARE) return b * b;
+    if (mode == POW_CUBE) return rnd(b * b) * b;
+    if (mode == POW_INV_SQUARE) return (C)(1.0 / (double)rnd(b * b));
+    return (C)pow((double)b, e);
+  }
+};
+// pow(base, exponent) elementwise, floating types: pow in double rounded once.
+template <typename C> struct PowOp {
+  static constexpr int arity = 2;
+  __device__ __forceinline__ C operator()(const C* x) const { return (C)pow((double)x[0], (double)x[1]); }
 };
 template <typename C> struct IsNanOp {
   static constexpr int arity = 1;

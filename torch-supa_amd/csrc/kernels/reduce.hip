@@ -176,7 +176,11 @@ template <typename Op, typename C, typename CT, typename OT, typename... S>
 int launch_reduce(const Op& op, const supa_amd_ew_desc& d, const int* tin, double scale, void* ws,
                   int64_t ws_bytes, hipStream_t st) {
   constexpr int N = sizeof...(S);
-  using ACC = typename std::conditional<std::is_same<C, double>::value, double, float>::type;
+  // float32 partials for the float family, float64 for double, int64 for
+  // the integer sums (exact and order-free: wrapping adds modulo 2^64)
+  using ACC = typename std::conditional<std::is_same<C, double>::value, double,
+                                        typename std::conditional<std::is_integral<C>::value, int64_t,
+                                                                  float>::type>::type;
   constexpr int VEC0 = 16 / min_size<S...>();
   constexpr int VEC = VEC0 < 1 ? 1 : VEC0;
   const int64_t n = desc_numel(&d);
@@ -267,10 +271,15 @@ int reduce_same(const Op& op, const supa_amd_ew_desc& d, const int* tin, double 
     else return launch_reduce<Op, C, T, OT, T, T, T, T>(op, d, tin, scale, ws, wsb, st);
   };
   const int od = d.op[0].dtype;
-  if (od == d.common_dtype) return with_out((T*)nullptr);
-  if (od == SUPA_AMD_F32) return with_out((float*)nullptr);
-  if (od == SUPA_AMD_F64) return with_out((double*)nullptr);
-  return SUPA_AMD_EDTYPE;
+  if constexpr (std::is_integral<C>::value) {
+    // integer and bool sums are int64 (upstream's sum of integral tensors)
+    return od == SUPA_AMD_I64 ? with_out((int64_t*)nullptr) : SUPA_AMD_EDTYPE;
+  } else {
+    if (od == d.common_dtype) return with_out((T*)nullptr);
+    if (od == SUPA_AMD_F32) return with_out((float*)nullptr);
+    if (od == SUPA_AMD_F64) return with_out((double*)nullptr);
+    return SUPA_AMD_EDTYPE;
+  }
 }
 
 template <typename Factory>
@@ -299,30 +308,48 @@ int run_reduce(const Factory& f, const supa_amd_ew_desc* d, double scale, void* 
     case SUPA_AMD_BF16: return go((float*)nullptr, (bf16*)nullptr);
     case SUPA_AMD_F16: return go((float*)nullptr, (f16*)nullptr);
     case SUPA_AMD_F64: return go((double*)nullptr, (double*)nullptr);
-    default: return SUPA_AMD_EDTYPE;
+    default: break;
   }
+  if constexpr (Factory::kIntegers) {
+    switch (d->common_dtype) {
+      case SUPA_AMD_BOOL: return go((int64_t*)nullptr, (b8*)nullptr);
+      case SUPA_AMD_U8: return go((int64_t*)nullptr, (uint8_t*)nullptr);
+      case SUPA_AMD_I8: return go((int64_t*)nullptr, (int8_t*)nullptr);
+      case SUPA_AMD_I16: return go((int64_t*)nullptr, (int16_t*)nullptr);
+      case SUPA_AMD_I32: return go((int64_t*)nullptr, (int32_t*)nullptr);
+      case SUPA_AMD_I64: return go((int64_t*)nullptr, (int64_t*)nullptr);
+      default: break;
+    }
+  }
+  return SUPA_AMD_EDTYPE;
 }
 
 struct IdentityFactory {
+  static constexpr bool kIntegers = true;  // sum has integer / bool forms
   template <typename C> IdentityOp<C> make() const { return IdentityOp<C>{}; }
 };
 struct MseTermFactory {
+  static constexpr bool kIntegers = false;
   template <typename C> MseTermOp<C> make() const { return MseTermOp<C>{}; }
 };
 struct SmoothL1TermFactory {
+  static constexpr bool kIntegers = false;
   double beta;
   template <typename C> SmoothL1TermOp<C> make() const { return SmoothL1TermOp<C>{static_cast<C>(beta)}; }
 };
 template <bool PW, bool W, bool HW = false>
 struct BceTermFactory {
+  static constexpr bool kIntegers = false;
   template <typename C> BceTermOp<PW, W, C, HW> make() const { return BceTermOp<PW, W, C, HW>{}; }
   template <typename C> static constexpr bool ok() { return std::is_floating_point<C>::value; }
 };
 struct MseTermEwFactory {
+  static constexpr bool kIntegers = false;
   template <typename C> static constexpr bool ok() { return std::is_floating_point<C>::value; }
   template <typename C> MseTermOp<C> make() const { return MseTermOp<C>{}; }
 };
 struct SmoothL1TermEwFactory {
+  static constexpr bool kIntegers = false;
   double beta;
   template <typename C> static constexpr bool ok() { return std::is_floating_point<C>::value; }
   template <typename C> SmoothL1TermOp<C> make() const { return SmoothL1TermOp<C>{static_cast<C>(beta)}; }
@@ -364,8 +391,10 @@ int supa_amd_sum_rows(const void* in, int32_t in_dtype, void* out, int32_t out_d
   auto go = [&](auto* ti, auto* to) -> int {
     using T = std::remove_pointer_t<decltype(ti)>;
     using OT = std::remove_pointer_t<decltype(to)>;
-    using ACC = typename std::conditional<std::is_same<T, double>::value || std::is_same<OT, double>::value, double,
-                                          float>::type;
+    using ACC = typename std::conditional<
+        std::is_integral<OT>::value, int64_t,
+        typename std::conditional<std::is_same<T, double>::value || std::is_same<OT, double>::value, double,
+                                  float>::type>::type;
     k_sum_rows<T, OT, ACC><<<(unsigned)outer, kBlock, 0, st>>>(static_cast<const T*>(in), static_cast<OT*>(out), inner,
                                                               (ACC)scale);
     return launch_status();
@@ -379,11 +408,20 @@ int supa_amd_sum_rows(const void* in, int32_t in_dtype, void* out, int32_t out_d
       default: return SUPA_AMD_EDTYPE;
     }
   };
+  auto intsel = [&](auto* ti) -> int {
+    return out_dtype == SUPA_AMD_I64 ? go(ti, (int64_t*)nullptr) : SUPA_AMD_EDTYPE;
+  };
   switch (in_dtype) {
     case SUPA_AMD_F32: return outsel((float*)nullptr);
     case SUPA_AMD_BF16: return outsel((bf16*)nullptr);
     case SUPA_AMD_F16: return outsel((f16*)nullptr);
     case SUPA_AMD_F64: return outsel((double*)nullptr);
+    case SUPA_AMD_BOOL: return intsel((b8*)nullptr);
+    case SUPA_AMD_U8: return intsel((uint8_t*)nullptr);
+    case SUPA_AMD_I8: return intsel((int8_t*)nullptr);
+    case SUPA_AMD_I16: return intsel((int16_t*)nullptr);
+    case SUPA_AMD_I32: return intsel((int32_t*)nullptr);
+    case SUPA_AMD_I64: return intsel((int64_t*)nullptr);
     default: return SUPA_AMD_EDTYPE;
   }
 }
