@@ -189,6 +189,11 @@ int supa_amd_pow_scalar(const supa_amd_ew_desc* d, double exponent, void* stream
  * once; op = {out, base, exponent}, either may be an immediate scalar.
  * Replaces pow.Tensor_Tensor_out NF:10466 and pow.Scalar_out NF:10481. */
 int supa_amd_pow(const supa_amd_ew_desc* d, void* stream);
+/* out = x * log(y), 0 where x == 0, NaN where y is NaN; floating dtypes,
+ * op = {out, x, y}, either may be an immediate scalar.  Replaces
+ * xlogy.OutTensor NF:3673, xlogy.OutScalar_Self NF:3683,
+ * xlogy.OutScalar_Other NF:3690 (upstream xlogy_kernel_cuda). */
+int supa_amd_xlogy(const supa_amd_ew_desc* d, void* stream);
 
 /* grad_in = f'(...) * dy.  op = {grad_in, dy, x} where x is the forward input
  * for GELU, GELU_TANH, SILU and the forward output for SIGMOID, TANH.
@@ -286,6 +291,8 @@ int supa_amd_fill(const supa_amd_ew_desc* d, void* stream);
 #define SUPA_AMD_LOSS_MSE 0
 #define SUPA_AMD_LOSS_SMOOTH_L1 1
 #define SUPA_AMD_LOSS_BCE_LOGITS 2
+#define SUPA_AMD_LOSS_HUBER 3 /* beta = delta */
+#define SUPA_AMD_LOSS_BCE 4   /* on probabilities; optional weight (has_weight) */
 
 #define SUPA_AMD_REDUCTION_NONE 0
 #define SUPA_AMD_REDUCTION_MEAN 1
@@ -306,7 +313,10 @@ int supa_amd_fill(const supa_amd_ew_desc* d, void* stream);
  * ReduceMomentKernel.cu:37-55), and
  * SUPANativeFunctions::binary_cross_entropy_with_logits,
  * torch_supa/csrc/aten/ops/BinaryCrossEntropyWithLogits.cpp:23-73 with its
- * kernel .../elementwise/BinaryCrossEntropyWithLogitsKernel.cu:17-113. */
+ * kernel .../elementwise/BinaryCrossEntropyWithLogitsKernel.cu:17-113.
+ * HUBER replaces huber_loss.out NF:12014 (upstream huber_kernel_cuda), BCE
+ * binary_cross_entropy.out NF:1178 ((t - 1) max(log1p(-x), -100) -
+ * t max(log x, -100), times the weight). */
 int supa_amd_loss_forward(const supa_amd_ew_desc* d, int loss, int reduction, double beta,
                           int has_pos_weight, int has_weight, void* out_scalar,
                           void* workspace, int64_t workspace_bytes, void* stream);
@@ -314,9 +324,12 @@ int64_t supa_amd_loss_workspace_bytes(int64_t numel);
 
 /* Loss gradients.  op = {grad_in, grad_out, input, target}; grad_out is
  * broadcast (0-dim) for MEAN/SUM.  norm is the reduction factor the reference
- * applies (2/n or 2 for MSE, 1/n or 1 for SMOOTH_L1).  Replaces
- * mse_loss_backward.grad_input NF:11846 and
- * smooth_l1_loss_backward.grad_input NF:12002. */
+ * applies (2/n or 2 for MSE, 1/n or 1 for SMOOTH_L1 and HUBER); for BCE
+ * op = {grad_in, grad_out, input, target[, weight]} and norm is the divisor
+ * (n for MEAN, else 1): g (x - t) / max((1 - x) x, 1e-12), times the weight,
+ * / norm.  Replaces mse_loss_backward.grad_input NF:11846,
+ * smooth_l1_loss_backward.grad_input NF:12002, huber_loss_backward.out
+ * NF:12026 and binary_cross_entropy_backward.grad_input NF:1195. */
 int supa_amd_loss_backward(const supa_amd_ew_desc* d, int loss, double norm, double beta,
                            void* stream);
 
@@ -554,6 +567,18 @@ int supa_amd_fused_adamw(int32_t ntensors, void* const* params, void* const* gra
                          double beta1, double beta2, double weight_decay, double eps,
                          int amsgrad, int maximize, const float* grad_scale,
                          const float* found_inf, void* stream);
+
+/* Fused Adam (weight decay added to the gradient, upstream adam_math's
+ * ADAM_MODE::ORIGINAL: grad += param * weight_decay after the maximize
+ * negation); otherwise as supa_amd_fused_adamw.  Replaces _fused_adam_
+ * NF:16021 and _fused_adam_.tensor_lr NF:16030 (upstream fused_adam_impl.cu). */
+int supa_amd_fused_adam(int32_t ntensors, void* const* params, void* const* grads,
+                        void* const* exp_avgs, void* const* exp_avg_sqs,
+                        void* const* max_exp_avg_sqs, void* const* state_steps,
+                        const int64_t* numel, int32_t dtype, double lr, const float* lr_ptr,
+                        double beta1, double beta2, double weight_decay, double eps,
+                        int amsgrad, int maximize, const float* grad_scale,
+                        const float* found_inf, void* stream);
 
 #ifdef __cplusplus
 }

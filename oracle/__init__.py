@@ -83,7 +83,7 @@ def lib():
             "or_ce_fwd": (c_int, [_f64p, _i64p, i64, i64, i64, c_int, _f64p, _f64p, _f64p]),
             "or_ce_bwd": (None, [_f64p, _f64p, _i64p, _f64p, c_double, i64, i64, i64, c_int, _f64p]),
             "or_adamw_step": (None, [_f32p, _f32p, _f32p, _f32p, i64, c_float, c_double, c_double,
-                                     c_double, c_double, c_double, c_int, _f32p, c_int, _f32p]),
+                                     c_double, c_double, c_double, c_int, _f32p, c_int, _f32p, c_int]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -374,9 +374,9 @@ def sum_f32(x) -> float:
 
 
 def adamw_step(p, g, m, v, step, lr, beta1, beta2, weight_decay, eps, maximize=False,
-               grad_scale=None, amsgrad=False, vmax=None):
+               grad_scale=None, amsgrad=False, vmax=None, l2=False):
     """In-place AdamW step on float32 numpy arrays (p, m, v and, with
-    grad_scale, g are updated)."""
+    grad_scale, g are updated); l2=True is the Adam step (_fused_adam_)."""
     for a in (p, g, m, v):
         assert a.dtype == np.float32 and a.flags.c_contiguous
     gs = None if grad_scale is None else np.asarray([grad_scale], np.float32)
@@ -384,7 +384,7 @@ def adamw_step(p, g, m, v, step, lr, beta1, beta2, weight_decay, eps, maximize=F
         assert vmax is not None and vmax.dtype == np.float32
     lib().or_adamw_step(_p(p, _f32p), _p(g, _f32p), _p(m, _f32p), _p(v, _f32p), p.size,
                         float(step), lr, beta1, beta2, weight_decay, eps, 1 if maximize else 0,
-                        _p(gs, _f32p), 1 if amsgrad else 0, _p(vmax, _f32p))
+                        _p(gs, _f32p), 1 if amsgrad else 0, _p(vmax, _f32p), 1 if l2 else 0)
 
 
 def vector_norm(x, ord=2.0) -> float:

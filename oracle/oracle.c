@@ -669,10 +669,12 @@ static double pow_int_steps(double beta, float step) {
  * correction :130-137): hyper-parameters are double, state is float, and each
  * mixed expression is evaluated in double and rounded once to float.  The
  * double expressions are written with the fused multiply-adds the device
- * compiler forms for them, so the float results match bit for bit. */
+ * compiler forms for them, so the float results match bit for bit.  l2 = 1:
+ * _fused_adam_ (NF:16021), ADAM_MODE::ORIGINAL, the weight decay added to
+ * the gradient (fused_adam_utils.cuh:49-51). */
 void or_adamw_step(float* p, float* g, float* m, float* v, int64_t n, float step,
                    double lr, double beta1, double beta2, double weight_decay, double eps,
-                   int maximize, const float* grad_scale, int amsgrad, float* vmax) {
+                   int maximize, const float* grad_scale, int amsgrad, float* vmax, int l2) {
   const float bc1 = (float)(1.0 - pow_int_steps(beta1, step));
   const float bc2_sqrt = (float)sqrt(1.0 - pow_int_steps(beta2, step));
   const float step_size = (float)(lr / (double)bc1);
@@ -684,7 +686,10 @@ void or_adamw_step(float* p, float* g, float* m, float* v, int64_t n, float step
     const float grad_to_store = grad;
     if (maximize) grad = -grad;
     float ea = m[i], eas = v[i];
-    if (weight_decay != 0.0) param = (float)fma(-lr_wd, (double)param, (double)param);
+    if (weight_decay != 0.0) {
+      if (l2) grad = (float)((double)grad + (double)param * weight_decay); /* ADAM_MODE::ORIGINAL */
+      else param = (float)fma(-lr_wd, (double)param, (double)param);
+    }
     ea = (float)fma(beta1, (double)ea, (1.0 - beta1) * (double)grad);
     eas = (float)fma(beta2, (double)eas, ((1.0 - beta2) * (double)grad) * (double)grad);
     float denom;

@@ -662,6 +662,31 @@ def test_c5_one_layer_fused_adamw_bit_exact(no_fallback):
         assert st["step"].item() == 10.0
 
 
+@pytest.mark.parametrize("amsgrad", [False, True])
+def test_fused_adam_bit_exact(amsgrad, no_fallback):
+    """torch.optim.Adam(fused=True) (the _fused_adam_ kernel: weight decay on
+    the gradient) for 6 steps on supa against the oracle's Adam step."""
+    shapes = [(1024, 513), (4097,), (3, 5)]
+    g = torch.Generator().manual_seed(3)
+    params = [torch.randn(s, generator=g) * 0.5 for s in shapes]
+    grads = [torch.randn(s, generator=g) * 1e-2 for s in shapes]
+    dp = [dev(p).requires_grad_() for p in params]
+    opt = torch.optim.Adam(dp, lr=1e-3, eps=1e-8, weight_decay=0.05, amsgrad=amsgrad, fused=True)
+    for _ in range(6):
+        for p, gr in zip(dp, grads):
+            p.grad = dev(gr)
+        opt.step()
+    for i, s in enumerate(shapes):
+        hp = params[i].numpy().ravel().copy()
+        hg = grads[i].numpy().ravel().copy()
+        hm, hv, hx = np.zeros_like(hp), np.zeros_like(hp), np.zeros_like(hp)
+        for step in range(1, 7):
+            O.adamw_step(hp, hg, hm, hv, float(step), 1e-3, 0.9, 0.999, 0.05, 1e-8, amsgrad=amsgrad,
+                         vmax=hx if amsgrad else None, l2=True)
+        assert np.array_equal(dp[i].detach().cpu().numpy().ravel(), hp), i
+        assert np.array_equal(opt.state[dp[i]]["exp_avg_sq"].cpu().numpy().ravel(), hv)
+
+
 def test_foreach_list_and_scalar(no_fallback):
     shapes = [(4096, 4096), (4096,), (333, 17)]
     xs = [seeded(s, 40 + i) for i, s in enumerate(shapes)]

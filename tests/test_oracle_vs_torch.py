@@ -373,6 +373,33 @@ def test_adamw_ten_steps_vs_cpu_and_restart():
         assert np.array_equal(p2, p) and np.array_equal(m2, m) and np.array_equal(v2, v)
 
 
+def test_adam_l2_ten_steps_vs_cpu():
+    """_fused_adam_ (weight decay added to the gradient) against upstream's
+    CPU fused Adam; a plant of the AdamW form instead must fail."""
+    shapes = [(256, 256), (300,)]
+    g = torch.Generator().manual_seed(52)
+    params = [torch.randn(s, generator=g) * 0.5 for s in shapes]
+    grads = [torch.randn(s, generator=g) * 1e-3 for s in shapes]
+    tp = [p.clone().requires_grad_() for p in params]
+    opt = torch.optim.Adam(tp, lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.1, fused=True)
+    for _ in range(10):
+        for t, gr in zip(tp, grads):
+            t.grad = gr.clone()
+        opt.step()
+    for i in range(len(shapes)):
+        p = params[i].numpy().copy().ravel()
+        gr = grads[i].numpy().copy().ravel()
+        m, v = np.zeros_like(p), np.zeros_like(p)
+        pw, mw, vw = p.copy(), m.copy(), v.copy()
+        for step in range(1, 11):
+            O.adamw_step(p, gr, m, v, float(step), 1e-3, 0.9, 0.999, 0.1, 1e-8, l2=True)
+            O.adamw_step(pw, gr, mw, vw, float(step), 1e-3, 0.9, 0.999, 0.1, 1e-8)
+        want = tp[i].detach().numpy().ravel()
+        np.testing.assert_allclose(p, want, rtol=1e-5, atol=1e-8)
+        np.testing.assert_allclose(m, opt.state[tp[i]]["exp_avg"].numpy().ravel(), rtol=1e-4, atol=1e-9)
+        assert not np.allclose(pw, want, rtol=1e-5, atol=1e-8)  # the decoupled form is a different update
+
+
 # ------------------------------------------------------------------ AMP
 def test_amp_unscale_vs_cpu():
     x = randn((5000,), 60, 1000.0)

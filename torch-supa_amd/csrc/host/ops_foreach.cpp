@@ -460,7 +460,7 @@ void fused_adamw_impl(at::TensorList params, at::TensorList grads, at::TensorLis
                       at::TensorList exp_avg_sqs, at::TensorList max_exp_avg_sqs, at::TensorList state_steps,
                       double lr, const at::Tensor& lr_tensor, double beta1, double beta2, double weight_decay,
                       double eps, bool amsgrad, bool maximize, const std::optional<at::Tensor>& grad_scale,
-                      const std::optional<at::Tensor>& found_inf) {
+                      const std::optional<at::Tensor>& found_inf, bool l2 = false) {
   const size_t n = params.size();
   TORCH_CHECK(grads.size() == n && exp_avgs.size() == n && exp_avg_sqs.size() == n && state_steps.size() == n,
               "_fused_adamw_: tensor lists must have the same length");
@@ -510,12 +510,13 @@ void fused_adamw_impl(at::TensorList params, at::TensorList grads, at::TensorLis
   if (found_inf.has_value() && found_inf->defined()) {
     fi = found_inf->to(dev).to(at::kFloat);
   }
-  const int rc = supa_amd_fused_adamw(
+  const auto entry = l2 ? supa_amd_fused_adam : supa_amd_fused_adamw;
+  const int rc = entry(
       (int32_t)n, p.data(), g.data(), m.data(), v.data(), amsgrad ? vm.data() : nullptr, st.data(), numel.data(),
       dtype_code(dt), lr, lr_ptr, beta1, beta2, weight_decay, eps, amsgrad ? 1 : 0, maximize ? 1 : 0,
       gs.defined() ? gs.data_ptr<float>() : nullptr, fi.defined() ? fi.data_ptr<float>() : nullptr,
       current_stream(dev.index()));
-  check_status(rc, "_fused_adamw_");
+  check_status(rc, l2 ? "_fused_adam_" : "_fused_adamw_");
 }
 
 void fused_adamw_(at::TensorList params, at::TensorList grads, at::TensorList exp_avgs, at::TensorList exp_avg_sqs,
@@ -524,6 +525,23 @@ void fused_adamw_(at::TensorList params, at::TensorList grads, at::TensorList ex
                   const std::optional<at::Tensor>& grad_scale, const std::optional<at::Tensor>& found_inf) {
   fused_adamw_impl(params, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs, state_steps, lr, at::Tensor(), beta1,
                    beta2, weight_decay, eps, amsgrad, maximize, grad_scale, found_inf);
+}
+
+// _fused_adam_: the same kernel in Adam mode (weight decay on the gradient)
+void fused_adam_(at::TensorList params, at::TensorList grads, at::TensorList exp_avgs, at::TensorList exp_avg_sqs,
+                 at::TensorList max_exp_avg_sqs, at::TensorList state_steps, double lr, double beta1, double beta2,
+                 double weight_decay, double eps, bool amsgrad, bool maximize,
+                 const std::optional<at::Tensor>& grad_scale, const std::optional<at::Tensor>& found_inf) {
+  fused_adamw_impl(params, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs, state_steps, lr, at::Tensor(), beta1,
+                   beta2, weight_decay, eps, amsgrad, maximize, grad_scale, found_inf, true);
+}
+void fused_adam_tensor_lr_(at::TensorList params, at::TensorList grads, at::TensorList exp_avgs,
+                           at::TensorList exp_avg_sqs, at::TensorList max_exp_avg_sqs, at::TensorList state_steps,
+                           const at::Tensor& lr, double beta1, double beta2, double weight_decay, double eps,
+                           bool amsgrad, bool maximize, const std::optional<at::Tensor>& grad_scale,
+                           const std::optional<at::Tensor>& found_inf) {
+  fused_adamw_impl(params, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs, state_steps, 0.0, lr, beta1, beta2,
+                   weight_decay, eps, amsgrad, maximize, grad_scale, found_inf, true);
 }
 
 void fused_adamw_tensor_lr_(at::TensorList params, at::TensorList grads, at::TensorList exp_avgs,
@@ -665,6 +683,8 @@ TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
   m.impl("linalg_vector_norm", TORCH_FN(vector_norm_supa));
   m.impl("_fused_adamw_", TORCH_FN(fused_adamw_));
   m.impl("_fused_adamw_.tensor_lr", TORCH_FN(fused_adamw_tensor_lr_));
+  m.impl("_fused_adam_", TORCH_FN(fused_adam_));
+  m.impl("_fused_adam_.tensor_lr", TORCH_FN(fused_adam_tensor_lr_));
   m.impl("_amp_foreach_non_finite_check_and_unscale_", TORCH_FN(amp_unscale_));
   m.impl("_amp_update_scale_", TORCH_FN(amp_update_scale_));
 }

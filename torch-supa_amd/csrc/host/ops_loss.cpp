@@ -255,18 +255,22 @@ at::Tensor bce_with_logits(const at::Tensor& self, const at::Tensor& target, con
 }
 
 at::Tensor loss_backward(int loss, const at::Tensor& grad, const at::Tensor& self, const at::Tensor& target,
-                         int64_t reduction, double beta, at::Tensor gi, const char* name) {
+                         int64_t reduction, double beta, at::Tensor gi, const char* name,
+                         const at::Tensor& weight = at::Tensor()) {
   reduction_code(reduction);
   at::native::ResultTypeState rts{};
   for (const at::Tensor* t : {&grad, &self, &target}) rts = at::native::update_result_type_state(*t, rts);
+  if (weight.defined()) rts = at::native::update_result_type_state(weight, rts);
   const c10::ScalarType common = at::native::result_type(rts);
   TORCH_CHECK(is_float_dtype(common), name, ": expected a floating-point input, got ", common);
   int64_t n = 1;
   for (int64_t s : at::infer_size(self.sizes(), target.sizes())) n *= s;
   double norm;
   if (loss == SUPA_AMD_LOSS_MSE) norm = reduction == kMean ? 2.0 / (double)n : 2.0;
+  else if (loss == SUPA_AMD_LOSS_BCE) norm = reduction == kMean ? (double)n : 1.0;  // the divisor
   else norm = reduction == kMean ? 1.0 / (double)n : 1.0;
   std::vector<EwIn> ins{EwIn::of(grad), EwIn::of(self), EwIn::of(target)};
+  if (weight.defined()) ins.push_back(EwIn::of(weight));
   return ew_apply(gi, gi.defined() ? gi.scalar_type() : common, common, ins,
                   [loss, norm, beta](const supa_amd_ew_desc* d, void* s) {
                     return supa_amd_loss_backward(d, loss, norm, beta, s);
@@ -293,6 +297,77 @@ at::Tensor& smooth_l1_loss_backward_out(const at::Tensor& grad, const at::Tensor
   check_beta(beta);
   loss_backward(SUPA_AMD_LOSS_SMOOTH_L1, grad, self, target, reduction, beta, gi,
                 "smooth_l1_loss_backward.grad_input");
+  return gi;
+}
+
+// huber_loss: smooth_l1's shape with delta (upstream huber_kernel_cuda,
+// huber_backward_cuda_kernel)
+void check_delta(double delta) {
+  TORCH_CHECK(delta > 0, "huber_loss does not support non-positive values for delta.");
+}
+at::Tensor huber_loss(const at::Tensor& self, const at::Tensor& target, int64_t reduction, double delta) {
+  check_delta(delta);
+  return loss_forward(SUPA_AMD_LOSS_HUBER, self, target, {}, {}, reduction, delta, {}, "huber_loss");
+}
+at::Tensor& huber_loss_out(const at::Tensor& self, const at::Tensor& target, int64_t reduction, double delta,
+                           at::Tensor& out) {
+  check_delta(delta);
+  loss_forward(SUPA_AMD_LOSS_HUBER, self, target, {}, {}, reduction, delta, out, "huber_loss.out");
+  return out;
+}
+at::Tensor huber_loss_backward(const at::Tensor& grad, const at::Tensor& self, const at::Tensor& target,
+                               int64_t reduction, double delta) {
+  check_delta(delta);
+  return loss_backward(SUPA_AMD_LOSS_HUBER, grad, self, target, reduction, delta, {}, "huber_loss_backward");
+}
+at::Tensor& huber_loss_backward_out(const at::Tensor& grad, const at::Tensor& self, const at::Tensor& target,
+                                    int64_t reduction, double delta, at::Tensor& gi) {
+  check_delta(delta);
+  loss_backward(SUPA_AMD_LOSS_HUBER, grad, self, target, reduction, delta, gi, "huber_loss_backward.out");
+  return gi;
+}
+
+// binary_cross_entropy on probabilities (upstream binary_cross_entropy_out /
+// _backward): the input's values are not checked to lie in [0, 1] (that would
+// need a device-to-host read); outside it the log is NaN.
+void check_bce(const at::Tensor& self, const at::Tensor& target, const std::optional<at::Tensor>& weight) {
+  TORCH_CHECK(self.sizes() == target.sizes(), "Using a target size (", target.sizes(),
+              ") that is different to the input size (", self.sizes(), ") is deprecated. ",
+              "Please ensure they have the same size.");
+  TORCH_CHECK(at::isFloatingType(self.scalar_type()), "binary_cross_entropy is only implemented for floating dtypes");
+  (void)weight;
+}
+at::Tensor bce_weight(const std::optional<at::Tensor>& weight) {
+  return weight.has_value() && weight->defined() ? *weight : at::Tensor();
+}
+at::Tensor binary_cross_entropy(const at::Tensor& self, const at::Tensor& target,
+                                const std::optional<at::Tensor>& weight, int64_t reduction) {
+  check_bce(self, target, weight);
+  at::Tensor out = empty_supa(self.sizes(), self.scalar_type(), self.device().index());
+  if (reduction != kNone) out = at::Tensor();
+  return loss_forward(SUPA_AMD_LOSS_BCE, self, target, {}, bce_weight(weight), reduction, 0.0, out,
+                      "binary_cross_entropy");
+}
+at::Tensor& binary_cross_entropy_out(const at::Tensor& self, const at::Tensor& target,
+                                     const std::optional<at::Tensor>& weight, int64_t reduction, at::Tensor& out) {
+  check_bce(self, target, weight);
+  loss_forward(SUPA_AMD_LOSS_BCE, self, target, {}, bce_weight(weight), reduction, 0.0, out,
+               "binary_cross_entropy.out");
+  return out;
+}
+at::Tensor binary_cross_entropy_backward(const at::Tensor& grad, const at::Tensor& self, const at::Tensor& target,
+                                         const std::optional<at::Tensor>& weight, int64_t reduction) {
+  check_bce(self, target, weight);
+  at::Tensor gi = empty_supa(self.sizes(), self.scalar_type(), self.device().index());
+  return loss_backward(SUPA_AMD_LOSS_BCE, grad, self, target, reduction, 0.0, gi, "binary_cross_entropy_backward",
+                       bce_weight(weight));
+}
+at::Tensor& binary_cross_entropy_backward_out(const at::Tensor& grad, const at::Tensor& self,
+                                              const at::Tensor& target, const std::optional<at::Tensor>& weight,
+                                              int64_t reduction, at::Tensor& gi) {
+  check_bce(self, target, weight);
+  loss_backward(SUPA_AMD_LOSS_BCE, grad, self, target, reduction, 0.0, gi,
+                "binary_cross_entropy_backward.grad_input", bce_weight(weight));
   return gi;
 }
 
@@ -789,6 +864,14 @@ TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
   m.impl("smooth_l1_loss.out", TORCH_FN(smooth_l1_loss_out));
   m.impl("smooth_l1_loss_backward", TORCH_FN(smooth_l1_loss_backward));
   m.impl("smooth_l1_loss_backward.grad_input", TORCH_FN(smooth_l1_loss_backward_out));
+  m.impl("huber_loss", TORCH_FN(huber_loss));
+  m.impl("huber_loss.out", TORCH_FN(huber_loss_out));
+  m.impl("huber_loss_backward", TORCH_FN(huber_loss_backward));
+  m.impl("huber_loss_backward.out", TORCH_FN(huber_loss_backward_out));
+  m.impl("binary_cross_entropy", TORCH_FN(binary_cross_entropy));
+  m.impl("binary_cross_entropy.out", TORCH_FN(binary_cross_entropy_out));
+  m.impl("binary_cross_entropy_backward", TORCH_FN(binary_cross_entropy_backward));
+  m.impl("binary_cross_entropy_backward.grad_input", TORCH_FN(binary_cross_entropy_backward_out));
   m.impl("binary_cross_entropy_with_logits", TORCH_FN(bce_with_logits));
   m.impl("_log_softmax", TORCH_FN(log_softmax));
   m.impl("_log_softmax.out", TORCH_FN(log_softmax_out));

@@ -1,6 +1,7 @@
 // PrivateUse1 registrations of the pointwise math around the loss path:
 // sign / sgn, floor / ceil / round / trunc, rsqrt, the bitwise and logical
-// families, and pow (tensor ** scalar, tensor ** tensor, scalar ** tensor)
+// families, xlogy, and pow (tensor ** scalar, tensor ** tensor, scalar **
+// tensor)
 // -- what losses, normalisations and masks written in plain torch call next
 // to the path's ops (label-smoothed cross-entropy builds its kept-row mask
 // with bitwise_not, RMS-style norms call pow and rsqrt).  Integer pow takes
@@ -276,6 +277,46 @@ at::Tensor& pow_st_out(const c10::Scalar& base, const at::Tensor& e, at::Tensor&
   return out;
 }
 
+// ------------------------------------------------------------- xlogy
+// x * log(y) with 0 where x == 0 (kl_div's target log target); integer
+// results promote to the default float dtype.
+at::Tensor xlogy_into(const EwIn& x, const EwIn& y, c10::ScalarType common, at::Tensor out, bool inplace,
+                      const char* name) {
+  if (at::isIntegralType(common, true)) common = default_float_dtype();
+  TORCH_CHECK(at::isFloatingType(common), name, ": not implemented for '", common, "'");
+  const EwLaunch fn = [](const supa_amd_ew_desc* d, void* s) { return supa_amd_xlogy(d, s); };
+  return apply({x, y}, common, common, out, inplace, fn, name);
+}
+at::Tensor xlogy_t(const at::Tensor& s, const at::Tensor& o) {
+  return xlogy_into(EwIn::of(s), EwIn::of(o), at::result_type(s, o), {}, false, "xlogy.Tensor");
+}
+at::Tensor& xlogy_t_out(const at::Tensor& s, const at::Tensor& o, at::Tensor& out) {
+  xlogy_into(EwIn::of(s), EwIn::of(o), at::result_type(s, o), out, false, "xlogy.OutTensor");
+  return out;
+}
+at::Tensor& xlogy_t_(at::Tensor& s, const at::Tensor& o) {
+  xlogy_into(EwIn::of(s), EwIn::of(o), at::result_type(s, o), {}, true, "xlogy_.Tensor");
+  return s;
+}
+at::Tensor xlogy_so(const at::Tensor& s, const c10::Scalar& o) {
+  return xlogy_into(EwIn::of(s), EwIn::num(o), at::result_type(s, o), {}, false, "xlogy.Scalar_Other");
+}
+at::Tensor& xlogy_so_out(const at::Tensor& s, const c10::Scalar& o, at::Tensor& out) {
+  xlogy_into(EwIn::of(s), EwIn::num(o), at::result_type(s, o), out, false, "xlogy.OutScalar_Other");
+  return out;
+}
+at::Tensor& xlogy_so_(at::Tensor& s, const c10::Scalar& o) {
+  xlogy_into(EwIn::of(s), EwIn::num(o), at::result_type(s, o), {}, true, "xlogy_.Scalar_Other");
+  return s;
+}
+at::Tensor xlogy_ss(const c10::Scalar& s, const at::Tensor& o) {
+  return xlogy_into(EwIn::num(s), EwIn::of(o), at::result_type(s, o), {}, false, "xlogy.Scalar_Self");
+}
+at::Tensor& xlogy_ss_out(const c10::Scalar& s, const at::Tensor& o, at::Tensor& out) {
+  xlogy_into(EwIn::num(s), EwIn::of(o), at::result_type(s, o), out, false, "xlogy.OutScalar_Self");
+  return out;
+}
+
 }  // namespace
 }  // namespace supa
 
@@ -322,4 +363,12 @@ TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
   m.impl("pow_.Tensor", TORCH_FN(pow_tt_));
   m.impl("pow.Scalar", TORCH_FN(pow_st));
   m.impl("pow.Scalar_out", TORCH_FN(pow_st_out));
+  m.impl("xlogy.Tensor", TORCH_FN(xlogy_t));
+  m.impl("xlogy.OutTensor", TORCH_FN(xlogy_t_out));
+  m.impl("xlogy_.Tensor", TORCH_FN(xlogy_t_));
+  m.impl("xlogy.Scalar_Other", TORCH_FN(xlogy_so));
+  m.impl("xlogy.OutScalar_Other", TORCH_FN(xlogy_so_out));
+  m.impl("xlogy_.Scalar_Other", TORCH_FN(xlogy_so_));
+  m.impl("xlogy.Scalar_Self", TORCH_FN(xlogy_ss));
+  m.impl("xlogy.OutScalar_Self", TORCH_FN(xlogy_ss_out));
 }

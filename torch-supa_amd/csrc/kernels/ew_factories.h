@@ -74,6 +74,19 @@ struct SmoothL1BwdFactory {
   }
 };
 
+struct HuberBwdFactory {
+  double norm, delta;
+  template <typename C> static constexpr bool ok() { return std::is_floating_point<C>::value; }
+  template <typename C> HuberBwdOp<C> make() const { return HuberBwdOp<C>{static_cast<C>(norm), static_cast<C>(delta)}; }
+};
+template <bool W>
+struct BceProbBwdFactory {
+  double div;
+  int half;
+  template <typename C> static constexpr bool ok() { return std::is_floating_point<C>::value; }
+  template <typename C> BceProbBwdOp<W, C> make() const { return BceProbBwdOp<W, C>{static_cast<C>(div), half}; }
+};
+
 template <template <typename> class Op, bool FloatOnly = false>
 struct ValueFactory {  // ternary ops with one bound value (addcmul, addcdiv)
   double value;

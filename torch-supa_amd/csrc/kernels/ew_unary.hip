@@ -80,6 +80,10 @@ int supa_amd_pow_scalar(const supa_amd_ew_desc* d, double exponent, void* stream
   return run_ew(PowScalarFactory{mode, half, exponent}, d, stream, 2);
 }
 
+int supa_amd_xlogy(const supa_amd_ew_desc* d, void* stream) {
+  return run_ew(SimpleFactory<XlogyOp, true>{}, d, stream, 3);
+}
+
 int supa_amd_pow(const supa_amd_ew_desc* d, void* stream) {
   return run_ew(SimpleFactory<PowOp, true>{}, d, stream, 3);
 }

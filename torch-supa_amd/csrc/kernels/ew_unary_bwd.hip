@@ -20,6 +20,14 @@ int supa_amd_loss_backward(const supa_amd_ew_desc* d, int loss, double norm, dou
   switch (loss) {
     case SUPA_AMD_LOSS_MSE: return run_ew(MseBwdFactory{norm}, d, stream, 4);
     case SUPA_AMD_LOSS_SMOOTH_L1: return run_ew(SmoothL1BwdFactory{norm, beta}, d, stream, 4);
+    case SUPA_AMD_LOSS_HUBER: return run_ew(HuberBwdFactory{norm, beta}, d, stream, 4);
+    case SUPA_AMD_LOSS_BCE:
+      if (!d) return SUPA_AMD_EINVAL;
+      {
+        const int half = d->common_dtype == SUPA_AMD_BF16 ? 1 : (d->common_dtype == SUPA_AMD_F16 ? 2 : 0);
+        return d->noperands == 5 ? run_ew(BceProbBwdFactory<true>{norm, half}, d, stream, 5)
+                                 : run_ew(BceProbBwdFactory<false>{norm, half}, d, stream, 4);
+      }
     default: return SUPA_AMD_EINVAL;
   }
 }

@@ -29,6 +29,7 @@ struct AdamHyper {
   const float* grad_scale;
   const float* found_inf;
   int amsgrad, maximize;
+  int l2;  // 1: Adam (weight decay added to the gradient), 0: AdamW (decoupled)
 };
 
 // beta^step for integral step counts by square-and-multiply in double (the
@@ -46,7 +47,7 @@ __device__ __forceinline__ double pow_steps(double beta, float step) {
   return r;
 }
 
-// One element of upstream adam_math in ADAMW mode
+// One element of upstream adam_math in ADAMW mode (ORIGINAL mode with h.l2)
 // (torch/include/ATen/native/cuda/fused_adam_utils.cuh:27-93): hyper-parameters
 // in double, state in the storage type's opmath (float), each mixed
 // expression evaluated in double and rounded once.
@@ -61,7 +62,10 @@ __device__ __forceinline__ void adamw_elem(T& pr, T& gr, T& mr, T& vr, T* vmx, c
   if (h.maximize) grad = -grad;
   C ea = (C)to_arith(mr);
   C eas = (C)to_arith(vr);
-  if (h.weight_decay != 0.0) param = (C)fma(-lr_wd, (double)param, (double)param);
+  if (h.weight_decay != 0.0) {
+    if (h.l2) grad = (C)((double)grad + (double)param * h.weight_decay);  // ADAM_MODE::ORIGINAL
+    else param = (C)fma(-lr_wd, (double)param, (double)param);
+  }
   ea = (C)fma(h.beta1, (double)ea, (1.0 - h.beta1) * (double)grad);
   eas = (C)fma(h.beta2, (double)eas, ((1.0 - h.beta2) * (double)grad) * (double)grad);
   C denom;
@@ -250,21 +254,48 @@ int supa_amd_amp_update_scale(float* scale, int32_t* growth_tracker, const float
   return launch_status();
 }
 
-int supa_amd_fused_adamw(int32_t ntensors, void* const* params, void* const* grads, void* const* exp_avgs,
-                         void* const* exp_avg_sqs, void* const* max_exp_avg_sqs, void* const* state_steps,
-                         const int64_t* numel, int32_t dtype, double lr, const float* lr_ptr, double beta1,
-                         double beta2, double weight_decay, double eps, int amsgrad, int maximize,
-                         const float* grad_scale, const float* found_inf, void* stream) {
+}  // extern "C"
+
+namespace {
+int fused_adam_any(int l2, int32_t ntensors, void* const* params, void* const* grads, void* const* exp_avgs,
+                   void* const* exp_avg_sqs, void* const* max_exp_avg_sqs, void* const* state_steps,
+                   const int64_t* numel, int32_t dtype, double lr, const float* lr_ptr, double beta1, double beta2,
+                   double weight_decay, double eps, int amsgrad, int maximize, const float* grad_scale,
+                   const float* found_inf, void* stream) {
   if (ntensors < 0) return SUPA_AMD_EINVAL;
   if (ntensors > 0 && (!params || !grads || !exp_avgs || !exp_avg_sqs || !state_steps || !numel)) return SUPA_AMD_EINVAL;
   if (amsgrad && ntensors > 0 && !max_exp_avg_sqs) return SUPA_AMD_EINVAL;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const AdamHyper h{lr, beta1, beta2, weight_decay, eps, lr_ptr, grad_scale, found_inf, amsgrad ? 1 : 0, maximize ? 1 : 0};
+  const AdamHyper h{lr,        beta1,      beta2,     weight_decay,          eps, lr_ptr,
+                    grad_scale, found_inf, amsgrad ? 1 : 0, maximize ? 1 : 0, l2};
   return with_mta_storage(dtype, [&](auto* tag) -> int {
     using T = std::remove_pointer_t<decltype(tag)>;
     return launch_adamw<T, chunk_one<T>(), 1>(ntensors, params, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs, state_steps, numel,
                                    h, st);
   });
+}
+}  // namespace
+
+extern "C" {
+
+int supa_amd_fused_adamw(int32_t ntensors, void* const* params, void* const* grads, void* const* exp_avgs,
+                         void* const* exp_avg_sqs, void* const* max_exp_avg_sqs, void* const* state_steps,
+                         const int64_t* numel, int32_t dtype, double lr, const float* lr_ptr, double beta1,
+                         double beta2, double weight_decay, double eps, int amsgrad, int maximize,
+                         const float* grad_scale, const float* found_inf, void* stream) {
+  return fused_adam_any(0, ntensors, params, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs, state_steps, numel,
+                        dtype, lr, lr_ptr, beta1, beta2, weight_decay, eps, amsgrad, maximize, grad_scale, found_inf,
+                        stream);
+}
+
+int supa_amd_fused_adam(int32_t ntensors, void* const* params, void* const* grads, void* const* exp_avgs,
+                        void* const* exp_avg_sqs, void* const* max_exp_avg_sqs, void* const* state_steps,
+                        const int64_t* numel, int32_t dtype, double lr, const float* lr_ptr, double beta1,
+                        double beta2, double weight_decay, double eps, int amsgrad, int maximize,
+                        const float* grad_scale, const float* found_inf, void* stream) {
+  return fused_adam_any(1, ntensors, params, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs, state_steps, numel,
+                        dtype, lr, lr_ptr, beta1, beta2, weight_decay, eps, amsgrad, maximize, grad_scale, found_inf,
+                        stream);
 }
 
 }  // extern "C"

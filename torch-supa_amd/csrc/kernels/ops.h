@@ -555,6 +555,83 @@ template <typename C> struct MseBwdOp {
   __device__ __forceinline__ C operator()(const C* v) const { return ((v[1] - v[2]) * norm) * v[0]; }
 };
 // smooth_l1 backward (inputs g, x, t)
+// huber (upstream huber_kernel_cuda): z = |a - b|; 0.5 z z below delta,
+// delta (z - 0.5 delta) above.
+template <typename C> struct HuberTermOp {
+  static constexpr int arity = 2;
+  C delta;
+  __device__ __forceinline__ C operator()(const C* v) const {
+    const C z = fabs(v[0] - v[1]);
+    return z < delta ? (C(0.5) * z) * z : delta * (z - C(0.5) * delta);
+  }
+};
+// huber backward (upstream huber_backward_cuda_kernel), v = {grad, input, target}.
+template <typename C> struct HuberBwdOp {
+  static constexpr int arity = 3;
+  C norm, delta;
+  __device__ __forceinline__ C operator()(const C* v) const {
+    const C g = v[0], x = v[1] - v[2];
+    if (x < -delta) return ((-norm) * g) * delta;
+    if (x > delta) return (norm * g) * delta;
+    return (norm * x) * g;
+  }
+};
+// binary_cross_entropy on probabilities (upstream binary_cross_entropy_out
+// kernel): (t - 1) max(log1p(-x), -100) - t max(log(x), -100), times the
+// weight as a second op; v = {x, t[, w]}.  std::max keeps a NaN log.  For a
+// 16-bit storage type (`half` 1 = bf16, 2 = f16) every intermediate is
+// rounded to it, as the upstream kernel computes in scalar_t.
+template <typename C> __device__ __forceinline__ C round_half(C v, int half) {
+  if constexpr (std::is_same<C, float>::value) {
+    if (half == 1) return to_arith(from_arith<bf16>(v));
+    if (half == 2) return to_arith(from_arith<f16>(v));
+  }
+  return v;
+}
+template <bool W, typename C> struct BceProbTermOp {
+  static constexpr int arity = W ? 3 : 2;
+  int half;
+  __device__ __forceinline__ static C keep_max(C a, C b) { return a < b ? b : a; }
+  __device__ __forceinline__ C operator()(const C* v) const {
+    const C x = v[0], t = v[1];
+    const C lx = keep_max(round_half(logx<C>(x), half), C(-100));
+    const C l1mx = keep_max(round_half(log1px<C>(-x), half), C(-100));
+    const C a = round_half((round_half(t - C(1), half)) * l1mx, half);
+    const C b = round_half(t * lx, half);
+    C r = a - b;
+    if constexpr (W) r = round_half(r, half) * v[2];
+    return r;
+  }
+};
+// its gradient (upstream binary_cross_entropy_backward): g (x - t) /
+// max((1 - x) x, 1e-12), then times the weight, then / n for a mean;
+// v = {grad, x, t[, w]}, div = n for MEAN else 1; intermediates rounded to a
+// 16-bit storage type as in the forward.
+template <bool W, typename C> struct BceProbBwdOp {
+  static constexpr int arity = W ? 4 : 3;
+  C div;
+  int half;
+  __device__ __forceinline__ C operator()(const C* v) const {
+    const C g = v[0], x = v[1], t = v[2];
+    const C d0 = round_half(round_half(C(1) - x, half) * x, half);
+    const C eps = round_half(C(1e-12), half);
+    const C den = d0 < eps ? eps : d0;
+    C r = round_half(round_half(g * round_half(x - t, half), half) / den, half);
+    if constexpr (W) r = round_half(r * v[3], half);
+    return r / div;
+  }
+};
+// xlogy (upstream xlogy_kernel_cuda): NaN for a NaN y, 0 for x == 0, x log y.
+template <typename C> struct XlogyOp {
+  static constexpr int arity = 2;
+  __device__ __forceinline__ C operator()(const C* v) const {
+    const C x = v[0], y = v[1];
+    if (y != y) return y;
+    if (x == C(0)) return C(0);
+    return x * logx<C>(y);
+  }
+};
+
 template <typename C> struct SmoothL1BwdOp {
   static constexpr int arity = 3;
   C norm, beta;

@@ -343,6 +343,23 @@ struct BceTermFactory {
   template <typename C> BceTermOp<PW, W, C, HW> make() const { return BceTermOp<PW, W, C, HW>{}; }
   template <typename C> static constexpr bool ok() { return std::is_floating_point<C>::value; }
 };
+// 1 / 2 when the common dtype is bf16 / f16 (terms rounded in that type)
+inline int half_code(const supa_amd_ew_desc* d) {
+  return d->common_dtype == SUPA_AMD_BF16 ? 1 : (d->common_dtype == SUPA_AMD_F16 ? 2 : 0);
+}
+struct HuberTermFactory {
+  static constexpr bool kIntegers = false;
+  double delta;
+  template <typename C> static constexpr bool ok() { return std::is_floating_point<C>::value; }
+  template <typename C> HuberTermOp<C> make() const { return HuberTermOp<C>{static_cast<C>(delta)}; }
+};
+template <bool W>
+struct BceProbTermFactory {
+  static constexpr bool kIntegers = false;
+  int half;
+  template <typename C> static constexpr bool ok() { return std::is_floating_point<C>::value; }
+  template <typename C> BceProbTermOp<W, C> make() const { return BceProbTermOp<W, C>{half}; }
+};
 struct MseTermEwFactory {
   static constexpr bool kIntegers = false;
   template <typename C> static constexpr bool ok() { return std::is_floating_point<C>::value; }
@@ -429,9 +446,14 @@ int supa_amd_sum_rows(const void* in, int32_t in_dtype, void* out, int32_t out_d
 int supa_amd_loss_forward(const supa_amd_ew_desc* d, int loss, int reduction, double beta, int has_pos_weight,
                           int has_weight, void* out_scalar, void* workspace, int64_t workspace_bytes, void* stream) {
   if (!d) return SUPA_AMD_EINVAL;
-  if (loss != SUPA_AMD_LOSS_BCE_LOGITS && (has_pos_weight || has_weight)) return SUPA_AMD_EINVAL;
+  if (loss != SUPA_AMD_LOSS_BCE_LOGITS && has_pos_weight) return SUPA_AMD_EINVAL;
+  if (loss != SUPA_AMD_LOSS_BCE_LOGITS && loss != SUPA_AMD_LOSS_BCE && has_weight) return SUPA_AMD_EINVAL;
   if (reduction == SUPA_AMD_REDUCTION_NONE) {
     switch (loss) {
+      case SUPA_AMD_LOSS_HUBER: return run_ew(HuberTermFactory{beta}, d, stream, 3);
+      case SUPA_AMD_LOSS_BCE:
+        return has_weight ? run_ew(BceProbTermFactory<true>{half_code(d)}, d, stream, 4)
+                          : run_ew(BceProbTermFactory<false>{half_code(d)}, d, stream, 3);
       case SUPA_AMD_LOSS_MSE: return run_ew(MseTermEwFactory{}, d, stream, 3);
       case SUPA_AMD_LOSS_SMOOTH_L1: return run_ew(SmoothL1TermEwFactory{beta}, d, stream, 3);
       case SUPA_AMD_LOSS_BCE_LOGITS:
@@ -450,6 +472,11 @@ int supa_amd_loss_forward(const supa_amd_ew_desc* d, int loss, int reduction, do
   supa_amd_ew_desc e = *d;
   e.op[0].data = out_scalar;
   switch (loss) {
+    case SUPA_AMD_LOSS_HUBER: return run_reduce(HuberTermFactory{beta}, &e, scale, workspace, workspace_bytes, stream);
+    case SUPA_AMD_LOSS_BCE:
+      return has_weight
+                 ? run_reduce(BceProbTermFactory<true>{half_code(d)}, &e, scale, workspace, workspace_bytes, stream)
+                 : run_reduce(BceProbTermFactory<false>{half_code(d)}, &e, scale, workspace, workspace_bytes, stream);
     case SUPA_AMD_LOSS_MSE: return run_reduce(MseTermFactory{}, &e, scale, workspace, workspace_bytes, stream);
     case SUPA_AMD_LOSS_SMOOTH_L1:
       return run_reduce(SmoothL1TermFactory{beta}, &e, scale, workspace, workspace_bytes, stream);
