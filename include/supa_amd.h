@@ -568,6 +568,22 @@ int supa_amd_fused_adamw(int32_t ntensors, void* const* params, void* const* gra
                          int amsgrad, int maximize, const float* grad_scale,
                          const float* found_inf, void* stream);
 
+/* ----------------------------------------------- max / min with index */
+/* For each of `outer` rows of a contiguous input with `inner` elements, and
+ * each chunk of `chunk` elements of the row (chunk = inner: one per row), the
+ * extremal element: a NaN beats every number, equal values (and NaNs) go to
+ * the smaller index, otherwise the larger (is_min = 0) or smaller value.
+ * Writes the value (out_val, the input dtype; may be NULL) and its index
+ * (out_idx, int64; may be NULL) at [row * nchunks + chunk].  The index is the
+ * position in the row, or in_idx[row * inner + j] when in_idx is given (the
+ * second launch over chunk winners).  Any dtype but complex.  Replaces
+ * amax.out NF:3926, amin.out NF:4115, max.dim_max NF:3894, min.dim_min
+ * NF:4091, argmax.out NF:839, argmin.out NF:852, max.unary_out NF:10274,
+ * min.unary_out NF:10204. */
+int supa_amd_argext_rows(const void* in, int32_t dtype, const int64_t* in_idx, int64_t outer,
+                         int64_t inner, int64_t chunk, int is_min, void* out_val,
+                         int64_t* out_idx, void* stream);
+
 /* Fused Adam (weight decay added to the gradient, upstream adam_math's
  * ADAM_MODE::ORIGINAL: grad += param * weight_decay after the maximize
  * negation); otherwise as supa_amd_fused_adamw.  Replaces _fused_adam_
