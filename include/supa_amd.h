@@ -268,10 +268,16 @@ int supa_amd_mask_scale(const supa_amd_ew_desc* d, double scale, void* stream);
  *   bernoulli: out = u < p ? 1 : 0              bernoulli_.float NF:1146
  *   dropout:   mask = u < keep, out = (x * mask) * (1 / keep)
  *                                               native_dropout NF:286
+ *   normal:    Box-Muller in double on word pairs (0,1) and (2,3) of each
+ *              Philox call: r = sqrt(-2 log u1), u1 = (hi24 + 1) 2^-24,
+ *              t = 2 pi u2; elements r cos t, r sin t; out = mean + std z
+ *                                               normal_ NF:10552
  * (The reference draws through curand's Philox; the streams differ.) */
 int supa_amd_uniform(void* out, int32_t dtype, int64_t n, double lo, double hi, uint64_t seed, uint64_t offset,
                      void* stream);
 int supa_amd_bernoulli(void* out, int32_t dtype, int64_t n, double p, uint64_t seed, uint64_t offset, void* stream);
+int supa_amd_normal(void* out, int32_t dtype, int64_t n, double mean, double stdv, uint64_t seed, uint64_t offset,
+                    void* stream);
 int supa_amd_dropout(const void* x, int32_t dtype, void* out, uint8_t* mask, int64_t n, double keep, uint64_t seed,
                      uint64_t offset, void* stream);
 

@@ -70,6 +70,7 @@ def lib():
             "or_philox4x32_10": (None, [_u32p, _u32p, _u32p]),
             "or_rng_u32": (None, [ctypes.c_uint64, ctypes.c_uint64, i64, _u32p]),
             "or_uniform_f32": (None, [ctypes.c_uint64, ctypes.c_uint64, i64, c_float, c_float, _u32p, _f32p]),
+            "or_normal_f32": (None, [ctypes.c_uint64, ctypes.c_uint64, i64, c_double, c_double, _f32p]),
             "or_dropout_f32": (None, [ctypes.c_uint64, ctypes.c_uint64, i64, _f32p, c_float, _u32p, _f32p,
                                       ctypes.POINTER(ctypes.c_uint8)]),
             "or_softmax_bwd": (None, [_f32p, _f32p, _f32p, i64, i64]),
@@ -424,6 +425,12 @@ def uniform(seed: int, offset: int, n: int, lo=0.0, hi=1.0) -> np.ndarray:
     scratch = np.empty(n, np.uint32)
     out = np.empty(n, np.float32)
     lib().or_uniform_f32(seed, offset, n, lo, hi, _p(scratch, _u32p), _p(out, _f32p))
+    return out
+
+
+def normal(seed: int, offset: int, n: int, mean=0.0, std=1.0) -> np.ndarray:
+    out = np.empty(n, np.float32)
+    lib().or_normal_f32(seed, offset, n, mean, std, _p(out, _f32p))
     return out
 
 

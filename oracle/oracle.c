@@ -752,6 +752,30 @@ void or_uniform_f32(uint64_t seed, uint64_t offset, int64_t n, float lo, float h
   for (int64_t i = 0; i < n; ++i) out[i] = fmaf(or_u01(scratch[i]), range, lo);
 }
 
+/* normal_(mean, std): Box-Muller in double on the word pairs (0, 1) and
+ * (2, 3) of each Philox call; u1 = (hi24 + 1) 2^-24 in (0, 1], u2 = hi24
+ * 2^-24; r = sqrt(-2 log u1), t = 2 pi u2; z = r cos t, r sin t;
+ * out = (float)(mean + std z).  (The device evaluates sin / cos as
+ * sincospi(2 u2); the two differ by rounding far below float precision.) */
+void or_normal_f32(uint64_t seed, uint64_t offset, int64_t n, double mean, double stdv, float* out) {
+  const double pi = 3.14159265358979323846;
+  const uint32_t key[2] = {(uint32_t)seed, (uint32_t)(seed >> 32)};
+  for (int64_t q = 0; q * 4 < n; ++q) {
+    const uint32_t ctr[4] = {(uint32_t)q, (uint32_t)((uint64_t)q >> 32), (uint32_t)offset, (uint32_t)(offset >> 32)};
+    uint32_t r[4];
+    or_philox4x32_10(ctr, key, r);
+    double z[4];
+    for (int h = 0; h < 2; ++h) {
+      const double u1 = ((double)(r[2 * h] >> 8) + 1.0) * 5.9604644775390625e-08;
+      const double u2 = (double)(r[2 * h + 1] >> 8) * 5.9604644775390625e-08;
+      const double rr = sqrt(-2.0 * log(u1));
+      z[2 * h] = rr * cos(2.0 * pi * u2);
+      z[2 * h + 1] = rr * sin(2.0 * pi * u2);
+    }
+    for (int j = 0; j < 4 && q * 4 + j < n; ++j) out[q * 4 + j] = (float)(mean + stdv * z[j]);
+  }
+}
+
 /* dropout with keep probability q: mask = u < q; out = (x * mask) * scale,
  * scale = 1.0 / q divided in double and rounded to float (upstream
  * Dropout.cu fused_dropout_kernel: accscalar_t scale = 1.0 / p). */

@@ -9,6 +9,7 @@ import torch
 import torch.nn.functional as F
 
 import oracle as O
+from helpers import f32_ulp_dist
 
 pytestmark = pytest.mark.gpu
 
@@ -149,3 +150,34 @@ def test_moments_at_full_size(no_fallback):
     seed, off = 12, 0
     r = O.rng_u32(seed, off, n)[-5:]
     assert np.array_equal(tail, (r >> 8).astype(np.float32) * np.float32(2.0 ** -24))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_normal_against_oracle(dtype, no_fallback):
+    torch.supa.manual_seed(51)
+    t = torch.empty(100003, dtype=dtype, device="supa")
+    seed, off = state()
+    t.normal_(1.5, 0.25)
+    assert state() == (seed, off + 1)
+    want = O.normal(seed, off, t.numel(), 1.5, 0.25)
+    got = t.cpu().float().numpy()
+    if dtype == torch.float32:
+        # double sin / cos / log on the device and on the host: equal after rounding to float
+        # but for the rare value within a double rounding of a float midpoint
+        assert (f32_ulp_dist(got, want) > 1).sum() == 0
+        assert (got != want).mean() < 1e-3
+    else:
+        assert torch.equal(t.cpu(), torch.from_numpy(want).to(dtype)) or \
+            (t.cpu() != torch.from_numpy(want).to(dtype)).float().mean().item() < 1e-3
+
+
+def test_randn_like_and_moments(no_fallback):
+    torch.supa.manual_seed(52)
+    x = torch.randn(1 << 24, device="supa")
+    assert abs(x.mean().item()) < 2e-3
+    c = x - x.mean()
+    assert abs((c * c).mean().item() - 1.0) < 2e-3
+    y = torch.randn_like(x)
+    assert not torch.equal(x.cpu()[:100], y.cpu()[:100])
+    torch.supa.manual_seed(52)
+    assert torch.equal(torch.randn(1 << 24, device="supa").cpu()[:1000], x.cpu()[:1000])

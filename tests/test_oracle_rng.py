@@ -61,3 +61,21 @@ def test_dropout(keep):
     assert abs(mask.mean() - keep) < 5 * np.sqrt(keep * (1 - keep) / n) + 1e-9
     if keep == 1.0:
         assert mask.all() and np.array_equal(out, x)
+
+
+def test_normal_moments_and_pairs():
+    """Box-Muller pairs: z0^2 + z1^2 = -2 log u1 and atan2(z1, z0) = 2 pi u2
+    for the words the stream layout assigns; moments of N(0, 1)."""
+    n = 1 << 20
+    z = O.normal(21, 4, n).astype(np.float64)
+    r = O.rng_u32(21, 4, n)
+    u1 = ((r[0::2] >> 8).astype(np.float64) + 1) * 2.0 ** -24
+    u2 = (r[1::2] >> 8).astype(np.float64) * 2.0 ** -24
+    np.testing.assert_allclose(z[0::2] ** 2 + z[1::2] ** 2, -2 * np.log(u1), rtol=1e-6, atol=1e-6)
+    ang = np.mod(np.arctan2(z[1::2], z[0::2]), 2 * np.pi)
+    d = np.abs(ang - 2 * np.pi * u2)
+    assert np.minimum(d, 2 * np.pi - d).max() < 1e-5
+    assert abs(z.mean()) < 5e-3 and abs(z.var() - 1) < 5e-3
+    assert abs(((z - z.mean()) ** 3).mean()) < 1e-2 and abs((z ** 4).mean() - 3) < 3e-2
+    w = O.normal(21, 4, 1000, mean=2.0, std=0.5)
+    np.testing.assert_allclose(w, (2.0 + 0.5 * z[:1000]).astype(np.float32), rtol=1e-6, atol=1e-6)

@@ -1,10 +1,12 @@
 // PrivateUse1 registrations of the random ops beside the activation path:
-// uniform_, bernoulli_.float and native_dropout / native_dropout_backward
+// uniform_, normal_ (what randn / randn_like run), bernoulli_.float and
+// native_dropout / native_dropout_backward
 // (what F.dropout runs on this device), on the Philox kernels with the
 // device generator's (seed, offset).  Other dtypes and the other random ops
 // take the counted CPU fallback.
 #include <ATen/native/CPUFallback.h>
 #include <ATen/ops/bernoulli_ops.h>
+#include <ATen/ops/normal_ops.h>
 #include <ATen/ops/uniform_ops.h>
 #include <torch/library.h>
 
@@ -38,6 +40,21 @@ at::Tensor& uniform_(at::Tensor& self, double from, double to, std::optional<at:
     check_status(supa_amd_uniform(t.data_ptr(), dtype_code(t.scalar_type()), t.numel(), from, to, seed, offset,
                                   current_stream(dev)),
                  "uniform_");
+  });
+  return self;
+}
+
+at::Tensor& normal_(at::Tensor& self, double mean, double stdv, std::optional<at::Generator> gen) {
+  if (!rng_dtype(self.scalar_type()))
+    return at::native::call_fallback_fn<&supa_cpu_fallback, at::_ops::normal_>::call(self, mean, stdv, gen);
+  TORCH_CHECK(stdv >= 0.0, "normal expects std >= 0.0, but found std ", stdv);
+  if (self.numel() == 0) return self;
+  const auto dev = self.device().index();
+  const auto [seed, offset] = philox_inputs(gen, dev);
+  fill_dense(self, [&](at::Tensor& t) {
+    check_status(supa_amd_normal(t.data_ptr(), dtype_code(t.scalar_type()), t.numel(), mean, stdv, seed, offset,
+                                 current_stream(dev)),
+                 "normal_");
   });
   return self;
 }
@@ -92,6 +109,7 @@ at::Tensor native_dropout_backward(const at::Tensor& grad, const at::Tensor& mas
 TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
   using namespace supa;
   m.impl("uniform_", TORCH_FN(uniform_));
+  m.impl("normal_", TORCH_FN(normal_));
   m.impl("bernoulli_.float", TORCH_FN(bernoulli_float_));
   m.impl("native_dropout", TORCH_FN(native_dropout));
   m.impl("native_dropout_backward", TORCH_FN(native_dropout_backward));

@@ -1,5 +1,5 @@
-// Counter-based random numbers: uniform_, bernoulli_ and the fused dropout
-// forward (native_dropout) on Philox4x32-10 (Salmon et al., SC 2011).
+// Counter-based random numbers: uniform_, normal_, bernoulli_ and the fused
+// dropout forward (native_dropout) on Philox4x32-10 (Salmon et al., SC 2011).
 //
 // Element i draws word i % 4 of philox(counter = (i / 4, offset), key =
 // seed), so every element's value depends only on (seed, offset, i): the
@@ -60,6 +60,33 @@ k_rng_fill(T* __restrict__ out, int64_t n, uint64_t seed, uint64_t offset, float
   } else {
     for (int j = 0; j < 4 && e0 + j < n; ++j) out[e0 + j] = from_arith<T>(v[j]);
   }
+}
+
+// normal(mean, std): Box-Muller on two words per pair of outputs, in double
+// (u1 = (hi24(w) + 1) 2^-24 in (0, 1], u2 = hi24(w') 2^-24): elements 4q + 0,1
+// are r cos(t), r sin(t) of words 0, 1, elements 4q + 2,3 of words 2, 3, with
+// r = sqrt(-2 log u1), t = 2 pi u2; out = mean + std z rounded once.
+__device__ __forceinline__ void box_muller(uint32_t w1, uint32_t w2, double& z0, double& z1) {
+  const double u1 = ((double)(w1 >> 8) + 1.0) * 5.9604644775390625e-08;
+  const double u2 = (double)(w2 >> 8) * 5.9604644775390625e-08;
+  const double r = sqrt(-2.0 * log(u1));
+  double sn, cs;
+  sincospi(2.0 * u2, &sn, &cs);
+  z0 = r * cs;
+  z1 = r * sn;
+}
+
+template <typename T>
+__global__ void __launch_bounds__(kBlock)
+k_rng_normal(T* __restrict__ out, int64_t n, uint64_t seed, uint64_t offset, double mean, double stdv) {
+  const uint64_t q = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
+  const int64_t e0 = (int64_t)q * 4;
+  if (e0 >= n) return;
+  const uint4 r = draw4(q, seed, offset);
+  double z[4];
+  box_muller(r.x, r.y, z[0], z[1]);
+  box_muller(r.z, r.w, z[2], z[3]);
+  for (int j = 0; j < 4 && e0 + j < n; ++j) out[e0 + j] = from_arith<T>((float)(mean + stdv * z[j]));
 }
 
 // dropout with keep probability q: mask = u < q, out = (x * mask) * scale.
@@ -135,6 +162,19 @@ int supa_amd_bernoulli(void* out, int32_t dtype, int64_t n, double p, uint64_t s
   return with_rng_storage(dtype, [&](auto* tag) -> int {
     using T = std::remove_pointer_t<decltype(tag)>;
     k_rng_fill<T, 1><<<rng_blocks(n), kBlock, 0, st>>>(static_cast<T*>(out), n, seed, offset, (float)p, 0.0f);
+    return launch_status();
+  });
+}
+
+int supa_amd_normal(void* out, int32_t dtype, int64_t n, double mean, double stdv, uint64_t seed, uint64_t offset,
+                    void* stream) {
+  if (n < 0 || (n > 0 && !out) || !(stdv >= 0.0)) return SUPA_AMD_EINVAL;
+  if ((n + 3) / 4 > (int64_t)kBlock * 0x7fffffffll) return SUPA_AMD_ELAYOUT;
+  if (n == 0) return SUPA_AMD_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return with_rng_storage(dtype, [&](auto* tag) -> int {
+    using T = std::remove_pointer_t<decltype(tag)>;
+    k_rng_normal<T><<<rng_blocks(n), kBlock, 0, st>>>(static_cast<T*>(out), n, seed, offset, mean, stdv);
     return launch_status();
   });
 }
