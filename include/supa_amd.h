@@ -540,6 +540,36 @@ int supa_amd_foreach_norm(int32_t ntensors, const void* const* x, const int64_t*
                           double ord, void* out, int32_t out_dtype, void* workspace, int64_t ws_bytes,
                           void* stream);
 
+/* Vector norm of each row of a contiguous [outer, inner] input (f32 / bf16 /
+ * f16 / f64; inner >= 1) into out[outer] (the input dtype, or f32), for
+ * every order: 0 (count of non-zeros), 1, 2, +inf / -inf (largest /
+ * smallest |x|, NaN propagating), any other finite p (sum |x|^p, then
+ * ^(1/p)); accumulated in f32 (f64 for f64).  Long rows with few of them
+ * reduce in two launches through a workspace of
+ * supa_amd_norm_rows_workspace_bytes (0: none needed).  The caller moves
+ * the reduced dims last.  Replaces linalg_vector_norm.out NF:14470 over
+ * dims (upstream ReduceNormKernel.cu: NormZeroOps / NormOneOps /
+ * NormTwoOps / AbsMaxOps / AbsMinOps / NormOps). */
+int64_t supa_amd_norm_rows_workspace_bytes(int64_t outer, int64_t inner, int32_t dtype);
+int supa_amd_norm_rows(const void* in, int32_t dtype, void* out, int32_t out_dtype, int64_t outer, int64_t inner,
+                       double ord, void* workspace, int64_t ws_bytes, void* stream);
+
+/* Variance (take_sqrt 0) or standard deviation (1) of each row of a
+ * contiguous [outer, inner] input (f32 / bf16 / f16 / f64; inner >= 1) into
+ * out_var[outer], and the row mean into out_mean[outer] when it is not NULL,
+ * both in the input dtype: Welford's (count, mean, M2) accumulated in f32
+ * (f64 for f64), var = M2 / max(0, count - correction).  Long rows with few
+ * of them reduce in two launches through a workspace of
+ * supa_amd_moments_rows_workspace_bytes (0: none needed).  The caller moves
+ * the reduced dims last.  Replaces var.correction_out NF:6629,
+ * std.correction_out NF:6088, var_mean.correction NF:6668,
+ * std_mean.correction NF:6063 (upstream ReduceMomentKernel.cu over
+ * WelfordOps). */
+int64_t supa_amd_moments_rows_workspace_bytes(int64_t outer, int64_t inner, int32_t dtype);
+int supa_amd_moments_rows(const void* in, int32_t dtype, int64_t outer, int64_t inner, double correction,
+                          int take_sqrt, void* out_var, void* out_mean, void* workspace, int64_t ws_bytes,
+                          void* stream);
+
 /* Mixed-precision gradient unscale: every element of the `ntensors`
  * contiguous tensors (f32 / bf16 / f16 / f64) is multiplied in place by
  * *inv_scale (left as is when that is exactly 1), and *found_inf (device

@@ -389,21 +389,48 @@ def adamw_step(p, g, m, v, step, lr, beta1, beta2, weight_decay, eps, maximize=F
 
 
 def vector_norm(x, ord=2.0) -> float:
-    """||x||_ord for ord 1, 2 or inf, accumulated in float64: the quantity
-    upstream's _foreach_norm (ForeachReduceOp.cu) and linalg_vector_norm
-    (ReduceNormKernel) estimate in float.  A NaN anywhere gives NaN and an
-    empty x gives 0."""
+    """||x||_ord accumulated in float64: the quantity upstream's _foreach_norm
+    (ForeachReduceOp.cu) and linalg_vector_norm (ReduceNormKernel.cu's
+    NormZeroOps / NormOneOps / NormTwoOps / AbsMaxOps / AbsMinOps / NormOps)
+    estimate in float.  ord 0 counts the non-zeros (a NaN counts), +-inf is
+    the largest / smallest |x|, any other p is (sum |x|^p)^(1/p).  A NaN
+    gives NaN (except ord 0) and an empty x gives 0 (_foreach_norm's value;
+    linalg_vector_norm raises instead for a negative or infinite order)."""
     x = np.asarray(x, dtype=np.float64).ravel()
     if x.size == 0:
         return 0.0
     a = np.abs(x)
+    if ord == 0:
+        return float(np.count_nonzero(x))
+    if np.isnan(a).any():
+        return float("nan")
     if ord == 1:
         return float(a.sum())
     if ord == 2:
         return float(np.sqrt((a * a).sum()))
     if ord == float("inf"):
-        return float("nan") if np.isnan(a).any() else float(a.max())
-    raise ValueError(f"ord {ord} not supported")
+        return float(a.max())
+    if ord == float("-inf"):
+        return float(a.min())
+    with np.errstate(divide="ignore", over="ignore"):
+        return float(np.power(np.power(a, ord).sum(), 1.0 / ord))
+
+
+def moments(x, correction=1.0):
+    """(variance, mean) of x in float64, the quantities upstream's var / std
+    / var_mean / std_mean (ReduceMomentKernel.cu over WelfordOps in
+    SharedReduceOps.h) estimate in float: the two-pass sum of squared
+    deviations over max(0, n - correction).  n <= correction divides by
+    zero (inf, or NaN for a zero sum); an empty x gives NaN, NaN."""
+    x = np.asarray(x, dtype=np.float64).ravel()
+    n = x.size
+    if n == 0:
+        return float("nan"), float("nan")
+    mean = x.sum() / n
+    m2 = ((x - mean) ** 2).sum()
+    div = n - correction if n > correction else 0.0
+    with np.errstate(divide="ignore", invalid="ignore"):
+        return float(np.float64(m2) / np.float64(div)), float(mean)
 
 
 # ------------------------------------------------------------ random numbers

@@ -280,13 +280,76 @@ def test_linalg_vector_norm(no_fallback):
     assert torch.linalg.vector_norm(torch.zeros(0, device="supa")).item() == 0.0
 
 
-def test_linalg_vector_norm_other_cases_use_counted_fallback(supa):
-    """A reduction over some dims is not on the path: the CPU fallback runs
-    it, and counts it."""
-    x = torch.randn(40, 30)
+NORM_ORDS = [0.0, 1.0, 2.0, math.inf, -math.inf, 3.0, 0.5, -1.5]
+
+
+@pytest.mark.parametrize("p", NORM_ORDS)
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float64])
+def test_linalg_vector_norm_over_dims(p, dtype, no_fallback):
+    """Norms over one dim, several dims and every element, each order the
+    row-norm kernel knows: each row against the float64 oracle (rtol 1e-5;
+    1e-2 for a bf16 result) and the layout against upstream CPU."""
+    g = torch.Generator().manual_seed(int(abs(p) * 10) % 97 if math.isfinite(p) else 5)
+    x = torch.randn(6, 37, 129, generator=g).to(dtype)
+    x[1, 3, 7] = 0.0
+    dx = x.to("supa")
+    rtol = 1e-2 if dtype == torch.bfloat16 else 1e-5
+    for dim, keepdim in [(-1, False), (0, True), ((0, 2), False), (None, False), ((2, 1, 0), True)]:
+        got = torch.linalg.vector_norm(dx, p, dim=dim, keepdim=keepdim)
+        want = torch.linalg.vector_norm(x.double(), p, dim=dim, keepdim=keepdim)
+        assert got.shape == want.shape and got.dtype == dtype
+        dims = tuple(range(3)) if dim is None else ((dim,) if isinstance(dim, int) else dim)
+        dims = tuple(d % 3 for d in dims)
+        keep = [d for d in range(3) if d not in dims]
+        rows = x.double().permute(keep + list(dims)).reshape(-1, int(np.prod([x.shape[d] for d in dims])))
+        ref = np.array([O.vector_norm(r.numpy(), p) for r in rows]).reshape(
+            [x.shape[d] for d in keep] or [])
+        np.testing.assert_allclose(got.double().cpu().reshape(ref.shape).numpy(), ref, rtol=rtol)
+        torch.testing.assert_close(got.double().cpu(), want, rtol=rtol, atol=0)
+
+
+@pytest.mark.parametrize("p", [2.0, math.inf, -math.inf, 0.0, 1.5])
+def test_linalg_vector_norm_long_rows_two_launches(p, no_fallback):
+    """Rows over 65536 elements (few of them) reduce per 16384-element chunk,
+    then over the chunk partials; a ragged last chunk and a NaN row too."""
+    g = torch.Generator().manual_seed(77)
+    x = torch.randn(3, 200003, generator=g)
+    x[2, 150001] = float("nan")
+    got = torch.linalg.vector_norm(x.to("supa"), p, dim=1).cpu()
+    ref = np.array([O.vector_norm(r.numpy(), p) for r in x.double()])
+    np.testing.assert_allclose(got.double().numpy(), ref, rtol=1e-5)
+    whole = torch.linalg.vector_norm(x[:2].to("supa"), p).item()  # every element, one row of 400006
+    assert whole == pytest.approx(O.vector_norm(x[:2].double().numpy(), p), rel=1e-5)
+
+
+def test_linalg_vector_norm_dtypes_and_edges(supa, no_fallback):
+    x = torch.randn(33, 70)
+    dx = x.to("supa")
+    # a narrow input into f32 reads it directly; into f64 converts it first
+    got = torch.linalg.vector_norm(dx.bfloat16(), 3.0, dim=1, dtype=torch.float32)
+    want = torch.linalg.vector_norm(x.bfloat16(), 3.0, dim=1, dtype=torch.float32)
+    assert got.dtype == torch.float32
+    torch.testing.assert_close(got.cpu(), want, rtol=1e-5, atol=0)
+    got = torch.linalg.vector_norm(dx, 2.0, dim=0, dtype=torch.float64)
+    assert got.dtype == torch.float64
+    torch.testing.assert_close(got.cpu(), torch.linalg.vector_norm(x.double(), 2.0, dim=0), rtol=1e-12, atol=0)
+    out = torch.empty(5, device="supa")
+    torch.linalg.vector_norm(dx, 0.5, dim=0, out=out)
+    torch.testing.assert_close(out.cpu(), torch.linalg.vector_norm(x, 0.5, dim=0), rtol=1e-5, atol=0)
+    # empty reductions: zeros for orders with an identity, empty outputs for empty kept dims
+    e = torch.empty(0, 4, device="supa")
+    assert torch.equal(torch.linalg.vector_norm(e, 2.0, dim=0).cpu(), torch.zeros(4))
+    assert torch.linalg.vector_norm(e, -1.0, dim=1).shape == (0,)
+    s = torch.tensor(-2.5, device="supa")
+    assert torch.linalg.vector_norm(s, 3.0).item() == 2.5
+
+
+def test_linalg_vector_norm_errors_take_the_counted_fallback(supa):
+    """Orders without an identity on an empty reduction raise upstream's
+    error from the CPU fallback, which counts the call."""
     supa.supa.reset_fallback_counts()
-    got = torch.linalg.vector_norm(x.to("supa"), 2, dim=0)
-    torch.testing.assert_close(got.cpu(), torch.linalg.vector_norm(x, 2, dim=0))
+    with pytest.raises(RuntimeError, match="does not have an identity"):
+        torch.linalg.vector_norm(torch.empty(0, device="supa"), math.inf)
     assert supa.supa.fallback_counts().get("aten::linalg_vector_norm", 0) == 1
 
 

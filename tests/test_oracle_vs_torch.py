@@ -489,6 +489,41 @@ def test_vector_norm_vs_cpu_and_closed_forms():
     assert math.isnan(O.vector_norm(np.array([1.0, float("nan")]), 2))
 
 
+@pytest.mark.parametrize("p", [0.0, 0.5, 3.0, -1.0, -2.5, float("-inf")])
+def test_vector_norm_other_orders(p):
+    """Orders beyond 1 / 2 / inf: against upstream CPU, and closed forms that
+    a wrong exponent, a missing root or a sum-for-min swap would break."""
+    x = randn((4099,), 83, 2.0).double()
+    assert O.vector_norm(x.numpy(), p) == pytest.approx(torch.linalg.vector_norm(x, p).item(), rel=1e-12)
+    n = 64
+    if p == 0:
+        assert O.vector_norm(np.array([0.0, -0.0, 2.0, float("nan"), -1e-300]), 0) == 3.0
+    elif math.isinf(p):
+        assert O.vector_norm(np.array([3.0, -0.25, 7.0]), p) == 0.25
+    else:
+        assert O.vector_norm(np.ones(n), p) == pytest.approx(n ** (1.0 / p), rel=1e-14)  # n^(1/p)
+        assert O.vector_norm(np.array([2.0]), p) == pytest.approx(2.0, rel=1e-15)  # |x| for one element
+    if p < 0:
+        assert O.vector_norm(np.array([1.0, 0.0]), p) == 0.0  # a zero makes the sum inf, the root 0
+
+
+def test_moments_vs_cpu_and_closed_forms():
+    x = randn((5003,), 85, 3.0).double() + 7.0
+    for c in (0.0, 1.0, 2.5):
+        v, m = O.moments(x.numpy(), c)
+        assert v == pytest.approx(torch.var(x, correction=c).item(), rel=1e-13)
+        assert m == pytest.approx(x.mean().item(), rel=1e-14)
+    n = 1000
+    r = np.arange(n, dtype=np.float64)  # var of 0..n-1: n(n+1)/12 with Bessel's correction, (n^2-1)/12 without
+    assert O.moments(r, 1)[0] == pytest.approx(n * (n + 1) / 12, rel=1e-14)
+    assert O.moments(r, 0)[0] == pytest.approx((n * n - 1) / 12, rel=1e-14)
+    assert O.moments(r, 0)[1] == (n - 1) / 2
+    assert O.moments(np.full(17, 3.25), 1) == (0.0, 3.25)  # a constant: no spread, however large the mean
+    assert O.moments(np.array([1.0, 3.0]), 2) == (float("inf"), 2.0)  # n <= correction: divides by zero
+    assert math.isnan(O.moments(np.array([4.0]), 1)[0])  # 0 / 0
+    assert all(math.isnan(v) for v in O.moments(np.zeros(0)))
+
+
 @pytest.mark.parametrize("reduction", ["mean", "sum", "none"])
 @pytest.mark.parametrize("weighted", [False, True])
 def test_nll_loss2d_vs_cpu(reduction, weighted):

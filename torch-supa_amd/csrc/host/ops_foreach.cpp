@@ -10,12 +10,16 @@
 // multi-tensor-apply launch per 40 tensors.  Anything else takes the slow
 // path the upstream CompositeExplicitAutograd foreach kernels take: one
 // elementwise op per tensor (still on the supa kernels where they exist).
+#include <ATen/WrapDimUtilsMulti.h>
 #include <ATen/native/ForeachUtils.h>
+#include <ATen/native/Resize.h>
 #include <ATen/native/CPUFallback.h>
 #include <ATen/ops/linalg_vector_norm.h>
 #include <ATen/ops/linalg_vector_norm_ops.h>
 #include <torch/library.h>
 
+#include <bitset>
+#include <cmath>
 #include <map>
 
 #include "common.h"
@@ -333,26 +337,84 @@ std::vector<at::Tensor> foreach_norm(at::TensorList self, const c10::Scalar& ord
   return res;
 }
 
-// linalg_vector_norm over every element (dim None) of a contiguous tensor,
-// ord 1 / 2 / inf: the same kernels with a one-tensor list.  Reductions over
-// some dims, other orders, and the inf-norm of an empty tensor (an error
-// upstream) go to the CPU fallback, which counts them.
+// linalg_vector_norm.  Over every element of a contiguous tensor with ord
+// 1 / 2 / inf: the multi-tensor norm kernels with a one-tensor list.  Any
+// other dims or order: the reduced dims go last in a contiguous copy and the
+// row-norm kernel reduces each row.  A dtype of double on a narrower input
+// converts the input first (upstream computes in the result dtype then);
+// bf16 / f16 into f32 reads the narrow input directly.  Empty reductions
+// without an identity (negative or infinite order) and complex inputs go to
+// the CPU fallback, which raises or counts them.
 at::Tensor vector_norm_supa(const at::Tensor& self, const c10::Scalar& ord, at::OptionalIntArrayRef dim,
                             bool keepdim, std::optional<at::ScalarType> dtype) {
-  double p = 0.0;
-  const c10::ScalarType res_dt = dtype.value_or(self.scalar_type());
+  const c10::ScalarType in_dt = self.scalar_type();
+  const c10::ScalarType res_dt = dtype.value_or(in_dt);
+  const double p = ord.isComplex() ? NAN : ord.toDouble();
+  const bool dt_ok = res_dt == in_dt || res_dt == at::kDouble || (res_dt == at::kFloat && in_dt != at::kDouble);
   const bool all_dims = !dim.has_value() || dim->empty();
-  if (self.device().type() == kSupa && self.is_contiguous() && float_family(self.scalar_type()) && all_dims &&
-      norm_ord_ok(ord, &p) && !(p == HUGE_VAL && self.numel() == 0) &&
-      (res_dt == self.scalar_type() || res_dt == at::kFloat || res_dt == at::kDouble)) {
-    std::vector<int64_t> shape(keepdim ? self.dim() : 0, 1);
-    at::Tensor out = at::empty(shape, self.options().dtype(res_dt));
-    const at::Tensor list[1] = {self};
+  const int64_t nd = self.dim();
+  std::bitset<at::dim_bitset_size> red;
+  bool empty_reduction = false;
+  if (all_dims) {
+    for (int64_t i = 0; i < nd; ++i) red.set(i);
+  } else {
+    red = at::dim_list_to_bitset(*dim, nd);  // wraps, and rejects repeated dims
+  }
+  for (int64_t i = 0; i < nd; ++i) empty_reduction |= red[i] && self.size(i) == 0;
+  if (self.device().type() != kSupa || !float_family(in_dt) || p != p || !dt_ok ||
+      (empty_reduction && (p < 0 || std::isinf(p)))) {
+    return at::native::call_fallback_fn<&supa_cpu_fallback, at::_ops::linalg_vector_norm>::call(self, ord, dim,
+                                                                                             keepdim, dtype);
+  }
+  const at::Tensor x = (res_dt == at::kDouble && in_dt != at::kDouble) ? self.to(at::kDouble) : self;
+  if (all_dims && x.is_contiguous() && (p == 1.0 || p == 2.0 || p == HUGE_VAL)) {
+    std::vector<int64_t> shape(keepdim ? nd : 0, 1);
+    at::Tensor out = at::empty(shape, x.options().dtype(res_dt));
+    const at::Tensor list[1] = {x};
     norms_into(at::TensorList(list, 1), p, out, "linalg_vector_norm");
     return out;
   }
-  return at::native::call_fallback_fn<&supa_cpu_fallback, at::_ops::linalg_vector_norm>::call(self, ord, dim, keepdim,
-                                                                                           dtype);
+  std::vector<int64_t> oshape, perm;
+  int64_t inner = 1, outer = 1;
+  for (int64_t i = 0; i < nd; ++i) {
+    if (!red[i]) {
+      oshape.push_back(x.size(i));
+      perm.push_back(i);
+      outer *= x.size(i);
+    } else if (keepdim) {
+      oshape.push_back(1);
+    }
+  }
+  for (int64_t i = 0; i < nd; ++i) {
+    if (red[i]) {
+      perm.push_back(i);
+      inner *= x.size(i);
+    }
+  }
+  at::Tensor out = at::empty(oshape, x.options().dtype(res_dt));
+  if (outer == 0) return out;
+  if (inner == 0) return out.zero_();  // an empty sum (orders >= 0)
+  const at::Tensor rows = nd == 0 ? x.reshape({1}) : x.permute(perm).contiguous();
+  const int32_t dt = dtype_code(x.scalar_type());
+  const int64_t ws_bytes = supa_amd_norm_rows_workspace_bytes(outer, inner, dt);
+  TORCH_CHECK(ws_bytes >= 0, "linalg_vector_norm: ", supa_amd_status_string((int)ws_bytes));
+  at::Tensor ws;
+  if (ws_bytes > 0) ws = at::empty({ws_bytes}, x.options().dtype(at::kByte));
+  check_status(supa_amd_norm_rows(rows.data_ptr(), dt, out.data_ptr(), dtype_code(res_dt), outer, inner, p,
+                                  ws_bytes > 0 ? ws.data_ptr() : nullptr, ws_bytes,
+                                  current_stream(x.device().index())),
+               "linalg_vector_norm");
+  return out;
+}
+
+at::Tensor& vector_norm_out(const at::Tensor& self, const c10::Scalar& ord, at::OptionalIntArrayRef dim, bool keepdim,
+                            std::optional<at::ScalarType> dtype, at::Tensor& out) {
+  const at::Tensor r = vector_norm_supa(self, ord, dim, keepdim, dtype);
+  TORCH_CHECK(out.scalar_type() == r.scalar_type(), "linalg.vector_norm: Expected out tensor to have dtype ",
+              r.scalar_type(), ", but got ", out.scalar_type(), " instead");
+  at::native::resize_output(out, r.sizes());
+  out.copy_(r);
+  return out;
 }
 
 // ------------------------------------------------ registered signatures
@@ -681,6 +743,7 @@ TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
   m.impl("_foreach_zero_", TORCH_FN(foreach_zero_));
   m.impl("_foreach_norm.Scalar", TORCH_FN(foreach_norm));
   m.impl("linalg_vector_norm", TORCH_FN(vector_norm_supa));
+  m.impl("linalg_vector_norm.out", TORCH_FN(vector_norm_out));
   m.impl("_fused_adamw_", TORCH_FN(fused_adamw_));
   m.impl("_fused_adamw_.tensor_lr", TORCH_FN(fused_adamw_tensor_lr_));
   m.impl("_fused_adam_", TORCH_FN(fused_adam_));

@@ -315,6 +315,97 @@ int norm_launch(int32_t n, const void* const* x, const int64_t* numel, void* out
   });
 }
 
+
+// ------------------------------------------------------ norm over rows
+// linalg_vector_norm over the last dim of a contiguous [outer, inner] input,
+// every order upstream's norm kernel knows: 0 (count of non-zeros), 1, 2,
+// inf / -inf (largest / smallest |x|, NaN propagating) and any other p
+// (sum of |x|^p, then ^(1/p)), accumulated in opmath.
+constexpr int kRowOrdZero = 3, kRowOrdNegInf = 4, kRowOrdP = 5;
+
+template <int ORD, typename A> __device__ __forceinline__ A row_norm_term(A x, A p) {
+  if constexpr (ORD == kRowOrdZero) return x != A(0) ? A(1) : A(0);
+  else if constexpr (ORD == kRowOrdP) return pow(fabs(x), p);
+  else return norm_term<ORD>(x);
+}
+template <int ORD, typename A> __device__ __forceinline__ A row_norm_combine(A a, A b) {
+  if constexpr (ORD == kRowOrdNegInf) return (a != a || a < b) ? a : b;
+  else if constexpr (ORD == kOrdInf) return norm_combine<kOrdInf>(a, b);
+  else return a + b;
+}
+template <int ORD, typename A> __device__ __forceinline__ A row_norm_init() {
+  if constexpr (ORD == kRowOrdNegInf) return A(INFINITY);
+  else return A(0);
+}
+
+// One workgroup per (row, chunk of `chunk` elements): a single wavefront for
+// rows up to kNormWaveRow elements (no LDS stage), four for longer ones.
+// TERM: the input holds elements (else partials of an earlier launch); PROJ:
+// write the norm (else the chunk's partial, in A).
+constexpr int64_t kNormWaveRow = 4096;
+
+template <int BS, typename T, typename OT, typename A, int ORD, bool TERM, bool PROJ>
+__global__ void __launch_bounds__(BS)
+k_norm_rows(const T* __restrict__ in, OT* __restrict__ out, int64_t inner, int64_t chunk, uint32_t nchunks, A p) {
+  __shared__ A part[BS / 64];
+  const uint32_t row = blockIdx.x / nchunks, c = blockIdx.x % nchunks;
+  const int64_t lo = (int64_t)c * chunk;
+  const int64_t n = lo + chunk < inner ? chunk : inner - lo;
+  const T* src = in + (int64_t)row * inner + lo;
+  auto comb = [](A a, A b) { return row_norm_combine<ORD>(a, b); };
+  A acc = fold_strided<8>(
+      row_norm_init<ORD, A>(), threadIdx.x, BS, n,
+      [&](int64_t i) {
+        const A x = (A)to_arith(src[i]);
+        if constexpr (TERM) return row_norm_term<ORD>(x, p);
+        else return x;
+      },
+      comb);
+  for (int off = 32; off > 0; off >>= 1) acc = comb(acc, __shfl_xor(acc, off, 64));
+  if constexpr (BS > 64) {
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = acc;
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+#pragma unroll
+    for (int w = 1; w < BS / 64; ++w) acc = comb(acc, part[w]);
+    if constexpr (PROJ) {
+      if constexpr (ORD == 2) acc = sqrt(acc);
+      else if constexpr (ORD == kRowOrdP) acc = pow(acc, A(1) / p);
+    }
+    out[blockIdx.x] = from_arith<OT>(acc);
+  }
+}
+
+constexpr int64_t kNormRowChunk = 16384;       // elements per workgroup in the first of two launches
+constexpr int64_t kNormRowTwoPass = 65536;     // rows longer than this (with few rows) take two launches
+
+inline int64_t norm_row_chunks(int64_t outer, int64_t inner) {
+  return inner > kNormRowTwoPass && outer < 2048 ? (inner + kNormRowChunk - 1) / kNormRowChunk : 1;
+}
+
+template <typename T, typename OT, int ORD>
+int norm_rows_launch(const T* in, OT* out, int64_t outer, int64_t inner, double p, void* ws, hipStream_t st) {
+  using A = opmath_t<T>;
+  const int64_t nch = norm_row_chunks(outer, inner);
+  if (nch == 1 && inner <= kNormWaveRow) {
+    k_norm_rows<64, T, OT, A, ORD, true, true><<<(unsigned)outer, 64, 0, st>>>(in, out, inner, inner, 1u, (A)p);
+    return launch_status();
+  }
+  if (nch == 1) {
+    k_norm_rows<kNormBlock, T, OT, A, ORD, true, true><<<(unsigned)outer, kNormBlock, 0, st>>>(in, out, inner, inner,
+                                                                                             1u, (A)p);
+    return launch_status();
+  }
+  A* part = static_cast<A*>(ws);
+  k_norm_rows<kNormBlock, T, A, A, ORD, true, false><<<(unsigned)(outer * nch), kNormBlock, 0, st>>>(
+      in, part, inner, kNormRowChunk, (uint32_t)nch, (A)p);
+  const int rc = launch_status();
+  if (rc) return rc;
+  k_norm_rows<kNormBlock, A, OT, A, ORD, false, true><<<(unsigned)outer, kNormBlock, 0, st>>>(part, out, nch, nch, 1u, (A)p);
+  return launch_status();
+}
+
 }  // namespace sa
 
 using namespace sa;
@@ -383,6 +474,45 @@ int supa_amd_foreach_norm(int32_t ntensors, const void* const* x, const int64_t*
     if (out_dtype == dtype) return go((T*)nullptr);
     if (out_dtype == SUPA_AMD_F32) return go((float*)nullptr);
     if (out_dtype == SUPA_AMD_F64) return go((double*)nullptr);
+    return SUPA_AMD_EDTYPE;
+  });
+}
+
+
+int64_t supa_amd_norm_rows_workspace_bytes(int64_t outer, int64_t inner, int32_t dtype) {
+  if (outer < 0 || inner <= 0) return -1;
+  const int64_t nch = norm_row_chunks(outer, inner);
+  if (nch == 1) return 0;
+  if (dtype != SUPA_AMD_F32 && dtype != SUPA_AMD_BF16 && dtype != SUPA_AMD_F16 && dtype != SUPA_AMD_F64)
+    return SUPA_AMD_EDTYPE;
+  return outer * nch * (dtype == SUPA_AMD_F64 ? 8 : 4);  // opmath partials
+}
+
+int supa_amd_norm_rows(const void* in, int32_t dtype, void* out, int32_t out_dtype, int64_t outer, int64_t inner,
+                       double ord, void* workspace, int64_t ws_bytes, void* stream) {
+  if (!in || !out || outer < 0 || inner <= 0) return SUPA_AMD_EINVAL;
+  if (ord != ord) return SUPA_AMD_EINVAL;
+  if (outer == 0) return SUPA_AMD_OK;
+  if (outer * norm_row_chunks(outer, inner) >= (int64_t(1) << 31)) return SUPA_AMD_ELAYOUT;
+  const int64_t need = supa_amd_norm_rows_workspace_bytes(outer, inner, dtype);
+  if (need < 0) return need == -1 ? SUPA_AMD_EINVAL : (int)need;
+  if (need > 0 && (!workspace || ws_bytes < need)) return SUPA_AMD_EWORKSPACE;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return with_mta_storage(dtype, [&](auto* tag) -> int {
+    using T = std::remove_pointer_t<decltype(tag)>;
+    auto go = [&](auto* otag) -> int {
+      using OT = std::remove_pointer_t<decltype(otag)>;
+      const T* x = static_cast<const T*>(in);
+      OT* o = static_cast<OT*>(out);
+      if (ord == 0.0) return norm_rows_launch<T, OT, kRowOrdZero>(x, o, outer, inner, ord, workspace, st);
+      if (ord == 1.0) return norm_rows_launch<T, OT, 1>(x, o, outer, inner, ord, workspace, st);
+      if (ord == 2.0) return norm_rows_launch<T, OT, 2>(x, o, outer, inner, ord, workspace, st);
+      if (ord == HUGE_VAL) return norm_rows_launch<T, OT, kOrdInf>(x, o, outer, inner, ord, workspace, st);
+      if (ord == -HUGE_VAL) return norm_rows_launch<T, OT, kRowOrdNegInf>(x, o, outer, inner, ord, workspace, st);
+      return norm_rows_launch<T, OT, kRowOrdP>(x, o, outer, inner, ord, workspace, st);
+    };
+    if (out_dtype == dtype) return go((T*)nullptr);
+    if (out_dtype == SUPA_AMD_F32) return go((float*)nullptr);
     return SUPA_AMD_EDTYPE;
   });
 }
