@@ -491,9 +491,14 @@ int supa_amd_cross_entropy_backward(const void* grad_out, const void* logits, in
 #define SUPA_AMD_FOREACH_ADDCDIV 6  /* out = a + s * (b / c)                  */
 #define SUPA_AMD_FOREACH_LERP 7     /* out = lerp(a, b, w)                    */
 #define SUPA_AMD_FOREACH_ZERO 8     /* out = 0                                */
+#define SUPA_AMD_FOREACH_POW 9      /* out = a ** y (LIST or SCALARS; a SCALARS
+                                       exponent must be exact in `dtype`)     */
+#define SUPA_AMD_FOREACH_RPOW 10    /* out = scalars[k] ** a (SCALARS only)   */
+#define SUPA_AMD_FOREACH_COPY 11    /* out = a                                */
 #define SUPA_AMD_FOREACH_UNARY 32   /* + SUPA_AMD_SIGMOID, _TANH, _EXP, _LOG, _ERF,
                                        _NEG, _RECIPROCAL, _ABS, _SQRT, _EXPM1,
-                                       _LOG1P: out = f(a) */
+                                       _LOG1P, _SIGN, _FLOOR, _CEIL, _ROUND,
+                                       _TRUNC, _RSQRT: out = f(a) */
 /* Where y (lerp: the weight w) comes from: */
 #define SUPA_AMD_FOREACH_LIST 0       /* y = b[k][i]; lerp w = c[k][i]            */
 #define SUPA_AMD_FOREACH_SCALARS 1    /* y = scalars[k] (a Scalar repeats)        */
@@ -515,7 +520,14 @@ int supa_amd_cross_entropy_backward(const void* grad_out, const void* logits, in
  * _foreach_maximum_ / _minimum_ NF:10997-11075, _foreach_addcdiv_
  * NF:11104-11120, _foreach_addcmul_ NF:11150-11167, _foreach_lerp_
  * NF:11380-11412, _foreach_sqrt_ NF:11691, _foreach_zero_ NF:11745, the
- * other unary ops listed above, and the out-of-place forms. */
+ * other unary ops listed above (_foreach_ceil_ NF:11244, _foreach_floor_
+ * NF:11349, _foreach_round_ NF:11601, _foreach_rsqrt_ NF:11616,
+ * _foreach_sign_ NF:11646, _foreach_trunc_ NF:11737), _foreach_pow in its
+ * List / Scalar / ScalarList / ScalarAndTensor forms NF:11527-11571
+ * (upstream ForeachBinaryOp*.cu over pow), _foreach_copy_ NF:11753, and the
+ * out-of-place forms.  POW with SCALARS evaluates each exponent as the
+ * per-tensor pow(Tensor, Scalar) does: 0 gives 1, 1 a copy, 0.5 / -0.5 / -1
+ * sqrt / rsqrt / reciprocal, 2 / 3 / -2 products, else pow in double. */
 int supa_amd_foreach(int op, int form, int32_t ntensors, void* const* out, const void* const* a,
                      const void* const* b, const void* const* c, const int64_t* numel, int32_t dtype,
                      const double* scalars, double alpha, const void* scalar_ptr, void* stream);

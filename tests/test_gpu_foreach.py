@@ -162,6 +162,84 @@ def test_unary_and_zero(dtype, no_fallback):
         assert not t.cpu().any()
 
 
+ROUNDING = ["sign", "floor", "ceil", "round", "trunc", "rsqrt"]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_rounding_unary_and_copy(dtype, no_fallback):
+    """sign / floor / ceil / round / trunc / rsqrt and copy_ in one launch each:
+    equal to the per-tensor supa op bit for bit, and (all but rsqrt, whose
+    per-tensor kernel has its own test) to upstream CPU."""
+    xs = lists(11, dtype)
+    xs[1][0, :6] = torch.tensor([0.5, -0.5, 2.5, -2.5, -0.0, float("nan")])  # ties to even, -0, NaN
+    d = dev(xs)
+    for name in ROUNDING:
+        src = [t.abs() + 0.01 for t in d] if name == "rsqrt" else d
+        got = getattr(torch, f"_foreach_{name}")(src)
+        for o, x in zip(got, src):
+            same(o, getattr(torch, name)(x).cpu())
+        work = [t.clone() for t in src]
+        getattr(torch, f"_foreach_{name}_")(work)
+        for w, o in zip(work, got):
+            same(w, o.cpu())
+        if name != "rsqrt":
+            for o, x in zip(got, xs):
+                same(o, getattr(torch, name)(x))
+    dst = [torch.empty_like(t) for t in d]
+    torch._foreach_copy_(dst, d)
+    for a, x in zip(dst, xs):
+        same(a, x)
+    # a cast or a strided member takes copy_ per tensor
+    mixed = [torch.empty(t.shape, dtype=torch.float64, device="supa") for t in d]
+    torch._foreach_copy_(mixed, d)
+    for a, x in zip(mixed, xs):
+        same(a, x.double())
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_pow_forms(dtype, no_fallback):
+    """_foreach_pow (List, Scalar, ScalarList, ScalarAndTensor) and its in-place
+    forms equal the per-tensor pow bit for bit, over every special exponent the
+    per-tensor op routes (0, 1, +-0.5, -1, 2, 3, -2), general ones, and an
+    exponent that is not exact in the dtype (per-tensor path)."""
+    xs = lists(12, dtype, positive=True)
+    xs[0][:4] = torch.tensor([0.0, float("nan"), float("inf"), 1.0])
+    ys = [(t.float() * 0.5 - 0.3).to(dtype) for t in lists(13, dtype)]
+    d, dy = dev(xs), dev(ys)
+    for e in [0.0, 1.0, 0.5, -0.5, -1.0, 2.0, 3.0, -2.0, 1.75, -0.375, 2.5, 1.7, 2]:
+        got = torch._foreach_pow(d, e)
+        for o, t in zip(got, d):
+            same(o, torch.pow(t, e).cpu())
+        work = [t.clone() for t in d]
+        torch._foreach_pow_(work, e)
+        for w, o in zip(work, got):
+            same(w, o.cpu())
+    if dtype == torch.float32:
+        # x*x, (x*x)*x and 1/(x*x) as upstream CPU evaluates them; sqrt the
+        # correctly rounded root (this CPU build's float32 sqrt is not IEEE)
+        for e in (2.0, 3.0, -2.0):
+            for o, x in zip(torch._foreach_pow(d, e), xs):
+                same(o, torch.pow(x, e))
+        for o, x in zip(torch._foreach_pow(d, 0.5), xs):
+            same(o, torch.sqrt(x.double()).float())
+    sl = [2.0, -0.5, 1.25, 3]
+    for o, t, e in zip(torch._foreach_pow(d, sl), d, sl):
+        same(o, torch.pow(t, e).cpu())
+    work = [t.clone() for t in d]
+    torch._foreach_pow_(work, sl)
+    for w, t, e in zip(work, d, sl):
+        same(w, torch.pow(t, e).cpu())
+    for o, t, e in zip(torch._foreach_pow(d, dy), d, dy):
+        same(o, torch.pow(t, e).cpu())
+    work = [t.clone() for t in d]
+    torch._foreach_pow_(work, dy)
+    for w, t, e in zip(work, d, dy):
+        same(w, torch.pow(t, e).cpu())
+    for base in (2.0, 0.75, 1.0, -1.5):
+        for o, e in zip(torch._foreach_pow(base, dy), dy):
+            same(o, torch.pow(base, e).cpu())
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_norm(dtype, no_fallback):
     xs = lists(9, dtype) + [torch.zeros(0, dtype=dtype), torch.full((3000,), 0.5, dtype=dtype)]

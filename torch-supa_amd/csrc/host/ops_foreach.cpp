@@ -1,7 +1,8 @@
 // PrivateUse1 registrations of the optimizer path: the _foreach_* family
 // (add / sub / mul / div / maximum / minimum / clamp_min / clamp_max in their
-// List, Scalar, ScalarList and Tensor forms; addcmul / addcdiv; lerp; the
-// unary ops the elementwise kernels have; zero_; norm), in-place and
+// List, Scalar, ScalarList and Tensor forms; addcmul / addcdiv; lerp; pow in
+// its List, Scalar, ScalarList and ScalarAndTensor forms; the unary ops the
+// elementwise kernels have; copy_; zero_; norm), in-place and
 // out-of-place, _fused_adamw_, and the mixed-precision pieces beside it
 // (_amp_foreach_non_finite_check_and_unscale_, _amp_update_scale_).
 //
@@ -267,6 +268,12 @@ at::Tensor unary_one(int u, const at::Tensor& a, bool inplace) {
     case SUPA_AMD_ABS: return inplace ? s.abs_() : at::abs(a);
     case SUPA_AMD_EXPM1: return inplace ? s.expm1_() : at::expm1(a);
     case SUPA_AMD_LOG1P: return inplace ? s.log1p_() : at::log1p(a);
+    case SUPA_AMD_SIGN: return inplace ? s.sign_() : at::sign(a);
+    case SUPA_AMD_FLOOR: return inplace ? s.floor_() : at::floor(a);
+    case SUPA_AMD_CEIL: return inplace ? s.ceil_() : at::ceil(a);
+    case SUPA_AMD_ROUND: return inplace ? s.round_() : at::round(a);
+    case SUPA_AMD_TRUNC: return inplace ? s.trunc_() : at::trunc(a);
+    case SUPA_AMD_RSQRT: return inplace ? s.rsqrt_() : at::rsqrt(a);
     default: return inplace ? s.sqrt_() : at::sqrt(a);
   }
 }
@@ -280,6 +287,87 @@ std::vector<at::Tensor> unary(int u, at::TensorList self, bool inplace, const ch
   std::vector<at::Tensor> out;
   for (const auto& t : self) out.push_back(unary_one(u, t, inplace));
   return out;
+}
+
+// ---------------------------------------------------------------- pow
+// The per-tensor pow(Tensor, Scalar) rounds the exponent to the tensor's
+// dtype before choosing its special cases; the multi-tensor kernel takes
+// exponents that round to themselves, the rest go tensor by tensor.
+bool exact_in(c10::ScalarType dt, double e) {
+  switch (dt) {
+    case at::kDouble: return true;
+    case at::kFloat: return (double)(float)e == e;
+    case at::kBFloat16: return (double)(float)c10::BFloat16((float)e) == e;
+    case at::kHalf: return (double)(float)c10::Half((float)e) == e;
+    default: return false;
+  }
+}
+
+at::Tensor pow_one(const at::Tensor& a, const c10::Scalar& e, bool inplace) {
+  return inplace ? const_cast<at::Tensor&>(a).pow_(e) : at::pow(a, e);
+}
+
+std::vector<at::Tensor> pow_list(at::TensorList self, at::TensorList exps, bool inplace) {
+  at::native::check_foreach_api_restrictions(self, exps);
+  if (fast_ok({self, exps})) {
+    std::vector<at::Tensor> out = inplace ? self.vec() : empty_like_list(self);
+    fe_launch(SUPA_AMD_FOREACH_POW, SUPA_AMD_FOREACH_LIST, out, self, exps, {}, {}, 1.0, {}, "_foreach_pow");
+    return out;
+  }
+  std::vector<at::Tensor> out;
+  for (size_t i = 0; i < self.size(); ++i)
+    out.push_back(inplace ? const_cast<at::Tensor&>(self[i]).pow_(exps[i]) : at::pow(self[i], exps[i]));
+  return out;
+}
+
+std::vector<at::Tensor> pow_scalars(at::TensorList self, at::ArrayRef<c10::Scalar> es, bool inplace) {
+  at::native::check_foreach_api_restrictions(self, es);
+  bool fast = fast_ok({self}) && real_scalars(es);
+  for (size_t i = 0; fast && i < es.size(); ++i) fast = exact_in(self[0].scalar_type(), es[i].toDouble());
+  if (fast) {
+    std::vector<at::Tensor> out = inplace ? self.vec() : empty_like_list(self);
+    fe_launch(SUPA_AMD_FOREACH_POW, SUPA_AMD_FOREACH_SCALARS, out, self, {}, {}, to_doubles(es), 1.0, {},
+              "_foreach_pow");
+    return out;
+  }
+  std::vector<at::Tensor> out;
+  for (size_t i = 0; i < self.size(); ++i) out.push_back(pow_one(self[i], es[i], inplace));
+  return out;
+}
+
+void pow_list_(at::TensorList s, at::TensorList e) { pow_list(s, e, true); }
+std::vector<at::Tensor> pow_list_f(at::TensorList s, at::TensorList e) { return pow_list(s, e, false); }
+void pow_scalar_(at::TensorList s, const c10::Scalar& e) { pow_scalars(s, std::vector<c10::Scalar>(s.size(), e), true); }
+std::vector<at::Tensor> pow_scalar(at::TensorList s, const c10::Scalar& e) {
+  return pow_scalars(s, std::vector<c10::Scalar>(s.size(), e), false);
+}
+void pow_scalarlist_(at::TensorList s, at::ArrayRef<c10::Scalar> e) { pow_scalars(s, e, true); }
+std::vector<at::Tensor> pow_scalarlist(at::TensorList s, at::ArrayRef<c10::Scalar> e) { return pow_scalars(s, e, false); }
+
+// base ** exps[k]: the base is read in the list's opmath type, as the
+// per-tensor pow(Scalar, Tensor) binds it; a base of 1 (ones, whatever the
+// exponent) goes tensor by tensor.
+std::vector<at::Tensor> pow_scalar_base(const c10::Scalar& base, at::TensorList exps) {
+  at::native::check_foreach_api_restrictions(exps);
+  if (fast_ok({exps}) && real_scalar(base) && !base.equal(1.0)) {
+    std::vector<at::Tensor> out = empty_like_list(exps);
+    fe_launch(SUPA_AMD_FOREACH_RPOW, SUPA_AMD_FOREACH_SCALARS, out, exps, {}, {},
+              std::vector<double>(exps.size(), base.toDouble()), 1.0, {}, "_foreach_pow");
+    return out;
+  }
+  std::vector<at::Tensor> out;
+  for (const auto& t : exps) out.push_back(at::pow(base, t));
+  return out;
+}
+
+// _foreach_copy_: same-dtype dense lists in one launch, otherwise copy_ per
+// tensor (casts, layouts, other devices).
+void foreach_copy_(at::TensorList self, at::TensorList src, bool non_blocking) {
+  at::native::check_foreach_api_restrictions(self, src);
+  if (fast_ok({self, src}))
+    return fe_launch(SUPA_AMD_FOREACH_COPY, SUPA_AMD_FOREACH_SCALARS, self, src, {}, {}, {}, 1.0, {},
+                     "_foreach_copy_");
+  for (size_t i = 0; i < self.size(); ++i) const_cast<at::Tensor&>(self[i]).copy_(src[i], non_blocking);
 }
 
 void foreach_zero_(at::TensorList self) {
@@ -515,6 +603,12 @@ SUPA_FE_UNARY(abs, SUPA_AMD_ABS)
 SUPA_FE_UNARY(sqrt, SUPA_AMD_SQRT)
 SUPA_FE_UNARY(expm1, SUPA_AMD_EXPM1)
 SUPA_FE_UNARY(log1p, SUPA_AMD_LOG1P)
+SUPA_FE_UNARY(sign, SUPA_AMD_SIGN)
+SUPA_FE_UNARY(floor, SUPA_AMD_FLOOR)
+SUPA_FE_UNARY(ceil, SUPA_AMD_CEIL)
+SUPA_FE_UNARY(round, SUPA_AMD_ROUND)
+SUPA_FE_UNARY(trunc, SUPA_AMD_TRUNC)
+SUPA_FE_UNARY(rsqrt, SUPA_AMD_RSQRT)
 #undef SUPA_FE_UNARY
 
 // ------------------------------------------------------------ fused AdamW
@@ -739,7 +833,22 @@ TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
   SUPA_FE_REG_UNARY(sqrt)
   SUPA_FE_REG_UNARY(expm1)
   SUPA_FE_REG_UNARY(log1p)
+  SUPA_FE_REG_UNARY(sign)
+  SUPA_FE_REG_UNARY(floor)
+  SUPA_FE_REG_UNARY(ceil)
+  SUPA_FE_REG_UNARY(round)
+  SUPA_FE_REG_UNARY(trunc)
+  SUPA_FE_REG_UNARY(rsqrt)
 #undef SUPA_FE_REG_UNARY
+  // pow, copy_
+  m.impl("_foreach_pow_.List", TORCH_FN(pow_list_));
+  m.impl("_foreach_pow.List", TORCH_FN(pow_list_f));
+  m.impl("_foreach_pow_.Scalar", TORCH_FN(pow_scalar_));
+  m.impl("_foreach_pow.Scalar", TORCH_FN(pow_scalar));
+  m.impl("_foreach_pow_.ScalarList", TORCH_FN(pow_scalarlist_));
+  m.impl("_foreach_pow.ScalarList", TORCH_FN(pow_scalarlist));
+  m.impl("_foreach_pow.ScalarAndTensor", TORCH_FN(pow_scalar_base));
+  m.impl("_foreach_copy_", TORCH_FN(foreach_copy_));
   m.impl("_foreach_zero_", TORCH_FN(foreach_zero_));
   m.impl("_foreach_norm.Scalar", TORCH_FN(foreach_norm));
   m.impl("linalg_vector_norm", TORCH_FN(vector_norm_supa));

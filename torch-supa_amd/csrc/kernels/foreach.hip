@@ -1,7 +1,7 @@
 // Generic multi-tensor apply for the _foreach_* family: one kernel template
 // covers the unary, binary (List / ScalarList / device-scalar Tensor forms)
-// and pointwise ternary ops (addcmul, addcdiv, lerp), plus _foreach_zero_;
-// and a two-kernel _foreach_norm.
+// and pointwise ternary ops (addcmul, addcdiv, lerp), pow in its three forms,
+// _foreach_copy_ and _foreach_zero_; and a two-kernel _foreach_norm.
 //
 // Arithmetic per element is the one the elementwise kernels use (ops.h), in
 // the storage type's opmath, so _foreach_op(xs, ys)[k] equals op(xs[k], ys[k])
@@ -20,6 +20,8 @@ struct MtaTable {
   int64_t numel[kMtaTensors];
   uint32_t chunk_start[kMtaTensors + 1];
   int32_t ntensors;
+  uint32_t bucket_shift;
+  uint8_t bucket[kMtaBuckets];
 };
 
 constexpr int kFeList = SUPA_AMD_FOREACH_LIST;
@@ -36,12 +38,38 @@ constexpr int fe_inputs(int op, int form) {
                                                                              : (form == kFeList ? 2 : 1);
 }
 
+// base ** e for a per-tensor exponent e that is exact in the storage type T,
+// evaluated as the per-tensor pow(Tensor, Scalar) evaluates it: upstream
+// pow_out's fill / copy for 0 and 1, its sqrt / rsqrt / reciprocal routes for
+// 0.5 / -0.5 / -1, then pow_tensor_scalar_kernel's 2 / 3 / -2 special cases
+// (PowScalarOp) and pow in double rounded once.
+template <typename T, typename C>
+__device__ __forceinline__ C fe_pow_scalar(C b, C e) {
+  if (e == C(0)) return C(1);
+  if (e == C(1)) return b;
+  if (e == C(0.5)) return sqrt(b);
+  if (e == C(-0.5)) return C(1) / sqrt(b);
+  if (e == C(-1)) return C(1) / b;
+  constexpr int half = std::is_same<T, bf16>::value ? 1 : (std::is_same<T, f16>::value ? 2 : 0);
+  const int mode = e == C(2) ? POW_SQUARE : e == C(3) ? POW_CUBE : e == C(-2) ? POW_INV_SQUARE : POW_GENERAL;
+  const C xb[1] = {b};
+  return PowScalarOp<C>{mode, half, (double)e}(xb);
+}
+
 // One element.  x[0..NIN) are the loaded operands, s the tensor's scalar
 // (or the device scalar), al the add/sub alpha.
-template <int OP, int FORM, typename C>
+template <typename T, int OP, int FORM, typename C>
 __device__ __forceinline__ C fe_apply(const C* x, C s, C al) {
   if constexpr (OP == SUPA_AMD_FOREACH_ZERO) {
     return C(0);
+  } else if constexpr (OP == SUPA_AMD_FOREACH_COPY) {
+    return x[0];
+  } else if constexpr (OP == SUPA_AMD_FOREACH_POW) {
+    if constexpr (FORM == kFeList) return PowOp<C>{}(x);
+    else return fe_pow_scalar<T, C>(x[0], s);
+  } else if constexpr (OP == SUPA_AMD_FOREACH_RPOW) {
+    const C sx[2] = {s, x[0]};
+    return PowOp<C>{}(sx);
   } else if constexpr (OP >= kFeUnary) {
     return UnaryOp<OP - kFeUnary, C>{}(x);
   } else if constexpr (OP == SUPA_AMD_FOREACH_ADDCMUL) {
@@ -72,7 +100,7 @@ k_foreach(MtaTable tab, double alpha, const void* sp) {
   constexpr int NIN = fe_inputs(OP, FORM);
   constexpr int NL = NIN > 0 ? NIN : 1;
   constexpr int V = 16 / sizeof(T);
-  const MtaRange r = mta_range<CHUNK>(tab.chunk_start, tab.numel, tab.ntensors);
+  const MtaRange r = mta_range<CHUNK>(tab);
   T* out = static_cast<T*>(tab.out[r.k]);
   const T* in[NL];
   bool vec = aligned(out, 16);
@@ -99,7 +127,7 @@ k_foreach(MtaTable tab, double alpha, const void* sp) {
         C xi[NL];
 #pragma unroll
         for (int j = 0; j < NIN; ++j) xi[j] = (C)to_arith(xv[j].v[i]);
-        res.v[i] = from_arith<T>(fe_apply<OP, FORM, C>(xi, s, al));
+        res.v[i] = from_arith<T>(fe_apply<T, OP, FORM, C>(xi, s, al));
       }
       st_stream(reinterpret_cast<Vec<T, V>*>(out + e), res);
     }
@@ -109,7 +137,7 @@ k_foreach(MtaTable tab, double alpha, const void* sp) {
     C xi[NL];
 #pragma unroll
     for (int j = 0; j < NIN; ++j) xi[j] = (C)to_arith(in[j][e]);
-    out[e] = from_arith<T>(fe_apply<OP, FORM, C>(xi, s, al));
+    out[e] = from_arith<T>(fe_apply<T, OP, FORM, C>(xi, s, al));
   }
 }
 
@@ -167,6 +195,14 @@ int fe_dispatch(int op, int form, const FeArgs& a, hipStream_t st) {
       if (form == kFeList) return fe_launch<T, SUPA_AMD_FOREACH_LERP, kFeList>(a, st);
       return fe_launch<T, SUPA_AMD_FOREACH_LERP, kFeScalars>(a, st);
     case SUPA_AMD_FOREACH_ZERO: return fe_launch<T, SUPA_AMD_FOREACH_ZERO, kFeScalars>(a, st);
+    case SUPA_AMD_FOREACH_COPY: return fe_launch<T, SUPA_AMD_FOREACH_COPY, kFeScalars>(a, st);
+    case SUPA_AMD_FOREACH_POW:
+      if (form == kFeList) return fe_launch<T, SUPA_AMD_FOREACH_POW, kFeList>(a, st);
+      if (form == kFeScalars) return fe_launch<T, SUPA_AMD_FOREACH_POW, kFeScalars>(a, st);
+      return SUPA_AMD_EINVAL;
+    case SUPA_AMD_FOREACH_RPOW:
+      if (form == kFeScalars) return fe_launch<T, SUPA_AMD_FOREACH_RPOW, kFeScalars>(a, st);
+      return SUPA_AMD_EINVAL;
     SA_FE_UNARY(SUPA_AMD_SIGMOID)
     SA_FE_UNARY(SUPA_AMD_TANH)
     SA_FE_UNARY(SUPA_AMD_EXP)
@@ -178,6 +214,12 @@ int fe_dispatch(int op, int form, const FeArgs& a, hipStream_t st) {
     SA_FE_UNARY(SUPA_AMD_SQRT)
     SA_FE_UNARY(SUPA_AMD_EXPM1)
     SA_FE_UNARY(SUPA_AMD_LOG1P)
+    SA_FE_UNARY(SUPA_AMD_SIGN)
+    SA_FE_UNARY(SUPA_AMD_FLOOR)
+    SA_FE_UNARY(SUPA_AMD_CEIL)
+    SA_FE_UNARY(SUPA_AMD_ROUND)
+    SA_FE_UNARY(SUPA_AMD_TRUNC)
+    SA_FE_UNARY(SUPA_AMD_RSQRT)
     default: return SUPA_AMD_EINVAL;
   }
 #undef SA_FE_BINARY
@@ -218,7 +260,7 @@ __global__ void __launch_bounds__(kNormBlock)
 k_norm_partial(MtaTable tab, opmath_t<T>* __restrict__ ws) {
   using A = opmath_t<T>;
   constexpr int V = 16 / sizeof(T);
-  const MtaRange r = mta_range<CHUNK>(tab.chunk_start, tab.numel, tab.ntensors);
+  const MtaRange r = mta_range<CHUNK>(tab);
   const T* x = static_cast<const T*>(tab.in[0][r.k]);
   A acc = A(0);
   int64_t start = r.lo;
@@ -251,8 +293,8 @@ k_norm_final(MtaTable tab, const A* __restrict__ ws) {
 }
 
 // Chunks per table: tensors are packed kMtaTensors at a time, empty ones
-// included (they own no chunk; the bisection still finds the non-empty
-// tensor that owns a block because it takes the last equal start).
+// included (they own no chunk; the lookup still finds the non-empty tensor
+// that owns a block because it takes the last equal start).
 template <int64_t CHUNK, typename F>
 int norm_tables(int32_t n, const int64_t* numel, F&& per_table) {
   int i = 0;
@@ -274,6 +316,7 @@ int norm_tables(int32_t n, const int64_t* numel, F&& per_table) {
     }
     tab.chunk_start[nt] = chunks;
     tab.ntensors = nt;
+    mta_index(tab, chunks);
     const int rc = per_table(tab, chunks, first);
     if (rc) return rc;
   }

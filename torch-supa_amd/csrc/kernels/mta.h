@@ -3,16 +3,17 @@
 // One launch covers up to kMtaTensors tensors.  The tensor table (pointers,
 // element counts, chunk prefix sums) travels in the kernel arguments, so a
 // launch needs no device-side metadata and no allocation.  Each workgroup
-// owns one chunk of one tensor, found by bisection of the chunk prefix table.
+// owns one chunk of one tensor, found through a bucket index of the chunk
+// prefix table.
 // The reference's counterpart is upstream MultiTensorApply.cuh (kChunkSize
 // 65536, 512 threads, ILP 4, <= 110 / 36 tensors per launch).
 #pragma once
 
 #include "ew_launch.h"
+#include "mta_index.h"
 
 namespace sa {
 
-constexpr int kMtaTensors = 40;
 // One wavefront per workgroup: c5's fused AdamW moved 74 % of peak HBM
 // bandwidth with 64-thread workgroups against 71 % with 256 and 70 % with 128.
 constexpr int kMtaBlock = 64;
@@ -21,29 +22,17 @@ constexpr int kMtaBlock = 64;
 // at 256 threads: 71 % of HBM peak against 66 % with 16384-element chunks).
 template <typename T> constexpr int64_t chunk_one() { return (int64_t)kMtaBlock * (16 / (int64_t)sizeof(T)); }
 
-// The tensor whose chunk range holds block `blk`: the last k with
-// chunk_start[k] <= blk (chunk_start is strictly increasing), by bisection.
-__device__ __forceinline__ int find_tensor(const uint32_t* chunk_start, int nt, uint32_t blk) {
-  int lo = 0, hi = nt - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (chunk_start[mid] <= blk) lo = mid;
-    else hi = mid - 1;
-  }
-  return lo;
-}
-
 // The [lo, hi) element range of block `blk` within tensor k.
 struct MtaRange {
   int k;
   int64_t lo, hi;
 };
-template <int64_t CHUNK>
-__device__ __forceinline__ MtaRange mta_range(const uint32_t* chunk_start, const int64_t* numel, int nt) {
+template <int64_t CHUNK, typename Table>
+__device__ __forceinline__ MtaRange mta_range(const Table& tab) {
   MtaRange r;
-  r.k = find_tensor(chunk_start, nt, blockIdx.x);
-  r.lo = (int64_t)(blockIdx.x - chunk_start[r.k]) * CHUNK;
-  const int64_t n = numel[r.k];
+  r.k = find_tensor(tab, blockIdx.x);
+  r.lo = (int64_t)(blockIdx.x - tab.chunk_start[r.k]) * CHUNK;
+  const int64_t n = tab.numel[r.k];
   r.hi = r.lo + CHUNK < n ? r.lo + CHUNK : n;
   return r;
 }
@@ -52,8 +41,9 @@ __device__ __forceinline__ MtaRange mta_range(const uint32_t* chunk_start, const
 // tensors and fewer than 2^31 chunks, and launches once per table.
 //   fill(tab, slot, i)   copies tensor i's pointers into table slot `slot`
 //   launch(tab, chunks)  launches the kernel over one table
-// Table must have numel[], chunk_start[] and ntensors.  Empty tensors are
-// skipped; a negative numel is an argument error.
+// Table must have numel[], chunk_start[], ntensors, bucket[] and
+// bucket_shift.  Empty tensors are skipped; a negative numel is an argument
+// error.
 template <int64_t CHUNK, typename Table, typename Fill, typename Launch>
 int mta_for_tables(int32_t ntensors, const int64_t* numel, Fill&& fill, Launch&& launch) {
   int i = 0;
@@ -79,6 +69,7 @@ int mta_for_tables(int32_t ntensors, const int64_t* numel, Fill&& fill, Launch&&
     tab.chunk_start[nt] = chunks;
     tab.ntensors = nt;
     if (nt == 0) continue;
+    mta_index(tab, chunks);
     launch(tab, chunks);
     const int rc = launch_status();
     if (rc) return rc;

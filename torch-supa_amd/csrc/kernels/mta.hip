@@ -21,6 +21,8 @@ struct AdamTable {
   int64_t numel[kMtaTensors];
   uint32_t chunk_start[kMtaTensors + 1];
   int32_t ntensors;
+  uint32_t bucket_shift;
+  uint8_t bucket[kMtaBuckets];
 };
 
 struct AdamHyper {
@@ -89,7 +91,7 @@ __global__ void __launch_bounds__(kMtaBlock)
 k_adamw(AdamTable tab, AdamHyper h) {
   if (h.found_inf && *h.found_inf == 1.0f) return;
   constexpr int V = 16 / sizeof(T);
-  const MtaRange r = mta_range<CHUNK>(tab.chunk_start, tab.numel, tab.ntensors);
+  const MtaRange r = mta_range<CHUNK>(tab);
   const int k = r.k;
   const int64_t lo = r.lo, hi = r.hi;
   const double lr = h.lr_ptr ? (double)(*h.lr_ptr) : h.lr;
@@ -152,6 +154,8 @@ struct UnscaleTable {
   int64_t numel[kMtaTensors];
   uint32_t chunk_start[kMtaTensors + 1];
   int32_t ntensors;
+  uint32_t bucket_shift;
+  uint8_t bucket[kMtaBuckets];
 };
 
 template <typename T, int64_t CHUNK>
@@ -159,7 +163,7 @@ __global__ void __launch_bounds__(kMtaBlock)
 k_amp_unscale(UnscaleTable tab, float* __restrict__ found_inf, const float* __restrict__ inv_scale) {
   using C = opmath_t<T>;
   constexpr int V = 16 / sizeof(T);
-  const MtaRange r = mta_range<CHUNK>(tab.chunk_start, tab.numel, tab.ntensors);
+  const MtaRange r = mta_range<CHUNK>(tab);
   const int64_t lo = r.lo, hi = r.hi;
   T* x = static_cast<T*>(tab.x[r.k]);
   const C inv = (C)*inv_scale;
