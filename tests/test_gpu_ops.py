@@ -276,7 +276,7 @@ def test_cross_entropy_small_rows(dtype, no_fallback):
     out, tw = O.nll_loss(y, t.numpy(), None, "mean", -100)
     tol = 1e-5 if dtype == torch.float32 else 1e-2
     assert abs(loss.float().item() - float(out)) <= tol * abs(float(out))
-    twv = float(O.round_bf16(tw)) if dtype == torch.bfloat16 else float(tw)
+    twv = O.round_bf16(tw).item() if dtype == torch.bfloat16 else float(tw)
     gn = O.nll_loss_backward(np.ones(1, np.float32), t.numpy(), N, V, twv, None, "mean", -100,
                              bf16=dtype == torch.bfloat16)
     gcpu = lsm.grad.cpu().float().numpy()
