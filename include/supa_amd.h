@@ -145,6 +145,15 @@ int supa_amd_pointwise(const supa_amd_ew_desc* d, int op, double value, int64_t 
 #define SUPA_AMD_TRUNC 19
 #define SUPA_AMD_RSQRT 20
 #define SUPA_AMD_BITWISE_NOT 21
+/* Opt-in gelu forms free of the cancellation of 1 + erf / 1 + tanh for
+ * x << 0 (not the reference's arithmetic; the host selects them only when
+ * torch.supa.set_accurate_gelu_enabled(True) or SUPA_AMD_ACCURATE_GELU=1):
+ * GELU_LOGERFC = x - (x/2) erfc(|x|/sqrt2) (x >= 0) / (x/2) erfc(|x|/sqrt2)
+ * (x < 0); GELU_TANH_LOGISTIC = x / (1 + exp(-2u)), u = b (x + k x^3).
+ * Both are accepted by supa_amd_unary and supa_amd_unary_backward (whose
+ * GELU_TANH_LOGISTIC gradient is GELU_TANH's). */
+#define SUPA_AMD_GELU_LOGERFC 22
+#define SUPA_AMD_GELU_TANH_LOGISTIC 23
 
 /* out = f(x), floating dtypes (RELU, NEG and ABS also integer).  op = {out, x}.
  * Replaces the reference's upstream-ATen activation kernels: gelu.out NF:5216,
@@ -368,6 +377,7 @@ int supa_amd_bce_logits_backward(const supa_amd_ew_desc* d, int has_pos_weight, 
 int supa_amd_sum(const supa_amd_ew_desc* d, double scale, void* workspace,
                  int64_t workspace_bytes, void* stream);
 int64_t supa_amd_sum_workspace_bytes(int64_t numel);
+
 
 /* Reduction of the innermost `inner` elements of each of `outer` rows of a
  * contiguous input: out[r] = scale * sum(in[r*inner .. r*inner+inner)).

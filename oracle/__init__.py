@@ -27,6 +27,8 @@ _lib = None
 ADD, MUL, DIV, DIV_TRUNC, DIV_FLOOR, MAXIMUM, MINIMUM = 0, 1, 2, 3, 4, 5, 6
 ADDCMUL, ADDCDIV, LERP = 0, 1, 2
 GELU, GELU_TANH, SILU, SIGMOID, TANH, EXP, LOG, ERF, RELU, NEG, RECIPROCAL, ABS, SQRT, EXPM1, LOG1P = range(15)
+# the opt-in cancellation-free gelu forms (C-ABI codes SUPA_AMD_GELU_LOGERFC / _TANH_LOGISTIC)
+GELU_LOGERFC, GELU_TANH_LOGISTIC = 22, 23
 (ACT_LEAKY_RELU, ACT_HARDTANH, ACT_ELU, ACT_SOFTPLUS, ACT_HARDSWISH, ACT_HARDSIGMOID, ACT_MISH, ACT_LOG_SIGMOID,
  ACT_THRESHOLD) = range(9)
 MSE, SMOOTH_L1, BCE_LOGITS = 0, 1, 2
@@ -448,11 +450,19 @@ def rng_u32(seed: int, offset: int, n: int) -> np.ndarray:
     return out
 
 
-def uniform(seed: int, offset: int, n: int, lo=0.0, hi=1.0) -> np.ndarray:
+def uniform(seed: int, offset: int, n: int, lo=0.0, hi=1.0, dtype="f32") -> np.ndarray:
+    """uniform_(lo, hi) for storage dtype "f32", "bf16" or "f16", as float32
+    values: fma(u, hi - lo, lo) in float, rounded to the storage type, and a
+    value equal to hi rounded to that type replaced by lo (upstream
+    uniform_kernel, DistributionTemplates.h: the result stays in [lo, hi))."""
     scratch = np.empty(n, np.uint32)
     out = np.empty(n, np.float32)
     lib().or_uniform_f32(seed, offset, n, lo, hi, _p(scratch, _u32p), _p(out, _f32p))
-    return out
+    rnd = {"f32": lambda a: np.asarray(a, np.float32),
+           "bf16": lambda a: bf16_to_f32(f32_to_bf16(np.asarray(a, np.float32))),
+           "f16": lambda a: np.asarray(a, np.float32).astype(np.float16).astype(np.float32)}[dtype]
+    out = rnd(out)
+    return np.where(out == rnd(np.float32([hi]))[0], rnd(np.float32([lo]))[0], out).astype(np.float32)
 
 
 def normal(seed: int, offset: int, n: int, mean=0.0, std=1.0) -> np.ndarray:

@@ -175,7 +175,9 @@ void or_ternary_f32(int op, const float* a, const float* b, const float* c, floa
 enum {
   OR_GELU = 0, OR_GELU_TANH = 1, OR_SILU = 2, OR_SIGMOID = 3, OR_TANH = 4,
   OR_EXP = 5, OR_LOG = 6, OR_ERF = 7, OR_RELU = 8, OR_NEG = 9, OR_RECIPROCAL = 10, OR_ABS = 11,
-  OR_SQRT = 12, OR_EXPM1 = 13, OR_LOG1P = 14
+  OR_SQRT = 12, OR_EXPM1 = 13, OR_LOG1P = 14,
+  /* the opt-in cancellation-free gelu forms (same codes as the C ABI) */
+  OR_GELU_LOGERFC = 22, OR_GELU_TANH_LOGISTIC = 23
 };
 
 #define OR_SQRT1_2 0.70710678118654752440f
@@ -183,22 +185,32 @@ enum {
 #define OR_GELU_BETA_TANH 0.7978845608028654f /* M_SQRT2 * M_2_SQRTPI * 0.5  */
 #define OR_GELU_KAPPA 0.044715f
 
-/* Forward formulas (all in float32 opmath):
- *  gelu 'none': x*0.5*(1+erf(x*sqrt(1/2))) rewritten as x - (x/2) erfc(|x|/sqrt2)
- *               (x >= 0) or (x/2) erfc(|x|/sqrt2) (x < 0)   NF:5216, CPU Gelu.h:61-65
- *               (or_gelu_none: no cancellation of 1 + erf for x << 0)
- *  gelu 'tanh': 0.5*x*(1+tanh(b*(x+k*x^3))) rewritten exactly as
- *               x / (1 + exp(-2*b*(x+k*x^3)))         NF:5216, CPU Gelu.h:34-41
- *               (the identity 0.5*(1+tanh(u)) = 1/(1+exp(-2u)); it removes the
- *               cancellation of 1+tanh(u) for u << 0)
- *  silu:        x / (1 + exp(-x))                     NF:5374
- *  sigmoid:     1 / (1 + exp(-x))                     NF:5441
+/* Forward formulas (all in float32 opmath), in the reference's operation
+ * order (upstream GeluKernel.cu / CPU Gelu.h:34-41, 61-65):
+ *  gelu 'none': (x*0.5)*(1+erf(x*M_SQRT1_2))          NF:5216, CPU Gelu.h:61-65
+ *  gelu 'tanh': (0.5*x)*(1+tanh(b*(x+k*x^3))), x^3 = (x*x)*x and x + k*x^3
+ *               one fused multiply-add (the contraction the reference's
+ *               compilers apply)                       NF:5216, CPU Gelu.h:34-41
+ *  silu:        x / (1 + exp(-x))                      NF:5374
+ *  sigmoid:     1 / (1 + exp(-x))                      NF:5441
  *  tanh, exp, log, erf, expm1, log1p: the primitives of oracle_math.h;
- *  reciprocal, abs, sqrt: IEEE 1/x, |x| and correctly rounded sqrt. */
+ *  reciprocal, abs, sqrt: IEEE 1/x, |x| and correctly rounded sqrt.
+ * Opt-in forms (not the reference's arithmetic; they avoid the cancellation
+ * of 1 + erf and 1 + tanh for x << 0):
+ *  GELU_LOGERFC:        x - (x/2) erfc(|x|/sqrt2) (x >= 0), (x/2) erfc(|x|/sqrt2)
+ *                       (x < 0), erfc through log erfc (or_gelu_none)
+ *  GELU_TANH_LOGISTIC:  x / (1 + exp(-2*b*(x+k*x^3))) (the identity
+ *                       0.5*(1+tanh(u)) = 1/(1+exp(-2u))) */
+static inline float gelu_tanh_inner(float x) {
+  const float x3 = (x * x) * x;
+  return OR_GELU_BETA_TANH * fmaf(OR_GELU_KAPPA, x3, x);
+}
 static inline float act_fwd(int op, float x) {
   switch (op) {
-    case OR_GELU: return or_gelu_none(x);
-    case OR_GELU_TANH: {
+    case OR_GELU: return (x * 0.5f) * (1.0f + or_erff(x * OR_SQRT1_2));
+    case OR_GELU_TANH: return (0.5f * x) * (1.0f + or_tanhf(gelu_tanh_inner(x)));
+    case OR_GELU_LOGERFC: return or_gelu_none(x);
+    case OR_GELU_TANH_LOGISTIC: {
       const float x3 = (x * x) * x;
       const float inner = (-2.0f * OR_GELU_BETA_TANH) * fmaf(OR_GELU_KAPPA, x3, x);
       return x / (1.0f + or_expf(inner));
@@ -220,8 +232,10 @@ static inline float act_fwd(int op, float x) {
 }
 
 /* Backward formulas (upstream aten activation backward functors, float32):
- *  gelu 'none': dy*(cdf + x*pdf), cdf = Phi(x) (or_phif, the same erfc form),
- *               pdf = exp(-0.5*x*x) * (M_2_SQRTPI*M_SQRT1_2*0.5)     NF:5245
+ *  gelu 'none': dy*(cdf + x*pdf), cdf = 0.5*(1+erf(x*M_SQRT1_2)),
+ *               pdf = exp(-0.5*x*x) * (M_2_SQRTPI*M_SQRT1_2*0.5)      NF:5245
+ *               (GELU_LOGERFC: cdf = Phi(x) through the same erfc as its
+ *               forward, or_phif)
  *  gelu 'tanh': dy*(0.5*(1+t) + 0.5*x*(1-t*t)*b*(1+3k*x^2)),
  *               t = tanh(b*(x+k*x^3))                                NF:5245
  *  silu:        s = 1/(1+exp(-x)); dy*s*(1+x*(1-s))                  NF:5383
@@ -229,12 +243,14 @@ static inline float act_fwd(int op, float x) {
  *  tanh:        dy*(1-y*y)        (input is the forward output y) */
 static inline float act_bwd(int op, float dy, float x) {
   switch (op) {
-    case OR_GELU: {
-      const float cdf = or_phif(x);
+    case OR_GELU:
+    case OR_GELU_LOGERFC: {
+      const float cdf = (op == OR_GELU) ? 0.5f * (1.0f + or_erff(x * OR_SQRT1_2)) : or_phif(x);
       const float pdf = or_expf((-0.5f * x) * x) * OR_GELU_BETA_NONE;
       return dy * fmaf(x, pdf, cdf);
     }
-    case OR_GELU_TANH: {
+    case OR_GELU_TANH:
+    case OR_GELU_TANH_LOGISTIC: {
       const float x2 = x * x;
       const float x3 = x2 * x;
       const float inner = OR_GELU_BETA_TANH * fmaf(OR_GELU_KAPPA, x3, x);
@@ -745,7 +761,9 @@ void or_rng_u32(uint64_t seed, uint64_t offset, int64_t n, uint32_t* out) {
 static inline float or_u01(uint32_t r) { return (float)(r >> 8) * 5.9604644775390625e-08f; }
 
 /* uniform_(from, to): fma(u, to - from, from) in float, with `to - from`
- * rounded to float first. */
+ * rounded to float first (float32 storage; the front end rounds to a 16-bit
+ * storage type and maps a value equal to `to` back to `from`, as upstream's
+ * uniform_kernel does). */
 void or_uniform_f32(uint64_t seed, uint64_t offset, int64_t n, float lo, float hi, uint32_t* scratch, float* out) {
   or_rng_u32(seed, offset, n, scratch);
   const float range = hi - lo;
@@ -755,7 +773,8 @@ void or_uniform_f32(uint64_t seed, uint64_t offset, int64_t n, float lo, float h
 /* normal_(mean, std): Box-Muller in double on the word pairs (0, 1) and
  * (2, 3) of each Philox call; u1 = (hi24 + 1) 2^-24 in (0, 1], u2 = hi24
  * 2^-24; r = sqrt(-2 log u1), t = 2 pi u2; z = r cos t, r sin t;
- * out = (float)(mean + std z).  (The device evaluates sin / cos as
+ * out = (float)(mean + std z); a 16-bit storage type rounds that float
+ * once more.  (The device evaluates sin / cos as
  * sincospi(2 u2); the two differ by rounding far below float precision.) */
 void or_normal_f32(uint64_t seed, uint64_t offset, int64_t n, double mean, double stdv, float* out) {
   const double pi = 3.14159265358979323846;

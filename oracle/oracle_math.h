@@ -10,20 +10,22 @@
  * fma, division and ldexp (x86-64 with FMA3 here, gfx950 VALU there).
  *
  * The polynomials were fitted for this project (weighted least squares with
- * Lawson reweighting towards minimax, then rounded to binary32); they do not
- * come from any vendor math library.  Their accuracy against double-precision
- * libm is pinned by tests/test_oracle_math.py:
- *   or_expf  <= 1 ulp,  or_logf <= 1 ulp,  or_erff <= 2 ulp,  or_tanhf <= 2 ulp,
- *   or_expm1f <= 2 ulp, or_log1pf <= 2 ulp.
+ * Lawson reweighting towards minimax); they do not come from any vendor math
+ * library.  Their accuracy against double-precision libm (exhaustive over
+ * every binary32 input for erf and tanh) is pinned by
+ * tests/test_oracle_math.py:
+ *   or_expf <= 1.01 ulp, or_logf <= 0.94 ulp, or_erff <= 0.502 ulp,
+ *   or_tanhf <= 0.5001 ulp, or_expm1f <= 1.5 ulp, or_log1pf <= 2 ulp.
  *
  * The reductions used by every primitive:
  *   exp:  Cody-Waite split x = k*ln2 + r, |r| <= ln2/2, e^r = 1 + r + r^2 P(r).
  *   log:  x = m * 2^e with m in [sqrt(1/2), sqrt(2)), f = m - 1 (exact),
  *         log1p(f) = f - f^2/2 + f^3 Q(f).
- *   erf:  |x| < 0.921875: erf(x) = x + x P(x^2);
- *         otherwise erf(|x|) = 1 - exp(L(|x|)) with L ~ log(erfc) on
- *         [0.921875, 3.925); 1 beyond.
- *   tanh: |x| < 0.55: x + x^3 T(x^2); otherwise 1 - 2/(exp(2|x|)+1).
+ *   erf:  binary64 core: |x| < 0.921875: x P(x^2); otherwise
+ *         1 - Q(|x| - 2.4296875), Q ~ erfc on [0.921875, 3.9375); 1 beyond.
+ *   tanh: binary64 core: tanh(a) = m / (m + 2), m = e^{2a} - 1 from
+ *         2a = k ln2 + 2s and e^{2s} - 1 = s (2 + s Q(s)); the quotient
+ *         through Newton steps for 1 / (m + 2).
  */
 #ifndef SUPA_AMD_ORACLE_MATH_H
 #define SUPA_AMD_ORACLE_MATH_H
@@ -77,47 +79,95 @@ static inline float or_logf(float x) {
   return fmaf(ef, 0.693145751953125f, fmaf(ef, 1.42860677e-06f, y));
 }
 
+/* erf and tanh round a binary64 core once to binary32, so they are correctly
+ * rounded except where the exact value lies within the core's error of a
+ * binary32 rounding boundary.  Binary64 fma runs at the binary32 rate on the
+ * device, and only IEEE-specified operations are used (fma, multiply, add,
+ * divide, integer operations on the bits, conversions), so device and
+ * oracle agree bit for bit.
+ *
+ * erf: |x| < 0.921875: x P(x^2), P of degree 7 (relative error 2^-36.6
+ *      against erf(x)/x); 0.921875 <= |x| < 3.9375: 1 - Q(|x| - 2.4296875),
+ *      Q ~ erfc of degree 17 (absolute error 2^-33); beyond, +-1 (erfc(3.9375)
+ *      < 2^-25, so erf rounds to 1 there). */
 static inline float or_erff(float x) {
   const float a = fabsf(x);
+  double r;
   if (a < 0.921875f) {
-    const float s = x * x;
-    float p = 8.370234718313441e-05f;
-    p = fmaf(p, s, -0.0008142741280607879f);
-    p = fmaf(p, s, 0.005201036110520363f);
-    p = fmaf(p, s, -0.026859400793910027f);
-    p = fmaf(p, s, 0.11283695697784424f);
-    p = fmaf(p, s, -0.37612634897232056f);
-    p = fmaf(p, s, 0.12837916612625122f);
-    return fmaf(x, p, x);
+    const double d = (double)x;
+    const double s = d * d;  /* exact */
+    double p = -1.0281769310087121e-05;
+    p = fma(p, s, 0.00011451093107524197);
+    p = fma(p, s, -0.0008505904931369332);
+    p = fma(p, s, 0.005222301651988579);
+    p = fma(p, s, -0.026865807757633163);
+    p = fma(p, s, 0.11283787785379987);
+    p = fma(p, s, -0.37612638743636956);
+    p = fma(p, s, 1.128379167084688);
+    r = d * p;
+  } else {
+    const double t = (double)a - 2.4296875;  /* exact */
+    double q = -4.35060772382569e-08;
+    q = fma(q, t, 3.5200901969516026e-08);
+    q = fma(q, t, 7.491007346106996e-07);
+    q = fma(q, t, -1.545774571442501e-06);
+    q = fma(q, t, -3.911918849002945e-06);
+    q = fma(q, t, 1.9361311419525163e-05);
+    q = fma(q, t, -1.91757881378122e-05);
+    q = fma(q, t, -7.12297171015646e-05);
+    q = fma(q, t, 0.0003035279625931749);
+    q = fma(q, t, -0.0004350357024353315);
+    q = fma(q, t, -0.0003482345792284581);
+    q = fma(q, t, 0.003021214976043654);
+    q = fma(q, t, -0.007348327594475376);
+    q = fma(q, t, 0.010986727890450968);
+    q = fma(q, t, -0.011097466611553876);
+    q = fma(q, t, 0.007485125362503697);
+    q = fma(q, t, -0.0030806975343408726);
+    q = fma(q, t, 0.0005901597081677841);
+    r = copysign(1.0 - q, (double)x);
   }
-  float l = -5.02841658089892e-07f;
-  l = fmaf(l, a, -1.4578058653569315e-05f);
-  l = fmaf(l, a, 0.00039830547757446766f);
-  l = fmaf(l, a, -0.0040588537231087685f);
-  l = fmaf(l, a, 0.024906275793910027f);
-  l = fmaf(l, a, -0.10802615433931351f);
-  l = fmaf(l, a, -0.6335323452949524f);
-  l = fmaf(l, a, -1.1294389963150024f);
-  l = fmaf(l, a, 0.00016132958990056068f);
-  float r = 1.0f - or_expf(l);
-  r = (a >= 3.925f) ? 1.0f : r;
-  return copysignf(r, x);
+  float y = (float)r;
+  y = (a >= 3.9375f) ? copysignf(1.0f, x) : y;
+  return isnan(x) ? x : y;
 }
 
+/* tanh: with a = min(|x|, 9.5) (tanh(9.5) rounds to 1), 2a = k ln2 + 2s,
+ * |s| <= ln2/4, k from the 1.5 * 2^52 shifter (the low word of the sum);
+ * e^{2s} - 1 = s (2 + s Q(s)), Q of degree 6 (relative error 2^-37.5);
+ * m = e^{2a} - 1 = 2^k (e^{2s} - 1) + (2^k - 1), 2^k built from its exponent
+ * field, which keeps its relative accuracy as a -> 0; tanh(a) = m / (m + 2)
+ * with 1 / (m + 2) from four Newton steps off a seed read from the high word
+ * (0x7FDE6238 - hi: relative error <= 0.051). */
+static inline double or_hilo(uint32_t hi, uint32_t lo) {
+  const uint64_t u = ((uint64_t)hi << 32) | lo;
+  double d;
+  memcpy(&d, &u, 8);
+  return d;
+}
+static inline uint64_t or_bits64(double d) { uint64_t u; memcpy(&u, &d, 8); return u; }
 static inline float or_tanhf(float x) {
-  const float a = fabsf(x);
-  if (a < 0.55f) {
-    const float s = x * x;
-    float p = -0.006274243351072073f;
-    p = fmaf(p, s, 0.02107168175280094f);
-    p = fmaf(p, s, -0.05385231226682663f);
-    p = fmaf(p, s, 0.13332585990428925f);
-    p = fmaf(p, s, -0.33333316445350647f);
-    return fmaf(x * s, p, x);
-  }
-  const float e = or_expf(a + a);
-  const float r = 1.0f - 2.0f / (e + 1.0f);
-  return copysignf(r, x);
+  const float a = fminf(fabsf(x), 9.5f);
+  const double d = (double)a;
+  const double kb = fma(d, 2.8853900817779268, 6755399441055744.0);
+  const double k = kb - 6755399441055744.0;
+  const double s = fma(-k, 0.34657359027997264, d);
+  double q = 0.006347872054606616;
+  q = fma(q, s, 0.025478283984500305);
+  q = fma(q, s, 0.08888950583696928);
+  q = fma(q, s, 0.2666652497217727);
+  q = fma(q, s, 0.666666655245032);
+  q = fma(q, s, 1.3333333403307956);
+  q = fma(q, s, 2.000000000042128);
+  const double e = s * fma(s, q, 2.0);
+  const int32_t ki = (int32_t)(uint32_t)or_bits64(kb);
+  const double p2 = or_hilo((uint32_t)(ki + 1023) << 20, 0);
+  const double m = fma(p2, e, p2 - 1.0);
+  const double h = m + 2.0;
+  double y = or_hilo(0x7FDE6238u - (uint32_t)(or_bits64(h) >> 32), 0);
+  for (int i = 0; i < 4; ++i) y = fma(y, fma(-h, y, 1.0), y);
+  const float r = copysignf((float)(m * y), x);
+  return isnan(x) ? x : r;
 }
 
 /* gelu 'none' and the normal CDF through log erfc: t = |x| / sqrt(2)

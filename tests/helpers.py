@@ -52,3 +52,11 @@ def sample_f32(n, seed, lo=-30.0, hi=30.0):
     v = (s * mag).astype(np.float32)
     v = v[(v >= lo) & (v <= hi)]
     return np.concatenate([u, v])
+
+
+def f32_ulp(v):
+    """ulp of float32 values of magnitude |v| (2^-149 at and below the
+    subnormal range)."""
+    a = np.abs(np.asarray(v, np.float64))
+    e = np.frexp(np.where(np.isfinite(a), a, 3.4e38))[1]
+    return np.where(a == 0, 2.0 ** -149, np.ldexp(1.0, np.maximum(e - 24, -149)))

@@ -5,8 +5,10 @@ import os
 import numpy as np
 import pytest
 
+from scipy import special
+
 import oracle as O
-from helpers import f32_ulp_dist
+from helpers import f32_ulp, f32_ulp_dist
 
 G = np.load(os.path.join(os.path.dirname(__file__), "golden", "golden_cpu_aten.npz"))
 
@@ -24,11 +26,27 @@ def test_activations():
     a = G["a"]
     for op, key in [(O.SILU, "silu"), (O.SIGMOID, "sigmoid"), (O.TANH, "tanh")]:
         assert f32_ulp_dist(O.unary(op, a), G[key]).max() <= 2, key
-    xa = np.abs(a.astype(np.float64))
-    for op, key, slope in [(O.GELU, "gelu", 0.5e-6), (O.GELU_TANH, "gelu_tanh", 2.0 ** -24)]:
-        ref = G[key].astype(np.float64)
-        ulp = np.ldexp(1.0, np.maximum(np.frexp(np.abs(ref))[1] - 24, -149))
-        assert np.all(np.abs(O.unary(op, a) - ref) <= 2 * ulp + slope * xa), key
+    # gelu: 2 ulp, except where the float32 cancellation of 1 + erf / 1 + tanh
+    # carries a one-ulp difference of the rounded erf / tanh value into the
+    # output (the attribution of tests/test_gelu_parity.py: for 'tanh' one
+    # ulp of T = tanh(inner), for 'none' our derived bound plus the CPU's own
+    # distance from the exact function)
+    x = a.astype(np.float64)
+    ref = G["gelu_tanh"]
+    got = O.unary(O.GELU_TANH, a)
+    inner = np.float32(0.7978845608028654) * ((np.float32(0.044715) * ((a * a) * a)).astype(np.float64) + x).astype(np.float32)
+    far = f32_ulp_dist(got, ref) > 2
+    bound = 2 * f32_ulp(ref) + 0.5 * np.abs(x) * f32_ulp(O.unary(O.TANH, inner))
+    assert far.mean() <= 1e-3 and np.all(np.abs(got - ref.astype(np.float64))[far] <= bound[far])
+    ref = G["gelu"]
+    got = O.unary(O.GELU, a)
+    exact = 0.5 * x * special.erfc(-x / np.sqrt(2.0))
+    z = x * np.float32(0.70710678118654752440)
+    ours = 0.5 * np.abs(x) * (0.502 * f32_ulp(special.erf(z)) + 1.45 * 2.0 ** -24 * np.abs(z) * np.exp(-z * z)) \
+        + 1.5 * f32_ulp(exact)
+    far = f32_ulp_dist(got, ref) > 2
+    gap = np.abs(got - ref.astype(np.float64))
+    assert far.mean() <= 0.08 and np.all(gap[far] <= ours[far] + np.abs(ref - exact)[far])
 
 
 def test_log_softmax_and_cross_entropy():

@@ -25,6 +25,9 @@ def as_dtype(arr, dtype):
     return torch.from_numpy(arr).to(dtype)
 
 
+DT = {torch.float32: "f32", torch.bfloat16: "bf16", torch.float16: "f16"}
+
+
 def test_torch_manual_seed_reaches_the_device(supa):
     torch.manual_seed(1234)
     assert torch.supa.initial_seed() == 1234
@@ -41,8 +44,23 @@ def test_uniform_bitexact(n, dtype, no_fallback):
     seed, off = state()
     t.uniform_(-1.5, 2.5)
     assert state() == (seed, off + 1)
-    want = O.uniform(seed, off, n, -1.5, 2.5)
+    want = O.uniform(seed, off, n, -1.5, 2.5, DT[dtype])
     assert torch.equal(t.cpu(), as_dtype(want, dtype))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("lo, hi", [(0.0, 1.0), (1.0, 2.0), (-3.0, 100.0)])
+def test_uniform_stays_below_to(dtype, lo, hi, no_fallback):
+    """[from, to) for every dtype: a value that rounds to `to` in a 16-bit
+    type comes back as `from` (upstream's bound reversal), bit-exact with the
+    oracle on 4M draws."""
+    torch.supa.manual_seed(7)
+    t = torch.empty(1 << 22, dtype=dtype, device="supa")
+    seed, off = state()
+    t.uniform_(lo, hi)
+    c = t.cpu().float()
+    assert float(c.min()) >= lo and float(c.max()) < hi
+    assert torch.equal(t.cpu(), as_dtype(O.uniform(seed, off, t.numel(), lo, hi, DT[dtype]), dtype))
 
 
 def test_uniform_noncontiguous_and_misaligned(no_fallback):

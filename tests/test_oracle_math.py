@@ -22,8 +22,8 @@ EDGES = np.array([0.0, -0.0, 1e-45, -1e-45, 1e-38, 1.17549435e-38, 0.5, 1.0, 2.0
     [
         (O.EXP, np.exp, 1.01, -104.0, 89.0),
         (O.LOG, np.log, 0.94, 1e-30, 1e30),
-        (O.ERF, special.erf, 1.12, -6.0, 6.0),
-        (O.TANH, np.tanh, 1.47, -12.0, 12.0),
+        (O.ERF, special.erf, 0.503, -6.0, 6.0),
+        (O.TANH, np.tanh, 0.5002, -12.0, 12.0),
     ],
 )
 def test_primitive_accuracy(op, ref, bound, lo, hi):
@@ -63,20 +63,13 @@ def test_expm1_log1p_accuracy_and_edges():
     assert np.isnan(l[5])
 
 
-def test_gelu_none_against_exact():
-    """gelu 'none' through log erfc: within 1.6 ulp of x * Phi(x) in double for
-    x >= 0, 9 ulp down to -2 and 50 ulp down to -5.5 (the conditioning of
-    exp of a rounded argument); x * (1 + erf)/2 in float is off by thousands
-    of ulps there.  Beyond |x| = 5.55 the result is x or -0, as upstream's."""
-    x = np.concatenate([np.linspace(-6, 6, 600001), np.linspace(-1, 1, 200001)]).astype(np.float32)
-    exact = x.astype(np.float64) * special.ndtr(x.astype(np.float64))
-    err = ulp_vs_exact(O.unary(O.GELU, x), exact)
-    assert err[x >= 0].max() <= 1.6
-    assert err[(x < 0) & (x > -2)].max() <= 9.0
-    assert err[(x < 0) & (x > -5.5)].max() <= 50.0
-    tail = O.unary(O.GELU, np.float32([-6.0, -20.0, 6.0, 20.0, np.inf, np.nan]))
-    assert tail[0] == 0.0 and np.signbit(tail[0]) and tail[2] == 6.0 and tail[3] == 20.0 and tail[4] == np.inf
-    assert np.isnan(tail[5])
+def test_gelu_tails():
+    """Beyond |x| = 5.6 erf(x / sqrt2) rounds to +-1: gelu is x or -0 there,
+    as upstream's; inf and NaN propagate."""
+    for op in (O.GELU, O.GELU_TANH):
+        tail = O.unary(op, np.float32([-6.0, -20.0, 6.0, 20.0, np.inf, np.nan]))
+        assert tail[0] == 0.0 and np.signbit(tail[0]) and tail[1] == 0.0 and np.signbit(tail[1])
+        assert tail[2] == 6.0 and tail[3] == 20.0 and tail[4] == np.inf and np.isnan(tail[5])
 
 
 def test_primitive_edges():
@@ -124,20 +117,6 @@ def test_activation_vs_exact(op, exact):
     ex = exact(x.astype(np.float64))
     keep = np.abs(ex) > 1e-30
     assert ulp_vs_exact(got[keep], ex[keep]).max() <= 3.0
-
-
-def test_gelu_tanh_vs_exact():
-    """gelu 'tanh' = x / (1 + exp(v)), v = -2b(x + k x^3) formed in float32:
-    the few-ulp relative rounding of v is amplified by |v| in the result, so
-    the error against the exact function is at most 3 (1 + |v|) ulp."""
-    x = np.random.default_rng(7).standard_normal(1 << 20).astype(np.float32) * 3
-    xd = x.astype(np.float64)
-    v = -2 * math.sqrt(2 / math.pi) * (xd + 0.044715 * xd ** 3)
-    ex = xd / (1 + np.exp(v))
-    got = O.unary(O.GELU_TANH, x)
-    keep = np.abs(ex) > 1e-30
-    err = ulp_vs_exact(got[keep], ex[keep])
-    assert np.all(err <= 3.0 * (1.0 + np.abs(v[keep])))
 
 
 def test_gelu_none_error_is_the_reference_formula_conditioning():

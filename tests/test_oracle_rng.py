@@ -79,3 +79,22 @@ def test_normal_moments_and_pairs():
     assert abs(((z - z.mean()) ** 3).mean()) < 1e-2 and abs((z ** 4).mean() - 3) < 3e-2
     w = O.normal(21, 4, 1000, mean=2.0, std=0.5)
     np.testing.assert_allclose(w, (2.0 + 0.5 * z[:1000]).astype(np.float32), rtol=1e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("lo, hi", [(0.0, 1.0), (1.0, 2.0), (-3.0, 100.0)])
+def test_uniform_range_is_half_open(dtype, lo, hi):
+    """uniform_ stays in [from, to) after rounding to the storage type: about
+    0.2 % of bf16 draws on (0, 1) round up to 1.0 and are mapped back to
+    `from` (upstream uniform_kernel's bound reversal); float32 never rounds
+    up (u <= 1 - 2^-24)."""
+    u = O.uniform(3, 9, 1 << 22, lo, hi, dtype)
+    assert u.min() >= lo and u.max() < hi
+    raw = O.uniform(3, 9, 1 << 22, lo, hi, "f32")
+    if dtype == "f32":
+        assert np.array_equal(u, raw)
+    else:
+        # the only change besides rounding: values that rounded to `to`
+        rnd = O.bf16_to_f32(O.f32_to_bf16(raw)) if dtype == "bf16" else raw.astype(np.float16).astype(np.float32)
+        moved = rnd != u
+        assert np.all(rnd[moved] == np.float32(hi)) and np.all(u[moved] == np.float32(lo))

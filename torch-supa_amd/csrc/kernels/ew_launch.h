@@ -7,6 +7,7 @@
 #include <algorithm>
 
 #include "ew_engine.h"
+#include "split32.h"
 
 namespace sa {
 
@@ -35,42 +36,11 @@ inline int check_desc(const supa_amd_ew_desc* d, int min_ops, int max_ops) {
   return SUPA_AMD_OK;
 }
 
-// Calls fn(sub_desc) on pieces whose element count is below 2^31 (splitting
-// the outermost dims), so the 32-bit coordinate arithmetic of the N-d kernels
-// is exact.  The reference splits the same way (Loops.cuh:100-105).
+// Calls fn(sub_desc) on pieces whose element count is below 2^31, so the
+// 32-bit coordinate arithmetic of the N-d kernels is exact (split32.h).
 template <typename Fn>
 int for_each_32bit_piece(const supa_amd_ew_desc& d, Fn&& fn) {
-  const int64_t lim = (int64_t(1) << 31) - 1;
-  int64_t n = 1;
-  for (int i = 0; i < d.ndim; ++i) n *= d.sizes[i];
-  if (n <= lim) return fn(d);
-  const int last = d.ndim - 1;
-  int64_t inner = 1;
-  for (int i = 0; i < last; ++i) inner *= d.sizes[i];
-  const int64_t outer = d.sizes[last];
-  if (inner <= lim) {
-    const int64_t step = std::max<int64_t>(1, lim / std::max<int64_t>(inner, 1));
-    for (int64_t o = 0; o < outer; o += step) {
-      supa_amd_ew_desc s = d;
-      s.sizes[last] = std::min(step, outer - o);
-      for (int k = 0; k < d.noperands; ++k)
-        if (!s.op[k].is_scalar)
-          s.op[k].data = static_cast<char*>(d.op[k].data) + o * d.op[k].strides[last] * dtype_size(d.op[k].dtype);
-      const int rc = fn(s);
-      if (rc) return rc;
-    }
-    return SUPA_AMD_OK;
-  }
-  for (int64_t o = 0; o < outer; ++o) {
-    supa_amd_ew_desc s = d;
-    s.ndim = last;
-    for (int k = 0; k < d.noperands; ++k)
-      if (!s.op[k].is_scalar)
-        s.op[k].data = static_cast<char*>(d.op[k].data) + o * d.op[k].strides[last] * dtype_size(d.op[k].dtype);
-    const int rc = for_each_32bit_piece(s, fn);
-    if (rc) return rc;
-  }
-  return SUPA_AMD_OK;
+  return split_32bit(d, fn, [](int dtype) { return (int64_t)dtype_size(dtype); });
 }
 
 inline NdGeom make_geom(const supa_amd_ew_desc& d) {
@@ -168,7 +138,8 @@ int launch_static(const Op& op, const supa_amd_ew_desc& d, const int* tin, hipSt
       // write-only streams (fills) keep four wavefronts per workgroup: 83-85 %
       // of peak against 47-60 % with one
       constexpr int BS = N == 0 ? kBlock : kStreamBlock;
-      const int64_t blocks = std::max<int64_t>(1, (n / VEC + BS - 1) / BS);
+      constexpr int U = contig_unroll<Op>();
+      const int64_t blocks = std::max<int64_t>(1, (n / VEC + BS * U - 1) / (BS * U));
       k_contig<BS, VEC, Op, C, CT, OT, S...><<<dim3((unsigned)blocks), dim3(BS), 0, st>>>(op, a, n);
       return launch_status();
     }

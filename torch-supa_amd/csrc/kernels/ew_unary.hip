@@ -43,6 +43,8 @@ int supa_amd_unary(const supa_amd_ew_desc* d, int op, void* stream) {
     case SUPA_AMD_TRUNC: return run_unary<U_TRUNC, false>(d, stream);
     case SUPA_AMD_RSQRT: return run_unary<U_RSQRT, false>(d, stream);
     case SUPA_AMD_BITWISE_NOT: return run_unary<U_BITNOT, false>(d, stream);
+    case SUPA_AMD_GELU_LOGERFC: return run_unary<U_GELU_LOGERFC, false>(d, stream);
+    case SUPA_AMD_GELU_TANH_LOGISTIC: return run_unary<U_GELU_TANH_LOGISTIC, false>(d, stream);
     default: return SUPA_AMD_EINVAL;
   }
 }

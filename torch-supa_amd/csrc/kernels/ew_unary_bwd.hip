@@ -12,6 +12,8 @@ int supa_amd_unary_backward(const supa_amd_ew_desc* d, int op, void* stream) {
     case SUPA_AMD_SILU: return run_unary<U_SILU, true>(d, stream);
     case SUPA_AMD_SIGMOID: return run_unary<U_SIGMOID, true>(d, stream);
     case SUPA_AMD_TANH: return run_unary<U_TANH, true>(d, stream);
+    case SUPA_AMD_GELU_LOGERFC: return run_unary<U_GELU_LOGERFC, true>(d, stream);
+    case SUPA_AMD_GELU_TANH_LOGISTIC: return run_unary<U_GELU_TANH_LOGISTIC, true>(d, stream);
     default: return SUPA_AMD_EINVAL;
   }
 }

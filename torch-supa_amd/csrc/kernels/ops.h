@@ -102,19 +102,38 @@ static_assert((float)kGeluBetaNone == 0.3989422804014327f, "constant rounding");
 static_assert((float)kGeluBetaTanh == 0.7978845608028654f, "constant rounding");
 static_assert((float)kGeluKappa == 0.044715f, "constant rounding");
 
+// gelu in the reference's operation order (upstream GeluKernel.cu, CPU
+// Gelu.h:34-41 and 61-65): 'none' (x * 0.5) * (1 + erf(x * sqrt(1/2)));
+// 'tanh' (0.5 * x) * (1 + tanh(b * (x + k x^3))), x^3 = (x * x) * x and
+// x + k x^3 one fused multiply-add, as the reference's compilers contract it.
 template <typename C> __device__ __forceinline__ C gelu_none(C x) {
-  if constexpr (std::is_same<C, float>::value) return sa_gelu_none(x);
+  if constexpr (std::is_same<C, float>::value) return (x * 0.5f) * (1.0f + sa_erff(x * (float)kSqrt1_2));
   else return (x * C(0.5)) * (C(1) + erf(x * C(kSqrt1_2)));
 }
-// gelu 'tanh' as x * sigmoid(2u), u = b (x + k x^3): the same function as
-// 0.5 x (1 + tanh(u)) without the cancellation of 1 + tanh(u) for u << 0.
 template <typename C> __device__ __forceinline__ C gelu_tanh(C x) {
+  const C x3 = (x * x) * x;
   if constexpr (std::is_same<C, float>::value) {
-    const float x3 = (x * x) * x;
+    const float inner = (float)kGeluBetaTanh * fmaf((float)kGeluKappa, x3, x);
+    return (0.5f * x) * (1.0f + sa_tanhf_nn(inner));  // a NaN x makes 0.5 x NaN
+  } else {
+    const C inner = C(kGeluBetaTanh) * fma(C(kGeluKappa), x3, x);
+    return (C(0.5) * x) * (C(1) + tanh(inner));
+  }
+}
+// Opt-in cancellation-free forms (not the reference's arithmetic).  'none':
+// x - (x/2) erfc(|x|/sqrt2) for x >= 0, (x/2) erfc(|x|/sqrt2) for x < 0, erfc
+// through log erfc (sa_gelu_none); 'tanh': x / (1 + exp(-2u)), u = b (x + k
+// x^3), from 0.5 (1 + tanh(u)) = 1 / (1 + exp(-2u)).
+template <typename C> __device__ __forceinline__ C gelu_logerfc(C x) {
+  if constexpr (std::is_same<C, float>::value) return sa_gelu_none(x);
+  else return (x * C(0.5)) * erfc(-x * C(kSqrt1_2));
+}
+template <typename C> __device__ __forceinline__ C gelu_tanh_logistic(C x) {
+  const C x3 = (x * x) * x;
+  if constexpr (std::is_same<C, float>::value) {
     const float inner = (-2.0f * (float)kGeluBetaTanh) * fmaf((float)kGeluKappa, x3, x);
     return x / (1.0f + sa_expf_nn(inner));  // a NaN x makes the quotient NaN
   } else {
-    const C x3 = (x * x) * x;
     const C inner = C(-2.0 * kGeluBetaTanh) * fma(C(kGeluKappa), x3, x);
     return x / (C(1) + exp(inner));
   }
@@ -147,15 +166,21 @@ template <typename C> __device__ __forceinline__ C sigmoidx(C x) { return C(1) /
 
 enum UnaryKind {
   U_GELU = 0, U_GELU_TANH, U_SILU, U_SIGMOID, U_TANH, U_EXP, U_LOG, U_ERF, U_RELU, U_NEG, U_RECIPROCAL, U_ABS, U_SQRT,
-  U_EXPM1, U_LOG1P, U_SIGN, U_FLOOR, U_CEIL, U_ROUND, U_TRUNC, U_RSQRT, U_BITNOT
+  U_EXPM1, U_LOG1P, U_SIGN, U_FLOOR, U_CEIL, U_ROUND, U_TRUNC, U_RSQRT, U_BITNOT, U_GELU_LOGERFC,
+  U_GELU_TANH_LOGISTIC
 };
 
 template <int K, typename C> struct UnaryOp {
   static constexpr int arity = 1;
+  // binary64-core activations: arithmetic about as long as the memory time
+  static constexpr bool kHeavy = std::is_same<C, float>::value &&
+                                 (K == U_GELU || K == U_GELU_TANH || K == U_ERF || K == U_TANH);
   __device__ __forceinline__ C operator()(const C* v) const {
     const C x = v[0];
     if constexpr (K == U_GELU) return gelu_none<C>(x);
     else if constexpr (K == U_GELU_TANH) return gelu_tanh<C>(x);
+    else if constexpr (K == U_GELU_LOGERFC) return gelu_logerfc<C>(x);
+    else if constexpr (K == U_GELU_TANH_LOGISTIC) return gelu_tanh_logistic<C>(x);
     else if constexpr (K == U_SILU) {
       if constexpr (std::is_same<C, float>::value) return x / (1.0f + sa_expf_nn(-x));  // NaN x: NaN quotient
       else return x / (C(1) + expx<C>(-x));
@@ -208,15 +233,16 @@ template <int K, typename C> struct UnaryOp {
 // output (sigmoid, tanh); upstream aten activation backward formulas.
 template <int K, typename C> struct UnaryBwdOp {
   static constexpr int arity = 2;
+  static constexpr bool kHeavy = std::is_same<C, float>::value && (K == U_GELU || K == U_GELU_TANH);
   __device__ __forceinline__ C operator()(const C* v) const {
     const C dy = v[0], x = v[1];
-    if constexpr (K == U_GELU) {
+    if constexpr (K == U_GELU || K == U_GELU_LOGERFC) {
       C cdf;
-      if constexpr (std::is_same<C, float>::value) cdf = sa_phif(x);
-      else cdf = C(0.5) * (C(1) + erf(x * C(kSqrt1_2)));
+      if constexpr (K == U_GELU_LOGERFC && std::is_same<C, float>::value) cdf = sa_phif(x);
+      else cdf = C(0.5) * (C(1) + erfx<C>(x * C(kSqrt1_2)));
       const C pdf = expx<C>((C(-0.5) * x) * x) * C(kGeluBetaNone);
       return dy * muladd<C>(x, pdf, cdf);
-    } else if constexpr (K == U_GELU_TANH) {
+    } else if constexpr (K == U_GELU_TANH || K == U_GELU_TANH_LOGISTIC) {
       const C x2 = x * x;
       const C x3 = x2 * x;
       const C inner = C(kGeluBetaTanh) * muladd<C>(C(kGeluKappa), x3, x);

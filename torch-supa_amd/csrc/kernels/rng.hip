@@ -38,10 +38,13 @@ __device__ __forceinline__ uint32_t word(const uint4& r, int j) {
   return j == 0 ? r.x : (j == 1 ? r.y : (j == 2 ? r.z : r.w));
 }
 
-// MODE 0: uniform (a = lo, b = hi - lo); 1: bernoulli (a = p).
+// MODE 0: uniform (a = lo, b = hi - lo, c = hi): a value that rounds to hi
+// in T is replaced by lo, keeping [lo, hi) for 16-bit types (upstream
+// uniform_kernel's bound reversal, DistributionTemplates.h); 1: bernoulli
+// (a = p).
 template <typename T, int MODE>
 __global__ void __launch_bounds__(kBlock)
-k_rng_fill(T* __restrict__ out, int64_t n, uint64_t seed, uint64_t offset, float a, float b) {
+k_rng_fill(T* __restrict__ out, int64_t n, uint64_t seed, uint64_t offset, float a, float b, float c) {
   const uint64_t q = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
   const int64_t e0 = (int64_t)q * 4;
   if (e0 >= n) return;
@@ -52,20 +55,29 @@ k_rng_fill(T* __restrict__ out, int64_t n, uint64_t seed, uint64_t offset, float
     const float u = u01(word(r, j));
     v[j] = MODE == 0 ? fmaf(u, b, a) : (u < a ? 1.0f : 0.0f);
   }
-  if (e0 + 4 <= n && aligned(out + e0, 4 * sizeof(T))) {
-    Vec<T, 4> w;
+  T w[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) w.v[j] = from_arith<T>(v[j]);
-    *reinterpret_cast<Vec<T, 4>*>(out + e0) = w;
+  for (int j = 0; j < 4; ++j) {
+    w[j] = from_arith<T>(v[j]);
+    if constexpr (MODE == 0) {
+      if (to_arith(w[j]) == to_arith(from_arith<T>(c))) w[j] = from_arith<T>(a);
+    }
+  }
+  if (e0 + 4 <= n && aligned(out + e0, 4 * sizeof(T))) {
+    Vec<T, 4> wv;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) wv.v[j] = w[j];
+    *reinterpret_cast<Vec<T, 4>*>(out + e0) = wv;
   } else {
-    for (int j = 0; j < 4 && e0 + j < n; ++j) out[e0 + j] = from_arith<T>(v[j]);
+    for (int j = 0; j < 4 && e0 + j < n; ++j) out[e0 + j] = w[j];
   }
 }
 
 // normal(mean, std): Box-Muller on two words per pair of outputs, in double
 // (u1 = (hi24(w) + 1) 2^-24 in (0, 1], u2 = hi24(w') 2^-24): elements 4q + 0,1
 // are r cos(t), r sin(t) of words 0, 1, elements 4q + 2,3 of words 2, 3, with
-// r = sqrt(-2 log u1), t = 2 pi u2; out = mean + std z rounded once.
+// r = sqrt(-2 log u1), t = 2 pi u2; out = mean + std z in double, rounded to
+// float (and for a 16-bit storage type, from float to that type).
 __device__ __forceinline__ void box_muller(uint32_t w1, uint32_t w2, double& z0, double& z1) {
   const double u1 = ((double)(w1 >> 8) + 1.0) * 5.9604644775390625e-08;
   const double u2 = (double)(w2 >> 8) * 5.9604644775390625e-08;
@@ -149,7 +161,7 @@ int supa_amd_uniform(void* out, int32_t dtype, int64_t n, double lo, double hi, 
   const float a = (float)lo, b = (float)hi - (float)lo;
   return with_rng_storage(dtype, [&](auto* tag) -> int {
     using T = std::remove_pointer_t<decltype(tag)>;
-    k_rng_fill<T, 0><<<rng_blocks(n), kBlock, 0, st>>>(static_cast<T*>(out), n, seed, offset, a, b);
+    k_rng_fill<T, 0><<<rng_blocks(n), kBlock, 0, st>>>(static_cast<T*>(out), n, seed, offset, a, b, (float)hi);
     return launch_status();
   });
 }
@@ -161,7 +173,8 @@ int supa_amd_bernoulli(void* out, int32_t dtype, int64_t n, double p, uint64_t s
   hipStream_t st = static_cast<hipStream_t>(stream);
   return with_rng_storage(dtype, [&](auto* tag) -> int {
     using T = std::remove_pointer_t<decltype(tag)>;
-    k_rng_fill<T, 1><<<rng_blocks(n), kBlock, 0, st>>>(static_cast<T*>(out), n, seed, offset, (float)p, 0.0f);
+    k_rng_fill<T, 1><<<rng_blocks(n), kBlock, 0, st>>>(static_cast<T*>(out), n, seed, offset, (float)p, 0.0f,
+                                                        0.0f);
     return launch_status();
   });
 }
