@@ -30,9 +30,19 @@ void check_status(int status, const char* what);
 c10::DeviceIndex device_count() noexcept;
 c10::DeviceIndex current_device();
 void set_device(c10::DeviceIndex d);
-// The stream kernels are enqueued on for device d (the legacy default stream).
-hipStream_t current_stream(c10::DeviceIndex d);
-void synchronize(c10::DeviceIndex d);
+// Streams: per device a non-blocking default stream (id 0) and a pool of 32
+// (ids 1..32); the current stream is thread-local per device.
+hipStream_t current_stream(c10::DeviceIndex d);  // the current stream's handle
+hipStream_t stream_handle(c10::DeviceIndex d, c10::StreamId id);
+c10::Stream current_stream_obj(c10::DeviceIndex d);
+c10::Stream default_stream_obj(c10::DeviceIndex d);
+c10::Stream pool_stream(c10::DeviceIndex d);        // round-robin over the pool
+c10::Stream exchange_stream(const c10::Stream& s);  // makes s current on its device, returns the previous
+void synchronize(c10::DeviceIndex d);               // every stream of device d
+// Host <-> device copies ordered after the current stream's work; they return
+// once the copy is complete.
+void memcpy_h2d(void* dst, const void* src, size_t n, c10::DeviceIndex d);
+void memcpy_d2h(void* dst, const void* src, size_t n, c10::DeviceIndex d);
 c10::Allocator* allocator();
 
 struct AllocatorStats {
@@ -42,17 +52,23 @@ struct AllocatorStats {
   int64_t num_allocs = 0;
   int64_t num_device_mallocs = 0;
   int64_t num_frees = 0;
+  int64_t num_ooms_retried = 0;  // hipMalloc failures retried after releasing the cache
+  int64_t pending_blocks = 0;    // freed blocks waiting for other streams' events
 };
 AllocatorStats allocator_stats(c10::DeviceIndex d);
 void allocator_reset_peak(c10::DeviceIndex d);
 void allocator_empty_cache();
+// record_stream: the block holding ptr is also used on stream s.
+void allocator_record_stream(void* ptr, const c10::Stream& s);
+// Test hook: the next n device allocations fail as out of memory.
+void allocator_inject_oom(int n);
 
-// Per-device scratch owned by the runtime: allocated and zeroed once, never
-// returned to the caching allocator.  Holds the reduction workspace (whose
-// counter every reduction leaves at zero) and the device error flag.
+// Per-device state owned by the runtime, allocated and zeroed once: the
+// device error flag, which kernels only ever set (to report an out-of-range
+// target) and the host clears when it reads it.  Reduction workspaces are not
+// here: they come from the caching allocator per call, ordered on the
+// calling stream.
 struct DeviceScratch {
-  void* reduce_ws = nullptr;
-  int64_t reduce_ws_bytes = 0;
   int32_t* error_flag = nullptr;
 };
 const DeviceScratch& device_scratch(c10::DeviceIndex d);
@@ -70,6 +86,10 @@ bool fused_cross_entropy_enabled();
 // One-pass BCE-with-logits gradient (default on, env SUPA_AMD_FUSED_BCE=0 turns it off).
 void set_fused_bce_backward_enabled(bool on);
 bool fused_bce_backward_enabled();
+// Cancellation-free gelu forms instead of the reference's (x/2)(1 + erf) and
+// (x/2)(1 + tanh) (opt-in; default off, env SUPA_AMD_ACCURATE_GELU=1 turns it on).
+void set_accurate_gelu_enabled(bool on);
+bool accurate_gelu_enabled();
 std::vector<std::pair<std::string, int64_t>> fallback_counts();
 void reset_fallback_counts();
 // The boxed CPU fallback itself (counted; an error while disabled), for

@@ -1,5 +1,5 @@
-// Python module torch_supa._C: device queries, allocator statistics, CPU
-// fallback control, timing events, and the planner (exposed for the CPU test
+// Python module torch_supa._C: device queries, streams and events, allocator
+// statistics, CPU fallback control, and the planner (exposed for the CPU test
 // tier).  The reference's counterpart is torch_supa/csrc/InitSupaBindings.cpp
 // plus csrc/supa/Module.cpp:1133-1162 (device/stream/memory APIs).
 #include <pybind11/pybind11.h>
@@ -23,6 +23,8 @@ py::dict memory_stats(int dev) {
   d["num_allocs"] = s.num_allocs;
   d["num_device_mallocs"] = s.num_device_mallocs;
   d["num_frees"] = s.num_frees;
+  d["num_ooms_retried"] = s.num_ooms_retried;
+  d["pending_blocks"] = s.pending_blocks;
   return d;
 }
 
@@ -60,8 +62,47 @@ uintptr_t event_create() {
   SUPA_HIP_CHECK(hipEventCreate(&e));
   return reinterpret_cast<uintptr_t>(e);
 }
-void event_record(uintptr_t e) {
-  SUPA_HIP_CHECK(hipEventRecord(reinterpret_cast<hipEvent_t>(e), supa::current_stream(supa::current_device())));
+// Records on stream `id` of device `dev` (-1: the current device / stream).
+void event_record(uintptr_t e, int dev, int64_t id) {
+  const auto d = dev < 0 ? supa::current_device() : static_cast<c10::DeviceIndex>(dev);
+  const hipStream_t st = id < 0 ? supa::current_stream(d) : supa::stream_handle(d, id);
+  SUPA_HIP_CHECK(hipEventRecord(reinterpret_cast<hipEvent_t>(e), st));
+}
+// Stream `id` of device `dev` waits for the event.
+void event_wait(uintptr_t e, int dev, int64_t id) {
+  const auto d = dev < 0 ? supa::current_device() : static_cast<c10::DeviceIndex>(dev);
+  const hipStream_t st = id < 0 ? supa::current_stream(d) : supa::stream_handle(d, id);
+  SUPA_HIP_CHECK(hipStreamWaitEvent(st, reinterpret_cast<hipEvent_t>(e), 0));
+}
+bool event_query(uintptr_t e) {
+  const hipError_t rc = hipEventQuery(reinterpret_cast<hipEvent_t>(e));
+  if (rc == hipErrorNotReady) {
+    (void)hipGetLastError();
+    return false;
+  }
+  SUPA_HIP_CHECK(rc);
+  return true;
+}
+int64_t current_stream_id(int dev) { return supa::current_stream_obj(static_cast<c10::DeviceIndex>(dev)).id(); }
+int64_t set_current_stream_id(int dev, int64_t id) {
+  const c10::Stream s(c10::Stream::UNSAFE, c10::Device(supa::kSupa, static_cast<c10::DeviceIndex>(dev)), id);
+  return supa::exchange_stream(s).id();
+}
+int64_t pool_stream_id(int dev) { return supa::pool_stream(static_cast<c10::DeviceIndex>(dev)).id(); }
+uintptr_t stream_ptr(int dev, int64_t id) {
+  return reinterpret_cast<uintptr_t>(supa::stream_handle(static_cast<c10::DeviceIndex>(dev), id));
+}
+void stream_synchronize(int dev, int64_t id) {
+  SUPA_HIP_CHECK(hipStreamSynchronize(supa::stream_handle(static_cast<c10::DeviceIndex>(dev), id)));
+}
+bool stream_query(int dev, int64_t id) {
+  const hipError_t rc = hipStreamQuery(supa::stream_handle(static_cast<c10::DeviceIndex>(dev), id));
+  if (rc == hipErrorNotReady) {
+    (void)hipGetLastError();
+    return false;
+  }
+  SUPA_HIP_CHECK(rc);
+  return true;
 }
 void event_synchronize(uintptr_t e) { SUPA_HIP_CHECK(hipEventSynchronize(reinterpret_cast<hipEvent_t>(e))); }
 float event_elapsed_ms(uintptr_t a, uintptr_t b) {
@@ -121,12 +162,27 @@ PYBIND11_MODULE(_C, m) {
   m.def("fused_cross_entropy_enabled", &supa::fused_cross_entropy_enabled);
   m.def("set_fused_bce_backward_enabled", &supa::set_fused_bce_backward_enabled);
   m.def("fused_bce_backward_enabled", &supa::fused_bce_backward_enabled);
+  m.def("set_accurate_gelu_enabled", &supa::set_accurate_gelu_enabled);
+  m.def("accurate_gelu_enabled", &supa::accurate_gelu_enabled);
   m.def("fallback_counts", &supa::fallback_counts);
   m.def("reset_fallback_counts", &supa::reset_fallback_counts);
   m.def("plan", &plan);
   m.def("abi_version", []() { return supa_amd_abi_version(); });
   m.def("event_create", &event_create);
-  m.def("event_record", &event_record);
+  m.def("event_record", &event_record, py::arg("event"), py::arg("device") = -1, py::arg("stream_id") = -1);
+  m.def("event_wait", &event_wait, py::arg("event"), py::arg("device") = -1, py::arg("stream_id") = -1);
+  m.def("event_query", &event_query);
+  m.def("current_stream_id", &current_stream_id);
+  m.def("set_current_stream_id", &set_current_stream_id);
+  m.def("pool_stream_id", &pool_stream_id);
+  m.def("stream_ptr", &stream_ptr);
+  m.def("stream_synchronize", &stream_synchronize);
+  m.def("stream_query", &stream_query);
+  m.def("record_stream", [](const at::Tensor& t, int dev, int64_t id) {
+    const c10::Stream s(c10::Stream::UNSAFE, c10::Device(supa::kSupa, static_cast<c10::DeviceIndex>(dev)), id);
+    supa::allocator_record_stream(t.storage().data_ptr().get(), s);
+  });
+  m.def("inject_oom", [](int n) { supa::allocator_inject_oom(n); });
   m.def("event_synchronize", &event_synchronize);
   m.def("event_elapsed_ms", &event_elapsed_ms);
   m.def("event_destroy", &event_destroy);

@@ -231,7 +231,7 @@ at::Tensor copy_from(const at::Tensor& self, const at::Tensor& dst, bool /*non_b
     TORCH_CHECK(self.device().is_cpu(), "supa copy: unsupported source device ", self.device());
     if (dst.is_contiguous()) {
       at::Tensor h = self.to(dst.scalar_type()).expand(dst.sizes()).contiguous();
-      SUPA_HIP_CHECK(hipMemcpy(dst.data_ptr(), h.data_ptr(), dst.nbytes(), hipMemcpyHostToDevice));
+      memcpy_h2d(dst.data_ptr(), h.data_ptr(), dst.nbytes(), dst.device().index());
     } else {
       at::Tensor tmp = empty_supa(dst.sizes(), dst.scalar_type(), dst.device().index());
       copy_from(self, tmp, false);
@@ -241,20 +241,21 @@ at::Tensor copy_from(const at::Tensor& self, const at::Tensor& dst, bool /*non_b
   }
   // device -> host
   TORCH_CHECK(dst.device().is_cpu(), "supa copy: unsupported destination device ", dst.device());
-  check_device_errors(self.device().index());
+  const auto dev = self.device().index();
   at::Tensor src = self;
   if (!src.is_contiguous()) {
-    at::Tensor tmp = empty_supa(src.sizes(), src.scalar_type(), src.device().index());
+    at::Tensor tmp = empty_supa(src.sizes(), src.scalar_type(), dev);
     copy_from(src, tmp, false);
     src = tmp;
   }
   if (dst.is_contiguous() && dst.scalar_type() == src.scalar_type() && dst.sizes() == src.sizes()) {
-    SUPA_HIP_CHECK(hipMemcpy(dst.data_ptr(), src.data_ptr(), dst.nbytes(), hipMemcpyDeviceToHost));
+    memcpy_d2h(dst.data_ptr(), src.data_ptr(), dst.nbytes(), dev);
   } else {
     at::Tensor h = at::empty(src.sizes(), src.options().device(at::kCPU));
-    SUPA_HIP_CHECK(hipMemcpy(h.data_ptr(), src.data_ptr(), h.nbytes(), hipMemcpyDeviceToHost));
+    memcpy_d2h(h.data_ptr(), src.data_ptr(), h.nbytes(), dev);
     dst.copy_(h);
   }
+  check_device_errors(dev);  // the kernels that produced src are done
   return dst;
 }
 
@@ -269,7 +270,7 @@ at::Tensor copy_from_and_resize(const at::Tensor& self, const at::Tensor& dst) {
 c10::Scalar local_scalar_dense(const at::Tensor& self) {
   TORCH_CHECK(self.numel() == 1, "a Tensor with ", self.numel(), " elements cannot be converted to Scalar");
   at::Tensor h = at::empty({}, self.options().device(at::kCPU));
-  SUPA_HIP_CHECK(hipMemcpy(h.data_ptr(), self.data_ptr(), self.dtype().itemsize(), hipMemcpyDeviceToHost));
+  memcpy_d2h(h.data_ptr(), self.data_ptr(), self.dtype().itemsize(), self.device().index());
   check_device_errors(self.device().index());
   return h.item();
 }
@@ -746,8 +747,9 @@ at::Tensor unary_bwd(const at::Tensor& grad, const at::Tensor& x, at::Tensor out
 }
 
 int gelu_op(c10::string_view approximate) {
-  if (approximate == "none") return SUPA_AMD_GELU;
-  if (approximate == "tanh") return SUPA_AMD_GELU_TANH;
+  const bool acc = accurate_gelu_enabled();
+  if (approximate == "none") return acc ? SUPA_AMD_GELU_LOGERFC : SUPA_AMD_GELU;
+  if (approximate == "tanh") return acc ? SUPA_AMD_GELU_TANH_LOGISTIC : SUPA_AMD_GELU_TANH;
   TORCH_CHECK(false, "approximate argument must be either none or tanh.");
 }
 

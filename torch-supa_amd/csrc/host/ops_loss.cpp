@@ -75,10 +75,13 @@ void reduce_apply(const at::Tensor& out, const std::vector<at::Tensor>& ins, c10
     o.dtype = dtype_code(ins[k].scalar_type());
     for (int i = 0; i < d.ndim; ++i) o.strides[i] = plan.it_strides[1 + k][i];
   }
-  const DeviceScratch& s = device_scratch(dev);
   const auto prev = current_device();
   if (prev != dev) set_device(dev);
-  const int rc = launch(&d, s.reduce_ws, s.reduce_ws_bytes, current_stream(dev));
+  // the two-stage reduction's partials: a per-call block of the stream-ordered
+  // caching allocator (no content requirement)
+  const int64_t ws_bytes = std::max(supa_amd_sum_workspace_bytes(0), supa_amd_loss_workspace_bytes(0));
+  const at::Tensor ws = empty_supa({ws_bytes}, at::kByte, dev);
+  const int rc = launch(&d, ws.data_ptr(), ws_bytes, current_stream(dev));
   if (prev != dev) set_device(prev);
   check_status(rc, name);
 }
@@ -604,9 +607,11 @@ std::tuple<at::Tensor&, at::Tensor&> nll2d_fwd_into(const at::Tensor& self, cons
   if (red == SUPA_AMD_REDUCTION_NONE) tw.zero_();
   at::Tensor res = out.is_contiguous() ? out : empty_supa(oshape, self.scalar_type(), dev);
   const DeviceScratch& s = device_scratch(dev);
+  const int64_t ws_bytes = supa_amd_nll_loss2d_workspace_bytes();
+  const at::Tensor ws = empty_supa({ws_bytes}, at::kByte, dev);
   const int rc = supa_amd_nll_loss2d_forward(x.data_ptr(), dtype_code(x.scalar_type()), t.data_ptr<int64_t>(),
                                              w.defined() ? w.data_ptr() : nullptr, n, c, sp, red, ignore_index,
-                                             res.data_ptr(), tw.data_ptr(), s.reduce_ws, s.reduce_ws_bytes,
+                                             res.data_ptr(), tw.data_ptr(), ws.data_ptr(), ws_bytes,
                                              s.error_flag, current_stream(dev));
   check_status(rc, "nll_loss2d_forward");
   if (!res.is_same(out)) out.copy_(res);

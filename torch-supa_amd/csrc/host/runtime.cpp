@@ -7,14 +7,24 @@
 // SUPAGuardImpl (C10_REGISTER_GUARD_IMPL at impl/SUPAGuardImpl.cpp:254),
 // SUPAHooks, and the CPU fallback of aten/VariableFallbackKernel.cpp:31-64.
 //
+// Streams.  Each device has a default stream and a pool of 32 streams, all
+// created non-blocking (so they never serialise with the legacy NULL stream
+// other HIP code in the process uses) at the default priority; the current
+// stream is thread-local per device, as SUPAStream.cpp:26-27,147 keeps it.
+// A c10::Stream id is 0 for the default stream and 1..32 for the pool.
+//
 // Allocator design.  Device memory comes from hipMalloc in size classes
 // (512 B granules below 1 MiB, 2 MiB granules above) and is cached per device
-// on free.  All kernels of this library run on one stream per device, so a
-// block freed by the caller is reusable by the next allocation immediately:
-// stream order already places the new user after the old one.  When hipMalloc
-// fails the cache is released and the allocation retried once before an
-// OutOfMemoryError.  Blocks are never split, so a cached block is reused only
-// by a request of at least half its size.
+// and per stream on free: a block belongs to the stream current when it was
+// allocated, and a freed block is reused only by allocations on that stream,
+// which stream order makes safe.  record_stream(t, s) marks a block as used
+// on another stream too; freeing it then records an event on each such
+// stream and the block returns to its pool once every event has completed
+// (the semantics of SUPACachingAllocator's recordStream, RecordStream.cpp:10-16).
+// When hipMalloc fails the cache, including blocks still waiting on events
+// (after waiting for them), is released and the allocation retried once
+// before an OutOfMemoryError.  Blocks are never split, so a cached block is
+// reused only by a request of at least half its size.
 #include <ATen/detail/PrivateUse1HooksInterface.h>
 #include <ATen/native/CPUFallback.h>
 #include <c10/core/Allocator.h>
@@ -30,6 +40,7 @@
 #include <map>
 #include <mutex>
 #include <unordered_map>
+#include <vector>
 
 #include "common.h"
 
@@ -86,7 +97,82 @@ void set_device(c10::DeviceIndex d) {
   }
 }
 
-hipStream_t current_stream(c10::DeviceIndex /*d*/) { return nullptr; }
+// --------------------------------------------------------------- streams
+namespace {
+constexpr int kStreamDevices = 64;
+constexpr int kPoolStreams = 32;
+
+struct DeviceStreams {
+  std::once_flag once;
+  hipStream_t def = nullptr;
+  hipStream_t pool[kPoolStreams] = {};
+  std::atomic<uint32_t> next{0};
+};
+DeviceStreams g_streams[kStreamDevices];
+thread_local c10::StreamId tls_stream[kStreamDevices] = {};
+
+DeviceStreams& streams_of(c10::DeviceIndex d) {
+  TORCH_CHECK(d >= 0 && d < kStreamDevices && d < device_count(), "supa: invalid device index ", int(d));
+  DeviceStreams& ds = g_streams[d];
+  std::call_once(ds.once, [&ds, d] {
+    int prev = 0;
+    SUPA_HIP_CHECK(hipGetDevice(&prev));
+    SUPA_HIP_CHECK(hipSetDevice(d));
+    SUPA_HIP_CHECK(hipStreamCreateWithFlags(&ds.def, hipStreamNonBlocking));
+    for (auto& st : ds.pool) SUPA_HIP_CHECK(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
+    SUPA_HIP_CHECK(hipSetDevice(prev));
+  });
+  return ds;
+}
+}  // namespace
+
+hipStream_t stream_handle(c10::DeviceIndex d, c10::StreamId id) {
+  DeviceStreams& ds = streams_of(d);
+  if (id == 0) return ds.def;
+  TORCH_CHECK(id >= 1 && id <= kPoolStreams, "supa: unknown stream id ", id, " on device ", int(d));
+  return ds.pool[id - 1];
+}
+
+c10::Stream current_stream_obj(c10::DeviceIndex d) {
+  (void)streams_of(d);
+  return c10::Stream(c10::Stream::UNSAFE, c10::Device(kSupa, d), tls_stream[d]);
+}
+
+c10::Stream pool_stream(c10::DeviceIndex d) {
+  DeviceStreams& ds = streams_of(d);
+  const uint32_t k = ds.next.fetch_add(1) % kPoolStreams;
+  return c10::Stream(c10::Stream::UNSAFE, c10::Device(kSupa, d), (c10::StreamId)(k + 1));
+}
+
+c10::Stream default_stream_obj(c10::DeviceIndex d) {
+  (void)streams_of(d);
+  return c10::Stream(c10::Stream::UNSAFE, c10::Device(kSupa, d), 0);
+}
+
+c10::Stream exchange_stream(const c10::Stream& s) {
+  const c10::DeviceIndex d = s.device_index();
+  (void)stream_handle(d, s.id());  // validates
+  const c10::Stream old = current_stream_obj(d);
+  tls_stream[d] = s.id();
+  return old;
+}
+
+hipStream_t current_stream(c10::DeviceIndex d) {
+  DeviceStreams& ds = streams_of(d);
+  const c10::StreamId id = tls_stream[d];
+  return id == 0 ? ds.def : ds.pool[id - 1];
+}
+
+void memcpy_h2d(void* dst, const void* src, size_t n, c10::DeviceIndex d) {
+  const hipStream_t st = current_stream(d);
+  SUPA_HIP_CHECK(hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, st));
+  SUPA_HIP_CHECK(hipStreamSynchronize(st));
+}
+void memcpy_d2h(void* dst, const void* src, size_t n, c10::DeviceIndex d) {
+  const hipStream_t st = current_stream(d);
+  SUPA_HIP_CHECK(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, st));
+  SUPA_HIP_CHECK(hipStreamSynchronize(st));
+}
 
 void synchronize(c10::DeviceIndex d) {
   const auto prev = current_device();
@@ -106,18 +192,15 @@ const DeviceScratch& device_scratch(c10::DeviceIndex d) {
   TORCH_CHECK(d >= 0 && d < kScratchDevices, "supa: device index out of range");
   std::lock_guard<std::mutex> g(g_scratch_mu);
   DeviceScratch& s = g_scratch[d];
-  if (!s.reduce_ws) {
+  if (!s.error_flag) {
     const auto prev = current_device();
     if (prev != d) set_device(d);
-    const int64_t ws = std::max({supa_amd_sum_workspace_bytes(0), supa_amd_loss_workspace_bytes(0),
-                                 supa_amd_nll_loss2d_workspace_bytes()});
-    const int64_t ws_rounded = (ws + 255) / 256 * 256;
     void* p = nullptr;
-    SUPA_HIP_CHECK(hipMalloc(&p, ws_rounded + 256));
-    SUPA_HIP_CHECK(hipMemset(p, 0, ws_rounded + 256));
-    s.reduce_ws = p;
-    s.reduce_ws_bytes = ws;
-    s.error_flag = reinterpret_cast<int32_t*>(static_cast<char*>(p) + ws_rounded);
+    SUPA_HIP_CHECK(hipMalloc(&p, 256));
+    const hipStream_t st = stream_handle(d, 0);
+    SUPA_HIP_CHECK(hipMemsetAsync(p, 0, 256, st));
+    SUPA_HIP_CHECK(hipStreamSynchronize(st));
+    s.error_flag = static_cast<int32_t*>(p);
     if (prev != d) set_device(prev);
   }
   return s;
@@ -131,10 +214,10 @@ void check_device_errors(c10::DeviceIndex d) {
     flag = g_scratch[d].error_flag;
   }
   int32_t h = 0;
-  SUPA_HIP_CHECK(hipMemcpy(&h, flag, sizeof(h), hipMemcpyDeviceToHost));
+  memcpy_d2h(&h, flag, sizeof(h), d);
   if (h != 0) {
     const int32_t zero = 0;
-    SUPA_HIP_CHECK(hipMemcpy(flag, &zero, sizeof(zero), hipMemcpyHostToDevice));
+    memcpy_h2d(flag, &zero, sizeof(zero), d);
     TORCH_CHECK_INDEX(false, "supa: a kernel reported an out-of-bounds target index (nll_loss target outside "
                              "[0, n_classes) and not ignore_index)");
   }
@@ -156,6 +239,14 @@ struct Block {
   void* ptr;
   size_t size;
   int device;
+  hipStream_t stream;                // the stream current at allocation: owns the block's reuse
+  std::vector<hipStream_t> uses;     // other streams recorded by record_stream
+};
+
+// A freed block waiting for the events recorded on the streams that used it.
+struct Pending {
+  Block block;
+  std::vector<hipEvent_t> events;
 };
 
 class CachingAllocator final : public c10::Allocator {
@@ -164,27 +255,24 @@ class CachingAllocator final : public c10::Allocator {
     const int dev = current_device();
     if (nbytes == 0) return {nullptr, nullptr, &CachingAllocator::raw_delete, c10::Device(kSupa, dev)};
     const size_t sz = round_size(nbytes);
+    const hipStream_t st = current_stream(dev);
     void* p = nullptr;
     {
       std::lock_guard<std::mutex> g(mu_);
-      auto& fl = free_[dev];
-      auto it = fl.lower_bound(sz);
-      if (it != fl.end() && it->first <= 2 * sz) {
-        p = it->second;
-        const size_t bsz = it->first;
-        fl.erase(it);
-        live_[p] = Block{p, bsz, dev};
-        account_alloc(dev, bsz, false);
-      }
+      process_pending_locked(dev, false);
+      p = take_cached_locked(dev, st, sz);
     }
-    if (!p) p = device_malloc(dev, sz);
+    if (!p) p = device_malloc(dev, st, sz);
     return {p, p, &CachingAllocator::raw_delete, c10::Device(kSupa, dev)};
   }
 
   c10::DeleterFnPtr raw_deleter() const override { return &CachingAllocator::raw_delete; }
 
   void copy_data(void* dest, const void* src, std::size_t count) const override {
-    SUPA_HIP_CHECK(hipMemcpy(dest, src, count, hipMemcpyDeviceToDevice));
+    const int dev = current_device();
+    const hipStream_t st = current_stream(dev);
+    SUPA_HIP_CHECK(hipMemcpyAsync(dest, src, count, hipMemcpyDeviceToDevice, st));
+    SUPA_HIP_CHECK(hipStreamSynchronize(st));
   }
 
   static void raw_delete(void* p) {
@@ -193,32 +281,127 @@ class CachingAllocator final : public c10::Allocator {
 
   static CachingAllocator& instance();
 
+  // The block holding p is also used on stream st (record_stream): its reuse
+  // waits for the work st has queued when the block is freed.
+  void record_stream(void* p, hipStream_t st) {
+    std::lock_guard<std::mutex> g(mu_);
+    auto it = live_.find(p);
+    TORCH_CHECK(it != live_.end(), "supa record_stream: pointer was not allocated by the supa caching allocator");
+    Block& b = it->second;
+    if (st == b.stream) return;
+    if (std::find(b.uses.begin(), b.uses.end(), st) == b.uses.end()) b.uses.push_back(st);
+  }
+
   void release(void* p) {
     std::lock_guard<std::mutex> g(mu_);
     auto it = live_.find(p);
     if (it == live_.end()) return;
-    const Block b = it->second;
+    Block b = std::move(it->second);
     live_.erase(it);
-    free_[b.device].emplace(b.size, b.ptr);
     stats_[b.device].allocated -= (int64_t)b.size;
     stats_[b.device].num_frees += 1;
+    if (b.uses.empty()) {
+      free_[b.device][b.stream].emplace(b.size, b.ptr);
+      return;
+    }
+    // an event on every other stream that used the block; reuse waits for all
+    Pending pend;
+    const int prev = current_device();
+    if (prev != b.device) (void)hipSetDevice(b.device);
+    for (hipStream_t use : b.uses) {
+      hipEvent_t e = get_event_locked(b.device);
+      const hipError_t rc = hipEventRecord(e, use);
+      if (rc != hipSuccess) {
+        (void)hipGetLastError();
+        (void)hipStreamSynchronize(use);  // a stream that cannot take an event: wait for it instead
+        events_[b.device].push_back(e);
+        continue;
+      }
+      pend.events.push_back(e);
+    }
+    if (prev != b.device) (void)hipSetDevice(prev);
+    b.uses.clear();
+    pend.block = std::move(b);
+    pending_[pend.block.device].push_back(std::move(pend));
   }
 
   void empty_cache() {
     std::lock_guard<std::mutex> g(mu_);
+    for (int d = 0; d < kMaxDevices; ++d) process_pending_locked(d, true);
     release_cached_locked(-1);
   }
 
   AllocatorStats stats(int dev) {
     std::lock_guard<std::mutex> g(mu_);
-    return stats_[dev];
+    AllocatorStats s = stats_[dev];
+    s.pending_blocks = (int64_t)pending_[dev].size();
+    return s;
   }
   void reset_peak(int dev) {
     std::lock_guard<std::mutex> g(mu_);
     stats_[dev].peak_allocated = stats_[dev].allocated;
   }
+  // Test hook: the next `n` device allocations fail as if hipMalloc returned
+  // hipErrorOutOfMemory (before and after the cache is released).
+  void inject_oom(int n) {
+    std::lock_guard<std::mutex> g(mu_);
+    inject_oom_ = n;
+  }
 
  private:
+  void* take_cached_locked(int dev, hipStream_t st, size_t sz) {
+    auto pit = free_[dev].find(st);
+    if (pit == free_[dev].end()) return nullptr;
+    auto& fl = pit->second;
+    auto it = fl.lower_bound(sz);
+    if (it == fl.end() || it->first > 2 * sz) return nullptr;
+    void* p = it->second;
+    const size_t bsz = it->first;
+    fl.erase(it);
+    live_[p] = Block{p, bsz, dev, st, {}};
+    account_alloc(dev, bsz, false);
+    return p;
+  }
+
+  hipEvent_t get_event_locked(int dev) {
+    auto& pool = events_[dev];
+    if (!pool.empty()) {
+      hipEvent_t e = pool.back();
+      pool.pop_back();
+      return e;
+    }
+    hipEvent_t e;
+    SUPA_HIP_CHECK(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+    return e;
+  }
+
+  // Moves freed blocks whose events have all completed to their stream's
+  // pool; with wait, waits for every event first.
+  void process_pending_locked(int dev, bool wait) {
+    auto& pl = pending_[dev];
+    for (size_t i = 0; i < pl.size();) {
+      bool done = true;
+      for (hipEvent_t e : pl[i].events) {
+        const hipError_t rc = wait ? hipEventSynchronize(e) : hipEventQuery(e);
+        if (rc == hipErrorNotReady) {
+          (void)hipGetLastError();
+          done = false;
+          break;
+        }
+        if (rc != hipSuccess) (void)hipGetLastError();
+      }
+      if (!done) {
+        ++i;
+        continue;
+      }
+      for (hipEvent_t e : pl[i].events) events_[dev].push_back(e);
+      const Block& b = pl[i].block;
+      free_[dev][b.stream].emplace(b.size, b.ptr);
+      pl[i] = std::move(pl.back());
+      pl.pop_back();
+    }
+  }
+
   void account_alloc(int dev, size_t bsz, bool fresh) {
     auto& s = stats_[dev];
     s.allocated += (int64_t)bsz;
@@ -236,25 +419,40 @@ class CachingAllocator final : public c10::Allocator {
       if (dev >= 0 && d != dev) continue;
       if (free_[d].empty()) continue;
       (void)hipSetDevice(d);
-      for (auto& kv : free_[d]) {
-        (void)hipFree(kv.second);
-        stats_[d].reserved -= (int64_t)kv.first;
+      for (auto& pool : free_[d]) {
+        for (auto& kv : pool.second) {
+          (void)hipFree(kv.second);
+          stats_[d].reserved -= (int64_t)kv.first;
+        }
       }
       free_[d].clear();
     }
     (void)hipSetDevice(prev);
   }
 
-  void* device_malloc(int dev, size_t sz) {
+  hipError_t try_malloc(void** p, size_t sz) {
+    {
+      std::lock_guard<std::mutex> g(mu_);
+      if (inject_oom_ > 0) {
+        --inject_oom_;
+        return hipErrorOutOfMemory;
+      }
+    }
+    return hipMalloc(p, sz);
+  }
+
+  void* device_malloc(int dev, hipStream_t st, size_t sz) {
     void* p = nullptr;
-    hipError_t e = hipMalloc(&p, sz);
+    hipError_t e = try_malloc(&p, sz);
     if (e != hipSuccess) {
       (void)hipGetLastError();
       {
         std::lock_guard<std::mutex> g(mu_);
+        process_pending_locked(dev, true);
         release_cached_locked(dev);
+        stats_[dev].num_ooms_retried += 1;
       }
-      e = hipMalloc(&p, sz);
+      e = try_malloc(&p, sz);
     }
     if (e != hipSuccess) {
       (void)hipGetLastError();
@@ -267,15 +465,18 @@ class CachingAllocator final : public c10::Allocator {
                        " allocated and ", s.reserved, " reserved by the caching allocator)");
     }
     std::lock_guard<std::mutex> g(mu_);
-    live_[p] = Block{p, sz, dev};
+    live_[p] = Block{p, sz, dev, st, {}};
     account_alloc(dev, sz, true);
     return p;
   }
 
   std::mutex mu_;
-  std::multimap<size_t, void*> free_[kMaxDevices];
+  std::map<hipStream_t, std::multimap<size_t, void*>> free_[kMaxDevices];
+  std::vector<Pending> pending_[kMaxDevices];
+  std::vector<hipEvent_t> events_[kMaxDevices];
   std::unordered_map<void*, Block> live_;
   AllocatorStats stats_[kMaxDevices];
+  int inject_oom_ = 0;
 };
 
 CachingAllocator& CachingAllocator::instance() {
@@ -292,6 +493,10 @@ AllocatorRegistrar g_allocator_registrar;
 
 c10::Allocator* allocator() { return &CachingAllocator::instance(); }
 AllocatorStats allocator_stats(c10::DeviceIndex d) { return CachingAllocator::instance().stats(d); }
+void allocator_record_stream(void* ptr, const c10::Stream& s) {
+  CachingAllocator::instance().record_stream(ptr, stream_handle(s.device_index(), s.id()));
+}
+void allocator_inject_oom(int n) { CachingAllocator::instance().inject_oom(n); }
 void allocator_reset_peak(c10::DeviceIndex d) { CachingAllocator::instance().reset_peak(d); }
 void allocator_empty_cache() { CachingAllocator::instance().empty_cache(); }
 
@@ -330,15 +535,13 @@ struct SupaGuardImpl final : public c10::impl::DeviceGuardImplInterface {
   void uncheckedSetDevice(c10::Device d) const noexcept override {
     if (hipSetDevice(d.index()) == hipSuccess) tls_device = d.index();
   }
-  c10::Stream getStream(c10::Device d) const override { return c10::Stream(c10::Stream::DEFAULT, d); }
-  c10::Stream getDefaultStream(c10::Device d) const override { return c10::Stream(c10::Stream::DEFAULT, d); }
+  c10::Stream getStream(c10::Device d) const override { return current_stream_obj(d.index()); }
+  c10::Stream getDefaultStream(c10::Device d) const override { return default_stream_obj(d.index()); }
   c10::Stream getStreamFromGlobalPool(c10::Device d, bool /*high_priority*/) const override {
-    return c10::Stream(c10::Stream::DEFAULT, d);
+    return pool_stream(d.index());  // every stream has the default priority
   }
-  c10::Stream getNewStream(c10::Device d, int /*priority*/) const override {
-    return c10::Stream(c10::Stream::DEFAULT, d);
-  }
-  c10::Stream exchangeStream(c10::Stream s) const override { return c10::Stream(c10::Stream::DEFAULT, s.device()); }
+  c10::Stream getNewStream(c10::Device d, int /*priority*/) const override { return pool_stream(d.index()); }
+  c10::Stream exchangeStream(c10::Stream s) const override { return exchange_stream(s); }
   c10::DeviceIndex deviceCount() const noexcept override { return device_count(); }
 
   void destroyEvent(void* event, const c10::DeviceIndex /*device_index*/) const noexcept override {
@@ -355,12 +558,13 @@ struct SupaGuardImpl final : public c10::impl::DeviceGuardImplInterface {
           &e, flag == c10::EventFlag::BACKEND_DEFAULT ? hipEventDisableTiming : hipEventDefault));
       *event = e;
     }
-    SUPA_HIP_CHECK(hipEventRecord(static_cast<hipEvent_t>(*event), current_stream(stream.device_index())));
+    SUPA_HIP_CHECK(hipEventRecord(static_cast<hipEvent_t>(*event), stream_handle(stream.device_index(), stream.id())));
     if (stream.device_index() != prev) set_device(prev);
   }
   void block(void* event, const c10::Stream& stream) const override {
     if (!event) return;
-    SUPA_HIP_CHECK(hipStreamWaitEvent(current_stream(stream.device_index()), static_cast<hipEvent_t>(event), 0));
+    SUPA_HIP_CHECK(hipStreamWaitEvent(stream_handle(stream.device_index(), stream.id()),
+                                      static_cast<hipEvent_t>(event), 0));
   }
   bool queryEvent(void* event) const override {
     if (!event) return true;
@@ -373,7 +577,7 @@ struct SupaGuardImpl final : public c10::impl::DeviceGuardImplInterface {
     return true;
   }
   bool queryStream(const c10::Stream& stream) const override {
-    const hipError_t e = hipStreamQuery(current_stream(stream.device_index()));
+    const hipError_t e = hipStreamQuery(stream_handle(stream.device_index(), stream.id()));
     if (e == hipErrorNotReady) {
       (void)hipGetLastError();
       return false;
@@ -382,13 +586,15 @@ struct SupaGuardImpl final : public c10::impl::DeviceGuardImplInterface {
     return true;
   }
   void synchronizeStream(const c10::Stream& stream) const override {
-    SUPA_HIP_CHECK(hipStreamSynchronize(current_stream(stream.device_index())));
+    SUPA_HIP_CHECK(hipStreamSynchronize(stream_handle(stream.device_index(), stream.id())));
   }
   void synchronizeEvent(void* event) const override {
     if (event) SUPA_HIP_CHECK(hipEventSynchronize(static_cast<hipEvent_t>(event)));
   }
   void synchronizeDevice(const c10::DeviceIndex device_index) const override { synchronize(device_index); }
-  void recordDataPtrOnStream(const c10::DataPtr&, const c10::Stream&) const override {}
+  void recordDataPtrOnStream(const c10::DataPtr& data_ptr, const c10::Stream& stream) const override {
+    if (data_ptr.get()) allocator_record_stream(data_ptr.get(), stream);
+  }
   double elapsedTime(void* e1, void* e2, const c10::DeviceIndex /*device_index*/) const override {
     float ms = 0.f;
     SUPA_HIP_CHECK(hipEventElapsedTime(&ms, static_cast<hipEvent_t>(e1), static_cast<hipEvent_t>(e2)));
@@ -433,7 +639,9 @@ struct SupaHooks final : public at::PrivateUse1HooksInterface {
     if (newsize == old) return;
     c10::DataPtr fresh = allocator()->allocate(newsize);
     const size_t n = std::min(old, newsize);
-    if (n > 0) SUPA_HIP_CHECK(hipMemcpy(fresh.get(), impl->data(), n, hipMemcpyDeviceToDevice));
+    if (n > 0)
+      SUPA_HIP_CHECK(hipMemcpyAsync(fresh.get(), impl->data(), n, hipMemcpyDeviceToDevice,
+                                    current_stream(current_device())));
     impl->set_data_ptr_noswap(std::move(fresh));
     impl->set_nbytes(newsize);
   }
@@ -485,6 +693,15 @@ std::atomic<bool> g_fused_bce{[] {
 }  // namespace
 void set_fused_bce_backward_enabled(bool on) { g_fused_bce.store(on); }
 bool fused_bce_backward_enabled() { return g_fused_bce.load(); }
+
+namespace {
+std::atomic<bool> g_accurate_gelu{[] {
+  const char* e = std::getenv("SUPA_AMD_ACCURATE_GELU");
+  return e && std::string(e) == "1";
+}()};
+}  // namespace
+void set_accurate_gelu_enabled(bool on) { g_accurate_gelu.store(on); }
+bool accurate_gelu_enabled() { return g_accurate_gelu.load(); }
 std::vector<std::pair<std::string, int64_t>> fallback_counts() {
   std::lock_guard<std::mutex> g(g_fb_mu);
   return {g_fb_counts.begin(), g_fb_counts.end()};
@@ -499,4 +716,16 @@ void reset_fallback_counts() {
 TORCH_LIBRARY_IMPL(_, PrivateUse1, m) {
   m.fallback(torch::CppFunction::makeFromBoxedFunction<&supa::supa_cpu_fallback>());
 }
+
+namespace {
+// Tensor.record_stream(s): the tensor's block is also used on stream s
+// (replaces the reference's aten/ops/RecordStream.cpp:10-16).
+void record_stream_supa(at::Tensor& self, c10::Stream s) {
+  TORCH_CHECK(s.device_type() == supa::kSupa, "record_stream: expected a supa stream, got ", s);
+  TORCH_CHECK(self.device() == s.device(), "record_stream: tensor on ", self.device(), ", stream on ", s.device());
+  supa::allocator_record_stream(self.storage().data_ptr().get(), s);
+}
+}  // namespace
+
+TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) { m.impl("record_stream", TORCH_FN(record_stream_supa)); }
 

@@ -2,9 +2,10 @@
 
 The subset of the reference's ``torch.supa`` (``torch_supa/supa/*.py``,
 ``csrc/supa/Module.cpp:1133-1162``) that the elementwise + loss path and its
-harnesses use: device queries, synchronisation, allocator statistics, a timing
-event, RNG seeding hooks (random numbers are drawn on the CPU and copied), and
-the CPU-fallback switch.
+harnesses use: device queries, synchronisation, streams (a pool of 32 per
+device, a thread-local current stream) and events, allocator statistics, the
+device generator's seeding API, and the switches of the opt-in kernels and of
+the CPU fallback.
 """
 from __future__ import annotations
 
@@ -159,6 +160,19 @@ def fused_bce_backward_enabled() -> bool:
     return bool(_C.fused_bce_backward_enabled())
 
 
+def set_accurate_gelu_enabled(on: bool) -> None:
+    """Evaluate gelu without the cancellation of 1 + erf(x/sqrt2) and
+    1 + tanh(u) for x << 0: 'none' as x - (x/2) erfc(|x|/sqrt2) or
+    (x/2) erfc(|x|/sqrt2), 'tanh' as x / (1 + exp(-2u)).  Off by default: the
+    default is the reference's formula, (x/2)(1 + erf) / (x/2)(1 + tanh),
+    whose results these forms do not reproduce for x << 0."""
+    _C.set_accurate_gelu_enabled(bool(on))
+
+
+def accurate_gelu_enabled() -> bool:
+    return bool(_C.accurate_gelu_enabled())
+
+
 def fallback_counts() -> dict:
     """Ops that went through the CPU fallback since the last reset, with counts."""
     return dict(_C.fallback_counts())
@@ -168,14 +182,123 @@ def reset_fallback_counts() -> None:
     _C.reset_fallback_counts()
 
 
+# c10::DeviceType::PrivateUse1, the device type of supa streams
+_SUPA_DEVICE_TYPE = 20
+
+
+class Stream(torch.Stream):
+    """A supa stream: an in-order queue on one device (the reference's
+    torch_supa/supa/streams.py).  ``Stream()`` takes a stream of the device's
+    pool of 32 (round-robin, as the reference's getStreamFromPool; every stream
+    is non-blocking and has the default priority); ``stream_id=0`` is the
+    device's default stream.  ``with s:`` makes it the current stream of its
+    device on this thread."""
+
+    def __new__(cls, device=None, priority=0, stream_id=None, device_index=None, device_type=None):
+        if stream_id is None:
+            device_index = _index(device) if device is not None else _C.current_device()
+            stream_id = _C.pool_stream_id(device_index)
+        elif device_index is None:
+            device_index = _index(device) if device is not None else _C.current_device()
+        return super().__new__(cls, stream_id=int(stream_id), device_index=int(device_index),
+                               device_type=_SUPA_DEVICE_TYPE)
+
+    @property
+    def hip_stream(self) -> int:
+        """The hipStream_t of this stream, as an integer."""
+        return _C.stream_ptr(self.device_index, self.stream_id)
+
+    def synchronize(self) -> None:
+        _C.stream_synchronize(self.device_index, self.stream_id)
+
+    def query(self) -> bool:
+        return _C.stream_query(self.device_index, self.stream_id)
+
+    def record_event(self, event: "Event" = None) -> "Event":
+        event = Event() if event is None else event
+        event.record(self)
+        return event
+
+    def wait_event(self, event: "Event") -> None:
+        event.wait(self)
+
+    def wait_stream(self, stream: "Stream") -> None:
+        self.wait_event(stream.record_event())
+
+    def __enter__(self):
+        self._prev = _C.set_current_stream_id(self.device_index, self.stream_id)
+        return self
+
+    def __exit__(self, *exc):
+        _C.set_current_stream_id(self.device_index, self._prev)
+        return False
+
+    def __eq__(self, other):
+        return isinstance(other, torch.Stream) and (self.stream_id, self.device_index, self.device_type) == (
+            other.stream_id, other.device_index, other.device_type)
+
+    def __hash__(self):
+        return hash((self.stream_id, self.device_index, self.device_type))
+
+    def __repr__(self):
+        return f"torch.supa.Stream(device=supa:{self.device_index}, stream_id={self.stream_id})"
+
+
+def current_stream(device=None) -> Stream:
+    """The current stream of `device` on this thread (the default stream
+    until set_stream or ``with stream(...)`` changes it)."""
+    idx = _index(device) if device is not None else _C.current_device()
+    return Stream(stream_id=_C.current_stream_id(idx), device_index=idx)
+
+
+def default_stream(device=None) -> Stream:
+    idx = _index(device) if device is not None else _C.current_device()
+    return Stream(stream_id=0, device_index=idx)
+
+
+def set_stream(s: Stream) -> None:
+    if s is not None:
+        _C.set_current_stream_id(s.device_index, s.stream_id)
+
+
+class stream:  # noqa: N801 (the torch.cuda.stream spelling)
+    """Context manager: `s` is the current stream of its device inside."""
+
+    def __init__(self, s):
+        self.s = s
+
+    def __enter__(self):
+        if self.s is not None:
+            self._prev = _C.set_current_stream_id(self.s.device_index, self.s.stream_id)
+        return self.s
+
+    def __exit__(self, *exc):
+        if self.s is not None:
+            _C.set_current_stream_id(self.s.device_index, self._prev)
+        return False
+
+
 class Event:
-    """A device event on the stream the supa kernels run on."""
+    """A device event (hipEvent_t): recorded on a stream (the current one by
+    default), waited on by streams, timed against another event."""
 
     def __init__(self, enable_timing: bool = True):
         self._h = _C.event_create()
 
-    def record(self) -> None:
-        _C.event_record(self._h)
+    def record(self, stream: Stream = None) -> None:
+        if stream is None:
+            _C.event_record(self._h)
+        else:
+            _C.event_record(self._h, stream.device_index, stream.stream_id)
+
+    def wait(self, stream: Stream = None) -> None:
+        if stream is None:
+            _C.event_wait(self._h)
+        else:
+            _C.event_wait(self._h, stream.device_index, stream.stream_id)
+
+    def query(self) -> bool:
+        return _C.event_query(self._h)
 
     def synchronize(self) -> None:
         _C.event_synchronize(self._h)
