@@ -318,23 +318,7 @@ def cpu_port_baseline():
                       f"{reps} reps, {per * 1e3:.1f} ms per rep incl. the bf16 widening"}
 
 
-def cpu_aten_baseline(torch):
-    """Upstream aten CPU kernels (torch 2.10.0) on the same 1/16 sample, all
-    host threads."""
-    import torch.nn.functional as F
-    torch.set_num_threads(os.cpu_count() or 1)
-    g = torch.Generator().manual_seed(0)
-    x = torch.randn(4, 2048, 4096, generator=g).to(torch.bfloat16)
-    bias = torch.randn(4096, generator=g) * 0.02
-    F.gelu(x + bias, approximate="tanh")
-    times = []
-    for _ in range(3):
-        t0 = time.perf_counter()
-        F.gelu(x + bias, approximate="tanh")
-        times.append(time.perf_counter() - t0)
-    per = sorted(times)[1]
-    n = x.numel()
-    nbytes = (2 * n + 4 * n + 4 * 4096) + 8 * n
+def _cpu_host_info(torch):
     cpu_model = ""
     try:
         for line in open("/proc/cpuinfo"):
@@ -343,9 +327,118 @@ def cpu_aten_baseline(torch):
                 break
     except OSError:
         pass
-    return {"value": round(nbytes / per / 1e9, 3), "unit": "GB/s", "threads": torch.get_num_threads(),
-            "cpu_count": os.cpu_count(), "cpu": cpu_model, "torch": torch.__version__,
-            "sample": "upstream aten CPU add + gelu(tanh) on x[4,2048,4096] bf16 + bias f32, median of 3"}
+    return {"threads": torch.get_num_threads(), "cpu_count": os.cpu_count(), "cpu": cpu_model,
+            "torch": torch.__version__}
+
+
+def _cpu_time(fn, reps=3):
+    """1 warm-up, then the median of `reps` wall-clock runs (seconds)."""
+    fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return sorted(ts)[len(ts) // 2]
+
+
+def _cpu_entry(nbytes, sec, sample):
+    g = nbytes / sec / 1e9
+    return {"ms": round(sec * 1e3, 3), "GB/s": round(g, 2), "sample": sample}
+
+
+def cpu_aten_baselines(torch, configs):
+    """Upstream aten CPU kernels of the installed torch, on the same seeded
+    inputs (drawn on the CPU) and the same algorithmic bytes as the GPU
+    figures, on this host's torch threads (OMP_NUM_THREADS; 16 on the GPU
+    boxes): 1 warm-up, median of 3.  Bounded samples keep the whole baseline
+    near a minute; each entry names its sample.  Reported beside the GPU
+    figures, never a pass/fail bar."""
+    import torch.nn.functional as F
+    res = {"host": _cpu_host_info(torch)}
+    g = torch.Generator().manual_seed(0)
+    if "c1" in configs:
+        a = torch.randn(4096, 4096, generator=g)
+        b = torch.randn(4096, 4096, generator=g)
+        o = torch.empty_like(a)
+        n = a.numel()
+        full = "full size [4096,4096] f32"
+        res["c1"] = {
+            "add": _cpu_entry(12 * n, _cpu_time(lambda: torch.add(a, b, alpha=1, out=o)), full),
+            "mul": _cpu_entry(12 * n, _cpu_time(lambda: torch.mul(a, b, out=o)), full),
+            "gelu": _cpu_entry(8 * n, _cpu_time(lambda: torch.ops.aten.gelu.out(a, approximate="none", out=o)), full),
+            "silu": _cpu_entry(8 * n, _cpu_time(lambda: torch.ops.aten.silu.out(a, out=o)), full),
+        }
+        del a, b, o
+    # c2 (the headline workload) on 1/16 of the config: x [4,2048,4096]
+    x = torch.randn(4, 2048, 4096, generator=g).to(torch.bfloat16)
+    bias = torch.randn(4096, generator=g) * 0.02
+    n = x.numel()
+    sample = "x[4,2048,4096] bf16 + bias f32 (1/16 of c2), contiguous"
+    t_add = _cpu_time(lambda: x + bias)
+    y = x + bias
+    t_gelu = _cpu_time(lambda: F.gelu(y, approximate="tanh"))
+    t_step = _cpu_time(lambda: F.gelu(x + bias, approximate="tanh"))
+    res["c2_contiguous"] = {"add": _cpu_entry(2 * n + 4 * n + 16384, t_add, sample),
+                            "gelu_tanh": _cpu_entry(8 * n, t_gelu, sample),
+                            "step": _cpu_entry(14 * n + 16384, t_step, sample)}
+    del x, y
+    if "c3" in configs:
+        rows = 512
+        logits = (torch.randn(rows, C3_V, generator=g) * 2).to(torch.bfloat16).requires_grad_()
+        t = torch.randint(0, C3_V, (rows,), generator=g)
+        t[torch.randperm(rows, generator=g)[:round(0.05 * rows)]] = -100
+
+        def step():
+            logits.grad = None
+            F.cross_entropy(logits, t, ignore_index=-100).backward()
+        sec = _cpu_time(step)
+        nbytes = sum(C3_BYTES.values()) * rows / C3_N
+        res["c3"] = {"fwd_bwd": dict(_cpu_entry(nbytes, sec, f"{rows} of the 8192 rows (1/16), bf16 [{rows},128256]"),
+                                     rows_per_s=round(rows / sec, 1))}
+        del logits
+    if "c4" in configs:
+        R, C = 4, 1048576
+        n = R * C
+        xc = torch.randn(R, C, generator=g)
+        tc = torch.randn(R, C, generator=g)
+        tb = (torch.rand(R, C, generator=g) < 0.3).float()
+        pw = torch.rand(C, generator=g) * 1.5 + 0.5
+        sample = "4 of the 32 rows (1/8): [4,1048576] f32"
+        c4 = {}
+        for red in ("none", "sum", "mean"):
+            fwd_b = 12 * n if red == "none" else 8 * n + 4
+            c4[f"mse_{red}_fwd"] = _cpu_entry(fwd_b, _cpu_time(lambda: F.mse_loss(xc, tc, reduction=red)), sample)
+            c4[f"smooth_l1_{red}_fwd"] = _cpu_entry(
+                fwd_b, _cpu_time(lambda: F.smooth_l1_loss(xc, tc, reduction=red, beta=1.0)), sample)
+            bwd_b = 16 * n if red == "none" else 12 * n + 4
+            rc = {"none": 0, "mean": 1, "sum": 2}[red]
+            gl = torch.randn(R, C, generator=g) if red == "none" else torch.ones(())
+            c4[f"mse_{red}_bwd"] = _cpu_entry(bwd_b, _cpu_time(
+                lambda: torch.ops.aten.mse_loss_backward(gl, xc, tc, rc)), sample)
+            c4[f"smooth_l1_{red}_bwd"] = _cpu_entry(bwd_b, _cpu_time(
+                lambda: torch.ops.aten.smooth_l1_loss_backward(gl, xc, tc, rc, 1.0)), sample)
+            c4[f"bce_{red}_fwd"] = _cpu_entry(fwd_b + 4 * C, _cpu_time(
+                lambda: F.binary_cross_entropy_with_logits(xc, tb, pos_weight=pw, reduction=red)), sample)
+            xg = xc.detach().requires_grad_()
+            loss = F.binary_cross_entropy_with_logits(xg, tb, pos_weight=pw, reduction=red)
+            go = torch.ones_like(loss)
+            gsz = 4 if red != "none" else 4 * n
+            c4[f"bce_{red}_bwd"] = _cpu_entry(gsz + 12 * n + 4 * C, _cpu_time(
+                lambda: torch.autograd.grad(loss, xg, go, retain_graph=True)), sample)
+        res["c4"] = c4
+        del xc, tc, tb
+    if "c5" in configs:
+        shapes = C5_SHAPES[:9]  # one decoder layer of the 8
+        ps = [(torch.randn(s, generator=g) * 0.02).requires_grad_() for s in shapes]
+        for p in ps:
+            p.grad = torch.randn(p.shape, generator=g) * 1e-3
+        P = sum(p.numel() for p in ps)
+        opt = torch.optim.AdamW(ps, lr=1e-4, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01, fused=True)
+        sample = f"one layer of the 8 (9 tensors, {P} parameters), fused=True"
+        res["c5"] = {"fused_adamw_step": dict(_cpu_entry(28 * P, _cpu_time(opt.step), sample), params=P)}
+        del ps, opt
+    return res
 
 
 def traffic_from_profiles():
@@ -515,11 +608,19 @@ def main():
     fb = torch.supa.fallback_counts()
 
     cpu = None
-    cpu_aten = None
+    cpu_port = None
     if not a.no_cpu:
         log("cpu baselines")
-        cpu = cpu_port_baseline()
-        cpu_aten = cpu_aten_baseline(torch)
+        aten = cpu_aten_baselines(torch, configs)
+        host = aten.pop("host")
+        for k, v in aten.items():
+            per.setdefault(k, {})["cpu_aten"] = v
+        head = aten["c2_contiguous"]["step"]
+        cpu = {"value": head["GB/s"], "unit": "GB/s", "cores": host["threads"], "kind": "reference",
+               "sample": "upstream aten CPU kernels (torch " + host["torch"] + "), the reference outputs' "
+                         "producer: c2 add + gelu(tanh) on " + head["sample"] + ", median of 3",
+               "host": host}
+        cpu_port = cpu_port_baseline()
 
     line = {
         "metric": METRIC,
@@ -539,7 +640,7 @@ def main():
                    "pct_roofline": round(100 * value / PEAK_GBS, 1), "parallelism": "none (1 GPU)"},
         "roofline": roofline,
         "cpu_baseline": cpu,
-        "cpu_aten": cpu_aten,
+        "cpu_port": cpu_port,
         "per_config": per,
         "cpu_fallback_ops": fb,
         "host": platform.node(),
