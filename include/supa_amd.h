@@ -378,6 +378,20 @@ int supa_amd_sum(const supa_amd_ew_desc* d, double scale, void* workspace,
                  int64_t workspace_bytes, void* stream);
 int64_t supa_amd_sum_workspace_bytes(int64_t numel);
 
+/* supa_amd_sum without a workspace argument and without any allocation.
+ * No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  The workspace is a file-scope device array of the
+ * library, 8448 bytes on each GPU it runs on, held until the process ends and
+ * set up on the first call on a device; a reduction needing more than
+ * supa_amd_sum_noalloc_max_workspace_bytes() is refused with
+ * SUPA_AMD_EWORKSPACE (supa_amd_sum's need is that size for every numel).
+ * The array needs no initial contents.  Every call on one GPU shares it:
+ * calls that overlap in time on that GPU (different streams, or threads
+ * without ordering) race and must not be issued; calls in one stream's order
+ * are safe.  Same arguments, results and errors as supa_amd_sum otherwise. */
+int supa_amd_sum_noalloc(const supa_amd_ew_desc* d, double scale, void* stream);
+int64_t supa_amd_sum_noalloc_max_workspace_bytes(void);
 
 /* Reduction of the innermost `inner` elements of each of `outer` rows of a
  * contiguous input: out[r] = scale * sum(in[r*inner .. r*inner+inner)).

@@ -16,6 +16,8 @@
 // Workspace contract: supa_amd_*_workspace_bytes() bytes of device memory
 // with no required contents; calls that overlap in time on different streams
 // need separate buffers.
+#include <mutex>
+
 #include "ew_launch.h"
 #include "ops.h"
 
@@ -389,6 +391,40 @@ k_sum_rows(const T* __restrict__ in, OT* __restrict__ out, int64_t inner, ACC sc
 
 using namespace sa;
 
+// ------------------------------------------------ no-allocation variant
+// supa_amd_sum_noalloc's workspace: a file-scope device array of exactly the
+// two-stage reduction's workspace (256 reserved bytes + one partial per
+// stage-1 block), which each GPU the library runs on holds until the process
+// ends.  Host code never passes `scratch` itself (on the host it is only a
+// stand-in symbol): its device address comes from hipGetSymbolAddress, once
+// per device with that device current, and is kept per device.
+namespace {
+constexpr int64_t kNoAllocScratchBytes = sa::kCounterBytes + (int64_t)sa::kRedBlocks * 8;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+constexpr int kNoAllocDevices = 64;
+std::mutex g_noalloc_mu;
+void* g_noalloc_ptr[kNoAllocDevices] = {};
+
+// The current device's scratch address (set up on the first call on a
+// device), or a hipError_t.
+int noalloc_scratch(void** out) {
+  int dev = 0;
+  hipError_t rc = hipGetDevice(&dev);
+  if (rc != hipSuccess) return (int)rc;
+  if (dev < 0 || dev >= kNoAllocDevices) return SUPA_AMD_EINVAL;
+  std::lock_guard<std::mutex> g(g_noalloc_mu);
+  if (!g_noalloc_ptr[dev]) {
+    void* ptr = nullptr;
+    rc = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (rc != hipSuccess || !ptr) return rc != hipSuccess ? (int)rc : (int)hipErrorInvalidSymbol;
+    g_noalloc_ptr[dev] = ptr;
+  }
+  *out = g_noalloc_ptr[dev];
+  return SUPA_AMD_OK;
+}
+}  // namespace
+
 extern "C" {
 
 int64_t supa_amd_sum_workspace_bytes(int64_t /*numel*/) { return kCounterBytes + (int64_t)kRedBlocks * 8; }
@@ -398,6 +434,20 @@ int supa_amd_sum(const supa_amd_ew_desc* d, double scale, void* workspace, int64
   if (!d || d->noperands != 2) return SUPA_AMD_EINVAL;
   if (desc_numel(d) == 0) return SUPA_AMD_EINVAL;  // the caller writes the empty-sum value
   return run_reduce(IdentityFactory{}, d, scale, workspace, workspace_bytes, stream);
+}
+
+int64_t supa_amd_sum_noalloc_max_workspace_bytes(void) { return kNoAllocScratchBytes; }
+
+int supa_amd_sum_noalloc(const supa_amd_ew_desc* d, double scale, void* stream) {
+  if (!d || d->noperands != 2) return SUPA_AMD_EINVAL;
+  if (desc_numel(d) == 0) return SUPA_AMD_EINVAL;
+  // the reduction's workspace is a fixed size; refuse anything needing more
+  // than the scratch array holds
+  if (supa_amd_sum_workspace_bytes(desc_numel(d)) > kNoAllocScratchBytes) return SUPA_AMD_EWORKSPACE;
+  void* ws = nullptr;
+  const int rc = noalloc_scratch(&ws);
+  if (rc != SUPA_AMD_OK) return rc;
+  return run_reduce(IdentityFactory{}, d, scale, ws, kNoAllocScratchBytes, stream);
 }
 
 int supa_amd_sum_rows(const void* in, int32_t in_dtype, void* out, int32_t out_dtype, int64_t outer, int64_t inner,
