@@ -46,8 +46,15 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--configs", default="c1,c2,c3,c4,c5")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
-    ap.add_argument("--probe", action="store_true",
-                    help="only launch the c2 gelu(tanh) kernel and a copy-like calibration kernel (for rocprofv3 --pmc)")
+    ap.add_argument("--probe", nargs="?", const="c2", default=None, metavar="CONFIG",
+                    help="only launch the dominant kernels of CONFIG (c1..c5; default c2), after a copy-like "
+                         "calibration kernel, three times each (for rocprofv3 --pmc)")
+    ap.add_argument("--derive-counters", nargs="+", metavar="CSV",
+                    help="CPU only: turn the counter_collection.csv files of rocprofv3 --pmc runs of "
+                         "--probe CONFIG into profiles/<CONFIG>_counters.{json,md} (with --config)")
+    ap.add_argument("--config", default="c2", help="the config of --derive-counters")
+    ap.add_argument("--stats", default=None, help="with --derive-counters: the kernel_stats.csv of a "
+                                                  "rocprofv3 --kernel-trace --stats run of the same probe")
     ap.add_argument("--derive-traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="CPU only: turn the counter_collection.csv files of two `rocprofv3 --pmc FETCH_SIZE` / "
                          "`--pmc WRITE_SIZE` runs of --probe into profiles/gelu_tanh_c2_traffic.json")
@@ -506,32 +513,251 @@ def derive_traffic(fetch_csv, write_csv):
     print(json.dumps(out))
 
 
-def probe(torch):
-    """Kernel launches for counter collection: 10x abs.out over a 1 GiB f32
+PROBE_REPS = 3
+
+
+def _probe_ops(torch, cfg):
+    """(name, fn) of the config's dominant aten calls, inputs already on the
+    device."""
+    import torch.nn.functional as F
+    if cfg == "c1":
+        a = gen(torch, (4096, 4096), 10, torch.float32)
+        b = gen(torch, (4096, 4096), 20, torch.float32)
+        o = torch.empty_like(a)
+        return [("add", lambda: torch.add(a, b, out=o)), ("mul", lambda: torch.mul(a, b, out=o)),
+                ("gelu", lambda: torch.ops.aten.gelu.out(a, approximate="none", out=o)),
+                ("silu", lambda: torch.ops.aten.silu.out(a, out=o))]
+    if cfg == "c2":
+        x, bias = c2_inputs(torch, transposed=False)
+        y = x + bias
+        z = torch.empty_like(y)
+        return [("add", lambda: torch.add(x, bias, out=y)),
+                ("gelu_tanh", lambda: torch.ops.aten.gelu.out(y, approximate="tanh", out=z))]
+    if cfg == "c3":
+        lx = gen(torch, (C3_N, C3_V), 4, torch.bfloat16, b=2.0)
+        tgt = torch.randint(0, C3_V, (C3_N,)).to("supa")
+        lsm = torch.ops.aten._log_softmax(lx, 1, False)
+        out, tw = torch.ops.aten.nll_loss_forward(lsm, tgt, None, 1, -100)
+        go = torch.ones((), dtype=torch.bfloat16, device="supa")
+        gn = torch.ops.aten.nll_loss_backward(go, lsm, tgt, None, 1, -100, tw)
+        gi = torch.empty_like(lx)
+        return [("_log_softmax", lambda: torch.ops.aten._log_softmax.out(lx, 1, False, out=lsm)),
+                ("nll_loss_forward", lambda: torch.ops.aten.nll_loss_forward(lsm, tgt, None, 1, -100)),
+                ("nll_loss_backward", lambda: torch.ops.aten.nll_loss_backward.grad_input(
+                    go, lsm, tgt, None, 1, -100, tw, grad_input=gn)),
+                ("_log_softmax_backward_data", lambda: torch.ops.aten._log_softmax_backward_data.out(
+                    gn, lsm, 1, torch.bfloat16, out=gi))]
+    if cfg == "c4":
+        R, C = 32, 1048576
+        xc = gen(torch, (R, C), 6, torch.float32)
+        tc = gen(torch, (R, C), 7, torch.float32)
+        tb = gen(torch, (R, C), 8, torch.float32, kind="bernoulli", a=0.3)
+        pw = gen(torch, (C,), 9, torch.float32, kind="uniform", a=0.5, b=2.0)
+        xg = xc.detach().requires_grad_()
+        loss = F.binary_cross_entropy_with_logits(xg, tb, pos_weight=pw, reduction="none")
+        go = gen(torch, (R, C), 11, torch.float32)
+        return [("mse_none_fwd", lambda: F.mse_loss(xc, tc, reduction="none")),
+                ("mse_sum_fwd", lambda: F.mse_loss(xc, tc, reduction="sum")),
+                ("bce_none_fwd", lambda: F.binary_cross_entropy_with_logits(xc, tb, pos_weight=pw,
+                                                                             reduction="none")),
+                ("bce_none_bwd", lambda: torch.autograd.grad(loss, xg, go, retain_graph=True))]
+    if cfg == "c5":
+        params, grads = [], []
+        for i, sh in enumerate(C5_SHAPES):
+            params.append(gen(torch, sh, 100 + i, torch.float32, b=0.02).requires_grad_())
+            grads.append(gen(torch, sh, 1000 + i, torch.float32, b=1e-3))
+        opt = torch.optim.AdamW(params, lr=1e-4, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01, fused=True)
+        for p_, g_ in zip(params, grads):
+            p_.grad = g_
+        pd = [p_.detach() for p_ in params]
+        return [("fused_adamw_step", opt.step),
+                ("_foreach_add_List", lambda: torch._foreach_add_(pd, grads)),
+                ("_foreach_mul_Scalar", lambda: torch._foreach_mul_(pd, 1.0))]
+    raise SystemExit(f"--probe: unknown config {cfg}")
+
+
+def probe(torch, cfg):
+    """Kernel launches for counter collection: 3x abs.out over a 1 GiB f32
     buffer (reads 1 GiB, writes 1 GiB: the calibration of FETCH_SIZE and
-    WRITE_SIZE), then 10x the headline's dominant kernel, gelu(tanh) over the
-    c2 f32 tensor (algorithmic 2 GiB read + 2 GiB write)."""
+    WRITE_SIZE), then each dominant aten call of the config 3 times, with a
+    device synchronisation between calls."""
     cal = gen(torch, (1 << 28,), 42, torch.float32)
     cal_out = torch.empty_like(cal)
-    for _ in range(10):
+    for _ in range(PROBE_REPS):
         torch.ops.aten.abs.out(cal, out=cal_out)
     torch.supa.synchronize()
     del cal, cal_out
-    x, bias = c2_inputs(torch, transposed=False)
-    y = x + bias
-    del x
-    z = torch.empty_like(y)
-    for _ in range(10):
-        torch.ops.aten.gelu.out(y, approximate="tanh", out=z)
-    torch.supa.synchronize()
-    print(json.dumps({"probe": "done", "calibration_bytes_read": 1 << 30, "calibration_bytes_written": 1 << 30,
-                      "gelu_bytes_read": C2_N * 4, "gelu_bytes_written": C2_N * 4}))
+    ops = _probe_ops(torch, cfg)
+    for name, fn in ops:
+        for _ in range(PROBE_REPS):
+            fn()
+        torch.supa.synchronize()
+        log(f"probe {cfg}: {name} x{PROBE_REPS}")
+    print(json.dumps({"probe": cfg, "ops": [n for n, _ in ops], "reps": PROBE_REPS}))
+
+
+# Algorithmic bytes per dispatch of each config's dominant kernels, keyed by
+# substrings of the kernel name (the functor or kernel template).
+C1_N = 4096 * 4096
+PROBE_ALG_BYTES = {
+    "c1": [("AddOp", 12 * C1_N), ("MulOp", 12 * C1_N), ("UnaryOpILi0EfE", 8 * C1_N), ("UnaryOpILi2EfE", 8 * C1_N),
+           ("UnaryOp<0,", 8 * C1_N), ("UnaryOp<2,", 8 * C1_N)],
+    "c2": [("AddOp", C2_ADD_BYTES), ("UnaryOp<1,", C2_GELU_BYTES), ("UnaryOpILi1EfE", C2_GELU_BYTES)],
+    "c3": [("k_lsm_fwd_reg", C3_BYTES["_log_softmax"]), ("k_nll_bwd", C3_BYTES["nll_loss_backward"]),
+           ("k_lsm_bwd_reg", C3_BYTES["_log_softmax_backward_data"])],
+    "c4": [("MseOp", 12 * 32 * 1048576), ("BceBwdOp", 16 * 32 * 1048576 + 4 * 1048576)],
+    # two k_adamw launches (40 + 32 tensors) per step: the average dispatch moves half of 28 P
+    "c5": [("k_adamw", 14 * 1619066880)],
+}
+
+
+PROBE_NOTES = {
+    "c1": "c1: [4096,4096] f32 add, mul, gelu('none'), silu (64 MiB operands; the probe runs one buffer set, "
+          "so a repeat can hit the 256 MB MALL -- the bench rotates six sets)",
+    "c2": "c2 contiguous: bf16 [64,2048,4096] + f32 bias -> f32, then gelu('tanh') over the f32 tensor",
+    "c3": "c3: bf16 logits [8192,128256]: _log_softmax, nll_loss_forward, nll_loss_backward, "
+          "_log_softmax_backward_data",
+    "c4": "c4: [32,1048576] f32: mse 'none' and 'sum' forward, BCE-with-logits (pos_weight) 'none' forward "
+          "and backward",
+    "c5": "c5: AdamW(fused=True) step over the 72 tensors (1.62 G params), _foreach_add_.List, "
+          "_foreach_mul_.Scalar",
+}
+CU_NUM = 256
+ENGINE_GHZ = 2.4  # MI355X peak engine clock
+
+
+def _fmt(v, nd=1):
+    return "" if v is None else (f"{v:,.{nd}f}" if isinstance(v, float) else f"{v:,}")
+
+
+def derive_counters(csvs, cfg, stats_csv=None):
+    """Per-kernel averages of every counter in the given counter_collection.csv
+    files (one file per rocprofv3 --pmc pass of --probe CFG).  FETCH_SIZE and
+    WRITE_SIZE (KiB per dispatch) are scaled by known / measured for the
+    calibration kernel (abs.out: 1 GiB read, 1 GiB written)."""
+    import csv
+    from collections import defaultdict
+
+    vals = defaultdict(lambda: defaultdict(list))  # kernel -> counter -> values
+    for path in csvs:
+        with open(path) as f:
+            for r in csv.DictReader(f):
+                name = r["Kernel_Name"]
+                vals[name][r["Counter_Name"]].append(float(r["Counter_Value"]))
+    cal = [k for k in vals if "k_contig" in k and PROBE_CAL_KERNEL in k]
+    if not cal:
+        raise SystemExit("calibration dispatches (abs.out) missing")
+    cal = cal[0]
+    known_kib = float(1 << 20)
+    scale = {}
+    for c in ("FETCH_SIZE", "WRITE_SIZE"):
+        if vals[cal].get(c):
+            scale[c] = known_kib / (sum(vals[cal][c]) / len(vals[cal][c]))
+    rows = []
+    for name, cs in vals.items():
+        if name == cal:
+            continue
+        row = {"kernel": name.split("(")[0].replace("void ", ""),
+               "dispatches": max(len(v) for v in cs.values())}
+        for c, v in sorted(cs.items()):
+            row[c] = sum(v) / len(v)
+        if "FETCH_SIZE" in scale and "FETCH_SIZE" in row:
+            row["read_bytes"] = row["FETCH_SIZE"] * scale["FETCH_SIZE"] * 1024
+        if "WRITE_SIZE" in scale and "WRITE_SIZE" in row:
+            row["write_bytes"] = row["WRITE_SIZE"] * scale["WRITE_SIZE"] * 1024
+        for sub, b in PROBE_ALG_BYTES.get(cfg, []):
+            if sub in name:
+                row["algorithmic_bytes"] = b
+                break
+        if "read_bytes" in row and "write_bytes" in row and row.get("algorithmic_bytes"):
+            row["traffic_over_algorithmic"] = (row["read_bytes"] + row["write_bytes"]) / row["algorithmic_bytes"]
+        rows.append(row)
+    durations = {}
+    if stats_csv:
+        with open(stats_csv) as f:
+            for r in csv.DictReader(f):
+                durations[r["Name"].split("(")[0].replace("void ", "")] = (int(r["Calls"]), float(r["AverageNs"]))
+    for row in rows:
+        if row["kernel"] in durations:
+            row["calls_traced"], row["avg_ns"] = durations[row["kernel"]]
+            if row.get("algorithmic_bytes"):
+                row["achieved_pct_of_8TBs"] = 100.0 * row["algorithmic_bytes"] / (row["avg_ns"] * 1e-9) / 8e12
+        if row.get("SQ_WAVES"):
+            row["valu_insts_per_wave"] = row.get("SQ_INSTS_VALU", 0.0) / row["SQ_WAVES"]
+        if row.get("avg_ns"):
+            # cycles of the traced kernel duration at the peak engine clock (a lower bound on busy
+            # fractions when the clock runs below it)
+            cyc = row["avg_ns"] * ENGINE_GHZ
+            if "SQ_INSTS_VALU" in row:
+                # wave64 VALU instructions issue in 4 cycles on a 16-lane SIMD (4 per CU); the f32
+                # transcendentals are quarter rate
+                issue = row["SQ_INSTS_VALU"] + 3.0 * row.get("SQ_INSTS_VALU_TRANS_F32", 0.0)
+                row["valu_busy_pct"] = 100.0 * issue / CU_NUM / cyc
+            if "SQ_WAVE_CYCLES" in row:
+                row["waves_per_cu"] = 4.0 * row["SQ_WAVE_CYCLES"] / cyc / CU_NUM
+            if "SQ_LDS_BANK_CONFLICT" in row:
+                row["lds_bank_conflict_pct"] = 100.0 * row["SQ_LDS_BANK_CONFLICT"] / cyc / CU_NUM
+    # this library's kernels (the probe's input generation runs torch's own HIP kernels)
+    rows = [r for r in rows if r["kernel"].startswith("sa::")]
+    rows.sort(key=lambda r: -(r.get("read_bytes", 0) + r.get("write_bytes", 0)))
+    out = {"config": cfg, "calibration": "abs.out over 2^28 f32 (1 GiB read, 1 GiB written)",
+           "scale": scale, "kernels": rows}
+    base = os.path.join(HERE, "profiles", f"{cfg}_counters")
+    with open(base + ".json", "w") as f:
+        json.dump(out, f, indent=1)
+        f.write("\n")
+    # the summary table
+    lines = [f"# {cfg}: per-kernel counters (rocprofv3 on MI355X)", "", PROBE_NOTES.get(cfg, cfg) + ".", "",
+             "Each dominant aten call runs 3 times after 3 calibration dispatches (`abs.out` over 2^28 f32: "
+             "1 GiB read, 1 GiB written).  Commands (from the repository root, on the GPU box):", "", "```",
+             "cd /tmp && export TMPDIR=/tmp && cd $GRAFT_REPO_ROOT",
+             f"rocprofv3 --kernel-trace --stats --output-format csv -d gpurun_out/prof/{cfg}_trace -o run -- "
+             f"python3 bench.py --probe {cfg}",
+             f"rocprofv3 --pmc FETCH_SIZE --output-format csv -d gpurun_out/prof/{cfg}_fetch -o run -- "
+             f"python3 bench.py --probe {cfg}",
+             f"rocprofv3 --pmc WRITE_SIZE --output-format csv -d gpurun_out/prof/{cfg}_write -o run -- "
+             f"python3 bench.py --probe {cfg}",
+             "rocprofv3 --pmc SQ_WAVES SQ_INSTS_VALU SQ_ACTIVE_INST_VALU SQ_WAVE_CYCLES SQ_BUSY_CYCLES "
+             "SQ_LDS_BANK_CONFLICT SQ_LDS_IDX_ACTIVE SQ_INSTS_VALU_TRANS_F32 GRBM_GUI_ACTIVE --output-format csv "
+             f"-d gpurun_out/prof/{cfg}_sq -o run -- python3 bench.py --probe {cfg}",
+             f"python3 bench.py --derive-counters gpurun_out/prof/{cfg}_fetch/run_counter_collection.csv "
+             f"gpurun_out/prof/{cfg}_write/run_counter_collection.csv "
+             f"gpurun_out/prof/{cfg}_sq/run_counter_collection.csv --config {cfg} "
+             f"--stats gpurun_out/prof/{cfg}_trace/run_kernel_stats.csv",
+             "```", "",
+             f"FETCH_SIZE scale {scale.get('FETCH_SIZE', 0):.5f}, WRITE_SIZE scale {scale.get('WRITE_SIZE', 0):.5f} "
+             "(known bytes / counter for the calibration kernel).  Traffic = scaled FETCH + WRITE per dispatch.  "
+             "Cycles = the traced average duration x 2.4 GHz (the peak engine clock, so the busy fractions are "
+             "lower bounds).  VALU busy = 100 (SQ_INSTS_VALU + 3 SQ_INSTS_VALU_TRANS_F32) / CU_NUM / cycles "
+             "(a wave64 VALU instruction issues in 4 cycles on one of a CU's 4 SIMDs; f32 transcendentals "
+             "are quarter rate).  Waves per CU = 4 SQ_WAVE_CYCLES / cycles / CU_NUM (SQ_WAVE_CYCLES counts "
+             "quad cycles; 32 waves fit a CU).  LDS bank conflicts = 100 SQ_LDS_BANK_CONFLICT / cycles / "
+             "CU_NUM.  Only this library's kernels are listed (the probe's input generation runs torch's own "
+             "HIP kernels).", "",
+             "| kernel | avg us | algorithmic B | % of 8 TB/s | traffic B | traffic / alg | waves | VALU insts / wave "
+             "| VALU busy % | waves / CU | LDS conflict % | transcendental f32 insts |",
+             "|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|"]
+    for r in rows:
+        tr = (r.get("read_bytes") or 0) + (r.get("write_bytes") or 0)
+        lines.append("| `{}` | {} | {} | {} | {} | {} | {} | {} | {} | {} | {} | {} |".format(
+            r["kernel"][:110], _fmt(r.get("avg_ns", 0) / 1e3 if r.get("avg_ns") else None),
+            _fmt(r.get("algorithmic_bytes")), _fmt(r.get("achieved_pct_of_8TBs")), _fmt(int(tr)) if tr else "",
+            _fmt(r.get("traffic_over_algorithmic"), 4), _fmt(int(r["SQ_WAVES"]) if r.get("SQ_WAVES") else None),
+            _fmt(r.get("valu_insts_per_wave")), _fmt(r.get("valu_busy_pct")), _fmt(r.get("waves_per_cu")),
+            _fmt(r.get("lds_bank_conflict_pct"), 3),
+            _fmt(int(r["SQ_INSTS_VALU_TRANS_F32"]) if r.get("SQ_INSTS_VALU_TRANS_F32") is not None else None)))
+    with open(base + ".md", "w") as f:
+        f.write("\n".join(lines) + "\n")
+    print(json.dumps(out))
 
 
 def main():
     a = parse()
     if a.derive_traffic:
         derive_traffic(*a.derive_traffic)
+        return
+    if a.derive_counters:
+        derive_counters(a.derive_counters, a.config, a.stats)
         return
     if a.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {a.gpus} is not supported "
@@ -544,7 +770,7 @@ def main():
     assert torch.supa.is_available(), "no supa device"
     timer = Timer(torch)
     if a.probe:
-        probe(torch)
+        probe(torch, a.probe)
         return
     configs = [c.strip() for c in a.configs.split(",") if c.strip()]
     per = {}
