@@ -55,6 +55,9 @@ def parse():
     ap.add_argument("--config", default="c2", help="the config of --derive-counters")
     ap.add_argument("--stats", default=None, help="with --derive-counters: the kernel_stats.csv of a "
                                                   "rocprofv3 --kernel-trace --stats run of the same probe")
+    ap.add_argument("--render-kernel-stats", nargs=2, metavar=("STATS_CSV", "BENCH_LOG"),
+                    help="CPU only: write profiles/kernel_stats_all_configs.md from the kernel_stats.csv of a "
+                         "rocprofv3 --kernel-trace --stats run of bench.py --no-cpu and that run's output")
     ap.add_argument("--derive-traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="CPU only: turn the counter_collection.csv files of two `rocprofv3 --pmc FETCH_SIZE` / "
                          "`--pmc WRITE_SIZE` runs of --probe into profiles/gelu_tanh_c2_traffic.json")
@@ -143,6 +146,7 @@ def c2_inputs(torch, transposed):
     return x, bias
 
 
+C1_N = 4096 * 4096
 C2_N = 64 * 2048 * 4096
 C2_ADD_BYTES = 2 * C2_N + 4 * C2_N + 4 * 4096
 C2_GELU_BYTES = 8 * C2_N
@@ -510,7 +514,110 @@ def derive_traffic(fetch_csv, write_csv):
     with open(path, "w") as f:
         json.dump(out, f, indent=1)
         f.write("\n")
+    md = ["# HBM traffic of the c2 gelu(tanh) kernel (rocprofv3 PMC)", "",
+          f"Two counter runs of the bench's probe mode ({PROBE_REPS}x `abs.out` over 2^28 f32 as the calibration -- "
+          f"exactly 1 GiB read and 1 GiB written per dispatch -- then {PROBE_REPS}x `gelu.out(approximate='tanh')` "
+          "over the c2 f32 tensor [64,2048,4096]):", "", "```",
+          "cd /tmp && export TMPDIR=/tmp && cd $GRAFT_REPO_ROOT",
+          "timeout -s KILL 120 rocprofv3 --pmc FETCH_SIZE --output-format csv -d gpurun_out/prof_fetch -o probe -- "
+          "python3 bench.py --probe",
+          "timeout -s KILL 120 rocprofv3 --pmc WRITE_SIZE --output-format csv -d gpurun_out/prof_write -o probe -- "
+          "python3 bench.py --probe",
+          "python3 bench.py --derive-traffic gpurun_out/prof_fetch/probe_counter_collection.csv \\",
+          "                                  gpurun_out/prof_write/probe_counter_collection.csv", "```", "",
+          "The last command (CPU only) writes `gelu_tanh_c2_traffic.json` and this file; `bench.py` reports the "
+          "json's `bytes_per_launch` as `roofline.traffic`.", f"Kernel: `{out['kernel']}`.", "",
+          "| dispatch | FETCH_SIZE KiB | WRITE_SIZE KiB |", "|---|---:|---:|",
+          f"| abs.out calibration (1 GiB each way) | {f_cal:.1f} | {w_cal:.1f} |",
+          f"| gelu(tanh) c2 (2 GiB each way) | {f_gel:.1f} | {w_gel:.1f} |", "",
+          f"FETCH_SIZE counts half of the bytes a streaming kernel reads on gfx950 (scale {f_scale:.5f} from the "
+          f"calibration); WRITE_SIZE is exact (scale {w_scale:.5f}).  Scaled traffic of one gelu launch: "
+          f"{int(round(read_b))} B read + {int(round(write_b))} B written = {out['bytes_per_launch']} B against "
+          f"{C2_GELU_BYTES} B algorithmic ({out['bytes_per_launch'] / C2_GELU_BYTES:.4f}): no re-reads and no write "
+          "amplification, so the gap to the roofline is achieved bandwidth, not extra traffic."]
+    with open(os.path.join(HERE, "profiles", "gelu_tanh_c2_traffic.md"), "w") as f:
+        f.write("\n".join(md) + "\n")
     print(json.dumps(out))
+
+
+# (label, exact kernel name, algorithmic bytes per launch) of the bench's
+# dominant kernels, for the roofline rows of --render-kernel-stats
+STATS_ROOFLINE_ROWS = [
+    ("c2 gelu('tanh') f32 [64,2048,4096] -- the headline kernel",
+     "sa::k_contig<64, 4, sa::UnaryOp<1, float>, float, float, float, float>", 8 * C2_N),
+    ("c2 add bf16 x + f32 bias -> f32 (both legs)",
+     "sa::k_row2d<64, 4, sa::AddOp<float>, float, float, float, sa::bf16, float>", C2_ADD_BYTES),
+    ("c1 add f32 [4096,4096]", "sa::k_contig<64, 4, sa::AddOp<float>, float, float, float, float, float>", 12 * C1_N),
+    ("c1 mul", "sa::k_contig<64, 4, sa::MulOp<float>, float, float, float, float, float>", 12 * C1_N),
+    ("c1 gelu('none')", "sa::k_contig<64, 4, sa::UnaryOp<0, float>, float, float, float, float>", 8 * C1_N),
+    ("c1 silu", "sa::k_contig<64, 4, sa::UnaryOp<2, float>, float, float, float, float>", 8 * C1_N),
+    ("c3 _log_softmax", "sa::k_lsm_fwd_reg<sa::bf16, sa::bf16, 16, true>", 4 * C3_NV),
+    ("c3 nll_loss_backward", "sa::k_nll_bwd<sa::bf16, 8>", 2 * C3_NV + 65538),
+    ("c3 _log_softmax_backward_data", "sa::k_lsm_bwd_reg<sa::bf16, sa::bf16, 16>", 6 * C3_NV),
+    ("c3 fused cross-entropy forward (opt-in)", "sa::k_ce_fwd<sa::bf16, true>", 2 * C3_NV),
+    ("c3 fused cross-entropy backward (opt-in)", "sa::k_ce_bwd<sa::bf16, true>", 4 * C3_NV),
+    ("c5 _fused_adamw_ (two launches per step, 40 + 32 tensors; half of 28 B x 1.62 G each on average)",
+     "sa::k_adamw<float, 256l, 1>", 14 * 1619066880),
+]
+
+
+def render_kernel_stats(stats_csv, bench_log):
+    """profiles/kernel_stats_all_configs.md from the kernel_stats.csv of a
+    `rocprofv3 --kernel-trace --stats` run of `bench.py --no-cpu` and that
+    run's JSON line (the bench's live HIP-event timing of the same launches)."""
+    import csv
+
+    with open(stats_csv) as f:
+        rows = [r for r in csv.DictReader(f) if "sa::" in r["Name"]]
+    line = [l for l in open(bench_log) if l.startswith("{")][-1]
+    bench = json.loads(line)
+
+    def short(n):
+        n = n.replace("void ", "")
+        return n[: n.index(">(") + 1] if ">(" in n else n.split("(")[0]
+
+    by_name = {short(r["Name"]): r for r in rows}
+    out = ["# Kernel statistics, every bench config (MI355X, gfx950)", "",
+           "Commands (repo root on the GPU box; the second runs on any machine):", "", "```",
+           "cd /tmp && export TMPDIR=/tmp && cd $GRAFT_REPO_ROOT",
+           "rocprofv3 --kernel-trace --stats --output-format csv -d gpurun_out/prof_all -o bench -- \\",
+           "    python3 bench.py --no-cpu --steps 10 > gpurun_out/prof_all/bench.log",
+           "python3 bench.py --render-kernel-stats gpurun_out/prof_all/bench_kernel_stats.csv "
+           "gpurun_out/prof_all/bench.log", "```", "",
+           "Every config runs: c1 with 6 rotating buffer sets, c2 both legs, c3 (decomposition and fused), c4 with "
+           "3 rotating input sets, c5 = 72-tensor fused AdamW, the default foreach AdamW, clip_grad_norm_ and the "
+           "foreach / AMP lines.  `k_contig<BS, VEC, ...>`, `k_row2d<BS, VEC, ...>`: BS threads per workgroup "
+           "(64 = one wavefront).  Only this library's kernels are listed; the rest of the trace is torch's own "
+           "input generation on its HIP device before the copies into supa tensors.", "",
+           "## Roofline rows (algorithmic bytes per launch / average duration)", "",
+           "| kernel | name | calls | avg us | algorithmic B | GB/s | % of 8 TB/s |",
+           "|---|---|---:|---:|---:|---:|---:|"]
+    for label, name, nbytes in STATS_ROOFLINE_ROWS:
+        r = by_name.get(name)
+        if r is None:
+            continue
+        us = float(r["AverageNs"]) / 1e3
+        g = nbytes / (us * 1e-6) / 1e9
+        out.append(f"| {label} | `{name}` | {r['Calls']} | {us:.1f} | {nbytes:,} | {g:.0f} | {g / 80:.1f} |")
+    rf = bench.get("roofline", {})
+    head = by_name.get(STATS_ROOFLINE_ROWS[0][1])
+    if head is not None and rf.get("avg_launch_ms"):
+        us = float(head["AverageNs"]) / 1e3
+        bus = rf["avg_launch_ms"] * 1e3
+        out += ["", f"Cross-check of the headline's dominant kernel: {us:.1f} us average here, {bus:.1f} us in the "
+                f"same run's live HIP-event timing (`bench.py` `roofline.avg_launch_ms`): within "
+                f"{abs(us - bus) / bus * 100:.1f} %.  The bench reports roofline.achieved = {rf.get('achieved')} GB/s "
+                f"(frac {rf.get('frac')}); HBM traffic per launch from the PMC runs "
+                f"(`gelu_tanh_c2_traffic.md`): {rf.get('traffic')} B."]
+    out += ["", "## All kernels", "", "| kernel | calls | avg us | min us | max us | % of GPU time |",
+            "|---|---:|---:|---:|---:|---:|"]
+    for r in rows:
+        out.append(f"| `{short(r['Name'])}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | "
+                   f"{float(r['MinNs']) / 1e3:.1f} | {float(r['MaxNs']) / 1e3:.1f} | {float(r['Percentage']):.4g} |")
+    path = os.path.join(HERE, "profiles", "kernel_stats_all_configs.md")
+    with open(path, "w") as f:
+        f.write("\n".join(out) + "\n")
+    print(path)
 
 
 PROBE_REPS = 3
@@ -598,7 +705,6 @@ def probe(torch, cfg):
 
 # Algorithmic bytes per dispatch of each config's dominant kernels, keyed by
 # substrings of the kernel name (the functor or kernel template).
-C1_N = 4096 * 4096
 PROBE_ALG_BYTES = {
     "c1": [("AddOp", 12 * C1_N), ("MulOp", 12 * C1_N), ("UnaryOpILi0EfE", 8 * C1_N), ("UnaryOpILi2EfE", 8 * C1_N),
            ("UnaryOp<0,", 8 * C1_N), ("UnaryOp<2,", 8 * C1_N)],
@@ -758,6 +864,9 @@ def main():
         return
     if a.derive_counters:
         derive_counters(a.derive_counters, a.config, a.stats)
+        return
+    if a.render_kernel_stats:
+        render_kernel_stats(*a.render_kernel_stats)
         return
     if a.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {a.gpus} is not supported "

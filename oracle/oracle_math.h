@@ -14,15 +14,15 @@
  * library.  Their accuracy against double-precision libm (exhaustive over
  * every binary32 input for erf and tanh) is pinned by
  * tests/test_oracle_math.py:
- *   or_expf <= 1.01 ulp, or_logf <= 0.94 ulp, or_erff <= 0.502 ulp,
+ *   or_expf <= 1.01 ulp, or_logf <= 0.94 ulp, or_erff <= 0.978 ulp,
  *   or_tanhf <= 0.5001 ulp, or_expm1f <= 1.5 ulp, or_log1pf <= 2 ulp.
  *
  * The reductions used by every primitive:
  *   exp:  Cody-Waite split x = k*ln2 + r, |r| <= ln2/2, e^r = 1 + r + r^2 P(r).
  *   log:  x = m * 2^e with m in [sqrt(1/2), sqrt(2)), f = m - 1 (exact),
  *         log1p(f) = f - f^2/2 + f^3 Q(f).
- *   erf:  binary64 core: |x| < 0.921875: x P(x^2); otherwise
- *         1 - Q(|x| - 2.4296875), Q ~ erfc on [0.921875, 3.9375); 1 beyond.
+ *   erf:  |x| < 0.921875: x + x P(x^2); otherwise 1 - Q(|x| - c), Q ~ erfc
+ *         on [0.921875, 2.25) and [2.25, 3.9375); +-1 beyond.
  *   tanh: binary64 core: tanh(a) = m / (m + 2), m = e^{2a} - 1 from
  *         2a = k ln2 + 2s and e^{2s} - 1 = s (2 + s Q(s)); the quotient
  *         through Newton steps for 1 / (m + 2).
@@ -79,60 +79,70 @@ static inline float or_logf(float x) {
   return fmaf(ef, 0.693145751953125f, fmaf(ef, 1.42860677e-06f, y));
 }
 
-/* erf and tanh round a binary64 core once to binary32, so they are correctly
- * rounded except where the exact value lies within the core's error of a
- * binary32 rounding boundary.  Binary64 fma runs at the binary32 rate on the
- * device, and only IEEE-specified operations are used (fma, multiply, add,
- * divide, integer operations on the bits, conversions), so device and
- * oracle agree bit for bit.
+/* Only IEEE-specified operations are used below (fma, multiply, add,
+ * divide, integer operations on the bits, conversions), so device and oracle
+ * agree bit for bit.
  *
- * erf: |x| < 0.921875: x P(x^2), P of degree 7 (relative error 2^-36.6
- *      against erf(x)/x); 0.921875 <= |x| < 3.9375: 1 - Q(|x| - 2.4296875),
- *      Q ~ erfc of degree 17 (absolute error 2^-33); beyond, +-1 (erfc(3.9375)
- *      < 2^-25, so erf rounds to 1 there). */
+ * erf (binary32, <= 0.978 ulp over every input; 1.5 % of results are not
+ * correctly rounded).  Three ranges of |x|:
+ *   [0, 0.921875):    x + x P(x^2), P of degree 6 (relative error 2^-31
+ *                     against erf(x)/x - 1);
+ *   [0.921875, 2.25): 1 - M(|x| - 1.5859375), M ~ erfc of degree 9;
+ *   [2.25, 3.9375):   1 - T(|x| - 3.09375), T ~ erfc of degree 9 (absolute
+ *                     errors 2^-27);
+ *   beyond: +-1 (erfc(3.9375) < 2^-25, so erf rounds to 1 there).
+ * |x| - c is exact in both erfc ranges (Sterbenz). */
 static inline float or_erff(float x) {
   const float a = fabsf(x);
-  double r;
+  float r;
   if (a < 0.921875f) {
-    const double d = (double)x;
-    const double s = d * d;  /* exact */
-    double p = -1.0281769310087121e-05;
-    p = fma(p, s, 0.00011451093107524197);
-    p = fma(p, s, -0.0008505904931369332);
-    p = fma(p, s, 0.005222301651988579);
-    p = fma(p, s, -0.026865807757633163);
-    p = fma(p, s, 0.11283787785379987);
-    p = fma(p, s, -0.37612638743636956);
-    p = fma(p, s, 1.128379167084688);
-    r = d * p;
+    const float s = x * x;
+    float p = 8.370154682779685e-05f;
+    p = fmaf(p, s, -0.0008142719161696732f);
+    p = fmaf(p, s, 0.005201033782213926f);
+    p = fmaf(p, s, -0.026859398931264877f);
+    p = fmaf(p, s, 0.11283695697784424f);
+    p = fmaf(p, s, -0.37612634897232056f);
+    p = fmaf(p, s, 0.12837916612625122f);
+    r = fmaf(x, p, x);
   } else {
-    const double t = (double)a - 2.4296875;  /* exact */
-    double q = -4.35060772382569e-08;
-    q = fma(q, t, 3.5200901969516026e-08);
-    q = fma(q, t, 7.491007346106996e-07);
-    q = fma(q, t, -1.545774571442501e-06);
-    q = fma(q, t, -3.911918849002945e-06);
-    q = fma(q, t, 1.9361311419525163e-05);
-    q = fma(q, t, -1.91757881378122e-05);
-    q = fma(q, t, -7.12297171015646e-05);
-    q = fma(q, t, 0.0003035279625931749);
-    q = fma(q, t, -0.0004350357024353315);
-    q = fma(q, t, -0.0003482345792284581);
-    q = fma(q, t, 0.003021214976043654);
-    q = fma(q, t, -0.007348327594475376);
-    q = fma(q, t, 0.010986727890450968);
-    q = fma(q, t, -0.011097466611553876);
-    q = fma(q, t, 0.007485125362503697);
-    q = fma(q, t, -0.0030806975343408726);
-    q = fma(q, t, 0.0005901597081677841);
-    r = copysign(1.0 - q, (double)x);
+    float q;
+    if (a < 2.25f) {
+      const float t = a - 1.5859375f;
+      q = -0.001323151052929461f;
+      q = fmaf(q, t, 0.0013511608121916652f);
+      q = fmaf(q, t, 0.0058217644691467285f);
+      q = fmaf(q, t, -0.01616346836090088f);
+      q = fmaf(q, t, 0.005730860400944948f);
+      q = fmaf(q, t, 0.048972442746162415f);
+      q = fmaf(q, t, -0.12256082892417908f);
+      q = fmaf(q, t, 0.1446780115365982f);
+      q = fmaf(q, t, -0.09122593700885773f);
+      q = fmaf(q, t, 0.02490621618926525f);
+    } else {
+      const float t = a - 3.09375f;
+      q = -7.529089998570271e-06f;
+      q = fmaf(q, t, 0.00010170548193855211f);
+      q = fmaf(q, t, -0.0003080983296968043f);
+      q = fmaf(q, t, 0.0005250130197964609f);
+      q = fmaf(q, t, -0.0006629122071899474f);
+      q = fmaf(q, t, 0.0006516603752970695f);
+      q = fmaf(q, t, -0.00047629239270463586f);
+      q = fmaf(q, t, 0.00024359175586141646f);
+      q = fmaf(q, t, -7.862227357691154e-05f);
+      q = fmaf(q, t, 1.2126994079153519e-05f);
+    }
+    r = copysignf(1.0f - q, x);
+    r = (a >= 3.9375f) ? copysignf(1.0f, x) : r;
   }
-  float y = (float)r;
-  y = (a >= 3.9375f) ? copysignf(1.0f, x) : y;
-  return isnan(x) ? x : y;
+  return isnan(x) ? x : r;
 }
 
-/* tanh: with a = min(|x|, 9.5) (tanh(9.5) rounds to 1), 2a = k ln2 + 2s,
+/* tanh rounds a binary64 core once to binary32, so it is correctly rounded
+ * except where the exact value lies within the core's error of a binary32
+ * rounding boundary (binary64 fma runs at the binary32 rate on the device).
+ *
+ * tanh: with a = min(|x|, 9.5) (tanh(9.5) rounds to 1), 2a = k ln2 + 2s,
  * |s| <= ln2/4, k from the 1.5 * 2^52 shifter (the low word of the sum);
  * e^{2s} - 1 = s (2 + s Q(s)), Q of degree 6 (relative error 2^-37.5);
  * m = e^{2a} - 1 = 2^k (e^{2s} - 1) + (2^k - 1), 2^k built from its exponent

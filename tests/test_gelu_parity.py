@@ -73,10 +73,10 @@ def _gelu_cr(x, approx):
 @pytest.mark.parametrize("approx, op", [("none", O.GELU), ("tanh", O.GELU_TANH)])
 def test_oracle_is_the_reference_formula(c1, approx, op):
     """Bit-exact with the reference formula evaluated with correctly rounded
-    erf / tanh, except where the oracle's erf / tanh (within 0.502 / 0.5001
-    ulp, exhaustively) is not the correctly rounded value; there the gap is
-    that one ulp of E carried through (x/2)(1 + E), plus at most one ulp of
-    the rounded 1 + E."""
+    erf / tanh, except where the oracle's erf / tanh (within 0.978 / 0.5001
+    ulp, exhaustively) is not the correctly rounded value; there the two
+    differ by one ulp of E, and the gap is that ulp carried through
+    (x/2)(1 + E), plus at most one ulp of the rounded 1 + E."""
     x = c1.numpy().ravel()
     got = O.unary(op, x)
     ref = _gelu_cr(x, approx)
@@ -87,7 +87,10 @@ def test_oracle_is_the_reference_formula(c1, approx, op):
         inner = BETA * _fma32(KAPPA, (x * x) * x, x)
         e_or, e_cr = O.unary(O.TANH, inner), np.tanh(inner.astype(np.float64)).astype(F32)
     off = e_or != e_cr
-    assert off.mean() < 5e-4  # measured: erf 0.029 % (its upper branch's 2^-33), tanh 0.00 %
+    # measured on c1: erf 5.82 % (1.46 % over all binary32 inputs; c1's
+    # arguments sit where the mid range's rounding is closest), tanh 0.00 %
+    assert off.mean() < (0.065 if approx == "none" else 5e-4)
+    assert np.all(np.abs(e_or[off].astype(np.float64) - e_cr[off]) <= f32_ulp(e_cr[off]))
     assert np.array_equal(got[~off], ref[~off])
     gap = np.abs(got[off].astype(np.float64) - ref[off])
     e = e_cr[off].astype(np.float64)
@@ -122,7 +125,7 @@ def _check_none_vs_cpu(x_t):
     Derived bound of the oracle against the exact gelu x Phi(x): z = fl(x M_SQRT1_2)
     is within 1.28 2^-24 relative of x / sqrt2 (rounding plus the float32
     constant), which moves erf by at most (2/sqrt(pi)) |z| e^-z^2 1.28 2^-24; E
-    rounds erf(z) within 0.502 ulp(E); 1 + E and the two products add at most
+    rounds erf(z) within 0.978 ulp(E); 1 + E and the two products add at most
     1.5 ulp(y).  Exempt: an element more than 2 ulp from the CPU whose gap
     is at most that bound plus the CPU's own measured distance from the exact
     value -- the gap is then the two float32 erf roundings, carried through
@@ -134,7 +137,7 @@ def _check_none_vs_cpu(x_t):
     exact = 0.5 * xd * special.erfc(-xd / math.sqrt(2.0))
     z = (x * ALPHA).astype(np.float64)
     E = special.erf(z)
-    ours = 0.5 * np.abs(xd) * (0.502 * f32_ulp(E) + 1.45 * 2.0 ** -24 * np.abs(z) * np.exp(-z * z)) \
+    ours = 0.5 * np.abs(xd) * (0.978 * f32_ulp(E) + 1.45 * 2.0 ** -24 * np.abs(z) * np.exp(-z * z)) \
         + 1.5 * f32_ulp(exact)
     assert np.all(np.abs(got - exact) <= ours)  # the derived bound itself holds
     d = f32_ulp_dist(got, cpu)
@@ -154,9 +157,9 @@ def test_gelu_tanh_vs_cpu_c2(c2_slice):
 
 
 def test_gelu_none_vs_cpu_c1(c1):
-    # measured 5.77 %: the formula's float32 cancellation for x < -1 on both
-    # sides (the same fraction as for the formula with a correctly rounded erf)
-    assert _check_none_vs_cpu(c1) <= 0.06
+    # measured 5.93 % (5.77 % for the formula with a correctly rounded erf):
+    # the formula's float32 cancellation for x < -1 on both sides
+    assert _check_none_vs_cpu(c1) <= 0.065
 
 
 def test_gelu_opt_in_forms_are_accurate():

@@ -42,7 +42,7 @@ def test_activations():
     got = O.unary(O.GELU, a)
     exact = 0.5 * x * special.erfc(-x / np.sqrt(2.0))
     z = x * np.float32(0.70710678118654752440)
-    ours = 0.5 * np.abs(x) * (0.502 * f32_ulp(special.erf(z)) + 1.45 * 2.0 ** -24 * np.abs(z) * np.exp(-z * z)) \
+    ours = 0.5 * np.abs(x) * (0.978 * f32_ulp(special.erf(z)) + 1.45 * 2.0 ** -24 * np.abs(z) * np.exp(-z * z)) \
         + 1.5 * f32_ulp(exact)
     far = f32_ulp_dist(got, ref) > 2
     gap = np.abs(got - ref.astype(np.float64))

@@ -1,9 +1,13 @@
 """Pins the oracle's float32 primitives (oracle/oracle_math.h) against
-double-precision math: random dense samples, edge values and identities.
+double-precision math: erf and tanh exhaustively over every binary32 input
+(tests/cpp/exhaustive_math.c), the others on random dense samples, edge
+values and identities.
 
 The same polynomials run on the device (csrc/kernels/devmath.h), so these
 bounds are also the accuracy of the device primitives."""
 import math
+import os
+import subprocess
 
 import numpy as np
 import pytest
@@ -22,7 +26,7 @@ EDGES = np.array([0.0, -0.0, 1e-45, -1e-45, 1e-38, 1.17549435e-38, 0.5, 1.0, 2.0
     [
         (O.EXP, np.exp, 1.01, -104.0, 89.0),
         (O.LOG, np.log, 0.94, 1e-30, 1e30),
-        (O.ERF, special.erf, 0.503, -6.0, 6.0),
+        (O.ERF, special.erf, 0.978, -6.0, 6.0),
         (O.TANH, np.tanh, 0.5002, -12.0, 12.0),
     ],
 )
@@ -38,6 +42,24 @@ def test_primitive_accuracy(op, ref, bound, lo, hi):
         exact = ref(x.astype(np.float64))
     err = ulp_vs_exact(got, exact)
     assert err.max() <= bound, (op, float(x[np.argmax(err)]), float(err.max()))
+
+
+def test_erf_tanh_exhaustive(tmp_path):
+    """Every non-negative binary32 input below saturation (erf |x| < 4, tanh
+    |x| < 10), the saturated range and the odd symmetry on a stride: erf
+    within 0.978 ulp (1.455 % of results not correctly rounded), tanh within
+    0.5001 ulp (correctly rounded but for a handful)."""
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    exe = tmp_path / "exhaustive_math"
+    subprocess.run(["gcc", "-O2", "-march=x86-64-v3", "-ffp-contract=off", "-fno-fast-math", "-fopenmp",
+                    "-std=c11", "-I", os.path.join(root, "oracle"), os.path.join(root, "tests", "cpp", "exhaustive_math.c"),
+                    "-o", str(exe), "-lm"], check=True)
+    r = subprocess.run([str(exe), "0.978", "0.5001"], capture_output=True, text=True, timeout=900)
+    assert r.returncode == 0, r.stdout + r.stderr
+    lines = r.stdout.split("\n")
+    assert lines[0].startswith("OK erf") and lines[1].startswith("OK tanh"), r.stdout
+    notcr = float(lines[0].split("notcr=")[1].split()[0])
+    assert notcr < 0.0146
 
 
 def test_expm1_log1p_accuracy_and_edges():

@@ -5,7 +5,7 @@
 // result is reproducible bit for bit by any IEEE machine with correctly
 // rounded binary32/binary64 fma, add, multiply, division, rint and ldexp.  Accuracy against
 // double-precision math, measured over every binary32 input:
-//   sa_expf <= 1.01 ulp, sa_logf <= 0.93 ulp, sa_erff <= 0.502 ulp,
+//   sa_expf <= 1.01 ulp, sa_logf <= 0.93 ulp, sa_erff <= 0.978 ulp,
 //   sa_tanhf <= 0.5001 ulp, sa_expm1f <= 1.5 ulp, sa_log1pf <= 2 ulp.
 // The polynomial coefficients were fitted for this project (weighted least
 // squares with Lawson reweighting towards minimax).
@@ -15,36 +15,26 @@
 //         e^r = 1 + r + r^2 P(r), result = ldexp(e^r, k).
 //   log:  x = m 2^e, m in [sqrt(1/2), sqrt(2)), f = m - 1 (exact),
 //         log(x) = e ln2 + f - f^2/2 + f^3 Q(f).
-//   erf:  binary64 core rounded once: |x| < 0.921875: x P(x^2); otherwise
-//         1 - Q(|x| - 2.4296875), Q ~ erfc on [0.921875, 3.9375); +-1 beyond.
+//   erf:  |x| < 0.921875: x + x P(x^2); otherwise 1 - Q(|x| - c), Q ~ erfc
+//         on [0.921875, 2.25) and on [2.25, 3.9375); +-1 beyond.
 //   tanh: binary64 core rounded once: tanh(a) = m / (m + 2), m = e^{2a} - 1
 //         from 2a = k ln2 + 2s and e^{2s} - 1 = s (2 + s Q(s)); the quotient
 //         through Newton steps for 1 / (m + 2).
-// Binary64 fma runs at the binary32 rate on gfx950, so the binary64 cores of
-// erf and tanh cost about what a binary32 evaluation with the same number of
-// terms does, and round correctly except within 2^-33 (erf) / 2^-37 (tanh)
-// of a binary32 rounding boundary.
+// Binary64 fma runs at the binary32 rate on gfx950, so tanh's binary64 core
+// costs about what a binary32 evaluation with the same number of terms does,
+// and rounds correctly except within 2^-37 of a binary32 rounding boundary.
 #pragma once
 
 #include <hip/hip_runtime.h>
 
 namespace sa {
 
-// Binary64 polynomial coefficients of the erf and tanh cores, highest degree
-// first.  They live in constant memory (not const-qualified, so the compiler
-// loads them instead of folding them): a kernel reads them once into SGPRs,
-// where every v_fma_f64 can take them as its scalar operand; as 64-bit
-// literals each use would cost two v_mov_b32 into VGPRs (gfx9 VOP3 takes no
-// literal operand).
-__constant__ inline double kErfSmall[8] = {
-    -1.0281769310087121e-05, 0.00011451093107524197, -0.0008505904931369332, 0.005222301651988579,
-    -0.026865807757633163, 0.11283787785379987, -0.37612638743636956, 1.128379167084688};
-__constant__ inline double kErfcLarge[18] = {
-    -4.35060772382569e-08, 3.5200901969516026e-08, 7.491007346106996e-07, -1.545774571442501e-06,
-    -3.911918849002945e-06, 1.9361311419525163e-05, -1.91757881378122e-05, -7.12297171015646e-05,
-    0.0003035279625931749, -0.0004350357024353315, -0.0003482345792284581, 0.003021214976043654,
-    -0.007348327594475376, 0.010986727890450968, -0.011097466611553876, 0.007485125362503697,
-    -0.0030806975343408726, 0.0005901597081677841};
+// Binary64 polynomial coefficients of the tanh core, highest degree first.
+// They live in constant memory (not const-qualified, so the compiler loads
+// them instead of folding them): a kernel reads them once into SGPRs, where
+// every v_fma_f64 can take them as its scalar operand; as 64-bit literals
+// each use would cost two v_mov_b32 into VGPRs (gfx9 VOP3 takes no literal
+// operand).
 __constant__ inline double kTanhQ[7] = {
     0.006347872054606616, 0.025478283984500305, 0.08888950583696928, 0.2666652497217727,
     0.666666655245032, 1.3333333403307956, 2.000000000042128};
@@ -134,28 +124,59 @@ __device__ __forceinline__ float sa_logf_normal(float x) {
   return fmaf(ef, 0.693145751953125f, fmaf(ef, 1.42860677e-06f, y));
 }
 
-// A branch per range: both run in a mixed wavefront, but as branches they
-// measured faster than a straight-line select (c1 gelu 26.6 us against 31.4 us).
+// erf in binary32, <= 0.978 ulp over every input (1.5 % of results not
+// correctly rounded).  Three ranges of |x|:
+//   [0, 0.921875):     x + x P(x^2), P of degree 6 (relative error 2^-31);
+//   [0.921875, 2.25):  1 - M(|x| - 1.5859375), M ~ erfc of degree 9;
+//   [2.25, 3.9375):    1 - T(|x| - 3.09375),   T ~ erfc of degree 9
+//                      (absolute errors 2^-27); +-1 beyond.
+// The subtractions |x| - c are exact (Sterbenz).  A branch per range: a
+// wavefront pays for every range one of its lanes falls in, and for N(0, 1)
+// data only about one wavefront-element in eleven reaches the tail range.
 __device__ __forceinline__ float sa_erff(float x) {
   const float a = fabsf(x);
-  double r;
+  float r;
   if (a < 0.921875f) {
-    const double d = (double)x;
-    const double s = d * d;  // exact
-    double p = kErfSmall[0];
-#pragma unroll
-    for (int i = 1; i < 8; ++i) p = fma(p, s, kErfSmall[i]);
-    r = d * p;
+    const float s = x * x;
+    float p = 8.370154682779685e-05f;
+    p = fmaf(p, s, -0.0008142719161696732f);
+    p = fmaf(p, s, 0.005201033782213926f);
+    p = fmaf(p, s, -0.026859398931264877f);
+    p = fmaf(p, s, 0.11283695697784424f);
+    p = fmaf(p, s, -0.37612634897232056f);
+    p = fmaf(p, s, 0.12837916612625122f);
+    r = fmaf(x, p, x);
   } else {
-    const double t = (double)a - 2.4296875;  // exact
-    double q = kErfcLarge[0];
-#pragma unroll
-    for (int i = 1; i < 18; ++i) q = fma(q, t, kErfcLarge[i]);
-    r = copysign(1.0 - q, (double)x);
+    float q;
+    if (a < 2.25f) {
+      const float t = a - 1.5859375f;
+      q = -0.001323151052929461f;
+      q = fmaf(q, t, 0.0013511608121916652f);
+      q = fmaf(q, t, 0.0058217644691467285f);
+      q = fmaf(q, t, -0.01616346836090088f);
+      q = fmaf(q, t, 0.005730860400944948f);
+      q = fmaf(q, t, 0.048972442746162415f);
+      q = fmaf(q, t, -0.12256082892417908f);
+      q = fmaf(q, t, 0.1446780115365982f);
+      q = fmaf(q, t, -0.09122593700885773f);
+      q = fmaf(q, t, 0.02490621618926525f);
+    } else {
+      const float t = a - 3.09375f;
+      q = -7.529089998570271e-06f;
+      q = fmaf(q, t, 0.00010170548193855211f);
+      q = fmaf(q, t, -0.0003080983296968043f);
+      q = fmaf(q, t, 0.0005250130197964609f);
+      q = fmaf(q, t, -0.0006629122071899474f);
+      q = fmaf(q, t, 0.0006516603752970695f);
+      q = fmaf(q, t, -0.00047629239270463586f);
+      q = fmaf(q, t, 0.00024359175586141646f);
+      q = fmaf(q, t, -7.862227357691154e-05f);
+      q = fmaf(q, t, 1.2126994079153519e-05f);
+    }
+    r = copysignf(1.0f - q, x);
+    r = (a >= 3.9375f) ? copysignf(1.0f, x) : r;
   }
-  float y = (float)r;
-  y = (a >= 3.9375f) ? copysignf(1.0f, x) : y;
-  return (x != x) ? x : y;
+  return (x != x) ? x : r;
 }
 
 // expm1: sa_expf's reduction and polynomial (r + r^2 P(r) is e^r - 1), then

@@ -177,11 +177,11 @@ __device__ __forceinline__ A fold_strided(A acc, int64_t first, int64_t stride, 
 // U vectors per thread: thread t of workgroup b moves vectors
 // b * BS + t + u * gridDim.x * BS (u < U) of every operand, all loads issued
 // before the first element is computed.  U = 1 for streams the memory system
-// bounds; U = 2 for functors with the kHeavy trait (the binary64 erf / tanh
+// bounds; U = 2 for functors with the kHeavy trait (the binary64 tanh
 // activations), whose arithmetic is as long as their memory time: a wave's
 // second load is then in flight while it computes the first vector (c2 gelu
-// 'tanh' 56.8 -> 68.5 %, c1 gelu 40.8 -> 60.3 % in a launch-shape sweep;
-// 4 vectors and persistent prefetching loops were no better).
+// 'tanh' 66.4 -> 70.5 % of the HBM roofline; 4 vectors and persistent
+// prefetching loops were no better in a launch-shape sweep).
 template <typename Op, typename = void> struct IsHeavy : std::false_type {};
 template <typename Op> struct IsHeavy<Op, std::void_t<decltype(Op::kHeavy)>> : std::bool_constant<Op::kHeavy> {};
 template <typename Op> constexpr int contig_unroll() { return IsHeavy<Op>::value ? 2 : 1; }

@@ -172,9 +172,10 @@ enum UnaryKind {
 
 template <int K, typename C> struct UnaryOp {
   static constexpr int arity = 1;
-  // binary64-core activations: arithmetic about as long as the memory time
-  static constexpr bool kHeavy = std::is_same<C, float>::value &&
-                                 (K == U_GELU || K == U_GELU_TANH || K == U_ERF || K == U_TANH);
+  // binary64 tanh core: arithmetic about as long as the memory time (the erf
+  // activations keep one vector per thread: their ranges are branches, and
+  // with two vectors live across them c1 gelu measured slower)
+  static constexpr bool kHeavy = std::is_same<C, float>::value && (K == U_GELU_TANH || K == U_TANH);
   __device__ __forceinline__ C operator()(const C* v) const {
     const C x = v[0];
     if constexpr (K == U_GELU) return gelu_none<C>(x);
@@ -233,7 +234,7 @@ template <int K, typename C> struct UnaryOp {
 // output (sigmoid, tanh); upstream aten activation backward formulas.
 template <int K, typename C> struct UnaryBwdOp {
   static constexpr int arity = 2;
-  static constexpr bool kHeavy = std::is_same<C, float>::value && (K == U_GELU || K == U_GELU_TANH);
+  static constexpr bool kHeavy = std::is_same<C, float>::value && K == U_GELU_TANH;
   __device__ __forceinline__ C operator()(const C* v) const {
     const C dy = v[0], x = v[1];
     if constexpr (K == U_GELU || K == U_GELU_LOGERFC) {
