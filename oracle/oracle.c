@@ -207,7 +207,7 @@ static inline float gelu_tanh_inner(float x) {
 }
 static inline float act_fwd(int op, float x) {
   switch (op) {
-    case OR_GELU: return (x * 0.5f) * (1.0f + or_erff(x * OR_SQRT1_2));
+    case OR_GELU: return (x * 0.5f) * (1.0f + or_erff_nn(x * OR_SQRT1_2));
     case OR_GELU_TANH: return (0.5f * x) * (1.0f + or_tanhf(gelu_tanh_inner(x)));
     case OR_GELU_LOGERFC: return or_gelu_none(x);
     case OR_GELU_TANH_LOGISTIC: {
@@ -245,7 +245,7 @@ static inline float act_bwd(int op, float dy, float x) {
   switch (op) {
     case OR_GELU:
     case OR_GELU_LOGERFC: {
-      const float cdf = (op == OR_GELU) ? 0.5f * (1.0f + or_erff(x * OR_SQRT1_2)) : or_phif(x);
+      const float cdf = (op == OR_GELU) ? 0.5f * (1.0f + or_erff_nn(x * OR_SQRT1_2)) : or_phif(x);
       const float pdf = or_expf((-0.5f * x) * x) * OR_GELU_BETA_NONE;
       return dy * fmaf(x, pdf, cdf);
     }

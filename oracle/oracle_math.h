@@ -92,7 +92,9 @@ static inline float or_logf(float x) {
  *                     errors 2^-27);
  *   beyond: +-1 (erfc(3.9375) < 2^-25, so erf rounds to 1 there).
  * |x| - c is exact in both erfc ranges (Sterbenz). */
-static inline float or_erff(float x) {
+/* or_erff without the NaN select (the device's sa_erff_nn): the same value
+ * for every non-NaN x; gelu uses it. */
+static inline float or_erff_nn(float x) {
   const float a = fabsf(x);
   float r;
   if (a < 0.921875f) {
@@ -131,12 +133,14 @@ static inline float or_erff(float x) {
       q = fmaf(q, t, 0.00024359175586141646f);
       q = fmaf(q, t, -7.862227357691154e-05f);
       q = fmaf(q, t, 1.2126994079153519e-05f);
+      q = (a >= 3.9375f) ? 0.0f : q;  // erf rounds to +-1 beyond
     }
     r = copysignf(1.0f - q, x);
-    r = (a >= 3.9375f) ? copysignf(1.0f, x) : r;
   }
-  return isnan(x) ? x : r;
+  return r;
 }
+
+static inline float or_erff(float x) { return isnan(x) ? x : or_erff_nn(x); }
 
 /* tanh rounds a binary64 core once to binary32, so it is correctly rounded
  * except where the exact value lies within the core's error of a binary32

@@ -133,7 +133,9 @@ __device__ __forceinline__ float sa_logf_normal(float x) {
 // The subtractions |x| - c are exact (Sterbenz).  A branch per range: a
 // wavefront pays for every range one of its lanes falls in, and for N(0, 1)
 // data only about one wavefront-element in eleven reaches the tail range.
-__device__ __forceinline__ float sa_erff(float x) {
+// sa_erff without the NaN select, for callers whose result is NaN for a NaN
+// x anyway (gelu's (x/2)(1 + erf)): the same value for every other x.
+__device__ __forceinline__ float sa_erff_nn(float x) {
   const float a = fabsf(x);
   float r;
   if (a < 0.921875f) {
@@ -172,12 +174,14 @@ __device__ __forceinline__ float sa_erff(float x) {
       q = fmaf(q, t, 0.00024359175586141646f);
       q = fmaf(q, t, -7.862227357691154e-05f);
       q = fmaf(q, t, 1.2126994079153519e-05f);
+      q = (a >= 3.9375f) ? 0.0f : q;  // erf rounds to +-1 beyond
     }
     r = copysignf(1.0f - q, x);
-    r = (a >= 3.9375f) ? copysignf(1.0f, x) : r;
   }
-  return (x != x) ? x : r;
+  return r;
 }
+
+__device__ __forceinline__ float sa_erff(float x) { return (x != x) ? x : sa_erff_nn(x); }
 
 // expm1: sa_expf's reduction and polynomial (r + r^2 P(r) is e^r - 1), then
 // 2^k (e^r - 1) + (2^k - 1), or 2^k e^r - 1 from k = 25 on.

@@ -107,7 +107,8 @@ static_assert((float)kGeluKappa == 0.044715f, "constant rounding");
 // 'tanh' (0.5 * x) * (1 + tanh(b * (x + k x^3))), x^3 = (x * x) * x and
 // x + k x^3 one fused multiply-add, as the reference's compilers contract it.
 template <typename C> __device__ __forceinline__ C gelu_none(C x) {
-  if constexpr (std::is_same<C, float>::value) return (x * 0.5f) * (1.0f + sa_erff(x * (float)kSqrt1_2));
+  // a NaN x makes x * 0.5 NaN, so erf needs no NaN select
+  if constexpr (std::is_same<C, float>::value) return (x * 0.5f) * (1.0f + sa_erff_nn(x * (float)kSqrt1_2));
   else return (x * C(0.5)) * (C(1) + erf(x * C(kSqrt1_2)));
 }
 template <typename C> __device__ __forceinline__ C gelu_tanh(C x) {
@@ -240,7 +241,8 @@ template <int K, typename C> struct UnaryBwdOp {
     if constexpr (K == U_GELU || K == U_GELU_LOGERFC) {
       C cdf;
       if constexpr (K == U_GELU_LOGERFC && std::is_same<C, float>::value) cdf = sa_phif(x);
-      else cdf = C(0.5) * (C(1) + erfx<C>(x * C(kSqrt1_2)));
+      else if constexpr (std::is_same<C, float>::value) cdf = 0.5f * (1.0f + sa_erff_nn(x * (float)kSqrt1_2));
+      else cdf = C(0.5) * (C(1) + erf(x * C(kSqrt1_2)));
       const C pdf = expx<C>((C(-0.5) * x) * x) * C(kGeluBetaNone);
       return dy * muladd<C>(x, pdf, cdf);
     } else if constexpr (K == U_GELU_TANH || K == U_GELU_TANH_LOGISTIC) {
