@@ -73,7 +73,7 @@ def _gelu_cr(x, approx):
 @pytest.mark.parametrize("approx, op", [("none", O.GELU), ("tanh", O.GELU_TANH)])
 def test_oracle_is_the_reference_formula(c1, approx, op):
     """Bit-exact with the reference formula evaluated with correctly rounded
-    erf / tanh, except where the oracle's erf / tanh (within 0.978 / 0.5001
+    erf / tanh, except where the oracle's erf / tanh (within 0.978 / 0.5031
     ulp, exhaustively) is not the correctly rounded value; there the two
     differ by one ulp of E, and the gap is that ulp carried through
     (x/2)(1 + E), plus at most one ulp of the rounded 1 + E."""
@@ -88,8 +88,9 @@ def test_oracle_is_the_reference_formula(c1, approx, op):
         e_or, e_cr = O.unary(O.TANH, inner), np.tanh(inner.astype(np.float64)).astype(F32)
     off = e_or != e_cr
     # measured on c1: erf 5.82 % (1.46 % over all binary32 inputs; c1's
-    # arguments sit where the mid range's rounding is closest), tanh 0.00 %
-    assert off.mean() < (0.065 if approx == "none" else 5e-4)
+    # arguments sit where the mid range's rounding is closest), tanh 0.056 %
+    # (0.008 % over all inputs)
+    assert off.mean() < (0.065 if approx == "none" else 1e-3)
     assert np.all(np.abs(e_or[off].astype(np.float64) - e_cr[off]) <= f32_ulp(e_cr[off]))
     assert np.array_equal(got[~off], ref[~off])
     gap = np.abs(got[off].astype(np.float64) - ref[off])
@@ -100,7 +101,7 @@ def test_oracle_is_the_reference_formula(c1, approx, op):
 
 def _check_tanh_vs_cpu(x_t):
     """CPU: Gelu.h:43-51 with Sleef_tanhf16_u10 (within 1.0 ulp;
-    vec512_float.h:516); the oracle's tanh is within 0.5001 ulp, so the two
+    vec512_float.h:516); the oracle's tanh is within 0.5031 ulp, so the two
     rounded tanh values T differ by at most one ulp(T).  Exempt: an element
     more than 2 ulp from the CPU whose gap is at most 2 ulp + 0.5 |x| ulp(T)."""
     x = x_t.numpy().ravel()

@@ -27,7 +27,7 @@ EDGES = np.array([0.0, -0.0, 1e-45, -1e-45, 1e-38, 1.17549435e-38, 0.5, 1.0, 2.0
         (O.EXP, np.exp, 1.01, -104.0, 89.0),
         (O.LOG, np.log, 0.94, 1e-30, 1e30),
         (O.ERF, special.erf, 0.978, -6.0, 6.0),
-        (O.TANH, np.tanh, 0.5002, -12.0, 12.0),
+        (O.TANH, np.tanh, 0.5032, -12.0, 12.0),
     ],
 )
 def test_primitive_accuracy(op, ref, bound, lo, hi):
@@ -48,13 +48,13 @@ def test_erf_tanh_exhaustive(tmp_path):
     """Every non-negative binary32 input below saturation (erf |x| < 4, tanh
     |x| < 10), the saturated range and the odd symmetry on a stride: erf
     within 0.978 ulp (1.455 % of results not correctly rounded), tanh within
-    0.5001 ulp (correctly rounded but for a handful)."""
+    0.5031 ulp (0.008 % not correctly rounded)."""
     root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
     exe = tmp_path / "exhaustive_math"
     subprocess.run(["gcc", "-O2", "-march=x86-64-v3", "-ffp-contract=off", "-fno-fast-math", "-fopenmp",
                     "-std=c11", "-I", os.path.join(root, "oracle"), os.path.join(root, "tests", "cpp", "exhaustive_math.c"),
                     "-o", str(exe), "-lm"], check=True)
-    r = subprocess.run([str(exe), "0.978", "0.5001"], capture_output=True, text=True, timeout=900)
+    r = subprocess.run([str(exe), "0.978", "0.5031"], capture_output=True, text=True, timeout=900)
     assert r.returncode == 0, r.stdout + r.stderr
     lines = r.stdout.split("\n")
     assert lines[0].startswith("OK erf") and lines[1].startswith("OK tanh"), r.stdout
