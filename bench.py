@@ -457,6 +457,20 @@ def cpu_aten_baselines(torch, configs):
     return res
 
 
+def _run_args(path, suffix):
+    """(-d directory, -o prefix) of the rocprofv3 run that wrote `path`
+    (`<dir>/<prefix><suffix>`), for the commands a summary records."""
+    d, b = os.path.split(path)
+    return (d or "."), (b[: -len(suffix)] if b.endswith(suffix) else b)
+
+
+def _counters_in(path):
+    import csv
+
+    with open(path) as f:
+        return sorted({r["Counter_Name"] for r in csv.DictReader(f)})
+
+
 def traffic_from_profiles():
     p = os.path.join(HERE, "profiles", "gelu_tanh_c2_traffic.json")
     if os.path.exists(p):
@@ -524,12 +538,11 @@ def derive_traffic(fetch_csv, write_csv):
           f"exactly 1 GiB read and 1 GiB written per dispatch -- then {PROBE_REPS}x `gelu.out(approximate='tanh')` "
           "over the c2 f32 tensor [64,2048,4096]):", "", "```",
           "cd /tmp && export TMPDIR=/tmp && cd $GRAFT_REPO_ROOT",
-          "timeout -s KILL 120 rocprofv3 --pmc FETCH_SIZE --output-format csv -d gpurun_out/prof_fetch -o probe -- "
-          "python3 bench.py --probe",
-          "timeout -s KILL 120 rocprofv3 --pmc WRITE_SIZE --output-format csv -d gpurun_out/prof_write -o probe -- "
-          "python3 bench.py --probe",
-          "python3 bench.py --derive-traffic gpurun_out/prof_fetch/probe_counter_collection.csv \\",
-          "                                  gpurun_out/prof_write/probe_counter_collection.csv", "```", "",
+          "timeout -s KILL 120 rocprofv3 --pmc FETCH_SIZE --output-format csv -d {} -o {} -- python3 bench.py --probe"
+          .format(*_run_args(fetch_csv, "_counter_collection.csv")),
+          "timeout -s KILL 120 rocprofv3 --pmc WRITE_SIZE --output-format csv -d {} -o {} -- python3 bench.py --probe"
+          .format(*_run_args(write_csv, "_counter_collection.csv")),
+          f"python3 bench.py --derive-traffic {fetch_csv} {write_csv}", "```", "",
           "The last command (CPU only) writes `gelu_tanh_c2_traffic.json` and this file; `bench.py` reports the "
           "json's `bytes_per_launch` as `roofline.traffic`.", f"Kernel: `{out['kernel']}`.", "",
           "| dispatch | FETCH_SIZE KiB | WRITE_SIZE KiB |", "|---|---:|---:|",
@@ -585,10 +598,10 @@ def render_kernel_stats(stats_csv, bench_log):
     out = ["# Kernel statistics, every bench config (MI355X, gfx950)", "",
            "Commands (repo root on the GPU box; the second runs on any machine):", "", "```",
            "cd /tmp && export TMPDIR=/tmp && cd $GRAFT_REPO_ROOT",
-           "rocprofv3 --kernel-trace --stats --output-format csv -d gpurun_out/prof_all -o bench -- \\",
-           "    python3 bench.py --no-cpu --steps 10 > gpurun_out/prof_all/bench.log",
-           "python3 bench.py --render-kernel-stats gpurun_out/prof_all/bench_kernel_stats.csv "
-           "gpurun_out/prof_all/bench.log", "```", "",
+           "rocprofv3 --kernel-trace --stats --output-format csv -d {} -o {} -- \\".format(
+               *_run_args(stats_csv, "_kernel_stats.csv")),
+           f"    python3 bench.py --no-cpu --steps 10 > {bench_log}",
+           f"python3 bench.py --render-kernel-stats {stats_csv} {bench_log}", "```", "",
            "Every config runs: c1 with 6 rotating buffer sets, c2 both legs, c3 (decomposition and fused), c4 with "
            "3 rotating input sets, c5 = 72-tensor fused AdamW, the default foreach AdamW, clip_grad_norm_ and the "
            "foreach / AMP lines.  `k_contig<BS, VEC, ...>`, `k_row2d<BS, VEC, ...>`: BS threads per workgroup "
@@ -652,10 +665,10 @@ def render_patterns(stats_csv, log_path):
            "Each library kernel's fraction of the 8 TB/s roofline is read against the row of its pattern.", "",
            "Commands (repo root on the GPU box; the last runs on any machine):", "", "```",
            "cd /tmp && export TMPDIR=/tmp && cd $GRAFT_REPO_ROOT",
-           "rocprofv3 --kernel-trace --stats --output-format csv -d gpurun_out/prof_patterns -o patterns -- \\",
-           "    torch-supa_amd/torch_supa/supa_patterns > gpurun_out/prof_patterns/patterns.log",
-           "python3 bench.py --render-patterns gpurun_out/prof_patterns/patterns_kernel_stats.csv "
-           "gpurun_out/prof_patterns/patterns.log", "```", "",
+           "rocprofv3 --kernel-trace --stats --output-format csv -d {} -o {} -- \\".format(
+               *_run_args(stats_csv, "_kernel_stats.csv")),
+           f"    torch-supa_amd/torch_supa/supa_patterns > {log_path}",
+           f"python3 bench.py --render-patterns {stats_csv} {log_path}", "```", "",
            "`python3 bench.py --patterns` runs the probe alone.", "",
            "## The probe's own timing (HIP events, average over the timed launches)", "", text, "",
            "## rocprofv3 per-kernel averages (all launches, warm-up included)", "",
@@ -863,24 +876,22 @@ def derive_counters(csvs, cfg, stats_csv=None):
     with open(base + ".json", "w") as f:
         json.dump(out, f, indent=1)
         f.write("\n")
+    # the commands that produced the inputs, from their paths
+    cmds = []
+    if stats_csv:
+        cmds.append("rocprofv3 --kernel-trace --stats --output-format csv -d {} -o {} -- python3 bench.py --probe {}"
+                    .format(*_run_args(stats_csv, "_kernel_stats.csv"), cfg))
+    for path in csvs:
+        cmds.append("rocprofv3 --pmc {} --output-format csv -d {} -o {} -- python3 bench.py --probe {}"
+                    .format(" ".join(_counters_in(path)), *_run_args(path, "_counter_collection.csv"), cfg))
+    cmds.append(f"python3 bench.py --derive-counters {' '.join(csvs)} --config {cfg}"
+                + (f" --stats {stats_csv}" if stats_csv else ""))
     # the summary table
     lines = [f"# {cfg}: per-kernel counters (rocprofv3 on MI355X)", "", PROBE_NOTES.get(cfg, cfg) + ".", "",
              "Each dominant aten call runs 3 times after 3 calibration dispatches (`abs.out` over 2^28 f32: "
              "1 GiB read, 1 GiB written).  Commands (from the repository root, on the GPU box):", "", "```",
              "cd /tmp && export TMPDIR=/tmp && cd $GRAFT_REPO_ROOT",
-             f"rocprofv3 --kernel-trace --stats --output-format csv -d gpurun_out/prof/{cfg}_trace -o run -- "
-             f"python3 bench.py --probe {cfg}",
-             f"rocprofv3 --pmc FETCH_SIZE --output-format csv -d gpurun_out/prof/{cfg}_fetch -o run -- "
-             f"python3 bench.py --probe {cfg}",
-             f"rocprofv3 --pmc WRITE_SIZE --output-format csv -d gpurun_out/prof/{cfg}_write -o run -- "
-             f"python3 bench.py --probe {cfg}",
-             "rocprofv3 --pmc SQ_WAVES SQ_INSTS_VALU SQ_ACTIVE_INST_VALU SQ_WAVE_CYCLES SQ_BUSY_CYCLES "
-             "SQ_LDS_BANK_CONFLICT SQ_LDS_IDX_ACTIVE SQ_INSTS_VALU_TRANS_F32 GRBM_GUI_ACTIVE --output-format csv "
-             f"-d gpurun_out/prof/{cfg}_sq -o run -- python3 bench.py --probe {cfg}",
-             f"python3 bench.py --derive-counters gpurun_out/prof/{cfg}_fetch/run_counter_collection.csv "
-             f"gpurun_out/prof/{cfg}_write/run_counter_collection.csv "
-             f"gpurun_out/prof/{cfg}_sq/run_counter_collection.csv --config {cfg} "
-             f"--stats gpurun_out/prof/{cfg}_trace/run_kernel_stats.csv",
+             *cmds,
              "```", "",
              f"FETCH_SIZE scale {scale.get('FETCH_SIZE', 0):.5f}, WRITE_SIZE scale {scale.get('WRITE_SIZE', 0):.5f} "
              "(known bytes / counter for the calibration kernel).  Traffic = scaled FETCH + WRITE per dispatch.  "
