@@ -69,24 +69,38 @@ def parse():
     return ap.parse_args()
 
 
+BATCH_MS = 50.0  # a timed batch lasts at least this long
+BATCHES = 5
+TIMING = (f"per_config: warm-up, then the median of {BATCHES} batches of back-to-back calls, each batch at least "
+          f"{BATCH_MS:.0f} ms (or the config's call count if longer), between two HIP events on the supa stream")
+
+
 class Timer:
-    """HIP events on the supa stream."""
+    """HIP events on the supa stream: warm-up calls, then BATCHES batches of
+    back-to-back calls, each batch at least BATCH_MS long (and at least
+    `iters` calls); returns the median batch's time per call in ms."""
 
     def __init__(self, torch):
         self.torch = torch
 
-    def time(self, fn, iters, warmup=2):
+    def _batch(self, fn, k):
         t = self.torch
-        for _ in range(warmup):
-            fn()
         t.supa.synchronize()
         e0, e1 = t.supa.Event(), t.supa.Event()
         e0.record()
-        for _ in range(iters):
+        for _ in range(k):
             fn()
         e1.record()
         e1.synchronize()
-        return e0.elapsed_time(e1) / iters  # ms
+        return e0.elapsed_time(e1) / k
+
+    def time(self, fn, iters, warmup=2):
+        for _ in range(warmup):
+            fn()
+        per_call = self._batch(fn, max(1, min(iters, 3)))  # sizes the batches
+        k = max(iters, int(BATCH_MS / max(per_call, 1e-4)) + 1)
+        times = sorted(self._batch(fn, k) for _ in range(BATCHES))
+        return times[len(times) // 2]  # ms
 
 
 def gen(torch, shape, seed, dtype, kind="normal", a=0.0, b=1.0):
@@ -1045,6 +1059,7 @@ def main():
         "cpu_port": cpu_port,
         "per_config": per,
         "cpu_fallback_ops": fb,
+        "timing": TIMING,
         "host": platform.node(),
     }
     print(json.dumps(line), flush=True)
