@@ -25,6 +25,8 @@ constexpr c10::DeviceType kSupa = c10::DeviceType::PrivateUse1;
 
 // Turns a non-zero C-ABI status into a c10::Error naming the op.
 void check_status(int status, const char* what);
+// SUPA_LAUNCH_BLOCKING / CUDA_LAUNCH_BLOCKING: check_status synchronises after each launch.
+bool launch_blocking();
 
 // ------------------------------------------------------------- runtime
 c10::DeviceIndex device_count() noexcept;

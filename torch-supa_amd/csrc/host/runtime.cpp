@@ -25,6 +25,8 @@
 // (after waiting for them), is released and the allocation retried once
 // before an OutOfMemoryError.  Blocks are never split, so a cached block is
 // reused only by a request of at least half its size.
+// PYTORCH_NO_SUPA_MEMORY_CACHING turns caching off (each free waits for the
+// block's streams and calls hipFree), for device memory debugging.
 #include <ATen/detail/PrivateUse1HooksInterface.h>
 #include <ATen/native/CPUFallback.h>
 #include <c10/core/Allocator.h>
@@ -46,8 +48,33 @@
 
 namespace supa {
 
+namespace {
+bool env_on(const char* name) {
+  const char* e = std::getenv(name);
+  return e && *e && std::string(e) != "0";
+}
+// SUPA_LAUNCH_BLOCKING=1 or CUDA_LAUNCH_BLOCKING=1, the switches the
+// reference reads (SUPAMiscFunctions.cpp:10-12): every launch is followed by
+// a synchronisation of the current stream, so a kernel error (or an nll
+// target out of range) is reported by the op that caused it.
+const bool g_launch_blocking = env_on("SUPA_LAUNCH_BLOCKING") || env_on("CUDA_LAUNCH_BLOCKING");
+}  // namespace
+
+bool launch_blocking() { return g_launch_blocking; }
+
 void check_status(int status, const char* what) {
-  TORCH_CHECK(status == SUPA_AMD_OK, what, ": ", supa_amd_status_string(status), " (status ", status, ")");
+  TORCH_CHECK(status == SUPA_AMD_OK, what, ": ", supa_amd_status_string(status), " (status ", status, ")",
+              status > 0 && !g_launch_blocking
+                  ? "\nsupa kernel errors can surface at a later call; SUPA_LAUNCH_BLOCKING=1 reports them at "
+                    "the launch"
+                  : "");
+  if (g_launch_blocking) {
+    const c10::DeviceIndex d = current_device();
+    const hipError_t e = hipStreamSynchronize(current_stream(d));
+    if (e != hipSuccess) (void)hipGetLastError();
+    TORCH_CHECK(e == hipSuccess, what, ": kernel failed: ", hipGetErrorString(e));
+    check_device_errors(d);
+  }
 }
 
 bool dtype_supported(c10::ScalarType t) {
@@ -257,7 +284,7 @@ class CachingAllocator final : public c10::Allocator {
     const size_t sz = round_size(nbytes);
     const hipStream_t st = current_stream(dev);
     void* p = nullptr;
-    {
+    if (!uncached_) {
       std::lock_guard<std::mutex> g(mu_);
       process_pending_locked(dev, false);
       p = take_cached_locked(dev, st, sz);
@@ -300,6 +327,18 @@ class CachingAllocator final : public c10::Allocator {
     live_.erase(it);
     stats_[b.device].allocated -= (int64_t)b.size;
     stats_[b.device].num_frees += 1;
+    if (uncached_) {
+      // no caching: wait for every stream that used the block, then free it
+      const int prev = current_device();
+      if (prev != b.device) (void)hipSetDevice(b.device);
+      (void)hipStreamSynchronize(b.stream);
+      for (hipStream_t use : b.uses) (void)hipStreamSynchronize(use);
+      (void)hipFree(b.ptr);
+      (void)hipGetLastError();
+      if (prev != b.device) (void)hipSetDevice(prev);
+      stats_[b.device].reserved -= (int64_t)b.size;
+      return;
+    }
     if (b.uses.empty()) {
       free_[b.device][b.stream].emplace(b.size, b.ptr);
       return;
@@ -470,6 +509,10 @@ class CachingAllocator final : public c10::Allocator {
     return p;
   }
 
+  // PYTORCH_NO_SUPA_MEMORY_CACHING (any value), as the reference reads it
+  // (SUPACachingAllocator.cpp:2975-2978): every block goes to hipMalloc and
+  // back to hipFree, so device memory checkers see each allocation.
+  const bool uncached_ = std::getenv("PYTORCH_NO_SUPA_MEMORY_CACHING") != nullptr;
   std::mutex mu_;
   std::map<hipStream_t, std::multimap<size_t, void*>> free_[kMaxDevices];
   std::vector<Pending> pending_[kMaxDevices];
