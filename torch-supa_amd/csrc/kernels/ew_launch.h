@@ -168,18 +168,19 @@ int launch_static(const Op& op, const supa_amd_ew_desc& d, const int* tin, hipSt
           tg.in_sb = bd > 0 ? b.st[1][bd] : 0;
           tg.out_sk = b.st[0][k];
           tg.out_sb = bd > 0 ? b.st[0][bd] : 0;
-          const uint32_t t0 = (tg.d0 + kTile - 1) / kTile, tk = (tg.dk + kTile - 1) / kTile;
+          using S0 = typename NthT<0, S...>::type;
+          constexpr int VI = 16 / (int)sizeof(S0), VO = 16 / (int)sizeof(OT);
+          const bool vec = VI > 1 && VO > 1 && tg.d0 % VO == 0 && tg.dk % VI == 0 && tg.in_s0 % VI == 0 &&
+                           tg.in_sb % VI == 0 && tg.out_sk % VO == 0 && tg.out_sb % VO == 0 && aligned(b.p[1], 16) &&
+                           aligned(b.p[0], 16);
+          const uint32_t tile_k = vec ? (uint32_t)tile_k_vec<S0>() : (uint32_t)kTile;  // the kernel's tile width
+          const uint32_t t0 = (tg.d0 + kTile - 1) / kTile, tk = (tg.dk + tile_k - 1) / tile_k;
           tg.t0 = FastDiv(t0);
           tg.tk = FastDiv(tk);
           const uint64_t blocks = (uint64_t)t0 * tk * tg.db;
           if (blocks < (1ull << 31)) {
-            using S0 = typename NthT<0, S...>::type;
-            constexpr int VI = 16 / (int)sizeof(S0), VO = 16 / (int)sizeof(OT);
-            const bool vec = VI > 1 && VO > 1 && tg.d0 % VO == 0 && tg.dk % VI == 0 && tg.in_s0 % VI == 0 &&
-                             tg.in_sb % VI == 0 && tg.out_sk % VO == 0 && tg.out_sb % VO == 0 && aligned(b.p[1], 16) &&
-                             aligned(b.p[0], 16);
             if (vec)
-              k_transpose_vec<Op, C, CT, OT, S0><<<(unsigned)blocks, kBlock, 0, st>>>(
+              k_transpose_vec<Op, C, CT, OT, S0><<<(unsigned)blocks, kTileVecBlock, 0, st>>>(
                   op, static_cast<const S0*>(b.p[1]), static_cast<OT*>(b.p[0]), tg);
             else
               k_transpose<Op, C, CT, OT, S0><<<(unsigned)blocks, kBlock, 0, st>>>(

@@ -493,6 +493,7 @@ template <typename C> struct WhereOp {
 // ------------------------------------------------------------ copy/fill
 template <typename C> struct IdentityOp {
   static constexpr int arity = 1;
+  static constexpr bool kIdentity = true;  // a same-dtype copy may move the stored bits
   __device__ __forceinline__ C operator()(const C* x) const { return x[0]; }
 };
 
