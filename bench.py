@@ -579,6 +579,8 @@ STATS_ROOFLINE_ROWS = [
      "sa::k_contig<64, 4, sa::UnaryOp<1, float>, float, float, float, float>", 8 * C2_N),
     ("c2 add bf16 x + f32 bias -> f32 (both legs)",
      "sa::k_row2d<64, 4, sa::AddOp<float>, float, float, float, sa::bf16, float>", C2_ADD_BYTES),
+    ("c2 transposed leg: bf16 x `.contiguous()` (LDS-tiled transpose)",
+     "sa::k_transpose_vec<sa::IdentityOp<float>, float, sa::bf16, sa::bf16, sa::bf16>", 4 * C2_N),
     ("c1 add f32 [4096,4096]", "sa::k_contig<64, 4, sa::AddOp<float>, float, float, float, float, float>", 12 * C1_N),
     ("c1 mul", "sa::k_contig<64, 4, sa::MulOp<float>, float, float, float, float, float>", 12 * C1_N),
     ("c1 gelu('none')", "sa::k_contig<64, 4, sa::UnaryOp<0, float>, float, float, float, float>", 8 * C1_N),
@@ -716,8 +718,11 @@ def _probe_ops(torch, cfg):
         x, bias = c2_inputs(torch, transposed=False)
         y = x + bias
         z = torch.empty_like(y)
+        xt, _ = c2_inputs(torch, transposed=True)
+        xc = torch.empty(xt.shape, dtype=xt.dtype, device="supa")
         return [("add", lambda: torch.add(x, bias, out=y)),
-                ("gelu_tanh", lambda: torch.ops.aten.gelu.out(y, approximate="tanh", out=z))]
+                ("gelu_tanh", lambda: torch.ops.aten.gelu.out(y, approximate="tanh", out=z)),
+                ("transposed_contiguous", lambda: xc.copy_(xt))]
     if cfg == "c3":
         lx = gen(torch, (C3_N, C3_V), 4, torch.bfloat16, b=2.0)
         tgt = torch.randint(0, C3_V, (C3_N,)).to("supa")
@@ -786,7 +791,8 @@ def probe(torch, cfg):
 PROBE_ALG_BYTES = {
     "c1": [("AddOp", 12 * C1_N), ("MulOp", 12 * C1_N), ("UnaryOpILi0EfE", 8 * C1_N), ("UnaryOpILi2EfE", 8 * C1_N),
            ("UnaryOp<0,", 8 * C1_N), ("UnaryOp<2,", 8 * C1_N)],
-    "c2": [("AddOp", C2_ADD_BYTES), ("UnaryOp<1,", C2_GELU_BYTES), ("UnaryOpILi1EfE", C2_GELU_BYTES)],
+    "c2": [("AddOp", C2_ADD_BYTES), ("UnaryOp<1,", C2_GELU_BYTES), ("UnaryOpILi1EfE", C2_GELU_BYTES),
+           ("k_transpose_vec", 4 * C2_N)],
     "c3": [("k_lsm_fwd_reg", C3_BYTES["_log_softmax"]), ("k_nll_bwd", C3_BYTES["nll_loss_backward"]),
            ("k_lsm_bwd_reg", C3_BYTES["_log_softmax_backward_data"])],
     "c4": [("MseOp", 12 * 32 * 1048576), ("BceBwdOp", 16 * 32 * 1048576 + 4 * 1048576)],
@@ -798,7 +804,8 @@ PROBE_ALG_BYTES = {
 PROBE_NOTES = {
     "c1": "c1: [4096,4096] f32 add, mul, gelu('none'), silu (64 MiB operands; the probe runs one buffer set, "
           "so a repeat can hit the 256 MB MALL -- the bench rotates six sets)",
-    "c2": "c2 contiguous: bf16 [64,2048,4096] + f32 bias -> f32, then gelu('tanh') over the f32 tensor",
+    "c2": "c2 contiguous: bf16 [64,2048,4096] + f32 bias -> f32, then gelu('tanh') over the f32 tensor; "
+          "c2 transposed leg: `.contiguous()` of the bf16 [64,4096,2048] tensor's (1, 2) transpose",
     "c3": "c3: bf16 logits [8192,128256]: _log_softmax, nll_loss_forward, nll_loss_backward, "
           "_log_softmax_backward_data",
     "c4": "c4: [32,1048576] f32: mse 'none' and 'sum' forward, BCE-with-logits (pos_weight) 'none' forward "

@@ -490,7 +490,14 @@ template <typename Op, typename C, typename CT, typename OT, typename S>
 __global__ void __launch_bounds__(kTileVecBlock)
 k_transpose_vec(Op op, const S* __restrict__ in, OT* __restrict__ out, TransposeGeom g) {
   constexpr int VI = 16 / sizeof(S), VO = 16 / sizeof(OT), TK = tile_k_vec<S>();
-  __shared__ __align__(16) S tile[kTile][TK + VI];
+  // LDS swizzle: 16-byte chunk q of tile row r sits at chunk q ^ swz(r).  The
+  // store loop reads, per instruction, one element of each of the 64 / VO
+  // rows wv * VO + j (wv = 0 .. 64 / VO - 1) in a run of VO columns
+  // (max(1, SW) chunks); in unswizzled 512-byte rows those rows fall in the
+  // same banks.  swz(r) = (r / VO) SW moves each wv to its own chunks.
+  constexpr int SW = sizeof(S) > sizeof(OT) ? (int)(sizeof(S) / sizeof(OT)) : 1;
+  static_assert((kTile / VO) * SW <= TK / VI, "the swizzle stays inside a row");
+  __shared__ __align__(16) S tile[kTile][TK];
   uint32_t q, i0t, ikt, ib;
   g.tk.divmod(blockIdx.x, q, ikt);
   g.t0.divmod(q, ib, i0t);
@@ -516,7 +523,8 @@ k_transpose_vec(Op op, const S* __restrict__ in, OT* __restrict__ out, Transpose
 #pragma unroll
   for (int p = 0; p < NP; ++p) {
     const uint32_t i0 = a0 + lr + p * RPI;
-    if (i0 < g.d0 && ik < g.dk) *reinterpret_cast<u32x4_t*>(&tile[lr + p * RPI][lv * VI]) = buf[p];
+    const int r = lr + p * RPI;
+    if (i0 < g.d0 && ik < g.dk) *reinterpret_cast<u32x4_t*>(&tile[r][(lv ^ (r / VO * SW)) * VI]) = buf[p];
   }
   __syncthreads();
   constexpr int VPC = kTile / VO, CPI = kTileVecBlock / VPC;  // store: vectors per tile column, columns per pass
@@ -524,14 +532,15 @@ k_transpose_vec(Op op, const S* __restrict__ in, OT* __restrict__ out, Transpose
 #pragma unroll
   for (int c = wc; c < TK; c += CPI) {
     const uint32_t ik = ak + c, i0 = a0 + wv * VO;
+    const int pc = ((c / VI) ^ (wv * SW)) * VI + c % VI;  // rows wv * VO + j share swz
     if (ik < g.dk && i0 < g.d0) {
       Vec<OT, VO> o;
 #pragma unroll
       for (int j = 0; j < VO; ++j) {
         if constexpr (IsIdentity<Op>::value && std::is_same<S, OT>::value) {
-          o.v[j] = tile[wv * VO + j][c];  // a same-dtype copy moves the stored bits (NaN payloads too)
+          o.v[j] = tile[wv * VO + j][pc];  // a same-dtype copy moves the stored bits (NaN payloads too)
         } else {
-          const C x = load_cvt<C, CT>(tile[wv * VO + j][c]);
+          const C x = load_cvt<C, CT>(tile[wv * VO + j][pc]);
           o.v[j] = from_arith<OT>(op(&x));
         }
       }
