@@ -173,6 +173,39 @@ def test_transpose_copies(shape, dtype, no_fallback):
         assert torch.equal(out.cpu(), torch.neg(xt))
 
 
+INT_DTYPES = (torch.uint8, torch.int8, torch.int32, torch.int64)
+
+
+def _cast_source(src, dst, shape, seed):
+    """Values every src -> dst conversion maps alike on both sides: with an
+    integer on either side they stay in [0, 200) ([0, 128) with int8)."""
+    x = seeded(shape, seed, 3.0)
+    if src in INT_DTYPES or dst in INT_DTYPES:
+        x = (x.abs() * 20.0).clamp(max=127.0 if torch.int8 in (src, dst) else 199.0)
+    return x > 0 if src == torch.bool else x.to(src)
+
+
+@pytest.mark.parametrize("src, dst", [
+    (torch.float32, torch.bfloat16), (torch.float32, torch.float16), (torch.float64, torch.float32),
+    (torch.float64, torch.bfloat16), (torch.float64, torch.uint8), (torch.int64, torch.int32),
+    (torch.bfloat16, torch.float32), (torch.uint8, torch.float32), (torch.int8, torch.float64),
+    (torch.float32, torch.int32), (torch.bool, torch.float32), (torch.uint8, torch.uint8)])
+def test_transposing_casts(src, dst, no_fallback):
+    """copy_ of a permuted view into a contiguous tensor of another dtype.  The
+    float32 / bfloat16 / float16 pairs take the LDS-tiled transposes, which
+    convert on the way out (element-size ratios 2 and 1/2 set the LDS swizzle);
+    the other pairs take the per-element run-time-dtype kernel.  Two shapes: one
+    whose tiled dims both end in partial tiles (208 = 3 x 64 + 16 rows, 1040
+    columns: the 16-byte tile kernel) and one with odd sizes (the per-element
+    tile kernel)."""
+    for shape in [(2, 208, 1040), (3, 99, 517)]:
+        x = _cast_source(src, dst, shape, 60)
+        view_cpu = x.permute(0, 2, 1)
+        out = torch.empty(view_cpu.shape, dtype=dst, device="supa")
+        out.copy_(dev(x).permute(0, 2, 1))
+        assert torch.equal(out.cpu(), view_cpu.to(dst).contiguous()), (shape, src, dst)
+
+
 def test_transposed_and_strided_views(no_fallback):
     base = seeded((1, 5120, 1024), 9)
     a = base.transpose(1, 2)  # [1, 1024, 5120] with strides (5242880, 1, 1024): the reference's worst case
