@@ -55,6 +55,8 @@ def lib():
                                      ctypes.c_int, ctypes.c_int, vp, vp, vp],
             "supa_amd_cross_entropy_forward": [vp, i32, vp, i64, i64, i64, ctypes.c_int, vp, vp, vp, vp, i64, vp, vp],
             "supa_amd_cross_entropy_backward": [vp, vp, i32, vp, vp, vp, i64, i64, i64, ctypes.c_int, vp, vp, vp],
+            "supa_amd_amp_unscale": [i32, vp, vp, i32, vp, vp, vp],
+            "supa_amd_amp_update_scale": [vp, vp, vp, dbl, dbl, i64, vp],
         }
         for name, args in sig.items():
             fn = getattr(L, name)

@@ -335,3 +335,72 @@ def test_bce_logits_backward_capi(reduction):
     red = "none" if reduction == A.RED_NONE else "mean"
     gref = O.loss_backward(O.BCE_LOGITS, go.numpy(), x.numpy(), t.numpy(), pw.numpy(), w.numpy(), reduction=red)
     assert np.array_equal(gi.cpu().numpy(), gref)
+
+
+def _bits(t):
+    return t.cpu().view({1: torch.uint8, 2: torch.int16, 4: torch.int32, 8: torch.int64}[t.element_size()])
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_amp_unscale_capi(dtype):
+    """_amp_foreach_non_finite_check_and_unscale_ through the C ABI against
+    upstream torch's own CPU kernel on the same tensors: every element times
+    inv_scale (1/3 rounds, 2^-16 is exact, exactly 1 leaves the tensors
+    untouched), and found_inf set by one inf or NaN anywhere in the list.
+    NaN elements compare as NaN: upstream's CPU kernel rewrites a bfloat16 NaN
+    as 0xFFFF even when inv_scale is 1 (its vectorised bfloat16 conversion),
+    where the device kernel leaves the element as it was."""
+    L = A.lib()
+    shapes = [(4096, 1030), (7,), (333, 17)]
+    for inv, poison in [(1.0 / 3.0, None), (2.0 ** -16, None), (0.5, float("inf")), (1.0, float("nan")),
+                        (0.25, float("-inf"))]:
+        host = [seeded(s, 100 + i, 50.0).to(dtype) for i, s in enumerate(shapes)]
+        if poison is not None:
+            host[2].view(-1)[100] = poison
+        devs = [h.to(DEV) for h in host]
+        found = torch.zeros(1, device=DEV)
+        inv_t = torch.tensor([inv], dtype=torch.float32)
+        dinv = inv_t.to(DEV)
+        run(L.supa_amd_amp_unscale(len(devs), A.ptr_array(devs), A.i64_array([t.numel() for t in devs]),
+                                   A.dtype_code(dtype), found.data_ptr(), dinv.data_ptr(), None))
+        ref_found = torch.zeros(1)
+        torch._amp_foreach_non_finite_check_and_unscale_(host, ref_found, inv_t)
+        assert found.item() == ref_found.item() == (0.0 if poison is None else 1.0), (inv, poison)
+        for d, h in zip(devs, host):
+            nan = torch.isnan(h)
+            assert torch.equal(torch.isnan(d.cpu()), nan), (inv, poison, d.shape)
+            assert torch.equal(_bits(d)[~nan], _bits(h)[~nan]), (inv, poison, d.shape)
+
+
+def test_amp_update_scale_capi():
+    """_amp_update_scale_ through the C ABI against upstream torch's CPU kernel
+    over a run of overflow / clean steps (growth every 3 clean steps, backoff
+    on overflow), then a growth that would overflow float32 (scale kept)."""
+    L = A.lib()
+    for start in [65536.0, 3.0e38]:
+        scale = torch.tensor([start], device=DEV)
+        tracker = torch.zeros(1, dtype=torch.int32, device=DEV)
+        rs, rt = torch.tensor([start]), torch.zeros(1, dtype=torch.int32)
+        for f in [0, 0, 0, 1, 0, 0, 0, 0, 1, 1, 0, 0, 0, 0]:
+            fi = torch.tensor([float(f)])
+            dfi = fi.to(DEV)
+            run(L.supa_amd_amp_update_scale(scale.data_ptr(), tracker.data_ptr(), dfi.data_ptr(), 2.0, 0.5, 3, None))
+            torch._amp_update_scale_(rs, rt, fi, 2.0, 0.5, 3)
+            assert scale.item() == rs.item() and tracker.item() == rt.item(), (start, f)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16, torch.int64, torch.uint8,
+                                   torch.bool])
+def test_fill_capi(dtype):
+    """fill_ through the C ABI (the value as an immediate scalar operand)
+    against torch.full on the CPU, at sizes with and without a vector tail."""
+    L = A.lib()
+    values = [0, 1, 7] if dtype in (torch.uint8, torch.bool) else [0, 1, 3.25, -7, 0.1]
+    if dtype == torch.int64:
+        values = [0, 1, -7, 2 ** 40 + 3]
+    for n in [1, 1000, 4096 * 1024 + 5]:
+        out = torch.empty(n, dtype=dtype, device=DEV)
+        for v in values:
+            d = A.flat_desc(out, v)
+            run(L.supa_amd_fill(ctypes.byref(d), None))
+            assert torch.equal(out.cpu(), torch.full((n,), v, dtype=dtype)), (n, v)
