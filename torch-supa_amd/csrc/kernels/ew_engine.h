@@ -477,8 +477,9 @@ k_transpose(Op op, const S* __restrict__ in, OT* __restrict__ out, TransposeGeom
 // adjacent 512-byte runs of the same input rows.  Tile rows load as 16-byte
 // vectors into LDS in the storage type, and each thread assembles 16-byte
 // output vectors along dim 0 from LDS columns.  On c2's bf16 .contiguous()
-// this shape measured 77 % of the HBM roofline against 69-71 % for 64 x 64
-// tiles; taller tiles (shorter output runs) and wider ones were slower.
+// this shape runs at 78-79 % of the HBM roofline (a flat copy of the same
+// bytes: 83-84 %); with 512 threads 76 %, with 32 / 128 / 256 tile rows
+// (64 / 256 / 512-byte output runs) 60 / 75 / 72 %, with 64 x 64 tiles 69-71 %.
 // Needs d0 % VO == 0, dk % VI == 0, every stride a multiple of the vector
 // and 16-byte aligned bases (checked on the host).
 constexpr int kTileVecBlock = 1024;
