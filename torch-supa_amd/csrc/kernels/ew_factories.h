@@ -1,6 +1,8 @@
 // Op factories shared by the elementwise translation units.
 #pragma once
 
+#include <cmath>
+
 #include "ew_launch.h"
 #include "ops.h"
 
@@ -118,7 +120,10 @@ struct BceBwdFactory {
   double n;
   int mean, rt;
   template <typename C> static constexpr bool ok() { return std::is_floating_point<C>::value; }
-  template <typename C> BceBwdOp<PW, W, C> make() const { return BceBwdOp<PW, W, C>{static_cast<C>(n), mean, rt}; }
+  template <typename C> BceBwdOp<PW, W, C> make() const {
+    const bool pow2 = n >= 1.0 && std::ldexp(1.0, std::ilogb(n)) == n;
+    return BceBwdOp<PW, W, C>{static_cast<C>(n), mean, rt, pow2 ? static_cast<C>(1.0 / n) : C(0)};
+  }
 };
 
 }  // namespace sa

@@ -555,6 +555,9 @@ template <bool PW, bool W, typename C> struct BceBwdOp {
   C n;
   int mean;
   int rt;
+  // 1 / n when n is a power of two, else 0: r * inv_n and r / n are then the
+  // same correctly rounded value (the exact quotient), without the division
+  C inv_n;
   __device__ __forceinline__ C rnd(C v) const {
     if constexpr (std::is_same<C, float>::value) {
       if (rt == 1) return bf16_to_f32(f32_to_bf16(v));
@@ -574,7 +577,7 @@ template <bool PW, bool W, typename C> struct BceBwdOp {
     }
     r = rnd(r * g);
     if constexpr (W) r = rnd(r * v[3 + (PW ? 1 : 0)]);
-    if (mean) r = r / n;
+    if (mean) r = inv_n != C(0) ? r * inv_n : r / n;
     return r;
   }
 };
