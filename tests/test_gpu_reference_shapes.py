@@ -10,7 +10,13 @@
 * /root/reference/test/test_binary_mul_kernel.py:96-139 -- the contiguous
   mixed-dtype (131072, 128) product both ways round, and the 11 bf16 x
   float32 broadcast shapes of its perf table, bit-exact (IEEE products of
-  exactly widened values).
+  exactly widened values);
+* /root/reference/test/test_copy_permute_3d_fastpath.py:49-139 -- copy_ and
+  .contiguous() of a permute(0, 2, 1) stride layout built with as_strided on
+  (4, 8, 16) and (3, 5, 7) in bfloat16 / float16, the float32 permute, a
+  non-permute stride (100, 10, 1) and the contiguous identity, all bit-exact
+  (rtol = atol = 0 there too); plus two shapes large enough for this build's
+  tiled transposes.
 
 Inputs are seeded N(0, 1) like the reference's create_random_tensor; targets
 uniform over the classes (the reference's random_(C)).  Tolerances: the
@@ -152,3 +158,46 @@ def test_mul_bf16_float_broadcast_reference_shapes(shape, shape1, no_fallback):
     want = a * b
     assert torch.equal(c.cpu(), want)
     assert np.array_equal(c.cpu().numpy(), O.binary(O.MUL, a.float().numpy(), b.numpy()))
+
+
+def _contiguous_strides(shape):
+    strides, acc = [0] * len(shape), 1
+    for i in range(len(shape) - 1, -1, -1):
+        strides[i] = acc
+        acc *= shape[i]
+    return strides
+
+
+def _strided_pair(shape, stride, dtype, seed):
+    """A (cpu, supa) pair of as_strided views of the same seeded storage."""
+    base = _seeded((int(np.prod(shape)) + 1024,), seed, dtype)
+    return torch.as_strided(base, shape, stride), torch.as_strided(base.to("supa"), shape, stride)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("shape", [(4, 8, 16), (3, 5, 7), (4, 64, 256), (2, 208, 1040)])
+def test_copy_permute_021(shape, dtype, no_fallback):
+    """test_copy_permute_3d_fastpath.py:49-83: the permute(0, 2, 1) layout
+    (strides (b c, 1, b)) copied into a contiguous layout, and .contiguous()."""
+    a, b, c = shape
+    src_cpu, src_dev = _strided_pair(shape, (b * c, 1, b), dtype, 80)
+    dst_cpu, dst_dev = _strided_pair(shape, _contiguous_strides(shape), dtype, 81)
+    torch.ops.aten.copy_(dst_cpu, src_cpu)
+    torch.ops.aten.copy_(dst_dev, src_dev)
+    assert torch.equal(dst_dev.cpu(), dst_cpu)
+    assert torch.equal(src_dev.contiguous().cpu(), src_cpu.contiguous())
+
+
+@pytest.mark.parametrize("case", ["float32_permute", "non_permute_stride", "identity"])
+def test_copy_permute_021_bypass_cases(case, no_fallback):
+    """test_copy_permute_3d_fastpath.py:85-139: layouts the reference's
+    bf16 / f16 permute fast path must not take, still copied exactly."""
+    shape = (4, 8, 16)
+    dtype = torch.float32 if case == "float32_permute" else torch.bfloat16
+    src_stride = {"float32_permute": (8 * 16, 1, 8), "non_permute_stride": (100, 10, 1),
+                  "identity": tuple(_contiguous_strides(shape))}[case]
+    src_cpu, src_dev = _strided_pair(shape, src_stride, dtype, 82)
+    dst_cpu, dst_dev = _strided_pair(shape, _contiguous_strides(shape), dtype, 83)
+    torch.ops.aten.copy_(dst_cpu, src_cpu)
+    torch.ops.aten.copy_(dst_dev, src_dev)
+    assert torch.equal(dst_dev.cpu(), dst_cpu)
