@@ -770,5 +770,26 @@ void record_stream_supa(at::Tensor& self, c10::Stream s) {
 }
 }  // namespace
 
-TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) { m.impl("record_stream", TORCH_FN(record_stream_supa)); }
+namespace {
+// tensor.data = other across the host and the device: upstream counts only
+// its own dense backends as shallow-copy compatible; a supa tensor and a CPU
+// tensor are both dense storages here too (the reference's
+// aten/ops/HasCompatibleShallowCopyType.cpp:12-23).  Registered for the supa
+// keys, so dispatch reaches it whenever either tensor is on the device.
+bool has_compatible_shallow_copy_type_supa(const at::Tensor& self, const at::Tensor& from) {
+  const c10::DispatchKeySet a = self.key_set(), b = from.key_set();
+  auto dense = [](c10::DispatchKeySet ks) {
+    return ks.has(c10::DispatchKey::CPU) || ks.has(c10::DispatchKey::PrivateUse1);
+  };
+  return a == b || (dense(a) && dense(b));
+}
+}  // namespace
+
+TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
+  m.impl("record_stream", TORCH_FN(record_stream_supa));
+  m.impl("_has_compatible_shallow_copy_type", TORCH_FN(has_compatible_shallow_copy_type_supa));
+}
+TORCH_LIBRARY_IMPL(aten, AutogradPrivateUse1, m) {
+  m.impl("_has_compatible_shallow_copy_type", TORCH_FN(has_compatible_shallow_copy_type_supa));
+}
 
