@@ -12,7 +12,10 @@ supa result):
 * test_reduce_sum_prod_kernel.py's shapes and keepdim cases for sum, and
   test_reduce_ops.py's mean cases;
 * test_foreach_binary_op_list.py (with its clip_grad_norm_ case),
-  test_foreach_binary_op_scalar.py, test_foreach_pointwise_op.py,
+  test_foreach_binary_op_scalar.py, test_foreach_binary_op_scalar_list.py,
+  test_foreach_binary_op_scalar_tensor.py, test_foreach_ternary_op.py
+  (lerp), test_foreach_unary_op.py (the ops outside this build's native set
+  through the counted CPU fallback), test_foreach_pointwise_op.py,
   test_foreach_reduce_op.py (with its accumulation-count tolerance);
 * test_fused_adam_w_kernel.py (5 steps of AdamW(fused=True) on a
   cross-entropy loss against the CPU's unfused AdamW);
@@ -394,3 +397,113 @@ def test_amp_update_scale_known_answers(no_fallback):
     found_inf.fill_(1.0)
     torch._amp_update_scale_(scale, tracker, found_inf, 2.0, 0.25, 2)
     assert tracker.item() == 0 and scale.item() == 2.0
+
+
+# ------------------------------------------------------------ foreach, continued
+def _scalar(v, dtype, device):
+    return torch.tensor(v, dtype=dtype).to(device)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("func", FE_BINARY_LIST[:6])
+@pytest.mark.parametrize("shape", FOREACH_SHAPES)
+def test_foreach_binary_scalar_list(shape, func, dtype, no_fallback):
+    """test_foreach_binary_op_scalar_list.py:47-72: f(list, [2, 3]) with the
+    scalars as 0-dim tensors of the dtype (on each call's device)."""
+    c = [rand(shape, dtype), rand(shape, dtype)]
+    s = [t.to(SUPA) for t in c]
+    fn = getattr(torch, func)
+    rc = fn(c, [_scalar(2.0, dtype, "cpu"), _scalar(3.0, dtype, "cpu")])
+    rs = fn(s, [_scalar(2.0, dtype, SUPA), _scalar(3.0, dtype, SUPA)])
+    for a, b in zip(rc, rs):
+        ref_allclose(a, b, RTOL[dtype], ATOL[dtype], equal_nan=True)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("shape", FOREACH_SHAPES)
+def test_foreach_pow_scalar_list(shape, dtype, no_fallback):
+    """test_foreach_binary_op_scalar_list.py:74-96: _foreach_pow(list, [2, 3])."""
+    c = [rand(shape, dtype), rand(shape, dtype)]
+    s = [t.to(SUPA) for t in c]
+    rc = torch._foreach_pow(c, [_scalar(2.0, dtype, "cpu"), _scalar(3.0, dtype, "cpu")])
+    rs = torch._foreach_pow(s, [_scalar(2.0, dtype, SUPA), _scalar(3.0, dtype, SUPA)])
+    for a, b in zip(rc, rs):
+        ref_allclose(a, b, RTOL[dtype], ATOL[dtype], equal_nan=True)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("func", FE_BINARY_LIST[:6])
+@pytest.mark.parametrize("shape", FOREACH_SHAPES)
+def test_foreach_binary_scalar_tensor(shape, func, dtype, no_fallback):
+    """test_foreach_binary_op_scalar_tensor.py:48-68: f(list, 0-dim tensor 2)."""
+    c = [rand(shape, dtype), rand(shape, dtype)]
+    s = [t.to(SUPA) for t in c]
+    fn = getattr(torch, func)
+    for a, b in zip(fn(c, _scalar(2.0, dtype, "cpu")), fn(s, _scalar(2.0, dtype, SUPA))):
+        ref_allclose(a, b, RTOL[dtype], ATOL[dtype], equal_nan=True)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("shape", FOREACH_SHAPES)
+def test_foreach_pow_scalar_tensor_base(shape, dtype, no_fallback):
+    """test_foreach_binary_op_scalar_tensor.py:70-90: _foreach_pow(0-dim 2, list)."""
+    c = [rand(shape, dtype), rand(shape, dtype)]
+    s = [t.to(SUPA) for t in c]
+    rc = torch._foreach_pow(_scalar(2.0, dtype, "cpu"), c)
+    rs = torch._foreach_pow(_scalar(2.0, dtype, SUPA), s)
+    for a, b in zip(rc, rs):
+        ref_allclose(a, b, RTOL[dtype], ATOL[dtype], equal_nan=True)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("shape", FOREACH_SHAPES)
+def test_foreach_lerp_lists(shape, dtype, no_fallback):
+    """test_foreach_ternary_op.py:39-60: _foreach_lerp(list, list, weights)."""
+    t1, t2, t3 = rand(shape, dtype), rand(shape, dtype), rand(shape, dtype)
+    c1, c2, c3 = [t1, t1], [t2, t2], [t3, t3]
+    s1, s2, s3 = ([t.to(SUPA) for t in lst] for lst in (c1, c2, c3))
+    for a, b in zip(torch._foreach_lerp(c1, c2, c3), torch._foreach_lerp(s1, s2, s3)):
+        ref_allclose(a, b, RTOL[dtype], ATOL[dtype], equal_nan=True)
+
+
+FE_UNARY_NATIVE = ["_foreach_abs", "_foreach_ceil", "_foreach_erf", "_foreach_exp", "_foreach_expm1",
+                   "_foreach_floor", "_foreach_log1p", "_foreach_log", "_foreach_neg", "_foreach_reciprocal",
+                   "_foreach_round", "_foreach_sigmoid", "_foreach_sign", "_foreach_sqrt", "_foreach_tanh",
+                   "_foreach_trunc", "_foreach_zero_"]
+FE_UNARY_FALLBACK = ["_foreach_acos", "_foreach_asin", "_foreach_atan", "_foreach_cos", "_foreach_cosh",
+                     "_foreach_erfc", "_foreach_frac", "_foreach_log10", "_foreach_log2", "_foreach_sin",
+                     "_foreach_sinh", "_foreach_tan"]
+
+
+def _foreach_unary(shape, func, dtype):
+    c = [rand(shape, dtype), rand(shape, dtype)]
+    s = [t.to(SUPA) for t in c]
+    fn = getattr(torch, func)
+    rc, rs = fn(c), fn(s)
+    if func == "_foreach_zero_":  # in place, returns None
+        rc, rs = c, s
+    for a, b in zip(rc, rs):
+        ref_allclose(a, b, RTOL[dtype], ATOL[dtype], equal_nan=True)
+
+
+# the reference compares float32 and float16 only (its bf16 and lgamma cases
+# run the op without a comparison, test_foreach_unary_op.py:74-95)
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+@pytest.mark.parametrize("func", FE_UNARY_NATIVE)
+@pytest.mark.parametrize("shape", FOREACH_SHAPES)
+def test_foreach_unary_native(shape, func, dtype, no_fallback):
+    """test_foreach_unary_op.py, the ops this build runs on the device."""
+    _foreach_unary(shape, func, dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+@pytest.mark.parametrize("func", FE_UNARY_FALLBACK)
+def test_foreach_unary_outside_the_path(func, dtype, supa):
+    """test_foreach_unary_op.py, the ops outside this build's native set: they
+    run through the counted CPU fallback (the reference's own fallback,
+    VariableFallbackKernel.cpp:44-64, does the same for its missing ops) and
+    still match."""
+    torch.supa.set_cpu_fallback_enabled(True)
+    before = dict(torch.supa.fallback_counts())
+    _foreach_unary((1023, 511), func, dtype)
+    assert sum(dict(torch.supa.fallback_counts()).values()) > sum(before.values())
