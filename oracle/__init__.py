@@ -151,6 +151,16 @@ def binary(op: int, a, b, alpha: float = 1.0, dtype=np.float32) -> np.ndarray:
     return out
 
 
+def div_trunc_16(a, b, dtype: str) -> np.ndarray:
+    """Trunc division of bfloat16 / float16 operands (given as float32
+    values): std::trunc(a / b) on the storage type (BinaryDivTruncKernel.cu:
+    46-52), the float32 quotient rounded to the 16-bit type, then truncated.
+    dtype: "bf16" or "f16"; float32 result."""
+    q = binary(DIV, a, b)
+    q = round_bf16(q) if dtype == "bf16" else np.asarray(q, np.float32).astype(np.float16).astype(np.float32)
+    return np.trunc(q)
+
+
 def binary_int(op: int, a, b, alpha: int = 1, dtype=np.int64) -> np.ndarray:
     """Wrapping integer arithmetic (UfuncCUDA_add.cu:13-16 add, BinaryInternal.h
     mul, BinaryDivTruncKernel.cu / BinaryDivFloorKernel.cu integer paths)."""

@@ -220,6 +220,21 @@ def test_transposed_and_strided_views(no_fallback):
     assert torch.equal(torch.sigmoid(s).cpu(), torch.from_numpy(O.unary(O.SIGMOID, s.cpu().numpy())))
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_div_trunc_16bit_bit_exact(dtype, no_fallback):
+    """bf16 / f16 trunc division truncates the quotient rounded to the 16-bit
+    type, as the reference's kernel does (the oracle's rule, pinned against
+    upstream CPU's vectorised path): bit-exact, contiguous and broadcast."""
+    name = "bf16" if dtype == torch.bfloat16 else "f16"
+    a, b = seeded((1023, 517), 70).to(dtype), seeded((1023, 517), 71).to(dtype)
+    got = torch.div(dev(a), dev(b), rounding_mode="trunc").cpu().float().numpy()
+    assert np.array_equal(got, O.div_trunc_16(a.float().numpy(), b.float().numpy(), name))
+    row = seeded((517,), 72).to(dtype)
+    got = torch.div(dev(a), dev(row), rounding_mode="trunc").cpu().float().numpy()
+    ref = O.div_trunc_16(a.float().numpy(), np.broadcast_to(row.float().numpy(), a.shape), name)
+    assert np.array_equal(got, ref)
+
+
 def test_integer_bool_and_mixed_dtypes(no_fallback):
     g = torch.Generator().manual_seed(12)
     ia = torch.randint(-1000, 1000, (999,), generator=g)

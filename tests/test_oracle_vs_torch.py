@@ -61,6 +61,23 @@ def test_bf16_binary_matches_cpu():
         assert np.array_equal(got, ref.view(torch.int16).numpy().view(np.uint16)), op
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_div_trunc_16bit_rounds_the_quotient(dtype):
+    """trunc division of 16-bit operands truncates the quotient rounded to the
+    16-bit type (the reference's std::trunc(a / b) on scalar_t).  Upstream
+    CPU's vectorised path computes the same thing (Vectorized<T> division,
+    then trunc); 4096 elements are whole vectors, so no element takes its
+    scalar tail, which truncates the float quotient instead.  The rule is not
+    vacuous: on N(0, 1) pairs it differs from truncating the float quotient."""
+    a, b = randn((4096,), 8, dtype=dtype), randn((4096,), 9, dtype=dtype)
+    af, bf = a.float().numpy(), b.float().numpy()
+    name = "bf16" if dtype == torch.bfloat16 else "f16"
+    got = O.div_trunc_16(af, bf, name)
+    cpu = torch.div(a, b, rounding_mode="trunc").float().numpy()
+    assert np.array_equal(got, cpu)
+    assert (got != np.trunc(af / bf)).sum() > 0
+
+
 def test_mixed_bf16_f32_promotion():
     """c2's add: bf16 x + f32 bias -> f32 (the bf16 value widens exactly)."""
     x = randn((8, 64, 128), 6, dtype=torch.bfloat16)

@@ -14,7 +14,10 @@ int supa_amd_mul(const supa_amd_ew_desc* d, void* stream) { return run_ew(Simple
 int supa_amd_div(const supa_amd_ew_desc* d, int mode, void* stream) {
   switch (mode) {
     case SUPA_AMD_DIV_TRUE: return run_ew(SimpleFactory<DivTrueOp, true>{}, d, stream, 3);
-    case SUPA_AMD_DIV_TRUNC: return run_ew(SimpleFactory<DivTruncOp>{}, d, stream, 3);
+    case SUPA_AMD_DIV_TRUNC: {
+      const int rt = d->common_dtype == SUPA_AMD_BF16 ? 1 : (d->common_dtype == SUPA_AMD_F16 ? 2 : 0);
+      return run_ew(DivTruncFactory{rt}, d, stream, 3);
+    }
     case SUPA_AMD_DIV_FLOOR: return run_ew(SimpleFactory<DivFloorOp>{}, d, stream, 3);
     default: return SUPA_AMD_EINVAL;
   }

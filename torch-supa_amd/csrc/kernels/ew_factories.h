@@ -14,6 +14,17 @@ struct SimpleFactory {
   template <typename C> Op<C> make() const { return Op<C>{}; }
 };
 
+// trunc division with the 16-bit storage type it rounds its quotient to
+struct DivTruncFactory {
+  int rt;
+  template <typename C> static constexpr bool ok() { return true; }
+  template <typename C> DivTruncOp<C> make() const {
+    DivTruncOp<C> o{};
+    o.rt = rt;
+    return o;
+  }
+};
+
 struct AddFactory {
   double alpha;
   int64_t ialpha;

@@ -48,14 +48,27 @@ template <typename C> struct DivTrueOp {
   static constexpr int arity = 2;
   __device__ __forceinline__ C operator()(const C* x) const { return x[0] / x[1]; }
 };
-// trunc division (BinaryDivTruncKernel.cu:22-55).  Integer division by zero
-// has no defined value on the device; it yields 0 here.
+// trunc division (BinaryDivTruncKernel.cu:22-55): std::trunc(a / b) on the
+// storage type, so for bf16 / f16 the quotient is rounded to that type before
+// it is truncated (rt 1: bf16, 2: f16; c10's 16-bit division computes in
+// float and rounds).  Integer division by zero has no defined value on the
+// device; it yields 0 here.
 template <typename C> struct DivTruncOp {
   static constexpr int arity = 2;
+  int rt = 0;
   __device__ __forceinline__ C operator()(const C* x) const {
-    if constexpr (std::is_floating_point<C>::value) return trunc(x[0] / x[1]);
-    else if constexpr (std::is_same<C, bool>::value) return x[0];
-    else return x[1] == 0 ? C(0) : x[0] / x[1];
+    if constexpr (std::is_floating_point<C>::value) {
+      C q = x[0] / x[1];
+      if constexpr (std::is_same<C, float>::value) {
+        if (rt == 1) q = bf16_to_f32(f32_to_bf16(q));
+        if (rt == 2) q = (float)f32_to_f16(q);
+      }
+      return trunc(q);
+    } else if constexpr (std::is_same<C, bool>::value) {
+      return x[0];
+    } else {
+      return x[1] == 0 ? C(0) : x[0] / x[1];
+    }
   }
 };
 // floor division with Python semantics: c10::div_floor_floating /
