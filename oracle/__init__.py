@@ -381,6 +381,74 @@ def loss_backward(op: int, grad, x, t, pos_weight=None, weight=None, reduction="
     return out
 
 
+def round16(v, dtype: str) -> np.ndarray:
+    """float32 values rounded to bfloat16 ("bf16") or float16 ("f16") and back."""
+    v = np.asarray(v, np.float32)
+    return round_bf16(v) if dtype == "bf16" else v.astype(np.float16).astype(np.float32)
+
+
+def loss_16(name: str, x, t, dtype: str, reduction="mean", beta=1.0):
+    """mse / smooth_l1 / huber forward on bfloat16 or float16 operands
+    (given as float32 values), as upstream's device kernels compute them in
+    scalar_t (mse_kernel_cuda, smooth_l1_kernel_cuda, huber_kernel_cuda): an
+    operation between two c10::BFloat16 / c10::Half values is done in float32
+    and rounded back to the type, one between such a value and a float stays
+    in float32.  So d = x - t is rounded; mse squares d and rounds; smooth_l1
+    and huber take z = |d| in float32 with beta / delta and 0.5 * beta in the
+    16-bit type, and round the result.  A reduction adds the rounded terms
+    (in float64 here, float32 on the device) and rounds the sum or mean.
+    name: "mse", "smooth_l1" or "huber"; float32 result."""
+    x = np.asarray(x, np.float32)
+    t = np.broadcast_to(np.asarray(t, np.float32), x.shape)
+    d = round16(x - t, dtype)
+    if name == "mse":
+        term = round16(d * d, dtype)
+    else:
+        b = round16(np.float32(beta), dtype)
+        half_b = round16(np.float32(0.5) * b, dtype)
+        z = np.abs(d)
+        with np.errstate(divide="ignore", invalid="ignore"):
+            quad = (np.float32(0.5) * z) * z
+            if name == "smooth_l1":
+                term = np.where(z < b, quad / b, z - half_b)
+            else:
+                term = np.where(z < b, quad, b * (z - half_b))
+        term = round16(term.astype(np.float32), dtype)
+    if reduction == "none":
+        return term
+    s = term.astype(np.float64).sum()
+    if reduction == "mean":
+        s = s / term.size
+    return round16(np.float32(s), dtype).reshape(())
+
+
+def loss_backward_16(name: str, grad, x, t, dtype: str, reduction="mean", beta=1.0) -> np.ndarray:
+    """The gradients of :func:`loss_16` w.r.t. x (mse_backward_cuda_kernel,
+    smooth_l1_backward_cuda_kernel, huber_backward_cuda_kernel): every
+    operand is a 16-bit value (norm = 2/n or 2 for mse, 1/n or 1 otherwise,
+    rounded to the type) and every operation is rounded:
+      mse:       (norm d) g
+      smooth_l1: -norm g below -beta, norm g above beta, ((norm d) g) / beta
+      huber:     (-norm g) delta, (norm g) delta, (norm d) g
+    grad is n values for 'none', one otherwise; float32 result."""
+    x = np.asarray(x, np.float32)
+    t = np.broadcast_to(np.asarray(t, np.float32), x.shape)
+    g = np.asarray(grad, np.float32)
+    g = np.broadcast_to(g.reshape(x.shape) if reduction == "none" else g.reshape(()), x.shape)
+    norm = (2.0 if name == "mse" else 1.0) / (x.size if reduction == "mean" else 1)
+    n = round16(np.float32(norm), dtype)
+    d = round16(x - t, dtype)
+    r = lambda v: round16(v, dtype)  # noqa: E731
+    if name == "mse":
+        return r(r(d * n) * g)
+    b = r(np.float32(beta))
+    if name == "smooth_l1":
+        with np.errstate(divide="ignore", invalid="ignore"):
+            mid = r(r(r(n * d) * g) / b)
+        return np.where(d < -b, r(-n * g), np.where(d > b, r(n * g), mid)).astype(np.float32)
+    return np.where(d < -b, r(r(-n * g) * b), np.where(d > b, r(r(n * g) * b), r(r(n * d) * g))).astype(np.float32)
+
+
 def sum_f32(x) -> float:
     x = _c(x, np.float32)
     return float(lib().or_sum_f32(_p(x, _f32p), x.size))

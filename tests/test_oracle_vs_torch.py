@@ -78,6 +78,74 @@ def test_div_trunc_16bit_rounds_the_quotient(dtype):
     assert (got != np.trunc(af / bf)).sum() > 0
 
 
+_LOSS16 = {"mse": lambda a, b, red, beta: F.mse_loss(a, b, reduction=red),
+           "smooth_l1": lambda a, b, red, beta: F.smooth_l1_loss(a, b, reduction=red, beta=beta),
+           "huber": lambda a, b, red, beta: F.huber_loss(a, b, reduction=red, delta=beta)}
+
+
+def _loss16_inputs(dtype, n=1 << 16):
+    g = torch.Generator().manual_seed(41)
+    x = (torch.rand(n, generator=g) * 2 - 1).to(dtype)
+    t = (torch.rand(n, generator=g) * 2 - 1).to(dtype)
+    gr = torch.rand(n, generator=g).to(dtype)
+    return x, t, gr
+
+
+def _cpu_loss16_grad(name, x, t, gr, red, beta):
+    xx = x.clone().requires_grad_()
+    y = _LOSS16[name](xx, t, red, beta)
+    y.backward(gr if red == "none" else None)
+    return xx.grad.float().numpy()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_loss_16bit_rounding_rule(dtype):
+    """The 16-bit mse / smooth_l1 / huber rule (loss_16, loss_backward_16:
+    the difference rounded to the type, every operation between two 16-bit
+    values rounded) against the upstream CPU kernels that compute in
+    scalar_t, bit for bit:
+    * mse forward and backward (every reduction), in both types;
+    * huber backward (every reduction, delta 1 and 0.3), in both types;
+    * smooth_l1 forward at beta 1 in float16, huber forward at delta 1 in
+      bfloat16 (upstream CPU's other 16-bit forward kernels widen to float32
+      first and skip the rounding of the difference);
+    and smooth_l1's backward at beta 1 equals huber's at delta 1 (the same
+    operations).  The rule is not vacuous: without the rounding of the
+    difference the mse forward differs from CPU on most elements."""
+    name = "bf16" if dtype == torch.bfloat16 else "f16"
+    x, t, gr = _loss16_inputs(dtype)
+    xf, tf, gf = x.float().numpy(), t.float().numpy(), gr.float().numpy()
+    cpu = F.mse_loss(x, t, reduction="none").float().numpy()
+    assert np.array_equal(O.loss_16("mse", xf, tf, name, "none"), cpu)
+    assert np.mean(O.round16((xf - tf) * (xf - tf), name) != cpu) > 0.1
+    one = "smooth_l1" if dtype == torch.float16 else "huber"
+    assert np.array_equal(O.loss_16(one, xf, tf, name, "none", 1.0),
+                          _LOSS16[one](x, t, "none", 1.0).float().numpy())
+    for red in ("none", "mean", "sum"):
+        g = gf if red == "none" else 1.0
+        assert np.array_equal(O.loss_backward_16("mse", g, xf, tf, name, red),
+                              _cpu_loss16_grad("mse", x, t, gr, red, 1.0))
+        for delta in (1.0, 0.3):
+            assert np.array_equal(O.loss_backward_16("huber", g, xf, tf, name, red, delta),
+                                  _cpu_loss16_grad("huber", x, t, gr, red, delta))
+        assert np.array_equal(O.loss_backward_16("smooth_l1", g, xf, tf, name, red, 1.0),
+                              O.loss_backward_16("huber", g, xf, tf, name, red, 1.0))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("name", ["mse", "smooth_l1", "huber"])
+def test_loss_16bit_reductions(name, dtype):
+    """loss_16's sum / mean add the rounded terms and round once: within one
+    16-bit ulp of upstream CPU, which sums its 16-bit loss tensor in float32."""
+    tname = "bf16" if dtype == torch.bfloat16 else "f16"
+    x, t, _ = _loss16_inputs(dtype, 1 << 12)
+    rtol = 2.0 ** -7 if dtype == torch.bfloat16 else 2.0 ** -10
+    for red in ("mean", "sum"):
+        got = float(O.loss_16(name, x.float().numpy(), t.float().numpy(), tname, red, 1.0))
+        want = float(_LOSS16[name](x, t, red, 1.0))
+        assert abs(got - want) <= rtol * abs(want)
+
+
 def test_mixed_bf16_f32_promotion():
     """c2's add: bf16 x + f32 bias -> f32 (the bf16 value widens exactly)."""
     x = randn((8, 64, 128), 6, dtype=torch.bfloat16)

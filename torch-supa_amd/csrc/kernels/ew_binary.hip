@@ -15,7 +15,7 @@ int supa_amd_div(const supa_amd_ew_desc* d, int mode, void* stream) {
   switch (mode) {
     case SUPA_AMD_DIV_TRUE: return run_ew(SimpleFactory<DivTrueOp, true>{}, d, stream, 3);
     case SUPA_AMD_DIV_TRUNC: {
-      const int rt = d->common_dtype == SUPA_AMD_BF16 ? 1 : (d->common_dtype == SUPA_AMD_F16 ? 2 : 0);
+      const int rt = half_code(d);
       return run_ew(DivTruncFactory{rt}, d, stream, 3);
     }
     case SUPA_AMD_DIV_FLOOR: return run_ew(SimpleFactory<DivFloorOp>{}, d, stream, 3);

@@ -76,21 +76,26 @@ int run_unary(const supa_amd_ew_desc* d, void* stream) {
 
 struct MseBwdFactory {
   double norm;
+  int half;
   template <typename C> static constexpr bool ok() { return std::is_floating_point<C>::value; }
-  template <typename C> MseBwdOp<C> make() const { return MseBwdOp<C>{static_cast<C>(norm)}; }
+  template <typename C> MseBwdOp<C> make() const { return MseBwdOp<C>{loss_param<C>(norm, half), half}; }
 };
 struct SmoothL1BwdFactory {
   double norm, beta;
+  int half;
   template <typename C> static constexpr bool ok() { return std::is_floating_point<C>::value; }
   template <typename C> SmoothL1BwdOp<C> make() const {
-    return SmoothL1BwdOp<C>{static_cast<C>(norm), static_cast<C>(beta)};
+    return SmoothL1BwdOp<C>{loss_param<C>(norm, half), loss_param<C>(beta, half), half};
   }
 };
 
 struct HuberBwdFactory {
   double norm, delta;
+  int half;
   template <typename C> static constexpr bool ok() { return std::is_floating_point<C>::value; }
-  template <typename C> HuberBwdOp<C> make() const { return HuberBwdOp<C>{static_cast<C>(norm), static_cast<C>(delta)}; }
+  template <typename C> HuberBwdOp<C> make() const {
+    return HuberBwdOp<C>{loss_param<C>(norm, half), loss_param<C>(delta, half), half};
+  }
 };
 template <bool W>
 struct BceProbBwdFactory {

@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
+#include <cstdint>
 
 #include "ew_engine.h"
 #include "split32.h"
@@ -12,6 +14,45 @@
 namespace sa {
 
 __host__ __device__ inline bool aligned(const void* p, int bytes) { return (reinterpret_cast<uintptr_t>(p) % bytes) == 0; }
+
+// 1 / 2 when the common dtype is bf16 / f16, else 0: the ops that follow
+// upstream's scalar_t arithmetic round their intermediates to that type.
+inline int half_code(const supa_amd_ew_desc* d) {
+  return d->common_dtype == SUPA_AMD_BF16 ? 1 : (d->common_dtype == SUPA_AMD_F16 ? 2 : 0);
+}
+
+// Host-side rounding of a float to bf16 / f16 precision (round to nearest
+// even; NaN kept NaN), for parameters a kernel takes already rounded.
+inline float host_round_bf16(float f) {
+  uint32_t u;
+  __builtin_memcpy(&u, &f, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return f;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  u &= 0xffff0000u;
+  float r;
+  __builtin_memcpy(&r, &u, 4);
+  return r;
+}
+inline float host_round_f16(float f) {
+  const float a = std::fabs(f);
+  if (a != a) return f;
+  if (!(a < 65520.0f)) return std::copysign(HUGE_VALF, f);  // rounds past the largest finite f16
+  if (a < 6.103515625e-05f) return std::nearbyint(f * 16777216.0f) / 16777216.0f;  // subnormal: 2^-24 steps
+  uint32_t u;
+  __builtin_memcpy(&u, &f, 4);
+  u += 0xfffu + ((u >> 13) & 1u);
+  u &= ~0x1fffu;
+  float r;
+  __builtin_memcpy(&r, &u, 4);
+  return r;
+}
+// A kernel parameter in the compute type C: v rounded to the 16-bit storage
+// type for `half` 1 / 2 (upstream's scalar_t parameters), else C(v).
+template <typename C> inline C loss_param(double v, int half) {
+  if (half == 1) return static_cast<C>(host_round_bf16(static_cast<float>(v)));
+  if (half == 2) return static_cast<C>(host_round_f16(static_cast<float>(v)));
+  return static_cast<C>(v);
+}
 
 inline int64_t desc_numel(const supa_amd_ew_desc* d) {
   int64_t n = 1;

@@ -3,20 +3,6 @@
 
 using namespace sa;
 
-namespace {
-// float -> bf16 -> float on the host: round to nearest even, NaN kept NaN.
-float host_round_bf16(float f) {
-  uint32_t u;
-  __builtin_memcpy(&u, &f, 4);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return f;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  u &= 0xffff0000u;
-  float r;
-  __builtin_memcpy(&r, &u, 4);
-  return r;
-}
-}  // namespace
-
 extern "C" {
 
 int supa_amd_unary(const supa_amd_ew_desc* d, int op, void* stream) {
@@ -78,7 +64,7 @@ int supa_amd_pow_scalar(const supa_amd_ew_desc* d, double exponent, void* stream
                    : exponent == 3.0 ? POW_CUBE
                    : exponent == -2.0 ? POW_INV_SQUARE
                                       : POW_GENERAL;
-  const int half = d->common_dtype == SUPA_AMD_BF16 ? 1 : (d->common_dtype == SUPA_AMD_F16 ? 2 : 0);
+  const int half = half_code(d);
   return run_ew(PowScalarFactory{mode, half, exponent}, d, stream, 2);
 }
 

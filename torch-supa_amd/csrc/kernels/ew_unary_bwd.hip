@@ -20,13 +20,15 @@ int supa_amd_unary_backward(const supa_amd_ew_desc* d, int op, void* stream) {
 
 int supa_amd_loss_backward(const supa_amd_ew_desc* d, int loss, double norm, double beta, void* stream) {
   switch (loss) {
-    case SUPA_AMD_LOSS_MSE: return run_ew(MseBwdFactory{norm}, d, stream, 4);
-    case SUPA_AMD_LOSS_SMOOTH_L1: return run_ew(SmoothL1BwdFactory{norm, beta}, d, stream, 4);
-    case SUPA_AMD_LOSS_HUBER: return run_ew(HuberBwdFactory{norm, beta}, d, stream, 4);
+    case SUPA_AMD_LOSS_MSE: return d ? run_ew(MseBwdFactory{norm, half_code(d)}, d, stream, 4) : SUPA_AMD_EINVAL;
+    case SUPA_AMD_LOSS_SMOOTH_L1:
+      return d ? run_ew(SmoothL1BwdFactory{norm, beta, half_code(d)}, d, stream, 4) : SUPA_AMD_EINVAL;
+    case SUPA_AMD_LOSS_HUBER:
+      return d ? run_ew(HuberBwdFactory{norm, beta, half_code(d)}, d, stream, 4) : SUPA_AMD_EINVAL;
     case SUPA_AMD_LOSS_BCE:
       if (!d) return SUPA_AMD_EINVAL;
       {
-        const int half = d->common_dtype == SUPA_AMD_BF16 ? 1 : (d->common_dtype == SUPA_AMD_F16 ? 2 : 0);
+        const int half = half_code(d);
         return d->noperands == 5 ? run_ew(BceProbBwdFactory<true>{norm, half}, d, stream, 5)
                                  : run_ew(BceProbBwdFactory<false>{norm, half}, d, stream, 4);
       }
@@ -41,7 +43,7 @@ int supa_amd_bce_logits_backward(const supa_amd_ew_desc* d, int has_pos_weight, 
   if (d->noperands != want) return SUPA_AMD_EINVAL;
   for (int k = 0; k < d->noperands; ++k)
     if (!d->op[k].is_scalar && d->op[k].dtype != d->common_dtype) return SUPA_AMD_EDTYPE;
-  const int rt = d->common_dtype == SUPA_AMD_BF16 ? 1 : (d->common_dtype == SUPA_AMD_F16 ? 2 : 0);
+  const int rt = half_code(d);
   const int m = mean ? 1 : 0;
   if (has_pos_weight && has_weight) return run_ew(BceBwdFactory<true, true>{numel, m, rt}, d, stream, want);
   if (has_pos_weight) return run_ew(BceBwdFactory<true, false>{numel, m, rt}, d, stream, want);

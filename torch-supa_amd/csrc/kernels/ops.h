@@ -511,21 +511,49 @@ template <typename C> struct IdentityOp {
 };
 
 // ------------------------------------------------------ pointwise losses
-// mse term: d = x - t; d * d.
-template <typename C> struct MseTermOp {
+// round_half(v, half): for a 16-bit storage type (`half` 1 = bf16, 2 = f16)
+// v rounded to it; otherwise v.  Upstream's loss kernels compute in
+// scalar_t, and an operation between two c10::BFloat16 / c10::Half values
+// returns that type (one between such a value and a float returns float), so
+// these ops round exactly where that arithmetic does.
+template <typename C> __device__ __forceinline__ C round_half(C v, int half) {
+  if constexpr (std::is_same<C, float>::value) {
+    if (half == 1) return to_arith(from_arith<bf16>(v));
+    if (half == 2) return to_arith(from_arith<f16>(v));
+  }
+  return v;
+}
+// The 16-bit storage code of storage type T: 1 bf16, 2 f16, 0 otherwise.
+template <typename T> constexpr int half_of() {
+  return std::is_same<T, bf16>::value ? 1 : (std::is_same<T, f16>::value ? 2 : 0);
+}
+// round_half with the storage code fixed at compile time (H >= 0: the
+// branches fold away) or read from `half` at run time (H < 0).
+template <int H, typename C> __device__ __forceinline__ C round_half_t(C v, int half) {
+  if constexpr (H < 0) return round_half(v, half);
+  else return round_half(v, H);
+}
+// mse term (upstream mse_kernel_cuda): d = x - t; d * d.  The term itself is
+// rounded so that a fused sum adds what the reference's loss tensor holds.
+template <typename C, int H = -1> struct MseTermOp {
   static constexpr int arity = 2;
+  int half = 0;
   __device__ __forceinline__ C operator()(const C* v) const {
-    const C d = v[0] - v[1];
-    return d * d;
+    const C d = round_half_t<H>(v[0] - v[1], half);
+    return round_half_t<H>(d * d, half);
   }
 };
-// smooth_l1 term: z = |x - t|; z < beta ? 0.5 z z / beta : z - 0.5 beta.
-template <typename C> struct SmoothL1TermOp {
+// smooth_l1 term (upstream smooth_l1_kernel_cuda): z = |x - t| (the
+// difference in scalar_t, its magnitude in float); z < beta ? 0.5 z z / beta :
+// z - 0.5 beta.  beta and half_beta (0.5 beta) come in scalar_t, i.e. already
+// rounded to a 16-bit storage type by the host.
+template <typename C, int H = -1> struct SmoothL1TermOp {
   static constexpr int arity = 2;
-  C beta;
+  C beta, half_beta;
+  int half = 0;
   __device__ __forceinline__ C operator()(const C* v) const {
-    const C z = fabs(v[0] - v[1]);
-    return z < beta ? ((C(0.5) * z) * z) / beta : z - C(0.5) * beta;
+    const C z = fabs(round_half_t<H>(v[0] - v[1], half));
+    return round_half_t<H>(z < beta ? ((C(0.5) * z) * z) / beta : z - half_beta, half);
   }
 };
 // BCE-with-logits term (BinaryCrossEntropyWithLogitsKernel.cu:17-35):
@@ -594,46 +622,49 @@ template <bool PW, bool W, typename C> struct BceBwdOp {
     return r;
   }
 };
-// mse backward: ((x - t) * norm) * g   (inputs g, x, t)
+// mse backward (upstream mse_backward_cuda_kernel): norm (x - t) g, inputs
+// g, x, t; in scalar_t, so every product is rounded for a 16-bit type (norm
+// comes rounded to it).
 template <typename C> struct MseBwdOp {
   static constexpr int arity = 3;
   C norm;
-  __device__ __forceinline__ C operator()(const C* v) const { return ((v[1] - v[2]) * norm) * v[0]; }
-};
-// smooth_l1 backward (inputs g, x, t)
-// huber (upstream huber_kernel_cuda): z = |a - b|; 0.5 z z below delta,
-// delta (z - 0.5 delta) above.
-template <typename C> struct HuberTermOp {
-  static constexpr int arity = 2;
-  C delta;
+  int half = 0;
   __device__ __forceinline__ C operator()(const C* v) const {
-    const C z = fabs(v[0] - v[1]);
-    return z < delta ? (C(0.5) * z) * z : delta * (z - C(0.5) * delta);
+    return round_half(round_half(v[1] - v[2], half) * norm, half) * v[0];
   }
 };
-// huber backward (upstream huber_backward_cuda_kernel), v = {grad, input, target}.
+// huber (upstream huber_kernel_cuda): z = |a - b|; 0.5 z z below delta,
+// delta (z - 0.5 delta) above.
+// Rounded for a 16-bit type as the smooth_l1 term (delta and half_delta come
+// rounded).
+template <typename C, int H = -1> struct HuberTermOp {
+  static constexpr int arity = 2;
+  C delta, half_delta;
+  int half = 0;
+  __device__ __forceinline__ C operator()(const C* v) const {
+    const C z = fabs(round_half_t<H>(v[0] - v[1], half));
+    return round_half_t<H>(z < delta ? (C(0.5) * z) * z : delta * (z - half_delta), half);
+  }
+};
+// huber backward (upstream huber_backward_cuda_kernel), v = {grad, input,
+// target}; in scalar_t, every operation rounded for a 16-bit type (norm and
+// delta come rounded).
 template <typename C> struct HuberBwdOp {
   static constexpr int arity = 3;
   C norm, delta;
+  int half = 0;
   __device__ __forceinline__ C operator()(const C* v) const {
-    const C g = v[0], x = v[1] - v[2];
-    if (x < -delta) return ((-norm) * g) * delta;
-    if (x > delta) return (norm * g) * delta;
-    return (norm * x) * g;
+    const C g = v[0], x = round_half(v[1] - v[2], half);
+    if (x < -delta) return round_half((-norm) * g, half) * delta;
+    if (x > delta) return round_half(norm * g, half) * delta;
+    return round_half(norm * x, half) * g;
   }
 };
 // binary_cross_entropy on probabilities (upstream binary_cross_entropy_out
 // kernel): (t - 1) max(log1p(-x), -100) - t max(log(x), -100), times the
 // weight as a second op; v = {x, t[, w]}.  std::max keeps a NaN log.  For a
-// 16-bit storage type (`half` 1 = bf16, 2 = f16) every intermediate is
-// rounded to it, as the upstream kernel computes in scalar_t.
-template <typename C> __device__ __forceinline__ C round_half(C v, int half) {
-  if constexpr (std::is_same<C, float>::value) {
-    if (half == 1) return to_arith(from_arith<bf16>(v));
-    if (half == 2) return to_arith(from_arith<f16>(v));
-  }
-  return v;
-}
+// 16-bit storage type every intermediate is rounded to it, as the upstream
+// kernel computes in scalar_t.
 template <bool W, typename C> struct BceProbTermOp {
   static constexpr int arity = W ? 3 : 2;
   int half;
@@ -678,12 +709,18 @@ template <typename C> struct XlogyOp {
   }
 };
 
+// smooth_l1 backward (upstream smooth_l1_backward_cuda_kernel), v = {grad,
+// input, target}: -norm g below -beta, norm g above beta, norm x g / beta
+// between; in scalar_t, every operation rounded for a 16-bit type (norm and
+// beta come rounded).
 template <typename C> struct SmoothL1BwdOp {
   static constexpr int arity = 3;
   C norm, beta;
+  int half = 0;
   __device__ __forceinline__ C operator()(const C* v) const {
-    const C g = v[0], d = v[1] - v[2];
-    return d < -beta ? (-norm) * g : (d > beta ? norm * g : ((norm * d) * g) / beta);
+    const C g = v[0], d = round_half(v[1] - v[2], half);
+    return d < -beta ? (-norm) * g
+                     : (d > beta ? norm * g : round_half(round_half(norm * d, half) * g, half) / beta);
   }
 };
 

@@ -299,8 +299,14 @@ int run_reduce(const Factory& f, const supa_amd_ew_desc* d, double scale, void* 
   auto go = [&](auto* ctag, auto* ttag) -> int {
     using C = std::remove_pointer_t<decltype(ctag)>;
     using T = std::remove_pointer_t<decltype(ttag)>;
-    using Op = decltype(f.template make<C>());
-    const Op op = f.template make<C>();
+    // a storage-aware factory builds its op for the storage type as well,
+    // so that 16-bit rounding is fixed at compile time
+    auto make_op = [&]() {
+      if constexpr (Factory::kStorageAware) return f.template make<C, T>();
+      else return f.template make<C>();
+    };
+    using Op = decltype(make_op());
+    const Op op = make_op();
     constexpr int A = Op::arity;
     if (nt != A) return SUPA_AMD_EINVAL;
     return reduce_same<A, Op, C, T>(op, *d, tin, scale, ws, wsb, st);
@@ -326,52 +332,75 @@ int run_reduce(const Factory& f, const supa_amd_ew_desc* d, double scale, void* 
   return SUPA_AMD_EDTYPE;
 }
 
+// Reduction factories.  kStorageAware ones have make<C, T>() (T the storage
+// type) beside the elementwise engine's make<C>() (T = void: the 16-bit
+// rounding of the term is then chosen at run time from `half`).
+template <typename T> constexpr int storage_half() {
+  if constexpr (std::is_void<T>::value) return -1;
+  else return half_of<T>();
+}
 struct IdentityFactory {
   static constexpr bool kIntegers = true;  // sum has integer / bool forms
+  static constexpr bool kStorageAware = false;
   template <typename C> IdentityOp<C> make() const { return IdentityOp<C>{}; }
 };
 struct MseTermFactory {
   static constexpr bool kIntegers = false;
-  template <typename C> MseTermOp<C> make() const { return MseTermOp<C>{}; }
+  static constexpr bool kStorageAware = true;
+  int half;
+  template <typename C, typename T = void> auto make() const { return MseTermOp<C, storage_half<T>()>{half}; }
 };
 struct SmoothL1TermFactory {
   static constexpr bool kIntegers = false;
+  static constexpr bool kStorageAware = true;
   double beta;
-  template <typename C> SmoothL1TermOp<C> make() const { return SmoothL1TermOp<C>{static_cast<C>(beta)}; }
+  int half;
+  template <typename C, typename T = void> auto make() const {
+    const C b = loss_param<C>(beta, half);
+    return SmoothL1TermOp<C, storage_half<T>()>{b, loss_param<C>(0.5 * static_cast<double>(b), half), half};
+  }
 };
 template <bool PW, bool W, bool HW = false>
 struct BceTermFactory {
   static constexpr bool kIntegers = false;
+  static constexpr bool kStorageAware = false;
   template <typename C> BceTermOp<PW, W, C, HW> make() const { return BceTermOp<PW, W, C, HW>{}; }
   template <typename C> static constexpr bool ok() { return std::is_floating_point<C>::value; }
 };
-// 1 / 2 when the common dtype is bf16 / f16 (terms rounded in that type)
-inline int half_code(const supa_amd_ew_desc* d) {
-  return d->common_dtype == SUPA_AMD_BF16 ? 1 : (d->common_dtype == SUPA_AMD_F16 ? 2 : 0);
-}
 struct HuberTermFactory {
   static constexpr bool kIntegers = false;
+  static constexpr bool kStorageAware = true;
   double delta;
+  int half;
   template <typename C> static constexpr bool ok() { return std::is_floating_point<C>::value; }
-  template <typename C> HuberTermOp<C> make() const { return HuberTermOp<C>{static_cast<C>(delta)}; }
+  template <typename C, typename T = void> auto make() const {
+    const C dl = loss_param<C>(delta, half);
+    return HuberTermOp<C, storage_half<T>()>{dl, loss_param<C>(0.5 * static_cast<double>(dl), half), half};
+  }
 };
 template <bool W>
 struct BceProbTermFactory {
   static constexpr bool kIntegers = false;
+  static constexpr bool kStorageAware = false;
   int half;
   template <typename C> static constexpr bool ok() { return std::is_floating_point<C>::value; }
   template <typename C> BceProbTermOp<W, C> make() const { return BceProbTermOp<W, C>{half}; }
 };
 struct MseTermEwFactory {
   static constexpr bool kIntegers = false;
+  int half;
   template <typename C> static constexpr bool ok() { return std::is_floating_point<C>::value; }
-  template <typename C> MseTermOp<C> make() const { return MseTermOp<C>{}; }
+  template <typename C> MseTermOp<C> make() const { return MseTermOp<C>{half}; }
 };
 struct SmoothL1TermEwFactory {
   static constexpr bool kIntegers = false;
   double beta;
+  int half;
   template <typename C> static constexpr bool ok() { return std::is_floating_point<C>::value; }
-  template <typename C> SmoothL1TermOp<C> make() const { return SmoothL1TermOp<C>{static_cast<C>(beta)}; }
+  template <typename C> SmoothL1TermOp<C> make() const {
+    const C b = loss_param<C>(beta, half);
+    return SmoothL1TermOp<C>{b, loss_param<C>(0.5 * static_cast<double>(b), half), half};
+  }
 };
 
 // ---------------------------------------------------------------- rows
@@ -500,12 +529,12 @@ int supa_amd_loss_forward(const supa_amd_ew_desc* d, int loss, int reduction, do
   if (loss != SUPA_AMD_LOSS_BCE_LOGITS && loss != SUPA_AMD_LOSS_BCE && has_weight) return SUPA_AMD_EINVAL;
   if (reduction == SUPA_AMD_REDUCTION_NONE) {
     switch (loss) {
-      case SUPA_AMD_LOSS_HUBER: return run_ew(HuberTermFactory{beta}, d, stream, 3);
+      case SUPA_AMD_LOSS_HUBER: return run_ew(HuberTermFactory{beta, half_code(d)}, d, stream, 3);
       case SUPA_AMD_LOSS_BCE:
         return has_weight ? run_ew(BceProbTermFactory<true>{half_code(d)}, d, stream, 4)
                           : run_ew(BceProbTermFactory<false>{half_code(d)}, d, stream, 3);
-      case SUPA_AMD_LOSS_MSE: return run_ew(MseTermEwFactory{}, d, stream, 3);
-      case SUPA_AMD_LOSS_SMOOTH_L1: return run_ew(SmoothL1TermEwFactory{beta}, d, stream, 3);
+      case SUPA_AMD_LOSS_MSE: return run_ew(MseTermEwFactory{half_code(d)}, d, stream, 3);
+      case SUPA_AMD_LOSS_SMOOTH_L1: return run_ew(SmoothL1TermEwFactory{beta, half_code(d)}, d, stream, 3);
       case SUPA_AMD_LOSS_BCE_LOGITS:
         if (has_pos_weight && has_weight) return run_ew(BceTermFactory<true, true>{}, d, stream, 5);
         if (has_pos_weight) return run_ew(BceTermFactory<true, false>{}, d, stream, 4);
@@ -522,14 +551,16 @@ int supa_amd_loss_forward(const supa_amd_ew_desc* d, int loss, int reduction, do
   supa_amd_ew_desc e = *d;
   e.op[0].data = out_scalar;
   switch (loss) {
-    case SUPA_AMD_LOSS_HUBER: return run_reduce(HuberTermFactory{beta}, &e, scale, workspace, workspace_bytes, stream);
+    case SUPA_AMD_LOSS_HUBER:
+      return run_reduce(HuberTermFactory{beta, half_code(d)}, &e, scale, workspace, workspace_bytes, stream);
     case SUPA_AMD_LOSS_BCE:
       return has_weight
                  ? run_reduce(BceProbTermFactory<true>{half_code(d)}, &e, scale, workspace, workspace_bytes, stream)
                  : run_reduce(BceProbTermFactory<false>{half_code(d)}, &e, scale, workspace, workspace_bytes, stream);
-    case SUPA_AMD_LOSS_MSE: return run_reduce(MseTermFactory{}, &e, scale, workspace, workspace_bytes, stream);
+    case SUPA_AMD_LOSS_MSE:
+      return run_reduce(MseTermFactory{half_code(d)}, &e, scale, workspace, workspace_bytes, stream);
     case SUPA_AMD_LOSS_SMOOTH_L1:
-      return run_reduce(SmoothL1TermFactory{beta}, &e, scale, workspace, workspace_bytes, stream);
+      return run_reduce(SmoothL1TermFactory{beta, half_code(d)}, &e, scale, workspace, workspace_bytes, stream);
     case SUPA_AMD_LOSS_BCE_LOGITS:
       if (has_pos_weight && has_weight)
         return run_reduce(BceTermFactory<true, true, true>{}, &e, scale, workspace, workspace_bytes, stream);
