@@ -223,6 +223,10 @@ int supa_amd_unary_backward(const supa_amd_ew_desc* d, int op, void* stream);
  *   LOG_SIGMOID  -                            log_sigmoid_forward NF:12260, _backward NF:12276
  *   THRESHOLD    p0 threshold, p1 value (forward); backward: x <= p0 ? 0 : grad
  *                                             threshold.out NF:6244, threshold_backward NF:6252
+ *   HARDSHRINK   p0 lambda                    hardshrink.out NF:5268, hardshrink_backward NF:5281
+ *   SOFTSHRINK   p0 lambda                    softshrink.out NF:12345, softshrink_backward NF:12359
+ *                (both backwards: |x| <= lambda ? 0 : grad; lambda is rounded
+ *                to a 16-bit common dtype, upstream's scalar_t lambda)
  * The formulas are upstream's CUDA activation functors, evaluated in float
  * (double for f64) with the parameters rounded to it. */
 #define SUPA_AMD_ACT_LEAKY_RELU 0
@@ -234,9 +238,33 @@ int supa_amd_unary_backward(const supa_amd_ew_desc* d, int op, void* stream);
 #define SUPA_AMD_ACT_MISH 6
 #define SUPA_AMD_ACT_LOG_SIGMOID 7
 #define SUPA_AMD_ACT_THRESHOLD 8
+#define SUPA_AMD_ACT_HARDSHRINK 9
+#define SUPA_AMD_ACT_SOFTSHRINK 10
 int supa_amd_activation(const supa_amd_ew_desc* d, int act, double p0, double p1, double p2, void* stream);
 int supa_amd_activation_backward(const supa_amd_ew_desc* d, int act, double p0, double p1, double p2, int flag,
                                  void* stream);
+
+/* glu: out = a * sigmoid(b), a and b the two halves of the input along the
+ * gated dim (strided views; sigmoid = 1 / (1 + exp(-b)) in float).  op = {out,
+ * a, b}.  Replaces glu.out NF:12087 (upstream ActivationGluKernel.cu
+ * glu_kernel).
+ * glu_backward, one half per call: half 0 writes the first half's gradient
+ * sigmoid(b) g, op = {grad_a, b, g}; half 1 the second half's
+ * ((1 - s) s) g a, op = {grad_b, a, b, g}.  Replaces
+ * glu_backward.grad_input NF:12100 (upstream glu_backward_kernel, which writes
+ * both halves from one launch). */
+int supa_amd_glu(const supa_amd_ew_desc* d, void* stream);
+int supa_amd_glu_backward(const supa_amd_ew_desc* d, int half, void* stream);
+
+/* prelu: out = x > 0 ? x : w x, w broadcast to x.  op = {out, x, w}.
+ * Replaces _prelu_kernel NF:5203 (upstream prelu_kernel).
+ * prelu backward, one output per call: which 0 the input gradient
+ * x > 0 ? g : w g, op = {grad_x, x, w, g}; which 1 the elementwise weight
+ * gradient x > 0 ? 0 : x g, op = {grad_w, x, g} (full shape; autograd sums
+ * it to the weight's).  Replaces _prelu_kernel_backward NF:5210 (upstream
+ * prelu_backward_kernel, one launch with two outputs). */
+int supa_amd_prelu(const supa_amd_ew_desc* d, void* stream);
+int supa_amd_prelu_backward(const supa_amd_ew_desc* d, int which, void* stream);
 
 /* ------------------------------------------ comparisons and selects */
 

@@ -449,6 +449,67 @@ def loss_backward_16(name: str, grad, x, t, dtype: str, reduction="mean", beta=1
     return np.where(d < -b, r(r(-n * g) * b), np.where(d > b, r(r(n * g) * b), r(r(n * d) * g))).astype(np.float32)
 
 
+def _store(v, dtype: str) -> np.ndarray:
+    """A float32 result stored in dtype ("f32", "bf16", "f16"), as float32."""
+    v = np.asarray(v, np.float32)
+    return v if dtype == "f32" else round16(v, dtype)
+
+
+def shrink(kind: str, x, lambd=0.5, dtype="f32") -> np.ndarray:
+    """hardshrink / softshrink (upstream ActivationHardshrinkKernel.cu,
+    ActivationSoftshrinkKernel.cu) on dtype values given as float32, lambda
+    in the storage type:
+      hardshrink: -lambda <= x <= lambda ? 0 : x
+      softshrink: NaN stays NaN; x > lambda ? x - lambda : x < -lambda ? x + lambda : 0."""
+    x = np.asarray(x, np.float32)
+    lam = _store(np.float32(lambd), dtype)
+    with np.errstate(invalid="ignore"):
+        inside = (x >= -lam) & (x <= lam)
+        if kind == "hardshrink":
+            return np.where(inside, np.float32(0), x).astype(np.float32)
+        r = np.where(x > lam, x - lam, np.where(x < -lam, x + lam, np.float32(0)))
+    return _store(np.where(np.isnan(x), x, r), dtype)
+
+
+def shrink_backward(g, x, lambd=0.5, dtype="f32") -> np.ndarray:
+    """shrink_backward_kernel: -lambda <= x <= lambda ? 0 : g."""
+    x, g = np.broadcast_arrays(np.asarray(x, np.float32), np.asarray(g, np.float32))
+    lam = _store(np.float32(lambd), dtype)
+    return np.where((x >= -lam) & (x <= lam), np.float32(0), g).astype(np.float32)
+
+
+def _sigmoid_f32(b) -> np.ndarray:
+    """1 / (1 + exp(-b)) in float32 with the oracle's exp."""
+    b = np.asarray(b, np.float32)
+    return (np.float32(1) / (np.float32(1) + unary(EXP, -b))).astype(np.float32)
+
+
+def glu(a, b, dtype="f32") -> np.ndarray:
+    """glu's halves (upstream glu_kernel): a sigmoid(b) in float32."""
+    return _store(np.asarray(a, np.float32) * _sigmoid_f32(b), dtype)
+
+
+def glu_backward(a, b, g, dtype="f32"):
+    """glu_backward_kernel: (sigmoid(b) g, ((1 - s) s) g a) for the two halves."""
+    a, b, g = (np.asarray(v, np.float32) for v in (a, b, g))
+    s = _sigmoid_f32(b)
+    return _store(s * g, dtype), _store((((np.float32(1) - s) * s) * g) * a, dtype)
+
+
+def prelu(x, w, dtype="f32") -> np.ndarray:
+    """prelu_kernel: x > 0 ? x : w x (w broadcast to x)."""
+    x, w = np.broadcast_arrays(np.asarray(x, np.float32), np.asarray(w, np.float32))
+    return _store(np.where(x > 0, x, w * x), dtype)
+
+
+def prelu_backward(x, w, g, dtype="f32"):
+    """prelu_backward_kernel: (x > 0 ? g : w g, x > 0 ? 0 : x g), both at the
+    broadcast shape."""
+    x, w, g = np.broadcast_arrays(*(np.asarray(v, np.float32) for v in (x, w, g)))
+    pos = x > 0
+    return _store(np.where(pos, g, w * g), dtype), _store(np.where(pos, np.float32(0), x * g), dtype)
+
+
 def sum_f32(x) -> float:
     x = _c(x, np.float32)
     return float(lib().or_sum_f32(_p(x, _f32p), x.size))

@@ -97,3 +97,83 @@ def test_expm1_log1p_and_foreach(no_fallback):
     zs = [dz.clone(), dz[7:].clone()]
     torch._foreach_log1p_(zs)
     assert torch.equal(zs[1].cpu(), torch.from_numpy(O.unary(O.LOG1P, z[7:].numpy())))
+
+
+def _dname(dtype):
+    return {torch.float32: "f32", torch.bfloat16: "bf16", torch.float16: "f16"}[dtype]
+
+
+@pytest.mark.parametrize("lam", [0.5, 0.3])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_shrink_forward_backward(dtype, lam, no_fallback):
+    """hardshrink / softshrink and their backward against the oracle bit for
+    bit (lambda in the storage type), including +-lambda, 0 and NaN inputs,
+    and a non-contiguous input."""
+    name = _dname(dtype)
+    x = data((517, 129), 60, 1.0, dtype)
+    lt = torch.tensor(lam).to(dtype).item()
+    x.view(-1)[6:11] = torch.tensor([lt, -lt, float("nan"), 2 * lt, -0.0]).to(dtype)
+    g = data((517, 129), 61, 1.0, dtype)
+    for kind, fn in (("hardshrink", F.hardshrink), ("softshrink", F.softshrink)):
+        for view in (lambda t: t, lambda t: t.t()):
+            xs = view(x.to("supa")).detach().requires_grad_()
+            y = fn(xs, lam)
+            xf = view(x).float().numpy()
+            assert np.array_equal(y.detach().cpu().float().numpy(), O.shrink(kind, xf, lam, name),
+                                  equal_nan=True), kind
+            y.backward(view(g.to("supa")))
+            assert np.array_equal(xs.grad.cpu().float().numpy(),
+                                  O.shrink_backward(view(g).float().numpy(), xf, lam, name)), kind
+    with pytest.raises(RuntimeError, match="lambda must be greater or equal to 0"):
+        F.softshrink(x.to("supa"), -0.5)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("dim", [-1, 0, 1])
+def test_glu_forward_backward(dim, dtype, no_fallback):
+    """glu along each dim of a 3-d input (the halves are strided views) and
+    its backward, against the oracle bit for bit; an odd halving dim is an
+    error."""
+    name = _dname(dtype)
+    x = data((34, 18, 66), 62, 2.0, dtype)
+    h = x.shape[dim] // 2
+    xs = x.to("supa").requires_grad_()
+    y = F.glu(xs, dim)
+    a = x.narrow(dim, 0, h).float().numpy()
+    b = x.narrow(dim, h, h).float().numpy()
+    assert np.array_equal(y.detach().cpu().float().numpy(), O.glu(a, b, name))
+    g = data(tuple(y.shape), 63, 1.0, dtype)
+    y.backward(g.to("supa"))
+    ga, gb = O.glu_backward(a, b, g.float().numpy(), name)
+    got = xs.grad.cpu()
+    assert np.array_equal(got.narrow(dim, 0, h).float().numpy(), ga)
+    assert np.array_equal(got.narrow(dim, h, h).float().numpy(), gb)
+    with pytest.raises(RuntimeError, match="Halving dimension must be even"):
+        F.glu(torch.zeros(3, 5, device="supa", dtype=dtype), -1)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("shape, nw", [((16,), 1), ((64, 33), 33), ((8, 6, 5, 7), 6), ((8, 6, 5, 7), 1)])
+def test_prelu_forward_backward(shape, nw, dtype, no_fallback):
+    """nn.PReLU: the forward and the input gradient against the oracle bit
+    for bit; the weight gradient (the elementwise x g, summed by autograd to
+    the weight's shape on the device) within the sum's float32 rounding."""
+    name = _dname(dtype)
+    x = data(shape, 64, 1.0, dtype)
+    w = (torch.randn(nw, generator=torch.Generator().manual_seed(65)) * 0.3).abs().to(dtype)
+    g = data(shape, 66, 1.0, dtype)
+    xs = x.to("supa").requires_grad_()
+    ws = w.to("supa").requires_grad_()
+    y = F.prelu(xs, ws)
+    wshape = [1] * len(shape)
+    if nw > 1:
+        wshape[1] = nw
+    wf = w.float().numpy().reshape(wshape)
+    assert np.array_equal(y.detach().cpu().float().numpy(), O.prelu(x.float().numpy(), wf, name))
+    y.backward(g.to("supa"))
+    gi, gw = O.prelu_backward(x.float().numpy(), wf, g.float().numpy(), name)
+    assert np.array_equal(xs.grad.cpu().float().numpy(), gi)
+    red = tuple(i for i in range(len(shape)) if i != 1 or nw == 1)
+    want_w = gw.astype(np.float64).sum(axis=red).reshape(nw)
+    tol = 1e-5 if dtype == torch.float32 else (2e-2 if dtype == torch.bfloat16 else 2e-3)
+    np.testing.assert_allclose(ws.grad.cpu().float().numpy(), want_w, rtol=tol, atol=tol * np.abs(gw).sum() / nw)

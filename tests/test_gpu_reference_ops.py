@@ -2,9 +2,18 @@
 dtypes, tolerances and comparisons (CPU result against the supa result):
 
 * test_activation_{elu,hardsigmoid,hardswish,hardtanh,leaky_relu,
-  log_sigmoid,mish,softplus,threshold}_kernel.py: forward and backward at
-  default parameters (threshold exact at (0.5 | 1.0, 20), elu and threshold
-  in place too; hardswish's inputs of exactly +-3 moved off the kink);
+  log_sigmoid,mish,softplus,threshold,hardshrink,softshrink}_kernel.py:
+  forward and backward at default parameters (threshold exact at
+  (0.5 | 1.0, 20), elu and threshold in place too; hardswish's inputs of
+  exactly +-3 moved off the kink);
+* test_activation_glu_kernel.py (its bfloat16 atol 1e-2; it compares the
+  gradients for bfloat16 only and the outputs again otherwise; here float32's
+  gradients are compared too.  Upstream CPU's float16 glu backward rounds
+  its steps to float16, so where 1 - sigmoid cancels it is a few percent
+  from the device's float32 arithmetic, which the oracle checks bit for bit
+  in test_gpu_activations.py) and test_activation_prelu_kernel.py
+  (forward only there: its backward case waits on a sum it lacks; the
+  backward is checked in test_gpu_activations.py);
 * test_binary_div_floor_kernel.py, test_binary_div_trunc_kernel.py: true
   division, rounding_mode 'floor' / 'trunc' (float16 quotients kept within
   512 for floor, as there) and their backward;
@@ -61,6 +70,7 @@ def ref_allclose(golden, compare, rtol, atol, equal_nan=False):
 ACTS = {
     "elu": F.elu, "hardsigmoid": F.hardsigmoid, "hardswish": F.hardswish, "hardtanh": F.hardtanh,
     "leaky_relu": F.leaky_relu, "log_sigmoid": torch.nn.LogSigmoid(), "mish": F.mish, "softplus": F.softplus,
+    "hardshrink": F.hardshrink, "softshrink": F.softshrink,
 }
 
 
@@ -82,6 +92,38 @@ def test_activation_forward_backward(name, shape, dtype, no_fallback):
     yc.backward(gc)
     ys.backward(gs)
     ref_allclose(xc.grad, xs.grad, RTOL[dtype], ATOL[dtype])
+
+
+GLU_SHAPES = [(16,), (1024, 512), (1023, 510), (1025, 514), (1028, 2136)]
+GLU_ATOL = {torch.float32: 1e-5, torch.bfloat16: 1e-2, torch.float16: 1e-5}
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("shape", GLU_SHAPES)
+def test_glu(shape, dtype, no_fallback):
+    """test_activation_glu_kernel.py: glu over the last dim, forward and
+    backward with an N(0, 1) upstream gradient."""
+    xc, xs = pair(shape, dtype, True)
+    yc, ys = F.glu(xc), F.glu(xs)
+    ref_allclose(yc, ys, RTOL[dtype], GLU_ATOL[dtype])
+    gc, gs = pair(yc.shape, dtype)
+    yc.backward(gc)
+    ys.backward(gs)
+    if dtype == torch.float16:
+        ref_allclose(yc, ys, RTOL[dtype], GLU_ATOL[dtype])
+    else:
+        ref_allclose(xc.grad, xs.grad, RTOL[dtype], GLU_ATOL[dtype])
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("shape", BR200)
+def test_prelu(shape, dtype, no_fallback):
+    """test_activation_prelu_kernel.py: nn.PReLU with one weight per channel
+    (dim 1; one weight for a 1-d input), an N(0, 1) weight."""
+    xc, xs = pair(shape, dtype)
+    n = shape[1] if len(shape) >= 2 else 1
+    wc, ws = pair((n,), dtype)
+    ref_allclose(F.prelu(xc, wc), F.prelu(xs, ws), RTOL[dtype], ATOL[dtype])
 
 
 @pytest.mark.parametrize("dtype", DTYPES)

@@ -694,3 +694,75 @@ def test_elu_backward_from_result():
         F.elu(xr, alpha).backward(g.double())
         got = O.activation_backward(O.ACT_ELU, g.numpy(), y.float().numpy(), alpha, 1.0, 1.0, 1)
         np.testing.assert_allclose(got, xr.grad.numpy(), rtol=2e-6, atol=1e-7)
+
+
+def _dname(dtype):
+    return {torch.float32: "f32", torch.bfloat16: "bf16", torch.float16: "f16"}[dtype]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_shrink_and_prelu_bit_exact(dtype):
+    """hardshrink / softshrink (lambda 0.5, and 0.3, which no 16-bit type
+    holds exactly) with their shared backward, and prelu with its backward:
+    the oracle equals upstream CPU bit for bit, on inputs that include
+    +-lambda, 0 and NaN.  At a NaN input the backward passes the gradient
+    (upstream's scalar form, -lambda <= x <= lambda ? 0 : g, which the
+    device kernel uses); upstream CPU's vectorised form gives 0 there, so the
+    NaN gradient is pinned on a tensor short enough for CPU's scalar loop.
+    Lambda is a value of the storage type (upstream's device kernels take
+    value.to<scalar_t>()); upstream CPU's 16-bit softshrink keeps a float32
+    lambda, so it is handed the rounded lambda for the comparison."""
+    name = _dname(dtype)
+    x = randn((4096,), 51, 1.0, dtype)
+    g = randn((4096,), 52, 1.0, dtype)
+    for lam in (0.5, 0.3):
+        lam_t = torch.tensor(lam).to(dtype).item()
+        x[:6] = torch.tensor([lam_t, -lam_t, 0.0, float("nan"), 2 * lam_t, -2 * lam_t]).to(dtype)
+        xf, gf = x.float().numpy(), g.float().numpy()
+        for kind, fn in (("hardshrink", F.hardshrink), ("softshrink", F.softshrink)):
+            want = fn(x, lam_t).float().numpy()
+            assert np.array_equal(O.shrink(kind, xf, lam, name), want, equal_nan=True), (kind, lam)
+            xx = x.clone().requires_grad_()
+            fn(xx, lam).backward(g)
+            keep = ~np.isnan(xf)
+            assert np.array_equal(O.shrink_backward(gf, xf, lam, name)[keep],
+                                  xx.grad.float().numpy()[keep]), (kind, lam)
+            xs = x[:6].clone().requires_grad_()
+            fn(xs, lam).backward(g[:6])
+            assert np.array_equal(O.shrink_backward(gf[:6], xf[:6], lam, name), xs.grad.float().numpy())
+    xc = randn((8, 6, 5, 7), 53, 1.0, dtype)
+    w = randn((6,), 54, 0.5, dtype)
+    gc = randn((8, 6, 5, 7), 55, 1.0, dtype)
+    xf, wf, gf = xc.float().numpy(), w.float().numpy().reshape(1, 6, 1, 1), gc.float().numpy()
+    assert np.array_equal(O.prelu(xf, wf, name), F.prelu(xc, w).float().numpy())
+    gi, gw = torch.ops.aten._prelu_kernel_backward(gc, xc, w.reshape(1, 6, 1, 1))
+    ogi, ogw = O.prelu_backward(xf, wf, gf, name)
+    assert np.array_equal(ogi, gi.float().numpy()) and np.array_equal(ogw, gw.float().numpy())
+
+
+def test_glu_against_cpu_and_closed_forms():
+    """glu and its backward: within 4 float32 ulps of upstream CPU (whose
+    vectorised exp differs from the oracle's in the last bit; the sigmoid's
+    division and the products add a rounding each), and exactly
+    the closed forms at b = 0 (sigmoid 1/2: a / 2; gradients g / 2 and
+    g a / 4) and at b = +-100 (sigmoid 1, and 0 once exp(100) overflows)."""
+    x = randn((64, 258), 56)
+    g = randn((64, 129), 57)
+    a, b = x[:, :129].numpy(), x[:, 129:].numpy()
+    assert f32_ulp_dist(O.glu(a, b), F.glu(x, -1).numpy()).max() <= 4
+    xx = x.clone().requires_grad_()
+    F.glu(xx, -1).backward(g)
+    ga, gb = O.glu_backward(a, b, g.numpy())
+    assert f32_ulp_dist(ga, xx.grad[:, :129].numpy()).max() <= 4
+    # (1 - s) s cancels as s -> 1: an error of an ulp of s moves the second
+    # half's gradient by up to |g a| 2^-24 whatever its own size
+    gn = g.numpy()
+    cpu_gb = xx.grad[:, 129:].numpy()
+    assert np.all(np.abs(gb - cpu_gb) <= 4 * 2.0 ** -24 * np.abs(gn * a) + 4 * np.spacing(np.abs(cpu_gb)))
+    zero = np.zeros_like(b)
+    assert np.array_equal(O.glu(a, zero), a * np.float32(0.5))
+    ga, gb = O.glu_backward(a, zero, gn)
+    assert np.array_equal(ga, gn * np.float32(0.5)) and np.array_equal(gb, (gn * a) * np.float32(0.25))
+    assert np.array_equal(O.glu(a, zero + 100), a)
+    # exp(100) overflows float32: sigmoid 1 / (1 + inf) = 0, the product a signed zero
+    assert np.array_equal(O.glu(a, zero - 100), a * np.float32(0))

@@ -1105,6 +1105,118 @@ at::Tensor& threshold_backward_out(const at::Tensor& g, const at::Tensor& s, con
   return gi;
 }
 
+// hardshrink / softshrink and their shared backward (upstream Activation.cpp:
+// softshrink refuses a negative lambda)
+void check_softshrink(const c10::Scalar& l) {
+  TORCH_CHECK(sd(l) >= 0, "lambda must be greater or equal to 0, but found to be ", sd(l), ".");
+}
+at::Tensor hardshrink(const at::Tensor& s, const c10::Scalar& l) {
+  return act_apply(s, {}, false, SUPA_AMD_ACT_HARDSHRINK, sd(l), 0, 0, "hardshrink");
+}
+at::Tensor& hardshrink_out(const at::Tensor& s, const c10::Scalar& l, at::Tensor& out) {
+  act_apply(s, out, false, SUPA_AMD_ACT_HARDSHRINK, sd(l), 0, 0, "hardshrink.out");
+  return out;
+}
+at::Tensor hardshrink_backward(const at::Tensor& g, const at::Tensor& s, const c10::Scalar& l) {
+  return act_bwd_apply(g, s, {}, SUPA_AMD_ACT_HARDSHRINK, sd(l), 0, 0, 0, "hardshrink_backward");
+}
+at::Tensor& hardshrink_backward_out(const at::Tensor& g, const at::Tensor& s, const c10::Scalar& l, at::Tensor& gi) {
+  act_bwd_apply(g, s, gi, SUPA_AMD_ACT_HARDSHRINK, sd(l), 0, 0, 0, "hardshrink_backward.grad_input");
+  return gi;
+}
+at::Tensor softshrink(const at::Tensor& s, const c10::Scalar& l) {
+  check_softshrink(l);
+  return act_apply(s, {}, false, SUPA_AMD_ACT_SOFTSHRINK, sd(l), 0, 0, "softshrink");
+}
+at::Tensor& softshrink_out(const at::Tensor& s, const c10::Scalar& l, at::Tensor& out) {
+  check_softshrink(l);
+  act_apply(s, out, false, SUPA_AMD_ACT_SOFTSHRINK, sd(l), 0, 0, "softshrink.out");
+  return out;
+}
+at::Tensor softshrink_backward(const at::Tensor& g, const at::Tensor& s, const c10::Scalar& l) {
+  return act_bwd_apply(g, s, {}, SUPA_AMD_ACT_SOFTSHRINK, sd(l), 0, 0, 0, "softshrink_backward");
+}
+at::Tensor& softshrink_backward_out(const at::Tensor& g, const at::Tensor& s, const c10::Scalar& l, at::Tensor& gi) {
+  act_bwd_apply(g, s, gi, SUPA_AMD_ACT_SOFTSHRINK, sd(l), 0, 0, 0, "softshrink_backward.grad_input");
+  return gi;
+}
+
+// glu: the two halves along dim as strided views of the input, one binary
+// launch (upstream GatedLinearUnit.cpp's checks and halving).
+int64_t glu_dim(const at::Tensor& self, int64_t dim) {
+  TORCH_CHECK(self.dim() > 0, "glu does not support scalars because halving size must be even");
+  const int64_t wd = at::maybe_wrap_dim(dim, self.dim());
+  TORCH_CHECK(self.size(wd) % 2 == 0, "Halving dimension must be even, but dimension ", wd, " is size ",
+              self.size(wd));
+  return wd;
+}
+at::Tensor glu_into(const at::Tensor& self, int64_t dim, at::Tensor out, const char* name) {
+  const int64_t wd = glu_dim(self, dim);
+  const int64_t h = self.size(wd) / 2;
+  const c10::ScalarType common = self.scalar_type();
+  TORCH_CHECK(at::isFloatingType(common), name, ": \"glu\" not implemented for '", common, "'");
+  const Launch fn = [](const supa_amd_ew_desc* d, void* s) { return supa_amd_glu(d, s); };
+  std::vector<EwIn> ins{EwIn::of(self.narrow(wd, 0, h)), EwIn::of(self.narrow(wd, h, h))};
+  if (out.defined()) {
+    check_cast(common, out, name);
+    return ew_apply(out, out.scalar_type(), common, ins, fn, name);
+  }
+  return ew_apply(at::Tensor(), common, common, ins, fn, name);
+}
+at::Tensor glu(const at::Tensor& self, int64_t dim) { return glu_into(self, dim, {}, "glu"); }
+at::Tensor& glu_out(const at::Tensor& self, int64_t dim, at::Tensor& out) {
+  glu_into(self, dim, out, "glu.out");
+  return out;
+}
+// glu_backward writes each half of grad_input (sized as the input) through a
+// strided view of it, one launch per half.
+at::Tensor& glu_backward_into(const at::Tensor& g, const at::Tensor& self, int64_t dim, at::Tensor& gi,
+                              const char* name) {
+  const int64_t wd = glu_dim(self, dim);
+  const int64_t h = self.size(wd) / 2;
+  const c10::ScalarType common = at::result_type(g, self);
+  TORCH_CHECK(at::isFloatingType(common), name, ": not implemented for '", common, "'");
+  at::native::resize_output(gi, self.sizes());
+  const at::Tensor a = self.narrow(wd, 0, h), b = self.narrow(wd, h, h);
+  at::Tensor ga = gi.narrow(wd, 0, h), gb = gi.narrow(wd, h, h);
+  ew_apply(ga, gi.scalar_type(), common, {EwIn::of(b), EwIn::of(g)},
+           [](const supa_amd_ew_desc* d, void* s) { return supa_amd_glu_backward(d, 0, s); }, name);
+  ew_apply(gb, gi.scalar_type(), common, {EwIn::of(a), EwIn::of(b), EwIn::of(g)},
+           [](const supa_amd_ew_desc* d, void* s) { return supa_amd_glu_backward(d, 1, s); }, name);
+  return gi;
+}
+at::Tensor glu_backward(const at::Tensor& g, const at::Tensor& self, int64_t dim) {
+  at::Tensor gi = at::empty_like(self);
+  return glu_backward_into(g, self, dim, gi, "glu_backward");
+}
+at::Tensor& glu_backward_out(const at::Tensor& g, const at::Tensor& self, int64_t dim, at::Tensor& gi) {
+  return glu_backward_into(g, self, dim, gi, "glu_backward.grad_input");
+}
+
+// prelu's kernels (upstream _prelu_kernel / _prelu_kernel_backward; the
+// composite prelu has already shaped the weight to broadcast over self).  The
+// backward's weight gradient is elementwise, at the broadcast shape.
+at::Tensor prelu_kernel(const at::Tensor& self, const at::Tensor& weight) {
+  const c10::ScalarType common = at::result_type(self, weight);
+  TORCH_CHECK(at::isFloatingType(common), "_prelu_kernel: \"prelu\" not implemented for '", common, "'");
+  return ew_apply(at::Tensor(), self.scalar_type(), common, {EwIn::of(self), EwIn::of(weight)},
+                  [](const supa_amd_ew_desc* d, void* s) { return supa_amd_prelu(d, s); }, "_prelu_kernel");
+}
+std::tuple<at::Tensor, at::Tensor> prelu_kernel_backward(const at::Tensor& g, const at::Tensor& self,
+                                                         const at::Tensor& weight) {
+  const c10::ScalarType common = c10::promoteTypes(at::result_type(self, weight), g.scalar_type());
+  TORCH_CHECK(at::isFloatingType(common), "_prelu_kernel_backward: not implemented for '", common, "'");
+  at::Tensor gs = ew_apply(at::Tensor(), self.scalar_type(), common,
+                           {EwIn::of(self), EwIn::of(weight), EwIn::of(g)},
+                           [](const supa_amd_ew_desc* d, void* s) { return supa_amd_prelu_backward(d, 0, s); },
+                           "_prelu_kernel_backward");
+  at::Tensor gw = ew_apply(at::Tensor(), weight.scalar_type(), common,
+                           {EwIn::of(self), EwIn::of(g)},
+                           [](const supa_amd_ew_desc* d, void* s) { return supa_amd_prelu_backward(d, 1, s); },
+                           "_prelu_kernel_backward");
+  return {gs, gw};
+}
+
 }  // namespace
 }  // namespace supa
 
@@ -1237,6 +1349,20 @@ TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
   m.impl("threshold.out", TORCH_FN(threshold_out));
   m.impl("threshold_backward", TORCH_FN(threshold_backward));
   m.impl("threshold_backward.grad_input", TORCH_FN(threshold_backward_out));
+  m.impl("hardshrink", TORCH_FN(hardshrink));
+  m.impl("hardshrink.out", TORCH_FN(hardshrink_out));
+  m.impl("hardshrink_backward", TORCH_FN(hardshrink_backward));
+  m.impl("hardshrink_backward.grad_input", TORCH_FN(hardshrink_backward_out));
+  m.impl("softshrink", TORCH_FN(softshrink));
+  m.impl("softshrink.out", TORCH_FN(softshrink_out));
+  m.impl("softshrink_backward", TORCH_FN(softshrink_backward));
+  m.impl("softshrink_backward.grad_input", TORCH_FN(softshrink_backward_out));
+  m.impl("glu", TORCH_FN(glu));
+  m.impl("glu.out", TORCH_FN(glu_out));
+  m.impl("glu_backward", TORCH_FN(glu_backward));
+  m.impl("glu_backward.grad_input", TORCH_FN(glu_backward_out));
+  m.impl("_prelu_kernel", TORCH_FN(prelu_kernel));
+  m.impl("_prelu_kernel_backward", TORCH_FN(prelu_kernel_backward));
   m.impl("gelu", TORCH_FN(gelu));
   m.impl("gelu_", TORCH_FN(gelu_));
   m.impl("gelu.out", TORCH_FN(gelu_out));

@@ -78,14 +78,14 @@ struct MseBwdFactory {
   double norm;
   int half;
   template <typename C> static constexpr bool ok() { return std::is_floating_point<C>::value; }
-  template <typename C> MseBwdOp<C> make() const { return MseBwdOp<C>{loss_param<C>(norm, half), half}; }
+  template <typename C> MseBwdOp<C> make() const { return MseBwdOp<C>{storage_param<C>(norm, half), half}; }
 };
 struct SmoothL1BwdFactory {
   double norm, beta;
   int half;
   template <typename C> static constexpr bool ok() { return std::is_floating_point<C>::value; }
   template <typename C> SmoothL1BwdOp<C> make() const {
-    return SmoothL1BwdOp<C>{loss_param<C>(norm, half), loss_param<C>(beta, half), half};
+    return SmoothL1BwdOp<C>{storage_param<C>(norm, half), storage_param<C>(beta, half), half};
   }
 };
 
@@ -94,7 +94,7 @@ struct HuberBwdFactory {
   int half;
   template <typename C> static constexpr bool ok() { return std::is_floating_point<C>::value; }
   template <typename C> HuberBwdOp<C> make() const {
-    return HuberBwdOp<C>{loss_param<C>(norm, half), loss_param<C>(delta, half), half};
+    return HuberBwdOp<C>{storage_param<C>(norm, half), storage_param<C>(delta, half), half};
   }
 };
 template <bool W>

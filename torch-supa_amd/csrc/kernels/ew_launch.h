@@ -48,7 +48,7 @@ inline float host_round_f16(float f) {
 }
 // A kernel parameter in the compute type C: v rounded to the 16-bit storage
 // type for `half` 1 / 2 (upstream's scalar_t parameters), else C(v).
-template <typename C> inline C loss_param(double v, int half) {
+template <typename C> inline C storage_param(double v, int half) {
   if (half == 1) return static_cast<C>(host_round_bf16(static_cast<float>(v)));
   if (half == 2) return static_cast<C>(host_round_f16(static_cast<float>(v)));
   return static_cast<C>(v);

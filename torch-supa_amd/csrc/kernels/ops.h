@@ -290,13 +290,18 @@ template <int K, typename C> struct UnaryBwdOp {
 // `a + b * c` forms are one fma, as that compiler contracts them.  std::max /
 // std::min are the device forms (a < b) ? b : a and (b < a) ? b : a.
 enum ActKind {
-  A_LEAKY_RELU = 0, A_HARDTANH, A_ELU, A_SOFTPLUS, A_HARDSWISH, A_HARDSIGMOID, A_MISH, A_LOG_SIGMOID, A_THRESHOLD
+  A_LEAKY_RELU = 0, A_HARDTANH, A_ELU, A_SOFTPLUS, A_HARDSWISH, A_HARDSIGMOID, A_MISH, A_LOG_SIGMOID, A_THRESHOLD,
+  A_HARDSHRINK, A_SOFTSHRINK
 };
 template <typename C> __device__ __forceinline__ C max_lt(C a, C b) { return (a < b) ? b : a; }
 template <typename C> __device__ __forceinline__ C min_lt(C a, C b) { return (b < a) ? b : a; }
 
 // p0, p1, p2: leaky_relu (slope); elu (alpha, scale, input_scale); softplus
-// (beta, threshold); threshold (threshold, value).
+// (beta, threshold); threshold (threshold, value); hardshrink / softshrink
+// (lambda, in scalar_t as upstream's ActivationHardshrinkKernel.cu /
+// ActivationSoftshrinkKernel.cu take it: rounded to a 16-bit storage type).
+// softshrink keeps a NaN input (its _isnan test); hardshrink's comparisons
+// are false for NaN, which passes it through as well.
 template <int K, typename C> struct ActOp {
   static constexpr int arity = 1;
   C p0, p1, p2;
@@ -309,6 +314,8 @@ template <int K, typename C> struct ActOp {
     else if constexpr (K == A_HARDSIGMOID) return min_lt<C>(max_lt<C>(x + C(3), C(0)), C(6)) * C(1.0f / 6.0f);
     else if constexpr (K == A_MISH) return x * tanhx<C>(log1px<C>(expx<C>(x)));
     else if constexpr (K == A_LOG_SIGMOID) return min_lt<C>(C(0), x) - log1px<C>(expx<C>(-fabs(x)));
+    else if constexpr (K == A_HARDSHRINK) return (x >= -p0 && x <= p0) ? C(0) : x;
+    else if constexpr (K == A_SOFTSHRINK) return x != x ? x : (x > p0 ? x - p0 : (x < -p0 ? x + p0 : C(0)));
     else return x <= p0 ? p1 : x;  // threshold
   }
 };
@@ -344,10 +351,55 @@ template <int K, typename C> struct ActBwdOp {
       const bool neg = x < C(0);
       const C z = expx<C>(-fabs(x));
       return g * muladd<C>(neg ? C(-1) : C(1), z / (C(1) + z), neg ? C(1) : C(0));
+    } else if constexpr (K == A_HARDSHRINK || K == A_SOFTSHRINK) {
+      return (x >= -p0 && x <= p0) ? C(0) : g;  // upstream shrink_backward_kernel
     } else {
       return x <= p0 ? C(0) : g;  // threshold_backward
     }
   }
+};
+
+// glu (upstream glu_kernel, ActivationGluKernel.cu): a sigmoid(b) in opmath,
+// sigmoid = 1 / (1 + exp(-b)); inputs a, b (the two halves).
+template <typename C> struct GluOp {
+  static constexpr int arity = 2;
+  __device__ __forceinline__ C operator()(const C* v) const {
+    const C s = C(1) / (C(1) + expx<C>(-v[1]));
+    return v[0] * s;
+  }
+};
+// glu_backward's halves (upstream glu_backward_kernel): the first half's
+// gradient sigmoid(b) g (inputs b, g); the second half's ((1 - s) s) g a
+// (inputs a, b, g).
+template <typename C> struct GluBwdFirstOp {
+  static constexpr int arity = 2;
+  __device__ __forceinline__ C operator()(const C* v) const {
+    const C s = C(1) / (C(1) + expx<C>(-v[0]));
+    return s * v[1];
+  }
+};
+template <typename C> struct GluBwdSecondOp {
+  static constexpr int arity = 3;
+  __device__ __forceinline__ C operator()(const C* v) const {
+    const C s = C(1) / (C(1) + expx<C>(-v[1]));
+    return (((C(1) - s) * s) * v[2]) * v[0];
+  }
+};
+// prelu (upstream prelu_kernel / prelu_backward_kernel, in scalar_t: one
+// operation each, rounded once at the store): x > 0 ? x : w x (inputs x, w);
+// the input gradient x > 0 ? g : w g (inputs x, w, g); the elementwise weight
+// gradient x > 0 ? 0 : x g (inputs x, g).
+template <typename C> struct PreluOp {
+  static constexpr int arity = 2;
+  __device__ __forceinline__ C operator()(const C* v) const { return v[0] > C(0) ? v[0] : v[1] * v[0]; }
+};
+template <typename C> struct PreluBwdInputOp {
+  static constexpr int arity = 3;
+  __device__ __forceinline__ C operator()(const C* v) const { return v[0] > C(0) ? v[2] : v[1] * v[2]; }
+};
+template <typename C> struct PreluBwdWeightOp {
+  static constexpr int arity = 2;
+  __device__ __forceinline__ C operator()(const C* v) const { return v[0] > C(0) ? C(0) : v[0] * v[1]; }
 };
 
 // ------------------------------------------------------------ ternary

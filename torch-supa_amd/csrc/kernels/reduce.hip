@@ -356,8 +356,8 @@ struct SmoothL1TermFactory {
   double beta;
   int half;
   template <typename C, typename T = void> auto make() const {
-    const C b = loss_param<C>(beta, half);
-    return SmoothL1TermOp<C, storage_half<T>()>{b, loss_param<C>(0.5 * static_cast<double>(b), half), half};
+    const C b = storage_param<C>(beta, half);
+    return SmoothL1TermOp<C, storage_half<T>()>{b, storage_param<C>(0.5 * static_cast<double>(b), half), half};
   }
 };
 template <bool PW, bool W, bool HW = false>
@@ -374,8 +374,8 @@ struct HuberTermFactory {
   int half;
   template <typename C> static constexpr bool ok() { return std::is_floating_point<C>::value; }
   template <typename C, typename T = void> auto make() const {
-    const C dl = loss_param<C>(delta, half);
-    return HuberTermOp<C, storage_half<T>()>{dl, loss_param<C>(0.5 * static_cast<double>(dl), half), half};
+    const C dl = storage_param<C>(delta, half);
+    return HuberTermOp<C, storage_half<T>()>{dl, storage_param<C>(0.5 * static_cast<double>(dl), half), half};
   }
 };
 template <bool W>
@@ -398,8 +398,8 @@ struct SmoothL1TermEwFactory {
   int half;
   template <typename C> static constexpr bool ok() { return std::is_floating_point<C>::value; }
   template <typename C> SmoothL1TermOp<C> make() const {
-    const C b = loss_param<C>(beta, half);
-    return SmoothL1TermOp<C>{b, loss_param<C>(0.5 * static_cast<double>(b), half), half};
+    const C b = storage_param<C>(beta, half);
+    return SmoothL1TermOp<C>{b, storage_param<C>(0.5 * static_cast<double>(b), half), half};
   }
 };
 
