@@ -696,6 +696,24 @@ int supa_amd_fused_adam(int32_t ntensors, void* const* params, void* const* grad
                         int amsgrad, int maximize, const float* grad_scale,
                         const float* found_inf, void* stream);
 
+/* _fused_sgd_ over a tensor list, in place: one multi-tensor launch per
+ * table of tensors, as supa_amd_fused_adamw.  params, grads and (with momentum) momentum_buffers are
+ * device pointers to contiguous tensors of `dtype` (f32, bf16, f16, f64) with
+ * numel[i] elements each.  momentum_buffers is NULL exactly when momentum is
+ * 0; with is_first_step each buffer is written with the gradient instead of
+ * read.  lr_ptr (a device float, may be NULL) overrides lr; grad_scale divides
+ * the gradients first (and they are stored back unscaled); a found_inf of 1
+ * makes the step a no-op.  Per element, as upstream sgd_math
+ * (FusedSgdKernel.cu) with double hyper-parameters:
+ *   g /= grad_scale; g = -g if maximize; g += weight_decay p;
+ *   buf = first ? g : momentum buf + (1 - dampening) g;
+ *   g = nesterov ? g + momentum buf : buf;  p -= lr g
+ * Replaces _fused_sgd_ NF:16061 and _fused_sgd_.tensor_lr NF:16070. */
+int supa_amd_fused_sgd(int32_t ntensors, void* const* params, void* const* grads, void* const* momentum_buffers,
+                       const int64_t* numel, int32_t dtype, double weight_decay, double momentum, double lr,
+                       const float* lr_ptr, double dampening, int nesterov, int maximize, int is_first_step,
+                       const float* grad_scale, const float* found_inf, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

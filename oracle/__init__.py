@@ -87,6 +87,8 @@ def lib():
             "or_ce_bwd": (None, [_f64p, _f64p, _i64p, _f64p, c_double, i64, i64, i64, c_int, _f64p]),
             "or_adamw_step": (None, [_f32p, _f32p, _f32p, _f32p, i64, c_float, c_double, c_double,
                                      c_double, c_double, c_double, c_int, _f32p, c_int, _f32p, c_int]),
+            "or_sgd_step": (None, [_f32p, _f32p, _f32p, i64, c_double, c_double, c_double, c_double, c_int, c_int,
+                                   c_int, _f32p]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -447,6 +449,18 @@ def loss_backward_16(name: str, grad, x, t, dtype: str, reduction="mean", beta=1
             mid = r(r(r(n * d) * g) / b)
         return np.where(d < -b, r(-n * g), np.where(d > b, r(n * g), mid)).astype(np.float32)
     return np.where(d < -b, r(r(-n * g) * b), np.where(d > b, r(r(n * g) * b), r(r(n * d) * g))).astype(np.float32)
+
+
+def sgd_step(p, g, buf, lr, momentum=0.0, dampening=0.0, weight_decay=0.0, nesterov=False, maximize=False,
+             first=False, grad_scale=None):
+    """In-place _fused_sgd_ step on float32 numpy arrays (p, buf and, with
+    grad_scale, g are updated); buf is None without momentum."""
+    for a in (p, g) + (() if buf is None else (buf,)):
+        assert a.dtype == np.float32 and a.flags.c_contiguous
+    gs = None if grad_scale is None else np.asarray([grad_scale], np.float32)
+    lib().or_sgd_step(_p(p, _f32p), _p(g, _f32p), _p(buf, _f32p), p.size, float(weight_decay), float(momentum),
+                      float(lr), float(dampening), 1 if nesterov else 0, 1 if maximize else 0, 1 if first else 0,
+                      _p(gs, _f32p))
 
 
 def _store(v, dtype: str) -> np.ndarray:

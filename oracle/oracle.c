@@ -724,6 +724,31 @@ void or_adamw_step(float* p, float* g, float* m, float* v, int64_t n, float step
   }
 }
 
+/* _fused_sgd_ step (upstream sgd_math, FusedSgdKernel.cu; the reference
+ * registers upstream's kernel): float32 state, double hyper-parameters, each
+ * mixed expression in double with a + b c as one fma, rounded once.  buf is
+ * NULL without momentum; `first` writes it with the gradient.  The double
+ * buffer value feeds the nesterov step before its rounding for storage. */
+void or_sgd_step(float* p, float* g, float* buf, int64_t n, double weight_decay, double momentum, double lr,
+                 double dampening, int nesterov, int maximize, int first, const float* grad_scale) {
+  for (int64_t i = 0; i < n; ++i) {
+    float param = p[i];
+    float grad = g[i];
+    if (grad_scale) {
+      grad = (float)((double)grad / (double)(*grad_scale));
+      g[i] = grad;
+    }
+    if (maximize) grad = -grad;
+    if (weight_decay != 0.0) grad = (float)fma(weight_decay, (double)param, (double)grad);
+    if (buf) {
+      const double b = first ? (double)grad : fma(momentum, (double)buf[i], (1.0 - dampening) * (double)grad);
+      buf[i] = (float)b;
+      grad = nesterov ? (float)fma(momentum, b, (double)grad) : (float)b;
+    }
+    p[i] = (float)fma(-lr, (double)grad, (double)param);
+  }
+}
+
 /* ------------------------------------------------------ random numbers -- */
 
 /* Philox4x32-10 (Salmon, Moraes, Dror, Shaw, "Parallel random numbers: as

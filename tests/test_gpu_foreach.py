@@ -450,3 +450,80 @@ def test_clip_grad_norm(norm_type, no_fallback):
     assert total.item() == pytest.approx(total_cpu.item(), rel=1e-5)
     for p, pc in zip(ps, ps_cpu):
         torch.testing.assert_close(p.grad.cpu(), pc.grad, rtol=1e-5, atol=1e-9)
+
+
+def _store16(a, dtype):
+    """float32 results stored in dtype, as float32."""
+    return a if dtype == torch.float32 else torch.from_numpy(a).to(dtype).float().numpy()
+
+
+SGD_CFGS = [dict(momentum=0.0), dict(momentum=0.9), dict(momentum=0.9, nesterov=True, weight_decay=0.01),
+            dict(momentum=0.9, dampening=0.2, weight_decay=0.01, maximize=True),
+            dict(momentum=0.0, weight_decay=0.05, grad_scale=8.0),
+            dict(momentum=0.5, grad_scale=2.0, lr_tensor="supa"), dict(momentum=0.9, lr_tensor="cpu")]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("ci", range(len(SGD_CFGS)))
+def test_fused_sgd_bit_exact(ci, dtype, no_fallback):
+    """_fused_sgd_ over ragged tensors (one misaligned by an element, so it
+    takes the scalar path) for three steps, fresh gradients each step:
+    params, momentum buffers and (with grad_scale) the unscaled gradients
+    equal the oracle's step bit for bit, the 16-bit ones being its float32
+    results rounded once per step."""
+    cfg = dict(SGD_CFGS[ci])
+    gsc = cfg.pop("grad_scale", None)
+    lr_kind = cfg.pop("lr_tensor", None)
+    mom = cfg["momentum"] != 0
+    lr = 0.01
+    ps = [t.to("supa") for t in lists(80, dtype)]
+    base = torch.zeros(1001, dtype=dtype, device="supa")
+    odd = base[1:]
+    odd.copy_(torch.randn(1000, generator=torch.Generator().manual_seed(81)).to(dtype))
+    ps.append(odd)  # data pointer 2 or 4 bytes past 16-byte alignment
+    ref_p = [f32(t.cpu()) for t in ps]
+    ref_b = [np.zeros_like(a) for a in ref_p] if mom else None
+    bufs = [torch.empty_like(t) for t in ps] if mom else []
+    lr_arg = lr if lr_kind is None else torch.tensor(lr, device=lr_kind)
+    scale = None if gsc is None else torch.tensor(gsc, device="supa")
+    for step in range(3):
+        grads = [t.to("supa") for t in lists(82 + step, dtype)] + [
+            torch.randn(1000, generator=torch.Generator().manual_seed(90 + step)).to(dtype).to("supa")]
+        ref_g = [f32(t.cpu()) for t in grads]
+        torch._fused_sgd_(ps, grads, bufs, weight_decay=cfg.get("weight_decay", 0.0), momentum=cfg["momentum"],
+                          lr=lr_arg, dampening=cfg.get("dampening", 0.0), nesterov=cfg.get("nesterov", False),
+                          maximize=cfg.get("maximize", False), is_first_step=step == 0, grad_scale=scale)
+        for i in range(len(ps)):
+            p, g = ref_p[i].copy(), ref_g[i].copy()
+            b = ref_b[i].copy() if mom else None
+            # a tensor lr is a float32 value (read on the device, or item() on the host)
+            O.sgd_step(p, g, b, np.float32(lr) if lr_kind else lr, first=step == 0, grad_scale=gsc, **cfg)
+            ref_p[i] = _store16(p, dtype)
+            assert np.array_equal(f32(ps[i].cpu()), ref_p[i]), (i, step)
+            if mom:
+                ref_b[i] = _store16(b, dtype)
+                assert np.array_equal(f32(bufs[i].cpu()), ref_b[i]), (i, step)
+            if gsc is not None:
+                assert np.array_equal(f32(grads[i].cpu()), _store16(g, dtype)), (i, step)
+
+
+def test_fused_sgd_found_inf_and_checks(no_fallback):
+    """found_inf = 1 leaves every tensor unchanged, 0 steps; a momentum list
+    needs momentum > 0 and its absence momentum == 0."""
+    p = torch.randn(4099, generator=torch.Generator().manual_seed(85)).to("supa")
+    g = torch.randn(4099, generator=torch.Generator().manual_seed(86)).to("supa")
+    b = torch.randn(4099, generator=torch.Generator().manual_seed(87)).to("supa")
+    p0, b0 = p.clone(), b.clone()
+    one = torch.ones((), device="supa")
+    torch._fused_sgd_([p], [g], [b], weight_decay=0.0, momentum=0.9, lr=0.1, dampening=0.0, nesterov=False,
+                      maximize=False, is_first_step=False, found_inf=one)
+    assert torch.equal(p.cpu(), p0.cpu()) and torch.equal(b.cpu(), b0.cpu())
+    torch._fused_sgd_([p], [g], [b], weight_decay=0.0, momentum=0.9, lr=0.1, dampening=0.0, nesterov=False,
+                      maximize=False, is_first_step=False, found_inf=one * 0)
+    assert not torch.equal(p.cpu(), p0.cpu())
+    with pytest.raises(RuntimeError, match="momentum"):
+        torch._fused_sgd_([p], [g], [], weight_decay=0.0, momentum=0.9, lr=0.1, dampening=0.0, nesterov=False,
+                          maximize=False, is_first_step=False)
+    with pytest.raises(RuntimeError, match="momentum"):
+        torch._fused_sgd_([p], [g], [b], weight_decay=0.0, momentum=0.0, lr=0.1, dampening=0.0, nesterov=False,
+                          maximize=False, is_first_step=False)

@@ -21,7 +21,9 @@ dtypes, tolerances and comparisons (CPU result against the supa result):
   and in-place Scalar products (its mixed-dtype cases are in
   test_gpu_reference_shapes.py);
 * test_lerp.py, test_linalg_vector_norm.py (bf16 input, float32
-  accumulation), test_fused_adam_kernel.py;
+  accumulation), test_fused_adam_kernel.py, test_fused_sgd_kernel.py (one
+  step of SGD(fused=True) on a cross-entropy loss against the CPU's
+  unfused SGD);
 * test_amp.py: GradScaler.scale and load_state_dict, and its clipping
   scaling cases (a two-layer Linear model trained with and without
   GradScaler + clip_grad_norm_; the matrix products are outside this path
@@ -342,3 +344,28 @@ def test_grad_scaling_clipping(separate_unscale, supa):
     _scaling_case(_run_clipping(separate_unscale), unskipped=3, skipped=1, atol=1e-7 if separate_unscale else 1e-5)
     # only the Linear layers' matrix products left the device
     assert all("mm" in k for k in dict(torch.supa.fallback_counts())), torch.supa.fallback_counts()
+
+
+SGD_SHAPES = [(1, 1000), (512, 1024), (1023, 511), (1025, 513), (1028, 2135)]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("shape", SGD_SHAPES)
+def test_fused_sgd_on_cross_entropy(shape, dtype, no_fallback):
+    """test_fused_sgd_kernel.py: weights uniform in [-1, 1] used as the
+    logits of CrossEntropyLoss over random class targets; one step of
+    SGD(lr 0.1, fused=True) on the device against SGD(fused=False) on the
+    CPU, rtol 1e-3 / atol 1e-4."""
+    wc, ws = pair(shape, dtype, lo=-1, hi=1)
+    t = torch.empty(shape[0], dtype=torch.long).random_(shape[1], generator=torch.Generator().manual_seed(99))
+    ts = t.to(SUPA)
+    wc.requires_grad_(True)
+    ws.requires_grad_(True)
+    crit = torch.nn.CrossEntropyLoss()
+    oc = torch.optim.SGD([wc], lr=0.1, momentum=0, weight_decay=0, dampening=0, nesterov=False, fused=False)
+    os_ = torch.optim.SGD([ws], lr=0.1, momentum=0, weight_decay=0, dampening=0, nesterov=False, fused=True)
+    crit(wc, t).backward()
+    oc.step()
+    crit(ws, ts).backward()
+    os_.step()
+    ref_allclose(wc, ws, 1e-3, 1e-4)

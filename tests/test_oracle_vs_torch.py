@@ -766,3 +766,60 @@ def test_glu_against_cpu_and_closed_forms():
     assert np.array_equal(O.glu(a, zero + 100), a)
     # exp(100) overflows float32: sigmoid 1 / (1 + inf) = 0, the product a signed zero
     assert np.array_equal(O.glu(a, zero - 100), a * np.float32(0))
+
+
+def test_sgd_step_against_cpu_and_closed_forms():
+    """The _fused_sgd_ step (double hyper-parameters, one rounding per
+    expression) against upstream CPU's _fused_sgd_, which computes in float32
+    (lr and momentum rounded to float32 too): within a float32 rounding of the
+    operands' size, 2^-23 (|new| + |old value| + 1), over momentum / nesterov /
+    dampening / weight decay / maximize / grad_scale (an ulp count would
+    blow up where p - lr g cancels); and exactly the closed forms at lr =
+    momentum = 0.5
+    (products by 1/2 and the sums of two float32 values below are exact in
+    double, so each stored value is that sum rounded once)."""
+    rng = np.random.default_rng(70)
+    p0 = rng.standard_normal(4096).astype(np.float32)
+    g0 = rng.standard_normal(4096).astype(np.float32)
+    cfgs = [dict(momentum=0.0), dict(momentum=0.9), dict(momentum=0.9, nesterov=True),
+            dict(momentum=0.9, dampening=0.1, weight_decay=0.01), dict(momentum=0.0, weight_decay=0.05, maximize=True),
+            dict(momentum=0.9, nesterov=True, weight_decay=0.01, maximize=True, grad_scale=4.0)]
+    for cfg in cfgs:
+        cfg = dict(cfg)
+        gsc = cfg.pop("grad_scale", None)
+        mom = cfg["momentum"] != 0
+        p, g = p0.copy(), g0.copy()
+        b = np.zeros_like(p) if mom else None
+        tp, tg = torch.from_numpy(p0.copy()), torch.from_numpy(g0.copy())
+        tb = [torch.zeros(4096)] if mom else []
+        for step in range(3):
+            first = step == 0
+            p_prev, b_prev = p.copy(), (b.copy() if mom else None)
+            O.sgd_step(p, g, b, 0.01, first=first, grad_scale=gsc, **cfg)
+            torch._fused_sgd_([tp], [tg], tb, weight_decay=cfg.get("weight_decay", 0.0), momentum=cfg["momentum"],
+                              lr=0.01, dampening=cfg.get("dampening", 0.0), nesterov=cfg.get("nesterov", False),
+                              maximize=cfg.get("maximize", False), is_first_step=first,
+                              grad_scale=None if gsc is None else torch.tensor(gsc))
+            assert np.all(np.abs(p - tp.numpy()) <= 2.0 ** -23 * (np.abs(tp.numpy()) + np.abs(p_prev) + 1)), (cfg, step)
+            assert np.array_equal(g, tg.numpy())
+            if mom:
+                assert np.all(np.abs(b - tb[0].numpy()) <= 2.0 ** -23 * (np.abs(tb[0].numpy()) + np.abs(b_prev) + 1)), \
+                    (cfg, step)
+            p, b = tp.numpy().copy(), (tb[0].numpy().copy() if mom else None)  # realign on CPU's state
+    p, g = p0.copy(), g0.copy()
+    O.sgd_step(p, g, None, 0.5)
+    assert np.array_equal(p, (p0.astype(np.float64) - 0.5 * g0.astype(np.float64)).astype(np.float32))
+    p, g, b = p0.copy(), g0.copy(), np.zeros_like(p0)
+    O.sgd_step(p, g, b, 0.5, momentum=0.5, first=True)
+    assert np.array_equal(b, g0)
+    p1 = p.copy()
+    O.sgd_step(p, g, b, 0.5, momentum=0.5)
+    b2 = 0.5 * g0.astype(np.float64) + g0.astype(np.float64)
+    assert np.array_equal(b, b2.astype(np.float32))
+    # g takes the buffer rounded to float32 (g is float32), then p -= lr g
+    assert np.array_equal(p, (p1.astype(np.float64) - 0.5 * b2.astype(np.float32).astype(np.float64)).astype(np.float32))
+    p, g, b = p0.copy(), g0.copy(), g0.copy()
+    O.sgd_step(p, g, b, 0.5, momentum=0.5, nesterov=True)
+    bn = 0.5 * g0.astype(np.float64) + g0.astype(np.float64)
+    gn = (g0.astype(np.float64) + 0.5 * bn).astype(np.float32)
+    assert np.array_equal(p, (p0.astype(np.float64) - 0.5 * gn.astype(np.float64)).astype(np.float32))

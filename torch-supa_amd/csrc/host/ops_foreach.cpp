@@ -683,6 +683,77 @@ void fused_adamw_(at::TensorList params, at::TensorList grads, at::TensorList ex
                    beta2, weight_decay, eps, amsgrad, maximize, grad_scale, found_inf);
 }
 
+// ------------------------------------------------------------- fused SGD
+// upstream _fused_sgd_kernel_cuda_'s checks: a momentum buffer list exactly
+// when momentum > 0; one device and dtype, contiguous tensors.
+void fused_sgd_impl(at::TensorList params, at::TensorList grads, at::TensorList bufs, double weight_decay,
+                    double momentum, double lr, const at::Tensor& lr_tensor, double dampening, bool nesterov,
+                    bool maximize, bool is_first_step, const std::optional<at::Tensor>& grad_scale,
+                    const std::optional<at::Tensor>& found_inf) {
+  const size_t n = params.size();
+  TORCH_CHECK(grads.size() == n, "_fused_sgd_: params and grads must have the same length");
+  const bool mom = !bufs.empty();
+  if (mom) {
+    TORCH_CHECK(momentum > 0, "_fused_sgd_: expected momentum > 0 with a momentum buffer list, got ", momentum);
+    TORCH_CHECK(bufs.size() == n, "_fused_sgd_: momentum_buffer_list must match params");
+  } else {
+    TORCH_CHECK(momentum == 0, "_fused_sgd_: expected momentum == 0 without a momentum buffer list, got ",
+                momentum);
+    if (is_first_step) TORCH_WARN_ONCE("`is_first_step` argument has no effect when `momentum_buffer_list` is empty");
+  }
+  if (n == 0) return;
+  const auto dev = params[0].device();
+  const c10::ScalarType dt = params[0].scalar_type();
+  TORCH_CHECK(float_family(dt), "_fused_sgd_: unsupported dtype ", dt);
+  std::vector<void*> p(n), g(n), b(mom ? n : 0);
+  std::vector<int64_t> numel(n);
+  for (size_t i = 0; i < n; ++i) {
+    std::vector<const at::Tensor*> ts{&params[i], &grads[i]};
+    if (mom) ts.push_back(&bufs[i]);
+    for (const at::Tensor* t : ts) {
+      TORCH_CHECK(t->device() == dev && t->scalar_type() == dt && t->is_contiguous(),
+                  "_fused_sgd_: params, grads and momentum buffers must be contiguous ", dt, " tensors on ", dev);
+      TORCH_CHECK(t->numel() == params[i].numel(), "_fused_sgd_: tensor sizes differ at index ", i);
+    }
+    p[i] = params[i].data_ptr();
+    g[i] = grads[i].data_ptr();
+    if (mom) b[i] = bufs[i].data_ptr();
+    numel[i] = params[i].numel();
+  }
+  const float* lr_ptr = nullptr;
+  at::Tensor lr_f;
+  if (lr_tensor.defined()) {
+    if (lr_tensor.device().type() == kSupa) {
+      lr_f = lr_tensor.to(at::kFloat);
+      lr_ptr = lr_f.data_ptr<float>();
+    } else {
+      lr = lr_tensor.item<double>();
+    }
+  }
+  at::Tensor gs, fi;
+  if (grad_scale.has_value() && grad_scale->defined()) gs = grad_scale->to(dev).to(at::kFloat);
+  if (found_inf.has_value() && found_inf->defined()) fi = found_inf->to(dev).to(at::kFloat);
+  const int rc = supa_amd_fused_sgd((int32_t)n, p.data(), g.data(), mom ? b.data() : nullptr, numel.data(),
+                                    dtype_code(dt), weight_decay, momentum, lr, lr_ptr, dampening, nesterov ? 1 : 0,
+                                    maximize ? 1 : 0, is_first_step ? 1 : 0,
+                                    gs.defined() ? gs.data_ptr<float>() : nullptr,
+                                    fi.defined() ? fi.data_ptr<float>() : nullptr, current_stream(dev.index()));
+  check_status(rc, "_fused_sgd_");
+}
+void fused_sgd_(at::TensorList params, at::TensorList grads, at::TensorList bufs, double weight_decay,
+                double momentum, double lr, double dampening, bool nesterov, bool maximize, bool is_first_step,
+                const std::optional<at::Tensor>& grad_scale, const std::optional<at::Tensor>& found_inf) {
+  fused_sgd_impl(params, grads, bufs, weight_decay, momentum, lr, at::Tensor(), dampening, nesterov, maximize,
+                 is_first_step, grad_scale, found_inf);
+}
+void fused_sgd_tensor_lr_(at::TensorList params, at::TensorList grads, at::TensorList bufs, double weight_decay,
+                          double momentum, const at::Tensor& lr, double dampening, bool nesterov, bool maximize,
+                          bool is_first_step, const std::optional<at::Tensor>& grad_scale,
+                          const std::optional<at::Tensor>& found_inf) {
+  fused_sgd_impl(params, grads, bufs, weight_decay, momentum, 0.0, lr, dampening, nesterov, maximize, is_first_step,
+                 grad_scale, found_inf);
+}
+
 // _fused_adam_: the same kernel in Adam mode (weight decay on the gradient)
 void fused_adam_(at::TensorList params, at::TensorList grads, at::TensorList exp_avgs, at::TensorList exp_avg_sqs,
                  at::TensorList max_exp_avg_sqs, at::TensorList state_steps, double lr, double beta1, double beta2,
@@ -857,6 +928,8 @@ TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
   m.impl("_fused_adamw_.tensor_lr", TORCH_FN(fused_adamw_tensor_lr_));
   m.impl("_fused_adam_", TORCH_FN(fused_adam_));
   m.impl("_fused_adam_.tensor_lr", TORCH_FN(fused_adam_tensor_lr_));
+  m.impl("_fused_sgd_", TORCH_FN(fused_sgd_));
+  m.impl("_fused_sgd_.tensor_lr", TORCH_FN(fused_sgd_tensor_lr_));
   m.impl("_amp_foreach_non_finite_check_and_unscale_", TORCH_FN(amp_unscale_));
   m.impl("_amp_update_scale_", TORCH_FN(amp_update_scale_));
 }

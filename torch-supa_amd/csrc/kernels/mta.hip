@@ -143,6 +143,90 @@ k_adamw(AdamTable tab, AdamHyper h) {
     adamw_elem<T>(p[e], g[e], m[e], v[e], h.amsgrad ? vm + e : nullptr, h, lr, lr_wd, bc1, bc2_sqrt, step_size);
 }
 
+// ------------------------------------------------------------- fused SGD
+struct SgdTable {
+  void* p[kMtaTensors];
+  void* g[kMtaTensors];
+  void* b[kMtaTensors];
+  int64_t numel[kMtaTensors];
+  uint32_t chunk_start[kMtaTensors + 1];
+  int32_t ntensors;
+  uint32_t bucket_shift;
+  uint8_t bucket[kMtaBuckets];
+};
+
+struct SgdHyper {
+  double weight_decay, momentum, lr, dampening;
+  const float* lr_ptr;
+  const float* grad_scale;
+  const float* found_inf;
+  int nesterov, maximize, first;
+};
+
+// One element of upstream sgd_math (FusedSgdKernel.cu): the state in the
+// storage type's opmath, the hyper-parameters in double, so every mixed
+// expression is evaluated in double (a + b c contracted into one fma, as that
+// compiler does) and rounded once.  MOM: a momentum buffer (depth 3).
+//   g = g / grad_scale (stored back); -g if maximize; g += wd p;
+//   buf = first ? g : momentum buf + (1 - dampening) g;
+//   g = nesterov ? g + momentum buf : buf;  p -= lr g
+// The double buf feeds the nesterov step before it is rounded for storage.
+template <typename T, bool MOM>
+__device__ __forceinline__ void sgd_elem(T& pr, T& gr, T* br, const SgdHyper& h, double lr) {
+  using C = opmath_t<T>;
+  C p = (C)to_arith(pr);
+  C g = (C)to_arith(gr);
+  if (h.grad_scale) {
+    g = (C)((double)g / (double)(*h.grad_scale));
+    gr = from_arith<T>(g);
+  }
+  if (h.maximize) g = -g;
+  if (h.weight_decay != 0.0) g = (C)fma(h.weight_decay, (double)p, (double)g);
+  if constexpr (MOM) {
+    const double buf =
+        h.first ? (double)g : fma(h.momentum, (double)(C)to_arith(*br), (1.0 - h.dampening) * (double)g);
+    *br = from_arith<T>((C)buf);
+    g = h.nesterov ? (C)fma(h.momentum, buf, (double)g) : (C)buf;
+  }
+  p = (C)fma(-lr, (double)g, (double)p);
+  pr = from_arith<T>(p);
+}
+
+template <typename T, bool MOM, int64_t CHUNK>
+__global__ void __launch_bounds__(kMtaBlock)
+k_sgd(SgdTable tab, SgdHyper h) {
+  if (h.found_inf && *h.found_inf == 1.0f) return;
+  constexpr int V = 16 / sizeof(T);
+  const MtaRange r = mta_range<CHUNK>(tab);
+  const int k = r.k;
+  const int64_t lo = r.lo, hi = r.hi;
+  const double lr = h.lr_ptr ? (double)(*h.lr_ptr) : h.lr;
+  T* p = static_cast<T*>(tab.p[k]);
+  T* g = static_cast<T*>(tab.g[k]);
+  T* b = static_cast<T*>(tab.b[k]);
+  const bool vec = aligned(p, 16) && aligned(g, 16) && (!MOM || aligned(b, 16));
+  int64_t start = lo;
+  if (vec) {
+    const int64_t nv = (hi - lo) / V;
+    for (int64_t i = threadIdx.x; i < nv; i += kMtaBlock) {
+      const int64_t e = lo + i * V;
+      Vec<T, V> P = ld_stream(reinterpret_cast<const Vec<T, V>*>(p + e));
+      Vec<T, V> G = ld_stream(reinterpret_cast<const Vec<T, V>*>(g + e));
+      Vec<T, V> B;
+      if constexpr (MOM) {
+        if (!h.first) B = ld_stream(reinterpret_cast<const Vec<T, V>*>(b + e));
+      }
+#pragma unroll
+      for (int j = 0; j < V; ++j) sgd_elem<T, MOM>(P.v[j], G.v[j], &B.v[j], h, lr);
+      st_stream(reinterpret_cast<Vec<T, V>*>(p + e), P);
+      if (h.grad_scale) st_stream(reinterpret_cast<Vec<T, V>*>(g + e), G);
+      if constexpr (MOM) st_stream(reinterpret_cast<Vec<T, V>*>(b + e), B);
+    }
+    start = lo + nv * V;
+  }
+  for (int64_t e = start + threadIdx.x; e < hi; e += kMtaBlock) sgd_elem<T, MOM>(p[e], g[e], b + e, h, lr);
+}
+
 // ------------------------------------------------------------ AMP
 // In-place unscale of a gradient list with the non-finite check of upstream
 // _amp_foreach_non_finite_check_and_unscale_ (AmpKernels.cu): each element is
@@ -225,11 +309,46 @@ int launch_adamw(int32_t ntensors, void* const* params, void* const* grads, void
       [&](const AdamTable& tab, uint32_t chunks) { k_adamw<T, CHUNK, UNR><<<chunks, kMtaBlock, 0, st>>>(tab, h); });
 }
 
+template <typename T, bool MOM>
+int launch_sgd(int32_t ntensors, void* const* params, void* const* grads, void* const* bufs, const int64_t* numel,
+               const SgdHyper& h, hipStream_t st) {
+  constexpr int64_t CHUNK = chunk_one<T>();
+  return mta_for_tables<CHUNK, SgdTable>(
+      ntensors, numel,
+      [&](SgdTable& tab, int slot, int i) -> int {
+        if (MOM && !bufs[i]) return SUPA_AMD_EINVAL;
+        tab.p[slot] = params[i];
+        tab.g[slot] = grads[i];
+        tab.b[slot] = MOM ? bufs[i] : nullptr;
+        return SUPA_AMD_OK;
+      },
+      [&](const SgdTable& tab, uint32_t chunks) { k_sgd<T, MOM, CHUNK><<<chunks, kMtaBlock, 0, st>>>(tab, h); });
+}
+
 }  // namespace sa
 
 using namespace sa;
 
 extern "C" {
+
+int supa_amd_fused_sgd(int32_t ntensors, void* const* params, void* const* grads, void* const* momentum_buffers,
+                       const int64_t* numel, int32_t dtype, double weight_decay, double momentum, double lr,
+                       const float* lr_ptr, double dampening, int nesterov, int maximize, int is_first_step,
+                       const float* grad_scale, const float* found_inf, void* stream) {
+  if (ntensors < 0) return SUPA_AMD_EINVAL;
+  if (ntensors > 0 && (!params || !grads || !numel)) return SUPA_AMD_EINVAL;
+  const bool mom = momentum_buffers != nullptr;
+  // upstream: a momentum buffer list exactly when momentum > 0
+  if (mom ? !(momentum > 0.0) : momentum != 0.0) return SUPA_AMD_EINVAL;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const SgdHyper h{weight_decay, momentum, lr, dampening, lr_ptr, grad_scale, found_inf,
+                   nesterov ? 1 : 0, maximize ? 1 : 0, is_first_step ? 1 : 0};
+  return with_mta_storage(dtype, [&](auto* tag) -> int {
+    using T = std::remove_pointer_t<decltype(tag)>;
+    return mom ? launch_sgd<T, true>(ntensors, params, grads, momentum_buffers, numel, h, st)
+               : launch_sgd<T, false>(ntensors, params, grads, nullptr, numel, h, st);
+  });
+}
 
 int supa_amd_amp_unscale(int32_t ntensors, void* const* tensors, const int64_t* numel, int32_t dtype,
                          float* found_inf, const float* inv_scale, void* stream) {
