@@ -51,6 +51,7 @@ struct AllocatorStats {
   int64_t allocated = 0;
   int64_t reserved = 0;
   int64_t peak_allocated = 0;
+  int64_t peak_reserved = 0;
   int64_t num_allocs = 0;
   int64_t num_device_mallocs = 0;
   int64_t num_frees = 0;
@@ -60,6 +61,16 @@ struct AllocatorStats {
 AllocatorStats allocator_stats(c10::DeviceIndex d);
 void allocator_reset_peak(c10::DeviceIndex d);
 void allocator_empty_cache();
+// the cached pinned host blocks back to the driver
+void pinned_empty_cache();
+// caching_allocator_alloc / _delete: a raw block of the allocator for stream
+// st of device d (nullptr for 0 bytes), and its release.
+void* allocator_raw_alloc(size_t nbytes, c10::DeviceIndex d, hipStream_t st);
+void allocator_raw_delete(void* p);
+// set_ / get_per_process_memory_fraction: at most fraction x total memory
+// reserved on device d.
+void allocator_set_memory_fraction(double fraction, c10::DeviceIndex d);
+double allocator_get_memory_fraction(c10::DeviceIndex d);
 // record_stream: the block holding ptr is also used on stream s.
 void allocator_record_stream(void* ptr, const c10::Stream& s);
 // Test hook: the next n device allocations fail as out of memory.

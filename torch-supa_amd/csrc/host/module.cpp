@@ -24,8 +24,36 @@ py::dict memory_stats(int dev) {
   d["num_device_mallocs"] = s.num_device_mallocs;
   d["num_frees"] = s.num_frees;
   d["num_ooms_retried"] = s.num_ooms_retried;
+  d["peak_reserved_bytes"] = s.peak_reserved;
   d["pending_blocks"] = s.pending_blocks;
   return d;
+}
+
+// hipGetDeviceProperties, the fields torch.supa.get_device_properties shows.
+py::dict device_properties(int dev) {
+  hipDeviceProp_t p;
+  SUPA_HIP_CHECK(hipGetDeviceProperties(&p, dev));
+  py::dict d;
+  d["name"] = std::string(p.name);
+  d["total_memory"] = (int64_t)p.totalGlobalMem;
+  d["major"] = p.major;
+  d["minor"] = p.minor;
+  d["multi_processor_count"] = p.multiProcessorCount;
+  d["gcn_arch_name"] = std::string(p.gcnArchName);
+  d["l2_cache_size"] = (int64_t)p.l2CacheSize;
+  d["uuid"] = py::bytes(reinterpret_cast<const char*>(p.uuid.bytes), 16);
+  return d;
+}
+
+// (free, total) device memory in bytes, as hipMemGetInfo reports them.
+py::tuple mem_get_info(int dev) {
+  const auto prev = supa::current_device();
+  if (dev != prev) supa::set_device(static_cast<c10::DeviceIndex>(dev));
+  size_t free_b = 0, total_b = 0;
+  const hipError_t rc = hipMemGetInfo(&free_b, &total_b);
+  if (dev != prev) supa::set_device(prev);
+  SUPA_HIP_CHECK(rc);
+  return py::make_tuple((int64_t)free_b, (int64_t)total_b);
 }
 
 // Planner entry for tests: operands are dicts {sizes, strides, is_output,
@@ -156,6 +184,7 @@ PYBIND11_MODULE(_C, m) {
   m.def("memory_stats", &memory_stats);
   m.def("reset_peak_memory_stats", [](int d) { supa::allocator_reset_peak(static_cast<c10::DeviceIndex>(d)); });
   m.def("empty_cache", []() { supa::allocator_empty_cache(); });
+  m.def("empty_host_cache", []() { supa::pinned_empty_cache(); });
   m.def("set_cpu_fallback_enabled", &supa::set_cpu_fallback_enabled);
   m.def("cpu_fallback_enabled", &supa::cpu_fallback_enabled);
   m.def("set_fused_cross_entropy_enabled", &supa::set_fused_cross_entropy_enabled);
@@ -183,6 +212,18 @@ PYBIND11_MODULE(_C, m) {
     supa::allocator_record_stream(t.storage().data_ptr().get(), s);
   });
   m.def("inject_oom", [](int n) { supa::allocator_inject_oom(n); });
+  m.def("device_properties", &device_properties);
+  m.def("mem_get_info", &mem_get_info);
+  m.def("raw_alloc", [](size_t nbytes, int dev, uintptr_t stream) {
+    return reinterpret_cast<uintptr_t>(
+        supa::allocator_raw_alloc(nbytes, static_cast<c10::DeviceIndex>(dev), reinterpret_cast<hipStream_t>(stream)));
+  });
+  m.def("raw_delete", [](uintptr_t p) { supa::allocator_raw_delete(reinterpret_cast<void*>(p)); });
+  m.def("set_memory_fraction", [](double f, int dev) {
+    supa::allocator_set_memory_fraction(f, static_cast<c10::DeviceIndex>(dev));
+  });
+  m.def("get_memory_fraction",
+        [](int dev) { return supa::allocator_get_memory_fraction(static_cast<c10::DeviceIndex>(dev)); });
   m.def("event_synchronize", &event_synchronize);
   m.def("event_elapsed_ms", &event_elapsed_ms);
   m.def("event_destroy", &event_destroy);

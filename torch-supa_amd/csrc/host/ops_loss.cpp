@@ -165,6 +165,32 @@ at::Tensor& sum_mean_into(const at::Tensor& self, at::OptionalIntArrayRef dim, b
   return out;
 }
 
+// all() / any() over every element: the count of nonzero elements (NaN
+// counts, as upstream's truthiness) against numel / 0, by the device's compare
+// and integer sum; a uint8 input gives a uint8 result, as upstream.
+at::Tensor& all_any_into(const at::Tensor& self, bool any, at::Tensor& out, const char* name) {
+  const c10::ScalarType odt = self.scalar_type() == at::kByte ? at::kByte : at::kBool;
+  if (out.defined()) {
+    TORCH_CHECK(out.scalar_type() == odt, name, ": expected out dtype ", odt, " but got ", out.scalar_type());
+    at::native::resize_output(out, {});
+  } else {
+    out = empty_supa({}, odt, self.device().index());
+  }
+  at::Tensor cnt = at::ne(self, 0).sum();
+  out.copy_(any ? at::gt(cnt, 0) : at::eq(cnt, self.numel()));
+  return out;
+}
+at::Tensor all_all(const at::Tensor& self) {
+  at::Tensor out;
+  return all_any_into(self, false, out, "all");
+}
+at::Tensor& all_all_out(const at::Tensor& self, at::Tensor& out) { return all_any_into(self, false, out, "all.all_out"); }
+at::Tensor any_all(const at::Tensor& self) {
+  at::Tensor out;
+  return all_any_into(self, true, out, "any");
+}
+at::Tensor& any_all_out(const at::Tensor& self, at::Tensor& out) { return all_any_into(self, true, out, "any.all_out"); }
+
 at::Tensor sum_dim(const at::Tensor& self, at::OptionalIntArrayRef dim, bool keepdim,
                    std::optional<c10::ScalarType> dtype) {
   at::Tensor out;
@@ -858,6 +884,10 @@ at::Tensor cross_entropy_loss(const at::Tensor& self, const at::Tensor& target,
 TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
   using namespace supa;
   m.impl("sum.dim_IntList", TORCH_FN(sum_dim));
+  m.impl("all", TORCH_FN(all_all));
+  m.impl("all.all_out", TORCH_FN(all_all_out));
+  m.impl("any", TORCH_FN(any_all));
+  m.impl("any.all_out", TORCH_FN(any_all_out));
   m.impl("sum.IntList_out", TORCH_FN(sum_out));
   m.impl("mean.dim", TORCH_FN(mean_dim));
   m.impl("mean.out", TORCH_FN(mean_out));

@@ -74,6 +74,21 @@ at::Tensor& bernoulli_float_(at::Tensor& self, double p, std::optional<at::Gener
   return self;
 }
 
+// bernoulli_(p_tensor) (upstream bernoulli_tensor_cuda_kernel: 1 where a
+// uniform draw in [0, 1) is below p): the draws come from the device's
+// Philox stream through uniform_, the comparison and the cast are device
+// kernels too.
+at::Tensor& bernoulli_tensor_(at::Tensor& self, const at::Tensor& p, std::optional<at::Generator> gen) {
+  TORCH_CHECK(rng_dtype(self.scalar_type()) || self.scalar_type() == at::kBool ||
+                  at::isIntegralType(self.scalar_type(), false),
+              "bernoulli_: unsupported dtype ", self.scalar_type());
+  if (self.numel() == 0) return self;
+  at::Tensor u = at::empty(self.sizes(), self.options().dtype(at::kFloat));
+  u.uniform_(0.0, 1.0, gen);
+  self.copy_(at::lt(u, p.to(self.device())));
+  return self;
+}
+
 // upstream native_dropout_cuda: train == false -> (clone, ones); p == 1 ->
 // zeros; otherwise keep with probability 1 - p and scale by 1 / (1 - p).
 std::tuple<at::Tensor, at::Tensor> native_dropout(const at::Tensor& input, double p, std::optional<bool> train) {
@@ -111,6 +126,7 @@ TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
   m.impl("uniform_", TORCH_FN(uniform_));
   m.impl("normal_", TORCH_FN(normal_));
   m.impl("bernoulli_.float", TORCH_FN(bernoulli_float_));
+  m.impl("bernoulli_.Tensor", TORCH_FN(bernoulli_tensor_));
   m.impl("native_dropout", TORCH_FN(native_dropout));
   m.impl("native_dropout_backward", TORCH_FN(native_dropout_backward));
 }

@@ -39,6 +39,8 @@
 #include <algorithm>
 #include <atomic>
 #include <cstdlib>
+#include <cstring>
+#include <sstream>
 #include <map>
 #include <mutex>
 #include <unordered_map>
@@ -276,13 +278,36 @@ struct Pending {
   std::vector<hipEvent_t> events;
 };
 
+// upstream's format_size (the reference's OOM message uses it): bytes up to
+// 1 KiB, then KiB / MiB / GiB with two decimals.
+std::string format_size(uint64_t size) {
+  std::ostringstream os;
+  os.precision(2);
+  os << std::fixed;
+  if (size <= 1024) os << size << " bytes";
+  else if (size <= 1048576) os << (double)size / 1024.0 << " KiB";
+  else if (size <= 1073741824ULL) os << (double)size / 1048576.0 << " MiB";
+  else os << (double)size / 1073741824.0 << " GiB";
+  return os.str();
+}
+
 class CachingAllocator final : public c10::Allocator {
  public:
   c10::DataPtr allocate(size_t nbytes) override {
     const int dev = current_device();
-    if (nbytes == 0) return {nullptr, nullptr, &CachingAllocator::raw_delete, c10::Device(kSupa, dev)};
+    void* p = allocate_on(dev, current_stream(dev), nbytes);
+    return {p, p, &CachingAllocator::raw_delete, c10::Device(kSupa, dev)};
+  }
+
+  // A block of nbytes for stream st of device dev (the current device);
+  // nullptr for 0 bytes.  The reference refuses 1 EiB and more before
+  // anything else (SUPACachingAllocator.cpp:3261-3263).
+  void* allocate_on(int dev, hipStream_t st, size_t nbytes) {
+    constexpr size_t kOneExaByte = size_t(1) << 60;
+    TORCH_CHECK_WITH(OutOfMemoryError, nbytes < kOneExaByte,
+                     "SUPA out of memory. Tried to allocate more than 1EB memory.");
+    if (nbytes == 0) return nullptr;
     const size_t sz = round_size(nbytes);
-    const hipStream_t st = current_stream(dev);
     void* p = nullptr;
     if (!uncached_) {
       std::lock_guard<std::mutex> g(mu_);
@@ -290,7 +315,22 @@ class CachingAllocator final : public c10::Allocator {
       p = take_cached_locked(dev, st, sz);
     }
     if (!p) p = device_malloc(dev, st, sz);
-    return {p, p, &CachingAllocator::raw_delete, c10::Device(kSupa, dev)};
+    return p;
+  }
+
+  // set_per_process_memory_fraction: the allocator reserves at most
+  // fraction x the device's total memory; a request beyond it releases the
+  // cache and then fails as out of memory.
+  void set_fraction(int dev, double fraction) {
+    size_t free_b = 0, total_b = 0;
+    SUPA_HIP_CHECK(hipMemGetInfo(&free_b, &total_b));
+    std::lock_guard<std::mutex> g(mu_);
+    fraction_[dev] = fraction;
+    limit_[dev] = (size_t)(fraction * (double)total_b);
+  }
+  double get_fraction(int dev) {
+    std::lock_guard<std::mutex> g(mu_);
+    return fraction_[dev];
   }
 
   c10::DeleterFnPtr raw_deleter() const override { return &CachingAllocator::raw_delete; }
@@ -379,6 +419,7 @@ class CachingAllocator final : public c10::Allocator {
   void reset_peak(int dev) {
     std::lock_guard<std::mutex> g(mu_);
     stats_[dev].peak_allocated = stats_[dev].allocated;
+    stats_[dev].peak_reserved = stats_[dev].reserved;
   }
   // Test hook: the next `n` device allocations fail as if hipMalloc returned
   // hipErrorOutOfMemory (before and after the cache is released).
@@ -448,6 +489,7 @@ class CachingAllocator final : public c10::Allocator {
     s.num_allocs += 1;
     if (fresh) {
       s.reserved += (int64_t)bsz;
+      s.peak_reserved = std::max(s.peak_reserved, s.reserved);
       s.num_device_mallocs += 1;
     }
   }
@@ -469,20 +511,30 @@ class CachingAllocator final : public c10::Allocator {
     (void)hipSetDevice(prev);
   }
 
-  hipError_t try_malloc(void** p, size_t sz) {
+  // hipMalloc, unless a test hook fails it, the request cannot fit the
+  // device at all (no driver call for it), or it would take the reserved
+  // bytes past the memory-fraction limit.
+  hipError_t try_malloc(int dev, void** p, size_t sz, size_t total) {
     {
       std::lock_guard<std::mutex> g(mu_);
       if (inject_oom_ > 0) {
         --inject_oom_;
         return hipErrorOutOfMemory;
       }
+      if (sz > total) return hipErrorOutOfMemory;
+      if (limit_[dev] != SIZE_MAX && (size_t)stats_[dev].reserved + sz > limit_[dev]) return hipErrorOutOfMemory;
     }
     return hipMalloc(p, sz);
   }
 
   void* device_malloc(int dev, hipStream_t st, size_t sz) {
     void* p = nullptr;
-    hipError_t e = try_malloc(&p, sz);
+    size_t free_b = 0, total_b = 0;
+    if (hipMemGetInfo(&free_b, &total_b) != hipSuccess) {
+      (void)hipGetLastError();
+      total_b = SIZE_MAX;
+    }
+    hipError_t e = try_malloc(dev, &p, sz, total_b);
     if (e != hipSuccess) {
       (void)hipGetLastError();
       {
@@ -491,17 +543,25 @@ class CachingAllocator final : public c10::Allocator {
         release_cached_locked(dev);
         stats_[dev].num_ooms_retried += 1;
       }
-      e = try_malloc(&p, sz);
+      e = try_malloc(dev, &p, sz, total_b);
     }
     if (e != hipSuccess) {
       (void)hipGetLastError();
-      size_t free_b = 0, total_b = 0;
       (void)hipMemGetInfo(&free_b, &total_b);
       (void)hipGetLastError();
       AllocatorStats s = stats(dev);
-      TORCH_CHECK_WITH(OutOfMemoryError, false, "supa out of memory: tried to allocate ", sz, " bytes on device ",
-                       dev, " (", free_b, " of ", total_b, " bytes free; ", s.allocated,
-                       " allocated and ", s.reserved, " reserved by the caching allocator)");
+      std::string allowed;
+      {
+        std::lock_guard<std::mutex> g(mu_);
+        if (limit_[dev] != SIZE_MAX) allowed = format_size(limit_[dev]) + " allowed; ";
+      }
+      // the reference's message (SUPACachingAllocator.cpp:1080-1101), so that
+      // code matching on it keeps working
+      TORCH_CHECK_WITH(OutOfMemoryError, false, "SUPA out of memory. Tried to allocate ", format_size(sz), ". GPU ",
+                       dev, " has a total capacity of ", format_size(total_b), " of which ", format_size(free_b),
+                       " is free. ", allowed, "Of the allocated memory ", format_size(s.allocated),
+                       " is allocated by PyTorch, and ", format_size(s.reserved - s.allocated),
+                       " is reserved by PyTorch but unallocated.");
     }
     std::lock_guard<std::mutex> g(mu_);
     live_[p] = Block{p, sz, dev, st, {}};
@@ -519,7 +579,83 @@ class CachingAllocator final : public c10::Allocator {
   std::vector<hipEvent_t> events_[kMaxDevices];
   std::unordered_map<void*, Block> live_;
   AllocatorStats stats_[kMaxDevices];
+  double fraction_[kMaxDevices] = {};
+  size_t limit_[kMaxDevices] = {};
   int inject_oom_ = 0;
+
+ public:
+  CachingAllocator() {
+    for (int d = 0; d < kMaxDevices; ++d) {
+      fraction_[d] = 1.0;
+      limit_[d] = SIZE_MAX;
+    }
+  }
+};
+
+// Pinned host memory (pin_memory(), pin_memory=True, the accelerator's host
+// allocator): hipHostMalloc blocks in power-of-two size classes from 4 KiB,
+// cached on free and returned to the driver only by empty_host_cache.  Copies
+// between the host and a supa device are synchronous in this build, so a
+// freed block can be reused at once.
+class PinnedAllocator final : public c10::Allocator {
+ public:
+  c10::DataPtr allocate(size_t nbytes) override {
+    if (nbytes == 0) return {nullptr, nullptr, &PinnedAllocator::raw_delete, c10::Device(c10::DeviceType::CPU)};
+    size_t sz = 4096;
+    while (sz < nbytes) sz <<= 1;
+    void* p = nullptr;
+    {
+      std::lock_guard<std::mutex> g(mu_);
+      auto it = free_.find(sz);
+      if (it != free_.end()) {
+        p = it->second;
+        free_.erase(it);
+      }
+    }
+    if (!p) {
+      hipError_t e = hipHostMalloc(&p, sz, hipHostMallocDefault);
+      if (e != hipSuccess) {
+        (void)hipGetLastError();
+        empty_cache();
+        e = hipHostMalloc(&p, sz, hipHostMallocDefault);
+      }
+      if (e != hipSuccess) {
+        (void)hipGetLastError();
+        TORCH_CHECK_WITH(OutOfMemoryError, false, "SUPA out of memory. Tried to allocate ", format_size(sz),
+                         " of pinned host memory.");
+      }
+    }
+    std::lock_guard<std::mutex> g(mu_);
+    live_[p] = sz;
+    return {p, p, &PinnedAllocator::raw_delete, c10::Device(c10::DeviceType::CPU)};
+  }
+  c10::DeleterFnPtr raw_deleter() const override { return &PinnedAllocator::raw_delete; }
+  void copy_data(void* dest, const void* src, std::size_t count) const override { std::memcpy(dest, src, count); }
+
+  static void raw_delete(void* p) {
+    if (!p) return;
+    PinnedAllocator& a = instance();
+    std::lock_guard<std::mutex> g(a.mu_);
+    auto it = a.live_.find(p);
+    if (it == a.live_.end()) return;
+    a.free_.emplace(it->second, p);
+    a.live_.erase(it);
+  }
+  void empty_cache() {
+    std::lock_guard<std::mutex> g(mu_);
+    for (auto& kv : free_) (void)hipHostFree(kv.second);
+    (void)hipGetLastError();
+    free_.clear();
+  }
+  static PinnedAllocator& instance() {
+    static PinnedAllocator* a = new PinnedAllocator();  // never destroyed: frees can arrive at exit
+    return *a;
+  }
+
+ private:
+  std::mutex mu_;
+  std::multimap<size_t, void*> free_;
+  std::unordered_map<void*, size_t> live_;
 };
 
 CachingAllocator& CachingAllocator::instance() {
@@ -542,6 +678,22 @@ void allocator_record_stream(void* ptr, const c10::Stream& s) {
 void allocator_inject_oom(int n) { CachingAllocator::instance().inject_oom(n); }
 void allocator_reset_peak(c10::DeviceIndex d) { CachingAllocator::instance().reset_peak(d); }
 void allocator_empty_cache() { CachingAllocator::instance().empty_cache(); }
+void pinned_empty_cache() { PinnedAllocator::instance().empty_cache(); }
+void* allocator_raw_alloc(size_t nbytes, c10::DeviceIndex d, hipStream_t st) {
+  const auto prev = current_device();
+  if (d != prev) set_device(d);
+  void* p = CachingAllocator::instance().allocate_on(d, st, nbytes);
+  if (d != prev) set_device(prev);
+  return p;
+}
+void allocator_raw_delete(void* p) { CachingAllocator::raw_delete(p); }
+void allocator_set_memory_fraction(double fraction, c10::DeviceIndex d) {
+  const auto prev = current_device();
+  if (d != prev) set_device(d);
+  CachingAllocator::instance().set_fraction(d, fraction);
+  if (d != prev) set_device(prev);
+}
+double allocator_get_memory_fraction(c10::DeviceIndex d) { return CachingAllocator::instance().get_fraction(d); }
 
 at::Tensor empty_strided_supa(c10::IntArrayRef size, c10::IntArrayRef stride, c10::ScalarType dtype,
                               c10::DeviceIndex device) {
@@ -673,8 +825,18 @@ struct SupaHooks final : public at::PrivateUse1HooksInterface {
     return default_generator(device_index);
   }
   at::Generator getNewGenerator(c10::DeviceIndex device_index) const override { return new_generator(device_index); }
-  bool isPinnedPtr(const void* /*data*/) const override { return false; }
-  at::Allocator* getPinnedMemoryAllocator() const override { return at::getCPUAllocator(); }
+  // any address inside page-locked host memory (an interior pointer of a
+  // pinned block too), as the HIP runtime reports it
+  bool isPinnedPtr(const void* data) const override {
+    if (!data) return false;
+    hipPointerAttribute_t attr;
+    if (hipPointerGetAttributes(&attr, data) != hipSuccess) {
+      (void)hipGetLastError();
+      return false;
+    }
+    return attr.type == hipMemoryTypeHost;
+  }
+  at::Allocator* getPinnedMemoryAllocator() const override { return &PinnedAllocator::instance(); }
   void resizePrivateUse1Bytes(const c10::Storage& storage, size_t newsize) const override {
     // grow or shrink by reallocating and copying the overlap
     c10::StorageImpl* impl = storage.unsafeGetStorageImpl();

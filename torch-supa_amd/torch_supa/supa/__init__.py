@@ -85,6 +85,100 @@ def empty_cache() -> None:
     _C.empty_cache()
 
 
+def max_memory_reserved(device=None) -> int:
+    return memory_stats(device)["peak_reserved_bytes"]
+
+
+def mem_get_info(device=None):
+    """(free, total) device memory in bytes."""
+    return _C.mem_get_info(_index(device) if device is not None else _C.current_device())
+
+
+# The reference's allocator API (torch_supa/supa/memory.py:79-180): raw blocks
+# of the caching allocator for other frameworks, and a per-process cap on the
+# memory it reserves.
+def caching_allocator_alloc(size, device=None, stream=None) -> int:
+    """A block of `size` bytes from the caching allocator for `stream` (a
+    torch.supa.Stream or a hipStream_t as an int; the device's current stream
+    by default); returns its address.  Release it with
+    caching_allocator_delete."""
+    idx = _index(device) if device is not None else _C.current_device()
+    if stream is None:
+        stream = current_stream(idx)
+    if isinstance(stream, Stream):
+        stream = stream.hip_stream
+    if not isinstance(stream, int):
+        raise TypeError("Invalid type for stream argument, must be `torch.supa.Stream` or `int` representing a "
+                        "pointer to a existing stream")
+    return _C.raw_alloc(int(size), idx, stream)
+
+
+def caching_allocator_delete(mem_ptr: int) -> None:
+    _C.raw_delete(int(mem_ptr))
+
+
+def set_per_process_memory_fraction(fraction, device=None) -> None:
+    """Cap the memory the caching allocator reserves on `device` at
+    fraction x its total memory; a request beyond the cap (after releasing
+    the cache) raises an out-of-memory error."""
+    idx = _index(device) if device is not None else _C.current_device()
+    if not isinstance(fraction, float):
+        raise TypeError("Invalid type for fraction argument, must be `float`")
+    if fraction < 0 or fraction > 1:
+        raise ValueError(f"Invalid fraction value: {fraction}. Allowed range: 0~1")
+    _C.set_memory_fraction(fraction, idx)
+
+
+def get_per_process_memory_fraction(device=None) -> float:
+    return _C.get_memory_fraction(_index(device) if device is not None else _C.current_device())
+
+
+class _UUID:
+    """A device UUID: 16 bytes, printed as 8-4-4-4-12 hex digits."""
+
+    def __init__(self, raw: bytes):
+        self.bytes = bytes(raw)
+
+    def __str__(self):
+        h = self.bytes.hex()
+        return f"{h[:8]}-{h[8:12]}-{h[12:16]}-{h[16:20]}-{h[20:]}"
+
+    __repr__ = __str__
+
+
+class _DeviceProperties:
+    """hipGetDeviceProperties' fields: name, total_memory, major, minor,
+    multi_processor_count, gcnArchName, L2_cache_size, uuid."""
+
+    def __init__(self, d: dict):
+        self.name = d["name"]
+        self.total_memory = d["total_memory"]
+        self.major = d["major"]
+        self.minor = d["minor"]
+        self.multi_processor_count = d["multi_processor_count"]
+        self.gcnArchName = d["gcn_arch_name"]
+        self.L2_cache_size = d["l2_cache_size"]
+        self.uuid = _UUID(d["uuid"])
+
+    def __repr__(self):
+        return (f"_SupaDeviceProperties(name='{self.name}', major={self.major}, minor={self.minor}, "
+                f"gcnArchName='{self.gcnArchName}', total_memory={self.total_memory // (1 << 20)}MB, "
+                f"multi_processor_count={self.multi_processor_count}, uuid={self.uuid})")
+
+
+def get_device_properties(device=None) -> _DeviceProperties:
+    return _DeviceProperties(_C.device_properties(_index(device) if device is not None else _C.current_device()))
+
+
+def get_device_name(device=None) -> str:
+    return get_device_properties(device).name
+
+
+def get_device_capability(device=None):
+    p = get_device_properties(device)
+    return p.major, p.minor
+
+
 # Each supa device has a default Philox generator (seed + call offset) that
 # the native random ops (uniform_, bernoulli_, dropout) draw from.
 # torch.manual_seed reaches manual_seed_all through the PrivateUse1 module
