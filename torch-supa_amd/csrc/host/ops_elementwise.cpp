@@ -259,6 +259,33 @@ at::Tensor copy_from(const at::Tensor& self, const at::Tensor& dst, bool /*non_b
   return dst;
 }
 
+// equal (upstream cuda_equal): same shape, then every element equal (so a
+// NaN makes it false) by the device's compare and all(); an alias of itself
+// with the same view is equal without a launch.
+bool equal(const at::Tensor& self, const at::Tensor& other) {
+  TORCH_CHECK(self.device() == other.device(), "Cannot compare two tensors on different devices. Got: ",
+              self.device(), " and ", other.device());
+  if (self.sizes() != other.sizes()) return false;
+  if (self.numel() == 0) return true;
+  if (self.is_alias_of(other) && self.storage_offset() == other.storage_offset() && self.dtype() == other.dtype() &&
+      self.strides() == other.strides() && self.is_neg() == other.is_neg() && self.is_conj() == other.is_conj())
+    return true;
+  return at::eq(self, other).all().item<bool>();
+}
+
+// eye.out / eye.m_out (upstream eye_out_cuda): zeros, then ones on the
+// diagonal through a strided view of it.
+at::Tensor& eye_m_out(int64_t n, int64_t m, at::Tensor& out) {
+  TORCH_CHECK(n >= 0, "n must be greater or equal to 0, got ", n);
+  TORCH_CHECK(m >= 0, "m must be greater or equal to 0, got ", m);
+  at::native::resize_output(out, {n, m});
+  out.zero_();
+  const int64_t sz = std::min<int64_t>(n, m);
+  if (sz > 0) out.as_strided({sz}, {out.stride(0) + out.stride(1)}).fill_(1);
+  return out;
+}
+at::Tensor& eye_out(int64_t n, at::Tensor& out) { return eye_m_out(n, n, out); }
+
 at::Tensor copy_from_and_resize(const at::Tensor& self, const at::Tensor& dst) {
   if (dst.sizes() != self.sizes()) {
     if (dst.device().type() == kSupa) resize_(dst, self.sizes(), std::nullopt);
@@ -267,8 +294,10 @@ at::Tensor copy_from_and_resize(const at::Tensor& self, const at::Tensor& dst) {
   return copy_from(self, dst, false);
 }
 
+// upstream _local_scalar_dense reads the element at the data pointer with no
+// size check (item() checks numel before it calls this)
 c10::Scalar local_scalar_dense(const at::Tensor& self) {
-  TORCH_CHECK(self.numel() == 1, "a Tensor with ", self.numel(), " elements cannot be converted to Scalar");
+  TORCH_CHECK(self.numel() > 0, "_local_scalar_dense: the tensor has no elements");
   at::Tensor h = at::empty({}, self.options().device(at::kCPU));
   memcpy_d2h(h.data_ptr(), self.data_ptr(), self.dtype().itemsize(), self.device().index());
   check_device_errors(self.device().index());
@@ -1232,6 +1261,9 @@ TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
   m.impl("_copy_from", TORCH_FN(copy_from));
   m.impl("_copy_from_and_resize", TORCH_FN(copy_from_and_resize));
   m.impl("_local_scalar_dense", TORCH_FN(local_scalar_dense));
+  m.impl("equal", TORCH_FN(equal));
+  m.impl("eye.out", TORCH_FN(eye_out));
+  m.impl("eye.m_out", TORCH_FN(eye_m_out));
   m.impl("fill_.Scalar", TORCH_FN(fill_scalar));
   m.impl("fill_.Tensor", TORCH_FN(fill_tensor));
   m.impl("zero_", TORCH_FN(zero_));
