@@ -203,6 +203,10 @@ int supa_amd_pow(const supa_amd_ew_desc* d, void* stream);
  * xlogy.OutTensor NF:3673, xlogy.OutScalar_Self NF:3683,
  * xlogy.OutScalar_Other NF:3690 (upstream xlogy_kernel_cuda). */
 int supa_amd_xlogy(const supa_amd_ew_desc* d, void* stream);
+/* out = x * log1p(y), 0 where x == 0, NaN where y is NaN; as supa_amd_xlogy.
+ * Replaces special_xlog1py.out NF:13652, .self_scalar_out NF:13662 and
+ * .other_scalar_out NF:13670 (upstream xlog1py_kernel_cuda). */
+int supa_amd_xlog1py(const supa_amd_ew_desc* d, void* stream);
 
 /* grad_in = f'(...) * dy.  op = {grad_in, dy, x} where x is the forward input
  * for GELU, GELU_TANH, SILU and the forward output for SIGMOID, TANH.

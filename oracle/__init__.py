@@ -463,6 +463,15 @@ def sgd_step(p, g, buf, lr, momentum=0.0, dampening=0.0, weight_decay=0.0, neste
                       _p(gs, _f32p))
 
 
+def xlog1py(x, y, dtype="f32") -> np.ndarray:
+    """xlog1py_kernel_cuda: NaN for a NaN y, 0 for x == 0, else x log1p(y)
+    with the oracle's log1p, in float32."""
+    x, y = np.broadcast_arrays(np.asarray(x, np.float32), np.asarray(y, np.float32))
+    with np.errstate(invalid="ignore"):
+        r = np.where(np.isnan(y), y, np.where(x == 0, np.float32(0), x * unary(LOG1P, y)))
+    return _store(r.astype(np.float32), dtype)
+
+
 def _store(v, dtype: str) -> np.ndarray:
     """A float32 result stored in dtype ("f32", "bf16", "f16"), as float32."""
     v = np.asarray(v, np.float32)

@@ -154,3 +154,24 @@ def test_loss_16bit_bit_exact(name, dtype, beta, no_fallback):
         y.backward(gr.to("supa") if red == "none" else None)
         want = O.loss_backward_16(name, gf if red == "none" else 1.0, xf, tf, tname, red, beta)
         assert np.array_equal(dx.grad.cpu().float().numpy(), want), red
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_xlog1py(dtype, no_fallback):
+    """special.xlog1py (Tensor, Tensor / Scalar forms, out=) against the
+    oracle bit for bit, its special cases included."""
+    name = {torch.float32: "f32", torch.bfloat16: "bf16", torch.float16: "f16"}[dtype]
+    x = seeded((333, 65), 103).to(dtype)
+    y = (seeded((333, 65), 104).abs() * 3 - 0.9).to(dtype)
+    x.view(-1)[:4] = torch.tensor([0.0, 0.0, 2.0, 1.5]).to(dtype)
+    y.view(-1)[:4] = torch.tensor([-1.0, float("nan"), float("nan"), -1.0]).to(dtype)
+    xf, yf = x.float().numpy(), y.float().numpy()
+    got = torch.special.xlog1py(x.to("supa"), y.to("supa")).cpu().float().numpy()
+    assert np.array_equal(got, O.xlog1py(xf, yf, name), equal_nan=True)
+    got = torch.special.xlog1py(x.to("supa"), 0.5).cpu().float().numpy()
+    assert np.array_equal(got, O.xlog1py(xf, np.float32(0.5), name), equal_nan=True)
+    got = torch.special.xlog1py(2.0, y.to("supa")).cpu().float().numpy()
+    assert np.array_equal(got, O.xlog1py(np.float32(2.0), yf, name), equal_nan=True)
+    out = torch.empty(0, dtype=dtype, device="supa")
+    torch.special.xlog1py(x.to("supa"), y.to("supa"), out=out)
+    assert np.array_equal(out.cpu().float().numpy(), O.xlog1py(xf, yf, name), equal_nan=True)

@@ -11,8 +11,8 @@ result):
 * test_binary_misc_ops_kernels.py: the SmoothL1Loss (CPU in float64), HuberLoss
   (CPU in the dtype) and MSELoss (CPU in float32) gradients over its shapes,
   reductions and dtypes, and its six binary_cross_entropy_with_logits cases
-  (weight, pos_weight, a (3, 1) pos_weight broadcast over (2, 3, 4)).  Its
-  xlogy / xlog1py cases are not on this path and are not mirrored;
+  (weight, pos_weight, a (3, 1) pos_weight broadcast over (2, 3, 4)), and
+  its xlogy / xlog1py cases (N(0, 1) operands, NaN where the log is);
 * test_nllloss2d.py: nll_loss forward and backward, and the weighted
   backward, over its br200 params in every dtype, with its
   accumulation-count tolerance.
@@ -275,6 +275,16 @@ def test_bce_with_logits(shape, dtype, reduction, with_weight, with_pos_weight, 
                                            pos_weight=None if pw is None else pw.float(), reduction=reduction)
     y_s = F.binary_cross_entropy_with_logits(x_s, t_s, weight=w_s, pos_weight=pw_s, reduction=reduction)
     ref_allclose(y.to(y_s.dtype), y_s, RTOL[dtype], ATOL[dtype])
+
+
+@pytest.mark.parametrize("fn", [torch.xlogy, torch.special.xlog1py], ids=["xlogy", "xlog1py"])
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("shape", MISC_SHAPES)
+def test_misc_xlogy_xlog1py(shape, dtype, fn, no_fallback):
+    """test_binary_misc_ops_kernels.py:248-268."""
+    a, a_s = pair(shape, dtype)
+    b, b_s = pair(shape, dtype)
+    ref_allclose(fn(a, b), fn(a_s, b_s), RTOL[dtype], ATOL[dtype], equal_nan=True)
 
 
 # ------------------------------------------------------- test_nllloss2d.py

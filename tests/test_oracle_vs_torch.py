@@ -823,3 +823,19 @@ def test_sgd_step_against_cpu_and_closed_forms():
     bn = 0.5 * g0.astype(np.float64) + g0.astype(np.float64)
     gn = (g0.astype(np.float64) + 0.5 * bn).astype(np.float32)
     assert np.array_equal(p, (p0.astype(np.float64) - 0.5 * gn.astype(np.float64)).astype(np.float32))
+
+
+def test_xlog1py_against_cpu():
+    """xlog1py: 0 where x == 0 (even for y = -1, where log1p is -inf), NaN
+    where y is NaN (even for x == 0), x log1p(y) otherwise within 4 float32
+    ulps of upstream CPU (both log1p's within 2 ulps of exact)."""
+    x = randn((4096,), 71)
+    y = randn((4096,), 72).abs() * 3 - 0.9
+    x[:4] = torch.tensor([0.0, 0.0, 2.0, 1.5])
+    y[:4] = torch.tensor([-1.0, float("nan"), float("nan"), -1.0])
+    got = O.xlog1py(x.numpy(), y.numpy())
+    want = torch.special.xlog1py(x, y).numpy()
+    assert got[0] == 0.0 and np.isnan(got[1]) and np.isnan(got[2]) and got[3] == -np.inf
+    m = np.isfinite(want)
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    assert f32_ulp_dist(got[m], want[m]).max() <= 4

@@ -287,6 +287,35 @@ at::Tensor xlogy_into(const EwIn& x, const EwIn& y, c10::ScalarType common, at::
   const EwLaunch fn = [](const supa_amd_ew_desc* d, void* s) { return supa_amd_xlogy(d, s); };
   return apply({x, y}, common, common, out, inplace, fn, name);
 }
+// special_xlog1py: x * log1p(y) with the same special cases and promotion
+at::Tensor xlog1py_into(const EwIn& x, const EwIn& y, c10::ScalarType common, at::Tensor out, const char* name) {
+  if (at::isIntegralType(common, true)) common = default_float_dtype();
+  TORCH_CHECK(at::isFloatingType(common), name, ": not implemented for '", common, "'");
+  const EwLaunch fn = [](const supa_amd_ew_desc* d, void* s) { return supa_amd_xlog1py(d, s); };
+  return apply({x, y}, common, common, out, false, fn, name);
+}
+at::Tensor xlog1py_t(const at::Tensor& s, const at::Tensor& o) {
+  return xlog1py_into(EwIn::of(s), EwIn::of(o), at::result_type(s, o), {}, "special_xlog1py");
+}
+at::Tensor& xlog1py_t_out(const at::Tensor& s, const at::Tensor& o, at::Tensor& out) {
+  xlog1py_into(EwIn::of(s), EwIn::of(o), at::result_type(s, o), out, "special_xlog1py.out");
+  return out;
+}
+at::Tensor xlog1py_so(const at::Tensor& s, const c10::Scalar& o) {
+  return xlog1py_into(EwIn::of(s), EwIn::num(o), at::result_type(s, o), {}, "special_xlog1py.other_scalar");
+}
+at::Tensor& xlog1py_so_out(const at::Tensor& s, const c10::Scalar& o, at::Tensor& out) {
+  xlog1py_into(EwIn::of(s), EwIn::num(o), at::result_type(s, o), out, "special_xlog1py.other_scalar_out");
+  return out;
+}
+at::Tensor xlog1py_ss(const c10::Scalar& s, const at::Tensor& o) {
+  return xlog1py_into(EwIn::num(s), EwIn::of(o), at::result_type(s, o), {}, "special_xlog1py.self_scalar");
+}
+at::Tensor& xlog1py_ss_out(const c10::Scalar& s, const at::Tensor& o, at::Tensor& out) {
+  xlog1py_into(EwIn::num(s), EwIn::of(o), at::result_type(s, o), out, "special_xlog1py.self_scalar_out");
+  return out;
+}
+
 at::Tensor xlogy_t(const at::Tensor& s, const at::Tensor& o) {
   return xlogy_into(EwIn::of(s), EwIn::of(o), at::result_type(s, o), {}, false, "xlogy.Tensor");
 }
@@ -363,6 +392,12 @@ TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
   m.impl("pow_.Tensor", TORCH_FN(pow_tt_));
   m.impl("pow.Scalar", TORCH_FN(pow_st));
   m.impl("pow.Scalar_out", TORCH_FN(pow_st_out));
+  m.impl("special_xlog1py", TORCH_FN(xlog1py_t));
+  m.impl("special_xlog1py.out", TORCH_FN(xlog1py_t_out));
+  m.impl("special_xlog1py.other_scalar", TORCH_FN(xlog1py_so));
+  m.impl("special_xlog1py.other_scalar_out", TORCH_FN(xlog1py_so_out));
+  m.impl("special_xlog1py.self_scalar", TORCH_FN(xlog1py_ss));
+  m.impl("special_xlog1py.self_scalar_out", TORCH_FN(xlog1py_ss_out));
   m.impl("xlogy.Tensor", TORCH_FN(xlogy_t));
   m.impl("xlogy.OutTensor", TORCH_FN(xlogy_t_out));
   m.impl("xlogy_.Tensor", TORCH_FN(xlogy_t_));

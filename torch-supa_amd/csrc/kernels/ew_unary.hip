@@ -72,6 +72,10 @@ int supa_amd_xlogy(const supa_amd_ew_desc* d, void* stream) {
   return run_ew(SimpleFactory<XlogyOp, true>{}, d, stream, 3);
 }
 
+int supa_amd_xlog1py(const supa_amd_ew_desc* d, void* stream) {
+  return run_ew(SimpleFactory<Xlog1pyOp, true>{}, d, stream, 3);
+}
+
 int supa_amd_pow(const supa_amd_ew_desc* d, void* stream) {
   return run_ew(SimpleFactory<PowOp, true>{}, d, stream, 3);
 }

@@ -765,6 +765,18 @@ template <typename C> struct XlogyOp {
 // input, target}: -norm g below -beta, norm g above beta, norm x g / beta
 // between; in scalar_t, every operation rounded for a 16-bit type (norm and
 // beta come rounded).
+// xlog1py (upstream xlog1py_kernel_cuda): NaN for a NaN y, 0 for x == 0,
+// x log1p(y).
+template <typename C> struct Xlog1pyOp {
+  static constexpr int arity = 2;
+  __device__ __forceinline__ C operator()(const C* v) const {
+    const C x = v[0], y = v[1];
+    if (y != y) return y;
+    if (x == C(0)) return C(0);
+    return x * log1px<C>(y);
+  }
+};
+
 template <typename C> struct SmoothL1BwdOp {
   static constexpr int arity = 3;
   C norm, beta;
