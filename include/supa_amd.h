@@ -208,6 +208,18 @@ int supa_amd_xlogy(const supa_amd_ew_desc* d, void* stream);
  * .other_scalar_out NF:13670 (upstream xlog1py_kernel_cuda). */
 int supa_amd_xlog1py(const supa_amd_ew_desc* d, void* stream);
 
+/* scatter_(dim, index, value), the assign form: for every element of index
+ * (ndim dims of index_sizes, index_strides in elements, int64 values), the
+ * element of out at the same coordinates but with coordinate `dim` replaced
+ * by the index value becomes value (ivalue for integer and bool dtypes).
+ * out_strides in elements; an index outside [0, out_dim_size) writes nothing
+ * and sets *error_flag (when given) to 2.  Replaces scatter_.value NF:8458
+ * and scatter.value_out NF:8462 (upstream scatter_fill_kernel), which one_hot
+ * runs. */
+int supa_amd_scatter_fill(void* out, int32_t dtype, const int64_t* out_strides, int64_t out_dim_size,
+                          const int64_t* index, const int64_t* index_sizes, const int64_t* index_strides, int32_t ndim,
+                          int32_t dim, double value, int64_t ivalue, int32_t* error_flag, void* stream);
+
 /* grad_in = f'(...) * dy.  op = {grad_in, dy, x} where x is the forward input
  * for GELU, GELU_TANH, SILU and the forward output for SIGMOID, TANH.
  * Replaces gelu_backward.grad_input NF:5245, silu_backward.grad_input NF:5383,

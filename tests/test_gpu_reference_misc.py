@@ -3,7 +3,11 @@
 (torch.equal on random pairs in three dtypes, plus equal and NaN pairs
 here), test_resize.py (resize_ to the same element count keeps the data) and
 test_cuda_scalar.py (_local_scalar_dense reads the first element of any
-tensor, as upstream's does)."""
+tensor, as upstream's does), test_one_hot_fused.py (one_hot, whose
+scatter_ runs on the device) and test_normalize_fused.py (F.normalize: the
+vector norm, clamp_min and the division, all device kernels; the reference
+calls its own torch.normalize, which upstream torch does not have)."""
+import numpy as np
 import copy
 
 import pytest
@@ -59,3 +63,53 @@ def test_local_scalar_dense(shape, no_fallback):
     x = torch.randn(shape, generator=torch.Generator().manual_seed(9))
     xs = copy.deepcopy(x).to(SUPA)
     assert torch.ops.aten._local_scalar_dense.default(x) == torch.ops.aten._local_scalar_dense.default(xs)
+
+
+@pytest.mark.parametrize("shape, num_classes", [((8,), 4), ((64,), 32), ((1000,), 10), ((4, 16), 7), ((1024,), 128),
+                                                ((262144,), 32)])
+def test_one_hot(shape, num_classes, no_fallback):
+    """test_one_hot_fused.py: int64 result of shape + [num_classes], exact."""
+    idx = torch.randint(0, num_classes, shape, dtype=torch.int64, generator=torch.Generator().manual_seed(20260605))
+    out = torch.nn.functional.one_hot(idx.to(SUPA).contiguous(), num_classes=num_classes)
+    assert out.dtype == torch.int64 and list(out.shape) == list(shape) + [num_classes]
+    assert torch.equal(out.cpu(), torch.nn.functional.one_hot(idx, num_classes=num_classes))
+
+
+@pytest.mark.parametrize("shape", [(7, 48), (8, 64), (9, 96), (31, 128), (5, 192), (8, 256), (11, 384), (8, 512)])
+def test_normalize(shape, no_fallback):
+    """test_normalize_fused.py: p = 2 over the last dim, eps 1e-12, rtol 1e-5
+    / atol 1e-6."""
+    x = torch.randn(shape, generator=torch.Generator().manual_seed(20260604))
+    want = torch.nn.functional.normalize(x, p=2.0, dim=-1, eps=1.0e-12)
+    got = torch.nn.functional.normalize(x.to(SUPA).contiguous(), p=2.0, dim=-1, eps=1.0e-12)
+    np.testing.assert_allclose(want.numpy(), got.cpu().numpy(), rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.int64, torch.bool])
+@pytest.mark.parametrize("dim", [0, 1, -1])
+def test_scatter_value(dim, dtype, no_fallback):
+    """scatter_ / scatter with a scalar against the CPU, exact: an index
+    smaller than self along the other dims, a transposed destination, the
+    out-of-place and out= forms; an index past the destination's size is
+    reported (as an IndexError) at the next synchronisation."""
+    g = torch.Generator().manual_seed(31)
+    base = (torch.randn(6, 9, 11, generator=g) * 4).to(dtype)
+    d = dim % 3
+    isz = [5, 7, 8]
+    isz[d] = 13
+    index = torch.randint(0, base.shape[d], isz, generator=g)
+    value = True if dtype == torch.bool else (7 if dtype == torch.int64 else -2.5)
+    want = base.clone().scatter_(dim, index, value)
+    got = base.to(SUPA).scatter_(dim, index.to(SUPA), value)
+    assert torch.equal(got.cpu(), want)
+    assert torch.equal(torch.scatter(base.to(SUPA), dim, index.to(SUPA), value).cpu(), want)
+    t = base.transpose(0, 2).contiguous().transpose(0, 2)
+    ts = base.transpose(0, 2).contiguous().to(SUPA).transpose(0, 2)
+    assert torch.equal(ts.scatter_(dim, index.to(SUPA), value).cpu(), t.scatter_(dim, index, value))
+    out = torch.empty(0, dtype=dtype, device=SUPA)
+    torch.scatter(base.to(SUPA), dim, index.to(SUPA), value, out=out)
+    assert torch.equal(out.cpu(), want)
+    bad = index.clone()
+    bad.view(-1)[5] = base.shape[d]
+    with pytest.raises(IndexError, match="scatter_ index"):
+        base.to(SUPA).scatter_(dim, bad.to(SUPA), value).cpu()

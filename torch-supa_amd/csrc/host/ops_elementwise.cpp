@@ -273,6 +273,49 @@ bool equal(const at::Tensor& self, const at::Tensor& other) {
   return at::eq(self, other).all().item<bool>();
 }
 
+// scatter_(dim, index, value) with upstream's shape checks (ScatterGatherChecks.h)
+// and the assign form of scatter_fill_kernel; an index outside the
+// destination's dim sets the device error flag, reported at the next sync.
+at::Tensor& scatter_value_(at::Tensor& self, int64_t dim, const at::Tensor& index, const c10::Scalar& value) {
+  TORCH_CHECK(index.scalar_type() == at::kLong, "scatter_(): Expected dtype int64 for index");
+  TORCH_CHECK(self.device() == index.device(), "scatter_: expected self and index on the same device, got ",
+              self.device(), " and ", index.device());
+  const int64_t nd = std::max<int64_t>(self.dim(), 1);
+  TORCH_CHECK(std::max<int64_t>(index.dim(), 1) == nd,
+              "Index tensor must have the same number of dimensions as self tensor");
+  const int64_t wd = at::maybe_wrap_dim(dim, nd);
+  if (index.numel() == 0) return self;
+  at::Tensor out = self.dim() == 0 ? self.view({1}) : self;
+  at::Tensor idx = index.dim() == 0 ? index.view({1}) : index;
+  for (int64_t d = 0; d < nd; ++d) {
+    if (d == wd) continue;
+    TORCH_CHECK(idx.size(d) <= out.size(d), "Expected index ", index.sizes(), " to be smaller than self ",
+                self.sizes(), " apart from dimension ", wd);
+  }
+  TORCH_CHECK(nd <= SUPA_AMD_MAX_DIMS, "scatter_: supa supports up to ", SUPA_AMD_MAX_DIMS, " dimensions");
+  TORCH_CHECK(dtype_supported(self.scalar_type()), "scatter_: unsupported dtype ", self.scalar_type());
+  const auto dev = self.device().index();
+  const int rc = supa_amd_scatter_fill(out.data_ptr(), dtype_code(out.scalar_type()), out.strides().data(),
+                                       out.size(wd), idx.data_ptr<int64_t>(), idx.sizes().data(),
+                                       idx.strides().data(), (int32_t)nd, (int32_t)wd, value.toDouble(),
+                                       value.isIntegral(true) ? value.toLong() : (int64_t)value.toDouble(),
+                                       device_scratch(dev).error_flag, current_stream(dev));
+  check_status(rc, "scatter_");
+  return self;
+}
+at::Tensor scatter_value(const at::Tensor& self, int64_t dim, const at::Tensor& index, const c10::Scalar& value) {
+  at::Tensor out = self.clone(at::MemoryFormat::Preserve);
+  return scatter_value_(out, dim, index, value);
+}
+at::Tensor& scatter_value_out(const at::Tensor& self, int64_t dim, const at::Tensor& index, const c10::Scalar& value,
+                              at::Tensor& out) {
+  if (!out.is_same(self)) {
+    at::native::resize_output(out, self.sizes());
+    out.copy_(self);
+  }
+  return scatter_value_(out, dim, index, value);
+}
+
 // eye.out / eye.m_out (upstream eye_out_cuda): zeros, then ones on the
 // diagonal through a strided view of it.
 at::Tensor& eye_m_out(int64_t n, int64_t m, at::Tensor& out) {
@@ -1263,6 +1306,9 @@ TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
   m.impl("_local_scalar_dense", TORCH_FN(local_scalar_dense));
   m.impl("equal", TORCH_FN(equal));
   m.impl("eye.out", TORCH_FN(eye_out));
+  m.impl("scatter_.value", TORCH_FN(scatter_value_));
+  m.impl("scatter.value", TORCH_FN(scatter_value));
+  m.impl("scatter.value_out", TORCH_FN(scatter_value_out));
   m.impl("eye.m_out", TORCH_FN(eye_m_out));
   m.impl("fill_.Scalar", TORCH_FN(fill_scalar));
   m.impl("fill_.Tensor", TORCH_FN(fill_tensor));

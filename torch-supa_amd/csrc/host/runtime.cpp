@@ -247,6 +247,8 @@ void check_device_errors(c10::DeviceIndex d) {
   if (h != 0) {
     const int32_t zero = 0;
     memcpy_h2d(flag, &zero, sizeof(zero), d);
+    TORCH_CHECK_INDEX(h != 2, "supa: a kernel reported an out-of-bounds index (a scatter_ index outside the "
+                              "destination's size along dim)");
     TORCH_CHECK_INDEX(false, "supa: a kernel reported an out-of-bounds target index (nll_loss target outside "
                              "[0, n_classes) and not ignore_index)");
   }
