@@ -20,6 +20,9 @@ dtypes, tolerances and comparisons (CPU result against the supa result):
 * test_binary_mul_kernel.py: Tensor, one-element broadcast, in place, Scalar
   and in-place Scalar products (its mixed-dtype cases are in
   test_gpu_reference_shapes.py);
+* test_pow_kernel.py (tensor ** tensor and tensor ** a 0-dim CPU int
+  tensor, out of place and in place), test_abs_kernel.py (N(0, 1) and
+  all-zero inputs, out of place and in place);
 * test_lerp.py, test_linalg_vector_norm.py (bf16 input, float32
   accumulation), test_fused_adam_kernel.py, test_fused_sgd_kernel.py (one
   step of SGD(fused=True) on a cross-entropy loss against the CPU's
@@ -369,3 +372,46 @@ def test_fused_sgd_on_cross_entropy(shape, dtype, no_fallback):
     crit(ws, ts).backward()
     os_.step()
     ref_allclose(wc, ws, 1e-3, 1e-4)
+
+
+POW_PARAMS = [((1, 16), True), ((1, 16), False), ((512, 1024), True), ((512, 1024), False), ((1023, 511), True),
+              ((1025, 513), True), ((1028, 2135), True), ((1023, 511), False), ((1025, 513), False),
+              ((1028, 2135), False)]
+
+
+@pytest.mark.parametrize("shape, scalar", POW_PARAMS)
+def test_pow_ptwise(shape, scalar, no_fallback):
+    """test_pow_kernel.py: float32; the exponent an N(0, 1) tensor or
+    torch.tensor(2) (a 0-dim CPU int64 tensor, taken as a scalar)."""
+    dtype = torch.float32
+    x, x_s = pair(shape, dtype)
+    if scalar:
+        y = y_s = torch.tensor(2)
+    else:
+        y, y_s = pair(shape, dtype)
+    out, out_s = torch.pow(x, y), torch.pow(x_s, y_s)
+    x.pow_(y)
+    x_s.pow_(y_s)
+    ref_allclose(x, x_s, RTOL[dtype], ATOL[dtype], equal_nan=True)
+    ref_allclose(out, out_s, RTOL[dtype], ATOL[dtype], equal_nan=True)
+    ref_allclose(x_s.cpu(), out_s, RTOL[dtype], ATOL[dtype], equal_nan=True)
+
+
+ABS_SHAPES = [(32,), (1024, 512), (1023, 511), (1025, 513), (1028, 2135)]
+
+
+@pytest.mark.parametrize("zeros", [False, True])
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("shape", ABS_SHAPES)
+def test_abs_forms(shape, dtype, zeros, no_fallback):
+    """test_abs_kernel.py: test_abs and test_abs_out (abs_) over N(0, 1) and
+    all-zero (uniform in [0, 0]) inputs."""
+    x, x_s = (torch.zeros(shape, dtype=dtype), torch.zeros(shape, dtype=dtype, device=SUPA)) if zeros else \
+        pair(shape, dtype)
+    y, y_s = torch.abs(x), torch.abs(x_s)
+    ref_allclose(y, y_s, RTOL[dtype], ATOL[dtype], equal_nan=True)
+    x.abs_()
+    x_s.abs_()
+    ref_allclose(x, y, RTOL[dtype], ATOL[dtype], equal_nan=True)
+    ref_allclose(x, x_s.cpu(), RTOL[dtype], ATOL[dtype], equal_nan=True)
+    ref_allclose(x_s.cpu(), y_s.cpu(), RTOL[dtype], ATOL[dtype], equal_nan=True)
