@@ -12,7 +12,8 @@ torch.cuda under its transfer_to_supa mode):
 * test_copy_non_blocking (pinned host memory both ways, and a pinned view
   whose data pointer is not its storage's), test_to_cpu_blocking_by_default;
 * test_torch_manual_seed_seeds_cuda_devices, test_manual_seed;
-* test_streams, test_events.
+* test_streams, test_events, test_generic_stream_event (torch.Stream /
+  torch.Event on the supa device through the device guard).
 
 Not mirrored: the reference's timing sleeps (torch.cuda._sleep is a kernel
 of torch's own HIP runtime, outside the supa stream), the assertion that the
@@ -213,3 +214,31 @@ def test_all_any_and_bernoulli_tensor(no_fallback):
     n = 1 << 20
     m = float(torch.bernoulli(torch.full((n,), 0.3, device=SUPA)).mean())
     assert abs(m - 0.3) < 5 * (0.3 * 0.7 / n) ** 0.5
+
+
+def test_generic_stream_event(no_fallback):
+    """test_supa.py's test_generic_stream_event: torch.Stream / torch.Event on
+    the supa device, through the device guard's stream and event methods."""
+    stream = torch.Stream(SUPA)
+    assert stream.device_index == S().current_device()
+    s = S().Stream(stream_id=stream.stream_id, device_index=stream.device_index, device_type=stream.device_type)
+    assert isinstance(s, torch.Stream) and torch.Stream in type(s).mro()
+    assert stream.stream_id == s.stream_id
+    assert stream.stream_id != S().current_stream().stream_id
+    event1 = torch.Event(SUPA, enable_timing=True)
+    event2 = torch.Event(SUPA, enable_timing=True)
+    a = torch.randn(1000, generator=torch.Generator().manual_seed(5))
+    b = torch.randn(1000, generator=torch.Generator().manual_seed(6))
+    with S().stream(s):
+        a_s = a.to(SUPA, non_blocking=True)
+        b_s = b.to(SUPA, non_blocking=True)
+        assert stream.stream_id == S().current_stream().stream_id
+    event1.record(stream)
+    event1.synchronize()
+    assert event1.query()
+    c = a_s + b_s
+    event2.record()
+    event2.synchronize()
+    assert event2.query()
+    assert torch.equal(c.cpu(), a + b)
+    assert event1.elapsed_time(event2) >= 0

@@ -732,12 +732,14 @@ struct SupaGuardImpl final : public c10::impl::DeviceGuardImplInterface {
   void uncheckedSetDevice(c10::Device d) const noexcept override {
     if (hipSetDevice(d.index()) == hipSuccess) tls_device = d.index();
   }
-  c10::Stream getStream(c10::Device d) const override { return current_stream_obj(d.index()); }
-  c10::Stream getDefaultStream(c10::Device d) const override { return default_stream_obj(d.index()); }
+  // a device without an index (torch.Stream("supa")) is the current device
+  static c10::DeviceIndex index_of(c10::Device d) { return d.has_index() ? d.index() : current_device(); }
+  c10::Stream getStream(c10::Device d) const override { return current_stream_obj(index_of(d)); }
+  c10::Stream getDefaultStream(c10::Device d) const override { return default_stream_obj(index_of(d)); }
   c10::Stream getStreamFromGlobalPool(c10::Device d, bool /*high_priority*/) const override {
-    return pool_stream(d.index());  // every stream has the default priority
+    return pool_stream(index_of(d));  // every stream has the default priority
   }
-  c10::Stream getNewStream(c10::Device d, int /*priority*/) const override { return pool_stream(d.index()); }
+  c10::Stream getNewStream(c10::Device d, int /*priority*/) const override { return pool_stream(index_of(d)); }
   c10::Stream exchangeStream(c10::Stream s) const override { return exchange_stream(s); }
   c10::DeviceIndex deviceCount() const noexcept override { return device_count(); }
 
@@ -751,8 +753,10 @@ struct SupaGuardImpl final : public c10::impl::DeviceGuardImplInterface {
     if (stream.device_index() != prev) set_device(stream.device_index());
     if (!*event) {
       hipEvent_t e;
+      // as the CUDA guard: PYTORCH_DEFAULT events skip timing, BACKEND_DEFAULT
+      // ones (torch.Event(enable_timing=True)) keep it
       SUPA_HIP_CHECK(hipEventCreateWithFlags(
-          &e, flag == c10::EventFlag::BACKEND_DEFAULT ? hipEventDisableTiming : hipEventDefault));
+          &e, flag == c10::EventFlag::PYTORCH_DEFAULT ? hipEventDisableTiming : hipEventDefault));
       *event = e;
     }
     SUPA_HIP_CHECK(hipEventRecord(static_cast<hipEvent_t>(*event), stream_handle(stream.device_index(), stream.id())));
