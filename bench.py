@@ -958,7 +958,7 @@ def main():
         run_patterns()
     if a.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {a.gpus} is not supported "
-              "(the path's multi-GPU sharding is described in DESIGN.md, not run)", file=sys.stderr)
+              "(the path's multi-GPU sharding is a design, not a measured run)", file=sys.stderr)
         sys.exit(2)
     import torch
     import torch_supa  # noqa: F401
