@@ -177,3 +177,27 @@ def test_prelu_forward_backward(shape, nw, dtype, no_fallback):
     want_w = gw.astype(np.float64).sum(axis=red).reshape(nw)
     tol = 1e-5 if dtype == torch.float32 else (2e-2 if dtype == torch.bfloat16 else 2e-3)
     np.testing.assert_allclose(ws.grad.cpu().float().numpy(), want_w, rtol=tol, atol=tol * np.abs(gw).sum() / nw)
+
+
+def test_new_ops_on_empty_and_scalar_inputs(no_fallback):
+    """Empty tensors through hardshrink / softshrink / glu / prelu and their
+    backwards, special.xlog1py, scatter_ and _fused_sgd_ (an empty tensor in
+    its list): empty results of the right shape, no launch
+    errors; a 0-dim scatter_ target takes its one element."""
+    e = torch.empty(0, 6, device="supa", requires_grad=True)
+    for y in (F.hardshrink(e), F.softshrink(e), F.glu(e, -1), F.prelu(e, torch.ones(6, device="supa"))):
+        assert y.shape[0] == 0
+        y.sum().backward()
+    assert torch.special.xlog1py(torch.empty(0, device="supa"), torch.empty(0, device="supa")).numel() == 0
+    t = torch.zeros(3, device="supa")
+    t.scatter_(0, torch.empty(0, dtype=torch.long, device="supa"), 1.0)
+    assert torch.equal(t.cpu(), torch.zeros(3))
+    z = torch.zeros((), device="supa")
+    z.scatter_(0, torch.zeros((), dtype=torch.long, device="supa"), 2.5)
+    assert float(z) == 2.5
+    # (an all-empty list has no tensor to dispatch on, here as on any backend)
+    p = [torch.empty(0, device="supa"), torch.ones(5, device="supa")]
+    g = [torch.empty(0, device="supa"), torch.ones(5, device="supa")]
+    torch._fused_sgd_(p, g, [], weight_decay=0.0, momentum=0.0, lr=0.5, dampening=0.0, nesterov=False,
+                      maximize=False, is_first_step=False)
+    assert torch.equal(p[1].cpu(), torch.full((5,), 0.5))
