@@ -55,11 +55,6 @@ def parse():
     ap.add_argument("--config", default="c2", help="the config of --derive-counters")
     ap.add_argument("--stats", default=None, help="with --derive-counters: the kernel_stats.csv of a "
                                                   "rocprofv3 --kernel-trace --stats run of the same probe")
-    ap.add_argument("--patterns", action="store_true",
-                    help="run the access-pattern ceilings probe (torch_supa/supa_patterns) and print its tables")
-    ap.add_argument("--render-patterns", nargs=2, metavar=("STATS_CSV", "PATTERNS_LOG"),
-                    help="CPU only: write profiles/access_patterns.md from the kernel_stats.csv of a rocprofv3 "
-                         "--kernel-trace --stats run of supa_patterns and that run's output")
     ap.add_argument("--render-kernel-stats", nargs=2, metavar=("STATS_CSV", "BENCH_LOG"),
                     help="CPU only: write profiles/kernel_stats_all_configs.md from the kernel_stats.csv of a "
                          "rocprofv3 --kernel-trace --stats run of bench.py --no-cpu and that run's output")
@@ -654,52 +649,6 @@ def render_kernel_stats(stats_csv, bench_log):
     print(path)
 
 
-PATTERNS_EXE = os.path.join(HERE, "torch-supa_amd", "torch_supa", "supa_patterns")
-
-
-def run_patterns():
-    """The access-pattern ceilings probe: a separate program (no torch), so it
-    runs as a child process; its exit status is this call's."""
-    import subprocess
-
-    if not os.path.exists(PATTERNS_EXE):
-        raise SystemExit(f"{PATTERNS_EXE} is missing: build first (python __graft_entry__.py)")
-    sys.exit(subprocess.call([PATTERNS_EXE]))
-
-
-def render_patterns(stats_csv, log_path):
-    """profiles/access_patterns.md: the probe's own HIP-event table, and
-    rocprofv3's per-kernel averages for the same launches."""
-    import csv
-
-    with open(stats_csv) as f:
-        rows = [r for r in csv.DictReader(f) if "p_" in r["Name"]]
-    text = open(log_path).read().strip("\n")
-    out = ["# Access-pattern ceilings on MI355X (`torch-supa_amd/csrc/probe/patterns.hip`)", "",
-           "Trivial kernels with the launch shapes and the nontemporal 16-byte accesses of this library's kernels "
-           "(copy, add, fill, the c3 row pattern, AdamW's 4-read / 3-write stream), and the FMA issue rates.  "
-           "Each library kernel's fraction of the 8 TB/s roofline is read against the row of its pattern.", "",
-           "Commands (repo root on the GPU box; the last runs on any machine):", "", "```",
-           "cd /tmp && export TMPDIR=/tmp && cd $GRAFT_REPO_ROOT",
-           "rocprofv3 --kernel-trace --stats --output-format csv -d {} -o {} -- \\".format(
-               *_run_args(stats_csv, "_kernel_stats.csv")),
-           f"    torch-supa_amd/torch_supa/supa_patterns > {log_path}",
-           f"python3 bench.py --render-patterns {stats_csv} {log_path}", "```", "",
-           "`python3 bench.py --patterns` runs the probe alone.", "",
-           "## The probe's own timing (HIP events, average over the timed launches)", "", text, "",
-           "## rocprofv3 per-kernel averages (all launches, warm-up included)", "",
-           "| kernel | calls | avg us | min us | max us |", "|---|---:|---:|---:|---:|"]
-    for r in rows:
-        name = r["Name"].replace("void ", "")
-        name = name[: name.index(">(") + 1] if ">(" in name else name.split("(")[0]
-        out.append(f"| `{name}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | "
-                   f"{float(r['MinNs']) / 1e3:.1f} | {float(r['MaxNs']) / 1e3:.1f} |")
-    path = os.path.join(HERE, "profiles", "access_patterns.md")
-    with open(path, "w") as f:
-        f.write("\n".join(out) + "\n")
-    print(path)
-
-
 PROBE_REPS = 3
 
 
@@ -951,11 +900,6 @@ def main():
     if a.render_kernel_stats:
         render_kernel_stats(*a.render_kernel_stats)
         return
-    if a.render_patterns:
-        render_patterns(*a.render_patterns)
-        return
-    if a.patterns:
-        run_patterns()
     if a.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {a.gpus} is not supported "
               "(the path's multi-GPU sharding is a design, not a measured run)", file=sys.stderr)

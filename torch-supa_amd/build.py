@@ -32,8 +32,6 @@ ARCH = "gfx950"
 KERNELS_SO = os.path.join(PKG, "libsupa_amd_kernels.so")
 EXT_SUFFIX = sysconfig.get_config_var("EXT_SUFFIX") or ".so"
 C_SO = os.path.join(PKG, "_C" + EXT_SUFFIX)
-PATTERNS_SRC = os.path.join(HERE, "csrc", "probe", "patterns.hip")
-PATTERNS_EXE = os.path.join(PKG, "supa_patterns")  # the access-pattern ceilings probe
 
 HIP_FLAGS = [
     f"--offload-arch={ARCH}", "-std=c++20", "-O3", "-fPIC",
@@ -129,9 +127,6 @@ def build(jobs: int | None = None, incremental: bool = False, verbose: bool = Tr
           "-L", torch_lib, "-lc10", "-ltorch", "-ltorch_cpu", "-ltorch_python", "-lamdhip64",
           "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{torch_lib}"])
     os.replace(C_SO + ".tmp", C_SO)
-    if not incremental or _stale(PATTERNS_SRC, PATTERNS_EXE, kdeps):
-        _run([HIPCC, *HIP_FLAGS, PATTERNS_SRC, "-o", PATTERNS_EXE + ".tmp"])
-        os.replace(PATTERNS_EXE + ".tmp", PATTERNS_EXE)
     if verbose:
         print(f"[torch_supa build] wrote {os.path.relpath(KERNELS_SO, REPO)} and {os.path.relpath(C_SO, REPO)}",
               flush=True)
