@@ -92,7 +92,10 @@ int supa_amd_add(const supa_amd_ew_desc* d, double alpha, int64_t ialpha, void* 
 int supa_amd_mul(const supa_amd_ew_desc* d, void* stream);
 
 /* Division.  mode 0 = true division (IEEE a / b, also for a CPU-scalar
- * divisor), 1 = trunc, 2 = floor.  op = {out, a, b}.  Replaces
+ * divisor), 1 = trunc, 2 = floor.  op = {out, a, b}.  Trunc of bf16 / f16
+ * tensors truncates the quotient rounded to the 16-bit type; with an
+ * immediate divisor (op[2].is_scalar) it truncates the float quotient.
+ * Replaces
  * div_true_stub / div_trunc_stub / div_floor_stub:
  * .../elementwise/BinaryDivTrueKernel.cu:22-65, BinaryDivTruncKernel.cu:22-55,
  * BinaryDivFloorKernel.cu:22-82. */

@@ -29,6 +29,9 @@ ADDCMUL, ADDCDIV, LERP = 0, 1, 2
 GELU, GELU_TANH, SILU, SIGMOID, TANH, EXP, LOG, ERF, RELU, NEG, RECIPROCAL, ABS, SQRT, EXPM1, LOG1P = range(15)
 # the opt-in cancellation-free gelu forms (C-ABI codes SUPA_AMD_GELU_LOGERFC / _TANH_LOGISTIC)
 GELU_LOGERFC, GELU_TANH_LOGISTIC = 22, 23
+# oracle only: gelu('tanh') with the other binary32 neighbour of tanh where the
+# device's forward quotient may round the other way (see gelu_tanh_forward_equal)
+GELU_TANH_FAST_ALT = 100
 (ACT_LEAKY_RELU, ACT_HARDTANH, ACT_ELU, ACT_SOFTPLUS, ACT_HARDSWISH, ACT_HARDSIGMOID, ACT_MISH, ACT_LOG_SIGMOID,
  ACT_THRESHOLD) = range(9)
 MSE, SMOOTH_L1, BCE_LOGITS = 0, 1, 2
@@ -163,6 +166,17 @@ def div_trunc_16(a, b, dtype: str) -> np.ndarray:
     return np.trunc(q)
 
 
+def div_trunc_16_scalar(a, b: float, dtype: str) -> np.ndarray:
+    """Trunc division of bfloat16 / float16 values (given as float32) by a
+    CPU scalar b: the float32 quotient a / float(b) truncated, then rounded to
+    the 16-bit type.  The reference's is_cpu_scalar branch
+    (BinaryDivTruncKernel.cu:30-41) truncates the float product a * (1 / b)
+    without the 16-bit rounding; upstream CPU truncates the float quotient
+    a / b.  dtype: "bf16" or "f16"; float32 result."""
+    q = np.trunc(binary(DIV, a, np.full(np.shape(a), np.float32(b), np.float32)))
+    return round_bf16(q) if dtype == "bf16" else np.asarray(q, np.float32).astype(np.float16).astype(np.float32)
+
+
 def binary_int(op: int, a, b, alpha: int = 1, dtype=np.int64) -> np.ndarray:
     """Wrapping integer arithmetic (UfuncCUDA_add.cu:13-16 add, BinaryInternal.h
     mul, BinaryDivTruncKernel.cu / BinaryDivFloorKernel.cu integer paths)."""
@@ -186,6 +200,29 @@ def unary(op: int, x) -> np.ndarray:
     out = np.empty(x.shape, np.float32)
     lib().or_unary_f32(op, _p(x, _f32p), _p(out, _f32p), x.size)
     return out
+
+
+def gelu_tanh_forward_equal(got, x) -> bool:
+    """Whether a device gelu('tanh') forward result equals the oracle's.
+
+    The forward kernel takes tanh's binary64 quotient m / (m + 2) without the
+    final residual correction that makes it the exact binary64 quotient (the
+    correction costs two binary64 fma per element on the headline kernel):
+    its quotient is within 2^-48.5 (relative) of m / (m + 2), so its tanh
+    equals the oracle's except where m / (m + 2) lies that close to a binary32
+    rounding boundary, where it may be the other neighbour.  Each element of
+    ``got`` must equal the oracle's gelu('tanh') of ``x`` or, where the
+    quotient is within 2^-44 of a boundary, the value with that other
+    neighbour (``GELU_TANH_FAST_ALT``).  NaN matches NaN."""
+    got = np.asarray(got, np.float32)
+    ref = unary(GELU_TANH, x)
+    if got.shape != ref.shape:
+        return False
+    ok = (got == ref) | (np.isnan(got) & np.isnan(ref))
+    if ok.all():
+        return True
+    alt = unary(GELU_TANH_FAST_ALT, x)
+    return bool(np.all(ok | (got == alt)))
 
 
 def unary_backward(op: int, dy, x) -> np.ndarray:

@@ -177,7 +177,10 @@ enum {
   OR_EXP = 5, OR_LOG = 6, OR_ERF = 7, OR_RELU = 8, OR_NEG = 9, OR_RECIPROCAL = 10, OR_ABS = 11,
   OR_SQRT = 12, OR_EXPM1 = 13, OR_LOG1P = 14,
   /* the opt-in cancellation-free gelu forms (same codes as the C ABI) */
-  OR_GELU_LOGERFC = 22, OR_GELU_TANH_LOGISTIC = 23
+  OR_GELU_LOGERFC = 22, OR_GELU_TANH_LOGISTIC = 23,
+  /* oracle only: gelu('tanh') with or_tanhf_fast_alt's neighbour (the other
+   * value the device's forward may return) */
+  OR_GELU_TANH_FAST_ALT = 100
 };
 
 #define OR_SQRT1_2 0.70710678118654752440f
@@ -209,6 +212,7 @@ static inline float act_fwd(int op, float x) {
   switch (op) {
     case OR_GELU: return (x * 0.5f) * (1.0f + or_erff_nn(x * OR_SQRT1_2));
     case OR_GELU_TANH: return (0.5f * x) * (1.0f + or_tanhf(gelu_tanh_inner(x)));
+    case OR_GELU_TANH_FAST_ALT: return (0.5f * x) * (1.0f + or_tanhf_fast_alt(gelu_tanh_inner(x)));
     case OR_GELU_LOGERFC: return or_gelu_none(x);
     case OR_GELU_TANH_LOGISTIC: {
       const float x3 = (x * x) * x;

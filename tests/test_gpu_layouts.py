@@ -43,6 +43,10 @@ def test_contiguous_gelu_whole_and_sliced(approx, dtype, vec, no_fallback):
     for sl in (slice(0, 4096), slice(n - 4099, n)):
         xs = x[sl].float().cpu().numpy()
         want = torch.from_numpy(O.unary(k, xs)).to(dtype)
+        if approx == "tanh":  # the forward's tanh may be the other neighbour near a rounding boundary
+            alt = torch.from_numpy(O.unary(O.GELU_TANH_FAST_ALT, xs)).to(dtype)
+            assert bool(((y[sl].cpu() == want) | (y[sl].cpu() == alt)).all())
+            continue
         assert torch.equal(y[sl].cpu(), want)
 
 

@@ -72,6 +72,9 @@ def test_activations_ladder_bit_exact(shape, no_fallback):
         if op == O.SQRT:
             assert np.array_equal(fn(dx).cpu().numpy(), O.unary(op, np.abs(xn)))
             continue
+        if op == O.GELU_TANH:
+            assert O.gelu_tanh_forward_equal(fn(dx).cpu().numpy(), xn)
+            continue
         assert np.array_equal(fn(dx).cpu().numpy(), O.unary(op, xn))
 
 
@@ -233,6 +236,15 @@ def test_div_trunc_16bit_bit_exact(dtype, no_fallback):
     got = torch.div(dev(a), dev(row), rounding_mode="trunc").cpu().float().numpy()
     ref = O.div_trunc_16(a.float().numpy(), np.broadcast_to(row.float().numpy(), a.shape), name)
     assert np.array_equal(got, ref)
+    # a CPU-scalar divisor truncates the float quotient (202 / 1.5 -> 134)
+    a100 = (a.float() * 100).to(dtype)
+    a100[0, 0] = 202.0
+    for div in (1.5, -0.3, 7.0):
+        got = torch.div(dev(a100), div, rounding_mode="trunc").cpu().float().numpy()
+        assert np.array_equal(got, O.div_trunc_16_scalar(a100.float().numpy(), div, name)), div
+        got_cpu_t = torch.div(dev(a100), torch.tensor(div), rounding_mode="trunc").cpu().float().numpy()
+        assert np.array_equal(got_cpu_t, O.div_trunc_16_scalar(a100.float().numpy(), div, name)), div
+    assert torch.div(dev(a100), 1.5, rounding_mode="trunc").cpu()[0, 0].item() == 134.0
 
 
 def test_integer_bool_and_mixed_dtypes(no_fallback):
@@ -299,7 +311,7 @@ def test_c2_full_size(transposed, no_fallback):
     assert z.stride() == y.stride()
     zc = z.cpu().numpy()
     del y, z
-    assert np.array_equal(zc, O.unary(O.GELU_TANH, ref_y))
+    assert O.gelu_tanh_forward_equal(zc, ref_y)
 
 
 # ------------------------------------------------------------ c3 config

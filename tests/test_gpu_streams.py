@@ -77,7 +77,9 @@ def test_two_streams_with_events_match_serial(no_fallback):
     with torch.supa.stream(s2):
         z = x * y
     torch.supa.current_stream().wait_stream(s2)
-    ref_x = O.unary(O.GELU_TANH, a.numpy())
+    x0 = torch.nn.functional.gelu(da, approximate="tanh").cpu().numpy()  # default stream, same kernel
+    assert O.gelu_tanh_forward_equal(x0, a.numpy())
+    ref_x = x0
     for _ in range(8):
         ref_x = O.binary(O.MUL, ref_x, np.float32(1.0001))
     ref = O.binary(O.MUL, ref_x, O.binary(O.ADD, a.numpy(), b.numpy()))

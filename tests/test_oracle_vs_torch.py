@@ -78,6 +78,25 @@ def test_div_trunc_16bit_rounds_the_quotient(dtype):
     assert (got != np.trunc(af / bf)).sum() > 0
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("divisor", [1.5, -0.3, 7.0, 0.0])
+def test_div_trunc_16bit_by_a_cpu_scalar(dtype, divisor):
+    """trunc division of 16-bit values by a CPU scalar truncates the float
+    quotient (no rounding to the 16-bit type first).  Pinned against upstream
+    CPU on whole vectors and a scalar tail (4099 elements); 202 / 1.5 is 134
+    (the float quotient 134.67 truncated), where rounding the quotient to bf16
+    first (135) would give 135."""
+    a = randn((4099,), 10, dtype=dtype) * 100
+    a[0] = 202.0
+    af = a.float().numpy()
+    name = "bf16" if dtype == torch.bfloat16 else "f16"
+    got = O.div_trunc_16_scalar(af, divisor, name)
+    cpu = torch.div(a, divisor, rounding_mode="trunc").float().numpy()
+    assert np.array_equal(got, cpu, equal_nan=True)
+    if divisor == 1.5:
+        assert got[0] == 134.0
+
+
 _LOSS16 = {"mse": lambda a, b, red, beta: F.mse_loss(a, b, reduction=red),
            "smooth_l1": lambda a, b, red, beta: F.smooth_l1_loss(a, b, reduction=red, beta=beta),
            "huber": lambda a, b, red, beta: F.huber_loss(a, b, reduction=red, delta=beta)}

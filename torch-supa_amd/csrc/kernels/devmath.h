@@ -3,7 +3,10 @@
 // Own implementations (not the device libm), evaluated with an explicit
 // fused-multiply-add sequence and compiled with -ffp-contract=off, so every
 // result is reproducible bit for bit by any IEEE machine with correctly
-// rounded binary32/binary64 fma, add, multiply, division, rint and ldexp.  Accuracy against
+// rounded binary32/binary64 fma, add, multiply, division, rint and ldexp
+// (tanh's quotient starts from the hardware reciprocal and is corrected to
+// the binary64 quotient; gelu('tanh') forward's uncorrected quotient is the
+// one exception, described at sa_tanhf_fast_nn).  Accuracy against
 // double-precision math, measured over every binary32 input:
 //   sa_expf <= 1.01 ulp, sa_logf <= 0.93 ulp, sa_erff <= 0.978 ulp,
 //   sa_tanhf <= 0.5031 ulp, sa_expm1f <= 1.5 ulp, sa_log1pf <= 2 ulp.
@@ -19,7 +22,7 @@
 //         on [0.921875, 2.25) and on [2.25, 3.9375); +-1 beyond.
 //   tanh: binary64 core rounded once: tanh(a) = m / (m + 2), m = e^{2a} - 1
 //         from 2a = k ln2 + 2s and e^{2s} - 1 = s (2 + s Q(s)); the quotient
-//         through Newton steps for 1 / (m + 2).
+//         m / (m + 2) as the correctly rounded binary64 quotient.
 // Binary64 fma runs at the binary32 rate on gfx950, so tanh's binary64 core
 // costs about what a binary32 evaluation with the same number of terms does,
 // and rounds correctly except within 2^-31.7 of a binary32 rounding boundary
@@ -254,15 +257,15 @@ __device__ __forceinline__ float sa_phif(float x) {
   return (x != x) ? x : p;
 }
 
-// tanh for |x| <= 9.5 as a binary64 value (larger |x| are clamped: tanh(9.5)
-// rounds to 1 in binary32); callers round it once.  A NaN x yields +1 here.
-// Only fma, add, multiply and integer operations on the bits: k comes from
-// the 1.5 * 2^52 shifter (the low word of the sum is k), 2^k is built from
-// its exponent field, and 1 / (m + 2) is three Newton steps from a seed read
-// off the exponent and leading mantissa bits (relative error <= 0.051, then
-// 0.051^8 = 2^-34.3), so the result is reproducible on any IEEE machine.
-// e^{2s} - 1 = s (2 + s Q(s)), Q of degree 5 (relative error 2^-32.0).
-__device__ __forceinline__ double sa_tanh_core(float x) {
+// tanh's binary64 core, for |x|: with a = min(|x|, 9.5) (tanh(9.5) rounds to
+// 1 in binary32), 2a = k ln2 + 2s, |s| <= ln2/4, k from the 1.5 * 2^52
+// shifter (the low word of the sum is k); e^{2s} - 1 = s (2 + s Q(s)), Q of
+// degree 5 (relative error 2^-32.0); m = e^{2a} - 1 = 2^k (e^{2s} - 1) +
+// (2^k - 1), 2^k built from its exponent field, which keeps m's relative
+// accuracy as a -> 0; h = m + 2; tanh(a) = m / h.  The callers give the
+// result x's sign, so tanh(-x) = -tanh(x) exactly.  A NaN x yields a number
+// here.
+__device__ __forceinline__ void sa_tanh_mh(float x, double& m, double& h) {
   const float a = fminf(fabsf(x), 9.5f);
   const double d = (double)a;
   const double kb = fma(d, 2.8853900817779268, 6755399441055744.0);  // 2 / ln2, 1.5 * 2^52
@@ -273,17 +276,51 @@ __device__ __forceinline__ double sa_tanh_core(float x) {
   for (int i = 1; i < 6; ++i) q = fma(q, s, kTanhQ[i]);
   const double e = s * fma(s, q, 2.0);  // e^{2s} - 1
   const double p2 = __hiloint2double((__double2loint(kb) + 1023) << 20, 0);
-  const double m = fma(p2, e, p2 - 1.0);  // e^{2a} - 1
-  const double h = m + 2.0;
-  double y = __hiloint2double(0x7FDE6238 - __double2hiint(h), 0);
-#pragma unroll
-  for (int i = 0; i < 3; ++i) y = fma(y, fma(-h, y, 1.0), y);
+  m = fma(p2, e, p2 - 1.0);  // e^{2a} - 1
+  h = m + 2.0;
+}
+// m / h to within 2^-48.5 (relative): the hardware reciprocal seed
+// (v_rcp_f64, relative error below 2^-24 on this range) and one Newton step
+// give y = (1 / h)(1 + e), |e| <= 2^-48.7, and m * y rounds once more.
+__device__ __forceinline__ double sa_tanh_quot_fast(double m, double h) {
+  double y = __builtin_amdgcn_rcp(h);
+  y = fma(y, fma(-h, y, 1.0), y);
   return m * y;
 }
-// For callers whose result is NaN whenever x is NaN anyway.
-__device__ __forceinline__ float sa_tanhf_nn(float x) { return copysignf((float)sa_tanh_core(x), x); }
+// m / h correctly rounded to binary64: the quotient q0 of sa_tanh_quot_fast
+// and one correction q0 + r y with the residual r = m - h q0 (one fma, exact
+// but for a rounding 2^-53 relative to r).  Before its final rounding the
+// corrected value is m / h within 2^-97 (relative), so it rounds to the
+// binary64 quotient unless m / h lies that close to a binary64 rounding
+// midpoint, where a quotient of two binary64 numbers can come within 2^-107
+// but, over uniformly placed values, with probability 2^-44 per element;
+// the binary32 result then changes only if that binary64 value is also a
+// binary32 rounding boundary.  Any IEEE binary64 division m / h is therefore
+// the reproducible restatement of this value.
+__device__ __forceinline__ double sa_tanh_quot(double m, double h) {
+  double y = __builtin_amdgcn_rcp(h);
+  y = fma(y, fma(-h, y, 1.0), y);
+  const double q0 = m * y;
+  const double r = fma(-h, q0, m);
+  return fma(r, y, q0);
+}
+__device__ __forceinline__ double sa_tanh_core(float x) {
+  double m, h;
+  sa_tanh_mh(x, m, h);
+  return sa_tanh_quot(m, h);
+}
+// The core with the quotient of sa_tanh_quot_fast: the same binary32 value
+// as sa_tanh_core except where m / h lies within 2^-48.5 (relative) of a
+// binary32 rounding boundary (about one element in 2^24), where it may be the
+// other neighbour.  Two binary64 fma fewer per element; gelu('tanh') forward
+// uses it.
+__device__ __forceinline__ float sa_tanhf_fast_nn(float x) {
+  double m, h;
+  sa_tanh_mh(x, m, h);
+  return copysignf((float)sa_tanh_quot_fast(m, h), x);
+}
 __device__ __forceinline__ float sa_tanhf(float x) {
-  const float y = sa_tanhf_nn(x);
+  const float y = copysignf((float)sa_tanh_core(x), x);
   return (x != x) ? x : y;
 }
 

@@ -15,7 +15,11 @@ int supa_amd_div(const supa_amd_ew_desc* d, int mode, void* stream) {
   switch (mode) {
     case SUPA_AMD_DIV_TRUE: return run_ew(SimpleFactory<DivTrueOp, true>{}, d, stream, 3);
     case SUPA_AMD_DIV_TRUNC: {
-      const int rt = half_code(d);
+      // a 16-bit quotient is rounded to its storage type before the trunc,
+      // except for an immediate (CPU-scalar) divisor: the reference's
+      // is_cpu_scalar branch (BinaryDivTruncKernel.cu:30-41) and upstream CPU
+      // truncate the float quotient there
+      const int rt = (d->noperands > 2 && d->op[2].is_scalar) ? 0 : half_code(d);
       return run_ew(DivTruncFactory{rt}, d, stream, 3);
     }
     case SUPA_AMD_DIV_FLOOR: return run_ew(SimpleFactory<DivFloorOp>{}, d, stream, 3);

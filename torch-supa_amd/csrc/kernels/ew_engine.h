@@ -174,75 +174,140 @@ __device__ __forceinline__ A fold_strided(A acc, int64_t first, int64_t stride, 
 }
 
 // ------------------------------------------------------------ CONTIG
-// U vectors per thread: thread t of workgroup b moves vectors
-// b * BS + t + u * gridDim.x * BS (u < U) of every operand, all loads issued
-// before the first element is computed.  U = 1 for streams the memory system
-// bounds; U = 2 for functors with the kHeavy trait (the binary64 tanh
-// activations), whose arithmetic is as long as their memory time: a wave's
-// second load is then in flight while it computes the first vector (c2 gelu
-// 'tanh' 66.4 -> 70.5 % of the HBM roofline; 4 vectors and persistent
-// prefetching loops were no better in a launch-shape sweep).
+// U vectors per thread: U = 1 for streams the memory system bounds; U = 2
+// for functors with the kHeavy trait (the binary64 tanh activations), whose
+// arithmetic is about as long as their memory time: a wave's second load is
+// then in flight while it computes the first vector.
 template <typename Op, typename = void> struct IsHeavy : std::false_type {};
 template <typename Op> struct IsHeavy<Op, std::void_t<decltype(Op::kHeavy)>> : std::bool_constant<Op::kHeavy> {};
 template <typename Op> constexpr int contig_unroll() { return IsHeavy<Op>::value ? 2 : 1; }
 
-template <int BS, int VEC, typename Op, typename C, typename CT, typename OT, typename... S>
-__global__ void __launch_bounds__(BS)
-k_contig(Op op, TArgs<1 + sizeof...(S)> a, int64_t n) {
+// Loads of vector v of every operand into x[k][I] (k < VEC).  BCAST: some
+// operand may be a one-element broadcast (a.mode[1 + I] != 0), a uniform
+// branch per operand; without it the loads are straight-line code.
+template <bool BCAST, int VEC, typename C, typename CT, typename... S, int... I>
+__device__ __forceinline__ void contig_load(const TArgs<1 + sizeof...(S)>& a, int64_t v,
+                                            C (&x)[VEC][sizeof...(S) > 0 ? sizeof...(S) : 1],
+                                            std::integer_sequence<int, I...>) {
+  (([&] {
+     using St = typename NthT<I, S...>::type;
+     const St* p = static_cast<const St*>(a.p[1 + I]);
+     if (BCAST && a.mode[1 + I]) {
+       const C s = load_cvt<C, CT>(p[0]);
+#pragma unroll
+       for (int k = 0; k < VEC; ++k) x[k][I] = s;
+     } else {
+       const Vec<St, VEC> w = ld_stream(reinterpret_cast<const Vec<St, VEC>*>(p + v * VEC));
+#pragma unroll
+       for (int k = 0; k < VEC; ++k) x[k][I] = load_cvt<C, CT>(w.v[k]);
+     }
+   }()),
+   ...);
+}
+
+// The full tiles: U vectors per thread, vector b * BS + t + u * nfull * BS
+// of workgroup b < nfull (the U vectors of a thread lie 1/U of the tiled
+// range apart), every one in bounds, so the loads need no guard and each
+// vector's arithmetic waits for its own loads only.  With U > 1 (the
+// arithmetic-heavy functors) the wave raises its priority while it issues
+// its loads: a wave that has just started then gets its loads out ahead of
+// the arithmetic of the waves that already hold their data, which keeps more
+// bytes in flight (c2 gelu('tanh') 75.5 -> 77.9 % of the HBM roofline).
+template <bool BCAST, int BS, int VEC, int U, typename Op, typename C, typename CT, typename OT, typename... S>
+__device__ __forceinline__ void contig_tiles(const Op& op, const TArgs<1 + sizeof...(S)>& a, uint32_t nfull) {
   constexpr int N = sizeof...(S);
-  constexpr int U = contig_unroll<Op>();
-  const int64_t nvec = n / VEC;
   const int64_t v0 = (int64_t)blockIdx.x * BS + threadIdx.x;
-  const int64_t gstride = (int64_t)gridDim.x * BS;
+  const int64_t span = (int64_t)nfull * BS;
   OT* out = static_cast<OT*>(a.p[0]);
   C x[U][VEC][N > 0 ? N : 1];
+  if constexpr (N > 0 && U > 1) __builtin_amdgcn_s_setprio(3);
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+    contig_load<BCAST, VEC, C, CT, S...>(a, v0 + u * span, x[u], std::make_integer_sequence<int, N>{});
+  if constexpr (N > 0 && U > 1) __builtin_amdgcn_s_setprio(0);
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    const int64_t v = v0 + u * gstride;
-    if (v < nvec) {
-      [&]<int... I>(std::integer_sequence<int, I...>) {
-        (([&] {
-           using St = typename NthT<I, S...>::type;
-           const St* p = static_cast<const St*>(a.p[1 + I]);
-           if (a.mode[1 + I]) {
-             const C s = load_cvt<C, CT>(p[0]);
+    Vec<OT, VEC> w;
 #pragma unroll
-             for (int k = 0; k < VEC; ++k) x[u][k][I] = s;
-           } else {
-             const Vec<St, VEC> w = ld_stream(reinterpret_cast<const Vec<St, VEC>*>(p + v * VEC));
-#pragma unroll
-             for (int k = 0; k < VEC; ++k) x[u][k][I] = load_cvt<C, CT>(w.v[k]);
-           }
-         }()),
-         ...);
-      }(std::make_integer_sequence<int, N>{});
-    }
+    for (int k = 0; k < VEC; ++k) w.v[k] = from_arith<OT>(op(x[u][k]));
+    st_stream(reinterpret_cast<Vec<OT, VEC>*>(out + (v0 + u * span) * VEC), w);
   }
-#pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const int64_t v = v0 + u * gstride;
+}
+
+// U = 1: one vector per thread, thread t of workgroup b moving vector
+// b * BS + t (guarded), the last workgroup also the last n mod VEC elements.
+// The guard costs nothing here, and the waves are short, so the kernel reads
+// its arguments in one batch before the first load: a first branch on a
+// workgroup class, with its own scalar-load round trip before the vector
+// loads, measured 6 points slower on c1 (add 79.3 -> 73.8 %).
+// U > 1: workgroups [0, nfull) take the full tiles of BS * U vectors
+// (contig_tiles); one more workgroup (launched when there is a rest) takes
+// the vectors after them, one per thread per step, and the last n mod VEC
+// elements.
+template <int BS, int VEC, typename Op, typename C, typename CT, typename OT, typename... S>
+__global__ void __launch_bounds__(BS)
+k_contig(Op op, TArgs<1 + sizeof...(S)> a, int64_t n, uint32_t nfull) {
+  constexpr int N = sizeof...(S);
+  constexpr int U = contig_unroll<Op>();
+  if constexpr (U == 1) {
+    OT* out = static_cast<OT*>(a.p[0]);
+    const int64_t nvec = n / VEC;
+    const int64_t v = (int64_t)blockIdx.x * BS + threadIdx.x;
     if (v < nvec) {
+      C x[VEC][N > 0 ? N : 1];
+      contig_load<true, VEC, C, CT, S...>(a, v, x, std::make_integer_sequence<int, N>{});
       Vec<OT, VEC> w;
 #pragma unroll
-      for (int k = 0; k < VEC; ++k) w.v[k] = from_arith<OT>(op(x[u][k]));
+      for (int k = 0; k < VEC; ++k) w.v[k] = from_arith<OT>(op(x[k]));
       st_stream(reinterpret_cast<Vec<OT, VEC>*>(out + v * VEC), w);
     }
-  }
-  // tail (fewer than VEC elements): the last workgroup
-  if (blockIdx.x == gridDim.x - 1) {
-    const int64_t t = nvec * VEC + threadIdx.x;
-    if (t < n) {
-      C y[N > 0 ? N : 1];
-      [&]<int... I>(std::integer_sequence<int, I...>) {
-        (([&] {
-           using St = typename NthT<I, S...>::type;
-           const St* p = static_cast<const St*>(a.p[1 + I]);
-           y[I] = load_cvt<C, CT>(a.mode[1 + I] ? p[0] : p[t]);
-         }()),
-         ...);
-      }(std::make_integer_sequence<int, N>{});
-      out[t] = from_arith<OT>(op(y));
+    if (blockIdx.x == gridDim.x - 1) {
+      const int64_t t = nvec * VEC + threadIdx.x;  // fewer than VEC elements
+      if (t < n) {
+        C y[N > 0 ? N : 1];
+        [&]<int... I>(std::integer_sequence<int, I...>) {
+          (([&] {
+             using St = typename NthT<I, S...>::type;
+             const St* p = static_cast<const St*>(a.p[1 + I]);
+             y[I] = load_cvt<C, CT>(a.mode[1 + I] ? p[0] : p[t]);
+           }()),
+           ...);
+        }(std::make_integer_sequence<int, N>{});
+        out[t] = from_arith<OT>(op(y));
+      }
     }
+    return;
+  }
+  if (blockIdx.x < nfull) {
+    bool bcast = false;
+#pragma unroll
+    for (int i = 1; i <= N; ++i) bcast |= a.mode[i] != 0;
+    if (bcast) contig_tiles<true, BS, VEC, U, Op, C, CT, OT, S...>(op, a, nfull);
+    else contig_tiles<false, BS, VEC, U, Op, C, CT, OT, S...>(op, a, nfull);
+    return;
+  }
+  OT* out = static_cast<OT*>(a.p[0]);
+  const int64_t nvec = n / VEC;
+  for (int64_t v = (int64_t)nfull * BS * U + threadIdx.x; v < nvec; v += BS) {
+    C x[VEC][N > 0 ? N : 1];
+    contig_load<true, VEC, C, CT, S...>(a, v, x, std::make_integer_sequence<int, N>{});
+    Vec<OT, VEC> w;
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) w.v[k] = from_arith<OT>(op(x[k]));
+    st_stream(reinterpret_cast<Vec<OT, VEC>*>(out + v * VEC), w);
+  }
+  const int64_t t = nvec * VEC + threadIdx.x;  // fewer than VEC elements
+  if (t < n) {
+    C y[N > 0 ? N : 1];
+    [&]<int... I>(std::integer_sequence<int, I...>) {
+      (([&] {
+         using St = typename NthT<I, S...>::type;
+         const St* p = static_cast<const St*>(a.p[1 + I]);
+         y[I] = load_cvt<C, CT>(a.mode[1 + I] ? p[0] : p[t]);
+       }()),
+       ...);
+    }(std::make_integer_sequence<int, N>{});
+    out[t] = from_arith<OT>(op(y));
   }
 }
 

@@ -180,8 +180,15 @@ int launch_static(const Op& op, const supa_amd_ew_desc& d, const int* tin, hipSt
       // of peak against 47-60 % with one
       constexpr int BS = N == 0 ? kBlock : kStreamBlock;
       constexpr int U = contig_unroll<Op>();
-      const int64_t blocks = std::max<int64_t>(1, (n / VEC + BS * U - 1) / (BS * U));
-      k_contig<BS, VEC, Op, C, CT, OT, S...><<<dim3((unsigned)blocks), dim3(BS), 0, st>>>(op, a, n);
+      int64_t blocks, nfull = 0;
+      if (U == 1) {  // one guarded vector per thread
+        blocks = std::max<int64_t>(1, (n / VEC + BS - 1) / BS);
+      } else {  // full tiles of BS * U vectors, plus one workgroup for the rest
+        nfull = n / VEC / (BS * U);
+        blocks = nfull + (nfull * BS * U * VEC < n ? 1 : 0);
+      }
+      k_contig<BS, VEC, Op, C, CT, OT, S...><<<dim3((unsigned)blocks), dim3(BS), 0, st>>>(op, a, n,
+                                                                                          (uint32_t)nfull);
       return launch_status();
     }
   }

@@ -49,10 +49,14 @@ template <typename C> struct DivTrueOp {
   __device__ __forceinline__ C operator()(const C* x) const { return x[0] / x[1]; }
 };
 // trunc division (BinaryDivTruncKernel.cu:22-55): std::trunc(a / b) on the
-// storage type, so for bf16 / f16 the quotient is rounded to that type before
-// it is truncated (rt 1: bf16, 2: f16; c10's 16-bit division computes in
-// float and rounds).  Integer division by zero has no defined value on the
-// device; it yields 0 here.
+// storage type, so for bf16 / f16 tensor operands the quotient is rounded to
+// that type before it is truncated (rt 1: bf16, 2: f16; c10's 16-bit division
+// computes in float and rounds).  An immediate (CPU-scalar) divisor takes
+// rt 0: the float quotient is truncated, as the reference's is_cpu_scalar
+// branch (:30-41) and upstream CPU do; the quotient is the IEEE a / b, where
+// that branch multiplies by a float reciprocal (the same choice as true
+// division's, for bit-exact agreement with the CPU).  Integer division by
+// zero has no defined value on the device; it yields 0 here.
 template <typename C> struct DivTruncOp {
   static constexpr int arity = 2;
   int rt = 0;
@@ -128,7 +132,7 @@ template <typename C> __device__ __forceinline__ C gelu_tanh(C x) {
   const C x3 = (x * x) * x;
   if constexpr (std::is_same<C, float>::value) {
     const float inner = (float)kGeluBetaTanh * fmaf((float)kGeluKappa, x3, x);
-    return (0.5f * x) * (1.0f + sa_tanhf_nn(inner));  // a NaN x makes 0.5 x NaN
+    return (0.5f * x) * (1.0f + sa_tanhf_fast_nn(inner));  // a NaN x makes 0.5 x NaN
   } else {
     const C inner = C(kGeluBetaTanh) * fma(C(kGeluKappa), x3, x);
     return (C(0.5) * x) * (C(1) + tanh(inner));
