@@ -78,6 +78,34 @@ def test_activations_ladder_bit_exact(shape, no_fallback):
         assert np.array_equal(fn(dx).cpu().numpy(), O.unary(op, xn))
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_opt_in_accurate_gelu_forms(dtype, no_fallback):
+    """torch.supa.set_accurate_gelu_enabled(True) selects the cancellation-free
+    forms for both approximations, forward (x - (x/2) erfc(|x|/sqrt2) through
+    log erfc; x / (1 + e^{-2u})) and backward: bit-exact against the oracle's
+    GELU_LOGERFC / GELU_TANH_LOGISTIC in float32, and those rounded once to
+    bfloat16 for bf16 tensors.  The switch is restored afterwards."""
+    x = seeded((1000, 257), 60, 3.0)
+    dy = seeded((1000, 257), 61)
+    if dtype == torch.bfloat16:
+        x, dy = x.to(dtype), dy.to(dtype)
+    xn, dyn = x.float().numpy(), dy.float().numpy()
+    was = torch.supa.accurate_gelu_enabled()
+    try:
+        torch.supa.set_accurate_gelu_enabled(True)
+        for approx, op in [("none", O.GELU_LOGERFC), ("tanh", O.GELU_TANH_LOGISTIC)]:
+            y = F.gelu(dev(x), approximate=approx).cpu().float().numpy()
+            gx = torch.ops.aten.gelu_backward(dev(dy), dev(x), approximate=approx).cpu().float().numpy()
+            want_y, want_gx = O.unary(op, xn), O.unary_backward(op, dyn, xn)
+            if dtype == torch.bfloat16:
+                want_y, want_gx = O.round_bf16(want_y), O.round_bf16(want_gx)
+            assert np.array_equal(y, want_y), approx
+            assert np.array_equal(gx, want_gx), approx
+    finally:
+        torch.supa.set_accurate_gelu_enabled(was)
+    assert torch.supa.accurate_gelu_enabled() == was
+
+
 def test_activation_backward_through_autograd(no_fallback):
     x = seeded((1000, 257), 4, 3.0)
     dy = seeded((1000, 257), 5)

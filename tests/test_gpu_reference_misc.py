@@ -1,5 +1,8 @@
 """The reference's small tensor tests, case for case: test_tensor_factories.py
-(eye n and n x m exact, empty, empty_strided's strides), test_equal.py
+(eye n and n x m exact, empty, empty_strided's strides), test_native_ci.py's
+test_deterministic_empty_float32 (every factory form filled with NaN under
+deterministic algorithms; here also the integer maximum and resize_'s new
+bytes, as upstream), test_equal.py
 (torch.equal on random pairs in three dtypes, plus equal and NaN pairs
 here), test_resize.py (resize_ to the same element count keeps the data) and
 test_cuda_scalar.py (_local_scalar_dense reads the first element of any
@@ -7,8 +10,10 @@ tensor, as upstream's does), test_one_hot_fused.py (one_hot, whose
 scatter_ runs on the device) and test_normalize_fused.py (F.normalize: the
 vector norm, clamp_min and the division, all device kernels; the reference
 calls its own torch.normalize, which upstream torch does not have)."""
-import numpy as np
+import contextlib
 import copy
+
+import numpy as np
 
 import pytest
 import torch
@@ -34,6 +39,60 @@ def test_empty_and_empty_strided(no_fallback):
     c = torch.empty_strided((2, 3), (1, 2))
     s = torch.empty_strided((2, 3), (1, 2), device=SUPA)
     assert c.stride() == s.stride() and c.size() == s.size()
+
+
+@contextlib.contextmanager
+def _deterministic_fill_enabled():
+    was_enabled = torch.are_deterministic_algorithms_enabled()
+    was_warn_only = torch.is_deterministic_algorithms_warn_only_enabled()
+    was_fill = torch.utils.deterministic.fill_uninitialized_memory
+    torch.use_deterministic_algorithms(True)
+    torch.utils.deterministic.fill_uninitialized_memory = True
+    try:
+        yield
+    finally:
+        torch.use_deterministic_algorithms(was_enabled, warn_only=was_warn_only)
+        torch.utils.deterministic.fill_uninitialized_memory = was_fill
+
+
+def _factories(dtype):
+    """test_native_ci.py:51-78: the factory forms of the reference's test."""
+    return [
+        lambda: torch.empty(10, 9, device=SUPA, dtype=dtype),
+        lambda: torch.empty(10, 9, out=torch.zeros(1, device=SUPA, dtype=dtype)),
+        lambda: torch.empty_like(torch.zeros(10, 9, device=SUPA, dtype=dtype)),
+        lambda: torch.empty_like(torch.zeros(10, 9, device=SUPA, dtype=dtype), memory_format=torch.contiguous_format),
+        lambda: torch.empty_strided((10, 9), (1, 5), device=SUPA, dtype=dtype),
+        lambda: torch.empty_permuted((2, 3, 5), (1, 0, 2), device=SUPA, dtype=dtype),
+    ]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_deterministic_empty_is_nan(dtype, no_fallback):
+    for i, gen_fn in enumerate(_factories(dtype)):
+        torch.supa.empty_cache()
+        with _deterministic_fill_enabled():
+            result = gen_fn()
+        assert result.device.type == "supa"
+        assert bool(result.isnan().all()), i
+
+
+def test_deterministic_empty_integers_and_resize(no_fallback):
+    """Integers take the type's maximum (upstream fill_empty_deterministic_);
+    resize_ fills the bytes a grown storage adds and keeps the old ones."""
+    with _deterministic_fill_enabled():
+        t = torch.empty(7, 5, device=SUPA, dtype=torch.int32)
+        assert bool((t.cpu() == torch.iinfo(torch.int32).max).all())
+        t = torch.empty_strided((4, 3), (1, 4), device=SUPA, dtype=torch.int64)
+        assert bool((t.cpu() == torch.iinfo(torch.int64).max).all())
+        x = torch.arange(6, dtype=torch.float32).to(SUPA)
+        x.resize_(4, 3)
+        got = x.cpu().flatten()
+        assert torch.equal(got[:6], torch.arange(6, dtype=torch.float32))
+        assert bool(got[6:].isnan().all())
+    # with the switch off, nothing is filled (no extra kernel): the values are
+    # whatever the block held, so only the shape is checked
+    assert torch.empty(10, 9, device=SUPA).shape == (10, 9)
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
@@ -113,3 +172,22 @@ def test_scatter_value(dim, dtype, no_fallback):
     bad.view(-1)[5] = base.shape[d]
     with pytest.raises(IndexError, match="scatter_ index"):
         base.to(SUPA).scatter_(dim, bad.to(SUPA), value).cpu()
+
+
+def test_scatter_value_conversions(no_fallback):
+    """The scalar in the destination's type, as upstream's value.to<T>(): a
+    float scalar into bool is value != 0 (0.5 -> True), into an integer type
+    it truncates, and an integer destination refuses a value it cannot hold;
+    a destination that overlaps itself is refused."""
+    g = torch.Generator().manual_seed(32)
+    index = torch.randint(0, 9, (4, 9), generator=g)
+    for dtype, value in [(torch.bool, 0.5), (torch.bool, 0.0), (torch.int32, 3.75), (torch.int64, -2.5),
+                         (torch.uint8, 200.0)]:
+        base = torch.zeros(4, 9, dtype=dtype)
+        want = base.clone().scatter_(1, index, value)
+        got = base.to(SUPA).scatter_(1, index.to(SUPA), value)
+        assert torch.equal(got.cpu(), want), (dtype, value)
+    with pytest.raises(RuntimeError):
+        torch.zeros(4, 9, dtype=torch.int8, device=SUPA).scatter_(1, index.to(SUPA), 1e10)
+    with pytest.raises(RuntimeError, match="unsupported operation|overlap"):
+        torch.zeros(1, device=SUPA).expand(4, 9).scatter_(1, index.to(SUPA), 1.0)

@@ -117,18 +117,22 @@ def test_record_stream_defers_reuse(supa):
     torch.supa.empty_cache()  # no other cached block of this size class
     m = (1 << 22) + 7919
     s = torch.supa.Stream()
-    s.wait_stream(torch.supa.current_stream())
     big = torch.randn(1 << 24).to("supa")
     x = torch.ones(m, device="supa")
     p = x.data_ptr()
+    s.wait_stream(torch.supa.current_stream())  # s reads x and big after they are written
     keep = _busy(s, big)  # s is busy for a while
     with torch.supa.stream(s):
         y = x * 2  # s reads x after the busy work
     x.record_stream(s)
     del x
     assert torch.supa.memory_stats()["pending_blocks"] >= 1
+    busy_before = not s.query()
     w = torch.empty(m, device="supa")
-    assert w.data_ptr() != p  # s has not finished with the block yet
+    busy_after = not s.query()
+    assert busy_before  # milliseconds of queued work: s cannot have drained yet
+    if busy_after:  # s busy throughout the allocation: its event had not completed
+        assert w.data_ptr() != p
     s.synchronize()
     w2 = torch.empty(m, device="supa")
     assert w2.data_ptr() == p  # s's event completed: the block is back
@@ -155,3 +159,32 @@ def test_injected_oom_is_retried_then_raised(supa):
         _C.inject_oom(0)
     u = torch.ones(5 << 20, device="supa")  # the allocator still works
     assert float(u.sum()) == float(5 << 20)
+
+
+def test_index_errors_are_reported_per_stream(supa):
+    """A bad nll target on a side stream sets that stream's error flag: a
+    read on the default stream (which did not wait for it) does not report
+    it; a read on the side stream after it synchronises does, once."""
+    import torch.nn.functional as F
+    torch.supa.synchronize()
+    g = torch.Generator().manual_seed(5)
+    lp = torch.log_softmax(torch.randn(8, 10, generator=g), 1).to("supa")
+    bad = torch.tensor([0, 1, 2, 3, 4, 5, 6, 12]).to("supa")
+    good = torch.zeros(8, dtype=torch.int64).to("supa")
+    s = torch.supa.Stream()
+    s.wait_stream(torch.supa.current_stream())
+    with torch.supa.stream(s):
+        loss_bad = F.nll_loss(lp, bad)
+    s.synchronize()
+    # the default stream's own work reads clean
+    assert F.nll_loss(lp, good).item() == pytest.approx(-lp[:, 0].mean().item(), rel=1e-6)
+    with torch.supa.stream(s):
+        with pytest.raises(IndexError):
+            loss_bad.item()
+        assert F.nll_loss(lp, good).item() == pytest.approx(-lp[:, 0].mean().item(), rel=1e-6)  # cleared
+    # torch.supa.synchronize() reads every stream's flag
+    with torch.supa.stream(s):
+        F.nll_loss(lp, bad)
+    with pytest.raises(IndexError):
+        torch.supa.synchronize()
+    torch.supa.synchronize()  # cleared

@@ -81,12 +81,21 @@ void allocator_inject_oom(int n);
 // target) and the host clears when it reads it.  Reduction workspaces are not
 // here: they come from the caching allocator per call, ordered on the
 // calling stream.
+// Device-side error flags: one int32 per stream of a device (the default
+// stream and the pool), in one 256-byte block.  A kernel that finds a bad
+// index (an nll_loss target, a scatter_ index) sets the flag of the stream it
+// runs on, so a flag is read only once that stream's work is done.
 struct DeviceScratch {
-  int32_t* error_flag = nullptr;
+  int32_t* error_flags = nullptr;  // [stream id], ids 0..32
 };
 const DeviceScratch& device_scratch(c10::DeviceIndex d);
-// Raises (and clears) a pending device-side error, e.g. an out-of-range
-// nll_loss target.  Called at every host synchronisation point.
+// The flag of device d's current stream, for the kernels launched on it.
+int32_t* stream_error_flag(c10::DeviceIndex d);
+// Raises (and clears) a pending device-side error of device d's current
+// stream, e.g. an out-of-range nll_loss target.  Called after the current
+// stream has synchronised (device-to-host copies, .item(), launch-blocking
+// mode); an error of a kernel on another stream is reported once that stream
+// has been synchronised (or by torch.supa.synchronize()).
 void check_device_errors(c10::DeviceIndex d);
 
 // CPU fallback bookkeeping (the fallback never runs for an op this library

@@ -14,6 +14,8 @@
 #include <ATen/ExpandUtils.h>
 #include <ATen/MemoryOverlap.h>
 #include <ATen/native/Resize.h>
+#include <ATen/native/ResizeCommon.h>
+#include <ATen/native/TensorFactories.h>
 #include <ATen/ops/as_strided_native.h>
 #include <ATen/ops/view_native.h>
 #include <ATen/ops/_reshape_alias_native.h>
@@ -165,6 +167,16 @@ void check_cast(c10::ScalarType common, const at::Tensor& out, const char* name)
 }
 
 // ----------------------------------------------------- factories / views
+// Under torch.use_deterministic_algorithms(True) with
+// torch.utils.deterministic.fill_uninitialized_memory (its default), new
+// tensors are filled with NaN (floating types) or the type's maximum
+// (integers), as the reference's empty / empty_strided
+// (torch_supa/csrc/aten/common/TensorFactories.cpp:18-50) and upstream's.
+bool deterministic_fill() {
+  return C10_UNLIKELY(at::globalContext().deterministicAlgorithms() &&
+                      at::globalContext().deterministicFillUninitializedMemory());
+}
+
 at::Tensor empty_memory_format(c10::IntArrayRef size, std::optional<c10::ScalarType> dtype,
                                std::optional<c10::Layout> layout, std::optional<c10::Device> device,
                                std::optional<bool> pin_memory, std::optional<c10::MemoryFormat> fmt) {
@@ -172,7 +184,9 @@ at::Tensor empty_memory_format(c10::IntArrayRef size, std::optional<c10::ScalarT
   TORCH_CHECK(!pin_memory || !*pin_memory, "supa: pin_memory applies to CPU tensors only");
   const auto dt = dtype.value_or(default_float());
   const c10::DeviceIndex dev = device && device->has_index() ? device->index() : current_device();
-  return empty_supa(size, dt, dev, fmt.value_or(c10::MemoryFormat::Contiguous));
+  at::Tensor t = empty_supa(size, dt, dev, fmt.value_or(c10::MemoryFormat::Contiguous));
+  if (deterministic_fill()) at::native::fill_empty_deterministic_(t);
+  return t;
 }
 
 at::Tensor empty_strided(c10::IntArrayRef size, c10::IntArrayRef stride, std::optional<c10::ScalarType> dtype,
@@ -181,7 +195,9 @@ at::Tensor empty_strided(c10::IntArrayRef size, c10::IntArrayRef stride, std::op
   TORCH_CHECK(!layout || *layout == c10::Layout::Strided, "supa: only strided tensors are supported");
   const auto dt = dtype.value_or(default_float());
   const c10::DeviceIndex dev = device && device->has_index() ? device->index() : current_device();
-  return empty_strided_supa(size, stride, dt, dev);
+  at::Tensor t = empty_strided_supa(size, stride, dt, dev);
+  if (deterministic_fill()) at::native::fill_empty_deterministic_(t);
+  return t;
 }
 
 const at::Tensor& resize_(const at::Tensor& self, c10::IntArrayRef size, std::optional<c10::MemoryFormat> fmt) {
@@ -193,11 +209,14 @@ const at::Tensor& resize_(const at::Tensor& self, c10::IntArrayRef size, std::op
   const size_t needed =
       at::detail::computeStorageNbytesContiguous(size, self.dtype().itemsize(), impl->storage_offset());
   const c10::Storage& storage = impl->unsafe_storage();
+  const int64_t old_nbytes = (int64_t)storage.nbytes();
   if (needed > storage.nbytes()) {
     TORCH_CHECK(storage.resizable(), "supa: trying to resize storage that is not resizable");
     at::detail::getPrivateUse1Hooks().resizePrivateUse1Bytes(storage, needed);
   }
   if (fmt) impl->empty_tensor_restride(*fmt);
+  // the bytes a grown storage adds, as upstream's resize_
+  if (deterministic_fill()) at::native::fill_resize_deterministic_(self, old_nbytes);
   return self;
 }
 
@@ -294,12 +313,25 @@ at::Tensor& scatter_value_(at::Tensor& self, int64_t dim, const at::Tensor& inde
   }
   TORCH_CHECK(nd <= SUPA_AMD_MAX_DIMS, "scatter_: supa supports up to ", SUPA_AMD_MAX_DIMS, " dimensions");
   TORCH_CHECK(dtype_supported(self.scalar_type()), "scatter_: unsupported dtype ", self.scalar_type());
+  at::assert_no_internal_overlap(self);
+  // the value in the destination's type, as upstream's value.to<scalar_t>()
+  // (a checked conversion: an integer destination refuses a value it cannot
+  // hold; a bool destination takes value != 0)
+  int64_t ivalue = 0;
+  switch (self.scalar_type()) {
+    case at::kBool: ivalue = value.to<bool>() ? 1 : 0; break;
+    case at::kByte: ivalue = value.to<uint8_t>(); break;
+    case at::kChar: ivalue = value.to<int8_t>(); break;
+    case at::kShort: ivalue = value.to<int16_t>(); break;
+    case at::kInt: ivalue = value.to<int32_t>(); break;
+    case at::kLong: ivalue = value.to<int64_t>(); break;
+    default: break;  // floating destinations take the double
+  }
   const auto dev = self.device().index();
   const int rc = supa_amd_scatter_fill(out.data_ptr(), dtype_code(out.scalar_type()), out.strides().data(),
                                        out.size(wd), idx.data_ptr<int64_t>(), idx.sizes().data(),
-                                       idx.strides().data(), (int32_t)nd, (int32_t)wd, value.toDouble(),
-                                       value.isIntegral(true) ? value.toLong() : (int64_t)value.toDouble(),
-                                       device_scratch(dev).error_flag, current_stream(dev));
+                                       idx.strides().data(), (int32_t)nd, (int32_t)wd, value.toDouble(), ivalue,
+                                       stream_error_flag(dev), current_stream(dev));
   check_status(rc, "scatter_");
   return self;
 }

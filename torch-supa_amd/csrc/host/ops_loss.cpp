@@ -533,10 +533,10 @@ std::tuple<at::Tensor&, at::Tensor&> nll_fwd_into(const at::Tensor& self, const 
   at::Tensor t = target.contiguous();
   at::Tensor w = weight.defined() ? to_dtype(weight, self.scalar_type()).contiguous() : at::Tensor();
   if (red == SUPA_AMD_REDUCTION_NONE) tw.zero_();
-  const DeviceScratch& s = device_scratch(dev);
+  int32_t* const eflag = stream_error_flag(dev);
   const int rc = supa_amd_nll_loss_forward(x.data_ptr(), dtype_code(x.scalar_type()), t.data_ptr<int64_t>(),
                                            w.defined() ? w.data_ptr() : nullptr, n, c, red, ignore_index,
-                                           out.data_ptr(), tw.data_ptr(), s.error_flag, current_stream(dev));
+                                           out.data_ptr(), tw.data_ptr(), eflag, current_stream(dev));
   check_status(rc, "nll_loss_forward");
   return {out, tw};
 }
@@ -572,12 +572,12 @@ at::Tensor& nll_bwd_into(const at::Tensor& grad, const at::Tensor& self, const a
   at::Tensor tw = to_dtype(total_weight, self.scalar_type());
   if (red == SUPA_AMD_REDUCTION_NONE && self.dim() == 2)
     TORCH_CHECK(g.numel() == n, "Expected a tensor of dimension 1 and tensor.size[0] == ", n);
-  const DeviceScratch& s = device_scratch(dev);
+  int32_t* const eflag = stream_error_flag(dev);
   const int rc = supa_amd_nll_loss_backward(g.data_ptr(), dtype_code(self.scalar_type()), t.data_ptr<int64_t>(),
                                             w.defined() ? w.data_ptr() : nullptr, tw.data_ptr(), n, c,
                                             red == SUPA_AMD_REDUCTION_NONE && self.dim() == 1 ? SUPA_AMD_REDUCTION_SUM
                                                                                                : red,
-                                            ignore_index, res.data_ptr(), s.error_flag, current_stream(dev));
+                                            ignore_index, res.data_ptr(), eflag, current_stream(dev));
   check_status(rc, "nll_loss_backward");
   if (!res.is_same(gi)) gi.copy_(res);
   return gi;
@@ -632,13 +632,13 @@ std::tuple<at::Tensor&, at::Tensor&> nll2d_fwd_into(const at::Tensor& self, cons
   at::Tensor w = weight.defined() ? to_dtype(weight, self.scalar_type()).contiguous() : at::Tensor();
   if (red == SUPA_AMD_REDUCTION_NONE) tw.zero_();
   at::Tensor res = out.is_contiguous() ? out : empty_supa(oshape, self.scalar_type(), dev);
-  const DeviceScratch& s = device_scratch(dev);
+  int32_t* const eflag = stream_error_flag(dev);
   const int64_t ws_bytes = supa_amd_nll_loss2d_workspace_bytes();
   const at::Tensor ws = empty_supa({ws_bytes}, at::kByte, dev);
   const int rc = supa_amd_nll_loss2d_forward(x.data_ptr(), dtype_code(x.scalar_type()), t.data_ptr<int64_t>(),
                                              w.defined() ? w.data_ptr() : nullptr, n, c, sp, red, ignore_index,
                                              res.data_ptr(), tw.data_ptr(), ws.data_ptr(), ws_bytes,
-                                             s.error_flag, current_stream(dev));
+                                             eflag, current_stream(dev));
   check_status(rc, "nll_loss2d_forward");
   if (!res.is_same(out)) out.copy_(res);
   return {out, tw};
@@ -680,10 +680,10 @@ at::Tensor& nll2d_bwd_into(const at::Tensor& grad, const at::Tensor& self, const
   at::Tensor t = target.contiguous();
   at::Tensor w = weight.defined() ? to_dtype(weight, self.scalar_type()).contiguous() : at::Tensor();
   at::Tensor tw = to_dtype(total_weight, self.scalar_type());
-  const DeviceScratch& s = device_scratch(dev);
+  int32_t* const eflag = stream_error_flag(dev);
   const int rc = supa_amd_nll_loss2d_backward(g.data_ptr(), dtype_code(self.scalar_type()), t.data_ptr<int64_t>(),
                                               w.defined() ? w.data_ptr() : nullptr, tw.data_ptr(), n, c, sp, red,
-                                              ignore_index, res.data_ptr(), s.error_flag, current_stream(dev));
+                                              ignore_index, res.data_ptr(), eflag, current_stream(dev));
   check_status(rc, "nll_loss2d_backward");
   if (!res.is_same(gi)) gi.copy_(res);
   return gi;
@@ -834,11 +834,11 @@ class FusedCrossEntropy : public torch::autograd::Function<FusedCrossEntropy> {
     at::Tensor lse = empty_supa({n}, at::kFloat, dev);
     at::Tensor count = empty_supa({}, at::kFloat, dev);
     at::Tensor ws = empty_supa({std::max<int64_t>(n, 1)}, at::kFloat, dev);
-    const DeviceScratch& s = device_scratch(dev);
+    int32_t* const eflag = stream_error_flag(dev);
     const int rc = supa_amd_cross_entropy_forward(x.data_ptr(), dtype_code(x.scalar_type()), t.data_ptr<int64_t>(), n,
                                                   c, ignore_index, red, out.data_ptr(), lse.data_ptr<float>(),
                                                   count.data_ptr<float>(), ws.data_ptr(), ws.numel() * 4,
-                                                  s.error_flag, current_stream(dev));
+                                                  eflag, current_stream(dev));
     check_status(rc, "cross_entropy (fused forward)");
     ctx->save_for_backward({x, t, lse, count});
     ctx->saved_data["reduction"] = reduction;
@@ -859,11 +859,11 @@ class FusedCrossEntropy : public torch::autograd::Function<FusedCrossEntropy> {
     const auto dev = x.device().index();
     at::Tensor g = to_dtype(grads[0], x.scalar_type()).contiguous();
     at::Tensor gx = empty_supa(x.sizes(), x.scalar_type(), dev);
-    const DeviceScratch& s = device_scratch(dev);
+    int32_t* const eflag = stream_error_flag(dev);
     const int rc = supa_amd_cross_entropy_backward(g.data_ptr(), x.data_ptr(), dtype_code(x.scalar_type()),
                                                    t.data_ptr<int64_t>(), lse.data_ptr<float>(),
                                                    count.data_ptr<float>(), n, c, ignore_index, red, gx.data_ptr(),
-                                                   s.error_flag, current_stream(dev));
+                                                   eflag, current_stream(dev));
     check_status(rc, "cross_entropy (fused backward)");
     return {gx, at::Tensor(), at::Tensor(), at::Tensor()};
   }

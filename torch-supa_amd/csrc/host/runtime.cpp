@@ -203,55 +203,77 @@ void memcpy_d2h(void* dst, const void* src, size_t n, c10::DeviceIndex d) {
   SUPA_HIP_CHECK(hipStreamSynchronize(st));
 }
 
+namespace {
+constexpr int kScratchDevices = 64;
+constexpr int kFlagSlots = 64;  // int32 slots in the 256-byte flag block: ids 0..kPoolStreams
+static_assert(kPoolStreams + 1 <= kFlagSlots, "one error flag per stream");
+std::mutex g_scratch_mu;
+DeviceScratch g_scratch[kScratchDevices];
+
+// Reads and clears flags [first, first + n) of device d on its current
+// stream (which the caller has synchronised, or every stream has been), and
+// raises the first error found.
+void check_flags(c10::DeviceIndex d, int first, int n) {
+  int32_t* flags = nullptr;
+  {
+    std::lock_guard<std::mutex> g(g_scratch_mu);
+    if (d < 0 || d >= kScratchDevices || !g_scratch[d].error_flags) return;
+    flags = g_scratch[d].error_flags;
+  }
+  int32_t h[kFlagSlots] = {};
+  memcpy_d2h(h, flags + first, sizeof(int32_t) * n, d);
+  int32_t code = 0;
+  for (int i = 0; i < n; ++i) {
+    if (h[i] != 0) {
+      if (code == 0) code = h[i];
+      const int32_t zero = 0;
+      memcpy_h2d(flags + first + i, &zero, sizeof(zero), d);
+    }
+  }
+  if (code != 0) {
+    TORCH_CHECK_INDEX(code != 2, "supa: a kernel reported an out-of-bounds index (a scatter_ index outside the "
+                                 "destination's size along dim)");
+    TORCH_CHECK_INDEX(false, "supa: a kernel reported an out-of-bounds target index (nll_loss target outside "
+                             "[0, n_classes) and not ignore_index)");
+  }
+}
+}  // namespace
+
 void synchronize(c10::DeviceIndex d) {
   const auto prev = current_device();
   set_device(d);
   SUPA_HIP_CHECK(hipDeviceSynchronize());
   set_device(prev);
-  check_device_errors(d);
+  check_flags(d, 0, kPoolStreams + 1);  // every stream has drained
 }
-
-namespace {
-constexpr int kScratchDevices = 64;
-std::mutex g_scratch_mu;
-DeviceScratch g_scratch[kScratchDevices];
-}  // namespace
 
 const DeviceScratch& device_scratch(c10::DeviceIndex d) {
   TORCH_CHECK(d >= 0 && d < kScratchDevices, "supa: device index out of range");
   std::lock_guard<std::mutex> g(g_scratch_mu);
   DeviceScratch& s = g_scratch[d];
-  if (!s.error_flag) {
+  if (!s.error_flags) {
     const auto prev = current_device();
     if (prev != d) set_device(d);
     void* p = nullptr;
-    SUPA_HIP_CHECK(hipMalloc(&p, 256));
+    SUPA_HIP_CHECK(hipMalloc(&p, sizeof(int32_t) * kFlagSlots));
     const hipStream_t st = stream_handle(d, 0);
-    SUPA_HIP_CHECK(hipMemsetAsync(p, 0, 256, st));
+    SUPA_HIP_CHECK(hipMemsetAsync(p, 0, sizeof(int32_t) * kFlagSlots, st));
     SUPA_HIP_CHECK(hipStreamSynchronize(st));
-    s.error_flag = static_cast<int32_t*>(p);
+    s.error_flags = static_cast<int32_t*>(p);
     if (prev != d) set_device(prev);
   }
   return s;
 }
 
+int32_t* stream_error_flag(c10::DeviceIndex d) {
+  int32_t* base = device_scratch(d).error_flags;
+  (void)streams_of(d);
+  return base + tls_stream[d];
+}
+
 void check_device_errors(c10::DeviceIndex d) {
-  int32_t* flag = nullptr;
-  {
-    std::lock_guard<std::mutex> g(g_scratch_mu);
-    if (d < 0 || d >= kScratchDevices || !g_scratch[d].error_flag) return;
-    flag = g_scratch[d].error_flag;
-  }
-  int32_t h = 0;
-  memcpy_d2h(&h, flag, sizeof(h), d);
-  if (h != 0) {
-    const int32_t zero = 0;
-    memcpy_h2d(flag, &zero, sizeof(zero), d);
-    TORCH_CHECK_INDEX(h != 2, "supa: a kernel reported an out-of-bounds index (a scatter_ index outside the "
-                              "destination's size along dim)");
-    TORCH_CHECK_INDEX(false, "supa: a kernel reported an out-of-bounds target index (nll_loss target outside "
-                             "[0, n_classes) and not ignore_index)");
-  }
+  if (d < 0 || d >= kStreamDevices) return;
+  check_flags(d, (int)tls_stream[d], 1);
 }
 
 // ------------------------------------------------------------- allocator
