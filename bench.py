@@ -212,11 +212,12 @@ def bench_c3(torch, timer, iters=10):
     # the opt-in fused path (not the config's decomposition): forward reads the
     # logits once, backward reads them once and writes the gradient once --
     # 6 N V bytes plus per-row targets, lse and losses
+    was = torch.supa.fused_cross_entropy_enabled()
     torch.supa.set_fused_cross_entropy_enabled(True)
     try:
         ms_f = timer.time(step, iters, warmup=2)
     finally:
-        torch.supa.set_fused_cross_entropy_enabled(False)
+        torch.supa.set_fused_cross_entropy_enabled(was)
     fused_bytes = 6 * C3_NV + C3_N * (8 + 4 + 4) * 2
     res["fused_fwd_bwd"] = dict(entry(fused_bytes, ms_f), rows_per_s=round(C3_N / (ms_f * 1e-3), 1),
                                 speedup_vs_decomposition=round(ms / ms_f, 3))
@@ -234,7 +235,49 @@ def bench_c3(torch, timer, iters=10):
     gi = torch.empty_like(lx)
     res["_log_softmax_backward_data"] = entry(C3_BYTES["_log_softmax_backward_data"], timer.time(
         lambda: torch.ops.aten._log_softmax_backward_data.out(gn, lsm, 1, torch.bfloat16, out=gi), iters))
+    del lsm, gn, gi, lx
+    logits.grad = None
+    del logits
+    res["fp32_routing"] = bench_c3_fp32(torch, timer, tgt)
     return res
+
+
+def bench_c3_fp32(torch, timer, tgt, iters=5):
+    """c3's shape with float32 logits (not the config: the reference's routing
+    of float32 cross-entropy).  fused: the default route, as the reference
+    routes 2-d float32 logits to its fast path; decomposition: the
+    log_softmax + nll_loss route that bfloat16 takes.  Also 512 rows with a
+    probability target [512, 128256] float32, fused and decomposed."""
+    import torch.nn.functional as F
+    x = gen(torch, (C3_N, C3_V), 4, torch.float32, b=2.0).requires_grad_()
+    was = torch.supa.fused_cross_entropy_enabled()
+    out = {}
+    try:
+        for name, mode in (("fused", True), ("decomposition", False)):
+            torch.supa.set_fused_cross_entropy_enabled(mode)
+
+            def step():
+                x.grad = None
+                F.cross_entropy(x, tgt, ignore_index=-100).backward()
+            ms = timer.time(step, iters, warmup=2)
+            # fused: 4 NV forward + 8 NV backward; decomposition: _log_softmax 8 NV, nll_loss_backward 4 NV,
+            # _log_softmax_backward_data 12 NV (float32 bytes)
+            nbytes = (12 if mode else 24) * C3_NV
+            out[name] = dict(entry(nbytes, ms), rows_per_s=round(C3_N / (ms * 1e-3), 1))
+        out["fused_speedup"] = round(out["decomposition"]["ms"] / out["fused"]["ms"], 3)
+        xp = x.detach()[:512].clone().requires_grad_()
+        p = gen(torch, (512, C3_V), 11, torch.float32, kind="uniform", a=0.0, b=2.0 / C3_V)
+        for name, mode in (("prob_fused", True), ("prob_decomposition", False)):
+            torch.supa.set_fused_cross_entropy_enabled(mode)
+
+            def stepp():
+                xp.grad = None
+                F.cross_entropy(xp, p).backward()
+            ms = timer.time(stepp, iters, warmup=2)
+            out[name] = {"ms": round(ms, 5), "rows": 512}
+    finally:
+        torch.supa.set_fused_cross_entropy_enabled(was)
+    return out
 
 
 def bench_c4(torch, timer, iters=21, sets=3):

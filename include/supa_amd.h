@@ -552,6 +552,27 @@ int supa_amd_cross_entropy_backward(const void* grad_out, const void* logits, in
                                     int64_t c, int64_t ignore_index, int reduction, void* grad_logits,
                                     int32_t* error_flag, void* stream);
 
+/* Probability (soft-label) targets: target is [n, c] in the logits' dtype
+ * (both contiguous); loss_i = sum_j t_ij (lse_i - x_ij), reduced over rows
+ * as none / sum / mean (mean divides by n; NaN for n = 0).  The forward reads
+ * logits and target once each and saves lse [n] and tsum [n] = sum_j t_ij
+ * (float32); the backward writes
+ * grad[i, j] = g_i (exp(x_ij - lse_i) tsum_i - t_ij), g_i = grad_out[i]
+ * (NONE), grad_out[0] (SUM) or grad_out[0] / n (MEAN).  workspace: as
+ * supa_amd_cross_entropy_workspace_bytes(n).  Replaces the reference's
+ * fp32 probability-target fast path: cross_entropy_prob_kernel,
+ * .../kernels/elementwise/CrossEntropyLossKernel.cu:532-576 (forward), and
+ * CrossEntropyLossFastPathFunction::backward's prob_target branch,
+ * torch_supa/csrc/aten/ops/CrossEntropyLoss.cpp:94-131 (backward through
+ * -target * grad_factor and _log_softmax_backward_data), for f32 / bf16 /
+ * f16. */
+int supa_amd_cross_entropy_prob_forward(const void* logits, const void* target, int32_t dtype, int64_t n,
+                                        int64_t c, int reduction, void* out, float* lse, float* tsum,
+                                        void* workspace, int64_t workspace_bytes, void* stream);
+int supa_amd_cross_entropy_prob_backward(const void* grad_out, const void* logits, const void* target,
+                                         int32_t dtype, const float* lse, const float* tsum, int64_t n,
+                                         int64_t c, int reduction, void* grad_logits, void* stream);
+
 /* ------------------------------------------------- multi-tensor apply */
 #define SUPA_AMD_FOREACH_ADD 0      /* out = a + alpha * y                    */
 #define SUPA_AMD_FOREACH_MUL 1      /* out = a * y                            */

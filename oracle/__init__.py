@@ -80,6 +80,8 @@ def lib():
                                       ctypes.POINTER(ctypes.c_uint8)]),
             "or_softmax_bwd": (None, [_f32p, _f32p, _f32p, i64, i64]),
             "or_nll_loss_fwd": (c_int, [_f32p, _i64p, _f32p, i64, i64, c_int, i64, _f32p, _f32p]),
+            "or_ce_prob_fwd": (None, [_f64p, _f64p, i64, i64, c_int, _f64p, _f64p, _f64p]),
+            "or_ce_prob_bwd": (None, [_f64p, _f64p, _f64p, _f64p, _f64p, i64, i64, c_int, _f64p]),
             "or_nll_loss_bwd": (c_int, [_f32p, _i64p, _f32p, i64, i64, c_int, i64, c_float, c_int, _f32p]),
             "or_loss_fwd": (None, [c_int, _f32p, _f32p, _f32p, _f32p, i64, c_int, c_float, _f32p]),
             "or_loss_bwd": (None, [c_int, _f32p, _f32p, _f32p, _f32p, _f32p, i64, c_int, c_float, _f32p]),
@@ -392,6 +394,34 @@ def cross_entropy_backward(g, x, target, lse, count, reduction="mean", ignore_in
     out = np.empty((n, c), np.float64)
     lib().or_ce_bwd(_p(g, _f64p), _p(x, _f64p), _p(target, _i64p), _p(lse, _f64p), float(count), n, c,
                     ignore_index, REDUCTION[reduction], _p(out, _f64p))
+    return out
+
+
+def cross_entropy_prob(x, t, reduction="mean"):
+    """Cross-entropy with probability targets in float64 (x, t: [n, c], any
+    float dtype, converted to float64).  Returns (loss, lse, tsum): loss [n]
+    for 'none', a 0-d array otherwise; tsum[i] = sum_j t[i, j]."""
+    x = _c(x, np.float64)
+    n, c = x.shape
+    t = _c(np.broadcast_to(t, x.shape), np.float64)
+    red = REDUCTION[reduction]
+    out = np.empty(n if red == 0 else 1, np.float64)
+    lse = np.empty(n, np.float64)
+    tsum = np.empty(n, np.float64)
+    lib().or_ce_prob_fwd(_p(x, _f64p), _p(t, _f64p), n, c, red, _p(out, _f64p), _p(lse, _f64p), _p(tsum, _f64p))
+    return (out if red == 0 else out.reshape(())), lse, tsum
+
+
+def cross_entropy_prob_backward(g, x, t, lse, tsum, reduction="mean") -> np.ndarray:
+    """Gradient of cross_entropy_prob w.r.t. x in float64."""
+    x = _c(x, np.float64)
+    n, c = x.shape
+    g = _c(g, np.float64).reshape(-1)
+    t = _c(np.broadcast_to(t, x.shape), np.float64)
+    lse, tsum = _c(lse, np.float64), _c(tsum, np.float64)
+    out = np.empty((n, c), np.float64)
+    lib().or_ce_prob_bwd(_p(g, _f64p), _p(x, _f64p), _p(t, _f64p), _p(lse, _f64p), _p(tsum, _f64p), n, c,
+                         REDUCTION[reduction], _p(out, _f64p))
     return out
 
 

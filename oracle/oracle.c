@@ -541,6 +541,52 @@ void or_ce_bwd(const double* g, const double* x, const int64_t* target, const do
   }
 }
 
+/* Cross-entropy with probability targets, in float64 (t: [n, c] class
+ * probabilities): loss_i = sum_j t_ij (lse_i - x_ij), the reference's
+ * cross_entropy_prob_kernel (CrossEntropyLossKernel.cu:532-576: row max, the
+ * sum of exp, log_denom = log(sum) + max, then sum_j t_j (log_denom - x_j))
+ * and upstream's cross_entropy_loss_prob_target -(log_softmax(x) * t);
+ * mean divides the row sum by n (NaN for n = 0).  lse_i and
+ * tsum_i = sum_j t_ij are returned for the gradient. */
+void or_ce_prob_fwd(const double* x, const double* t, int64_t n, int64_t c, int reduction, double* loss,
+                    double* lse, double* tsum) {
+  double sum = 0.0;
+  for (int64_t i = 0; i < n; ++i) {
+    const double* r = x + i * c;
+    const double* tr = t + i * c;
+    double m = -INFINITY;
+    for (int64_t j = 0; j < c; ++j) m = r[j] > m ? r[j] : m;
+    double s = 0.0, T = 0.0, l = 0.0;
+    for (int64_t j = 0; j < c; ++j) s += exp(r[j] - m);
+    const double ld = m + log(s);
+    for (int64_t j = 0; j < c; ++j) {
+      l += tr[j] * (ld - r[j]);
+      T += tr[j];
+    }
+    lse[i] = ld;
+    tsum[i] = T;
+    if (reduction == 0) loss[i] = l;
+    sum += l;
+  }
+  if (reduction == 1) loss[0] = sum / (double)n;
+  else if (reduction == 2) loss[0] = sum;
+}
+
+/* Its gradient w.r.t. x: g_i (exp(x_ij - lse_i) tsum_i - t_ij), g_i = g[i]
+ * (none), g / n (mean), g (sum): the reference's prob_target backward
+ * (CrossEntropyLoss.cpp:94-131), grad_lp = -t g_i through
+ * _log_softmax_backward_data (grad_lp - softmax * sum_j grad_lp). */
+void or_ce_prob_bwd(const double* g, const double* x, const double* t, const double* lse, const double* tsum,
+                    int64_t n, int64_t c, int reduction, double* gx) {
+  for (int64_t i = 0; i < n; ++i) {
+    const double gi = reduction == 0 ? g[i] : (reduction == 1 ? g[0] / (double)n : g[0]);
+    const double* r = x + i * c;
+    const double* tr = t + i * c;
+    double* o = gx + i * c;
+    for (int64_t j = 0; j < c; ++j) o[j] = (exp(r[j] - lse[i]) * tsum[i] - tr[j]) * gi;
+  }
+}
+
 /* ------------------------------------------------------------- losses -- */
 
 enum { OR_MSE = 0, OR_SMOOTH_L1 = 1, OR_BCE_LOGITS = 2 };

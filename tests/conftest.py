@@ -46,7 +46,9 @@ def no_fallback(supa):
 
 @pytest.fixture
 def fused_ce(supa):
-    """Route cross_entropy through the fused kernels for one test."""
+    """Route cross_entropy through the fused kernels (every dtype) for one
+    test, then restore the routing it found."""
+    was = supa.supa.fused_cross_entropy_enabled()
     supa.supa.set_fused_cross_entropy_enabled(True)
     yield
-    supa.supa.set_fused_cross_entropy_enabled(False)
+    supa.supa.set_fused_cross_entropy_enabled(was)

@@ -60,6 +60,19 @@ def test_argument_errors_need_no_device(lib):
                                               None, i64(0), None, None) == -4
     assert lib.supa_amd_cross_entropy_backward(None, fake, 6, fake, fake, fake, i64(4), i64(10), i64(-100), 1,
                                                fake, None, None) == -1
+    # probability targets: the same checks, and the float32 target sums
+    assert lib.supa_amd_cross_entropy_prob_forward(fake, fake, 6, i64(4), i64(10), 9, fake, fake, fake, fake,
+                                                   i64(16), None) == -1
+    assert lib.supa_amd_cross_entropy_prob_forward(fake, fake, 6, i64(4), i64(10), 1, fake, fake, None, fake,
+                                                   i64(16), None) == -1
+    assert lib.supa_amd_cross_entropy_prob_forward(fake, fake, 6, i64(4), i64(10), 1, fake, fake, fake, None,
+                                                   i64(0), None) == -4
+    assert lib.supa_amd_cross_entropy_prob_forward(fake, fake, 4, i64(4), i64(10), 1, fake, fake, fake, fake,
+                                                   i64(16), None) == -2  # int64 logits
+    assert lib.supa_amd_cross_entropy_prob_backward(fake, fake, None, 6, fake, fake, i64(4), i64(10), 1, fake,
+                                                    None) == -1
+    assert lib.supa_amd_cross_entropy_prob_backward(fake, fake, fake, 6, fake, fake, i64(4), i64(0), 1, fake,
+                                                    None) == -1
 
 
 def test_foreach_argument_errors(lib):

@@ -527,6 +527,7 @@ def test_fused_cross_entropy_matches_decomposition_and_edges(no_fallback, supa):
     t = torch.randint(0, V, (N,), generator=g)
     t[:3] = -100
     res = {}
+    was = supa.supa.fused_cross_entropy_enabled()
     for fused in (False, True):
         supa.supa.set_fused_cross_entropy_enabled(fused)
         try:
@@ -535,7 +536,7 @@ def test_fused_cross_entropy_matches_decomposition_and_edges(no_fallback, supa):
             loss.backward()
             res[fused] = (loss.float().item(), dl.grad.float().cpu())
         finally:
-            supa.supa.set_fused_cross_entropy_enabled(False)
+            supa.supa.set_fused_cross_entropy_enabled(was)
     assert abs(res[True][0] - res[False][0]) <= 1e-2 * abs(res[False][0])
     gdiff = (res[True][1] - res[False][1]).abs().max().item()
     assert gdiff <= 1e-2 * res[False][1].abs().max().item()
@@ -553,7 +554,7 @@ def test_fused_cross_entropy_matches_decomposition_and_edges(no_fallback, supa):
         with pytest.raises(IndexError):
             torch.supa.synchronize()
     finally:
-        supa.supa.set_fused_cross_entropy_enabled(False)
+        supa.supa.set_fused_cross_entropy_enabled(was)
 
 
 def test_fused_cross_entropy_c3_full_size(no_fallback, fused_ce):
@@ -582,6 +583,79 @@ def test_fused_cross_entropy_c3_full_size(no_fallback, fused_ce):
     tg = gcpu[torch.arange(N)[keep], t[keep]].float()
     assert (tg < 0).all()
     assert not gcpu[~keep].any()
+
+
+def _prob_targets(n, c, seed, dtype):
+    g = torch.Generator().manual_seed(seed)
+    x = (torch.randn(n, c, generator=g) * 2).to(dtype)
+    p = torch.softmax(torch.randn(n, c, generator=g) * 3, 1)
+    p[:2] *= 0.5  # rows whose mass is not one
+    return x, p.to(dtype)
+
+
+@pytest.mark.parametrize("routing", [None, True, False])
+@pytest.mark.parametrize("reduction", ["none", "sum", "mean"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("shape", [(64, 32000), (33, 1001)])
+def test_cross_entropy_probability_targets(shape, dtype, reduction, routing, no_fallback, supa):
+    """F.cross_entropy(x, p) with a class-probability target, forward and
+    backward, against the float64 oracle (the oracle pinned to upstream CPU
+    in test_oracle_vs_torch.py): float32 within rtol 1e-5, bfloat16 within
+    1e-2, under each routing -- the reference's (None: float32 fused,
+    bfloat16 decomposed), every dtype fused (True) and none (False).  The
+    gradient is checked against the oracle's to 1e-5 (1e-2 for bf16) of the
+    largest gradient element."""
+    n, c = shape
+    x, p = _prob_targets(n, c, 90 + c % 7, dtype)
+    go = torch.randn(n, generator=torch.Generator().manual_seed(91)).to(dtype) if reduction == "none" \
+        else torch.tensor(1.5).to(dtype)
+    tol = 1e-5 if dtype == torch.float32 else 1e-2
+    was = supa.supa.fused_cross_entropy_enabled()
+    supa.supa.set_fused_cross_entropy_enabled(routing)
+    try:
+        dx = dev(x).requires_grad_()
+        loss = F.cross_entropy(dx, dev(p), reduction=reduction)
+        loss.backward(dev(go))
+        got, gx = loss.detach().float().cpu().double().numpy(), dx.grad.float().cpu().double().numpy()
+    finally:
+        supa.supa.set_fused_cross_entropy_enabled(was)
+    ref, lse, tsum = O.cross_entropy_prob(x.double().numpy(), p.double().numpy(), reduction)
+    np.testing.assert_allclose(got, ref, rtol=tol, atol=tol * 1e-3)
+    gref = O.cross_entropy_prob_backward(go.double().numpy(), x.double().numpy(), p.double().numpy(), lse, tsum,
+                                         reduction)
+    assert np.abs(gx - gref).max() <= tol * np.abs(gref).max()
+
+
+def test_cross_entropy_probability_target_edges(no_fallback, supa):
+    """A target that needs its own gradient takes the decomposition (the fused
+    backward writes the logits' gradient only) and matches the CPU; a
+    non-negative ignore_index with a probability target is refused as
+    upstream refuses it; create_graph through the fused float32 paths (class
+    and probability targets) gives a differentiable gradient whose second
+    derivative matches the CPU's in float64."""
+    x, p = _prob_targets(16, 300, 93, torch.float32)
+    xs, ps = dev(x).requires_grad_(), dev(p).requires_grad_()
+    F.cross_entropy(xs, ps).backward()
+    xc, pc = x.clone().requires_grad_(), p.clone().requires_grad_()
+    F.cross_entropy(xc, pc).backward()
+    np.testing.assert_allclose(xs.grad.cpu().numpy(), xc.grad.numpy(), rtol=1e-4, atol=1e-7)
+    np.testing.assert_allclose(ps.grad.cpu().numpy(), pc.grad.numpy(), rtol=1e-4, atol=1e-7)
+    with pytest.raises(RuntimeError, match="ignore_index"):
+        F.cross_entropy(dev(x), dev(p), ignore_index=3)
+    t = torch.randint(0, 300, (16,), generator=torch.Generator().manual_seed(94))
+    t[3] = -100
+    w = torch.randn(16, 300, generator=torch.Generator().manual_seed(95))
+    for tgt, tgt_dev in [(t, dev(t)), (p, dev(p))]:
+        assert supa.supa.fused_cross_entropy_enabled() is None  # the reference's routing: float32 fused
+        xd = dev(x).requires_grad_()
+        gx, = torch.autograd.grad(F.cross_entropy(xd, tgt_dev, ignore_index=-100), xd, create_graph=True)
+        (gx * dev(w)).sum().backward()
+        xr = x.double().requires_grad_()
+        gr, = torch.autograd.grad(F.cross_entropy(xr, tgt.double() if tgt.is_floating_point() else tgt,
+                                                  ignore_index=-100), xr, create_graph=True)
+        (gr * w.double()).sum().backward()
+        np.testing.assert_allclose(gx.detach().cpu().double().numpy(), gr.detach().numpy(), rtol=1e-4, atol=1e-8)
+        np.testing.assert_allclose(xd.grad.cpu().double().numpy(), xr.grad.numpy(), rtol=1e-3, atol=1e-7)
 
 
 def test_cross_entropy_c3_full_size_properties(no_fallback):

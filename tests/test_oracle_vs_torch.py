@@ -333,6 +333,55 @@ def test_fused_cross_entropy_closed_forms():
         O.cross_entropy(x, np.array([0, 1, 50, 2]), "mean", -100)
 
 
+@pytest.mark.parametrize("reduction", ["none", "mean", "sum"])
+def test_cross_entropy_prob_oracle_vs_cpu_f64(reduction):
+    """The probability-target cross-entropy oracle (float64) against
+    upstream's float64 cross_entropy with class-probability targets and its
+    autograd gradient on the CPU; targets that do not sum to one included
+    (rows scaled by 0.5 and 2)."""
+    N, C = 150, 2003
+    x = randn((N, C), 45, 3.0).double()
+    g = torch.Generator().manual_seed(46)
+    p = torch.softmax(torch.randn(N, C, generator=g, dtype=torch.float64) * 2, 1)
+    p[:5] *= 0.5
+    p[5:9] *= 2.0
+    xg = x.clone().requires_grad_()
+    loss = F.cross_entropy(xg, p, reduction=reduction)
+    go = torch.ones_like(loss) if reduction != "none" else randn((N,), 47).double()
+    loss.backward(go)
+    out, lse, tsum = O.cross_entropy_prob(x.numpy(), p.numpy(), reduction)
+    np.testing.assert_allclose(out, loss.detach().numpy(), rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(tsum, p.sum(1).numpy(), rtol=1e-14)
+    gx = O.cross_entropy_prob_backward(go.numpy(), x.numpy(), p.numpy(), lse, tsum, reduction)
+    np.testing.assert_allclose(gx, xg.grad.numpy(), rtol=1e-10, atol=1e-15)
+
+
+def test_cross_entropy_prob_closed_forms():
+    """Uniform logits with any probability target give log C per unit of
+    target mass; a one-hot target equals the class-index form; the target
+    softmax(x) gives the entropy; gradient rows of a unit-mass target sum
+    to zero."""
+    C = 1000
+    t = np.random.default_rng(5).dirichlet(np.ones(C), size=3)
+    out, _, tsum = O.cross_entropy_prob(np.zeros((3, C)), t, "none")
+    np.testing.assert_allclose(out, math.log(C) * tsum, rtol=1e-13)
+    x = np.random.default_rng(6).standard_normal((4, 50)) * 2
+    idx = np.array([3, 0, 49, 7])
+    oh = np.eye(50)[idx]
+    a, lse_a, _ = O.cross_entropy_prob(x, oh, "none")
+    b, lse_b, _ = O.cross_entropy(x, idx, "none", -100)
+    np.testing.assert_allclose(a, b, rtol=1e-13)
+    sm = np.exp(x - lse_a[:, None])
+    ent, _, _ = O.cross_entropy_prob(x, sm, "none")
+    np.testing.assert_allclose(ent, -(sm * np.log(sm)).sum(1), rtol=1e-12)
+    gx = O.cross_entropy_prob_backward(np.ones(1), x, sm, lse_a, sm.sum(1), "sum")
+    np.testing.assert_allclose(gx, 0.0, atol=1e-14)  # the target is the softmax: zero gradient
+    gx = O.cross_entropy_prob_backward(np.ones(1), x, oh, lse_a, oh.sum(1), "mean")
+    np.testing.assert_allclose(gx.sum(1), 0.0, atol=1e-15)
+    out, _, _ = O.cross_entropy_prob(np.zeros((0, 5)), np.zeros((0, 5)), "mean")
+    assert np.isnan(out)
+
+
 def test_cross_entropy_bf16_decomposition_vs_cpu():
     """c3's semantics at a small row count: bf16 logits, 5% ignore_index,
     mean.  Each decomposed op is compared on the reference's own inputs (the

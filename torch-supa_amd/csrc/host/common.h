@@ -102,9 +102,11 @@ void check_device_errors(c10::DeviceIndex d);
 // registers; tests assert that with these counters).
 void set_cpu_fallback_enabled(bool on);
 bool cpu_fallback_enabled();
-// Fused cross-entropy (opt-in; default off, env SUPA_AMD_FUSED_CE=1 turns it on).
-void set_fused_cross_entropy_enabled(bool on);
-bool fused_cross_entropy_enabled();
+// Fused cross-entropy routing: -1 the reference's (float32 logits fused,
+// bfloat16 / float16 through the log_softmax + nll_loss decomposition), 0 no
+// dtype fused, 1 every floating dtype fused.  Env SUPA_AMD_FUSED_CE=0 / 1.
+void set_fused_cross_entropy_mode(int mode);
+int fused_cross_entropy_mode();
 // One-pass BCE-with-logits gradient (default on, env SUPA_AMD_FUSED_BCE=0 turns it off).
 void set_fused_bce_backward_enabled(bool on);
 bool fused_bce_backward_enabled();

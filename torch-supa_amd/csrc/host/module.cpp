@@ -187,8 +187,8 @@ PYBIND11_MODULE(_C, m) {
   m.def("empty_host_cache", []() { supa::pinned_empty_cache(); });
   m.def("set_cpu_fallback_enabled", &supa::set_cpu_fallback_enabled);
   m.def("cpu_fallback_enabled", &supa::cpu_fallback_enabled);
-  m.def("set_fused_cross_entropy_enabled", &supa::set_fused_cross_entropy_enabled);
-  m.def("fused_cross_entropy_enabled", &supa::fused_cross_entropy_enabled);
+  m.def("set_fused_cross_entropy_mode", &supa::set_fused_cross_entropy_mode);
+  m.def("fused_cross_entropy_mode", &supa::fused_cross_entropy_mode);
   m.def("set_fused_bce_backward_enabled", &supa::set_fused_bce_backward_enabled);
   m.def("fused_bce_backward_enabled", &supa::fused_bce_backward_enabled);
   m.def("set_accurate_gelu_enabled", &supa::set_accurate_gelu_enabled);

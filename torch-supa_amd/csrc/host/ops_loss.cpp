@@ -4,13 +4,16 @@
 // _softmax with their backwards, nll_loss and nll_loss2d forward / backward.
 //
 // cross_entropy_loss is registered the way the reference registers it
-// (SUPANativeFunctions::cross_entropy_loss, CrossEntropyLoss.cpp:140-151): by
-// default it calls upstream's composite cross_entropy_loss_symint, i.e. the
-// _log_softmax + nll_loss decomposition whose nested calls record autograd --
-// the path the reference takes for every non-fp32 input (:23-52).  With the
-// fused path enabled (torch.supa.set_fused_cross_entropy_enabled), 2-d
-// f32/bf16/f16 logits with int64 targets, no weight and no label smoothing go
-// through a custom autograd function on the fused kernels instead.
+// (SUPANativeFunctions::cross_entropy_loss, CrossEntropyLoss.cpp:140-151),
+// with its routing: 2-d float32 logits with int64 class targets or a float32
+// probability target of the logits' shape, no class weight and no label
+// smoothing take the fused kernels (a custom autograd function, as the
+// reference's CrossEntropyLossFastPathFunction); everything else, bfloat16 and
+// float16 logits included, calls upstream's composite cross_entropy_loss_symint,
+// i.e. the _log_softmax + nll_loss decomposition whose nested calls record
+// autograd -- the path the reference takes for every non-fp32 input (:23-52).
+// torch.supa.set_fused_cross_entropy_enabled(True / False) routes every
+// floating dtype to the fused kernels, or none.
 // binary_cross_entropy_with_logits is registered, as the reference registers
 // it (supa_native_functions.yaml:59-61; BinaryCrossEntropyWithLogits.cpp:23-73);
 // its backward is the autograd formula's op sequence on the kernels above.
@@ -810,13 +813,39 @@ at::Tensor bce_with_logits_autograd(const at::Tensor& self, const at::Tensor& ta
 }
 
 // ------------------------------------------------------ fused cross-entropy
+// The routing of CrossEntropyLoss.cpp:23-33 (supported_fast_path): 2-d logits,
+// no class weight, no label smoothing, a valid reduction, and an int64 class
+// target [n] or a probability target of the logits' shape.  The reference
+// takes it for float32; the routing mode widens it to every floating dtype
+// or turns it off.  A probability target must have the logits' dtype and
+// need no gradient (the fused backward writes the logits' gradient only);
+// its ignore_index must be negative, as the reference checks (other cases go
+// to the composite, which raises upstream's error).
+bool fused_ce_dtype_on(at::ScalarType dt) {
+  const int mode = fused_cross_entropy_mode();
+  if (mode == 0) return false;
+  if (mode < 0) return dt == at::kFloat;
+  return dt == at::kFloat || dt == at::kBFloat16 || dt == at::kHalf;
+}
+
+bool fused_ce_base(const at::Tensor& self, const at::Tensor& target, const std::optional<at::Tensor>& weight,
+                   int64_t reduction, double label_smoothing) {
+  return fused_ce_dtype_on(self.scalar_type()) && self.dim() == 2 && !(weight.has_value() && weight->defined()) &&
+         label_smoothing == 0.0 && target.device() == self.device() &&
+         (reduction == at::Reduction::None || reduction == at::Reduction::Mean || reduction == at::Reduction::Sum);
+}
+
 bool fused_ce_supported(const at::Tensor& self, const at::Tensor& target, const std::optional<at::Tensor>& weight,
-                        double label_smoothing) {
-  const auto dt = self.scalar_type();
-  return fused_cross_entropy_enabled() && self.dim() == 2 &&
-         (dt == at::kFloat || dt == at::kBFloat16 || dt == at::kHalf) && target.dim() == 1 &&
-         target.scalar_type() == at::kLong && target.size(0) == self.size(0) &&
-         !(weight.has_value() && weight->defined()) && label_smoothing == 0.0 && target.device() == self.device();
+                        int64_t reduction, double label_smoothing) {
+  return fused_ce_base(self, target, weight, reduction, label_smoothing) && target.dim() == 1 &&
+         target.scalar_type() == at::kLong && target.size(0) == self.size(0);
+}
+
+bool fused_ce_prob_supported(const at::Tensor& self, const at::Tensor& target,
+                             const std::optional<at::Tensor>& weight, int64_t reduction, int64_t ignore_index,
+                             double label_smoothing) {
+  return fused_ce_base(self, target, weight, reduction, label_smoothing) && target.sizes() == self.sizes() &&
+         target.scalar_type() == self.scalar_type() && !target.requires_grad() && ignore_index < 0;
 }
 
 class FusedCrossEntropy : public torch::autograd::Function<FusedCrossEntropy> {
@@ -857,6 +886,17 @@ class FusedCrossEntropy : public torch::autograd::Function<FusedCrossEntropy> {
     const int64_t ignore_index = ctx->saved_data["ignore_index"].toInt();
     const int64_t n = x.size(0), c = x.size(1);
     const auto dev = x.device().index();
+    if (at::GradMode::is_enabled()) {
+      // create_graph: the same gradient from differentiable ops,
+      // (softmax(x) - onehot(t)) g_i over the kept rows
+      const at::Tensor kept = ((t != ignore_index) * (t >= 0) * (t < c)).to(x.scalar_type());
+      const at::Tensor oh = at::one_hot(t.clamp(0, c - 1), c).to(x.scalar_type());
+      at::Tensor gr = red == SUPA_AMD_REDUCTION_NONE ? grads[0] : grads[0].expand({n});
+      gr = gr * kept;
+      if (red == SUPA_AMD_REDUCTION_MEAN) gr = gr / count.to(x.scalar_type());
+      return {(at::softmax(x, 1, x.scalar_type()) - oh) * gr.unsqueeze(1), at::Tensor(), at::Tensor(),
+              at::Tensor()};
+    }
     at::Tensor g = to_dtype(grads[0], x.scalar_type()).contiguous();
     at::Tensor gx = empty_supa(x.sizes(), x.scalar_type(), dev);
     int32_t* const eflag = stream_error_flag(dev);
@@ -869,11 +909,71 @@ class FusedCrossEntropy : public torch::autograd::Function<FusedCrossEntropy> {
   }
 };
 
+// Probability targets: loss_i = sum_j t_ij (lse_i - x_ij), as the
+// reference's cross_entropy_prob_kernel (CrossEntropyLossKernel.cu:532-576);
+// the backward is its prob_target branch (CrossEntropyLoss.cpp:94-131),
+// -t g through _log_softmax_backward_data, in one pass:
+// g_i (softmax(x_i) sum_j t_ij - t_i).
+class FusedCrossEntropyProb : public torch::autograd::Function<FusedCrossEntropyProb> {
+ public:
+  static at::Tensor forward(torch::autograd::AutogradContext* ctx, const at::Tensor& self, const at::Tensor& target,
+                            int64_t reduction) {
+    const int red = reduction_code(reduction);
+    const int64_t n = self.size(0), c = self.size(1);
+    TORCH_CHECK(c > 0, "cross_entropy: expected at least one class");
+    const auto dev = self.device().index();
+    at::Tensor x = self.contiguous();
+    at::Tensor t = target.contiguous();
+    at::Tensor out = empty_supa(red == SUPA_AMD_REDUCTION_NONE ? std::vector<int64_t>{n} : std::vector<int64_t>{},
+                                self.scalar_type(), dev);
+    at::Tensor lse = empty_supa({n}, at::kFloat, dev);
+    at::Tensor tsum = empty_supa({n}, at::kFloat, dev);
+    at::Tensor ws = empty_supa({std::max<int64_t>(n, 1)}, at::kFloat, dev);
+    const int rc = supa_amd_cross_entropy_prob_forward(x.data_ptr(), t.data_ptr(), dtype_code(x.scalar_type()), n, c,
+                                                       red, out.data_ptr(), lse.data_ptr<float>(),
+                                                       tsum.data_ptr<float>(), ws.data_ptr(), ws.numel() * 4,
+                                                       current_stream(dev));
+    check_status(rc, "cross_entropy (fused forward, probability target)");
+    ctx->save_for_backward({x, t, lse, tsum});
+    ctx->saved_data["reduction"] = reduction;
+    return out;
+  }
+
+  static torch::autograd::variable_list backward(torch::autograd::AutogradContext* ctx,
+                                                 torch::autograd::variable_list grads) {
+    const auto saved = ctx->get_saved_variables();
+    const at::Tensor& x = saved[0];
+    const at::Tensor& t = saved[1];
+    const at::Tensor& lse = saved[2];
+    const at::Tensor& tsum = saved[3];
+    const int red = reduction_code(ctx->saved_data["reduction"].toInt());
+    const int64_t n = x.size(0), c = x.size(1);
+    const auto dev = x.device().index();
+    if (at::GradMode::is_enabled()) {
+      // create_graph: (softmax(x) sum_j t_j - t) g_i from differentiable ops
+      at::Tensor gr = red == SUPA_AMD_REDUCTION_NONE ? grads[0] : grads[0].expand({n});
+      if (red == SUPA_AMD_REDUCTION_MEAN) gr = gr / (double)n;
+      const at::Tensor p = at::softmax(x, 1, x.scalar_type());
+      return {(p * t.sum(1, true) - t) * gr.unsqueeze(1), at::Tensor(), at::Tensor()};
+    }
+    at::Tensor g = to_dtype(grads[0], x.scalar_type()).contiguous();
+    at::Tensor gx = empty_supa(x.sizes(), x.scalar_type(), dev);
+    const int rc = supa_amd_cross_entropy_prob_backward(g.data_ptr(), x.data_ptr(), t.data_ptr(),
+                                                        dtype_code(x.scalar_type()), lse.data_ptr<float>(),
+                                                        tsum.data_ptr<float>(), n, c, red, gx.data_ptr(),
+                                                        current_stream(dev));
+    check_status(rc, "cross_entropy (fused backward, probability target)");
+    return {gx, at::Tensor(), at::Tensor()};
+  }
+};
+
 at::Tensor cross_entropy_loss(const at::Tensor& self, const at::Tensor& target,
                               const std::optional<at::Tensor>& weight, int64_t reduction, c10::SymInt ignore_index,
                               double label_smoothing) {
-  if (fused_ce_supported(self, target, weight, label_smoothing))
+  if (fused_ce_supported(self, target, weight, reduction, label_smoothing))
     return FusedCrossEntropy::apply(self, target, reduction, ignore_index.expect_int());
+  if (fused_ce_prob_supported(self, target, weight, reduction, ignore_index.expect_int(), label_smoothing))
+    return FusedCrossEntropyProb::apply(self, target, reduction);
   return at::native::cross_entropy_loss_symint(self, target, weight, reduction, std::move(ignore_index),
                                                label_smoothing);
 }

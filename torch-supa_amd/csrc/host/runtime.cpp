@@ -910,13 +910,18 @@ void set_cpu_fallback_enabled(bool on) { g_fallback_enabled.store(on); }
 bool cpu_fallback_enabled() { return g_fallback_enabled.load(); }
 
 namespace {
-std::atomic<bool> g_fused_ce{[] {
+// -1: the reference's routing (float32 fused, 16-bit decomposed); 0: none
+// fused; 1: every floating dtype fused.  SUPA_AMD_FUSED_CE=0 / 1 sets the
+// start value.
+std::atomic<int> g_fused_ce{[] {
   const char* e = std::getenv("SUPA_AMD_FUSED_CE");
-  return e && std::string(e) == "1";
+  if (e && std::string(e) == "1") return 1;
+  if (e && std::string(e) == "0") return 0;
+  return -1;
 }()};
 }  // namespace
-void set_fused_cross_entropy_enabled(bool on) { g_fused_ce.store(on); }
-bool fused_cross_entropy_enabled() { return g_fused_ce.load(); }
+void set_fused_cross_entropy_mode(int mode) { g_fused_ce.store(mode < 0 ? -1 : (mode > 0 ? 1 : 0)); }
+int fused_cross_entropy_mode() { return g_fused_ce.load(); }
 
 namespace {
 std::atomic<bool> g_fused_bce{[] {

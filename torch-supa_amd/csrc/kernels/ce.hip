@@ -15,6 +15,13 @@
 //
 // Out-of-range targets set *error_flag (when given); their rows count as
 // ignored.
+//
+// Probability targets (a float [n, c] target of the logits' dtype, the
+// reference's other fp32 fast-path case): the forward reads logits and
+// target once each, folds per thread an online (max m, sum of exp(x - m) s,
+// sum of t T, sum of t (x - m) B) state, combines it across the workgroup and
+// writes loss = T log(s) - B = sum_j t_j (lse - x_j) with lse and T saved per
+// row; the backward writes g_i (exp(x - lse_i) T_i - t) in one pass.
 #include "devmath.h"
 #include "ew_launch.h"
 
@@ -139,7 +146,8 @@ k_ce_fwd(const T* __restrict__ x, const int64_t* __restrict__ target, int64_t c,
   }
 }
 
-// Stage 2: sum of the row losses and the kept-row count, fixed order.
+// Stage 2: sum of the row losses and the kept-row count, fixed order
+// (target null: every row counts, the probability-target form).
 template <typename T>
 __global__ void __launch_bounds__(kCeBlock)
 k_ce_final(const float* __restrict__ loss_rows, const int64_t* __restrict__ target, int64_t n, int64_t c,
@@ -156,13 +164,13 @@ k_ce_final(const float* __restrict__ loss_rows, const int64_t* __restrict__ targ
     for (int u = 0; u < U; ++u) {
       const int64_t i = i0 + (int64_t)u * kCeBlock;
       lv[u] = i < n ? loss_rows[i] : 0.0f;
-      tg[u] = i < n ? target[i] : ignore_index;
+      tg[u] = i < n && target ? target[i] : ignore_index;
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       if (i0 + (int64_t)u * kCeBlock < n) {
         v += lv[u];
-        k += ce_kept(tg[u], c, ignore_index) ? 1.0f : 0.0f;
+        k += (!target || ce_kept(tg[u], c, ignore_index)) ? 1.0f : 0.0f;
       }
     }
   }
@@ -233,6 +241,162 @@ k_ce_bwd(const T* __restrict__ grad_out, const T* __restrict__ x, const int64_t*
         r = (p - (col0 + k == t ? 1.0f : 0.0f)) * g;
       }
       dst[col0 + k] = from_arith<T>(r);
+    }
+  }
+}
+
+// ------------------------------------------------- probability targets
+// Online state of a row: max m, s = sum exp(x - m), T = sum t,
+// B = sum t (x - m).  (+) of two states rebases both to M = max(m, m2):
+// s -> s e^{m - M}, B -> B + T (m - M).  A state whose elements are all -inf
+// keeps m = -inf, s = 0 and B = sum t x (-inf, or NaN where a t is 0), which
+// no rebase changes: its elements add t (lse - x) = +inf (or NaN for t = 0)
+// to the loss, as -t log_softmax(x) does in the decomposition.
+struct CeProbState {
+  float m, s, T, B;
+};
+__device__ __forceinline__ CeProbState ce_prob_elem(float x, float t) {
+  if (x == -__builtin_inff()) return CeProbState{x, 0.0f, t, t * x};
+  return CeProbState{x, 1.0f, t, 0.0f};
+}
+__device__ __forceinline__ void ce_prob_combine(CeProbState& a, const CeProbState& b) {
+  const float M = fmaxf(a.m, b.m);
+  const bool fa = a.m != -__builtin_inff(), fb = b.m != -__builtin_inff();
+  const float ea = fa ? __builtin_amdgcn_exp2f((a.m - M) * kCeLog2e) : 0.0f;
+  const float eb = fb ? __builtin_amdgcn_exp2f((b.m - M) * kCeLog2e) : 0.0f;
+  const float Ba = fa ? fmaf(a.T, a.m - M, a.B) : a.B;
+  const float Bb = fb ? fmaf(b.T, b.m - M, b.B) : b.B;
+  a.s = a.s * ea + b.s * eb;
+  a.B = Ba + Bb;
+  a.T = a.T + b.T;
+  a.m = M;
+}
+
+// loss_rows[i] = T log(s) - B (float32); lse[i] = m + log(s); tsum[i] = T;
+// out_none (may be null): the loss in the logits dtype.
+template <typename T, bool VECOK>
+__global__ void __launch_bounds__(kCeBlock)
+k_ce_prob_fwd(const T* __restrict__ x, const T* __restrict__ tgt, int64_t c, float* __restrict__ loss_rows,
+              float* __restrict__ lse, float* __restrict__ tsum, T* __restrict__ out_none) {
+  constexpr int V = CeVec<T>::V;
+  constexpr int NW = kCeBlock / 64;
+  constexpr int U = 2;  // vectors of each stream in flight per thread
+  __shared__ CeProbState lds[NW];
+  const int64_t row = blockIdx.x;
+  const T* xr = x + row * c;
+  const T* tr = tgt + row * c;
+  const uint4* xs = reinterpret_cast<const uint4*>(xr);
+  const uint4* ts = reinterpret_cast<const uint4*>(tr);
+  const int64_t nvec = VECOK ? c / V : 0;
+  CeProbState st{-__builtin_inff(), 0.0f, 0.0f, 0.0f};
+  for (int64_t v0 = threadIdx.x; v0 < nvec; v0 += (int64_t)kCeBlock * U) {
+    uint4 wx[U], wt[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t v = v0 + (int64_t)u * kCeBlock;
+      if (v < nvec) {
+        wx[u] = ld_stream(xs + v);
+        wt[u] = ld_stream(ts + v);
+      }
+    }
+    float mb = -__builtin_inff();
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (v0 + (int64_t)u * kCeBlock < nvec) {
+#pragma unroll
+        for (int k = 0; k < V; ++k) mb = fmaxf(mb, ce_elem<T>(wx[u], k));
+      }
+    const float M = fmaxf(st.m, mb);
+    if (M != -__builtin_inff()) {
+      if (st.m != -__builtin_inff()) {
+        st.s *= __builtin_amdgcn_exp2f((st.m - M) * kCeLog2e);
+        st.B = fmaf(st.T, st.m - M, st.B);
+      }
+      st.m = M;
+      const float ml = M * kCeLog2e;
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (v0 + (int64_t)u * kCeBlock < nvec) {
+#pragma unroll
+          for (int k = 0; k < V; ++k) {
+            const float xv = ce_elem<T>(wx[u], k), tv = ce_elem<T>(wt[u], k);
+            st.s += __builtin_amdgcn_exp2f(fmaf(xv, kCeLog2e, -ml));
+            st.T += tv;
+            st.B = fmaf(tv, xv - M, st.B);
+          }
+        }
+    } else {  // every value so far -inf: s stays 0, B = sum t x
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (v0 + (int64_t)u * kCeBlock < nvec) {
+#pragma unroll
+          for (int k = 0; k < V; ++k) {
+            const float xv = ce_elem<T>(wx[u], k), tv = ce_elem<T>(wt[u], k);
+            st.T += tv;
+            st.B = fmaf(tv, xv, st.B);
+          }
+        }
+    }
+  }
+  // elements not covered by whole vectors (all of them when !VECOK)
+  for (int64_t j = nvec * V + threadIdx.x; j < c; j += kCeBlock)
+    ce_prob_combine(st, ce_prob_elem((float)to_arith(xr[j]), (float)to_arith(tr[j])));
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const CeProbState o{__shfl_xor(st.m, off, 64), __shfl_xor(st.s, off, 64), __shfl_xor(st.T, off, 64),
+                        __shfl_xor(st.B, off, 64)};
+    ce_prob_combine(st, o);
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) lds[wave] = st;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    CeProbState a = lds[0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) ce_prob_combine(a, lds[w]);
+    const float L = sa_logf(a.s);
+    const float loss = fmaf(a.T, L, -a.B);
+    loss_rows[row] = loss;
+    lse[row] = a.m + L;
+    tsum[row] = a.T;
+    if (out_none) out_none[row] = from_arith<T>(loss);
+  }
+}
+
+// grad[i, j] = g_i (exp(x - lse_i) T_i - t_ij); g_i = grad_out[i] (none),
+// grad_out[0] (sum) or grad_out[0] / n (mean).
+template <typename T, bool VECOK>
+__global__ void __launch_bounds__(kCeBwdBlock)
+k_ce_prob_bwd(const T* __restrict__ grad_out, const T* __restrict__ x, const T* __restrict__ tgt,
+              const float* __restrict__ lse, const float* __restrict__ tsum, int64_t c, int reduction, float inv_n,
+              T* __restrict__ gx) {
+  constexpr int V = CeVec<T>::V;
+  const int64_t row = blockIdx.y;
+  float g;
+  if (reduction == SUPA_AMD_REDUCTION_NONE) g = (float)to_arith(grad_out[row]);
+  else if (reduction == SUPA_AMD_REDUCTION_MEAN) g = (float)to_arith(grad_out[0]) * inv_n;
+  else g = (float)to_arith(grad_out[0]);
+  const float ll = lse[row] * kCeLog2e;
+  const float Tr = tsum[row];
+  const T* xr = x + row * c;
+  const T* tr = tgt + row * c;
+  T* dst = gx + row * c;
+  const int64_t col0 = ((int64_t)blockIdx.x * kCeBwdBlock + threadIdx.x) * V;
+  if (col0 >= c) return;
+  if (VECOK && col0 + V <= c) {
+    const Vec<T, V> w = ld_stream(reinterpret_cast<const Vec<T, V>*>(xr + col0));
+    const Vec<T, V> wt = ld_stream(reinterpret_cast<const Vec<T, V>*>(tr + col0));
+    Vec<T, V> o;
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+      const float p = __builtin_amdgcn_exp2f(fmaf((float)to_arith(w.v[k]), kCeLog2e, -ll));
+      o.v[k] = from_arith<T>(fmaf(p, Tr, -(float)to_arith(wt.v[k])) * g);
+    }
+    st_stream(reinterpret_cast<Vec<T, V>*>(dst + col0), o);
+  } else {
+    for (int k = 0; k < V && col0 + k < c; ++k) {
+      const float p = __builtin_amdgcn_exp2f(fmaf((float)to_arith(xr[col0 + k]), kCeLog2e, -ll));
+      dst[col0 + k] = from_arith<T>(fmaf(p, Tr, -(float)to_arith(tr[col0 + k])) * g);
     }
   }
 }
@@ -317,6 +481,76 @@ int supa_amd_cross_entropy_backward(const void* grad_out, const void* logits, in
       else
         k_ce_bwd<T, false><<<grid, kCeBwdBlock, 0, st>>>(gs, x + r0 * c, target + r0, lse + r0, count, c, ignore_index,
                                                       reduction, gx + r0 * c);
+      const int rc = launch_status();
+      if (rc) return rc;
+    }
+    return SUPA_AMD_OK;
+  });
+}
+
+int supa_amd_cross_entropy_prob_forward(const void* logits, const void* target, int32_t dtype, int64_t n, int64_t c,
+                                        int reduction, void* out, float* lse, float* tsum, void* workspace,
+                                        int64_t workspace_bytes, void* stream) {
+  if (n < 0 || c <= 0 || n >= (int64_t(1) << 31)) return SUPA_AMD_EINVAL;
+  if (reduction != SUPA_AMD_REDUCTION_NONE && reduction != SUPA_AMD_REDUCTION_MEAN &&
+      reduction != SUPA_AMD_REDUCTION_SUM)
+    return SUPA_AMD_EINVAL;
+  if (!out || (n > 0 && (!logits || !target || !lse || !tsum))) return SUPA_AMD_EINVAL;
+  if (n > 0 && (!workspace || workspace_bytes < supa_amd_cross_entropy_workspace_bytes(n))) return SUPA_AMD_EWORKSPACE;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return with_ce_storage(dtype, [&](auto* tag) -> int {
+    using T = std::remove_pointer_t<decltype(tag)>;
+    constexpr int V = CeVec<T>::V;
+    float* rows = static_cast<float*>(workspace);
+    T* o = static_cast<T*>(out);
+    if (n > 0) {
+      const T* x = static_cast<const T*>(logits);
+      const T* t = static_cast<const T*>(target);
+      T* on = reduction == SUPA_AMD_REDUCTION_NONE ? o : nullptr;
+      if (aligned(logits, 16) && aligned(target, 16) && (c % V) == 0)
+        k_ce_prob_fwd<T, true><<<(unsigned)n, kCeBlock, 0, st>>>(x, t, c, rows, lse, tsum, on);
+      else
+        k_ce_prob_fwd<T, false><<<(unsigned)n, kCeBlock, 0, st>>>(x, t, c, rows, lse, tsum, on);
+      const int rc = launch_status();
+      if (rc) return rc;
+    }
+    if (reduction == SUPA_AMD_REDUCTION_NONE) return SUPA_AMD_OK;
+    k_ce_final<T><<<1, kCeBlock, 0, st>>>(rows, nullptr, n, c, 0, reduction == SUPA_AMD_REDUCTION_MEAN ? 1 : 0, o,
+                                          nullptr);
+    return launch_status();
+  });
+}
+
+int supa_amd_cross_entropy_prob_backward(const void* grad_out, const void* logits, const void* target, int32_t dtype,
+                                         const float* lse, const float* tsum, int64_t n, int64_t c, int reduction,
+                                         void* grad_logits, void* stream) {
+  if (n < 0 || c <= 0 || n >= (int64_t(1) << 31)) return SUPA_AMD_EINVAL;
+  if (n == 0) return SUPA_AMD_OK;
+  if (!grad_out || !logits || !target || !lse || !tsum || !grad_logits) return SUPA_AMD_EINVAL;
+  if (reduction != SUPA_AMD_REDUCTION_NONE && reduction != SUPA_AMD_REDUCTION_MEAN &&
+      reduction != SUPA_AMD_REDUCTION_SUM)
+    return SUPA_AMD_EINVAL;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return with_ce_storage(dtype, [&](auto* tag) -> int {
+    using T = std::remove_pointer_t<decltype(tag)>;
+    constexpr int V = CeVec<T>::V;
+    const bool vecok = aligned(logits, 16) && aligned(target, 16) && aligned(grad_logits, 16) && (c % V) == 0;
+    const T* g = static_cast<const T*>(grad_out);
+    const T* x = static_cast<const T*>(logits);
+    const T* t = static_cast<const T*>(target);
+    T* gx = static_cast<T*>(grad_logits);
+    const float inv_n = 1.0f / (float)n;
+    const unsigned gx_blocks = (unsigned)((c + (int64_t)kCeBwdBlock * V - 1) / ((int64_t)kCeBwdBlock * V));
+    for (int64_t r0 = 0; r0 < n; r0 += 65535) {
+      const int64_t rows = std::min<int64_t>(65535, n - r0);
+      const T* gs = reduction == SUPA_AMD_REDUCTION_NONE ? g + r0 : g;
+      const dim3 grid(gx_blocks, (unsigned)rows);
+      if (vecok)
+        k_ce_prob_bwd<T, true><<<grid, kCeBwdBlock, 0, st>>>(gs, x + r0 * c, t + r0 * c, lse + r0, tsum + r0, c,
+                                                          reduction, inv_n, gx + r0 * c);
+      else
+        k_ce_prob_bwd<T, false><<<grid, kCeBwdBlock, 0, st>>>(gs, x + r0 * c, t + r0 * c, lse + r0, tsum + r0, c,
+                                                           reduction, inv_n, gx + r0 * c);
       const int rc = launch_status();
       if (rc) return rc;
     }

@@ -230,16 +230,21 @@ def set_cpu_fallback_enabled(on: bool) -> None:
     _C.set_cpu_fallback_enabled(bool(on))
 
 
-def set_fused_cross_entropy_enabled(on: bool) -> None:
-    """Route 2-d cross_entropy (f32/bf16/f16 logits, int64 targets, no class
-    weight, no label smoothing) through the fused kernels: one read of the
-    logits forward, one read + one write backward.  Off by default: the
-    default is the reference's log_softmax + nll_loss decomposition."""
-    _C.set_fused_cross_entropy_enabled(bool(on))
+def set_fused_cross_entropy_enabled(on) -> None:
+    """Routing of 2-d cross_entropy (f32/bf16/f16 logits; int64 class targets
+    or a probability target of the logits' shape and dtype; no class weight,
+    no label smoothing) to the fused kernels: one read of the logits (and
+    target) forward, one read + one write backward.
+    None (the default): the reference's routing -- float32 logits fused,
+    bfloat16 / float16 through the log_softmax + nll_loss decomposition.
+    True: every floating dtype fused.  False: none fused."""
+    _C.set_fused_cross_entropy_mode(-1 if on is None else (1 if on else 0))
 
 
-def fused_cross_entropy_enabled() -> bool:
-    return bool(_C.fused_cross_entropy_enabled())
+def fused_cross_entropy_enabled():
+    """None (the reference's routing: float32 fused), True or False."""
+    m = int(_C.fused_cross_entropy_mode())
+    return None if m < 0 else bool(m)
 
 
 def set_fused_bce_backward_enabled(on: bool) -> None:
