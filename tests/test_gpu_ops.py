@@ -849,6 +849,44 @@ def test_fused_adam_bit_exact(amsgrad, no_fallback):
         assert np.array_equal(opt.state[dp[i]]["exp_avg_sq"].cpu().numpy().ravel(), hv)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+@pytest.mark.parametrize("weight_decay", [0.0, 0.01])
+def test_fused_adamw_plain_modes(dtype, weight_decay, no_fallback):
+    """AdamW(fused=True) without weight decay and with it, float32 and
+    float16, on shapes with full chunks, a partial chunk, a partial vector and
+    an unaligned view's scalar path: bit-exact against the oracle's step
+    (16-bit state rounded after every step)."""
+    shapes = [(1024, 513), (4097,), (3, 5)]
+    g = torch.Generator().manual_seed(76)
+    params = [(torch.randn(s, generator=g) * 0.02).to(dtype) for s in shapes]
+    grads = [(torch.randn(s, generator=g) * 1e-3).to(dtype) for s in shapes]
+    dp = [dev(p).requires_grad_() for p in params]
+    # an unaligned parameter: a view one element into its storage
+    base = dev(torch.zeros(4098, dtype=dtype))
+    off = base[1:].view(4097)
+    off.copy_(dp[1].detach())
+    dp[1] = off.requires_grad_()
+    opt = torch.optim.AdamW(dp, lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=weight_decay, fused=True)
+    for _ in range(4):
+        for p, gr in zip(dp, grads):
+            p.grad = dev(gr)
+        opt.step()
+    rnd = (lambda a: a) if dtype == torch.float32 else \
+        (lambda a: a.astype(np.float16).astype(np.float32))
+    for i in range(len(shapes)):
+        hp = params[i].float().numpy().ravel().copy()
+        hg = grads[i].float().numpy().ravel().copy()
+        hm, hv = np.zeros_like(hp), np.zeros_like(hp)
+        for step in range(1, 5):
+            O.adamw_step(hp, hg, hm, hv, float(step), 1e-3, 0.9, 0.999, weight_decay, 1e-8)
+            for a in (hp, hm, hv):
+                a[:] = rnd(a)
+        assert np.array_equal(dp[i].detach().float().cpu().numpy().ravel(), hp), i
+        st = opt.state[dp[i]]
+        assert np.array_equal(st["exp_avg"].float().cpu().numpy().ravel(), hm), i
+        assert np.array_equal(st["exp_avg_sq"].float().cpu().numpy().ravel(), hv), i
+
+
 def test_foreach_list_and_scalar(no_fallback):
     shapes = [(4096, 4096), (4096,), (333, 17)]
     xs = [seeded(s, 40 + i) for i, s in enumerate(shapes)]

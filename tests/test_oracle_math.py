@@ -151,3 +151,34 @@ def test_gelu_none_error_is_the_reference_formula_conditioning():
     ex = 0.5 * xd * special.erfc(-xd / math.sqrt(2))
     ulp = np.ldexp(1.0, np.maximum(np.frexp(np.abs(ex))[1] - 24, -149))
     assert np.all(np.abs(got - ex) <= 2 * ulp + np.abs(0.5 * xd) * 2.0 ** -23)
+
+
+def test_quotient_by_a_constant_from_a_binary64_reciprocal():
+    """The fused AdamW kernel rounds sqrt(v) / c (c = bias_correction2_sqrt, a
+    per-tensor float32 constant in [2^-60, 1]) from the binary64 product
+    sqrt(v) * RN64(1 / c).  Within 2^-52 of the exact quotient, that rounds
+    to the IEEE float32 quotient for every float32 dividend: checked here on
+    whole binades of dividends (every float32 in [1, 2) and [2^-70, 2^-69))
+    for c of AdamW's first ten steps (beta2 = 0.999), and 2^20 random
+    dividends over the whole normal range for c of steps 1..2000 (every 37th;
+    beta2 = 0.999, 0.95) and 32 random c in [2^-60, 1]."""
+    lo = np.arange(0x3F800000, 0x40000000, dtype=np.uint32).view(np.float32)
+    tiny = np.arange(0x1C800000, 0x1D000000, dtype=np.uint32).view(np.float32)
+    rng = np.random.default_rng(7)
+    wide = np.exp2(rng.uniform(-125, 125, 1 << 20)).astype(np.float32)
+
+    def check(c, s):
+        c = np.float32(c)
+        assert 2.0 ** -60 <= c <= 1.0
+        got = (s.astype(np.float64) * (1.0 / np.float64(c))).astype(np.float32)
+        want = s / c  # IEEE float32 division
+        assert np.array_equal(got, want), (float(c), int((got != want).sum()))
+
+    for step in range(1, 11):
+        c = math.sqrt(1.0 - 0.999 ** step)
+        check(c, lo)
+        check(c, tiny)
+    cs = [math.sqrt(1.0 - b ** k) for b in (0.999, 0.95) for k in range(1, 2001, 37)]
+    cs += list(np.exp2(rng.uniform(-60, 0, 32)))
+    for c in cs:
+        check(c, wide)

@@ -143,6 +143,122 @@ k_adamw(AdamTable tab, AdamHyper h) {
     adamw_elem<T>(p[e], g[e], m[e], v[e], h.amsgrad ? vm + e : nullptr, h, lr, lr_wd, bc1, bc2_sqrt, step_size);
 }
 
+// AdamW / Adam without amsgrad, maximize, grad_scale, found_inf or a device
+// lr (what torch.optim.AdamW(fused=True) runs by default): the same
+// arithmetic as adamw_elem with the configuration fixed at compile time
+// (MODE 0: AdamW with weight decay, 1: Adam with weight decay, 2: no weight
+// decay), so the four elements of a vector are straight-line code, and one
+// division fewer per element: sqrt(v) / bc2_sqrt, a float32 quotient by a
+// per-tensor constant c, is rounded from the binary64 product
+// sqrt(v) * RN64(1 / c).  That product is within 2^-52 (relative) of the
+// exact quotient, and a quotient of two binary32 numbers that is not a
+// binary32 midpoint lies at least 2^-49 (relative) from every midpoint, so
+// the rounding to binary32 is the IEEE quotient's, for every c in
+// [2^-60, 1] (a normal-range quotient; other c take the division).  The
+// wave runs at raised priority while it issues its loads (as k_contig's
+// heavy functors).
+// One vector of each stream per thread: two (with the loads of both issued
+// first) measured 60 % of the HBM roofline against 74-75 % at c5.
+constexpr int kAdamPlainUnroll = 1;
+
+template <int MODE>
+__device__ __forceinline__ void adamw_plain_elem(float& param, float grad, float& ea, float& eas, double lr_wd,
+                                                 double wd, double beta1, double omb1, double beta2, double omb2,
+                                                 double eps, float c, double rc, bool exact_rc, float step_size) {
+  if constexpr (MODE == 0) param = (float)fma(-lr_wd, (double)param, (double)param);
+  if constexpr (MODE == 1) grad = (float)((double)grad + (double)param * wd);
+  ea = (float)fma(beta1, (double)ea, omb1 * (double)grad);
+  eas = (float)fma(beta2, (double)eas, (omb2 * (double)grad) * (double)grad);
+  const float sq = sqrtf(eas);
+  const float q = exact_rc ? (float)((double)sq * rc) : sq / c;
+  const float denom = (float)((double)q + eps);
+  param = param - (step_size * ea) / denom;
+}
+
+template <typename T, int64_t CHUNK, int MODE, int UNR>
+__global__ void __launch_bounds__(kMtaBlock)
+k_adamw_plain(AdamTable tab, AdamHyper h) {
+  constexpr int V = 16 / sizeof(T);
+  const MtaRange r = mta_range<CHUNK>(tab);
+  const int k = r.k;
+  const int64_t lo = r.lo, hi = r.hi;
+  const double lr = h.lr;
+  const float step = *tab.step[k];
+  const float bc1 = (float)(1.0 - pow_steps(h.beta1, step));
+  const float bc2_sqrt = (float)sqrt(1.0 - pow_steps(h.beta2, step));
+  const float step_size = (float)(lr / (double)bc1);
+  const double lr_wd = lr * h.weight_decay;
+  const double omb1 = 1.0 - h.beta1, omb2 = 1.0 - h.beta2;
+  const bool exact_rc = bc2_sqrt >= 0x1p-60f && bc2_sqrt <= 1.0f;
+  const double rc = 1.0 / (double)bc2_sqrt;
+  T* p = static_cast<T*>(tab.p[k]);
+  T* g = static_cast<T*>(tab.g[k]);
+  T* m = static_cast<T*>(tab.m[k]);
+  T* v = static_cast<T*>(tab.v[k]);
+  int64_t start = lo;
+  if (aligned(p, 16) && aligned(g, 16) && aligned(m, 16) && aligned(v, 16)) {
+    const int64_t nv = (hi - lo) / V;  // at most UNR * kMtaBlock vectors
+    if (nv == (int64_t)UNR * kMtaBlock) {  // a full chunk: no guards
+      Vec<T, V> P[UNR], G[UNR], M[UNR], W[UNR];
+      __builtin_amdgcn_s_setprio(3);
+#pragma unroll
+      for (int u = 0; u < UNR; ++u) {
+        const int64_t e = lo + (threadIdx.x + (int64_t)u * kMtaBlock) * V;
+        P[u] = ld_stream(reinterpret_cast<const Vec<T, V>*>(p + e));
+        G[u] = ld_stream(reinterpret_cast<const Vec<T, V>*>(g + e));
+        M[u] = ld_stream(reinterpret_cast<const Vec<T, V>*>(m + e));
+        W[u] = ld_stream(reinterpret_cast<const Vec<T, V>*>(v + e));
+      }
+      __builtin_amdgcn_s_setprio(0);
+#pragma unroll
+      for (int u = 0; u < UNR; ++u) {
+        const int64_t e = lo + (threadIdx.x + (int64_t)u * kMtaBlock) * V;
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+          float pp = (float)to_arith(P[u].v[j]), ea = (float)to_arith(M[u].v[j]), eas = (float)to_arith(W[u].v[j]);
+          adamw_plain_elem<MODE>(pp, (float)to_arith(G[u].v[j]), ea, eas, lr_wd, h.weight_decay, h.beta1, omb1,
+                                 h.beta2, omb2, h.eps, bc2_sqrt, rc, exact_rc, step_size);
+          P[u].v[j] = from_arith<T>(pp);
+          M[u].v[j] = from_arith<T>(ea);
+          W[u].v[j] = from_arith<T>(eas);
+        }
+        st_stream(reinterpret_cast<Vec<T, V>*>(p + e), P[u]);
+        st_stream(reinterpret_cast<Vec<T, V>*>(m + e), M[u]);
+        st_stream(reinterpret_cast<Vec<T, V>*>(v + e), W[u]);
+      }
+      return;
+    }
+    for (int64_t i = threadIdx.x; i < nv; i += kMtaBlock) {
+      const int64_t e = lo + i * V;
+      Vec<T, V> P = ld_stream(reinterpret_cast<const Vec<T, V>*>(p + e));
+      const Vec<T, V> G = ld_stream(reinterpret_cast<const Vec<T, V>*>(g + e));
+      Vec<T, V> M = ld_stream(reinterpret_cast<const Vec<T, V>*>(m + e));
+      Vec<T, V> W = ld_stream(reinterpret_cast<const Vec<T, V>*>(v + e));
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        float pp = (float)to_arith(P.v[j]), ea = (float)to_arith(M.v[j]), eas = (float)to_arith(W.v[j]);
+        adamw_plain_elem<MODE>(pp, (float)to_arith(G.v[j]), ea, eas, lr_wd, h.weight_decay, h.beta1, omb1,
+                               h.beta2, omb2, h.eps, bc2_sqrt, rc, exact_rc, step_size);
+        P.v[j] = from_arith<T>(pp);
+        M.v[j] = from_arith<T>(ea);
+        W.v[j] = from_arith<T>(eas);
+      }
+      st_stream(reinterpret_cast<Vec<T, V>*>(p + e), P);
+      st_stream(reinterpret_cast<Vec<T, V>*>(m + e), M);
+      st_stream(reinterpret_cast<Vec<T, V>*>(v + e), W);
+    }
+    start = lo + nv * V;
+  }
+  for (int64_t e = start + threadIdx.x; e < hi; e += kMtaBlock) {
+    float pp = (float)to_arith(p[e]), ea = (float)to_arith(m[e]), eas = (float)to_arith(v[e]);
+    adamw_plain_elem<MODE>(pp, (float)to_arith(g[e]), ea, eas, lr_wd, h.weight_decay, h.beta1, omb1, h.beta2, omb2,
+                           h.eps, bc2_sqrt, rc, exact_rc, step_size);
+    p[e] = from_arith<T>(pp);
+    m[e] = from_arith<T>(ea);
+    v[e] = from_arith<T>(eas);
+  }
+}
+
 // ------------------------------------------------------------- fused SGD
 struct SgdTable {
   void* p[kMtaTensors];
@@ -309,6 +425,35 @@ int launch_adamw(int32_t ntensors, void* const* params, void* const* grads, void
       [&](const AdamTable& tab, uint32_t chunks) { k_adamw<T, CHUNK, UNR><<<chunks, kMtaBlock, 0, st>>>(tab, h); });
 }
 
+// The plain configurations (k_adamw_plain): PU vectors per thread, chunks of
+// PU * kMtaBlock vectors.
+template <typename T, int PU>
+int launch_adamw_plain(int32_t ntensors, void* const* params, void* const* grads, void* const* exp_avgs,
+                       void* const* exp_avg_sqs, void* const* state_steps, const int64_t* numel, const AdamHyper& h,
+                       hipStream_t st) {
+  constexpr int64_t CHUNK = chunk_one<T>() * PU;
+  return mta_for_tables<CHUNK, AdamTable>(
+      ntensors, numel,
+      [&](AdamTable& tab, int slot, int i) -> int {
+        if (!state_steps[i]) return SUPA_AMD_EINVAL;
+        tab.p[slot] = params[i];
+        tab.g[slot] = grads[i];
+        tab.m[slot] = exp_avgs[i];
+        tab.v[slot] = exp_avg_sqs[i];
+        tab.vmax[slot] = nullptr;
+        tab.step[slot] = static_cast<const float*>(state_steps[i]);
+        return SUPA_AMD_OK;
+      },
+      [&](const AdamTable& tab, uint32_t chunks) {
+        if (h.weight_decay == 0.0)
+          k_adamw_plain<T, CHUNK, 2, PU><<<chunks, kMtaBlock, 0, st>>>(tab, h);
+        else if (h.l2)
+          k_adamw_plain<T, CHUNK, 1, PU><<<chunks, kMtaBlock, 0, st>>>(tab, h);
+        else
+          k_adamw_plain<T, CHUNK, 0, PU><<<chunks, kMtaBlock, 0, st>>>(tab, h);
+      });
+}
+
 template <typename T, bool MOM>
 int launch_sgd(int32_t ntensors, void* const* params, void* const* grads, void* const* bufs, const int64_t* numel,
                const SgdHyper& h, hipStream_t st) {
@@ -391,8 +536,14 @@ int fused_adam_any(int l2, int32_t ntensors, void* const* params, void* const* g
   hipStream_t st = static_cast<hipStream_t>(stream);
   const AdamHyper h{lr,        beta1,      beta2,     weight_decay,          eps, lr_ptr,
                     grad_scale, found_inf, amsgrad ? 1 : 0, maximize ? 1 : 0, l2};
+  const bool plain = !amsgrad && !maximize && !grad_scale && !found_inf && !lr_ptr;
   return with_mta_storage(dtype, [&](auto* tag) -> int {
     using T = std::remove_pointer_t<decltype(tag)>;
+    if constexpr (!std::is_same<T, double>::value) {
+      if (plain)
+        return launch_adamw_plain<T, kAdamPlainUnroll>(ntensors, params, grads, exp_avgs, exp_avg_sqs, state_steps,
+                                                       numel, h, st);
+    }
     return launch_adamw<T, chunk_one<T>(), 1>(ntensors, params, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs, state_steps, numel,
                                    h, st);
   });
