@@ -618,33 +618,39 @@ def derive_traffic(fetch_csv, write_csv):
     print(json.dumps(out))
 
 
-# (label, exact kernel name, algorithmic bytes per launch) of the bench's
-# dominant kernels, for the roofline rows of --render-kernel-stats
+# (label, exact kernel name, launch grid in threads or None for any, algorithmic
+# bytes per launch) of the bench's dominant kernels, for the roofline rows of
+# --render-kernel-stats.  The grid singles out c1's launches of templates that
+# other configs launch too (c4's and c5's muls run the same k_contig).
 STATS_ROOFLINE_ROWS = [
     ("c2 gelu('tanh') f32 [64,2048,4096] -- the headline kernel",
-     "sa::k_contig<64, 4, sa::UnaryOp<1, float>, float, float, float, float>", 8 * C2_N),
+     "sa::k_contig<64, 4, sa::UnaryOp<1, float>, float, float, float, float>", None, 8 * C2_N),
     ("c2 add bf16 x + f32 bias -> f32 (both legs)",
-     "sa::k_row2d<64, 4, sa::AddOp<float>, float, float, float, sa::bf16, float>", C2_ADD_BYTES),
+     "sa::k_row2d<64, 4, sa::AddOp<float>, float, float, float, sa::bf16, float>", None, C2_ADD_BYTES),
     ("c2 transposed leg: bf16 x `.contiguous()` (LDS-tiled transpose)",
-     "sa::k_transpose_vec<sa::IdentityOp<float>, float, sa::bf16, sa::bf16, sa::bf16>", 4 * C2_N),
-    ("c1 add f32 [4096,4096]", "sa::k_contig<64, 4, sa::AddOp<float>, float, float, float, float, float>", 12 * C1_N),
-    ("c1 mul", "sa::k_contig<64, 4, sa::MulOp<float>, float, float, float, float, float>", 12 * C1_N),
-    ("c1 gelu('none')", "sa::k_contig<64, 4, sa::UnaryOp<0, float>, float, float, float, float>", 8 * C1_N),
-    ("c1 silu", "sa::k_contig<64, 4, sa::UnaryOp<2, float>, float, float, float, float>", 8 * C1_N),
-    ("c3 _log_softmax", "sa::k_lsm_fwd_reg<sa::bf16, sa::bf16, 16, true>", 4 * C3_NV),
-    ("c3 nll_loss_backward", "sa::k_nll_bwd<sa::bf16, 8>", 2 * C3_NV + 65538),
-    ("c3 _log_softmax_backward_data", "sa::k_lsm_bwd_reg<sa::bf16, sa::bf16, 16>", 6 * C3_NV),
-    ("c3 fused cross-entropy forward (opt-in)", "sa::k_ce_fwd<sa::bf16, true>", 2 * C3_NV),
-    ("c3 fused cross-entropy backward (opt-in)", "sa::k_ce_bwd<sa::bf16, true>", 4 * C3_NV),
+     "sa::k_transpose_vec<sa::IdentityOp<float>, float, sa::bf16, sa::bf16, sa::bf16>", None, 4 * C2_N),
+    ("c1 add f32 [4096,4096]", "sa::k_contig<64, 4, sa::AddOp<float>, float, float, float, float, float>",
+     C1_N // 4, 12 * C1_N),
+    ("c1 mul", "sa::k_contig<64, 4, sa::MulOp<float>, float, float, float, float, float>", C1_N // 4, 12 * C1_N),
+    ("c1 gelu('none')", "sa::k_contig<64, 4, sa::UnaryOp<0, float>, float, float, float, float>", C1_N // 4,
+     8 * C1_N),
+    ("c1 silu", "sa::k_contig<64, 4, sa::UnaryOp<2, float>, float, float, float, float>", C1_N // 4, 8 * C1_N),
+    ("c3 _log_softmax", "sa::k_lsm_fwd_reg<sa::bf16, sa::bf16, 16, true>", None, 4 * C3_NV),
+    ("c3 nll_loss_backward", "sa::k_nll_bwd<sa::bf16, 8>", None, 2 * C3_NV + 65538),
+    ("c3 _log_softmax_backward_data", "sa::k_lsm_bwd_reg<sa::bf16, sa::bf16, 16>", None, 6 * C3_NV),
+    ("c3 fused cross-entropy forward (opt-in)", "sa::k_ce_fwd<sa::bf16, true>", None, 2 * C3_NV),
+    ("c3 fused cross-entropy backward (opt-in)", "sa::k_ce_bwd<sa::bf16, true>", None, 4 * C3_NV),
     ("c5 _fused_adamw_ (two launches per step, 40 + 32 tensors; half of 28 B x 1.62 G each on average)",
-     "sa::k_adamw<float, 256l, 1>", 14 * 1619066880),
+     "sa::k_adamw_plain<float, 256l, 0, 1>", None, 14 * 1619066880),
 ]
 
 
 def render_kernel_stats(stats_csv, bench_log):
     """profiles/kernel_stats_all_configs.md from the kernel_stats.csv of a
-    `rocprofv3 --kernel-trace --stats` run of `bench.py --no-cpu` and that
-    run's JSON line (the bench's live HIP-event timing of the same launches)."""
+    `rocprofv3 --kernel-trace --stats` run of `bench.py --no-cpu`, the
+    kernel_trace.csv beside it (each roofline row's launches, by grid) and
+    that run's JSON line (the bench's live HIP-event timing of the same
+    launches)."""
     import csv
 
     with open(stats_csv) as f:
@@ -655,6 +661,20 @@ def render_kernel_stats(stats_csv, bench_log):
     def short(n):
         n = n.replace("void ", "")
         return n[: n.index(">(") + 1] if ">(" in n else n.split("(")[0]
+
+    # per (kernel, grid) launch durations from the trace
+    wanted = {name for _, name, _, _ in STATS_ROOFLINE_ROWS}
+    durations = {}
+    with open(stats_csv.replace("_kernel_stats.csv", "_kernel_trace.csv")) as f:
+        for r in csv.DictReader(f):
+            name = short(r["Kernel_Name"])
+            if name in wanted:
+                ns = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+                durations.setdefault((name, int(r["Grid_Size_X"])), []).append(ns)
+
+    def launches(name, grid):
+        got = [d for (n, g), v in durations.items() if n == name and (grid is None or g == grid) for d in v]
+        return (len(got), sum(got) / len(got) / 1e3) if got else (0, None)
 
     by_name = {short(r["Name"]): r for r in rows}
     out = ["# Kernel statistics, every bench config (MI355X, gfx950)", "",
@@ -668,21 +688,23 @@ def render_kernel_stats(stats_csv, bench_log):
            "3 rotating input sets, c5 = 72-tensor fused AdamW, the default foreach AdamW, clip_grad_norm_ and the "
            "foreach / AMP lines.  `k_contig<BS, VEC, ...>`, `k_row2d<BS, VEC, ...>`: BS threads per workgroup "
            "(64 = one wavefront).  Only this library's kernels are listed; the rest of the trace is torch's own "
-           "input generation on its HIP device before the copies into supa tensors.", "",
+           "input generation on its HIP device before the copies into supa tensors.  The roofline rows average "
+           "the kernel trace's launches of that kernel at that grid (c1's rows: c1's grid of 4 194 304 threads, "
+           "since c4 and c5 launch the same templates at other sizes); the table of all kernels averages every "
+           "launch of a name.", "",
            "## Roofline rows (algorithmic bytes per launch / average duration)", "",
-           "| kernel | name | calls | avg us | algorithmic B | GB/s | % of 8 TB/s |",
-           "|---|---|---:|---:|---:|---:|---:|"]
-    for label, name, nbytes in STATS_ROOFLINE_ROWS:
-        r = by_name.get(name)
-        if r is None:
+           "| kernel | name | grid (threads) | calls | avg us | algorithmic B | GB/s | % of 8 TB/s |",
+           "|---|---|---:|---:|---:|---:|---:|---:|"]
+    for label, name, grid, nbytes in STATS_ROOFLINE_ROWS:
+        calls, us = launches(name, grid)
+        if not calls:
             continue
-        us = float(r["AverageNs"]) / 1e3
         g = nbytes / (us * 1e-6) / 1e9
-        out.append(f"| {label} | `{name}` | {r['Calls']} | {us:.1f} | {nbytes:,} | {g:.0f} | {g / 80:.1f} |")
+        out.append(f"| {label} | `{name}` | {'any' if grid is None else f'{grid:,}'} | {calls} | {us:.1f} | "
+                   f"{nbytes:,} | {g:.0f} | {g / 80:.1f} |")
     rf = bench.get("roofline", {})
-    head = by_name.get(STATS_ROOFLINE_ROWS[0][1])
-    if head is not None and rf.get("avg_launch_ms"):
-        us = float(head["AverageNs"]) / 1e3
+    calls, us = launches(STATS_ROOFLINE_ROWS[0][1], STATS_ROOFLINE_ROWS[0][2])
+    if calls and rf.get("avg_launch_ms"):
         bus = rf["avg_launch_ms"] * 1e3
         out += ["", f"Cross-check of the headline's dominant kernel: {us:.1f} us average here, {bus:.1f} us in the "
                 f"same run's live HIP-event timing (`bench.py` `roofline.avg_launch_ms`): within "
