@@ -13,7 +13,7 @@ struct Tab {
   uint32_t chunk_start[sa::kMtaTensors + 1];
   int32_t ntensors;
   uint32_t bucket_shift;
-  uint8_t bucket[sa::kMtaBuckets];
+  sa::MtaBucket bucket[sa::kMtaBuckets];
 };
 
 static int bisect(const Tab& t, uint32_t blk) {

@@ -21,7 +21,7 @@ struct MtaTable {
   uint32_t chunk_start[kMtaTensors + 1];
   int32_t ntensors;
   uint32_t bucket_shift;
-  uint8_t bucket[kMtaBuckets];
+  MtaBucket bucket[kMtaBuckets];
 };
 
 constexpr int kFeList = SUPA_AMD_FOREACH_LIST;

@@ -22,7 +22,7 @@ struct AdamTable {
   uint32_t chunk_start[kMtaTensors + 1];
   int32_t ntensors;
   uint32_t bucket_shift;
-  uint8_t bucket[kMtaBuckets];
+  MtaBucket bucket[kMtaBuckets];
 };
 
 struct AdamHyper {
@@ -268,7 +268,7 @@ struct SgdTable {
   uint32_t chunk_start[kMtaTensors + 1];
   int32_t ntensors;
   uint32_t bucket_shift;
-  uint8_t bucket[kMtaBuckets];
+  MtaBucket bucket[kMtaBuckets];
 };
 
 struct SgdHyper {
@@ -355,7 +355,7 @@ struct UnscaleTable {
   uint32_t chunk_start[kMtaTensors + 1];
   int32_t ntensors;
   uint32_t bucket_shift;
-  uint8_t bucket[kMtaBuckets];
+  MtaBucket bucket[kMtaBuckets];
 };
 
 template <typename T, int64_t CHUNK>

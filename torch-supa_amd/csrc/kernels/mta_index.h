@@ -24,7 +24,13 @@ namespace sa {
 
 constexpr int kMtaTensors = 40;
 constexpr int kMtaBuckets = 64;
-static_assert(kMtaTensors <= 255, "bucket entries are bytes");
+// 32-bit entries: gfx9 scalar loads read whole dwords, so with byte entries
+// the compiler fetched a workgroup's entry with a vector load and waited for
+// it before the scalar lookups and the first data load could issue.  Over
+// c5's 72 tensors the norm partials ran at 77-80 % of the HBM roofline with
+// byte entries and at 90-92 % with 32-bit ones (the kernel over one flat
+// buffer with no lookup: 91 %).
+using MtaBucket = uint32_t;
 
 // Fills tab.bucket / tab.bucket_shift from tab.chunk_start[0..ntensors] and
 // the table's chunk count.
@@ -38,7 +44,7 @@ void mta_index(Table& tab, uint32_t chunks) {
   for (int b = 0; b < kMtaBuckets; ++b) {
     const uint64_t first = (uint64_t)b << s;
     while (k + 1 < tab.ntensors && tab.chunk_start[k + 1] <= first) ++k;
-    tab.bucket[b] = (uint8_t)k;
+    tab.bucket[b] = (MtaBucket)k;
   }
 }
 
