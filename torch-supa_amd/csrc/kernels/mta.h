@@ -17,9 +17,9 @@ namespace sa {
 // One wavefront per workgroup: c5's fused AdamW moved 74 % of peak HBM
 // bandwidth with 64-thread workgroups against 71 % with 256 and 70 % with 128.
 constexpr int kMtaBlock = 64;
-// Elements per workgroup: one 16-byte vector per thread for the list forms and
-// AdamW, two for the scalar forms -- the fastest measured on MI355X (c5 AdamW
-// at 256 threads: 71 % of HBM peak against 66 % with 16384-element chunks).
+// Elements per workgroup: one 16-byte vector per thread -- the fastest
+// measured on MI355X (c5 AdamW at 256 threads: 71 % of HBM peak against 66 %
+// with 16384-element chunks).
 template <typename T> constexpr int64_t chunk_one() { return (int64_t)kMtaBlock * (16 / (int64_t)sizeof(T)); }
 
 // The [lo, hi) element range of block `blk` within tensor k.
