@@ -638,8 +638,8 @@ STATS_ROOFLINE_ROWS = [
     ("c3 _log_softmax", "sa::k_lsm_fwd_reg<sa::bf16, sa::bf16, 16, true>", None, 4 * C3_NV),
     ("c3 nll_loss_backward", "sa::k_nll_bwd<sa::bf16, 8>", None, 2 * C3_NV + 65538),
     ("c3 _log_softmax_backward_data", "sa::k_lsm_bwd_reg<sa::bf16, sa::bf16, 16>", None, 6 * C3_NV),
-    ("c3 fused cross-entropy forward (opt-in)", "sa::k_ce_fwd<sa::bf16, true>", None, 2 * C3_NV),
-    ("c3 fused cross-entropy backward (opt-in)", "sa::k_ce_bwd<sa::bf16, true>", None, 4 * C3_NV),
+    ("c3 fused cross-entropy forward (bf16 opt-in; float32 takes it by default)", "sa::k_ce_fwd<sa::bf16, true>", None, 2 * C3_NV),
+    ("c3 fused cross-entropy backward (bf16 opt-in; float32 takes it by default)", "sa::k_ce_bwd<sa::bf16, true>", None, 4 * C3_NV),
     ("c5 _fused_adamw_ (two launches per step, 40 + 32 tensors; half of 28 B x 1.62 G each on average)",
      "sa::k_adamw_plain<float, 256l, 0, 1>", None, 14 * 1619066880),
 ]
