@@ -734,11 +734,14 @@ def test_c4_full_size_losses(reduction, no_fallback):
 @pytest.mark.parametrize("reduction", ["none", "mean", "sum"])
 @pytest.mark.parametrize("with_pw,with_w", [(False, False), (True, False), (False, True), (True, True)])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_fused_bce_backward_matches_op_sequence(reduction, with_pw, with_w, dtype, no_fallback, supa):
+@pytest.mark.parametrize("shape", [(33, 4100), (5, 8200), (40, 1000)])
+def test_fused_bce_backward_matches_op_sequence(shape, reduction, with_pw, with_w, dtype, no_fallback, supa):
     """The one-kernel BCE-with-logits input gradient is bit-identical to the
     autograd formula's op-by-op evaluation on the same kernels (and, in
-    float32, to the oracle), for every pos_weight / weight combination."""
-    R, C = 33, 4100
+    float32, to the oracle), for every pos_weight / weight combination; rows
+    of more than 16 KiB take the one-vector row kernel (f32 at 4100 columns,
+    both dtypes at 8200), shorter ones the paired-row kernel."""
+    R, C = shape
     g = torch.Generator().manual_seed(101)
     x = (torch.randn(R, C, generator=g) * 2).to(dtype)
     tb = (torch.rand(R, C, generator=g) < 0.3).to(dtype)

@@ -262,6 +262,28 @@ int launch_static(const Op& op, const supa_amd_ew_desc& d, const int* tin, hipSt
         const uint32_t rows = (uint32_t)(pn / d0);
         const uint32_t bpr = (inner / VEC + kStreamBlock - 1) / kStreamBlock;
         const uint32_t K = row2d_pair(inner * (uint32_t)sizeof(OT), rows);
+        if constexpr (IsRowB<Op>::value) {
+          // long rows: one vector per thread (k_rowb), the functor's rounding
+          // and mean switches fixed at compile time (kRowB functors carry
+          // rt, mean and fixed<RT, MEAN>())
+          constexpr int kRt = std::is_same<OT, bf16>::value ? 1 : (std::is_same<OT, f16>::value ? 2 : 0);
+          bool rb = K == 1 && (uint64_t)inner * sizeof(OT) > kPairBytes / 2 && op.rt == kRt;
+          for (int k = 1; k <= N && rb; ++k)
+            if (c.mode[k] == R2_MID) rb = false;
+          if (rb) {
+            const uint32_t nvec = (uint32_t)(pn / VEC);
+            const unsigned nb = (nvec + kStreamBlock - 1) / kStreamBlock;
+            const FastDiv ivec(inner / VEC);
+            if (op.mean) {
+              const auto fop = op.template fixed<kRt, 1>();
+              k_rowb<VEC, decltype(fop), C, CT, OT, S...><<<nb, kStreamBlock, 0, st>>>(fop, c, nvec, ivec);
+            } else {
+              const auto fop = op.template fixed<kRt, 0>();
+              k_rowb<VEC, decltype(fop), C, CT, OT, S...><<<nb, kStreamBlock, 0, st>>>(fop, c, nvec, ivec);
+            }
+            return launch_status();
+          }
+        }
         const uint64_t blocks = (uint64_t)bpr * K * ((rows + kRow2dRows * K - 1) / (kRow2dRows * K));
         if (blocks < (1ull << 31)) {
           k_row2d<kStreamBlock, VEC, Op, C, CT, OT, S...><<<(unsigned)blocks, kStreamBlock, 0, st>>>(

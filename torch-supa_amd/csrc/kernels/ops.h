@@ -646,19 +646,26 @@ template <bool PW, bool W, typename C, bool HW = false> struct BceTermOp {
 // t [, pw] [, w]): u = pw * t; ((u + 1) - t) * sigmoid(x) - u, or
 // sigmoid(x) - t; * g; * w; / n.  rt: the storage dtype every intermediate is
 // rounded to (0 keep C, 1 bf16, 2 f16), as the op-by-op evaluation stores
-// each intermediate tensor.
-template <bool PW, bool W, typename C> struct BceBwdOp {
+// each intermediate tensor.  RT / MEAN >= 0 fix rt / mean at compile time
+// (the one-vector row-broadcast kernel, k_rowb, launches those forms: with
+// the switches read per element the c4 backward ran 3 points slower there).
+template <bool PW, bool W, typename C, int RT = -1, int MEAN = -1> struct BceBwdOp {
   static constexpr int arity = 3 + (PW ? 1 : 0) + (W ? 1 : 0);
+  static constexpr bool kRowB = true;
   C n;
   int mean;
   int rt;
   // 1 / n when n is a power of two, else 0: r * inv_n and r / n are then the
   // same correctly rounded value (the exact quotient), without the division
   C inv_n;
+  template <int R, int M> __device__ __host__ BceBwdOp<PW, W, C, R, M> fixed() const {
+    return BceBwdOp<PW, W, C, R, M>{n, mean, rt, inv_n};
+  }
   __device__ __forceinline__ C rnd(C v) const {
     if constexpr (std::is_same<C, float>::value) {
-      if (rt == 1) return bf16_to_f32(f32_to_bf16(v));
-      if (rt == 2) return (float)f32_to_f16(v);
+      const int r = RT >= 0 ? RT : rt;
+      if (r == 1) return bf16_to_f32(f32_to_bf16(v));
+      if (r == 2) return (float)f32_to_f16(v);
     }
     return v;
   }
@@ -674,7 +681,7 @@ template <bool PW, bool W, typename C> struct BceBwdOp {
     }
     r = rnd(r * g);
     if constexpr (W) r = rnd(r * v[3 + (PW ? 1 : 0)]);
-    if (mean) r = inv_n != C(0) ? r * inv_n : r / n;
+    if (MEAN >= 0 ? MEAN != 0 : mean != 0) r = inv_n != C(0) ? r * inv_n : r / n;
     return r;
   }
 };
