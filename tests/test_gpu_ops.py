@@ -733,7 +733,7 @@ def test_c4_full_size_losses(reduction, no_fallback):
 
 @pytest.mark.parametrize("reduction", ["none", "mean", "sum"])
 @pytest.mark.parametrize("with_pw,with_w", [(False, False), (True, False), (False, True), (True, True)])
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("shape", [(33, 4100), (5, 8200), (40, 1000)])
 def test_fused_bce_backward_matches_op_sequence(shape, reduction, with_pw, with_w, dtype, no_fallback, supa):
     """The one-kernel BCE-with-logits input gradient is bit-identical to the
