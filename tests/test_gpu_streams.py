@@ -131,9 +131,12 @@ def test_record_stream_defers_reuse(supa):
     w = torch.empty(m, device="supa")
     busy_after = not s.query()
     assert busy_before  # milliseconds of queued work: s cannot have drained yet
+    reused = w.data_ptr() == p
     if busy_after:  # s busy throughout the allocation: its event had not completed
-        assert w.data_ptr() != p
+        assert not reused
     s.synchronize()
+    if reused:  # s drained before the allocation looked: w holds the block; give it back
+        w = None
     w2 = torch.empty(m, device="supa")
     assert w2.data_ptr() == p  # s's event completed: the block is back
     assert torch.equal(y.cpu(), torch.full((m,), 2.0))
