@@ -733,21 +733,22 @@ def test_c4_full_size_losses(reduction, no_fallback):
 
 @pytest.mark.parametrize("reduction", ["none", "mean", "sum"])
 @pytest.mark.parametrize("with_pw,with_w", [(False, False), (True, False), (False, True), (True, True)])
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("shape", [(33, 4100), (5, 8200), (40, 1000)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16, torch.float64])
+@pytest.mark.parametrize("shape", [(33, 4100), (5, 8200), (40, 1000), (3, 2, 4100)])
 def test_fused_bce_backward_matches_op_sequence(shape, reduction, with_pw, with_w, dtype, no_fallback, supa):
     """The one-kernel BCE-with-logits input gradient is bit-identical to the
     autograd formula's op-by-op evaluation on the same kernels (and, in
     float32, to the oracle), for every pos_weight / weight combination; rows
-    of more than 16 KiB take the one-vector row kernel (f32 at 4100 columns,
-    both dtypes at 8200), shorter ones the paired-row kernel."""
-    R, C = shape
+    of more than 16 KiB take the one-vector row kernel (f32 / f64 at 4100
+    columns, every dtype at 8200; the 3-d shape's outer dims flattened into
+    rows, its weight per row), shorter ones the paired-row kernel."""
+    *R, C = shape
     g = torch.Generator().manual_seed(101)
-    x = (torch.randn(R, C, generator=g) * 2).to(dtype)
-    tb = (torch.rand(R, C, generator=g) < 0.3).to(dtype)
+    x = (torch.randn(*R, C, generator=g) * 2).to(dtype)
+    tb = (torch.rand(*R, C, generator=g) < 0.3).to(dtype)
     pw = (torch.rand(C, generator=g) * 1.5 + 0.5).to(dtype) if with_pw else None
-    w = (torch.rand(R, 1, generator=g) + 0.5).to(dtype) if with_w else None
-    go = (torch.randn(R, C, generator=g) if reduction == "none" else torch.ones(())).to(dtype)
+    w = (torch.rand(*R, 1, generator=g) + 0.5).to(dtype) if with_w else None
+    go = (torch.randn(*R, C, generator=g) if reduction == "none" else torch.ones(())).to(dtype)
     grads = {}
     for fused in (True, False):
         supa.supa.set_fused_bce_backward_enabled(fused)
