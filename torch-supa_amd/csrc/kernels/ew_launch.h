@@ -286,7 +286,11 @@ int launch_static(const Op& op, const supa_amd_ew_desc& d, const int* tin, hipSt
         }
         const uint64_t blocks = (uint64_t)bpr * K * ((rows + kRow2dRows * K - 1) / (kRow2dRows * K));
         if (blocks < (1ull << 31)) {
-          k_row2d<kStreamBlock, VEC, Op, C, CT, OT, S...><<<(unsigned)blocks, kStreamBlock, 0, st>>>(
+          // long launches: dynamic LDS the kernel does not use caps residency
+          // at 26 one-wave workgroups per CU (c2's bias add 81.7-82.3 ->
+          // 83.3-83.7 % of the HBM roofline; short launches lose from it)
+          const unsigned lds = blocks >= (1u << 19) ? 6144u : 0u;
+          k_row2d<kStreamBlock, VEC, Op, C, CT, OT, S...><<<(unsigned)blocks, kStreamBlock, lds, st>>>(
               op, c, inner, rows, FastDiv(bpr), FastDiv((uint32_t)d1), FastDiv(K));
           return launch_status();
         }

@@ -175,6 +175,42 @@ __device__ __forceinline__ void adamw_plain_elem(float& param, float grad, float
   param = param - (step_size * ea) / denom;
 }
 
+// The per-tensor constants of a step (from the tensor's device step count).
+struct AdamStepConst {
+  float bc2_sqrt, step_size;
+  double lr_wd, omb1, omb2, rc;
+  bool exact_rc;
+};
+__device__ __forceinline__ AdamStepConst adam_step_const(const AdamHyper& h, float step) {
+  AdamStepConst c;
+  const float bc1 = (float)(1.0 - pow_steps(h.beta1, step));
+  c.bc2_sqrt = (float)sqrt(1.0 - pow_steps(h.beta2, step));
+  c.step_size = (float)(h.lr / (double)bc1);
+  c.lr_wd = h.lr * h.weight_decay;
+  c.omb1 = 1.0 - h.beta1;
+  c.omb2 = 1.0 - h.beta2;
+  c.exact_rc = c.bc2_sqrt >= 0x1p-60f && c.bc2_sqrt <= 1.0f;
+  c.rc = 1.0 / (double)c.bc2_sqrt;
+  return c;
+}
+
+template <int MODE, typename T, int V>
+__device__ __forceinline__ void adamw_plain_vec(Vec<T, V>& P, const Vec<T, V>& G, Vec<T, V>& M, Vec<T, V>& W,
+                                                const AdamHyper& h, const AdamStepConst& c) {
+#pragma unroll
+  for (int j = 0; j < V; ++j) {
+    float pp = (float)to_arith(P.v[j]), ea = (float)to_arith(M.v[j]), eas = (float)to_arith(W.v[j]);
+    adamw_plain_elem<MODE>(pp, (float)to_arith(G.v[j]), ea, eas, c.lr_wd, h.weight_decay, h.beta1, c.omb1, h.beta2,
+                           c.omb2, h.eps, c.bc2_sqrt, c.rc, c.exact_rc, c.step_size);
+    P.v[j] = from_arith<T>(pp);
+    M.v[j] = from_arith<T>(ea);
+    W.v[j] = from_arith<T>(eas);
+  }
+}
+
+// A full, aligned chunk issues its four loads before it reads the step count
+// and computes the bias corrections (a chain of dependent scalar loads and
+// binary64 arithmetic), so the loads are in flight meanwhile.
 template <typename T, int64_t CHUNK, int MODE, int UNR>
 __global__ void __launch_bounds__(kMtaBlock)
 k_adamw_plain(AdamTable tab, AdamHyper h) {
@@ -182,67 +218,45 @@ k_adamw_plain(AdamTable tab, AdamHyper h) {
   const MtaRange r = mta_range<CHUNK>(tab);
   const int k = r.k;
   const int64_t lo = r.lo, hi = r.hi;
-  const double lr = h.lr;
-  const float step = *tab.step[k];
-  const float bc1 = (float)(1.0 - pow_steps(h.beta1, step));
-  const float bc2_sqrt = (float)sqrt(1.0 - pow_steps(h.beta2, step));
-  const float step_size = (float)(lr / (double)bc1);
-  const double lr_wd = lr * h.weight_decay;
-  const double omb1 = 1.0 - h.beta1, omb2 = 1.0 - h.beta2;
-  const bool exact_rc = bc2_sqrt >= 0x1p-60f && bc2_sqrt <= 1.0f;
-  const double rc = 1.0 / (double)bc2_sqrt;
   T* p = static_cast<T*>(tab.p[k]);
   T* g = static_cast<T*>(tab.g[k]);
   T* m = static_cast<T*>(tab.m[k]);
   T* v = static_cast<T*>(tab.v[k]);
-  int64_t start = lo;
-  if (aligned(p, 16) && aligned(g, 16) && aligned(m, 16) && aligned(v, 16)) {
-    const int64_t nv = (hi - lo) / V;  // at most UNR * kMtaBlock vectors
-    if (nv == (int64_t)UNR * kMtaBlock) {  // a full chunk: no guards
-      Vec<T, V> P[UNR], G[UNR], M[UNR], W[UNR];
-      __builtin_amdgcn_s_setprio(3);
+  const bool vec = aligned(p, 16) && aligned(g, 16) && aligned(m, 16) && aligned(v, 16);
+  const int64_t nv = (hi - lo) / V;  // at most UNR * kMtaBlock vectors
+  if (vec && nv == (int64_t)UNR * kMtaBlock) {  // a full chunk: no guards
+    Vec<T, V> P[UNR], G[UNR], M[UNR], W[UNR];
+    __builtin_amdgcn_s_setprio(3);
 #pragma unroll
-      for (int u = 0; u < UNR; ++u) {
-        const int64_t e = lo + (threadIdx.x + (int64_t)u * kMtaBlock) * V;
-        P[u] = ld_stream(reinterpret_cast<const Vec<T, V>*>(p + e));
-        G[u] = ld_stream(reinterpret_cast<const Vec<T, V>*>(g + e));
-        M[u] = ld_stream(reinterpret_cast<const Vec<T, V>*>(m + e));
-        W[u] = ld_stream(reinterpret_cast<const Vec<T, V>*>(v + e));
-      }
-      __builtin_amdgcn_s_setprio(0);
-#pragma unroll
-      for (int u = 0; u < UNR; ++u) {
-        const int64_t e = lo + (threadIdx.x + (int64_t)u * kMtaBlock) * V;
-#pragma unroll
-        for (int j = 0; j < V; ++j) {
-          float pp = (float)to_arith(P[u].v[j]), ea = (float)to_arith(M[u].v[j]), eas = (float)to_arith(W[u].v[j]);
-          adamw_plain_elem<MODE>(pp, (float)to_arith(G[u].v[j]), ea, eas, lr_wd, h.weight_decay, h.beta1, omb1,
-                                 h.beta2, omb2, h.eps, bc2_sqrt, rc, exact_rc, step_size);
-          P[u].v[j] = from_arith<T>(pp);
-          M[u].v[j] = from_arith<T>(ea);
-          W[u].v[j] = from_arith<T>(eas);
-        }
-        st_stream(reinterpret_cast<Vec<T, V>*>(p + e), P[u]);
-        st_stream(reinterpret_cast<Vec<T, V>*>(m + e), M[u]);
-        st_stream(reinterpret_cast<Vec<T, V>*>(v + e), W[u]);
-      }
-      return;
+    for (int u = 0; u < UNR; ++u) {
+      const int64_t e = lo + (threadIdx.x + (int64_t)u * kMtaBlock) * V;
+      P[u] = ld_stream(reinterpret_cast<const Vec<T, V>*>(p + e));
+      G[u] = ld_stream(reinterpret_cast<const Vec<T, V>*>(g + e));
+      M[u] = ld_stream(reinterpret_cast<const Vec<T, V>*>(m + e));
+      W[u] = ld_stream(reinterpret_cast<const Vec<T, V>*>(v + e));
     }
+    __builtin_amdgcn_s_setprio(0);
+    const AdamStepConst c = adam_step_const(h, *tab.step[k]);
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) {
+      const int64_t e = lo + (threadIdx.x + (int64_t)u * kMtaBlock) * V;
+      adamw_plain_vec<MODE, T, V>(P[u], G[u], M[u], W[u], h, c);
+      st_stream(reinterpret_cast<Vec<T, V>*>(p + e), P[u]);
+      st_stream(reinterpret_cast<Vec<T, V>*>(m + e), M[u]);
+      st_stream(reinterpret_cast<Vec<T, V>*>(v + e), W[u]);
+    }
+    return;
+  }
+  const AdamStepConst c = adam_step_const(h, *tab.step[k]);
+  int64_t start = lo;
+  if (vec) {
     for (int64_t i = threadIdx.x; i < nv; i += kMtaBlock) {
       const int64_t e = lo + i * V;
       Vec<T, V> P = ld_stream(reinterpret_cast<const Vec<T, V>*>(p + e));
       const Vec<T, V> G = ld_stream(reinterpret_cast<const Vec<T, V>*>(g + e));
       Vec<T, V> M = ld_stream(reinterpret_cast<const Vec<T, V>*>(m + e));
       Vec<T, V> W = ld_stream(reinterpret_cast<const Vec<T, V>*>(v + e));
-#pragma unroll
-      for (int j = 0; j < V; ++j) {
-        float pp = (float)to_arith(P.v[j]), ea = (float)to_arith(M.v[j]), eas = (float)to_arith(W.v[j]);
-        adamw_plain_elem<MODE>(pp, (float)to_arith(G.v[j]), ea, eas, lr_wd, h.weight_decay, h.beta1, omb1,
-                               h.beta2, omb2, h.eps, bc2_sqrt, rc, exact_rc, step_size);
-        P.v[j] = from_arith<T>(pp);
-        M.v[j] = from_arith<T>(ea);
-        W.v[j] = from_arith<T>(eas);
-      }
+      adamw_plain_vec<MODE, T, V>(P, G, M, W, h, c);
       st_stream(reinterpret_cast<Vec<T, V>*>(p + e), P);
       st_stream(reinterpret_cast<Vec<T, V>*>(m + e), M);
       st_stream(reinterpret_cast<Vec<T, V>*>(v + e), W);
@@ -251,8 +265,8 @@ k_adamw_plain(AdamTable tab, AdamHyper h) {
   }
   for (int64_t e = start + threadIdx.x; e < hi; e += kMtaBlock) {
     float pp = (float)to_arith(p[e]), ea = (float)to_arith(m[e]), eas = (float)to_arith(v[e]);
-    adamw_plain_elem<MODE>(pp, (float)to_arith(g[e]), ea, eas, lr_wd, h.weight_decay, h.beta1, omb1, h.beta2, omb2,
-                           h.eps, bc2_sqrt, rc, exact_rc, step_size);
+    adamw_plain_elem<MODE>(pp, (float)to_arith(g[e]), ea, eas, c.lr_wd, h.weight_decay, h.beta1, c.omb1, h.beta2,
+                           c.omb2, h.eps, c.bc2_sqrt, c.rc, c.exact_rc, c.step_size);
     p[e] = from_arith<T>(pp);
     m[e] = from_arith<T>(ea);
     v[e] = from_arith<T>(eas);
@@ -425,6 +439,14 @@ int launch_adamw(int32_t ntensors, void* const* params, void* const* grads, void
       [&](const AdamTable& tab, uint32_t chunks) { k_adamw<T, CHUNK, UNR><<<chunks, kMtaBlock, 0, st>>>(tab, h); });
 }
 
+// Dynamic LDS (unused by the kernel) that caps a long plain-AdamW launch at
+// 16 resident one-wave workgroups per CU: with all 32 the seven streams'
+// requests contend in HBM (c5: 74.8 % of the roofline at 32, 77.5 % at 16
+// with the bias corrections first, 80.3 % with the loads first; 13 or fewer
+// lose again).  Short launches keep the full occupancy.
+constexpr unsigned kAdamCapLds = 9728;
+inline unsigned adam_occupancy_lds(uint32_t chunks) { return chunks >= (1u << 16) ? kAdamCapLds : 0u; }
+
 // The plain configurations (k_adamw_plain): PU vectors per thread, chunks of
 // PU * kMtaBlock vectors.
 template <typename T, int PU>
@@ -446,11 +468,11 @@ int launch_adamw_plain(int32_t ntensors, void* const* params, void* const* grads
       },
       [&](const AdamTable& tab, uint32_t chunks) {
         if (h.weight_decay == 0.0)
-          k_adamw_plain<T, CHUNK, 2, PU><<<chunks, kMtaBlock, 0, st>>>(tab, h);
+          k_adamw_plain<T, CHUNK, 2, PU><<<chunks, kMtaBlock, adam_occupancy_lds(chunks), st>>>(tab, h);
         else if (h.l2)
-          k_adamw_plain<T, CHUNK, 1, PU><<<chunks, kMtaBlock, 0, st>>>(tab, h);
+          k_adamw_plain<T, CHUNK, 1, PU><<<chunks, kMtaBlock, adam_occupancy_lds(chunks), st>>>(tab, h);
         else
-          k_adamw_plain<T, CHUNK, 0, PU><<<chunks, kMtaBlock, 0, st>>>(tab, h);
+          k_adamw_plain<T, CHUNK, 0, PU><<<chunks, kMtaBlock, adam_occupancy_lds(chunks), st>>>(tab, h);
       });
 }
 
