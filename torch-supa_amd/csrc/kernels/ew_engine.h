@@ -181,6 +181,17 @@ __device__ __forceinline__ A fold_strided(A acc, int64_t first, int64_t stride, 
 template <typename Op, typename = void> struct IsHeavy : std::false_type {};
 template <typename Op> struct IsHeavy<Op, std::void_t<decltype(Op::kHeavy)>> : std::bool_constant<Op::kHeavy> {};
 template <typename Op> constexpr int contig_unroll() { return IsHeavy<Op>::value ? 2 : 1; }
+// Functors with the kCapOccupancy trait (the mse gradient: three input
+// streams and one output, little arithmetic) with three tensor inputs (a
+// per-element upstream gradient) run long launches at 16 resident
+// one-wave workgroups per CU, capped by dynamic LDS the kernel does not use:
+// with all 32 the four streams' requests contend in HBM (c4's mse gradient
+// 79.5 -> 84.4 % of the roofline).  Two- and three-stream functors lose from
+// the cap, and so did the smooth_l1 gradient (a division per element: 80.5
+// -> 74.3 %) and the BCE gradient.
+template <typename Op, typename = void> struct CapsOccupancy : std::false_type {};
+template <typename Op> struct CapsOccupancy<Op, std::void_t<decltype(Op::kCapOccupancy)>> : std::bool_constant<Op::kCapOccupancy> {};
+constexpr unsigned kStreamCapLds = 9728;
 
 // Loads of vector v of every operand into x[k][I] (k < VEC).  BCAST: some
 // operand may be a one-element broadcast (a.mode[1 + I] != 0), a uniform

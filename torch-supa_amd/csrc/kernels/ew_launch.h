@@ -187,8 +187,11 @@ int launch_static(const Op& op, const supa_amd_ew_desc& d, const int* tin, hipSt
         nfull = n / VEC / (BS * U);
         blocks = nfull + (nfull * BS * U * VEC < n ? 1 : 0);
       }
-      k_contig<BS, VEC, Op, C, CT, OT, S...><<<dim3((unsigned)blocks), dim3(BS), 0, st>>>(op, a, n,
-                                                                                          (uint32_t)nfull);
+      int dense = 0;  // tensor inputs (not one-element broadcasts)
+      for (int k = 1; k <= N; ++k) dense += a.mode[k] == 0 ? 1 : 0;
+      const unsigned lds = CapsOccupancy<Op>::value && dense >= 3 && blocks >= (1 << 17) ? kStreamCapLds : 0u;
+      k_contig<BS, VEC, Op, C, CT, OT, S...><<<dim3((unsigned)blocks), dim3(BS), lds, st>>>(op, a, n,
+                                                                                            (uint32_t)nfull);
       return launch_status();
     }
   }

@@ -690,6 +690,9 @@ template <bool PW, bool W, typename C, int RT = -1, int MEAN = -1> struct BceBwd
 // comes rounded to it).
 template <typename C> struct MseBwdOp {
   static constexpr int arity = 3;
+  // four light streams: k_contig caps residency (the smooth_l1 gradient, with
+  // its division, lost 6 points from the same cap)
+  static constexpr bool kCapOccupancy = true;
   C norm;
   int half = 0;
   __device__ __forceinline__ C operator()(const C* v) const {
