@@ -143,11 +143,11 @@ k_adamw(AdamTable tab, AdamHyper h) {
     adamw_elem<T>(p[e], g[e], m[e], v[e], h.amsgrad ? vm + e : nullptr, h, lr, lr_wd, bc1, bc2_sqrt, step_size);
 }
 
-// AdamW / Adam without amsgrad, maximize, grad_scale, found_inf or a device
-// lr (what torch.optim.AdamW(fused=True) runs by default): the same
-// arithmetic as adamw_elem with the configuration fixed at compile time
-// (MODE 0: AdamW with weight decay, 1: Adam with weight decay, 2: no weight
-// decay), so the four elements of a vector are straight-line code, and one
+// AdamW / Adam without maximize or a device lr (what torch.optim.AdamW(fused
+// =True) runs, also with amsgrad and under GradScaler): the same arithmetic
+// as adamw_elem with the configuration fixed at compile time (MODE 0: AdamW
+// with weight decay, 1: Adam with weight decay, 2: no weight decay; GS, AMS
+// below), so the four elements of a vector are straight-line code, and one
 // division fewer per element: sqrt(v) / bc2_sqrt, a float32 quotient by a
 // per-tensor constant c, is rounded from the binary64 product
 // sqrt(v) * RN64(1 / c).  That product is within 2^-52 (relative) of the
@@ -161,15 +161,28 @@ k_adamw(AdamTable tab, AdamHyper h) {
 // first) measured 60 % of the HBM roofline against 74-75 % at c5.
 constexpr int kAdamPlainUnroll = 1;
 
-template <int MODE>
-__device__ __forceinline__ void adamw_plain_elem(float& param, float grad, float& ea, float& eas, double lr_wd,
-                                                 double wd, double beta1, double omb1, double beta2, double omb2,
-                                                 double eps, float c, double rc, bool exact_rc, float step_size) {
+// GS: grad_scale and found_inf given (GradScaler's AMP step): the gradient is
+// divided by the scale (the binary64 quotient rounded once: the IEEE float32
+// quotient) and stored back, and a step with found_inf set changes nothing.
+// AMS: amsgrad, the running maximum of exp_avg_sq in max_exp_avg_sq.  As
+// adamw_elem's arithmetic for those switches.
+template <int MODE, bool GS, bool AMS>
+__device__ __forceinline__ void adamw_plain_elem(float& param, float& grad, float& ea, float& eas, float& mx,
+                                                 double lr_wd, double wd, double beta1, double omb1, double beta2,
+                                                 double omb2, double eps, float c, double rc, bool exact_rc,
+                                                 float step_size, float scale) {
+  if constexpr (GS) grad = (float)((double)grad / (double)scale);
+  float gr = grad;  // `grad` is what GS stores back; the update uses gr
   if constexpr (MODE == 0) param = (float)fma(-lr_wd, (double)param, (double)param);
-  if constexpr (MODE == 1) grad = (float)((double)grad + (double)param * wd);
-  ea = (float)fma(beta1, (double)ea, omb1 * (double)grad);
-  eas = (float)fma(beta2, (double)eas, (omb2 * (double)grad) * (double)grad);
-  const float sq = sqrtf(eas);
+  if constexpr (MODE == 1) gr = (float)((double)gr + (double)param * wd);
+  ea = (float)fma(beta1, (double)ea, omb1 * (double)gr);
+  eas = (float)fma(beta2, (double)eas, (omb2 * (double)gr) * (double)gr);
+  float vv = eas;
+  if constexpr (AMS) {
+    mx = mx > eas ? mx : eas;
+    vv = mx;
+  }
+  const float sq = sqrtf(vv);
   const float q = exact_rc ? (float)((double)sq * rc) : sq / c;
   const float denom = (float)((double)q + eps);
   param = param - (step_size * ea) / denom;
@@ -194,24 +207,25 @@ __device__ __forceinline__ AdamStepConst adam_step_const(const AdamHyper& h, flo
   return c;
 }
 
-template <int MODE, typename T, int V>
-__device__ __forceinline__ void adamw_plain_vec(Vec<T, V>& P, const Vec<T, V>& G, Vec<T, V>& M, Vec<T, V>& W,
-                                                const AdamHyper& h, const AdamStepConst& c) {
-#pragma unroll
-  for (int j = 0; j < V; ++j) {
-    float pp = (float)to_arith(P.v[j]), ea = (float)to_arith(M.v[j]), eas = (float)to_arith(W.v[j]);
-    adamw_plain_elem<MODE>(pp, (float)to_arith(G.v[j]), ea, eas, c.lr_wd, h.weight_decay, h.beta1, c.omb1, h.beta2,
-                           c.omb2, h.eps, c.bc2_sqrt, c.rc, c.exact_rc, c.step_size);
-    P.v[j] = from_arith<T>(pp);
-    M.v[j] = from_arith<T>(ea);
-    W.v[j] = from_arith<T>(eas);
-  }
+template <int MODE, bool GS, bool AMS, typename T>
+__device__ __forceinline__ void adamw_plain_one(T& p, T& g, T& m, T& v, T& x, const AdamHyper& h,
+                                                const AdamStepConst& c, float scale) {
+  float pp = (float)to_arith(p), gg = (float)to_arith(g), ea = (float)to_arith(m), eas = (float)to_arith(v);
+  float mx = AMS ? (float)to_arith(x) : 0.0f;
+  adamw_plain_elem<MODE, GS, AMS>(pp, gg, ea, eas, mx, c.lr_wd, h.weight_decay, h.beta1, c.omb1, h.beta2, c.omb2,
+                                  h.eps, c.bc2_sqrt, c.rc, c.exact_rc, c.step_size, scale);
+  p = from_arith<T>(pp);
+  if constexpr (GS) g = from_arith<T>(gg);
+  m = from_arith<T>(ea);
+  v = from_arith<T>(eas);
+  if constexpr (AMS) x = from_arith<T>(mx);
 }
 
-// A full, aligned chunk issues its four loads before it reads the step count
-// and computes the bias corrections (a chain of dependent scalar loads and
-// binary64 arithmetic), so the loads are in flight meanwhile.
-template <typename T, int64_t CHUNK, int MODE, int UNR>
+// A full, aligned chunk issues its loads before it reads the step count (and
+// found_inf / grad_scale) and computes the bias corrections (a chain of
+// dependent scalar loads and binary64 arithmetic), so the loads are in flight
+// meanwhile; a step with found_inf set then returns before any store.
+template <typename T, int64_t CHUNK, int MODE, int UNR, bool GS, bool AMS>
 __global__ void __launch_bounds__(kMtaBlock)
 k_adamw_plain(AdamTable tab, AdamHyper h) {
   constexpr int V = 16 / sizeof(T);
@@ -222,10 +236,11 @@ k_adamw_plain(AdamTable tab, AdamHyper h) {
   T* g = static_cast<T*>(tab.g[k]);
   T* m = static_cast<T*>(tab.m[k]);
   T* v = static_cast<T*>(tab.v[k]);
-  const bool vec = aligned(p, 16) && aligned(g, 16) && aligned(m, 16) && aligned(v, 16);
+  T* x = static_cast<T*>(tab.vmax[k]);
+  const bool vec = aligned(p, 16) && aligned(g, 16) && aligned(m, 16) && aligned(v, 16) && (!AMS || aligned(x, 16));
   const int64_t nv = (hi - lo) / V;  // at most UNR * kMtaBlock vectors
   if (vec && nv == (int64_t)UNR * kMtaBlock) {  // a full chunk: no guards
-    Vec<T, V> P[UNR], G[UNR], M[UNR], W[UNR];
+    Vec<T, V> P[UNR], G[UNR], M[UNR], W[UNR], X[AMS ? UNR : 1];
     __builtin_amdgcn_s_setprio(3);
 #pragma unroll
     for (int u = 0; u < UNR; ++u) {
@@ -234,42 +249,62 @@ k_adamw_plain(AdamTable tab, AdamHyper h) {
       G[u] = ld_stream(reinterpret_cast<const Vec<T, V>*>(g + e));
       M[u] = ld_stream(reinterpret_cast<const Vec<T, V>*>(m + e));
       W[u] = ld_stream(reinterpret_cast<const Vec<T, V>*>(v + e));
+      if constexpr (AMS) X[u] = ld_stream(reinterpret_cast<const Vec<T, V>*>(x + e));
     }
     __builtin_amdgcn_s_setprio(0);
+    if constexpr (GS) {
+      if (*h.found_inf == 1.0f) return;
+    }
+    const float scale = GS ? *h.grad_scale : 1.0f;
     const AdamStepConst c = adam_step_const(h, *tab.step[k]);
 #pragma unroll
     for (int u = 0; u < UNR; ++u) {
       const int64_t e = lo + (threadIdx.x + (int64_t)u * kMtaBlock) * V;
-      adamw_plain_vec<MODE, T, V>(P[u], G[u], M[u], W[u], h, c);
+#pragma unroll
+      for (int j = 0; j < V; ++j)
+        adamw_plain_one<MODE, GS, AMS, T>(P[u].v[j], G[u].v[j], M[u].v[j], W[u].v[j], X[AMS ? u : 0].v[j], h, c,
+                                          scale);
       st_stream(reinterpret_cast<Vec<T, V>*>(p + e), P[u]);
+      if constexpr (GS) st_stream(reinterpret_cast<Vec<T, V>*>(g + e), G[u]);
       st_stream(reinterpret_cast<Vec<T, V>*>(m + e), M[u]);
       st_stream(reinterpret_cast<Vec<T, V>*>(v + e), W[u]);
+      if constexpr (AMS) st_stream(reinterpret_cast<Vec<T, V>*>(x + e), X[u]);
     }
     return;
   }
+  if constexpr (GS) {
+    if (*h.found_inf == 1.0f) return;
+  }
+  const float scale = GS ? *h.grad_scale : 1.0f;
   const AdamStepConst c = adam_step_const(h, *tab.step[k]);
   int64_t start = lo;
   if (vec) {
     for (int64_t i = threadIdx.x; i < nv; i += kMtaBlock) {
       const int64_t e = lo + i * V;
       Vec<T, V> P = ld_stream(reinterpret_cast<const Vec<T, V>*>(p + e));
-      const Vec<T, V> G = ld_stream(reinterpret_cast<const Vec<T, V>*>(g + e));
+      Vec<T, V> G = ld_stream(reinterpret_cast<const Vec<T, V>*>(g + e));
       Vec<T, V> M = ld_stream(reinterpret_cast<const Vec<T, V>*>(m + e));
       Vec<T, V> W = ld_stream(reinterpret_cast<const Vec<T, V>*>(v + e));
-      adamw_plain_vec<MODE, T, V>(P, G, M, W, h, c);
+      Vec<T, V> X;
+      if constexpr (AMS) X = ld_stream(reinterpret_cast<const Vec<T, V>*>(x + e));
+#pragma unroll
+      for (int j = 0; j < V; ++j)
+        adamw_plain_one<MODE, GS, AMS, T>(P.v[j], G.v[j], M.v[j], W.v[j], X.v[j], h, c, scale);
       st_stream(reinterpret_cast<Vec<T, V>*>(p + e), P);
+      if constexpr (GS) st_stream(reinterpret_cast<Vec<T, V>*>(g + e), G);
       st_stream(reinterpret_cast<Vec<T, V>*>(m + e), M);
       st_stream(reinterpret_cast<Vec<T, V>*>(v + e), W);
+      if constexpr (AMS) st_stream(reinterpret_cast<Vec<T, V>*>(x + e), X);
     }
     start = lo + nv * V;
   }
   for (int64_t e = start + threadIdx.x; e < hi; e += kMtaBlock) {
-    float pp = (float)to_arith(p[e]), ea = (float)to_arith(m[e]), eas = (float)to_arith(v[e]);
-    adamw_plain_elem<MODE>(pp, (float)to_arith(g[e]), ea, eas, c.lr_wd, h.weight_decay, h.beta1, c.omb1, h.beta2,
-                           c.omb2, h.eps, c.bc2_sqrt, c.rc, c.exact_rc, c.step_size);
-    p[e] = from_arith<T>(pp);
-    m[e] = from_arith<T>(ea);
-    v[e] = from_arith<T>(eas);
+    if constexpr (AMS) {
+      adamw_plain_one<MODE, GS, AMS, T>(p[e], g[e], m[e], v[e], x[e], h, c, scale);
+    } else {
+      T unused = T{};
+      adamw_plain_one<MODE, GS, AMS, T>(p[e], g[e], m[e], v[e], unused, h, c, scale);
+    }
   }
 }
 
@@ -451,8 +486,8 @@ inline unsigned adam_occupancy_lds(uint32_t chunks) { return chunks >= (1u << 16
 // PU * kMtaBlock vectors.
 template <typename T, int PU>
 int launch_adamw_plain(int32_t ntensors, void* const* params, void* const* grads, void* const* exp_avgs,
-                       void* const* exp_avg_sqs, void* const* state_steps, const int64_t* numel, const AdamHyper& h,
-                       hipStream_t st) {
+                       void* const* exp_avg_sqs, void* const* max_exp_avg_sqs, void* const* state_steps,
+                       const int64_t* numel, const AdamHyper& h, hipStream_t st) {
   constexpr int64_t CHUNK = chunk_one<T>() * PU;
   return mta_for_tables<CHUNK, AdamTable>(
       ntensors, numel,
@@ -462,17 +497,27 @@ int launch_adamw_plain(int32_t ntensors, void* const* params, void* const* grads
         tab.g[slot] = grads[i];
         tab.m[slot] = exp_avgs[i];
         tab.v[slot] = exp_avg_sqs[i];
-        tab.vmax[slot] = nullptr;
+        tab.vmax[slot] = h.amsgrad ? max_exp_avg_sqs[i] : nullptr;
         tab.step[slot] = static_cast<const float*>(state_steps[i]);
         return SUPA_AMD_OK;
       },
       [&](const AdamTable& tab, uint32_t chunks) {
-        if (h.weight_decay == 0.0)
-          k_adamw_plain<T, CHUNK, 2, PU><<<chunks, kMtaBlock, adam_occupancy_lds(chunks), st>>>(tab, h);
-        else if (h.l2)
-          k_adamw_plain<T, CHUNK, 1, PU><<<chunks, kMtaBlock, adam_occupancy_lds(chunks), st>>>(tab, h);
-        else
-          k_adamw_plain<T, CHUNK, 0, PU><<<chunks, kMtaBlock, adam_occupancy_lds(chunks), st>>>(tab, h);
+        const unsigned lds = adam_occupancy_lds(chunks);
+        const int mode = h.weight_decay == 0.0 ? 2 : (h.l2 ? 1 : 0);
+        const bool gs = h.grad_scale != nullptr, ams = h.amsgrad != 0;
+        auto go = [&](auto mode_c, auto gs_c, auto ams_c) {
+          k_adamw_plain<T, CHUNK, decltype(mode_c)::value, PU, decltype(gs_c)::value, decltype(ams_c)::value>
+              <<<chunks, kMtaBlock, lds, st>>>(tab, h);
+        };
+        auto by_flags = [&](auto mode_c) {
+          if (gs && ams) go(mode_c, std::true_type{}, std::true_type{});
+          else if (gs) go(mode_c, std::true_type{}, std::false_type{});
+          else if (ams) go(mode_c, std::false_type{}, std::true_type{});
+          else go(mode_c, std::false_type{}, std::false_type{});
+        };
+        if (mode == 2) by_flags(std::integral_constant<int, 2>{});
+        else if (mode == 1) by_flags(std::integral_constant<int, 1>{});
+        else by_flags(std::integral_constant<int, 0>{});
       });
 }
 
@@ -489,7 +534,12 @@ int launch_sgd(int32_t ntensors, void* const* params, void* const* grads, void* 
         tab.b[slot] = MOM ? bufs[i] : nullptr;
         return SUPA_AMD_OK;
       },
-      [&](const SgdTable& tab, uint32_t chunks) { k_sgd<T, MOM, CHUNK><<<chunks, kMtaBlock, 0, st>>>(tab, h); });
+      [&](const SgdTable& tab, uint32_t chunks) {
+        // with a momentum buffer (three address streams, five accesses) long
+        // launches run at 20 workgroups per CU (c5's tensors: 79.5 -> 81 %)
+        const unsigned lds = MOM && chunks >= (1u << 16) ? 8192u : 0u;
+        k_sgd<T, MOM, CHUNK><<<chunks, kMtaBlock, lds, st>>>(tab, h);
+      });
 }
 
 }  // namespace sa
@@ -558,13 +608,15 @@ int fused_adam_any(int l2, int32_t ntensors, void* const* params, void* const* g
   hipStream_t st = static_cast<hipStream_t>(stream);
   const AdamHyper h{lr,        beta1,      beta2,     weight_decay,          eps, lr_ptr,
                     grad_scale, found_inf, amsgrad ? 1 : 0, maximize ? 1 : 0, l2};
-  const bool plain = !amsgrad && !maximize && !grad_scale && !found_inf && !lr_ptr;
+  // the plain kernel: no maximize, no device lr, grad_scale and found_inf
+  // together or neither (GradScaler passes both)
+  const bool plain = !maximize && !lr_ptr && (grad_scale == nullptr) == (found_inf == nullptr);
   return with_mta_storage(dtype, [&](auto* tag) -> int {
     using T = std::remove_pointer_t<decltype(tag)>;
     if constexpr (!std::is_same<T, double>::value) {
       if (plain)
-        return launch_adamw_plain<T, kAdamPlainUnroll>(ntensors, params, grads, exp_avgs, exp_avg_sqs, state_steps,
-                                                       numel, h, st);
+        return launch_adamw_plain<T, kAdamPlainUnroll>(ntensors, params, grads, exp_avgs, exp_avg_sqs,
+                                                       max_exp_avg_sqs, state_steps, numel, h, st);
     }
     return launch_adamw<T, chunk_one<T>(), 1>(ntensors, params, grads, exp_avgs, exp_avg_sqs, max_exp_avg_sqs, state_steps, numel,
                                    h, st);
