@@ -641,7 +641,7 @@ STATS_ROOFLINE_ROWS = [
     ("c3 fused cross-entropy forward (bf16 opt-in; float32 takes it by default)", "sa::k_ce_fwd<sa::bf16, true>", None, 2 * C3_NV),
     ("c3 fused cross-entropy backward (bf16 opt-in; float32 takes it by default)", "sa::k_ce_bwd<sa::bf16, true>", None, 4 * C3_NV),
     ("c5 _fused_adamw_ (two launches per step, 40 + 32 tensors; half of 28 B x 1.62 G each on average)",
-     "sa::k_adamw_plain<float, 256l, 0, 1>", None, 14 * 1619066880),
+     "sa::k_adamw_plain<float, 256l, 0, 1, false, false>", None, 14 * 1619066880),
 ]
 
 
