@@ -990,6 +990,60 @@ def test_grad_scaler_with_fused_adamw(supa):
     assert not any("amp" in k or "adamw" in k for k in used), used
 
 
+@pytest.mark.parametrize("amsgrad", [False, True])
+@pytest.mark.parametrize("scaled", [False, True])
+def test_fused_adamw_amsgrad_and_grad_scale_bit_exact(amsgrad, scaled, no_fallback):
+    """_fused_adamw_ with amsgrad and / or GradScaler's grad_scale + found_inf
+    (the compile-time kernel's AMS / GS forms) for 4 steps on full chunks, a
+    partial chunk and a partial vector: p, g (unscaled, stored back), m, v and
+    max_exp_avg_sq bit-exact against the oracle's step; then a step with
+    found_inf = 1 changes nothing."""
+    shapes = [(1024, 513), (4097,), (3, 5)]
+    g = torch.Generator().manual_seed(77)
+    params = [torch.randn(s, generator=g) * 0.5 for s in shapes]
+    grads = [torch.randn(s, generator=g) * 1e-2 for s in shapes]
+    scale = 1024.0 * 3.0 if scaled else None  # not a power of two: a real division
+    dp = [dev(p) for p in params]
+    dm = [torch.zeros_like(x) for x in dp]
+    dv = [torch.zeros_like(x) for x in dp]
+    dx = [torch.zeros_like(x) for x in dp]
+    steps = [dev(torch.zeros(())) for _ in dp]
+    hp = [p.numpy().ravel().copy() for p in params]
+    hm = [np.zeros_like(x) for x in hp]
+    hv = [np.zeros_like(x) for x in hp]
+    hx = [np.zeros_like(x) for x in hp]
+    gs = dev(torch.tensor(scale if scaled else 1.0))
+    fi = dev(torch.zeros(()))
+    for step in range(1, 5):
+        dg = [dev(gr * scale) if scaled else dev(gr) for gr in grads]
+        for t in steps:
+            t.add_(1.0)
+        torch._fused_adamw_(dp, dg, dm, dv, dx, steps, lr=1e-3, beta1=0.9, beta2=0.999, weight_decay=0.01,
+                            eps=1e-8, amsgrad=amsgrad, maximize=False, grad_scale=gs if scaled else None,
+                            found_inf=fi if scaled else None)
+        for i in range(len(shapes)):
+            hg = (grads[i].numpy().ravel() * np.float32(scale)).astype(np.float32) if scaled else \
+                grads[i].numpy().ravel().copy()
+            O.adamw_step(hp[i], hg, hm[i], hv[i], float(step), 1e-3, 0.9, 0.999, 0.01, 1e-8,
+                         grad_scale=scale, amsgrad=amsgrad, vmax=hx[i] if amsgrad else None)
+            if scaled:
+                assert np.array_equal(dg[i].cpu().numpy().ravel(), hg), (step, i)
+    for i in range(len(shapes)):
+        assert np.array_equal(dp[i].cpu().numpy().ravel(), hp[i]), i
+        assert np.array_equal(dm[i].cpu().numpy().ravel(), hm[i]), i
+        assert np.array_equal(dv[i].cpu().numpy().ravel(), hv[i]), i
+        if amsgrad:
+            assert np.array_equal(dx[i].cpu().numpy().ravel(), hx[i]), i
+    if scaled:
+        before = [x.clone() for x in dp]
+        fi.fill_(1.0)
+        torch._fused_adamw_(dp, [dev(gr) for gr in grads], dm, dv, dx, steps, lr=1e-3, beta1=0.9, beta2=0.999,
+                            weight_decay=0.01, eps=1e-8, amsgrad=amsgrad, maximize=False, grad_scale=gs,
+                            found_inf=fi)
+        for a, b in zip(dp, before):
+            assert torch.equal(a.cpu(), b.cpu())
+
+
 def test_fused_adamw_bf16_params(no_fallback):
     """bf16 parameters and state: every element is loaded to float, stepped
     with the float32 arithmetic and stored back as bf16 (upstream's opmath
