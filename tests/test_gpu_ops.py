@@ -517,6 +517,72 @@ def test_fused_cross_entropy(dtype, reduction, shape, no_fallback, fused_ce):
     assert not gd[t == -100].any()
 
 
+def confident_logits(shape, seed, dtype):
+    """N(0, 2) logits whose even rows hold one dominant logit (60 to 72, at
+    least 50 above the rest), so those rows' max term is the whole row sum
+    even in float64: a log-probability of exactly 0 and a zero gradient at
+    the dominant class.  Every probability stays above 2^-126 (the hardware
+    exp flushes smaller results to 0, where upstream's expf keeps denormals)."""
+    x = seeded(shape, seed, 2.0)
+    N, C = shape
+    g = torch.Generator().manual_seed(seed + 1)
+    cols = torch.randint(0, C, (N,), generator=g)
+    for r in range(0, N, 2):
+        x[r, cols[r]] = 60.0 + 12.0 * r / N
+    return x.to(dtype), cols
+
+
+@pytest.mark.parametrize("dtype,shape", [(torch.bfloat16, (96, 128256)), (torch.bfloat16, (64, 32000)),
+                                         (torch.float16, (64, 32000)), (torch.float32, (32, 128256)),
+                                         (torch.float32, (64, 32000))])
+def test_log_softmax_confident_rows(dtype, shape, no_fallback):
+    """The row kernels' exp terms are exp(x - max): the dominant logit's
+    log-probability is exactly 0, as in the oracle (the float64 row sum is 1)."""
+    x, cols = confident_logits(shape, 300, dtype)
+    out = torch.log_softmax(dev(x), dim=1)
+    ref = O.log_softmax(x.float().numpy())
+    rows = np.arange(0, shape[0], 2)
+    assert (ref[rows, cols.numpy()[rows]] == 0).all()
+    assert (out.cpu().float().numpy()[rows, cols.numpy()[rows]] == 0).all()
+    if dtype == torch.float32:
+        np.testing.assert_allclose(out.cpu().numpy(), ref, rtol=1e-5, atol=1e-5)
+    elif dtype == torch.bfloat16:
+        assert bf16_ulp_dist(bits(out), O.f32_to_bf16(ref)).max() <= 1
+    else:
+        np.testing.assert_allclose(out.cpu().float().numpy(), ref, rtol=1e-3, atol=1e-3)
+    sm = torch.softmax(dev(x), dim=1)
+    sref = O.softmax(x.float().numpy())
+    if dtype == torch.float32:
+        np.testing.assert_allclose(sm.cpu().numpy(), sref, rtol=1e-5, atol=1e-12)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_fused_cross_entropy_confident_rows(dtype, no_fallback, fused_ce):
+    """Fused cross-entropy on rows with a dominant logit (the target on half of
+    them): loss 0 and a zero gradient where the oracle has them, the rest of
+    the gradient to the usual bar."""
+    N, C = 64, 128256
+    x, cols = confident_logits((N, C), 310, dtype)
+    g = torch.Generator().manual_seed(312)
+    t = torch.randint(0, C, (N,), generator=g)
+    t[0::4] = cols[0::4]
+    dl = dev(x).requires_grad_()
+    loss = F.cross_entropy(dl, dev(t), reduction="none")
+    loss.backward(dev(torch.ones(N, dtype=dtype)))
+    x64 = x.double().numpy()
+    ref, lse, cnt = O.cross_entropy(x64, t.numpy(), "none", -100)
+    assert (loss.detach().cpu().double().numpy()[0::4] == 0).all() and (ref[0::4] == 0).all()
+    np.testing.assert_allclose(loss.detach().cpu().double().numpy(), ref, rtol=CE_TOL[dtype], atol=1e-6)
+    gref = O.cross_entropy_backward(np.ones(N), x64, t.numpy(), lse, cnt, "none", -100)
+    gd = dl.grad.cpu()
+    r4 = np.arange(0, N, 4)
+    assert (gd.float().numpy()[r4, t.numpy()[r4]] == 0).all()
+    if dtype == torch.float32:
+        np.testing.assert_allclose(gd.numpy(), gref, rtol=1e-5, atol=1e-6 * np.abs(gref).max())
+    else:
+        assert bf16_ulp_dist(bits(gd), O.f64_to_bf16(gref)).max() <= 1
+
+
 def test_fused_cross_entropy_matches_decomposition_and_edges(no_fallback, supa):
     """The fused path against the default log_softmax + nll_loss path on the
     same bf16 input (within the bf16 tolerance), every row ignored (mean NaN,

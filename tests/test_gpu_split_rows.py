@@ -1,0 +1,179 @@
+"""Rows split over several workgroups: the log_softmax backward from 3 parts
+of 4096 16-byte vectors on, and the log_softmax / softmax forwards past what
+one workgroup holds (up to 16 parts).  The parts of a row exchange their row
+partials through a per-stream buffer; a part that finds a peer's slot still
+empty after its spin limit computes that peer's partial itself.
+
+Covered here: parity with the oracle at every part count boundary (2 parts:
+one-row kernel, 3, 4, 8, 16, 17: streaming kernel), ragged last parts, the
+fallback (SUPA_AMD_ROW_SPLIT_SPIN=0: a part never waits) bit-identical to the
+normal path, the path switched off (SUPA_AMD_ROW_SPLIT=0), launches chunked
+over many rows, an in-place backward (never split), and rows holding +-inf
+and NaN."""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from helpers import bf16_ulp_dist
+
+pytestmark = pytest.mark.gpu
+
+LSM_BWD = torch.ops.aten._log_softmax_backward_data
+
+
+def seeded(shape, seed, scale=1.0, dtype=torch.float32):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(shape, generator=g) * scale).to(dtype)
+
+
+def bits16(t):
+    return t.cpu().view(torch.int16).numpy().view(np.uint16)
+
+
+def round16(a, dtype):
+    """float32 array rounded to dtype (round to nearest even), as 16-bit patterns."""
+    t = torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(dtype)
+    return t.view(torch.int16).numpy().view(np.uint16)
+
+
+def assert_close16(got, ref, dtype):
+    """<= 1 ulp of dtype, NaN where the reference is NaN."""
+    r = np.asarray(ref, np.float32)
+    gf = got.cpu().float().numpy()
+    assert np.array_equal(np.isnan(gf), np.isnan(r))
+    fin = ~np.isnan(r)
+    assert bf16_ulp_dist(bits16(got)[fin], round16(r, dtype)[fin]).max(initial=0) <= 1
+
+
+def bwd_inputs(rows, cols, dtype, seed):
+    x = seeded((rows, cols), seed, 2.0)
+    y = O.log_softmax(x.numpy())
+    g = seeded((rows, cols), seed + 1, 1.0)
+    yd = torch.from_numpy(y).to(dtype)
+    gd = g.to(dtype)
+    return gd, yd
+
+
+# cols -> parts of 4096 16-byte vectors: bf16 / f16 hold 8 elements a vector, float32 4
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("cols", [40000, 65600, 128256, 128264, 262144, 524288, 524296])
+def test_log_softmax_backward_split_matches_oracle(dtype, cols, no_fallback):
+    rows = 3 if cols > 200000 else 6
+    g, y = bwd_inputs(rows, cols, dtype, 31)
+    out = LSM_BWD(g.to("supa"), y.to("supa"), 1, dtype)
+    ref = O.log_softmax_backward(g.float().numpy(), y.float().numpy())
+    if dtype == torch.float32:
+        np.testing.assert_allclose(out.cpu().numpy(), ref, rtol=1e-5, atol=1e-6)
+    else:
+        assert_close16(out, ref, dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("cols", [131080, 200000, 262144, 524288])
+def test_log_softmax_forward_split_matches_oracle(dtype, cols, no_fallback):
+    x = seeded((3, cols), 41, 2.0, dtype)
+    out = torch.log_softmax(x.to("supa"), dim=1)
+    ref = O.log_softmax(x.float().numpy())
+    if dtype == torch.float32:
+        np.testing.assert_allclose(out.cpu().numpy(), ref, rtol=1e-5, atol=1e-5)
+    else:
+        assert_close16(out, ref, dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_softmax_forward_split_matches_oracle(dtype, no_fallback):
+    cols = 140000 if dtype == torch.bfloat16 else 128256
+    x = seeded((4, cols), 43, 2.0, dtype)
+    out = torch.softmax(x.to("supa"), dim=1)
+    ref = O.softmax(x.float().numpy())
+    if dtype == torch.float32:
+        np.testing.assert_allclose(out.cpu().numpy(), ref, rtol=1e-5, atol=1e-9)
+    else:
+        assert_close16(out, ref, dtype)
+
+
+def test_split_fallback_is_bit_identical(no_fallback, monkeypatch):
+    """With a spin limit of 0 a part never waits: every partial it finds
+    unpublished it computes from the peer's data, in the peer's order."""
+    g, y = bwd_inputs(64, 128256, torch.bfloat16, 51)
+    gd, yd = g.to("supa"), y.to("supa")
+    xf = seeded((64, 128256), 52, 2.0).to("supa")
+    ref_b = LSM_BWD(gd, yd, 1, torch.bfloat16)
+    ref_f = torch.log_softmax(xf, dim=1)
+    torch.supa.synchronize()
+    monkeypatch.setenv("SUPA_AMD_ROW_SPLIT_SPIN", "0")
+    for _ in range(3):
+        assert torch.equal(LSM_BWD(gd, yd, 1, torch.bfloat16).cpu(), ref_b.cpu())
+        assert torch.equal(torch.log_softmax(xf, dim=1).cpu(), ref_f.cpu())
+
+
+def test_split_switched_off_agrees(no_fallback, monkeypatch):
+    """SUPA_AMD_ROW_SPLIT=0: the one-row backward; the two reduce the row sum
+    in different orders, so they agree to 1 bf16 ulp."""
+    g, y = bwd_inputs(16, 128256, torch.bfloat16, 61)
+    gd, yd = g.to("supa"), y.to("supa")
+    on = LSM_BWD(gd, yd, 1, torch.bfloat16)
+    monkeypatch.setenv("SUPA_AMD_ROW_SPLIT", "0")
+    off = LSM_BWD(gd, yd, 1, torch.bfloat16)
+    assert bf16_ulp_dist(bits16(on), bits16(off)).max() <= 1
+
+
+def test_split_many_rows_chunked(no_fallback):
+    """16 parts a row: 4096 rows a launch, so 4100 rows take two launches that
+    reuse the buffer; each row matches the same row computed alone."""
+    rows, cols = 4100, 524288
+    gen = torch.Generator().manual_seed(71)
+    # per-row scaled copies of one random grad row keep the host side small;
+    # every row's output is the same log-softmax row
+    base_g = torch.randn(1, cols, generator=gen)
+    base_y = torch.from_numpy(O.log_softmax((torch.randn(1, cols, generator=gen) * 2.0).numpy()))
+    k = torch.arange(rows, dtype=torch.float32)[:, None]
+    gd = (base_g.to("supa") * (1.0 + k.to("supa") / rows)).to(torch.bfloat16)
+    yd = base_y.to(torch.bfloat16).to("supa").expand(rows, cols).contiguous()
+    full = LSM_BWD(gd, yd, 1, torch.bfloat16)
+    for lo, hi in ((0, 3), (4094, 4100)):
+        part = LSM_BWD(gd[lo:hi].contiguous(), yd[lo:hi].contiguous(), 1, torch.bfloat16)
+        assert torch.equal(full[lo:hi].cpu(), part.cpu()), (lo, hi)
+    ref = O.log_softmax_backward(gd[4097:4100].float().cpu().numpy(), yd[4097:4100].float().cpu().numpy())
+    assert_close16(full[4097:4100], ref, torch.bfloat16)
+    del full, gd, yd
+
+
+def test_split_backward_in_place(no_fallback):
+    """grad_input written over grad: the host sees the overlap and keeps the
+    one-row kernel (a split part may read a peer's grad)."""
+    g, y = bwd_inputs(8, 128256, torch.bfloat16, 81)
+    gd, yd = g.to("supa"), y.to("supa")
+    ref = LSM_BWD(gd, yd, 1, torch.bfloat16)
+    LSM_BWD.out(gd, yd, 1, torch.bfloat16, out=gd)
+    assert bf16_ulp_dist(bits16(gd), bits16(ref)).max() <= 1
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_split_forward_special_values(dtype, no_fallback):
+    """+inf (in a bf16 word's high element next to a nonzero low one, and in a
+    low element), -inf, an all -inf row, NaN and a dominant element (a tiny
+    log-sum) against the oracle, NaN for NaN."""
+    cols = 200000 if dtype != torch.float32 else 140000
+    x = seeded((8, cols), 91, 2.0)
+    x[0, 1001] = float("inf")
+    x[0, 1000] = 1.5
+    x[1, 70000] = float("inf")
+    x[2, ::7] = float("-inf")
+    x[3, :] = float("-inf")
+    x[4, 12345] = float("nan")
+    x[5, 99] = 60.0
+    x[6, -1] = float("inf")
+    x = x.to(dtype)
+    out = torch.log_softmax(x.to("supa"), dim=1)
+    ref = O.log_softmax(x.float().numpy())
+    if dtype == torch.float32:
+        o = out.cpu().numpy()
+        assert np.array_equal(np.isnan(o), np.isnan(ref))
+        fin = ~np.isnan(ref)
+        np.testing.assert_allclose(o[fin], ref[fin], rtol=1e-5, atol=1e-5)
+    else:
+        assert_close16(out, ref, dtype)
+    cpu = torch.log_softmax(x.float(), dim=1).numpy()
+    assert np.array_equal(np.isnan(cpu), np.isnan(out.cpu().float().numpy()))

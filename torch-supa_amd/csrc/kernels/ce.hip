@@ -108,13 +108,12 @@ k_ce_fwd(const T* __restrict__ x, const int64_t* __restrict__ target, int64_t c,
     }
     const float M = fmaxf(m, mb);
     if (M != -__builtin_inff()) {
-      const float ml = M * kCeLog2e;
       float sb = 0.0f;
 #pragma unroll
       for (int u = 0; u < kCeUnroll; ++u) {
         if (v0 + (int64_t)u * kCeBlock < nvec) {
 #pragma unroll
-          for (int k = 0; k < V; ++k) sb += __builtin_amdgcn_exp2f(fmaf(ce_elem<T>(w[u], k), kCeLog2e, -ml));
+          for (int k = 0; k < V; ++k) sb += __builtin_amdgcn_exp2f((ce_elem<T>(w[u], k) - M) * kCeLog2e);
         }
       }
       s = s * __builtin_amdgcn_exp2f((m - M) * kCeLog2e) + sb;
@@ -225,12 +224,12 @@ k_ce_bwd(const T* __restrict__ grad_out, const T* __restrict__ x, const int64_t*
     else if (reduction == SUPA_AMD_REDUCTION_MEAN) g = (float)to_arith(grad_out[0]) / count[0];
     else g = (float)to_arith(grad_out[0]);
   }
-  const float ll = kept ? lse[row] * kCeLog2e : 0.0f;
+  const float l = kept ? lse[row] : 0.0f;
   if constexpr (VECOK) {
     Vec<T, V> o;
 #pragma unroll
     for (int k = 0; k < V; ++k) {
-      const float p = __builtin_amdgcn_exp2f(fmaf((float)to_arith(w.v[k]), kCeLog2e, -ll));
+      const float p = __builtin_amdgcn_exp2f(((float)to_arith(w.v[k]) - l) * kCeLog2e);
       o.v[k] = from_arith<T>(kept ? (p - (col0 + k == t ? 1.0f : 0.0f)) * g : 0.0f);
     }
     st_stream(reinterpret_cast<Vec<T, V>*>(dst + col0), o);
@@ -238,7 +237,7 @@ k_ce_bwd(const T* __restrict__ grad_out, const T* __restrict__ x, const int64_t*
     for (int k = 0; k < V && col0 + k < c; ++k) {
       float r = 0.0f;
       if (kept) {
-        const float p = __builtin_amdgcn_exp2f(fmaf((float)to_arith(xr[col0 + k]), kCeLog2e, -ll));
+        const float p = __builtin_amdgcn_exp2f(((float)to_arith(xr[col0 + k]) - l) * kCeLog2e);
         r = (p - (col0 + k == t ? 1.0f : 0.0f)) * g;
       }
       dst[col0 + k] = from_arith<T>(r);
@@ -314,14 +313,13 @@ k_ce_prob_fwd(const T* __restrict__ x, const T* __restrict__ tgt, int64_t c, flo
         st.B = fmaf(st.T, st.m - M, st.B);
       }
       st.m = M;
-      const float ml = M * kCeLog2e;
 #pragma unroll
       for (int u = 0; u < U; ++u)
         if (v0 + (int64_t)u * kCeBlock < nvec) {
 #pragma unroll
           for (int k = 0; k < V; ++k) {
             const float xv = ce_elem<T>(wx[u], k), tv = ce_elem<T>(wt[u], k);
-            st.s += __builtin_amdgcn_exp2f(fmaf(xv, kCeLog2e, -ml));
+            st.s += __builtin_amdgcn_exp2f((xv - M) * kCeLog2e);
             st.T += tv;
             st.B = fmaf(tv, xv - M, st.B);
           }
@@ -377,7 +375,7 @@ k_ce_prob_bwd(const T* __restrict__ grad_out, const T* __restrict__ x, const T* 
   if (reduction == SUPA_AMD_REDUCTION_NONE) g = (float)to_arith(grad_out[row]);
   else if (reduction == SUPA_AMD_REDUCTION_MEAN) g = (float)to_arith(grad_out[0]) * inv_n;
   else g = (float)to_arith(grad_out[0]);
-  const float ll = lse[row] * kCeLog2e;
+  const float l = lse[row];
   const float Tr = tsum[row];
   const T* xr = x + row * c;
   const T* tr = tgt + row * c;
@@ -390,13 +388,13 @@ k_ce_prob_bwd(const T* __restrict__ grad_out, const T* __restrict__ x, const T* 
     Vec<T, V> o;
 #pragma unroll
     for (int k = 0; k < V; ++k) {
-      const float p = __builtin_amdgcn_exp2f(fmaf((float)to_arith(w.v[k]), kCeLog2e, -ll));
+      const float p = __builtin_amdgcn_exp2f(((float)to_arith(w.v[k]) - l) * kCeLog2e);
       o.v[k] = from_arith<T>(fmaf(p, Tr, -(float)to_arith(wt.v[k])) * g);
     }
     st_stream(reinterpret_cast<Vec<T, V>*>(dst + col0), o);
   } else {
     for (int k = 0; k < V && col0 + k < c; ++k) {
-      const float p = __builtin_amdgcn_exp2f(fmaf((float)to_arith(xr[col0 + k]), kCeLog2e, -ll));
+      const float p = __builtin_amdgcn_exp2f(((float)to_arith(xr[col0 + k]) - l) * kCeLog2e);
       dst[col0 + k] = from_arith<T>(fmaf(p, Tr, -(float)to_arith(tr[col0 + k])) * g);
     }
   }

@@ -8,8 +8,17 @@
 // Row statistics: per-thread partials, a 64-lane butterfly inside each
 // wavefront, then the 16 wavefront results through LDS (the forward combines
 // (max, sum) pairs in one exchange and walks rows with a persistent grid).  exp() of the row
-// statistics uses the hardware base-2 exponential on a pre-scaled argument;
-// the row results are rounded to bf16/f16 (or kept in f32) exactly once.
+// statistics is the hardware base-2 exponential of (x - max) * log2 e: the
+// row maximum's term is exactly 1, as upstream's exp(x - max) makes it (a
+// pre-scaled x * log2 e - max * log2 e leaves max's term 1 +- 2^-18 at
+// |max| near 60, and a row with one dominant logit then gets a log-probability
+// of -1.7e-6 where upstream gives 0); the row results are rounded to bf16/f16
+// (or kept in f32) exactly once.
+//
+// Split rows (the log_softmax backward from 3 parts of 4096 vectors on, the
+// forwards past what one workgroup holds, up to 16 parts): K workgroups share
+// a row, exchanging row partials through a small per-stream buffer, so the
+// same single pass runs with two rows' parts per CU (the section below).
 //
 // Fallback (any cols, any alignment): one 256-thread workgroup per row,
 // online max/sum in a first pass over memory, the output in a second pass.
@@ -18,6 +27,10 @@
 // (NF:3763), _softmax.out and _softmax_backward_data.out, upstream SoftMax.cu /
 // PersistentSoftmax.cuh in the reference's operator library.  softmax's
 // epilogue is exp(x - max) * (1 / sum) and its gradient y (g - sum(g y)).
+#include <cstdlib>
+#include <map>
+#include <mutex>
+
 #include "devmath.h"
 #include "ew_launch.h"
 
@@ -178,14 +191,14 @@ k_lsm_fwd_reg(const TI* __restrict__ in, TO* __restrict__ out, int64_t rows, int
         for (int k = 0; k < V; ++k) m = fmaxf(m, elem_f<TI>(x[j], k));
       }
     }
-    const float mbl = (m == -__builtin_inff() ? 0.0f : m) * kLog2e;  // all -inf: keep exp args finite
+    const float mb = m == -__builtin_inff() ? 0.0f : m;  // all -inf: keep exp args finite
     opaque<VPT>(x);
     float s = 0.0f;
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
       if (j < full || tid + j * kRowBlock < nvec) {
 #pragma unroll
-        for (int k = 0; k < V; ++k) s += __builtin_amdgcn_exp2f(fmaf(elem_f<TI>(x[j], k), kLog2e, -mbl));
+        for (int k = 0; k < V; ++k) s += __builtin_amdgcn_exp2f((elem_f<TI>(x[j], k) - mb) * kLog2e);
       }
     }
 #pragma unroll
@@ -203,7 +216,7 @@ k_lsm_fwd_reg(const TI* __restrict__ in, TO* __restrict__ out, int64_t rows, int
     // scaled max of the sum (an all -inf row gives 0 * inf = NaN, as upstream)
     const float logsum = LOG ? sa_logf(S) : 0.0f;
     const float inv = LOG ? 0.0f : 1.0f / S;
-    const float Mb = (M == -__builtin_inff() ? 0.0f : M) * kLog2e;
+    const float Mb = M == -__builtin_inff() ? 0.0f : M;
     opaque<VPT>(x);
     Vec<TO, V>* dst = reinterpret_cast<Vec<TO, V>*>(out + row * cols);
 #pragma unroll
@@ -213,7 +226,7 @@ k_lsm_fwd_reg(const TI* __restrict__ in, TO* __restrict__ out, int64_t rows, int
 #pragma unroll
         for (int k = 0; k < V; ++k) {
           if constexpr (LOG) f[k] = (elem_f<TI>(x[j], k) - M) - logsum;
-          else f[k] = __builtin_amdgcn_exp2f(fmaf(elem_f<TI>(x[j], k), kLog2e, -Mb)) * inv;
+          else f[k] = __builtin_amdgcn_exp2f((elem_f<TI>(x[j], k) - Mb) * kLog2e) * inv;
         }
         store_row_vec<TO, V>(dst, tid + j * kRowBlock, f);
       }
@@ -377,6 +390,395 @@ k_sm_bwd_stream(const TG* __restrict__ grad, const TG* __restrict__ outp, TO* __
     gin[base + c] = from_arith<TO>((float)to_arith(outp[base + c]) * ((float)to_arith(grad[base + c]) - s));
 }
 
+// ------------------------------------------------------- split rows
+// Rows of 3 to 16 parts of kSplitPart 16-byte vectors (a bf16 row of 24577 to
+// 524288 elements, float32 half that) are split over K workgroups, one part
+// each (1024 threads x kSplitNV vectors = 64 KiB in registers), so two parts
+// of different rows share a CU and one part's stores overlap the other's
+// loads; a whole row per workgroup leaves a CU with one row, whose stores
+// never overlap the next row's loads.  Workgroup b takes part b % K of row
+// b / K.  Each part publishes its row partial -- (max, sum of exp) forward,
+// sum of grad backward -- to slots[row * K + part] with a device-scope
+// atomic store, then waits for the row's other parts by polling their slots
+// (device-scope loads, a short s_sleep between polls), and every part folds
+// the K partials in slot order, so the K parts of a row use one bit-identical
+// total.
+//
+// A part that is still missing after spin_limit polls (a peer not yet
+// resident) is computed by the waiting workgroup itself: it loads that part
+// with the same thread layout and reduces it in the same order, so the value
+// is bit-identical to the one the peer publishes, and no wait depends on
+// another workgroup being scheduled.  The inputs must not overlap the output
+// for this (the host checks it).
+//
+// Slots are 64-bit; ~0 marks an empty slot (a published forward partial has
+// its sum's NaN canonicalised, a backward one a zero high word, so neither is
+// ~0).  done[row] counts the parts that have read the row's slots; the last
+// one resets the row's slots to ~0 and done[row] to 0, so the buffer is clean
+// after every launch.  The buffer is per (device, stream) and lives until the
+// process ends; launches on one stream are ordered, so they never share it.
+constexpr int kSplitNV = 4;
+constexpr int kSplitPart = kRowBlock * kSplitNV;
+constexpr int kSplitMinK = 3;
+constexpr int kSplitMaxK = 16;
+constexpr int64_t kSplitSlots = int64_t(1) << 16;  // row parts per launch
+constexpr uint64_t kSlotEmpty = ~uint64_t(0);
+constexpr uint32_t kSplitSpinDefault = 1u << 16;
+
+__device__ __forceinline__ void slot_store(uint64_t* p, uint64_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t slot_load(const uint64_t* p) {
+  return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Polls the row's K slots (wave 0; lane q < K reads slot q) for at most
+// spin_limit rounds; stores every published partial to part_w[q] and returns
+// the bit mask of parts still missing (same value in every thread).
+__device__ __forceinline__ uint32_t split_wait(const uint64_t* rs, int K, uint32_t spin_limit, uint64_t* part_w,
+                                               uint32_t* lds_missing) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (wave == 0) {
+    uint64_t v = kSlotEmpty;
+    if (lane < K) {
+      v = slot_load(rs + lane);
+      for (uint32_t n = 0; v == kSlotEmpty && n < spin_limit; ++n) {
+        __builtin_amdgcn_s_sleep(8);
+        v = slot_load(rs + lane);
+      }
+      part_w[lane] = v;
+    }
+    const uint64_t miss = __ballot(lane < K && v == kSlotEmpty);
+    if (lane == 0) *lds_missing = (uint32_t)miss;
+  }
+  __syncthreads();
+  return *lds_missing;
+}
+
+// After every part of the row has read the slots, the last one clears them.
+__device__ __forceinline__ void split_release(uint64_t* rs, uint32_t* done_row, int K) {
+  if (threadIdx.x == 0) {
+    const uint32_t d = __hip_atomic_fetch_add(done_row, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (d == (uint32_t)K - 1) {
+      for (int q = 0; q < K; ++q) slot_store(rs + q, kSlotEmpty);
+      __hip_atomic_store(done_row, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
+// A whole part (every part but a row's last) loads without per-vector guards
+// (a uniform branch), so its loads are not split by divergent ones.
+template <typename T>
+__device__ __forceinline__ void split_load(uint4 (&x)[kSplitNV], const uint4* src, int base, int nvec) {
+  const int tid = threadIdx.x;
+  if (base + kSplitPart <= nvec) {
+#pragma unroll
+    for (int j = 0; j < kSplitNV; ++j) x[j] = ld_stream(src + base + tid + j * kRowBlock);
+  } else {
+#pragma unroll
+    for (int j = 0; j < kSplitNV; ++j)
+      if (base + tid + j * kRowBlock < nvec) x[j] = ld_stream(src + base + tid + j * kRowBlock);
+  }
+}
+
+// The 16 wavefront values of a 1024-thread workgroup, combined by a
+// butterfly over lanes (lane l reads wavefront l % 16); every step is
+// symmetric in its operands, so every lane ends with the same value.
+__device__ __forceinline__ void block_lse16(float& M, float& S, const float* lds_m, const float* lds_s) {
+  const int lane = threadIdx.x & 63;
+  M = lds_m[lane & 15];
+  S = lds_s[lane & 15];
+#pragma unroll
+  for (int off = 8; off > 0; off >>= 1) lse_combine(M, S, __shfl_xor(M, off, 64), __shfl_xor(S, off, 64));
+}
+__device__ __forceinline__ float block_sum16(const float* lds) {
+  float S = lds[threadIdx.x & 15];
+#pragma unroll
+  for (int off = 8; off > 0; off >>= 1) S += __shfl_xor(S, off, 64);
+  return S;
+}
+
+// Per-thread (max, sum of exp(x - max)) over the thread's vectors of a part;
+// WHOLE: every vector is in the row (no per-vector guard).  bf16 maxima come
+// from the raw words: a word read as float orders like its high element (the
+// low element only adds less than one bf16 ulp), so the high elements need no
+// unpacking, and clearing the low 16 bits of the result gives the exact bf16
+// maximum.  The one case this misses, +inf in a high element next to a
+// nonzero low element (a NaN word, which max ignores), makes that element's
+// exp term +inf; a finite sum cannot reach +inf (every term is at most 1), so
+// s = +inf becomes NaN -- the row's result whenever it holds +inf.
+template <typename TI, bool WHOLE>
+__device__ __forceinline__ void thread_lse(uint4 (&x)[kSplitNV], int base, int nvec, float& m, float& s) {
+  constexpr int V = VecOf<TI>::V;
+  const int tid = threadIdx.x;
+  m = -__builtin_inff();
+  if constexpr (std::is_same<TI, bf16>::value) {
+#pragma unroll
+    for (int j = 0; j < kSplitNV; ++j)
+      if (WHOLE || base + tid + j * kRowBlock < nvec) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const uint32_t w = word_of(x[j], k);
+          m = fmaxf(m, fmaxf(__uint_as_float(w), __uint_as_float(w << 16)));
+        }
+      }
+    m = __uint_as_float(__float_as_uint(m) & 0xffff0000u);
+  } else {
+#pragma unroll
+    for (int j = 0; j < kSplitNV; ++j)
+      if (WHOLE || base + tid + j * kRowBlock < nvec) {
+#pragma unroll
+        for (int k = 0; k < V; ++k) m = fmaxf(m, elem_f<TI>(x[j], k));
+      }
+  }
+  const float mb = m == -__builtin_inff() ? 0.0f : m;
+  opaque<kSplitNV>(x);
+  s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < kSplitNV; ++j)
+    if (WHOLE || base + tid + j * kRowBlock < nvec) {
+#pragma unroll
+      for (int k = 0; k < V; ++k) s += __builtin_amdgcn_exp2f((elem_f<TI>(x[j], k) - mb) * kLog2e);
+    }
+  if (std::is_same<TI, bf16>::value && s == __builtin_inff()) s = __builtin_nanf("");
+}
+
+// (max, sum of exp(x - max)) of one part, the same in every thread; the
+// sum's NaN is canonical.
+template <typename TI>
+__device__ __forceinline__ uint64_t part_lse(uint4 (&x)[kSplitNV], int base, int nvec, float* lds_m, float* lds_s) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  float m, s;
+  if (base + kSplitPart <= nvec) thread_lse<TI, true>(x, base, nvec, m, s);
+  else thread_lse<TI, false>(x, base, nvec, m, s);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) lse_combine(m, s, __shfl_xor(m, off, 64), __shfl_xor(s, off, 64));
+  __syncthreads();
+  if (lane == 0) {
+    lds_m[wave] = m;
+    lds_s[wave] = s;
+  }
+  __syncthreads();
+  float M, S;
+  block_lse16(M, S, lds_m, lds_s);
+  const uint32_t sb = S != S ? 0x7fc00000u : __float_as_uint(S);
+  return ((uint64_t)sb << 32) | __float_as_uint(M);
+}
+
+template <typename TI, typename TO, bool LOG, bool WHOLE>
+__device__ __forceinline__ void fwd_split_out(const uint4 (&x)[kSplitNV], Vec<TO, VecOf<TI>::V>* dst, int base, int nvec,
+                                              float M, float logsum, float Mb, float inv) {
+  constexpr int V = VecOf<TI>::V;
+#pragma unroll
+  for (int j = 0; j < kSplitNV; ++j) {
+    const int v = base + (int)threadIdx.x + j * kRowBlock;
+    if (WHOLE || v < nvec) {
+      float f[V];
+#pragma unroll
+      for (int k = 0; k < V; ++k) {
+        if constexpr (LOG) f[k] = (elem_f<TI>(x[j], k) - M) - logsum;
+        else f[k] = __builtin_amdgcn_exp2f((elem_f<TI>(x[j], k) - Mb) * kLog2e) * inv;
+      }
+      store_row_vec<TO, V>(dst, v, f);
+    }
+  }
+}
+
+template <typename TI, typename TO, bool LOG>
+__global__ void __launch_bounds__(kRowBlock, 8)
+k_lsm_fwd_split(const TI* __restrict__ in, TO* __restrict__ out, int64_t cols, int K, uint64_t* __restrict__ slots,
+                uint32_t* __restrict__ done, uint32_t spin_limit) {
+  constexpr int V = VecOf<TI>::V;
+  constexpr int NW = kRowBlock / 64;
+  __shared__ float lds_m[NW];
+  __shared__ float lds_s[NW];
+  __shared__ uint64_t part_w[kSplitMaxK];
+  __shared__ uint32_t lds_missing;
+  const int row = (int)(blockIdx.x / (unsigned)K);
+  const int part = (int)(blockIdx.x - (unsigned)row * (unsigned)K);
+  const int nvec = (int)(cols / V);
+  const uint4* src = reinterpret_cast<const uint4*>(in + (int64_t)row * cols);
+  uint4 x[kSplitNV];
+  split_load<TI>(x, src, part * kSplitPart, nvec);
+  const uint64_t mine = part_lse<TI>(x, part * kSplitPart, nvec, lds_m, lds_s);
+  opaque<kSplitNV>(x);
+  uint64_t* rs = slots + (int64_t)row * K;
+  if (threadIdx.x == 0) slot_store(rs + part, mine);
+  uint32_t miss = split_wait(rs, K, spin_limit, part_w, &lds_missing);
+  split_release(rs, done + row, K);
+  if (miss) {  // uniform; the own part is loaded again afterwards, so the fallback reuses its registers
+    do {
+      const int q = __builtin_ctz(miss);
+      miss &= miss - 1;
+      split_load<TI>(x, src, q * kSplitPart, nvec);
+      const uint64_t w = part_lse<TI>(x, q * kSplitPart, nvec, lds_m, lds_s);
+      if (threadIdx.x == 0) part_w[q] = w;
+    } while (miss);
+    split_load<TI>(x, src, part * kSplitPart, nvec);
+  }
+  __syncthreads();
+  float M = __uint_as_float((uint32_t)part_w[0]), S = __uint_as_float((uint32_t)(part_w[0] >> 32));
+  for (int q = 1; q < K; ++q)
+    lse_combine(M, S, __uint_as_float((uint32_t)part_w[q]), __uint_as_float((uint32_t)(part_w[q] >> 32)));
+  const float logsum = LOG ? sa_logf(S) : 0.0f;
+  const float inv = LOG ? 0.0f : 1.0f / S;
+  const float Mb = M == -__builtin_inff() ? 0.0f : M;
+  opaque<kSplitNV>(x);
+  Vec<TO, V>* dst = reinterpret_cast<Vec<TO, V>*>(out + (int64_t)row * cols);
+  const int base = part * kSplitPart;
+  if (base + kSplitPart <= nvec) fwd_split_out<TI, TO, LOG, true>(x, dst, base, nvec, M, logsum, Mb, inv);
+  else fwd_split_out<TI, TO, LOG, false>(x, dst, base, nvec, M, logsum, Mb, inv);
+}
+
+template <typename TG, bool WHOLE>
+__device__ __forceinline__ float thread_sum(const uint4 (&g)[kSplitNV], int base, int nvec) {
+  constexpr int V = VecOf<TG>::V;
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < kSplitNV; ++j)
+    if (WHOLE || base + (int)threadIdx.x + j * kRowBlock < nvec) {
+#pragma unroll
+      for (int k = 0; k < V; ++k) s += elem_f<TG>(g[j], k);
+    }
+  return s;
+}
+
+// Sum of one part of grad, the same in every thread.
+template <typename TG>
+__device__ __forceinline__ uint64_t part_sum(uint4 (&g)[kSplitNV], int base, int nvec, float* lds) {
+  float s = base + kSplitPart <= nvec ? thread_sum<TG, true>(g, base, nvec) : thread_sum<TG, false>(g, base, nvec);
+  s = wave_sum(s);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) lds[threadIdx.x >> 6] = s;
+  __syncthreads();
+  return (uint64_t)__float_as_uint(block_sum16(lds));
+}
+
+template <typename TG, typename TO, bool WHOLE>
+__device__ __forceinline__ void bwd_split_out(const uint4 (&gv)[kSplitNV], const uint4 (&yv)[kSplitNV],
+                                              Vec<TO, VecOf<TG>::V>* dst, int base, int nvec, float S) {
+  constexpr int V = VecOf<TG>::V;
+#pragma unroll
+  for (int j = 0; j < kSplitNV; ++j) {
+    const int v = base + (int)threadIdx.x + j * kRowBlock;
+    if (WHOLE || v < nvec) {
+      float f[V];
+#pragma unroll
+      for (int k = 0; k < V; ++k)
+        f[k] = fmaf(-__builtin_amdgcn_exp2f(elem_f<TG>(yv[j], k) * kLog2e), S, elem_f<TG>(gv[j], k));
+      store_row_vec<TO, V>(dst, v, f);
+    }
+  }
+}
+
+template <typename TG, typename TO>
+__global__ void __launch_bounds__(kRowBlock, 8)
+k_lsm_bwd_split(const TG* __restrict__ grad, const TG* __restrict__ outp, TO* __restrict__ gin, int64_t cols, int K,
+                uint64_t* __restrict__ slots, uint32_t* __restrict__ done, uint32_t spin_limit) {
+  constexpr int V = VecOf<TG>::V;
+  __shared__ float lds[kRowBlock / 64];
+  __shared__ uint64_t part_w[kSplitMaxK];
+  __shared__ uint32_t lds_missing;
+  const int row = (int)(blockIdx.x / (unsigned)K);
+  const int part = (int)(blockIdx.x - (unsigned)row * (unsigned)K);
+  const int nvec = (int)(cols / V);
+  const int base = part * kSplitPart;
+  const uint4* g = reinterpret_cast<const uint4*>(grad + (int64_t)row * cols);
+  const uint4* y = reinterpret_cast<const uint4*>(outp + (int64_t)row * cols);
+  uint4 gv[kSplitNV], yv[kSplitNV];
+  split_load<TG>(gv, g, base, nvec);
+  split_load<TG>(yv, y, base, nvec);
+  const uint64_t mine = part_sum<TG>(gv, base, nvec, lds);
+  opaque<kSplitNV>(gv);
+  uint64_t* rs = slots + (int64_t)row * K;
+  if (threadIdx.x == 0) slot_store(rs + part, mine);
+  uint32_t miss = split_wait(rs, K, spin_limit, part_w, &lds_missing);
+  split_release(rs, done + row, K);
+  if (miss) {  // uniform; the own part is loaded again afterwards, so the fallback reuses its registers
+    do {
+      const int q = __builtin_ctz(miss);
+      miss &= miss - 1;
+      split_load<TG>(gv, g, q * kSplitPart, nvec);
+      const uint64_t w = part_sum<TG>(gv, q * kSplitPart, nvec, lds);
+      if (threadIdx.x == 0) part_w[q] = w;
+    } while (miss);
+    split_load<TG>(gv, g, base, nvec);
+  }
+  __syncthreads();
+  float S = __uint_as_float((uint32_t)part_w[0]);
+  for (int q = 1; q < K; ++q) S += __uint_as_float((uint32_t)part_w[q]);
+  opaque<kSplitNV>(gv);
+  opaque<kSplitNV>(yv);
+  Vec<TO, V>* dst = reinterpret_cast<Vec<TO, V>*>(gin + (int64_t)row * cols);
+  if (base + kSplitPart <= nvec) bwd_split_out<TG, TO, true>(gv, yv, dst, base, nvec, S);
+  else bwd_split_out<TG, TO, false>(gv, yv, dst, base, nvec, S);
+}
+
+__global__ void __launch_bounds__(kBlock) k_split_init(uint64_t* slots, uint32_t* done, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (i < n) {
+    slots[i] = kSlotEmpty;
+    done[i] = 0u;
+  }
+}
+
+struct SplitScratch {
+  uint64_t* slots = nullptr;
+  uint32_t* done = nullptr;
+};
+
+// The split kernels' buffer for (current device, st), made on first use;
+// false when the split path is switched off (SUPA_AMD_ROW_SPLIT=0), the
+// stream is capturing a graph, or the buffer cannot be made -- the caller
+// then takes the one-row kernels.
+inline bool split_scratch(hipStream_t st, SplitScratch& out, uint32_t& spin_limit) {
+  const char* e = std::getenv("SUPA_AMD_ROW_SPLIT");
+  if (e && e[0] == '0') return false;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return false;
+  const char* sp = std::getenv("SUPA_AMD_ROW_SPLIT_SPIN");
+  spin_limit = sp ? (uint32_t)std::strtoul(sp, nullptr, 10) : kSplitSpinDefault;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return false;
+  static std::mutex mu;
+  static std::map<std::pair<int, hipStream_t>, SplitScratch> bufs;
+  std::lock_guard<std::mutex> lock(mu);
+  const auto key = std::make_pair(dev, st);
+  auto it = bufs.find(key);
+  if (it != bufs.end()) {
+    out = it->second;
+    return true;
+  }
+  void* p = nullptr;
+  if (hipMalloc(&p, (size_t)kSplitSlots * (sizeof(uint64_t) + sizeof(uint32_t))) != hipSuccess) {
+    (void)hipGetLastError();
+    return false;
+  }
+  SplitScratch b;
+  b.slots = static_cast<uint64_t*>(p);
+  b.done = reinterpret_cast<uint32_t*>(b.slots + kSplitSlots);
+  k_split_init<<<(unsigned)(kSplitSlots / kBlock), kBlock, 0, st>>>(b.slots, b.done, kSplitSlots);
+  if (hipGetLastError() != hipSuccess) {
+    (void)hipFree(p);
+    return false;
+  }
+  bufs.emplace(key, b);
+  out = b;
+  return true;
+}
+
+// Parts per row for the split kernels, 0 when the row takes another kernel.
+inline int split_parts(int64_t nvec, const void* a, const void* b, int64_t a_bytes, const void* o, int64_t o_bytes) {
+  const int64_t K = (nvec + kSplitPart - 1) / kSplitPart;
+  if (K < kSplitMinK || K > kSplitMaxK) return 0;
+  auto overlap = [](const void* x, int64_t xb, const void* y, int64_t yb) {
+    const uintptr_t x0 = reinterpret_cast<uintptr_t>(x), y0 = reinterpret_cast<uintptr_t>(y);
+    return x0 < y0 + (uintptr_t)yb && y0 < x0 + (uintptr_t)xb;
+  };
+  if (overlap(a, a_bytes, o, o_bytes) || (b && overlap(b, a_bytes, o, o_bytes))) return 0;
+  return (int)K;
+}
+
 template <typename F>
 int with_float_storage(int dtype, F&& f) {
   switch (dtype) {
@@ -399,7 +801,28 @@ int softmax_forward(const void* in, int32_t in_dtype, void* out, int32_t out_dty
       using TO = std::remove_pointer_t<decltype(to)>;
       if (in_dtype != out_dtype && out_dtype != SUPA_AMD_F32) return SUPA_AMD_EDTYPE;
       constexpr int V = VecOf<TI>::V;
-      const bool reg_ok = (cols % V) == 0 && aligned(in, 16) && aligned(out, V * sizeof(TO)) && (cols / V) <= 16 * kRowBlock;
+      const bool vec_ok = (cols % V) == 0 && aligned(in, 16) && aligned(out, V * sizeof(TO));
+      // The forward splits only rows the one-row kernel cannot hold: on a c3
+      // row (bf16 [8192, 128256]) the split forward measured 70-72.5 % against
+      // the one-row kernel's 71.7-72.4 % (its exp pass, between the part's
+      // loads and its exchange, is what each part waits on).
+      const int K = vec_ok && cols / V > 16 * kRowBlock
+                        ? split_parts(cols / V, in, nullptr, rows * cols * (int64_t)sizeof(TI), out,
+                                      rows * cols * (int64_t)sizeof(TO))
+                        : 0;
+      SplitScratch sb;
+      uint32_t spin = 0;
+      if (K > 0 && split_scratch(st, sb, spin)) {
+        const int64_t chunk = kSplitSlots / K;
+        for (int64_t r0 = 0; r0 < rows; r0 += chunk) {
+          const int64_t nr = std::min(chunk, rows - r0);
+          k_lsm_fwd_split<TI, TO, LOG><<<(unsigned)(nr * K), kRowBlock, 0, st>>>(
+              static_cast<const TI*>(in) + r0 * cols, static_cast<TO*>(out) + r0 * cols, cols, K, sb.slots, sb.done,
+              spin);
+        }
+        return launch_status();
+      }
+      const bool reg_ok = vec_ok && (cols / V) <= 16 * kRowBlock;
       if (reg_ok) {
         const int64_t nvec = cols / V;
         const int vpt = (int)((nvec + kRowBlock - 1) / kRowBlock);
@@ -447,11 +870,26 @@ int supa_amd_log_softmax_backward(const void* grad, const void* output, int32_t 
       using TO = std::remove_pointer_t<decltype(to)>;
       if (gy_dtype != gin_dtype && gin_dtype != SUPA_AMD_F32) return SUPA_AMD_EDTYPE;
       constexpr int V = VecOf<TG>::V;
-      const bool reg_ok = (cols % V) == 0 && aligned(grad, 16) && aligned(output, 16) && aligned(grad_in, V * sizeof(TO)) &&
-                          (cols / V) <= 16 * kRowBlock;
+      const bool vec_ok = (cols % V) == 0 && aligned(grad, 16) && aligned(output, 16) && aligned(grad_in, V * sizeof(TO));
       const TG* pg = static_cast<const TG*>(grad);
       const TG* py = static_cast<const TG*>(output);
       TO* po = static_cast<TO*>(grad_in);
+      const int K = vec_ok ? split_parts(cols / V, grad, output, rows * cols * (int64_t)sizeof(TG), grad_in,
+                                         rows * cols * (int64_t)sizeof(TO))
+                           : 0;
+      SplitScratch sb;
+      uint32_t spin = 0;
+      if (K > 0 && split_scratch(st, sb, spin)) {
+        const int64_t chunk = kSplitSlots / K;
+        for (int64_t r0 = 0; r0 < rows; r0 += chunk) {
+          const int64_t nr = std::min(chunk, rows - r0);
+          k_lsm_bwd_split<TG, TO><<<(unsigned)(nr * K), kRowBlock, 0, st>>>(pg + r0 * cols, py + r0 * cols,
+                                                                           po + r0 * cols, cols, K, sb.slots,
+                                                                           sb.done, spin);
+        }
+        return launch_status();
+      }
+      const bool reg_ok = vec_ok && (cols / V) <= 16 * kRowBlock;
       if (reg_ok) {
         const int64_t nvec = cols / V;
         const int vpt = (int)((nvec + kRowBlock - 1) / kRowBlock);
