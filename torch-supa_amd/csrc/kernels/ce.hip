@@ -226,11 +226,28 @@ k_ce_bwd(const T* __restrict__ grad_out, const T* __restrict__ x, const int64_t*
   }
   const float l = kept ? lse[row] : 0.0f;
   if constexpr (VECOK) {
+    // p g everywhere, (p - 1) g at the target: the one thread of the row that
+    // holds the target patches its element in a branch, so the other threads
+    // spend no compare or select per element (the same values as
+    // (p - [j == t]) g; ignored rows, uniform in the workgroup, store zeros)
     Vec<T, V> o;
+    if (kept) {
+      float p[V];
 #pragma unroll
-    for (int k = 0; k < V; ++k) {
-      const float p = __builtin_amdgcn_exp2f(((float)to_arith(w.v[k]) - l) * kCeLog2e);
-      o.v[k] = from_arith<T>(kept ? (p - (col0 + k == t ? 1.0f : 0.0f)) * g : 0.0f);
+      for (int k = 0; k < V; ++k) p[k] = __builtin_amdgcn_exp2f(((float)to_arith(w.v[k]) - l) * kCeLog2e);
+      float r[V];
+#pragma unroll
+      for (int k = 0; k < V; ++k) r[k] = p[k] * g;
+      if ((uint64_t)(t - col0) < (uint64_t)V) {
+#pragma unroll
+        for (int k = 0; k < V; ++k)
+          if (col0 + k == t) r[k] = (p[k] - 1.0f) * g;
+      }
+#pragma unroll
+      for (int k = 0; k < V; ++k) o.v[k] = from_arith<T>(r[k]);
+    } else {
+#pragma unroll
+      for (int k = 0; k < V; ++k) o.v[k] = from_arith<T>(0.0f);
     }
     st_stream(reinterpret_cast<Vec<T, V>*>(dst + col0), o);
   } else {
