@@ -8,8 +8,8 @@ Covered here: parity with the oracle at every part count boundary (2 parts:
 one-row kernel, 3, 4, 8, 16, 17: streaming kernel), ragged last parts, the
 fallback (SUPA_AMD_ROW_SPLIT_SPIN=0: a part never waits) bit-identical to the
 normal path, the path switched off (SUPA_AMD_ROW_SPLIT=0), launches chunked
-over many rows, an in-place backward (never split), and rows holding +-inf
-and NaN."""
+over many rows, an in-place backward (never split), rows holding +-inf and
+NaN, and a graph capture (never split)."""
 import numpy as np
 import pytest
 import torch
@@ -177,3 +177,40 @@ def test_split_forward_special_values(dtype, no_fallback):
         assert_close16(out, ref, dtype)
     cpu = torch.log_softmax(x.float(), dim=1).numpy()
     assert np.array_equal(np.isnan(cpu), np.isnan(out.cpu().float().numpy()))
+
+
+def test_backward_under_graph_capture():
+    """A stream that is capturing a graph never takes the split kernels (their
+    slot buffer is made with hipMalloc on a stream's first use, and the
+    per-launch state must not be replayed blindly): the captured launch is the
+    one-row kernel's, and every replay equals the eager result to 1 bf16 ulp.
+    Called through the C ABI on torch's own HIP stream."""
+    import ctypes
+
+    import capi as A
+
+    L = A.lib()
+    rows, cols = 8, 128256
+    g, y = bwd_inputs(rows, cols, torch.bfloat16, 101)
+    dg, dy = g.to("cuda"), y.to("cuda")
+    eager = torch.empty_like(dg)
+    code = A.dtype_code(torch.bfloat16)
+    assert L.supa_amd_log_softmax_backward(dg.data_ptr(), dy.data_ptr(), code, eager.data_ptr(), code, rows, cols,
+                                           None) == 0
+    torch.cuda.synchronize()
+    out = torch.empty_like(dg)
+    s = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        graph.capture_begin()
+        rc = L.supa_amd_log_softmax_backward(dg.data_ptr(), dy.data_ptr(), code, out.data_ptr(), code, rows, cols,
+                                             ctypes.c_void_p(s.cuda_stream))
+        graph.capture_end()
+    assert rc == 0
+    for _ in range(3):
+        out.fill_(0)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert bf16_ulp_dist(bits16(out), bits16(eager)).max() <= 1
+        assert not torch.equal(out, torch.zeros_like(out))
