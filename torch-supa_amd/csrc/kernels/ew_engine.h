@@ -600,7 +600,9 @@ k_transpose(Op op, const S* __restrict__ in, OT* __restrict__ out, TransposeGeom
 // output vectors along dim 0 from LDS columns.  On c2's bf16 .contiguous()
 // this shape runs at 78-79 % of the HBM roofline (a flat copy of the same
 // bytes: 83-84 %); with 512 threads 76 %, with 32 / 128 / 256 tile rows
-// (64 / 256 / 512-byte output runs) 60 / 75 / 72 %, with 64 x 64 tiles 69-71 %.
+// (64 / 256 / 512-byte output runs) 60 / 75 / 72 %, with 64 x 64 tiles 69-71 %,
+// and as a persistent grid (512-2048 workgroups) that issues the next tile's
+// loads before storing the current tile 64-68 %.
 // Needs d0 % VO == 0, dk % VI == 0, every stride a multiple of the vector
 // and 16-byte aligned bases (checked on the host).
 constexpr int kTileVecBlock = 1024;
