@@ -9,7 +9,8 @@ one-row kernel, 3, 4, 8, 16, 17: streaming kernel), ragged last parts, the
 fallback (SUPA_AMD_ROW_SPLIT_SPIN=0: a part never waits) bit-identical to the
 normal path, the path switched off (SUPA_AMD_ROW_SPLIT=0), launches chunked
 over many rows, an in-place backward (never split), rows holding +-inf and
-NaN, and a graph capture (never split)."""
+NaN, a graph capture (never split) and two streams at once (a slot buffer
+each)."""
 import numpy as np
 import pytest
 import torch
@@ -214,3 +215,30 @@ def test_backward_under_graph_capture():
         torch.cuda.synchronize()
         assert bf16_ulp_dist(bits16(out), bits16(eager)).max() <= 1
         assert not torch.equal(out, torch.zeros_like(out))
+
+
+def test_split_on_two_streams(no_fallback):
+    """Split launches on two streams at once keep their own slot buffers: each
+    stream's results equal the same call's on the default stream bit for bit
+    (a shared buffer would mix the two launches' row partials)."""
+    data = [bwd_inputs(64, 128256, torch.bfloat16, seed) for seed in (111, 113)]
+    data = [(g.to("supa"), y.to("supa")) for g, y in data]
+    ref = [LSM_BWD(g, y, 1, torch.bfloat16).cpu() for g, y in data]
+    s1, s2 = torch.supa.Stream(), torch.supa.Stream()
+    while s2.stream_id == s1.stream_id:
+        s2 = torch.supa.Stream()
+    cur = torch.supa.current_stream()
+    s1.wait_stream(cur)
+    s2.wait_stream(cur)
+    outs = []
+    for _ in range(4):
+        with torch.supa.stream(s1):
+            o1 = LSM_BWD(data[0][0], data[0][1], 1, torch.bfloat16)
+        with torch.supa.stream(s2):
+            o2 = LSM_BWD(data[1][0], data[1][1], 1, torch.bfloat16)
+        outs.append((o1, o2))
+    cur.wait_stream(s1)
+    cur.wait_stream(s2)
+    for o1, o2 in outs:
+        assert torch.equal(o1.cpu(), ref[0])
+        assert torch.equal(o2.cpu(), ref[1])
