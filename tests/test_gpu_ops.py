@@ -1110,6 +1110,44 @@ def test_fused_adamw_amsgrad_and_grad_scale_bit_exact(amsgrad, scaled, no_fallba
             assert torch.equal(a.cpu(), b.cpu())
 
 
+@pytest.mark.parametrize("adam", [False, True])
+@pytest.mark.parametrize("weight_decay", [0.0, 0.01])
+@pytest.mark.parametrize("tensor_lr", [False, True])
+def test_fused_adam_maximize_and_device_lr_bit_exact(adam, weight_decay, tensor_lr, no_fallback):
+    """_fused_adamw_ / _fused_adam_ with maximize=True, the lr a float or a
+    device tensor (the tensor_lr overload, read on the device), for 4 steps
+    on full chunks, a partial chunk and a partial vector: p, m and v
+    bit-exact against the oracle's step.  Adam with weight decay under
+    maximize runs the general kernel, every other case the plain one."""
+    shapes = [(1024, 513), (4097,), (3, 5)]
+    g = torch.Generator().manual_seed(91)
+    params = [torch.randn(s, generator=g) * 0.5 for s in shapes]
+    grads = [torch.randn(s, generator=g) * 1e-2 for s in shapes]
+    lr = float(np.float32(7e-4))  # a float32 value, as the device tensor holds it
+    dp = [dev(p) for p in params]
+    dm = [torch.zeros_like(x) for x in dp]
+    dv = [torch.zeros_like(x) for x in dp]
+    steps = [dev(torch.zeros(())) for _ in dp]
+    hp = [p.numpy().ravel().copy() for p in params]
+    hm = [np.zeros_like(x) for x in hp]
+    hv = [np.zeros_like(x) for x in hp]
+    fn = torch._fused_adam_ if adam else torch._fused_adamw_
+    lr_arg = dev(torch.tensor(lr)) if tensor_lr else lr
+    for step in range(1, 5):
+        dg = [dev(gr) for gr in grads]
+        for t in steps:
+            t.add_(1.0)
+        fn(dp, dg, dm, dv, [], steps, lr=lr_arg, beta1=0.9, beta2=0.999, weight_decay=weight_decay, eps=1e-8,
+           amsgrad=False, maximize=True)
+        for i in range(len(shapes)):
+            O.adamw_step(hp[i], grads[i].numpy().ravel().copy(), hm[i], hv[i], float(step), lr, 0.9, 0.999,
+                         weight_decay, 1e-8, maximize=True, l2=adam)
+    for i in range(len(shapes)):
+        assert np.array_equal(dp[i].cpu().numpy().ravel(), hp[i]), i
+        assert np.array_equal(dm[i].cpu().numpy().ravel(), hm[i]), i
+        assert np.array_equal(dv[i].cpu().numpy().ravel(), hv[i]), i
+
+
 def test_fused_adamw_bf16_params(no_fallback):
     """bf16 parameters and state: every element is loaded to float, stepped
     with the float32 arithmetic and stored back as bf16 (upstream's opmath

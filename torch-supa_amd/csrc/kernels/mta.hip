@@ -143,8 +143,9 @@ k_adamw(AdamTable tab, AdamHyper h) {
     adamw_elem<T>(p[e], g[e], m[e], v[e], h.amsgrad ? vm + e : nullptr, h, lr, lr_wd, bc1, bc2_sqrt, step_size);
 }
 
-// AdamW / Adam without maximize or a device lr (what torch.optim.AdamW(fused
-// =True) runs, also with amsgrad and under GradScaler): the same arithmetic
+// AdamW / Adam (what torch.optim.AdamW(fused=True) runs, also with amsgrad,
+// maximize, a device lr and under GradScaler; Adam's weight decay under
+// maximize takes k_adamw): the same arithmetic
 // as adamw_elem with the configuration fixed at compile time (MODE 0: AdamW
 // with weight decay, 1: Adam with weight decay, 2: no weight decay; GS, AMS
 // below), so the four elements of a vector are straight-line code, and one
@@ -194,13 +195,18 @@ struct AdamStepConst {
   double lr_wd, omb1, omb2, rc;
   bool exact_rc;
 };
+// maximize negates the gradient the update uses; outside Adam's weight decay
+// (which adds to that gradient first) the gradient enters the step only
+// through (1 - beta1) g and the sign-free g g, and (-(1 - beta1)) g rounds
+// to exactly -((1 - beta1) g), so maximize is the sign of omb1.
 __device__ __forceinline__ AdamStepConst adam_step_const(const AdamHyper& h, float step) {
   AdamStepConst c;
+  const double lr = h.lr_ptr ? (double)(*h.lr_ptr) : h.lr;
   const float bc1 = (float)(1.0 - pow_steps(h.beta1, step));
   c.bc2_sqrt = (float)sqrt(1.0 - pow_steps(h.beta2, step));
-  c.step_size = (float)(h.lr / (double)bc1);
-  c.lr_wd = h.lr * h.weight_decay;
-  c.omb1 = 1.0 - h.beta1;
+  c.step_size = (float)(lr / (double)bc1);
+  c.lr_wd = lr * h.weight_decay;
+  c.omb1 = h.maximize ? -(1.0 - h.beta1) : 1.0 - h.beta1;
   c.omb2 = 1.0 - h.beta2;
   c.exact_rc = c.bc2_sqrt >= 0x1p-60f && c.bc2_sqrt <= 1.0f;
   c.rc = 1.0 / (double)c.bc2_sqrt;
@@ -608,9 +614,10 @@ int fused_adam_any(int l2, int32_t ntensors, void* const* params, void* const* g
   hipStream_t st = static_cast<hipStream_t>(stream);
   const AdamHyper h{lr,        beta1,      beta2,     weight_decay,          eps, lr_ptr,
                     grad_scale, found_inf, amsgrad ? 1 : 0, maximize ? 1 : 0, l2};
-  // the plain kernel: no maximize, no device lr, grad_scale and found_inf
-  // together or neither (GradScaler passes both)
-  const bool plain = !maximize && !lr_ptr && (grad_scale == nullptr) == (found_inf == nullptr);
+  // the plain kernel: grad_scale and found_inf together or neither
+  // (GradScaler passes both), and not maximize with Adam's weight decay
+  // (the plain kernel folds maximize into the sign of 1 - beta1)
+  const bool plain = !(maximize && l2 && weight_decay != 0.0) && (grad_scale == nullptr) == (found_inf == nullptr);
   return with_mta_storage(dtype, [&](auto* tag) -> int {
     using T = std::remove_pointer_t<decltype(tag)>;
     if constexpr (!std::is_same<T, double>::value) {
