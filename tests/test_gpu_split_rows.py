@@ -9,8 +9,9 @@ one-row kernel, 3, 4, 8, 16, 17: streaming kernel), ragged last parts, the
 fallback (SUPA_AMD_ROW_SPLIT_SPIN=0: a part never waits) bit-identical to the
 normal path, the path switched off (SUPA_AMD_ROW_SPLIT=0), launches chunked
 over many rows, an in-place backward (never split), rows holding +-inf and
-NaN, a graph capture (never split) and two streams at once (a slot buffer
-each)."""
+NaN, a graph capture (never split), two streams at once (a slot buffer
+each) and more streams than a device has slot buffers (the rest run the
+one-row kernel)."""
 import numpy as np
 import pytest
 import torch
@@ -121,8 +122,8 @@ def test_split_switched_off_agrees(no_fallback, monkeypatch):
 
 
 def test_split_many_rows_chunked(no_fallback):
-    """16 parts a row: 4096 rows a launch, so 4100 rows take two launches that
-    reuse the buffer; each row matches the same row computed alone."""
+    """16 parts a row: 2048 rows a launch, so 4100 rows take three launches
+    that reuse the buffer; each row matches the same row computed alone."""
     rows, cols = 4100, 524288
     gen = torch.Generator().manual_seed(71)
     # per-row scaled copies of one random grad row keep the host side small;
@@ -133,7 +134,7 @@ def test_split_many_rows_chunked(no_fallback):
     gd = (base_g.to("supa") * (1.0 + k.to("supa") / rows)).to(torch.bfloat16)
     yd = base_y.to(torch.bfloat16).to("supa").expand(rows, cols).contiguous()
     full = LSM_BWD(gd, yd, 1, torch.bfloat16)
-    for lo, hi in ((0, 3), (4094, 4100)):
+    for lo, hi in ((0, 3), (2046, 2050), (4094, 4100)):
         part = LSM_BWD(gd[lo:hi].contiguous(), yd[lo:hi].contiguous(), 1, torch.bfloat16)
         assert torch.equal(full[lo:hi].cpu(), part.cpu()), (lo, hi)
     ref = O.log_softmax_backward(gd[4097:4100].float().cpu().numpy(), yd[4097:4100].float().cpu().numpy())
@@ -242,3 +243,30 @@ def test_split_on_two_streams(no_fallback):
     for o1, o2 in outs:
         assert torch.equal(o1.cpu(), ref[0])
         assert torch.equal(o2.cpu(), ref[1])
+
+
+def test_split_buffers_run_out(no_fallback, monkeypatch):
+    """A device gives out 8 slot buffers; a stream after that takes the one-row
+    kernel.  Each of 16 streams gives exactly the split result or exactly the
+    one-row result."""
+    g, y = bwd_inputs(16, 128256, torch.bfloat16, 121)
+    gd, yd = g.to("supa"), y.to("supa")
+    split = LSM_BWD(gd, yd, 1, torch.bfloat16).cpu()
+    monkeypatch.setenv("SUPA_AMD_ROW_SPLIT", "0")
+    one_row = LSM_BWD(gd, yd, 1, torch.bfloat16).cpu()
+    monkeypatch.delenv("SUPA_AMD_ROW_SPLIT")
+    cur = torch.supa.current_stream()
+    streams = {}
+    while len(streams) < 16:
+        s = torch.supa.Stream()
+        streams[s.stream_id] = s
+    kinds = []
+    for s in streams.values():
+        s.wait_stream(cur)
+        with torch.supa.stream(s):
+            o = LSM_BWD(gd, yd, 1, torch.bfloat16)
+        cur.wait_stream(s)
+        o = o.cpu()
+        kinds.append("split" if torch.equal(o, split) else ("one_row" if torch.equal(o, one_row) else "other"))
+    assert "other" not in kinds
+    assert "one_row" in kinds  # at most 7 of these streams (the default stream has one) got a buffer

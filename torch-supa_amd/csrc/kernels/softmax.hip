@@ -411,23 +411,32 @@ k_sm_bwd_stream(const TG* __restrict__ grad, const TG* __restrict__ outp, TO* __
 // another workgroup being scheduled.  The inputs must not overlap the output
 // for this (the host checks it).
 //
-// Slots are 64-bit; ~0 marks an empty slot (a published forward partial has
-// its sum's NaN canonicalised, a backward one a zero high word, so neither is
-// ~0).  done[row] counts the parts that have read the row's slots; the last
-// one resets the row's slots to ~0 and done[row] to 0, so the buffer is clean
-// after every launch.  The buffer is per (device, stream) and lives until the
-// process ends; launches on one stream are ordered, so they never share it.
+// Slots are 64-bit; 0 marks an empty slot (kSlotTag below).  done[row]
+// counts the parts that have read the row's slots; the last one resets the
+// row's slots and done[row] to 0, so a buffer is clean after every launch.
+// A buffer belongs to one (device, stream) until the process ends; launches
+// on one stream are ordered, so they never share it (a stream destroyed with
+// split work still queued, whose handle a new stream then receives, would
+// share it with that work).
 constexpr int kSplitNV = 4;
 constexpr int kSplitPart = kRowBlock * kSplitNV;
 constexpr int kSplitMinK = 3;
 constexpr int kSplitMaxK = 16;
-constexpr int64_t kSplitSlots = int64_t(1) << 16;  // row parts per launch
-constexpr uint64_t kSlotEmpty = ~uint64_t(0);
+constexpr int64_t kSplitSlots = int64_t(1) << 15;  // row parts per launch
+// An empty slot holds 0; a partial v is published as v ^ kSlotTag, whose high
+// word is never 0 (a forward partial's high word is its sum, a non-negative
+// float or the canonical NaN, below 0x80000000; a backward partial's is 0).
+constexpr uint64_t kSlotTag = 0xFFFFFFFF00000000ull;
 constexpr uint32_t kSplitSpinDefault = 1u << 16;
+// Slot buffers per device (in the library's own device memory, 3 MiB a
+// device): streams past the 8th of a device that reach a split call take the
+// one-row or streaming kernels instead.
+constexpr int kSplitBuffers = 8;
 
 __device__ __forceinline__ void slot_store(uint64_t* p, uint64_t v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+__device__ __forceinline__ void slot_publish(uint64_t* p, uint64_t v) { slot_store(p, v ^ kSlotTag); }
 __device__ __forceinline__ uint64_t slot_load(const uint64_t* p) {
   return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -439,16 +448,16 @@ __device__ __forceinline__ uint32_t split_wait(const uint64_t* rs, int K, uint32
                                                uint32_t* lds_missing) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   if (wave == 0) {
-    uint64_t v = kSlotEmpty;
+    uint64_t v = 0;
     if (lane < K) {
       v = slot_load(rs + lane);
-      for (uint32_t n = 0; v == kSlotEmpty && n < spin_limit; ++n) {
+      for (uint32_t n = 0; v == 0 && n < spin_limit; ++n) {
         __builtin_amdgcn_s_sleep(8);
         v = slot_load(rs + lane);
       }
-      part_w[lane] = v;
+      part_w[lane] = v ^ kSlotTag;
     }
-    const uint64_t miss = __ballot(lane < K && v == kSlotEmpty);
+    const uint64_t miss = __ballot(lane < K && v == 0);
     if (lane == 0) *lds_missing = (uint32_t)miss;
   }
   __syncthreads();
@@ -460,7 +469,7 @@ __device__ __forceinline__ void split_release(uint64_t* rs, uint32_t* done_row, 
   if (threadIdx.x == 0) {
     const uint32_t d = __hip_atomic_fetch_add(done_row, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (d == (uint32_t)K - 1) {
-      for (int q = 0; q < K; ++q) slot_store(rs + q, kSlotEmpty);
+      for (int q = 0; q < K; ++q) slot_store(rs + q, 0);
       __hip_atomic_store(done_row, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
@@ -603,7 +612,7 @@ k_lsm_fwd_split(const TI* __restrict__ in, TO* __restrict__ out, int64_t cols, i
   const uint64_t mine = part_lse<TI>(x, part * kSplitPart, nvec, lds_m, lds_s);
   opaque<kSplitNV>(x);
   uint64_t* rs = slots + (int64_t)row * K;
-  if (threadIdx.x == 0) slot_store(rs + part, mine);
+  if (threadIdx.x == 0) slot_publish(rs + part, mine);
   uint32_t miss = split_wait(rs, K, spin_limit, part_w, &lds_missing);
   split_release(rs, done + row, K);
   if (miss) {  // uniform; the own part is loaded again afterwards, so the fallback reuses its registers
@@ -691,7 +700,7 @@ k_lsm_bwd_split(const TG* __restrict__ grad, const TG* __restrict__ outp, TO* __
   const uint64_t mine = part_sum<TG>(gv, base, nvec, lds);
   opaque<kSplitNV>(gv);
   uint64_t* rs = slots + (int64_t)row * K;
-  if (threadIdx.x == 0) slot_store(rs + part, mine);
+  if (threadIdx.x == 0) slot_publish(rs + part, mine);
   uint32_t miss = split_wait(rs, K, spin_limit, part_w, &lds_missing);
   split_release(rs, done + row, K);
   if (miss) {  // uniform; the own part is loaded again afterwards, so the fallback reuses its registers
@@ -717,20 +726,27 @@ k_lsm_bwd_split(const TG* __restrict__ grad, const TG* __restrict__ outp, TO* __
 __global__ void __launch_bounds__(kBlock) k_split_init(uint64_t* slots, uint32_t* done, int64_t n) {
   const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
   if (i < n) {
-    slots[i] = kSlotEmpty;
+    slots[i] = 0;
     done[i] = 0u;
   }
 }
+
+// The slot buffers live in the library's own device memory (a copy on every
+// device), so the entry points allocate nothing.  Host code reaches them only
+// through the addresses hipGetSymbolAddress gives on each device.
+static __device__ __align__(256) uint64_t g_split_slots[kSplitBuffers * kSplitSlots];
+static __device__ __align__(256) uint32_t g_split_done[kSplitBuffers * kSplitSlots];
 
 struct SplitScratch {
   uint64_t* slots = nullptr;
   uint32_t* done = nullptr;
 };
 
-// The split kernels' buffer for (current device, st), made on first use;
-// false when the split path is switched off (SUPA_AMD_ROW_SPLIT=0), the
-// stream is capturing a graph, or the buffer cannot be made -- the caller
-// then takes the one-row kernels.
+// The split kernels' buffer for (current device, st): one of the device's
+// kSplitBuffers, given to the stream on its first split call (and cleared on
+// it then) and kept; false when the split path is switched off
+// (SUPA_AMD_ROW_SPLIT=0), the stream is capturing a graph, or the device has
+// given out every buffer -- the caller then takes the one-row kernels.
 inline bool split_scratch(hipStream_t st, SplitScratch& out, uint32_t& spin_limit) {
   const char* e = std::getenv("SUPA_AMD_ROW_SPLIT");
   if (e && e[0] == '0') return false;
@@ -742,6 +758,7 @@ inline bool split_scratch(hipStream_t st, SplitScratch& out, uint32_t& spin_limi
   if (hipGetDevice(&dev) != hipSuccess) return false;
   static std::mutex mu;
   static std::map<std::pair<int, hipStream_t>, SplitScratch> bufs;
+  static std::map<int, std::pair<SplitScratch, int>> base;  // device -> (symbol addresses, buffers given out)
   std::lock_guard<std::mutex> lock(mu);
   const auto key = std::make_pair(dev, st);
   auto it = bufs.find(key);
@@ -749,19 +766,28 @@ inline bool split_scratch(hipStream_t st, SplitScratch& out, uint32_t& spin_limi
     out = it->second;
     return true;
   }
-  void* p = nullptr;
-  if (hipMalloc(&p, (size_t)kSplitSlots * (sizeof(uint64_t) + sizeof(uint32_t))) != hipSuccess) {
-    (void)hipGetLastError();
-    return false;
+  auto bt = base.find(dev);
+  if (bt == base.end()) {
+    SplitScratch a;
+    void* ps = nullptr;
+    void* pd = nullptr;
+    if (hipGetSymbolAddress(&ps, HIP_SYMBOL(g_split_slots)) != hipSuccess ||
+        hipGetSymbolAddress(&pd, HIP_SYMBOL(g_split_done)) != hipSuccess) {
+      (void)hipGetLastError();
+      return false;
+    }
+    a.slots = static_cast<uint64_t*>(ps);
+    a.done = static_cast<uint32_t*>(pd);
+    bt = base.emplace(dev, std::make_pair(a, 0)).first;
   }
+  if (bt->second.second >= kSplitBuffers) return false;
+  const int idx = bt->second.second;
   SplitScratch b;
-  b.slots = static_cast<uint64_t*>(p);
-  b.done = reinterpret_cast<uint32_t*>(b.slots + kSplitSlots);
+  b.slots = bt->second.first.slots + (int64_t)idx * kSplitSlots;
+  b.done = bt->second.first.done + (int64_t)idx * kSplitSlots;
   k_split_init<<<(unsigned)(kSplitSlots / kBlock), kBlock, 0, st>>>(b.slots, b.done, kSplitSlots);
-  if (hipGetLastError() != hipSuccess) {
-    (void)hipFree(p);
-    return false;
-  }
+  if (hipGetLastError() != hipSuccess) return false;
+  ++bt->second.second;
   bufs.emplace(key, b);
   out = b;
   return true;
