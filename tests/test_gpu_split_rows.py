@@ -1,17 +1,18 @@
-"""Rows split over several workgroups: the log_softmax backward from 3 parts
-of 4096 16-byte vectors on, and the log_softmax / softmax forwards past what
-one workgroup holds (up to 16 parts).  The parts of a row exchange their row
-partials through a per-stream buffer; a part that finds a peer's slot still
-empty after its spin limit computes that peer's partial itself.
+"""Rows split over several workgroups: rows of more than 8192 16-byte
+vectors in the log_softmax backward and the log_softmax / softmax forwards,
+up to 32 parts (2048 vectors a backward part, 2560 a forward part).  The
+parts of a row exchange their row partials through a per-stream buffer; a
+part that finds a peer's slot still empty after its spin limit computes that
+peer's partial itself.
 
-Covered here: parity with the oracle at every part count boundary (2 parts:
-one-row kernel, 3, 4, 8, 16, 17: streaming kernel), ragged last parts, the
-fallback (SUPA_AMD_ROW_SPLIT_SPIN=0: a part never waits) bit-identical to the
-normal path, the path switched off (SUPA_AMD_ROW_SPLIT=0), launches chunked
-over many rows, an in-place backward (never split), rows holding +-inf and
-NaN, a graph capture (never split), two streams at once (a slot buffer
-each) and more streams than a device has slot buffers (the rest run the
-one-row kernel)."""
+Covered here: parity with the oracle on both sides of the split threshold
+and of the 32-part limit (past it, the streaming kernel), ragged last parts,
+the fallback (SUPA_AMD_ROW_SPLIT_SPIN=0: a part never waits) bit-identical to
+the normal path, the path switched off (SUPA_AMD_ROW_SPLIT=0), launches
+chunked over many rows, an in-place backward (never split), rows holding
++-inf and NaN, a graph capture (never split), two streams at once (a slot
+buffer each) and more streams than a device has slot buffers (the rest run
+the one-row kernel)."""
 import numpy as np
 import pytest
 import torch
@@ -57,7 +58,8 @@ def bwd_inputs(rows, cols, dtype, seed):
     return gd, yd
 
 
-# cols -> parts of 4096 16-byte vectors: bf16 / f16 hold 8 elements a vector, float32 4
+# cols -> backward parts of 2048 16-byte vectors (bf16 / f16: 8 elements a vector, float32 4): 40000 bf16
+# (5000 vectors) stays whole, 65600 bf16 splits in 5, 524288 bf16 in 32, 524296 bf16 and 524288 float32 stream
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("cols", [40000, 65600, 128256, 128264, 262144, 524288, 524296])
 def test_log_softmax_backward_split_matches_oracle(dtype, cols, no_fallback):
@@ -72,7 +74,7 @@ def test_log_softmax_backward_split_matches_oracle(dtype, cols, no_fallback):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
-@pytest.mark.parametrize("cols", [131080, 200000, 262144, 524288])
+@pytest.mark.parametrize("cols", [65536, 65544, 131080, 200000, 262144, 524288])
 def test_log_softmax_forward_split_matches_oracle(dtype, cols, no_fallback):
     x = seeded((3, cols), 41, 2.0, dtype)
     out = torch.log_softmax(x.to("supa"), dim=1)
@@ -122,7 +124,7 @@ def test_split_switched_off_agrees(no_fallback, monkeypatch):
 
 
 def test_split_many_rows_chunked(no_fallback):
-    """16 parts a row: 2048 rows a launch, so 4100 rows take three launches
+    """32 parts a row: 1024 rows a launch, so 4100 rows take five launches
     that reuse the buffer; each row matches the same row computed alone."""
     rows, cols = 4100, 524288
     gen = torch.Generator().manual_seed(71)
@@ -134,7 +136,7 @@ def test_split_many_rows_chunked(no_fallback):
     gd = (base_g.to("supa") * (1.0 + k.to("supa") / rows)).to(torch.bfloat16)
     yd = base_y.to(torch.bfloat16).to("supa").expand(rows, cols).contiguous()
     full = LSM_BWD(gd, yd, 1, torch.bfloat16)
-    for lo, hi in ((0, 3), (2046, 2050), (4094, 4100)):
+    for lo, hi in ((0, 3), (1022, 1026), (4094, 4100)):
         part = LSM_BWD(gd[lo:hi].contiguous(), yd[lo:hi].contiguous(), 1, torch.bfloat16)
         assert torch.equal(full[lo:hi].cpu(), part.cpu()), (lo, hi)
     ref = O.log_softmax_backward(gd[4097:4100].float().cpu().numpy(), yd[4097:4100].float().cpu().numpy())
@@ -246,15 +248,17 @@ def test_split_on_two_streams(no_fallback):
 
 
 def test_split_buffers_run_out(no_fallback, monkeypatch):
-    """A device gives out 8 slot buffers; a stream after that takes the one-row
-    kernel.  Each of 16 streams gives exactly the split result or exactly the
-    one-row result."""
-    g, y = bwd_inputs(16, 128256, torch.bfloat16, 121)
+    """A device gives out 8 slot buffers; a stream after that takes the
+    unsplit kernel.  Each of 16 streams gives exactly the split result or
+    exactly the unsplit one (float32 outputs, where the two kernels' row sums,
+    added in different orders, show)."""
+    g, y = bwd_inputs(16, 128256, torch.float32, 121)
     gd, yd = g.to("supa"), y.to("supa")
-    split = LSM_BWD(gd, yd, 1, torch.bfloat16).cpu()
+    split = LSM_BWD(gd, yd, 1, torch.float32).cpu()
     monkeypatch.setenv("SUPA_AMD_ROW_SPLIT", "0")
-    one_row = LSM_BWD(gd, yd, 1, torch.bfloat16).cpu()
+    one_row = LSM_BWD(gd, yd, 1, torch.float32).cpu()
     monkeypatch.delenv("SUPA_AMD_ROW_SPLIT")
+    assert not torch.equal(split, one_row)
     cur = torch.supa.current_stream()
     streams = {}
     while len(streams) < 16:
@@ -264,7 +268,7 @@ def test_split_buffers_run_out(no_fallback, monkeypatch):
     for s in streams.values():
         s.wait_stream(cur)
         with torch.supa.stream(s):
-            o = LSM_BWD(gd, yd, 1, torch.bfloat16)
+            o = LSM_BWD(gd, yd, 1, torch.float32)
         cur.wait_stream(s)
         o = o.cpu()
         kinds.append("split" if torch.equal(o, split) else ("one_row" if torch.equal(o, one_row) else "other"))

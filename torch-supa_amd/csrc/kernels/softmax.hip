@@ -15,10 +15,10 @@
 // of -1.7e-6 where upstream gives 0); the row results are rounded to bf16/f16
 // (or kept in f32) exactly once.
 //
-// Split rows (the log_softmax backward from 3 parts of 4096 vectors on, the
-// forwards past what one workgroup holds, up to 16 parts): K workgroups share
-// a row, exchanging row partials through a small per-stream buffer, so the
-// same single pass runs with two rows' parts per CU (the section below).
+// Split rows (rows of more than 8192 vectors, up to 32 parts): K workgroups
+// of 512 threads share a row, exchanging row partials through a small
+// per-stream buffer, so the same single pass runs with four parts per CU
+// (the section below).
 //
 // Fallback (any cols, any alignment): one 256-thread workgroup per row,
 // online max/sum in a first pass over memory, the output in a second pass.
@@ -391,18 +391,23 @@ k_sm_bwd_stream(const TG* __restrict__ grad, const TG* __restrict__ outp, TO* __
 }
 
 // ------------------------------------------------------- split rows
-// Rows of 3 to 16 parts of kSplitPart 16-byte vectors (a bf16 row of 24577 to
-// 524288 elements, float32 half that) are split over K workgroups, one part
-// each (1024 threads x kSplitNV vectors = 64 KiB in registers), so two parts
-// of different rows share a CU and one part's stores overlap the other's
-// loads; a whole row per workgroup leaves a CU with one row, whose stores
-// never overlap the next row's loads.  Workgroup b takes part b % K of row
-// b / K.  Each part publishes its row partial -- (max, sum of exp) forward,
-// sum of grad backward -- to slots[row * K + part] with a device-scope
-// atomic store, then waits for the row's other parts by polling their slots
-// (device-scope loads, a short s_sleep between polls), and every part folds
-// the K partials in slot order, so the K parts of a row use one bit-identical
-// total.
+// Rows of more than 8192 16-byte vectors (a bf16 row of more than 65536
+// elements, float32 half that) are split over K workgroups of 512 threads,
+// one part each: the backward's parts are 2048 vectors (4 per thread, 32 KiB
+// of grad and of output), the forward's 2560 (5 per thread, 40 KiB), up to 32
+// parts a row.  Four such workgroups share a CU, so one part's statistics and
+// stores overlap other parts' loads; a whole row per 1024-thread workgroup
+// leaves a CU with one row, whose stores never overlap the next row's loads.
+// On c3's rows (bf16 [8192, 128256]) the backward ran 79.9-80.0 % of the HBM
+// roofline against 75.5-76.3 % with 1024-thread parts of 4096 vectors and
+// 73.2-73.6 % with a whole row per workgroup, the forward 75.3-75.6 %
+// against 69.3-69.7 % and 71.0-71.3 % (parts of 2048 / 2304 / 2688 vectors,
+// 256-768 threads: 59-76 %).  Workgroup b takes part b % K of row b / K.  Each
+// part publishes its row partial -- (max, sum of exp) forward, sum of grad
+// backward -- to slots[row * K + part] with a device-scope atomic store, then
+// waits for the row's other parts by polling their slots (device-scope loads,
+// a short s_sleep between polls), and every part folds the K partials in slot
+// order, so the K parts of a row use one bit-identical total.
 //
 // A part that is still missing after spin_limit polls (a peer not yet
 // resident) is computed by the waiting workgroup itself: it loads that part
@@ -418,10 +423,11 @@ k_sm_bwd_stream(const TG* __restrict__ grad, const TG* __restrict__ outp, TO* __
 // on one stream are ordered, so they never share it (a stream destroyed with
 // split work still queued, whose handle a new stream then receives, would
 // share it with that work).
-constexpr int kSplitNV = 4;
-constexpr int kSplitPart = kRowBlock * kSplitNV;
-constexpr int kSplitMinK = 3;
-constexpr int kSplitMaxK = 16;
+constexpr int kSplitBlock = 512;
+constexpr int kSplitNW = kSplitBlock / 64;
+constexpr int kFwdNV = 5, kBwdNV = 4;  // vectors per thread of a forward / backward part
+constexpr int kSplitMinVec = 8192;     // rows of more vectors split
+constexpr int kSplitMaxK = 32;
 constexpr int64_t kSplitSlots = int64_t(1) << 15;  // row parts per launch
 // An empty slot holds 0; a partial v is published as v ^ kSlotTag, whose high
 // word is never 0 (a forward partial's high word is its sum, a non-negative
@@ -458,7 +464,7 @@ __device__ __forceinline__ uint32_t split_wait(const uint64_t* rs, int K, uint32
       part_w[lane] = v ^ kSlotTag;
     }
     const uint64_t miss = __ballot(lane < K && v == 0);
-    if (lane == 0) *lds_missing = (uint32_t)miss;
+    if (lane == 0) *lds_missing = (uint32_t)miss;  // K <= 32
   }
   __syncthreads();
   return *lds_missing;
@@ -477,89 +483,71 @@ __device__ __forceinline__ void split_release(uint64_t* rs, uint32_t* done_row, 
 
 // A whole part (every part but a row's last) loads without per-vector guards
 // (a uniform branch), so its loads are not split by divergent ones.
-template <typename T>
-__device__ __forceinline__ void split_load(uint4 (&x)[kSplitNV], const uint4* src, int base, int nvec) {
+template <int NV>
+__device__ __forceinline__ void split_load(uint4 (&x)[NV], const uint4* src, int base, int nvec) {
   const int tid = threadIdx.x;
-  if (base + kSplitPart <= nvec) {
+  if (base + kSplitBlock * NV <= nvec) {
 #pragma unroll
-    for (int j = 0; j < kSplitNV; ++j) x[j] = ld_stream(src + base + tid + j * kRowBlock);
+    for (int j = 0; j < NV; ++j) x[j] = ld_stream(src + base + tid + j * kSplitBlock);
   } else {
 #pragma unroll
-    for (int j = 0; j < kSplitNV; ++j)
-      if (base + tid + j * kRowBlock < nvec) x[j] = ld_stream(src + base + tid + j * kRowBlock);
+    for (int j = 0; j < NV; ++j)
+      if (base + tid + j * kSplitBlock < nvec) x[j] = ld_stream(src + base + tid + j * kSplitBlock);
   }
 }
 
-// The 16 wavefront values of a 1024-thread workgroup, combined by a
-// butterfly over lanes (lane l reads wavefront l % 16); every step is
-// symmetric in its operands, so every lane ends with the same value.
-__device__ __forceinline__ void block_lse16(float& M, float& S, const float* lds_m, const float* lds_s) {
-  const int lane = threadIdx.x & 63;
-  M = lds_m[lane & 15];
-  S = lds_s[lane & 15];
+// The kSplitNW wavefront values of a workgroup, combined by a butterfly over
+// 16 lanes (lane l reads wavefront l % 16, or the identity past kSplitNW);
+// every step is symmetric in its operands, so every lane ends with the same
+// value.
+__device__ __forceinline__ void block_lse(float& M, float& S, const float* lds_m, const float* lds_s) {
+  const int i = threadIdx.x & 15;
+  M = i < kSplitNW ? lds_m[i] : -__builtin_inff();
+  S = i < kSplitNW ? lds_s[i] : 0.0f;
 #pragma unroll
   for (int off = 8; off > 0; off >>= 1) lse_combine(M, S, __shfl_xor(M, off, 64), __shfl_xor(S, off, 64));
 }
-__device__ __forceinline__ float block_sum16(const float* lds) {
-  float S = lds[threadIdx.x & 15];
+__device__ __forceinline__ float block_sum(const float* lds) {
+  const int i = threadIdx.x & 15;
+  float S = i < kSplitNW ? lds[i] : 0.0f;
 #pragma unroll
   for (int off = 8; off > 0; off >>= 1) S += __shfl_xor(S, off, 64);
   return S;
 }
 
-// Per-thread (max, sum of exp(x - max)) over the thread's vectors of a part;
-// WHOLE: every vector is in the row (no per-vector guard).  bf16 maxima come
-// from the raw words: a word read as float orders like its high element (the
-// low element only adds less than one bf16 ulp), so the high elements need no
-// unpacking, and clearing the low 16 bits of the result gives the exact bf16
-// maximum.  The one case this misses, +inf in a high element next to a
-// nonzero low element (a NaN word, which max ignores), makes that element's
-// exp term +inf; a finite sum cannot reach +inf (every term is at most 1), so
-// s = +inf becomes NaN -- the row's result whenever it holds +inf.
-template <typename TI, bool WHOLE>
-__device__ __forceinline__ void thread_lse(uint4 (&x)[kSplitNV], int base, int nvec, float& m, float& s) {
+// Per-thread (max, sum of exp(x - max)) over the thread's vectors of a part.
+// The forward keeps its per-vector guards on whole parts too: a specialization
+// without them took 62 VGPRs against 57 and ran at 71.1-71.9 % of the HBM
+// roofline against 73.2-74.7 % on c3's rows.
+template <typename TI, int NV>
+__device__ __forceinline__ void thread_lse(uint4 (&x)[NV], int base, int nvec, float& m, float& s) {
   constexpr int V = VecOf<TI>::V;
   const int tid = threadIdx.x;
   m = -__builtin_inff();
-  if constexpr (std::is_same<TI, bf16>::value) {
 #pragma unroll
-    for (int j = 0; j < kSplitNV; ++j)
-      if (WHOLE || base + tid + j * kRowBlock < nvec) {
+  for (int j = 0; j < NV; ++j)
+    if (base + tid + j * kSplitBlock < nvec) {
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const uint32_t w = word_of(x[j], k);
-          m = fmaxf(m, fmaxf(__uint_as_float(w), __uint_as_float(w << 16)));
-        }
-      }
-    m = __uint_as_float(__float_as_uint(m) & 0xffff0000u);
-  } else {
-#pragma unroll
-    for (int j = 0; j < kSplitNV; ++j)
-      if (WHOLE || base + tid + j * kRowBlock < nvec) {
-#pragma unroll
-        for (int k = 0; k < V; ++k) m = fmaxf(m, elem_f<TI>(x[j], k));
-      }
-  }
+      for (int k = 0; k < V; ++k) m = fmaxf(m, elem_f<TI>(x[j], k));
+    }
   const float mb = m == -__builtin_inff() ? 0.0f : m;
-  opaque<kSplitNV>(x);
+  opaque<NV>(x);
   s = 0.0f;
 #pragma unroll
-  for (int j = 0; j < kSplitNV; ++j)
-    if (WHOLE || base + tid + j * kRowBlock < nvec) {
+  for (int j = 0; j < NV; ++j)
+    if (base + tid + j * kSplitBlock < nvec) {
 #pragma unroll
       for (int k = 0; k < V; ++k) s += __builtin_amdgcn_exp2f((elem_f<TI>(x[j], k) - mb) * kLog2e);
     }
-  if (std::is_same<TI, bf16>::value && s == __builtin_inff()) s = __builtin_nanf("");
 }
 
 // (max, sum of exp(x - max)) of one part, the same in every thread; the
 // sum's NaN is canonical.
-template <typename TI>
-__device__ __forceinline__ uint64_t part_lse(uint4 (&x)[kSplitNV], int base, int nvec, float* lds_m, float* lds_s) {
+template <typename TI, int NV>
+__device__ __forceinline__ uint64_t part_lse(uint4 (&x)[NV], int base, int nvec, float* lds_m, float* lds_s) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   float m, s;
-  if (base + kSplitPart <= nvec) thread_lse<TI, true>(x, base, nvec, m, s);
-  else thread_lse<TI, false>(x, base, nvec, m, s);
+  thread_lse<TI, NV>(x, base, nvec, m, s);
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) lse_combine(m, s, __shfl_xor(m, off, 64), __shfl_xor(s, off, 64));
   __syncthreads();
@@ -569,19 +557,19 @@ __device__ __forceinline__ uint64_t part_lse(uint4 (&x)[kSplitNV], int base, int
   }
   __syncthreads();
   float M, S;
-  block_lse16(M, S, lds_m, lds_s);
+  block_lse(M, S, lds_m, lds_s);
   const uint32_t sb = S != S ? 0x7fc00000u : __float_as_uint(S);
   return ((uint64_t)sb << 32) | __float_as_uint(M);
 }
 
-template <typename TI, typename TO, bool LOG, bool WHOLE>
-__device__ __forceinline__ void fwd_split_out(const uint4 (&x)[kSplitNV], Vec<TO, VecOf<TI>::V>* dst, int base, int nvec,
-                                              float M, float logsum, float Mb, float inv) {
+template <typename TI, typename TO, bool LOG>
+__device__ __forceinline__ void fwd_split_out(const uint4 (&x)[kFwdNV], Vec<TO, VecOf<TI>::V>* dst, int base,
+                                              int nvec, float M, float logsum, float Mb, float inv) {
   constexpr int V = VecOf<TI>::V;
 #pragma unroll
-  for (int j = 0; j < kSplitNV; ++j) {
-    const int v = base + (int)threadIdx.x + j * kRowBlock;
-    if (WHOLE || v < nvec) {
+  for (int j = 0; j < kFwdNV; ++j) {
+    const int v = base + (int)threadIdx.x + j * kSplitBlock;
+    if (v < nvec) {
       float f[V];
 #pragma unroll
       for (int k = 0; k < V; ++k) {
@@ -594,23 +582,24 @@ __device__ __forceinline__ void fwd_split_out(const uint4 (&x)[kSplitNV], Vec<TO
 }
 
 template <typename TI, typename TO, bool LOG>
-__global__ void __launch_bounds__(kRowBlock, 8)
+__global__ void __launch_bounds__(kSplitBlock, 8)
 k_lsm_fwd_split(const TI* __restrict__ in, TO* __restrict__ out, int64_t cols, int K, uint64_t* __restrict__ slots,
                 uint32_t* __restrict__ done, uint32_t spin_limit) {
   constexpr int V = VecOf<TI>::V;
-  constexpr int NW = kRowBlock / 64;
-  __shared__ float lds_m[NW];
-  __shared__ float lds_s[NW];
+  constexpr int PART = kSplitBlock * kFwdNV;
+  __shared__ float lds_m[kSplitNW];
+  __shared__ float lds_s[kSplitNW];
   __shared__ uint64_t part_w[kSplitMaxK];
   __shared__ uint32_t lds_missing;
   const int row = (int)(blockIdx.x / (unsigned)K);
   const int part = (int)(blockIdx.x - (unsigned)row * (unsigned)K);
   const int nvec = (int)(cols / V);
+  const int base = part * PART;
   const uint4* src = reinterpret_cast<const uint4*>(in + (int64_t)row * cols);
-  uint4 x[kSplitNV];
-  split_load<TI>(x, src, part * kSplitPart, nvec);
-  const uint64_t mine = part_lse<TI>(x, part * kSplitPart, nvec, lds_m, lds_s);
-  opaque<kSplitNV>(x);
+  uint4 x[kFwdNV];
+  split_load<kFwdNV>(x, src, base, nvec);
+  const uint64_t mine = part_lse<TI, kFwdNV>(x, base, nvec, lds_m, lds_s);
+  opaque<kFwdNV>(x);
   uint64_t* rs = slots + (int64_t)row * K;
   if (threadIdx.x == 0) slot_publish(rs + part, mine);
   uint32_t miss = split_wait(rs, K, spin_limit, part_w, &lds_missing);
@@ -619,11 +608,11 @@ k_lsm_fwd_split(const TI* __restrict__ in, TO* __restrict__ out, int64_t cols, i
     do {
       const int q = __builtin_ctz(miss);
       miss &= miss - 1;
-      split_load<TI>(x, src, q * kSplitPart, nvec);
-      const uint64_t w = part_lse<TI>(x, q * kSplitPart, nvec, lds_m, lds_s);
+      split_load<kFwdNV>(x, src, q * PART, nvec);
+      const uint64_t w = part_lse<TI, kFwdNV>(x, q * PART, nvec, lds_m, lds_s);
       if (threadIdx.x == 0) part_w[q] = w;
     } while (miss);
-    split_load<TI>(x, src, part * kSplitPart, nvec);
+    split_load<kFwdNV>(x, src, base, nvec);
   }
   __syncthreads();
   float M = __uint_as_float((uint32_t)part_w[0]), S = __uint_as_float((uint32_t)(part_w[0] >> 32));
@@ -632,20 +621,18 @@ k_lsm_fwd_split(const TI* __restrict__ in, TO* __restrict__ out, int64_t cols, i
   const float logsum = LOG ? sa_logf(S) : 0.0f;
   const float inv = LOG ? 0.0f : 1.0f / S;
   const float Mb = M == -__builtin_inff() ? 0.0f : M;
-  opaque<kSplitNV>(x);
+  opaque<kFwdNV>(x);
   Vec<TO, V>* dst = reinterpret_cast<Vec<TO, V>*>(out + (int64_t)row * cols);
-  const int base = part * kSplitPart;
-  if (base + kSplitPart <= nvec) fwd_split_out<TI, TO, LOG, true>(x, dst, base, nvec, M, logsum, Mb, inv);
-  else fwd_split_out<TI, TO, LOG, false>(x, dst, base, nvec, M, logsum, Mb, inv);
+  fwd_split_out<TI, TO, LOG>(x, dst, base, nvec, M, logsum, Mb, inv);
 }
 
 template <typename TG, bool WHOLE>
-__device__ __forceinline__ float thread_sum(const uint4 (&g)[kSplitNV], int base, int nvec) {
+__device__ __forceinline__ float thread_sum(const uint4 (&g)[kBwdNV], int base, int nvec) {
   constexpr int V = VecOf<TG>::V;
   float s = 0.0f;
 #pragma unroll
-  for (int j = 0; j < kSplitNV; ++j)
-    if (WHOLE || base + (int)threadIdx.x + j * kRowBlock < nvec) {
+  for (int j = 0; j < kBwdNV; ++j)
+    if (WHOLE || base + (int)threadIdx.x + j * kSplitBlock < nvec) {
 #pragma unroll
       for (int k = 0; k < V; ++k) s += elem_f<TG>(g[j], k);
     }
@@ -654,22 +641,23 @@ __device__ __forceinline__ float thread_sum(const uint4 (&g)[kSplitNV], int base
 
 // Sum of one part of grad, the same in every thread.
 template <typename TG>
-__device__ __forceinline__ uint64_t part_sum(uint4 (&g)[kSplitNV], int base, int nvec, float* lds) {
-  float s = base + kSplitPart <= nvec ? thread_sum<TG, true>(g, base, nvec) : thread_sum<TG, false>(g, base, nvec);
+__device__ __forceinline__ uint64_t part_sum(uint4 (&g)[kBwdNV], int base, int nvec, float* lds) {
+  float s = base + kSplitBlock * kBwdNV <= nvec ? thread_sum<TG, true>(g, base, nvec)
+                                                : thread_sum<TG, false>(g, base, nvec);
   s = wave_sum(s);
   __syncthreads();
   if ((threadIdx.x & 63) == 0) lds[threadIdx.x >> 6] = s;
   __syncthreads();
-  return (uint64_t)__float_as_uint(block_sum16(lds));
+  return (uint64_t)__float_as_uint(block_sum(lds));
 }
 
 template <typename TG, typename TO, bool WHOLE>
-__device__ __forceinline__ void bwd_split_out(const uint4 (&gv)[kSplitNV], const uint4 (&yv)[kSplitNV],
+__device__ __forceinline__ void bwd_split_out(const uint4 (&gv)[kBwdNV], const uint4 (&yv)[kBwdNV],
                                               Vec<TO, VecOf<TG>::V>* dst, int base, int nvec, float S) {
   constexpr int V = VecOf<TG>::V;
 #pragma unroll
-  for (int j = 0; j < kSplitNV; ++j) {
-    const int v = base + (int)threadIdx.x + j * kRowBlock;
+  for (int j = 0; j < kBwdNV; ++j) {
+    const int v = base + (int)threadIdx.x + j * kSplitBlock;
     if (WHOLE || v < nvec) {
       float f[V];
 #pragma unroll
@@ -681,24 +669,25 @@ __device__ __forceinline__ void bwd_split_out(const uint4 (&gv)[kSplitNV], const
 }
 
 template <typename TG, typename TO>
-__global__ void __launch_bounds__(kRowBlock, 8)
+__global__ void __launch_bounds__(kSplitBlock, 8)
 k_lsm_bwd_split(const TG* __restrict__ grad, const TG* __restrict__ outp, TO* __restrict__ gin, int64_t cols, int K,
                 uint64_t* __restrict__ slots, uint32_t* __restrict__ done, uint32_t spin_limit) {
   constexpr int V = VecOf<TG>::V;
-  __shared__ float lds[kRowBlock / 64];
+  constexpr int PART = kSplitBlock * kBwdNV;
+  __shared__ float lds[kSplitNW];
   __shared__ uint64_t part_w[kSplitMaxK];
   __shared__ uint32_t lds_missing;
   const int row = (int)(blockIdx.x / (unsigned)K);
   const int part = (int)(blockIdx.x - (unsigned)row * (unsigned)K);
   const int nvec = (int)(cols / V);
-  const int base = part * kSplitPart;
+  const int base = part * PART;
   const uint4* g = reinterpret_cast<const uint4*>(grad + (int64_t)row * cols);
   const uint4* y = reinterpret_cast<const uint4*>(outp + (int64_t)row * cols);
-  uint4 gv[kSplitNV], yv[kSplitNV];
-  split_load<TG>(gv, g, base, nvec);
-  split_load<TG>(yv, y, base, nvec);
+  uint4 gv[kBwdNV], yv[kBwdNV];
+  split_load<kBwdNV>(gv, g, base, nvec);
+  split_load<kBwdNV>(yv, y, base, nvec);
   const uint64_t mine = part_sum<TG>(gv, base, nvec, lds);
-  opaque<kSplitNV>(gv);
+  opaque<kBwdNV>(gv);
   uint64_t* rs = slots + (int64_t)row * K;
   if (threadIdx.x == 0) slot_publish(rs + part, mine);
   uint32_t miss = split_wait(rs, K, spin_limit, part_w, &lds_missing);
@@ -707,19 +696,19 @@ k_lsm_bwd_split(const TG* __restrict__ grad, const TG* __restrict__ outp, TO* __
     do {
       const int q = __builtin_ctz(miss);
       miss &= miss - 1;
-      split_load<TG>(gv, g, q * kSplitPart, nvec);
-      const uint64_t w = part_sum<TG>(gv, q * kSplitPart, nvec, lds);
+      split_load<kBwdNV>(gv, g, q * PART, nvec);
+      const uint64_t w = part_sum<TG>(gv, q * PART, nvec, lds);
       if (threadIdx.x == 0) part_w[q] = w;
     } while (miss);
-    split_load<TG>(gv, g, base, nvec);
+    split_load<kBwdNV>(gv, g, base, nvec);
   }
   __syncthreads();
   float S = __uint_as_float((uint32_t)part_w[0]);
   for (int q = 1; q < K; ++q) S += __uint_as_float((uint32_t)part_w[q]);
-  opaque<kSplitNV>(gv);
-  opaque<kSplitNV>(yv);
+  opaque<kBwdNV>(gv);
+  opaque<kBwdNV>(yv);
   Vec<TO, V>* dst = reinterpret_cast<Vec<TO, V>*>(gin + (int64_t)row * cols);
-  if (base + kSplitPart <= nvec) bwd_split_out<TG, TO, true>(gv, yv, dst, base, nvec, S);
+  if (base + PART <= nvec) bwd_split_out<TG, TO, true>(gv, yv, dst, base, nvec, S);
   else bwd_split_out<TG, TO, false>(gv, yv, dst, base, nvec, S);
 }
 
@@ -793,10 +782,12 @@ inline bool split_scratch(hipStream_t st, SplitScratch& out, uint32_t& spin_limi
   return true;
 }
 
-// Parts per row for the split kernels, 0 when the row takes another kernel.
-inline int split_parts(int64_t nvec, const void* a, const void* b, int64_t a_bytes, const void* o, int64_t o_bytes) {
-  const int64_t K = (nvec + kSplitPart - 1) / kSplitPart;
-  if (K < kSplitMinK || K > kSplitMaxK) return 0;
+// Parts of `part` vectors per row for the split kernels, 0 when the row
+// takes another kernel.
+inline int split_parts(int64_t nvec, int part, const void* a, const void* b, int64_t a_bytes, const void* o,
+                       int64_t o_bytes) {
+  const int64_t K = (nvec + part - 1) / part;
+  if (nvec <= kSplitMinVec || K > kSplitMaxK) return 0;
   auto overlap = [](const void* x, int64_t xb, const void* y, int64_t yb) {
     const uintptr_t x0 = reinterpret_cast<uintptr_t>(x), y0 = reinterpret_cast<uintptr_t>(y);
     return x0 < y0 + (uintptr_t)yb && y0 < x0 + (uintptr_t)xb;
@@ -828,21 +819,16 @@ int softmax_forward(const void* in, int32_t in_dtype, void* out, int32_t out_dty
       if (in_dtype != out_dtype && out_dtype != SUPA_AMD_F32) return SUPA_AMD_EDTYPE;
       constexpr int V = VecOf<TI>::V;
       const bool vec_ok = (cols % V) == 0 && aligned(in, 16) && aligned(out, V * sizeof(TO));
-      // The forward splits only rows the one-row kernel cannot hold: on a c3
-      // row (bf16 [8192, 128256]) the split forward measured 70-72.5 % against
-      // the one-row kernel's 71.7-72.4 % (its exp pass, between the part's
-      // loads and its exchange, is what each part waits on).
-      const int K = vec_ok && cols / V > 16 * kRowBlock
-                        ? split_parts(cols / V, in, nullptr, rows * cols * (int64_t)sizeof(TI), out,
-                                      rows * cols * (int64_t)sizeof(TO))
-                        : 0;
+      const int K = vec_ok ? split_parts(cols / V, kSplitBlock * kFwdNV, in, nullptr,
+                                         rows * cols * (int64_t)sizeof(TI), out, rows * cols * (int64_t)sizeof(TO))
+                           : 0;
       SplitScratch sb;
       uint32_t spin = 0;
       if (K > 0 && split_scratch(st, sb, spin)) {
         const int64_t chunk = kSplitSlots / K;
         for (int64_t r0 = 0; r0 < rows; r0 += chunk) {
           const int64_t nr = std::min(chunk, rows - r0);
-          k_lsm_fwd_split<TI, TO, LOG><<<(unsigned)(nr * K), kRowBlock, 0, st>>>(
+          k_lsm_fwd_split<TI, TO, LOG><<<(unsigned)(nr * K), kSplitBlock, 0, st>>>(
               static_cast<const TI*>(in) + r0 * cols, static_cast<TO*>(out) + r0 * cols, cols, K, sb.slots, sb.done,
               spin);
         }
@@ -900,8 +886,8 @@ int supa_amd_log_softmax_backward(const void* grad, const void* output, int32_t 
       const TG* pg = static_cast<const TG*>(grad);
       const TG* py = static_cast<const TG*>(output);
       TO* po = static_cast<TO*>(grad_in);
-      const int K = vec_ok ? split_parts(cols / V, grad, output, rows * cols * (int64_t)sizeof(TG), grad_in,
-                                         rows * cols * (int64_t)sizeof(TO))
+      const int K = vec_ok ? split_parts(cols / V, kSplitBlock * kBwdNV, grad, output,
+                                         rows * cols * (int64_t)sizeof(TG), grad_in, rows * cols * (int64_t)sizeof(TO))
                            : 0;
       SplitScratch sb;
       uint32_t spin = 0;
@@ -909,7 +895,7 @@ int supa_amd_log_softmax_backward(const void* grad, const void* output, int32_t 
         const int64_t chunk = kSplitSlots / K;
         for (int64_t r0 = 0; r0 < rows; r0 += chunk) {
           const int64_t nr = std::min(chunk, rows - r0);
-          k_lsm_bwd_split<TG, TO><<<(unsigned)(nr * K), kRowBlock, 0, st>>>(pg + r0 * cols, py + r0 * cols,
+          k_lsm_bwd_split<TG, TO><<<(unsigned)(nr * K), kSplitBlock, 0, st>>>(pg + r0 * cols, py + r0 * cols,
                                                                            po + r0 * cols, cols, K, sb.slots,
                                                                            sb.done, spin);
         }
