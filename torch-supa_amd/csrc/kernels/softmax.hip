@@ -428,13 +428,13 @@ constexpr int kSplitNW = kSplitBlock / 64;
 constexpr int kFwdNV = 5, kBwdNV = 4;  // vectors per thread of a forward / backward part
 constexpr int kSplitMinVec = 8192;     // rows of more vectors split
 constexpr int kSplitMaxK = 32;
-constexpr int64_t kSplitSlots = int64_t(1) << 15;  // row parts per launch
+constexpr int64_t kSplitSlots = int64_t(1) << 16;  // row parts per launch (c3's 8192 rows x 8 parts: one)
 // An empty slot holds 0; a partial v is published as v ^ kSlotTag, whose high
 // word is never 0 (a forward partial's high word is its sum, a non-negative
 // float or the canonical NaN, below 0x80000000; a backward partial's is 0).
 constexpr uint64_t kSlotTag = 0xFFFFFFFF00000000ull;
 constexpr uint32_t kSplitSpinDefault = 1u << 16;
-// Slot buffers per device (in the library's own device memory, 3 MiB a
+// Slot buffers per device (in the library's own device memory, 6 MiB a
 // device): streams past the 8th of a device that reach a split call take the
 // one-row or streaming kernels instead.
 constexpr int kSplitBuffers = 8;
