@@ -635,7 +635,7 @@ STATS_ROOFLINE_ROWS = [
     ("c1 gelu('none')", "sa::k_contig<64, 4, sa::UnaryOp<0, float>, float, float, float, float>", C1_N // 4,
      8 * C1_N),
     ("c1 silu", "sa::k_contig<64, 4, sa::UnaryOp<2, float>, float, float, float, float>", C1_N // 4, 8 * C1_N),
-    ("c3 _log_softmax", "sa::k_lsm_fwd_reg<sa::bf16, sa::bf16, 16, true>", None, 4 * C3_NV),
+    ("c3 _log_softmax", "sa::k_lsm_fwd_split<sa::bf16, sa::bf16, true>", None, 4 * C3_NV),
     ("c3 nll_loss_backward", "sa::k_nll_bwd<sa::bf16, 8>", None, 2 * C3_NV + 65538),
     ("c3 _log_softmax_backward_data", "sa::k_lsm_bwd_split<sa::bf16, sa::bf16>", None, 6 * C3_NV),
     ("c3 fused cross-entropy forward (bf16 opt-in; float32 takes it by default)", "sa::k_ce_fwd<sa::bf16, true>", None, 2 * C3_NV),
@@ -815,7 +815,7 @@ PROBE_ALG_BYTES = {
            ("UnaryOp<0,", 8 * C1_N), ("UnaryOp<2,", 8 * C1_N)],
     "c2": [("AddOp", C2_ADD_BYTES), ("UnaryOp<1,", C2_GELU_BYTES), ("UnaryOpILi1EfE", C2_GELU_BYTES),
            ("k_transpose_vec", 4 * C2_N)],
-    "c3": [("k_lsm_fwd_reg", C3_BYTES["_log_softmax"]), ("k_nll_bwd", C3_BYTES["nll_loss_backward"]),
+    "c3": [("k_lsm_fwd_split", C3_BYTES["_log_softmax"]), ("k_nll_bwd", C3_BYTES["nll_loss_backward"]),
            ("k_lsm_bwd_split", C3_BYTES["_log_softmax_backward_data"])],
     "c4": [("MseOp", 12 * 32 * 1048576), ("BceBwdOp", 16 * 32 * 1048576 + 4 * 1048576)],
     # two k_adamw launches (40 + 32 tensors) per step: the average dispatch moves half of 28 P
