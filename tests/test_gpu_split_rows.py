@@ -1,12 +1,13 @@
-"""Rows split over several workgroups: rows of more than 8192 16-byte
-vectors in the log_softmax backward and the log_softmax / softmax forwards,
-up to 32 parts (2048 vectors a backward part, 2560 a forward part).  The
-parts of a row exchange their row partials through a per-stream buffer; a
-part that finds a peer's slot still empty after its spin limit computes that
-peer's partial itself.
+"""Rows split over several workgroups: log_softmax backward and log_softmax
+/ softmax forward rows of 2 to 32 parts (2048 16-byte vectors a backward
+part, 2560 a forward part; a row of fewer than 6 parts splits only when its
+last part holds at least 40 % of a part).  The parts of a row exchange their
+row partials through a per-stream buffer; a part that finds a peer's slot
+still empty after its spin limit computes that peer's partial itself.
 
-Covered here: parity with the oracle on both sides of the split threshold
-and of the 32-part limit (past it, the streaming kernel), ragged last parts,
+Covered here: parity with the oracle on rows that split and rows that do not
+(too few parts, a short last part, past the 32-part limit: the streaming
+kernel), ragged last parts,
 the fallback (SUPA_AMD_ROW_SPLIT_SPIN=0: a part never waits) bit-identical to
 the normal path, the path switched off (SUPA_AMD_ROW_SPLIT=0), launches
 chunked over many rows, an in-place backward (never split), rows holding
@@ -59,7 +60,8 @@ def bwd_inputs(rows, cols, dtype, seed):
 
 
 # cols -> backward parts of 2048 16-byte vectors (bf16 / f16: 8 elements a vector, float32 4): 40000 bf16
-# (5000 vectors) stays whole, 65600 bf16 splits in 5, 524288 bf16 in 32, 524296 bf16 and 524288 float32 stream
+# (5000 vectors) splits in 3, 65600 bf16 (4 parts and 8 vectors) stays whole, 524288 bf16 splits in 32,
+# 524296 bf16 and 524288 float32 stream
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("cols", [40000, 65600, 128256, 128264, 262144, 524288, 524296])
 def test_log_softmax_backward_split_matches_oracle(dtype, cols, no_fallback):
@@ -74,7 +76,7 @@ def test_log_softmax_backward_split_matches_oracle(dtype, cols, no_fallback):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
-@pytest.mark.parametrize("cols", [65536, 65544, 131080, 200000, 262144, 524288])
+@pytest.mark.parametrize("cols", [32000, 50304, 65536, 65544, 131080, 200000, 262144, 524288])
 def test_log_softmax_forward_split_matches_oracle(dtype, cols, no_fallback):
     x = seeded((3, cols), 41, 2.0, dtype)
     out = torch.log_softmax(x.to("supa"), dim=1)

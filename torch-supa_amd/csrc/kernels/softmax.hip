@@ -15,7 +15,7 @@
 // of -1.7e-6 where upstream gives 0); the row results are rounded to bf16/f16
 // (or kept in f32) exactly once.
 //
-// Split rows (rows of more than 8192 vectors, up to 32 parts): K workgroups
+// Split rows (rows of 2 to 32 parts of 2048 or 2560 vectors): K workgroups
 // of 512 threads share a row, exchanging row partials through a small
 // per-stream buffer, so the same single pass runs with four parts per CU
 // (the section below).
@@ -391,11 +391,10 @@ k_sm_bwd_stream(const TG* __restrict__ grad, const TG* __restrict__ outp, TO* __
 }
 
 // ------------------------------------------------------- split rows
-// Rows of more than 8192 16-byte vectors (a bf16 row of more than 65536
-// elements, float32 half that) are split over K workgroups of 512 threads,
-// one part each: the backward's parts are 2048 vectors (4 per thread, 32 KiB
-// of grad and of output), the forward's 2560 (5 per thread, 40 KiB), up to 32
-// parts a row.  Four such workgroups share a CU, so one part's statistics and
+// Rows of 2 to 32 parts (split_parts below says which) are split over K
+// workgroups of 512 threads, one part each: the backward's parts are 2048
+// 16-byte vectors (4 per thread, 32 KiB of grad and of output), the forward's
+// 2560 (5 per thread, 40 KiB).  Four such workgroups share a CU, so one part's statistics and
 // stores overlap other parts' loads; a whole row per 1024-thread workgroup
 // leaves a CU with one row, whose stores never overlap the next row's loads.
 // On c3's rows (bf16 [8192, 128256]) the backward ran 79.9-80.0 % of the HBM
@@ -426,7 +425,6 @@ k_sm_bwd_stream(const TG* __restrict__ grad, const TG* __restrict__ outp, TO* __
 constexpr int kSplitBlock = 512;
 constexpr int kSplitNW = kSplitBlock / 64;
 constexpr int kFwdNV = 5, kBwdNV = 4;  // vectors per thread of a forward / backward part
-constexpr int kSplitMinVec = 8192;     // rows of more vectors split
 constexpr int kSplitMaxK = 32;
 constexpr int64_t kSplitSlots = int64_t(1) << 16;  // row parts per launch (c3's 8192 rows x 8 parts: one)
 // An empty slot holds 0; a partial v is published as v ^ kSlotTag, whose high
@@ -783,11 +781,18 @@ inline bool split_scratch(hipStream_t st, SplitScratch& out, uint32_t& spin_limi
 }
 
 // Parts of `part` vectors per row for the split kernels, 0 when the row
-// takes another kernel.
+// takes another kernel: at least 2 and at most kSplitMaxK parts, and a last
+// part of at least 40 % of a part unless there are 6 or more.  Measured
+// against the one-row kernels (bf16 rows): [32768, 32000] forward 68.8 ->
+// 72.4 %, backward 73.4 -> 77.2 % (2 parts each); [16384, 50304] forward
+// 68.1 -> 76.4 % (3 parts, the last 46 %), backward 75.0 -> 73.5 % (4 parts,
+// the last 7 %: kept whole); [16384, 65536] forward 72.8 -> 70.5 % (4 parts,
+// the last 20 %: kept whole), backward 70.5 -> 80.9 % (4 whole parts).
 inline int split_parts(int64_t nvec, int part, const void* a, const void* b, int64_t a_bytes, const void* o,
                        int64_t o_bytes) {
   const int64_t K = (nvec + part - 1) / part;
-  if (nvec <= kSplitMinVec || K > kSplitMaxK) return 0;
+  if (K < 2 || K > kSplitMaxK) return 0;
+  if (K < 6 && 5 * (nvec - (K - 1) * part) < 2 * (int64_t)part) return 0;
   auto overlap = [](const void* x, int64_t xb, const void* y, int64_t yb) {
     const uintptr_t x0 = reinterpret_cast<uintptr_t>(x), y0 = reinterpret_cast<uintptr_t>(y);
     return x0 < y0 + (uintptr_t)yb && y0 < x0 + (uintptr_t)xb;
