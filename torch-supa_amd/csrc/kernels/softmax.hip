@@ -494,16 +494,35 @@ __device__ __forceinline__ void split_load(uint4 (&x)[NV], const uint4* src, int
   }
 }
 
-// The kSplitNW wavefront values of a workgroup, combined by a butterfly over
-// 16 lanes (lane l reads wavefront l % 16, or the identity past kSplitNW);
-// every step is symmetric in its operands, so every lane ends with the same
-// value.
+// s = sum of exp(x - m) rescaled to a maximum M >= m: s e^(m - M) (an all
+// -inf M leaves s, which is then 0; a NaN s stays NaN).
+__device__ __forceinline__ float lse_rescale(float s, float m, float M) {
+  return M != -__builtin_inff() ? s * __builtin_amdgcn_exp2f((m - M) * kLog2e) : s;
+}
+
+// (max, sum of exp) pairs of `width` lanes (a power of two; lanes w apart in
+// the XOR pattern hold the other pairs) combined: a max butterfly, one
+// rescale per lane to that max, and a sum butterfly -- one exponential per
+// lane where pairwise (m, s) combining takes two per step.  Every butterfly
+// step is symmetric in its operands, so every lane ends with the same value.
+template <int WIDTH>
+__device__ __forceinline__ void lanes_lse(float& m, float& s) {
+  float M = m;
+#pragma unroll
+  for (int off = WIDTH / 2; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+  s = lse_rescale(s, m, M);
+#pragma unroll
+  for (int off = WIDTH / 2; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+  m = M;
+}
+
+// The kSplitNW wavefront values of a workgroup, combined over 16 lanes (lane
+// l reads wavefront l % 16, or the identity past kSplitNW).
 __device__ __forceinline__ void block_lse(float& M, float& S, const float* lds_m, const float* lds_s) {
   const int i = threadIdx.x & 15;
   M = i < kSplitNW ? lds_m[i] : -__builtin_inff();
   S = i < kSplitNW ? lds_s[i] : 0.0f;
-#pragma unroll
-  for (int off = 8; off > 0; off >>= 1) lse_combine(M, S, __shfl_xor(M, off, 64), __shfl_xor(S, off, 64));
+  lanes_lse<16>(M, S);
 }
 __device__ __forceinline__ float block_sum(const float* lds) {
   const int i = threadIdx.x & 15;
@@ -546,8 +565,7 @@ __device__ __forceinline__ uint64_t part_lse(uint4 (&x)[NV], int base, int nvec,
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   float m, s;
   thread_lse<TI, NV>(x, base, nvec, m, s);
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) lse_combine(m, s, __shfl_xor(m, off, 64), __shfl_xor(s, off, 64));
+  lanes_lse<64>(m, s);
   __syncthreads();
   if (lane == 0) {
     lds_m[wave] = m;
@@ -613,9 +631,13 @@ k_lsm_fwd_split(const TI* __restrict__ in, TO* __restrict__ out, int64_t cols, i
     split_load<kFwdNV>(x, src, base, nvec);
   }
   __syncthreads();
-  float M = __uint_as_float((uint32_t)part_w[0]), S = __uint_as_float((uint32_t)(part_w[0] >> 32));
-  for (int q = 1; q < K; ++q)
-    lse_combine(M, S, __uint_as_float((uint32_t)part_w[q]), __uint_as_float((uint32_t)(part_w[q] >> 32)));
+  // the row's (max, sum) from the K part pairs, in part order: the max, then
+  // each part's sum rescaled to it (K exponentials)
+  float M = __uint_as_float((uint32_t)part_w[0]);
+  for (int q = 1; q < K; ++q) M = fmaxf(M, __uint_as_float((uint32_t)part_w[q]));
+  float S = 0.0f;
+  for (int q = 0; q < K; ++q)
+    S += lse_rescale(__uint_as_float((uint32_t)(part_w[q] >> 32)), __uint_as_float((uint32_t)part_w[q]), M);
   const float logsum = LOG ? sa_logf(S) : 0.0f;
   const float inv = LOG ? 0.0f : 1.0f / S;
   const float Mb = M == -__builtin_inff() ? 0.0f : M;
