@@ -164,6 +164,29 @@ __device__ __forceinline__ void lse_combine(float& m, float& s, float m2, float 
   m = M;
 }
 
+// s = sum of exp(x - m) rescaled to a maximum M >= m: s e^(m - M) (an all
+// -inf M leaves s, which is then 0; a NaN s stays NaN).
+__device__ __forceinline__ float lse_rescale(float s, float m, float M) {
+  return M != -__builtin_inff() ? s * __builtin_amdgcn_exp2f((m - M) * kLog2e) : s;
+}
+
+// (max, sum of exp) pairs of `width` lanes (a power of two; lanes w apart in
+// the XOR pattern hold the other pairs) combined: a max butterfly, one
+// rescale per lane to that max, and a sum butterfly -- one exponential per
+// lane where pairwise (m, s) combining takes two per step.  Every butterfly
+// step is symmetric in its operands, so every lane ends with the same value.
+template <int WIDTH>
+__device__ __forceinline__ void lanes_lse(float& m, float& s) {
+  float M = m;
+#pragma unroll
+  for (int off = WIDTH / 2; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+  s = lse_rescale(s, m, M);
+#pragma unroll
+  for (int off = WIDTH / 2; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+  m = M;
+}
+
+
 template <typename TI, typename TO, int VPT, bool LOG>
 __global__ void __launch_bounds__(kRowBlock)
 k_lsm_fwd_reg(const TI* __restrict__ in, TO* __restrict__ out, int64_t rows, int64_t cols) {
@@ -201,17 +224,15 @@ k_lsm_fwd_reg(const TI* __restrict__ in, TO* __restrict__ out, int64_t rows, int
         for (int k = 0; k < V; ++k) s += __builtin_amdgcn_exp2f((elem_f<TI>(x[j], k) - mb) * kLog2e);
       }
     }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) lse_combine(m, s, __shfl_xor(m, off, 64), __shfl_xor(s, off, 64));
+    lanes_lse<64>(m, s);
     __syncthreads();  // the previous row's readers are done with the slots
     if (lane == 0) {
       lds_m[wave] = m;
       lds_s[wave] = s;
     }
     __syncthreads();
-    float M = lds_m[0], S = lds_s[0];
-#pragma unroll
-    for (int w = 1; w < NW; ++w) lse_combine(M, S, lds_m[w], lds_s[w]);
+    float M = lds_m[lane & 15], S = lds_s[lane & 15];
+    lanes_lse<NW>(M, S);
     // log: (x - M) - log S;  softmax: 2^(x log2e - M log2e) / S with the
     // scaled max of the sum (an all -inf row gives 0 * inf = NaN, as upstream)
     const float logsum = LOG ? sa_logf(S) : 0.0f;
@@ -492,28 +513,6 @@ __device__ __forceinline__ void split_load(uint4 (&x)[NV], const uint4* src, int
     for (int j = 0; j < NV; ++j)
       if (base + tid + j * kSplitBlock < nvec) x[j] = ld_stream(src + base + tid + j * kSplitBlock);
   }
-}
-
-// s = sum of exp(x - m) rescaled to a maximum M >= m: s e^(m - M) (an all
-// -inf M leaves s, which is then 0; a NaN s stays NaN).
-__device__ __forceinline__ float lse_rescale(float s, float m, float M) {
-  return M != -__builtin_inff() ? s * __builtin_amdgcn_exp2f((m - M) * kLog2e) : s;
-}
-
-// (max, sum of exp) pairs of `width` lanes (a power of two; lanes w apart in
-// the XOR pattern hold the other pairs) combined: a max butterfly, one
-// rescale per lane to that max, and a sum butterfly -- one exponential per
-// lane where pairwise (m, s) combining takes two per step.  Every butterfly
-// step is symmetric in its operands, so every lane ends with the same value.
-template <int WIDTH>
-__device__ __forceinline__ void lanes_lse(float& m, float& s) {
-  float M = m;
-#pragma unroll
-  for (int off = WIDTH / 2; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
-  s = lse_rescale(s, m, M);
-#pragma unroll
-  for (int off = WIDTH / 2; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
-  m = M;
 }
 
 // The kSplitNW wavefront values of a workgroup, combined over 16 lanes (lane
