@@ -276,3 +276,19 @@ def test_split_buffers_run_out(no_fallback, monkeypatch):
         kinds.append("split" if torch.equal(o, split) else ("one_row" if torch.equal(o, one_row) else "other"))
     assert "other" not in kinds
     assert "one_row" in kinds  # at most 7 of these streams (the default stream has one) got a buffer
+
+
+def test_split_mixed_dtypes(no_fallback):
+    """bf16 rows with float32 results (half_to_float forward; a float32
+    grad_input from bf16 grad and output) through the split kernels."""
+    x = seeded((4, 128256), 131, 2.0, torch.bfloat16)
+    out = torch.ops.aten._log_softmax(x.to("supa"), 1, True)
+    assert out.dtype == torch.float32
+    np.testing.assert_allclose(out.cpu().numpy(), O.log_softmax(x.float().numpy()), rtol=1e-5, atol=1e-5)
+    sm = torch.ops.aten._softmax(x.to("supa"), 1, True)
+    np.testing.assert_allclose(sm.cpu().numpy(), O.softmax(x.float().numpy()), rtol=1e-5, atol=1e-9)
+    g, y = bwd_inputs(4, 128256, torch.bfloat16, 133)
+    gi = LSM_BWD(g.to("supa"), y.to("supa"), 1, torch.float32)
+    assert gi.dtype == torch.float32
+    ref = O.log_softmax_backward(g.float().numpy(), y.float().numpy())
+    np.testing.assert_allclose(gi.cpu().numpy(), ref, rtol=1e-5, atol=1e-6)
