@@ -1,13 +1,14 @@
 """Rows split over several workgroups: log_softmax backward and log_softmax
-/ softmax forward rows of 2 to 32 parts (2048 16-byte vectors a backward
-part, 2560 a forward part; a row of fewer than 6 parts splits only when its
-last part holds at least 40 % of a part).  The parts of a row exchange their
-row partials through a per-stream buffer; a part that finds a peer's slot
-still empty after its spin limit computes that peer's partial itself.
+/ softmax forward rows of 2 to 32 parts (at most 2048 16-byte vectors a
+backward part, 2560 a forward part; a row spread evenly over its parts,
+rounded up to whole wavefronts, but for backward rows of 6 or more parts,
+which take full parts and a short last one).  The parts of a row exchange
+their row partials through a per-stream buffer; a part that finds a peer's
+slot still empty after its spin limit computes that peer's partial itself.
 
 Covered here: parity with the oracle on rows that split and rows that do not
-(too few parts, a short last part, past the 32-part limit: the streaming
-kernel), ragged last parts,
+(one part: the one-row kernel; past the 32-part limit: the streaming
+kernel), even and ragged parts,
 the fallback (SUPA_AMD_ROW_SPLIT_SPIN=0: a part never waits) bit-identical to
 the normal path, the path switched off (SUPA_AMD_ROW_SPLIT=0), launches
 chunked over many rows, an in-place backward (never split), rows holding
@@ -59,9 +60,9 @@ def bwd_inputs(rows, cols, dtype, seed):
     return gd, yd
 
 
-# cols -> backward parts of 2048 16-byte vectors (bf16 / f16: 8 elements a vector, float32 4): 40000 bf16
-# (5000 vectors) splits in 3, 65600 bf16 (4 parts and 8 vectors) stays whole, 524288 bf16 splits in 32,
-# 524296 bf16 and 524288 float32 stream
+# cols -> backward parts of at most 2048 16-byte vectors (bf16 / f16: 8 elements a vector, float32 4):
+# 40000 bf16 (5000 vectors) splits in 3 parts of 1728, 65600 bf16 in 5 of 1664, 128264 bf16 in 7 full parts
+# and one of 1697, 524288 bf16 in 32; 524296 bf16 and 524288 float32 stream
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("cols", [40000, 65600, 128256, 128264, 262144, 524288, 524296])
 def test_log_softmax_backward_split_matches_oracle(dtype, cols, no_fallback):
@@ -76,7 +77,11 @@ def test_log_softmax_backward_split_matches_oracle(dtype, cols, no_fallback):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
-@pytest.mark.parametrize("cols", [32000, 50304, 65536, 65544, 131080, 200000, 262144, 524288])
+# cols -> forward parts of at most 2560 vectors: 20480 bf16 (2560 vectors) is one part (the one-row
+# kernel), 28664 bf16 splits in 2 parts of 1792, 65544 bf16 in 4 of 2112 (the last 1857), 655360 bf16 in
+# 32 full parts; 655368 bf16 and every float32 row past 327680 stream
+@pytest.mark.parametrize("cols", [20480, 28664, 32000, 50304, 65536, 65544, 131080, 200000, 262144, 524288,
+                                  655360, 655368])
 def test_log_softmax_forward_split_matches_oracle(dtype, cols, no_fallback):
     x = seeded((3, cols), 41, 2.0, dtype)
     out = torch.log_softmax(x.to("supa"), dim=1)
@@ -99,12 +104,15 @@ def test_softmax_forward_split_matches_oracle(dtype, no_fallback):
         assert_close16(out, ref, dtype)
 
 
-def test_split_fallback_is_bit_identical(no_fallback, monkeypatch):
+@pytest.mark.parametrize("cols", [128256, 50304])
+def test_split_fallback_is_bit_identical(cols, no_fallback, monkeypatch):
     """With a spin limit of 0 a part never waits: every partial it finds
-    unpublished it computes from the peer's data, in the peer's order."""
-    g, y = bwd_inputs(64, 128256, torch.bfloat16, 51)
+    unpublished it computes from the peer's data, in the peer's order (128256
+    bf16: 8 full backward parts, 7 even forward parts of 2304 vectors; 50304:
+    4 even backward parts of 1600, 3 forward parts of 2112)."""
+    g, y = bwd_inputs(64, cols, torch.bfloat16, 51)
     gd, yd = g.to("supa"), y.to("supa")
-    xf = seeded((64, 128256), 52, 2.0).to("supa")
+    xf = seeded((64, cols), 52, 2.0).to("supa")
     ref_b = LSM_BWD(gd, yd, 1, torch.bfloat16)
     ref_f = torch.log_softmax(xf, dim=1)
     torch.supa.synchronize()

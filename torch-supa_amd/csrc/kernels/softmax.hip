@@ -413,9 +413,10 @@ k_sm_bwd_stream(const TG* __restrict__ grad, const TG* __restrict__ outp, TO* __
 
 // ------------------------------------------------------- split rows
 // Rows of 2 to 32 parts (split_parts below says which) are split over K
-// workgroups of 512 threads, one part each: the backward's parts are 2048
-// 16-byte vectors (4 per thread, 32 KiB of grad and of output), the forward's
-// 2560 (5 per thread, 40 KiB).  Four such workgroups share a CU, so one part's statistics and
+// workgroups of 512 threads, one part each: the backward's parts are at most
+// 2048 16-byte vectors (4 per thread, 32 KiB of grad and of output), the
+// forward's 2560 (5 per thread, 40 KiB), and a row is spread evenly over its
+// K parts (split_part_len below).  Four such workgroups share a CU, so one part's statistics and
 // stores overlap other parts' loads; a whole row per 1024-thread workgroup
 // leaves a CU with one row, whose stores never overlap the next row's loads.
 // On c3's rows (bf16 [8192, 128256]) the backward ran 79.9-80.0 % of the HBM
@@ -490,6 +491,10 @@ __device__ __forceinline__ uint32_t split_wait(const uint64_t* rs, int K, uint32
 }
 
 // After every part of the row has read the slots, the last one clears them.
+// A part's own publish is complete before its increment: thread 0 stores it
+// and then waits on its own slot loads in split_wait, and on gfx9 the vector
+// memory counter that wait drains covers stores too, so no slot is published
+// after the last part's clear.
 __device__ __forceinline__ void split_release(uint64_t* rs, uint32_t* done_row, int K) {
   if (threadIdx.x == 0) {
     const uint32_t d = __hip_atomic_fetch_add(done_row, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -500,14 +505,21 @@ __device__ __forceinline__ void split_release(uint64_t* rs, uint32_t* done_row, 
   }
 }
 
-// A whole part (every part but a row's last) loads without per-vector guards
-// (a uniform branch), so its loads are not split by divergent ones.
+// A whole part loads without per-vector guards (a uniform branch), so its
+// loads are not split by divergent ones; a part that fills all but its
+// threads' last vector guards only that one.  `end` is one past the part's
+// last vector.
 template <int NV>
-__device__ __forceinline__ void split_load(uint4 (&x)[NV], const uint4* src, int base, int nvec) {
+__device__ __forceinline__ void split_load(uint4 (&x)[NV], const uint4* src, int base, int end) {
   const int tid = threadIdx.x;
+  const int nvec = end;
   if (base + kSplitBlock * NV <= nvec) {
 #pragma unroll
     for (int j = 0; j < NV; ++j) x[j] = ld_stream(src + base + tid + j * kSplitBlock);
+  } else if (base + kSplitBlock * (NV - 1) <= nvec) {
+#pragma unroll
+    for (int j = 0; j < NV - 1; ++j) x[j] = ld_stream(src + base + tid + j * kSplitBlock);
+    if (base + tid + (NV - 1) * kSplitBlock < nvec) x[NV - 1] = ld_stream(src + base + tid + (NV - 1) * kSplitBlock);
   } else {
 #pragma unroll
     for (int j = 0; j < NV; ++j)
@@ -598,10 +610,9 @@ __device__ __forceinline__ void fwd_split_out(const uint4 (&x)[kFwdNV], Vec<TO, 
 
 template <typename TI, typename TO, bool LOG>
 __global__ void __launch_bounds__(kSplitBlock, 8)
-k_lsm_fwd_split(const TI* __restrict__ in, TO* __restrict__ out, int64_t cols, int K, uint64_t* __restrict__ slots,
-                uint32_t* __restrict__ done, uint32_t spin_limit) {
+k_lsm_fwd_split(const TI* __restrict__ in, TO* __restrict__ out, int64_t cols, int K, int plen,
+                uint64_t* __restrict__ slots, uint32_t* __restrict__ done, uint32_t spin_limit) {
   constexpr int V = VecOf<TI>::V;
-  constexpr int PART = kSplitBlock * kFwdNV;
   __shared__ float lds_m[kSplitNW];
   __shared__ float lds_s[kSplitNW];
   __shared__ uint64_t part_w[kSplitMaxK];
@@ -609,11 +620,12 @@ k_lsm_fwd_split(const TI* __restrict__ in, TO* __restrict__ out, int64_t cols, i
   const int row = (int)(blockIdx.x / (unsigned)K);
   const int part = (int)(blockIdx.x - (unsigned)row * (unsigned)K);
   const int nvec = (int)(cols / V);
-  const int base = part * PART;
+  const int base = part * plen;
+  const int end = min(base + plen, nvec);
   const uint4* src = reinterpret_cast<const uint4*>(in + (int64_t)row * cols);
   uint4 x[kFwdNV];
-  split_load<kFwdNV>(x, src, base, nvec);
-  const uint64_t mine = part_lse<TI, kFwdNV>(x, base, nvec, lds_m, lds_s);
+  split_load<kFwdNV>(x, src, base, end);
+  const uint64_t mine = part_lse<TI, kFwdNV>(x, base, end, lds_m, lds_s);
   opaque<kFwdNV>(x);
   uint64_t* rs = slots + (int64_t)row * K;
   if (threadIdx.x == 0) slot_publish(rs + part, mine);
@@ -623,11 +635,12 @@ k_lsm_fwd_split(const TI* __restrict__ in, TO* __restrict__ out, int64_t cols, i
     do {
       const int q = __builtin_ctz(miss);
       miss &= miss - 1;
-      split_load<kFwdNV>(x, src, q * PART, nvec);
-      const uint64_t w = part_lse<TI, kFwdNV>(x, q * PART, nvec, lds_m, lds_s);
+      const int qb = q * plen, qe = min(qb + plen, nvec);
+      split_load<kFwdNV>(x, src, qb, qe);
+      const uint64_t w = part_lse<TI, kFwdNV>(x, qb, qe, lds_m, lds_s);
       if (threadIdx.x == 0) part_w[q] = w;
     } while (miss);
-    split_load<kFwdNV>(x, src, base, nvec);
+    split_load<kFwdNV>(x, src, base, end);
   }
   __syncthreads();
   // the row's (max, sum) from the K part pairs, in part order: the max, then
@@ -642,7 +655,7 @@ k_lsm_fwd_split(const TI* __restrict__ in, TO* __restrict__ out, int64_t cols, i
   const float Mb = M == -__builtin_inff() ? 0.0f : M;
   opaque<kFwdNV>(x);
   Vec<TO, V>* dst = reinterpret_cast<Vec<TO, V>*>(out + (int64_t)row * cols);
-  fwd_split_out<TI, TO, LOG>(x, dst, base, nvec, M, logsum, Mb, inv);
+  fwd_split_out<TI, TO, LOG>(x, dst, base, end, M, logsum, Mb, inv);
 }
 
 template <typename TG, bool WHOLE>
@@ -690,22 +703,22 @@ __device__ __forceinline__ void bwd_split_out(const uint4 (&gv)[kBwdNV], const u
 template <typename TG, typename TO>
 __global__ void __launch_bounds__(kSplitBlock, 8)
 k_lsm_bwd_split(const TG* __restrict__ grad, const TG* __restrict__ outp, TO* __restrict__ gin, int64_t cols, int K,
-                uint64_t* __restrict__ slots, uint32_t* __restrict__ done, uint32_t spin_limit) {
+                int plen, uint64_t* __restrict__ slots, uint32_t* __restrict__ done, uint32_t spin_limit) {
   constexpr int V = VecOf<TG>::V;
-  constexpr int PART = kSplitBlock * kBwdNV;
   __shared__ float lds[kSplitNW];
   __shared__ uint64_t part_w[kSplitMaxK];
   __shared__ uint32_t lds_missing;
   const int row = (int)(blockIdx.x / (unsigned)K);
   const int part = (int)(blockIdx.x - (unsigned)row * (unsigned)K);
   const int nvec = (int)(cols / V);
-  const int base = part * PART;
+  const int base = part * plen;
+  const int end = min(base + plen, nvec);
   const uint4* g = reinterpret_cast<const uint4*>(grad + (int64_t)row * cols);
   const uint4* y = reinterpret_cast<const uint4*>(outp + (int64_t)row * cols);
   uint4 gv[kBwdNV], yv[kBwdNV];
-  split_load<kBwdNV>(gv, g, base, nvec);
-  split_load<kBwdNV>(yv, y, base, nvec);
-  const uint64_t mine = part_sum<TG>(gv, base, nvec, lds);
+  split_load<kBwdNV>(gv, g, base, end);
+  split_load<kBwdNV>(yv, y, base, end);
+  const uint64_t mine = part_sum<TG>(gv, base, end, lds);
   opaque<kBwdNV>(gv);
   uint64_t* rs = slots + (int64_t)row * K;
   if (threadIdx.x == 0) slot_publish(rs + part, mine);
@@ -715,11 +728,12 @@ k_lsm_bwd_split(const TG* __restrict__ grad, const TG* __restrict__ outp, TO* __
     do {
       const int q = __builtin_ctz(miss);
       miss &= miss - 1;
-      split_load<kBwdNV>(gv, g, q * PART, nvec);
-      const uint64_t w = part_sum<TG>(gv, q * PART, nvec, lds);
+      const int qb = q * plen, qe = min(qb + plen, nvec);
+      split_load<kBwdNV>(gv, g, qb, qe);
+      const uint64_t w = part_sum<TG>(gv, qb, qe, lds);
       if (threadIdx.x == 0) part_w[q] = w;
     } while (miss);
-    split_load<kBwdNV>(gv, g, base, nvec);
+    split_load<kBwdNV>(gv, g, base, end);
   }
   __syncthreads();
   float S = __uint_as_float((uint32_t)part_w[0]);
@@ -727,8 +741,8 @@ k_lsm_bwd_split(const TG* __restrict__ grad, const TG* __restrict__ outp, TO* __
   opaque<kBwdNV>(gv);
   opaque<kBwdNV>(yv);
   Vec<TO, V>* dst = reinterpret_cast<Vec<TO, V>*>(gin + (int64_t)row * cols);
-  if (base + PART <= nvec) bwd_split_out<TG, TO, true>(gv, yv, dst, base, nvec, S);
-  else bwd_split_out<TG, TO, false>(gv, yv, dst, base, nvec, S);
+  if (base + kSplitBlock * kBwdNV <= end) bwd_split_out<TG, TO, true>(gv, yv, dst, base, end, S);
+  else bwd_split_out<TG, TO, false>(gv, yv, dst, base, end, S);
 }
 
 __global__ void __launch_bounds__(kBlock) k_split_init(uint64_t* slots, uint32_t* done, int64_t n) {
@@ -801,25 +815,35 @@ inline bool split_scratch(hipStream_t st, SplitScratch& out, uint32_t& spin_limi
   return true;
 }
 
-// Parts of `part` vectors per row for the split kernels, 0 when the row
-// takes another kernel: at least 2 and at most kSplitMaxK parts, and a last
-// part of at least 40 % of a part unless there are 6 or more.  Measured
-// against the one-row kernels (bf16 rows): [32768, 32000] forward 68.8 ->
-// 72.4 %, backward 73.4 -> 77.2 % (2 parts each); [16384, 50304] forward
-// 68.1 -> 76.4 % (3 parts, the last 46 %), backward 75.0 -> 73.5 % (4 parts,
-// the last 7 %: kept whole); [16384, 65536] forward 72.8 -> 70.5 % (4 parts,
-// the last 20 %: kept whole), backward 70.5 -> 80.9 % (4 whole parts).
+// Parts per row for the split kernels (at most `part` vectors each), 0 when
+// the row takes another kernel: 2 to kSplitMaxK parts, inputs that do not
+// overlap the output.
 inline int split_parts(int64_t nvec, int part, const void* a, const void* b, int64_t a_bytes, const void* o,
                        int64_t o_bytes) {
   const int64_t K = (nvec + part - 1) / part;
   if (K < 2 || K > kSplitMaxK) return 0;
-  if (K < 6 && 5 * (nvec - (K - 1) * part) < 2 * (int64_t)part) return 0;
   auto overlap = [](const void* x, int64_t xb, const void* y, int64_t yb) {
     const uintptr_t x0 = reinterpret_cast<uintptr_t>(x), y0 = reinterpret_cast<uintptr_t>(y);
     return x0 < y0 + (uintptr_t)yb && y0 < x0 + (uintptr_t)xb;
   };
   if (overlap(a, a_bytes, o, o_bytes) || (b && overlap(b, a_bytes, o, o_bytes))) return 0;
   return (int)K;
+}
+
+// Vectors per part when a row of nvec vectors is split in K parts of at most
+// `part`: the row spread evenly, rounded up to whole wavefronts (a part's
+// guards are then uniform in every wavefront but the last part's), or, from
+// `whole_from` parts on, full parts and a short last one (the backward's
+// whole parts run unguarded loops).  Measured on MI355X, % of the HBM
+// roofline, even parts / full parts and a short last / one-row kernel:
+// forward bf16 [8192, 128256] (7 parts) 77.6 / 76.7 / 71.8, [16384, 65536]
+// (4) 79.0 / 73.5 / 73.1, [16384, 50304] (3) 78.8 / 77.9 / 70.2; backward
+// bf16 [16384, 50304] (4) 79.8 / 74.9 / 75.3, [2048, 57344] (4) 78.3 /
+// 76.3 / 73.6, float32 [5120, 50304] (7) 68.4 / 71.2 / 72.5 (bf16 rows of
+// those 12576 vectors 74.6 / 76.0 / 74.0).
+inline int split_part_len(int64_t nvec, int K, int part, int whole_from) {
+  if (K >= whole_from) return part;
+  return (int)(((nvec + K - 1) / K + 63) / 64 * 64);
 }
 
 template <typename F>
@@ -851,12 +875,13 @@ int softmax_forward(const void* in, int32_t in_dtype, void* out, int32_t out_dty
       SplitScratch sb;
       uint32_t spin = 0;
       if (K > 0 && split_scratch(st, sb, spin)) {
+        const int plen = split_part_len(cols / V, K, kSplitBlock * kFwdNV, kSplitMaxK + 1);
         const int64_t chunk = kSplitSlots / K;
         for (int64_t r0 = 0; r0 < rows; r0 += chunk) {
           const int64_t nr = std::min(chunk, rows - r0);
           k_lsm_fwd_split<TI, TO, LOG><<<(unsigned)(nr * K), kSplitBlock, 0, st>>>(
-              static_cast<const TI*>(in) + r0 * cols, static_cast<TO*>(out) + r0 * cols, cols, K, sb.slots, sb.done,
-              spin);
+              static_cast<const TI*>(in) + r0 * cols, static_cast<TO*>(out) + r0 * cols, cols, K, plen, sb.slots,
+              sb.done, spin);
         }
         return launch_status();
       }
@@ -918,11 +943,12 @@ int supa_amd_log_softmax_backward(const void* grad, const void* output, int32_t 
       SplitScratch sb;
       uint32_t spin = 0;
       if (K > 0 && split_scratch(st, sb, spin)) {
+        const int plen = split_part_len(cols / V, K, kSplitBlock * kBwdNV, 6);
         const int64_t chunk = kSplitSlots / K;
         for (int64_t r0 = 0; r0 < rows; r0 += chunk) {
           const int64_t nr = std::min(chunk, rows - r0);
           k_lsm_bwd_split<TG, TO><<<(unsigned)(nr * K), kSplitBlock, 0, st>>>(pg + r0 * cols, py + r0 * cols,
-                                                                           po + r0 * cols, cols, K, sb.slots,
+                                                                           po + r0 * cols, cols, K, plen, sb.slots,
                                                                            sb.done, spin);
         }
         return launch_status();
