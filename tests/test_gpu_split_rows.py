@@ -61,10 +61,11 @@ def bwd_inputs(rows, cols, dtype, seed):
 
 
 # cols -> backward parts of at most 2048 16-byte vectors (bf16 / f16: 8 elements a vector, float32 4):
-# 40000 bf16 (5000 vectors) splits in 3 parts of 1728, 65600 bf16 in 5 of 1664, 128264 bf16 in 7 full parts
-# and one of 1697, 524288 bf16 in 32; 524296 bf16 and 524288 float32 stream
+# 16392 bf16 (2049 vectors, the fewest that split) splits in 2 parts of 1088, 40000 bf16 (5000 vectors) in 3
+# of 1728, 65600 bf16 in 5 of 1664, 128264 bf16 in 7 full parts and one of 1697, 524288 bf16 in 32;
+# 524296 bf16 and 524288 float32 stream
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
-@pytest.mark.parametrize("cols", [40000, 65600, 128256, 128264, 262144, 524288, 524296])
+@pytest.mark.parametrize("cols", [16392, 40000, 65600, 128256, 128264, 262144, 524288, 524296])
 def test_log_softmax_backward_split_matches_oracle(dtype, cols, no_fallback):
     rows = 3 if cols > 200000 else 6
     g, y = bwd_inputs(rows, cols, dtype, 31)
@@ -78,9 +79,10 @@ def test_log_softmax_backward_split_matches_oracle(dtype, cols, no_fallback):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 # cols -> forward parts of at most 2560 vectors: 20480 bf16 (2560 vectors) is one part (the one-row
-# kernel), 28664 bf16 splits in 2 parts of 1792, 65544 bf16 in 4 of 2112 (the last 1857), 655360 bf16 in
-# 32 full parts; 655368 bf16 and every float32 row past 327680 stream
-@pytest.mark.parametrize("cols", [20480, 28664, 32000, 50304, 65536, 65544, 131080, 200000, 262144, 524288,
+# kernel), 20488 bf16 (the fewest that split) splits in 2 parts of 1344, 28664 bf16 in 2 of 1792, 65544
+# bf16 in 4 of 2112 (the last 1857), 655360 bf16 in 32 full parts; 655368 bf16 and every float32 row past
+# 327680 stream
+@pytest.mark.parametrize("cols", [20480, 20488, 28664, 32000, 50304, 65536, 65544, 131080, 200000, 262144, 524288,
                                   655360, 655368])
 def test_log_softmax_forward_split_matches_oracle(dtype, cols, no_fallback):
     x = seeded((3, cols), 41, 2.0, dtype)
