@@ -106,21 +106,22 @@ def test_softmax_forward_split_matches_oracle(dtype, no_fallback):
         assert_close16(out, ref, dtype)
 
 
-@pytest.mark.parametrize("cols", [128256, 50304])
-def test_split_fallback_is_bit_identical(cols, no_fallback, monkeypatch):
+@pytest.mark.parametrize("dtype,cols", [(torch.bfloat16, 128256), (torch.bfloat16, 50304), (torch.float32, 28672)])
+def test_split_fallback_is_bit_identical(dtype, cols, no_fallback, monkeypatch):
     """With a spin limit of 0 a part never waits: every partial it finds
     unpublished it computes from the peer's data, in the peer's order (128256
-    bf16: 8 full backward parts, 7 even forward parts of 2304 vectors; 50304:
-    4 even backward parts of 1600, 3 forward parts of 2112)."""
-    g, y = bwd_inputs(64, cols, torch.bfloat16, 51)
+    bf16: 8 full backward parts, 7 even forward parts of 2304 vectors; 50304
+    bf16: 4 even backward parts of 1600, 3 forward parts of 2112; 28672
+    float32: 4 backward parts of 1792, 3 forward parts of 2432)."""
+    g, y = bwd_inputs(64, cols, dtype, 51)
     gd, yd = g.to("supa"), y.to("supa")
-    xf = seeded((64, cols), 52, 2.0).to("supa")
-    ref_b = LSM_BWD(gd, yd, 1, torch.bfloat16)
+    xf = seeded((64, cols), 52, 2.0, dtype).to("supa")
+    ref_b = LSM_BWD(gd, yd, 1, dtype)
     ref_f = torch.log_softmax(xf, dim=1)
     torch.supa.synchronize()
     monkeypatch.setenv("SUPA_AMD_ROW_SPLIT_SPIN", "0")
     for _ in range(3):
-        assert torch.equal(LSM_BWD(gd, yd, 1, torch.bfloat16).cpu(), ref_b.cpu())
+        assert torch.equal(LSM_BWD(gd, yd, 1, dtype).cpu(), ref_b.cpu())
         assert torch.equal(torch.log_softmax(xf, dim=1).cpu(), ref_f.cpu())
 
 
